@@ -1,0 +1,239 @@
+/*
+ * sili_hip.h -- C ABI of the MI355X (gfx950) FP4 delta-CSR sparse linear layer.
+ *
+ * Drop-in boundary for sili's SparseLinearLayer hot path
+ * (SimLeek/sili__new sili/cpu_backend.cpp:349-984, bindings :1506-1743).
+ * Plain C: opaque handle, int status codes, thread-local last-error string,
+ * plain pointers and sizes, streams passed as void* (a hipStream_t, or NULL
+ * for the layer's own stream).  No torch or HIP types appear here.
+ *
+ * Memory: arguments documented "device" are device pointers; "host" are host
+ * pointers.  Compute entry points are asynchronous on the given stream unless
+ * documented otherwise; sili_synchronize() waits for the layer's stream.
+ *
+ * Layout conventions (the reference's):
+ *   - matrix rows are INPUT neurons: y[b,c] = sum_r x[b,r] * W(r,c)
+ *     (linear_disldo.hpp:63-65);
+ *   - activations are fp32 [batch, n] row-major (linear_disldo.hpp:41-44);
+ *   - scattered value byte = (w_code<<4)|imp_code (fp4quant.hpp:280-383);
+ *   - block4 slot byte = (imp_code<<4)|w_code, slot = lj*4+li (block4.hpp:300-312);
+ *   - sparse activations are CSR: int32 ptrs[batch+1], int32 indices sorted
+ *     ascending within each batch row, fp32 values (sisldo_ops.hpp:372-378).
+ */
+#ifndef SILI_HIP_H
+#define SILI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  The Python binding maps them to the exception types the
+ * reference raises (sili/cpu_backend.cpp: std::invalid_argument -> ValueError,
+ * std::bad_alloc -> MemoryError, std::runtime_error -> RuntimeError,
+ * std::out_of_range -> IndexError). */
+enum {
+    SILI_OK = 0,
+    SILI_ERR_INVALID = 1,   /* ValueError   */
+    SILI_ERR_NOMEM = 2,     /* MemoryError  */
+    SILI_ERR_RUNTIME = 3,   /* RuntimeError */
+    SILI_ERR_RANGE = 4,     /* IndexError   */
+    SILI_ERR_HIP = 5        /* RuntimeError (HIP runtime failure) */
+};
+
+typedef struct sili_layer sili_layer;
+
+/* Last error message of the calling thread ("" when none). */
+const char *sili_last_error(void);
+
+/* ---- lifetime --------------------------------------------------------- */
+
+/* SparseLinearLayer(n_inputs, n_outputs, max_weights, num_cpus)
+ * (sili/cpu_backend.cpp:375-447).  max_weights sets the same byte budgets as
+ * the reference (index bytes max_weights*8+4096, values max_weights+64,
+ * block4 tiles max(4,max_weights/16)*16); loads beyond them fail with
+ * SILI_ERR_NOMEM.  device = HIP device ordinal. */
+int sili_create(int64_t n_inputs, int64_t n_outputs, int64_t max_weights, int device,
+                sili_layer **out);
+void sili_destroy(sili_layer *layer);
+/* Wait for all work queued on the layer's stream. */
+int sili_synchronize(sili_layer *layer);
+/* The layer's own hipStream_t (as void*). */
+void *sili_stream(sili_layer *layer);
+
+/* ---- construction / state -------------------------------------------- */
+
+/* load_weights(ptrs, indices, vals) (sili/cpu_backend.cpp:859-901): host
+ * absolute CSR over input rows; vals are fp4-quantized (fp4quant.hpp:86-126),
+ * importance 0.  imp may be NULL; when given it is quantized into the low
+ * nibble (delta_csr_memory.hpp:16-93 takes importance per synapse).  Columns
+ * must be strictly increasing within a row and < n_outputs.  Replaces the
+ * scattered store; the block4 store is left as is. */
+int sili_load_weights(sili_layer *layer, const int32_t *ptrs, const int32_t *indices,
+                      const float *vals, const float *imp, int64_t nnz);
+
+/* Same, from raw value bytes (w_code<<4 | imp_code), no quantization. */
+int sili_load_weight_bytes(sili_layer *layer, const int32_t *ptrs, const int32_t *indices,
+                           const uint8_t *bytes, int64_t nnz);
+
+/* load_dense_codes(weight_codes, importance_codes) (sili/cpu_backend.cpp:910-921,
+ * delta_csr_memory.hpp:841-945): host uint8 [n_in*n_out] code matrices; every
+ * 4x4 block becomes a block4 tile (byte = w | imp<<4), replacing the block4
+ * store. */
+int sili_load_dense_codes(sili_layer *layer, const uint8_t *weight_codes,
+                          const uint8_t *importance_codes);
+
+/* Block4 store from a tile list (no reference counterpart as one call: the
+ * reference builds the same store tile by tile with Block4Store::get_or_create,
+ * block4.hpp:1168-1188).  host int32 br[n], bc[n] (any order, no duplicates),
+ * host uint8 tile_bytes[16*n] in slot order lj*4+li. Replaces the block4 store. */
+int sili_load_block4_tiles(sili_layer *layer, const int32_t *br, const int32_t *bc,
+                           const uint8_t *tile_bytes, int64_t n_tiles);
+
+/* set_scale_rank(k) (sili/cpu_backend.cpp:455-461): 1 <= k <= 4, else
+ * SILI_ERR_INVALID.  Resets scales to the reference defaults (component 0 = 1,
+ * others 0; delta_csr_types.hpp:1116-1121). */
+int sili_set_scale_rank(sili_layer *layer, int rank);
+int sili_get_scale_rank(const sili_layer *layer);
+
+/* Bulk set_value_scale_raw_k / set_output_scale_raw_k /
+ * set_importance_scale_raw / set_output_importance_scale_raw
+ * (sili/cpu_backend.cpp:792-806, delta_csr_types.hpp:1013-1196).
+ * host fp32, value/output scales laid out [n*rank] (row-major per
+ * component).  Setting output scales marks them trainable, like
+ * set_output_scale_raw (delta_csr_types.hpp:1190-1196). */
+int sili_set_value_scale(sili_layer *layer, const float *vs);
+int sili_set_output_scale(sili_layer *layer, const float *os);
+int sili_set_importance_scale(sili_layer *layer, const float *is);
+int sili_set_output_importance_scale(sili_layer *layer, const float *ois);
+/* host fp32 outputs, same layouts. */
+int sili_get_value_scale(const sili_layer *layer, float *vs);
+int sili_get_output_scale(const sili_layer *layer, float *os);
+
+/* ---- compute ------------------------------------------------------------ */
+
+/* forward_dense (sili/cpu_backend.cpp:475-492, linear_disldo.hpp:68-345):
+ * device x [batch,n_in] -> device y [batch,n_out] (overwritten). */
+int sili_forward_dense(sili_layer *layer, const float *x, int64_t batch, float *y,
+                       void *stream);
+
+/* backward_dense at learning_rate 0 (sili/cpu_backend.cpp:496-529,
+ * linear_disldo.hpp:462-2113): dx [batch,n_in] = W^T-gather of dy
+ * (overwritten); always accumulates neuron_input_accum += sum_b|x| and
+ * neuron_grad_accum += sum_b|dy| (linear_disldo.hpp:515-520).  When gw_s /
+ * gw_b are non-NULL, also writes the nnz-sampled grad-W (see
+ * sili_sampled_gradw).  learning_rate must be 0 (the fused optimizer update
+ * is not implemented yet: SILI_ERR_INVALID otherwise). */
+int sili_backward_dense(sili_layer *layer, const float *x, const float *dy, int64_t batch,
+                        float *dx, float *gw_s, float *gw_b, float learning_rate,
+                        void *stream);
+
+/* nnz-pattern-sampled grad-W: gw_s[e] = sum_b x[b,r(e)]*dy[b,c(e)] for every
+ * scattered synapse e in storage order; gw_b[16*t + slot] likewise for every
+ * slot of block4 tile t (tile storage order, slot = lj*4+li).  The reference
+ * consumes g = dy*x per synapse inside its optimizer
+ * (linear_disldo.hpp:811-882) and never materialises it. */
+int sili_sampled_gradw(sili_layer *layer, const float *x, const float *dy, int64_t batch,
+                       float *gw_s, float *gw_b, void *stream);
+
+/* forward_sparse (sili/cpu_backend.cpp:571-585, sisldo_ops.hpp:198-551):
+ * device CSR input (ptrs[batch+1], indices[nnz_x], values[nnz_x]) ->
+ * device y [batch,n_out] (overwritten). */
+int sili_forward_sparse(sili_layer *layer, const int32_t *ptrs, const int32_t *indices,
+                        const float *values, int64_t nnz_x, int64_t batch, float *y,
+                        void *stream);
+
+/* backward_sparse at learning_rate 0 (sili/cpu_backend.cpp:587-603,
+ * sisldo_ops.hpp:589-1104): dense x [batch,n_in], sparse dy CSR -> device dx
+ * [batch,n_in] (overwritten); accumulates neuron_input_accum / neuron_grad_accum. */
+int sili_backward_sparse(sili_layer *layer, const float *x, const int32_t *dy_ptrs,
+                         const int32_t *dy_indices, const float *dy_values, int64_t nnz_dy,
+                         int64_t batch, float *dx, float learning_rate, void *stream);
+
+/* ---- synaptogenesis ----------------------------------------------------- */
+
+/* Bulk synaptogenesis step, on the GPU.  Selection policy (new; the reference
+ * prunes by importance row by row, delta_csr_memory.hpp:1019-1258): prune the
+ * round(prune_frac*N) stored synapses (scattered + live block4 slots) with the
+ * smallest |dec(code)*S(r,c)|, ties by (row, col) ascending; regrow as many
+ * at the host candidates (cand_rows/cols/vals, optional cand_scores), taking
+ * the first valid ones in list order (in range, not stored, not just pruned,
+ * not a repeat).  A new synapse's code is fp4_encode(val/S(r,c)); its
+ * importance code is fp4_encode(score), or default_imp_code without scores.
+ * Structural rules follow the reference: a tile whose live count drops below
+ * 2 is demoted (delta_csr_memory.hpp:949-999), an insert into a window that
+ * holds a tile writes the tile (:620-646), a window that ends up with >= 2
+ * scattered synapses after an insert is promoted (:648-700).  The delta-CSR,
+ * block4 store and derived device structures are rebuilt by device scan,
+ * sort and compaction.  host candidate arrays; results (host) in out_stats[7]:
+ * target, pruned, grown, demoted tiles, promoted tiles, scattered nnz, tiles.
+ * Synchronous. */
+int sili_synapto_step(sili_layer *layer, float prune_frac, const int32_t *cand_rows,
+                      const int32_t *cand_cols, const float *cand_vals,
+                      const float *cand_scores, int64_t n_cand, int default_imp_code,
+                      int64_t *out_stats);
+
+/* ---- accumulators ------------------------------------------------------- */
+
+/* neuron_input_accum / neuron_grad_accum (sili/cpu_backend.cpp:946-951):
+ * host copies (n_in / n_out fp32).  Synchronous. */
+int sili_get_accumulators(sili_layer *layer, float *acc_in, float *acc_grad);
+/* zero_accum() (sili/cpu_backend.cpp:840-843). */
+int sili_zero_accum(sili_layer *layer);
+
+/* ---- introspection / export (parity) ------------------------------------ */
+
+typedef struct {
+    int64_t n_inputs, n_outputs;
+    int64_t nnz_scattered;     /* stored scattered synapses */
+    int64_t index_bytes;       /* ULEB128 bytes of the scattered store */
+    int64_t n_tiles;           /* block4 tiles */
+    int64_t block_index_bytes; /* ULEB128 bytes of the block4 store */
+    int64_t live_block4;       /* live (byte != 0) block4 slots */
+    int64_t n_segments;        /* decode work items of the scattered store */
+    int32_t scale_rank;
+    int32_t has_nonfinite;     /* a weight code 8 (NaN) or non-finite scale */
+} sili_info;
+int sili_get_info(sili_layer *layer, sili_info *out);
+
+/* Scattered store exactly as held on the device (compact: no headroom):
+ * host uint64 row_byte_start[n_in+1], row_elem_start[n_in+1],
+ * uint8 idx[index_bytes], uint8 val[nnz_scattered].  NULL skips an array.
+ * Synchronous.  (Reference equivalent: DeltaCSRWeights after compact(),
+ * sisldo_ops.hpp:44-96.) */
+int sili_export_scattered(sili_layer *layer, uint64_t *row_byte_start,
+                          uint64_t *row_elem_start, uint8_t *idx, uint8_t *val);
+
+/* Block4 store: host int32 br[n_tiles], bc[n_tiles] in storage order, uint8
+ * tiles[16*n_tiles], uint64 brow_byte_start/brow_tile_start [ceil(n_in/4)+1],
+ * uint8 bidx[block_index_bytes].  NULL skips an array.  Synchronous. */
+int sili_export_block4(sili_layer *layer, int32_t *br, int32_t *bc, uint8_t *tiles,
+                       uint64_t *brow_byte_start, uint64_t *brow_tile_start,
+                       uint8_t *bidx);
+
+/* Device decode of the scattered store (ULEB128 prefix-scan decode + FP4
+ * dequant): host int32 cols[nnz_scattered] and fp32 w_true[nnz_scattered]
+ * = fl32(dec(code)*S(r,c)) in storage order.  Either may be NULL. Synchronous. */
+int sili_decode_scattered(sili_layer *layer, int32_t *cols, float *w_true);
+
+/* Combined absolute CSR, scattered + live block4 slots, columns ascending per
+ * row, decoded stored values (get_ptrs/get_indices/get_weights_vals/
+ * get_importance, sili/cpu_backend.cpp:956-983,
+ * delta_csr_memory.hpp:127-213).  Call with NULL outputs to get the count in
+ * *n_out_entries.  host outputs.  Synchronous. */
+int sili_export_absolute(sili_layer *layer, int32_t *ptrs, int32_t *indices, float *w,
+                         float *imp, int64_t *n_out_entries);
+
+/* ---- device memory helpers (for callers without HIP headers) ------------ */
+int sili_device_alloc(sili_layer *layer, size_t bytes, void **out);
+int sili_device_free(sili_layer *layer, void *ptr);
+int sili_memcpy_h2d(sili_layer *layer, void *dst, const void *src, size_t bytes);
+int sili_memcpy_d2h(sili_layer *layer, void *dst, const void *src, size_t bytes);
+int sili_memset_device(sili_layer *layer, void *dst, int value, size_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SILI_HIP_H */

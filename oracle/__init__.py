@@ -1,0 +1,13 @@
+"""CPU oracle for the FP4 delta-CSR sparse layer -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this package, and only as the checker / the timed CPU baseline.  The
+product (sili__new_amd) never imports, links or runs anything here.
+
+    liboracle.so   (_build/)  CPU restatement of the reference (sili_oracle.cpp)
+    libsili_ref.so (_ref/)    the reference's own headers compiled in place
+                              (only where /root/reference exists at build time)
+"""
+from .oracle import (  # noqa: F401
+    HostLayer, RefLayer, build, have_ref, lib, reflib,
+)

@@ -1,0 +1,449 @@
+"""ctypes front-end of the CPU oracle (test infrastructure only).
+
+HostLayer holds one layer in the compact host format (numpy arrays) and runs
+the restatement's arithmetic on it; RefLayer drives the reference's own
+compiled headers through ref_shim.cpp for pinning the restatement.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "_build" / "liboracle.so"
+REF_PATH = HERE / "_ref" / "libsili_ref.so"
+
+_u8p = C.POINTER(C.c_uint8)
+_u64p = C.POINTER(C.c_uint64)
+_i32p = C.POINTER(C.c_int32)
+_f32p = C.POINTER(C.c_float)
+
+
+def build(ref: bool = True) -> None:
+    """Compile the oracle (and, where the reference tree exists, _ref)."""
+    targets = ["oracle", "ref"] if ref else ["oracle"]
+    subprocess.run(["make", "-s", "-C", str(HERE), *targets], check=True)
+
+
+class _OracleLayerC(C.Structure):
+    _fields_ = [
+        ("n_in", C.c_int64), ("n_out", C.c_int64), ("rank", C.c_int32),
+        ("row_byte_start", _u64p), ("row_elem_start", _u64p), ("idx", _u8p), ("val", _u8p),
+        ("n_tiles", C.c_int64), ("brow_byte_start", _u64p), ("brow_tile_start", _u64p),
+        ("bidx", _u8p), ("tiles", _u8p),
+        ("value_scale", _f32p), ("output_scale", _f32p),
+    ]
+
+
+class _SynStats(C.Structure):
+    _fields_ = [(n, C.c_int64) for n in (
+        "n_prune_target", "n_pruned", "n_grown", "n_demoted_tiles", "n_promoted_tiles",
+        "n_scattered", "n_tiles")]
+
+
+def _p(a: np.ndarray | None, t):
+    if a is None:
+        return None
+    return a.ctypes.data_as(t)
+
+
+_lib = None
+_ref = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build(ref=False)
+        L = C.CDLL(str(LIB_PATH))
+        L.oracle_fp4_decode.restype = C.c_float
+        L.oracle_fp4_decode.argtypes = [C.c_uint8]
+        L.oracle_fp4_encode.restype = C.c_uint8
+        L.oracle_fp4_encode.argtypes = [C.c_float]
+        L.oracle_fp4_encode_array.argtypes = [_f32p, C.c_int64, _u8p]
+        L.oracle_uleb_encode.restype = C.c_size_t
+        L.oracle_uleb_encode.argtypes = [C.c_uint32, _u8p]
+        L.oracle_csr_index_bytes.restype = C.c_int64
+        L.oracle_csr_index_bytes.argtypes = [C.c_int64, _i32p, _i32p]
+        L.oracle_csr_encode.argtypes = [C.c_int64, _i32p, _i32p, _f32p, _f32p, _u64p, _u64p, _u8p, _u8p]
+        L.oracle_csr_encode_bytes.argtypes = [C.c_int64, _i32p, _i32p, _u8p, _u64p, _u64p, _u8p, _u8p]
+        L.oracle_csr_decode.argtypes = [C.c_int64, _u64p, _u64p, _u8p, _i32p]
+        L.oracle_combined_to_absolute.restype = C.c_int64
+        L.oracle_combined_to_absolute.argtypes = [C.POINTER(_OracleLayerC), _i32p, _i32p, _f32p, _f32p]
+        L.oracle_dense_weights.argtypes = [C.POINTER(_OracleLayerC), _f32p]
+        L.oracle_forward_dense.argtypes = [C.POINTER(_OracleLayerC), _f32p, C.c_int64, _f32p, C.c_int, C.c_int]
+        L.oracle_backward_dense.argtypes = [C.POINTER(_OracleLayerC), _f32p, _f32p, C.c_int64, _f32p,
+                                            _f32p, _f32p, C.c_int, C.c_int]
+        L.oracle_forward_sparse.argtypes = [C.POINTER(_OracleLayerC), _i32p, _i32p, _f32p, C.c_int64,
+                                            _f32p, C.c_int, C.c_int]
+        L.oracle_backward_sparse.argtypes = [C.POINTER(_OracleLayerC), _f32p, _i32p, _i32p, _f32p,
+                                             C.c_int64, _f32p, _f32p, _f32p, C.c_int, C.c_int]
+        L.oracle_sampled_gradw.argtypes = [C.POINTER(_OracleLayerC), _f32p, _f32p, C.c_int64, _f32p,
+                                           _f32p, C.c_int, C.c_int]
+        L.oracle_synapto_step.argtypes = [C.POINTER(_OracleLayerC), C.c_float, _i32p, _i32p, _f32p, _f32p,
+                                          C.c_int64, C.c_int, _i32p, _i32p, _u8p, _i32p, _i32p, _u8p,
+                                          C.POINTER(_SynStats)]
+        _lib = L
+    return _lib
+
+
+def have_ref() -> bool:
+    return REF_PATH.exists()
+
+
+def reflib():
+    global _ref
+    if _ref is None:
+        if not REF_PATH.exists():
+            raise FileNotFoundError(f"{REF_PATH} not built (needs the reference tree at build time)")
+        R = C.CDLL(str(REF_PATH))
+        R.ref_fp4_encode.restype = C.c_uint8
+        R.ref_fp4_encode.argtypes = [C.c_float]
+        R.ref_fp4_decode.restype = C.c_float
+        R.ref_fp4_decode.argtypes = [C.c_uint8]
+        R.ref_fp4_table.restype = C.c_float
+        R.ref_fp4_table.argtypes = [C.c_uint8]
+        R.ref_uleb_encode.restype = C.c_size_t
+        R.ref_uleb_encode.argtypes = [C.c_uint32, _u8p]
+        R.ref_layer_new.restype = C.c_void_p
+        R.ref_layer_new.argtypes = [C.c_int, C.c_int, _i32p, _i32p, _f32p, _f32p]
+        R.ref_layer_free.argtypes = [C.c_void_p]
+        R.ref_layer_set_scales.argtypes = [C.c_void_p, _f32p, _f32p, C.c_int]
+        R.ref_layer_load_dense_codes.argtypes = [C.c_void_p, _u8p, _u8p]
+        R.ref_layer_put_tile.argtypes = [C.c_void_p, C.c_int, C.c_int, _u8p]
+        R.ref_layer_compact.argtypes = [C.c_void_p]
+        R.ref_layer_export.restype = C.c_int64
+        R.ref_layer_export.argtypes = [C.c_void_p, _u64p, _u64p, _u8p, _u8p]
+        R.ref_layer_nnz_scattered.restype = C.c_int64
+        R.ref_layer_nnz_scattered.argtypes = [C.c_void_p]
+        R.ref_layer_export_tiles.restype = C.c_int64
+        R.ref_layer_export_tiles.argtypes = [C.c_void_p, _i32p, _i32p, _u8p]
+        R.ref_layer_combined.restype = C.c_int64
+        R.ref_layer_combined.argtypes = [C.c_void_p, _i32p, _i32p, _f32p, _f32p]
+        R.ref_forward_dense.argtypes = [C.c_void_p, _f32p, C.c_int, _f32p, C.c_int]
+        R.ref_backward_dense.argtypes = [C.c_void_p, _f32p, _f32p, C.c_int, _f32p, _f32p, _f32p, C.c_int]
+        R.ref_forward_sparse.argtypes = [C.c_void_p, _i32p, _i32p, _f32p, C.c_int, _f32p, C.c_int]
+        R.ref_backward_sparse.argtypes = [C.c_void_p, _f32p, _i32p, _i32p, _f32p, C.c_int, _f32p, _f32p,
+                                          _f32p, C.c_int]
+        R.ref_row_remove_col.restype = C.c_int
+        R.ref_row_remove_col.argtypes = [C.c_void_p, C.c_int, C.c_int]
+        R.ref_row_insert_col.restype = C.c_int
+        R.ref_row_insert_col.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_float, C.c_float]
+        R.ref_maybe_promote.argtypes = [C.c_void_p, C.c_int, C.c_int]
+        R.ref_demote_tile.argtypes = [C.c_void_p, C.c_int, C.c_int]
+        R.ref_zero_tile_slot.restype = C.c_int
+        R.ref_zero_tile_slot.argtypes = [C.c_void_p, C.c_int, C.c_int]
+        _ref = R
+    return _ref
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def encode_tiles(n_in: int, br: np.ndarray, bc: np.ndarray, tiles: np.ndarray):
+    """Block4 store (block-row CSR, ULEB block-column deltas) from a tile
+    list; returns (brow_byte_start, brow_tile_start, bidx, tiles sorted)."""
+    br = np.asarray(br, np.int64)
+    bc = np.asarray(bc, np.int64)
+    order = np.lexsort((bc, br))
+    br, bc = br[order], bc[order]
+    t = np.ascontiguousarray(np.asarray(tiles, np.uint8).reshape(-1, 16)[order]).ravel()
+    brows = (n_in + 3) // 4
+    ptrs = np.zeros(brows + 1, np.int32)
+    np.add.at(ptrs, br + 1, 1)
+    ptrs = np.cumsum(ptrs).astype(np.int32)
+    L = lib()
+    nb = L.oracle_csr_index_bytes(brows, _p(ptrs, _i32p), _p(_c(bc, np.int32), _i32p))
+    bs = np.zeros(brows + 1, np.uint64)
+    ts = np.zeros(brows + 1, np.uint64)
+    idx = np.zeros(max(1, nb), np.uint8)
+    dummy = np.zeros(max(1, len(bc)), np.uint8)
+    rc = L.oracle_csr_encode_bytes(brows, _p(ptrs, _i32p), _p(_c(bc, np.int32), _i32p), _p(dummy, _u8p),
+                                   _p(bs, _u64p), _p(ts, _u64p), _p(idx, _u8p), _p(dummy.copy(), _u8p))
+    if rc != 0:
+        raise ValueError("tile list has duplicates")
+    return bs, ts, idx[:nb], t, br.astype(np.int32), bc.astype(np.int32)
+
+
+class HostLayer:
+    """A layer in the compact host format, evaluated by the CPU restatement."""
+
+    def __init__(self, n_in: int, n_out: int, rank: int = 1):
+        self.n_in, self.n_out, self.rank = int(n_in), int(n_out), int(rank)
+        self.row_byte_start = np.zeros(n_in + 1, np.uint64)
+        self.row_elem_start = np.zeros(n_in + 1, np.uint64)
+        self.idx = np.zeros(1, np.uint8)
+        self.val = np.zeros(1, np.uint8)
+        self.n_tiles = 0
+        self.brow_byte_start = np.zeros((n_in + 3) // 4 + 1, np.uint64)
+        self.brow_tile_start = np.zeros((n_in + 3) // 4 + 1, np.uint64)
+        self.bidx = np.zeros(1, np.uint8)
+        self.tiles = np.zeros(16, np.uint8)
+        self.tile_br = np.zeros(0, np.int32)
+        self.tile_bc = np.zeros(0, np.int32)
+        vs = np.zeros(n_in * rank, np.float32)
+        vs[::rank] = 1.0
+        os_ = np.zeros(n_out * rank, np.float32)
+        os_[::rank] = 1.0
+        self.value_scale, self.output_scale = vs, os_
+
+    # -- construction ----------------------------------------------------------
+    def load_csr(self, ptrs, cols, w=None, imp=None, bytes_=None):
+        ptrs = _c(ptrs, np.int32)
+        cols = _c(cols, np.int32)
+        L = lib()
+        nb = L.oracle_csr_index_bytes(self.n_in, _p(ptrs, _i32p), _p(cols, _i32p))
+        self.idx = np.zeros(max(1, nb), np.uint8)
+        self.val = np.zeros(max(1, len(cols)), np.uint8)
+        if bytes_ is not None:
+            rc = L.oracle_csr_encode_bytes(self.n_in, _p(ptrs, _i32p), _p(cols, _i32p),
+                                           _p(_c(bytes_, np.uint8), _u8p), _p(self.row_byte_start, _u64p),
+                                           _p(self.row_elem_start, _u64p), _p(self.idx, _u8p),
+                                           _p(self.val, _u8p))
+        else:
+            wv = _c(w, np.float32)
+            iv = None if imp is None else _c(imp, np.float32)
+            rc = L.oracle_csr_encode(self.n_in, _p(ptrs, _i32p), _p(cols, _i32p), _p(wv, _f32p),
+                                     _p(iv, _f32p), _p(self.row_byte_start, _u64p),
+                                     _p(self.row_elem_start, _u64p), _p(self.idx, _u8p), _p(self.val, _u8p))
+        if rc != 0:
+            raise ValueError("columns must be strictly increasing within a row")
+        self.nnz = len(cols)
+        self.index_bytes = nb
+        return self
+
+    def load_tiles(self, br, bc, tiles):
+        (self.brow_byte_start, self.brow_tile_start, self.bidx, self.tiles,
+         self.tile_br, self.tile_bc) = encode_tiles(self.n_in, br, bc, tiles)
+        self.n_tiles = len(self.tile_br)
+        if self.n_tiles == 0:
+            self.tiles = np.zeros(16, np.uint8)
+        if len(self.bidx) == 0:
+            self.bidx = np.zeros(1, np.uint8)
+        return self
+
+    def set_scales(self, vs=None, os_=None):
+        if vs is not None:
+            self.value_scale = _c(vs, np.float32).copy()
+        if os_ is not None:
+            self.output_scale = _c(os_, np.float32).copy()
+        return self
+
+    def _cstruct(self) -> _OracleLayerC:
+        s = _OracleLayerC()
+        s.n_in, s.n_out, s.rank = self.n_in, self.n_out, self.rank
+        s.row_byte_start = _p(self.row_byte_start, _u64p)
+        s.row_elem_start = _p(self.row_elem_start, _u64p)
+        s.idx, s.val = _p(self.idx, _u8p), _p(self.val, _u8p)
+        s.n_tiles = self.n_tiles
+        s.brow_byte_start = _p(self.brow_byte_start, _u64p)
+        s.brow_tile_start = _p(self.brow_tile_start, _u64p)
+        s.bidx, s.tiles = _p(self.bidx, _u8p), _p(self.tiles, _u8p)
+        s.value_scale, s.output_scale = _p(self.value_scale, _f32p), _p(self.output_scale, _f32p)
+        return s
+
+    # -- structure ---------------------------------------------------------------
+    def decode_cols(self) -> np.ndarray:
+        n = int(self.row_elem_start[-1])
+        out = np.zeros(max(1, n), np.int32)
+        if lib().oracle_csr_decode(self.n_in, _p(self.row_byte_start, _u64p), _p(self.row_elem_start, _u64p),
+                                   _p(self.idx, _u8p), _p(out, _i32p)) != 0:
+            raise ValueError("index stream does not match its row ends")
+        return out[:n]
+
+    def absolute(self):
+        s = self._cstruct()
+        n = lib().oracle_combined_to_absolute(C.byref(s), None, None, None, None)
+        p = np.zeros(self.n_in + 1, np.int32)
+        ix = np.zeros(max(1, n), np.int32)
+        w = np.zeros(max(1, n), np.float32)
+        imp = np.zeros(max(1, n), np.float32)
+        lib().oracle_combined_to_absolute(C.byref(s), _p(p, _i32p), _p(ix, _i32p), _p(w, _f32p), _p(imp, _f32p))
+        return p, ix[:n], w[:n], imp[:n]
+
+    def dense(self) -> np.ndarray:
+        W = np.zeros((self.n_in, self.n_out), np.float32)
+        s = self._cstruct()
+        lib().oracle_dense_weights(C.byref(s), _p(W, _f32p))
+        return W
+
+    # -- compute (fresh outputs) ---------------------------------------------------
+    def forward_dense(self, x, threads=8, absmode=False):
+        x = _c(np.atleast_2d(x), np.float32)
+        y = np.zeros((x.shape[0], self.n_out), np.float32)
+        s = self._cstruct()
+        lib().oracle_forward_dense(C.byref(s), _p(x, _f32p), x.shape[0], _p(y, _f32p), threads, int(absmode))
+        return y
+
+    def backward_dense(self, x, dy, threads=8, absmode=False, acc=None):
+        x = _c(np.atleast_2d(x), np.float32)
+        dy = _c(np.atleast_2d(dy), np.float32)
+        dx = np.zeros_like(x)
+        ai = np.zeros(self.n_in, np.float32) if acc is None else acc[0]
+        ag = np.zeros(self.n_out, np.float32) if acc is None else acc[1]
+        s = self._cstruct()
+        lib().oracle_backward_dense(C.byref(s), _p(x, _f32p), _p(dy, _f32p), x.shape[0], _p(dx, _f32p),
+                                    _p(ai, _f32p), _p(ag, _f32p), threads, int(absmode))
+        return dx, ai, ag
+
+    def forward_sparse(self, ptrs, idx, vals, batch, threads=8, absmode=False):
+        ptrs, idx, vals = _c(ptrs, np.int32), _c(idx, np.int32), _c(vals, np.float32)
+        y = np.zeros((batch, self.n_out), np.float32)
+        s = self._cstruct()
+        lib().oracle_forward_sparse(C.byref(s), _p(ptrs, _i32p), _p(idx, _i32p), _p(vals, _f32p), batch,
+                                    _p(y, _f32p), threads, int(absmode))
+        return y
+
+    def backward_sparse(self, x, dptrs, didx, dvals, batch, threads=8, absmode=False):
+        x = _c(np.atleast_2d(x), np.float32)
+        dptrs, didx, dvals = _c(dptrs, np.int32), _c(didx, np.int32), _c(dvals, np.float32)
+        dx = np.zeros_like(x)
+        ai = np.zeros(self.n_in, np.float32)
+        ag = np.zeros(self.n_out, np.float32)
+        s = self._cstruct()
+        lib().oracle_backward_sparse(C.byref(s), _p(x, _f32p), _p(dptrs, _i32p), _p(didx, _i32p),
+                                     _p(dvals, _f32p), batch, _p(dx, _f32p), _p(ai, _f32p), _p(ag, _f32p),
+                                     threads, int(absmode))
+        return dx, ai, ag
+
+    def sampled_gradw(self, x, dy, threads=8, absmode=False):
+        x = _c(np.atleast_2d(x), np.float32)
+        dy = _c(np.atleast_2d(dy), np.float32)
+        gs = np.zeros(max(1, int(self.row_elem_start[-1])), np.float32)
+        gb = np.zeros(max(16, self.n_tiles * 16), np.float32)
+        s = self._cstruct()
+        lib().oracle_sampled_gradw(C.byref(s), _p(x, _f32p), _p(dy, _f32p), x.shape[0], _p(gs, _f32p),
+                                   _p(gb, _f32p), threads, int(absmode))
+        return gs[:int(self.row_elem_start[-1])], gb[:self.n_tiles * 16]
+
+    def synapto_step(self, prune_frac, cand_r, cand_c, cand_v, cand_s=None, default_imp_code=1):
+        cand_r, cand_c, cand_v = _c(cand_r, np.int32), _c(cand_c, np.int32), _c(cand_v, np.float32)
+        cs = None if cand_s is None else _c(cand_s, np.float32)
+        nnz = int(self.row_elem_start[-1])
+        cap_s = nnz + len(cand_r) + 16 * self.n_tiles + 1
+        cap_t = self.n_tiles + len(cand_r) + 1
+        p = np.zeros(self.n_in + 1, np.int32)
+        cols = np.zeros(cap_s, np.int32)
+        byts = np.zeros(cap_s, np.uint8)
+        tbr = np.zeros(cap_t, np.int32)
+        tbc = np.zeros(cap_t, np.int32)
+        tby = np.zeros(cap_t * 16, np.uint8)
+        st = _SynStats()
+        s = self._cstruct()
+        rc = lib().oracle_synapto_step(C.byref(s), prune_frac, _p(cand_r, _i32p), _p(cand_c, _i32p),
+                                       _p(cand_v, _f32p), _p(cs, _f32p), len(cand_r), default_imp_code,
+                                       _p(p, _i32p), _p(cols, _i32p), _p(byts, _u8p), _p(tbr, _i32p),
+                                       _p(tbc, _i32p), _p(tby, _u8p), C.byref(st))
+        if rc != 0:
+            raise RuntimeError("oracle synapto_step failed")
+        ns, nt = st.n_scattered, st.n_tiles
+        out = HostLayer(self.n_in, self.n_out, self.rank).set_scales(self.value_scale, self.output_scale)
+        out.load_csr(p, cols[:ns], bytes_=byts[:ns])
+        out.load_tiles(tbr[:nt], tbc[:nt], tby[:nt * 16])
+        stats = {f[0]: getattr(st, f[0]) for f in _SynStats._fields_}
+        return out, stats
+
+
+class RefLayer:
+    """The reference's own SparseLinearWeightsDelta, through ref_shim.cpp."""
+
+    def __init__(self, n_in, n_out, ptrs, cols, w, imp=None):
+        self.n_in, self.n_out = int(n_in), int(n_out)
+        R = reflib()
+        self._keep = [_c(ptrs, np.int32), _c(cols, np.int32), _c(w, np.float32)]
+        if imp is not None:
+            self._keep.append(_c(imp, np.float32))
+        self.h = R.ref_layer_new(self.n_in, self.n_out, _p(self._keep[0], _i32p), _p(self._keep[1], _i32p),
+                                 _p(self._keep[2], _f32p), _p(self._keep[3], _f32p) if imp is not None else None)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            reflib().ref_layer_free(self.h)
+            self.h = None
+
+    def set_scales(self, vs, os_=None, rank=1):
+        vs = _c(vs, np.float32)
+        osv = None if os_ is None else _c(os_, np.float32)
+        if reflib().ref_layer_set_scales(self.h, _p(vs, _f32p), _p(osv, _f32p), rank) != 0:
+            raise ValueError("bad scale rank")
+        return self
+
+    def put_tile(self, br, bc, tile16):
+        t = _c(tile16, np.uint8)
+        reflib().ref_layer_put_tile(self.h, int(br), int(bc), _p(t, _u8p))
+
+    def load_dense_codes(self, wc, ic):
+        wc, ic = _c(wc, np.uint8), _c(ic, np.uint8)
+        reflib().ref_layer_load_dense_codes(self.h, _p(wc, _u8p), _p(ic, _u8p))
+
+    def compact(self):
+        reflib().ref_layer_compact(self.h)
+
+    def export(self):
+        R = reflib()
+        nb = R.ref_layer_export(self.h, None, None, None, None)
+        n = R.ref_layer_nnz_scattered(self.h)
+        bs = np.zeros(self.n_in + 1, np.uint64)
+        es = np.zeros(self.n_in + 1, np.uint64)
+        idx = np.zeros(max(1, nb), np.uint8)
+        val = np.zeros(max(1, n), np.uint8)
+        R.ref_layer_export(self.h, _p(bs, _u64p), _p(es, _u64p), _p(idx, _u8p), _p(val, _u8p))
+        return bs, es, idx[:nb], val[:n]
+
+    def export_tiles(self):
+        R = reflib()
+        n = R.ref_layer_export_tiles(self.h, None, None, None)
+        br = np.zeros(max(1, n), np.int32)
+        bc = np.zeros(max(1, n), np.int32)
+        t = np.zeros(max(16, 16 * n), np.uint8)
+        R.ref_layer_export_tiles(self.h, _p(br, _i32p), _p(bc, _i32p), _p(t, _u8p))
+        return br[:n], bc[:n], t[:16 * n]
+
+    def combined(self):
+        R = reflib()
+        n = R.ref_layer_combined(self.h, None, None, None, None)
+        p = np.zeros(self.n_in + 1, np.int32)
+        ix = np.zeros(max(1, n), np.int32)
+        w = np.zeros(max(1, n), np.float32)
+        imp = np.zeros(max(1, n), np.float32)
+        R.ref_layer_combined(self.h, _p(p, _i32p), _p(ix, _i32p), _p(w, _f32p), _p(imp, _f32p))
+        return p, ix[:n], w[:n], imp[:n]
+
+    def forward_dense(self, x, threads=1):
+        x = _c(np.atleast_2d(x), np.float32)
+        y = np.zeros((x.shape[0], self.n_out), np.float32)
+        reflib().ref_forward_dense(self.h, _p(x, _f32p), x.shape[0], _p(y, _f32p), threads)
+        return y
+
+    def backward_dense(self, x, dy, threads=1):
+        x = _c(np.atleast_2d(x), np.float32)
+        dy = _c(np.atleast_2d(dy), np.float32)
+        dx = np.zeros_like(x)
+        ai = np.zeros(self.n_in, np.float32)
+        ag = np.zeros(self.n_out, np.float32)
+        reflib().ref_backward_dense(self.h, _p(x, _f32p), _p(dy, _f32p), x.shape[0], _p(dx, _f32p),
+                                    _p(ai, _f32p), _p(ag, _f32p), threads)
+        return dx, ai, ag
+
+    def forward_sparse(self, ptrs, idx, vals, batch, threads=1):
+        ptrs, idx, vals = _c(ptrs, np.int32), _c(idx, np.int32), _c(vals, np.float32)
+        y = np.zeros((batch, self.n_out), np.float32)
+        reflib().ref_forward_sparse(self.h, _p(ptrs, _i32p), _p(idx, _i32p), _p(vals, _f32p), batch,
+                                    _p(y, _f32p), threads)
+        return y
+
+    def backward_sparse(self, x, dptrs, didx, dvals, batch, threads=1):
+        x = _c(np.atleast_2d(x), np.float32)
+        dptrs, didx, dvals = _c(dptrs, np.int32), _c(didx, np.int32), _c(dvals, np.float32)
+        dx = np.zeros_like(x)
+        ai = np.zeros(self.n_in, np.float32)
+        ag = np.zeros(self.n_out, np.float32)
+        reflib().ref_backward_sparse(self.h, _p(x, _f32p), _p(dptrs, _i32p), _p(didx, _i32p), _p(dvals, _f32p),
+                                     batch, _p(dx, _f32p), _p(ai, _f32p), _p(ag, _f32p), threads)
+        return dx, ai, ag

@@ -1,0 +1,234 @@
+// ref_shim.cpp -- a thin extern "C" wrapper around the REFERENCE's own
+// header-only C++ (SimLeek/sili__new sili/lib/headers), compiled in place from
+// /root/reference by oracle/Makefile into oracle/_ref/libsili_ref.so.
+//
+// TEST INFRASTRUCTURE ONLY.  It exists to (a) pin the CPU restatement
+// (sili_oracle.cpp) against the reference's real arithmetic and structure and
+// write golden vectors (tests/golden/make_golden.py), and (b) time the
+// reference's own CPU path as bench.py's "reference" CPU baseline.  None of
+// the reference's source is copied here: the headers are #included from
+// where they lie.  The product never loads this library.
+#include "linear_disldo.hpp"
+#include "sisldo_ops.hpp"
+#include "delta_csr_memory.hpp"
+
+#include <cstdint>
+#include <cstring>
+#include <memory>
+#include <vector>
+
+using S = int;
+using COL = uint32_t;
+using Weights = SparseLinearWeightsDelta<S, FP4BiPacked, COL>;
+
+struct RefLayer {
+    Weights w;
+    int n_in = 0, n_out = 0;
+};
+
+static CSRInput<S, float> make_input(const int32_t *ptrs, const int32_t *idx, const float *vals,
+                                     int batch, int cols) {
+    // Same construction as sili/cpu_backend.cpp:540-551 (_numpy_to_csr_input).
+    CSRInput<S, float> csr;
+    const int nz = ptrs[batch];
+    csr.rows = batch;
+    csr.cols = cols;
+    csr.ptrs[0] = std::make_shared<std::vector<S>>(ptrs, ptrs + batch + 1);
+    csr.indices[0] = std::make_shared<std::vector<S>>(idx, idx + nz);
+    csr.values[0] = std::make_shared<std::vector<float>>(vals, vals + nz);
+    return csr;
+}
+
+extern "C" {
+
+uint8_t ref_fp4_encode(float v) { return fp4_encode_bits(v); }
+float ref_fp4_decode(uint8_t c) { return fp4_decode_bits(c); }
+float ref_fp4_table(uint8_t c) { return FP4_TABLE[c & 0xF]; }
+size_t ref_uleb_encode(uint32_t v, uint8_t *out) { return uleb128_encode<uint32_t>(v, out); }
+
+// Layer construction mirrors SparseLinearLayerImpl's constructor and
+// load_weights (sili/cpu_backend.cpp:375-447, 859-901).
+void *ref_layer_new(int n_in, int n_out, const int32_t *ptrs, const int32_t *idx,
+                    const float *w, const float *imp) {
+    auto *L = new RefLayer();
+    L->n_in = n_in;
+    L->n_out = n_out;
+    std::vector<S> p(ptrs, ptrs + n_in + 1);
+    const size_t nnz = size_t(p.back());
+    std::vector<S> ix(idx, idx + nnz);
+    std::vector<float> ww(w, w + nnz);
+    std::vector<float> ii(nnz, 0.0f);
+    if (imp) ii.assign(imp, imp + nnz);
+    L->w.connections = delta_csr_from_absolute<S, FP4BiPacked, COL>(
+        p, ix, ww, ii, size_t(n_in), size_t(n_out), nnz * 8 + 4096, nnz + 64);
+    L->w.block4.init(size_t(n_in), size_t(n_out));
+    L->w.out_degree.assign(size_t(n_out), 0);
+    for (S c : ix) ++L->w.out_degree[size_t(c)];
+    L->w.recompute_stats();
+    return L;
+}
+
+void ref_layer_free(void *h) { delete static_cast<RefLayer *>(h); }
+
+int ref_layer_set_scales(void *h, const float *vs, const float *os, int rank) {
+    auto *L = static_cast<RefLayer *>(h);
+    if (rank < 1 || size_t(rank) > Weights::SCALE_RANK_MAX) return -1;
+    L->w.scale_rank = size_t(rank);
+    L->w.value_scale.assign(size_t(L->n_in) * rank, 1.0f);
+    for (int r = 0; r < L->n_in; ++r)
+        for (int k = 0; k < rank; ++k) L->w.set_value_scale_raw_k(size_t(r), size_t(k), vs[r * rank + k]);
+    if (os) {
+        L->w.output_scale.assign(size_t(L->n_out) * rank, 1.0f);
+        for (int c = 0; c < L->n_out; ++c)
+            for (int k = 0; k < rank; ++k) L->w.set_output_scale_raw_k(size_t(c), size_t(k), os[c * rank + k]);
+    }
+    return 0;
+}
+
+// sili/cpu_backend.cpp:910-921 (load_dense_codes -> block4_load_dense).
+void ref_layer_load_dense_codes(void *h, const uint8_t *wc, const uint8_t *ic) {
+    auto *L = static_cast<RefLayer *>(h);
+    block4_load_dense<S, FP4BiPacked, COL>(L->w, wc, ic, size_t(L->n_in), size_t(L->n_out));
+}
+
+// Hand-placed tile, the way the reference's own tests build block4 fixtures
+// (tests/unit/test_disldo_block4_forward.cpp:34-45).
+void ref_layer_put_tile(void *h, int br, int bc, const uint8_t *tile16) {
+    auto *L = static_cast<RefLayer *>(h);
+    auto t = L->w.block4.get_or_create(uint32_t(br), uint32_t(bc));
+    for (uint32_t lj = 0; lj < 4; ++lj)
+        for (uint32_t li = 0; li < 4; ++li) t.at(li, lj) = tile16[lj * 4 + li];
+}
+
+void ref_layer_compact(void *h) {
+    auto *L = static_cast<RefLayer *>(h);
+    L->w.connections = compact<S, FP4BiPacked, COL>(L->w.connections);
+}
+
+// Scattered structure, compacted view: per-row byte/elem starts, the row
+// streams concatenated, value bytes concatenated.  Returns total index bytes.
+int64_t ref_layer_export(void *h, uint64_t *byte_start, uint64_t *elem_start, uint8_t *idx,
+                         uint8_t *val) {
+    auto *L = static_cast<RefLayer *>(h);
+    const auto &dc = L->w.connections;
+    const auto &Ly = dc.layout;
+    uint64_t bc = 0, ec = 0;
+    for (size_t r = 0; r < Ly.rows; ++r) {
+        const size_t bl = Ly.row_byte_len(r), n = Ly.row_nnz(r);
+        if (byte_start) byte_start[r] = bc;
+        if (elem_start) elem_start[r] = ec;
+        if (idx) std::memcpy(idx + bc, dc.indices_buf.data() + Ly.byte_start[r], bl);
+        if (val) std::memcpy(val + ec, dc.values._data->data() + Ly.elem_start[r], n);
+        bc += bl;
+        ec += n;
+    }
+    if (byte_start) byte_start[Ly.rows] = bc;
+    if (elem_start) elem_start[Ly.rows] = ec;
+    return int64_t(bc);
+}
+
+int64_t ref_layer_nnz_scattered(void *h) {
+    return int64_t(static_cast<RefLayer *>(h)->w.connections.nnz());
+}
+
+// Block4 store as a list of (br, bc, 16 unpacked slot bytes) in storage order.
+int64_t ref_layer_export_tiles(void *h, int32_t *br_out, int32_t *bc_out, uint8_t *tiles) {
+    auto *L = static_cast<RefLayer *>(h);
+    auto &B = L->w.block4;
+    int64_t k = 0;
+    for (size_t br = 0; br < B.block_layout.rows; ++br) {
+        auto cur = B.row_cursor(br);
+        const size_t n = B.block_layout.row_nnz(br);
+        for (size_t e = 0; e < n; ++e) {
+            const uint32_t bc = cur.advance();
+            if (br_out) br_out[k] = int32_t(br);
+            if (bc_out) bc_out[k] = int32_t(bc);
+            if (tiles) {
+                const auto t = B.find(uint32_t(br), bc);
+                for (uint32_t lj = 0; lj < 4; ++lj)
+                    for (uint32_t li = 0; li < 4; ++li) tiles[16 * k + lj * 4 + li] = t.at(li, lj);
+            }
+            ++k;
+        }
+    }
+    return k;
+}
+
+int64_t ref_layer_combined(void *h, int32_t *ptrs, int32_t *idx, float *w, float *imp) {
+    auto *L = static_cast<RefLayer *>(h);
+    std::vector<S> op, oi;
+    std::vector<float> ow, oimp;
+    delta_csr_combined_to_absolute<S, FP4BiPacked, COL>(L->w, op, oi, ow, oimp);
+    if (ptrs) std::memcpy(ptrs, op.data(), op.size() * sizeof(S));
+    if (idx) std::memcpy(idx, oi.data(), oi.size() * sizeof(S));
+    if (w) std::memcpy(w, ow.data(), ow.size() * sizeof(float));
+    if (imp) std::memcpy(imp, oimp.data(), oimp.size() * sizeof(float));
+    return int64_t(oi.size());
+}
+
+// sili/cpu_backend.cpp:475-492 (forward_dense): output zeroed, then accumulated.
+void ref_forward_dense(void *h, const float *x, int batch, float *y, int threads) {
+    auto *L = static_cast<RefLayer *>(h);
+    std::memset(y, 0, sizeof(float) * size_t(batch) * size_t(L->n_out));
+    disldo_forward<S, FP4BiPacked, COL>(x, S(batch), S(L->n_in), L->w, y, threads);
+}
+
+// sili/cpu_backend.cpp:496-529 (backward_dense) at learning_rate = 0 with the
+// production policy constants.
+void ref_backward_dense(void *h, const float *x, const float *dy, int batch, float *dx,
+                        float *acc_in, float *acc_grad, int threads) {
+    auto *L = static_cast<RefLayer *>(h);
+    std::memset(dx, 0, sizeof(float) * size_t(batch) * size_t(L->n_in));
+    disldo_backward<S, FP4BiPacked, COL>(x, S(batch), S(L->n_in), dy, L->w, dx, acc_in, acc_grad,
+                                        0.0f, threads, false, true, 0.999f, 1e-8f, 0.9f, 0.0f,
+                                        2.0f, 100.0f);
+}
+
+// sili/cpu_backend.cpp:571-585 (forward_sparse).
+void ref_forward_sparse(void *h, const int32_t *ptrs, const int32_t *idx, const float *vals,
+                        int batch, float *y, int threads) {
+    auto *L = static_cast<RefLayer *>(h);
+    auto in = make_input(ptrs, idx, vals, batch, L->n_in);
+    std::memset(y, 0, sizeof(float) * size_t(batch) * size_t(L->n_out));
+    sisldo_forward<S, FP4BiPacked, COL>(in, L->w, y, threads);
+}
+
+// sili/cpu_backend.cpp:587-603 (backward_sparse) at learning_rate = 0.
+void ref_backward_sparse(void *h, const float *x, const int32_t *dptrs, const int32_t *didx,
+                         const float *dvals, int batch, float *dx, float *acc_in,
+                         float *acc_grad, int threads) {
+    auto *L = static_cast<RefLayer *>(h);
+    auto g = make_input(dptrs, didx, dvals, batch, L->n_out);
+    std::memset(dx, 0, sizeof(float) * size_t(batch) * size_t(L->n_in));
+    disldo_backward_sparse_grad<S, FP4BiPacked, COL>(x, S(batch), L->w, g, dx, acc_in, acc_grad,
+                                                    0.0f, threads, false, true, 0.999f, 1e-8f);
+}
+
+// Structural edits used by the synaptogenesis rules.
+int ref_row_remove_col(void *h, int row, int col) {
+    auto *L = static_cast<RefLayer *>(h);
+    return delta_csr_row_remove_col<S, FP4BiPacked, COL>(L->w.connections, size_t(row), COL(col)) ? 1 : 0;
+}
+int ref_row_insert_col(void *h, int row, int col, float w, float imp) {
+    auto *L = static_cast<RefLayer *>(h);
+    return delta_csr_row_insert_col<S, FP4BiPacked, COL>(L->w.connections, size_t(row), COL(col), w, imp) ? 1 : 0;
+}
+void ref_maybe_promote(void *h, int row, int col) {
+    auto *L = static_cast<RefLayer *>(h);
+    block4_maybe_promote<S, FP4BiPacked, COL>(L->w, size_t(row), COL(col));
+}
+void ref_demote_tile(void *h, int br, int bc) {
+    auto *L = static_cast<RefLayer *>(h);
+    block4_demote_tile<S, FP4BiPacked, COL>(L->w, uint32_t(br), uint32_t(bc));
+}
+// Zero one block4 slot (the prune half of delta_csr_memory.hpp:1203-1225);
+// returns the tile's live count afterwards, or -1 when the tile is absent.
+int ref_zero_tile_slot(void *h, int row, int col) {
+    auto *L = static_cast<RefLayer *>(h);
+    auto t = L->w.block4.find(uint32_t(row / 4), uint32_t(col / 4));
+    if (!t) return -1;
+    t.at(uint32_t(row % 4), uint32_t(col % 4)) = 0;
+    return int(t.count_live());
+}
+
+}  // extern "C"

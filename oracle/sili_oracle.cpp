@@ -1,0 +1,774 @@
+// sili_oracle.cpp -- CPU restatement of the reference's FP4 delta-CSR sparse
+// layer (TEST INFRASTRUCTURE ONLY: see sili_oracle.h).
+//
+// Written from the reference's documented semantics; each function names the
+// reference file:line it follows.  Parallel loops mirror the reference's
+// OpenMP structure (static row split, per-thread private outputs, serial
+// reduce -- linear_disldo.hpp:91-125) so the timed CPU baseline runs the same
+// algorithm the reference does.
+#include "sili_oracle.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <numeric>
+#include <vector>
+#include <omp.h>
+
+namespace {
+
+constexpr int TILE = 4;          // block4.hpp:15-27 (SILI_BLOCK4_TILE_SIZE)
+constexpr int TILE_SLOTS = 16;
+constexpr int PROMOTE_MIN_LIVE = 2;  // block4.hpp:19-21
+
+inline uint32_t f2u(float f) { uint32_t u; std::memcpy(&u, &f, 4); return u; }
+inline float u2f(uint32_t u) { float f; std::memcpy(&f, &u, 4); return f; }
+
+// fp4quant.hpp:68-84 -- E2M1, bias 1, code 8 repurposed as NaN 0x7FC00000.
+inline float fp4_dec(uint32_t code) {
+    const uint32_t s = (code >> 3) & 1u, e = (code >> 1) & 3u, m = code & 1u;
+    uint32_t bits;
+    if (e == 0) bits = m ? (0x3F000000u | (s << 31)) : (s ? 0x7FC00000u : 0u);
+    else        bits = (s << 31) | ((e + 126u) << 23) | (m << 22);
+    return u2f(bits);
+}
+
+// fp4quant.hpp:86-121 -- nearest, ties away from zero via the carry trick,
+// saturate at 6, NaN -> 0, |v| < 0.25 -> 0 (never the NaN slot).
+inline uint8_t fp4_enc(float v) {
+    const uint32_t bits = f2u(v);
+    const uint32_t sign = bits & 0x80000000u, a = bits & 0x7FFFFFFFu;
+    uint32_t mag;
+    if (a > 0x7F800000u) return 0;
+    if (a < 0x3E800000u) mag = 0;
+    else if (a < 0x3F400000u) mag = 1;
+    else if (a < 0x3F800000u) mag = 2;
+    else {
+        uint32_t r = a + (1u << 21);
+        if (r > 0x40C00000u) r = 0x40C00000u;
+        mag = (((r >> 23) & 0xFFu) - 126u) << 1 | ((r >> 22) & 1u);
+    }
+    if (mag == 0) return 0;
+    return uint8_t((sign ? 8u : 0u) | mag);
+}
+
+// delta_csr_types.hpp:217-241
+inline size_t uleb_enc(uint32_t v, uint8_t *out) {
+    size_t n = 0;
+    do {
+        uint8_t b = uint8_t(v & 0x7Fu);
+        v >>= 7;
+        if (v) b |= 0x80u;
+        out[n++] = b;
+    } while (v);
+    return n;
+}
+inline size_t uleb_len(uint32_t v) {
+    size_t n = 1;
+    while (v >= 0x80u) { v >>= 7; ++n; }
+    return n;
+}
+inline uint32_t uleb_dec(const uint8_t *buf, uint64_t &pos) {
+    uint32_t r = 0;
+    int sh = 0;
+    uint8_t b;
+    do {
+        b = buf[pos++];
+        r |= uint32_t(b & 0x7Fu) << sh;
+        sh += 7;
+    } while (b & 0x80u);
+    return r;
+}
+
+// delta_csr_types.hpp:1206-1240 -- S(r,c) = sum_k vs[r,k]*os[c,k], accumulated
+// from 0.  Components k >= 1 use the contracted (fma) form a -ffast-math
+// -march=native build of the reference produces; rank 1 is exact either way.
+inline float scale_rc(const OracleLayer *L, int64_t r, int64_t c) {
+    const int rk = L->rank;
+    float s = L->value_scale[r * rk] * L->output_scale[c * rk];
+    for (int k = 1; k < rk; ++k)
+        s = std::fma(L->value_scale[r * rk + k], L->output_scale[c * rk + k], s);
+    return s;
+}
+// Component-0-only scale (sisldo_ops.hpp:302-305, 527-531).
+inline float vs0(const OracleLayer *L, int64_t r) { return L->value_scale[r * L->rank]; }
+inline float os0(const OracleLayer *L, int64_t c) { return L->output_scale[c * L->rank]; }
+
+inline float maybe_abs(float v, int absmode) { return absmode ? std::fabs(v) : v; }
+
+struct TileRef { int64_t br, bc, t; };
+
+// Walk the block4 store row by row (block4.hpp:1103-1131, linear_disldo.hpp:164-197).
+std::vector<TileRef> collect_tiles(const OracleLayer *L) {
+    std::vector<TileRef> v;
+    if (L->n_tiles <= 0) return v;
+    v.reserve(size_t(L->n_tiles));
+    const int64_t brows = (L->n_in + TILE - 1) / TILE;
+    for (int64_t br = 0; br < brows; ++br) {
+        uint64_t pos = L->brow_byte_start[br];
+        uint32_t bc = 0;
+        for (uint64_t t = L->brow_tile_start[br]; t < L->brow_tile_start[br + 1]; ++t) {
+            bc += uleb_dec(L->bidx, pos);
+            v.push_back({br, int64_t(bc), int64_t(t)});
+        }
+    }
+    return v;
+}
+
+int nthreads_of(int threads) { return threads > 0 ? threads : 1; }
+
+}  // namespace
+
+extern "C" {
+
+float oracle_fp4_decode(uint8_t code) { return fp4_dec(code & 0xFu); }
+uint8_t oracle_fp4_encode(float v) { return fp4_enc(v); }
+void oracle_fp4_encode_array(const float *v, int64_t n, uint8_t *out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = fp4_enc(v[i]);
+}
+size_t oracle_uleb_encode(uint32_t v, uint8_t *out) { return uleb_enc(v, out); }
+uint32_t oracle_uleb_decode(const uint8_t *buf, uint64_t *pos) { return uleb_dec(buf, *pos); }
+
+int64_t oracle_csr_index_bytes(int64_t rows, const int32_t *ptrs, const int32_t *idx) {
+    int64_t total = 0;
+    for (int64_t r = 0; r < rows; ++r) {
+        uint32_t prev = 0;
+        for (int64_t i = ptrs[r]; i < ptrs[r + 1]; ++i) {
+            total += int64_t(uleb_len(uint32_t(idx[i]) - prev));
+            prev = uint32_t(idx[i]);
+        }
+    }
+    return total;
+}
+
+// delta_csr_memory.hpp:16-93 followed by sisldo_ops.hpp:44-96 (compact): the
+// compacted stream is the concatenation of each row's canonical ULEB bytes;
+// value bytes are (fp4_encode(w) << 4) | fp4_encode(imp).
+int oracle_csr_encode_bytes(int64_t rows, const int32_t *ptrs, const int32_t *idx,
+                            const uint8_t *bytes, uint64_t *row_byte_start,
+                            uint64_t *row_elem_start, uint8_t *idx_out,
+                            uint8_t *val_out) {
+    uint64_t bpos = 0;
+    for (int64_t r = 0; r < rows; ++r) {
+        row_byte_start[r] = bpos;
+        row_elem_start[r] = uint64_t(ptrs[r]);
+        uint32_t prev = 0;
+        for (int64_t i = ptrs[r]; i < ptrs[r + 1]; ++i) {
+            const uint32_t c = uint32_t(idx[i]);
+            if (i > ptrs[r] && c <= prev) return -1;  // strictly increasing required
+            bpos += uleb_enc(c - prev, idx_out + bpos);
+            prev = c;
+            val_out[i] = bytes[i];
+        }
+    }
+    row_byte_start[rows] = bpos;
+    row_elem_start[rows] = uint64_t(ptrs[rows]);
+    return 0;
+}
+
+int oracle_csr_encode(int64_t rows, const int32_t *ptrs, const int32_t *idx,
+                      const float *w, const float *imp, uint64_t *row_byte_start,
+                      uint64_t *row_elem_start, uint8_t *idx_out, uint8_t *val_out) {
+    const int64_t nnz = ptrs[rows];
+    std::vector<uint8_t> bytes(size_t(std::max<int64_t>(nnz, 1)));
+    for (int64_t i = 0; i < nnz; ++i)
+        bytes[size_t(i)] = uint8_t((fp4_enc(w[i]) << 4) | fp4_enc(imp ? imp[i] : 0.0f));
+    return oracle_csr_encode_bytes(rows, ptrs, idx, bytes.data(), row_byte_start,
+                                   row_elem_start, idx_out, val_out);
+}
+
+// delta_csr_memory.hpp:95-123 (delta_csr_to_absolute), columns only.
+int oracle_csr_decode(int64_t rows, const uint64_t *row_byte_start,
+                      const uint64_t *row_elem_start, const uint8_t *idx,
+                      int32_t *cols_out) {
+    for (int64_t r = 0; r < rows; ++r) {
+        uint64_t pos = row_byte_start[r];
+        uint32_t col = 0;
+        for (uint64_t e = row_elem_start[r]; e < row_elem_start[r + 1]; ++e) {
+            col += uleb_dec(idx, pos);
+            cols_out[e] = int32_t(col);
+        }
+        if (pos != row_byte_start[r + 1]) return -1;
+    }
+    return 0;
+}
+
+// delta_csr_memory.hpp:127-213 (delta_csr_combined_to_absolute): scattered
+// entries plus live (byte != 0) block4 slots, per row sorted by column.
+int64_t oracle_combined_to_absolute(const OracleLayer *L, int32_t *ptrs, int32_t *idx,
+                                    float *w, float *imp) {
+    struct E { uint32_t c; float w, imp; };
+    const auto tiles = collect_tiles(L);
+    // tiles grouped by block row, in bc order already
+    std::vector<size_t> tb((L->n_in + TILE - 1) / TILE + 1, 0);
+    for (const auto &t : tiles) tb[size_t(t.br) + 1]++;
+    for (size_t i = 1; i < tb.size(); ++i) tb[i] += tb[i - 1];
+    int64_t flat = 0;
+    if (ptrs) ptrs[0] = 0;
+    std::vector<E> row;
+    for (int64_t r = 0; r < L->n_in; ++r) {
+        row.clear();
+        uint64_t pos = L->row_byte_start[r];
+        uint32_t col = 0;
+        for (uint64_t e = L->row_elem_start[r]; e < L->row_elem_start[r + 1]; ++e) {
+            col += uleb_dec(L->idx, pos);
+            row.push_back({col, fp4_dec(L->val[e] >> 4), fp4_dec(L->val[e] & 0xFu)});
+        }
+        if (L->n_tiles > 0) {
+            const int64_t br = r / TILE, li = r % TILE;
+            for (size_t k = tb[size_t(br)]; k < tb[size_t(br) + 1]; ++k) {
+                const uint8_t *td = L->tiles + 16 * tiles[k].t;
+                for (int lj = 0; lj < TILE; ++lj) {
+                    const uint8_t b = td[lj * TILE + li];
+                    const int64_t c = tiles[k].bc * TILE + lj;
+                    if (b == 0 || c >= L->n_out) continue;
+                    row.push_back({uint32_t(c), fp4_dec(b & 0xFu), fp4_dec(b >> 4)});
+                }
+            }
+        }
+        std::stable_sort(row.begin(), row.end(), [](const E &a, const E &b) { return a.c < b.c; });
+        for (const auto &e : row) {
+            if (idx) idx[flat] = int32_t(e.c);
+            if (w) w[flat] = e.w;
+            if (imp) imp[flat] = e.imp;
+            ++flat;
+        }
+        if (ptrs) ptrs[r + 1] = int32_t(flat);
+    }
+    return flat;
+}
+
+void oracle_dense_weights(const OracleLayer *L, float *W) {
+    std::fill(W, W + L->n_in * L->n_out, 0.0f);
+    for (int64_t r = 0; r < L->n_in; ++r) {
+        uint64_t pos = L->row_byte_start[r];
+        uint32_t col = 0;
+        for (uint64_t e = L->row_elem_start[r]; e < L->row_elem_start[r + 1]; ++e) {
+            col += uleb_dec(L->idx, pos);
+            W[r * L->n_out + col] = fp4_dec(L->val[e] >> 4) * scale_rc(L, r, col);
+        }
+    }
+    for (const auto &t : collect_tiles(L)) {
+        const uint8_t *td = L->tiles + 16 * t.t;
+        for (int li = 0; li < TILE; ++li)
+            for (int lj = 0; lj < TILE; ++lj) {
+                const int64_t r = t.br * TILE + li, c = t.bc * TILE + lj;
+                if (r >= L->n_in || c >= L->n_out) continue;
+                W[r * L->n_out + c] = fp4_dec(td[lj * TILE + li] & 0xFu) * scale_rc(L, r, c);
+            }
+    }
+}
+
+// linear_disldo.hpp:68-345 (disldo_forward).  Scattered pass skips exact-zero
+// inputs (:114); block4 pass does 4-term dots per output column (:297-326).
+void oracle_forward_dense(const OracleLayer *L, const float *x, int64_t batch, float *y,
+                          int threads, int absmode) {
+    const int nt = nthreads_of(threads);
+    const int64_t n_in = L->n_in, n_out = L->n_out;
+    const size_t ost = size_t(batch * n_out);
+    std::vector<float> t_out(size_t(nt) * ost, 0.0f);
+#pragma omp parallel num_threads(nt)
+    {
+        float *mo = t_out.data() + size_t(omp_get_thread_num()) * ost;
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < n_in; ++r) {
+            uint64_t pos = L->row_byte_start[r];
+            uint32_t col = 0;
+            for (uint64_t e = L->row_elem_start[r]; e < L->row_elem_start[r + 1]; ++e) {
+                col += uleb_dec(L->idx, pos);
+                const float w = maybe_abs(fp4_dec(L->val[e] >> 4) * scale_rc(L, r, col), absmode);
+                for (int64_t b = 0; b < batch; ++b) {
+                    const float iv = maybe_abs(x[b * n_in + r], absmode);
+                    if (iv == 0.0f) continue;
+                    mo[b * n_out + col] += w * iv;
+                }
+            }
+        }
+    }
+    for (int t = 0; t < nt; ++t)
+        for (size_t i = 0; i < ost; ++i) y[i] += t_out[size_t(t) * ost + i];
+    if (L->n_tiles <= 0) return;
+    const auto tiles = collect_tiles(L);
+    std::fill(t_out.begin(), t_out.end(), 0.0f);
+#pragma omp parallel num_threads(nt)
+    {
+        float *mo = t_out.data() + size_t(omp_get_thread_num()) * ost;
+#pragma omp for schedule(static)
+        for (int64_t ti = 0; ti < int64_t(tiles.size()); ++ti) {
+            const auto &t = tiles[size_t(ti)];
+            const uint8_t *td = L->tiles + 16 * t.t;
+            for (int lj = 0; lj < TILE; ++lj) {
+                const int64_t col = t.bc * TILE + lj;
+                if (col >= n_out) continue;
+                float w4[TILE];
+                int64_t ri[TILE];
+                for (int li = 0; li < TILE; ++li) {
+                    const int64_t row = t.br * TILE + li;
+                    if (row < n_in) {
+                        w4[li] = maybe_abs(fp4_dec(td[lj * TILE + li] & 0xFu) * scale_rc(L, row, col), absmode);
+                        ri[li] = row;
+                    } else { w4[li] = 0.0f; ri[li] = 0; }
+                }
+                for (int64_t b = 0; b < batch; ++b) {
+                    float acc = 0.0f;
+                    for (int li = 0; li < TILE; ++li)
+                        acc += w4[li] * maybe_abs(x[b * n_in + ri[li]], absmode);
+                    mo[b * n_out + col] += acc;
+                }
+            }
+        }
+    }
+    for (int t = 0; t < nt; ++t)
+        for (size_t i = 0; i < ost; ++i) y[i] += t_out[size_t(t) * ost + i];
+}
+
+// linear_disldo.hpp:462-2113 at learning_rate == 0: accumulators (:515-520),
+// scattered dx (:884 with quant = stored code, cw = quant*S), block4 dx
+// (:1617/1662/1701), per-thread dx buffers reduced serially (:2044-2049).
+void oracle_backward_dense(const OracleLayer *L, const float *x, const float *dy,
+                           int64_t batch, float *dx, float *acc_in, float *acc_grad,
+                           int threads, int absmode) {
+    const int nt = nthreads_of(threads);
+    const int64_t n_in = L->n_in, n_out = L->n_out;
+    if (acc_in && acc_grad) {
+        for (int64_t b = 0; b < batch; ++b) {
+            for (int64_t r = 0; r < n_in; ++r) acc_in[r] += std::fabs(x[b * n_in + r]);
+            for (int64_t c = 0; c < n_out; ++c) acc_grad[c] += std::fabs(dy[b * n_out + c]);
+        }
+    }
+    const size_t dst = size_t(batch * n_in);
+    std::vector<float> t_dx(size_t(nt) * dst, 0.0f);
+    const auto tiles = collect_tiles(L);
+    std::vector<size_t> tb((n_in + TILE - 1) / TILE + 1, 0);
+    for (const auto &t : tiles) tb[size_t(t.br) + 1]++;
+    for (size_t i = 1; i < tb.size(); ++i) tb[i] += tb[i - 1];
+#pragma omp parallel num_threads(nt)
+    {
+        float *mdx = t_dx.data() + size_t(omp_get_thread_num()) * dst;
+#pragma omp for schedule(static)
+        for (int64_t r = 0; r < n_in; ++r) {
+            uint64_t pos = L->row_byte_start[r];
+            uint32_t col = 0;
+            for (uint64_t e = L->row_elem_start[r]; e < L->row_elem_start[r + 1]; ++e) {
+                col += uleb_dec(L->idx, pos);
+                const float cw = maybe_abs(fp4_dec(L->val[e] >> 4) * scale_rc(L, r, col), absmode);
+                for (int64_t b = 0; b < batch; ++b)
+                    mdx[b * n_in + r] += cw * maybe_abs(dy[b * n_out + col], absmode);
+            }
+        }
+        // block4 rows: per tile row li, 4-wide dot over lj (hsum of w*dy)
+#pragma omp for schedule(static)
+        for (int64_t br = 0; br < int64_t(tb.size()) - 1; ++br) {
+            for (size_t k = tb[size_t(br)]; k < tb[size_t(br) + 1]; ++k) {
+                const auto &t = tiles[k];
+                const uint8_t *td = L->tiles + 16 * t.t;
+                for (int li = 0; li < TILE; ++li) {
+                    const int64_t row = br * TILE + li;
+                    if (row >= n_in) continue;
+                    float w4[TILE];
+                    bool ok[TILE];
+                    for (int lj = 0; lj < TILE; ++lj) {
+                        const int64_t col = t.bc * TILE + lj;
+                        ok[lj] = col < n_out;
+                        w4[lj] = ok[lj] ? maybe_abs(fp4_dec(td[lj * TILE + li] & 0xFu) * scale_rc(L, row, col), absmode) : 0.0f;
+                    }
+                    for (int64_t b = 0; b < batch; ++b) {
+                        float hs = 0.0f;
+                        for (int lj = 0; lj < TILE; ++lj)
+                            if (ok[lj]) hs += w4[lj] * maybe_abs(dy[b * n_out + t.bc * TILE + lj], absmode);
+                        mdx[b * n_in + row] += hs;
+                    }
+                }
+            }
+        }
+    }
+    for (int t = 0; t < nt; ++t)
+        for (size_t i = 0; i < dst; ++i) dx[i] += t_dx[size_t(t) * dst + i];
+}
+
+// sisldo_ops.hpp:198-551 (sisldo_forward).  Scattered weights use
+// stored*(vs0*os0) (:302-306); block4 windows skip dead slots and use
+// (dec*vs0)*os0 (:527-531).  Inputs must be sorted within each batch row.
+void oracle_forward_sparse(const OracleLayer *L, const int32_t *ptrs, const int32_t *idx,
+                           const float *vals, int64_t batch, float *y, int threads,
+                           int absmode) {
+    const int nt = nthreads_of(threads);
+    const int64_t n_out = L->n_out;
+    const size_t ost = size_t(batch * n_out);
+    std::vector<float> t_out(size_t(nt) * ost, 0.0f);
+    // Scattered: per batch row, split the (active row, element) work evenly.
+#pragma omp parallel num_threads(nt)
+    {
+        float *mo = t_out.data() + size_t(omp_get_thread_num()) * ost;
+        for (int64_t b = 0; b < batch; ++b) {
+#pragma omp for schedule(static)
+            for (int64_t i = ptrs[b]; i < ptrs[b + 1]; ++i) {
+                const int64_t r = idx[i];
+                const float v = maybe_abs(vals[i], absmode);
+                uint64_t pos = L->row_byte_start[r];
+                uint32_t col = 0;
+                const float vsr = vs0(L, r);
+                for (uint64_t e = L->row_elem_start[r]; e < L->row_elem_start[r + 1]; ++e) {
+                    col += uleb_dec(L->idx, pos);
+                    const float w = maybe_abs(fp4_dec(L->val[e] >> 4) * (vsr * os0(L, col)), absmode);
+                    mo[b * n_out + col] += w * v;
+                }
+            }
+        }
+    }
+    for (int t = 0; t < nt; ++t)
+        for (size_t i = 0; i < ost; ++i) y[i] += t_out[size_t(t) * ost + i];
+    if (L->n_tiles <= 0) return;
+    const auto tiles = collect_tiles(L);
+    std::vector<size_t> tb((L->n_in + TILE - 1) / TILE + 1, 0);
+    for (const auto &t : tiles) tb[size_t(t.br) + 1]++;
+    for (size_t i = 1; i < tb.size(); ++i) tb[i] += tb[i - 1];
+    for (int64_t b = 0; b < batch; ++b) {
+        int64_t i = ptrs[b];
+        while (i < ptrs[b + 1]) {
+            const int64_t br = idx[i] / TILE, lo = br * TILE, hi = lo + TILE;
+            float local[TILE] = {0, 0, 0, 0};
+            int64_t j = i;
+            while (j < ptrs[b + 1] && idx[j] < hi) { local[idx[j] - lo] = maybe_abs(vals[j], absmode); ++j; }
+            for (size_t k = tb[size_t(br)]; k < tb[size_t(br) + 1]; ++k) {
+                const auto &t = tiles[k];
+                const uint8_t *td = L->tiles + 16 * t.t;
+                for (int lj = 0; lj < TILE; ++lj) {
+                    const int64_t col = t.bc * TILE + lj;
+                    if (col >= n_out) continue;
+                    float acc = 0.0f;
+                    for (int li = 0; li < TILE; ++li) {
+                        const int64_t row = br * TILE + li;
+                        if (row >= L->n_in) continue;
+                        const uint8_t byte = td[lj * TILE + li];
+                        if (byte == 0) continue;
+                        const float wt = maybe_abs(fp4_dec(byte & 0xFu) * vs0(L, row) * os0(L, col), absmode);
+                        acc += wt * local[li];
+                    }
+                    y[b * n_out + col] += acc;
+                }
+            }
+            i = j;
+        }
+    }
+}
+
+// sisldo_ops.hpp:589-1104 (disldo_backward_sparse_grad) at lr == 0: per row a
+// merge-join against the sorted sparse dy; weight = stored*(vs0*os0); block4
+// slots skip dy == 0 and use dec*vs0*os0.
+void oracle_backward_sparse(const OracleLayer *L, const float *x, const int32_t *dptrs,
+                            const int32_t *didx, const float *dvals, int64_t batch,
+                            float *dx, float *acc_in, float *acc_grad, int threads,
+                            int absmode) {
+    const int nt = nthreads_of(threads);
+    const int64_t n_in = L->n_in, n_out = L->n_out;
+    if (acc_in && acc_grad) {
+        for (int64_t b = 0; b < batch; ++b)
+            for (int64_t r = 0; r < n_in; ++r) acc_in[r] += std::fabs(x[b * n_in + r]);
+        for (int64_t b = 0; b < batch; ++b)
+            for (int64_t j = dptrs[b]; j < dptrs[b + 1]; ++j) acc_grad[didx[j]] += std::fabs(dvals[j]);
+    }
+    for (int64_t b = 0; b < batch; ++b) {
+        const int64_t og0 = dptrs[b], og1 = dptrs[b + 1];
+#pragma omp parallel for num_threads(nt) schedule(static)
+        for (int64_t r = 0; r < n_in; ++r) {
+            uint64_t pos = L->row_byte_start[r];
+            uint32_t col = 0;
+            int64_t og = og0;
+            float acc = 0.0f;
+            const float vsr = vs0(L, r);
+            for (uint64_t e = L->row_elem_start[r]; e < L->row_elem_start[r + 1]; ++e) {
+                col += uleb_dec(L->idx, pos);
+                const float w = maybe_abs(fp4_dec(L->val[e] >> 4) * (vsr * os0(L, col)), absmode);
+                while (og < og1 && didx[og] < int32_t(col)) ++og;
+                if (og >= og1 || didx[og] != int32_t(col)) continue;
+                acc += w * maybe_abs(dvals[og], absmode);
+            }
+            dx[b * n_in + r] += acc;
+        }
+    }
+    if (L->n_tiles <= 0) return;
+    const auto tiles = collect_tiles(L);
+    std::vector<size_t> tb((n_in + TILE - 1) / TILE + 1, 0);
+    for (const auto &t : tiles) tb[size_t(t.br) + 1]++;
+    for (size_t i = 1; i < tb.size(); ++i) tb[i] += tb[i - 1];
+    for (int64_t b = 0; b < batch; ++b) {
+        const int64_t og0 = dptrs[b], og1 = dptrs[b + 1];
+#pragma omp parallel for num_threads(nt) schedule(static)
+        for (int64_t br = 0; br < int64_t(tb.size()) - 1; ++br) {
+            float dxa[TILE] = {0, 0, 0, 0};
+            int64_t og = og0;
+            for (size_t k = tb[size_t(br)]; k < tb[size_t(br) + 1]; ++k) {
+                const auto &t = tiles[k];
+                const int64_t lo = t.bc * TILE, hi = lo + TILE;
+                while (og < og1 && didx[og] < lo) ++og;
+                float dl[TILE] = {0, 0, 0, 0};
+                bool any = false;
+                for (int64_t p = og; p < og1 && didx[p] < hi; ++p) { dl[didx[p] - lo] = maybe_abs(dvals[p], absmode); any = true; }
+                if (!any) continue;
+                const uint8_t *td = L->tiles + 16 * t.t;
+                for (int li = 0; li < TILE; ++li) {
+                    const int64_t row = br * TILE + li;
+                    if (row >= n_in) continue;
+                    for (int lj = 0; lj < TILE; ++lj) {
+                        if (dl[lj] == 0.0f) continue;
+                        const int64_t col = lo + lj;
+                        if (col >= n_out) continue;
+                        const float w = maybe_abs(fp4_dec(td[lj * TILE + li] & 0xFu) * vs0(L, row) * os0(L, col), absmode);
+                        dxa[li] += w * dl[lj];
+                    }
+                }
+            }
+            for (int li = 0; li < TILE; ++li)
+                if (br * TILE + li < n_in) dx[b * n_in + br * TILE + li] += dxa[li];
+        }
+    }
+}
+
+// Explicit nnz-sampled grad-W.  The reference never materialises it: it is
+// the g = dy*x consumed per (synapse, b) by disldo_backward's optimizer
+// (linear_disldo.hpp:811-882).  GW[e] = sum_b x[b,r(e)] * dy[b,c(e)].
+void oracle_sampled_gradw(const OracleLayer *L, const float *x, const float *dy,
+                          int64_t batch, float *gw_scattered, float *gw_tiles,
+                          int threads, int absmode) {
+    const int nt = nthreads_of(threads);
+    const int64_t n_in = L->n_in, n_out = L->n_out;
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (int64_t r = 0; r < n_in; ++r) {
+        uint64_t pos = L->row_byte_start[r];
+        uint32_t col = 0;
+        for (uint64_t e = L->row_elem_start[r]; e < L->row_elem_start[r + 1]; ++e) {
+            col += uleb_dec(L->idx, pos);
+            double s = 0.0;
+            for (int64_t b = 0; b < batch; ++b)
+                s += double(maybe_abs(x[b * n_in + r], absmode)) * double(maybe_abs(dy[b * n_out + col], absmode));
+            gw_scattered[e] = float(s);
+        }
+    }
+    if (L->n_tiles <= 0 || !gw_tiles) return;
+    const auto tiles = collect_tiles(L);
+#pragma omp parallel for num_threads(nt) schedule(static)
+    for (int64_t ti = 0; ti < int64_t(tiles.size()); ++ti) {
+        const auto &t = tiles[size_t(ti)];
+        for (int lj = 0; lj < TILE; ++lj)
+            for (int li = 0; li < TILE; ++li) {
+                const int64_t r = t.br * TILE + li, c = t.bc * TILE + lj;
+                double s = 0.0;
+                if (r < n_in && c < n_out)
+                    for (int64_t b = 0; b < batch; ++b)
+                        s += double(maybe_abs(x[b * n_in + r], absmode)) * double(maybe_abs(dy[b * n_out + c], absmode));
+                gw_tiles[16 * t.t + lj * TILE + li] = float(s);
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Bulk synaptogenesis (magnitude prune + candidate regrow).  The selection
+// policy is new (no reference equivalent); the structural rules follow the
+// reference:
+//   - removing a block4 slot zeroes its byte, and a tile whose live count
+//     drops below 2 is demoted to scattered (delta_csr_memory.hpp:1203-1225,
+//     949-999; demoted bytes requantize dec->enc, i.e. code 8 -> 0);
+//   - an insert whose 4x4 window already holds a tile writes into the tile
+//     (delta_csr_memory.hpp:620-646); otherwise it is a scattered insert, and a
+//     window that then holds >= 2 scattered synapses is promoted into a tile
+//     (delta_csr_memory.hpp:648-700).
+// Phase order: select -> prune -> demote -> insert -> promote -> rebuild.
+int oracle_synapto_step(const OracleLayer *L, float prune_frac, const int32_t *cand_r,
+                        const int32_t *cand_c, const float *cand_v, const float *cand_score,
+                        int64_t n_cand, int default_imp_code, int32_t *out_ptrs,
+                        int32_t *out_cols, uint8_t *out_bytes, int32_t *out_tile_br,
+                        int32_t *out_tile_bc, uint8_t *out_tile_bytes,
+                        OracleSynaptoStats *stats) {
+    const int64_t n_in = L->n_in, n_out = L->n_out;
+    struct Syn { uint32_t absw; int64_t r, c; int64_t where; };  // where>=0: scattered elem; <0: -(tile*16+slot)-1
+    std::vector<Syn> all;
+    // scattered
+    std::vector<int32_t> cols(size_t(L->row_elem_start[n_in]));
+    if (oracle_csr_decode(n_in, L->row_byte_start, L->row_elem_start, L->idx, cols.data()) != 0) return -1;
+    for (int64_t r = 0; r < n_in; ++r)
+        for (uint64_t e = L->row_elem_start[r]; e < L->row_elem_start[r + 1]; ++e) {
+            const int64_t c = cols[e];
+            const float w = fp4_dec(L->val[e] >> 4) * scale_rc(L, r, c);
+            all.push_back({f2u(w) & 0x7FFFFFFFu, r, c, int64_t(e)});
+        }
+    const auto tiles = collect_tiles(L);
+    std::vector<std::vector<uint8_t>> tdata(tiles.size(), std::vector<uint8_t>(16));
+    for (size_t k = 0; k < tiles.size(); ++k) {
+        std::memcpy(tdata[k].data(), L->tiles + 16 * tiles[k].t, 16);
+        for (int lj = 0; lj < TILE; ++lj)
+            for (int li = 0; li < TILE; ++li) {
+                const uint8_t b = tdata[k][lj * TILE + li];
+                const int64_t r = tiles[k].br * TILE + li, c = tiles[k].bc * TILE + lj;
+                if (b == 0 || r >= n_in || c >= n_out) continue;
+                const float w = fp4_dec(b & 0xFu) * scale_rc(L, r, c);
+                all.push_back({f2u(w) & 0x7FFFFFFFu, r, c, -(int64_t(k) * 16 + lj * TILE + li) - 1});
+            }
+    }
+    const int64_t N = int64_t(all.size());
+    const int64_t k_prune = std::min<int64_t>(N, int64_t(std::llround(double(prune_frac) * double(N))));
+    // k smallest by (|w| bits, r, c)
+    std::vector<size_t> order(all.size());
+    std::iota(order.begin(), order.end(), size_t(0));
+    auto less = [&](size_t a, size_t b) {
+        const Syn &x = all[a], &y = all[b];
+        if (x.absw != y.absw) return x.absw < y.absw;
+        if (x.r != y.r) return x.r < y.r;
+        return x.c < y.c;
+    };
+    if (k_prune > 0 && k_prune < N)
+        std::nth_element(order.begin(), order.begin() + k_prune, order.end(), less);
+    std::vector<char> s_removed(cols.size(), 0);
+    std::vector<char> tile_touched(tiles.size(), 0);
+    // pruned (r,c) set for the "not just-pruned" regrow rule
+    std::vector<std::pair<int64_t, int64_t>> pruned_rc;
+    for (int64_t i = 0; i < k_prune; ++i) {
+        const Syn &s = all[order[size_t(i)]];
+        pruned_rc.push_back({s.r, s.c});
+        if (s.where >= 0) s_removed[size_t(s.where)] = 1;
+        else {
+            const int64_t q = -s.where - 1;
+            tdata[size_t(q / 16)][size_t(q % 16)] = 0;
+            tile_touched[size_t(q / 16)] = 1;
+        }
+    }
+    std::sort(pruned_rc.begin(), pruned_rc.end());
+    // scattered survivors per row: map row -> sorted (col, byte)
+    std::vector<std::vector<std::pair<int64_t, uint8_t>>> rows{size_t(n_in)};
+    for (int64_t r = 0; r < n_in; ++r)
+        for (uint64_t e = L->row_elem_start[r]; e < L->row_elem_start[r + 1]; ++e)
+            if (!s_removed[e]) rows[size_t(r)].push_back({cols[e], L->val[e]});
+    // demote touched tiles with live < 2
+    std::vector<char> tile_alive(tiles.size(), 1);
+    int64_t n_demoted = 0;
+    auto requant = [](uint8_t code) -> uint8_t { return code == 8 ? 0 : code; };
+    for (size_t k = 0; k < tiles.size(); ++k) {
+        if (!tile_touched[k]) continue;
+        int live = 0;
+        for (int s = 0; s < 16; ++s) live += tdata[k][size_t(s)] != 0;
+        if (live >= PROMOTE_MIN_LIVE) continue;
+        tile_alive[k] = 0;
+        ++n_demoted;
+        for (int lj = 0; lj < TILE; ++lj)
+            for (int li = 0; li < TILE; ++li) {
+                const uint8_t b = tdata[k][size_t(lj * TILE + li)];
+                const int64_t r = tiles[k].br * TILE + li, c = tiles[k].bc * TILE + lj;
+                if (b == 0 || r >= n_in || c >= n_out) continue;
+                const uint8_t sb = uint8_t((requant(b & 0xFu) << 4) | requant(b >> 4));
+                auto &row = rows[size_t(r)];
+                row.insert(std::lower_bound(row.begin(), row.end(), std::make_pair(c, uint8_t(0))), {c, sb});
+            }
+    }
+    // tile lookup by window after demotion
+    auto win_key = [&](int64_t br, int64_t bc) { return br * ((n_out + TILE - 1) / TILE) + bc; };
+    std::vector<std::pair<int64_t, size_t>> tile_index;  // (window key, tile k)
+    for (size_t k = 0; k < tiles.size(); ++k)
+        if (tile_alive[k]) tile_index.push_back({win_key(tiles[k].br, tiles[k].bc), k});
+    std::sort(tile_index.begin(), tile_index.end());
+    auto find_tile = [&](int64_t br, int64_t bc) -> int64_t {
+        const int64_t key = win_key(br, bc);
+        auto it = std::lower_bound(tile_index.begin(), tile_index.end(), std::make_pair(key, size_t(0)));
+        if (it != tile_index.end() && it->first == key) return int64_t(it->second);
+        return -1;
+    };
+    auto stored = [&](int64_t r, int64_t c) -> bool {
+        const auto &row = rows[size_t(r)];
+        auto it = std::lower_bound(row.begin(), row.end(), std::make_pair(c, uint8_t(0)));
+        if (it != row.end() && it->first == c) return true;
+        const int64_t k = find_tile(r / TILE, c / TILE);
+        return k >= 0 && tdata[size_t(k)][size_t((c % TILE) * TILE + (r % TILE))] != 0;
+    };
+    // inserts: candidates in list order, first k_pruned valid ones
+    int64_t n_grown = 0;
+    std::vector<std::pair<int64_t, int64_t>> accepted;   // sorted set of accepted (r,c)
+    std::vector<int64_t> touched_windows;
+    for (int64_t i = 0; i < n_cand && n_grown < k_prune; ++i) {
+        const int64_t r = cand_r[i], c = cand_c[i];
+        if (r < 0 || r >= n_in || c < 0 || c >= n_out) continue;
+        if (std::binary_search(pruned_rc.begin(), pruned_rc.end(), std::make_pair(r, c))) continue;
+        if (std::binary_search(accepted.begin(), accepted.end(), std::make_pair(r, c))) continue;
+        if (stored(r, c)) continue;
+        accepted.insert(std::lower_bound(accepted.begin(), accepted.end(), std::make_pair(r, c)), {r, c});
+        ++n_grown;
+        const float S = scale_rc(L, r, c);
+        const uint8_t wc = fp4_enc(cand_v[i] / S);
+        const uint8_t ic = cand_score ? fp4_enc(cand_score[i]) : uint8_t(default_imp_code & 0xF);
+        const int64_t k = find_tile(r / TILE, c / TILE);
+        if (k >= 0) {
+            tdata[size_t(k)][size_t((c % TILE) * TILE + (r % TILE))] = uint8_t((ic << 4) | wc);
+        } else {
+            auto &row = rows[size_t(r)];
+            row.insert(std::lower_bound(row.begin(), row.end(), std::make_pair(c, uint8_t(0))),
+                       {c, uint8_t((wc << 4) | ic)});
+            touched_windows.push_back(win_key(r / TILE, c / TILE));
+        }
+    }
+    // promote windows that received a scattered insert and now hold >= 2
+    std::sort(touched_windows.begin(), touched_windows.end());
+    touched_windows.erase(std::unique(touched_windows.begin(), touched_windows.end()), touched_windows.end());
+    const int64_t bcols = (n_out + TILE - 1) / TILE;
+    struct NewTile { int64_t br, bc; uint8_t d[16]; };
+    std::vector<NewTile> new_tiles;
+    for (const int64_t key : touched_windows) {
+        const int64_t br = key / bcols, bc = key % bcols;
+        int cnt = 0;
+        for (int li = 0; li < TILE; ++li) {
+            const int64_t r = br * TILE + li;
+            if (r >= n_in) continue;
+            const auto &row = rows[size_t(r)];
+            for (const auto &e : row) if (e.first >= bc * TILE && e.first < bc * TILE + TILE) ++cnt;
+        }
+        if (cnt < PROMOTE_MIN_LIVE) continue;
+        NewTile nt{br, bc, {0}};
+        for (int li = 0; li < TILE; ++li) {
+            const int64_t r = br * TILE + li;
+            if (r >= n_in) continue;
+            auto &row = rows[size_t(r)];
+            std::vector<std::pair<int64_t, uint8_t>> keep;
+            for (const auto &e : row) {
+                if (e.first >= bc * TILE && e.first < bc * TILE + TILE) {
+                    const uint8_t b = e.second;
+                    nt.d[(e.first - bc * TILE) * TILE + li] = uint8_t(requant(b >> 4) | (requant(b & 0xFu) << 4));
+                } else keep.push_back(e);
+            }
+            row.swap(keep);
+        }
+        new_tiles.push_back(nt);
+    }
+    // rebuild outputs
+    int64_t flat = 0;
+    out_ptrs[0] = 0;
+    for (int64_t r = 0; r < n_in; ++r) {
+        for (const auto &e : rows[size_t(r)]) {
+            out_cols[flat] = int32_t(e.first);
+            out_bytes[flat] = e.second;
+            ++flat;
+        }
+        out_ptrs[r + 1] = int32_t(flat);
+    }
+    struct OutTile { int64_t br, bc; const uint8_t *d; };
+    std::vector<OutTile> ot;
+    for (size_t k = 0; k < tiles.size(); ++k)
+        if (tile_alive[k]) ot.push_back({tiles[k].br, tiles[k].bc, tdata[k].data()});
+    for (const auto &t : new_tiles) ot.push_back({t.br, t.bc, t.d});
+    std::sort(ot.begin(), ot.end(), [](const OutTile &a, const OutTile &b) {
+        return a.br != b.br ? a.br < b.br : a.bc < b.bc;
+    });
+    for (size_t k = 0; k < ot.size(); ++k) {
+        out_tile_br[k] = int32_t(ot[k].br);
+        out_tile_bc[k] = int32_t(ot[k].bc);
+        std::memcpy(out_tile_bytes + 16 * k, ot[k].d, 16);
+    }
+    if (stats) {
+        stats->n_prune_target = k_prune;
+        stats->n_pruned = k_prune;
+        stats->n_grown = n_grown;
+        stats->n_demoted_tiles = n_demoted;
+        stats->n_promoted_tiles = int64_t(new_tiles.size());
+        stats->n_scattered = flat;
+        stats->n_tiles = int64_t(ot.size());
+    }
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,136 @@
+/*
+ * sili_oracle.h -- CPU restatement of the reference's FP4 delta-CSR sparse
+ * layer arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (sili__new_amd/, the
+ * C-ABI library, bench.py's GPU leg) may link, load or call this code.  It
+ * is the checker for the HIP path (tests/, __graft_entry__.smoke()) and the
+ * timed CPU baseline in bench.py's cpu_baseline leg.
+ *
+ * Every function cites the reference file:line it restates (paths relative
+ * to the SimLeek/sili__new tree).  Pinning status of each function is listed
+ * in oracle/README.md.
+ *
+ * Layout conventions (reference semantics):
+ *   - rows of the weight matrix are INPUT neurons (linear_disldo.hpp:63-65);
+ *   - activations are [batch, n] row-major fp32 (linear_disldo.hpp:41-44);
+ *   - scattered value byte = (w_code << 4) | imp_code (fp4quant.hpp:280-383);
+ *   - block4 slot byte     = (imp_code << 4) | w_code, slot = lj*4 + li
+ *     (block4.hpp:300-312);
+ *   - column indices are ULEB128 deltas, first delta from 0 on every row
+ *     (delta_csr_memory.hpp:45-52,78-90).
+ */
+#ifndef SILI_ORACLE_H
+#define SILI_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Flat, compact (headroom-free) view of one layer. */
+typedef struct {
+    int64_t n_in, n_out;
+    int32_t rank;                   /* scale rank, 1..4 */
+    /* scattered delta-CSR */
+    const uint64_t *row_byte_start; /* [n_in+1] */
+    const uint64_t *row_elem_start; /* [n_in+1] */
+    const uint8_t  *idx;            /* ULEB128 column deltas */
+    const uint8_t  *val;            /* (w<<4)|imp, one byte per synapse */
+    /* block4 store (dense 16-byte tiles) */
+    int64_t n_tiles;
+    const uint64_t *brow_byte_start; /* [ceil(n_in/4)+1] or NULL when n_tiles==0 */
+    const uint64_t *brow_tile_start; /* [ceil(n_in/4)+1] */
+    const uint8_t  *bidx;            /* ULEB128 block-column deltas */
+    const uint8_t  *tiles;           /* 16 bytes per tile */
+    /* scales, row-major per component: vs[r*rank+k], os[c*rank+k] */
+    const float *value_scale;       /* [n_in*rank] */
+    const float *output_scale;      /* [n_out*rank] */
+} OracleLayer;
+
+/* ---- codecs ---- */
+float   oracle_fp4_decode(uint8_t code);
+uint8_t oracle_fp4_encode(float v);
+void    oracle_fp4_encode_array(const float *v, int64_t n, uint8_t *out);
+size_t  oracle_uleb_encode(uint32_t v, uint8_t *out);
+uint32_t oracle_uleb_decode(const uint8_t *buf, uint64_t *pos);
+
+/* ---- structure ---- */
+/* Byte count of the compact ULEB stream for an absolute CSR. */
+int64_t oracle_csr_index_bytes(int64_t rows, const int32_t *ptrs, const int32_t *idx);
+/* Absolute CSR -> compact delta-CSR.  w/imp are quantized with fp4_encode. */
+int oracle_csr_encode(int64_t rows, const int32_t *ptrs, const int32_t *idx,
+                      const float *w, const float *imp,
+                      uint64_t *row_byte_start, uint64_t *row_elem_start,
+                      uint8_t *idx_out, uint8_t *val_out);
+/* Same, from pre-built value bytes (no quantization). */
+int oracle_csr_encode_bytes(int64_t rows, const int32_t *ptrs, const int32_t *idx,
+                            const uint8_t *bytes,
+                            uint64_t *row_byte_start, uint64_t *row_elem_start,
+                            uint8_t *idx_out, uint8_t *val_out);
+/* Compact delta-CSR -> absolute columns (int32) in elem order. */
+int oracle_csr_decode(int64_t rows, const uint64_t *row_byte_start,
+                      const uint64_t *row_elem_start, const uint8_t *idx,
+                      int32_t *cols_out);
+
+/* Combined (scattered + block4 live slots) absolute CSR, per row sorted by
+ * column, decoded values (FP4_TABLE) -- delta_csr_memory.hpp:127-213.
+ * Returns total entries; call with NULL outputs to size. */
+int64_t oracle_combined_to_absolute(const OracleLayer *L, int32_t *ptrs,
+                                    int32_t *idx, float *w, float *imp);
+
+/* Dense true-weight matrix W[r*n_out+c] = dec(code)*S(r,c) (scattered
+ * association dec*(vs*os)); 0 where nothing is stored. */
+void oracle_dense_weights(const OracleLayer *L, float *W);
+
+/* ---- compute (lr = 0 semantics; outputs ACCUMULATE, caller zeroes) ----
+ * absmode != 0 replaces every weight and activation by its magnitude, giving
+ * the per-output sum of |terms| used by the condition-aware tolerance. */
+void oracle_forward_dense(const OracleLayer *L, const float *x, int64_t batch,
+                          float *y, int threads, int absmode);
+void oracle_backward_dense(const OracleLayer *L, const float *x, const float *dy,
+                           int64_t batch, float *dx, float *acc_in,
+                           float *acc_grad, int threads, int absmode);
+void oracle_forward_sparse(const OracleLayer *L, const int32_t *ptrs,
+                           const int32_t *idx, const float *vals, int64_t batch,
+                           float *y, int threads, int absmode);
+void oracle_backward_sparse(const OracleLayer *L, const float *x,
+                            const int32_t *dptrs, const int32_t *didx,
+                            const float *dvals, int64_t batch, float *dx,
+                            float *acc_in, float *acc_grad, int threads,
+                            int absmode);
+/* nnz-sampled grad-W, one value per stored synapse in storage order:
+ * gw_scattered[elem], gw_tiles[tile*16 + slot].  fp64 accumulation. */
+void oracle_sampled_gradw(const OracleLayer *L, const float *x, const float *dy,
+                          int64_t batch, float *gw_scattered, float *gw_tiles,
+                          int threads, int absmode);
+
+/* ---- bulk synaptogenesis step (magnitude prune + candidate regrow) ----
+ * Output capacities: scattered entries <= nnz + n_cand + 16*n_tiles,
+ * tiles <= n_tiles + n_cand.  Outputs are absolute: out_ptrs[n_in+1],
+ * out_cols/out_bytes (scattered, row-major, sorted), out_tile_br/bc sorted by
+ * (br,bc), out_tile_bytes 16 per tile. */
+typedef struct {
+    int64_t n_prune_target;
+    int64_t n_pruned;
+    int64_t n_grown;
+    int64_t n_demoted_tiles;
+    int64_t n_promoted_tiles;
+    int64_t n_scattered;
+    int64_t n_tiles;
+} OracleSynaptoStats;
+
+int oracle_synapto_step(const OracleLayer *L, float prune_frac,
+                        const int32_t *cand_r, const int32_t *cand_c,
+                        const float *cand_v, const float *cand_score,
+                        int64_t n_cand, int default_imp_code,
+                        int32_t *out_ptrs, int32_t *out_cols, uint8_t *out_bytes,
+                        int32_t *out_tile_br, int32_t *out_tile_bc,
+                        uint8_t *out_tile_bytes, OracleSynaptoStats *stats);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SILI_ORACLE_H */

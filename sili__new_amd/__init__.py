@@ -1,0 +1,29 @@
+"""sili__new_amd -- MI355X (gfx950) FP4 delta-CSR sparse linear layer.
+
+Drop-in for sili's `sili._cpu.SparseLinearLayer` hot path
+(SimLeek/sili__new sili/cpu_backend.cpp:349-984): same constructor, method
+names, argument meaning and exception types, with every compute call running
+in hand-written HIP kernels behind the C ABI in include/sili_hip.h.
+
+There is no CPU fallback: importing this package fails loudly when the HIP
+extension has not been built (python -m sili__new_amd.build).
+"""
+from __future__ import annotations
+
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+
+try:
+    from . import _sili_hip as _ext  # noqa: F401
+except ImportError as e:  # pragma: no cover - exercised only on an unbuilt tree
+    raise ImportError(
+        "sili__new_amd: the HIP extension is not built; run `python -m sili__new_amd.build` "
+        f"(looked in {_HERE}): {e}") from e
+
+SparseLinearLayer = _ext.SparseLinearLayer
+fp4_quantize_array = _ext.fp4_quantize_array
+
+LIB_PATH = os.path.join(_HERE, "libsili_hip.so")
+
+__all__ = ["SparseLinearLayer", "fp4_quantize_array", "LIB_PATH"]

@@ -1,0 +1,452 @@
+// build.hip -- device builders for the delta-CSR and block4 stores.
+//
+// Every store is (re)built on the GPU from row-sorted absolute entries:
+// per-entry ULEB128 lengths -> exclusive scan -> byte offsets -> encode, plus
+// the segment (decode work item) table.  The transposed shadow used by the
+// forward pass is a stable radix sort of the canonical entries by column
+// (rocprim), re-encoded the same way.  Load, load_dense_codes and every
+// synaptogenesis rebuild go through these routines, so a structure is a pure
+// function of its entry set -- the canonical encoding
+// (delta_csr_memory.hpp:16-93 + sisldo_ops.hpp:44-96).
+#include "layer.hpp"
+#include "wave.hpp"
+
+#include <algorithm>
+#include <cstring>  // host memset, needed before rocprim's headers
+
+#include <rocprim/rocprim.hpp>
+
+namespace sili {
+
+namespace {
+
+constexpr unsigned TPB = 256;
+inline unsigned nblk(int64_t n) { return (unsigned)((n + TPB - 1) / TPB); }
+
+__device__ __forceinline__ uint32_t row_of(const uint32_t *__restrict__ ptrs, int64_t rows, uint32_t i) {
+    // largest r with ptrs[r] <= i (ptrs non-decreasing, ptrs[0] = 0)
+    int64_t lo = 0, hi = rows - 1;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) >> 1;
+        if (ptrs[mid] <= i) lo = mid;
+        else hi = mid - 1;
+    }
+    return (uint32_t)lo;
+}
+
+// Per entry: ULEB length of its column delta; validates order and range.
+__global__ void k_entry_len(const uint32_t *__restrict__ ptrs, int64_t rows, int64_t ncols,
+                            const uint32_t *__restrict__ cols, int64_t N,
+                            uint64_t *__restrict__ len, uint32_t *__restrict__ rowid,
+                            int *__restrict__ bad) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= N) return;
+    const uint32_t r = row_of(ptrs, rows, (uint32_t)i);
+    const uint32_t c = cols[i];
+    const bool first = (uint32_t)i == ptrs[r];
+    const uint32_t prev = first ? 0u : cols[i - 1];
+    if ((int64_t)c >= ncols || (!first && c <= prev)) atomicOr(bad, 1);
+    len[i] = uleb_len(c - prev);
+    rowid[i] = r;
+}
+
+__global__ void k_entry_write(const uint32_t *__restrict__ ptrs, const uint32_t *__restrict__ rowid,
+                              const uint32_t *__restrict__ cols, int64_t N,
+                              const uint64_t *__restrict__ pos, uint8_t *__restrict__ idx) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= N) return;
+    const uint32_t r = rowid[i];
+    const uint32_t c = cols[i];
+    uint32_t v = ((uint32_t)i == ptrs[r]) ? c : c - cols[i - 1];
+    uint64_t p = pos[i];
+    do {
+        uint32_t b = v & 0x7Fu;
+        v >>= 7;
+        if (v) b |= 0x80u;
+        idx[p++] = (uint8_t)b;
+    } while (v);
+}
+
+__global__ void k_row_starts(const uint32_t *__restrict__ ptrs, int64_t rows, int64_t N,
+                             const uint64_t *__restrict__ pos, uint64_t total,
+                             uint32_t *__restrict__ byte_start, uint32_t *__restrict__ elem_start,
+                             uint32_t seg_len, int emit_empty, uint32_t *__restrict__ segcnt) {
+    const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (r > rows) return;
+    const uint32_t e = ptrs[r];
+    byte_start[r] = (uint32_t)(((int64_t)e < N) ? pos[e] : total);
+    elem_start[r] = e;
+    if (r < rows) {
+        const uint32_t n = ptrs[r + 1] - e;
+        segcnt[r] = n == 0u ? (emit_empty ? 1u : 0u) : (n + seg_len - 1u) / seg_len;
+    }
+}
+
+__global__ void k_seg_write(const uint32_t *__restrict__ ptrs, int64_t rows,
+                            const uint32_t *__restrict__ byte_start, const uint32_t *__restrict__ cols,
+                            const uint64_t *__restrict__ pos, const uint32_t *__restrict__ segoff,
+                            uint32_t seg_len, int emit_empty, SegDesc *__restrict__ seg,
+                            int *__restrict__ any_split) {
+    const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (r >= rows) return;
+    const uint32_t e0 = ptrs[r], e1 = ptrs[r + 1];
+    const uint32_t n = e1 - e0;
+    const uint32_t cnt = n == 0u ? (emit_empty ? 1u : 0u) : (n + seg_len - 1u) / seg_len;
+    if (cnt > 1u) atomicOr(any_split, 1);
+    for (uint32_t j = 0; j < cnt; ++j) {
+        SegDesc d;
+        const uint32_t eb = e0 + j * seg_len;
+        d.row = (uint32_t)r;
+        d.elem_begin = eb;
+        d.byte_begin = (j == 0u) ? byte_start[r] : (uint32_t)pos[eb];
+        d.byte_end = (j + 1u == cnt) ? byte_start[r + 1] : (uint32_t)pos[eb + seg_len];
+        d.base_col = (j == 0u) ? 0u : cols[eb - 1];
+        d.split = cnt > 1u ? 1u : 0u;
+        d.pad0 = d.pad1 = 0u;
+        seg[segoff[r] + j] = d;
+    }
+}
+
+// ptrs[r] = first index i with keys[i] >= r  (keys sorted ascending)
+__global__ void k_ptrs_from_sorted(const uint32_t *__restrict__ keys, int64_t N, int64_t rows,
+                                   uint32_t *__restrict__ ptrs) {
+    const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (r > rows) return;
+    int64_t lo = 0, hi = N;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if ((int64_t)keys[mid] < r) lo = mid + 1;
+        else hi = mid;
+    }
+    ptrs[r] = (uint32_t)lo;
+}
+
+__global__ void k_gather_u32(const uint32_t *__restrict__ src, const uint32_t *__restrict__ perm,
+                             int64_t N, uint32_t *__restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < N) dst[i] = src[perm[i]];
+}
+__global__ void k_gather_u8(const uint8_t *__restrict__ src, const uint32_t *__restrict__ perm,
+                            int64_t N, uint8_t *__restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < N) dst[i] = src[perm[i]];
+}
+__global__ void k_iota(uint32_t *__restrict__ v, int64_t N) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < N) v[i] = (uint32_t)i;
+}
+
+// Block4: key = major * minor_extent + minor.
+__global__ void k_tile_keys(const uint32_t *__restrict__ major, const uint32_t *__restrict__ minor,
+                            int64_t N, uint64_t minor_extent, int64_t major_extent,
+                            uint64_t *__restrict__ key, int *__restrict__ bad) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= N) return;
+    if ((int64_t)major[i] >= major_extent || (uint64_t)minor[i] >= minor_extent) atomicOr(bad, 1);
+    key[i] = (uint64_t)major[i] * minor_extent + minor[i];
+}
+__global__ void k_split_keys(const uint64_t *__restrict__ key, int64_t N, uint64_t minor_extent,
+                             uint32_t *__restrict__ major, uint32_t *__restrict__ minor,
+                             int *__restrict__ bad) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= N) return;
+    const uint64_t k = key[i];
+    if (i > 0 && key[i - 1] == k) atomicOr(bad, 2);  // duplicate tile
+    major[i] = (uint32_t)(k / minor_extent);
+    minor[i] = (uint32_t)(k % minor_extent);
+}
+// dst tile i = src tile perm[i], optionally 4x4-transposed (slot lj*4+li <-> li*4+lj).
+__global__ void k_gather_tiles(const uint8_t *__restrict__ src, const uint32_t *__restrict__ perm,
+                               int64_t N, int transpose, uint8_t *__restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= N) return;
+    const uint4 v = *reinterpret_cast<const uint4 *>(src + (size_t)perm[i] * 16u);
+    if (!transpose) {
+        *reinterpret_cast<uint4 *>(dst + (size_t)i * 16u) = v;
+        return;
+    }
+    uint8_t in[16], out[16];
+    *reinterpret_cast<uint4 *>(in) = v;
+#pragma unroll
+    for (int li = 0; li < 4; ++li)
+#pragma unroll
+        for (int lj = 0; lj < 4; ++lj) out[li * 4 + lj] = in[lj * 4 + li];
+    *reinterpret_cast<uint4 *>(dst + (size_t)i * 16u) = *reinterpret_cast<uint4 *>(out);
+}
+
+// Scattered weight code 8 (NaN) present?
+__global__ void k_scan_nan_codes(const uint8_t *__restrict__ v, int64_t N, int hi_nibble,
+                                 int *__restrict__ flag) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= N) return;
+    const uint32_t code = hi_nibble ? ((uint32_t)v[i] >> 4) : ((uint32_t)v[i] & 0xFu);
+    if (code == 8u) atomicOr(flag, 1);
+}
+
+void check_flag(Layer &L, int *d_flag, const char *what) {
+    int h = 0;
+    SILI_HIP(hipMemcpyAsync(&h, d_flag, sizeof(int), hipMemcpyDeviceToHost, L.stream));
+    SILI_HIP(hipStreamSynchronize(L.stream));
+    if (h) throw_error(1, std::string(what) + (h & 2 ? ": duplicate entries" : ": malformed input (unsorted, duplicate or out-of-range index)"));
+}
+
+void zero_flag(Layer &L) {
+    L.scratch.flag.ensure(4, 0);
+    SILI_HIP(hipMemsetAsync(L.scratch.flag.p, 0, 4 * sizeof(int), L.stream));
+}
+
+// Encode rows: ptrs[rows+1] (device u32), cols[N].  Fills byte_start,
+// elem_start, idx, seg of a store.
+struct Encoded {
+    int64_t nbytes = 0, nseg = 0;
+    bool has_split = false;
+};
+
+Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint32_t *d_ptrs,
+                    const uint32_t *d_cols, uint32_t seg_len, bool emit_empty,
+                    DevBuf<uint32_t> &byte_start, DevBuf<uint32_t> &elem_start, DevBuf<uint8_t> &idx,
+                    DevBuf<SegDesc> &seg, const char *what) {
+    Encoded out;
+    hipStream_t st = L.stream;
+    DevBuf<uint64_t> len, pos;
+    DevBuf<uint32_t> rowid, segcnt, segoff;
+    len.ensure((size_t)N + 1);
+    pos.ensure((size_t)N + 1);
+    rowid.ensure((size_t)N + 1);
+    zero_flag(L);
+    if (N > 0) {
+        hipLaunchKernelGGL(k_entry_len, dim3(nblk(N)), dim3(TPB), 0, st, d_ptrs, rows, ncols, d_cols, N,
+                           len.p, rowid.p, L.scratch.flag.p);
+        SILI_HIP(hipGetLastError());
+    }
+    check_flag(L, L.scratch.flag.p, what);
+    // pos = exclusive scan of len (N+1 entries: pos[N] = total)
+    SILI_HIP(hipMemsetAsync(len.p + N, 0, sizeof(uint64_t), st));
+    device_exclusive_scan_u64(L, len.p, pos.p, N + 1);
+    uint64_t total = 0;
+    SILI_HIP(hipMemcpyAsync(&total, pos.p + N, sizeof(uint64_t), hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipStreamSynchronize(st));
+    if (total >= (1ull << 32)) throw_error(2, std::string(what) + ": index stream exceeds 4 GiB");
+    out.nbytes = (int64_t)total;
+    idx.ensure((size_t)total + 64);
+    byte_start.ensure((size_t)rows + 1);
+    elem_start.ensure((size_t)rows + 1);
+    segcnt.ensure((size_t)rows + 1);
+    segoff.ensure((size_t)rows + 1);
+    if (N > 0) {
+        hipLaunchKernelGGL(k_entry_write, dim3(nblk(N)), dim3(TPB), 0, st, d_ptrs, rowid.p, d_cols, N,
+                           pos.p, idx.p);
+        SILI_HIP(hipGetLastError());
+    }
+    hipLaunchKernelGGL(k_row_starts, dim3(nblk(rows + 1)), dim3(TPB), 0, st, d_ptrs, rows, N, pos.p,
+                       total, byte_start.p, elem_start.p, seg_len, emit_empty ? 1 : 0, segcnt.p);
+    SILI_HIP(hipGetLastError());
+    SILI_HIP(hipMemsetAsync(segcnt.p + rows, 0, sizeof(uint32_t), st));
+    device_exclusive_scan_u32(L, segcnt.p, segoff.p, rows + 1);
+    uint32_t nseg = 0;
+    SILI_HIP(hipMemcpyAsync(&nseg, segoff.p + rows, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipStreamSynchronize(st));
+    out.nseg = nseg;
+    seg.ensure((size_t)nseg + 1);
+    zero_flag(L);
+    if (rows > 0) {
+        hipLaunchKernelGGL(k_seg_write, dim3(nblk(rows)), dim3(TPB), 0, st, d_ptrs, rows, byte_start.p,
+                           d_cols, pos.p, segoff.p, seg_len, emit_empty ? 1 : 0, seg.p, L.scratch.flag.p);
+        SILI_HIP(hipGetLastError());
+    }
+    int split = 0;
+    SILI_HIP(hipMemcpyAsync(&split, L.scratch.flag.p, sizeof(int), hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipStreamSynchronize(st));
+    out.has_split = split != 0;
+    return out;
+}
+
+}  // namespace
+
+// ---- rocprim wrappers -------------------------------------------------------
+void device_exclusive_scan_u64(Layer &L, const uint64_t *in, uint64_t *out, int64_t n) {
+    size_t bytes = 0;
+    SILI_HIP(rocprim::exclusive_scan(nullptr, bytes, in, out, uint64_t(0), (size_t)n,
+                                     rocprim::plus<uint64_t>(), L.stream));
+    L.scratch.temp.ensure(bytes + 16);
+    SILI_HIP(rocprim::exclusive_scan(L.scratch.temp.p, bytes, in, out, uint64_t(0), (size_t)n,
+                                     rocprim::plus<uint64_t>(), L.stream));
+}
+void device_exclusive_scan_u32(Layer &L, const uint32_t *in, uint32_t *out, int64_t n) {
+    size_t bytes = 0;
+    SILI_HIP(rocprim::exclusive_scan(nullptr, bytes, in, out, uint32_t(0), (size_t)n,
+                                     rocprim::plus<uint32_t>(), L.stream));
+    L.scratch.temp.ensure(bytes + 16);
+    SILI_HIP(rocprim::exclusive_scan(L.scratch.temp.p, bytes, in, out, uint32_t(0), (size_t)n,
+                                     rocprim::plus<uint32_t>(), L.stream));
+}
+void device_sort_pairs_u32(Layer &L, const uint32_t *kin, uint32_t *kout, const uint32_t *vin,
+                           uint32_t *vout, int64_t n, int bits) {
+    size_t bytes = 0;
+    SILI_HIP(rocprim::radix_sort_pairs(nullptr, bytes, kin, kout, vin, vout, (size_t)n, 0u,
+                                       (unsigned)bits, L.stream));
+    L.scratch.temp.ensure(bytes + 16);
+    SILI_HIP(rocprim::radix_sort_pairs(L.scratch.temp.p, bytes, kin, kout, vin, vout, (size_t)n, 0u,
+                                       (unsigned)bits, L.stream));
+}
+void device_sort_pairs_u64(Layer &L, const uint64_t *kin, uint64_t *kout, const uint32_t *vin,
+                           uint32_t *vout, int64_t n, int bits) {
+    size_t bytes = 0;
+    SILI_HIP(rocprim::radix_sort_pairs(nullptr, bytes, kin, kout, vin, vout, (size_t)n, 0u,
+                                       (unsigned)bits, L.stream));
+    L.scratch.temp.ensure(bytes + 16);
+    SILI_HIP(rocprim::radix_sort_pairs(L.scratch.temp.p, bytes, kin, kout, vin, vout, (size_t)n, 0u,
+                                       (unsigned)bits, L.stream));
+}
+
+static int bits_for(uint64_t max_value) {
+    int b = 1;
+    while (b < 64 && (max_value >> b) != 0) ++b;
+    return b;
+}
+
+void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64_t N,
+                     const uint32_t *d_ptrs, const uint32_t *d_cols, const uint8_t *d_bytes) {
+    const Encoded e = encode_rows(L, rows, ncols, N, d_ptrs, d_cols, L.seg_len, true, dst.byte_start,
+                                  dst.elem_start, dst.idx, dst.seg, "load_weights");
+    dst.rows = rows;
+    dst.cols = ncols;
+    dst.nnz = N;
+    dst.nbytes = e.nbytes;
+    dst.nseg = e.nseg;
+    dst.has_split = e.has_split;
+    dst.val.ensure((size_t)N + 64);
+    if (N > 0)
+        SILI_HIP(hipMemcpyAsync(dst.val.p, d_bytes, (size_t)N, hipMemcpyDeviceToDevice, L.stream));
+}
+
+void decode_scattered(Layer &L, uint32_t *d_rows, uint32_t *d_cols) {
+    const ScaleView none{nullptr, nullptr, 1};
+    launch_decode(L.W.plan(), none, reinterpret_cast<int32_t *>(d_cols), nullptr, d_rows, L.stream);
+}
+
+void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const uint32_t *d_cols,
+                  DScatter &dst) {
+    hipStream_t st = L.stream;
+    const int64_t N = src.nnz;
+    DevBuf<uint32_t> keys_out, perm_in, perm, trows, ptrs;
+    DevBuf<uint8_t> tbytes;
+    keys_out.ensure((size_t)N + 1);
+    perm_in.ensure((size_t)N + 1);
+    perm.ensure((size_t)N + 1);
+    trows.ensure((size_t)N + 1);
+    tbytes.ensure((size_t)N + 1);
+    ptrs.ensure((size_t)src.cols + 1);
+    if (N > 0) {
+        hipLaunchKernelGGL(k_iota, dim3(nblk(N)), dim3(TPB), 0, st, perm_in.p, N);
+        // stable by column: entries keep ascending row order within a column
+        device_sort_pairs_u32(L, d_cols, keys_out.p, perm_in.p, perm.p, N,
+                              bits_for((uint64_t)std::max<int64_t>(src.cols - 1, 1)));
+        hipLaunchKernelGGL(k_gather_u32, dim3(nblk(N)), dim3(TPB), 0, st, d_rows, perm.p, N, trows.p);
+        hipLaunchKernelGGL(k_gather_u8, dim3(nblk(N)), dim3(TPB), 0, st, src.val.p, perm.p, N, tbytes.p);
+        SILI_HIP(hipGetLastError());
+    }
+    hipLaunchKernelGGL(k_ptrs_from_sorted, dim3(nblk(src.cols + 1)), dim3(TPB), 0, st, keys_out.p, N,
+                       src.cols, ptrs.p);
+    SILI_HIP(hipGetLastError());
+    const Encoded e = encode_rows(L, src.cols, src.rows, N, ptrs.p, trows.p, L.seg_len, true, dst.byte_start,
+                                  dst.elem_start, dst.idx, dst.seg, "shadow build");
+    dst.rows = src.cols;
+    dst.cols = src.rows;
+    dst.nnz = N;
+    dst.nbytes = e.nbytes;
+    dst.nseg = e.nseg;
+    dst.has_split = e.has_split;
+    dst.val.ensure((size_t)N + 64);
+    if (N > 0)
+        SILI_HIP(hipMemcpyAsync(dst.val.p, tbytes.p, (size_t)N, hipMemcpyDeviceToDevice, st));
+    SILI_HIP(hipStreamSynchronize(st));
+}
+
+// One orientation of block4 from tiles sorted by (major, minor).
+static void build_b4_orientation(Layer &L, DBlock4 &dst, int64_t N, int64_t brows, int64_t bcols,
+                                 int64_t rows, int64_t cols, const uint32_t *d_major,
+                                 const uint32_t *d_minor, const uint32_t *d_perm,
+                                 const uint8_t *d_src_tiles, bool transpose) {
+    hipStream_t st = L.stream;
+    DevBuf<uint32_t> ptrs;
+    ptrs.ensure((size_t)brows + 1);
+    hipLaunchKernelGGL(k_ptrs_from_sorted, dim3(nblk(brows + 1)), dim3(TPB), 0, st, d_major, N, brows,
+                       ptrs.p);
+    SILI_HIP(hipGetLastError());
+    const Encoded e = encode_rows(L, brows, bcols, N, ptrs.p, d_minor, L.seg_len_b4, false, dst.byte_start,
+                                  dst.tile_start, dst.idx, dst.seg, "block4 build");
+    dst.brows = brows;
+    dst.bcols = bcols;
+    dst.rows = rows;
+    dst.cols = cols;
+    dst.ntiles = N;
+    dst.nbytes = e.nbytes;
+    dst.nseg = e.nseg;
+    dst.has_split = e.has_split;
+    dst.tiles.ensure((size_t)N * 16u + 64);
+    if (N > 0) {
+        hipLaunchKernelGGL(k_gather_tiles, dim3(nblk(N)), dim3(TPB), 0, st, d_src_tiles, d_perm, N,
+                           transpose ? 1 : 0, dst.tiles.p);
+        SILI_HIP(hipGetLastError());
+    }
+}
+
+void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_t *d_bc,
+                  const uint8_t *d_tiles) {
+    hipStream_t st = L.stream;
+    const int64_t brows = (L.n_in + 3) / 4, bcols = (L.n_out + 3) / 4;
+    const int64_t N = n_tiles;
+    DevBuf<uint64_t> key, key_sorted;
+    DevBuf<uint32_t> perm_in, perm, major, minor;
+    key.ensure((size_t)N + 1);
+    key_sorted.ensure((size_t)N + 1);
+    perm_in.ensure((size_t)N + 1);
+    perm.ensure((size_t)N + 1);
+    major.ensure((size_t)N + 1);
+    minor.ensure((size_t)N + 1);
+    for (int orient = 0; orient < 2; ++orient) {
+        const bool canon = orient == 0;
+        const uint32_t *maj = canon ? d_br : d_bc;
+        const uint32_t *mnr = canon ? d_bc : d_br;
+        const int64_t maj_ext = canon ? brows : bcols, mnr_ext = canon ? bcols : brows;
+        zero_flag(L);
+        if (N > 0) {
+            hipLaunchKernelGGL(k_tile_keys, dim3(nblk(N)), dim3(TPB), 0, st, maj, mnr, N,
+                               (uint64_t)mnr_ext, maj_ext, key.p, L.scratch.flag.p);
+            hipLaunchKernelGGL(k_iota, dim3(nblk(N)), dim3(TPB), 0, st, perm_in.p, N);
+            SILI_HIP(hipGetLastError());
+            device_sort_pairs_u64(L, key.p, key_sorted.p, perm_in.p, perm.p, N,
+                                  bits_for((uint64_t)maj_ext * (uint64_t)mnr_ext));
+            hipLaunchKernelGGL(k_split_keys, dim3(nblk(N)), dim3(TPB), 0, st, key_sorted.p, N,
+                               (uint64_t)mnr_ext, major.p, minor.p, L.scratch.flag.p);
+            SILI_HIP(hipGetLastError());
+        }
+        check_flag(L, L.scratch.flag.p, "block4 tiles");
+        if (canon)
+            build_b4_orientation(L, L.B4, N, brows, bcols, L.n_in, L.n_out, major.p, minor.p, perm.p,
+                                 d_tiles, false);
+        else
+            build_b4_orientation(L, L.B4t, N, bcols, brows, L.n_out, L.n_in, major.p, minor.p, perm.p,
+                                 d_tiles, true);
+    }
+    SILI_HIP(hipStreamSynchronize(st));
+}
+
+void refresh_nonfinite(Layer &L) {
+    hipStream_t st = L.stream;
+    zero_flag(L);
+    if (L.W.nnz > 0)
+        hipLaunchKernelGGL(k_scan_nan_codes, dim3(nblk(L.W.nnz)), dim3(TPB), 0, st, L.W.val.p, L.W.nnz, 1,
+                           L.scratch.flag.p);
+    if (L.B4.ntiles > 0)
+        hipLaunchKernelGGL(k_scan_nan_codes, dim3(nblk(L.B4.ntiles * 16)), dim3(TPB), 0, st, L.B4.tiles.p,
+                           L.B4.ntiles * 16, 0, L.scratch.flag.p);
+    SILI_HIP(hipGetLastError());
+    int h = 0;
+    SILI_HIP(hipMemcpyAsync(&h, L.scratch.flag.p, sizeof(int), hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipStreamSynchronize(st));
+    L.has_nonfinite = (h != 0) || L.nonfinite_scales;
+}
+
+}  // namespace sili

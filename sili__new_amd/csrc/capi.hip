@@ -1,0 +1,771 @@
+// capi.hip -- the extern "C" boundary (include/sili_hip.h) and the layer's
+// host-side orchestration of the kernels.
+#include "../../include/sili_hip.h"
+#include "layer.hpp"
+#include "wave.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+struct sili_layer {
+    sili::Layer L;
+};
+
+namespace sili {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void throw_error(int code, const std::string &msg) { throw Error{code, msg}; }
+
+void hip_check(hipError_t e, const char *what) {
+    if (e != hipSuccess) {
+        const int code = (e == hipErrorOutOfMemory) ? SILI_ERR_NOMEM : SILI_ERR_HIP;
+        throw Error{code, std::string("HIP error ") + hipGetErrorString(e) + " in " + what};
+    }
+}
+
+namespace {
+
+template <typename F>
+int guarded(F &&f) {
+    try {
+        f();
+        g_last_error.clear();
+        return SILI_OK;
+    } catch (const Error &e) {
+        g_last_error = e.msg;
+        return e.code;
+    } catch (const std::bad_alloc &) {
+        g_last_error = "out of host memory";
+        return SILI_ERR_NOMEM;
+    } catch (const std::exception &e) {
+        g_last_error = e.what();
+        return SILI_ERR_RUNTIME;
+    }
+}
+
+constexpr unsigned TPB = 256;
+inline unsigned nblk(int64_t n) { return (unsigned)((n + TPB - 1) / TPB); }
+
+__global__ void k_fill_f32(float *__restrict__ p, int64_t n, float v) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+__global__ void k_quantize(const float *__restrict__ w, const float *__restrict__ imp, int64_t n,
+                           uint8_t *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t wc = fp4_encode(w[i]);
+    const uint32_t ic = imp ? fp4_encode(imp[i]) : 0u;
+    out[i] = (uint8_t)((wc << 4) | ic);
+}
+
+__global__ void k_i32_to_u32(const int32_t *__restrict__ s, int64_t n, uint32_t *__restrict__ d) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n) d[i] = (uint32_t)s[i];
+}
+
+void fill(float *p, int64_t n, float v, hipStream_t st) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_fill_f32, dim3(nblk(n)), dim3(TPB), 0, st, p, n, v);
+    SILI_HIP(hipGetLastError());
+}
+
+void set_device(const Layer &L) { SILI_HIP(hipSetDevice(L.device)); }
+
+hipStream_t pick(const Layer &L, void *stream) {
+    return stream ? reinterpret_cast<hipStream_t>(stream) : L.stream;
+}
+
+template <typename T>
+void upload(DevBuf<T> &dst, const T *src, size_t n, hipStream_t st) {
+    dst.ensure(n);
+    if (n) SILI_HIP(hipMemcpyAsync(dst.p, src, n * sizeof(T), hipMemcpyHostToDevice, st));
+}
+
+// Canonical scales: rows index vs, entries index os.  Shadow: the reverse.
+ScaleView canon_scales(const Layer &L) {
+    if (L.rank == 1) return ScaleView{L.vs_ones ? nullptr : L.vs.p, L.os_ones ? nullptr : L.os.p, 1};
+    return ScaleView{L.vs.p, L.os.p, L.rank};
+}
+ScaleView shadow_scales(const Layer &L) {
+    if (L.rank == 1) return ScaleView{L.os_ones ? nullptr : L.os.p, L.vs_ones ? nullptr : L.vs.p, 1};
+    return ScaleView{L.os.p, L.vs.p, L.rank};
+}
+
+void rebuild_shadow(Layer &L) {
+    DevBuf<uint32_t> rows, cols;
+    rows.ensure((size_t)L.W.nnz + 1);
+    cols.ensure((size_t)L.W.nnz + 1);
+    decode_scattered(L, rows.p, cols.p);
+    build_shadow(L, L.W, rows.p, cols.p, L.Wt);
+}
+
+void build_from_host_csr(Layer &L, const int32_t *ptrs, const int32_t *idx, const uint8_t *bytes_h,
+                         const float *w_h, const float *imp_h, int64_t nnz) {
+    if (!ptrs) throw_error(SILI_ERR_INVALID, "load_weights: ptrs is NULL");
+    if (nnz < 0 || nnz >= (int64_t(1) << 31)) throw_error(SILI_ERR_INVALID, "load_weights: nnz out of range");
+    if (ptrs[0] != 0 || ptrs[L.n_in] != nnz)
+        throw_error(SILI_ERR_INVALID, "load_weights: ptrs[0] must be 0 and ptrs[n_inputs] must equal nnz");
+    for (int64_t r = 0; r < L.n_in; ++r)
+        if (ptrs[r + 1] < ptrs[r]) throw_error(SILI_ERR_INVALID, "load_weights: ptrs must be non-decreasing");
+    if (nnz > 0 && (!idx || (!bytes_h && !w_h)))
+        throw_error(SILI_ERR_INVALID, "load_weights: indices/values missing");
+    // reference budgets grow to fit a load (sili/cpu_backend.cpp:866-872)
+    L.idx_budget = std::max<int64_t>(L.idx_budget, nnz * 8 + 4096);
+    L.val_budget = std::max<int64_t>(L.val_budget, nnz + 64);
+    hipStream_t st = L.stream;
+    DevBuf<int32_t> dptrs_i, didx_i;
+    DevBuf<uint32_t> dptrs, dcols;
+    DevBuf<uint8_t> dbytes;
+    DevBuf<float> dw, dimp;
+    upload(dptrs_i, ptrs, (size_t)L.n_in + 1, st);
+    dptrs.ensure((size_t)L.n_in + 1);
+    hipLaunchKernelGGL(k_i32_to_u32, dim3(nblk(L.n_in + 1)), dim3(TPB), 0, st, dptrs_i.p, L.n_in + 1, dptrs.p);
+    dcols.ensure((size_t)nnz + 1);
+    dbytes.ensure((size_t)nnz + 1);
+    if (nnz > 0) {
+        upload(didx_i, idx, (size_t)nnz, st);
+        hipLaunchKernelGGL(k_i32_to_u32, dim3(nblk(nnz)), dim3(TPB), 0, st, didx_i.p, nnz, dcols.p);
+        if (bytes_h) {
+            SILI_HIP(hipMemcpyAsync(dbytes.p, bytes_h, (size_t)nnz, hipMemcpyHostToDevice, st));
+        } else {
+            upload(dw, w_h, (size_t)nnz, st);
+            if (imp_h) upload(dimp, imp_h, (size_t)nnz, st);
+            hipLaunchKernelGGL(k_quantize, dim3(nblk(nnz)), dim3(TPB), 0, st, dw.p, imp_h ? dimp.p : nullptr,
+                               nnz, dbytes.p);
+        }
+        SILI_HIP(hipGetLastError());
+    }
+    // negative indices become huge u32 values and fail the range check
+    build_scattered(L, L.W, L.n_in, L.n_out, nnz, dptrs.p, dcols.p, dbytes.p);
+    rebuild_shadow(L);
+    refresh_nonfinite(L);
+}
+
+void empty_stores(Layer &L) {
+    std::vector<int32_t> p((size_t)L.n_in + 1, 0);
+    build_from_host_csr(L, p.data(), nullptr, nullptr, nullptr, nullptr, 0);
+    build_block4(L, 0, nullptr, nullptr, nullptr);
+}
+
+void check_scales_finite(Layer &L, const std::vector<float> &vs, const std::vector<float> &os) {
+    bool bad = false;
+    for (float v : vs) bad |= !std::isfinite(v);
+    for (float v : os) bad |= !std::isfinite(v);
+    L.nonfinite_scales = bad;
+}
+
+void refresh_scale_flags(Layer &L) {
+    std::vector<float> vs((size_t)L.n_in * L.rank), os((size_t)L.n_out * L.rank);
+    SILI_HIP(hipMemcpyAsync(vs.data(), L.vs.p, vs.size() * 4, hipMemcpyDeviceToHost, L.stream));
+    SILI_HIP(hipMemcpyAsync(os.data(), L.os.p, os.size() * 4, hipMemcpyDeviceToHost, L.stream));
+    SILI_HIP(hipStreamSynchronize(L.stream));
+    L.vs_ones = L.rank == 1 && std::all_of(vs.begin(), vs.end(), [](float v) { return v == 1.0f; });
+    L.os_ones = L.rank == 1 && std::all_of(os.begin(), os.end(), [](float v) { return v == 1.0f; });
+    check_scales_finite(L, vs, os);
+    refresh_nonfinite(L);
+}
+
+void reset_scales(Layer &L) {
+    // component 0 defaults to 1, k >= 1 to 0 (delta_csr_types.hpp:1116-1121)
+    std::vector<float> vs((size_t)L.n_in * L.rank, 0.0f), os((size_t)L.n_out * L.rank, 0.0f);
+    for (int64_t r = 0; r < L.n_in; ++r) vs[(size_t)r * L.rank] = 1.0f;
+    for (int64_t c = 0; c < L.n_out; ++c) os[(size_t)c * L.rank] = 1.0f;
+    upload(L.vs, vs.data(), vs.size(), L.stream);
+    upload(L.os, os.data(), os.size(), L.stream);
+    SILI_HIP(hipStreamSynchronize(L.stream));
+    L.vs_ones = L.os_ones = (L.rank == 1);
+    L.nonfinite_scales = false;
+}
+
+// Feature-major copy of activations [B, n] -> [n, B] (B == 1: no copy).
+const float *to_feature_major(Layer &L, DevBuf<float> &ws, const float *x, int64_t B, int64_t n,
+                              float *acc, hipStream_t st) {
+    if (B == 1) {
+        if (acc) launch_colabs(x, 1, n, acc, st);
+        return x;
+    }
+    ws.ensure((size_t)(n * B));
+    launch_transpose(x, B, n, ws.p, acc, st);
+    return ws.p;
+}
+
+void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st) {
+    if (B <= 0) throw_error(SILI_ERR_INVALID, "forward_dense: batch must be >= 1");
+    if (!x || !y) throw_error(SILI_ERR_INVALID, "forward_dense: NULL buffer");
+    const float *xT = to_feature_major(L, L.ws_xT, x, B, L.n_in, nullptr, st);
+    if (L.Wt.has_split) fill(y, B * L.n_out, 0.0f, st);
+    // scattered pass skips exact-zero inputs (linear_disldo.hpp:114); only
+    // observable with non-finite weights, so the skip is compiled in only then
+    launch_gather(L.Wt.plan(), shadow_scales(L), xT, B, y, L.n_out, B,
+                  L.has_nonfinite ? SKIP_ZERO : SKIP_NONE, st);
+    if (L.B4t.ntiles > 0)
+        launch_gather_b4(L.B4t.plan(), shadow_scales(L), xT, B, y, L.n_out, B, SKIP_NONE, st);
+}
+
+void sampled_gradw(Layer &L, const float *xT, const float *gT, int64_t B, float *gw_s, float *gw_b,
+                   hipStream_t st) {
+    if (gw_s && L.W.nnz > 0) launch_sddmm(L.W.plan(), xT, gT, B, gw_s, st);
+    if (gw_b && L.B4.ntiles > 0) launch_sddmm_b4(L.B4.plan(), nullptr, xT, gT, B, gw_b, st);
+}
+
+void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float *dx, float *gw_s,
+                    float *gw_b, hipStream_t st) {
+    if (B <= 0) throw_error(SILI_ERR_INVALID, "backward_dense: batch must be >= 1");
+    if (!x || !dy || !dx) throw_error(SILI_ERR_INVALID, "backward_dense: NULL buffer");
+    const bool want_gw = gw_s || gw_b;
+    // accumulators always advance (linear_disldo.hpp:515-520)
+    const float *gT = to_feature_major(L, L.ws_gT, dy, B, L.n_out, L.acc_grad.p, st);
+    const float *xT = nullptr;
+    if (want_gw) xT = to_feature_major(L, L.ws_xT, x, B, L.n_in, L.acc_in.p, st);
+    else launch_colabs(x, B, L.n_in, L.acc_in.p, st);
+    if (L.W.has_split) fill(dx, B * L.n_in, 0.0f, st);
+    launch_gather(L.W.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
+    if (L.B4.ntiles > 0)
+        launch_gather_b4(L.B4.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
+    if (want_gw) sampled_gradw(L, xT, gT, B, gw_s, gw_b, st);
+}
+
+void forward_sparse(Layer &L, const int32_t *ptrs, const int32_t *idx, const float *vals, int64_t B,
+                    float *y, hipStream_t st) {
+    if (B <= 0) throw_error(SILI_ERR_INVALID, "forward_sparse: batch must be >= 1");
+    if (!ptrs || !y) throw_error(SILI_ERR_INVALID, "forward_sparse: NULL buffer");
+    L.ws_xT.ensure((size_t)(L.n_in * B));
+    fill(L.ws_xT.p, L.n_in * B, 0.0f, st);
+    launch_densify(ptrs, idx, vals, B, L.n_in, L.ws_xT.p, nullptr, true, st);
+    if (L.Wt.has_split) fill(y, B * L.n_out, 0.0f, st);
+    // only the active rows of each batch row contribute (sisldo_ops.hpp:271-313)
+    launch_gather(L.Wt.plan(), shadow_scales(L), L.ws_xT.p, B, y, L.n_out, B, SKIP_POSZERO, st);
+    if (L.B4t.ntiles > 0)
+        launch_gather_b4(L.B4t.plan(), shadow_scales(L), L.ws_xT.p, B, y, L.n_out, B, SKIP_POSZERO, st);
+}
+
+void backward_sparse(Layer &L, const float *x, const int32_t *dptrs, const int32_t *didx,
+                     const float *dvals, int64_t B, float *dx, hipStream_t st) {
+    if (B <= 0) throw_error(SILI_ERR_INVALID, "backward_sparse: batch must be >= 1");
+    if (!x || !dptrs || !dx) throw_error(SILI_ERR_INVALID, "backward_sparse: NULL buffer");
+    launch_colabs(x, B, L.n_in, L.acc_in.p, st);
+    L.ws_gT.ensure((size_t)(L.n_out * B));
+    fill(L.ws_gT.p, L.n_out * B, 0.0f, st);
+    launch_densify(dptrs, didx, dvals, B, L.n_out, L.ws_gT.p, L.acc_grad.p, true, st);
+    if (L.W.has_split) fill(dx, B * L.n_in, 0.0f, st);
+    // scattered: merge-join visits only present dy entries (sisldo_ops.hpp:705-713);
+    // block4: skips dy == 0 per slot (sisldo_ops.hpp:886-897)
+    launch_gather(L.W.plan(), canon_scales(L), L.ws_gT.p, B, dx, L.n_in, B, SKIP_POSZERO, st);
+    if (L.B4.ntiles > 0)
+        launch_gather_b4(L.B4.plan(), canon_scales(L), L.ws_gT.p, B, dx, L.n_in, B, SKIP_ZERO, st);
+}
+
+void export_block4_coords(Layer &L, std::vector<uint32_t> &br, std::vector<uint32_t> &bc) {
+    const int64_t n = L.B4.ntiles;
+    br.assign((size_t)n, 0);
+    bc.assign((size_t)n, 0);
+    if (n == 0) return;
+    DevBuf<uint32_t> dbr, dbc;
+    dbr.ensure((size_t)n);
+    dbc.ensure((size_t)n);
+    launch_decode_b4(L.B4.plan(), dbr.p, dbc.p, L.stream);
+    SILI_HIP(hipMemcpyAsync(br.data(), dbr.p, (size_t)n * 4, hipMemcpyDeviceToHost, L.stream));
+    SILI_HIP(hipMemcpyAsync(bc.data(), dbc.p, (size_t)n * 4, hipMemcpyDeviceToHost, L.stream));
+    SILI_HIP(hipStreamSynchronize(L.stream));
+}
+
+}  // namespace
+}  // namespace sili
+
+using namespace sili;
+
+extern "C" {
+
+const char *sili_last_error(void) { return g_last_error.c_str(); }
+
+int sili_create(int64_t n_inputs, int64_t n_outputs, int64_t max_weights, int device, sili_layer **out) {
+    return guarded([&] {
+        if (!out) throw_error(SILI_ERR_INVALID, "out is NULL");
+        *out = nullptr;
+        if (n_inputs <= 0 || n_outputs <= 0 || n_inputs >= (int64_t(1) << 31) || n_outputs >= (int64_t(1) << 31))
+            throw_error(SILI_ERR_INVALID, "n_inputs and n_outputs must be in [1, 2^31)");
+        if (max_weights < 0) throw_error(SILI_ERR_INVALID, "max_weights must be >= 0");
+        auto h = std::make_unique<sili_layer>();
+        Layer &L = h->L;
+        L.device = device;
+        set_device(L);
+        SILI_HIP(hipStreamCreateWithFlags(&L.stream, hipStreamNonBlocking));
+        L.n_in = n_inputs;
+        L.n_out = n_outputs;
+        L.max_weights = max_weights;
+        // budgets of sili/cpu_backend.cpp:371-373,391-393
+        L.idx_budget = max_weights * 8 + 4096;
+        L.val_budget = max_weights + 64;
+        L.tile_budget = std::max<int64_t>(4, max_weights / 16) * 16;
+        if (const char *e = std::getenv("SILI_SEG_LEN")) L.seg_len = (uint32_t)std::max(16, std::atoi(e));
+        if (const char *e = std::getenv("SILI_SEG_LEN_B4")) L.seg_len_b4 = (uint32_t)std::max(4, std::atoi(e));
+        reset_scales(L);
+        std::vector<float> ones_in((size_t)n_inputs, 1.0f), ones_out((size_t)n_outputs, 1.0f);
+        upload(L.is, ones_in.data(), ones_in.size(), L.stream);
+        upload(L.ois, ones_out.data(), ones_out.size(), L.stream);
+        L.acc_in.ensure((size_t)n_inputs);
+        L.acc_grad.ensure((size_t)n_outputs);
+        fill(L.acc_in.p, n_inputs, 0.0f, L.stream);
+        fill(L.acc_grad.p, n_outputs, 0.0f, L.stream);
+        empty_stores(L);
+        SILI_HIP(hipStreamSynchronize(L.stream));
+        *out = h.release();
+    });
+}
+
+void sili_destroy(sili_layer *layer) {
+    if (!layer) return;
+    (void)hipSetDevice(layer->L.device);
+    (void)hipStreamSynchronize(layer->L.stream);
+    hipStream_t s = layer->L.stream;
+    delete layer;
+    if (s) (void)hipStreamDestroy(s);
+}
+
+int sili_synchronize(sili_layer *layer) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        SILI_HIP(hipStreamSynchronize(layer->L.stream));
+    });
+}
+
+void *sili_stream(sili_layer *layer) { return layer ? reinterpret_cast<void *>(layer->L.stream) : nullptr; }
+
+int sili_load_weights(sili_layer *layer, const int32_t *ptrs, const int32_t *indices, const float *vals,
+                      const float *imp, int64_t nnz) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        build_from_host_csr(layer->L, ptrs, indices, nullptr, vals, imp, nnz);
+    });
+}
+
+int sili_load_weight_bytes(sili_layer *layer, const int32_t *ptrs, const int32_t *indices,
+                           const uint8_t *bytes, int64_t nnz) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        if (nnz > 0 && !bytes) throw_error(SILI_ERR_INVALID, "bytes is NULL");
+        std::vector<uint8_t> dummy(1, 0);
+        build_from_host_csr(layer->L, ptrs, indices, nnz > 0 ? bytes : dummy.data(), nullptr, nullptr, nnz);
+    });
+}
+
+int sili_load_dense_codes(sili_layer *layer, const uint8_t *wc, const uint8_t *ic) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        if (!wc || !ic) throw_error(SILI_ERR_INVALID, "code arrays are NULL");
+        Layer &L = layer->L;
+        set_device(L);
+        const int64_t brows = (L.n_in + 3) / 4, bcols = (L.n_out + 3) / 4;
+        const int64_t n = brows * bcols;
+        std::vector<uint32_t> br((size_t)n), bc((size_t)n);
+        std::vector<uint8_t> tiles((size_t)n * 16, 0);
+        // delta_csr_memory.hpp:884-911: every 4x4 block becomes a tile,
+        // slot byte = w | (imp << 4)
+        for (int64_t i = 0; i < brows; ++i)
+            for (int64_t j = 0; j < bcols; ++j) {
+                const int64_t t = i * bcols + j;
+                br[(size_t)t] = (uint32_t)i;
+                bc[(size_t)t] = (uint32_t)j;
+                for (int li = 0; li < 4; ++li)
+                    for (int lj = 0; lj < 4; ++lj) {
+                        const int64_t r = i * 4 + li, c = j * 4 + lj;
+                        if (r >= L.n_in || c >= L.n_out) continue;
+                        const size_t k = (size_t)(r * L.n_out + c);
+                        tiles[(size_t)t * 16 + (size_t)(lj * 4 + li)] = (uint8_t)(wc[k] | (ic[k] << 4));
+                    }
+            }
+        DevBuf<uint32_t> dbr, dbc;
+        DevBuf<uint8_t> dt;
+        upload(dbr, br.data(), br.size(), L.stream);
+        upload(dbc, bc.data(), bc.size(), L.stream);
+        upload(dt, tiles.data(), tiles.size(), L.stream);
+        build_block4(L, n, dbr.p, dbc.p, dt.p);
+        refresh_nonfinite(L);
+    });
+}
+
+int sili_load_block4_tiles(sili_layer *layer, const int32_t *br, const int32_t *bc, const uint8_t *tile_bytes,
+                           int64_t n_tiles) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        Layer &L = layer->L;
+        set_device(L);
+        if (n_tiles < 0 || n_tiles >= (int64_t(1) << 31)) throw_error(SILI_ERR_INVALID, "n_tiles out of range");
+        if (n_tiles > 0 && (!br || !bc || !tile_bytes)) throw_error(SILI_ERR_INVALID, "tile arrays are NULL");
+        if (n_tiles * 16 > L.tile_budget)
+            throw_error(SILI_ERR_NOMEM, "block4 tiles exceed the layer's tile budget (max(4, max_weights/16)*16 bytes)");
+        std::vector<uint32_t> ubr((size_t)n_tiles), ubc((size_t)n_tiles);
+        for (int64_t i = 0; i < n_tiles; ++i) {
+            if (br[i] < 0 || bc[i] < 0) throw_error(SILI_ERR_INVALID, "negative tile coordinate");
+            ubr[(size_t)i] = (uint32_t)br[i];
+            ubc[(size_t)i] = (uint32_t)bc[i];
+        }
+        DevBuf<uint32_t> dbr, dbc;
+        DevBuf<uint8_t> dt;
+        upload(dbr, ubr.data(), ubr.size(), L.stream);
+        upload(dbc, ubc.data(), ubc.size(), L.stream);
+        upload(dt, tile_bytes, (size_t)n_tiles * 16, L.stream);
+        build_block4(L, n_tiles, dbr.p, dbc.p, dt.p);
+        refresh_nonfinite(L);
+    });
+}
+
+int sili_set_scale_rank(sili_layer *layer, int rank) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        // sili/cpu_backend.cpp:455-461
+        if (rank < 1) throw_error(SILI_ERR_INVALID, "scale_rank must be >= 1");
+        if (rank > 4) throw_error(SILI_ERR_INVALID, "scale_rank exceeds SCALE_RANK_MAX (4)");
+        Layer &L = layer->L;
+        set_device(L);
+        L.rank = rank;
+        reset_scales(L);
+        refresh_nonfinite(L);
+    });
+}
+
+int sili_get_scale_rank(const sili_layer *layer) { return layer ? layer->L.rank : 0; }
+
+static int set_scale_impl(sili_layer *layer, const float *v, int which) {
+    return guarded([&] {
+        if (!layer || !v) throw_error(SILI_ERR_INVALID, "NULL argument");
+        Layer &L = layer->L;
+        set_device(L);
+        switch (which) {
+            case 0: upload(L.vs, v, (size_t)(L.n_in * L.rank), L.stream); break;
+            case 1:
+                upload(L.os, v, (size_t)(L.n_out * L.rank), L.stream);
+                L.output_scale_trainable = true;
+                break;
+            case 2: upload(L.is, v, (size_t)L.n_in, L.stream); break;
+            default: upload(L.ois, v, (size_t)L.n_out, L.stream); break;
+        }
+        if (which <= 1) refresh_scale_flags(L);
+        else SILI_HIP(hipStreamSynchronize(L.stream));
+    });
+}
+
+int sili_set_value_scale(sili_layer *layer, const float *vs) { return set_scale_impl(layer, vs, 0); }
+int sili_set_output_scale(sili_layer *layer, const float *os) { return set_scale_impl(layer, os, 1); }
+int sili_set_importance_scale(sili_layer *layer, const float *is) { return set_scale_impl(layer, is, 2); }
+int sili_set_output_importance_scale(sili_layer *layer, const float *ois) { return set_scale_impl(layer, ois, 3); }
+
+static int get_scale_impl(const sili_layer *layer, float *out, bool value) {
+    return guarded([&] {
+        if (!layer || !out) throw_error(SILI_ERR_INVALID, "NULL argument");
+        const Layer &L = layer->L;
+        set_device(L);
+        const size_t n = (size_t)((value ? L.n_in : L.n_out) * L.rank);
+        SILI_HIP(hipMemcpyAsync(out, value ? L.vs.p : L.os.p, n * 4, hipMemcpyDeviceToHost, L.stream));
+        SILI_HIP(hipStreamSynchronize(L.stream));
+    });
+}
+int sili_get_value_scale(const sili_layer *layer, float *vs) { return get_scale_impl(layer, vs, true); }
+int sili_get_output_scale(const sili_layer *layer, float *os) { return get_scale_impl(layer, os, false); }
+
+int sili_forward_dense(sili_layer *layer, const float *x, int64_t batch, float *y, void *stream) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        forward_dense(layer->L, x, batch, y, pick(layer->L, stream));
+    });
+}
+
+int sili_backward_dense(sili_layer *layer, const float *x, const float *dy, int64_t batch, float *dx,
+                        float *gw_s, float *gw_b, float learning_rate, void *stream) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        if (learning_rate != 0.0f)
+            throw_error(SILI_ERR_INVALID, "backward_dense: only learning_rate == 0 is implemented on the GPU path");
+        set_device(layer->L);
+        backward_dense(layer->L, x, dy, batch, dx, gw_s, gw_b, pick(layer->L, stream));
+    });
+}
+
+int sili_sampled_gradw(sili_layer *layer, const float *x, const float *dy, int64_t batch, float *gw_s,
+                       float *gw_b, void *stream) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        Layer &L = layer->L;
+        if (batch <= 0 || !x || !dy) throw_error(SILI_ERR_INVALID, "sampled_gradw: bad arguments");
+        set_device(L);
+        hipStream_t st = pick(L, stream);
+        const float *xT = to_feature_major(L, L.ws_xT, x, batch, L.n_in, nullptr, st);
+        const float *gT = to_feature_major(L, L.ws_gT, dy, batch, L.n_out, nullptr, st);
+        sampled_gradw(L, xT, gT, batch, gw_s, gw_b, st);
+    });
+}
+
+int sili_forward_sparse(sili_layer *layer, const int32_t *ptrs, const int32_t *indices, const float *values,
+                        int64_t nnz_x, int64_t batch, float *y, void *stream) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        if (nnz_x < 0 || (nnz_x > 0 && (!indices || !values)))
+            throw_error(SILI_ERR_INVALID, "forward_sparse: bad CSR arguments");
+        set_device(layer->L);
+        forward_sparse(layer->L, ptrs, indices, values, batch, y, pick(layer->L, stream));
+    });
+}
+
+int sili_backward_sparse(sili_layer *layer, const float *x, const int32_t *dy_ptrs, const int32_t *dy_indices,
+                         const float *dy_values, int64_t nnz_dy, int64_t batch, float *dx, float learning_rate,
+                         void *stream) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        if (learning_rate != 0.0f)
+            throw_error(SILI_ERR_INVALID, "backward_sparse: only learning_rate == 0 is implemented on the GPU path");
+        if (nnz_dy < 0 || (nnz_dy > 0 && (!dy_indices || !dy_values)))
+            throw_error(SILI_ERR_INVALID, "backward_sparse: bad CSR arguments");
+        set_device(layer->L);
+        backward_sparse(layer->L, x, dy_ptrs, dy_indices, dy_values, batch, dx, pick(layer->L, stream));
+    });
+}
+
+int sili_synapto_step(sili_layer *layer, float prune_frac, const int32_t *cand_rows, const int32_t *cand_cols,
+                      const float *cand_vals, const float *cand_scores, int64_t n_cand, int default_imp_code,
+                      int64_t *out_stats) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        if (!(prune_frac >= 0.0f && prune_frac <= 1.0f)) throw_error(SILI_ERR_INVALID, "prune_frac must be in [0, 1]");
+        if (n_cand < 0 || (n_cand > 0 && (!cand_rows || !cand_cols || !cand_vals)))
+            throw_error(SILI_ERR_INVALID, "synapto_step: bad candidate arrays");
+        if (default_imp_code < 0 || default_imp_code > 15) throw_error(SILI_ERR_INVALID, "default_imp_code must be a 4-bit code");
+        set_device(layer->L);
+        synapto_step(layer->L, prune_frac, cand_rows, cand_cols, cand_vals, cand_scores, n_cand, default_imp_code,
+                     out_stats);
+    });
+}
+
+int sili_get_accumulators(sili_layer *layer, float *acc_in, float *acc_grad) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        Layer &L = layer->L;
+        set_device(L);
+        SILI_HIP(hipStreamSynchronize(L.stream));
+        if (acc_in) SILI_HIP(hipMemcpy(acc_in, L.acc_in.p, (size_t)L.n_in * 4, hipMemcpyDeviceToHost));
+        if (acc_grad) SILI_HIP(hipMemcpy(acc_grad, L.acc_grad.p, (size_t)L.n_out * 4, hipMemcpyDeviceToHost));
+    });
+}
+
+int sili_zero_accum(sili_layer *layer) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        Layer &L = layer->L;
+        set_device(L);
+        fill(L.acc_in.p, L.n_in, 0.0f, L.stream);
+        fill(L.acc_grad.p, L.n_out, 0.0f, L.stream);
+    });
+}
+
+int sili_get_info(sili_layer *layer, sili_info *out) {
+    return guarded([&] {
+        if (!layer || !out) throw_error(SILI_ERR_INVALID, "NULL argument");
+        Layer &L = layer->L;
+        set_device(L);
+        std::memset(out, 0, sizeof(*out));
+        out->n_inputs = L.n_in;
+        out->n_outputs = L.n_out;
+        out->nnz_scattered = L.W.nnz;
+        out->index_bytes = L.W.nbytes;
+        out->n_tiles = L.B4.ntiles;
+        out->block_index_bytes = L.B4.nbytes;
+        out->n_segments = L.W.nseg;
+        out->scale_rank = L.rank;
+        out->has_nonfinite = L.has_nonfinite ? 1 : 0;
+        if (L.B4.ntiles > 0) {
+            std::vector<uint32_t> br, bc;
+            export_block4_coords(L, br, bc);
+            std::vector<uint8_t> t((size_t)L.B4.ntiles * 16);
+            SILI_HIP(hipMemcpy(t.data(), L.B4.tiles.p, t.size(), hipMemcpyDeviceToHost));
+            int64_t live = 0;
+            for (size_t k = 0; k < br.size(); ++k)
+                for (int s = 0; s < 16; ++s) {
+                    const int64_t r = (int64_t)br[k] * 4 + (s & 3), c = (int64_t)bc[k] * 4 + (s >> 2);
+                    live += (t[k * 16 + (size_t)s] != 0 && r < L.n_in && c < L.n_out) ? 1 : 0;
+                }
+            out->live_block4 = live;
+        }
+    });
+}
+
+int sili_export_scattered(sili_layer *layer, uint64_t *row_byte_start, uint64_t *row_elem_start, uint8_t *idx,
+                          uint8_t *val) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        Layer &L = layer->L;
+        set_device(L);
+        SILI_HIP(hipStreamSynchronize(L.stream));
+        std::vector<uint32_t> tmp((size_t)L.n_in + 1);
+        if (row_byte_start) {
+            SILI_HIP(hipMemcpy(tmp.data(), L.W.byte_start.p, tmp.size() * 4, hipMemcpyDeviceToHost));
+            for (size_t i = 0; i < tmp.size(); ++i) row_byte_start[i] = tmp[i];
+        }
+        if (row_elem_start) {
+            SILI_HIP(hipMemcpy(tmp.data(), L.W.elem_start.p, tmp.size() * 4, hipMemcpyDeviceToHost));
+            for (size_t i = 0; i < tmp.size(); ++i) row_elem_start[i] = tmp[i];
+        }
+        if (idx && L.W.nbytes) SILI_HIP(hipMemcpy(idx, L.W.idx.p, (size_t)L.W.nbytes, hipMemcpyDeviceToHost));
+        if (val && L.W.nnz) SILI_HIP(hipMemcpy(val, L.W.val.p, (size_t)L.W.nnz, hipMemcpyDeviceToHost));
+    });
+}
+
+int sili_export_block4(sili_layer *layer, int32_t *br, int32_t *bc, uint8_t *tiles, uint64_t *brow_byte_start,
+                       uint64_t *brow_tile_start, uint8_t *bidx) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        Layer &L = layer->L;
+        set_device(L);
+        SILI_HIP(hipStreamSynchronize(L.stream));
+        if (br || bc) {
+            std::vector<uint32_t> ubr, ubc;
+            export_block4_coords(L, ubr, ubc);
+            for (size_t i = 0; i < ubr.size(); ++i) {
+                if (br) br[i] = (int32_t)ubr[i];
+                if (bc) bc[i] = (int32_t)ubc[i];
+            }
+        }
+        if (tiles && L.B4.ntiles)
+            SILI_HIP(hipMemcpy(tiles, L.B4.tiles.p, (size_t)L.B4.ntiles * 16, hipMemcpyDeviceToHost));
+        std::vector<uint32_t> tmp((size_t)L.B4.brows + 1);
+        if (brow_byte_start) {
+            SILI_HIP(hipMemcpy(tmp.data(), L.B4.byte_start.p, tmp.size() * 4, hipMemcpyDeviceToHost));
+            for (size_t i = 0; i < tmp.size(); ++i) brow_byte_start[i] = tmp[i];
+        }
+        if (brow_tile_start) {
+            SILI_HIP(hipMemcpy(tmp.data(), L.B4.tile_start.p, tmp.size() * 4, hipMemcpyDeviceToHost));
+            for (size_t i = 0; i < tmp.size(); ++i) brow_tile_start[i] = tmp[i];
+        }
+        if (bidx && L.B4.nbytes) SILI_HIP(hipMemcpy(bidx, L.B4.idx.p, (size_t)L.B4.nbytes, hipMemcpyDeviceToHost));
+    });
+}
+
+int sili_decode_scattered(sili_layer *layer, int32_t *cols, float *w_true) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        Layer &L = layer->L;
+        set_device(L);
+        const size_t n = (size_t)L.W.nnz;
+        if (n == 0) return;
+        DevBuf<int32_t> dc;
+        DevBuf<float> dw;
+        dc.ensure(n);
+        dw.ensure(n);
+        launch_decode(L.W.plan(), canon_scales(L), dc.p, dw.p, nullptr, L.stream);
+        SILI_HIP(hipStreamSynchronize(L.stream));
+        if (cols) SILI_HIP(hipMemcpy(cols, dc.p, n * 4, hipMemcpyDeviceToHost));
+        if (w_true) SILI_HIP(hipMemcpy(w_true, dw.p, n * 4, hipMemcpyDeviceToHost));
+    });
+}
+
+int sili_export_absolute(sili_layer *layer, int32_t *ptrs, int32_t *indices, float *w, float *imp,
+                         int64_t *n_out_entries) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        Layer &L = layer->L;
+        set_device(L);
+        const size_t n = (size_t)L.W.nnz;
+        std::vector<int32_t> cols(n);
+        std::vector<uint8_t> val(n);
+        std::vector<uint32_t> elem((size_t)L.n_in + 1);
+        if (n) {
+            DevBuf<int32_t> dc;
+            dc.ensure(n);
+            const ScaleView none{nullptr, nullptr, 1};
+            launch_decode(L.W.plan(), none, dc.p, nullptr, nullptr, L.stream);
+            SILI_HIP(hipStreamSynchronize(L.stream));
+            SILI_HIP(hipMemcpy(cols.data(), dc.p, n * 4, hipMemcpyDeviceToHost));
+            SILI_HIP(hipMemcpy(val.data(), L.W.val.p, n, hipMemcpyDeviceToHost));
+        }
+        SILI_HIP(hipMemcpy(elem.data(), L.W.elem_start.p, elem.size() * 4, hipMemcpyDeviceToHost));
+        std::vector<uint32_t> br, bc;
+        std::vector<uint8_t> tiles;
+        export_block4_coords(L, br, bc);
+        tiles.resize(br.size() * 16);
+        if (!br.empty()) SILI_HIP(hipMemcpy(tiles.data(), L.B4.tiles.p, tiles.size(), hipMemcpyDeviceToHost));
+        // tiles of each block row, in storage (bc ascending) order
+        std::vector<size_t> tb((size_t)((L.n_in + 3) / 4) + 1, 0);
+        for (uint32_t r : br) tb[(size_t)r + 1]++;
+        for (size_t i = 1; i < tb.size(); ++i) tb[i] += tb[i - 1];
+        struct E { int32_t c; float w, imp; };
+        std::vector<E> row;
+        int64_t flat = 0;
+        if (ptrs) ptrs[0] = 0;
+        for (int64_t r = 0; r < L.n_in; ++r) {
+            row.clear();
+            for (uint32_t e = elem[(size_t)r]; e < elem[(size_t)r + 1]; ++e)
+                row.push_back({cols[e], fp4_decode(val[e] >> 4), fp4_decode(val[e] & 0xFu)});
+            const int64_t b = r / 4, li = r % 4;
+            for (size_t k = tb[(size_t)b]; k < tb[(size_t)b + 1]; ++k)
+                for (int lj = 0; lj < 4; ++lj) {
+                    const uint8_t byte = tiles[k * 16 + (size_t)(lj * 4 + li)];
+                    const int64_t c = (int64_t)bc[k] * 4 + lj;
+                    if (byte == 0 || c >= L.n_out) continue;
+                    row.push_back({(int32_t)c, fp4_decode(byte & 0xFu), fp4_decode(byte >> 4)});
+                }
+            std::stable_sort(row.begin(), row.end(), [](const E &a, const E &b2) { return a.c < b2.c; });
+            for (const E &e : row) {
+                if (indices) indices[flat] = e.c;
+                if (w) w[flat] = e.w;
+                if (imp) imp[flat] = e.imp;
+                ++flat;
+            }
+            if (ptrs) ptrs[r + 1] = (int32_t)flat;
+        }
+        if (n_out_entries) *n_out_entries = flat;
+    });
+}
+
+int sili_device_alloc(sili_layer *layer, size_t bytes, void **out) {
+    return guarded([&] {
+        if (!layer || !out) throw_error(SILI_ERR_INVALID, "NULL argument");
+        set_device(layer->L);
+        SILI_HIP(hipMalloc(out, bytes ? bytes : 1));
+    });
+}
+int sili_device_free(sili_layer *layer, void *ptr) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "NULL argument");
+        set_device(layer->L);
+        if (ptr) SILI_HIP(hipFree(ptr));
+    });
+}
+int sili_memcpy_h2d(sili_layer *layer, void *dst, const void *src, size_t bytes) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "NULL argument");
+        set_device(layer->L);
+        SILI_HIP(hipStreamSynchronize(layer->L.stream));
+        if (bytes) SILI_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    });
+}
+int sili_memcpy_d2h(sili_layer *layer, void *dst, const void *src, size_t bytes) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "NULL argument");
+        set_device(layer->L);
+        SILI_HIP(hipStreamSynchronize(layer->L.stream));
+        if (bytes) SILI_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    });
+}
+int sili_memset_device(sili_layer *layer, void *dst, int value, size_t bytes) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "NULL argument");
+        set_device(layer->L);
+        if (bytes) SILI_HIP(hipMemsetAsync(dst, value, bytes, layer->L.stream));
+        SILI_HIP(hipStreamSynchronize(layer->L.stream));
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,140 @@
+// common.hpp -- shared definitions of the gfx950 FP4 delta-CSR layer library.
+//
+// Device storage per layer (all compact, no per-row headroom):
+//   scattered store, canonical (rows = input neurons) and shadow (rows =
+//   output neurons, the transpose rebuilt on the device after every
+//   structural change):
+//     byte_start[rows+1], elem_start[rows+1]  uint32
+//     idx[]   ULEB128 column deltas, first delta from 0 on every row
+//     val[]   one byte per synapse, (w_code<<4)|imp_code
+//     seg[]   decode work items (see SegDesc)
+//   block4 store, canonical (block rows over inputs) and shadow (block rows
+//   over outputs, tile bytes 4x4-transposed):
+//     byte_start/tile_start[brows+1] uint32, idx[] ULEB128 block-column
+//     deltas, tiles[16*n] (slot lj*4+li, byte (imp<<4)|w), seg[].
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+namespace sili {
+
+// ---- error plumbing (host) ------------------------------------------------
+struct Error {
+    int code;
+    std::string msg;
+};
+[[noreturn]] void throw_error(int code, const std::string &msg);
+void hip_check(hipError_t e, const char *what);
+#define SILI_HIP(expr) ::sili::hip_check((expr), #expr)
+
+// ---- decode work item ------------------------------------------------------
+// One contiguous run of a row's entries, starting at a varint boundary with a
+// known running column (the column of the entry before it, 0 at row start).
+// Rows longer than the segment limit are split; `split` marks every segment
+// of such a row (their partial sums are combined with atomics).
+struct alignas(32) SegDesc {
+    uint32_t row;
+    uint32_t byte_begin;
+    uint32_t byte_end;
+    uint32_t elem_begin;
+    uint32_t base_col;
+    uint32_t split;
+    uint32_t pad0, pad1;
+};
+
+// ---- FP4 E2M1 codec (device + host) -----------------------------------------
+// Code c = s<<3 | e<<1 | m, bias 1; code 8 is NaN (0x7FC00000), not -0
+// (reference fp4quant.hpp:16-33,68-84).
+__host__ __device__ __forceinline__ float fp4_decode(uint32_t code) {
+    const uint32_t s = (code >> 3) & 1u, e = (code >> 1) & 3u, m = code & 1u;
+    uint32_t bits;
+    if (e == 0) bits = m ? (0x3F000000u | (s << 31)) : (s ? 0x7FC00000u : 0u);
+    else bits = (s << 31) | ((e + 126u) << 23) | (m << 22);
+    return __builtin_bit_cast(float, bits);
+}
+
+// Nearest code; ties away from zero (rounding carry), saturate at 6, NaN -> 0,
+// |v| < 0.25 -> 0, never the NaN slot (reference fp4quant.hpp:86-121).
+__host__ __device__ __forceinline__ uint32_t fp4_encode(float v) {
+    const uint32_t bits = __builtin_bit_cast(uint32_t, v);
+    const uint32_t a = bits & 0x7FFFFFFFu;
+    uint32_t mag;
+    if (a > 0x7F800000u) return 0;
+    if (a < 0x3E800000u) mag = 0;
+    else if (a < 0x3F400000u) mag = 1;
+    else if (a < 0x3F800000u) mag = 2;
+    else {
+        uint32_t r = a + (1u << 21);
+        r = r > 0x40C00000u ? 0x40C00000u : r;
+        mag = ((((r >> 23) & 0xFFu) - 126u) << 1) | ((r >> 22) & 1u);
+    }
+    if (mag == 0) return 0;
+    return ((bits >> 31) << 3) | mag;
+}
+
+// ULEB128 length of v (1..5 bytes).
+__host__ __device__ __forceinline__ uint32_t uleb_len(uint32_t v) {
+    return v < (1u << 7) ? 1u : v < (1u << 14) ? 2u : v < (1u << 21) ? 3u : v < (1u << 28) ? 4u : 5u;
+}
+
+// ---- host-side launchers (kernels.hip / build.hip / synapto.hip) -----------
+struct ScaleView {
+    const float *row;   // scale indexed by the gather row   [rows*rank]
+    const float *ent;   // scale indexed by the entry index  [cols*rank], NULL = all ones (rank 1)
+    int rank;
+};
+
+enum SkipMode : int { SKIP_NONE = 0, SKIP_ZERO = 1, SKIP_POSZERO = 2 };
+
+struct GatherPlan {      // one orientation of the scattered store
+    const SegDesc *seg;
+    int64_t nseg;
+    const uint8_t *idx;
+    const uint8_t *val;
+    int64_t rows, cols;
+    bool has_split;
+};
+
+struct Block4Plan {
+    const SegDesc *seg;
+    int64_t nseg;
+    const uint8_t *idx;
+    const uint8_t *tiles;
+    int64_t rows, cols;  // element rows / cols of this orientation
+    bool has_split;
+};
+
+// out[b*out_ld + row] for b < nb: scattered gather (stores; atomics for split
+// rows -- then the caller has zeroed out).  in is feature-major in[c*in_ld + b].
+void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, int64_t in_ld,
+                   float *out, int64_t out_ld, int64_t nb, int skip, hipStream_t st);
+// Block4 contribution, added into out.
+void launch_gather_b4(const Block4Plan &p, const ScaleView &sc, const float *in, int64_t in_ld,
+                      float *out, int64_t out_ld, int64_t nb, int skip, hipStream_t st);
+// gw[e] = sum_b xT[row*B+b] * gT[col*B+b] over the canonical store.
+void launch_sddmm(const GatherPlan &p, const float *xT, const float *gT, int64_t B, float *gw,
+                  hipStream_t st);
+void launch_sddmm_b4(const Block4Plan &p, const uint32_t *tile_base, const float *xT,
+                     const float *gT, int64_t B, float *gw, hipStream_t st);
+// [B, n] -> [n, B]; when acc != NULL also acc[j] += sum_b |src[b, j]|.
+void launch_transpose(const float *src, int64_t B, int64_t n, float *dst, float *acc,
+                      hipStream_t st);
+// acc[j] += sum_b |src[b, j]| (no transpose).
+void launch_colabs(const float *src, int64_t B, int64_t n, float *acc, hipStream_t st);
+// CSR (ptrs[B+1], idx, vals) -> dense feature-major dst[idx*B + b] (dst pre-zeroed).
+// When mark_explicit, explicit zero values are written as -0.0 so that
+// SKIP_POSZERO can tell them from absent entries.
+void launch_densify(const int32_t *ptrs, const int32_t *idx, const float *vals, int64_t B,
+                    int64_t n, float *dst, float *acc_abs, bool mark_explicit, hipStream_t st);
+// Device decode of a scattered store: cols[e], w[e] = fl32(dec * S(row, col)).
+void launch_decode(const GatherPlan &p, const ScaleView &sc, int32_t *cols, float *w,
+                   uint32_t *rows_out, hipStream_t st);
+// Block4 decode: for every tile, its block row, block column and storage index.
+void launch_decode_b4(const Block4Plan &p, uint32_t *tile_br, uint32_t *tile_bc,
+                      hipStream_t st);
+
+}  // namespace sili

@@ -1,0 +1,126 @@
+// layer.hpp -- host-side state of one FP4 delta-CSR layer on one GPU.
+#pragma once
+
+#include "common.hpp"
+
+#include <utility>
+#include <vector>
+
+namespace sili {
+
+// Owning device buffer; grows, never shrinks (except reset()).
+template <typename T>
+struct DevBuf {
+    T *p = nullptr;
+    size_t n = 0;  // capacity in elements
+    DevBuf() = default;
+    DevBuf(const DevBuf &) = delete;
+    DevBuf &operator=(const DevBuf &) = delete;
+    DevBuf(DevBuf &&o) noexcept : p(o.p), n(o.n) { o.p = nullptr; o.n = 0; }
+    DevBuf &operator=(DevBuf &&o) noexcept {
+        if (this != &o) { reset(); p = o.p; n = o.n; o.p = nullptr; o.n = 0; }
+        return *this;
+    }
+    ~DevBuf() { reset(); }
+    void reset() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        n = 0;
+    }
+    // Ensure capacity for `count` elements (+ `pad` bytes of slack so vector
+    // loads near the end stay in bounds).  Contents are not preserved.
+    void ensure(size_t count, size_t pad = 64) {
+        const size_t want = count + (pad + sizeof(T) - 1) / sizeof(T);
+        if (want <= n && p) return;
+        reset();
+        SILI_HIP(hipMalloc(reinterpret_cast<void **>(&p), want * sizeof(T)));
+        n = want;
+    }
+    T *get() const { return p; }
+};
+
+// One orientation of the scattered store.
+struct DScatter {
+    int64_t rows = 0, cols = 0, nnz = 0, nbytes = 0, nseg = 0;
+    bool has_split = false;
+    DevBuf<uint32_t> byte_start, elem_start;  // rows+1
+    DevBuf<uint8_t> idx, val;
+    DevBuf<SegDesc> seg;
+    GatherPlan plan() const {
+        return GatherPlan{seg.p, nseg, idx.p, val.p, rows, cols, has_split};
+    }
+};
+
+// One orientation of the block4 store.
+struct DBlock4 {
+    int64_t brows = 0, bcols = 0, ntiles = 0, nbytes = 0, nseg = 0;
+    int64_t rows = 0, cols = 0;  // element extents of this orientation
+    bool has_split = false;
+    DevBuf<uint32_t> byte_start, tile_start;  // brows+1
+    DevBuf<uint8_t> idx;
+    DevBuf<uint8_t> tiles;                    // 16 * ntiles
+    DevBuf<SegDesc> seg;
+    Block4Plan plan() const {
+        return Block4Plan{seg.p, nseg, idx.p, tiles.p, rows, cols, has_split};
+    }
+};
+
+// Scratch that device builders need for one call.
+struct Scratch {
+    DevBuf<uint8_t> temp;    // rocprim temporary storage
+    DevBuf<int> flag;        // validation flag
+};
+
+struct Layer {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int64_t n_in = 0, n_out = 0, max_weights = 0;
+    int64_t idx_budget = 0, val_budget = 0, tile_budget = 0;
+    int rank = 1;
+    bool vs_ones = true, os_ones = true;  // rank 1 and all ones
+    bool output_scale_trainable = false;
+    bool has_nonfinite = false;
+    bool nonfinite_scales = false;
+    DScatter W, Wt;       // canonical, shadow
+    DBlock4 B4, B4t;      // canonical, shadow
+    DevBuf<float> vs, os, is, ois;
+    DevBuf<float> acc_in, acc_grad;
+    // per-call workspace (grown on demand)
+    DevBuf<float> ws_xT, ws_gT, ws_out;
+    Scratch scratch;
+    uint32_t seg_len = 512;     // max entries per decode work item (scattered)
+    uint32_t seg_len_b4 = 128;  // max tiles per decode work item (block4)
+};
+
+// ---- builders (build.hip) ---------------------------------------------------
+// Encode a store from row-sorted entries: ptrs[rows+1] (device), cols[N]
+// (device, strictly increasing within a row, < ncols), value bytes[N].
+// Throws SILI_ERR_INVALID on malformed input.
+void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64_t N,
+                     const uint32_t *d_ptrs, const uint32_t *d_cols, const uint8_t *d_bytes);
+// Build the shadow (transposed) store of `src` whose decoded entries are
+// (d_rows[e], d_cols[e], src.val[e]).
+void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const uint32_t *d_cols,
+                  DScatter &dst);
+// Block4 store (and its shadow) from an unsorted device tile list.
+void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_t *d_bc,
+                  const uint8_t *d_tiles);
+// Full decode of the canonical scattered store into device arrays.
+void decode_scattered(Layer &L, uint32_t *d_rows, uint32_t *d_cols);
+// Recompute has_nonfinite (code 8 anywhere, or a non-finite scale).
+void refresh_nonfinite(Layer &L);
+
+// rocprim wrappers
+void device_exclusive_scan_u64(Layer &L, const uint64_t *in, uint64_t *out, int64_t n);
+void device_exclusive_scan_u32(Layer &L, const uint32_t *in, uint32_t *out, int64_t n);
+void device_sort_pairs_u32(Layer &L, const uint32_t *kin, uint32_t *kout, const uint32_t *vin,
+                           uint32_t *vout, int64_t n, int bits);
+void device_sort_pairs_u64(Layer &L, const uint64_t *kin, uint64_t *kout, const uint32_t *vin,
+                           uint32_t *vout, int64_t n, int bits);
+
+// ---- synaptogenesis (synapto.hip) ---------------------------------------------
+void synapto_step(Layer &L, float prune_frac, const int32_t *cand_r, const int32_t *cand_c,
+                  const float *cand_v, const float *cand_s, int64_t n_cand, int default_imp,
+                  int64_t *stats);
+
+}  // namespace sili

@@ -1,0 +1,561 @@
+// pymod.cpp -- pybind11 module `_sili_hip`: the reference's
+// `sili._cpu.SparseLinearLayer` surface (sili/cpu_backend.cpp:1506-1743) over
+// the C ABI in include/sili_hip.h.  Host code only; every compute call runs
+// on the GPU through libsili_hip.so.
+//
+// Like the reference binding, arrays are copied in and results are fresh
+// arrays (never views); calls block until the GPU work is done.
+#include <pybind11/numpy.h>
+#include <pybind11/pybind11.h>
+#include <pybind11/stl.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "sili_hip.h"
+
+namespace py = pybind11;
+
+namespace {
+
+[[noreturn]] void raise(int code) {
+    const std::string msg = sili_last_error();
+    switch (code) {
+        case SILI_ERR_INVALID: throw py::value_error(msg);
+        case SILI_ERR_NOMEM: throw std::bad_alloc();
+        case SILI_ERR_RANGE: throw py::index_error(msg);
+        default: throw std::runtime_error(msg);
+    }
+}
+inline void ck(int code) {
+    if (code != SILI_OK) raise(code);
+}
+
+template <typename T>
+using carr = py::array_t<T, py::array::c_style | py::array::forcecast>;
+
+// A device buffer owned by one layer wrapper, grown on demand.
+struct DBuf {
+    sili_layer *L = nullptr;
+    void *p = nullptr;
+    size_t cap = 0;
+    void *get(size_t bytes) {
+        if (bytes <= cap && p) return p;
+        if (p) sili_device_free(L, p);
+        p = nullptr;
+        cap = 0;
+        ck(sili_device_alloc(L, bytes ? bytes : 4, &p));
+        cap = bytes;
+        return p;
+    }
+    void release() {
+        if (p && L) sili_device_free(L, p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
+class Layer {
+   public:
+    Layer(int64_t n_inputs, int64_t n_outputs, int64_t max_weights, int num_cpus, int device)
+        : num_cpus_(num_cpus) {
+        ck(sili_create(n_inputs, n_outputs, max_weights, device, &L_));
+        n_in_ = n_inputs;
+        n_out_ = n_outputs;
+        for (DBuf *b : bufs()) b->L = L_;
+        vs_.assign((size_t)n_in_, 1.0f);
+        os_.assign((size_t)n_out_, 1.0f);
+        is_.assign((size_t)n_in_, 1.0f);
+        ois_.assign((size_t)n_out_, 1.0f);
+    }
+    ~Layer() {
+        for (DBuf *b : bufs()) b->release();
+        sili_destroy(L_);
+    }
+    Layer(const Layer &) = delete;
+    Layer &operator=(const Layer &) = delete;
+
+    int64_t n_inputs() const { return n_in_; }
+    int64_t n_outputs() const { return n_out_; }
+    int num_cpus() const { return num_cpus_; }
+
+    int64_t nnz() {
+        sili_info info;
+        ck(sili_get_info(L_, &info));
+        return info.nnz_scattered + info.live_block4;
+    }
+
+    py::dict info() {
+        sili_info i;
+        ck(sili_get_info(L_, &i));
+        py::dict d;
+        d["n_inputs"] = i.n_inputs;
+        d["n_outputs"] = i.n_outputs;
+        d["nnz_scattered"] = i.nnz_scattered;
+        d["index_bytes"] = i.index_bytes;
+        d["n_tiles"] = i.n_tiles;
+        d["block_index_bytes"] = i.block_index_bytes;
+        d["live_block4"] = i.live_block4;
+        d["n_segments"] = i.n_segments;
+        d["scale_rank"] = i.scale_rank;
+        d["has_nonfinite"] = bool(i.has_nonfinite);
+        return d;
+    }
+
+    // ---- construction ------------------------------------------------------
+    void load_weights(carr<int32_t> ptrs, carr<int32_t> indices, carr<float> vals) {
+        check_ptrs(ptrs, indices.size());
+        if (vals.size() != indices.size()) throw py::value_error("vals and indices differ in length");
+        ck(sili_load_weights(L_, ptrs.data(), indices.data(), vals.data(), nullptr, (int64_t)indices.size()));
+    }
+    void load_weights_with_importance(carr<int32_t> ptrs, carr<int32_t> indices, carr<float> vals,
+                                      carr<float> imp) {
+        check_ptrs(ptrs, indices.size());
+        if (vals.size() != indices.size() || imp.size() != indices.size())
+            throw py::value_error("vals/importance and indices differ in length");
+        ck(sili_load_weights(L_, ptrs.data(), indices.data(), vals.data(), imp.data(), (int64_t)indices.size()));
+    }
+    void load_weight_bytes(carr<int32_t> ptrs, carr<int32_t> indices, carr<uint8_t> bytes) {
+        check_ptrs(ptrs, indices.size());
+        if (bytes.size() != indices.size()) throw py::value_error("bytes and indices differ in length");
+        ck(sili_load_weight_bytes(L_, ptrs.data(), indices.data(), bytes.data(), (int64_t)indices.size()));
+    }
+    void load_dense_codes(carr<uint8_t> wc, carr<uint8_t> ic) {
+        if (wc.size() != n_in_ * n_out_ || ic.size() != n_in_ * n_out_)
+            throw py::value_error("code arrays must hold n_inputs*n_outputs entries");
+        ck(sili_load_dense_codes(L_, wc.data(), ic.data()));
+    }
+    void load_block4_tiles(carr<int32_t> br, carr<int32_t> bc, carr<uint8_t> tiles) {
+        if (br.size() != bc.size() || tiles.size() != br.size() * 16)
+            throw py::value_error("need br[n], bc[n], tiles[16*n]");
+        ck(sili_load_block4_tiles(L_, br.data(), bc.data(), tiles.data(), (int64_t)br.size()));
+    }
+
+    // ---- scales (host mirror, uploaded before the next compute call) --------
+    int get_scale_rank() const { return rank_; }
+    void set_scale_rank(int rank) {
+        ck(sili_set_scale_rank(L_, rank));
+        rank_ = rank;
+        vs_.assign((size_t)(n_in_ * rank), 0.0f);
+        os_.assign((size_t)(n_out_ * rank), 0.0f);
+        for (int64_t r = 0; r < n_in_; ++r) vs_[(size_t)(r * rank)] = 1.0f;
+        for (int64_t c = 0; c < n_out_; ++c) os_[(size_t)(c * rank)] = 1.0f;
+        dirty_vs_ = dirty_os_ = false;
+    }
+    void set_value_scale_raw_k(int64_t row, int64_t k, float v) {
+        check_index(row, n_in_, "row");
+        check_index(k, rank_, "k");
+        vs_[(size_t)(row * rank_ + k)] = v;
+        dirty_vs_ = true;
+    }
+    void set_output_scale_raw_k(int64_t col, int64_t k, float v) {
+        check_index(col, n_out_, "col");
+        check_index(k, rank_, "k");
+        os_[(size_t)(col * rank_ + k)] = v;
+        dirty_os_ = true;
+    }
+    void set_value_scale_raw(int64_t row, float v) { set_value_scale_raw_k(row, 0, v); }
+    void set_output_scale_raw(int64_t col, float v) { set_output_scale_raw_k(col, 0, v); }
+    void set_importance_scale_raw(int64_t row, float v) {
+        check_index(row, n_in_, "row");
+        is_[(size_t)row] = v;
+        dirty_is_ = true;
+    }
+    void set_output_importance_scale_raw(int64_t col, float v) {
+        check_index(col, n_out_, "col");
+        ois_[(size_t)col] = v;
+        dirty_ois_ = true;
+    }
+    void set_value_scales(carr<float> v) {
+        if (v.size() != n_in_ * rank_) throw py::value_error("need n_inputs*scale_rank values");
+        std::memcpy(vs_.data(), v.data(), vs_.size() * 4);
+        dirty_vs_ = true;
+    }
+    void set_output_scales(carr<float> v) {
+        if (v.size() != n_out_ * rank_) throw py::value_error("need n_outputs*scale_rank values");
+        std::memcpy(os_.data(), v.data(), os_.size() * 4);
+        dirty_os_ = true;
+    }
+    float get_value_scale_k(int64_t row, int64_t k) const {
+        check_index(row, n_in_, "row");
+        check_index(k, rank_, "k");
+        return vs_[(size_t)(row * rank_ + k)];
+    }
+    float get_output_scale_k(int64_t col, int64_t k) const {
+        check_index(col, n_out_, "col");
+        check_index(k, rank_, "k");
+        return os_[(size_t)(col * rank_ + k)];
+    }
+    float get_value_scale(int64_t row) const { return get_value_scale_k(row, 0); }
+    float get_output_scale(int64_t col) const { return get_output_scale_k(col, 0); }
+    float get_importance_scale(int64_t row) const {
+        check_index(row, n_in_, "row");
+        return is_[(size_t)row];
+    }
+    float get_output_importance_scale(int64_t col) const {
+        check_index(col, n_out_, "col");
+        return ois_[(size_t)col];
+    }
+    // delta_csr_types.hpp:1235-1240 (k >= 1 accumulated with fma, like the GPU)
+    float get_scale(int64_t row, int64_t col) const {
+        check_index(row, n_in_, "row");
+        check_index(col, n_out_, "col");
+        float s = vs_[(size_t)(row * rank_)] * os_[(size_t)(col * rank_)];
+        for (int k = 1; k < rank_; ++k)
+            s = __builtin_fmaf(vs_[(size_t)(row * rank_ + k)], os_[(size_t)(col * rank_ + k)], s);
+        return s;
+    }
+
+    // ---- compute -------------------------------------------------------------
+    py::array_t<float> forward_dense(carr<float> x) {
+        flush();
+        const int64_t B = x.ndim() == 2 ? (int64_t)x.shape(0) : 1;
+        const int64_t cols = x.ndim() == 2 ? (int64_t)x.shape(1) : (int64_t)x.shape(0);
+        if (x.ndim() > 2 || cols != n_in_) throw py::value_error("x must be [batch, n_inputs] or [n_inputs]");
+        float *dx = (float *)last_x_.get((size_t)(B * n_in_) * 4);
+        ck(sili_memcpy_h2d(L_, dx, x.data(), (size_t)(B * n_in_) * 4));
+        last_batch_ = B;
+        float *dy = (float *)y_.get((size_t)(B * n_out_) * 4);
+        ck(sili_forward_dense(L_, dx, B, dy, nullptr));
+        return fetch(dy, B, n_out_);
+    }
+
+    py::array_t<float> backward_dense(carr<float> dy, float learning_rate, bool lr_per_row_nnz,
+                                      bool damp_by_importance, float beta2, float eps) {
+        (void)lr_per_row_nnz; (void)damp_by_importance; (void)beta2; (void)eps;
+        flush();
+        if (last_batch_ == 0) throw std::runtime_error("backward_dense called before forward_dense");
+        const int64_t B = last_batch_;
+        if (dy.size() != B * n_out_) throw py::value_error("dy must be [batch, n_outputs] of the last forward");
+        float *ddy = (float *)g_.get((size_t)(B * n_out_) * 4);
+        ck(sili_memcpy_h2d(L_, ddy, dy.data(), (size_t)(B * n_out_) * 4));
+        float *ddx = (float *)dx_.get((size_t)(B * n_in_) * 4);
+        ck(sili_backward_dense(L_, (const float *)last_x_.p, ddy, B, ddx, nullptr, nullptr, learning_rate, nullptr));
+        return fetch(ddx, B, n_in_);
+    }
+
+    // nnz-sampled grad-W for (x, dy): (per scattered synapse, per block4 slot)
+    py::tuple sampled_gradw(carr<float> x, carr<float> dy) {
+        flush();
+        const int64_t B = x.ndim() == 2 ? (int64_t)x.shape(0) : 1;
+        if (x.size() != B * n_in_ || dy.size() != B * n_out_) throw py::value_error("x [B,n_in], dy [B,n_out]");
+        sili_info i;
+        ck(sili_get_info(L_, &i));
+        float *dx = (float *)last_x_.get((size_t)(B * n_in_) * 4);
+        float *dg = (float *)g_.get((size_t)(B * n_out_) * 4);
+        ck(sili_memcpy_h2d(L_, dx, x.data(), (size_t)(B * n_in_) * 4));
+        ck(sili_memcpy_h2d(L_, dg, dy.data(), (size_t)(B * n_out_) * 4));
+        last_batch_ = B;
+        float *gs = (float *)gws_.get((size_t)i.nnz_scattered * 4 + 4);
+        float *gb = (float *)gwb_.get((size_t)i.n_tiles * 64 + 4);
+        ck(sili_sampled_gradw(L_, dx, dg, B, gs, gb, nullptr));
+        py::array_t<float> a((py::ssize_t)i.nnz_scattered), b((py::ssize_t)(i.n_tiles * 16));
+        ck(sili_memcpy_d2h(L_, a.mutable_data(), gs, (size_t)i.nnz_scattered * 4));
+        ck(sili_memcpy_d2h(L_, b.mutable_data(), gb, (size_t)i.n_tiles * 64));
+        return py::make_tuple(a, b);
+    }
+
+    py::array_t<float> forward_sparse(carr<int32_t> ptrs, carr<int32_t> indices, carr<float> values,
+                                      int64_t batch) {
+        flush();
+        check_csr(ptrs, indices, values, batch, n_in_);
+        int32_t *dp = upload_i32(p_, ptrs);
+        int32_t *di = upload_i32(i_, indices);
+        float *dv = upload_f32(v_, values);
+        float *dy = (float *)y_.get((size_t)(batch * n_out_) * 4);
+        ck(sili_forward_sparse(L_, dp, di, dv, (int64_t)indices.size(), batch, dy, nullptr));
+        return fetch(dy, batch, n_out_);
+    }
+
+    py::array_t<float> backward_sparse(carr<float> x, carr<int32_t> dptrs, carr<int32_t> didx, carr<float> dvals,
+                                       int64_t batch, float learning_rate, bool lr_per_row_nnz,
+                                       bool damp_by_importance, float beta2, float eps) {
+        (void)lr_per_row_nnz; (void)damp_by_importance; (void)beta2; (void)eps;
+        flush();
+        if (x.size() != batch * n_in_) throw py::value_error("x must be [batch, n_inputs]");
+        check_csr(dptrs, didx, dvals, batch, n_out_);
+        float *dxin = (float *)last_x_.get((size_t)(batch * n_in_) * 4);
+        ck(sili_memcpy_h2d(L_, dxin, x.data(), (size_t)(batch * n_in_) * 4));
+        int32_t *dp = upload_i32(p_, dptrs);
+        int32_t *di = upload_i32(i_, didx);
+        float *dv = upload_f32(v_, dvals);
+        float *ddx = (float *)dx_.get((size_t)(batch * n_in_) * 4);
+        ck(sili_backward_sparse(L_, dxin, dp, di, dv, (int64_t)didx.size(), batch, ddx, learning_rate, nullptr));
+        return fetch(ddx, batch, n_in_);
+    }
+
+    // ---- synaptogenesis ---------------------------------------------------------
+    py::dict synapto_step(float prune_frac, carr<int32_t> rows, carr<int32_t> cols, carr<float> vals,
+                          py::object scores, int default_imp_code) {
+        flush();
+        if (rows.size() != cols.size() || vals.size() != rows.size())
+            throw py::value_error("candidate arrays differ in length");
+        const float *sp = nullptr;
+        carr<float> sarr;
+        if (!scores.is_none()) {
+            sarr = scores.cast<carr<float>>();
+            if (sarr.size() != rows.size()) throw py::value_error("scores length differs");
+            sp = sarr.data();
+        }
+        int64_t st[7] = {0, 0, 0, 0, 0, 0, 0};
+        ck(sili_synapto_step(L_, prune_frac, rows.data(), cols.data(), vals.data(), sp, (int64_t)rows.size(),
+                             default_imp_code, st));
+        py::dict d;
+        const char *names[7] = {"n_prune_target", "n_pruned", "n_grown", "n_demoted_tiles",
+                                "n_promoted_tiles", "n_scattered", "n_tiles"};
+        for (int k = 0; k < 7; ++k) d[names[k]] = st[k];
+        return d;
+    }
+
+    // The device store is always compact and rebuilt on every structural
+    // change, so the reference's headroom management calls have nothing to
+    // do (sisldo_ops.hpp:44-186, delta_csr_memory.hpp:224-306, 767-823).
+    void compact() {}
+    void expand_headroom(float) {}
+    void expand_headroom_to(int, float) {}
+    void equalizer_step() {}
+    void equalize_to_capacity(int, int) {}
+    void expand_block4_headroom(float) {}
+    void compact_block4() {}
+
+    // ---- accumulators / exports -----------------------------------------------
+    py::array_t<float> neuron_input_accum() {
+        py::array_t<float> a((py::ssize_t)n_in_);
+        ck(sili_get_accumulators(L_, a.mutable_data(), nullptr));
+        return a;
+    }
+    py::array_t<float> neuron_grad_accum() {
+        py::array_t<float> a((py::ssize_t)n_out_);
+        ck(sili_get_accumulators(L_, nullptr, a.mutable_data()));
+        return a;
+    }
+    void zero_accum() { ck(sili_zero_accum(L_)); }
+
+    py::tuple absolute() {
+        int64_t n = 0;
+        ck(sili_export_absolute(L_, nullptr, nullptr, nullptr, nullptr, &n));
+        py::array_t<int32_t> p((py::ssize_t)(n_in_ + 1)), ix((py::ssize_t)n);
+        py::array_t<float> w((py::ssize_t)n), imp((py::ssize_t)n);
+        ck(sili_export_absolute(L_, p.mutable_data(), ix.mutable_data(), w.mutable_data(), imp.mutable_data(), &n));
+        return py::make_tuple(p, ix, w, imp);
+    }
+    py::array_t<int32_t> ptrs() { return absolute()[0].cast<py::array_t<int32_t>>(); }
+    py::array_t<int32_t> indices() { return absolute()[1].cast<py::array_t<int32_t>>(); }
+    py::array_t<float> weights_vals() { return absolute()[2].cast<py::array_t<float>>(); }
+    py::array_t<float> importance() { return absolute()[3].cast<py::array_t<float>>(); }
+    py::array_t<int32_t> out_degree() {
+        auto ix = indices();
+        py::array_t<int32_t> d((py::ssize_t)n_out_);
+        auto dm = d.mutable_unchecked<1>();
+        for (py::ssize_t c = 0; c < (py::ssize_t)n_out_; ++c) dm(c) = 0;
+        auto iu = ix.unchecked<1>();
+        for (py::ssize_t k = 0; k < ix.size(); ++k) dm(iu(k))++;
+        return d;
+    }
+    py::object last_input() {
+        if (last_batch_ == 0) return py::none();
+        return fetch((const float *)last_x_.p, last_batch_, n_in_);
+    }
+
+    py::dict export_scattered() {
+        sili_info i;
+        ck(sili_get_info(L_, &i));
+        py::array_t<uint64_t> bs((py::ssize_t)(n_in_ + 1)), es((py::ssize_t)(n_in_ + 1));
+        py::array_t<uint8_t> ix((py::ssize_t)i.index_bytes), v((py::ssize_t)i.nnz_scattered);
+        ck(sili_export_scattered(L_, bs.mutable_data(), es.mutable_data(), ix.mutable_data(), v.mutable_data()));
+        py::dict d;
+        d["row_byte_start"] = bs;
+        d["row_elem_start"] = es;
+        d["idx"] = ix;
+        d["val"] = v;
+        return d;
+    }
+    py::dict export_block4() {
+        sili_info i;
+        ck(sili_get_info(L_, &i));
+        const int64_t brows = (n_in_ + 3) / 4;
+        py::array_t<int32_t> br((py::ssize_t)i.n_tiles), bc((py::ssize_t)i.n_tiles);
+        py::array_t<uint8_t> t((py::ssize_t)(i.n_tiles * 16)), bix((py::ssize_t)i.block_index_bytes);
+        py::array_t<uint64_t> bs((py::ssize_t)(brows + 1)), ts((py::ssize_t)(brows + 1));
+        ck(sili_export_block4(L_, br.mutable_data(), bc.mutable_data(), t.mutable_data(), bs.mutable_data(),
+                              ts.mutable_data(), bix.mutable_data()));
+        py::dict d;
+        d["br"] = br;
+        d["bc"] = bc;
+        d["tiles"] = t;
+        d["brow_byte_start"] = bs;
+        d["brow_tile_start"] = ts;
+        d["bidx"] = bix;
+        return d;
+    }
+    py::tuple decode_scattered() {
+        sili_info i;
+        ck(sili_get_info(L_, &i));
+        flush();
+        py::array_t<int32_t> c((py::ssize_t)i.nnz_scattered);
+        py::array_t<float> w((py::ssize_t)i.nnz_scattered);
+        ck(sili_decode_scattered(L_, c.mutable_data(), w.mutable_data()));
+        return py::make_tuple(c, w);
+    }
+    void synchronize() { ck(sili_synchronize(L_)); }
+    uintptr_t handle() const { return reinterpret_cast<uintptr_t>(L_); }
+
+   private:
+    sili_layer *L_ = nullptr;
+    int64_t n_in_ = 0, n_out_ = 0;
+    int num_cpus_ = 4;
+    int rank_ = 1;
+    std::vector<float> vs_, os_, is_, ois_;
+    bool dirty_vs_ = false, dirty_os_ = false, dirty_is_ = false, dirty_ois_ = false;
+    int64_t last_batch_ = 0;
+    DBuf last_x_, y_, g_, dx_, p_, i_, v_, gws_, gwb_;
+
+    std::vector<DBuf *> bufs() { return {&last_x_, &y_, &g_, &dx_, &p_, &i_, &v_, &gws_, &gwb_}; }
+
+    void flush() {
+        if (dirty_vs_) ck(sili_set_value_scale(L_, vs_.data()));
+        if (dirty_os_) ck(sili_set_output_scale(L_, os_.data()));
+        if (dirty_is_) ck(sili_set_importance_scale(L_, is_.data()));
+        if (dirty_ois_) ck(sili_set_output_importance_scale(L_, ois_.data()));
+        dirty_vs_ = dirty_os_ = dirty_is_ = dirty_ois_ = false;
+    }
+    static void check_index(int64_t i, int64_t n, const char *what) {
+        if (i < 0 || i >= n) throw py::index_error(std::string(what) + " out of range");
+    }
+    void check_ptrs(const carr<int32_t> &ptrs, py::ssize_t nnz) const {
+        if (ptrs.size() != n_in_ + 1) throw py::value_error("ptrs must have n_inputs+1 entries");
+        if (ptrs.data()[n_in_] != nnz) throw py::value_error("ptrs[-1] must equal len(indices)");
+    }
+    static void check_csr(const carr<int32_t> &ptrs, const carr<int32_t> &idx, const carr<float> &vals,
+                          int64_t batch, int64_t n) {
+        if (batch <= 0) throw py::value_error("batch must be >= 1");
+        if (ptrs.size() != batch + 1) throw py::value_error("ptrs must have batch+1 entries");
+        if (idx.size() != vals.size()) throw py::value_error("indices and values differ in length");
+        const int32_t *p = ptrs.data();
+        if (p[0] != 0 || p[batch] != (int32_t)idx.size()) throw py::value_error("ptrs must span the indices");
+        for (int64_t b = 0; b < batch; ++b)
+            if (p[b + 1] < p[b]) throw py::value_error("ptrs must be non-decreasing");
+        const int32_t *ix = idx.data();
+        for (int64_t b = 0; b < batch; ++b)
+            for (int64_t k = p[b]; k < p[b + 1]; ++k) {
+                if (ix[k] < 0 || ix[k] >= n) throw py::value_error("sparse index out of range");
+                if (k > p[b] && ix[k] <= ix[k - 1])
+                    throw py::value_error("sparse indices must be strictly increasing within a batch row");
+            }
+    }
+    int32_t *upload_i32(DBuf &b, const carr<int32_t> &a) {
+        void *d = b.get((size_t)a.size() * 4 + 4);
+        ck(sili_memcpy_h2d(L_, d, a.data(), (size_t)a.size() * 4));
+        return (int32_t *)d;
+    }
+    float *upload_f32(DBuf &b, const carr<float> &a) {
+        void *d = b.get((size_t)a.size() * 4 + 4);
+        ck(sili_memcpy_h2d(L_, d, a.data(), (size_t)a.size() * 4));
+        return (float *)d;
+    }
+    py::array_t<float> fetch(const float *d, int64_t B, int64_t n) {
+        py::array_t<float> r({(py::ssize_t)B, (py::ssize_t)n});
+        ck(sili_memcpy_d2h(L_, r.mutable_data(), d, (size_t)(B * n) * 4));
+        return r;
+    }
+};
+
+// fp4_quantize_array (sili/cpu_backend.cpp:3157): fp32 -> uint8 codes.
+py::array_t<uint8_t> fp4_quantize_array(carr<float> v) {
+    py::array_t<uint8_t> out(v.request().shape);
+    const float *s = v.data();
+    uint8_t *d = out.mutable_data();
+    for (py::ssize_t i = 0; i < v.size(); ++i) {
+        uint32_t bits;
+        std::memcpy(&bits, &s[i], 4);
+        const uint32_t a = bits & 0x7FFFFFFFu;
+        uint32_t mag;
+        if (a > 0x7F800000u) { d[i] = 0; continue; }
+        if (a < 0x3E800000u) mag = 0;
+        else if (a < 0x3F400000u) mag = 1;
+        else if (a < 0x3F800000u) mag = 2;
+        else {
+            uint32_t r = a + (1u << 21);
+            if (r > 0x40C00000u) r = 0x40C00000u;
+            mag = ((((r >> 23) & 0xFFu) - 126u) << 1) | ((r >> 22) & 1u);
+        }
+        d[i] = mag == 0 ? 0 : (uint8_t)(((bits >> 31) << 3) | mag);
+    }
+    return out;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_sili_hip, m) {
+    m.doc() = "gfx950 FP4 delta-CSR sparse linear layer (sili SparseLinearLayer API)";
+    py::class_<Layer>(m, "SparseLinearLayer")
+        .def(py::init<int64_t, int64_t, int64_t, int, int>(), py::arg("n_inputs"), py::arg("n_outputs"),
+             py::arg("max_weights"), py::arg("num_cpus") = 4, py::arg("device") = 0)
+        .def("load_weights", &Layer::load_weights, py::arg("ptrs"), py::arg("indices"), py::arg("vals"))
+        .def("load_weights_with_importance", &Layer::load_weights_with_importance)
+        .def("load_weight_bytes", &Layer::load_weight_bytes)
+        .def("load_dense_codes", &Layer::load_dense_codes, py::arg("weight_codes"), py::arg("importance_codes"))
+        .def("load_block4_tiles", &Layer::load_block4_tiles, py::arg("br"), py::arg("bc"), py::arg("tiles"))
+        .def("get_scale_rank", &Layer::get_scale_rank)
+        .def("set_scale_rank", &Layer::set_scale_rank)
+        .def("set_value_scale_raw", &Layer::set_value_scale_raw)
+        .def("set_output_scale_raw", &Layer::set_output_scale_raw)
+        .def("set_value_scale_raw_k", &Layer::set_value_scale_raw_k)
+        .def("set_output_scale_raw_k", &Layer::set_output_scale_raw_k)
+        .def("set_importance_scale_raw", &Layer::set_importance_scale_raw)
+        .def("set_output_importance_scale_raw", &Layer::set_output_importance_scale_raw)
+        .def("set_value_scales", &Layer::set_value_scales)
+        .def("set_output_scales", &Layer::set_output_scales)
+        .def("get_value_scale", &Layer::get_value_scale)
+        .def("get_output_scale", &Layer::get_output_scale)
+        .def("get_value_scale_k", &Layer::get_value_scale_k)
+        .def("get_output_scale_k", &Layer::get_output_scale_k)
+        .def("get_importance_scale", &Layer::get_importance_scale)
+        .def("get_output_importance_scale", &Layer::get_output_importance_scale)
+        .def("get_scale", &Layer::get_scale)
+        .def("forward_dense", &Layer::forward_dense, py::arg("x"))
+        .def("backward_dense", &Layer::backward_dense, py::arg("dy"), py::arg("learning_rate"),
+             py::arg("lr_per_row_nnz") = false, py::arg("damp_by_importance") = true, py::arg("beta2") = 0.999f,
+             py::arg("eps") = 1e-8f)
+        .def("sampled_gradw", &Layer::sampled_gradw, py::arg("x"), py::arg("dy"))
+        .def("forward_sparse", &Layer::forward_sparse, py::arg("ptrs"), py::arg("indices"), py::arg("values"),
+             py::arg("batch"))
+        .def("backward_sparse", &Layer::backward_sparse, py::arg("x"), py::arg("dy_ptrs"), py::arg("dy_indices"),
+             py::arg("dy_values"), py::arg("batch"), py::arg("learning_rate") = 0.01f,
+             py::arg("lr_per_row_nnz") = false, py::arg("damp_by_importance") = true, py::arg("beta2") = 0.999f,
+             py::arg("eps") = 1e-8f)
+        .def("synapto_step", &Layer::synapto_step, py::arg("prune_frac"), py::arg("cand_rows"),
+             py::arg("cand_cols"), py::arg("cand_vals"), py::arg("cand_scores") = py::none(),
+             py::arg("default_imp_code") = 1)
+        .def("compact", &Layer::compact)
+        .def("expand_headroom", &Layer::expand_headroom, py::arg("blank_fraction") = 0.2f)
+        .def("expand_headroom_to", &Layer::expand_headroom_to, py::arg("min_nnz_per_row"),
+             py::arg("blank_fraction") = 0.2f)
+        .def("equalizer_step", &Layer::equalizer_step)
+        .def("equalize_to_capacity", &Layer::equalize_to_capacity, py::arg("target_elems_per_row"),
+             py::arg("target_bytes_per_row") = 0)
+        .def("expand_block4_headroom", &Layer::expand_block4_headroom, py::arg("blank_fraction") = 0.2f)
+        .def("compact_block4", &Layer::compact_block4)
+        .def("zero_accum", &Layer::zero_accum)
+        .def("info", &Layer::info)
+        .def("export_scattered", &Layer::export_scattered)
+        .def("export_block4", &Layer::export_block4)
+        .def("decode_scattered", &Layer::decode_scattered)
+        .def("synchronize", &Layer::synchronize)
+        .def_property_readonly("handle", &Layer::handle)
+        .def_property_readonly("n_inputs", &Layer::n_inputs)
+        .def_property_readonly("n_outputs", &Layer::n_outputs)
+        .def_property_readonly("num_cpus", &Layer::num_cpus)
+        .def_property_readonly("nnz", &Layer::nnz)
+        .def_property_readonly("out_degree", &Layer::out_degree)
+        .def_property_readonly("last_input", &Layer::last_input)
+        .def_property_readonly("weights_vals", &Layer::weights_vals)
+        .def_property_readonly("importance", &Layer::importance)
+        .def_property_readonly("indices", &Layer::indices)
+        .def_property_readonly("ptrs", &Layer::ptrs)
+        .def_property_readonly("neuron_input_accum", &Layer::neuron_input_accum)
+        .def_property_readonly("neuron_grad_accum", &Layer::neuron_grad_accum);
+    m.def("fp4_quantize_array", &fp4_quantize_array);
+}

@@ -1,0 +1,141 @@
+"""GPU parity: the HIP path (through the C ABI, via the pybind binding)
+against the CPU oracle on the same seeded inputs.
+
+Structure, decoded columns, FP4 codes and fl32(dec*S) must be bit-exact;
+fp32 outputs must satisfy |gpu - oracle| <= 1e-5 * sum|terms| (tests/util.py).
+"""
+import numpy as np
+import pytest
+
+from sili__new_amd.codec import fp4_decode_np
+from sili__new_amd.synth import make_config
+from tests.util import assert_close_terms, gpu_layer, host_layer
+
+pytestmark = pytest.mark.gpu
+
+SMALL = [(0, 0.25), (1, 0.125), (2, 0.0625)]
+
+
+@pytest.mark.parametrize("cfg,scale", SMALL)
+def test_structure_and_decode_bit_exact(hip, cfg, scale):
+    wl = make_config(cfg, scale=scale)
+    H = host_layer(wl)
+    L = gpu_layer(hip, wl)
+    ex = L.export_scattered()
+    assert np.array_equal(ex["row_byte_start"], H.row_byte_start)
+    assert np.array_equal(ex["row_elem_start"], H.row_elem_start)
+    assert np.array_equal(ex["idx"], H.idx[:H.index_bytes])
+    assert np.array_equal(ex["val"], H.val[:H.nnz])
+    cols, w = L.decode_scattered()
+    assert np.array_equal(cols, H.decode_cols())
+    row_of = np.repeat(np.arange(wl.n_in), np.diff(wl.ptrs))
+    want = fp4_decode_np(H.val[:H.nnz] >> 4) * wl.value_scale[row_of]
+    assert np.array_equal(w.view(np.uint32), want.astype(np.float32).view(np.uint32))
+    info = L.info()
+    assert info["nnz_scattered"] == wl.nnz and info["index_bytes"] == H.index_bytes
+
+
+@pytest.mark.parametrize("cfg,scale", SMALL)
+@pytest.mark.parametrize("batch", [1, 3, 8, 32, 64, 100, 256])
+def test_forward_dense(hip, cfg, scale, batch):
+    wl = make_config(cfg, scale=scale, batch=batch)
+    H = host_layer(wl)
+    L = gpu_layer(hip, wl)
+    x = wl.x
+    y = L.forward_dense(x)
+    assert_close_terms(y, H.forward_dense(x), H.forward_dense(x, absmode=True), f"fwd c{cfg} B{batch}")
+
+
+@pytest.mark.parametrize("cfg,scale", SMALL[1:])
+@pytest.mark.parametrize("batch", [1, 5, 32, 64, 128])
+def test_backward_dense_and_gradw(hip, cfg, scale, batch):
+    wl = make_config(cfg, scale=scale, batch=batch)
+    H = host_layer(wl)
+    L = gpu_layer(hip, wl)
+    L.forward_dense(wl.x)
+    dx = L.backward_dense(wl.g, 0.0)
+    dx_o, ai_o, ag_o = H.backward_dense(wl.x, wl.g)
+    assert_close_terms(dx, dx_o, H.backward_dense(wl.x, wl.g, absmode=True)[0], "dx")
+    assert_close_terms(L.neuron_input_accum, ai_o, ai_o, "acc_in")
+    assert_close_terms(L.neuron_grad_accum, ag_o, ag_o, "acc_grad")
+    gs, gb = L.sampled_gradw(wl.x, wl.g)
+    gs_o, _ = H.sampled_gradw(wl.x, wl.g)
+    assert_close_terms(gs, gs_o, H.sampled_gradw(wl.x, wl.g, absmode=True)[0], "gw")
+
+
+def test_sparse_input_forward_and_sparse_grad(hip):
+    wl = make_config(2, scale=0.0625)
+    H = host_layer(wl)
+    L = gpu_layer(hip, wl)
+    y = L.forward_sparse(wl.x_ptrs, wl.x_idx, wl.x_vals, wl.batch)
+    want = H.forward_sparse(wl.x_ptrs, wl.x_idx, wl.x_vals, wl.batch)
+    bnd = H.forward_sparse(wl.x_ptrs, wl.x_idx, wl.x_vals, wl.batch, absmode=True)
+    assert_close_terms(y, want, bnd, "sparse fwd")
+    # sparse upstream gradient: keep ~10% of G per row
+    g = wl.g.copy()
+    g[np.abs(g) < 1.6] = 0.0
+    gp = np.concatenate([[0], np.cumsum((g != 0).sum(1))]).astype(np.int32)
+    gi = np.nonzero(g)[1].astype(np.int32)
+    gv = g[g != 0].astype(np.float32)
+    dx = L.backward_sparse(wl.x, gp, gi, gv, wl.batch, 0.0)
+    dx_o, _, ag_o = H.backward_sparse(wl.x, gp, gi, gv, wl.batch)
+    bnd = H.backward_sparse(wl.x, gp, gi, gv, wl.batch, absmode=True)[0]
+    assert_close_terms(dx, dx_o, bnd, "sparse grad dx")
+    # at lr = 0 the sparse-gradient dx equals the dense dx of the densified G
+    # (test_block4_sparse_input_backward.cpp:62-117)
+    dx_dense = H.backward_dense(wl.x, g)[0]
+    assert_close_terms(dx, dx_dense, bnd, "sparse vs dense dx")
+
+
+@pytest.mark.parametrize("batch", [1, 7, 64, 256])
+def test_block4_paths(hip, batch):
+    wl = make_config(3, scale=0.03125, batch=batch)
+    H = host_layer(wl)
+    L = gpu_layer(hip, wl)
+    ex = L.export_block4()
+    assert np.array_equal(ex["br"], H.tile_br) and np.array_equal(ex["bc"], H.tile_bc)
+    assert np.array_equal(ex["tiles"], H.tiles[:16 * H.n_tiles])
+    assert np.array_equal(ex["bidx"], H.bidx[:len(ex["bidx"])])
+    y = L.forward_dense(wl.x)
+    assert_close_terms(y, H.forward_dense(wl.x), H.forward_dense(wl.x, absmode=True), "b4 fwd")
+    dx = L.backward_dense(wl.g, 0.0)
+    assert_close_terms(dx, H.backward_dense(wl.x, wl.g)[0],
+                       H.backward_dense(wl.x, wl.g, absmode=True)[0], "b4 dx")
+    gs, gb = L.sampled_gradw(wl.x, wl.g)
+    gb_o = H.sampled_gradw(wl.x, wl.g)[1]
+    assert_close_terms(gb, gb_o, H.sampled_gradw(wl.x, wl.g, absmode=True)[1], "b4 gw")
+
+
+def test_reference_kat_forward_backward(hip):
+    """test_disldo_synaptogenesis.cpp:14-89 hand-computed values."""
+    L = hip.SparseLinearLayer(3, 4, 64)
+    L.load_weights(np.array([0, 2, 3, 4], np.int32), np.array([0, 2, 1, 3], np.int32),
+                   np.array([1.5, -2.0, 0.5, 3.0], np.float32))
+    y = L.forward_dense(np.array([1.0, 0.6, 2.0], np.float32))
+    np.testing.assert_allclose(y[0], [1.5, 0.3, -2.0, 6.0], atol=1e-6)
+    dx = L.backward_dense(np.array([[0.3, -0.5, 0.2, 0.4]], np.float32), 0.0)
+    np.testing.assert_allclose(dx[0], [0.05, -0.25, 1.2], atol=1e-6)
+    np.testing.assert_allclose(L.neuron_input_accum, [1.0, 0.6, 2.0], atol=1e-7)
+    assert abs(L.neuron_grad_accum[0] - 0.3) < 1e-7
+
+
+def test_reference_kat_block4(hip):
+    """test_disldo_block4_forward.cpp:21-68 / _backward.cpp:45-70."""
+    L = hip.SparseLinearLayer(8, 8, 256)
+    ptrs = np.array([0, 1, 2, 2, 2, 2, 2, 2, 2], np.int32)
+    L.load_weights(ptrs, np.array([5, 2], np.int32), np.array([2.0, -1.5], np.float32))
+    tile = np.zeros(16, np.uint8)
+    tile[1 * 4 + 0] = 2 | (1 << 4)   # (row 0, col 1) = 1.0, imp 0.5
+    tile[3 * 4 + 2] = 1 | (1 << 4)   # (row 2, col 3) = 0.5
+    L.load_block4_tiles(np.array([0], np.int32), np.array([0], np.int32), tile)
+    x = np.zeros(8, np.float32)
+    x[:3] = [3.0, 1.0, 2.0]
+    y = L.forward_dense(x)[0]
+    want = np.zeros(8, np.float32)
+    want[[5, 2, 1, 3]] = [6.0, -1.5, 3.0, 1.0]
+    np.testing.assert_allclose(y, want, atol=1e-6)
+    dy = np.zeros((1, 8), np.float32)
+    dy[0, [5, 2, 1, 3]] = [0.7, -0.3, 0.4, -0.2]
+    dx = L.backward_dense(dy, 0.0)[0]
+    np.testing.assert_allclose(dx[:3], [1.8, 0.45, -0.1], atol=1e-6)
+    assert L.nnz == 4
