@@ -121,7 +121,10 @@ int sili_forward_dense(sili_layer *layer, const float *x, int64_t batch, float *
 
 /* backward_dense at learning_rate 0 (sili/cpu_backend.cpp:496-529,
  * linear_disldo.hpp:462-2113): dx [batch,n_in] = W^T-gather of dy
- * (overwritten); always accumulates neuron_input_accum += sum_b|x| and
+ * (overwritten).  x may be NULL: then the input of the last forward_dense on
+ * this layer is used, as the reference's backward_dense uses its stored
+ * last_input (available for batch > 1; with batch 1 pass x).  Always
+ * accumulates neuron_input_accum += sum_b|x| and
  * neuron_grad_accum += sum_b|dy| (linear_disldo.hpp:515-520).  When gw_s /
  * gw_b are non-NULL, also writes the nnz-sampled grad-W (see
  * sili_sampled_gradw).  learning_rate must be 0 (the fused optimizer update
@@ -225,6 +228,19 @@ int sili_decode_scattered(sili_layer *layer, int32_t *cols, float *w_true);
  * *n_out_entries.  host outputs.  Synchronous. */
 int sili_export_absolute(sili_layer *layer, int32_t *ptrs, int32_t *indices, float *w,
                          float *imp, int64_t *n_out_entries);
+
+/* ---- measurement (no reference counterpart: the reference is timed with
+ * ad-hoc std::chrono harnesses, scripts/bench_block4_vs_dense_fp4.cpp:58-68) --
+ * While enabled, every kernel the layer launches is bracketed by a hipEvent
+ * pair on the stream it runs on; sili_profile_read synchronizes, aggregates
+ * per "<op>:<kernel>" name in first-seen order, and clears the records. */
+typedef struct {
+    char name[56];
+    int64_t count;
+    double total_ms, min_ms, max_ms;
+} sili_prof_entry;
+int sili_profile_enable(sili_layer *layer, int enable);
+int sili_profile_read(sili_layer *layer, sili_prof_entry *out, int max_entries, int *n_entries);
 
 /* ---- device memory helpers (for callers without HIP headers) ------------ */
 int sili_device_alloc(sili_layer *layer, size_t bytes, void **out);

@@ -67,43 +67,66 @@ __global__ void k_entry_write(const uint32_t *__restrict__ ptrs, const uint32_t 
     } while (v);
 }
 
+// Segments split rows by index bytes: segment j holds the entries whose
+// varint starts at row offset [j*W, (j+1)*W), W = seg_bytes - 4, so a segment
+// never spans more than seg_bytes bytes and never starts inside a varint.
+__device__ __forceinline__ uint32_t seg_count(uint32_t n, uint64_t last_start_rel, uint32_t W, int emit_empty) {
+    return n == 0u ? (emit_empty ? 1u : 0u) : (uint32_t)(last_start_rel / W) + 1u;
+}
+
 __global__ void k_row_starts(const uint32_t *__restrict__ ptrs, int64_t rows, int64_t N,
                              const uint64_t *__restrict__ pos, uint64_t total,
                              uint32_t *__restrict__ byte_start, uint32_t *__restrict__ elem_start,
-                             uint32_t seg_len, int emit_empty, uint32_t *__restrict__ segcnt) {
+                             uint32_t seg_bytes, int emit_empty, uint32_t *__restrict__ segcnt) {
     const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (r > rows) return;
     const uint32_t e = ptrs[r];
     byte_start[r] = (uint32_t)(((int64_t)e < N) ? pos[e] : total);
     elem_start[r] = e;
     if (r < rows) {
-        const uint32_t n = ptrs[r + 1] - e;
-        segcnt[r] = n == 0u ? (emit_empty ? 1u : 0u) : (n + seg_len - 1u) / seg_len;
+        const uint32_t e1 = ptrs[r + 1], n = e1 - e;
+        segcnt[r] = seg_count(n, n ? pos[e1 - 1] - pos[e] : 0u, seg_bytes - 4u, emit_empty);
     }
+}
+
+// first entry in [lo, hi) whose varint starts at or after row offset `off`
+__device__ __forceinline__ uint32_t first_at(const uint64_t *__restrict__ pos, uint32_t lo, uint32_t hi,
+                                             uint64_t base, uint64_t off) {
+    while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        if (pos[mid] - base < off) lo = mid + 1u;
+        else hi = mid;
+    }
+    return lo;
 }
 
 __global__ void k_seg_write(const uint32_t *__restrict__ ptrs, int64_t rows,
                             const uint32_t *__restrict__ byte_start, const uint32_t *__restrict__ cols,
                             const uint64_t *__restrict__ pos, const uint32_t *__restrict__ segoff,
-                            uint32_t seg_len, int emit_empty, SegDesc *__restrict__ seg,
+                            uint32_t seg_bytes, int emit_empty, SegDesc *__restrict__ seg,
                             int *__restrict__ any_split) {
     const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (r >= rows) return;
     const uint32_t e0 = ptrs[r], e1 = ptrs[r + 1];
-    const uint32_t n = e1 - e0;
-    const uint32_t cnt = n == 0u ? (emit_empty ? 1u : 0u) : (n + seg_len - 1u) / seg_len;
+    const uint32_t n = e1 - e0, W = seg_bytes - 4u;
+    const uint64_t base = n ? pos[e0] : 0u;
+    const uint32_t cnt = seg_count(n, n ? pos[e1 - 1] - base : 0u, W, emit_empty);
     if (cnt > 1u) atomicOr(any_split, 1);
+    uint32_t eb = e0;
     for (uint32_t j = 0; j < cnt; ++j) {
+        const bool last = j + 1u == cnt;
+        const uint32_t ee = last ? e1 : first_at(pos, eb, e1, base, (uint64_t)(j + 1u) * W);
         SegDesc d;
-        const uint32_t eb = e0 + j * seg_len;
         d.row = (uint32_t)r;
         d.elem_begin = eb;
+        d.elem_end = ee;
         d.byte_begin = (j == 0u) ? byte_start[r] : (uint32_t)pos[eb];
-        d.byte_end = (j + 1u == cnt) ? byte_start[r + 1] : (uint32_t)pos[eb + seg_len];
-        d.base_col = (j == 0u) ? 0u : cols[eb - 1];
-        d.split = cnt > 1u ? 1u : 0u;
-        d.pad0 = d.pad1 = 0u;
+        d.byte_end = last ? byte_start[r + 1] : (uint32_t)pos[ee];
+        d.base_col = (eb > e0) ? cols[eb - 1] : 0u;
+        d.split = (cnt > 1u ? SEG_SPLIT : 0u) | (j == 0u ? SEG_FIRST : 0u);
+        d.pad1 = 0u;
         seg[segoff[r] + j] = d;
+        eb = ee;
     }
 }
 

@@ -21,7 +21,26 @@ namespace sili {
 
 namespace {
 thread_local std::string g_last_error;
+thread_local Profiler *t_prof = nullptr;
+thread_local const char *t_op = "";
+}  // namespace
+
+ProfOp::ProfOp(const char *op) : prev(t_op) { t_op = op; }
+ProfOp::~ProfOp() { t_op = prev; }
+
+ProfScope::ProfScope(const char *kernel, hipStream_t s) : slot(-1), st(s) {
+    if (!t_prof || !t_prof->enabled) return;
+    Profiler::Rec r{std::string(t_op) + ":" + kernel, t_prof->take(), t_prof->take()};
+    SILI_HIP(hipEventRecord(r.a, s));
+    slot = (int)t_prof->recs.size();
+    t_prof->recs.push_back(std::move(r));
 }
+ProfScope::~ProfScope() {
+    if (slot >= 0 && t_prof) (void)hipEventRecord(t_prof->recs[(size_t)slot].b, st);
+}
+
+ProfCtx::ProfCtx(Layer &L, const char *op) : prev(t_prof), op(op) { t_prof = &L.prof; }
+ProfCtx::~ProfCtx() { t_prof = prev; }
 
 void throw_error(int code, const std::string &msg) { throw Error{code, msg}; }
 
@@ -76,6 +95,7 @@ __global__ void k_i32_to_u32(const int32_t *__restrict__ s, int64_t n, uint32_t 
 
 void fill(float *p, int64_t n, float v, hipStream_t st) {
     if (n <= 0) return;
+    ProfScope ps("fill", st);
     hipLaunchKernelGGL(k_fill_f32, dim3(nblk(n)), dim3(TPB), 0, st, p, n, v);
     SILI_HIP(hipGetLastError());
 }
@@ -201,9 +221,13 @@ const float *to_feature_major(Layer &L, DevBuf<float> &ws, const float *x, int64
 }
 
 void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st) {
+    ProfCtx pc(L, "fwd");
     if (B <= 0) throw_error(SILI_ERR_INVALID, "forward_dense: batch must be >= 1");
     if (!x || !y) throw_error(SILI_ERR_INVALID, "forward_dense: NULL buffer");
     const float *xT = to_feature_major(L, L.ws_xT, x, B, L.n_in, nullptr, st);
+    // the feature-major copy doubles as the stored forward input that
+    // backward_dense reads when called without x (sili/cpu_backend.cpp:481)
+    L.xT_cached_batch = B > 1 ? B : 0;
     if (L.Wt.has_split) fill(y, B * L.n_out, 0.0f, st);
     // scattered pass skips exact-zero inputs (linear_disldo.hpp:114); only
     // observable with non-finite weights, so the skip is compiled in only then
@@ -213,34 +237,44 @@ void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st
         launch_gather_b4(L.B4t.plan(), shadow_scales(L), xT, B, y, L.n_out, B, SKIP_NONE, st);
 }
 
-void sampled_gradw(Layer &L, const float *xT, const float *gT, int64_t B, float *gw_s, float *gw_b,
-                   hipStream_t st) {
-    if (gw_s && L.W.nnz > 0) launch_sddmm(L.W.plan(), xT, gT, B, gw_s, st);
-    if (gw_b && L.B4.ntiles > 0) launch_sddmm_b4(L.B4.plan(), nullptr, xT, gT, B, gw_b, st);
-}
-
 void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float *dx, float *gw_s,
                     float *gw_b, hipStream_t st) {
+    ProfCtx pc(L, "bwd");
     if (B <= 0) throw_error(SILI_ERR_INVALID, "backward_dense: batch must be >= 1");
-    if (!x || !dy || !dx) throw_error(SILI_ERR_INVALID, "backward_dense: NULL buffer");
+    if (!dy || !dx) throw_error(SILI_ERR_INVALID, "backward_dense: NULL buffer");
     const bool want_gw = gw_s || gw_b;
-    // accumulators always advance (linear_disldo.hpp:515-520)
-    const float *gT = to_feature_major(L, L.ws_gT, dy, B, L.n_out, L.acc_grad.p, st);
     const float *xT = nullptr;
-    if (want_gw) xT = to_feature_major(L, L.ws_xT, x, B, L.n_in, L.acc_in.p, st);
-    else launch_colabs(x, B, L.n_in, L.acc_in.p, st);
+    if (!x) {
+        if (L.xT_cached_batch != B)
+            throw_error(SILI_ERR_INVALID, "backward_dense: x is NULL but no forward_dense input of this batch "
+                                          "(> 1) is stored; pass x");
+        xT = L.ws_xT.p;
+    } else if (want_gw) {
+        xT = to_feature_major(L, L.ws_xT, x, B, L.n_in, nullptr, st);
+        L.xT_cached_batch = 0;
+    }
+    // accumulators always advance (linear_disldo.hpp:515-520); sum|x| rides
+    // on the grad-W kernel when it runs
+    const float *gT = to_feature_major(L, L.ws_gT, dy, B, L.n_out, L.acc_grad.p, st);
+    if (!gw_s) {
+        if (xT) launch_rowabs(xT, B, L.n_in, L.acc_in.p, st);
+        else launch_colabs(x, B, L.n_in, L.acc_in.p, st);
+    }
     if (L.W.has_split) fill(dx, B * L.n_in, 0.0f, st);
     launch_gather(L.W.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
     if (L.B4.ntiles > 0)
         launch_gather_b4(L.B4.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
-    if (want_gw) sampled_gradw(L, xT, gT, B, gw_s, gw_b, st);
+    if (gw_s) launch_sddmm(L.W.plan(), xT, gT, B, gw_s, L.acc_in.p, st);
+    if (gw_b && L.B4.ntiles > 0) launch_sddmm_b4(L.B4.plan(), nullptr, xT, gT, B, gw_b, st);
 }
 
 void forward_sparse(Layer &L, const int32_t *ptrs, const int32_t *idx, const float *vals, int64_t B,
                     float *y, hipStream_t st) {
+    ProfCtx pc(L, "fwd_sparse");
     if (B <= 0) throw_error(SILI_ERR_INVALID, "forward_sparse: batch must be >= 1");
     if (!ptrs || !y) throw_error(SILI_ERR_INVALID, "forward_sparse: NULL buffer");
     L.ws_xT.ensure((size_t)(L.n_in * B));
+    L.xT_cached_batch = 0;
     fill(L.ws_xT.p, L.n_in * B, 0.0f, st);
     launch_densify(ptrs, idx, vals, B, L.n_in, L.ws_xT.p, nullptr, true, st);
     if (L.Wt.has_split) fill(y, B * L.n_out, 0.0f, st);
@@ -252,6 +286,7 @@ void forward_sparse(Layer &L, const int32_t *ptrs, const int32_t *idx, const flo
 
 void backward_sparse(Layer &L, const float *x, const int32_t *dptrs, const int32_t *didx,
                      const float *dvals, int64_t B, float *dx, hipStream_t st) {
+    ProfCtx pc(L, "bwd_sparse");
     if (B <= 0) throw_error(SILI_ERR_INVALID, "backward_sparse: batch must be >= 1");
     if (!x || !dptrs || !dx) throw_error(SILI_ERR_INVALID, "backward_sparse: NULL buffer");
     launch_colabs(x, B, L.n_in, L.acc_in.p, st);
@@ -308,8 +343,11 @@ int sili_create(int64_t n_inputs, int64_t n_outputs, int64_t max_weights, int de
         L.idx_budget = max_weights * 8 + 4096;
         L.val_budget = max_weights + 64;
         L.tile_budget = std::max<int64_t>(4, max_weights / 16) * 16;
-        if (const char *e = std::getenv("SILI_SEG_LEN")) L.seg_len = (uint32_t)std::max(16, std::atoi(e));
-        if (const char *e = std::getenv("SILI_SEG_LEN_B4")) L.seg_len_b4 = (uint32_t)std::max(4, std::atoi(e));
+        // segment byte limits (tuning knobs; the kernels stage at most SEG_BYTES_MAX)
+        if (const char *e = std::getenv("SILI_SEG_BYTES"))
+            L.seg_len = (uint32_t)std::min<int>((int)SEG_BYTES_MAX, std::max(16, std::atoi(e)));
+        if (const char *e = std::getenv("SILI_SEG_BYTES_B4"))
+            L.seg_len_b4 = (uint32_t)std::min<int>((int)SEG_BYTES_MAX, std::max(16, std::atoi(e)));
         reset_scales(L);
         std::vector<float> ones_in((size_t)n_inputs, 1.0f), ones_out((size_t)n_outputs, 1.0f);
         upload(L.is, ones_in.data(), ones_in.size(), L.stream);
@@ -503,10 +541,13 @@ int sili_sampled_gradw(sili_layer *layer, const float *x, const float *dy, int64
         Layer &L = layer->L;
         if (batch <= 0 || !x || !dy) throw_error(SILI_ERR_INVALID, "sampled_gradw: bad arguments");
         set_device(L);
+        ProfCtx pc(L, "gradw");
         hipStream_t st = pick(L, stream);
         const float *xT = to_feature_major(L, L.ws_xT, x, batch, L.n_in, nullptr, st);
+        L.xT_cached_batch = 0;
         const float *gT = to_feature_major(L, L.ws_gT, dy, batch, L.n_out, nullptr, st);
-        sampled_gradw(L, xT, gT, batch, gw_s, gw_b, st);
+        if (gw_s) launch_sddmm(L.W.plan(), xT, gT, batch, gw_s, nullptr, st);
+        if (gw_b && L.B4.ntiles > 0) launch_sddmm_b4(L.B4.plan(), nullptr, xT, gT, batch, gw_b, st);
     });
 }
 
@@ -726,6 +767,50 @@ int sili_export_absolute(sili_layer *layer, int32_t *ptrs, int32_t *indices, flo
             if (ptrs) ptrs[r + 1] = (int32_t)flat;
         }
         if (n_out_entries) *n_out_entries = flat;
+    });
+}
+
+int sili_profile_enable(sili_layer *layer, int enable) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        Profiler &P = layer->L.prof;
+        set_device(layer->L);
+        SILI_HIP(hipStreamSynchronize(layer->L.stream));
+        for (auto &r : P.recs) { P.pool.push_back(r.a); P.pool.push_back(r.b); }
+        P.recs.clear();
+        P.enabled = enable != 0;
+    });
+}
+
+int sili_profile_read(sili_layer *layer, sili_prof_entry *out, int max_entries, int *n_entries) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        Profiler &P = layer->L.prof;
+        set_device(layer->L);
+        std::vector<sili_prof_entry> agg;
+        for (auto &r : P.recs) {
+            SILI_HIP(hipEventSynchronize(r.b));
+            float ms = 0.0f;
+            SILI_HIP(hipEventElapsedTime(&ms, r.a, r.b));
+            sili_prof_entry *e = nullptr;
+            for (auto &a : agg)
+                if (r.name == a.name) e = &a;
+            if (!e) {
+                agg.push_back(sili_prof_entry{});
+                e = &agg.back();
+                std::strncpy(e->name, r.name.c_str(), sizeof(e->name) - 1);
+                e->min_ms = 1e30;
+            }
+            e->count += 1;
+            e->total_ms += ms;
+            e->min_ms = std::min(e->min_ms, (double)ms);
+            e->max_ms = std::max(e->max_ms, (double)ms);
+            P.pool.push_back(r.a);
+            P.pool.push_back(r.b);
+        }
+        P.recs.clear();
+        if (n_entries) *n_entries = (int)agg.size();
+        for (int i = 0; out && i < (int)agg.size() && i < max_entries; ++i) out[i] = agg[(size_t)i];
     });
 }
 

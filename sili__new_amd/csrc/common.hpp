@@ -31,20 +31,42 @@ struct Error {
 void hip_check(hipError_t e, const char *what);
 #define SILI_HIP(expr) ::sili::hip_check((expr), #expr)
 
+// ---- measurement ------------------------------------------------------------
+// When a layer's profiler is enabled, every kernel launch issued inside an
+// entry point is bracketed by a hipEvent pair on the stream it runs on and
+// accounted under "<op>:<kernel>" (sili_profile_read).  Disabled: no-op.
+struct ProfOp {              // names the entry point for the launches below it
+    explicit ProfOp(const char *op);
+    ~ProfOp();
+    const char *prev;
+};
+struct ProfScope {           // brackets one kernel launch
+    ProfScope(const char *kernel, hipStream_t st);
+    ~ProfScope();
+    int slot;
+    hipStream_t st;
+};
+
 // ---- decode work item ------------------------------------------------------
 // One contiguous run of a row's entries, starting at a varint boundary with a
-// known running column (the column of the entry before it, 0 at row start).
-// Rows longer than the segment limit are split; `split` marks every segment
-// of such a row (their partial sums are combined with atomics).
+// known running column (the column of the entry before it, 0 at row start),
+// spanning at most SEG_BYTES_MAX index bytes.  Rows longer than that are
+// split; `split` marks every segment of such a row (their partial sums are
+// combined with atomics).
 struct alignas(32) SegDesc {
     uint32_t row;
     uint32_t byte_begin;
     uint32_t byte_end;
     uint32_t elem_begin;
     uint32_t base_col;
-    uint32_t split;
-    uint32_t pad0, pad1;
+    uint32_t split;   // SEG_SPLIT | SEG_FIRST
+    uint32_t elem_end;
+    uint32_t pad1;
 };
+// Index bytes per segment are capped (the kernels stage a whole segment in LDS).
+constexpr uint32_t SEG_BYTES_MAX = 512;
+constexpr uint32_t SEG_SPLIT = 1u;  // the row has several segments (combine with atomics)
+constexpr uint32_t SEG_FIRST = 2u;  // first segment of its row
 
 // ---- FP4 E2M1 codec (device + host) -----------------------------------------
 // Code c = s<<3 | e<<1 | m, bias 1; code 8 is NaN (0x7FC00000), not -0
@@ -115,9 +137,12 @@ void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, in
 // Block4 contribution, added into out.
 void launch_gather_b4(const Block4Plan &p, const ScaleView &sc, const float *in, int64_t in_ld,
                       float *out, int64_t out_ld, int64_t nb, int skip, hipStream_t st);
-// gw[e] = sum_b xT[row*B+b] * gT[col*B+b] over the canonical store.
+// gw[e] = sum_b xT[row*B+b] * gT[col*B+b] over the canonical store; when
+// acc_in != NULL also acc_in[row] += sum_b |xT[row*B+b]| for every row.
 void launch_sddmm(const GatherPlan &p, const float *xT, const float *gT, int64_t B, float *gw,
-                  hipStream_t st);
+                  float *acc_in, hipStream_t st);
+// acc[j] += sum_b |xT[j*B+b]| (feature-major input).
+void launch_rowabs(const float *xT, int64_t B, int64_t n, float *acc, hipStream_t st);
 void launch_sddmm_b4(const Block4Plan &p, const uint32_t *tile_base, const float *xT,
                      const float *gT, int64_t B, float *gw, hipStream_t st);
 // [B, n] -> [n, B]; when acc != NULL also acc[j] += sum_b |src[b, j]|.

@@ -18,6 +18,8 @@
 // owns KB batch columns).
 #include "wave.hpp"
 
+#include <cstdlib>
+
 namespace sili {
 
 namespace {
@@ -35,13 +37,21 @@ struct GArgs {
     float *out;
     int64_t out_ld;
     int64_t nb;
+    uint32_t in_bytes;  // readable bytes from `in` (buffer range for the fast kernels)
 };
+
+// Per-wave FP4 code -> value table (dequant by lookup).
+__device__ __forceinline__ void fp4_table_init(float *tab) {
+    const uint32_t lane = lane_id();
+    if (lane < 16u) tab[lane] = fp4_decode(lane);
+}
 
 template <int G, int KB, int SKIP>
 __global__ __launch_bounds__(256) void k_gather(GArgs a) {
     __shared__ uint32_t s_col[WAVES][64];
     __shared__ float s_w[WAVES][64];
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    __shared__ SegStage s_stage[WAVES];
     const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
     if (si >= a.nseg) return;
     const SegDesc sd = a.seg[si];
@@ -51,19 +61,46 @@ __global__ __launch_bounds__(256) void k_gather(GArgs a) {
     float acc[KB];
 #pragma unroll
     for (int k = 0; k < KB; ++k) acc[k] = 0.0f;
-    uint32_t pos = sd.byte_begin, carry = sd.base_col, ebase = sd.elem_begin;
-    const uint32_t end = sd.byte_end;
+    const StagedSeg sg = stage_segment(s_stage[wave], a.idx, a.val, sd);
+    uint32_t pos = 0, carry = sd.base_col, ebase = sd.elem_begin;
+    const uint32_t end = sg.end;
     while (pos < end) {
-        const Chunk ch = decode_chunk(a.idx, pos, end, carry);
+        const Chunk ch = decode_chunk(sg.idx, pos, end, carry);
         if (ch.T == 0ull) break;  // malformed stream: never spin
         if (ch.term) {
-            const uint32_t code = (uint32_t)a.val[ebase + ch.rank] >> 4;
+            const uint32_t code = (uint32_t)sg.val[ebase + ch.rank - sd.elem_begin] >> 4;
             s_col[wave][ch.rank] = ch.col;
             s_w[wave][ch.rank] = fp4_decode(code) * scale_at(a.sc, row, ch.col);
         }
         wave_lds_sync();
         const uint32_t n = (uint32_t)__popcll(ch.T);
-        for (uint32_t j = 0; j < n; j += G) {
+        // U entries per group in flight: all loads issued before the FMAs
+        constexpr uint32_t U = KB >= 4 ? 4u : 8u;
+        uint32_t j = 0;
+        for (; j + G * U <= n; j += G * U) {
+            uint32_t c[U];
+            float w[U], x[U][KB];
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                c[u] = s_col[wave][j + u * G + g];
+                w[u] = s_w[wave][j + u * G + g];
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                const float *src = a.in + (int64_t)c[u] * a.in_ld;
+#pragma unroll
+                for (int k = 0; k < KB; ++k) {
+                    const int64_t b = (int64_t)bl + (int64_t)BL * k;
+                    x[u][k] = b < a.nb ? src[b] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u)
+#pragma unroll
+                for (int k = 0; k < KB; ++k)
+                    if (!skip_x<SKIP>(x[u][k])) acc[k] = __builtin_fmaf(w[u], x[u][k], acc[k]);
+        }
+        for (; j < n; j += G) {
             const uint32_t e = j + g;
             if (e < n) {
                 const uint32_t c = s_col[wave][e];
@@ -92,8 +129,163 @@ __global__ __launch_bounds__(256) void k_gather(GArgs a) {
             const int64_t b = (int64_t)bl + (int64_t)BL * k;
             if (b < a.nb) {
                 float *o = a.out + b * a.out_ld + row;
-                if (sd.split) atomicAdd(o, acc[k]);
+                if (sd.split & SEG_SPLIT) atomicAdd(o, acc[k]);
                 else *o = acc[k];
+            }
+        }
+    }
+}
+
+// Batch 1: each terminator lane applies its own entry (buffer gather of
+// in[col]); one wave reduction per segment, no entry staging.
+template <int SKIP>
+__global__ __launch_bounds__(256) void k_gather_b1(GArgs a) {
+    __shared__ SegStage s_stage[WAVES];
+    __shared__ float s_fp4[WAVES][16];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
+    if (si >= a.nseg) return;
+    const SegDesc sd = a.seg[si];
+    const uint32_t row = sd.row;
+    fp4_table_init(s_fp4[wave]);
+    const StagedSeg sg = stage_segment(s_stage[wave], a.idx, a.val, sd);
+    const __amdgpu_buffer_rsrc_t rin = buffer_rsrc(a.in, a.in_bytes);
+    const uint32_t ld_bytes = (uint32_t)a.in_ld * 4u;
+    float acc = 0.0f;
+    uint32_t pos = 0, carry = sd.base_col, ebase = sd.elem_begin;
+    const uint32_t end = sg.end;
+    while (pos < end) {
+        const Chunk ch = decode_chunk(sg.idx, pos, end, carry);
+        if (ch.T == 0ull) break;
+        if (ch.term) {
+            const float x = buffer_load_f1(rin, ch.col * ld_bytes);
+            const uint32_t code = (uint32_t)sg.val[ebase + ch.rank - sd.elem_begin] >> 4;
+            const float w = s_fp4[wave][code] * scale_at(a.sc, row, ch.col);
+            if (!skip_x<SKIP>(x)) acc = __builtin_fmaf(w, x, acc);
+        }
+        carry = chunk_advance(ch, pos, ebase);
+    }
+    acc = group_sum_last<64>(acc);
+    if (lane == 63u) {
+        float *o = a.out + row;
+        if (sd.split & SEG_SPLIT) atomicAdd(o, acc);
+        else *o = acc;
+    }
+}
+
+// Decode a whole staged segment into an LDS entry table: ent[k] = (byte
+// offset of entry k's input row, weight bits), k < n; the table is padded up
+// to a multiple of `step` with out-of-range offsets (their buffer loads read
+// 0).  Returns n.  `ent` holds at least SEG_BYTES_MAX + 64 entries.
+__device__ __forceinline__ uint32_t decode_segment_entries(const StagedSeg &sg, const SegDesc &sd,
+                                                           const ScaleView &sc, const float *fp4tab,
+                                                           uint32_t ld_bytes, uint32_t step, uint2 *ent) {
+    const uint32_t lane = lane_id();
+    uint32_t pos = 0, carry = sd.base_col, ebase = sd.elem_begin;
+    while (pos < sg.end) {
+        const Chunk ch = decode_chunk(sg.idx, pos, sg.end, carry);
+        if (ch.T == 0ull) break;
+        if (ch.term) {
+            const uint32_t e = ebase - sd.elem_begin + ch.rank;
+            const uint32_t code = (uint32_t)sg.val[e] >> 4;
+            const float w = fp4tab[code] * scale_at(sc, sd.row, ch.col);
+            ent[e] = make_uint2(ch.col * ld_bytes, __builtin_bit_cast(uint32_t, w));
+        }
+        carry = chunk_advance(ch, pos, ebase);
+    }
+    const uint32_t n = ebase - sd.elem_begin;
+    const uint32_t npad = (n + step - 1u) / step * step;
+    for (uint32_t k = n + lane; k < npad; k += 64u) ent[k] = make_uint2(OOB_OFFSET, 0u);
+    wave_lds_sync();
+    return n;
+}
+
+// float4 along the batch: groups of BL lanes take one entry each (G = 64/BL
+// entries per load instruction); lane bl of a group owns float4 chunks
+// q = bl + BL*k (k < KB) of the entry's feature-major input row.  The whole
+// segment is decoded first (decode_segment_entries); the gather loop then
+// keeps U loads per lane in flight with no predicates.  Needs nb % 4 == 0,
+// in_ld % 4 == 0 and a 16-byte aligned `in`.
+constexpr uint32_t ENT_CAP = SEG_BYTES_MAX + 64u;
+
+template <int BL, int KB, int U, int SKIP>
+__global__ __launch_bounds__(256) void k_gather_v4(GArgs a) {
+    __shared__ SegStage s_stage[WAVES];
+    __shared__ uint2 s_ent[WAVES][ENT_CAP];
+    __shared__ float s_fp4[WAVES][16];
+    constexpr uint32_t G = 64u / BL;
+    constexpr uint32_t STEP = G * U;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
+    if (si >= a.nseg) return;
+    const SegDesc sd = a.seg[si];
+    const uint32_t g = lane / BL, bl = lane % BL;
+    fp4_table_init(s_fp4[wave]);
+    const StagedSeg sg = stage_segment(s_stage[wave], a.idx, a.val, sd);
+    const __amdgpu_buffer_rsrc_t rin = buffer_rsrc(a.in, a.in_bytes);
+    const uint32_t nq = (uint32_t)(a.nb >> 2);
+    uint32_t lane_off[KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+        const uint32_t q = bl + BL * (uint32_t)k;
+        lane_off[k] = q < nq ? q * 16u : OOB_OFFSET;  // chunks past the batch read 0
+    }
+    uint2 *ent = s_ent[wave];
+    const uint32_t n = decode_segment_entries(sg, sd, a.sc, s_fp4[wave], (uint32_t)a.in_ld * 4u, STEP, ent);
+    float4 acc[KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t j = 0; j < n; j += STEP) {
+        uint2 e[U];
+        float4 x[U][KB];
+#pragma unroll
+        for (int u = 0; u < U; ++u) e[u] = ent[j + (uint32_t)u * G + g];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int k = 0; k < KB; ++k) x[u][k] = buffer_load_f4(rin, e[u].x + lane_off[k]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float w = __builtin_bit_cast(float, e[u].y);
+#pragma unroll
+            for (int k = 0; k < KB; ++k) {
+                if constexpr (SKIP == SKIP_NONE) {
+                    acc[k].x = __builtin_fmaf(w, x[u][k].x, acc[k].x);
+                    acc[k].y = __builtin_fmaf(w, x[u][k].y, acc[k].y);
+                    acc[k].z = __builtin_fmaf(w, x[u][k].z, acc[k].z);
+                    acc[k].w = __builtin_fmaf(w, x[u][k].w, acc[k].w);
+                } else {
+                    // padding reads x = 0 and is skipped like a zero input
+                    if (!skip_x<SKIP>(x[u][k].x)) acc[k].x = __builtin_fmaf(w, x[u][k].x, acc[k].x);
+                    if (!skip_x<SKIP>(x[u][k].y)) acc[k].y = __builtin_fmaf(w, x[u][k].y, acc[k].y);
+                    if (!skip_x<SKIP>(x[u][k].z)) acc[k].z = __builtin_fmaf(w, x[u][k].z, acc[k].z);
+                    if (!skip_x<SKIP>(x[u][k].w)) acc[k].w = __builtin_fmaf(w, x[u][k].w, acc[k].w);
+                }
+            }
+        }
+    }
+    // combine the G entry groups (lanes bl, bl+BL, ...)
+#pragma unroll
+    for (uint32_t off = BL; off < 64u; off <<= 1)
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            acc[k].x += __shfl_xor(acc[k].x, (int)off, 64);
+            acc[k].y += __shfl_xor(acc[k].y, (int)off, 64);
+            acc[k].z += __shfl_xor(acc[k].z, (int)off, 64);
+            acc[k].w += __shfl_xor(acc[k].w, (int)off, 64);
+        }
+    if (g == 0) {
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            const int64_t q = (int64_t)bl + (int64_t)BL * k;
+            if (q < nq) {
+                const float v4[4] = {acc[k].x, acc[k].y, acc[k].z, acc[k].w};
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float *o = a.out + (4 * q + v) * a.out_ld + sd.row;
+                    if (sd.split & SEG_SPLIT) atomicAdd(o, v4[v]);
+                    else *o = v4[v];
+                }
             }
         }
     }
@@ -208,7 +400,7 @@ __global__ __launch_bounds__(256) void k_gather_b4(BArgs a) {
                 const int64_t b = (int64_t)bl + (int64_t)BL * k;
                 if (b < a.nb) {
                     float *o = a.out + b * a.out_ld + r;
-                    if (sd.split) atomicAdd(o, acc[li][k]);
+                    if (sd.split & SEG_SPLIT) atomicAdd(o, acc[li][k]);
                     else *o += acc[li][k];
                 }
             }
@@ -224,46 +416,156 @@ struct SArgs {
     const float *gT;
     int64_t B;
     float *gw;
+    float *acc_in;  // optional: acc_in[row] += sum_b |xT[row,b]| (first segment of each row)
+    uint32_t gT_bytes;  // readable bytes from gT (buffer range for the fast kernel)
 };
+
+// acc += sum_b x[b]*g[b] over B floats (B % 4 == 0, 16-byte aligned), with
+// four float4 loads in flight.
+__device__ __forceinline__ float dot_f4(const float *__restrict__ x, const float *__restrict__ g, int64_t B) {
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    int64_t b = 0;
+    for (; b + 16 <= B; b += 16) {
+        const float4 g0 = *reinterpret_cast<const float4 *>(g + b);
+        const float4 g1 = *reinterpret_cast<const float4 *>(g + b + 4);
+        const float4 g2 = *reinterpret_cast<const float4 *>(g + b + 8);
+        const float4 g3 = *reinterpret_cast<const float4 *>(g + b + 12);
+        const float4 x0 = *reinterpret_cast<const float4 *>(x + b);
+        const float4 x1 = *reinterpret_cast<const float4 *>(x + b + 4);
+        const float4 x2 = *reinterpret_cast<const float4 *>(x + b + 8);
+        const float4 x3 = *reinterpret_cast<const float4 *>(x + b + 12);
+        a0 = __builtin_fmaf(x0.x, g0.x, a0); a1 = __builtin_fmaf(x0.y, g0.y, a1);
+        a2 = __builtin_fmaf(x0.z, g0.z, a2); a3 = __builtin_fmaf(x0.w, g0.w, a3);
+        a0 = __builtin_fmaf(x1.x, g1.x, a0); a1 = __builtin_fmaf(x1.y, g1.y, a1);
+        a2 = __builtin_fmaf(x1.z, g1.z, a2); a3 = __builtin_fmaf(x1.w, g1.w, a3);
+        a0 = __builtin_fmaf(x2.x, g2.x, a0); a1 = __builtin_fmaf(x2.y, g2.y, a1);
+        a2 = __builtin_fmaf(x2.z, g2.z, a2); a3 = __builtin_fmaf(x2.w, g2.w, a3);
+        a0 = __builtin_fmaf(x3.x, g3.x, a0); a1 = __builtin_fmaf(x3.y, g3.y, a1);
+        a2 = __builtin_fmaf(x3.z, g3.z, a2); a3 = __builtin_fmaf(x3.w, g3.w, a3);
+    }
+    for (; b < B; b += 4) {
+        const float4 gv = *reinterpret_cast<const float4 *>(g + b);
+        const float4 xv = *reinterpret_cast<const float4 *>(x + b);
+        a0 = __builtin_fmaf(xv.x, gv.x, a0); a1 = __builtin_fmaf(xv.y, gv.y, a1);
+        a2 = __builtin_fmaf(xv.z, gv.z, a2); a3 = __builtin_fmaf(xv.w, gv.w, a3);
+    }
+    return (a0 + a1) + (a2 + a3);
+}
 
 // gw[e] = sum_b xT[row,b] * gT[col_e,b]; each terminator lane owns one entry
 // and streams its gT row (float4 along b), xT[row,:] is staged in LDS.
 __global__ __launch_bounds__(256) void k_sddmm(SArgs a) {
     extern __shared__ __align__(16) float s_x[];  // [WAVES][B]
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    __shared__ SegStage s_stage[WAVES];
     const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
     if (si >= a.nseg) return;
     const SegDesc sd = a.seg[si];
     const int64_t B = a.B;
     float *sx = s_x + (int64_t)wave * B;
-    for (int64_t b = lane; b < B; b += 64) sx[b] = a.xT[(int64_t)sd.row * B + b];
+    float part = 0.0f;
+    for (int64_t b = lane; b < B; b += 64) {
+        const float v = a.xT[(int64_t)sd.row * B + b];
+        sx[b] = v;
+        part += __builtin_fabsf(v);
+    }
+    if (a.acc_in && (sd.split & SEG_FIRST)) {
+        part = wave_sum(part);
+        if (lane == 0) a.acc_in[sd.row] += part;
+    }
     wave_lds_sync();
-    uint32_t pos = sd.byte_begin, carry = sd.base_col, ebase = sd.elem_begin;
-    const uint32_t end = sd.byte_end;
+    const StagedSeg sg = stage_segment(s_stage[wave], a.idx, nullptr, sd);
+    uint32_t pos = 0, carry = sd.base_col, ebase = sd.elem_begin;
+    const uint32_t end = sg.end;
     const bool vec4 = (B & 3) == 0;
     while (pos < end) {
-        const Chunk ch = decode_chunk(a.idx, pos, end, carry);
+        const Chunk ch = decode_chunk(sg.idx, pos, end, carry);
         if (ch.T == 0ull) break;
         if (ch.term) {
             const float *gr = a.gT + (int64_t)ch.col * B;
             float acc = 0.0f;
             if (vec4) {
-                float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-                for (int64_t b = 0; b < B; b += 4) {
-                    const float4 gv = *reinterpret_cast<const float4 *>(gr + b);
-                    const float4 xv = *reinterpret_cast<const float4 *>(sx + b);
-                    a0 = __builtin_fmaf(xv.x, gv.x, a0);
-                    a1 = __builtin_fmaf(xv.y, gv.y, a1);
-                    a2 = __builtin_fmaf(xv.z, gv.z, a2);
-                    a3 = __builtin_fmaf(xv.w, gv.w, a3);
-                }
-                acc = (a0 + a1) + (a2 + a3);
+                acc = dot_f4(sx, gr, B);
             } else {
                 for (int64_t b = 0; b < B; ++b) acc = __builtin_fmaf(sx[b], gr[b], acc);
             }
             a.gw[ebase + ch.rank] = acc;
         }
         carry = chunk_advance(ch, pos, ebase);
+    }
+}
+
+// Grad-W with float4 along the batch: BL lanes per entry (G = 64/BL entries
+// per load instruction), each lane owning float4 chunks q = bl + BL*k of
+// both xT[row] (held in registers for the whole segment) and gT[col];
+// DPP row reductions finish each entry.  The segment is decoded first into
+// an LDS table of gT byte offsets (padding: out of range, loads read 0).
+// Needs B % 4 == 0 and 16-byte aligned xT / gT.
+template <int BL, int KB, int U>
+__global__ __launch_bounds__(256) void k_sddmm_v4(SArgs a) {
+    __shared__ SegStage s_stage[WAVES];
+    __shared__ uint32_t s_off[WAVES][ENT_CAP];
+    constexpr uint32_t G = 64u / BL;
+    constexpr uint32_t STEP = G * U;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
+    if (si >= a.nseg) return;
+    const SegDesc sd = a.seg[si];
+    const uint32_t g = lane / BL, bl = lane % BL;
+    const uint32_t nq = (uint32_t)(a.B >> 2);
+    const uint32_t ld_bytes = (uint32_t)a.B * 4u;
+    const float4 *x4p = reinterpret_cast<const float4 *>(a.xT) + (int64_t)sd.row * nq;
+    const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(a.gT, a.gT_bytes);
+    uint32_t lane_off[KB];
+    float4 xr[KB];
+    float part = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+        const uint32_t q = bl + BL * (uint32_t)k;
+        lane_off[k] = q < nq ? q * 16u : OOB_OFFSET;
+        xr[k] = q < nq ? x4p[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        part += (__builtin_fabsf(xr[k].x) + __builtin_fabsf(xr[k].y)) +
+                (__builtin_fabsf(xr[k].z) + __builtin_fabsf(xr[k].w));
+    }
+    if (a.acc_in && (sd.split & SEG_FIRST)) {
+        part = group_sum_last<BL>(part);  // every group holds the whole row; use group 0
+        if (lane == BL - 1u) a.acc_in[sd.row] += part;
+    }
+    const StagedSeg sg = stage_segment(s_stage[wave], a.idx, nullptr, sd);
+    uint32_t *offs = s_off[wave];
+    uint32_t pos = 0, carry = sd.base_col, ebase = sd.elem_begin;
+    while (pos < sg.end) {
+        const Chunk ch = decode_chunk(sg.idx, pos, sg.end, carry);
+        if (ch.T == 0ull) break;
+        if (ch.term) offs[ebase - sd.elem_begin + ch.rank] = ch.col * ld_bytes;
+        carry = chunk_advance(ch, pos, ebase);
+    }
+    const uint32_t n = ebase - sd.elem_begin;
+    const uint32_t npad = (n + STEP - 1u) / STEP * STEP;
+    for (uint32_t k = n + lane; k < npad; k += 64u) offs[k] = OOB_OFFSET;
+    wave_lds_sync();
+    for (uint32_t j = 0; j < n; j += STEP) {
+        float4 gv[U][KB];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t off = offs[j + (uint32_t)u * G + g];
+#pragma unroll
+            for (int k = 0; k < KB; ++k) gv[u][k] = buffer_load_f4(rg, off + lane_off[k]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+            for (int k = 0; k < KB; ++k) {
+                d0 = __builtin_fmaf(xr[k].x, gv[u][k].x, d0);
+                d1 = __builtin_fmaf(xr[k].y, gv[u][k].y, d1);
+                d0 = __builtin_fmaf(xr[k].z, gv[u][k].z, d0);
+                d1 = __builtin_fmaf(xr[k].w, gv[u][k].w, d1);
+            }
+            const float tot = group_sum_last<BL>(d0 + d1);
+            const uint32_t e = j + (uint32_t)u * G + g;
+            if (bl == BL - 1u && e < n) a.gw[sd.elem_begin + e] = tot;
+        }
     }
 }
 
@@ -316,16 +618,7 @@ __global__ __launch_bounds__(256) void k_sddmm_b4(SBArgs a) {
                 const float *gr = a.gT + (int64_t)c * B;
                 const float *xr = sx + (int64_t)li * B;
                 if (vec4) {
-                    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-                    for (int64_t b = 0; b < B; b += 4) {
-                        const float4 gv = *reinterpret_cast<const float4 *>(gr + b);
-                        const float4 xv = *reinterpret_cast<const float4 *>(xr + b);
-                        a0 = __builtin_fmaf(xv.x, gv.x, a0);
-                        a1 = __builtin_fmaf(xv.y, gv.y, a1);
-                        a2 = __builtin_fmaf(xv.z, gv.z, a2);
-                        a3 = __builtin_fmaf(xv.w, gv.w, a3);
-                    }
-                    acc = (a0 + a1) + (a2 + a3);
+                    acc = dot_f4(xr, gr, B);
                 } else {
                     for (int64_t b = 0; b < B; ++b) acc = __builtin_fmaf(xr[b], gr[b], acc);
                 }
@@ -337,35 +630,49 @@ __global__ __launch_bounds__(256) void k_sddmm_b4(SBArgs a) {
     }
 }
 
-// [B, n] -> [n, B] through a 64x65 LDS tile; optional acc[j] += sum_b |x[b,j]|.
+// [B, n] -> [n, B], one 64(b) x 16(j) tile per block through LDS; reads are
+// 64-byte row segments, writes 256-byte runs of b.  Optional
+// acc[j] += sum_b |x[b,j]| (atomics when B spans several tiles).
 __global__ __launch_bounds__(256) void k_transpose(const float *__restrict__ src, int64_t B,
                                                    int64_t n, float *__restrict__ dst,
                                                    float *__restrict__ acc) {
-    __shared__ float tile[64][65];
-    const int64_t j0 = (int64_t)blockIdx.x * 64, b0 = (int64_t)blockIdx.y * 64;
-    const uint32_t tx = threadIdx.x & 63u, ty = threadIdx.x >> 6;  // 64 x 4
-    float part = 0.0f;
-    for (uint32_t i = ty; i < 64u; i += 4u) {
-        const int64_t b = b0 + i, j = j0 + tx;
-        float v = 0.0f;
-        if (b < B && j < n) v = src[b * n + j];
-        tile[i][tx] = v;
-        part += __builtin_fabsf(v);
-    }
-    if (acc) {
-        __shared__ float red[4][64];
-        red[ty][tx] = part;
-        __syncthreads();
-        if (ty == 0 && j0 + tx < n) {
-            const float s = (red[0][tx] + red[1][tx]) + (red[2][tx] + red[3][tx]);
-            atomicAdd(acc + j0 + tx, s);
+    __shared__ float tile[64][17];
+    const int64_t j0 = (int64_t)blockIdx.x * 16, b0 = (int64_t)blockIdx.y * 64;
+    const uint32_t t = threadIdx.x;
+    {
+        const uint32_t jj = t & 15u, bb = t >> 4;  // 16 x 16
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const int64_t b = b0 + bb + 16u * i, j = j0 + jj;
+            tile[bb + 16u * i][jj] = (b < B && j < n) ? src[b * n + j] : 0.0f;
         }
     }
     __syncthreads();
-    for (uint32_t i = ty; i < 64u; i += 4u) {
-        const int64_t j = j0 + i, b = b0 + tx;
-        if (j < n && b < B) dst[j * B + b] = tile[tx][i];
+    if (acc && t < 16u && j0 + t < n) {
+        float s = 0.0f;
+        for (uint32_t i = 0; i < 64u; ++i) s += __builtin_fabsf(tile[i][t]);
+        if (gridDim.y == 1) acc[j0 + t] += s;
+        else atomicAdd(acc + j0 + t, s);
     }
+    {
+        const uint32_t bb = t & 63u, jj = t >> 6;  // 64 x 4
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const int64_t j = j0 + jj + 4u * i, b = b0 + bb;
+            if (j < n && b < B) dst[j * B + b] = tile[bb][jj + 4u * i];
+        }
+    }
+}
+
+// acc[j] += sum_b |xT[j*B + b]| over a feature-major copy (one wave per row).
+__global__ __launch_bounds__(256) void k_rowabs(const float *__restrict__ xT, int64_t B, int64_t n,
+                                                float *__restrict__ acc) {
+    const int64_t j = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (j >= n) return;
+    float s = 0.0f;
+    for (int64_t b = threadIdx.x & 63u; b < B; b += 64) s += __builtin_fabsf(xT[j * B + b]);
+    s = wave_sum(s);
+    if ((threadIdx.x & 63u) == 0) acc[j] += s;
 }
 
 __global__ __launch_bounds__(256) void k_colabs(const float *__restrict__ src, int64_t B, int64_t n,
@@ -407,18 +714,20 @@ struct DArgs {
 
 __global__ __launch_bounds__(256) void k_decode(DArgs a) {
     const uint32_t wave = threadIdx.x >> 6;
+    __shared__ SegStage s_stage[WAVES];
     const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
     if (si >= a.nseg) return;
     const SegDesc sd = a.seg[si];
-    uint32_t pos = sd.byte_begin, carry = sd.base_col, ebase = sd.elem_begin;
-    const uint32_t end = sd.byte_end;
+    const StagedSeg sg = stage_segment(s_stage[wave], a.idx, a.val, sd);
+    uint32_t pos = 0, carry = sd.base_col, ebase = sd.elem_begin;
+    const uint32_t end = sg.end;
     while (pos < end) {
-        const Chunk ch = decode_chunk(a.idx, pos, end, carry);
+        const Chunk ch = decode_chunk(sg.idx, pos, end, carry);
         if (ch.T == 0ull) break;
         if (ch.term) {
             const uint32_t e = ebase + ch.rank;
             if (a.cols) a.cols[e] = (int32_t)ch.col;
-            if (a.w) a.w[e] = fp4_decode((uint32_t)a.val[e] >> 4) * scale_at(a.sc, sd.row, ch.col);
+            if (a.w) a.w[e] = fp4_decode((uint32_t)sg.val[e - sd.elem_begin] >> 4) * scale_at(a.sc, sd.row, ch.col);
             if (a.rows_out) a.rows_out[e] = sd.row;
         }
         carry = chunk_advance(ch, pos, ebase);
@@ -468,15 +777,68 @@ void gather_b4_dispatch_skip(const BArgs &a, int skip, hipStream_t st) {
     }
 }
 
+template <int BL, int KB, int U>
+void gather_v4_skip_u(const GArgs &a, int skip, hipStream_t st) {
+    const dim3 grid(blocks_for(a.nseg)), block(256);
+    switch (skip) {
+        case SKIP_ZERO: hipLaunchKernelGGL((k_gather_v4<BL, KB, U, SKIP_ZERO>), grid, block, 0, st, a); break;
+        case SKIP_POSZERO: hipLaunchKernelGGL((k_gather_v4<BL, KB, U, SKIP_POSZERO>), grid, block, 0, st, a); break;
+        default: hipLaunchKernelGGL((k_gather_v4<BL, KB, U, SKIP_NONE>), grid, block, 0, st, a); break;
+    }
+}
+
+// entries in flight per lane: SILI_GATHER_U in {4, 8, 16} (tuning knob)
+inline int gather_u() {
+    static const int u = [] {
+        const char *e = std::getenv("SILI_GATHER_U");
+        const int v = e ? std::atoi(e) : 4;
+        return v >= 16 ? 16 : v >= 8 ? 8 : 4;
+    }();
+    return u;
+}
+
+template <int BL, int KB>
+void gather_v4_skip(const GArgs &a, int skip, hipStream_t st) {
+    constexpr int UMAX = (64 / (64 / BL)) >= 1 ? 16 : 16;
+    (void)UMAX;
+    const int u = gather_u();
+    if (u >= 16 && KB == 1) gather_v4_skip_u<BL, KB, 16>(a, skip, st);
+    else if (u >= 8 && KB <= 2) gather_v4_skip_u<BL, KB, 8>(a, skip, st);
+    else gather_v4_skip_u<BL, KB, 4>(a, skip, st);
+}
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 }  // namespace
 
 void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, int64_t in_ld,
                    float *out, int64_t out_ld, int64_t nb_total, int skip, hipStream_t st) {
     if (p.nseg == 0 || nb_total == 0) return;
+    ProfScope ps("gather", st);
     for (int64_t b0 = 0; b0 < nb_total; b0 += 512) {
         const int64_t nb = nb_total - b0 < 512 ? nb_total - b0 : 512;
-        GArgs a{p.seg, p.nseg, p.idx, p.val, sc, in + b0, in_ld, out + b0 * out_ld, out_ld, nb};
-        if (nb == 1) gather_dispatch_skip<64, 1>(a, skip, st);
+        const int64_t in_bytes = (p.cols * in_ld - b0) * 4;
+        const bool small = in_bytes < (int64_t)OOB_OFFSET;
+        GArgs a{p.seg, p.nseg, p.idx, p.val, sc, in + b0, in_ld, out + b0 * out_ld, out_ld, nb,
+                small ? (uint32_t)in_bytes : 0u};
+        const dim3 grid(blocks_for(a.nseg)), block(256);
+        if (nb == 1 && small) {
+            switch (skip) {
+                case SKIP_ZERO: hipLaunchKernelGGL(k_gather_b1<SKIP_ZERO>, grid, block, 0, st, a); break;
+                case SKIP_POSZERO: hipLaunchKernelGGL(k_gather_b1<SKIP_POSZERO>, grid, block, 0, st, a); break;
+                default: hipLaunchKernelGGL(k_gather_b1<SKIP_NONE>, grid, block, 0, st, a); break;
+            }
+        } else if (small && nb % 4 == 0 && in_ld % 4 == 0 && aligned16(a.in)) {
+            const int64_t nq = nb / 4;
+            if (nq <= 1) gather_v4_skip<1, 1>(a, skip, st);
+            else if (nq <= 2) gather_v4_skip<2, 1>(a, skip, st);
+            else if (nq <= 4) gather_v4_skip<4, 1>(a, skip, st);
+            else if (nq <= 8) gather_v4_skip<8, 1>(a, skip, st);
+            else if (nq <= 16) gather_v4_skip<16, 1>(a, skip, st);
+            else if (nq <= 32) gather_v4_skip<16, 2>(a, skip, st);
+            else if (nq <= 64) gather_v4_skip<16, 4>(a, skip, st);
+            else gather_v4_skip<16, 8>(a, skip, st);
+        } else if (nb <= 1) gather_dispatch_skip<64, 1>(a, skip, st);
         else if (nb <= 2) gather_dispatch_skip<32, 1>(a, skip, st);
         else if (nb <= 4) gather_dispatch_skip<16, 1>(a, skip, st);
         else if (nb <= 8) gather_dispatch_skip<8, 1>(a, skip, st);
@@ -493,6 +855,7 @@ void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, in
 void launch_gather_b4(const Block4Plan &p, const ScaleView &sc, const float *in, int64_t in_ld,
                       float *out, int64_t out_ld, int64_t nb_total, int skip, hipStream_t st) {
     if (p.nseg == 0 || nb_total == 0) return;
+    ProfScope ps("gather_b4", st);
     for (int64_t b0 = 0; b0 < nb_total; b0 += 256) {
         const int64_t nb = nb_total - b0 < 256 ? nb_total - b0 : 256;
         BArgs a{p.seg, p.nseg, p.idx, p.tiles, p.rows, p.cols, sc, in + b0, in_ld,
@@ -511,18 +874,41 @@ void launch_gather_b4(const Block4Plan &p, const ScaleView &sc, const float *in,
 }
 
 void launch_sddmm(const GatherPlan &p, const float *xT, const float *gT, int64_t B, float *gw,
-                  hipStream_t st) {
+                  float *acc_in, hipStream_t st) {
     if (p.nseg == 0) return;
-    SArgs a{p.seg, p.nseg, p.idx, xT, gT, B, gw};
-    const size_t lds = sizeof(float) * (size_t)WAVES * (size_t)B;
-    if (lds > 64 * 1024) throw_error(1, "sampled grad-W: batch too large for one launch (max 4096)");
-    hipLaunchKernelGGL(k_sddmm, dim3(blocks_for(p.nseg)), dim3(256), lds, st, a);
+    ProfScope ps("sddmm", st);
+    const int64_t gT_bytes = p.cols * B * 4;
+    SArgs a{p.seg, p.nseg, p.idx, xT, gT, B, gw, acc_in,
+            gT_bytes < (int64_t)OOB_OFFSET ? (uint32_t)gT_bytes : 0u};
+    const dim3 grid(blocks_for(p.nseg)), block(256);
+    if (gT_bytes < (int64_t)OOB_OFFSET && B % 4 == 0 && B <= 2048 && aligned16(xT) && aligned16(gT)) {
+        const int64_t nq = B / 4;
+        const int u = gather_u();
+        if (nq <= 1) hipLaunchKernelGGL((k_sddmm_v4<1, 1, 1>), grid, block, 0, st, a);
+        else if (nq <= 2) hipLaunchKernelGGL((k_sddmm_v4<2, 1, 2>), grid, block, 0, st, a);
+        else if (nq <= 4) hipLaunchKernelGGL((k_sddmm_v4<4, 1, 4>), grid, block, 0, st, a);
+        else if (nq <= 8) hipLaunchKernelGGL((k_sddmm_v4<8, 1, 8>), grid, block, 0, st, a);
+        else if (nq <= 16) {
+            if (u >= 16) hipLaunchKernelGGL((k_sddmm_v4<16, 1, 16>), grid, block, 0, st, a);
+            else if (u >= 8) hipLaunchKernelGGL((k_sddmm_v4<16, 1, 8>), grid, block, 0, st, a);
+            else hipLaunchKernelGGL((k_sddmm_v4<16, 1, 4>), grid, block, 0, st, a);
+        } else if (nq <= 32) hipLaunchKernelGGL((k_sddmm_v4<16, 2, 4>), grid, block, 0, st, a);
+        else if (nq <= 64) hipLaunchKernelGGL((k_sddmm_v4<16, 4, 2>), grid, block, 0, st, a);
+        else if (nq <= 128) hipLaunchKernelGGL((k_sddmm_v4<16, 8, 1>), grid, block, 0, st, a);
+        else if (nq <= 256) hipLaunchKernelGGL((k_sddmm_v4<16, 16, 1>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((k_sddmm_v4<16, 32, 1>), grid, block, 0, st, a);
+    } else {
+        const size_t lds = sizeof(float) * (size_t)WAVES * (size_t)B;
+        if (lds > 64 * 1024) throw_error(1, "sampled grad-W: batch too large for one launch (max 4096)");
+        hipLaunchKernelGGL(k_sddmm, grid, block, lds, st, a);
+    }
     SILI_HIP(hipGetLastError());
 }
 
 void launch_sddmm_b4(const Block4Plan &p, const uint32_t *, const float *xT, const float *gT,
                      int64_t B, float *gw, hipStream_t st) {
     if (p.nseg == 0) return;
+    ProfScope ps("sddmm_b4", st);
     SBArgs a{p.seg, p.nseg, p.idx, p.rows, p.cols, xT, gT, B, gw};
     const size_t lds = sizeof(float) * (size_t)WAVES * 4u * (size_t)B;
     if (lds > 64 * 1024) throw_error(1, "block4 sampled grad-W: batch too large (max 1024)");
@@ -533,13 +919,22 @@ void launch_sddmm_b4(const Block4Plan &p, const uint32_t *, const float *xT, con
 void launch_transpose(const float *src, int64_t B, int64_t n, float *dst, float *acc,
                       hipStream_t st) {
     if (B == 0 || n == 0) return;
-    const dim3 grid((unsigned)((n + 63) / 64), (unsigned)((B + 63) / 64));
+    ProfScope ps("transpose", st);
+    const dim3 grid((unsigned)((n + 15) / 16), (unsigned)((B + 63) / 64));
     hipLaunchKernelGGL(k_transpose, grid, dim3(256), 0, st, src, B, n, dst, acc);
+    SILI_HIP(hipGetLastError());
+}
+
+void launch_rowabs(const float *xT, int64_t B, int64_t n, float *acc, hipStream_t st) {
+    if (B == 0 || n == 0) return;
+    ProfScope ps("rowabs", st);
+    hipLaunchKernelGGL(k_rowabs, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, xT, B, n, acc);
     SILI_HIP(hipGetLastError());
 }
 
 void launch_colabs(const float *src, int64_t B, int64_t n, float *acc, hipStream_t st) {
     if (B == 0 || n == 0) return;
+    ProfScope ps("colabs", st);
     hipLaunchKernelGGL(k_colabs, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src, B, n, acc);
     SILI_HIP(hipGetLastError());
 }
@@ -547,6 +942,7 @@ void launch_colabs(const float *src, int64_t B, int64_t n, float *acc, hipStream
 void launch_densify(const int32_t *ptrs, const int32_t *idx, const float *vals, int64_t B,
                     int64_t n, float *dst, float *acc_abs, bool mark_explicit, hipStream_t st) {
     if (B == 0) return;
+    ProfScope ps("densify", st);
     hipLaunchKernelGGL(k_densify, dim3((unsigned)B), dim3(256), 0, st, ptrs, idx, vals, B, n, dst,
                        acc_abs, mark_explicit ? 1 : 0);
     SILI_HIP(hipGetLastError());

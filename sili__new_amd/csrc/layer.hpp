@@ -3,6 +3,7 @@
 
 #include "common.hpp"
 
+#include <string>
 #include <utility>
 #include <vector>
 
@@ -65,6 +66,43 @@ struct DBlock4 {
     }
 };
 
+// Per-kernel event timing of one layer (see ProfScope in common.hpp).
+struct Profiler {
+    bool enabled = false;
+    struct Rec {
+        std::string name;
+        hipEvent_t a, b;
+    };
+    std::vector<Rec> recs;
+    std::vector<hipEvent_t> pool;
+    Profiler() = default;
+    Profiler(const Profiler &) = delete;
+    Profiler &operator=(const Profiler &) = delete;
+    ~Profiler() {
+        for (auto &r : recs) { (void)hipEventDestroy(r.a); (void)hipEventDestroy(r.b); }
+        for (auto e : pool) (void)hipEventDestroy(e);
+    }
+    hipEvent_t take() {
+        if (!pool.empty()) {
+            hipEvent_t e = pool.back();
+            pool.pop_back();
+            return e;
+        }
+        hipEvent_t e;
+        SILI_HIP(hipEventCreate(&e));
+        return e;
+    }
+};
+
+// Makes L's profiler the target of ProfScopes issued by this thread while in
+// scope, and names the entry point ("fwd", "bwd", ...).
+struct ProfCtx {
+    ProfCtx(struct Layer &L, const char *op);
+    ~ProfCtx();
+    Profiler *prev;
+    ProfOp op;
+};
+
 // Scratch that device builders need for one call.
 struct Scratch {
     DevBuf<uint8_t> temp;    // rocprim temporary storage
@@ -87,9 +125,11 @@ struct Layer {
     DevBuf<float> acc_in, acc_grad;
     // per-call workspace (grown on demand)
     DevBuf<float> ws_xT, ws_gT, ws_out;
+    int64_t xT_cached_batch = 0;  // > 0: ws_xT holds the last forward_dense input, feature-major
     Scratch scratch;
-    uint32_t seg_len = 512;     // max entries per decode work item (scattered)
-    uint32_t seg_len_b4 = 128;  // max tiles per decode work item (block4)
+    Profiler prof;
+    uint32_t seg_len = 512;     // max index bytes per decode work item (scattered)
+    uint32_t seg_len_b4 = 128;  // max block-index bytes per decode work item (block4)
 };
 
 // ---- builders (build.hip) ---------------------------------------------------

@@ -19,21 +19,48 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Inclusive prefix sum over the 64 lanes.
+// DPP lane moves (gfx9 encodings).  Lanes whose source falls outside the
+// row (or rows not selected by ROW_MASK) read 0.  Call with all lanes active.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xF, false);
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __builtin_bit_cast(float, dpp_u32<CTRL, ROW_MASK>(__builtin_bit_cast(uint32_t, x)));
+}
+constexpr int DPP_ROW_SHR1 = 0x111, DPP_ROW_SHR2 = 0x112, DPP_ROW_SHR4 = 0x114, DPP_ROW_SHR8 = 0x118;
+constexpr int DPP_ROW_BCAST15 = 0x142, DPP_ROW_BCAST31 = 0x143;
+
+// Inclusive prefix sum over the 64 lanes: Hillis-Steele inside each 16-lane
+// row (row_shr 1,2,4,8), then row_bcast15 / row_bcast31 carry across rows.
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
-    const uint32_t lane = lane_id();
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t t = __shfl_up(x, d, 64);
-        if (lane >= (uint32_t)d) x += t;
-    }
+    x += dpp_u32<DPP_ROW_SHR1>(x);
+    x += dpp_u32<DPP_ROW_SHR2>(x);
+    x += dpp_u32<DPP_ROW_SHR4>(x);
+    x += dpp_u32<DPP_ROW_SHR8>(x);
+    x += dpp_u32<DPP_ROW_BCAST15, 0xA>(x);
+    x += dpp_u32<DPP_ROW_BCAST31, 0xC>(x);
     return x;
 }
 
+// Sum over each aligned group of BL lanes (BL a power of two <= 64); the
+// group's total lands in its last lane (lane % BL == BL-1).
+template <int BL>
+__device__ __forceinline__ float group_sum_last(float v) {
+    if constexpr (BL >= 2) v += dpp_f32<DPP_ROW_SHR1>(v);
+    if constexpr (BL >= 4) v += dpp_f32<DPP_ROW_SHR2>(v);
+    if constexpr (BL >= 8) v += dpp_f32<DPP_ROW_SHR4>(v);
+    if constexpr (BL >= 16) v += dpp_f32<DPP_ROW_SHR8>(v);
+    if constexpr (BL >= 32) v += dpp_f32<DPP_ROW_BCAST15, 0xA>(v);
+    if constexpr (BL >= 64) v += dpp_f32<DPP_ROW_BCAST31, 0xC>(v);
+    return v;
+}
+
+// Sum over all 64 lanes, broadcast to every lane.
 __device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) x += __shfl_xor(x, d, 64);
-    return x;
+    x = group_sum_last<64>(x);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
 }
 
 // One 64-byte window of a ULEB128 delta stream.  The window starts at a
@@ -56,22 +83,25 @@ __device__ __forceinline__ Chunk decode_chunk(const uint8_t *__restrict__ idx, u
     const uint32_t b = (p < end) ? (uint32_t)idx[p] : 0x80u;
     const bool term = (b & 0x80u) == 0u;
     const uint64_t T = __ballot(term);
-    const uint64_t below = lane ? (~0ull >> (64u - lane)) : 0ull;
-    const uint64_t prevT = T & below;
-    // first byte of this lane's varint: one past the previous terminator
-    const uint32_t s = prevT ? (64u - (uint32_t)__clzll(prevT)) : 0u;
-    const uint32_t len = lane - s + 1u;
-    const uint32_t b1 = __shfl_up(b, 1, 64), b2 = __shfl_up(b, 2, 64);
-    const uint32_t b3 = __shfl_up(b, 3, 64), b4 = __shfl_up(b, 4, 64);
+    // continuation flags of the 4 bytes before this lane, bit 3 = lane-1; the
+    // window starts at a varint boundary, so positions before it read as 0
+    const uint64_t E = (~T) << 4;
+    const uint32_t q = (uint32_t)(E >> lane) & 0xFu;
+    const uint32_t t = ~q & 0xFu;                             // first non-continuation from the top
+    const uint32_t run = t ? (uint32_t)__builtin_clz(t) - 28u : 4u;  // preceding bytes of this varint
     // little-endian 7-bit groups: the terminator holds the most significant one
+    const uint32_t b1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)b, 0x138, 0xF, 0xF, false);   // wave_shr:1
+    const uint32_t b2 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)b1, 0x138, 0xF, 0xF, false);
+    const uint32_t b3 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)b2, 0x138, 0xF, 0xF, false);
+    const uint32_t b4 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)b3, 0x138, 0xF, 0xF, false);
     uint32_t v = b & 0x7Fu;
-    v = len > 1u ? ((v << 7) | (b1 & 0x7Fu)) : v;
-    v = len > 2u ? ((v << 7) | (b2 & 0x7Fu)) : v;
-    v = len > 3u ? ((v << 7) | (b3 & 0x7Fu)) : v;
-    v = len > 4u ? ((v << 7) | (b4 & 0x7Fu)) : v;
+    v = run >= 1u ? ((v << 7) | (b1 & 0x7Fu)) : v;
+    v = run >= 2u ? ((v << 7) | (b2 & 0x7Fu)) : v;
+    v = run >= 3u ? ((v << 7) | (b3 & 0x7Fu)) : v;
+    v = run >= 4u ? ((v << 7) | (b4 & 0x7Fu)) : v;
     v = term ? v : 0u;
     ch.col = carry + wave_incl_scan(v);
-    ch.rank = (uint32_t)__popcll(prevT);
+    ch.rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(T >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)T, 0u));
     ch.term = term;
     ch.T = T;
     return ch;
@@ -86,6 +116,59 @@ __device__ __forceinline__ uint32_t chunk_advance(const Chunk &ch, uint32_t &pos
     ebase += (uint32_t)__popcll(ch.T);
     return carry;
 }
+
+// LDS copy of one segment's index bytes and value bytes (one per wave).
+struct alignas(16) SegStage {
+    uint32_t idx[SEG_BYTES_MAX / 4 + 4];
+    uint32_t val[SEG_BYTES_MAX / 4 + 4];
+};
+
+// Copy bytes [begin, end) of a device buffer into dst as aligned dwords
+// (every load in flight at once); `off` = position of `begin` in dst.  The
+// device buffers carry >= 4 bytes of padding, so the last dword is in bounds.
+__device__ __forceinline__ void stage_words(uint32_t *dst, const uint8_t *src_bytes, uint32_t begin,
+                                            uint32_t end, uint32_t &off) {
+    const uint32_t b0 = begin & ~3u;
+    off = begin - b0;
+    uint32_t nw = (end - b0 + 3u) >> 2;
+    nw = nw < SEG_BYTES_MAX / 4 + 4 ? nw : SEG_BYTES_MAX / 4 + 4;
+    const uint32_t *src = reinterpret_cast<const uint32_t *>(src_bytes + b0);
+    for (uint32_t i = lane_id(); i < nw; i += 64u) dst[i] = src[i];
+}
+
+// Stage a segment and return the LDS byte views; pos/end become relative.
+struct StagedSeg {
+    const uint8_t *idx;  // idx[0] = first index byte of the segment
+    const uint8_t *val;  // val[e - elem_begin] = value byte of entry e
+    uint32_t end;        // index bytes in the segment
+};
+__device__ __forceinline__ StagedSeg stage_segment(SegStage &S, const uint8_t *idx, const uint8_t *val,
+                                                   const SegDesc &sd) {
+    uint32_t ioff = 0, voff = 0;
+    stage_words(S.idx, idx, sd.byte_begin, sd.byte_end, ioff);
+    if (val) stage_words(S.val, val, sd.elem_begin, sd.elem_end, voff);
+    wave_lds_sync();
+    StagedSeg g;
+    g.idx = reinterpret_cast<const uint8_t *>(S.idx) + ioff;
+    g.val = reinterpret_cast<const uint8_t *>(S.val) + voff;
+    const uint32_t n = sd.byte_end - sd.byte_begin;
+    g.end = n < SEG_BYTES_MAX ? n : SEG_BYTES_MAX;
+    return g;
+}
+
+// Buffer resource over [base, base + bytes) for raw buffer loads; reads at
+// offsets >= bytes return 0 (hardware range check).  bytes < 2^31.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ float4 buffer_load_f4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ float buffer_load_f1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+// An offset no buffer used here reaches: loads from it return 0.
+constexpr uint32_t OOB_OFFSET = 0x80000000u;
 
 // S(row, ent) = sum_k row_scale[row,k] * ent_scale[ent,k]; NULL = all ones
 // (rank 1 only).  Components k >= 1 accumulate with fma.
