@@ -184,8 +184,8 @@ def cpu_baseline(wl, seconds):
 def main():
     a = parse()
     if a.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; multi-GPU sharding is designed "
-                                   "(DESIGN.md) but not built -- run with --gpus 1"}))
+        print(json.dumps({"error": "this build runs on one GPU: the layer is sharded by output "
+                                   "columns only on paper, no multi-GPU path is built -- run with --gpus 1"}))
         sys.exit(2)
     import sili__new_amd as hip
     from sili__new_amd.synth import make_config
