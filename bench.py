@@ -44,6 +44,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--verbose", action="store_true")
+    p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                   help="only run 3 device-to-device copies of MIB MiB (HBM counter calibration)")
     return p.parse_args()
 
 
@@ -80,6 +82,25 @@ class Hip:
 
     def sync(self):
         assert self.lib.hipDeviceSynchronize() == 0
+
+    def copy_probe(self, mib):
+        """Device-to-device copies of a known size: the runtime's blit kernel
+        reads and writes exactly `mib` MiB each, which scales the FETCH_SIZE /
+        WRITE_SIZE counters to bytes."""
+        L = self.lib
+        L.hipMalloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+        L.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+        L.hipMemset.argtypes = [C.c_void_p, C.c_int, C.c_size_t]
+        L.hipFree.argtypes = [C.c_void_p]
+        n = mib << 20
+        a, b = C.c_void_p(), C.c_void_p()
+        assert L.hipMalloc(C.byref(a), n) == 0 and L.hipMalloc(C.byref(b), n) == 0
+        assert L.hipMemset(a, 1, n) == 0
+        for _ in range(3):
+            assert L.hipMemcpy(b, a, n, 3) == 0  # hipMemcpyDeviceToDevice
+        self.sync()
+        assert L.hipFree(a) == 0 and L.hipFree(b) == 0
+        return n
 
 
 class CAbi:
@@ -127,6 +148,20 @@ class CAbi:
         return {buf[i].name.decode(): (buf[i].count, buf[i].total_ms) for i in range(n.value)}
 
 
+def measured_traffic(label, config):
+    """HBM-side bytes per launch of kernel `label`, from the committed
+    rocprofv3 --pmc summary of this workload (FETCH_SIZE and WRITE_SIZE
+    scaled by a copy kernel of known size).  None when no summary exists."""
+    path = os.path.join(ROOT, "profiles", f"c{config}_step_pmc_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic_bytes" and f[1] == label:
+            return int(f[2])
+    return None
+
+
 def algorithmic(info, n_in, n_out, B):
     """Algorithmic bytes per launch of each kernel (per-unit figures:
     Bv = 1 B/synapse, Bi = exact ULEB bytes, Bp = 8 B/row, Bs = 4 B per
@@ -137,6 +172,9 @@ def algorithmic(info, n_in, n_out, B):
         "fwd:gather": Bv + Bi + Bp + Bs + 4 * B * n_in + 4 * B * n_out,
         "bwd:gather": Bv + Bi + Bp + Bs + 4 * B * n_out + 4 * B * n_in,
         "bwd:sddmm": Bi + Bp + 4 * B * n_in + 4 * B * n_out + 4 * nnz,
+        # fused grad-input + grad-W: W (values, index, row starts, scales),
+        # gT and xT read once, dX and GW written once
+        "bwd:gather_gradw": Bv + Bi + Bp + Bs + 4 * B * n_out + 4 * B * n_in + 4 * B * n_in + 4 * nnz,
         "fwd:transpose": 8 * B * n_in,
         "bwd:transpose": 8 * B * n_out,
     }
@@ -187,6 +225,10 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU: the layer is sharded by output "
                                    "columns only on paper, no multi-GPU path is built -- run with --gpus 1"}))
         sys.exit(2)
+    if a.copy_probe:
+        n = Hip().copy_probe(a.copy_probe)
+        print(json.dumps({"copy_probe_bytes": n, "copies": 3}), flush=True)
+        return
     import sili__new_amd as hip
     from sili__new_amd.synth import make_config
 
@@ -284,6 +326,8 @@ def main():
     achieved = dom_bytes / (dom_avg_ms * 1e-3) / 1e9 if dom_bytes else None
 
     nnz = info["nnz_scattered"]
+    # one step's algorithmic bytes: forward + grad-input + sampled grad-W,
+    # each op counted as if run alone (the fused backward moves less)
     step_bytes = alg["fwd:gather"] + alg["bwd:gather"] + alg["bwd:sddmm"]
     gnnz = nnz / (ms_step * 1e-3) / 1e9
     step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
@@ -321,7 +365,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 5) if achieved else None,
-            "traffic": None,
+            "traffic": measured_traffic(dom_name, a.config),
             "avg_launch_ms": round(dom_avg_ms, 5),
             "algorithmic_bytes": dom_bytes,
         },

@@ -231,9 +231,12 @@ int sili_export_absolute(sili_layer *layer, int32_t *ptrs, int32_t *indices, flo
 
 /* ---- measurement (no reference counterpart: the reference is timed with
  * ad-hoc std::chrono harnesses, scripts/bench_block4_vs_dense_fp4.cpp:58-68) --
- * While enabled, every kernel the layer launches is bracketed by a hipEvent
- * pair on the stream it runs on; sili_profile_read synchronizes, aggregates
- * per "<op>:<kernel>" name in first-seen order, and clears the records. */
+ * While enabled, every hot-path kernel the layer launches carries a hipEvent
+ * pair that the runtime stamps with that dispatch's own begin and end
+ * (hipExtLaunchKernel on the stream it runs on: the kernel's time alone, no
+ * queue gaps); sili_profile_read synchronizes, aggregates per
+ * "<op>:<kernel>" name in first-seen order, and clears the records.  The
+ * backward with grad-W buffers reports its fused pass as "bwd:gather_gradw". */
 typedef struct {
     char name[56];
     int64_t count;

@@ -238,7 +238,7 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
     rowid.ensure((size_t)N + 1);
     zero_flag(L);
     if (N > 0) {
-        hipLaunchKernelGGL(k_entry_len, dim3(nblk(N)), dim3(TPB), 0, st, d_ptrs, rows, ncols, d_cols, N,
+        launch(k_entry_len, dim3(nblk(N)), dim3(TPB), 0, st, d_ptrs, rows, ncols, d_cols, N,
                            len.p, rowid.p, L.scratch.flag.p);
         SILI_HIP(hipGetLastError());
     }
@@ -257,11 +257,11 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
     segcnt.ensure((size_t)rows + 1);
     segoff.ensure((size_t)rows + 1);
     if (N > 0) {
-        hipLaunchKernelGGL(k_entry_write, dim3(nblk(N)), dim3(TPB), 0, st, d_ptrs, rowid.p, d_cols, N,
+        launch(k_entry_write, dim3(nblk(N)), dim3(TPB), 0, st, d_ptrs, rowid.p, d_cols, N,
                            pos.p, idx.p);
         SILI_HIP(hipGetLastError());
     }
-    hipLaunchKernelGGL(k_row_starts, dim3(nblk(rows + 1)), dim3(TPB), 0, st, d_ptrs, rows, N, pos.p,
+    launch(k_row_starts, dim3(nblk(rows + 1)), dim3(TPB), 0, st, d_ptrs, rows, N, pos.p,
                        total, byte_start.p, elem_start.p, seg_len, emit_empty ? 1 : 0, segcnt.p);
     SILI_HIP(hipGetLastError());
     SILI_HIP(hipMemsetAsync(segcnt.p + rows, 0, sizeof(uint32_t), st));
@@ -273,7 +273,7 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
     seg.ensure((size_t)nseg + 1);
     zero_flag(L);
     if (rows > 0) {
-        hipLaunchKernelGGL(k_seg_write, dim3(nblk(rows)), dim3(TPB), 0, st, d_ptrs, rows, byte_start.p,
+        launch(k_seg_write, dim3(nblk(rows)), dim3(TPB), 0, st, d_ptrs, rows, byte_start.p,
                            d_cols, pos.p, segoff.p, seg_len, emit_empty ? 1 : 0, seg.p, L.scratch.flag.p);
         SILI_HIP(hipGetLastError());
     }
@@ -361,15 +361,15 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
     tbytes.ensure((size_t)N + 1);
     ptrs.ensure((size_t)src.cols + 1);
     if (N > 0) {
-        hipLaunchKernelGGL(k_iota, dim3(nblk(N)), dim3(TPB), 0, st, perm_in.p, N);
+        launch(k_iota, dim3(nblk(N)), dim3(TPB), 0, st, perm_in.p, N);
         // stable by column: entries keep ascending row order within a column
         device_sort_pairs_u32(L, d_cols, keys_out.p, perm_in.p, perm.p, N,
                               bits_for((uint64_t)std::max<int64_t>(src.cols - 1, 1)));
-        hipLaunchKernelGGL(k_gather_u32, dim3(nblk(N)), dim3(TPB), 0, st, d_rows, perm.p, N, trows.p);
-        hipLaunchKernelGGL(k_gather_u8, dim3(nblk(N)), dim3(TPB), 0, st, src.val.p, perm.p, N, tbytes.p);
+        launch(k_gather_u32, dim3(nblk(N)), dim3(TPB), 0, st, d_rows, perm.p, N, trows.p);
+        launch(k_gather_u8, dim3(nblk(N)), dim3(TPB), 0, st, src.val.p, perm.p, N, tbytes.p);
         SILI_HIP(hipGetLastError());
     }
-    hipLaunchKernelGGL(k_ptrs_from_sorted, dim3(nblk(src.cols + 1)), dim3(TPB), 0, st, keys_out.p, N,
+    launch(k_ptrs_from_sorted, dim3(nblk(src.cols + 1)), dim3(TPB), 0, st, keys_out.p, N,
                        src.cols, ptrs.p);
     SILI_HIP(hipGetLastError());
     const Encoded e = encode_rows(L, src.cols, src.rows, N, ptrs.p, trows.p, L.seg_len, true, dst.byte_start,
@@ -394,7 +394,7 @@ static void build_b4_orientation(Layer &L, DBlock4 &dst, int64_t N, int64_t brow
     hipStream_t st = L.stream;
     DevBuf<uint32_t> ptrs;
     ptrs.ensure((size_t)brows + 1);
-    hipLaunchKernelGGL(k_ptrs_from_sorted, dim3(nblk(brows + 1)), dim3(TPB), 0, st, d_major, N, brows,
+    launch(k_ptrs_from_sorted, dim3(nblk(brows + 1)), dim3(TPB), 0, st, d_major, N, brows,
                        ptrs.p);
     SILI_HIP(hipGetLastError());
     const Encoded e = encode_rows(L, brows, bcols, N, ptrs.p, d_minor, L.seg_len_b4, false, dst.byte_start,
@@ -409,7 +409,7 @@ static void build_b4_orientation(Layer &L, DBlock4 &dst, int64_t N, int64_t brow
     dst.has_split = e.has_split;
     dst.tiles.ensure((size_t)N * 16u + 64);
     if (N > 0) {
-        hipLaunchKernelGGL(k_gather_tiles, dim3(nblk(N)), dim3(TPB), 0, st, d_src_tiles, d_perm, N,
+        launch(k_gather_tiles, dim3(nblk(N)), dim3(TPB), 0, st, d_src_tiles, d_perm, N,
                            transpose ? 1 : 0, dst.tiles.p);
         SILI_HIP(hipGetLastError());
     }
@@ -435,13 +435,13 @@ void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_
         const int64_t maj_ext = canon ? brows : bcols, mnr_ext = canon ? bcols : brows;
         zero_flag(L);
         if (N > 0) {
-            hipLaunchKernelGGL(k_tile_keys, dim3(nblk(N)), dim3(TPB), 0, st, maj, mnr, N,
+            launch(k_tile_keys, dim3(nblk(N)), dim3(TPB), 0, st, maj, mnr, N,
                                (uint64_t)mnr_ext, maj_ext, key.p, L.scratch.flag.p);
-            hipLaunchKernelGGL(k_iota, dim3(nblk(N)), dim3(TPB), 0, st, perm_in.p, N);
+            launch(k_iota, dim3(nblk(N)), dim3(TPB), 0, st, perm_in.p, N);
             SILI_HIP(hipGetLastError());
             device_sort_pairs_u64(L, key.p, key_sorted.p, perm_in.p, perm.p, N,
                                   bits_for((uint64_t)maj_ext * (uint64_t)mnr_ext));
-            hipLaunchKernelGGL(k_split_keys, dim3(nblk(N)), dim3(TPB), 0, st, key_sorted.p, N,
+            launch(k_split_keys, dim3(nblk(N)), dim3(TPB), 0, st, key_sorted.p, N,
                                (uint64_t)mnr_ext, major.p, minor.p, L.scratch.flag.p);
             SILI_HIP(hipGetLastError());
         }
@@ -460,10 +460,10 @@ void refresh_nonfinite(Layer &L) {
     hipStream_t st = L.stream;
     zero_flag(L);
     if (L.W.nnz > 0)
-        hipLaunchKernelGGL(k_scan_nan_codes, dim3(nblk(L.W.nnz)), dim3(TPB), 0, st, L.W.val.p, L.W.nnz, 1,
+        launch(k_scan_nan_codes, dim3(nblk(L.W.nnz)), dim3(TPB), 0, st, L.W.val.p, L.W.nnz, 1,
                            L.scratch.flag.p);
     if (L.B4.ntiles > 0)
-        hipLaunchKernelGGL(k_scan_nan_codes, dim3(nblk(L.B4.ntiles * 16)), dim3(TPB), 0, st, L.B4.tiles.p,
+        launch(k_scan_nan_codes, dim3(nblk(L.B4.ntiles * 16)), dim3(TPB), 0, st, L.B4.tiles.p,
                            L.B4.ntiles * 16, 0, L.scratch.flag.p);
     SILI_HIP(hipGetLastError());
     int h = 0;

@@ -23,20 +23,22 @@ namespace {
 thread_local std::string g_last_error;
 thread_local Profiler *t_prof = nullptr;
 thread_local const char *t_op = "";
+thread_local const char *t_kernel = nullptr;
 }  // namespace
 
 ProfOp::ProfOp(const char *op) : prev(t_op) { t_op = op; }
 ProfOp::~ProfOp() { t_op = prev; }
 
-ProfScope::ProfScope(const char *kernel, hipStream_t s) : slot(-1), st(s) {
-    if (!t_prof || !t_prof->enabled) return;
-    Profiler::Rec r{std::string(t_op) + ":" + kernel, t_prof->take(), t_prof->take()};
-    SILI_HIP(hipEventRecord(r.a, s));
-    slot = (int)t_prof->recs.size();
+ProfScope::ProfScope(const char *kernel, hipStream_t) : prev(t_kernel) { t_kernel = kernel; }
+ProfScope::~ProfScope() { t_kernel = prev; }
+
+bool prof_next(hipEvent_t *start, hipEvent_t *stop) {
+    if (!t_prof || !t_prof->enabled || !t_kernel) return false;
+    Profiler::Rec r{std::string(t_op) + ":" + t_kernel, t_prof->take(), t_prof->take()};
+    *start = r.a;
+    *stop = r.b;
     t_prof->recs.push_back(std::move(r));
-}
-ProfScope::~ProfScope() {
-    if (slot >= 0 && t_prof) (void)hipEventRecord(t_prof->recs[(size_t)slot].b, st);
+    return true;
 }
 
 ProfCtx::ProfCtx(Layer &L, const char *op) : prev(t_prof), op(op) { t_prof = &L.prof; }
@@ -96,7 +98,7 @@ __global__ void k_i32_to_u32(const int32_t *__restrict__ s, int64_t n, uint32_t 
 void fill(float *p, int64_t n, float v, hipStream_t st) {
     if (n <= 0) return;
     ProfScope ps("fill", st);
-    hipLaunchKernelGGL(k_fill_f32, dim3(nblk(n)), dim3(TPB), 0, st, p, n, v);
+    launch(k_fill_f32, dim3(nblk(n)), dim3(TPB), 0, st, p, n, v);
     SILI_HIP(hipGetLastError());
 }
 
@@ -150,18 +152,18 @@ void build_from_host_csr(Layer &L, const int32_t *ptrs, const int32_t *idx, cons
     DevBuf<float> dw, dimp;
     upload(dptrs_i, ptrs, (size_t)L.n_in + 1, st);
     dptrs.ensure((size_t)L.n_in + 1);
-    hipLaunchKernelGGL(k_i32_to_u32, dim3(nblk(L.n_in + 1)), dim3(TPB), 0, st, dptrs_i.p, L.n_in + 1, dptrs.p);
+    launch(k_i32_to_u32, dim3(nblk(L.n_in + 1)), dim3(TPB), 0, st, dptrs_i.p, L.n_in + 1, dptrs.p);
     dcols.ensure((size_t)nnz + 1);
     dbytes.ensure((size_t)nnz + 1);
     if (nnz > 0) {
         upload(didx_i, idx, (size_t)nnz, st);
-        hipLaunchKernelGGL(k_i32_to_u32, dim3(nblk(nnz)), dim3(TPB), 0, st, didx_i.p, nnz, dcols.p);
+        launch(k_i32_to_u32, dim3(nblk(nnz)), dim3(TPB), 0, st, didx_i.p, nnz, dcols.p);
         if (bytes_h) {
             SILI_HIP(hipMemcpyAsync(dbytes.p, bytes_h, (size_t)nnz, hipMemcpyHostToDevice, st));
         } else {
             upload(dw, w_h, (size_t)nnz, st);
             if (imp_h) upload(dimp, imp_h, (size_t)nnz, st);
-            hipLaunchKernelGGL(k_quantize, dim3(nblk(nnz)), dim3(TPB), 0, st, dw.p, imp_h ? dimp.p : nullptr,
+            launch(k_quantize, dim3(nblk(nnz)), dim3(TPB), 0, st, dw.p, imp_h ? dimp.p : nullptr,
                                nnz, dbytes.p);
         }
         SILI_HIP(hipGetLastError());
@@ -261,10 +263,13 @@ void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float 
         else launch_colabs(x, B, L.n_in, L.acc_in.p, st);
     }
     if (L.W.has_split) fill(dx, B * L.n_in, 0.0f, st);
-    launch_gather(L.W.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
+    // grad-input and grad-W read the same gT row per synapse: one fused pass
+    const bool fused = gw_s && launch_bwd_fused(L.W.plan(), canon_scales(L), gT, xT, B, dx, L.n_in, gw_s,
+                                                L.acc_in.p, st);
+    if (!fused) launch_gather(L.W.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
     if (L.B4.ntiles > 0)
         launch_gather_b4(L.B4.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
-    if (gw_s) launch_sddmm(L.W.plan(), xT, gT, B, gw_s, L.acc_in.p, st);
+    if (gw_s && !fused) launch_sddmm(L.W.plan(), xT, gT, B, gw_s, L.acc_in.p, st);
     if (gw_b && L.B4.ntiles > 0) launch_sddmm_b4(L.B4.plan(), nullptr, xT, gT, B, gw_b, st);
 }
 

@@ -15,10 +15,12 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <tuple>
 
 namespace sili {
 
@@ -32,20 +34,41 @@ void hip_check(hipError_t e, const char *what);
 #define SILI_HIP(expr) ::sili::hip_check((expr), #expr)
 
 // ---- measurement ------------------------------------------------------------
-// When a layer's profiler is enabled, every kernel launch issued inside an
-// entry point is bracketed by a hipEvent pair on the stream it runs on and
-// accounted under "<op>:<kernel>" (sili_profile_read).  Disabled: no-op.
+// When a layer's profiler is enabled, every kernel launched through launch()
+// inside a ProfScope carries a hipEvent pair that the runtime stamps with that
+// dispatch's own begin and end (hipExtLaunchKernel), accounted under
+// "<op>:<kernel>" (sili_profile_read).  The times are those of the kernel
+// alone, without the queue gaps a separate hipEventRecord marker would add.
+// Disabled: launch() is a plain hipLaunchKernelGGL.
 struct ProfOp {              // names the entry point for the launches below it
     explicit ProfOp(const char *op);
     ~ProfOp();
     const char *prev;
 };
-struct ProfScope {           // brackets one kernel launch
+struct ProfScope {           // names the kernel(s) launched while it lives
     ProfScope(const char *kernel, hipStream_t st);
     ~ProfScope();
-    int slot;
-    hipStream_t st;
+    const char *prev;
 };
+// Events for the next launch when it is profiled (false: not profiled).
+bool prof_next(hipEvent_t *start, hipEvent_t *stop);
+
+template <typename... KArgs, typename... Args>
+void launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, uint32_t shmem, hipStream_t st,
+            Args... args) {
+    static_assert(sizeof...(KArgs) == sizeof...(Args), "kernel argument count");
+    hipEvent_t a, b;
+    if (!prof_next(&a, &b)) {
+        hipLaunchKernelGGL(kernel, grid, block, shmem, st, static_cast<KArgs>(args)...);
+        return;
+    }
+    std::tuple<KArgs...> tup{static_cast<KArgs>(args)...};
+    std::apply([&](auto &...e) {
+        void *ptrs[] = {static_cast<void *>(&e)...};
+        SILI_HIP(hipExtLaunchKernel(reinterpret_cast<const void *>(kernel), grid, block, ptrs, shmem,
+                                    st, a, b, 0));
+    }, tup);
+}
 
 // ---- decode work item ------------------------------------------------------
 // One contiguous run of a row's entries, starting at a varint boundary with a
@@ -139,6 +162,11 @@ void launch_gather_b4(const Block4Plan &p, const ScaleView &sc, const float *in,
                       float *out, int64_t out_ld, int64_t nb, int skip, hipStream_t st);
 // gw[e] = sum_b xT[row*B+b] * gT[col*B+b] over the canonical store; when
 // acc_in != NULL also acc_in[row] += sum_b |xT[row*B+b]| for every row.
+// Fused grad-input gather + sampled grad-W over the canonical store (one
+// decode, one gT load per synapse).  Returns false, launching nothing, when
+// the operands do not fit the fused kernel (B % 4, B > 512, alignment).
+bool launch_bwd_fused(const GatherPlan &p, const ScaleView &sc, const float *gT, const float *xT,
+                      int64_t B, float *dx, int64_t dx_ld, float *gw, float *acc_in, hipStream_t st);
 void launch_sddmm(const GatherPlan &p, const float *xT, const float *gT, int64_t B, float *gw,
                   float *acc_in, hipStream_t st);
 // acc[j] += sum_b |xT[j*B+b]| (feature-major input).

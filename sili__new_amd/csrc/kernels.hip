@@ -569,6 +569,121 @@ __global__ __launch_bounds__(256) void k_sddmm_v4(SArgs a) {
     }
 }
 
+struct FArgs {
+    const SegDesc *seg;
+    int64_t nseg;
+    const uint8_t *idx;
+    const uint8_t *val;
+    ScaleView sc;
+    const float *gT;    // [cols, B] feature-major upstream gradient
+    uint32_t gT_bytes;
+    const float *xT;    // [rows, B] feature-major forward input
+    int64_t B;
+    float *dx;          // [B, dx_ld] batch-major
+    int64_t dx_ld;
+    float *gw;          // one value per stored synapse, elem order
+    float *acc_in;      // optional: acc_in[row] += sum_b |xT[row,b]|
+};
+
+// Fused grad-input + nnz-sampled grad-W over the canonical store: one decode
+// of the segment, one load of gT[col] per entry, used twice --
+//   dx[b,row] += w_e * gT[col_e,b]        (the grad-input gather)
+//   gw[e]      = sum_b xT[row,b]*gT[col_e,b] (the sampled grad-W)
+// Lane layout as k_gather_v4 (BL lanes per entry, float4 chunks of the
+// batch), xT[row] in registers as k_sddmm_v4.  Needs B % 4 == 0, 16-byte
+// aligned xT / gT and B <= 64*KB*4/ (64/BL) -- the launcher checks.
+template <int BL, int KB, int U>
+__global__ __launch_bounds__(256) void k_bwd_v4(FArgs a) {
+    __shared__ SegStage s_stage[WAVES];
+    __shared__ uint2 s_ent[WAVES][ENT_CAP];
+    __shared__ float s_fp4[WAVES][16];
+    constexpr uint32_t G = 64u / BL;
+    constexpr uint32_t STEP = G * U;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
+    if (si >= a.nseg) return;
+    const SegDesc sd = a.seg[si];
+    const uint32_t g = lane / BL, bl = lane % BL;
+    fp4_table_init(s_fp4[wave]);
+    const StagedSeg sg = stage_segment(s_stage[wave], a.idx, a.val, sd);
+    const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(a.gT, a.gT_bytes);
+    const uint32_t nq = (uint32_t)(a.B >> 2);
+    const float4 *x4p = reinterpret_cast<const float4 *>(a.xT) + (int64_t)sd.row * nq;
+    uint32_t lane_off[KB];
+    float4 xr[KB];
+    float part = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+        const uint32_t q = bl + BL * (uint32_t)k;
+        lane_off[k] = q < nq ? q * 16u : OOB_OFFSET;
+        xr[k] = q < nq ? x4p[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        part += (__builtin_fabsf(xr[k].x) + __builtin_fabsf(xr[k].y)) +
+                (__builtin_fabsf(xr[k].z) + __builtin_fabsf(xr[k].w));
+    }
+    if (a.acc_in && (sd.split & SEG_FIRST)) {
+        part = group_sum_last<BL>(part);  // every group holds the whole row; use group 0
+        if (lane == BL - 1u) a.acc_in[sd.row] += part;
+    }
+    uint2 *ent = s_ent[wave];
+    const uint32_t n = decode_segment_entries(sg, sd, a.sc, s_fp4[wave], (uint32_t)a.B * 4u, STEP, ent);
+    float4 acc[KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t j = 0; j < n; j += STEP) {
+        uint2 e[U];
+        float4 gv[U][KB];
+#pragma unroll
+        for (int u = 0; u < U; ++u) e[u] = ent[j + (uint32_t)u * G + g];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int k = 0; k < KB; ++k) gv[u][k] = buffer_load_f4(rg, e[u].x + lane_off[k]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const float w = __builtin_bit_cast(float, e[u].y);
+            float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+            for (int k = 0; k < KB; ++k) {
+                acc[k].x = __builtin_fmaf(w, gv[u][k].x, acc[k].x);
+                acc[k].y = __builtin_fmaf(w, gv[u][k].y, acc[k].y);
+                acc[k].z = __builtin_fmaf(w, gv[u][k].z, acc[k].z);
+                acc[k].w = __builtin_fmaf(w, gv[u][k].w, acc[k].w);
+                d0 = __builtin_fmaf(xr[k].x, gv[u][k].x, d0);
+                d1 = __builtin_fmaf(xr[k].y, gv[u][k].y, d1);
+                d0 = __builtin_fmaf(xr[k].z, gv[u][k].z, d0);
+                d1 = __builtin_fmaf(xr[k].w, gv[u][k].w, d1);
+            }
+            const float tot = group_sum_last<BL>(d0 + d1);
+            const uint32_t ei = j + (uint32_t)u * G + g;
+            if (bl == BL - 1u && ei < n) a.gw[sd.elem_begin + ei] = tot;
+        }
+    }
+#pragma unroll
+    for (uint32_t off = BL; off < 64u; off <<= 1)
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            acc[k].x += __shfl_xor(acc[k].x, (int)off, 64);
+            acc[k].y += __shfl_xor(acc[k].y, (int)off, 64);
+            acc[k].z += __shfl_xor(acc[k].z, (int)off, 64);
+            acc[k].w += __shfl_xor(acc[k].w, (int)off, 64);
+        }
+    if (g == 0) {
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            const int64_t q = (int64_t)bl + (int64_t)BL * k;
+            if (q < nq) {
+                const float v4[4] = {acc[k].x, acc[k].y, acc[k].z, acc[k].w};
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float *o = a.dx + (4 * q + v) * a.dx_ld + sd.row;
+                    if (sd.split & SEG_SPLIT) atomicAdd(o, v4[v]);
+                    else *o = v4[v];
+                }
+            }
+        }
+    }
+}
+
 struct SBArgs {
     const SegDesc *seg;
     int64_t nseg;
@@ -630,9 +745,9 @@ __global__ __launch_bounds__(256) void k_sddmm_b4(SBArgs a) {
     }
 }
 
-// [B, n] -> [n, B], one 64(b) x 16(j) tile per block through LDS; reads are
-// 64-byte row segments, writes 256-byte runs of b.  Optional
-// acc[j] += sum_b |x[b,j]| (atomics when B spans several tiles).
+// [B, n] -> [n, B], one 64(b) x 16(j) tile per block through LDS.  Any
+// shape and alignment.  Optional acc[j] += sum_b |x[b,j]| (atomics when B
+// spans several tiles).
 __global__ __launch_bounds__(256) void k_transpose(const float *__restrict__ src, int64_t B,
                                                    int64_t n, float *__restrict__ dst,
                                                    float *__restrict__ acc) {
@@ -648,11 +763,17 @@ __global__ __launch_bounds__(256) void k_transpose(const float *__restrict__ src
         }
     }
     __syncthreads();
-    if (acc && t < 16u && j0 + t < n) {
+    if (acc) {
+        // 16 lanes per column, 4 rows each
+        const uint32_t jj = t >> 4, r = t & 15u;
         float s = 0.0f;
-        for (uint32_t i = 0; i < 64u; ++i) s += __builtin_fabsf(tile[i][t]);
-        if (gridDim.y == 1) acc[j0 + t] += s;
-        else atomicAdd(acc + j0 + t, s);
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) s += __builtin_fabsf(tile[r * 4u + i][jj]);
+        s = group_sum_last<16>(s);
+        if (r == 15u && j0 + jj < n) {
+            if (gridDim.y == 1) acc[j0 + jj] += s;
+            else atomicAdd(acc + j0 + jj, s);
+        }
     }
     {
         const uint32_t bb = t & 63u, jj = t >> 6;  // 64 x 4
@@ -660,6 +781,52 @@ __global__ __launch_bounds__(256) void k_transpose(const float *__restrict__ src
         for (uint32_t i = 0; i < 4u; ++i) {
             const int64_t j = j0 + jj + 4u * i, b = b0 + bb;
             if (j < n && b < B) dst[j * B + b] = tile[bb][jj + 4u * i];
+        }
+    }
+}
+
+// The same with float4 rows: a 64(b) x 32(j) tile, 128-byte reads along j,
+// 256-byte writes along b.  Needs n % 4 == 0, B % 4 == 0 and 16-byte aligned
+// src / dst.
+__global__ __launch_bounds__(256) void k_transpose_v4(const float *__restrict__ src, int64_t B,
+                                                      int64_t n, float *__restrict__ dst,
+                                                      float *__restrict__ acc) {
+    __shared__ float tile[64][33];
+    const int64_t j0 = (int64_t)blockIdx.x * 32, b0 = (int64_t)blockIdx.y * 64;
+    const uint32_t t = threadIdx.x;
+    {
+        const uint32_t q = t & 7u, bb = t >> 3;  // 8 float4 per row, 32 rows per pass
+#pragma unroll
+        for (uint32_t i = 0; i < 2u; ++i) {
+            const int64_t b = b0 + bb + 32u * i, j = j0 + 4u * q;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (b < B && j < n) v = *reinterpret_cast<const float4 *>(src + b * n + j);
+            float *row = tile[bb + 32u * i];
+            row[4u * q] = v.x;
+            row[4u * q + 1u] = v.y;
+            row[4u * q + 2u] = v.z;
+            row[4u * q + 3u] = v.w;
+        }
+    }
+    __syncthreads();
+    {
+        const uint32_t q = t & 15u, jj = t >> 4;  // 16 float4 per column, 16 columns per pass
+#pragma unroll
+        for (uint32_t i = 0; i < 2u; ++i) {
+            const uint32_t jc = jj + 16u * i;
+            const int64_t j = j0 + jc, b = b0 + 4u * q;
+            const float4 v = make_float4(tile[4u * q][jc], tile[4u * q + 1u][jc], tile[4u * q + 2u][jc],
+                                         tile[4u * q + 3u][jc]);
+            if (j < n && b < B) *reinterpret_cast<float4 *>(dst + j * B + b) = v;
+            if (acc) {
+                float s = (__builtin_fabsf(v.x) + __builtin_fabsf(v.y)) +
+                          (__builtin_fabsf(v.z) + __builtin_fabsf(v.w));
+                s = group_sum_last<16>(s);
+                if (q == 15u && j < n) {
+                    if (gridDim.y == 1) acc[j] += s;
+                    else atomicAdd(acc + j, s);
+                }
+            }
         }
     }
 }
@@ -761,9 +928,9 @@ template <int G, int KB>
 void gather_dispatch_skip(const GArgs &a, int skip, hipStream_t st) {
     const dim3 grid(blocks_for(a.nseg)), block(256);
     switch (skip) {
-        case SKIP_ZERO: hipLaunchKernelGGL((k_gather<G, KB, SKIP_ZERO>), grid, block, 0, st, a); break;
-        case SKIP_POSZERO: hipLaunchKernelGGL((k_gather<G, KB, SKIP_POSZERO>), grid, block, 0, st, a); break;
-        default: hipLaunchKernelGGL((k_gather<G, KB, SKIP_NONE>), grid, block, 0, st, a); break;
+        case SKIP_ZERO: launch((k_gather<G, KB, SKIP_ZERO>), grid, block, 0, st, a); break;
+        case SKIP_POSZERO: launch((k_gather<G, KB, SKIP_POSZERO>), grid, block, 0, st, a); break;
+        default: launch((k_gather<G, KB, SKIP_NONE>), grid, block, 0, st, a); break;
     }
 }
 
@@ -771,9 +938,9 @@ template <int G, int KB>
 void gather_b4_dispatch_skip(const BArgs &a, int skip, hipStream_t st) {
     const dim3 grid(blocks_for(a.nseg)), block(256);
     switch (skip) {
-        case SKIP_ZERO: hipLaunchKernelGGL((k_gather_b4<G, KB, SKIP_ZERO>), grid, block, 0, st, a); break;
-        case SKIP_POSZERO: hipLaunchKernelGGL((k_gather_b4<G, KB, SKIP_POSZERO>), grid, block, 0, st, a); break;
-        default: hipLaunchKernelGGL((k_gather_b4<G, KB, SKIP_NONE>), grid, block, 0, st, a); break;
+        case SKIP_ZERO: launch((k_gather_b4<G, KB, SKIP_ZERO>), grid, block, 0, st, a); break;
+        case SKIP_POSZERO: launch((k_gather_b4<G, KB, SKIP_POSZERO>), grid, block, 0, st, a); break;
+        default: launch((k_gather_b4<G, KB, SKIP_NONE>), grid, block, 0, st, a); break;
     }
 }
 
@@ -781,9 +948,9 @@ template <int BL, int KB, int U>
 void gather_v4_skip_u(const GArgs &a, int skip, hipStream_t st) {
     const dim3 grid(blocks_for(a.nseg)), block(256);
     switch (skip) {
-        case SKIP_ZERO: hipLaunchKernelGGL((k_gather_v4<BL, KB, U, SKIP_ZERO>), grid, block, 0, st, a); break;
-        case SKIP_POSZERO: hipLaunchKernelGGL((k_gather_v4<BL, KB, U, SKIP_POSZERO>), grid, block, 0, st, a); break;
-        default: hipLaunchKernelGGL((k_gather_v4<BL, KB, U, SKIP_NONE>), grid, block, 0, st, a); break;
+        case SKIP_ZERO: launch((k_gather_v4<BL, KB, U, SKIP_ZERO>), grid, block, 0, st, a); break;
+        case SKIP_POSZERO: launch((k_gather_v4<BL, KB, U, SKIP_POSZERO>), grid, block, 0, st, a); break;
+        default: launch((k_gather_v4<BL, KB, U, SKIP_NONE>), grid, block, 0, st, a); break;
     }
 }
 
@@ -824,9 +991,9 @@ void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, in
         const dim3 grid(blocks_for(a.nseg)), block(256);
         if (nb == 1 && small) {
             switch (skip) {
-                case SKIP_ZERO: hipLaunchKernelGGL(k_gather_b1<SKIP_ZERO>, grid, block, 0, st, a); break;
-                case SKIP_POSZERO: hipLaunchKernelGGL(k_gather_b1<SKIP_POSZERO>, grid, block, 0, st, a); break;
-                default: hipLaunchKernelGGL(k_gather_b1<SKIP_NONE>, grid, block, 0, st, a); break;
+                case SKIP_ZERO: launch(k_gather_b1<SKIP_ZERO>, grid, block, 0, st, a); break;
+                case SKIP_POSZERO: launch(k_gather_b1<SKIP_POSZERO>, grid, block, 0, st, a); break;
+                default: launch(k_gather_b1<SKIP_NONE>, grid, block, 0, st, a); break;
             }
         } else if (small && nb % 4 == 0 && in_ld % 4 == 0 && aligned16(a.in)) {
             const int64_t nq = nb / 4;
@@ -884,25 +1051,47 @@ void launch_sddmm(const GatherPlan &p, const float *xT, const float *gT, int64_t
     if (gT_bytes < (int64_t)OOB_OFFSET && B % 4 == 0 && B <= 2048 && aligned16(xT) && aligned16(gT)) {
         const int64_t nq = B / 4;
         const int u = gather_u();
-        if (nq <= 1) hipLaunchKernelGGL((k_sddmm_v4<1, 1, 1>), grid, block, 0, st, a);
-        else if (nq <= 2) hipLaunchKernelGGL((k_sddmm_v4<2, 1, 2>), grid, block, 0, st, a);
-        else if (nq <= 4) hipLaunchKernelGGL((k_sddmm_v4<4, 1, 4>), grid, block, 0, st, a);
-        else if (nq <= 8) hipLaunchKernelGGL((k_sddmm_v4<8, 1, 8>), grid, block, 0, st, a);
+        if (nq <= 1) launch((k_sddmm_v4<1, 1, 1>), grid, block, 0, st, a);
+        else if (nq <= 2) launch((k_sddmm_v4<2, 1, 2>), grid, block, 0, st, a);
+        else if (nq <= 4) launch((k_sddmm_v4<4, 1, 4>), grid, block, 0, st, a);
+        else if (nq <= 8) launch((k_sddmm_v4<8, 1, 8>), grid, block, 0, st, a);
         else if (nq <= 16) {
-            if (u >= 16) hipLaunchKernelGGL((k_sddmm_v4<16, 1, 16>), grid, block, 0, st, a);
-            else if (u >= 8) hipLaunchKernelGGL((k_sddmm_v4<16, 1, 8>), grid, block, 0, st, a);
-            else hipLaunchKernelGGL((k_sddmm_v4<16, 1, 4>), grid, block, 0, st, a);
-        } else if (nq <= 32) hipLaunchKernelGGL((k_sddmm_v4<16, 2, 4>), grid, block, 0, st, a);
-        else if (nq <= 64) hipLaunchKernelGGL((k_sddmm_v4<16, 4, 2>), grid, block, 0, st, a);
-        else if (nq <= 128) hipLaunchKernelGGL((k_sddmm_v4<16, 8, 1>), grid, block, 0, st, a);
-        else if (nq <= 256) hipLaunchKernelGGL((k_sddmm_v4<16, 16, 1>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((k_sddmm_v4<16, 32, 1>), grid, block, 0, st, a);
+            if (u >= 16) launch((k_sddmm_v4<16, 1, 16>), grid, block, 0, st, a);
+            else if (u >= 8) launch((k_sddmm_v4<16, 1, 8>), grid, block, 0, st, a);
+            else launch((k_sddmm_v4<16, 1, 4>), grid, block, 0, st, a);
+        } else if (nq <= 32) launch((k_sddmm_v4<16, 2, 4>), grid, block, 0, st, a);
+        else if (nq <= 64) launch((k_sddmm_v4<16, 4, 2>), grid, block, 0, st, a);
+        else if (nq <= 128) launch((k_sddmm_v4<16, 8, 1>), grid, block, 0, st, a);
+        else if (nq <= 256) launch((k_sddmm_v4<16, 16, 1>), grid, block, 0, st, a);
+        else launch((k_sddmm_v4<16, 32, 1>), grid, block, 0, st, a);
     } else {
         const size_t lds = sizeof(float) * (size_t)WAVES * (size_t)B;
         if (lds > 64 * 1024) throw_error(1, "sampled grad-W: batch too large for one launch (max 4096)");
-        hipLaunchKernelGGL(k_sddmm, grid, block, lds, st, a);
+        launch(k_sddmm, grid, block, lds, st, a);
     }
     SILI_HIP(hipGetLastError());
+}
+
+bool launch_bwd_fused(const GatherPlan &p, const ScaleView &sc, const float *gT, const float *xT,
+                      int64_t B, float *dx, int64_t dx_ld, float *gw, float *acc_in, hipStream_t st) {
+    const int64_t gT_bytes = p.cols * B * 4;
+    if (B % 4 != 0 || B > 512 || gT_bytes >= (int64_t)OOB_OFFSET || !aligned16(xT) || !aligned16(gT))
+        return false;
+    if (p.nseg == 0) return true;
+    ProfScope ps("gather_gradw", st);
+    FArgs a{p.seg, p.nseg, p.idx, p.val, sc, gT, (uint32_t)gT_bytes, xT, B, dx, dx_ld, gw, acc_in};
+    const dim3 grid(blocks_for(p.nseg)), block(256);
+    const int64_t nq = B / 4;
+    if (nq <= 1) launch((k_bwd_v4<1, 1, 4>), grid, block, 0, st, a);
+    else if (nq <= 2) launch((k_bwd_v4<2, 1, 4>), grid, block, 0, st, a);
+    else if (nq <= 4) launch((k_bwd_v4<4, 1, 4>), grid, block, 0, st, a);
+    else if (nq <= 8) launch((k_bwd_v4<8, 1, 4>), grid, block, 0, st, a);
+    else if (nq <= 16) launch((k_bwd_v4<16, 1, 4>), grid, block, 0, st, a);
+    else if (nq <= 32) launch((k_bwd_v4<16, 2, 4>), grid, block, 0, st, a);
+    else if (nq <= 64) launch((k_bwd_v4<16, 4, 2>), grid, block, 0, st, a);
+    else launch((k_bwd_v4<16, 8, 1>), grid, block, 0, st, a);
+    SILI_HIP(hipGetLastError());
+    return true;
 }
 
 void launch_sddmm_b4(const Block4Plan &p, const uint32_t *, const float *xT, const float *gT,
@@ -912,7 +1101,7 @@ void launch_sddmm_b4(const Block4Plan &p, const uint32_t *, const float *xT, con
     SBArgs a{p.seg, p.nseg, p.idx, p.rows, p.cols, xT, gT, B, gw};
     const size_t lds = sizeof(float) * (size_t)WAVES * 4u * (size_t)B;
     if (lds > 64 * 1024) throw_error(1, "block4 sampled grad-W: batch too large (max 1024)");
-    hipLaunchKernelGGL(k_sddmm_b4, dim3(blocks_for(p.nseg)), dim3(256), lds, st, a);
+    launch(k_sddmm_b4, dim3(blocks_for(p.nseg)), dim3(256), lds, st, a);
     SILI_HIP(hipGetLastError());
 }
 
@@ -920,22 +1109,27 @@ void launch_transpose(const float *src, int64_t B, int64_t n, float *dst, float 
                       hipStream_t st) {
     if (B == 0 || n == 0) return;
     ProfScope ps("transpose", st);
-    const dim3 grid((unsigned)((n + 15) / 16), (unsigned)((B + 63) / 64));
-    hipLaunchKernelGGL(k_transpose, grid, dim3(256), 0, st, src, B, n, dst, acc);
+    if (n % 4 == 0 && B % 4 == 0 && aligned16(src) && aligned16(dst)) {
+        const dim3 grid((unsigned)((n + 31) / 32), (unsigned)((B + 63) / 64));
+        launch(k_transpose_v4, grid, dim3(256), 0, st, src, B, n, dst, acc);
+    } else {
+        const dim3 grid((unsigned)((n + 15) / 16), (unsigned)((B + 63) / 64));
+        launch(k_transpose, grid, dim3(256), 0, st, src, B, n, dst, acc);
+    }
     SILI_HIP(hipGetLastError());
 }
 
 void launch_rowabs(const float *xT, int64_t B, int64_t n, float *acc, hipStream_t st) {
     if (B == 0 || n == 0) return;
     ProfScope ps("rowabs", st);
-    hipLaunchKernelGGL(k_rowabs, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, xT, B, n, acc);
+    launch(k_rowabs, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, st, xT, B, n, acc);
     SILI_HIP(hipGetLastError());
 }
 
 void launch_colabs(const float *src, int64_t B, int64_t n, float *acc, hipStream_t st) {
     if (B == 0 || n == 0) return;
     ProfScope ps("colabs", st);
-    hipLaunchKernelGGL(k_colabs, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src, B, n, acc);
+    launch(k_colabs, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src, B, n, acc);
     SILI_HIP(hipGetLastError());
 }
 
@@ -943,7 +1137,7 @@ void launch_densify(const int32_t *ptrs, const int32_t *idx, const float *vals, 
                     int64_t n, float *dst, float *acc_abs, bool mark_explicit, hipStream_t st) {
     if (B == 0) return;
     ProfScope ps("densify", st);
-    hipLaunchKernelGGL(k_densify, dim3((unsigned)B), dim3(256), 0, st, ptrs, idx, vals, B, n, dst,
+    launch(k_densify, dim3((unsigned)B), dim3(256), 0, st, ptrs, idx, vals, B, n, dst,
                        acc_abs, mark_explicit ? 1 : 0);
     SILI_HIP(hipGetLastError());
 }
@@ -952,13 +1146,13 @@ void launch_decode(const GatherPlan &p, const ScaleView &sc, int32_t *cols, floa
                    uint32_t *rows_out, hipStream_t st) {
     if (p.nseg == 0) return;
     DArgs a{p.seg, p.nseg, p.idx, p.val, sc, cols, w, rows_out};
-    hipLaunchKernelGGL(k_decode, dim3(blocks_for(p.nseg)), dim3(256), 0, st, a);
+    launch(k_decode, dim3(blocks_for(p.nseg)), dim3(256), 0, st, a);
     SILI_HIP(hipGetLastError());
 }
 
 void launch_decode_b4(const Block4Plan &p, uint32_t *tile_br, uint32_t *tile_bc, hipStream_t st) {
     if (p.nseg == 0) return;
-    hipLaunchKernelGGL(k_decode_b4, dim3(blocks_for(p.nseg)), dim3(256), 0, st, p.seg, p.nseg, p.idx,
+    launch(k_decode_b4, dim3(blocks_for(p.nseg)), dim3(256), 0, st, p.seg, p.nseg, p.idx,
                        tile_br, tile_bc);
     SILI_HIP(hipGetLastError());
 }

@@ -97,3 +97,113 @@ def test_capi_forward_backward_null_x(api):
             api.ck(api.L.sili_device_free(h, p))
     finally:
         api.L.sili_destroy(h)
+
+
+def _capi_layer(api, wl):
+    h = C.c_void_p()
+    n_b4 = 0 if wl.tile_br is None else 16 * len(wl.tile_br)
+    api.ck(api.L.sili_create(wl.n_in, wl.n_out, max(1, wl.nnz + n_b4), 0, C.byref(h)))
+    if wl.cols is not None:
+        ptrs, cols, q = (np.ascontiguousarray(a) for a in (wl.ptrs, wl.cols, wl.q))
+        api.ck(api.L.sili_load_weights(h, _ptr(ptrs), _ptr(cols), _ptr(q), None, wl.nnz))
+    if wl.tile_br is not None:
+        api.L.sili_load_block4_tiles.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int64]
+        br, bc, tb = (np.ascontiguousarray(a) for a in (wl.tile_br, wl.tile_bc, wl.tile_bytes))
+        api.ck(api.L.sili_load_block4_tiles(h, _ptr(br), _ptr(bc), _ptr(tb), len(br)))
+    vs = np.ascontiguousarray(wl.value_scale, dtype=np.float32)
+    api.ck(api.L.sili_set_value_scale(h, _ptr(vs)))
+    return h
+
+
+@pytest.mark.parametrize("cfg,scale,batch", [
+    (1, 0.125, 1), (1, 0.125, 4), (1, 0.125, 8), (1, 0.125, 12), (1, 0.125, 64), (1, 0.125, 128),
+    (1, 0.125, 256), (1, 0.125, 512), (1, 0.125, 516), (1, 0.125, 6),
+    (2, 0.0625, 32), (2, 0.0625, 64), (3, 0.03125, 64)])
+def test_capi_backward_with_gradw(api, cfg, scale, batch):
+    """backward_dense with grad-W buffers: the fused grad-input + grad-W pass
+    (B % 4 == 0, B <= 512) and the separate kernels otherwise."""
+    wl = make_config(cfg, scale=scale, batch=batch)
+    if wl.g is None:
+        wl.g = np.random.default_rng(cfg).normal(size=(batch, wl.n_out)).astype(np.float32)
+    H = host_layer(wl)
+    h = _capi_layer(api, wl)
+    try:
+        n_s = max(1, wl.nnz)
+        n_b = 0 if wl.tile_br is None else 16 * len(wl.tile_br)
+        dev = {}
+        for name, n in (("x", wl.x.size), ("g", wl.g.size), ("y", batch * wl.n_out),
+                        ("dx", batch * wl.n_in), ("gws", n_s), ("gwb", max(1, n_b))):
+            p = C.c_void_p()
+            api.ck(api.L.sili_device_alloc(h, 4 * n, C.byref(p)))
+            dev[name] = p
+        x = np.ascontiguousarray(wl.x, dtype=np.float32)
+        g = np.ascontiguousarray(wl.g, dtype=np.float32)
+        api.ck(api.L.sili_memcpy_h2d(h, dev["x"], _ptr(x), x.nbytes))
+        api.ck(api.L.sili_memcpy_h2d(h, dev["g"], _ptr(g), g.nbytes))
+        st = api.L.sili_stream(h)
+        api.ck(api.L.sili_forward_dense(h, dev["x"], batch, dev["y"], st))
+        api.ck(api.L.sili_backward_dense(h, dev["x"], dev["g"], batch, dev["dx"], dev["gws"],
+                                         dev["gwb"] if n_b else None, 0.0, st))
+        api.ck(api.L.sili_synchronize(h))
+        dx = np.zeros((batch, wl.n_in), np.float32)
+        api.ck(api.L.sili_memcpy_d2h(h, _ptr(dx), dev["dx"], dx.nbytes))
+        dx_o, ai_o, ag_o = H.backward_dense(x, g)
+        assert_close_terms(dx, dx_o, H.backward_dense(x, g, absmode=True)[0], "dx")
+        gs_o, gb_o = H.sampled_gradw(x, g)
+        gs_a, gb_a = H.sampled_gradw(x, g, absmode=True)
+        if wl.nnz:
+            gs = np.zeros(wl.nnz, np.float32)
+            api.ck(api.L.sili_memcpy_d2h(h, _ptr(gs), dev["gws"], gs.nbytes))
+            assert_close_terms(gs, gs_o, gs_a, "gw scattered")
+        if n_b:
+            gb = np.zeros(n_b, np.float32)
+            api.ck(api.L.sili_memcpy_d2h(h, _ptr(gb), dev["gwb"], gb.nbytes))
+            assert_close_terms(gb, gb_o, gb_a, "gw block4")
+        ai = np.zeros(wl.n_in, np.float32)
+        ag = np.zeros(wl.n_out, np.float32)
+        api.ck(api.L.sili_get_accumulators(h, _ptr(ai), _ptr(ag)))
+        assert_close_terms(ai, ai_o, ai_o, "acc_in")
+        assert_close_terms(ag, ag_o, ag_o, "acc_grad")
+        for p in dev.values():
+            api.ck(api.L.sili_device_free(h, p))
+    finally:
+        api.L.sili_destroy(h)
+
+
+def test_capi_profiler_names_and_counts(api):
+    """Per-kernel times come from the dispatches' own begin/end stamps."""
+    wl = make_config(1, scale=0.125, batch=64)
+    h = _capi_layer(api, wl)
+
+    class Entry(C.Structure):
+        _fields_ = [("name", C.c_char * 56), ("count", C.c_int64), ("total_ms", C.c_double),
+                    ("min_ms", C.c_double), ("max_ms", C.c_double)]
+    api.L.sili_profile_read.argtypes = [C.c_void_p, C.POINTER(Entry), C.c_int, C.POINTER(C.c_int)]
+    try:
+        dev = {}
+        for name, n in (("x", wl.x.size), ("g", wl.g.size), ("y", wl.batch * wl.n_out),
+                        ("dx", wl.batch * wl.n_in), ("gw", wl.nnz)):
+            p = C.c_void_p()
+            api.ck(api.L.sili_device_alloc(h, 4 * n, C.byref(p)))
+            dev[name] = p
+        api.ck(api.L.sili_memcpy_h2d(h, dev["x"], _ptr(wl.x), wl.x.nbytes))
+        api.ck(api.L.sili_memcpy_h2d(h, dev["g"], _ptr(wl.g), wl.g.nbytes))
+        st = api.L.sili_stream(h)
+        api.ck(api.L.sili_profile_enable(h, 1))
+        for _ in range(3):
+            api.ck(api.L.sili_forward_dense(h, dev["x"], wl.batch, dev["y"], st))
+            api.ck(api.L.sili_backward_dense(h, None, dev["g"], wl.batch, dev["dx"], dev["gw"], None, 0.0, st))
+        api.ck(api.L.sili_synchronize(h))
+        buf = (Entry * 64)()
+        n = C.c_int()
+        api.ck(api.L.sili_profile_read(h, buf, 64, C.byref(n)))
+        got = {buf[i].name.decode(): (buf[i].count, buf[i].total_ms, buf[i].min_ms) for i in range(n.value)}
+        for name in ("fwd:transpose", "fwd:gather", "bwd:transpose", "bwd:gather_gradw"):
+            assert name in got, got
+            cnt, tot, mn = got[name]
+            assert cnt == 3 and tot > 0 and mn > 0, (name, got[name])
+        assert "bwd:gather" not in got and "bwd:sddmm" not in got
+        for p in dev.values():
+            api.ck(api.L.sili_device_free(h, p))
+    finally:
+        api.L.sili_destroy(h)

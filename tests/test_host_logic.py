@@ -77,6 +77,7 @@ def test_algorithmic_bytes_table():
     assert t["fwd:gather"] == base + 4 * 8 * 64 + 4 * 8 * 32
     assert t["bwd:sddmm"] == 1100 + 8 * 65 + 4 * 8 * 64 + 4 * 8 * 32 + 4 * 1000
     assert t["fwd:transpose"] == 8 * 8 * 64
+    assert t["bwd:gather_gradw"] == base + 4 * 8 * 32 + 2 * 4 * 8 * 64 + 4 * 1000
 
 
 def test_bench_refuses_more_than_one_gpu():
