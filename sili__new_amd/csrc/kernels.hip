@@ -208,6 +208,48 @@ __device__ __forceinline__ uint32_t decode_segment_entries(const StagedSeg &sg, 
 // in_ld % 4 == 0 and a 16-byte aligned `in`.
 constexpr uint32_t ENT_CAP = SEG_BYTES_MAX + 64u;
 
+// Block epilogue of the float4 kernels: out[b, row] for the block's (up to
+// WAVES) segments.  Each wave leaves its nb results in its own LDS slice
+// (`slice`, >= nb floats; lanes of group 0 hold float4 chunk q = bl + BL*k),
+// then the block writes them with consecutive lanes on consecutive rows, so
+// consecutive segments (rows) of one batch index leave as one run instead
+// of WAVES scattered 4-byte stores.  Split rows add atomically.  Every
+// thread of the block must call this (it holds a block barrier).
+template <int BL, int KB>
+__device__ __forceinline__ void store_rows_block(const float4 (&acc)[KB], bool active, uint32_t row,
+                                                 bool split, uint32_t nq, float *slice_base,
+                                                 uint32_t slice_stride, float *out, int64_t out_ld) {
+    __shared__ uint32_t s_row[WAVES];
+    __shared__ uint32_t s_flag[WAVES];  // bit 0: active, bit 1: split
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t g = lane / BL, bl = lane % BL;
+    float *slice = slice_base + wave * slice_stride;
+    if (active && g == 0) {
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            const uint32_t q = bl + BL * (uint32_t)k;
+            if (q < nq) reinterpret_cast<float4 *>(slice)[q] = acc[k];
+        }
+    }
+    if (lane == 0) {
+        s_row[wave] = row;
+        s_flag[wave] = (active ? 1u : 0u) | (split ? 2u : 0u);
+    }
+    __syncthreads();
+    const uint32_t nb = nq * 4u;
+    for (uint32_t i = threadIdx.x; i < nb * WAVES; i += blockDim.x) {
+        const uint32_t w = i % WAVES, b = i / WAVES;
+        const uint32_t f = s_flag[w];
+        if (!(f & 1u)) continue;
+        const float v = slice_base[w * slice_stride + b];
+        float *o = out + (int64_t)b * out_ld + s_row[w];
+        if (f & 2u) atomicAdd(o, v);
+        else *o = v;
+    }
+}
+
+
+
 template <int BL, int KB, int U, int SKIP>
 __global__ __launch_bounds__(256) void k_gather_v4(GArgs a) {
     __shared__ SegStage s_stage[WAVES];
@@ -217,13 +259,18 @@ __global__ __launch_bounds__(256) void k_gather_v4(GArgs a) {
     constexpr uint32_t STEP = G * U;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
-    if (si >= a.nseg) return;
-    const SegDesc sd = a.seg[si];
+    const bool active = si < a.nseg;  // inactive waves still join the block epilogue
     const uint32_t g = lane / BL, bl = lane % BL;
+    const uint32_t nq = (uint32_t)(a.nb >> 2);
+    float4 acc[KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    SegDesc sd{};
+    if (active) {
+    sd = a.seg[si];
     fp4_table_init(s_fp4[wave]);
     const StagedSeg sg = stage_segment(s_stage[wave], a.idx, a.val, sd);
     const __amdgpu_buffer_rsrc_t rin = buffer_rsrc(a.in, a.in_bytes);
-    const uint32_t nq = (uint32_t)(a.nb >> 2);
     uint32_t lane_off[KB];
 #pragma unroll
     for (int k = 0; k < KB; ++k) {
@@ -232,9 +279,6 @@ __global__ __launch_bounds__(256) void k_gather_v4(GArgs a) {
     }
     uint2 *ent = s_ent[wave];
     const uint32_t n = decode_segment_entries(sg, sd, a.sc, s_fp4[wave], (uint32_t)a.in_ld * 4u, STEP, ent);
-    float4 acc[KB];
-#pragma unroll
-    for (int k = 0; k < KB; ++k) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     for (uint32_t j = 0; j < n; j += STEP) {
         uint2 e[U];
         float4 x[U][KB];
@@ -274,21 +318,10 @@ __global__ __launch_bounds__(256) void k_gather_v4(GArgs a) {
             acc[k].z += __shfl_xor(acc[k].z, (int)off, 64);
             acc[k].w += __shfl_xor(acc[k].w, (int)off, 64);
         }
-    if (g == 0) {
-#pragma unroll
-        for (int k = 0; k < KB; ++k) {
-            const int64_t q = (int64_t)bl + (int64_t)BL * k;
-            if (q < nq) {
-                const float v4[4] = {acc[k].x, acc[k].y, acc[k].z, acc[k].w};
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    float *o = a.out + (4 * q + v) * a.out_ld + sd.row;
-                    if (sd.split & SEG_SPLIT) atomicAdd(o, v4[v]);
-                    else *o = v4[v];
-                }
-            }
-        }
+    wave_lds_sync();  // the entry table is reused as this wave's output slice
     }
+    store_rows_block<BL, KB>(acc, active, sd.row, (sd.split & SEG_SPLIT) != 0, nq,
+                             reinterpret_cast<float *>(&s_ent[0][0]), ENT_CAP * 2u, a.out, a.out_ld);
 }
 
 struct BArgs {
@@ -601,13 +634,18 @@ __global__ __launch_bounds__(256) void k_bwd_v4(FArgs a) {
     constexpr uint32_t STEP = G * U;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
-    if (si >= a.nseg) return;
-    const SegDesc sd = a.seg[si];
+    const bool active = si < a.nseg;  // inactive waves still join the block epilogue
     const uint32_t g = lane / BL, bl = lane % BL;
+    const uint32_t nq = (uint32_t)(a.B >> 2);
+    float4 acc[KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    SegDesc sd{};
+    if (active) {
+    sd = a.seg[si];
     fp4_table_init(s_fp4[wave]);
     const StagedSeg sg = stage_segment(s_stage[wave], a.idx, a.val, sd);
     const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(a.gT, a.gT_bytes);
-    const uint32_t nq = (uint32_t)(a.B >> 2);
     const float4 *x4p = reinterpret_cast<const float4 *>(a.xT) + (int64_t)sd.row * nq;
     uint32_t lane_off[KB];
     float4 xr[KB];
@@ -626,9 +664,6 @@ __global__ __launch_bounds__(256) void k_bwd_v4(FArgs a) {
     }
     uint2 *ent = s_ent[wave];
     const uint32_t n = decode_segment_entries(sg, sd, a.sc, s_fp4[wave], (uint32_t)a.B * 4u, STEP, ent);
-    float4 acc[KB];
-#pragma unroll
-    for (int k = 0; k < KB; ++k) acc[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     for (uint32_t j = 0; j < n; j += STEP) {
         uint2 e[U];
         float4 gv[U][KB];
@@ -667,21 +702,10 @@ __global__ __launch_bounds__(256) void k_bwd_v4(FArgs a) {
             acc[k].z += __shfl_xor(acc[k].z, (int)off, 64);
             acc[k].w += __shfl_xor(acc[k].w, (int)off, 64);
         }
-    if (g == 0) {
-#pragma unroll
-        for (int k = 0; k < KB; ++k) {
-            const int64_t q = (int64_t)bl + (int64_t)BL * k;
-            if (q < nq) {
-                const float v4[4] = {acc[k].x, acc[k].y, acc[k].z, acc[k].w};
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    float *o = a.dx + (4 * q + v) * a.dx_ld + sd.row;
-                    if (sd.split & SEG_SPLIT) atomicAdd(o, v4[v]);
-                    else *o = v4[v];
-                }
-            }
-        }
+    wave_lds_sync();  // the entry table is reused as this wave's output slice
     }
+    store_rows_block<BL, KB>(acc, active, sd.row, (sd.split & SEG_SPLIT) != 0, nq,
+                             reinterpret_cast<float *>(&s_ent[0][0]), ENT_CAP * 2u, a.dx, a.dx_ld);
 }
 
 struct SBArgs {
@@ -955,23 +979,41 @@ void gather_v4_skip_u(const GArgs &a, int skip, hipStream_t st) {
 }
 
 // entries in flight per lane: SILI_GATHER_U in {4, 8, 16} (tuning knob)
-inline int gather_u() {
-    static const int u = [] {
-        const char *e = std::getenv("SILI_GATHER_U");
-        const int v = e ? std::atoi(e) : 4;
-        return v >= 16 ? 16 : v >= 8 ? 8 : 4;
+// Launch-shape knobs of the float4 kernels (environment, read once):
+//   SILI_GATHER_BL  lanes per entry at batch 64 / 128 (4, 8 or 16)
+//   SILI_GATHER_U   entries per lane group in flight
+// Defaults: 8 lanes per entry (G = 8 entries per load instruction, two
+// float4 chunks per lane at batch 64) and 4 entries per group in flight --
+// the fastest measured shape for the fused backward at batch 64; the
+// forward gather is within 2% at every shape.
+inline int env_int(const char *name, int dflt) {
+    const char *e = std::getenv(name);
+    return e ? std::atoi(e) : dflt;
+}
+inline int gather_bl() {
+    static const int v = [] {
+        const int b = env_int("SILI_GATHER_BL", 8);
+        return b >= 16 ? 16 : b >= 8 ? 8 : 4;
     }();
-    return u;
+    return v;
+}
+inline int gather_u() {
+    static const int v = env_int("SILI_GATHER_U", 0);  // 0: per-shape default
+    return v;
 }
 
 template <int BL, int KB>
 void gather_v4_skip(const GArgs &a, int skip, hipStream_t st) {
-    constexpr int UMAX = (64 / (64 / BL)) >= 1 ? 16 : 16;
-    (void)UMAX;
     const int u = gather_u();
-    if (u >= 16 && KB == 1) gather_v4_skip_u<BL, KB, 16>(a, skip, st);
-    else if (u >= 8 && KB <= 2) gather_v4_skip_u<BL, KB, 8>(a, skip, st);
-    else gather_v4_skip_u<BL, KB, 4>(a, skip, st);
+    if constexpr (KB >= 4) {
+        if (u >= 4) gather_v4_skip_u<BL, KB, 4>(a, skip, st);
+        else if (u >= 2) gather_v4_skip_u<BL, KB, 2>(a, skip, st);
+        else gather_v4_skip_u<BL, KB, 1>(a, skip, st);
+    } else {
+        if (u >= 16 && KB == 1) gather_v4_skip_u<BL, KB, 16>(a, skip, st);
+        else if (u >= 8) gather_v4_skip_u<BL, KB, 8>(a, skip, st);
+        else gather_v4_skip_u<BL, KB, 4>(a, skip, st);
+    }
 }
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -1001,8 +1043,17 @@ void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, in
             else if (nq <= 2) gather_v4_skip<2, 1>(a, skip, st);
             else if (nq <= 4) gather_v4_skip<4, 1>(a, skip, st);
             else if (nq <= 8) gather_v4_skip<8, 1>(a, skip, st);
-            else if (nq <= 16) gather_v4_skip<16, 1>(a, skip, st);
-            else if (nq <= 32) gather_v4_skip<16, 2>(a, skip, st);
+            else if (nq <= 16) {
+                const int bl = gather_bl();
+                if (nq > 8 && bl == 4) gather_v4_skip<4, 4>(a, skip, st);
+                else if (nq > 8 && bl == 8) gather_v4_skip<8, 2>(a, skip, st);
+                else gather_v4_skip<16, 1>(a, skip, st);
+            } else if (nq <= 32) {
+                const int bl = gather_bl();
+                if (bl == 4) gather_v4_skip<4, 8>(a, skip, st);
+                else if (bl == 8) gather_v4_skip<8, 4>(a, skip, st);
+                else gather_v4_skip<16, 2>(a, skip, st);
+            }
             else if (nq <= 64) gather_v4_skip<16, 4>(a, skip, st);
             else gather_v4_skip<16, 8>(a, skip, st);
         } else if (nb <= 1) gather_dispatch_skip<64, 1>(a, skip, st);
@@ -1086,8 +1137,21 @@ bool launch_bwd_fused(const GatherPlan &p, const ScaleView &sc, const float *gT,
     else if (nq <= 2) launch((k_bwd_v4<2, 1, 4>), grid, block, 0, st, a);
     else if (nq <= 4) launch((k_bwd_v4<4, 1, 4>), grid, block, 0, st, a);
     else if (nq <= 8) launch((k_bwd_v4<8, 1, 4>), grid, block, 0, st, a);
-    else if (nq <= 16) launch((k_bwd_v4<16, 1, 4>), grid, block, 0, st, a);
-    else if (nq <= 32) launch((k_bwd_v4<16, 2, 4>), grid, block, 0, st, a);
+    else if (nq <= 16) {
+        const int bl = gather_bl(), u = gather_u();
+        if (nq > 8 && bl == 4) {
+            if (u >= 2) launch((k_bwd_v4<4, 4, 2>), grid, block, 0, st, a);
+            else launch((k_bwd_v4<4, 4, 1>), grid, block, 0, st, a);
+        } else if (nq > 8 && bl == 8) {
+            if (u == 0 || u >= 4) launch((k_bwd_v4<8, 2, 4>), grid, block, 0, st, a);
+            else launch((k_bwd_v4<8, 2, 2>), grid, block, 0, st, a);
+        } else launch((k_bwd_v4<16, 1, 4>), grid, block, 0, st, a);
+    } else if (nq <= 32) {
+        const int bl = gather_bl();
+        if (bl == 4) launch((k_bwd_v4<4, 8, 1>), grid, block, 0, st, a);
+        else if (bl == 8) launch((k_bwd_v4<8, 4, 1>), grid, block, 0, st, a);
+        else launch((k_bwd_v4<16, 2, 4>), grid, block, 0, st, a);
+    }
     else if (nq <= 64) launch((k_bwd_v4<16, 4, 2>), grid, block, 0, st, a);
     else launch((k_bwd_v4<16, 8, 1>), grid, block, 0, st, a);
     SILI_HIP(hipGetLastError());
