@@ -1,11 +1,613 @@
-// synapto.hip -- GPU bulk synaptogenesis step (filled in below).
+// synapto.hip -- the bulk synaptogenesis step on the GPU: magnitude prune,
+// regrowth at host-supplied candidates, block4 demote / promote, and the
+// rebuild of both stores, all by device sort, scan and compaction.
+//
+// Selection policy (new; the reference prunes by importance, row by row,
+// delta_csr_memory.hpp:1019-1258): the k = llround(prune_frac * N) stored
+// synapses (scattered + live block4 slots) with the smallest
+// |fl32(dec(code) * S(r,c))| (fp32 bit order, so NaN sorts above inf) are
+// removed, ties by (row, col) ascending; as many are regrown at the first
+// valid candidates in list order.  Structural rules follow the reference:
+//   - a pruned block4 slot is zeroed; a touched tile whose live count
+//     (nonzero bytes) drops below 2 is demoted, its remaining slot becoming
+//     a scattered synapse with both nibbles requantized (code 8 -> 0) and
+//     swapped into the scattered byte order (delta_csr_memory.hpp:949-999,
+//     1203-1225);
+//   - an insert whose 4x4 window holds a (surviving) tile writes that tile's
+//     slot (delta_csr_memory.hpp:620-646); otherwise it is a scattered
+//     insert, and every window that received one and then holds >= 2
+//     scattered synapses is promoted into a new tile (:648-700).
+// Phase order: select -> prune -> demote -> insert -> promote -> rebuild.
+//
+// Keys: a synapse is (row, col) packed as rc = row << 32 | col (rows and
+// cols < 2^31, so real keys never reach KEY_NONE); sorted rc arrays serve
+// the membership tests by binary search.
+#include "sili_hip.h"
 #include "layer.hpp"
+#include "wave.hpp"
+
+#include <cmath>
+#include <vector>
 
 namespace sili {
 
-void synapto_step(Layer &, float, const int32_t *, const int32_t *, const float *, const float *, int64_t, int,
-                  int64_t *) {
-    throw_error(3, "synapto_step: not implemented yet");
+namespace {
+
+constexpr unsigned TPB = 256;
+inline unsigned nblk(int64_t n) { return (unsigned)((n + TPB - 1) / TPB); }
+constexpr uint64_t KEY_NONE = ~0ull;
+
+__device__ __forceinline__ uint64_t rc_key(uint32_t r, uint32_t c) { return ((uint64_t)r << 32) | c; }
+__device__ __forceinline__ uint32_t requant(uint32_t code) { return code == 8u ? 0u : code; }
+
+// First index in sorted a[0, n) with a[i] >= key.
+__device__ __forceinline__ int64_t lower_bound_u64(const uint64_t *a, int64_t n, uint64_t key) {
+    int64_t lo = 0, hi = n;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (a[mid] < key) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+__device__ __forceinline__ bool contains_u64(const uint64_t *a, int64_t n, uint64_t key) {
+    const int64_t i = lower_bound_u64(a, n, key);
+    return i < n && a[i] == key;
+}
+// Surviving tile of window (br, bc), or -1.  tkey: canonical tile keys
+// br*bcols + bc, ascending (the store's own order).
+__device__ __forceinline__ int64_t find_tile(const uint64_t *tkey, int64_t T, const uint8_t *alive,
+                                             uint64_t wkey) {
+    const int64_t t = lower_bound_u64(tkey, T, wkey);
+    return (t < T && tkey[t] == wkey && alive[t]) ? t : -1;
+}
+
+__global__ void k_fill_u8(uint8_t *p, int64_t n, uint8_t v) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+__global__ void k_fill_u32(uint32_t *p, int64_t n, uint32_t v) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+__global__ void k_iota32(uint32_t *p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n) p[i] = (uint32_t)i;
+}
+
+// Keys of every stored synapse: scattered entries [0, Ns), then the 16
+// slots of every tile [Ns, Ns + 16T) (dead or out-of-range slots get
+// KEY_NONE / 0xFFFFFFFF so they sort after every live synapse).
+__global__ void k_syn_keys(int64_t Ns, const uint32_t *srow, const uint32_t *scol, const uint8_t *sval,
+                           int64_t T, const uint32_t *tbr, const uint32_t *tbc, const uint8_t *tiles,
+                           int64_t n_in, int64_t n_out, ScaleView sc, uint64_t *rc, uint32_t *absw) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < Ns) {
+        const uint32_t r = srow[i], c = scol[i];
+        const float w = fp4_decode((uint32_t)sval[i] >> 4) * scale_at(sc, r, c);
+        rc[i] = rc_key(r, c);
+        absw[i] = __builtin_bit_cast(uint32_t, w) & 0x7FFFFFFFu;
+        return;
+    }
+    const int64_t s = i - Ns;
+    if (s >= 16 * T) return;
+    const int64_t t = s >> 4;
+    const uint32_t sl = (uint32_t)(s & 15), lj = sl >> 2, li = sl & 3u;
+    const uint32_t r = tbr[t] * 4u + li, c = tbc[t] * 4u + lj;
+    const uint32_t b = tiles[s];
+    if (b == 0u || r >= n_in || c >= n_out) {
+        rc[i] = KEY_NONE;
+        absw[i] = 0xFFFFFFFFu;
+        return;
+    }
+    const float w = fp4_decode(b & 0xFu) * scale_at(sc, r, c);
+    rc[i] = rc_key(r, c);
+    absw[i] = __builtin_bit_cast(uint32_t, w) & 0x7FFFFFFFu;
+}
+
+// Number of live synapses: the KEY_NONE entries sort last.
+__global__ void k_count_live(const uint64_t *rc_sorted, int64_t n, unsigned long long *out) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) *out = (unsigned long long)lower_bound_u64(rc_sorted, n, KEY_NONE);
+}
+
+__global__ void k_gather_u8_by(const uint8_t *src, const uint32_t *perm, int64_t n, uint8_t *dst) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n) dst[i] = src[perm[i]];
+}
+
+__global__ void k_tile_wkeys(const uint32_t *tbr, const uint32_t *tbc, int64_t T, uint64_t bcols,
+                             uint64_t *tkey) {
+    const int64_t t = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (t < T) tkey[t] = (uint64_t)tbr[t] * bcols + tbc[t];
+}
+
+__global__ void k_gather_u32_by(const uint32_t *src, const uint32_t *perm, int64_t n, uint32_t *dst) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n) dst[i] = src[perm[i]];
+}
+
+// The k smallest: order[] lists synapse indices by (|w|, row, col).
+__global__ void k_syn_prune(const uint32_t *order, int64_t k, int64_t Ns, const uint64_t *rc,
+                            uint8_t *s_removed, uint8_t *tbytes, uint8_t *touched, uint64_t *pruned) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= k) return;
+    const uint32_t e = order[i];
+    pruned[i] = rc[e];
+    if ((int64_t)e < Ns) {
+        s_removed[e] = 1;
+    } else {
+        const int64_t s = (int64_t)e - Ns;
+        tbytes[s] = 0;
+        touched[s >> 4] = 1;
+    }
+}
+
+// Touched tiles with live < 2 die; their in-range live slot (at most one)
+// becomes a scattered synapse (dem_key / dem_byte per tile).
+__global__ void k_syn_demote(int64_t T, const uint32_t *tbr, const uint32_t *tbc, const uint8_t *tbytes,
+                             const uint8_t *touched, int64_t n_in, int64_t n_out, uint8_t *alive,
+                             uint64_t *dem_key, uint8_t *dem_byte, unsigned long long *n_demoted) {
+    const int64_t t = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (t >= T) return;
+    dem_key[t] = KEY_NONE;
+    dem_byte[t] = 0;
+    alive[t] = 1;
+    if (!touched[t]) return;
+    int live = 0;
+    for (int s = 0; s < 16; ++s) live += tbytes[t * 16 + s] != 0;
+    if (live >= 2) return;
+    alive[t] = 0;
+    atomicAdd(n_demoted, 1ull);
+    for (uint32_t s = 0; s < 16u; ++s) {
+        const uint32_t b = tbytes[t * 16 + s];
+        const uint32_t r = tbr[t] * 4u + (s & 3u), c = tbc[t] * 4u + (s >> 2);
+        if (b == 0u || r >= n_in || c >= n_out) continue;
+        dem_key[t] = rc_key(r, c);
+        dem_byte[t] = (uint8_t)((requant(b & 0xFu) << 4) | requant(b >> 4));
+    }
+}
+
+// The scattered set after prune + demote, unsorted: [0, Ns) survivors,
+// [Ns, Ns + T) demoted slots, [Ns + T, Ns + T + n_cand) scattered inserts
+// (filled later); KEY_NONE marks no entry.
+__global__ void k_syn_set1(int64_t Ns, int64_t T, const uint64_t *rc, const uint8_t *sval,
+                           const uint8_t *s_removed, const uint64_t *dem_key, const uint8_t *dem_byte,
+                           uint64_t *key, uint8_t *byte) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < Ns) {
+        key[i] = s_removed[i] ? KEY_NONE : rc[i];
+        byte[i] = sval[i];
+    } else if (i < Ns + T) {
+        key[i] = dem_key[i - Ns];
+        byte[i] = dem_byte[i - Ns];
+    }
+}
+
+// Static validity of each candidate: in range, not just pruned, not stored
+// (scattered after prune + demote, or a live slot of a surviving tile).
+// Valid ones get their rc key, the rest KEY_NONE.
+__global__ void k_syn_cand_static(int64_t n_cand, const int32_t *cr, const int32_t *cc, int64_t n_in,
+                                  int64_t n_out, const uint64_t *pruned, int64_t k, const uint64_t *set1,
+                                  int64_t n_set1, const uint64_t *tkey, int64_t T, const uint8_t *alive,
+                                  const uint8_t *tbytes, uint64_t bcols, uint64_t *ckey) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= n_cand) return;
+    const int32_t r = cr[i], c = cc[i];
+    uint64_t key = KEY_NONE;
+    if (r >= 0 && r < n_in && c >= 0 && c < n_out) {
+        const uint64_t rc = rc_key((uint32_t)r, (uint32_t)c);
+        bool ok = !contains_u64(pruned, k, rc) && !contains_u64(set1, n_set1, rc);
+        if (ok) {
+            const int64_t t = find_tile(tkey, T, alive, (uint64_t)(r >> 2) * bcols + (uint64_t)(c >> 2));
+            if (t >= 0 && tbytes[t * 16 + (c & 3) * 4 + (r & 3)] != 0) ok = false;
+        }
+        if (ok) key = rc;
+    }
+    ckey[i] = key;
+}
+
+// First occurrence (in list order) of each valid candidate position: the
+// stable sort keeps equal keys in ascending candidate index.
+__global__ void k_syn_first(int64_t n_cand, const uint64_t *ckey_sorted, const uint32_t *cidx_sorted,
+                            uint32_t *first) {
+    const int64_t p = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (p >= n_cand) return;
+    const uint64_t k = ckey_sorted[p];
+    if (k == KEY_NONE) return;
+    if (p == 0 || ckey_sorted[p - 1] != k) first[cidx_sorted[p]] = 1u;
+}
+
+// Apply the accepted candidates (first valid ones, rank < k_target): write
+// the slot of a surviving tile, else emit a scattered insert + its window.
+__global__ void k_syn_insert(int64_t n_cand, const uint32_t *first, const uint32_t *rank, int64_t k_target,
+                             const int32_t *cr, const int32_t *cc, const float *cv, const float *cs,
+                             uint32_t default_imp, ScaleView sc, const uint64_t *tkey, int64_t T,
+                             const uint8_t *alive, uint8_t *tbytes, uint64_t bcols, uint64_t *ins_key,
+                             uint8_t *ins_byte, uint64_t *win, unsigned long long *n_grown) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= n_cand) return;
+    ins_key[i] = KEY_NONE;
+    ins_byte[i] = 0;
+    win[i] = KEY_NONE;
+    if (!first[i] || (int64_t)rank[i] >= k_target) return;
+    atomicAdd(n_grown, 1ull);
+    const uint32_t r = (uint32_t)cr[i], c = (uint32_t)cc[i];
+    const float S = scale_at(sc, r, c);
+    const uint32_t wc = fp4_encode(cv[i] / S);
+    const uint32_t ic = cs ? fp4_encode(cs[i]) : (default_imp & 0xFu);
+    const uint64_t wkey = (uint64_t)(r >> 2) * bcols + (uint64_t)(c >> 2);
+    const int64_t t = find_tile(tkey, T, alive, wkey);
+    if (t >= 0) {
+        tbytes[t * 16 + (c & 3u) * 4u + (r & 3u)] = (uint8_t)((ic << 4) | wc);
+    } else {
+        ins_key[i] = rc_key(r, c);
+        ins_byte[i] = (uint8_t)((wc << 4) | ic);
+        win[i] = wkey;
+    }
+}
+
+// One thread per distinct touched window: count its scattered synapses
+// (final set, sorted); >= 2 makes a new tile (nibbles requantized and
+// swapped into the tile byte order) and removes them from the set.
+__global__ void k_syn_promote(int64_t n_win, const uint64_t *win_sorted, const uint64_t *key2, int64_t n2,
+                              const uint8_t *byte2, uint64_t bcols, int64_t n_in, uint8_t *removed2,
+                              uint32_t *nt_flag, uint32_t *nt_br, uint32_t *nt_bc, uint8_t *nt_bytes) {
+    const int64_t p = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (p >= n_win) return;
+    nt_flag[p] = 0u;
+    const uint64_t w = win_sorted[p];
+    if (w == KEY_NONE || (p > 0 && win_sorted[p - 1] == w)) return;
+    const uint32_t br = (uint32_t)(w / bcols), bc = (uint32_t)(w % bcols);
+    int64_t lo[4], hi[4];
+    int cnt = 0;
+    for (uint32_t li = 0; li < 4u; ++li) {
+        const uint32_t r = br * 4u + li;
+        if (r >= n_in) { lo[li] = hi[li] = 0; continue; }
+        lo[li] = lower_bound_u64(key2, n2, rc_key(r, bc * 4u));
+        hi[li] = lower_bound_u64(key2, n2, rc_key(r, bc * 4u + 4u));
+        cnt += (int)(hi[li] - lo[li]);
+    }
+    if (cnt < 2) return;
+    uint8_t d[16] = {0};
+    for (uint32_t li = 0; li < 4u; ++li)
+        for (int64_t e = lo[li]; e < hi[li]; ++e) {
+            const uint32_t c = (uint32_t)(key2[e] & 0xFFFFFFFFu);
+            const uint32_t b = byte2[e];
+            d[(c - bc * 4u) * 4u + li] = (uint8_t)(requant(b >> 4) | (requant(b & 0xFu) << 4));
+            removed2[e] = 1;
+        }
+    nt_flag[p] = 1u;
+    nt_br[p] = br;
+    nt_bc[p] = bc;
+    for (int s = 0; s < 16; ++s) nt_bytes[p * 16 + s] = d[s];
+}
+
+__global__ void k_flag_final(int64_t n2, const uint64_t *key2, const uint8_t *removed2, uint32_t *flag) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n2) flag[i] = (key2[i] != KEY_NONE && !removed2[i]) ? 1u : 0u;
+}
+
+__global__ void k_emit_final(int64_t n2, const uint64_t *key2, const uint8_t *byte2, const uint32_t *flag,
+                             const uint32_t *pos, uint32_t *rows, uint32_t *cols, uint8_t *bytes) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= n2 || !flag[i]) return;
+    const uint32_t o = pos[i];
+    rows[o] = (uint32_t)(key2[i] >> 32);
+    cols[o] = (uint32_t)(key2[i] & 0xFFFFFFFFu);
+    bytes[o] = byte2[i];
+}
+
+// ptrs[r] = first index of row r in rows[0, n) (sorted), r in [0, nrows].
+__global__ void k_row_ptrs(const uint32_t *rows, int64_t n, int64_t nrows, uint32_t *ptrs) {
+    const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (r > nrows) return;
+    int64_t lo = 0, hi = n;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if ((int64_t)rows[mid] < r) lo = mid + 1;
+        else hi = mid;
+    }
+    ptrs[r] = (uint32_t)lo;
+}
+
+// Tiles out: surviving old tiles [0, T) then promoted windows [T, T + n_win).
+__global__ void k_tile_flags(int64_t T, const uint8_t *alive, int64_t n_win, const uint32_t *nt_flag,
+                             uint32_t *flag) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < T) flag[i] = alive[i] ? 1u : 0u;
+    else if (i < T + n_win) flag[i] = nt_flag[i - T];
+}
+
+__global__ void k_emit_tiles(int64_t T, const uint32_t *tbr, const uint32_t *tbc, const uint8_t *tbytes,
+                             int64_t n_win, const uint32_t *nt_br, const uint32_t *nt_bc,
+                             const uint8_t *nt_bytes, const uint32_t *flag, const uint32_t *pos,
+                             uint32_t *obr, uint32_t *obc, uint8_t *obytes) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= T + n_win || !flag[i]) return;
+    const uint32_t o = pos[i];
+    const bool old = i < T;
+    const int64_t j = old ? i : i - T;
+    obr[o] = old ? tbr[j] : nt_br[j];
+    obc[o] = old ? tbc[j] : nt_bc[j];
+    const uint8_t *src = old ? tbytes + j * 16 : nt_bytes + j * 16;
+    for (int s = 0; s < 16; ++s) obytes[(int64_t)o * 16 + s] = src[s];
+}
+
+template <typename T>
+T read_back(const T *d, hipStream_t st) {
+    T h{};
+    SILI_HIP(hipMemcpyAsync(&h, d, sizeof(T), hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipStreamSynchronize(st));
+    return h;
+}
+
+// Exclusive scan of flag[0, n) into pos; returns the total.
+int64_t compact_positions(Layer &L, const uint32_t *flag, uint32_t *pos, int64_t n) {
+    if (n == 0) return 0;
+    device_exclusive_scan_u32(L, flag, pos, n);
+    const uint32_t last_pos = read_back(pos + n - 1, L.stream);
+    const uint32_t last_flag = read_back(flag + n - 1, L.stream);
+    return (int64_t)last_pos + last_flag;
+}
+
+}  // namespace
+
+void synapto_step(Layer &L, float prune_frac, const int32_t *cand_r, const int32_t *cand_c,
+                  const float *cand_v, const float *cand_s, int64_t n_cand, int default_imp,
+                  int64_t *stats) {
+    hipStream_t st = L.stream;
+    const int64_t Ns = L.W.nnz, T = L.B4.ntiles;
+    const int64_t n_in = L.n_in, n_out = L.n_out;
+    const uint64_t bcols = (uint64_t)((n_out + 3) / 4);
+    const int64_t M = Ns + 16 * T;  // synapse slots considered
+    if (Ns + T + n_cand >= (int64_t(1) << 32) - 1 || M >= (int64_t(1) << 32) - 1)
+        throw_error(SILI_ERR_RANGE, "synapto_step: layer too large for one step");
+    const ScaleView sc = L.rank == 1
+        ? ScaleView{L.vs_ones ? nullptr : L.vs.p, L.os_ones ? nullptr : L.os.p, 1}
+        : ScaleView{L.vs.p, L.os.p, L.rank};
+
+    // -- decode both stores --------------------------------------------------
+    DevBuf<uint32_t> srow, scol, tbr, tbc;
+    srow.ensure((size_t)Ns + 1);
+    scol.ensure((size_t)Ns + 1);
+    tbr.ensure((size_t)T + 1);
+    tbc.ensure((size_t)T + 1);
+    if (Ns > 0) decode_scattered(L, srow.p, scol.p);
+    if (T > 0) launch_decode_b4(L.B4.plan(), tbr.p, tbc.p, st);
+    DevBuf<uint8_t> tbytes;  // tile bytes being edited (canonical order)
+    tbytes.ensure((size_t)T * 16 + 1);
+    if (T > 0) SILI_HIP(hipMemcpyAsync(tbytes.p, L.B4.tiles.p, (size_t)T * 16, hipMemcpyDeviceToDevice, st));
+    DevBuf<uint64_t> tkey;  // window keys of the canonical tiles (ascending)
+    tkey.ensure((size_t)T + 1);
+
+    // -- select: order by (|w| bits, row, col) -------------------------------
+    DevBuf<uint64_t> rc, rc_sorted;
+    DevBuf<uint32_t> absw, absw_rc, absw_sorted, iota, perm_rc, order;
+    DevBuf<unsigned long long> counters;  // live slots, demoted, grown
+    counters.ensure(4);
+    rc.ensure((size_t)M + 1);
+    rc_sorted.ensure((size_t)M + 1);
+    absw.ensure((size_t)M + 1);
+    absw_rc.ensure((size_t)M + 1);
+    absw_sorted.ensure((size_t)M + 1);
+    iota.ensure((size_t)M + 1);
+    perm_rc.ensure((size_t)M + 1);
+    order.ensure((size_t)M + 1);
+    {
+        std::vector<unsigned long long> z(4, 0ull);
+        SILI_HIP(hipMemcpyAsync(counters.p, z.data(), 4 * sizeof(unsigned long long), hipMemcpyHostToDevice, st));
+    }
+    if (M > 0) {
+        launch(k_syn_keys, dim3(nblk(M)), dim3(TPB), 0, st, Ns, (const uint32_t *)srow.p,
+               (const uint32_t *)scol.p, (const uint8_t *)L.W.val.p, T, (const uint32_t *)tbr.p,
+               (const uint32_t *)tbc.p, (const uint8_t *)L.B4.tiles.p, n_in, n_out, sc, rc.p, absw.p);
+        launch(k_iota32, dim3(nblk(M)), dim3(TPB), 0, st, iota.p, M);
+        SILI_HIP(hipGetLastError());
+        // (row, col) order, then a stable sort by |w| bits
+        device_sort_pairs_u64(L, rc.p, rc_sorted.p, iota.p, perm_rc.p, M, 64);
+        launch(k_count_live, dim3(1), dim3(64), 0, st, (const uint64_t *)rc_sorted.p, M, counters.p);
+        launch(k_gather_u32_by, dim3(nblk(M)), dim3(TPB), 0, st, (const uint32_t *)absw.p,
+               (const uint32_t *)perm_rc.p, M, absw_rc.p);
+        SILI_HIP(hipGetLastError());
+        device_sort_pairs_u32(L, absw_rc.p, absw_sorted.p, perm_rc.p, order.p, M, 32);
+    }
+    const int64_t N = (int64_t)read_back(counters.p, st);  // scattered + live block4 slots
+    const int64_t k = std::min<int64_t>(N, (int64_t)std::llround((double)prune_frac * (double)N));
+
+    // -- prune ---------------------------------------------------------------
+    DevBuf<uint8_t> s_removed, touched, alive, dem_byte;
+    DevBuf<uint64_t> pruned, pruned_sorted, dem_key;
+    DevBuf<uint32_t> pruned_v, pruned_vs;
+    s_removed.ensure((size_t)Ns + 1);
+    touched.ensure((size_t)T + 1);
+    alive.ensure((size_t)T + 1);
+    dem_byte.ensure((size_t)T + 1);
+    dem_key.ensure((size_t)T + 1);
+    pruned.ensure((size_t)k + 1);
+    pruned_sorted.ensure((size_t)k + 1);
+    pruned_v.ensure((size_t)k + 1);
+    pruned_vs.ensure((size_t)k + 1);
+    if (Ns > 0) launch(k_fill_u8, dim3(nblk(Ns)), dim3(TPB), 0, st, s_removed.p, Ns, (uint8_t)0);
+    if (T > 0) launch(k_fill_u8, dim3(nblk(T)), dim3(TPB), 0, st, touched.p, T, (uint8_t)0);
+    if (k > 0) {
+        launch(k_syn_prune, dim3(nblk(k)), dim3(TPB), 0, st, (const uint32_t *)order.p, k, Ns,
+               (const uint64_t *)rc.p, s_removed.p, tbytes.p, touched.p, pruned.p);
+        launch(k_iota32, dim3(nblk(k)), dim3(TPB), 0, st, pruned_v.p, k);
+        SILI_HIP(hipGetLastError());
+        device_sort_pairs_u64(L, pruned.p, pruned_sorted.p, pruned_v.p, pruned_vs.p, k, 64);
+    }
+
+    // -- demote --------------------------------------------------------------
+    if (T > 0) {
+        launch(k_syn_demote, dim3(nblk(T)), dim3(TPB), 0, st, T, (const uint32_t *)tbr.p,
+               (const uint32_t *)tbc.p, (const uint8_t *)tbytes.p, (const uint8_t *)touched.p, n_in, n_out,
+               alive.p, dem_key.p, dem_byte.p, counters.p + 1);
+        SILI_HIP(hipGetLastError());
+        // window keys of the canonical tiles, in store order (ascending)
+        launch(k_tile_wkeys, dim3(nblk(T)), dim3(TPB), 0, st, (const uint32_t *)tbr.p, (const uint32_t *)tbc.p,
+               T, bcols, tkey.p);
+        SILI_HIP(hipGetLastError());
+    }
+
+    // -- scattered set after prune + demote (sorted for lookups) --------------
+    const int64_t M2 = Ns + T + n_cand;
+    DevBuf<uint64_t> key2, key2_sorted, set1_sorted;
+    DevBuf<uint8_t> byte2, byte2_sorted, removed2;
+    DevBuf<uint32_t> iota2, perm2;
+    key2.ensure((size_t)M2 + 1);
+    key2_sorted.ensure((size_t)M2 + 1);
+    set1_sorted.ensure((size_t)(Ns + T) + 1);
+    byte2.ensure((size_t)M2 + 1);
+    byte2_sorted.ensure((size_t)M2 + 1);
+    removed2.ensure((size_t)M2 + 1);
+    iota2.ensure((size_t)M2 + 1);
+    perm2.ensure((size_t)M2 + 1);
+    if (Ns + T > 0) {
+        launch(k_syn_set1, dim3(nblk(Ns + T)), dim3(TPB), 0, st, Ns, T, (const uint64_t *)rc.p,
+               (const uint8_t *)L.W.val.p, (const uint8_t *)s_removed.p, (const uint64_t *)dem_key.p,
+               (const uint8_t *)dem_byte.p, key2.p, byte2.p);
+        launch(k_iota32, dim3(nblk(Ns + T)), dim3(TPB), 0, st, iota2.p, Ns + T);
+        SILI_HIP(hipGetLastError());
+        device_sort_pairs_u64(L, key2.p, set1_sorted.p, iota2.p, perm2.p, Ns + T, 64);
+    }
+
+    // -- candidates: first valid ones in list order ---------------------------
+    DevBuf<int32_t> dcr, dcc;
+    DevBuf<float> dcv, dcs;
+    DevBuf<uint64_t> ckey, ckey_sorted, win, win_sorted;
+    DevBuf<uint32_t> cidx, cidx_sorted, first, rank, wv, wvs;
+    if (n_cand > 0) {
+        dcr.ensure((size_t)n_cand);
+        dcc.ensure((size_t)n_cand);
+        dcv.ensure((size_t)n_cand);
+        SILI_HIP(hipMemcpyAsync(dcr.p, cand_r, (size_t)n_cand * 4, hipMemcpyHostToDevice, st));
+        SILI_HIP(hipMemcpyAsync(dcc.p, cand_c, (size_t)n_cand * 4, hipMemcpyHostToDevice, st));
+        SILI_HIP(hipMemcpyAsync(dcv.p, cand_v, (size_t)n_cand * 4, hipMemcpyHostToDevice, st));
+        if (cand_s) {
+            dcs.ensure((size_t)n_cand);
+            SILI_HIP(hipMemcpyAsync(dcs.p, cand_s, (size_t)n_cand * 4, hipMemcpyHostToDevice, st));
+        }
+        ckey.ensure((size_t)n_cand);
+        ckey_sorted.ensure((size_t)n_cand);
+        cidx.ensure((size_t)n_cand);
+        cidx_sorted.ensure((size_t)n_cand);
+        first.ensure((size_t)n_cand);
+        rank.ensure((size_t)n_cand);
+        win.ensure((size_t)n_cand);
+        win_sorted.ensure((size_t)n_cand);
+        wv.ensure((size_t)n_cand);
+        wvs.ensure((size_t)n_cand);
+        const unsigned g = nblk(n_cand);
+        launch(k_syn_cand_static, dim3(g), dim3(TPB), 0, st, n_cand, (const int32_t *)dcr.p,
+               (const int32_t *)dcc.p, n_in, n_out, (const uint64_t *)pruned_sorted.p, k,
+               (const uint64_t *)set1_sorted.p, Ns + T, (const uint64_t *)tkey.p, T,
+               (const uint8_t *)alive.p, (const uint8_t *)tbytes.p, bcols, ckey.p);
+        launch(k_iota32, dim3(g), dim3(TPB), 0, st, cidx.p, n_cand);
+        launch(k_fill_u32, dim3(g), dim3(TPB), 0, st, first.p, n_cand, 0u);
+        SILI_HIP(hipGetLastError());
+        device_sort_pairs_u64(L, ckey.p, ckey_sorted.p, cidx.p, cidx_sorted.p, n_cand, 64);
+        launch(k_syn_first, dim3(g), dim3(TPB), 0, st, n_cand, (const uint64_t *)ckey_sorted.p,
+               (const uint32_t *)cidx_sorted.p, first.p);
+        SILI_HIP(hipGetLastError());
+        device_exclusive_scan_u32(L, first.p, rank.p, n_cand);
+        launch(k_syn_insert, dim3(g), dim3(TPB), 0, st, n_cand, (const uint32_t *)first.p,
+               (const uint32_t *)rank.p, k, (const int32_t *)dcr.p, (const int32_t *)dcc.p,
+               (const float *)dcv.p, cand_s ? (const float *)dcs.p : nullptr, (uint32_t)default_imp, sc,
+               (const uint64_t *)tkey.p, T, (const uint8_t *)alive.p, tbytes.p, bcols, key2.p + (Ns + T),
+               byte2.p + (Ns + T), win.p, counters.p + 2);
+        launch(k_iota32, dim3(g), dim3(TPB), 0, st, wv.p, n_cand);
+        SILI_HIP(hipGetLastError());
+        device_sort_pairs_u64(L, win.p, win_sorted.p, wv.p, wvs.p, n_cand, 64);
+    }
+
+    // -- final scattered set (sorted) and promotion ---------------------------
+    if (M2 > 0) {
+        launch(k_iota32, dim3(nblk(M2)), dim3(TPB), 0, st, iota2.p, M2);
+        launch(k_fill_u8, dim3(nblk(M2)), dim3(TPB), 0, st, removed2.p, M2, (uint8_t)0);
+        SILI_HIP(hipGetLastError());
+        device_sort_pairs_u64(L, key2.p, key2_sorted.p, iota2.p, perm2.p, M2, 64);
+        launch(k_gather_u8_by, dim3(nblk(M2)), dim3(TPB), 0, st, (const uint8_t *)byte2.p,
+               (const uint32_t *)perm2.p, M2, byte2_sorted.p);
+        SILI_HIP(hipGetLastError());
+    }
+    DevBuf<uint32_t> nt_flag, nt_br, nt_bc;
+    DevBuf<uint8_t> nt_bytes;
+    nt_flag.ensure((size_t)n_cand + 1);
+    nt_br.ensure((size_t)n_cand + 1);
+    nt_bc.ensure((size_t)n_cand + 1);
+    nt_bytes.ensure((size_t)n_cand * 16 + 1);
+    if (n_cand > 0) {
+        launch(k_syn_promote, dim3(nblk(n_cand)), dim3(TPB), 0, st, n_cand, (const uint64_t *)win_sorted.p,
+               (const uint64_t *)key2_sorted.p, M2, (const uint8_t *)byte2_sorted.p, bcols, n_in,
+               removed2.p, nt_flag.p, nt_br.p, nt_bc.p, nt_bytes.p);
+        SILI_HIP(hipGetLastError());
+    }
+
+    // -- compaction + rebuild -------------------------------------------------
+    DevBuf<uint32_t> fflag, fpos, frows, fcols, fptrs;
+    DevBuf<uint8_t> fbytes;
+    fflag.ensure((size_t)M2 + 1);
+    fpos.ensure((size_t)M2 + 1);
+    if (M2 > 0) {
+        launch(k_flag_final, dim3(nblk(M2)), dim3(TPB), 0, st, M2, (const uint64_t *)key2_sorted.p,
+               (const uint8_t *)removed2.p, fflag.p);
+        SILI_HIP(hipGetLastError());
+    }
+    const int64_t n_final = compact_positions(L, fflag.p, fpos.p, M2);
+    frows.ensure((size_t)n_final + 1);
+    fcols.ensure((size_t)n_final + 1);
+    fbytes.ensure((size_t)n_final + 1);
+    fptrs.ensure((size_t)n_in + 1);
+    if (M2 > 0) {
+        launch(k_emit_final, dim3(nblk(M2)), dim3(TPB), 0, st, M2, (const uint64_t *)key2_sorted.p,
+               (const uint8_t *)byte2_sorted.p, (const uint32_t *)fflag.p, (const uint32_t *)fpos.p, frows.p,
+               fcols.p, fbytes.p);
+        SILI_HIP(hipGetLastError());
+    }
+    launch(k_row_ptrs, dim3(nblk(n_in + 1)), dim3(TPB), 0, st, (const uint32_t *)frows.p, n_final, n_in,
+           fptrs.p);
+    SILI_HIP(hipGetLastError());
+
+    const int64_t MT = T + n_cand;
+    DevBuf<uint32_t> tflag, tpos, obr, obc;
+    DevBuf<uint8_t> obytes;
+    tflag.ensure((size_t)MT + 1);
+    tpos.ensure((size_t)MT + 1);
+    if (MT > 0) {
+        launch(k_tile_flags, dim3(nblk(MT)), dim3(TPB), 0, st, T, (const uint8_t *)alive.p, n_cand,
+               (const uint32_t *)nt_flag.p, tflag.p);
+        SILI_HIP(hipGetLastError());
+    }
+    const int64_t n_tiles = compact_positions(L, tflag.p, tpos.p, MT);
+    obr.ensure((size_t)n_tiles + 1);
+    obc.ensure((size_t)n_tiles + 1);
+    obytes.ensure((size_t)n_tiles * 16 + 1);
+    if (MT > 0) {
+        launch(k_emit_tiles, dim3(nblk(MT)), dim3(TPB), 0, st, T, (const uint32_t *)tbr.p,
+               (const uint32_t *)tbc.p, (const uint8_t *)tbytes.p, n_cand, (const uint32_t *)nt_br.p,
+               (const uint32_t *)nt_bc.p, (const uint8_t *)nt_bytes.p, (const uint32_t *)tflag.p,
+               (const uint32_t *)tpos.p, obr.p, obc.p, obytes.p);
+        SILI_HIP(hipGetLastError());
+    }
+    unsigned long long cnt[4];
+    SILI_HIP(hipMemcpyAsync(cnt, counters.p, sizeof(cnt), hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipStreamSynchronize(st));
+
+    build_scattered(L, L.W, n_in, n_out, n_final, fptrs.p, fcols.p, fbytes.p);
+    build_shadow(L, L.W, frows.p, fcols.p, L.Wt);
+    build_block4(L, n_tiles, obr.p, obc.p, obytes.p);
+    refresh_nonfinite(L);
+
+    int64_t n_promoted = n_tiles - (T - (int64_t)cnt[1]);
+    if (stats) {
+        stats[0] = k;
+        stats[1] = k;
+        stats[2] = (int64_t)cnt[2];
+        stats[3] = (int64_t)cnt[1];
+        stats[4] = n_promoted;
+        stats[5] = n_final;
+        stats[6] = n_tiles;
+    }
 }
 
 }  // namespace sili
