@@ -13,6 +13,8 @@ from __future__ import annotations
 import os
 import sys
 
+import hashlib
+
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -54,6 +56,11 @@ def fp4_cases(out):
         enc.append(bytes(buf[:n]).hex())
     out["uleb_values"] = kat
     out["uleb_hex"] = np.array(enc)
+    # the reference encoder over 2^22 seeded random fp32 bit patterns (NaN,
+    # Inf, subnormals included), kept as a SHA-256 of the code bytes
+    bits = Stream(7, 9).u64(1 << 22).astype(np.uint32)
+    codes = np.array([R.ref_fp4_encode(float(v)) for v in bits.view(np.float32)], np.uint8)
+    out["fp4_bits_sha256"] = np.array(hashlib.sha256(codes.tobytes()).hexdigest())
 
 
 def structure_case(out, name, n_in, n_out, ptrs, cols, w, imp=None):
