@@ -43,6 +43,7 @@ def parse():
     p.add_argument("--copies", type=int, default=0, help="0 = enough for > 512 MiB")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--synapto-reps", type=int, default=5, help="config 3: timed synaptogenesis steps")
     p.add_argument("--verbose", action="store_true")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run 3 device-to-device copies of MIB MiB (HBM counter calibration)")
@@ -117,6 +118,8 @@ class CAbi:
         L.sili_forward_dense.argtypes = [vp, vp, C.c_int64, vp, vp]
         L.sili_backward_dense.argtypes = [vp, vp, vp, C.c_int64, vp, vp, vp, C.c_float, vp]
         L.sili_sampled_gradw.argtypes = [vp, vp, vp, C.c_int64, vp, vp, vp]
+        L.sili_forward_sparse.argtypes = [vp, vp, vp, vp, C.c_int64, C.c_int64, vp, vp]
+        L.sili_backward_sparse.argtypes = [vp, vp, vp, vp, vp, C.c_int64, C.c_int64, vp, C.c_float, vp]
         L.sili_device_alloc.argtypes = [vp, C.c_size_t, C.POINTER(vp)]
         L.sili_device_free.argtypes = [vp, vp]
         L.sili_memcpy_h2d.argtypes = [vp, vp, vp, C.c_size_t]
@@ -162,13 +165,31 @@ def measured_traffic(label, config):
     return None
 
 
-def algorithmic(info, n_in, n_out, B):
+def uleb_row_bytes(ptrs, cols):
+    """Exact ULEB128 bytes of every row (deltas restart at 0 per row)."""
+    ptrs = np.asarray(ptrs, np.int64)
+    cols = np.asarray(cols, np.int64)
+    prev = np.zeros(len(cols), np.int64)
+    if len(cols):
+        prev[1:] = cols[:-1]
+        starts = ptrs[:-1][np.diff(ptrs) > 0]
+        prev[starts] = 0
+    d = cols - prev
+    lens = np.ones(len(cols), np.int64)
+    for k in (7, 14, 21, 28):
+        lens += d >= (1 << k)
+    csum = np.concatenate([[0], np.cumsum(lens)])
+    return csum[ptrs[1:]] - csum[ptrs[:-1]]
+
+
+def algorithmic(info, n_in, n_out, B, wl=None):
     """Algorithmic bytes per launch of each kernel (per-unit figures:
     Bv = 1 B/synapse, Bi = exact ULEB bytes, Bp = 8 B/row, Bs = 4 B per
-    row/col scale, activations 4 B per element)."""
+    row/col scale, activations 4 B per element; block4: 16 B/tile + exact
+    block-index bytes + 8 B per block row)."""
     nnz = info["nnz_scattered"]
     Bv, Bi, Bp, Bs = nnz, info["index_bytes"], 8 * (n_in + 1), 4 * (n_in + n_out)
-    return {
+    out = {
         "fwd:gather": Bv + Bi + Bp + Bs + 4 * B * n_in + 4 * B * n_out,
         "bwd:gather": Bv + Bi + Bp + Bs + 4 * B * n_out + 4 * B * n_in,
         "bwd:sddmm": Bi + Bp + 4 * B * n_in + 4 * B * n_out + 4 * nnz,
@@ -178,29 +199,134 @@ def algorithmic(info, n_in, n_out, B):
         "fwd:transpose": 8 * B * n_in,
         "bwd:transpose": 8 * B * n_out,
     }
+    T = info.get("n_tiles", 0)
+    if T:
+        bi = info.get("block_index_bytes", 0)
+        Bt_in = 16 * T + bi + 8 * ((n_in + 3) // 4 + 1)
+        Bt_out = 16 * T + bi + 8 * ((n_out + 3) // 4 + 1)
+        out["fwd:gather_b4"] = Bt_out + Bs + 4 * B * n_in + 4 * B * n_out
+        out["bwd:gather_b4"] = Bt_in + Bs + 4 * B * n_out + 4 * B * n_in
+        out["bwd:sddmm_b4"] = (Bt_in - 16 * T) + 4 * B * n_in + 4 * B * n_out + 4 * 16 * T
+    if wl is not None and wl.x_ptrs is not None and wl.cols is not None:
+        # sparse-input forward: value + index bytes of the rows any batch row
+        # activates, row starts, scales, the input CSR and the dense output
+        active = np.zeros(n_in, bool)
+        active[np.asarray(wl.x_idx, np.int64)] = True
+        rb = uleb_row_bytes(wl.ptrs, wl.cols)
+        rl = np.diff(np.asarray(wl.ptrs, np.int64))
+        s_act = int((rb[active] + rl[active]).sum())
+        out["fwd_sparse:gather"] = s_act + Bp + Bs + 8 * len(wl.x_idx) + 4 * (B + 1) + 4 * B * n_out
+    return out
 
 
-def cpu_baseline(wl, seconds):
+STEP_DOC = {
+    0: "step = forward (batch 1)",
+    1: "step = forward + grad-input + nnz-sampled grad-W",
+    2: "step = sparse-input forward (10% active inputs per batch row) + grad-input",
+    3: "step = block4 forward + grad-input + nnz-sampled grad-W (every slot)",
+}
+
+
+def workload_text(cfg, wl):
+    shapes = {0: "205 distinct columns per row", 1: "Poisson(164) rows", 2: "Zipf(1.2) rows, 1% density",
+              3: "block4 tiles at 3% block density, every slot live"}
+    fmt = "FP4 block4" if cfg == 3 else "FP4 delta-CSR"
+    return f"config {cfg}: {wl.n_in}x{wl.n_out} {fmt}, {shapes[cfg]}, batch {wl.batch}; {STEP_DOC[cfg]}"
+
+
+def build_copy(cfg, wl, hip, api):
+    """One layer plus its device-resident activations for config `cfg`."""
+    B, n_in, n_out = wl.batch, wl.n_in, wl.n_out
+    n_tiles = 0 if wl.tile_br is None else len(wl.tile_br)
+    L = hip.SparseLinearLayer(n_in, n_out, max(1, wl.nnz + 16 * n_tiles))
+    if wl.cols is not None:
+        L.load_weights(wl.ptrs, wl.cols, wl.q)
+    if wl.tile_br is not None:
+        L.load_block4_tiles(wl.tile_br, wl.tile_bc, wl.tile_bytes)
+    L.set_value_scales(wl.value_scale)
+    L.forward_dense(wl.x[:1])  # flushes scales, sizes workspaces
+    h = C.c_void_p(L.handle)
+    info = L.info()
+    d = {"L": L, "h": h, "info": info, "x": api.upload(h, wl.x.astype(np.float32)),
+         "y": api.alloc(h, 4 * B * n_out)}
+    if cfg != 0:
+        d["g"] = api.upload(h, wl.g.astype(np.float32))
+        d["dx"] = api.alloc(h, 4 * B * n_in)
+    if cfg == 1:
+        d["gws"] = api.alloc(h, 4 * max(1, info["nnz_scattered"]))
+    if cfg == 3:
+        d["gwb"] = api.alloc(h, 4 * 16 * max(1, info["n_tiles"]))
+    if cfg == 2:
+        d["xp"] = api.upload(h, np.asarray(wl.x_ptrs, np.int32))
+        d["xi"] = api.upload(h, np.asarray(wl.x_idx, np.int32))
+        d["xv"] = api.upload(h, np.asarray(wl.x_vals, np.float32))
+        d["nnz_x"] = len(wl.x_idx)
+    # weights (both orientations) + activations + outputs + workspaces
+    d["bytes"] = (2 * (info["nnz_scattered"] + info["index_bytes"]) + 2 * 16 * info["n_tiles"]
+                  + 4 * B * (3 * n_in + 3 * n_out) + 4 * info["nnz_scattered"] + 4 * 16 * info["n_tiles"])
+    return d
+
+
+def make_step(cfg, api, B, stream):
+    L = api.L
+
+    def step(d):
+        h = d["h"]
+        if cfg == 2:
+            api.ck(L.sili_forward_sparse(h, d["xp"], d["xi"], d["xv"], d["nnz_x"], B, d["y"], stream))
+            api.ck(L.sili_backward_dense(h, d["x"], d["g"], B, d["dx"], None, None, 0.0, stream))
+            return
+        api.ck(L.sili_forward_dense(h, d["x"], B, d["y"], stream))
+        if cfg == 1:
+            # x = NULL: backward reads the forward's stored input (feature-major
+            # copy), as the reference's backward_dense reads its last_input
+            api.ck(L.sili_backward_dense(h, None, d["g"], B, d["dx"], d["gws"], None, 0.0, stream))
+        elif cfg == 3:
+            api.ck(L.sili_backward_dense(h, None, d["g"], B, d["dx"], None, d["gwb"], 0.0, stream))
+    return step
+
+
+def cpu_baseline(cfg, wl, seconds):
     """The CPU port (oracle/: the reference's algorithm, OpenMP, per-thread
-    private outputs + serial reduce) on this host, same workload."""
+    private outputs + serial reduce) on this host, same workload and step."""
     from oracle import HostLayer, have_ref
     threads = os.cpu_count() or 1
-    H = HostLayer(wl.n_in, wl.n_out).load_csr(wl.ptrs, wl.cols, w=wl.q).set_scales(wl.value_scale)
+    H = HostLayer(wl.n_in, wl.n_out)
+    if wl.cols is not None:
+        H.load_csr(wl.ptrs, wl.cols, w=wl.q)
+    if wl.tile_br is not None:
+        H.load_tiles(wl.tile_br, wl.tile_bc, wl.tile_bytes)
+    H.set_scales(wl.value_scale)
+    x, g, B = wl.x.astype(np.float32), None if wl.g is None else wl.g.astype(np.float32), wl.batch
+
+    def step():
+        if cfg == 0:
+            H.forward_dense(x, threads=threads)
+        elif cfg == 2:
+            H.forward_sparse(wl.x_ptrs, wl.x_idx, wl.x_vals, B, threads=threads)
+            H.backward_dense(x, g, threads=threads)
+        else:
+            H.forward_dense(x, threads=threads)
+            H.backward_dense(x, g, threads=threads)
+            H.sampled_gradw(x, g, threads=threads)
     times = []
     t_end = time.perf_counter() + seconds
     while True:
         t0 = time.perf_counter()
-        H.forward_dense(wl.x, threads=threads)
-        H.backward_dense(wl.x, wl.g, threads=threads)
-        H.sampled_gradw(wl.x, wl.g, threads=threads)
+        step()
         times.append(time.perf_counter() - t0)
         if time.perf_counter() > t_end or len(times) >= 50:
             break
     med = float(np.median(times))
-    out = {"value": round(wl.nnz / med / 1e9, 4), "unit": "GNNZ/s", "cores": threads, "kind": "port",
-           "sample": f"full config-{wl.name[1:]} step (fwd + grad-input + sampled grad-W), "
-                     f"{len(times)} reps, median {med * 1e3:.1f} ms/step"}
-    if have_ref():
+    units = wl.nnz + (0 if wl.tile_br is None else 16 * len(wl.tile_br))
+    out = {"value": round(units / med / 1e9, 5), "unit": "GNNZ/s", "cores": threads, "kind": "port",
+           "sample": f"full config-{cfg} step ({STEP_DOC[cfg][7:]}), {len(times)} reps, "
+                     f"median {med * 1e3:.1f} ms/step"}
+    if cfg == 3 and wl.cand_r is not None:
+        t0 = time.perf_counter()
+        H.synapto_step(0.01, wl.cand_r, wl.cand_c, wl.cand_v)
+        out["synapto_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
+    if cfg == 1 and have_ref():
         from oracle import RefLayer
         R = RefLayer(wl.n_in, wl.n_out, wl.ptrs, wl.cols, wl.q).set_scales(wl.value_scale)
         R.compact()
@@ -208,8 +334,8 @@ def cpu_baseline(wl, seconds):
         t_end = time.perf_counter() + seconds / 2
         while True:
             t0 = time.perf_counter()
-            R.forward_dense(wl.x, threads=threads)
-            R.backward_dense(wl.x, wl.g, threads=threads)
+            R.forward_dense(x, threads=threads)
+            R.backward_dense(x, g, threads=threads)
             rt.append(time.perf_counter() - t0)
             if time.perf_counter() > t_end or len(rt) >= 30:
                 break
@@ -219,11 +345,37 @@ def cpu_baseline(wl, seconds):
     return out
 
 
+def time_synapto(hip, wl, reps):
+    """GPU bulk synaptogenesis on config 3: prune 1% by |w|, regrow at fresh
+    seeded candidates, rebuild both stores; wall time of the synchronous call
+    (candidate upload included)."""
+    from sili__new_amd.synth import SEED0, Stream
+    n_tiles = len(wl.tile_br)
+    L = hip.SparseLinearLayer(wl.n_in, wl.n_out, 16 * n_tiles + 1024)
+    L.load_block4_tiles(wl.tile_br, wl.tile_bc, wl.tile_bytes)
+    L.set_value_scales(wl.value_scale)
+    L.synchronize()
+    cands = [(wl.cand_r, wl.cand_c, wl.cand_v)]
+    m = len(wl.cand_r)
+    for i in range(1, reps + 1):
+        st = Stream(SEED0 + 3, 100 + i)
+        cands.append((st.integers(m, wl.n_in).astype(np.int32), st.integers(m, wl.n_out).astype(np.int32),
+                      Stream(SEED0 + 3, 200 + i).normal(m, 0.01)))
+    L.synapto_step(0.01, *cands[0])  # warm-up (allocations, code objects)
+    times, stats = [], None
+    for i in range(1, reps + 1):
+        t0 = time.perf_counter()
+        stats = L.synapto_step(0.01, *cands[i])
+        times.append((time.perf_counter() - t0) * 1e3)
+    return {"ms_median": round(float(np.median(times)), 3), "ms_min": round(min(times), 3), "reps": reps,
+            "last_stats": stats}
+
+
 def main():
     a = parse()
     if a.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU: the layer is sharded by output "
-                                   "columns only on paper, no multi-GPU path is built -- run with --gpus 1"}))
+        print(json.dumps({"error": "this build runs on one GPU: the layer is sharded by input "
+                                   "rows only on paper, no multi-GPU path is built -- run with --gpus 1"}))
         sys.exit(2)
     if a.copy_probe:
         n = Hip().copy_probe(a.copy_probe)
@@ -232,47 +384,29 @@ def main():
     import sili__new_amd as hip
     from sili__new_amd.synth import make_config
 
-    wl = make_config(a.config)
+    cfg = a.config
+    wl = make_config(cfg)
     B, n_in, n_out = wl.batch, wl.n_in, wl.n_out
     api = CAbi(hip.LIB_PATH)
     rt = Hip()
 
-    # one layer + activation set per copy, all driven on copy 0's stream
-    per_copy = None
-    layers, bufs = [], []
+    # one layer + activation set per copy, all driven on copy 0's stream;
+    # enough copies (> 512 MiB) that the 256 MiB MALL cannot serve a step
+    # from the previous one
     copies = a.copies
     t_build = time.perf_counter()
-    while True:
-        L = hip.SparseLinearLayer(n_in, n_out, wl.nnz)
-        L.load_weights(wl.ptrs, wl.cols, wl.q)
-        L.set_value_scales(wl.value_scale)
-        L.forward_dense(wl.x[:1])  # flushes scales, sizes workspaces
-        h = C.c_void_p(L.handle)
-        info = L.info()
-        x = api.upload(h, wl.x)
-        g = api.upload(h, wl.g)
-        y = api.alloc(h, 4 * B * n_out)
-        dx = api.alloc(h, 4 * B * n_in)
-        gw = api.alloc(h, 4 * max(1, info["nnz_scattered"]))
-        layers.append((L, h))
-        bufs.append((x, g, y, dx, gw))
-        if per_copy is None:
-            # weights (both orientations) + activations + outputs + workspaces
-            per_copy = 2 * (info["nnz_scattered"] + info["index_bytes"]) + 4 * B * (3 * n_in + 3 * n_out) \
-                + 4 * info["nnz_scattered"]
-            if copies <= 0:
-                copies = max(2, int(np.ceil(512 * 2**20 / per_copy)) + 1)
-        if len(layers) >= copies:
-            break
+    pool = [build_copy(cfg, wl, hip, api)]
+    per_copy = pool[0]["bytes"]
+    if copies <= 0:
+        copies = max(2, int(np.ceil(512 * 2**20 / per_copy)) + 1)
+    while len(pool) < copies:
+        pool.append(build_copy(cfg, wl, hip, api))
     t_build = time.perf_counter() - t_build
-    stream = api.L.sili_stream(layers[0][1])
+    stream = api.L.sili_stream(pool[0]["h"])
+    run = make_step(cfg, api, B, stream)
 
     def step(i):
-        (_, h), (x, g, y, dx, gw) = layers[i % copies], bufs[i % copies]
-        api.ck(api.L.sili_forward_dense(h, x, B, y, stream))
-        # x = NULL: backward reads the forward's stored input (feature-major
-        # copy), as the reference's backward_dense reads its last_input
-        api.ck(api.L.sili_backward_dense(h, None, g, B, dx, gw, None, 0.0, stream))
+        run(pool[i % copies])
 
     for i in range(a.warmup):
         step(i)
@@ -288,8 +422,7 @@ def main():
     rt.record(e1, stream)
     rt.sync()
     wall = time.perf_counter() - t0
-    ms = rt.elapsed_ms(e0, e1)
-    ms_step = ms / a.steps
+    ms_step = rt.elapsed_ms(e0, e1) / a.steps
 
     # warm (cache-resident) rate: a single copy, same step count
     w0, w1 = rt.event(), rt.event()
@@ -301,9 +434,10 @@ def main():
     rt.sync()
     warm_ms_step = rt.elapsed_ms(w0, w1) / a.steps
 
-    # profiled pass (same steps): per-kernel HIP events on the launch stream
-    for _, h in layers:
-        api.ck(api.L.sili_profile_enable(h, 1))
+    # profiled pass (same steps): per-kernel times from the dispatches' own
+    # begin/end stamps, on the stream the kernels run on
+    for d in pool:
+        api.ck(api.L.sili_profile_enable(d["h"], 1))
     p0, p1 = rt.event(), rt.event()
     rt.record(p0, stream)
     for i in range(a.steps):
@@ -312,30 +446,53 @@ def main():
     rt.sync()
     prof_ms_step = rt.elapsed_ms(p0, p1) / a.steps
     kern = {}
-    for _, h in layers:
-        for name, (cnt, tot) in api.profile(h).items():
+    for d in pool:
+        for name, (cnt, tot) in api.profile(d["h"]).items():
             c0, t0_ = kern.get(name, (0, 0.0))
             kern[name] = (c0 + cnt, t0_ + tot)
-        api.ck(api.L.sili_profile_enable(h, 0))
-    info = layers[0][0].info()
-    alg = algorithmic(info, n_in, n_out, B)
-    dom = max(kern.items(), key=lambda kv: kv[1][1])
-    dom_name, (dom_cnt, dom_tot) = dom
+        api.ck(api.L.sili_profile_enable(d["h"], 0))
+    info = pool[0]["L"].info()
+    alg = algorithmic(info, n_in, n_out, B, wl)
+    dom_name, (dom_cnt, dom_tot) = max(kern.items(), key=lambda kv: kv[1][1])
     dom_avg_ms = dom_tot / dom_cnt
-    dom_bytes = alg.get(dom_name)
-    achieved = dom_bytes / (dom_avg_ms * 1e-3) / 1e9 if dom_bytes else None
 
-    nnz = info["nnz_scattered"]
-    # one step's algorithmic bytes: forward + grad-input + sampled grad-W,
-    # each op counted as if run alone (the fused backward moves less)
-    step_bytes = alg["fwd:gather"] + alg["bwd:gather"] + alg["bwd:sddmm"]
-    gnnz = nnz / (ms_step * 1e-3) / 1e9
+    nnz_s, n_tiles = info["nnz_scattered"], info["n_tiles"]
+    units = nnz_s + 16 * n_tiles  # stored synapses (scattered + block4 slots)
+    if cfg == 3:
+        # FP32-compute bound: 2 flops per slot per batch column
+        dom_flops = 2 * 16 * n_tiles * B
+        achieved = dom_flops / (dom_avg_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "kernel": dom_name, "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 5),
+                "traffic": measured_traffic(dom_name, cfg), "avg_launch_ms": round(dom_avg_ms, 5),
+                "algorithmic_flops": dom_flops, "algorithmic_bytes": alg.get(dom_name),
+                "note": "fp32 vector FMA work (no MFMA); peak is MI355X dense fp32"}
+        step_bytes = alg["fwd:gather_b4"] + alg["bwd:gather_b4"] + alg["bwd:sddmm_b4"]
+        flops = 3 * 2 * units * B
+    else:
+        dom_bytes = alg.get(dom_name)
+        achieved = dom_bytes / (dom_avg_ms * 1e-3) / 1e9 if dom_bytes else None
+        roof = {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 2) if achieved else None,
+                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 5) if achieved else None,
+                "traffic": measured_traffic(dom_name, cfg), "avg_launch_ms": round(dom_avg_ms, 5),
+                "algorithmic_bytes": dom_bytes}
+        if cfg == 0:
+            step_bytes = alg["fwd:gather"]
+            flops = 2 * units * B
+        elif cfg == 2:
+            step_bytes = alg["fwd_sparse:gather"] + alg["bwd:gather"]
+            flops = 2 * int(np.diff(wl.ptrs)[np.asarray(wl.x_idx)].sum()) + 2 * units * B
+        else:
+            # forward + grad-input + sampled grad-W, each op counted as if run
+            # alone (the fused backward moves less)
+            step_bytes = alg["fwd:gather"] + alg["bwd:gather"] + alg["bwd:sddmm"]
+            flops = 3 * 2 * units * B
     step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
-    flops = 3 * 2 * nnz * B
 
     out = {
         "metric": "FP4 delta-CSR SpMM GNNZ/s + achieved HBM GB/s (% of peak), fwd+bwd",
-        "value": round(gnnz, 4),
+        "value": round(units / (ms_step * 1e-3) / 1e9, 4),
         "unit": "GNNZ/s",
         "n_gpus": 1,
         "steps": a.steps,
@@ -347,35 +504,25 @@ def main():
         "dtype": "fp32",
         "data": "synthetic",
         "config": {
-            "workload": f"config {a.config}: {n_in}x{n_out} FP4 delta-CSR, Poisson(164) rows, batch {B}; "
-                        "step = forward + grad-input + nnz-sampled grad-W",
-            "n_in": n_in, "n_out": n_out, "batch": B, "nnz": nnz, "index_bytes": info["index_bytes"],
+            "workload": workload_text(cfg, wl),
+            "n_in": n_in, "n_out": n_out, "batch": B, "nnz": units, "nnz_scattered": nnz_s,
+            "n_tiles": n_tiles, "index_bytes": info["index_bytes"],
             "copies_rotated": copies, "rotation_mib": round(copies * per_copy / 2**20, 1),
         },
         "achieved_gbs": round(step_gbs, 2),
         "pct_hbm_peak": round(100.0 * step_gbs / HBM_PEAK_GBS, 3),
         "gflops": round(flops / (ms_step * 1e-3) / 1e9, 2),
         "warm_ms_per_step": round(warm_ms_step, 5),
-        "warm_value": round(nnz / (warm_ms_step * 1e-3) / 1e9, 4),
+        "warm_value": round(units / (warm_ms_step * 1e-3) / 1e9, 4),
         "wall_s_timed": round(wall, 4),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": dom_name,
-            "achieved": round(achieved, 2) if achieved else None,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 5) if achieved else None,
-            "traffic": measured_traffic(dom_name, a.config),
-            "avg_launch_ms": round(dom_avg_ms, 5),
-            "algorithmic_bytes": dom_bytes,
-        },
+        "roofline": roof,
         "kernels_ms_per_step": {k: round(v[1] / a.steps, 5) for k, v in kern.items()},
         "profiled_ms_per_step": round(prof_ms_step, 5),
     }
-    if not a.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(wl, a.cpu_seconds)
-    else:
-        out["cpu_baseline"] = None
+    if cfg == 3 and a.synapto_reps > 0:
+        pool.clear()
+        out["synapto_gpu"] = time_synapto(hip, wl, a.synapto_reps)
+    out["cpu_baseline"] = None if a.no_cpu_baseline else cpu_baseline(cfg, wl, a.cpu_seconds)
     if a.verbose:
         print(f"build {t_build:.1f}s copies {copies}", file=sys.stderr)
     print(json.dumps(out), flush=True)

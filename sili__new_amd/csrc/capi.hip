@@ -230,11 +230,12 @@ void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st
     // the feature-major copy doubles as the stored forward input that
     // backward_dense reads when called without x (sili/cpu_backend.cpp:481)
     L.xT_cached_batch = B > 1 ? B : 0;
-    if (L.Wt.has_split) fill(y, B * L.n_out, 0.0f, st);
+    if (L.Wt.nnz == 0 || L.Wt.has_split) fill(y, B * L.n_out, 0.0f, st);
     // scattered pass skips exact-zero inputs (linear_disldo.hpp:114); only
     // observable with non-finite weights, so the skip is compiled in only then
-    launch_gather(L.Wt.plan(), shadow_scales(L), xT, B, y, L.n_out, B,
-                  L.has_nonfinite ? SKIP_ZERO : SKIP_NONE, st);
+    if (L.Wt.nnz > 0)
+        launch_gather(L.Wt.plan(), shadow_scales(L), xT, B, y, L.n_out, B,
+                      L.has_nonfinite ? SKIP_ZERO : SKIP_NONE, st);
     if (L.B4t.ntiles > 0)
         launch_gather_b4(L.B4t.plan(), shadow_scales(L), xT, B, y, L.n_out, B, SKIP_NONE, st);
 }
@@ -258,18 +259,20 @@ void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float 
     // accumulators always advance (linear_disldo.hpp:515-520); sum|x| rides
     // on the grad-W kernel when it runs
     const float *gT = to_feature_major(L, L.ws_gT, dy, B, L.n_out, L.acc_grad.p, st);
-    if (!gw_s) {
+    const bool scat = L.W.nnz > 0;
+    // sum|x| rides on the scattered grad-W kernel when that runs
+    if (!(scat && gw_s)) {
         if (xT) launch_rowabs(xT, B, L.n_in, L.acc_in.p, st);
         else launch_colabs(x, B, L.n_in, L.acc_in.p, st);
     }
-    if (L.W.has_split) fill(dx, B * L.n_in, 0.0f, st);
+    if (!scat || L.W.has_split) fill(dx, B * L.n_in, 0.0f, st);
     // grad-input and grad-W read the same gT row per synapse: one fused pass
-    const bool fused = gw_s && launch_bwd_fused(L.W.plan(), canon_scales(L), gT, xT, B, dx, L.n_in, gw_s,
-                                                L.acc_in.p, st);
-    if (!fused) launch_gather(L.W.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
+    const bool fused = scat && gw_s &&
+                       launch_bwd_fused(L.W.plan(), canon_scales(L), gT, xT, B, dx, L.n_in, gw_s, L.acc_in.p, st);
+    if (scat && !fused) launch_gather(L.W.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
     if (L.B4.ntiles > 0)
         launch_gather_b4(L.B4.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
-    if (gw_s && !fused) launch_sddmm(L.W.plan(), xT, gT, B, gw_s, L.acc_in.p, st);
+    if (scat && gw_s && !fused) launch_sddmm(L.W.plan(), xT, gT, B, gw_s, L.acc_in.p, st);
     if (gw_b && L.B4.ntiles > 0) launch_sddmm_b4(L.B4.plan(), nullptr, xT, gT, B, gw_b, st);
 }
 

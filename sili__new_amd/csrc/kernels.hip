@@ -708,6 +708,182 @@ __global__ __launch_bounds__(256) void k_bwd_v4(FArgs a) {
                              reinterpret_cast<float *>(&s_ent[0][0]), ENT_CAP * 2u, a.dx, a.dx_ld);
 }
 
+// Block epilogue for block4 waves: out[b, 4*brow+li] for the block's (up to
+// WAVES) segments over one batch chunk [b0, b0 + nbc).  Each wave leaves its
+// results in its LDS slice, row li at li * row_stride; the block then writes them
+// with consecutive lanes on consecutive rows (the 4*WAVES rows of one batch
+// index form one run when the block rows are consecutive).  The results
+// add to out (the scattered pass wrote it first); split rows add
+// atomically.  Every thread of the block calls this.
+__device__ __forceinline__ void store_rows4_block(bool active, uint32_t brow, bool split, uint32_t b0,
+                                                  uint32_t nbc, uint32_t row_stride, const float *slice_base,
+                                                  uint32_t slice_stride, int64_t rows, float *out, int64_t out_ld) {
+    __shared__ uint32_t s_brow[WAVES];
+    __shared__ uint32_t s_flag[WAVES];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    if (lane == 0) {
+        s_brow[wave] = brow;
+        s_flag[wave] = (active ? 1u : 0u) | (split ? 2u : 0u);
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < nbc * 4u * WAVES; i += blockDim.x) {
+        const uint32_t li = i & 3u, w = (i >> 2) % WAVES, b = i / (4u * WAVES);
+        const uint32_t f = s_flag[w];
+        const int64_t r = (int64_t)s_brow[w] * 4 + li;
+        if (!(f & 1u) || r >= rows) continue;
+        const float v = slice_base[w * slice_stride + li * row_stride + b];
+        float *o = out + (int64_t)(b0 + b) * out_ld + r;
+        if (f & 2u) atomicAdd(o, v);
+        else *o += v;
+    }
+}
+
+// Block4 gather with float4 batch lanes (dense paths, no skip rules): one
+// wave per (segment, batch chunk of 4*BL*KB columns -- blockIdx.y).  The
+// segment's block-column deltas are decoded 64 at a time; the lane that
+// decodes a tile dequantises its 16 slots into LDS (one 16-byte tile load);
+// then G = 64/BL tiles per load instruction, U tiles per group in flight,
+// each lane loading the 4 input rows 4bc+lj of its tile (float4 chunks of
+// the batch) and accumulating the tile's 4 output rows.  Needs nb % 4 == 0,
+// in_ld % 4 == 0, a 16-byte aligned `in` and a < 2 GiB input.
+template <int BL, int KB, int U>
+__global__ __launch_bounds__(256) void k_gather_b4_v4(BArgs a, uint32_t in_bytes) {
+    __shared__ uint32_t s_off[WAVES][64];
+    __shared__ __align__(16) float s_w[WAVES][64 * 16];
+    constexpr uint32_t G = 64u / BL;
+    constexpr uint32_t STEP = G * U;
+    constexpr uint32_t NBC = 4u * BL * KB;  // batch columns per wave
+    static_assert(4u * NBC <= 64u * 16u, "output slice must fit the weight table");
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
+    const bool active = si < a.nseg;
+    const uint32_t g = lane / BL, bl = lane % BL;
+    const uint32_t nq = (uint32_t)(a.nb >> 2);
+    const uint32_t q0 = blockIdx.y * (BL * KB);
+    float4 acc[4][KB];
+#pragma unroll
+    for (int li = 0; li < 4; ++li)
+#pragma unroll
+        for (int k = 0; k < KB; ++k) acc[li][k] = make_float4(0.f, 0.f, 0.f, 0.f);
+    SegDesc sd{};
+    if (active) {
+    sd = a.seg[si];
+    const uint32_t br = sd.row;
+    const __amdgpu_buffer_rsrc_t rin = buffer_rsrc(a.in, in_bytes);
+    const uint32_t ld_bytes = (uint32_t)a.in_ld * 4u;
+    uint32_t lane_off[KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+        const uint32_t q = q0 + bl + BL * (uint32_t)k;
+        lane_off[k] = q < nq ? q * 16u : OOB_OFFSET;
+    }
+    float *sw = s_w[wave];
+    // rank-1 scales of the block row's 4 rows (uniform over the segment)
+    float rs[4];
+#pragma unroll
+    for (int li = 0; li < 4; ++li) {
+        const uint32_t r = br * 4u + (uint32_t)li;
+        rs[li] = (a.sc.row && r < a.rows) ? a.sc.row[r] : 1.0f;
+    }
+    uint32_t pos = sd.byte_begin, carry = sd.base_col, ebase = sd.elem_begin;
+    const uint32_t end = sd.byte_end;
+    while (pos < end) {
+        const Chunk ch = decode_chunk(a.idx, pos, end, carry);
+        if (ch.T == 0ull) break;
+        const uint32_t n = (uint32_t)__popcll(ch.T);
+        const uint32_t npad = (n + STEP - 1u) / STEP * STEP;
+        if (ch.term) {
+            // the lane that decoded tile `rank` dequantises its 16 slots:
+            // one 16-byte load of the tile, scales S(r,c) as scale_at
+            const uint32_t bc = ch.col;
+            s_off[wave][ch.rank] = bc * 4u * ld_bytes;
+            const uint4 tb = *reinterpret_cast<const uint4 *>(a.tiles + (size_t)(ebase + ch.rank) * 16u);
+            const uint32_t words[4] = {tb.x, tb.y, tb.z, tb.w};  // word lj holds slots lj*4 .. lj*4+3
+#pragma unroll
+            for (int lj = 0; lj < 4; ++lj) {
+                const uint32_t c = bc * 4u + (uint32_t)lj;
+                const bool cok = c < a.cols;
+                const float cs = (a.sc.rank == 1 && a.sc.ent && cok) ? a.sc.ent[c] : 1.0f;
+                float wv[4];
+#pragma unroll
+                for (int li = 0; li < 4; ++li) {
+                    const uint32_t r = br * 4u + (uint32_t)li;
+                    const uint32_t code = (words[lj] >> (8 * li)) & 0xFu;
+                    float S;
+                    if (a.sc.rank == 1) S = a.sc.ent ? rs[li] * cs : rs[li];
+                    else S = (r < a.rows && cok) ? scale_at(a.sc, r, c) : 1.0f;
+                    wv[li] = (r < a.rows && cok) ? fp4_decode(code) * S : 0.0f;
+                }
+                reinterpret_cast<float4 *>(sw + ch.rank * 16u)[lj] = make_float4(wv[0], wv[1], wv[2], wv[3]);
+            }
+        } else if (lane >= n && lane < npad) {
+            // padding tiles: out-of-range rows (read 0), zero weights
+            s_off[wave][lane] = OOB_OFFSET;
+#pragma unroll
+            for (int lj = 0; lj < 4; ++lj)
+                reinterpret_cast<float4 *>(sw + lane * 16u)[lj] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        wave_lds_sync();
+        for (uint32_t j = 0; j < npad; j += STEP) {
+            float4 x[U][4][KB];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t off = s_off[wave][j + (uint32_t)u * G + g];
+#pragma unroll
+                for (int lj = 0; lj < 4; ++lj)
+#pragma unroll
+                    for (int k = 0; k < KB; ++k)
+                        x[u][lj][k] = buffer_load_f4(rin, off + (uint32_t)lj * ld_bytes + lane_off[k]);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float4 *wp = reinterpret_cast<const float4 *>(sw + (j + (uint32_t)u * G + g) * 16u);
+                const float4 wv[4] = {wp[0], wp[1], wp[2], wp[3]};  // wv[lj] = slots (lj, li = 0..3)
+#pragma unroll
+                for (int lj = 0; lj < 4; ++lj) {
+                    const float wl[4] = {wv[lj].x, wv[lj].y, wv[lj].z, wv[lj].w};
+#pragma unroll
+                    for (int li = 0; li < 4; ++li)
+#pragma unroll
+                        for (int k = 0; k < KB; ++k) {
+                            acc[li][k].x = __builtin_fmaf(wl[li], x[u][lj][k].x, acc[li][k].x);
+                            acc[li][k].y = __builtin_fmaf(wl[li], x[u][lj][k].y, acc[li][k].y);
+                            acc[li][k].z = __builtin_fmaf(wl[li], x[u][lj][k].z, acc[li][k].z);
+                            acc[li][k].w = __builtin_fmaf(wl[li], x[u][lj][k].w, acc[li][k].w);
+                        }
+                }
+            }
+        }
+        wave_lds_sync();
+        carry = chunk_advance(ch, pos, ebase);
+    }
+    // combine the G tile groups (lanes bl, bl+BL, ...)
+#pragma unroll
+    for (uint32_t off = BL; off < 64u; off <<= 1)
+#pragma unroll
+        for (int li = 0; li < 4; ++li)
+#pragma unroll
+            for (int k = 0; k < KB; ++k) {
+                acc[li][k].x += __shfl_xor(acc[li][k].x, (int)off, 64);
+                acc[li][k].y += __shfl_xor(acc[li][k].y, (int)off, 64);
+                acc[li][k].z += __shfl_xor(acc[li][k].z, (int)off, 64);
+                acc[li][k].w += __shfl_xor(acc[li][k].w, (int)off, 64);
+            }
+    // this wave's slice of the weight table now holds its 4 x NBC results
+    if (g == 0) {
+#pragma unroll
+        for (int li = 0; li < 4; ++li)
+#pragma unroll
+            for (int k = 0; k < KB; ++k)
+                reinterpret_cast<float4 *>(sw + (uint32_t)li * NBC)[bl + BL * (uint32_t)k] = acc[li][k];
+    }
+    }
+    const uint32_t b0 = q0 * 4u;
+    const uint32_t nbc = (uint32_t)a.nb > b0 ? ((uint32_t)a.nb - b0 < NBC ? (uint32_t)a.nb - b0 : NBC) : 0u;
+    store_rows4_block(active, sd.row, (sd.split & SEG_SPLIT) != 0, b0, nbc, NBC, &s_w[0][0], 64u * 16u, a.rows,
+                      a.out, a.out_ld);
+}
+
 struct SBArgs {
     const SegDesc *seg;
     int64_t nseg;
@@ -718,6 +894,395 @@ struct SBArgs {
     int64_t B;
     float *gw;
 };
+
+// Block4 gather, one tile per wave step: lane (lj = lane/16, bl = lane%16)
+// loads float4 chunk bl of input row 4bc+lj (64 batch columns per wave --
+// blockIdx.y) and accumulates the tile's 4 output rows with the 4 weights
+// (lj, li = 0..3); the 4 lj groups are summed once per segment.  U tiles in
+// flight per lane.  Same preconditions as k_gather_b4_v4 with
+// nb >= 64 columns per chunk layout (16 float4 per wave).
+template <int U>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6))) void k_gather_b4_w(BArgs a, uint32_t in_bytes) {
+    __shared__ uint32_t s_off[WAVES][64];
+    __shared__ __align__(16) float s_w[WAVES][64 * 16];
+    constexpr uint32_t NBC = 64u;  // batch columns per wave
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
+    const bool active = si < a.nseg;
+    const uint32_t lj = lane >> 4, bl = lane & 15u;
+    const uint32_t nq = (uint32_t)(a.nb >> 2);
+    const uint32_t q0 = blockIdx.y * 16u;
+    float4 acc[4];
+#pragma unroll
+    for (int li = 0; li < 4; ++li) acc[li] = make_float4(0.f, 0.f, 0.f, 0.f);
+    SegDesc sd{};
+    float *sw = s_w[wave];
+    if (active) {
+    sd = a.seg[si];
+    const uint32_t br = sd.row;
+    const __amdgpu_buffer_rsrc_t rin = buffer_rsrc(a.in, in_bytes);
+    const uint32_t ld_bytes = (uint32_t)a.in_ld * 4u;
+    const uint32_t q = q0 + bl;
+    const uint32_t lane_off = (q < nq ? q * 16u : OOB_OFFSET);
+    const uint32_t row_off = lj * ld_bytes;
+    float rs[4];
+#pragma unroll
+    for (int li = 0; li < 4; ++li) {
+        const uint32_t r = br * 4u + (uint32_t)li;
+        rs[li] = (a.sc.row && r < a.rows) ? a.sc.row[r] : 1.0f;
+    }
+    uint32_t pos = sd.byte_begin, carry = sd.base_col, ebase = sd.elem_begin;
+    const uint32_t end = sd.byte_end;
+    while (pos < end) {
+        const Chunk ch = decode_chunk(a.idx, pos, end, carry);
+        if (ch.T == 0ull) break;
+        const uint32_t n = (uint32_t)__popcll(ch.T);
+        const uint32_t npad = (n + U - 1u) / U * U;
+        if (ch.term) {
+            const uint32_t bc = ch.col;
+            s_off[wave][ch.rank] = bc * 4u * ld_bytes;
+            const uint4 tb = *reinterpret_cast<const uint4 *>(a.tiles + (size_t)(ebase + ch.rank) * 16u);
+            const uint32_t words[4] = {tb.x, tb.y, tb.z, tb.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t c = bc * 4u + (uint32_t)j;
+                const bool cok = c < a.cols;
+                const float cs = (a.sc.rank == 1 && a.sc.ent && cok) ? a.sc.ent[c] : 1.0f;
+                float wv[4];
+#pragma unroll
+                for (int li = 0; li < 4; ++li) {
+                    const uint32_t r = br * 4u + (uint32_t)li;
+                    const uint32_t code = (words[j] >> (8 * li)) & 0xFu;
+                    float S;
+                    if (a.sc.rank == 1) S = a.sc.ent ? rs[li] * cs : rs[li];
+                    else S = (r < a.rows && cok) ? scale_at(a.sc, r, c) : 1.0f;
+                    wv[li] = (r < a.rows && cok) ? fp4_decode(code) * S : 0.0f;
+                }
+                reinterpret_cast<float4 *>(sw + ch.rank * 16u)[j] = make_float4(wv[0], wv[1], wv[2], wv[3]);
+            }
+        } else if (lane >= n && lane < npad) {
+            s_off[wave][lane] = OOB_OFFSET;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                reinterpret_cast<float4 *>(sw + lane * 16u)[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        wave_lds_sync();
+        for (uint32_t e0 = 0; e0 < npad; e0 += U) {
+            float4 x[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t off = s_off[wave][e0 + (uint32_t)u];
+                x[u] = buffer_load_f4(rin, (off == OOB_OFFSET ? OOB_OFFSET : off + row_off) + lane_off);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float4 w = reinterpret_cast<const float4 *>(sw + (e0 + (uint32_t)u) * 16u)[lj];
+                const float wl[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int li = 0; li < 4; ++li) {
+                    acc[li].x = __builtin_fmaf(wl[li], x[u].x, acc[li].x);
+                    acc[li].y = __builtin_fmaf(wl[li], x[u].y, acc[li].y);
+                    acc[li].z = __builtin_fmaf(wl[li], x[u].z, acc[li].z);
+                    acc[li].w = __builtin_fmaf(wl[li], x[u].w, acc[li].w);
+                }
+            }
+        }
+        wave_lds_sync();
+        carry = chunk_advance(ch, pos, ebase);
+    }
+    // sum the 4 input-row groups (lanes bl, bl+16, bl+32, bl+48)
+#pragma unroll
+    for (uint32_t off = 16u; off < 64u; off <<= 1)
+#pragma unroll
+        for (int li = 0; li < 4; ++li) {
+            acc[li].x += __shfl_xor(acc[li].x, (int)off, 64);
+            acc[li].y += __shfl_xor(acc[li].y, (int)off, 64);
+            acc[li].z += __shfl_xor(acc[li].z, (int)off, 64);
+            acc[li].w += __shfl_xor(acc[li].w, (int)off, 64);
+        }
+    if (lj == 0) {
+#pragma unroll
+        for (int li = 0; li < 4; ++li) reinterpret_cast<float4 *>(sw + (uint32_t)li * NBC)[bl] = acc[li];
+    }
+    }
+    const uint32_t b0 = q0 * 4u;
+    const uint32_t nbc = (uint32_t)a.nb > b0 ? ((uint32_t)a.nb - b0 < NBC ? (uint32_t)a.nb - b0 : NBC) : 0u;
+    store_rows4_block(active, sd.row, (sd.split & SEG_SPLIT) != 0, b0, nbc, NBC, &s_w[0][0], 64u * 16u, a.rows,
+                      a.out, a.out_ld);
+}
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Block4 gather on the matrix cores: one wave per (segment, 64 batch
+// columns b0 = 64*blockIdx.y); lane l owns batch column b0+l.  With
+// v_mfma_f32_4x4x1 (16 blocks of D[4x4] += A[4x1]*B[1x4]; block b = lane/4,
+// A[b][i] from lane 4b+i, B[b][j] from lane 4b+j, D[b][i][j] in vgpr i of
+// lane 4b+j) the blocks are 16 groups of 4 batch columns: A = column lj of
+// the tile's weights (lane 4b+i: W[i][lj]), B = input row 4bc+lj (lane l:
+// x[4bc+lj][b0+l]), so vgpr li of lane l accumulates out[4br+li][b0+l].
+// 4 MFMAs per tile (one accumulator per lj), U tiles in flight.  Same
+// preconditions as k_gather_b4_v4.
+template <int U>
+__global__ __launch_bounds__(256) void k_gather_b4_mfma(BArgs a, uint32_t in_bytes) {
+    __shared__ uint32_t s_off[WAVES][64];
+    __shared__ __align__(16) float s_w[WAVES][64 * 16];  // per tile [li][lj]
+    constexpr uint32_t NBC = 64u;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
+    const bool active = si < a.nseg;
+    const uint32_t b0 = blockIdx.y * NBC;
+    v4f acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    SegDesc sd{};
+    float *sw = s_w[wave];
+    if (active) {
+    sd = a.seg[si];
+    const uint32_t br = sd.row;
+    const __amdgpu_buffer_rsrc_t rin = buffer_rsrc(a.in, in_bytes);
+    const uint32_t ld_bytes = (uint32_t)a.in_ld * 4u;
+    const uint32_t lane_off = (int64_t)(b0 + lane) < a.nb ? (b0 + lane) * 4u : OOB_OFFSET;
+    float rs[4];
+#pragma unroll
+    for (int li = 0; li < 4; ++li) {
+        const uint32_t r = br * 4u + (uint32_t)li;
+        rs[li] = (a.sc.row && r < a.rows) ? a.sc.row[r] : 1.0f;
+    }
+    uint32_t pos = sd.byte_begin, carry = sd.base_col, ebase = sd.elem_begin;
+    const uint32_t end = sd.byte_end;
+    while (pos < end) {
+        const Chunk ch = decode_chunk(a.idx, pos, end, carry);
+        if (ch.T == 0ull) break;
+        const uint32_t n = (uint32_t)__popcll(ch.T);
+        const uint32_t npad = (n + U - 1u) / U * U;
+        if (ch.term) {
+            const uint32_t bc = ch.col;
+            s_off[wave][ch.rank] = bc * 4u * ld_bytes;
+            const uint4 tb = *reinterpret_cast<const uint4 *>(a.tiles + (size_t)(ebase + ch.rank) * 16u);
+            const uint32_t words[4] = {tb.x, tb.y, tb.z, tb.w};  // word lj holds slots lj*4 .. lj*4+3
+            float wm[4][4];                                       // [li][lj]
+#pragma unroll
+            for (int lj = 0; lj < 4; ++lj) {
+                const uint32_t c = bc * 4u + (uint32_t)lj;
+                const bool cok = c < a.cols;
+                const float cs = (a.sc.rank == 1 && a.sc.ent && cok) ? a.sc.ent[c] : 1.0f;
+#pragma unroll
+                for (int li = 0; li < 4; ++li) {
+                    const uint32_t r = br * 4u + (uint32_t)li;
+                    const uint32_t code = (words[lj] >> (8 * li)) & 0xFu;
+                    float S;
+                    if (a.sc.rank == 1) S = a.sc.ent ? rs[li] * cs : rs[li];
+                    else S = (r < a.rows && cok) ? scale_at(a.sc, r, c) : 1.0f;
+                    wm[li][lj] = (r < a.rows && cok) ? fp4_decode(code) * S : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int li = 0; li < 4; ++li)
+                reinterpret_cast<float4 *>(sw + ch.rank * 16u)[li] = make_float4(wm[li][0], wm[li][1], wm[li][2], wm[li][3]);
+        } else if (lane >= n && lane < npad) {
+            s_off[wave][lane] = OOB_OFFSET;
+#pragma unroll
+            for (int li = 0; li < 4; ++li)
+                reinterpret_cast<float4 *>(sw + lane * 16u)[li] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        wave_lds_sync();
+        for (uint32_t e0 = 0; e0 < npad; e0 += U) {
+            float xv[U][4];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t off = s_off[wave][e0 + (uint32_t)u];
+#pragma unroll
+                for (int lj = 0; lj < 4; ++lj)
+                    xv[u][lj] = buffer_load_f1(rin, (off == OOB_OFFSET ? OOB_OFFSET : off + (uint32_t)lj * ld_bytes) + lane_off);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                // A operands: W[lane%4][lj] for lj = 0..3
+                const float4 w = reinterpret_cast<const float4 *>(sw + (e0 + (uint32_t)u) * 16u)[lane & 3u];
+                acc[0] = __builtin_amdgcn_mfma_f32_4x4x1f32(w.x, xv[u][0], acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_4x4x1f32(w.y, xv[u][1], acc[1], 0, 0, 0);
+                acc[2] = __builtin_amdgcn_mfma_f32_4x4x1f32(w.z, xv[u][2], acc[2], 0, 0, 0);
+                acc[3] = __builtin_amdgcn_mfma_f32_4x4x1f32(w.w, xv[u][3], acc[3], 0, 0, 0);
+            }
+        }
+        wave_lds_sync();
+        carry = chunk_advance(ch, pos, ebase);
+    }
+    // this wave's slice of the weight table now holds out[li][b0 + lane]
+#pragma unroll
+    for (int li = 0; li < 4; ++li)
+        sw[(uint32_t)li * NBC + lane] = (acc[0][li] + acc[1][li]) + (acc[2][li] + acc[3][li]);
+    }
+    const uint32_t nbc = (uint32_t)a.nb > b0 ? ((uint32_t)a.nb - b0 < NBC ? (uint32_t)a.nb - b0 : NBC) : 0u;
+    store_rows4_block(active, sd.row, (sd.split & SEG_SPLIT) != 0, b0, nbc, NBC, &s_w[0][0], 64u * 16u, a.rows,
+                      a.out, a.out_ld);
+}
+
+// Block4 grad-W on the matrix cores: gw[16t + lj*4+li] =
+// sum_b xT[4br+li, b] * gT[4bc+lj, b].  One wave per segment over the whole
+// batch (B <= 64*KQ).  v_mfma_f32_4x4x1 blocks split the batch: lane
+// l = 4*blk + i supplies A = xT[4br+i][n] and B = gT[4bc+i][n] for
+// n = 4*(blk + 16s) + c (s < KQ float4 loads, c < 4), so block blk
+// accumulates its batch share of the tile's 4x4 product; the 16 blocks are
+// summed over lanes with stride 4 (DPP row_shr 4, 8 within 16-lane rows,
+// then across rows).  U tiles in flight.  Needs B % 4 == 0 and 16-byte
+// aligned xT / gT / gw.
+template <int KQ, int U>
+__global__ __launch_bounds__(256) void k_sddmm_b4_mfma(SBArgs a, uint32_t gT_bytes) {
+    __shared__ uint32_t s_off[WAVES][64];
+    __shared__ uint32_t s_t[WAVES][64];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
+    if (si >= a.nseg) return;
+    const SegDesc sd = a.seg[si];
+    const uint32_t li = lane & 3u, blk = lane >> 2;
+    const uint32_t nq = (uint32_t)(a.B >> 2);
+    const uint32_t ld_bytes = (uint32_t)a.B * 4u;
+    const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(a.gT, gT_bytes);
+    uint32_t lane_off[KQ];
+    float4 xr[KQ];
+    const int64_t r = (int64_t)sd.row * 4 + li;
+#pragma unroll
+    for (int s = 0; s < KQ; ++s) {
+        const uint32_t q = blk + 16u * (uint32_t)s;
+        lane_off[s] = q < nq ? q * 16u : OOB_OFFSET;
+        xr[s] = (q < nq && r < a.rows) ? reinterpret_cast<const float4 *>(a.xT + r * a.B)[q]
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const uint32_t row_off = li * ld_bytes;  // this lane supplies gT row 4bc + li
+    uint32_t pos = sd.byte_begin, carry = sd.base_col, ebase = sd.elem_begin;
+    const uint32_t end = sd.byte_end;
+    while (pos < end) {
+        const Chunk ch = decode_chunk(a.idx, pos, end, carry);
+        if (ch.T == 0ull) break;
+        if (ch.term) {
+            s_off[wave][ch.rank] = ch.col * 4u * ld_bytes;
+            s_t[wave][ch.rank] = ebase + ch.rank;
+        }
+        wave_lds_sync();
+        const uint32_t n = (uint32_t)__popcll(ch.T);
+        for (uint32_t e0 = 0; e0 < n; e0 += U) {
+            float4 gv[U][KQ];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t e = e0 + (uint32_t)u;
+                const uint32_t off = e < n ? s_off[wave][e] + row_off : OOB_OFFSET;
+#pragma unroll
+                for (int s = 0; s < KQ; ++s)
+                    gv[u][s] = buffer_load_f4(rg, off == OOB_OFFSET ? OOB_OFFSET : off + lane_off[s]);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                v4f c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < KQ; ++s) {
+                    c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(xr[s].x, gv[u][s].x, c0, 0, 0, 0);
+                    c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(xr[s].y, gv[u][s].y, c1, 0, 0, 0);
+                    c0 = __builtin_amdgcn_mfma_f32_4x4x1f32(xr[s].z, gv[u][s].z, c0, 0, 0, 0);
+                    c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(xr[s].w, gv[u][s].w, c1, 0, 0, 0);
+                }
+                float d[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float x = c0[v] + c1[v];
+                    x += dpp_f32<DPP_ROW_SHR4>(x);  // lane 12+j of each row: its 4 blocks
+                    x += dpp_f32<DPP_ROW_SHR8>(x);
+                    x += __shfl_xor(x, 16, 64);     // across the 4 rows
+                    x += __shfl_xor(x, 32, 64);
+                    d[v] = x;
+                }
+                const uint32_t e = e0 + (uint32_t)u;
+                // lane 12 + j holds D[i = v][j]: slots j*4 + v of tile e
+                if (lane >= 12u && lane < 16u && e < n)
+                    reinterpret_cast<float4 *>(a.gw + (size_t)s_t[wave][e] * 16u)[lane - 12u] =
+                        make_float4(d[0], d[1], d[2], d[3]);
+            }
+        }
+        wave_lds_sync();
+        carry = chunk_advance(ch, pos, ebase);
+    }
+}
+
+// Block4 grad-W with float4 batch lanes: gw[16t + lj*4+li] =
+// sum_b xT[4br+li, b] * gT[4bc+lj, b].  One wave per segment over the whole
+// batch (B = 4*BL*KB at most): xT's 4 rows of the block row stay in
+// registers; G = 64/BL tiles per load instruction, each lane loading the 4
+// gT rows of its tile and forming 16 partial dots, reduced over the BL
+// batch lanes; the group's last lane stores the tile's 64 bytes.  Needs
+// B % 4 == 0, 16-byte aligned xT / gT / gw and a < 2 GiB gT.
+template <int BL, int KB>
+__global__ __launch_bounds__(256) void k_sddmm_b4_v4(SBArgs a, uint32_t gT_bytes) {
+    __shared__ uint32_t s_off[WAVES][64];
+    __shared__ uint32_t s_t[WAVES][64];
+    constexpr uint32_t G = 64u / BL;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
+    if (si >= a.nseg) return;
+    const SegDesc sd = a.seg[si];
+    const uint32_t g = lane / BL, bl = lane % BL;
+    const uint32_t nq = (uint32_t)(a.B >> 2);
+    const uint32_t ld_bytes = (uint32_t)a.B * 4u;
+    const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(a.gT, gT_bytes);
+    uint32_t lane_off[KB];
+    float4 xr[4][KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+        const uint32_t q = bl + BL * (uint32_t)k;
+        lane_off[k] = q < nq ? q * 16u : OOB_OFFSET;
+#pragma unroll
+        for (int li = 0; li < 4; ++li) {
+            const int64_t r = (int64_t)sd.row * 4 + li;
+            xr[li][k] = (q < nq && r < a.rows)
+                ? reinterpret_cast<const float4 *>(a.xT + r * a.B)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    uint32_t pos = sd.byte_begin, carry = sd.base_col, ebase = sd.elem_begin;
+    const uint32_t end = sd.byte_end;
+    while (pos < end) {
+        const Chunk ch = decode_chunk(a.idx, pos, end, carry);
+        if (ch.T == 0ull) break;
+        if (ch.term) {
+            s_off[wave][ch.rank] = ch.col * 4u * ld_bytes;
+            s_t[wave][ch.rank] = ebase + ch.rank;
+        }
+        wave_lds_sync();
+        const uint32_t n = (uint32_t)__popcll(ch.T);
+        for (uint32_t j = 0; j < n; j += G) {
+            const uint32_t e = j + g;
+            const uint32_t off = e < n ? s_off[wave][e] : OOB_OFFSET;
+            float d[16];
+#pragma unroll
+            for (int lj = 0; lj < 4; ++lj) {
+                float4 gv[KB];
+#pragma unroll
+                for (int k = 0; k < KB; ++k) gv[k] = buffer_load_f4(rg, off + (uint32_t)lj * ld_bytes + lane_off[k]);
+#pragma unroll
+                for (int li = 0; li < 4; ++li) {
+                    float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+                    for (int k = 0; k < KB; ++k) {
+                        d0 = __builtin_fmaf(xr[li][k].x, gv[k].x, d0);
+                        d1 = __builtin_fmaf(xr[li][k].y, gv[k].y, d1);
+                        d0 = __builtin_fmaf(xr[li][k].z, gv[k].z, d0);
+                        d1 = __builtin_fmaf(xr[li][k].w, gv[k].w, d1);
+                    }
+                    d[lj * 4 + li] = d0 + d1;
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < 16; ++s) d[s] = group_sum_last<BL>(d[s]);
+            if (bl == BL - 1u && e < n) {
+                float4 *o = reinterpret_cast<float4 *>(a.gw + (size_t)s_t[wave][e] * 16u);
+                o[0] = make_float4(d[0], d[1], d[2], d[3]);
+                o[1] = make_float4(d[4], d[5], d[6], d[7]);
+                o[2] = make_float4(d[8], d[9], d[10], d[11]);
+                o[3] = make_float4(d[12], d[13], d[14], d[15]);
+            }
+        }
+        wave_lds_sync();
+        carry = chunk_advance(ch, pos, ebase);
+    }
+}
 
 // gw[16*t + lj*4+li] = sum_b xT[4br+li, b] * gT[4bc+lj, b] for every slot.
 __global__ __launch_bounds__(256) void k_sddmm_b4(SBArgs a) {
@@ -1074,6 +1639,44 @@ void launch_gather_b4(const Block4Plan &p, const ScaleView &sc, const float *in,
                       float *out, int64_t out_ld, int64_t nb_total, int skip, hipStream_t st) {
     if (p.nseg == 0 || nb_total == 0) return;
     ProfScope ps("gather_b4", st);
+    const int64_t in_bytes = p.cols * in_ld * 4;
+    if (skip == SKIP_NONE && nb_total % 4 == 0 && in_ld % 4 == 0 && aligned16(in) &&
+        in_bytes < (int64_t)OOB_OFFSET) {
+        BArgs a{p.seg, p.nseg, p.idx, p.tiles, p.rows, p.cols, sc, in, in_ld, out, out_ld, nb_total};
+        const int64_t nq = nb_total / 4;
+        const unsigned gx = blocks_for(p.nseg);
+        const unsigned gy16 = (unsigned)((nq + 15) / 16);
+        static const int use_mfma = env_int("SILI_B4_MFMA", 0);
+        if (use_mfma && nq >= 12) {
+            // matrix cores: 64 batch columns per wave (SILI_B4_MFMA=0: vector path)
+            static const int u = env_int("SILI_B4_MFMA_U", 2);
+            if (u >= 4) launch((k_gather_b4_mfma<4>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
+            else if (u >= 2) launch((k_gather_b4_mfma<2>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
+            else launch((k_gather_b4_mfma<1>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
+        } else if (nq <= 4) {
+            launch((k_gather_b4_v4<4, 1, 2>), dim3(gx, 1), dim3(256), 0, st, a, (uint32_t)in_bytes);
+        } else if (nq <= 8) {
+            launch((k_gather_b4_v4<8, 1, 2>), dim3(gx, 1), dim3(256), 0, st, a, (uint32_t)in_bytes);
+        } else {
+            // 64 batch columns per wave; lanes per tile and tiles in flight
+            // (SILI_B4_BL / SILI_B4_U)
+            static const int bl = env_int("SILI_B4_BL", 16), u = env_int("SILI_B4_U", 2);
+            const unsigned gy8 = (unsigned)((nq + 7) / 8);
+            if (bl == 32 && u >= 4) launch((k_gather_b4_v4<8, 1, 4>), dim3(gx, gy8), dim3(256), 0, st, a, (uint32_t)in_bytes);
+            else if (bl == 32) launch((k_gather_b4_v4<8, 1, 2>), dim3(gx, gy8), dim3(256), 0, st, a, (uint32_t)in_bytes);
+            else if (bl == 64 && u >= 8) launch((k_gather_b4_w<8>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
+            else if (bl == 64 && u >= 4) launch((k_gather_b4_w<4>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
+            else if (bl == 64) launch((k_gather_b4_w<2>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
+            else if (bl == 8 && u >= 4) launch((k_gather_b4_v4<8, 2, 4>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
+            else if (bl == 8 && u >= 2) launch((k_gather_b4_v4<8, 2, 2>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
+            else if (bl == 8) launch((k_gather_b4_v4<8, 2, 1>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
+            else if (u >= 4) launch((k_gather_b4_v4<16, 1, 4>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
+            else if (u >= 2) launch((k_gather_b4_v4<16, 1, 2>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
+            else launch((k_gather_b4_v4<16, 1, 1>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
+        }
+        SILI_HIP(hipGetLastError());
+        return;
+    }
     for (int64_t b0 = 0; b0 < nb_total; b0 += 256) {
         const int64_t nb = nb_total - b0 < 256 ? nb_total - b0 : 256;
         BArgs a{p.seg, p.nseg, p.idx, p.tiles, p.rows, p.cols, sc, in + b0, in_ld,
@@ -1163,6 +1766,24 @@ void launch_sddmm_b4(const Block4Plan &p, const uint32_t *, const float *xT, con
     if (p.nseg == 0) return;
     ProfScope ps("sddmm_b4", st);
     SBArgs a{p.seg, p.nseg, p.idx, p.rows, p.cols, xT, gT, B, gw};
+    const int64_t gT_bytes = p.cols * B * 4;
+    if (B % 4 == 0 && B <= 256 && gT_bytes < (int64_t)OOB_OFFSET && aligned16(xT) && aligned16(gT) &&
+        aligned16(gw)) {
+        const dim3 grid(blocks_for(p.nseg)), block(256);
+        const int64_t nq = B / 4;
+        static const int use_mfma = env_int("SILI_B4_MFMA", 0);
+        if (use_mfma && nq >= 8) {
+            if (nq <= 16) launch((k_sddmm_b4_mfma<1, 2>), grid, block, 0, st, a, (uint32_t)gT_bytes);
+            else if (nq <= 32) launch((k_sddmm_b4_mfma<2, 2>), grid, block, 0, st, a, (uint32_t)gT_bytes);
+            else launch((k_sddmm_b4_mfma<4, 2>), grid, block, 0, st, a, (uint32_t)gT_bytes);
+        } else if (nq <= 4) launch((k_sddmm_b4_v4<4, 1>), grid, block, 0, st, a, (uint32_t)gT_bytes);
+        else if (nq <= 8) launch((k_sddmm_b4_v4<8, 1>), grid, block, 0, st, a, (uint32_t)gT_bytes);
+        else if (nq <= 16) launch((k_sddmm_b4_v4<16, 1>), grid, block, 0, st, a, (uint32_t)gT_bytes);
+        else if (nq <= 32) launch((k_sddmm_b4_v4<16, 2>), grid, block, 0, st, a, (uint32_t)gT_bytes);
+        else launch((k_sddmm_b4_v4<16, 4>), grid, block, 0, st, a, (uint32_t)gT_bytes);
+        SILI_HIP(hipGetLastError());
+        return;
+    }
     const size_t lds = sizeof(float) * (size_t)WAVES * 4u * (size_t)B;
     if (lds > 64 * 1024) throw_error(1, "block4 sampled grad-W: batch too large (max 1024)");
     launch(k_sddmm_b4, dim3(blocks_for(p.nseg)), dim3(256), lds, st, a);

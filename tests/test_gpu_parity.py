@@ -139,3 +139,65 @@ def test_reference_kat_block4(hip):
     dx = L.backward_dense(dy, 0.0)[0]
     np.testing.assert_allclose(dx[:3], [1.8, 0.45, -0.1], atol=1e-6)
     assert L.nnz == 4
+
+
+def _edge_block4_layer(n_in, n_out, seed, density=0.3):
+    """Tiles over a layer whose sides are not multiples of 4 (edge tiles hold
+    out-of-range slots), plus scattered synapses outside the tiles."""
+    rng = np.random.default_rng(seed)
+    brs, bcs = (n_in + 3) // 4, (n_out + 3) // 4
+    keys = np.flatnonzero(rng.random(brs * bcs) < density)
+    br, bc = (keys // bcs).astype(np.int32), (keys % bcs).astype(np.int32)
+    codes = rng.integers(0, 16, (len(keys), 16)).astype(np.uint8)
+    codes[codes == 8] = 3
+    tiles = (codes | (np.uint8(1) << 4)).astype(np.uint8)
+    cover = np.zeros((n_in, n_out), bool)
+    for a, b in zip(br, bc):
+        cover[a * 4:a * 4 + 4, b * 4:b * 4 + 4] = True
+    mask = (rng.random((n_in, n_out)) < 0.05) & ~cover
+    ptrs = np.concatenate([[0], np.cumsum(mask.sum(1))]).astype(np.int32)
+    cols = np.nonzero(mask)[1].astype(np.int32)
+    q = rng.normal(0, 2, len(cols)).astype(np.float32)
+    vs = rng.uniform(0.5, 2.0, n_in).astype(np.float32)
+    return br, bc, tiles.ravel(), ptrs, cols, q, vs
+
+
+@pytest.mark.parametrize("n_in,n_out", [(37, 53), (64, 48), (130, 7)])
+@pytest.mark.parametrize("batch", [1, 4, 8, 12, 32, 64, 68, 128, 256, 260])
+def test_block4_edges_and_batches(hip, n_in, n_out, batch):
+    from oracle import HostLayer
+    br, bc, tiles, ptrs, cols, q, vs = _edge_block4_layer(n_in, n_out, n_in * 1000 + batch)
+    H = HostLayer(n_in, n_out).load_csr(ptrs, cols, w=q).load_tiles(br, bc, tiles).set_scales(vs)
+    L = hip.SparseLinearLayer(n_in, n_out, len(cols) + 16 * len(br) + 64)
+    L.load_weights(ptrs, cols, q)
+    L.load_block4_tiles(br, bc, tiles)
+    L.set_value_scales(vs)
+    rng = np.random.default_rng(batch)
+    x = rng.normal(size=(batch, n_in)).astype(np.float32)
+    g = rng.normal(size=(batch, n_out)).astype(np.float32)
+    y = L.forward_dense(x)
+    assert_close_terms(y, H.forward_dense(x), H.forward_dense(x, absmode=True), "b4 edge fwd")
+    dx = L.backward_dense(g, 0.0)
+    assert_close_terms(dx, H.backward_dense(x, g)[0], H.backward_dense(x, g, absmode=True)[0], "b4 edge dx")
+    gs, gb = L.sampled_gradw(x, g)
+    gs_o, gb_o = H.sampled_gradw(x, g)
+    gs_a, gb_a = H.sampled_gradw(x, g, absmode=True)
+    assert_close_terms(gb, gb_o, gb_a, "b4 edge gw")
+    assert_close_terms(gs, gs_o, gs_a, "scattered edge gw")
+
+
+def test_block4_only_layer_forward_backward(hip):
+    """No scattered synapses: the output is zero-filled, then block4 adds."""
+    from oracle import HostLayer
+    br, bc, tiles, _, _, _, vs = _edge_block4_layer(64, 96, 5)
+    H = HostLayer(64, 96).load_tiles(br, bc, tiles).set_scales(vs)
+    L = hip.SparseLinearLayer(64, 96, 16 * len(br) + 64)
+    L.load_block4_tiles(br, bc, tiles)
+    L.set_value_scales(vs)
+    x = np.random.default_rng(1).normal(size=(64, 64)).astype(np.float32)
+    g = np.random.default_rng(2).normal(size=(64, 96)).astype(np.float32)
+    for _ in range(2):  # a second call must not see the first call's output
+        y = L.forward_dense(x)
+        assert_close_terms(y, H.forward_dense(x), H.forward_dense(x, absmode=True), "b4-only fwd")
+        dx = L.backward_dense(g, 0.0)
+        assert_close_terms(dx, H.backward_dense(x, g)[0], H.backward_dense(x, g, absmode=True)[0], "b4-only dx")

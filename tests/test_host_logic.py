@@ -84,3 +84,17 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stdout
+
+
+def test_uleb_row_bytes_matches_oracle_encoding():
+    sys.path.insert(0, ROOT)
+    import bench
+    from oracle import HostLayer
+    # empty rows first, in the middle and last; deltas across every varint length
+    ptrs = np.array([0, 0, 3, 3, 6, 6], np.int32)
+    cols = np.array([0, 127, 128, 5, 16384, 2**21 + 7], np.int32)
+    H = HostLayer(5, 2**22).load_csr(ptrs, cols, w=np.ones(6, np.float32))
+    assert np.array_equal(bench.uleb_row_bytes(ptrs, cols), np.diff(H.row_byte_start.astype(np.int64)))
+    wl = make_config(2, scale=0.03125)
+    H = HostLayer(wl.n_in, wl.n_out).load_csr(wl.ptrs, wl.cols, w=wl.q)
+    assert np.array_equal(bench.uleb_row_bytes(wl.ptrs, wl.cols), np.diff(H.row_byte_start.astype(np.int64)))
