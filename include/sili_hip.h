@@ -142,14 +142,15 @@ int sili_sampled_gradw(sili_layer *layer, const float *x, const float *dy, int64
                        float *gw_s, float *gw_b, void *stream);
 
 /* forward_sparse (sili/cpu_backend.cpp:571-585, sisldo_ops.hpp:198-551):
- * device CSR input (ptrs[batch+1], indices[nnz_x], values[nnz_x]) ->
- * device y [batch,n_out] (overwritten). */
+ * device CSR input (ptrs[batch+1], indices[nnz_x], values[nnz_x];
+ * nnz_x must equal ptrs[batch]) -> device y [batch,n_out] (overwritten). */
 int sili_forward_sparse(sili_layer *layer, const int32_t *ptrs, const int32_t *indices,
                         const float *values, int64_t nnz_x, int64_t batch, float *y,
                         void *stream);
 
 /* backward_sparse at learning_rate 0 (sili/cpu_backend.cpp:587-603,
- * sisldo_ops.hpp:589-1104): dense x [batch,n_in], sparse dy CSR -> device dx
+ * sisldo_ops.hpp:589-1104): dense x [batch,n_in], sparse dy CSR (nnz_dy =
+ * dy_ptrs[batch]) -> device dx
  * [batch,n_in] (overwritten); accumulates neuron_input_accum / neuron_grad_accum. */
 int sili_backward_sparse(sili_layer *layer, const float *x, const int32_t *dy_ptrs,
                          const int32_t *dy_indices, const float *dy_values, int64_t nnz_dy,

@@ -81,6 +81,12 @@ __global__ void k_fill_f32(float *__restrict__ p, int64_t n, float v) {
     if (i < n) p[i] = v;
 }
 
+// n4 float4 stores (16-byte aligned p)
+__global__ void k_fill_f32x4(float4 *__restrict__ p, int64_t n4, float v) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n4) p[i] = make_float4(v, v, v, v);
+}
+
 __global__ void k_quantize(const float *__restrict__ w, const float *__restrict__ imp, int64_t n,
                            uint8_t *__restrict__ out) {
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
@@ -98,7 +104,9 @@ __global__ void k_i32_to_u32(const int32_t *__restrict__ s, int64_t n, uint32_t 
 void fill(float *p, int64_t n, float v, hipStream_t st) {
     if (n <= 0) return;
     ProfScope ps("fill", st);
-    launch(k_fill_f32, dim3(nblk(n)), dim3(TPB), 0, st, p, n, v);
+    const int64_t n4 = (reinterpret_cast<uintptr_t>(p) & 15u) == 0 ? n / 4 : 0;
+    if (n4 > 0) launch(k_fill_f32x4, dim3(nblk(n4)), dim3(TPB), 0, st, reinterpret_cast<float4 *>(p), n4, v);
+    if (n - 4 * n4 > 0) launch(k_fill_f32, dim3(nblk(n - 4 * n4)), dim3(TPB), 0, st, p + 4 * n4, n - 4 * n4, v);
     SILI_HIP(hipGetLastError());
 }
 
@@ -230,7 +238,8 @@ void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st
     // the feature-major copy doubles as the stored forward input that
     // backward_dense reads when called without x (sili/cpu_backend.cpp:481)
     L.xT_cached_batch = B > 1 ? B : 0;
-    if (L.Wt.nnz == 0 || L.Wt.has_split) fill(y, B * L.n_out, 0.0f, st);
+    if (L.Wt.nnz == 0) fill(y, B * L.n_out, 0.0f, st);
+    else launch_zero_split_rows(L.Wt.plan(), y, L.n_out, B, st);
     // scattered pass skips exact-zero inputs (linear_disldo.hpp:114); only
     // observable with non-finite weights, so the skip is compiled in only then
     if (L.Wt.nnz > 0)
@@ -265,7 +274,8 @@ void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float 
         if (xT) launch_rowabs(xT, B, L.n_in, L.acc_in.p, st);
         else launch_colabs(x, B, L.n_in, L.acc_in.p, st);
     }
-    if (!scat || L.W.has_split) fill(dx, B * L.n_in, 0.0f, st);
+    if (!scat) fill(dx, B * L.n_in, 0.0f, st);
+    else launch_zero_split_rows(L.W.plan(), dx, L.n_in, B, st);
     // grad-input and grad-W read the same gT row per synapse: one fused pass
     const bool fused = scat && gw_s &&
                        launch_bwd_fused(L.W.plan(), canon_scales(L), gT, xT, B, dx, L.n_in, gw_s, L.acc_in.p, st);
@@ -276,16 +286,16 @@ void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float 
     if (gw_b && L.B4.ntiles > 0) launch_sddmm_b4(L.B4.plan(), nullptr, xT, gT, B, gw_b, st);
 }
 
-void forward_sparse(Layer &L, const int32_t *ptrs, const int32_t *idx, const float *vals, int64_t B,
-                    float *y, hipStream_t st) {
+void forward_sparse(Layer &L, const int32_t *ptrs, const int32_t *idx, const float *vals, int64_t nnz_x,
+                    int64_t B, float *y, hipStream_t st) {
     ProfCtx pc(L, "fwd_sparse");
     if (B <= 0) throw_error(SILI_ERR_INVALID, "forward_sparse: batch must be >= 1");
     if (!ptrs || !y) throw_error(SILI_ERR_INVALID, "forward_sparse: NULL buffer");
     L.ws_xT.ensure((size_t)(L.n_in * B));
     L.xT_cached_batch = 0;
     fill(L.ws_xT.p, L.n_in * B, 0.0f, st);
-    launch_densify(ptrs, idx, vals, B, L.n_in, L.ws_xT.p, nullptr, true, st);
-    if (L.Wt.has_split) fill(y, B * L.n_out, 0.0f, st);
+    launch_densify(ptrs, idx, vals, B, L.n_in, L.ws_xT.p, nullptr, true, nnz_x, st);
+    launch_zero_split_rows(L.Wt.plan(), y, L.n_out, B, st);
     // only the active rows of each batch row contribute (sisldo_ops.hpp:271-313)
     launch_gather(L.Wt.plan(), shadow_scales(L), L.ws_xT.p, B, y, L.n_out, B, SKIP_POSZERO, st);
     if (L.B4t.ntiles > 0)
@@ -293,15 +303,15 @@ void forward_sparse(Layer &L, const int32_t *ptrs, const int32_t *idx, const flo
 }
 
 void backward_sparse(Layer &L, const float *x, const int32_t *dptrs, const int32_t *didx,
-                     const float *dvals, int64_t B, float *dx, hipStream_t st) {
+                     const float *dvals, int64_t nnz_dy, int64_t B, float *dx, hipStream_t st) {
     ProfCtx pc(L, "bwd_sparse");
     if (B <= 0) throw_error(SILI_ERR_INVALID, "backward_sparse: batch must be >= 1");
     if (!x || !dptrs || !dx) throw_error(SILI_ERR_INVALID, "backward_sparse: NULL buffer");
     launch_colabs(x, B, L.n_in, L.acc_in.p, st);
     L.ws_gT.ensure((size_t)(L.n_out * B));
     fill(L.ws_gT.p, L.n_out * B, 0.0f, st);
-    launch_densify(dptrs, didx, dvals, B, L.n_out, L.ws_gT.p, L.acc_grad.p, true, st);
-    if (L.W.has_split) fill(dx, B * L.n_in, 0.0f, st);
+    launch_densify(dptrs, didx, dvals, B, L.n_out, L.ws_gT.p, L.acc_grad.p, true, nnz_dy, st);
+    launch_zero_split_rows(L.W.plan(), dx, L.n_in, B, st);
     // scattered: merge-join visits only present dy entries (sisldo_ops.hpp:705-713);
     // block4: skips dy == 0 per slot (sisldo_ops.hpp:886-897)
     launch_gather(L.W.plan(), canon_scales(L), L.ws_gT.p, B, dx, L.n_in, B, SKIP_POSZERO, st);
@@ -566,7 +576,7 @@ int sili_forward_sparse(sili_layer *layer, const int32_t *ptrs, const int32_t *i
         if (nnz_x < 0 || (nnz_x > 0 && (!indices || !values)))
             throw_error(SILI_ERR_INVALID, "forward_sparse: bad CSR arguments");
         set_device(layer->L);
-        forward_sparse(layer->L, ptrs, indices, values, batch, y, pick(layer->L, stream));
+        forward_sparse(layer->L, ptrs, indices, values, nnz_x, batch, y, pick(layer->L, stream));
     });
 }
 
@@ -580,7 +590,7 @@ int sili_backward_sparse(sili_layer *layer, const float *x, const int32_t *dy_pt
         if (nnz_dy < 0 || (nnz_dy > 0 && (!dy_indices || !dy_values)))
             throw_error(SILI_ERR_INVALID, "backward_sparse: bad CSR arguments");
         set_device(layer->L);
-        backward_sparse(layer->L, x, dy_ptrs, dy_indices, dy_values, batch, dx, pick(layer->L, stream));
+        backward_sparse(layer->L, x, dy_ptrs, dy_indices, dy_values, nnz_dy, batch, dx, pick(layer->L, stream));
     });
 }
 

@@ -181,8 +181,12 @@ void launch_colabs(const float *src, int64_t B, int64_t n, float *acc, hipStream
 // CSR (ptrs[B+1], idx, vals) -> dense feature-major dst[idx*B + b] (dst pre-zeroed).
 // When mark_explicit, explicit zero values are written as -0.0 so that
 // SKIP_POSZERO can tell them from absent entries.
+// nnz_hint: the number of stored entries (ptrs[batch]) when known on the
+// host -- one thread per entry; 0: one block per batch row.
 void launch_densify(const int32_t *ptrs, const int32_t *idx, const float *vals, int64_t B,
-                    int64_t n, float *dst, float *acc_abs, bool mark_explicit, hipStream_t st);
+                    int64_t n, float *dst, float *acc_abs, bool mark_explicit, int64_t nnz_hint, hipStream_t st);
+// Zero out[b, row] of the rows split over several work items of `p`.
+void launch_zero_split_rows(const GatherPlan &p, float *out, int64_t out_ld, int64_t nb, hipStream_t st);
 // Device decode of a scattered store: cols[e], w[e] = fl32(dec * S(row, col)).
 void launch_decode(const GatherPlan &p, const ScaleView &sc, int32_t *cols, float *w,
                    uint32_t *rows_out, hipStream_t st);

@@ -1440,6 +1440,76 @@ __global__ __launch_bounds__(256) void k_colabs(const float *__restrict__ src, i
     acc[j] += s;
 }
 
+// acc[j] += sum_b |src[b, j]| over a batch-major [B, n] array: 64 columns
+// per block as 16 float4 lanes x 16 batch groups, summed through LDS.
+// Needs n % 4 == 0 and a 16-byte aligned src.
+__global__ __launch_bounds__(256) void k_colabs_v4(const float *__restrict__ src, int64_t B, int64_t n,
+                                                   float *__restrict__ acc) {
+    __shared__ float4 part[16][16];
+    const uint32_t t = threadIdx.x, q = t & 15u, bg = t >> 4;
+    const int64_t j = (int64_t)blockIdx.x * 64 + 4 * q;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (j < n) {
+        for (int64_t b = bg; b < B; b += 16) {
+            const float4 v = *reinterpret_cast<const float4 *>(src + b * n + j);
+            s.x += __builtin_fabsf(v.x);
+            s.y += __builtin_fabsf(v.y);
+            s.z += __builtin_fabsf(v.z);
+            s.w += __builtin_fabsf(v.w);
+        }
+    }
+    part[bg][q] = s;
+    __syncthreads();
+    if (bg == 0 && j < n) {
+        float4 tot = part[0][q];
+        for (int g = 1; g < 16; ++g) {
+            const float4 v = part[g][q];
+            tot.x += v.x; tot.y += v.y; tot.z += v.z; tot.w += v.w;
+        }
+        float4 *a4 = reinterpret_cast<float4 *>(acc + j);
+        float4 cur = *a4;
+        cur.x += tot.x; cur.y += tot.y; cur.z += tot.z; cur.w += tot.w;
+        *a4 = cur;
+    }
+}
+
+// CSR activations -> feature-major dst[j, b] (zero-filled beforehand), one
+// thread per stored entry; its batch row comes from a binary search of
+// ptrs.  Explicit zeros are written as -0.0 when `mark` (so "+0.0 = absent"
+// stays distinguishable); optional acc_abs[j] += |v|.
+__global__ __launch_bounds__(256) void k_densify_entries(const int32_t *__restrict__ ptrs,
+                                                         const int32_t *__restrict__ idx,
+                                                         const float *__restrict__ vals, int64_t B, int64_t n,
+                                                         float *__restrict__ dst, float *__restrict__ acc_abs,
+                                                         int mark) {
+    const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t total = ptrs[B];
+    if (p >= total) return;
+    int64_t lo = 0, hi = B;  // last b with ptrs[b] <= p
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) >> 1;
+        if (ptrs[mid] <= p) lo = mid;
+        else hi = mid;
+    }
+    const int64_t j = idx[p];
+    if (j < 0 || j >= n) return;  // host validated; never write out of bounds
+    float v = vals[p];
+    if (acc_abs) atomicAdd(acc_abs + j, __builtin_fabsf(v));
+    if (mark && __builtin_bit_cast(uint32_t, v) == 0u) v = -0.0f;
+    dst[j * B + lo] = v;
+}
+
+// Zero out[b, row] for every row split over several work items (their
+// partial sums add atomically); rows with one work item are stored whole.
+__global__ __launch_bounds__(256) void k_zero_split_rows(const SegDesc *__restrict__ seg, int64_t nseg,
+                                                         float *__restrict__ out, int64_t out_ld, int64_t nb) {
+    const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (i >= nseg) return;
+    const SegDesc sd = seg[i];
+    if ((sd.split & (SEG_SPLIT | SEG_FIRST)) != (SEG_SPLIT | SEG_FIRST)) return;
+    for (int64_t b = threadIdx.x & 63u; b < nb; b += 64) out[b * out_ld + sd.row] = 0.0f;
+}
+
 __global__ __launch_bounds__(256) void k_densify(const int32_t *__restrict__ ptrs,
                                                  const int32_t *__restrict__ idx,
                                                  const float *__restrict__ vals, int64_t B,
@@ -1814,16 +1884,30 @@ void launch_rowabs(const float *xT, int64_t B, int64_t n, float *acc, hipStream_
 void launch_colabs(const float *src, int64_t B, int64_t n, float *acc, hipStream_t st) {
     if (B == 0 || n == 0) return;
     ProfScope ps("colabs", st);
-    launch(k_colabs, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src, B, n, acc);
+    if (n % 4 == 0 && aligned16(src) && aligned16(acc))
+        launch(k_colabs_v4, dim3((unsigned)((n + 63) / 64)), dim3(256), 0, st, src, B, n, acc);
+    else
+        launch(k_colabs, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, src, B, n, acc);
+    SILI_HIP(hipGetLastError());
+}
+
+void launch_zero_split_rows(const GatherPlan &p, float *out, int64_t out_ld, int64_t nb, hipStream_t st) {
+    if (p.nseg == 0 || nb == 0 || !p.has_split) return;
+    ProfScope ps("zero_split", st);
+    launch(k_zero_split_rows, dim3((unsigned)((p.nseg + 3) / 4)), dim3(256), 0, st, p.seg, p.nseg, out, out_ld, nb);
     SILI_HIP(hipGetLastError());
 }
 
 void launch_densify(const int32_t *ptrs, const int32_t *idx, const float *vals, int64_t B,
-                    int64_t n, float *dst, float *acc_abs, bool mark_explicit, hipStream_t st) {
+                    int64_t n, float *dst, float *acc_abs, bool mark_explicit, int64_t nnz_hint, hipStream_t st) {
     if (B == 0) return;
     ProfScope ps("densify", st);
-    launch(k_densify, dim3((unsigned)B), dim3(256), 0, st, ptrs, idx, vals, B, n, dst,
-                       acc_abs, mark_explicit ? 1 : 0);
+    if (nnz_hint > 0)
+        launch(k_densify_entries, dim3((unsigned)((nnz_hint + 255) / 256)), dim3(256), 0, st, ptrs, idx, vals, B, n,
+               dst, acc_abs, mark_explicit ? 1 : 0);
+    else
+        launch(k_densify, dim3((unsigned)B), dim3(256), 0, st, ptrs, idx, vals, B, n, dst,
+                           acc_abs, mark_explicit ? 1 : 0);
     SILI_HIP(hipGetLastError());
 }
 
