@@ -127,6 +127,7 @@ class CAbi:
         L.sili_stream.argtypes = [vp]
         L.sili_profile_enable.argtypes = [vp, C.c_int]
         L.sili_profile_read.argtypes = [vp, C.POINTER(CAbi.ProfEntry), C.c_int, C.POINTER(C.c_int)]
+        L.sili_device_free.argtypes = [vp, vp]
         self.L = L
 
     def ck(self, rc):
@@ -371,6 +372,131 @@ def time_synapto(hip, wl, reps):
             "last_stats": stats}
 
 
+# config 4: the 7 layer shapes of a folded 40 x Mistral-24B-like block stack
+# (SURVEY 8(d)): (name, n_in, n_out); 10% of each kept, |N(0, 0.02)| tail above
+# its 95th percentile, per-row FP4 scales, decode forward at batch 1 / 8 / 128
+C4_LAYERS = [("q", 5120, 204800), ("k", 5120, 204800), ("v", 5120, 204800), ("o", 5120, 204800),
+             ("gate", 5120, 1310720), ("up", 5120, 1310720), ("down", 32768, 204800)]
+C4_BATCHES = (1, 8, 128)
+
+
+def run_config4(a, hip, api, rt):
+    from sili__new_amd.synth import SEED0, Stream
+    t_build = time.perf_counter()
+    layers = []
+    for i, (name, n_in, n_out) in enumerate(C4_LAYERS):
+        L = hip.SparseLinearLayer(n_in, n_out, 1)
+        nnz = L.load_synthetic(SEED0 + 4 + 1000 * i, 0.1, 0.02, 0.95)
+        h = C.c_void_p(L.handle)
+        info = L.info()
+        layers.append({"name": name, "L": L, "h": h, "n_in": n_in, "n_out": n_out, "nnz": nnz, "info": info})
+    t_build = time.perf_counter() - t_build
+    nnz_total = sum(d["nnz"] for d in layers)
+    stream = api.L.sili_stream(layers[0]["h"])
+    results = {}
+    for B in C4_BATCHES:
+        for i, d in enumerate(layers):
+            x = Stream(SEED0 + 4, 10 + 100 * B + i).normal(B * d["n_in"]).astype(np.float32)
+            d["x"] = api.upload(d["h"], x)
+            d["y"] = api.alloc(d["h"], 4 * B * d["n_out"])
+
+        def step():
+            for d in layers:
+                api.ck(api.L.sili_forward_dense(d["h"], d["x"], B, d["y"], stream))
+        steps = max(3, a.steps // (10 if B == 1 else 50 if B == 8 else 200))
+        for _ in range(max(1, a.warmup // 5)):
+            step()
+        rt.sync()
+        e0, e1 = rt.event(), rt.event()
+        rt.record(e0, stream)
+        for _ in range(steps):
+            step()
+        rt.record(e1, stream)
+        rt.sync()
+        ms = rt.elapsed_ms(e0, e1) / steps
+        for d in layers:
+            api.ck(api.L.sili_profile_enable(d["h"], 1))
+        step()
+        rt.sync()
+        kern = {}
+        for d in layers:
+            for name, (cnt, tot) in api.profile(d["h"]).items():
+                kern[f"{d['name']}:{name}"] = tot / cnt
+            api.ck(api.L.sili_profile_enable(d["h"], 0))
+        # algorithmic bytes per layer forward (SURVEY 8(d) dense-input fwd)
+        alg = {}
+        for d in layers:
+            info = d["info"]
+            alg[d["name"]] = (info["nnz_scattered"] + info["index_bytes"] + 8 * (d["n_out"] + 1)
+                              + 4 * (d["n_in"] + d["n_out"]) + 4 * B * (d["n_in"] + d["n_out"]))
+        step_bytes = sum(alg.values())
+        gath = {k: v for k, v in kern.items() if k.endswith(":gather")}
+        dom = max(gath.items(), key=lambda kv: kv[1])
+        dom_layer = dom[0].split(":")[0]
+        ach = alg[dom_layer] / (dom[1] * 1e-3) / 1e9
+        results[B] = {"ms_per_step": round(ms, 4), "gnnz_s": round(nnz_total / (ms * 1e-3) / 1e9, 3),
+                      "achieved_gbs": round(step_bytes / (ms * 1e-3) / 1e9, 2),
+                      "pct_hbm_peak": round(100 * step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                      "steps": steps, "kernels_ms": {k: round(v, 4) for k, v in kern.items()},
+                      "dominant": {"kernel": dom[0], "avg_launch_ms": round(dom[1], 4),
+                                   "algorithmic_bytes": alg[dom_layer], "achieved_gbs": round(ach, 2),
+                                   "frac": round(ach / HBM_PEAK_GBS, 4)}}
+        for d in layers:
+            api.ck(api.L.sili_device_free(d["h"], d["x"]))
+            api.ck(api.L.sili_device_free(d["h"], d["y"]))
+    r1 = results[1]
+    out = {
+        "metric": "FP4 delta-CSR SpMM GNNZ/s + achieved HBM GB/s (% of peak), fwd+bwd",
+        "value": r1["gnnz_s"], "unit": "GNNZ/s", "n_gpus": 1, "steps": r1["steps"], "warmup": a.warmup,
+        "ms_per_step": r1["ms_per_step"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32", "data": "synthetic (seeded, generated on the device)",
+        "config": {"workload": "config 4: folded 40-block Mistral-24B-like stack, 7 FP4 delta-CSR layers "
+                               "(q,k,v,o 5120x204800; gate,up 5120x1310720; down 32768x204800) at 10% density; "
+                               "step = decode forward of all 7 layers at batch 1 (batches 8, 128 below)",
+                   "nnz": nnz_total, "layers": {d["name"]: d["nnz"] for d in layers},
+                   "index_bytes": sum(d["info"]["index_bytes"] for d in layers)},
+        "achieved_gbs": r1["achieved_gbs"], "pct_hbm_peak": r1["pct_hbm_peak"],
+        "roofline": {"bound": "hbm", "kernel": r1["dominant"]["kernel"], "achieved": r1["dominant"]["achieved_gbs"],
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": r1["dominant"]["frac"],
+                     "traffic": measured_traffic(r1["dominant"]["kernel"], 4),
+                     "avg_launch_ms": r1["dominant"]["avg_launch_ms"],
+                     "algorithmic_bytes": r1["dominant"]["algorithmic_bytes"]},
+        "batches": {str(B): r for B, r in results.items()},
+        "build_s": round(t_build, 2),
+    }
+    if not a.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline_c4(layers[0], a.cpu_seconds)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out), flush=True)
+
+
+def cpu_baseline_c4(d, seconds):
+    """The CPU port's forward over the q layer (exported from the device) at
+    batch 1, on this host's cores: a bounded sample of the config-4 step."""
+    from oracle import HostLayer
+    from sili__new_amd.synth import SEED0, Stream
+    L = d["L"]
+    threads = os.cpu_count() or 1
+    H = HostLayer(d["n_in"], d["n_out"])
+    ex = L.export_scattered()
+    H.load_encoded(ex["row_byte_start"], ex["row_elem_start"], ex["idx"], ex["val"])
+    H.set_scales(np.asarray(L.get_value_scales(), np.float32))
+    x = Stream(SEED0 + 4, 7).normal(d["n_in"]).astype(np.float32)[None, :]
+    times = []
+    t_end = time.perf_counter() + seconds
+    while True:
+        t0 = time.perf_counter()
+        H.forward_dense(x, threads=threads)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end or len(times) >= 50:
+            break
+    med = float(np.median(times))
+    return {"value": round(d["nnz"] / med / 1e9, 4), "unit": "GNNZ/s", "cores": threads, "kind": "port",
+            "sample": f"forward of the q layer ({d['nnz']} synapses, 5120x204800) at batch 1, "
+                      f"{len(times)} reps, median {med * 1e3:.1f} ms"}
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -385,6 +511,9 @@ def main():
     from sili__new_amd.synth import make_config
 
     cfg = a.config
+    if cfg == 4:
+        run_config4(a, hip, CAbi(hip.LIB_PATH), Hip())
+        return
     wl = make_config(cfg)
     B, n_in, n_out = wl.batch, wl.n_in, wl.n_out
     api = CAbi(hip.LIB_PATH)

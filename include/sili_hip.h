@@ -92,6 +92,19 @@ int sili_load_dense_codes(sili_layer *layer, const uint8_t *weight_codes,
 int sili_load_block4_tiles(sili_layer *layer, const int32_t *br, const int32_t *bc,
                            const uint8_t *tile_bytes, int64_t n_tiles);
 
+/* Seeded synthetic layer built on the device (no reference counterpart: the
+ * benchmark workloads of BASELINE config 4 are too large to build on the
+ * host; the reference's own builds go through load_weights).  Synapse (r, c)
+ * exists iff a 64-bit hash of (seed, r, c) falls below keep_prob; its weight
+ * is drawn from |N(0, sigma)| conditioned on |w| >= sigma * Phi^-1(tail_q)
+ * (tail_q = 0.5: plain half-normal) with a random sign, then quantized with
+ * the reference's per-row recipe (s_r = fl32(max_row|w| / 6), code =
+ * fp4_encode(w / s_r), sili/sparse_rnn.py:1022-1037; importance 0).  Replaces
+ * the scattered store and the value scales (rank must be 1); the synapse
+ * count goes to *nnz_out (may be NULL).  Synchronous. */
+int sili_load_synthetic(sili_layer *layer, uint64_t seed, double keep_prob, float sigma, float tail_q,
+                        int64_t *nnz_out);
+
 /* set_scale_rank(k) (sili/cpu_backend.cpp:455-461): 1 <= k <= 4, else
  * SILI_ERR_INVALID.  Resets scales to the reference defaults (component 0 = 1,
  * others 0; delta_csr_types.hpp:1116-1121). */

@@ -218,6 +218,16 @@ class HostLayer:
         self.index_bytes = nb
         return self
 
+    def load_encoded(self, row_byte_start, row_elem_start, idx, val):
+        """Take an already encoded scattered store (e.g. a device export)."""
+        self.row_byte_start = _c(row_byte_start, np.uint64).copy()
+        self.row_elem_start = _c(row_elem_start, np.uint64).copy()
+        self.index_bytes = int(self.row_byte_start[-1])
+        self.nnz = int(self.row_elem_start[-1])
+        self.idx = np.concatenate([_c(idx, np.uint8), np.zeros(8, np.uint8)])
+        self.val = np.concatenate([_c(val, np.uint8), np.zeros(8, np.uint8)])
+        return self
+
     def load_tiles(self, br, bc, tiles):
         (self.brow_byte_start, self.brow_tile_start, self.bidx, self.tiles,
          self.tile_br, self.tile_bc) = encode_tiles(self.n_in, br, bc, tiles)

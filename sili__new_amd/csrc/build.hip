@@ -223,12 +223,23 @@ void zero_flag(Layer &L) {
 struct Encoded {
     int64_t nbytes = 0, nseg = 0;
     bool has_split = false;
+    int64_t n_split = 0;
 };
+
+__global__ void k_split_flags(const uint32_t *__restrict__ segcnt, int64_t rows, uint32_t *__restrict__ flag) {
+    const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (r <= rows) flag[r] = (r < rows && segcnt[r] > 1u) ? 1u : 0u;
+}
+__global__ void k_split_list(const uint32_t *__restrict__ flag, const uint32_t *__restrict__ pos, int64_t rows,
+                             uint32_t *__restrict__ list) {
+    const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (r < rows && flag[r]) list[pos[r]] = (uint32_t)r;
+}
 
 Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint32_t *d_ptrs,
                     const uint32_t *d_cols, uint32_t seg_len, bool emit_empty,
                     DevBuf<uint32_t> &byte_start, DevBuf<uint32_t> &elem_start, DevBuf<uint8_t> &idx,
-                    DevBuf<SegDesc> &seg, const char *what) {
+                    DevBuf<SegDesc> &seg, const char *what, DevBuf<uint32_t> *split_rows = nullptr) {
     Encoded out;
     hipStream_t st = L.stream;
     DevBuf<uint64_t> len, pos;
@@ -281,6 +292,25 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
     SILI_HIP(hipMemcpyAsync(&split, L.scratch.flag.p, sizeof(int), hipMemcpyDeviceToHost, st));
     SILI_HIP(hipStreamSynchronize(st));
     out.has_split = split != 0;
+    if (out.has_split && split_rows) {
+        // list of the rows that span several work items (their outputs need
+        // zeroing before the atomically combined partial sums)
+        DevBuf<uint32_t> flag, fpos;
+        flag.ensure((size_t)rows + 1);
+        fpos.ensure((size_t)rows + 1);
+        launch(k_split_flags, dim3(nblk(rows + 1)), dim3(TPB), 0, st, (const uint32_t *)segcnt.p, rows, flag.p);
+        SILI_HIP(hipGetLastError());
+        device_exclusive_scan_u32(L, flag.p, fpos.p, rows + 1);
+        uint32_t ns = 0;
+        SILI_HIP(hipMemcpyAsync(&ns, fpos.p + rows, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+        SILI_HIP(hipStreamSynchronize(st));
+        split_rows->ensure((size_t)ns + 1);
+        launch(k_split_list, dim3(nblk(rows)), dim3(TPB), 0, st, (const uint32_t *)flag.p, (const uint32_t *)fpos.p,
+               rows, split_rows->p);
+        SILI_HIP(hipGetLastError());
+        SILI_HIP(hipStreamSynchronize(st));
+        out.n_split = ns;
+    }
     return out;
 }
 
@@ -331,7 +361,8 @@ static int bits_for(uint64_t max_value) {
 void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64_t N,
                      const uint32_t *d_ptrs, const uint32_t *d_cols, const uint8_t *d_bytes) {
     const Encoded e = encode_rows(L, rows, ncols, N, d_ptrs, d_cols, L.seg_len, true, dst.byte_start,
-                                  dst.elem_start, dst.idx, dst.seg, "load_weights");
+                                  dst.elem_start, dst.idx, dst.seg, "load_weights", &dst.split_rows);
+    dst.n_split = e.n_split;
     dst.rows = rows;
     dst.cols = ncols;
     dst.nnz = N;
@@ -373,7 +404,8 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
                        src.cols, ptrs.p);
     SILI_HIP(hipGetLastError());
     const Encoded e = encode_rows(L, src.cols, src.rows, N, ptrs.p, trows.p, L.seg_len, true, dst.byte_start,
-                                  dst.elem_start, dst.idx, dst.seg, "shadow build");
+                                  dst.elem_start, dst.idx, dst.seg, "shadow build", &dst.split_rows);
+    dst.n_split = e.n_split;
     dst.rows = src.cols;
     dst.cols = src.rows;
     dst.nnz = N;

@@ -419,6 +419,21 @@ int sili_load_weight_bytes(sili_layer *layer, const int32_t *ptrs, const int32_t
     });
 }
 
+int sili_load_synthetic(sili_layer *layer, uint64_t seed, double keep_prob, float sigma, float tail_q,
+                        int64_t *nnz_out) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        Layer &L = layer->L;
+        if (L.rank != 1) throw_error(SILI_ERR_INVALID, "load_synthetic: scale rank must be 1");
+        if (!(keep_prob >= 0.0 && keep_prob <= 1.0) || !(sigma > 0.0f) || !(tail_q >= 0.5f && tail_q < 1.0f))
+            throw_error(SILI_ERR_INVALID, "load_synthetic: need 0 <= keep_prob <= 1, sigma > 0, 0.5 <= tail_q < 1");
+        set_device(L);
+        const int64_t nnz = generate_synthetic(L, seed, keep_prob, sigma, tail_q);
+        refresh_scale_flags(L);
+        if (nnz_out) *nnz_out = nnz;
+    });
+}
+
 int sili_load_dense_codes(sili_layer *layer, const uint8_t *wc, const uint8_t *ic) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");

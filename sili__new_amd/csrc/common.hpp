@@ -142,6 +142,8 @@ struct GatherPlan {      // one orientation of the scattered store
     const uint8_t *val;
     int64_t rows, cols;
     bool has_split;
+    const uint32_t *split_rows;  // rows spanning several work items (n_split of them)
+    int64_t n_split;
 };
 
 struct Block4Plan {

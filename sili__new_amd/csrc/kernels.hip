@@ -18,6 +18,7 @@
 // owns KB batch columns).
 #include "wave.hpp"
 
+#include <algorithm>
 #include <cstdlib>
 
 namespace sili {
@@ -170,6 +171,319 @@ __global__ __launch_bounds__(256) void k_gather_b1(GArgs a) {
         float *o = a.out + row;
         if (sd.split & SEG_SPLIT) atomicAdd(o, acc);
         else *o = acc;
+    }
+}
+
+// Batch 1 with lane-parallel decode: lane L owns the index bytes
+// [8L, 8L+8) of the segment (SEG_BYTES_MAX = 512 = 64 x 8) and decodes the
+// varints whose last byte lies there (looking back over at most 4
+// continuation bytes for a varint that starts in the previous slice).  Two
+// wave scans give each lane its first entry index and the column before
+// its slice; the lane then gathers in[col] for its (at most 8) entries with
+// all loads in flight.  One wave reduction per segment.  The index bytes are
+// staged realigned (segment byte p at LDS byte 4 + p, a zero dword in
+// front: zero bytes end a lookback), so a lane's 12-byte window is three
+// aligned dwords.  RANK1: scale rank 1 (row factor uniform per segment).
+template <int SKIP, bool RANK1>
+__global__ __launch_bounds__(256) void k_gather_b1s(GArgs a, uint32_t ent_bytes) {
+    __shared__ SegStage s_stage[WAVES];
+    __shared__ float s_fp4[WAVES][16];
+    __shared__ uint2 s_ent[WAVES][SEG_BYTES_MAX];
+    static_assert(SEG_BYTES_MAX == 512, "one 8-byte slice per lane");
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
+    if (si >= a.nseg) return;
+    const SegDesc sd = a.seg[si];
+    fp4_table_init(s_fp4[wave]);
+    SegStage &S = s_stage[wave];
+    const uint32_t end = sd.byte_end - sd.byte_begin < SEG_BYTES_MAX ? sd.byte_end - sd.byte_begin : SEG_BYTES_MAX;
+    {
+        // realigned copy: dst dword k (k >= 1) = segment bytes 4(k-1) .. 4(k-1)+3
+        const uint32_t sh = sd.byte_begin & 3u;
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(a.idx + (sd.byte_begin & ~3u));
+        const uint32_t nw = (end + 3u) / 4u + 1u;  // dwords 0 .. nw-1 written (<= 129)
+        for (uint32_t k = lane; k < nw + 2u; k += 64u) {
+            uint32_t d = 0;
+            if (k >= 1u && k < nw) {
+                const uint32_t lo = src[k - 1u], hi = src[k];
+                d = sh ? __builtin_amdgcn_alignbyte(hi, lo, sh) : lo;
+            }
+            S.idx[k] = d;
+        }
+    }
+    uint32_t voff = 0;  // value byte e of the segment is S.val byte voff + e
+    stage_words(S.val, a.val, sd.elem_begin, sd.elem_end, voff);
+    wave_lds_sync();
+    const uint8_t *vals = reinterpret_cast<const uint8_t *>(S.val) + voff;
+    const __amdgpu_buffer_rsrc_t rin = buffer_rsrc(a.in, a.in_bytes);
+    const uint32_t ld_bytes = (uint32_t)a.in_ld * 4u;
+    const uint32_t p0 = lane * 8u;
+    // bytes [p0 - 4, p0 + 8): dwords 2L, 2L+1, 2L+2 of the realigned copy
+    const uint32_t w0 = S.idx[2u * lane], w1 = S.idx[2u * lane + 1u], w2 = S.idx[2u * lane + 2u];
+    uint32_t byte[12];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        byte[i] = (w0 >> (8 * i)) & 0xFFu;
+        byte[4 + i] = (w1 >> (8 * i)) & 0xFFu;
+        byte[8 + i] = (w2 >> (8 * i)) & 0xFFu;
+    }
+    // continuation prefix of the first varint ending in the slice
+    uint32_t k = 0;
+#pragma unroll
+    for (int i = 3; i >= 0; --i) {
+        const bool cont = (byte[i] & 0x80u) != 0u;
+        k = (k == 3u - (uint32_t)i && cont) ? k + 1u : k;
+    }
+    uint32_t acc = 0, shift = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const bool use = (uint32_t)i >= 4u - k;
+        acc = use ? (acc | ((byte[i] & 0x7Fu) << shift)) : acc;
+        shift = use ? shift + 7u : shift;
+    }
+    uint32_t v[8];
+    uint32_t cnt = 0, dsum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t b = byte[4 + i];
+        const bool in_seg = p0 + (uint32_t)i < end;
+        acc |= (b & 0x7Fu) << (shift < 32u ? shift : 0u);
+        const bool term = in_seg && (b & 0x80u) == 0u;
+        v[i] = term ? acc : 0xFFFFFFFFu;  // 0xFFFFFFFF: no entry ends here
+        dsum += term ? acc : 0u;
+        cnt += term ? 1u : 0u;
+        acc = term ? 0u : acc;
+        shift = term ? 0u : shift + 7u;
+    }
+    const uint32_t ebase = wave_incl_scan(cnt) - cnt;             // entries before this slice
+    uint32_t col = sd.base_col + (wave_incl_scan(dsum) - dsum);   // column before this slice
+    // entry table in LDS, segment order: (column, weight code)
+    uint2 *ent = s_ent[wave];
+    uint32_t e = ebase;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const bool has = v[i] != 0xFFFFFFFFu;
+        col += has ? v[i] : 0u;
+        if (has) ent[e] = make_uint2(col, (uint32_t)vals[e] >> 4);
+        e += has ? 1u : 0u;
+    }
+    const uint32_t n = (uint32_t)__builtin_amdgcn_readlane((int)(ebase + cnt), 63);
+    wave_lds_sync();
+    // gather with 64 consecutive entries per load instruction, U in flight
+    const float *tab = s_fp4[wave];
+    const float rs = (RANK1 && a.sc.row) ? a.sc.row[sd.row] : 1.0f;
+    // column factors (a zero-sized range when there are none: reads give 0)
+    const __amdgpu_buffer_rsrc_t rent = buffer_rsrc(a.sc.ent ? a.sc.ent : a.in, a.sc.ent ? ent_bytes : 0u);
+    constexpr uint32_t U = 4;
+    float sum = 0.0f;
+    for (uint32_t j = 0; j < n; j += 64u * U) {
+        uint2 en[U];
+        float xs[U], cs[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t idx = j + u * 64u + lane;
+            en[u] = idx < n ? ent[idx] : make_uint2(0xFFFFFFFFu, 0u);
+            const bool ok = en[u].x != 0xFFFFFFFFu;
+            xs[u] = buffer_load_f1(rin, ok ? en[u].x * ld_bytes : OOB_OFFSET);
+            if constexpr (RANK1) cs[u] = a.sc.ent ? buffer_load_f1(rent, ok ? en[u].x * 4u : OOB_OFFSET) : 1.0f;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            if (en[u].x == 0xFFFFFFFFu) continue;
+            float S;
+            if constexpr (RANK1) S = a.sc.ent ? rs * cs[u] : rs;
+            else S = scale_at(a.sc, sd.row, en[u].x);
+            const float w = tab[en[u].y] * S;
+            if (!skip_x<SKIP>(xs[u])) sum = __builtin_fmaf(w, xs[u], sum);
+        }
+    }
+    sum = group_sum_last<64>(sum);
+    if (lane == 63u) {
+        float *o = a.out + sd.row;
+        if (sd.split & SEG_SPLIT) atomicAdd(o, sum);
+        else *o = sum;
+    }
+}
+
+// Batch 1, persistent and software-pipelined: each wave walks segments
+// s = w, w + W, w + 2W, ... (W = waves in the grid).  While it decodes and
+// gathers segment s from LDS, the raw index / value dwords of segment s+W
+// are already in flight into registers (3 + 3 per lane) and the descriptor
+// of s+2W is loading, so the HBM latency of the weight stream hides behind
+// the work of the previous segment.  Per segment: lane-parallel decode of
+// 8-byte slices (as k_gather_b1s; the 12-byte window is read from the raw
+// staged bytes with the segment's byte alignment, a zero dword in front),
+// an LDS entry table in segment order, then the gather with 64 consecutive
+// entries per load instruction and one wave reduction.
+struct B1Stage {
+    uint32_t idx[SEG_BYTES_MAX / 4 + 8];  // idx[0] = 0, raw dwords from idx[1]
+    uint32_t val[SEG_BYTES_MAX / 4 + 8];
+};
+
+// XLDS (rank 1, no skip rules, in_ld == 1): the block first copies the
+// whole input, times the column scale, into LDS (dynamic shared memory,
+// n = a.in_bytes / 4 floats); the per-synapse gather then reads LDS and the
+// weight is dec(code) * row scale (the column factor rides on x).
+template <int SKIP, bool RANK1, bool XLDS = false>
+__global__ __launch_bounds__(256) void k_gather_b1p(GArgs a, uint32_t ent_bytes) {
+    __shared__ B1Stage s_stage[WAVES];
+    __shared__ float s_fp4[WAVES][16];
+    __shared__ uint32_t s_ent[WAVES][SEG_BYTES_MAX];  // col | code << 28
+    extern __shared__ float s_x[];
+    static_assert(SEG_BYTES_MAX == 512, "one 8-byte slice per lane");
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t W = (int64_t)gridDim.x * WAVES;
+    if constexpr (XLDS) {
+        const uint32_t nx = a.in_bytes / 4u;
+        for (uint32_t i = threadIdx.x; i < nx; i += blockDim.x)
+            s_x[i] = a.sc.ent ? a.in[i] * a.sc.ent[i] : a.in[i];
+        __syncthreads();
+    }
+    int64_t si = (int64_t)blockIdx.x * WAVES + wave;
+    if (si >= a.nseg) return;
+    fp4_table_init(s_fp4[wave]);
+    B1Stage &S = s_stage[wave];
+    uint32_t *ent = s_ent[wave];
+    const float *tab = s_fp4[wave];
+    const __amdgpu_buffer_rsrc_t rin = buffer_rsrc(a.in, a.in_bytes);
+    const __amdgpu_buffer_rsrc_t rent = buffer_rsrc(a.sc.ent ? a.sc.ent : a.in, a.sc.ent ? ent_bytes : 0u);
+    const uint32_t ld_bytes = (uint32_t)a.in_ld * 4u;
+    // raw dwords of a segment's index / value ranges (3 per lane each)
+    auto load_data = [&](const SegDesc &d, uint32_t (&ri)[3], uint32_t (&rv)[3]) {
+        const uint32_t *pi = reinterpret_cast<const uint32_t *>(a.idx + (d.byte_begin & ~3u));
+        const uint32_t *pv = reinterpret_cast<const uint32_t *>(a.val + (d.elem_begin & ~3u));
+        const uint32_t len = d.byte_end - d.byte_begin < SEG_BYTES_MAX ? d.byte_end - d.byte_begin : SEG_BYTES_MAX;
+        const uint32_t ni = ((d.byte_begin & 3u) + len + 3u) >> 2;
+        const uint32_t nv = ((d.elem_begin & 3u) + (d.elem_end - d.elem_begin) + 3u) >> 2;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const uint32_t q = lane + 64u * (uint32_t)k;
+            ri[k] = q < ni ? pi[q] : 0u;
+            rv[k] = q < nv ? pv[q] : 0u;
+        }
+    };
+    SegDesc cur = a.seg[si];
+    uint32_t ri[3], rv[3];
+    load_data(cur, ri, rv);
+    SegDesc nxt{};
+    if (si + W < a.nseg) nxt = a.seg[si + W];
+    for (; si < a.nseg; si += W) {
+        // stage the current segment's bytes
+        S.idx[0] = 0u;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const uint32_t q = lane + 64u * (uint32_t)k;
+            if (q < SEG_BYTES_MAX / 4 + 7u) {
+                S.idx[1u + q] = ri[k];
+                S.val[q] = rv[k];
+            }
+        }
+        // prefetch: data of the next segment, descriptor of the one after
+        const bool more = si + W < a.nseg;
+        SegDesc nn{};
+        if (more) {
+            load_data(nxt, ri, rv);
+            if (si + 2 * W < a.nseg) nn = a.seg[si + 2 * W];
+        }
+        wave_lds_sync();
+        const SegDesc &sd = cur;
+        const uint32_t end = sd.byte_end - sd.byte_begin < SEG_BYTES_MAX ? sd.byte_end - sd.byte_begin : SEG_BYTES_MAX;
+        const uint32_t ioff = sd.byte_begin & 3u;
+        const uint8_t *vals = reinterpret_cast<const uint8_t *>(S.val) + (sd.elem_begin & 3u);
+        const uint32_t p0 = lane * 8u;
+        // bytes [p0 - 4, p0 + 8) = staged bytes [ioff + p0, ioff + p0 + 12)
+        const uint32_t d0 = S.idx[2u * lane], d1 = S.idx[2u * lane + 1u], d2 = S.idx[2u * lane + 2u],
+                       d3 = S.idx[2u * lane + 3u];
+        const uint32_t w0 = ioff ? __builtin_amdgcn_alignbyte(d1, d0, ioff) : d0;
+        const uint32_t w1 = ioff ? __builtin_amdgcn_alignbyte(d2, d1, ioff) : d1;
+        const uint32_t w2 = ioff ? __builtin_amdgcn_alignbyte(d3, d2, ioff) : d2;
+        uint32_t byte[12];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            byte[i] = lane ? (w0 >> (8 * i)) & 0xFFu : 0u;  // before the segment: terminators
+            byte[4 + i] = (w1 >> (8 * i)) & 0xFFu;
+            byte[8 + i] = (w2 >> (8 * i)) & 0xFFu;
+        }
+        uint32_t k = 0;
+#pragma unroll
+        for (int i = 3; i >= 0; --i) {
+            const bool cont = (byte[i] & 0x80u) != 0u;
+            k = (k == 3u - (uint32_t)i && cont) ? k + 1u : k;
+        }
+        uint32_t acc = 0, shift = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const bool use = (uint32_t)i >= 4u - k;
+            acc = use ? (acc | ((byte[i] & 0x7Fu) << shift)) : acc;
+            shift = use ? shift + 7u : shift;
+        }
+        uint32_t v[8];
+        uint32_t cnt = 0, dsum = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t b = byte[4 + i];
+            const bool in_seg = p0 + (uint32_t)i < end;
+            acc |= (b & 0x7Fu) << (shift < 32u ? shift : 0u);
+            const bool term = in_seg && (b & 0x80u) == 0u;
+            v[i] = term ? acc : 0xFFFFFFFFu;
+            dsum += term ? acc : 0u;
+            cnt += term ? 1u : 0u;
+            acc = term ? 0u : acc;
+            shift = term ? 0u : shift + 7u;
+        }
+        const uint32_t ebase = wave_incl_scan(cnt) - cnt;
+        uint32_t col = sd.base_col + (wave_incl_scan(dsum) - dsum);
+        uint32_t e = ebase;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const bool has = v[i] != 0xFFFFFFFFu;
+            col += has ? v[i] : 0u;
+            if (has) ent[e] = col | (((uint32_t)vals[e] >> 4) << 28);
+            e += has ? 1u : 0u;
+        }
+        const uint32_t n = (uint32_t)__builtin_amdgcn_readlane((int)(ebase + cnt), 63);
+        wave_lds_sync();
+        const float rs = (RANK1 && a.sc.row) ? a.sc.row[sd.row] : 1.0f;
+        constexpr uint32_t U = 4;
+        float sum = 0.0f;
+        for (uint32_t j = 0; j < n; j += 64u * U) {
+            uint32_t en[U];
+            bool ok[U];
+            float xs[U], cs[U];
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                const uint32_t idx = j + u * 64u + lane;
+                ok[u] = idx < n;
+                en[u] = ok[u] ? ent[idx] : 0u;
+                const uint32_t c = en[u] & 0x0FFFFFFFu;
+                if constexpr (XLDS) {
+                    xs[u] = ok[u] ? s_x[c] : 0.0f;
+                } else {
+                    xs[u] = buffer_load_f1(rin, ok[u] ? c * ld_bytes : OOB_OFFSET);
+                    if constexpr (RANK1) cs[u] = a.sc.ent ? buffer_load_f1(rent, ok[u] ? c * 4u : OOB_OFFSET) : 1.0f;
+                }
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) {
+                if (!ok[u]) continue;
+                const uint32_t c = en[u] & 0x0FFFFFFFu;
+                float Sv;
+                if constexpr (XLDS) Sv = rs;
+                else if constexpr (RANK1) Sv = a.sc.ent ? rs * cs[u] : rs;
+                else Sv = scale_at(a.sc, sd.row, c);
+                const float w = tab[en[u] >> 28] * Sv;
+                if (!skip_x<SKIP>(xs[u])) sum = __builtin_fmaf(w, xs[u], sum);
+            }
+        }
+        sum = group_sum_last<64>(sum);
+        if (lane == 63u) {
+            float *o = a.out + sd.row;
+            if (sd.split & SEG_SPLIT) atomicAdd(o, sum);
+            else *o = sum;
+        }
+        wave_lds_sync();  // LDS buffers are rewritten by the next iteration
+        cur = nxt;
+        nxt = nn;
     }
 }
 
@@ -1501,13 +1815,22 @@ __global__ __launch_bounds__(256) void k_densify_entries(const int32_t *__restri
 
 // Zero out[b, row] for every row split over several work items (their
 // partial sums add atomically); rows with one work item are stored whole.
-__global__ __launch_bounds__(256) void k_zero_split_rows(const SegDesc *__restrict__ seg, int64_t nseg,
+// One thread per (batch index, split row).
+__global__ __launch_bounds__(256) void k_zero_split_rows(const uint32_t *__restrict__ rows, int64_t n_split,
                                                          float *__restrict__ out, int64_t out_ld, int64_t nb) {
-    const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (i >= nseg) return;
-    const SegDesc sd = seg[i];
-    if ((sd.split & (SEG_SPLIT | SEG_FIRST)) != (SEG_SPLIT | SEG_FIRST)) return;
-    for (int64_t b = threadIdx.x & 63u; b < nb; b += 64) out[b * out_ld + sd.row] = 0.0f;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n_split * nb) return;
+    const int64_t b = i / n_split, k = i - b * n_split;
+    out[b * out_ld + rows[k]] = 0.0f;
+}
+
+__global__ __launch_bounds__(256) void k_zero_f4(float4 *__restrict__ p, int64_t n4) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n4) p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+__global__ __launch_bounds__(256) void k_zero_f1(float *__restrict__ p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0.0f;
 }
 
 __global__ __launch_bounds__(256) void k_densify(const int32_t *__restrict__ ptrs,
@@ -1667,10 +1990,50 @@ void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, in
                 small ? (uint32_t)in_bytes : 0u};
         const dim3 grid(blocks_for(a.nseg)), block(256);
         if (nb == 1 && small) {
-            switch (skip) {
-                case SKIP_ZERO: launch(k_gather_b1<SKIP_ZERO>, grid, block, 0, st, a); break;
-                case SKIP_POSZERO: launch(k_gather_b1<SKIP_POSZERO>, grid, block, 0, st, a); break;
-                default: launch(k_gather_b1<SKIP_NONE>, grid, block, 0, st, a); break;
+            static const int lane_decode = env_int("SILI_B1_LANE_DECODE", 2);
+            // (static LDS ~12.8 KB + the input stay within 64 KB per block)
+            if (lane_decode == 2 && skip == SKIP_NONE && sc.rank == 1 && in_ld == 1 && p.cols * 4 + 13312 <= 65536) {
+                // input (times its column scale) held in LDS by each persistent block
+                const size_t lds = (size_t)p.cols * 4;
+                const unsigned gp = (unsigned)std::min<int64_t>((int64_t)blocks_for(a.nseg), 256 * (lds <= 24576 ? 4 : 2));
+                launch(k_gather_b1p<SKIP_NONE, true, true>, dim3(gp), block, (uint32_t)lds, st, a, 0u);
+                SILI_HIP(hipGetLastError());
+                continue;
+            }
+            if (lane_decode == 2 && p.cols < (1 << 28)) {
+                // persistent pipelined waves: enough to fill the chip, no more
+                const unsigned gp = (unsigned)std::min<int64_t>((int64_t)blocks_for(a.nseg), 256 * 6);
+                const uint32_t eb2 = (uint32_t)(p.cols * 4 < (int64_t)OOB_OFFSET ? p.cols * 4 : 0);
+                switch ((skip == SKIP_ZERO ? 0 : skip == SKIP_POSZERO ? 1 : 2) + (sc.rank == 1 ? 0 : 3)) {
+                    case 0: launch(k_gather_b1p<SKIP_ZERO, true>, dim3(gp), block, 0, st, a, eb2); break;
+                    case 1: launch(k_gather_b1p<SKIP_POSZERO, true>, dim3(gp), block, 0, st, a, eb2); break;
+                    case 2: launch(k_gather_b1p<SKIP_NONE, true>, dim3(gp), block, 0, st, a, eb2); break;
+                    case 3: launch(k_gather_b1p<SKIP_ZERO, false>, dim3(gp), block, 0, st, a, eb2); break;
+                    case 4: launch(k_gather_b1p<SKIP_POSZERO, false>, dim3(gp), block, 0, st, a, eb2); break;
+                    default: launch(k_gather_b1p<SKIP_NONE, false>, dim3(gp), block, 0, st, a, eb2); break;
+                }
+                SILI_HIP(hipGetLastError());
+                continue;
+            }
+            const uint32_t eb = (uint32_t)(p.cols * 4 < (int64_t)OOB_OFFSET ? p.cols * 4 : 0);
+            if (lane_decode && sc.rank == 1) {
+                switch (skip) {
+                    case SKIP_ZERO: launch(k_gather_b1s<SKIP_ZERO, true>, grid, block, 0, st, a, eb); break;
+                    case SKIP_POSZERO: launch(k_gather_b1s<SKIP_POSZERO, true>, grid, block, 0, st, a, eb); break;
+                    default: launch(k_gather_b1s<SKIP_NONE, true>, grid, block, 0, st, a, eb); break;
+                }
+            } else if (lane_decode) {
+                switch (skip) {
+                    case SKIP_ZERO: launch(k_gather_b1s<SKIP_ZERO, false>, grid, block, 0, st, a, eb); break;
+                    case SKIP_POSZERO: launch(k_gather_b1s<SKIP_POSZERO, false>, grid, block, 0, st, a, eb); break;
+                    default: launch(k_gather_b1s<SKIP_NONE, false>, grid, block, 0, st, a, eb); break;
+                }
+            } else {
+                switch (skip) {
+                    case SKIP_ZERO: launch(k_gather_b1<SKIP_ZERO>, grid, block, 0, st, a); break;
+                    case SKIP_POSZERO: launch(k_gather_b1<SKIP_POSZERO>, grid, block, 0, st, a); break;
+                    default: launch(k_gather_b1<SKIP_NONE>, grid, block, 0, st, a); break;
+                }
             }
         } else if (small && nb % 4 == 0 && in_ld % 4 == 0 && aligned16(a.in)) {
             const int64_t nq = nb / 4;
@@ -1892,9 +2255,19 @@ void launch_colabs(const float *src, int64_t B, int64_t n, float *acc, hipStream
 }
 
 void launch_zero_split_rows(const GatherPlan &p, float *out, int64_t out_ld, int64_t nb, hipStream_t st) {
-    if (p.nseg == 0 || nb == 0 || !p.has_split) return;
+    if (p.nseg == 0 || nb == 0 || !p.has_split || p.n_split == 0) return;
     ProfScope ps("zero_split", st);
-    launch(k_zero_split_rows, dim3((unsigned)((p.nseg + 3) / 4)), dim3(256), 0, st, p.seg, p.nseg, out, out_ld, nb);
+    if (p.n_split * 4 >= p.rows) {
+        // most rows split: one streaming fill of the whole output is cheaper
+        const int64_t n = nb * out_ld;
+        const int64_t n4 = aligned16(out) ? n / 4 : 0;
+        if (n4 > 0) launch(k_zero_f4, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, reinterpret_cast<float4 *>(out), n4);
+        if (n - 4 * n4 > 0) launch(k_zero_f1, dim3((unsigned)((n - 4 * n4 + 255) / 256)), dim3(256), 0, st, out + 4 * n4, n - 4 * n4);
+    } else {
+        const int64_t n = p.n_split * nb;
+        launch(k_zero_split_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p.split_rows, p.n_split, out,
+               out_ld, nb);
+    }
     SILI_HIP(hipGetLastError());
 }
 

@@ -47,8 +47,10 @@ struct DScatter {
     DevBuf<uint32_t> byte_start, elem_start;  // rows+1
     DevBuf<uint8_t> idx, val;
     DevBuf<SegDesc> seg;
+    DevBuf<uint32_t> split_rows;  // rows with more than one work item
+    int64_t n_split = 0;
     GatherPlan plan() const {
-        return GatherPlan{seg.p, nseg, idx.p, val.p, rows, cols, has_split};
+        return GatherPlan{seg.p, nseg, idx.p, val.p, rows, cols, has_split, split_rows.p, n_split};
     }
 };
 
@@ -157,6 +159,11 @@ void device_sort_pairs_u32(Layer &L, const uint32_t *kin, uint32_t *kout, const 
                            uint32_t *vout, int64_t n, int bits);
 void device_sort_pairs_u64(Layer &L, const uint64_t *kin, uint64_t *kout, const uint32_t *vin,
                            uint32_t *vout, int64_t n, int bits);
+
+// ---- seeded synthetic layers (gen.hip) ----------------------------------------
+// Rebuilds the scattered store (and its shadow) from the seeded generator and
+// writes the per-row value scales into L.vs (rank 1).  Returns the synapse count.
+int64_t generate_synthetic(Layer &L, uint64_t seed, double keep_prob, float sigma, float tail_q);
 
 // ---- synaptogenesis (synapto.hip) ---------------------------------------------
 void synapto_step(Layer &L, float prune_frac, const int32_t *cand_r, const int32_t *cand_c,

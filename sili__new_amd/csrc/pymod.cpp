@@ -189,6 +189,13 @@ class Layer {
         return os_[(size_t)(col * rank_ + k)];
     }
     float get_value_scale(int64_t row) const { return get_value_scale_k(row, 0); }
+    // bulk copies of the scale arrays, [n * rank] (flushed device state)
+    py::array_t<float> get_value_scales() {
+        flush();
+        py::array_t<float> a((py::ssize_t)vs_.size());
+        std::memcpy(a.mutable_data(), vs_.data(), vs_.size() * 4);
+        return a;
+    }
     float get_output_scale(int64_t col) const { return get_output_scale_k(col, 0); }
     float get_importance_scale(int64_t row) const {
         check_index(row, n_in_, "row");
@@ -307,6 +314,17 @@ class Layer {
                                 "n_promoted_tiles", "n_scattered", "n_tiles"};
         for (int k = 0; k < 7; ++k) d[names[k]] = st[k];
         return d;
+    }
+
+    // Seeded synthetic layer generated on the device (benchmark workloads);
+    // the value-scale mirror is refreshed from the device afterwards.
+    int64_t load_synthetic(uint64_t seed, double keep_prob, float sigma, float tail_q) {
+        flush();
+        int64_t nnz = 0;
+        ck(sili_load_synthetic(L_, seed, keep_prob, sigma, tail_q, &nnz));
+        ck(sili_get_value_scale(L_, vs_.data()));
+        dirty_vs_ = false;
+        return nnz;
     }
 
     // The device store is always compact and rebuilt on every structural
@@ -498,6 +516,8 @@ PYBIND11_MODULE(_sili_hip, m) {
         .def("load_weight_bytes", &Layer::load_weight_bytes)
         .def("load_dense_codes", &Layer::load_dense_codes, py::arg("weight_codes"), py::arg("importance_codes"))
         .def("load_block4_tiles", &Layer::load_block4_tiles, py::arg("br"), py::arg("bc"), py::arg("tiles"))
+        .def("load_synthetic", &Layer::load_synthetic, py::arg("seed"), py::arg("keep_prob"), py::arg("sigma") = 0.02f,
+             py::arg("tail_q") = 0.5f)
         .def("get_scale_rank", &Layer::get_scale_rank)
         .def("set_scale_rank", &Layer::set_scale_rank)
         .def("set_value_scale_raw", &Layer::set_value_scale_raw)
@@ -509,6 +529,7 @@ PYBIND11_MODULE(_sili_hip, m) {
         .def("set_value_scales", &Layer::set_value_scales)
         .def("set_output_scales", &Layer::set_output_scales)
         .def("get_value_scale", &Layer::get_value_scale)
+        .def("get_value_scales", &Layer::get_value_scales)
         .def("get_output_scale", &Layer::get_output_scale)
         .def("get_value_scale_k", &Layer::get_value_scale_k)
         .def("get_output_scale_k", &Layer::get_output_scale_k)

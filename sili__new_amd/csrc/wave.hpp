@@ -85,8 +85,10 @@ __device__ __forceinline__ Chunk decode_chunk(const uint8_t *__restrict__ idx, u
     const uint64_t T = __ballot(term);
     // continuation flags of the 4 bytes before this lane, bit 3 = lane-1; the
     // window starts at a varint boundary, so positions before it read as 0
-    const uint64_t E = (~T) << 4;
-    const uint32_t q = (uint32_t)(E >> lane) & 0xFu;
+    // (two shifts: a single (~T << 4) would drop the flags of lanes 60-63)
+    const uint64_t NT = ~T;
+    const uint64_t E = lane >= 4u ? (NT >> (lane - 4u)) : (NT << (4u - lane));
+    const uint32_t q = (uint32_t)E & 0xFu;
     const uint32_t t = ~q & 0xFu;                             // first non-continuation from the top
     const uint32_t run = t ? (uint32_t)__builtin_clz(t) - 28u : 4u;  // preceding bytes of this varint
     // little-endian 7-bit groups: the terminator holds the most significant one
