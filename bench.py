@@ -200,6 +200,10 @@ def algorithmic(info, n_in, n_out, B, wl=None):
         "fwd:transpose": 8 * B * n_in,
         "bwd:transpose": 8 * B * n_out,
     }
+    # batch-1 byte-split kernels move the same algorithmic bytes as the gather
+    for op in ("fwd", "bwd"):
+        for k in ("stream", "stream_lds"):
+            out[f"{op}:{k}"] = out[f"{op}:gather"]
     T = info.get("n_tiles", 0)
     if T:
         bi = info.get("block_index_bytes", 0)
@@ -430,7 +434,7 @@ def run_config4(a, hip, api, rt):
             alg[d["name"]] = (info["nnz_scattered"] + info["index_bytes"] + 8 * (d["n_out"] + 1)
                               + 4 * (d["n_in"] + d["n_out"]) + 4 * B * (d["n_in"] + d["n_out"]))
         step_bytes = sum(alg.values())
-        gath = {k: v for k, v in kern.items() if k.endswith(":gather")}
+        gath = {k: v for k, v in kern.items() if k.split(":")[-1] in ("gather", "stream", "stream_lds")}
         dom = max(gath.items(), key=lambda kv: kv[1])
         dom_layer = dom[0].split(":")[0]
         ach = alg[dom_layer] / (dom[1] * 1e-3) / 1e9

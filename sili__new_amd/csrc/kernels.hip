@@ -1944,10 +1944,6 @@ void gather_v4_skip_u(const GArgs &a, int skip, hipStream_t st) {
 // float4 chunks per lane at batch 64) and 4 entries per group in flight --
 // the fastest measured shape for the fused backward at batch 64; the
 // forward gather is within 2% at every shape.
-inline int env_int(const char *name, int dflt) {
-    const char *e = std::getenv(name);
-    return e ? std::atoi(e) : dflt;
-}
 inline int gather_bl() {
     static const int v = [] {
         const int b = env_int("SILI_GATHER_BL", 8);
@@ -1989,10 +1985,16 @@ void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, in
         GArgs a{p.seg, p.nseg, p.idx, p.val, sc, in + b0, in_ld, out + b0 * out_ld, out_ld, nb,
                 small ? (uint32_t)in_bytes : 0u};
         const dim3 grid(blocks_for(a.nseg)), block(256);
+        if (gather_stream_used(p, sc, nb, in_ld, skip)) {
+            launch_gather_stream(p, sc, in, out, st);
+            continue;
+        }
         if (nb == 1 && small) {
             static const int lane_decode = env_int("SILI_B1_LANE_DECODE", 2);
             // (static LDS ~12.8 KB + the input stay within 64 KB per block)
-            if (lane_decode == 2 && skip == SKIP_NONE && sc.rank == 1 && in_ld == 1 && p.cols * 4 + 13312 <= 65536) {
+            // (only when each resident block has many segments to amortize the copy over)
+            if (lane_decode == 2 && skip == SKIP_NONE && sc.rank == 1 && in_ld == 1 && p.cols * 4 + 13312 <= 65536 &&
+                p.nseg >= (int64_t)256 * 4 * WAVES * 8) {
                 // input (times its column scale) held in LDS by each persistent block
                 const size_t lds = (size_t)p.cols * 4;
                 const unsigned gp = (unsigned)std::min<int64_t>((int64_t)blocks_for(a.nseg), 256 * (lds <= 24576 ? 4 : 2));

@@ -49,8 +49,12 @@ struct DScatter {
     DevBuf<SegDesc> seg;
     DevBuf<uint32_t> split_rows;  // rows with more than one work item
     int64_t n_split = 0;
+    DevBuf<WinDesc> win;          // stream windows (nwin + 1)
+    int64_t nwin = 0;
+    bool stream_ok = false;       // every window starts < 64 rows, no row of 1-7 bytes
     GatherPlan plan() const {
-        return GatherPlan{seg.p, nseg, idx.p, val.p, rows, cols, has_split, split_rows.p, n_split};
+        return GatherPlan{seg.p, nseg, idx.p, val.p, rows, cols, has_split, split_rows.p, n_split,
+                          win.p, nwin, byte_start.p, nbytes, nnz, stream_ok};
     }
 };
 

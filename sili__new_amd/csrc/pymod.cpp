@@ -101,6 +101,8 @@ class Layer {
         d["n_segments"] = i.n_segments;
         d["scale_rank"] = i.scale_rank;
         d["has_nonfinite"] = bool(i.has_nonfinite);
+        d["stream_canonical"] = bool(i.stream_canonical);
+        d["stream_shadow"] = bool(i.stream_shadow);
         return d;
     }
 

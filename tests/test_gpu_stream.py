@@ -1,0 +1,208 @@
+"""GPU: the batch-1 byte-split ("stream") gather against the CPU oracle.
+
+The stream kernels cut a store's index stream into 512-byte windows, place
+rows on the lanes holding their first byte and combine per-row pieces with
+a segmented wave scan.  The layers here are built to hit what that design
+has to get right: row starts at every byte offset of a lane, rows spanning
+many windows, rows shorter than a window, empty rows, multi-byte deltas
+(general decode), a partial last window and an exactly full one, row scales
+on both sides, and non-finite inputs.  Stores outside the kernels' limits
+(a row of 1-7 index bytes, 64 row starts in one window) must fall back to
+the segment kernels.  The launcher's kernel choice is read back from the
+per-kernel profiler, so each variant is known to have run."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import HostLayer
+from sili__new_amd.synth import per_row_quantize
+from tests.util import assert_close_terms
+
+
+def uleb_len(v):
+    n = 1
+    while v >= 128:
+        v >>= 7
+        n += 1
+    return n
+
+
+def row_bytes(cols):
+    prev, n = 0, 0
+    for c in cols:
+        n += uleb_len(c - prev)
+        prev = c
+    return n
+
+
+def mixed_rows(n_out, seed, total_mod512=None):
+    """Rows of 0 and 8..2900 entries, random columns (mixed delta lengths),
+    plus a final run of consecutive columns sized so that the stream length
+    mod 512 is `total_mod512` when given."""
+    rng = np.random.default_rng(seed)
+    lens = [0, 8, 9, 10, 11, 12, 13, 14, 15, 16, 0, 17, 20, 33, 64, 65, 127, 128, 129, 300, 0,
+            505, 506, 507, 508, 509, 510, 511, 512, 513, 514, 700, 1023, 1500, 2900]
+    lens += list(rng.integers(8, 600, size=60))
+    rng.shuffle(lens)
+    rows = [np.sort(rng.choice(n_out, size=min(int(n), n_out), replace=False)) for n in lens]
+    if total_mod512 is not None:
+        tot = sum(row_bytes(r) for r in rows)
+        k = 16
+        while (tot + k) % 512 != total_mod512:
+            k += 1
+        rows.append(np.arange(k))  # k one-byte deltas
+    return rows
+
+
+def transpose_rows(rows, n_out):
+    pairs = [(c, r) for r, cs in enumerate(rows) for c in cs]
+    out = [[] for _ in range(n_out)]
+    for c, r in sorted(pairs):
+        out[c].append(r)
+    return [np.array(o, np.int64) for o in out]
+
+
+def make_pair(hip, rows, n_out, seed=5, out_scales=True):
+    n_in = len(rows)
+    ptrs = np.concatenate([[0], np.cumsum([len(r) for r in rows])]).astype(np.int32)
+    cols = (np.concatenate(rows) if ptrs[-1] else np.zeros(0)).astype(np.int32)
+    rng = np.random.default_rng(seed)
+    w = rng.normal(size=len(cols)).astype(np.float32)
+    q, s = per_row_quantize(ptrs, w, n_in)
+    os_ = rng.uniform(0.5, 2.0, size=n_out).astype(np.float32) if out_scales else None
+    H = HostLayer(n_in, n_out)
+    H.load_csr(ptrs, cols, w=q)
+    H.set_scales(s, os_)
+    L = hip.SparseLinearLayer(n_in, n_out, max(1, len(cols)))
+    L.load_weights(ptrs, cols, q)
+    L.set_value_scales(s)
+    if os_ is not None:
+        L.set_output_scales(os_)
+    return H, L
+
+
+@pytest.fixture(autouse=True)
+def stream_always(monkeypatch):
+    """Use the stream kernels on every store that allows them (by default
+    only stores of >= 1 MiB of index bytes take them)."""
+    monkeypatch.setenv("SILI_B1_STREAM", "2")
+    yield
+
+
+class Entry(C.Structure):
+    _fields_ = [("name", C.c_char * 56), ("count", C.c_int64), ("total_ms", C.c_double),
+                ("min_ms", C.c_double), ("max_ms", C.c_double)]
+
+
+def kernels_run(hip, L, fn):
+    """Run fn() with L's profiler on; return the profiled kernel names."""
+    lib = C.CDLL(hip.LIB_PATH)
+    lib.sili_profile_enable.argtypes = [C.c_void_p, C.c_int]
+    lib.sili_profile_read.argtypes = [C.c_void_p, C.POINTER(Entry), C.c_int, C.POINTER(C.c_int)]
+    h = C.c_void_p(L.handle)
+    assert lib.sili_profile_enable(h, 1) == 0
+    fn()
+    buf = (Entry * 64)()
+    n = C.c_int()
+    assert lib.sili_profile_read(h, buf, 64, C.byref(n)) == 0
+    assert lib.sili_profile_enable(h, 0) == 0
+    return {buf[i].name.decode() for i in range(n.value)}
+
+
+def check_fwd(H, L, x, what):
+    y = L.forward_dense(x)
+    assert_close_terms(y, H.forward_dense(x), H.forward_dense(x, absmode=True), what)
+
+
+def check_bwd(H, L, x, g, what):
+    L.forward_dense(x)
+    dx = L.backward_dense(g, 0.0)
+    assert_close_terms(dx, H.backward_dense(x, g)[0], H.backward_dense(x, g, absmode=True)[0], what)
+
+
+def test_mixed_rows_encode_with_stream_limits():
+    """CPU check of the designed layers: every non-empty row has >= 8 index
+    bytes; the requested stream lengths mod 512 are met."""
+    for mod in (None, 0, 37):
+        rows = mixed_rows(3000, 1, mod)
+        nb = [row_bytes(r) for r in rows]
+        assert all(b == 0 or b >= 8 for b in nb)
+        if mod is not None:
+            assert sum(nb) % 512 == mod
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mod", [None, 0, 1, 511])
+def test_stream_canonical_and_shadow(hip, mod):
+    n_out = 3000
+    rows = mixed_rows(n_out, 2 + (mod or 0), mod)
+    # canonical orientation: dx = W^T g at batch 1 gathers the designed rows
+    H, L = make_pair(hip, rows, n_out)
+    assert L.info()["stream_canonical"]
+    rng = np.random.default_rng(9)
+    x = rng.normal(size=(1, len(rows))).astype(np.float32)
+    g = rng.normal(size=(1, n_out)).astype(np.float32)
+    names = kernels_run(hip, L, lambda: check_bwd(H, L, x, g, f"dx mod{mod}"))
+    assert any(n.startswith("bwd:stream") for n in names), names
+    check_fwd(H, L, x, f"fwd mod{mod}")
+    # shadow orientation: the transposed layer's forward gathers them
+    T = transpose_rows(rows, n_out)
+    HT, LT = make_pair(hip, T, len(rows))
+    assert LT.info()["stream_shadow"]
+    xt = rng.normal(size=(1, n_out)).astype(np.float32)
+    names = kernels_run(hip, LT, lambda: check_fwd(HT, LT, xt, f"T fwd mod{mod}"))
+    assert any(n.startswith("fwd:stream") for n in names), names
+    # a second call must not see the first call's output
+    check_fwd(HT, LT, xt * 0.5, f"T fwd again mod{mod}")
+
+
+@pytest.mark.gpu
+def test_stream_nonfinite_inputs(hip):
+    rows = mixed_rows(2000, 7)
+    T = transpose_rows(rows, 2000)
+    H, L = make_pair(hip, T, len(rows))
+    x = np.random.default_rng(1).normal(size=(1, 2000)).astype(np.float32)
+    x[0, 5] = np.inf
+    x[0, 17] = -np.inf
+    x[0, 40] = np.nan
+    x[0, 100:120] = 0.0
+    check_fwd(H, L, x, "non-finite x")
+
+
+@pytest.mark.gpu
+def test_stream_limits_fall_back(hip):
+    # a row of 7 one-byte deltas: the stream kernels are not used
+    rows = [np.arange(0, 40), np.arange(3, 10), np.arange(100, 180)]
+    H, L = make_pair(hip, rows, 200)
+    assert not L.info()["stream_canonical"]
+    x = np.random.default_rng(2).normal(size=(1, 3)).astype(np.float32)
+    g = np.random.default_rng(3).normal(size=(1, 200)).astype(np.float32)
+    names = kernels_run(hip, L, lambda: check_bwd(H, L, x, g, "short-row dx"))
+    assert not any("stream" in n for n in names), names
+    # 64 rows of 8 one-byte deltas start in one window: fallback; 9 bytes: stream
+    for width, ok in ((8, False), (9, True)):
+        rows = [np.arange(width) + r % 100 for r in range(200)]
+        H, L = make_pair(hip, rows, 1000)
+        assert L.info()["stream_canonical"] == ok
+        x = np.random.default_rng(width).normal(size=(1, 200)).astype(np.float32)
+        g = np.random.default_rng(width + 1).normal(size=(1, 1000)).astype(np.float32)
+        check_bwd(H, L, x, g, f"rows of {width} bytes")
+
+
+@pytest.mark.gpu
+def test_stream_lds_and_global_variants(hip):
+    """A long stream over a narrow input stages the input in LDS; a short
+    one reads it through the cache; an input too wide for LDS always does."""
+    seen = set()
+    for n_in, n_out, keep in ((1024, 60000, 0.08), (512, 3000, 0.1), (40000, 300, 0.02)):
+        L = hip.SparseLinearLayer(n_in, n_out, 1)
+        L.load_synthetic(4242 + n_in, keep, 0.02, 0.5)
+        ex = L.export_scattered()
+        H = HostLayer(n_in, n_out).load_encoded(ex["row_byte_start"], ex["row_elem_start"], ex["idx"], ex["val"])
+        H.set_scales(np.asarray(L.get_value_scales(), np.float32))
+        assert L.info()["stream_shadow"]
+        x = np.random.default_rng(n_in).normal(size=(1, n_in)).astype(np.float32)
+        names = kernels_run(hip, L, lambda: check_fwd(H, L, x, f"synthetic {n_in}x{n_out}"))
+        seen |= {n for n in names if "stream" in n}
+    assert "fwd:stream_lds" in seen and "fwd:stream" in seen, seen

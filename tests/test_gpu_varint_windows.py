@@ -8,7 +8,8 @@ at index byte `off`.  Offsets sweep every lane of the first windows
 of the wave's terminator mask) and the 508-byte work-item boundary.  The
 canonical store of layer A carries the designed rows (backward / grad-W
 gather them); layer B = A transposed carries them in its shadow store (its
-forward gathers them).  Every kernel variant keyed on the batch runs."""
+forward gathers them).  Every kernel variant keyed on the batch runs, and
+batch 1 runs through both the segment and the byte-split kernels."""
 import numpy as np
 import pytest
 
@@ -17,6 +18,15 @@ from sili__new_amd.synth import per_row_quantize
 from tests.util import assert_close_terms
 
 BATCHES = [1, 2, 4, 8, 12, 64, 128, 256]
+
+
+@pytest.fixture(params=["1", "2"], autouse=True)
+def stream_mode(request, monkeypatch):
+    """Batch 1 through the segment kernels ("1": these stores are below the
+    stream kernels' default size) and through the byte-split stream kernels
+    ("2")."""
+    monkeypatch.setenv("SILI_B1_STREAM", request.param)
+    yield request.param
 
 
 def _designed_rows():
