@@ -212,8 +212,8 @@ typedef struct {
     int64_t n_segments;        /* decode work items of the scattered store */
     int32_t scale_rank;
     int32_t has_nonfinite;     /* a weight code 8 (NaN) or non-finite scale */
-    int32_t stream_canonical;  /* batch-1 byte-split kernels usable on the canonical store */
-    int32_t stream_shadow;     /* ... on the shadow (forward) store */
+    int32_t stream_canonical;  /* batch-1 stream copy of the canonical store is built */
+    int32_t stream_shadow;     /* ... of the shadow (forward) store */
 } sili_info;
 int sili_get_info(sili_layer *layer, sili_info *out);
 

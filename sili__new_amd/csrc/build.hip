@@ -224,62 +224,7 @@ struct Encoded {
     int64_t nbytes = 0, nseg = 0;
     bool has_split = false;
     int64_t n_split = 0;
-    int64_t nwin = 0;
-    bool stream_ok = false;
 };
-
-// Stream windows (WinDesc): one thread per window, binary searches over the
-// varint start positions pos[0..N] (pos[N] = total) and the row starts.
-__global__ void k_win_meta(const uint64_t *__restrict__ pos, int64_t N, const uint32_t *__restrict__ byte_start,
-                           const uint32_t *__restrict__ elem_start, int64_t rows, const uint32_t *__restrict__ cols,
-                           int64_t nwin, WinDesc *__restrict__ win) {
-    const int64_t w = (int64_t)blockIdx.x * TPB + threadIdx.x;
-    if (w > nwin) return;
-    if (w == nwin) {
-        win[w] = WinDesc{(uint32_t)N, (uint32_t)rows, 0u, (uint32_t)rows};
-        return;
-    }
-    const uint64_t b0 = (uint64_t)w * WIN_BYTES;
-    // entry j - 1 ends at pos[j] - 1: elem = #{j in [1, N] : pos[j] <= b0}
-    int64_t lo = 1, hi = N + 1;
-    while (lo < hi) {
-        const int64_t mid = (lo + hi) >> 1;
-        if (pos[mid] <= b0) lo = mid + 1;
-        else hi = mid;
-    }
-    const uint32_t elem = (uint32_t)(lo - 1);
-    // row0: last row starting at or before b0 (non-empty: the next start is > b0)
-    lo = 0;
-    hi = rows + 1;
-    while (lo < hi) {
-        const int64_t mid = (lo + hi) >> 1;
-        if ((uint64_t)byte_start[mid] <= b0) lo = mid + 1;
-        else hi = mid;
-    }
-    const int64_t row0 = lo - 1;
-    // rs_lo: first row starting at or after b0
-    lo = 0;
-    hi = rows;
-    while (lo < hi) {
-        const int64_t mid = (lo + hi) >> 1;
-        if ((uint64_t)byte_start[mid] < b0) lo = mid + 1;
-        else hi = mid;
-    }
-    uint32_t carry = 0;
-    if ((uint64_t)byte_start[row0] != b0 && elem > elem_start[row0]) carry = cols[elem - 1];
-    win[w] = WinDesc{elem, (uint32_t)row0, carry, (uint32_t)lo};
-}
-// Stream kernel limits: < 64 row starts per window (bit 0), no row of 1-7
-// index bytes, so an 8-byte lane slice holds at most one row start (bit 1).
-__global__ void k_win_check(const WinDesc *__restrict__ win, int64_t nwin, const uint32_t *__restrict__ byte_start,
-                            int64_t rows, int *__restrict__ flag) {
-    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
-    if (i < nwin && win[i + 1].rs_lo - win[i].rs_lo > 63u) atomicOr(flag, 1);
-    if (i < rows) {
-        const uint32_t len = byte_start[i + 1] - byte_start[i];
-        if (len > 0u && len < 8u) atomicOr(flag, 2);
-    }
-}
 
 __global__ void k_split_flags(const uint32_t *__restrict__ segcnt, int64_t rows, uint32_t *__restrict__ flag) {
     const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
@@ -294,8 +239,7 @@ __global__ void k_split_list(const uint32_t *__restrict__ flag, const uint32_t *
 Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint32_t *d_ptrs,
                     const uint32_t *d_cols, uint32_t seg_len, bool emit_empty,
                     DevBuf<uint32_t> &byte_start, DevBuf<uint32_t> &elem_start, DevBuf<uint8_t> &idx,
-                    DevBuf<SegDesc> &seg, const char *what, DevBuf<uint32_t> *split_rows = nullptr,
-                    DevBuf<WinDesc> *win = nullptr) {
+                    DevBuf<SegDesc> &seg, const char *what, DevBuf<uint32_t> *split_rows = nullptr) {
     Encoded out;
     hipStream_t st = L.stream;
     DevBuf<uint64_t> len, pos;
@@ -367,26 +311,6 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
         SILI_HIP(hipStreamSynchronize(st));
         out.n_split = ns;
     }
-    if (win) {
-        // stream windows over the index bytes
-        const int64_t nwin = (int64_t)((total + WIN_BYTES - 1) / WIN_BYTES);
-        win->ensure((size_t)nwin + 1);
-        launch(k_win_meta, dim3(nblk(nwin + 1)), dim3(TPB), 0, st, (const uint64_t *)pos.p, N,
-               (const uint32_t *)byte_start.p, (const uint32_t *)elem_start.p, rows, d_cols, nwin, win->p);
-        SILI_HIP(hipGetLastError());
-        zero_flag(L);
-        const int64_t nchk = std::max<int64_t>(nwin, rows);
-        if (nchk > 0)
-            launch(k_win_check, dim3(nblk(nchk)), dim3(TPB), 0, st, (const WinDesc *)win->p, nwin,
-                   (const uint32_t *)byte_start.p, rows, L.scratch.flag.p);
-        SILI_HIP(hipGetLastError());
-        int bad = 0;
-        SILI_HIP(hipMemcpyAsync(&bad, L.scratch.flag.p, sizeof(int), hipMemcpyDeviceToHost, st));
-        SILI_HIP(hipStreamSynchronize(st));
-        out.nwin = nwin;
-        // (byte offsets of the stream kernels stay below 2^31)
-        out.stream_ok = bad == 0 && nwin > 0 && total + WIN_BYTES < (1ull << 31) && (uint64_t)N < (1ull << 31);
-    }
     return out;
 }
 
@@ -437,10 +361,10 @@ static int bits_for(uint64_t max_value) {
 void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64_t N,
                      const uint32_t *d_ptrs, const uint32_t *d_cols, const uint8_t *d_bytes) {
     const Encoded e = encode_rows(L, rows, ncols, N, d_ptrs, d_cols, L.seg_len, true, dst.byte_start,
-                                  dst.elem_start, dst.idx, dst.seg, "load_weights", &dst.split_rows, &dst.win);
+                                  dst.elem_start, dst.idx, dst.seg, "load_weights", &dst.split_rows);
     dst.n_split = e.n_split;
-    dst.nwin = e.nwin;
-    dst.stream_ok = e.stream_ok;
+    dst.stream.valid = false;
+    dst.stream.failed = false;
     dst.rows = rows;
     dst.cols = ncols;
     dst.nnz = N;
@@ -482,10 +406,10 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
                        src.cols, ptrs.p);
     SILI_HIP(hipGetLastError());
     const Encoded e = encode_rows(L, src.cols, src.rows, N, ptrs.p, trows.p, L.seg_len, true, dst.byte_start,
-                                  dst.elem_start, dst.idx, dst.seg, "shadow build", &dst.split_rows, &dst.win);
+                                  dst.elem_start, dst.idx, dst.seg, "shadow build", &dst.split_rows);
     dst.n_split = e.n_split;
-    dst.nwin = e.nwin;
-    dst.stream_ok = e.stream_ok;
+    dst.stream.valid = false;
+    dst.stream.failed = false;
     dst.rows = src.cols;
     dst.cols = src.rows;
     dst.nnz = N;

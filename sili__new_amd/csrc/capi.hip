@@ -242,9 +242,14 @@ void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st
     // observable with non-finite weights, so the skip is compiled in only then
     const int skip = L.has_nonfinite ? SKIP_ZERO : SKIP_NONE;
     const ScaleView ssc = shadow_scales(L);
-    if (L.Wt.nnz == 0) fill(y, B * L.n_out, 0.0f, st);
-    else if (!gather_stream_used(L.Wt.plan(), ssc, B, B, skip)) launch_zero_split_rows(L.Wt.plan(), y, L.n_out, B, st);
-    if (L.Wt.nnz > 0) launch_gather(L.Wt.plan(), ssc, xT, B, y, L.n_out, B, skip, st);
+    if (L.Wt.nnz == 0) {
+        fill(y, B * L.n_out, 0.0f, st);
+    } else if (stream_wanted(L.Wt, ssc, B, B, skip)) {
+        stream_gather(L, L.Wt, ssc, xT, y, st);
+    } else {
+        launch_zero_split_rows(L.Wt.plan(), y, L.n_out, B, st);
+        launch_gather(L.Wt.plan(), ssc, xT, B, y, L.n_out, B, skip, st);
+    }
     if (L.B4t.ntiles > 0)
         launch_gather_b4(L.B4t.plan(), shadow_scales(L), xT, B, y, L.n_out, B, SKIP_NONE, st);
 }
@@ -274,13 +279,14 @@ void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float 
         if (xT) launch_rowabs(xT, B, L.n_in, L.acc_in.p, st);
         else launch_colabs(x, B, L.n_in, L.acc_in.p, st);
     }
+    const bool str = scat && stream_wanted(L.W, canon_scales(L), B, B, SKIP_NONE);
     if (!scat) fill(dx, B * L.n_in, 0.0f, st);
-    else if (!gather_stream_used(L.W.plan(), canon_scales(L), B, B, SKIP_NONE))
-        launch_zero_split_rows(L.W.plan(), dx, L.n_in, B, st);
+    else if (!str) launch_zero_split_rows(L.W.plan(), dx, L.n_in, B, st);
     // grad-input and grad-W read the same gT row per synapse: one fused pass
     const bool fused = scat && gw_s &&
                        launch_bwd_fused(L.W.plan(), canon_scales(L), gT, xT, B, dx, L.n_in, gw_s, L.acc_in.p, st);
-    if (scat && !fused) launch_gather(L.W.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
+    if (str) stream_gather(L, L.W, canon_scales(L), gT, dx, st);
+    else if (scat && !fused) launch_gather(L.W.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
     if (L.B4.ntiles > 0)
         launch_gather_b4(L.B4.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
     if (scat && gw_s && !fused) launch_sddmm(L.W.plan(), xT, gT, B, gw_s, L.acc_in.p, st);
@@ -661,8 +667,8 @@ int sili_get_info(sili_layer *layer, sili_info *out) {
         out->n_segments = L.W.nseg;
         out->scale_rank = L.rank;
         out->has_nonfinite = L.has_nonfinite ? 1 : 0;
-        out->stream_canonical = L.W.stream_ok ? 1 : 0;
-        out->stream_shadow = L.Wt.stream_ok ? 1 : 0;
+        out->stream_canonical = L.W.stream.valid ? 1 : 0;
+        out->stream_shadow = L.Wt.stream.valid ? 1 : 0;
         if (L.B4.ntiles > 0) {
             std::vector<uint32_t> br, bc;
             export_block4_coords(L, br, bc);

@@ -100,18 +100,18 @@ constexpr uint32_t SEG_SPLIT = 1u;  // the row has several segments (combine wit
 constexpr uint32_t SEG_FIRST = 2u;  // first segment of its row
 
 // ---- stream window ---------------------------------------------------------
-// Window w of a store's index stream = bytes [w*WIN_BYTES, (w+1)*WIN_BYTES)
-// of the concatenated rows (the batch-1 stream kernels split work by index
-// bytes, not by rows).  An entry belongs to the window holding the last byte
-// of its varint.
-//   elem  : entries ending before the window (first entry of the window)
+// The batch-1 stream kernels read a padded copy of a scattered store (see
+// DStream in layer.hpp) cut into windows of WIN_BYTES = 64 lanes x 16 bytes.
+// Per window:
 //   row0  : the row holding the window's first byte
-//   carry : column of row0's last entry ending before the window (0 if none)
-//   rs_lo : first row whose first byte is at or after the window start
-// A sentinel follows the last window: {nnz, rows, 0, rows}.
-constexpr uint32_t WIN_BYTES = 512;
+//   carry : shifted column (col + 1) of row0's last entry ending before the
+//           window (0 if none)
+//   rs_lo : first non-empty row (index into the store's list of non-empty
+//           rows) whose first byte is at or after the window start
+// A sentinel follows the last window: {rows, 0, number of non-empty rows, 0}.
+constexpr uint32_t WIN_BYTES = 1024;
 struct alignas(16) WinDesc {
-    uint32_t elem, row0, carry, rs_lo;
+    uint32_t row0, carry, rs_lo, pad;
 };
 
 // ---- FP4 E2M1 codec (device + host) -----------------------------------------
@@ -167,12 +167,6 @@ struct GatherPlan {      // one orientation of the scattered store
     bool has_split;
     const uint32_t *split_rows;  // rows spanning several work items (n_split of them)
     int64_t n_split;
-    // stream windows (batch-1 kernels); usable when stream_ok
-    const WinDesc *win;          // nwin + 1
-    int64_t nwin;
-    const uint32_t *byte_start;  // rows + 1
-    int64_t nbytes, nnz;
-    bool stream_ok;
 };
 
 struct Block4Plan {
@@ -218,11 +212,7 @@ void launch_densify(const int32_t *ptrs, const int32_t *idx, const float *vals, 
                     int64_t n, float *dst, float *acc_abs, bool mark_explicit, int64_t nnz_hint, hipStream_t st);
 // Zero out[b, row] of the rows split over several work items of `p`.
 void launch_zero_split_rows(const GatherPlan &p, float *out, int64_t out_ld, int64_t nb, hipStream_t st);
-// Batch-1 gather split by index bytes (stream.hip): used by launch_gather
-// when gather_stream_used(); it zeroes out[0, rows) itself, so callers skip
-// their split-row zeroing then.
-bool gather_stream_used(const GatherPlan &p, const ScaleView &sc, int64_t nb, int64_t in_ld, int skip);
-void launch_gather_stream(const GatherPlan &p, const ScaleView &sc, const float *in, float *out, hipStream_t st);
+
 // Device decode of a scattered store: cols[e], w[e] = fl32(dec * S(row, col)).
 void launch_decode(const GatherPlan &p, const ScaleView &sc, int32_t *cols, float *w,
                    uint32_t *rows_out, hipStream_t st);

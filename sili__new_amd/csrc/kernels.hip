@@ -1985,10 +1985,6 @@ void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, in
         GArgs a{p.seg, p.nseg, p.idx, p.val, sc, in + b0, in_ld, out + b0 * out_ld, out_ld, nb,
                 small ? (uint32_t)in_bytes : 0u};
         const dim3 grid(blocks_for(a.nseg)), block(256);
-        if (gather_stream_used(p, sc, nb, in_ld, skip)) {
-            launch_gather_stream(p, sc, in, out, st);
-            continue;
-        }
         if (nb == 1 && small) {
             static const int lane_decode = env_int("SILI_B1_LANE_DECODE", 2);
             // (static LDS ~12.8 KB + the input stay within 64 KB per block)

@@ -40,6 +40,25 @@ struct DevBuf {
     T *get() const { return p; }
 };
 
+// Padded stream copy of a scattered store, read by the batch-1 stream
+// kernels (built on first use, dropped when the store is rebuilt).  Row r
+// occupies bytes [pstart[r], pstart[r+1]) with pstart[r] a multiple of 16:
+// z zero bytes (delta 0: entries at shifted column 0), then the row's
+// varints for the shifted columns col + 1 (only the row's first, absolute
+// delta changes).  Shifted column 0 is a zero input slot, so the padding
+// entries (value byte 0) contribute exactly 0.  val[p] is the value byte of
+// the entry whose varint ends at byte p (0 elsewhere): value bytes run in
+// parallel with index bytes.
+struct DStream {
+    bool valid = false;
+    bool failed = false;          // too large for the kernels' 31-bit offsets
+    int64_t nbytes = 0, nwin = 0, n_ne = 0;
+    DevBuf<uint8_t> idx, val;     // nbytes (+ padding)
+    DevBuf<uint32_t> ne_row;      // non-empty rows, ascending (n_ne)
+    DevBuf<uint32_t> ne_start;    // their first padded byte (n_ne + 1; last = nbytes)
+    DevBuf<WinDesc> win;          // nwin + 1 (rs_lo indexes ne_row / ne_start)
+};
+
 // One orientation of the scattered store.
 struct DScatter {
     int64_t rows = 0, cols = 0, nnz = 0, nbytes = 0, nseg = 0;
@@ -49,12 +68,9 @@ struct DScatter {
     DevBuf<SegDesc> seg;
     DevBuf<uint32_t> split_rows;  // rows with more than one work item
     int64_t n_split = 0;
-    DevBuf<WinDesc> win;          // stream windows (nwin + 1)
-    int64_t nwin = 0;
-    bool stream_ok = false;       // every window starts < 64 rows, no row of 1-7 bytes
+    DStream stream;               // batch-1 stream copy (on demand)
     GatherPlan plan() const {
-        return GatherPlan{seg.p, nseg, idx.p, val.p, rows, cols, has_split, split_rows.p, n_split,
-                          win.p, nwin, byte_start.p, nbytes, nnz, stream_ok};
+        return GatherPlan{seg.p, nseg, idx.p, val.p, rows, cols, has_split, split_rows.p, n_split};
     }
 };
 
@@ -163,6 +179,15 @@ void device_sort_pairs_u32(Layer &L, const uint32_t *kin, uint32_t *kout, const 
                            uint32_t *vout, int64_t n, int bits);
 void device_sort_pairs_u64(Layer &L, const uint64_t *kin, uint64_t *kout, const uint32_t *vin,
                            uint32_t *vout, int64_t n, int bits);
+
+// ---- batch-1 stream kernels (stream.hip) ---------------------------------------
+// Whether stream_gather serves this call (batch 1, no skip rule, rank-1
+// scales, contiguous input; SILI_B1_STREAM: 0 never, 1 stores of >= 1 MiB of
+// index bytes (default), 2 always).
+bool stream_wanted(const DScatter &s, const ScaleView &sc, int64_t nb, int64_t in_ld, int skip);
+// out[row] = sum_e dec(code_e) * S(row, col_e) * in[col_e] for every row of s
+// (zeroes out first; builds s.stream on first use).
+void stream_gather(Layer &L, DScatter &s, const ScaleView &sc, const float *in, float *out, hipStream_t st);
 
 // ---- seeded synthetic layers (gen.hip) ----------------------------------------
 // Rebuilds the scattered store (and its shadow) from the seeded generator and

@@ -1,28 +1,34 @@
-// stream.hip -- batch-1 gather split by index bytes ("stream" kernels).
+// stream.hip -- batch-1 gather over a padded stream copy ("stream" kernels).
 //
 // out[row] = sum over the row's entries of dec(code) * S(row, col) * in[col]
-// for one input vector (the forward y = W x over the shadow store, or dx =
-// W^T g over the canonical one; linear_disldo.hpp:68-345 / :962-1951 at batch
-// 1).  The per-row segment kernels give every row its own work items, so a
-// row slightly longer than a work item costs two wave passes; here the work
-// is cut into fixed 512-byte windows of the concatenated index stream
-// (WinDesc), so every wave pass decodes 64 x 8 index bytes whatever the row
-// lengths.  Lane l of a window owns index bytes [8l, 8l + 8):
-//   - rows starting inside the window are placed on the lanes holding their
-//     first byte (at most one per lane: the store has no row of 1-7 bytes),
-//   - the running column of each lane comes from one wave prefix sum of the
-//     lanes' delta sums, restarted at row starts,
-//   - per-row partial sums are combined by a segmented wave scan and leave
-//     as one atomic add per row piece (the caller's output is zeroed first).
-// A window whose bytes are all one-byte varints (every byte ends an entry)
-// takes a decode without continuation handling; any other window (long
-// deltas, the stream's partial last window) takes the general decode.
+// for one input vector: the forward y = W x over the shadow store, or
+// dx = W^T g over the canonical one (linear_disldo.hpp:68-345 / :962-1951 at
+// batch 1).  The per-row segment kernels give every row its own work items,
+// so a row slightly longer than a work item costs two wave passes.  Here the
+// work is cut into fixed 1024-byte windows of a padded copy of the store's
+// index stream (DStream), so every wave pass decodes 64 x 16 index bytes
+// whatever the row lengths:
+//   - rows start on 16-byte boundaries (zero-delta padding entries in front,
+//     columns shifted by one so that shifted column 0 is a zero input slot):
+//     each lane's 16 bytes belong to one row, and the per-entry work is one
+//     add, one LDS (or cache) read, one FP4 conversion and one FMA,
+//   - value bytes run in parallel with index bytes (val[p] belongs to the
+//     entry whose varint ends at byte p), so no entry count is needed to
+//     find them,
+//   - the running column of each lane comes from a segmented wave scan of
+//     the lanes' delta sums (byte sums by v_sad_u8), restarted at row
+//     starts; per-row partial sums are combined by a second segmented scan
+//     and leave as one atomic add per row piece (the output is zeroed first).
+// A window whose bytes are all one-byte varints takes a decode without
+// continuation handling; any other window (long deltas, the stream's partial
+// last window) takes the general decode.
 //
-// XLDS: the block first stages in[c] * ent_scale[c] in LDS, so a synapse
-// costs one LDS read; otherwise in and the column scale come through buffer
-// loads.  The FP4 code is expanded by v_cvt_scalef32_pk_f32_fp4 (OCP E2M1:
-// the reference decode for every code but 8, which never reaches these
-// kernels: they serve only layers without non-finite weights, SKIP_NONE).
+// XLDS: the block first stages in[c] * ent_scale[c] in LDS (slot c + 1,
+// slot 0 = 0); otherwise in and the column scale come through buffer loads
+// whose out-of-range reads return 0.  The FP4 code is expanded by
+// v_cvt_scalef32_pk_f32_fp4 (OCP E2M1: the reference decode for every code
+// but 8, which never reaches these kernels: they serve only layers without
+// non-finite weights, SKIP_NONE).
 #include "layer.hpp"
 #include "wave.hpp"
 
@@ -35,16 +41,146 @@ namespace sili {
 
 namespace {
 
+constexpr unsigned TPB = 256;
 constexpr uint32_t SLOT_NONE = 0xFFFFFFFFu;
 constexpr uint32_t MAX_WAVES = 16;
+constexpr uint32_t BPL = 16;  // index bytes per lane
+
+inline unsigned nblk(int64_t n) { return (unsigned)((n + TPB - 1) / TPB); }
+
+// ---- building the stream copy ----------------------------------------------
+
+// First varint of a row of n bytes: value and length.
+__device__ __forceinline__ void first_varint(const uint8_t *p, uint32_t n, uint32_t &v, uint32_t &len) {
+    v = 0;
+    len = 0;
+    uint32_t shift = 0;
+    while (len < n && len < 5u) {
+        const uint32_t b = p[len++];
+        v |= (b & 0x7Fu) << shift;
+        shift += 7;
+        if (!(b & 0x80u)) break;
+    }
+}
+
+// Padded length of row r: its bytes with the first delta re-encoded for
+// col + 1, rounded up to 16.
+__global__ void k_sp_len(const uint32_t *__restrict__ bs, const uint8_t *__restrict__ idx, int64_t rows,
+                         uint32_t *__restrict__ len, uint32_t *__restrict__ nonempty) {
+    const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (r > rows) return;
+    if (r == rows) {
+        len[r] = 0;
+        nonempty[r] = 0;
+        return;
+    }
+    const uint32_t b = bs[r], n = bs[r + 1] - b;
+    uint32_t L = 0;
+    if (n) {
+        uint32_t c0, l0;
+        first_varint(idx + b, n, c0, l0);
+        L = (n - l0 + uleb_len(c0 + 1u) + 15u) & ~15u;
+    }
+    len[r] = L;
+    nonempty[r] = n ? 1u : 0u;
+}
+
+__global__ void k_sp_ne(const uint32_t *__restrict__ nonempty, const uint32_t *__restrict__ pos,
+                        const uint32_t *__restrict__ pstart, int64_t rows, uint32_t *__restrict__ ne_row,
+                        uint32_t *__restrict__ ne_start) {
+    const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (r > rows) return;
+    if (r == rows) {
+        ne_start[pos[r]] = pstart[r];  // sentinel: total bytes
+        return;
+    }
+    if (nonempty[r]) {
+        ne_row[pos[r]] = (uint32_t)r;
+        ne_start[pos[r]] = pstart[r];
+    }
+}
+
+// One wave per row: copy the row into the padded stream (first delta
+// re-encoded, value bytes placed at their terminators) and write row0 /
+// carry of every window that starts inside the row's padded range.
+__global__ __launch_bounds__(256) void k_sp_copy(const uint32_t *__restrict__ bs, const uint32_t *__restrict__ es,
+                                                 const uint8_t *__restrict__ idx, const uint8_t *__restrict__ val,
+                                                 const uint32_t *__restrict__ pstart, int64_t rows,
+                                                 uint8_t *__restrict__ sidx, uint8_t *__restrict__ sval,
+                                                 WinDesc *__restrict__ win) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + uniform(threadIdx.x >> 6);
+    if (r >= rows) return;
+    const uint32_t lane = lane_id();
+    const uint32_t b = bs[r], n = bs[r + 1] - b;
+    if (n == 0) return;
+    const uint32_t P = pstart[r], Lr = pstart[r + 1] - P;
+    uint32_t c0, l0;
+    first_varint(idx + b, n, c0, l0);
+    const uint32_t v1 = c0 + 1u, l1 = uleb_len(v1);
+    const uint32_t z = Lr - (n - l0 + l1);  // padding entries in front
+    const uint32_t D = P + z + l1;          // padded position of row byte l0
+    if (lane < l1) sidx[P + z + lane] = (uint8_t)(((v1 >> (7u * lane)) & 0x7Fu) | (lane + 1u < l1 ? 0x80u : 0u));
+    if (lane == 0u) sval[D - 1u] = val[es[r]];
+    // a window starting before the first entry's last byte: only padding
+    // entries (shifted column 0) precede it
+    const uint32_t w_pad = (P + WIN_BYTES - 1u) / WIN_BYTES * WIN_BYTES;
+    if (lane == 0u && w_pad < D) {
+        win[w_pad / WIN_BYTES].row0 = (uint32_t)r;
+        win[w_pad / WIN_BYTES].carry = 0u;
+    }
+    const uint8_t *row = idx + b;
+    uint32_t off = l0, carry = c0, ebase = es[r] + 1u;
+    while (off < n) {
+        const Chunk ch = decode_chunk(row, off, n, carry);
+        if (ch.T == 0ull) break;
+        const uint32_t hi = 63u - (uint32_t)__clzll(ch.T);  // last byte of the chunk's last entry
+        const uint32_t d0 = D + off - l0;                   // padded position of byte `off`
+        if (lane <= hi) {
+            sidx[d0 + lane] = row[off + lane];
+            if (ch.term) sval[d0 + lane] = val[ebase + ch.rank];
+        }
+        // a window starting inside the chunk's bytes [d0, d0 + hi]
+        const uint32_t ws = (d0 + WIN_BYTES - 1u) / WIN_BYTES * WIN_BYTES;
+        if (ws <= d0 + hi) {
+            const uint64_t before = ch.T & ((1ull << (ws - d0)) - 1ull);
+            uint32_t c = carry + 1u;
+            if (before) c = (uint32_t)__shfl((int)ch.col, 63 - (int)__clzll(before), 64) + 1u;
+            if (lane == 0u) {
+                win[ws / WIN_BYTES].row0 = (uint32_t)r;
+                win[ws / WIN_BYTES].carry = c;
+            }
+        }
+        carry = chunk_advance(ch, off, ebase);
+    }
+}
+
+// rs_lo of every window: first non-empty row starting at or after it.
+__global__ void k_sp_rs(const uint32_t *__restrict__ ne_start, int64_t n_ne, int64_t nwin, int64_t rows,
+                        WinDesc *__restrict__ win) {
+    const int64_t w = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (w > nwin) return;
+    if (w == nwin) {
+        win[w] = WinDesc{(uint32_t)rows, 0u, (uint32_t)n_ne, 0u};
+        return;
+    }
+    const uint64_t b0 = (uint64_t)w * WIN_BYTES;
+    int64_t lo = 0, hi = n_ne;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi) >> 1;
+        if ((uint64_t)ne_start[mid] < b0) lo = mid + 1;
+        else hi = mid;
+    }
+    win[w].rs_lo = (uint32_t)lo;
+}
+
+// ---- the gather ------------------------------------------------------------
 
 struct StreamArgs {
     const WinDesc *win;          // nwin + 1
     int64_t nwin;
-    const uint8_t *idx;
-    const uint8_t *val;
-    const uint32_t *byte_start;  // rows + 1
-    uint32_t nbytes, nnz;
+    const uint8_t *idx, *val;    // padded stream
+    const uint32_t *ne_row, *ne_start;
+    uint32_t nbytes;
     const float *in;             // in[c], c < nx
     const float *ent;            // column scale (NULL: ones)
     const float *rsc;            // row scale (NULL: ones)
@@ -52,98 +188,105 @@ struct StreamArgs {
     float *out;                  // out[row], zeroed beforehand
 };
 
-// Registers of one window: its descriptor and the next one (whose elem and
-// rs_lo bound this window's entries and rows), the lane's index bytes, the
-// index dword before the window (lane 0), the lane's value dwords and one
-// row start per lane.
+// Registers of one window: its descriptor and the next one's rs_lo, the
+// lane's 16 index and 16 value bytes, the index dword before the window
+// (lane 0), and one (first byte, row) of the non-empty rows starting in it.
 struct WinRegs {
-    WinDesc m, mn;
-    uint32_t i0, i1, ip;
-    uint32_t v0, v1, v2;
-    uint32_t R;
+    WinDesc m;
+    uint32_t rs_hi;
+    uint32_t i[4], v[4], ip;
+    uint32_t Rs, Rr;
 };
 
 __device__ __forceinline__ WinDesc uniform_win(const uint4 q) {
     return WinDesc{uniform(q.x), uniform(q.y), uniform(q.z), uniform(q.w)};
 }
 __device__ __forceinline__ uint4 load_win_raw(const WinDesc *p) { return *reinterpret_cast<const uint4 *>(p); }
-
-__device__ __forceinline__ uint2 buffer_load_u2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
-}
-__device__ __forceinline__ uint32_t buffer_load_u1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+__device__ __forceinline__ uint4 buffer_load_u4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
-// Issue the loads of window w (descriptors already in r.m / r.mn).
+// Issue the loads of window w (descriptors already in r.m / r.rs_hi).
 __device__ __forceinline__ void load_window(const StreamArgs &a, int64_t w, WinRegs &r) {
     const uint32_t lane = lane_id();
     const uint32_t b0 = (uint32_t)w * WIN_BYTES;
     const uint32_t nb = min(a.nbytes - b0, WIN_BYTES);
-    // index bytes (the store keeps >= 64 bytes of padding; lanes past the
-    // window's end read 0, bytes at or past nb are masked by the decode)
-    const uint2 iw = buffer_load_u2(buffer_rsrc(a.idx + b0, nb + 8u), 8u * lane);
-    r.i0 = iw.x;
-    r.i1 = iw.y;
+    // 16-byte aligned; lanes past the stream's end read 0, bytes at or past
+    // nb are masked by the decode
+    const uint4 iw = buffer_load_u4(buffer_rsrc(a.idx + b0, nb + 16u), BPL * lane);
+    const uint4 vw = buffer_load_u4(buffer_rsrc(a.val + b0, nb + 16u), BPL * lane);
+    r.i[0] = iw.x;
+    r.i[1] = iw.y;
+    r.i[2] = iw.z;
+    r.i[3] = iw.w;
+    r.v[0] = vw.x;
+    r.v[1] = vw.y;
+    r.v[2] = vw.z;
+    r.v[3] = vw.w;
     r.ip = (lane == 0u && b0 > 0u) ? *reinterpret_cast<const uint32_t *>(a.idx + b0 - 4u) : 0u;
-    // value bytes [elem, elem + 512) from their aligned dword
-    const uint32_t vbase = r.m.elem & ~3u;
-    const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(a.val + vbase, a.nnz - vbase + 8u);
-    r.v0 = buffer_load_u1(rv, 8u * lane);
-    r.v1 = buffer_load_u1(rv, 8u * lane + 4u);
-    r.v2 = buffer_load_u1(rv, 8u * lane + 8u);
-    // first bytes of the rows starting in the window, and of the one after
-    const uint32_t nr = r.mn.rs_lo - r.m.rs_lo;
-    r.R = lane <= nr ? a.byte_start[r.m.rs_lo + lane] : 0u;
+    const uint32_t nr = r.rs_hi - r.m.rs_lo;  // non-empty rows starting here (<= 64)
+    r.Rs = lane < nr ? a.ne_start[r.m.rs_lo + lane] : 0u;
+    r.Rr = lane < nr ? a.ne_row[r.m.rs_lo + lane] : 0u;
 }
 
-// Weight code of value byte k (0..3) of dw: the high nibble.  The conversion
+// Weight code of value byte K (0..3) of dw: the high nibble.  The conversion
 // yields both nibbles of the byte, low nibble first.
 template <int K>
 __device__ __forceinline__ float fp4_code_hi(uint32_t dw) {
     return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(dw, 1.0f, K)[1];
 }
+__device__ __forceinline__ float fp4_code_hi_byte(uint32_t dw, int k) {
+    switch (k & 3) {
+        case 0: return fp4_code_hi<0>(dw);
+        case 1: return fp4_code_hi<1>(dw);
+        case 2: return fp4_code_hi<2>(dw);
+        default: return fp4_code_hi<3>(dw);
+    }
+}
+
+// x at shifted column c (0: the zero slot)
+template <bool XLDS>
+__device__ __forceinline__ float stream_x(const StreamArgs &a, const float *s_x, __amdgpu_buffer_rsrc_t rin,
+                                          __amdgpu_buffer_rsrc_t rent, uint32_t c) {
+    if constexpr (XLDS) {
+        return s_x[c];
+    } else {
+        const uint32_t off = c * 4u - 4u;  // c = 0: out of range, reads 0
+        return buffer_load_f1(rin, off) * (a.ent ? buffer_load_f1(rent, off) : 1.0f);
+    }
+}
 
 template <bool XLDS, bool FAST>
 __device__ __forceinline__ void run_window(const StreamArgs &a, int64_t w, const WinRegs &r, uint32_t *slot,
-                                           uint32_t *vb, const float *s_x, __amdgpu_buffer_rsrc_t rin,
+                                           const float *s_x, __amdgpu_buffer_rsrc_t rin,
                                            __amdgpu_buffer_rsrc_t rent) {
     const uint32_t lane = lane_id();
     const uint32_t b0 = (uint32_t)w * WIN_BYTES;
-    const uint32_t nb = min(a.nbytes - b0, WIN_BYTES);
-    const uint32_t nr = r.mn.rs_lo - r.m.rs_lo;
+    const uint32_t nr = r.rs_hi - r.m.rs_lo;
 
-    // rows starting in the window -> the lane holding their first byte
+    // rows starting in the window -> the lane holding their first 16 bytes
     slot[lane] = SLOT_NONE;
     wave_lds_sync();
-    const uint32_t Rn = (uint32_t)__shfl_down((int)r.R, 1, 64);
-    const uint32_t rel = r.R - b0;
-    if (lane < nr && Rn > r.R && rel < WIN_BYTES) {
-        slot[rel >> 3] = (lane << 3) | (rel & 7u);
-    }
+    if (lane < nr) slot[(r.Rs - b0) / BPL] = r.Rr;
     wave_lds_sync();
     const uint32_t sl = slot[lane];
     const bool hs = sl != SLOT_NONE;
-    const uint32_t so = hs ? (sl & 7u) : 8u;        // byte of the row start
-    const uint32_t srow = r.m.rs_lo + (sl >> 3);    // the row starting there
     const uint64_t S = __ballot(hs);
-    const uint64_t lt = S & ((1ull << lane) - 1ull);
-    const int sp = lt ? 63 - (int)__clzll(lt) : -1;  // latest lane before this one with a row start
-    const int spc = sp < 0 ? 0 : sp;
-    const uint32_t hrow_s = (uint32_t)__shfl((int)srow, spc, 64);
-    const uint32_t hrow = sp < 0 ? r.m.row0 : hrow_s;  // row of this lane's first bytes
+    // the lane's row: the latest row start at or before it (rows ascend)
+    const uint32_t mrow = wave_max_scan(hs ? sl + 1u : 0u);
+    const uint32_t row = mrow ? mrow - 1u : r.m.row0;
 
     // deltas of the entries ending at each byte (0 where no entry ends)
-    uint32_t dv[8];
-    uint32_t tmask = 0xFFu;
+    uint32_t full = 0;
+    uint32_t dv[BPL];
+    uint32_t tmask = 0xFFFFu;
+    if constexpr (FAST) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        dv[i] = (r.i0 >> (8 * i)) & 0xFFu;
-        dv[4 + i] = (r.i1 >> (8 * i)) & 0xFFu;
-    }
-    if constexpr (!FAST) {
+        for (int k = 0; k < 4; ++k) full = __builtin_amdgcn_sad_u8(r.i[k], 0u, full);
+    } else {
+        const uint32_t nb = min(a.nbytes - b0, WIN_BYTES);
         // the previous 4 bytes: the previous lane's, or those before the window
-        const uint32_t pw0 = (uint32_t)__shfl_up((int)r.i1, 1, 64);
+        const uint32_t pw0 = (uint32_t)__shfl_up((int)r.i[3], 1, 64);
         const uint32_t pw = lane ? pw0 : r.ip;
         uint32_t k = 0;  // trailing continuation bytes before this lane (a varint ending here)
 #pragma unroll
@@ -160,116 +303,55 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, int64_t w, const
         }
         tmask = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t b = dv[i];
-            const bool valid = 8u * lane + (uint32_t)i < nb;
+        for (int i = 0; i < (int)BPL; ++i) {
+            const uint32_t b = (r.i[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+            const bool valid = BPL * lane + (uint32_t)i < nb;
             acc |= (b & 0x7Fu) << (shift < 32u ? shift : 0u);
             const bool term = valid && (b & 0x80u) == 0u;
             dv[i] = term ? acc : 0u;
             tmask |= term ? (1u << i) : 0u;
+            full += dv[i];
             acc = term ? 0u : acc;
             shift = term ? 0u : shift + 7u;
         }
     }
 
-    // column entering the lane: wave prefix of the lanes' delta sums, restarted
-    // at the latest row start (a row's first delta is absolute)
-    uint32_t full = 0, head = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        full += dv[i];
-        head += (uint32_t)i < so ? dv[i] : 0u;
-    }
-    const uint32_t dsum = hs ? full - head : full;
-    const uint32_t P = wave_incl_scan(dsum), Pe = P - dsum;
-    const uint32_t Pe_s = (uint32_t)__shfl((int)Pe, spc, 64);
-    uint32_t col = sp < 0 ? r.m.carry + Pe : Pe - Pe_s;
+    // shifted column entering the lane: segmented scan of the lanes' delta
+    // sums (a lane with a row start begins from 0; the window's first
+    // segment continues from the carried column)
+    const uint32_t K = wave_seg_scan(full + ((lane == 0u && !hs) ? r.m.carry : 0u), hs ? 1u : 0u);
+    const uint32_t kprev = wave_prev_u32(K);
+    uint32_t col = hs ? 0u : (lane ? kprev : r.m.carry);
 
-    // value bytes of the lane's entries, in entry order
-    const uint32_t va = r.m.elem & 3u;
-    const uint32_t w0 = __builtin_amdgcn_alignbyte(r.v1, r.v0, va);
-    const uint32_t w1 = __builtin_amdgcn_alignbyte(r.v2, r.v1, va);
-    uint32_t q0 = w0, q1 = w1;
-    if constexpr (!FAST) {
-        const uint32_t cnt = (uint32_t)__popc(tmask);
-        const uint32_t o = wave_incl_scan(cnt) - cnt;  // entries of the window before this lane
-        vb[2u * lane] = w0;
-        vb[2u * lane + 1u] = w1;
-        wave_lds_sync();
-        const uint32_t d0 = vb[o >> 2], d1 = vb[(o >> 2) + 1u], d2 = vb[(o >> 2) + 2u];
-        q0 = __builtin_amdgcn_alignbyte(d1, d0, o & 3u);
-        q1 = __builtin_amdgcn_alignbyte(d2, d1, o & 3u);
-    }
-
-    // gather; the lane's sum restarts at the row start (the part before it
-    // closes the previous row)
-    float acc = 0.0f, hsum = 0.0f;
-    uint32_t j = 0;  // entry ordinal in the lane
+    float acc = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        if ((uint32_t)i == so) {
-            hsum = acc;
-            acc = 0.0f;
-            col = 0u;
-        }
-        col += dv[i];
+    for (int i = 0; i < (int)BPL; ++i) {
         if constexpr (FAST) {
-            float wq;
-            switch (i & 3) {
-                case 0: wq = fp4_code_hi<0>(i < 4 ? q0 : q1); break;
-                case 1: wq = fp4_code_hi<1>(i < 4 ? q0 : q1); break;
-                case 2: wq = fp4_code_hi<2>(i < 4 ? q0 : q1); break;
-                default: wq = fp4_code_hi<3>(i < 4 ? q0 : q1); break;
-            }
-            float xv;
-            if constexpr (XLDS) xv = s_x[col];
-            else xv = buffer_load_f1(rin, col * 4u) * (a.ent ? buffer_load_f1(rent, col * 4u) : 1.0f);
-            acc = __builtin_fmaf(wq, xv, acc);
+            col += (r.i[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+            acc = __builtin_fmaf(fp4_code_hi_byte(r.v[i >> 2], i), stream_x<XLDS>(a, s_x, rin, rent, col), acc);
         } else {
-            if ((tmask >> i) & 1u) {
-                const uint32_t q = (j < 4u ? q0 : q1) >> (8u * (j & 3u));
-                const float wq = fp4_code_hi<0>(q);
-                float xv;
-                if constexpr (XLDS) xv = s_x[col];
-                else xv = buffer_load_f1(rin, col * 4u) * (a.ent ? buffer_load_f1(rent, col * 4u) : 1.0f);
-                acc = __builtin_fmaf(wq, xv, acc);
-                ++j;
-            }
+            col += dv[i];
+            if ((tmask >> i) & 1u)
+                acc = __builtin_fmaf(fp4_code_hi_byte(r.v[i >> 2], i), stream_x<XLDS>(a, s_x, rin, rent, col), acc);
         }
     }
-    if constexpr (!FAST) wave_lds_sync();  // vb is rewritten by the next window
 
-    // segmented inclusive scan of the open-row sums (segments begin at row
-    // starts and at lane 0)
-    const uint64_t le = S & (lane == 63u ? ~0ull : ((2ull << lane) - 1ull));
-    const uint32_t dist = le ? lane - (uint32_t)(63 - (int)__clzll(le)) : lane;
-    float c = acc;
-#pragma unroll
-    for (uint32_t d = 1; d < 64u; d <<= 1) {
-        const float t = __shfl_up(c, d, 64);
-        c = d <= dist ? c + t : c;
-    }
-    const float cin0 = __shfl_up(c, 1, 64);
-    const float cin = lane ? cin0 : 0.0f;  // open-row sum entering this lane
-    if (hs) {
-        const float tot = cin + hsum;  // the row open before this lane's row start ends here
-        if (tot != 0.0f) atomicAdd(a.out + hrow, a.rsc ? tot * a.rsc[hrow] : tot);
-    }
-    if (lane == 63u) {
-        const uint32_t orow = hs ? srow : hrow;
-        if (c != 0.0f) atomicAdd(a.out + orow, a.rsc ? c * a.rsc[orow] : c);
-    }
+    // per-row pieces: segmented sum over the lanes of each row; the last
+    // lane of a piece adds it to the output
+    const float c = wave_seg_scan(acc, hs ? 1u : 0u);
+    const bool last = lane == 63u || ((S >> (lane + 1u)) & 1ull) != 0ull;
+    if (last && c != 0.0f) atomicAdd(a.out + row, a.rsc ? c * a.rsc[row] : c);
 }
 
 template <bool XLDS>
 __global__ __launch_bounds__(1024) void k_stream1(StreamArgs a) {
     extern __shared__ float s_x[];
     __shared__ uint32_t s_slot[MAX_WAVES][64];
-    __shared__ uint32_t s_vb[MAX_WAVES][132];
     const uint32_t nw = blockDim.x >> 6;
     const uint32_t wave = uniform(threadIdx.x >> 6);
     if constexpr (XLDS) {
-        for (uint32_t i = threadIdx.x; i < a.nx; i += blockDim.x) s_x[i] = a.ent ? a.in[i] * a.ent[i] : a.in[i];
+        for (uint32_t i = threadIdx.x; i <= a.nx; i += blockDim.x)
+            s_x[i] = i == 0u ? 0.0f : (a.ent ? a.in[i - 1u] * a.ent[i - 1u] : a.in[i - 1u]);
         __syncthreads();
     }
     const int64_t W = (int64_t)gridDim.x * nw;
@@ -278,13 +360,12 @@ __global__ __launch_bounds__(1024) void k_stream1(StreamArgs a) {
     const __amdgpu_buffer_rsrc_t rin = buffer_rsrc(a.in, XLDS ? 0u : a.nx * 4u);
     const __amdgpu_buffer_rsrc_t rent = buffer_rsrc(a.ent ? a.ent : a.in, (!XLDS && a.ent) ? a.nx * 4u : 0u);
     uint32_t *slot = s_slot[wave];
-    uint32_t *vb = s_vb[wave];
     const uint32_t lane = lane_id();
     // software pipeline: data of the next window and descriptors of the one
     // after are in flight while a window is processed
     WinRegs cur;
     cur.m = uniform_win(load_win_raw(a.win + w));
-    cur.mn = uniform_win(load_win_raw(a.win + w + 1));
+    cur.rs_hi = uniform(load_win_raw(a.win + w + 1).z);
     load_window(a, w, cur);
     uint4 nm = make_uint4(0, 0, 0, 0), nmn = make_uint4(0, 0, 0, 0);
     if (w + W < a.nwin) {
@@ -295,7 +376,7 @@ __global__ __launch_bounds__(1024) void k_stream1(StreamArgs a) {
         WinRegs nxt = cur;
         if (w + W < a.nwin) {
             nxt.m = uniform_win(nm);
-            nxt.mn = uniform_win(nmn);
+            nxt.rs_hi = uniform(nmn.z);
             load_window(a, w + W, nxt);
             if (w + 2 * W < a.nwin) {
                 nm = load_win_raw(a.win + w + 2 * W);
@@ -305,9 +386,10 @@ __global__ __launch_bounds__(1024) void k_stream1(StreamArgs a) {
         // fast decode: a whole window of one-byte varints, none continuing
         // from the window before
         const bool full = a.nbytes - (uint32_t)w * WIN_BYTES >= WIN_BYTES;
-        const bool cont = ((cur.i0 | cur.i1) & 0x80808080u) != 0u || (lane == 0u && (cur.ip & 0x80000000u) != 0u);
-        if (full && __ballot(cont) == 0ull) run_window<XLDS, true>(a, w, cur, slot, vb, s_x, rin, rent);
-        else run_window<XLDS, false>(a, w, cur, slot, vb, s_x, rin, rent);
+        const bool cont = ((cur.i[0] | cur.i[1] | cur.i[2] | cur.i[3]) & 0x80808080u) != 0u ||
+                          (lane == 0u && (cur.ip & 0x80000000u) != 0u);
+        if (full && __ballot(cont) == 0ull) run_window<XLDS, true>(a, w, cur, slot, s_x, rin, rent);
+        else run_window<XLDS, false>(a, w, cur, slot, s_x, rin, rent);
         cur = nxt;
     }
 }
@@ -367,10 +449,10 @@ int stream_occupancy(bool xl, unsigned nt, uint32_t lds) {
 // larger than what is resident at once; XLDS when the input fits in LDS and
 // staging it (input and column scale) costs at most half of a block's share
 // of the stream (index + value bytes).
-StreamShape stream_shape(const GatherPlan &p) {
+StreamShape stream_shape(int64_t nwin, int64_t nx) {
     static const int force = env_int("SILI_STREAM_XLDS", -1);  // -1 auto, 0 off, 1 on when it fits
-    const int64_t static_lds = (int64_t)MAX_WAVES * (64 + 132) * 4;
-    const int64_t xbytes = p.cols * 4;
+    const int64_t static_lds = (int64_t)MAX_WAVES * 64 * 4;
+    const int64_t xbytes = (nx + 1) * 4;
     const bool fits = xbytes + static_lds <= max_lds_per_block();
     StreamShape best{256, 1, false, 0};
     int best_waves = -1;
@@ -381,10 +463,10 @@ StreamShape stream_shape(const GatherPlan &p) {
             const int per_cu = stream_occupancy(xl, nt, lds);
             if (per_cu <= 0) continue;
             const int64_t resident = (int64_t)per_cu * num_cus();
-            const int64_t need = (p.nwin + nt / 64 - 1) / (nt / 64);
+            const int64_t need = (nwin + nt / 64 - 1) / (nt / 64);
             const unsigned grid = (unsigned)std::max<int64_t>(1, std::min(resident, need));
             if (xl) {
-                const bool auto_ok = 2 * xbytes * (int64_t)grid <= p.nwin * (int64_t)WIN_BYTES;
+                const bool auto_ok = 2 * xbytes * (int64_t)grid <= nwin * (int64_t)WIN_BYTES;
                 if (force == 0 || (force < 0 && !auto_ok)) continue;
             }
             const int waves = per_cu * (int)(nt / 64);
@@ -400,28 +482,84 @@ StreamShape stream_shape(const GatherPlan &p) {
     return best;
 }
 
-}  // namespace
-
-// SILI_B1_STREAM (read at every call): 0 never, 1 (default) for stores of
-// at least 2048 windows (1 MiB of index bytes: below that one pass of the
-// machine covers the store and the segment kernels, which need no output
-// fill, finish first), 2 whenever the store allows.
-bool gather_stream_used(const GatherPlan &p, const ScaleView &sc, int64_t nb, int64_t in_ld, int skip) {
-    if (nb != 1) return false;
-    const int mode = env_int("SILI_B1_STREAM", 1);
-    if (mode == 0 || (mode == 1 && p.nwin < 2048)) return false;
-    return nb == 1 && p.stream_ok && p.nwin > 0 && skip == SKIP_NONE && sc.rank == 1 && in_ld == 1 &&
-           p.cols * 4 < (int64_t(1) << 31);
+// Build s.stream from s (device work on L's stream; synchronous).
+void build_stream(Layer &L, DScatter &s) {
+    hipStream_t st = L.stream;
+    DStream &d = s.stream;
+    const int64_t rows = s.rows;
+    DevBuf<uint32_t> len, pstart, ne, nepos;
+    len.ensure((size_t)rows + 1);
+    pstart.ensure((size_t)rows + 1);
+    ne.ensure((size_t)rows + 1);
+    nepos.ensure((size_t)rows + 1);
+    launch(k_sp_len, dim3(nblk(rows + 1)), dim3(TPB), 0, st, (const uint32_t *)s.byte_start.p,
+           (const uint8_t *)s.idx.p, rows, len.p, ne.p);
+    SILI_HIP(hipGetLastError());
+    device_exclusive_scan_u32(L, len.p, pstart.p, rows + 1);
+    device_exclusive_scan_u32(L, ne.p, nepos.p, rows + 1);
+    uint32_t tot[2] = {0, 0};
+    SILI_HIP(hipMemcpyAsync(&tot[0], pstart.p + rows, 4, hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipMemcpyAsync(&tot[1], nepos.p + rows, 4, hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipStreamSynchronize(st));
+    // the padded stream must keep 32-bit offsets below 2^31 (buffer loads);
+    // the padded lengths are summed in 32 bits, so bound them by the source
+    if ((uint64_t)s.nbytes + 16ull * (uint64_t)rows + 2 * WIN_BYTES >= (1ull << 31)) {
+        d.failed = true;
+        return;
+    }
+    const int64_t nbytes = tot[0], n_ne = tot[1];
+    const int64_t nwin = (nbytes + WIN_BYTES - 1) / WIN_BYTES;
+    d.idx.ensure((size_t)nbytes + WIN_BYTES);
+    d.val.ensure((size_t)nbytes + WIN_BYTES);
+    d.ne_row.ensure((size_t)n_ne + 1);
+    d.ne_start.ensure((size_t)n_ne + 1);
+    d.win.ensure((size_t)nwin + 1);
+    SILI_HIP(hipMemsetAsync(d.idx.p, 0, (size_t)nbytes + WIN_BYTES, st));
+    SILI_HIP(hipMemsetAsync(d.val.p, 0, (size_t)nbytes + WIN_BYTES, st));
+    launch(k_sp_ne, dim3(nblk(rows + 1)), dim3(TPB), 0, st, (const uint32_t *)ne.p, (const uint32_t *)nepos.p,
+           (const uint32_t *)pstart.p, rows, d.ne_row.p, d.ne_start.p);
+    if (rows > 0)
+        launch(k_sp_copy, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, (const uint32_t *)s.byte_start.p,
+               (const uint32_t *)s.elem_start.p, (const uint8_t *)s.idx.p, (const uint8_t *)s.val.p,
+               (const uint32_t *)pstart.p, rows, d.idx.p, d.val.p, d.win.p);
+    launch(k_sp_rs, dim3(nblk(nwin + 1)), dim3(TPB), 0, st, (const uint32_t *)d.ne_start.p, n_ne, nwin, rows,
+           d.win.p);
+    SILI_HIP(hipGetLastError());
+    SILI_HIP(hipStreamSynchronize(st));
+    d.nbytes = nbytes;
+    d.nwin = nwin;
+    d.n_ne = n_ne;
+    d.valid = true;
 }
 
-void launch_gather_stream(const GatherPlan &p, const ScaleView &sc, const float *in, float *out, hipStream_t st) {
+}  // namespace
+
+bool stream_wanted(const DScatter &s, const ScaleView &sc, int64_t nb, int64_t in_ld, int skip) {
+    if (nb != 1 || s.nnz == 0 || s.stream.failed) return false;
+    // SILI_B1_STREAM (read at every call): 0 never, 1 (default) for stores of
+    // at least 1 MiB of index bytes (below that one pass of the machine covers
+    // the store and the segment kernels, which need no output fill, finish
+    // first), 2 whenever the store allows
+    const int mode = env_int("SILI_B1_STREAM", 1);
+    if (mode == 0 || (mode == 1 && s.nbytes < (int64_t(1) << 20))) return false;
+    return skip == SKIP_NONE && sc.rank == 1 && in_ld == 1 && s.cols + 1 < (int64_t(1) << 29) &&
+           (uint64_t)s.nbytes + 16ull * (uint64_t)s.rows + 2 * WIN_BYTES < (1ull << 31);
+}
+
+void stream_gather(Layer &L, DScatter &s, const ScaleView &sc, const float *in, float *out, hipStream_t st) {
+    if (!s.stream.valid) {
+        build_stream(L, s);
+        if (!s.stream.valid) throw_error(3, "stream copy exceeds 2 GiB");
+    }
+    const DStream &d = s.stream;
     {
         ProfScope ps("stream_zero", st);
-        launch(k_fill0, dim3((unsigned)((p.rows + 255) / 256)), dim3(256), 0, st, out, p.rows);
+        launch(k_fill0, dim3((unsigned)((s.rows + 255) / 256)), dim3(256), 0, st, out, s.rows);
     }
-    StreamArgs a{p.win, p.nwin, p.idx, p.val, p.byte_start, (uint32_t)p.nbytes, (uint32_t)p.nnz,
-                 in, sc.ent, sc.row, (uint32_t)p.cols, out};
-    const StreamShape sh = stream_shape(p);
+    if (d.nwin == 0) return;
+    StreamArgs a{d.win.p, d.nwin, d.idx.p, d.val.p, d.ne_row.p, d.ne_start.p, (uint32_t)d.nbytes,
+                 in, sc.ent, sc.row, (uint32_t)s.cols, out};
+    const StreamShape sh = stream_shape(d.nwin, s.cols);
     if (sh.xlds) {
         ProfScope ps("stream_lds", st);
         launch(k_stream1<true>, dim3(sh.grid), dim3(sh.threads), sh.lds, st, a);

@@ -44,6 +44,58 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x) {
     return x;
 }
 
+// Segmented inclusive scans over the 64 lanes: f != 0 marks the first lane of
+// a segment (lane 0 always begins one).  The wave_incl_scan ladder with the
+// operator (a, fa) . (b, fb) = (fb ? b : a + b, fa | fb) (lanes outside a
+// DPP row read the identity (0, 0)).
+template <int CTRL, int RM>
+__device__ __forceinline__ void seg_step(float &v, uint32_t &f) {
+    const float t = dpp_f32<CTRL, RM>(v);
+    const uint32_t tf = dpp_u32<CTRL, RM>(f);
+    v = f ? v : v + t;
+    f |= tf;
+}
+template <int CTRL, int RM>
+__device__ __forceinline__ void seg_step(uint32_t &v, uint32_t &f) {
+    const uint32_t t = dpp_u32<CTRL, RM>(v);
+    const uint32_t tf = dpp_u32<CTRL, RM>(f);
+    v = f ? v : v + t;
+    f |= tf;
+}
+template <typename T>
+__device__ __forceinline__ T wave_seg_scan(T v, uint32_t f) {
+    seg_step<DPP_ROW_SHR1, 0xF>(v, f);
+    seg_step<DPP_ROW_SHR2, 0xF>(v, f);
+    seg_step<DPP_ROW_SHR4, 0xF>(v, f);
+    seg_step<DPP_ROW_SHR8, 0xF>(v, f);
+    seg_step<DPP_ROW_BCAST15, 0xA>(v, f);
+    seg_step<DPP_ROW_BCAST31, 0xC>(v, f);
+    return v;
+}
+// Inclusive running maximum over the lanes.
+__device__ __forceinline__ uint32_t wave_max_scan(uint32_t x) {
+    x = max(x, dpp_u32<DPP_ROW_SHR1>(x));
+    x = max(x, dpp_u32<DPP_ROW_SHR2>(x));
+    x = max(x, dpp_u32<DPP_ROW_SHR4>(x));
+    x = max(x, dpp_u32<DPP_ROW_SHR8>(x));
+    x = max(x, dpp_u32<DPP_ROW_BCAST15, 0xA>(x));
+    x = max(x, dpp_u32<DPP_ROW_BCAST31, 0xC>(x));
+    return x;
+}
+// Bitwise OR over all 64 lanes (wave-uniform result).
+__device__ __forceinline__ uint32_t wave_or_all(uint32_t x) {
+    x |= dpp_u32<DPP_ROW_SHR1>(x);
+    x |= dpp_u32<DPP_ROW_SHR2>(x);
+    x |= dpp_u32<DPP_ROW_SHR4>(x);
+    x |= dpp_u32<DPP_ROW_SHR8>(x);
+    x |= dpp_u32<DPP_ROW_BCAST15, 0xA>(x);
+    x |= dpp_u32<DPP_ROW_BCAST31, 0xC>(x);
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+// Value of the previous lane (lane 0 reads 0): DPP wave_shr:1.
+__device__ __forceinline__ uint32_t wave_prev_u32(uint32_t x) { return dpp_u32<0x138>(x); }
+__device__ __forceinline__ float wave_prev_f32(float x) { return dpp_f32<0x138>(x); }
+
 // Sum over each aligned group of BL lanes (BL a power of two <= 64); the
 // group's total lands in its last lane (lane % BL == BL-1).
 template <int BL>

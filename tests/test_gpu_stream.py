@@ -1,15 +1,18 @@
-"""GPU: the batch-1 byte-split ("stream") gather against the CPU oracle.
+"""GPU: the batch-1 stream gather (a padded copy of the store cut into
+1024-byte windows) against the CPU oracle.
 
-The stream kernels cut a store's index stream into 512-byte windows, place
-rows on the lanes holding their first byte and combine per-row pieces with
-a segmented wave scan.  The layers here are built to hit what that design
-has to get right: row starts at every byte offset of a lane, rows spanning
-many windows, rows shorter than a window, empty rows, multi-byte deltas
-(general decode), a partial last window and an exactly full one, row scales
-on both sides, and non-finite inputs.  Stores outside the kernels' limits
-(a row of 1-7 index bytes, 64 row starts in one window) must fall back to
-the segment kernels.  The launcher's kernel choice is read back from the
-per-kernel profiler, so each variant is known to have run."""
+The stream copy puts every row on a 16-byte boundary (zero-delta padding
+entries in front, columns shifted by one so that column 0 reads a zero
+input) and lays the value bytes out parallel to the index bytes; the kernel
+places rows on lanes and combines per-row pieces with a segmented wave scan.
+The layers here are built to hit what that design has to get right: rows of
+every length from 1 entry up, empty rows (many of them in one window), rows
+spanning many windows, multi-byte deltas (general decode) including a first
+delta whose encoding grows with the column shift (127 -> 128), a partial
+last window and an exactly full one, row scales on both sides, and
+non-finite inputs.  Layers with non-finite weights keep the segment kernels.
+The launcher's kernel choice is read back from the per-kernel profiler, so
+each variant is known to have run."""
 import ctypes as C
 
 import numpy as np
@@ -36,20 +39,23 @@ def row_bytes(cols):
     return n
 
 
-def mixed_rows(n_out, seed, total_mod512=None):
-    """Rows of 0 and 8..2900 entries, random columns (mixed delta lengths),
-    plus a final run of consecutive columns sized so that the stream length
-    mod 512 is `total_mod512` when given."""
+def mixed_rows(n_out, seed, total_mod=None):
+    """Rows of 0 and 1..2900 entries, random columns (mixed delta lengths),
+    rows whose first column is 127 (its shifted encoding needs 2 bytes), plus
+    a final run of consecutive columns sized so that the stream length mod
+    1024 is `total_mod` when given (the unpadded store's length)."""
     rng = np.random.default_rng(seed)
-    lens = [0, 8, 9, 10, 11, 12, 13, 14, 15, 16, 0, 17, 20, 33, 64, 65, 127, 128, 129, 300, 0,
-            505, 506, 507, 508, 509, 510, 511, 512, 513, 514, 700, 1023, 1500, 2900]
-    lens += list(rng.integers(8, 600, size=60))
+    lens = [0, 1, 2, 3, 5, 7, 8, 15, 16, 17, 0, 0, 31, 33, 64, 65, 127, 128, 129, 300, 0,
+            505, 506, 507, 508, 509, 510, 511, 512, 513, 514, 700, 1020, 1021, 1022, 1023, 1024,
+            1025, 1026, 1027, 1500, 2047, 2048, 2049, 2900]
+    lens += list(rng.integers(1, 1200, size=60))
     rng.shuffle(lens)
     rows = [np.sort(rng.choice(n_out, size=min(int(n), n_out), replace=False)) for n in lens]
-    if total_mod512 is not None:
+    rows += [np.arange(127, 127 + k) for k in (1, 3, 20)]
+    if total_mod is not None:
         tot = sum(row_bytes(r) for r in rows)
         k = 16
-        while (tot + k) % 512 != total_mod512:
+        while (tot + k) % 1024 != total_mod:
             k += 1
         rows.append(np.arange(k))  # k one-byte deltas
     return rows
@@ -121,38 +127,39 @@ def check_bwd(H, L, x, g, what):
     assert_close_terms(dx, H.backward_dense(x, g)[0], H.backward_dense(x, g, absmode=True)[0], what)
 
 
-def test_mixed_rows_encode_with_stream_limits():
-    """CPU check of the designed layers: every non-empty row has >= 8 index
-    bytes; the requested stream lengths mod 512 are met."""
+def test_mixed_rows_design():
+    """CPU check of the designed layers: the requested stream lengths mod
+    1024 are met and short, empty and 127-first rows are present."""
     for mod in (None, 0, 37):
         rows = mixed_rows(3000, 1, mod)
         nb = [row_bytes(r) for r in rows]
-        assert all(b == 0 or b >= 8 for b in nb)
+        assert min(nb) == 0 and any(0 < b < 16 for b in nb)
+        assert any(len(r) and r[0] == 127 for r in rows)
         if mod is not None:
-            assert sum(nb) % 512 == mod
+            assert sum(nb) % 1024 == mod
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("mod", [None, 0, 1, 511])
+@pytest.mark.parametrize("mod", [None, 0, 1, 1023])
 def test_stream_canonical_and_shadow(hip, mod):
     n_out = 3000
     rows = mixed_rows(n_out, 2 + (mod or 0), mod)
     # canonical orientation: dx = W^T g at batch 1 gathers the designed rows
     H, L = make_pair(hip, rows, n_out)
-    assert L.info()["stream_canonical"]
     rng = np.random.default_rng(9)
     x = rng.normal(size=(1, len(rows))).astype(np.float32)
     g = rng.normal(size=(1, n_out)).astype(np.float32)
     names = kernels_run(hip, L, lambda: check_bwd(H, L, x, g, f"dx mod{mod}"))
     assert any(n.startswith("bwd:stream") for n in names), names
+    assert L.info()["stream_canonical"]
     check_fwd(H, L, x, f"fwd mod{mod}")
     # shadow orientation: the transposed layer's forward gathers them
     T = transpose_rows(rows, n_out)
     HT, LT = make_pair(hip, T, len(rows))
-    assert LT.info()["stream_shadow"]
     xt = rng.normal(size=(1, n_out)).astype(np.float32)
     names = kernels_run(hip, LT, lambda: check_fwd(HT, LT, xt, f"T fwd mod{mod}"))
     assert any(n.startswith("fwd:stream") for n in names), names
+    assert LT.info()["stream_shadow"]
     # a second call must not see the first call's output
     check_fwd(HT, LT, xt * 0.5, f"T fwd again mod{mod}")
 
@@ -171,23 +178,47 @@ def test_stream_nonfinite_inputs(hip):
 
 
 @pytest.mark.gpu
-def test_stream_limits_fall_back(hip):
-    # a row of 7 one-byte deltas: the stream kernels are not used
-    rows = [np.arange(0, 40), np.arange(3, 10), np.arange(100, 180)]
-    H, L = make_pair(hip, rows, 200)
-    assert not L.info()["stream_canonical"]
-    x = np.random.default_rng(2).normal(size=(1, 3)).astype(np.float32)
-    g = np.random.default_rng(3).normal(size=(1, 200)).astype(np.float32)
-    names = kernels_run(hip, L, lambda: check_bwd(H, L, x, g, "short-row dx"))
+def test_stream_short_and_empty_rows(hip):
+    """Rows of 1-20 entries, with runs of empty rows longer than a window
+    holds lanes, and single-entry rows at column 0 and at the last column."""
+    rng = np.random.default_rng(4)
+    rows = []
+    for r in range(3000):
+        k = r % 23
+        if k >= 21 or (500 <= r < 700):
+            rows.append(np.zeros(0, np.int64))
+        else:
+            rows.append(np.sort(rng.choice(900, size=k, replace=False)))
+    rows[10] = np.array([0])
+    rows[11] = np.array([899])
+    H, L = make_pair(hip, rows, 900)
+    x = rng.normal(size=(1, len(rows))).astype(np.float32)
+    g = rng.normal(size=(1, 900)).astype(np.float32)
+    names = kernels_run(hip, L, lambda: check_bwd(H, L, x, g, "short rows dx"))
+    assert any(n.startswith("bwd:stream") for n in names), names
+
+
+@pytest.mark.gpu
+def test_stream_not_used_with_nonfinite_weights(hip):
+    """An infinite row scale (non-finite weights) needs the reference's skip
+    of zero inputs: the segment kernels run."""
+    rows = mixed_rows(2000, 5)
+    T = transpose_rows(rows, 2000)
+    n_in = len(T)
+    ptrs = np.concatenate([[0], np.cumsum([len(r) for r in T])]).astype(np.int32)
+    cols = np.concatenate(T).astype(np.int32)
+    w = np.random.default_rng(2).normal(size=len(cols)).astype(np.float32)
+    q, s = per_row_quantize(ptrs, w, n_in)
+    s[7] = np.inf
+    H = HostLayer(n_in, len(rows)).load_csr(ptrs, cols, w=q).set_scales(s)
+    L = hip.SparseLinearLayer(n_in, len(rows), len(cols))
+    L.load_weights(ptrs, cols, q)
+    L.set_value_scales(s)
+    x = np.random.default_rng(3).normal(size=(1, n_in)).astype(np.float32)
+    x[0, ::7] = 0.0
+    names = kernels_run(hip, L, lambda: check_fwd(H, L, x, "inf scale fwd"))
+    assert L.info()["has_nonfinite"]  # (scales reach the device with the call)
     assert not any("stream" in n for n in names), names
-    # 64 rows of 8 one-byte deltas start in one window: fallback; 9 bytes: stream
-    for width, ok in ((8, False), (9, True)):
-        rows = [np.arange(width) + r % 100 for r in range(200)]
-        H, L = make_pair(hip, rows, 1000)
-        assert L.info()["stream_canonical"] == ok
-        x = np.random.default_rng(width).normal(size=(1, 200)).astype(np.float32)
-        g = np.random.default_rng(width + 1).normal(size=(1, 1000)).astype(np.float32)
-        check_bwd(H, L, x, g, f"rows of {width} bytes")
 
 
 @pytest.mark.gpu
@@ -201,7 +232,6 @@ def test_stream_lds_and_global_variants(hip):
         ex = L.export_scattered()
         H = HostLayer(n_in, n_out).load_encoded(ex["row_byte_start"], ex["row_elem_start"], ex["idx"], ex["val"])
         H.set_scales(np.asarray(L.get_value_scales(), np.float32))
-        assert L.info()["stream_shadow"]
         x = np.random.default_rng(n_in).normal(size=(1, n_in)).astype(np.float32)
         names = kernels_run(hip, L, lambda: check_fwd(H, L, x, f"synthetic {n_in}x{n_out}"))
         seen |= {n for n in names if "stream" in n}
