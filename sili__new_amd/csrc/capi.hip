@@ -245,7 +245,7 @@ void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st
     if (L.Wt.nnz == 0) {
         fill(y, B * L.n_out, 0.0f, st);
     } else if (stream_wanted(L.Wt, ssc, B, B, skip)) {
-        stream_gather(L, L.Wt, ssc, xT, y, st);
+        stream_gather(L, L.Wt, ssc, xT, B, y, L.n_out, st);
     } else {
         launch_zero_split_rows(L.Wt.plan(), y, L.n_out, B, st);
         launch_gather(L.Wt.plan(), ssc, xT, B, y, L.n_out, B, skip, st);
@@ -279,13 +279,15 @@ void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float 
         if (xT) launch_rowabs(xT, B, L.n_in, L.acc_in.p, st);
         else launch_colabs(x, B, L.n_in, L.acc_in.p, st);
     }
-    const bool str = scat && stream_wanted(L.W, canon_scales(L), B, B, SKIP_NONE);
+    // grad-input and grad-W read the same gT row per synapse: one fused pass
+    // when grad-W is wanted; otherwise the stream kernels (small batches) or
+    // the segment gather
+    const bool str = scat && !gw_s && stream_wanted(L.W, canon_scales(L), B, B, SKIP_NONE);
     if (!scat) fill(dx, B * L.n_in, 0.0f, st);
     else if (!str) launch_zero_split_rows(L.W.plan(), dx, L.n_in, B, st);
-    // grad-input and grad-W read the same gT row per synapse: one fused pass
     const bool fused = scat && gw_s &&
                        launch_bwd_fused(L.W.plan(), canon_scales(L), gT, xT, B, dx, L.n_in, gw_s, L.acc_in.p, st);
-    if (str) stream_gather(L, L.W, canon_scales(L), gT, dx, st);
+    if (str) stream_gather(L, L.W, canon_scales(L), gT, B, dx, L.n_in, st);
     else if (scat && !fused) launch_gather(L.W.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
     if (L.B4.ntiles > 0)
         launch_gather_b4(L.B4.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);

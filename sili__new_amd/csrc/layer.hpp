@@ -181,13 +181,15 @@ void device_sort_pairs_u64(Layer &L, const uint64_t *kin, uint64_t *kout, const 
                            uint32_t *vout, int64_t n, int bits);
 
 // ---- batch-1 stream kernels (stream.hip) ---------------------------------------
-// Whether stream_gather serves this call (batch 1, no skip rule, rank-1
-// scales, contiguous input; SILI_B1_STREAM: 0 never, 1 stores of >= 1 MiB of
-// index bytes (default), 2 always).
+// Whether stream_gather serves this call (batch 1, 2, 4 or 8 with the input
+// feature-major and unpadded, no skip rule, rank-1 scales; SILI_B1_STREAM:
+// 0 never, 1 stores of >= 1 MiB of index bytes (default), 2 always).
 bool stream_wanted(const DScatter &s, const ScaleView &sc, int64_t nb, int64_t in_ld, int skip);
-// out[row] = sum_e dec(code_e) * S(row, col_e) * in[col_e] for every row of s
-// (zeroes out first; builds s.stream on first use).
-void stream_gather(Layer &L, DScatter &s, const ScaleView &sc, const float *in, float *out, hipStream_t st);
+// out[b*out_ld + row] = sum_e dec(code_e) * S(row, col_e) * in[col_e*B + b]
+// for every row of s and b < B (zeroes out first; builds s.stream on first
+// use).
+void stream_gather(Layer &L, DScatter &s, const ScaleView &sc, const float *in, int64_t B, float *out,
+                   int64_t out_ld, hipStream_t st);
 
 // ---- seeded synthetic layers (gen.hip) ----------------------------------------
 // Rebuilds the scattered store (and its shadow) from the seeded generator and

@@ -181,11 +181,13 @@ struct StreamArgs {
     const uint8_t *idx, *val;    // padded stream
     const uint32_t *ne_row, *ne_start;
     uint32_t nbytes;
-    const float *in;             // in[c], c < nx
+    const float *in;             // in[c * in_ld + j], c < nx, j < NB (this pass)
+    uint32_t in_ld;
     const float *ent;            // column scale (NULL: ones)
     const float *rsc;            // row scale (NULL: ones)
     uint32_t nx;
-    float *out;                  // out[row], zeroed beforehand
+    float *out;                  // out[j * out_ld + row], zeroed beforehand
+    int64_t out_ld;
 };
 
 // Registers of one window: its descriptor and the next one's rs_lo, the
@@ -244,19 +246,83 @@ __device__ __forceinline__ float fp4_code_hi_byte(uint32_t dw, int k) {
     }
 }
 
-// x at shifted column c (0: the zero slot)
-template <bool XLDS>
-__device__ __forceinline__ float stream_x(const StreamArgs &a, const float *s_x, __amdgpu_buffer_rsrc_t rin,
-                                          __amdgpu_buffer_rsrc_t rent, uint32_t c) {
+template <int NB>
+struct XVec {
+    float v[NB];
+};
+
+// The NB inputs at shifted column c (0: the zero slot).  XLDS: slot c holds
+// NB floats; otherwise buffer loads of in[(c - 1) * in_ld + j] (c = 0 wraps
+// out of range and reads 0).
+template <int NB, bool XLDS>
+__device__ __forceinline__ XVec<NB> stream_x(const StreamArgs &a, const float *s_x, __amdgpu_buffer_rsrc_t rin,
+                                             __amdgpu_buffer_rsrc_t rent, uint32_t c) {
+    XVec<NB> x;
     if constexpr (XLDS) {
-        return s_x[c];
+        const float *p = s_x + c * NB;
+        if constexpr (NB == 1) {
+            x.v[0] = p[0];
+        } else if constexpr (NB == 2) {
+            const float2 t = *reinterpret_cast<const float2 *>(p);
+            x.v[0] = t.x;
+            x.v[1] = t.y;
+        } else {
+#pragma unroll
+            for (int q = 0; q < NB / 4; ++q) {
+                const float4 t = reinterpret_cast<const float4 *>(p)[q];
+                x.v[4 * q] = t.x;
+                x.v[4 * q + 1] = t.y;
+                x.v[4 * q + 2] = t.z;
+                x.v[4 * q + 3] = t.w;
+            }
+        }
     } else {
-        const uint32_t off = c * 4u - 4u;  // c = 0: out of range, reads 0
-        return buffer_load_f1(rin, off) * (a.ent ? buffer_load_f1(rent, off) : 1.0f);
+        const uint32_t off = (c - 1u) * a.in_ld * 4u;
+        if constexpr (NB >= 4) {
+#pragma unroll
+            for (int q = 0; q < NB / 4; ++q) {
+                const float4 t = buffer_load_f4(rin, off + 16u * (uint32_t)q);
+                x.v[4 * q] = t.x;
+                x.v[4 * q + 1] = t.y;
+                x.v[4 * q + 2] = t.z;
+                x.v[4 * q + 3] = t.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) x.v[j] = buffer_load_f1(rin, off + 4u * (uint32_t)j);
+        }
+        if (a.ent) {
+            const float e = buffer_load_f1(rent, (c - 1u) * 4u);
+#pragma unroll
+            for (int j = 0; j < NB; ++j) x.v[j] *= e;
+        }
     }
+    return x;
 }
 
-template <bool XLDS, bool FAST>
+// Segmented inclusive scan of NB values sharing one flag ladder (see
+// wave_seg_scan).
+template <int NB, int CTRL, int RM>
+__device__ __forceinline__ void seg_step_n(float (&v)[NB], uint32_t &f) {
+    const uint32_t tf = dpp_u32<CTRL, RM>(f);
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const float t = dpp_f32<CTRL, RM>(v[j]);
+        v[j] = f ? v[j] : v[j] + t;
+    }
+    f |= tf;
+}
+template <int NB>
+__device__ __forceinline__ void wave_seg_scan_n(float (&v)[NB], uint32_t f) {
+    seg_step_n<NB, DPP_ROW_SHR1, 0xF>(v, f);
+    seg_step_n<NB, DPP_ROW_SHR2, 0xF>(v, f);
+    seg_step_n<NB, DPP_ROW_SHR4, 0xF>(v, f);
+    seg_step_n<NB, DPP_ROW_SHR8, 0xF>(v, f);
+    seg_step_n<NB, DPP_ROW_BCAST15, 0xA>(v, f);
+    seg_step_n<NB, DPP_ROW_BCAST31, 0xC>(v, f);
+}
+
+template <int NB, bool XLDS, bool FAST>
 __device__ __forceinline__ void run_window(const StreamArgs &a, int64_t w, const WinRegs &r, uint32_t *slot,
                                            const float *s_x, __amdgpu_buffer_rsrc_t rin,
                                            __amdgpu_buffer_rsrc_t rent) {
@@ -323,41 +389,50 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, int64_t w, const
     const uint32_t kprev = wave_prev_u32(K);
     uint32_t col = hs ? 0u : (lane ? kprev : r.m.carry);
 
-    float acc = 0.0f;
+    float acc[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[j] = 0.0f;
 #pragma unroll
     for (int i = 0; i < (int)BPL; ++i) {
-        if constexpr (FAST) {
-            col += (r.i[i >> 2] >> (8 * (i & 3))) & 0xFFu;
-            acc = __builtin_fmaf(fp4_code_hi_byte(r.v[i >> 2], i), stream_x<XLDS>(a, s_x, rin, rent, col), acc);
-        } else {
-            col += dv[i];
-            if ((tmask >> i) & 1u)
-                acc = __builtin_fmaf(fp4_code_hi_byte(r.v[i >> 2], i), stream_x<XLDS>(a, s_x, rin, rent, col), acc);
+        if constexpr (FAST) col += (r.i[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+        else col += dv[i];
+        if (FAST || ((tmask >> i) & 1u)) {
+            const float wq = fp4_code_hi_byte(r.v[i >> 2], i);
+            const XVec<NB> x = stream_x<NB, XLDS>(a, s_x, rin, rent, col);
+#pragma unroll
+            for (int j = 0; j < NB; ++j) acc[j] = __builtin_fmaf(wq, x.v[j], acc[j]);
         }
     }
 
-    // per-row pieces: segmented sum over the lanes of each row; the last
-    // lane of a piece adds it to the output
-    const float c = wave_seg_scan(acc, hs ? 1u : 0u);
+    // per-row pieces: segmented sums over the lanes of each row; the last
+    // lane of a piece adds them to the output
+    wave_seg_scan_n<NB>(acc, hs ? 1u : 0u);
     const bool last = lane == 63u || ((S >> (lane + 1u)) & 1ull) != 0ull;
-    if (last && c != 0.0f) atomicAdd(a.out + row, a.rsc ? c * a.rsc[row] : c);
+    if (last) {
+        const float rs = a.rsc ? a.rsc[row] : 1.0f;
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+            if (acc[j] != 0.0f) atomicAdd(a.out + (int64_t)j * a.out_ld + row, a.rsc ? acc[j] * rs : acc[j]);
+    }
 }
 
-template <bool XLDS>
-__global__ __launch_bounds__(1024) void k_stream1(StreamArgs a) {
+template <int NB, bool XLDS>
+__global__ __launch_bounds__(NB >= 4 ? 512 : 1024) void k_stream(StreamArgs a) {
     extern __shared__ float s_x[];
     __shared__ uint32_t s_slot[MAX_WAVES][64];
     const uint32_t nw = blockDim.x >> 6;
     const uint32_t wave = uniform(threadIdx.x >> 6);
     if constexpr (XLDS) {
-        for (uint32_t i = threadIdx.x; i <= a.nx; i += blockDim.x)
-            s_x[i] = i == 0u ? 0.0f : (a.ent ? a.in[i - 1u] * a.ent[i - 1u] : a.in[i - 1u]);
+        for (uint32_t i = threadIdx.x; i < (a.nx + 1u) * NB; i += blockDim.x) {
+            const uint32_t c = i / NB, j = i % NB;
+            s_x[i] = c == 0u ? 0.0f : (a.ent ? a.in[(c - 1u) * a.in_ld + j] * a.ent[c - 1u] : a.in[(c - 1u) * a.in_ld + j]);
+        }
         __syncthreads();
     }
     const int64_t W = (int64_t)gridDim.x * nw;
     int64_t w = (int64_t)blockIdx.x * nw + wave;
     if (w >= a.nwin) return;
-    const __amdgpu_buffer_rsrc_t rin = buffer_rsrc(a.in, XLDS ? 0u : a.nx * 4u);
+    const __amdgpu_buffer_rsrc_t rin = buffer_rsrc(a.in, XLDS ? 0u : a.nx * a.in_ld * 4u);
     const __amdgpu_buffer_rsrc_t rent = buffer_rsrc(a.ent ? a.ent : a.in, (!XLDS && a.ent) ? a.nx * 4u : 0u);
     uint32_t *slot = s_slot[wave];
     const uint32_t lane = lane_id();
@@ -388,8 +463,8 @@ __global__ __launch_bounds__(1024) void k_stream1(StreamArgs a) {
         const bool full = a.nbytes - (uint32_t)w * WIN_BYTES >= WIN_BYTES;
         const bool cont = ((cur.i[0] | cur.i[1] | cur.i[2] | cur.i[3]) & 0x80808080u) != 0u ||
                           (lane == 0u && (cur.ip & 0x80000000u) != 0u);
-        if (full && __ballot(cont) == 0ull) run_window<XLDS, true>(a, w, cur, slot, s_x, rin, rent);
-        else run_window<XLDS, false>(a, w, cur, slot, s_x, rin, rent);
+        if (full && __ballot(cont) == 0ull) run_window<NB, XLDS, true>(a, w, cur, slot, s_x, rin, rent);
+        else run_window<NB, XLDS, false>(a, w, cur, slot, s_x, rin, rent);
         cur = nxt;
     }
 }
@@ -397,6 +472,20 @@ __global__ __launch_bounds__(1024) void k_stream1(StreamArgs a) {
 __global__ __launch_bounds__(256) void k_fill0(float *__restrict__ p, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i < n) p[i] = 0.0f;
+}
+
+using StreamKernel = void (*)(StreamArgs);
+template <int NB>
+StreamKernel stream_kernel(bool xl) {
+    return xl ? k_stream<NB, true> : k_stream<NB, false>;
+}
+StreamKernel stream_kernel(int nb, bool xl) {
+    switch (nb) {
+        case 1: return stream_kernel<1>(xl);
+        case 2: return stream_kernel<2>(xl);
+        case 4: return stream_kernel<4>(xl);
+        default: return stream_kernel<8>(xl);
+    }
 }
 
 struct StreamShape {
@@ -424,18 +513,17 @@ int max_lds_per_block() {
     return n;
 }
 
-// Resident blocks per CU of k_stream1<xl> at nt threads and `lds` bytes of
+// Resident blocks per CU of a stream kernel at nt threads and `lds` bytes of
 // dynamic LDS (cached: the occupancy query is a host computation).
-int stream_occupancy(bool xl, unsigned nt, uint32_t lds) {
+int stream_occupancy(StreamKernel k, unsigned nt, uint32_t lds) {
     static std::mutex mu;
-    static std::map<std::tuple<bool, unsigned, uint32_t>, int> cache;
+    static std::map<std::tuple<const void *, unsigned, uint32_t>, int> cache;
     std::lock_guard<std::mutex> g(mu);
-    const auto key = std::make_tuple(xl, nt, lds);
+    const void *f = reinterpret_cast<const void *>(k);
+    const auto key = std::make_tuple(f, nt, lds);
     const auto it = cache.find(key);
     if (it != cache.end()) return it->second;
-    const void *f = reinterpret_cast<const void *>(xl ? k_stream1<true> : k_stream1<false>);
-    if (xl && lds > 65536u)
-        (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (lds > 65536u) (void)hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, (int)nt, lds) != hipSuccess) {
         (void)hipGetLastError();
@@ -445,22 +533,24 @@ int stream_occupancy(bool xl, unsigned nt, uint32_t lds) {
     return per_cu;
 }
 
-// Launch shape: block size with the most resident waves per CU, a grid no
-// larger than what is resident at once; XLDS when the input fits in LDS and
-// staging it (input and column scale) costs at most half of a block's share
-// of the stream (index + value bytes).
-StreamShape stream_shape(int64_t nwin, int64_t nx) {
-    static const int force = env_int("SILI_STREAM_XLDS", -1);  // -1 auto, 0 off, 1 on when it fits
-    const int64_t static_lds = (int64_t)MAX_WAVES * 64 * 4;
-    const int64_t xbytes = (nx + 1) * 4;
-    const bool fits = xbytes + static_lds <= max_lds_per_block();
+constexpr int64_t STATIC_LDS = (int64_t)MAX_WAVES * 64 * 4;
+
+// Launch shape for NB columns per pass: block size with the most resident
+// waves per CU, a grid no larger than what is resident at once; XLDS when
+// the input fits in LDS and staging it (input and column scale) costs at
+// most half of a block's share of the stream (index + value bytes).
+StreamShape stream_shape(int nb, int64_t nwin, int64_t nx, bool allow_xlds) {
+    const int force = env_int("SILI_STREAM_XLDS", -1);  // -1 auto, 0 off, 1 on when it fits (read per call)
+    const int64_t xbytes = (nx + 1) * 4 * nb;
+    const bool fits = allow_xlds && xbytes + STATIC_LDS <= max_lds_per_block();
     StreamShape best{256, 1, false, 0};
     int best_waves = -1;
     for (const bool xl : {false, true}) {
         if (xl && !fits) continue;
         for (const unsigned nt : {256u, 512u, 1024u}) {
+            if (nb >= 4 && nt > 512u) continue;
             const uint32_t lds = xl ? (uint32_t)xbytes : 0u;
-            const int per_cu = stream_occupancy(xl, nt, lds);
+            const int per_cu = stream_occupancy(stream_kernel(nb, xl), nt, lds);
             if (per_cu <= 0) continue;
             const int64_t resident = (int64_t)per_cu * num_cus();
             const int64_t need = (nwin + nt / 64 - 1) / (nt / 64);
@@ -532,21 +622,32 @@ void build_stream(Layer &L, DScatter &s) {
     d.valid = true;
 }
 
+// Columns per pass for a batch of B (1, 2, 4 or 8): all of them when the
+// input fits in LDS at that width, else the widest power of two that fits
+// (passes re-read the stream), else B in one pass through the cache.
+int stream_pass_width(int64_t B, int64_t nx) {
+    for (int64_t nb = B; nb >= 2; nb >>= 1)
+        if ((nx + 1) * 4 * nb + STATIC_LDS <= max_lds_per_block()) return (int)nb;
+    return (int)B;
+}
+
 }  // namespace
 
 bool stream_wanted(const DScatter &s, const ScaleView &sc, int64_t nb, int64_t in_ld, int skip) {
-    if (nb != 1 || s.nnz == 0 || s.stream.failed) return false;
+    if (!(nb == 1 || nb == 2 || nb == 4 || nb == 8) || s.nnz == 0 || s.stream.failed) return false;
     // SILI_B1_STREAM (read at every call): 0 never, 1 (default) for stores of
     // at least 1 MiB of index bytes (below that one pass of the machine covers
     // the store and the segment kernels, which need no output fill, finish
     // first), 2 whenever the store allows
     const int mode = env_int("SILI_B1_STREAM", 1);
     if (mode == 0 || (mode == 1 && s.nbytes < (int64_t(1) << 20))) return false;
-    return skip == SKIP_NONE && sc.rank == 1 && in_ld == 1 && s.cols + 1 < (int64_t(1) << 29) &&
+    return skip == SKIP_NONE && sc.rank == 1 && in_ld == nb && s.cols + 1 < (int64_t(1) << 26) &&
+           (uint64_t)s.cols * (uint64_t)nb * 4u < (1ull << 31) &&
            (uint64_t)s.nbytes + 16ull * (uint64_t)s.rows + 2 * WIN_BYTES < (1ull << 31);
 }
 
-void stream_gather(Layer &L, DScatter &s, const ScaleView &sc, const float *in, float *out, hipStream_t st) {
+void stream_gather(Layer &L, DScatter &s, const ScaleView &sc, const float *in, int64_t B, float *out,
+                   int64_t out_ld, hipStream_t st) {
     if (!s.stream.valid) {
         build_stream(L, s);
         if (!s.stream.valid) throw_error(3, "stream copy exceeds 2 GiB");
@@ -554,18 +655,22 @@ void stream_gather(Layer &L, DScatter &s, const ScaleView &sc, const float *in, 
     const DStream &d = s.stream;
     {
         ProfScope ps("stream_zero", st);
-        launch(k_fill0, dim3((unsigned)((s.rows + 255) / 256)), dim3(256), 0, st, out, s.rows);
+        for (int64_t b = 0; b < B; ++b)
+            launch(k_fill0, dim3((unsigned)((s.rows + 255) / 256)), dim3(256), 0, st, out + b * out_ld, s.rows);
     }
     if (d.nwin == 0) return;
-    StreamArgs a{d.win.p, d.nwin, d.idx.p, d.val.p, d.ne_row.p, d.ne_start.p, (uint32_t)d.nbytes,
-                 in, sc.ent, sc.row, (uint32_t)s.cols, out};
-    const StreamShape sh = stream_shape(d.nwin, s.cols);
-    if (sh.xlds) {
-        ProfScope ps("stream_lds", st);
-        launch(k_stream1<true>, dim3(sh.grid), dim3(sh.threads), sh.lds, st, a);
-    } else {
-        ProfScope ps("stream", st);
-        launch(k_stream1<false>, dim3(sh.grid), dim3(sh.threads), 0u, st, a);
+    // several passes only with the input in LDS; otherwise one pass of all B
+    int nb = stream_pass_width(B, s.cols);
+    StreamShape sh = stream_shape(nb, d.nwin, s.cols, true);
+    if (nb < B && !sh.xlds) {
+        nb = (int)B;
+        sh = stream_shape(nb, d.nwin, s.cols, false);
+    }
+    for (int64_t b0 = 0; b0 < B; b0 += nb) {
+        StreamArgs a{d.win.p, d.nwin, d.idx.p, d.val.p, d.ne_row.p, d.ne_start.p, (uint32_t)d.nbytes,
+                     in + b0, (uint32_t)B, sc.ent, sc.row, (uint32_t)s.cols, out + b0 * out_ld, out_ld};
+        ProfScope ps(sh.xlds ? "stream_lds" : "stream", st);
+        launch(stream_kernel(nb, sh.xlds), dim3(sh.grid), dim3(sh.threads), sh.xlds ? sh.lds : 0u, st, a);
     }
     SILI_HIP(hipGetLastError());
 }

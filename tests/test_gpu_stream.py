@@ -146,22 +146,23 @@ def test_stream_canonical_and_shadow(hip, mod):
     rows = mixed_rows(n_out, 2 + (mod or 0), mod)
     # canonical orientation: dx = W^T g at batch 1 gathers the designed rows
     H, L = make_pair(hip, rows, n_out)
-    rng = np.random.default_rng(9)
-    x = rng.normal(size=(1, len(rows))).astype(np.float32)
-    g = rng.normal(size=(1, n_out)).astype(np.float32)
-    names = kernels_run(hip, L, lambda: check_bwd(H, L, x, g, f"dx mod{mod}"))
-    assert any(n.startswith("bwd:stream") for n in names), names
-    assert L.info()["stream_canonical"]
-    check_fwd(H, L, x, f"fwd mod{mod}")
-    # shadow orientation: the transposed layer's forward gathers them
     T = transpose_rows(rows, n_out)
     HT, LT = make_pair(hip, T, len(rows))
-    xt = rng.normal(size=(1, n_out)).astype(np.float32)
-    names = kernels_run(hip, LT, lambda: check_fwd(HT, LT, xt, f"T fwd mod{mod}"))
-    assert any(n.startswith("fwd:stream") for n in names), names
-    assert LT.info()["stream_shadow"]
-    # a second call must not see the first call's output
-    check_fwd(HT, LT, xt * 0.5, f"T fwd again mod{mod}")
+    rng = np.random.default_rng(9)
+    for B in (1, 2, 4, 8):
+        x = rng.normal(size=(B, len(rows))).astype(np.float32)
+        g = rng.normal(size=(B, n_out)).astype(np.float32)
+        names = kernels_run(hip, L, lambda: check_bwd(H, L, x, g, f"dx mod{mod} B{B}"))
+        assert any(n.startswith("bwd:stream") for n in names), names
+        assert L.info()["stream_canonical"]
+        check_fwd(H, L, x, f"fwd mod{mod} B{B}")
+        # shadow orientation: the transposed layer's forward gathers them
+        xt = rng.normal(size=(B, n_out)).astype(np.float32)
+        names = kernels_run(hip, LT, lambda: check_fwd(HT, LT, xt, f"T fwd mod{mod} B{B}"))
+        assert any(n.startswith("fwd:stream") for n in names), names
+        assert LT.info()["stream_shadow"]
+        # a second call must not see the first call's output
+        check_fwd(HT, LT, xt * 0.5, f"T fwd again mod{mod} B{B}")
 
 
 @pytest.mark.gpu
@@ -221,18 +222,42 @@ def test_stream_not_used_with_nonfinite_weights(hip):
     assert not any("stream" in n for n in names), names
 
 
+def kernel_counts(hip, L, fn):
+    lib = C.CDLL(hip.LIB_PATH)
+    lib.sili_profile_enable.argtypes = [C.c_void_p, C.c_int]
+    lib.sili_profile_read.argtypes = [C.c_void_p, C.POINTER(Entry), C.c_int, C.POINTER(C.c_int)]
+    h = C.c_void_p(L.handle)
+    assert lib.sili_profile_enable(h, 1) == 0
+    fn()
+    buf = (Entry * 64)()
+    n = C.c_int()
+    assert lib.sili_profile_read(h, buf, 64, C.byref(n)) == 0
+    assert lib.sili_profile_enable(h, 0) == 0
+    return {buf[i].name.decode(): buf[i].count for i in range(n.value)}
+
+
 @pytest.mark.gpu
-def test_stream_lds_and_global_variants(hip):
-    """A long stream over a narrow input stages the input in LDS; a short
-    one reads it through the cache; an input too wide for LDS always does."""
-    seen = set()
-    for n_in, n_out, keep in ((1024, 60000, 0.08), (512, 3000, 0.1), (40000, 300, 0.02)):
-        L = hip.SparseLinearLayer(n_in, n_out, 1)
-        L.load_synthetic(4242 + n_in, keep, 0.02, 0.5)
-        ex = L.export_scattered()
-        H = HostLayer(n_in, n_out).load_encoded(ex["row_byte_start"], ex["row_elem_start"], ex["idx"], ex["val"])
-        H.set_scales(np.asarray(L.get_value_scales(), np.float32))
-        x = np.random.default_rng(n_in).normal(size=(1, n_in)).astype(np.float32)
-        names = kernels_run(hip, L, lambda: check_fwd(H, L, x, f"synthetic {n_in}x{n_out}"))
-        seen |= {n for n in names if "stream" in n}
-    assert "fwd:stream_lds" in seen and "fwd:stream" in seen, seen
+@pytest.mark.parametrize("n_in,B,xlds,want", [
+    (3000, 1, "0", {"fwd:stream": 1}),
+    (3000, 1, "1", {"fwd:stream_lds": 1}),
+    (3000, 2, "1", {"fwd:stream_lds": 1}),
+    (3000, 8, "1", {"fwd:stream_lds": 1}),
+    (6000, 8, "1", {"fwd:stream_lds": 2}),   # input too wide for LDS at 8 columns: 2 passes of 4
+    (6000, 8, "0", {"fwd:stream": 1}),
+    (6000, 4, "0", {"fwd:stream": 1}),
+    (40000, 2, "1", {"fwd:stream": 1}),      # too wide for LDS at any width: through the cache
+])
+def test_stream_variants(hip, monkeypatch, n_in, B, xlds, want):
+    """Each launch variant (input in LDS or through the cache, one pass or
+    several) against the oracle, the variant read back from the profiler."""
+    monkeypatch.setenv("SILI_STREAM_XLDS", xlds)
+    n_out = 20000 if n_in < 10000 else 800
+    L = hip.SparseLinearLayer(n_in, n_out, 1)
+    L.load_synthetic(4242 + n_in, 0.05, 0.02, 0.5)
+    ex = L.export_scattered()
+    H = HostLayer(n_in, n_out).load_encoded(ex["row_byte_start"], ex["row_elem_start"], ex["idx"], ex["val"])
+    H.set_scales(np.asarray(L.get_value_scales(), np.float32))
+    x = np.random.default_rng(n_in + B).normal(size=(B, n_in)).astype(np.float32)
+    got = kernel_counts(hip, L, lambda: check_fwd(H, L, x, f"synthetic {n_in}x{n_out} B{B}"))
+    got = {k: v for k, v in got.items() if k in ("fwd:stream", "fwd:stream_lds")}
+    assert got == want, got
