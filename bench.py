@@ -44,6 +44,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--synapto-reps", type=int, default=5, help="config 3: timed synaptogenesis steps")
+    p.add_argument("--c4-batches", default="1,8,128", help="config 4: token batches to time")
     p.add_argument("--verbose", action="store_true")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run 3 device-to-device copies of MIB MiB (HBM counter calibration)")
@@ -398,7 +399,7 @@ def run_config4(a, hip, api, rt):
     nnz_total = sum(d["nnz"] for d in layers)
     stream = api.L.sili_stream(layers[0]["h"])
     results = {}
-    for B in C4_BATCHES:
+    for B in [int(b) for b in a.c4_batches.split(",")]:
         for i, d in enumerate(layers):
             x = Stream(SEED0 + 4, 10 + 100 * B + i).normal(B * d["n_in"]).astype(np.float32)
             d["x"] = api.upload(d["h"], x)

@@ -363,8 +363,8 @@ void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64
     const Encoded e = encode_rows(L, rows, ncols, N, d_ptrs, d_cols, L.seg_len, true, dst.byte_start,
                                   dst.elem_start, dst.idx, dst.seg, "load_weights", &dst.split_rows);
     dst.n_split = e.n_split;
-    dst.stream.valid = false;
-    dst.stream.failed = false;
+    dst.stream1.valid = dst.streamK.valid = false;
+    dst.stream1.failed = dst.streamK.failed = false;
     dst.rows = rows;
     dst.cols = ncols;
     dst.nnz = N;
@@ -408,8 +408,8 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
     const Encoded e = encode_rows(L, src.cols, src.rows, N, ptrs.p, trows.p, L.seg_len, true, dst.byte_start,
                                   dst.elem_start, dst.idx, dst.seg, "shadow build", &dst.split_rows);
     dst.n_split = e.n_split;
-    dst.stream.valid = false;
-    dst.stream.failed = false;
+    dst.stream1.valid = dst.streamK.valid = false;
+    dst.stream1.failed = dst.streamK.failed = false;
     dst.rows = src.cols;
     dst.cols = src.rows;
     dst.nnz = N;

@@ -669,8 +669,8 @@ int sili_get_info(sili_layer *layer, sili_info *out) {
         out->n_segments = L.W.nseg;
         out->scale_rank = L.rank;
         out->has_nonfinite = L.has_nonfinite ? 1 : 0;
-        out->stream_canonical = L.W.stream.valid ? 1 : 0;
-        out->stream_shadow = L.Wt.stream.valid ? 1 : 0;
+        out->stream_canonical = (L.W.stream1.valid || L.W.streamK.valid) ? 1 : 0;
+        out->stream_shadow = (L.Wt.stream1.valid || L.Wt.streamK.valid) ? 1 : 0;
         if (L.B4.ntiles > 0) {
             std::vector<uint32_t> br, bc;
             export_block4_coords(L, br, bc);

@@ -40,23 +40,32 @@ struct DevBuf {
     T *get() const { return p; }
 };
 
-// Padded stream copy of a scattered store, read by the batch-1 stream
-// kernels (built on first use, dropped when the store is rebuilt).  Row r
-// occupies bytes [pstart[r], pstart[r+1]) with pstart[r] a multiple of 16:
-// z zero bytes (delta 0: entries at shifted column 0), then the row's
-// varints for the shifted columns col + 1 (only the row's first, absolute
-// delta changes).  Shifted column 0 is a zero input slot, so the padding
-// entries (value byte 0) contribute exactly 0.  val[p] is the value byte of
-// the entry whose varint ends at byte p (0 elsewhere): value bytes run in
-// parallel with index bytes.
+// Padded stream copy of a scattered store, read by the stream kernels
+// (built on first use, dropped when the store is rebuilt).  The store's
+// columns are cut into K blocks of cb columns; block k holds, for every row,
+// the row's entries with columns in [k*cb, (k+1)*cb) (K = 1: whole rows).
+// In a block, row r occupies bytes [pstart, pstart + L) with pstart a
+// multiple of 16: zero bytes first (delta 0: entries at shifted column 0),
+// then the varints of the shifted columns col - k*cb + 1 (only the first,
+// absolute delta differs from the store's).  Shifted column 0 is a zero
+// input slot, so the padding entries (value byte 0) contribute exactly 0.
+// val[p] is the value byte of the entry whose varint ends at byte p (0
+// elsewhere): value bytes run in parallel with index bytes.  Each block's
+// bytes start on a window boundary.
+struct DStreamBlock {
+    int64_t nbytes = 0, nwin = 0, n_ne = 0, c0 = 0, ncols = 0;
+    size_t off = 0, ne_off = 0, win_off = 0;  // into idx/val, ne_row/ne_start, win
+};
 struct DStream {
     bool valid = false;
     bool failed = false;          // too large for the kernels' 31-bit offsets
-    int64_t nbytes = 0, nwin = 0, n_ne = 0;
-    DevBuf<uint8_t> idx, val;     // nbytes (+ padding)
-    DevBuf<uint32_t> ne_row;      // non-empty rows, ascending (n_ne)
-    DevBuf<uint32_t> ne_start;    // their first padded byte (n_ne + 1; last = nbytes)
-    DevBuf<WinDesc> win;          // nwin + 1 (rs_lo indexes ne_row / ne_start)
+    int K = 0;
+    int64_t cb = 0;
+    std::vector<DStreamBlock> blocks;
+    DevBuf<uint8_t> idx, val;     // blocks' bytes (+ padding)
+    DevBuf<uint32_t> ne_row;      // per block: non-empty rows, ascending
+    DevBuf<uint32_t> ne_start;    // per block: their first byte (+ sentinel: block bytes)
+    DevBuf<WinDesc> win;          // per block: nwin + 1 (rs_lo indexes the block's ne lists)
 };
 
 // One orientation of the scattered store.
@@ -68,7 +77,7 @@ struct DScatter {
     DevBuf<SegDesc> seg;
     DevBuf<uint32_t> split_rows;  // rows with more than one work item
     int64_t n_split = 0;
-    DStream stream;               // batch-1 stream copy (on demand)
+    DStream stream1, streamK;     // stream copies: whole rows / the last column blocking used
     GatherPlan plan() const {
         return GatherPlan{seg.p, nseg, idx.p, val.p, rows, cols, has_split, split_rows.p, n_split};
     }

@@ -50,39 +50,72 @@ inline unsigned nblk(int64_t n) { return (unsigned)((n + TPB - 1) / TPB); }
 
 // ---- building the stream copy ----------------------------------------------
 
-// First varint of a row of n bytes: value and length.
-__device__ __forceinline__ void first_varint(const uint8_t *p, uint32_t n, uint32_t &v, uint32_t &len) {
-    v = 0;
-    len = 0;
-    uint32_t shift = 0;
-    while (len < n && len < 5u) {
-        const uint32_t b = p[len++];
-        v |= (b & 0x7Fu) << shift;
-        shift += 7;
-        if (!(b & 0x80u)) break;
+// Where column block k of row r begins and ends in the row's index bytes:
+// first entry's byte offset s, varint length lf, column c and entry index ei
+// (in the store), and the byte offset e where the block's entries end.
+// e == 0: the row has no entry in the block.
+struct BlkMeta {
+    uint32_t s, lf, e, c, ei;
+};
+
+// Pass 1: one wave per row.
+__global__ __launch_bounds__(256) void k_spb_meta(const uint32_t *__restrict__ bs, const uint32_t *__restrict__ es,
+                                                  const uint8_t *__restrict__ idx, int64_t rows, uint32_t cb,
+                                                  BlkMeta *__restrict__ meta) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + uniform(threadIdx.x >> 6);
+    if (r >= rows) return;
+    const uint32_t lane = lane_id();
+    const uint32_t b = bs[r], n = bs[r + 1] - b;
+    if (n == 0) return;
+    const uint8_t *row = idx + b;
+    uint32_t off = 0, carry = 0, ebase = es[r];
+    uint32_t kopen = 0xFFFFFFFFu;  // block of the entry before the chunk
+    while (off < n) {
+        const Chunk ch = decode_chunk(row, off, n, carry);
+        if (ch.T == 0ull) break;
+        const uint64_t below = ch.T & ((1ull << lane) - 1ull);
+        const int pl = below ? 63 - (int)__clzll(below) : -1;  // previous entry's last byte in the chunk
+        const uint32_t kb = ch.col / cb;
+        const uint32_t kpl = (uint32_t)__shfl((int)kb, pl < 0 ? 0 : pl, 64);
+        const uint32_t kp = pl < 0 ? kopen : kpl;
+        uint64_t F = __ballot(ch.term && kb != kp);  // entries that open a block
+        while (F) {
+            const int fl = __builtin_ctzll(F);
+            F &= F - 1ull;
+            const uint32_t kf = (uint32_t)__builtin_amdgcn_readlane((int)kb, fl);
+            const uint32_t cf = (uint32_t)__builtin_amdgcn_readlane((int)ch.col, fl);
+            const int pf = __builtin_amdgcn_readlane(pl, fl);
+            const uint32_t rk = (uint32_t)__builtin_amdgcn_readlane((int)ch.rank, fl);
+            const uint32_t s0 = off + (uint32_t)(pf + 1);
+            if (lane == 0u) {
+                BlkMeta &m = meta[(int64_t)kf * rows + r];
+                m.s = s0;
+                m.lf = (uint32_t)(fl - pf);
+                m.c = cf;
+                m.ei = ebase + rk;
+                if (kopen != 0xFFFFFFFFu) meta[(int64_t)kopen * rows + r].e = s0;
+            }
+            kopen = kf;
+        }
+        carry = chunk_advance(ch, off, ebase);
     }
+    if (lane == 0u && kopen != 0xFFFFFFFFu) meta[(int64_t)kopen * rows + r].e = n;
 }
 
-// Padded length of row r: its bytes with the first delta re-encoded for
-// col + 1, rounded up to 16.
-__global__ void k_sp_len(const uint32_t *__restrict__ bs, const uint8_t *__restrict__ idx, int64_t rows,
-                         uint32_t *__restrict__ len, uint32_t *__restrict__ nonempty) {
-    const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
-    if (r > rows) return;
-    if (r == rows) {
-        len[r] = 0;
-        nonempty[r] = 0;
-        return;
-    }
-    const uint32_t b = bs[r], n = bs[r + 1] - b;
+// Padded length of block k of row r (first delta re-encoded for the shifted
+// column, rounded up to 16); lens / nonempty are [K][rows + 1].
+__global__ void k_spb_len(const BlkMeta *__restrict__ meta, int64_t rows, int K, uint32_t cb,
+                          uint32_t *__restrict__ len, uint32_t *__restrict__ nonempty) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= (int64_t)K * (rows + 1)) return;
+    const int64_t k = i / (rows + 1), r = i - k * (rows + 1);
     uint32_t L = 0;
-    if (n) {
-        uint32_t c0, l0;
-        first_varint(idx + b, n, c0, l0);
-        L = (n - l0 + uleb_len(c0 + 1u) + 15u) & ~15u;
+    if (r < rows) {
+        const BlkMeta m = meta[k * rows + r];
+        if (m.e) L = (uleb_len(m.c - (uint32_t)k * cb + 1u) + (m.e - m.s - m.lf) + 15u) & ~15u;
     }
-    len[r] = L;
-    nonempty[r] = n ? 1u : 0u;
+    len[i] = L;
+    nonempty[i] = L ? 1u : 0u;
 }
 
 __global__ void k_sp_ne(const uint32_t *__restrict__ nonempty, const uint32_t *__restrict__ pos,
@@ -91,7 +124,7 @@ __global__ void k_sp_ne(const uint32_t *__restrict__ nonempty, const uint32_t *_
     const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (r > rows) return;
     if (r == rows) {
-        ne_start[pos[r]] = pstart[r];  // sentinel: total bytes
+        ne_start[pos[r]] = pstart[r];  // sentinel: the block's bytes
         return;
     }
     if (nonempty[r]) {
@@ -100,27 +133,27 @@ __global__ void k_sp_ne(const uint32_t *__restrict__ nonempty, const uint32_t *_
     }
 }
 
-// One wave per row: copy the row into the padded stream (first delta
-// re-encoded, value bytes placed at their terminators) and write row0 /
-// carry of every window that starts inside the row's padded range.
-__global__ __launch_bounds__(256) void k_sp_copy(const uint32_t *__restrict__ bs, const uint32_t *__restrict__ es,
-                                                 const uint8_t *__restrict__ idx, const uint8_t *__restrict__ val,
-                                                 const uint32_t *__restrict__ pstart, int64_t rows,
-                                                 uint8_t *__restrict__ sidx, uint8_t *__restrict__ sval,
-                                                 WinDesc *__restrict__ win) {
+// Pass 2: one wave per (block, row): copy the block's entries of the row into
+// the block's padded stream (first delta re-encoded for the shifted column,
+// value bytes placed at their terminators) and write row0 / carry of every
+// window of the block that starts inside the row's padded range.
+__global__ __launch_bounds__(256) void k_spb_copy(const uint32_t *__restrict__ bs, const uint8_t *__restrict__ idx,
+                                                  const uint8_t *__restrict__ val, const BlkMeta *__restrict__ meta,
+                                                  const uint32_t *__restrict__ pstart, int64_t rows, uint32_t c0,
+                                                  uint8_t *__restrict__ sidx, uint8_t *__restrict__ sval,
+                                                  WinDesc *__restrict__ win) {
     const int64_t r = (int64_t)blockIdx.x * 4 + uniform(threadIdx.x >> 6);
     if (r >= rows) return;
     const uint32_t lane = lane_id();
-    const uint32_t b = bs[r], n = bs[r + 1] - b;
-    if (n == 0) return;
+    const BlkMeta m = meta[r];
+    if (m.e == 0u) return;
     const uint32_t P = pstart[r], Lr = pstart[r + 1] - P;
-    uint32_t c0, l0;
-    first_varint(idx + b, n, c0, l0);
-    const uint32_t v1 = c0 + 1u, l1 = uleb_len(v1);
-    const uint32_t z = Lr - (n - l0 + l1);  // padding entries in front
-    const uint32_t D = P + z + l1;          // padded position of row byte l0
+    const uint32_t v1 = m.c - c0 + 1u, l1 = uleb_len(v1);
+    const uint32_t body = m.e - m.s - m.lf;  // bytes after the first entry
+    const uint32_t z = Lr - (l1 + body);      // padding entries in front
+    const uint32_t D = P + z + l1;            // padded position of row byte s + lf
     if (lane < l1) sidx[P + z + lane] = (uint8_t)(((v1 >> (7u * lane)) & 0x7Fu) | (lane + 1u < l1 ? 0x80u : 0u));
-    if (lane == 0u) sval[D - 1u] = val[es[r]];
+    if (lane == 0u) sval[D - 1u] = val[m.ei];
     // a window starting before the first entry's last byte: only padding
     // entries (shifted column 0) precede it
     const uint32_t w_pad = (P + WIN_BYTES - 1u) / WIN_BYTES * WIN_BYTES;
@@ -128,13 +161,14 @@ __global__ __launch_bounds__(256) void k_sp_copy(const uint32_t *__restrict__ bs
         win[w_pad / WIN_BYTES].row0 = (uint32_t)r;
         win[w_pad / WIN_BYTES].carry = 0u;
     }
-    const uint8_t *row = idx + b;
-    uint32_t off = l0, carry = c0, ebase = es[r] + 1u;
-    while (off < n) {
-        const Chunk ch = decode_chunk(row, off, n, carry);
+    const uint8_t *row = idx + bs[r];
+    const uint32_t o0 = m.s + m.lf;
+    uint32_t off = o0, carry = m.c, ebase = m.ei + 1u;
+    while (off < m.e) {
+        const Chunk ch = decode_chunk(row, off, m.e, carry);
         if (ch.T == 0ull) break;
         const uint32_t hi = 63u - (uint32_t)__clzll(ch.T);  // last byte of the chunk's last entry
-        const uint32_t d0 = D + off - l0;                   // padded position of byte `off`
+        const uint32_t d0 = D + off - o0;                   // padded position of byte `off`
         if (lane <= hi) {
             sidx[d0 + lane] = row[off + lane];
             if (ch.term) sval[d0 + lane] = val[ebase + ch.rank];
@@ -143,8 +177,8 @@ __global__ __launch_bounds__(256) void k_sp_copy(const uint32_t *__restrict__ bs
         const uint32_t ws = (d0 + WIN_BYTES - 1u) / WIN_BYTES * WIN_BYTES;
         if (ws <= d0 + hi) {
             const uint64_t before = ch.T & ((1ull << (ws - d0)) - 1ull);
-            uint32_t c = carry + 1u;
-            if (before) c = (uint32_t)__shfl((int)ch.col, 63 - (int)__clzll(before), 64) + 1u;
+            uint32_t c = carry - c0 + 1u;
+            if (before) c = (uint32_t)__shfl((int)ch.col, 63 - (int)__clzll(before), 64) - c0 + 1u;
             if (lane == 0u) {
                 win[ws / WIN_BYTES].row0 = (uint32_t)r;
                 win[ws / WIN_BYTES].carry = c;
@@ -154,7 +188,7 @@ __global__ __launch_bounds__(256) void k_sp_copy(const uint32_t *__restrict__ bs
     }
 }
 
-// rs_lo of every window: first non-empty row starting at or after it.
+// rs_lo of every window of a block: first non-empty row starting at or after it.
 __global__ void k_sp_rs(const uint32_t *__restrict__ ne_start, int64_t n_ne, int64_t nwin, int64_t rows,
                         WinDesc *__restrict__ win) {
     const int64_t w = (int64_t)blockIdx.x * TPB + threadIdx.x;
@@ -416,8 +450,9 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, int64_t w, const
     }
 }
 
+// (8 columns through the cache need more registers than 1024-thread blocks allow)
 template <int NB, bool XLDS>
-__global__ __launch_bounds__(NB >= 4 ? 512 : 1024) void k_stream(StreamArgs a) {
+__global__ __launch_bounds__((NB == 8 && !XLDS) ? 512 : 1024) void k_stream(StreamArgs a) {
     extern __shared__ float s_x[];
     __shared__ uint32_t s_slot[MAX_WAVES][64];
     const uint32_t nw = blockDim.x >> 6;
@@ -536,29 +571,26 @@ int stream_occupancy(StreamKernel k, unsigned nt, uint32_t lds) {
 constexpr int64_t STATIC_LDS = (int64_t)MAX_WAVES * 64 * 4;
 
 // Launch shape for NB columns per pass: block size with the most resident
-// waves per CU, a grid no larger than what is resident at once; XLDS when
-// the input fits in LDS and staging it (input and column scale) costs at
-// most half of a block's share of the stream (index + value bytes).
-StreamShape stream_shape(int nb, int64_t nwin, int64_t nx, bool allow_xlds) {
-    const int force = env_int("SILI_STREAM_XLDS", -1);  // -1 auto, 0 off, 1 on when it fits (read per call)
+// waves per CU, a grid no larger than what is resident at once.  xmode: 0
+// input through the cache, 2 input in LDS when it fits, 1 (auto) in LDS when
+// it fits and staging it (input and column scale) costs at most half of a
+// block's share of the stream (index + value bytes).
+StreamShape stream_shape(int nb, int64_t nwin, int64_t nx, int xmode) {
     const int64_t xbytes = (nx + 1) * 4 * nb;
-    const bool fits = allow_xlds && xbytes + STATIC_LDS <= max_lds_per_block();
+    const bool fits = xmode != 0 && xbytes + STATIC_LDS <= max_lds_per_block();
     StreamShape best{256, 1, false, 0};
     int best_waves = -1;
     for (const bool xl : {false, true}) {
         if (xl && !fits) continue;
         for (const unsigned nt : {256u, 512u, 1024u}) {
-            if (nb >= 4 && nt > 512u) continue;
+            if (nb == 8 && !xl && nt > 512u) continue;
             const uint32_t lds = xl ? (uint32_t)xbytes : 0u;
             const int per_cu = stream_occupancy(stream_kernel(nb, xl), nt, lds);
             if (per_cu <= 0) continue;
             const int64_t resident = (int64_t)per_cu * num_cus();
             const int64_t need = (nwin + nt / 64 - 1) / (nt / 64);
             const unsigned grid = (unsigned)std::max<int64_t>(1, std::min(resident, need));
-            if (xl) {
-                const bool auto_ok = 2 * xbytes * (int64_t)grid <= nwin * (int64_t)WIN_BYTES;
-                if (force == 0 || (force < 0 && !auto_ok)) continue;
-            }
+            if (xl && xmode == 1 && 2 * xbytes * (int64_t)grid > nwin * (int64_t)WIN_BYTES) continue;
             const int waves = per_cu * (int)(nt / 64);
             // prefer XLDS when allowed, then more resident waves, then larger blocks
             const bool better = best_waves < 0 || (xl && !best.xlds) ||
@@ -572,105 +604,182 @@ StreamShape stream_shape(int nb, int64_t nwin, int64_t nx, bool allow_xlds) {
     return best;
 }
 
-// Build s.stream from s (device work on L's stream; synchronous).
-void build_stream(Layer &L, DScatter &s) {
+// Build d = the stream copy of s cut into K column blocks of cb columns
+// (device work on L's stream; synchronous).  Sets d.failed when a block
+// would not keep 31-bit offsets.
+void build_stream(Layer &L, const DScatter &s, DStream &d, int K, int64_t cb) {
     hipStream_t st = L.stream;
-    DStream &d = s.stream;
     const int64_t rows = s.rows;
+    d.valid = false;
+    d.K = K;
+    d.cb = cb;
+    d.blocks.assign((size_t)K, DStreamBlock{});
+    const int64_t n1 = rows + 1;
+    DevBuf<BlkMeta> meta;
     DevBuf<uint32_t> len, pstart, ne, nepos;
-    len.ensure((size_t)rows + 1);
-    pstart.ensure((size_t)rows + 1);
-    ne.ensure((size_t)rows + 1);
-    nepos.ensure((size_t)rows + 1);
-    launch(k_sp_len, dim3(nblk(rows + 1)), dim3(TPB), 0, st, (const uint32_t *)s.byte_start.p,
-           (const uint8_t *)s.idx.p, rows, len.p, ne.p);
+    meta.ensure((size_t)K * (size_t)std::max<int64_t>(rows, 1));
+    len.ensure((size_t)K * n1);
+    pstart.ensure((size_t)K * n1);
+    ne.ensure((size_t)K * n1);
+    nepos.ensure((size_t)K * n1);
+    SILI_HIP(hipMemsetAsync(meta.p, 0, sizeof(BlkMeta) * (size_t)K * (size_t)std::max<int64_t>(rows, 1), st));
+    if (rows > 0)
+        launch(k_spb_meta, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, (const uint32_t *)s.byte_start.p,
+               (const uint32_t *)s.elem_start.p, (const uint8_t *)s.idx.p, rows, (uint32_t)cb, meta.p);
+    launch(k_spb_len, dim3(nblk((int64_t)K * n1)), dim3(TPB), 0, st, (const BlkMeta *)meta.p, rows, K,
+           (uint32_t)cb, len.p, ne.p);
     SILI_HIP(hipGetLastError());
-    device_exclusive_scan_u32(L, len.p, pstart.p, rows + 1);
-    device_exclusive_scan_u32(L, ne.p, nepos.p, rows + 1);
-    uint32_t tot[2] = {0, 0};
-    SILI_HIP(hipMemcpyAsync(&tot[0], pstart.p + rows, 4, hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipMemcpyAsync(&tot[1], nepos.p + rows, 4, hipMemcpyDeviceToHost, st));
+    for (int k = 0; k < K; ++k) {
+        device_exclusive_scan_u32(L, len.p + (size_t)k * n1, pstart.p + (size_t)k * n1, n1);
+        device_exclusive_scan_u32(L, ne.p + (size_t)k * n1, nepos.p + (size_t)k * n1, n1);
+    }
+    std::vector<uint32_t> tot((size_t)K * 2);
+    for (int k = 0; k < K; ++k) {
+        SILI_HIP(hipMemcpyAsync(&tot[2 * (size_t)k], pstart.p + (size_t)k * n1 + rows, 4, hipMemcpyDeviceToHost, st));
+        SILI_HIP(hipMemcpyAsync(&tot[2 * (size_t)k + 1], nepos.p + (size_t)k * n1 + rows, 4, hipMemcpyDeviceToHost, st));
+    }
     SILI_HIP(hipStreamSynchronize(st));
-    // the padded stream must keep 32-bit offsets below 2^31 (buffer loads);
-    // the padded lengths are summed in 32 bits, so bound them by the source
-    if ((uint64_t)s.nbytes + 16ull * (uint64_t)rows + 2 * WIN_BYTES >= (1ull << 31)) {
+    // offsets: every block starts on a window boundary; 32-bit offsets must
+    // stay below 2^31 (the padded lengths were summed in 32 bits, so bound
+    // them by the source first)
+    if ((uint64_t)s.nbytes + 16ull * (uint64_t)rows * (uint64_t)K + (uint64_t)K * 2 * WIN_BYTES >= (1ull << 31)) {
         d.failed = true;
         return;
     }
-    const int64_t nbytes = tot[0], n_ne = tot[1];
-    const int64_t nwin = (nbytes + WIN_BYTES - 1) / WIN_BYTES;
-    d.idx.ensure((size_t)nbytes + WIN_BYTES);
-    d.val.ensure((size_t)nbytes + WIN_BYTES);
-    d.ne_row.ensure((size_t)n_ne + 1);
-    d.ne_start.ensure((size_t)n_ne + 1);
-    d.win.ensure((size_t)nwin + 1);
-    SILI_HIP(hipMemsetAsync(d.idx.p, 0, (size_t)nbytes + WIN_BYTES, st));
-    SILI_HIP(hipMemsetAsync(d.val.p, 0, (size_t)nbytes + WIN_BYTES, st));
-    launch(k_sp_ne, dim3(nblk(rows + 1)), dim3(TPB), 0, st, (const uint32_t *)ne.p, (const uint32_t *)nepos.p,
-           (const uint32_t *)pstart.p, rows, d.ne_row.p, d.ne_start.p);
-    if (rows > 0)
-        launch(k_sp_copy, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, (const uint32_t *)s.byte_start.p,
-               (const uint32_t *)s.elem_start.p, (const uint8_t *)s.idx.p, (const uint8_t *)s.val.p,
-               (const uint32_t *)pstart.p, rows, d.idx.p, d.val.p, d.win.p);
-    launch(k_sp_rs, dim3(nblk(nwin + 1)), dim3(TPB), 0, st, (const uint32_t *)d.ne_start.p, n_ne, nwin, rows,
-           d.win.p);
-    SILI_HIP(hipGetLastError());
+    size_t off = 0, ne_off = 0, win_off = 0;
+    for (int k = 0; k < K; ++k) {
+        DStreamBlock &bk = d.blocks[(size_t)k];
+        bk.nbytes = tot[2 * (size_t)k];
+        bk.n_ne = tot[2 * (size_t)k + 1];
+        bk.nwin = (bk.nbytes + WIN_BYTES - 1) / WIN_BYTES;
+        bk.c0 = (int64_t)k * cb;
+        bk.ncols = std::min<int64_t>(cb, s.cols - bk.c0);
+        bk.off = off;
+        bk.ne_off = ne_off;
+        bk.win_off = win_off;
+        off += (size_t)bk.nwin * WIN_BYTES;
+        ne_off += (size_t)bk.n_ne + 1;
+        win_off += (size_t)bk.nwin + 1;
+    }
+    d.idx.ensure(off + WIN_BYTES);
+    d.val.ensure(off + WIN_BYTES);
+    d.ne_row.ensure(ne_off + 1);
+    d.ne_start.ensure(ne_off + 1);
+    d.win.ensure(win_off + 1);
+    SILI_HIP(hipMemsetAsync(d.idx.p, 0, off + WIN_BYTES, st));
+    SILI_HIP(hipMemsetAsync(d.val.p, 0, off + WIN_BYTES, st));
+    for (int k = 0; k < K; ++k) {
+        const DStreamBlock &bk = d.blocks[(size_t)k];
+        const size_t o = (size_t)k * n1;
+        launch(k_sp_ne, dim3(nblk(n1)), dim3(TPB), 0, st, (const uint32_t *)ne.p + o, (const uint32_t *)nepos.p + o,
+               (const uint32_t *)pstart.p + o, rows, d.ne_row.p + bk.ne_off, d.ne_start.p + bk.ne_off);
+        if (rows > 0)
+            launch(k_spb_copy, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, (const uint32_t *)s.byte_start.p,
+                   (const uint8_t *)s.idx.p, (const uint8_t *)s.val.p, (const BlkMeta *)meta.p + (size_t)k * rows,
+                   (const uint32_t *)pstart.p + o, rows, (uint32_t)bk.c0, d.idx.p + bk.off, d.val.p + bk.off,
+                   d.win.p + bk.win_off);
+        launch(k_sp_rs, dim3(nblk(bk.nwin + 1)), dim3(TPB), 0, st, (const uint32_t *)d.ne_start.p + bk.ne_off,
+               bk.n_ne, bk.nwin, rows, d.win.p + bk.win_off);
+        SILI_HIP(hipGetLastError());
+    }
     SILI_HIP(hipStreamSynchronize(st));
-    d.nbytes = nbytes;
-    d.nwin = nwin;
-    d.n_ne = n_ne;
     d.valid = true;
 }
 
-// Columns per pass for a batch of B (1, 2, 4 or 8): all of them when the
-// input fits in LDS at that width, else the widest power of two that fits
-// (passes re-read the stream), else B in one pass through the cache.
+// Columns per pass for a batch of B (1, 2, 4 or 8) when the input is not cut
+// into column blocks: all of them when the input fits in LDS at that width,
+// else the widest power of two that fits (passes re-read the stream:
+// measured, B passes of one column from LDS still beat one pass of B columns
+// gathered through the cache), else B in one pass through the cache.
 int stream_pass_width(int64_t B, int64_t nx) {
-    for (int64_t nb = B; nb >= 2; nb >>= 1)
+    for (int64_t nb = B; nb >= 1; nb >>= 1)
         if ((nx + 1) * 4 * nb + STATIC_LDS <= max_lds_per_block()) return (int)nb;
     return (int)B;
+}
+
+// Column blocking for a pass of B columns: none when the input fits in LDS
+// at that width (or cannot be staged at all), else the fewest equal blocks
+// whose slice of the input fits.  Returns K (0: no blocking is useful).
+int stream_blocks(int64_t B, int64_t cols, int64_t &cb) {
+    const int64_t avail = max_lds_per_block() - STATIC_LDS;
+    const int64_t cb_max = avail / (4 * B) - 1;
+    if (cb_max >= cols) {
+        cb = cols;
+        return 1;
+    }
+    if (cb_max < 256) return 0;
+    const int64_t K = (cols + cb_max - 1) / cb_max;
+    if (K > 16) return 0;
+    cb = (cols + K - 1) / K;
+    return (int)K;
 }
 
 }  // namespace
 
 bool stream_wanted(const DScatter &s, const ScaleView &sc, int64_t nb, int64_t in_ld, int skip) {
-    if (!(nb == 1 || nb == 2 || nb == 4 || nb == 8) || s.nnz == 0 || s.stream.failed) return false;
+    if (!(nb == 1 || nb == 2 || nb == 4 || nb == 8) || s.nnz == 0) return false;
     // SILI_B1_STREAM (read at every call): 0 never, 1 (default) for stores of
     // at least 1 MiB of index bytes (below that one pass of the machine covers
     // the store and the segment kernels, which need no output fill, finish
     // first), 2 whenever the store allows
     const int mode = env_int("SILI_B1_STREAM", 1);
     if (mode == 0 || (mode == 1 && s.nbytes < (int64_t(1) << 20))) return false;
+    if (s.stream1.failed && s.streamK.failed) return false;
     return skip == SKIP_NONE && sc.rank == 1 && in_ld == nb && s.cols + 1 < (int64_t(1) << 26) &&
-           (uint64_t)s.cols * (uint64_t)nb * 4u < (1ull << 31) &&
-           (uint64_t)s.nbytes + 16ull * (uint64_t)s.rows + 2 * WIN_BYTES < (1ull << 31);
+           (uint64_t)s.cols * (uint64_t)nb * 4u < (1ull << 31);
 }
 
 void stream_gather(Layer &L, DScatter &s, const ScaleView &sc, const float *in, int64_t B, float *out,
                    int64_t out_ld, hipStream_t st) {
-    if (!s.stream.valid) {
-        build_stream(L, s);
-        if (!s.stream.valid) throw_error(3, "stream copy exceeds 2 GiB");
+    // Plan: all B columns in one pass when the input fits in LDS (whole or in
+    // column blocks); else passes of fewer columns from LDS; else one pass of
+    // B columns through the cache.  SILI_STREAM_XLDS=0 forces the last.
+    const int force = env_int("SILI_STREAM_XLDS", -1);
+    int64_t cb = s.cols;
+    int K = force == 0 ? 1 : stream_blocks(B, s.cols, cb);
+    int nb = (int)B;
+    if (K == 0) {
+        K = 1;
+        cb = s.cols;
+        nb = stream_pass_width(B, s.cols);
     }
-    const DStream &d = s.stream;
+    DStream *d = nullptr;
+    if (K == 1) {
+        d = &s.stream1;
+        if (!d->valid && !d->failed) build_stream(L, s, *d, 1, s.cols);
+    } else {
+        d = &s.streamK;
+        if (!d->valid || d->K != K || d->cb != cb) {
+            d->failed = false;
+            build_stream(L, s, *d, K, cb);
+        }
+    }
+    if (!d->valid) throw_error(3, "stream copy exceeds 2 GiB");
     {
         ProfScope ps("stream_zero", st);
         for (int64_t b = 0; b < B; ++b)
             launch(k_fill0, dim3((unsigned)((s.rows + 255) / 256)), dim3(256), 0, st, out + b * out_ld, s.rows);
     }
-    if (d.nwin == 0) return;
-    // several passes only with the input in LDS; otherwise one pass of all B
-    int nb = stream_pass_width(B, s.cols);
-    StreamShape sh = stream_shape(nb, d.nwin, s.cols, true);
-    if (nb < B && !sh.xlds) {
-        nb = (int)B;
-        sh = stream_shape(nb, d.nwin, s.cols, false);
-    }
-    for (int64_t b0 = 0; b0 < B; b0 += nb) {
-        StreamArgs a{d.win.p, d.nwin, d.idx.p, d.val.p, d.ne_row.p, d.ne_start.p, (uint32_t)d.nbytes,
-                     in + b0, (uint32_t)B, sc.ent, sc.row, (uint32_t)s.cols, out + b0 * out_ld, out_ld};
-        ProfScope ps(sh.xlds ? "stream_lds" : "stream", st);
-        launch(stream_kernel(nb, sh.xlds), dim3(sh.grid), dim3(sh.threads), sh.xlds ? sh.lds : 0u, st, a);
+    // input staging: off when forced, forced on when forced or when column
+    // blocks (made for it) or several passes are in use, else automatic
+    const int xmode = force == 0 ? 0 : (force > 0 || K > 1 || nb < B) ? 2 : 1;
+    for (const DStreamBlock &bk : d->blocks) {
+        if (bk.nwin == 0) continue;
+        // several passes only with the input in LDS; otherwise one pass of all B
+        int pnb = nb;
+        StreamShape sh = stream_shape(pnb, bk.nwin, bk.ncols, xmode);
+        if (pnb < B && !sh.xlds) {
+            pnb = (int)B;
+            sh = stream_shape(pnb, bk.nwin, bk.ncols, 0);
+        }
+        for (int64_t b0 = 0; b0 < B; b0 += pnb) {
+            StreamArgs a{d->win.p + bk.win_off, bk.nwin, d->idx.p + bk.off, d->val.p + bk.off,
+                         d->ne_row.p + bk.ne_off, d->ne_start.p + bk.ne_off, (uint32_t)bk.nbytes,
+                         in + bk.c0 * B + b0, (uint32_t)B, sc.ent ? sc.ent + bk.c0 : nullptr, sc.row,
+                         (uint32_t)bk.ncols, out + b0 * out_ld, out_ld};
+            ProfScope ps(sh.xlds ? "stream_lds" : "stream", st);
+            launch(stream_kernel(pnb, sh.xlds), dim3(sh.grid), dim3(sh.threads), sh.xlds ? sh.lds : 0u, st, a);
+        }
     }
     SILI_HIP(hipGetLastError());
 }

@@ -242,14 +242,19 @@ def kernel_counts(hip, L, fn):
     (3000, 1, "1", {"fwd:stream_lds": 1}),
     (3000, 2, "1", {"fwd:stream_lds": 1}),
     (3000, 8, "1", {"fwd:stream_lds": 1}),
-    (6000, 8, "1", {"fwd:stream_lds": 2}),   # input too wide for LDS at 8 columns: 2 passes of 4
+    (6000, 8, "1", {"fwd:stream_lds": 2}),    # input too wide for LDS at 8 columns: 2 column blocks
     (6000, 8, "0", {"fwd:stream": 1}),
     (6000, 4, "0", {"fwd:stream": 1}),
-    (40000, 2, "1", {"fwd:stream": 1}),      # too wide for LDS at any width: through the cache
+    (12000, 4, "-1", {"fwd:stream_lds": 2}),  # automatic choice: 2 column blocks
+    (36000, 2, "1", {"fwd:stream_lds": 2}),
+    (36000, 2, "0", {"fwd:stream": 1}),
+    (42000, 2, "1", {"fwd:stream_lds": 3}),
+    (100000, 8, "-1", {"fwd:stream": 1}),     # more than 16 blocks: through the cache
 ])
 def test_stream_variants(hip, monkeypatch, n_in, B, xlds, want):
-    """Each launch variant (input in LDS or through the cache, one pass or
-    several) against the oracle, the variant read back from the profiler."""
+    """Each launch variant (input in LDS or through the cache, whole rows or
+    column blocks) against the oracle, the variant read back from the
+    profiler."""
     monkeypatch.setenv("SILI_STREAM_XLDS", xlds)
     n_out = 20000 if n_in < 10000 else 800
     L = hip.SparseLinearLayer(n_in, n_out, 1)
@@ -261,3 +266,20 @@ def test_stream_variants(hip, monkeypatch, n_in, B, xlds, want):
     got = kernel_counts(hip, L, lambda: check_fwd(H, L, x, f"synthetic {n_in}x{n_out} B{B}"))
     got = {k: v for k, v in got.items() if k in ("fwd:stream", "fwd:stream_lds")}
     assert got == want, got
+
+
+@pytest.mark.gpu
+def test_stream_column_blocks_designed_rows(hip):
+    """Column blocks over the designed rows (canonical orientation, 60000
+    columns: 2 blocks at batch 1, 13 at batch 8): block boundaries fall
+    inside rows, between multi-byte deltas and in rows with a single entry."""
+    n_out = 60000
+    rows = mixed_rows(n_out, 11)
+    rows += [np.array([4990, 4991, 4992, 9983, 9984]), np.array([59999]), np.array([0, 59999])]
+    H, L = make_pair(hip, rows, n_out)
+    rng = np.random.default_rng(12)
+    for B in (1, 2, 4, 8):
+        x = rng.normal(size=(B, len(rows))).astype(np.float32)
+        g = rng.normal(size=(B, n_out)).astype(np.float32)
+        got = kernel_counts(hip, L, lambda: check_bwd(H, L, x, g, f"blocked dx B{B}"))
+        assert got.get("bwd:stream_lds", 0) >= 2, got
