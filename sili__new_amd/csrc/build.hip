@@ -365,6 +365,8 @@ void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64
     dst.n_split = e.n_split;
     dst.stream1.valid = dst.streamK.valid = false;
     dst.stream1.failed = dst.streamK.failed = false;
+    dst.cblk.clear();
+    dst.cblk_cb = 0;
     dst.rows = rows;
     dst.cols = ncols;
     dst.nnz = N;
@@ -410,6 +412,8 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
     dst.n_split = e.n_split;
     dst.stream1.valid = dst.streamK.valid = false;
     dst.stream1.failed = dst.streamK.failed = false;
+    dst.cblk.clear();
+    dst.cblk_cb = 0;
     dst.rows = src.cols;
     dst.cols = src.rows;
     dst.nnz = N;
@@ -420,6 +424,63 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
     if (N > 0)
         SILI_HIP(hipMemcpyAsync(dst.val.p, tbytes.p, (size_t)N, hipMemcpyDeviceToDevice, st));
     SILI_HIP(hipStreamSynchronize(st));
+}
+
+// Column-block selection: flag entries of block k; gather them with columns
+// relative to the block.
+__global__ void k_cb_flag(const uint32_t *__restrict__ cols, int64_t N, uint32_t cb, uint32_t k,
+                          uint32_t *__restrict__ flag) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i <= N) flag[i] = (i < N && cols[i] / cb == k) ? 1u : 0u;
+}
+__global__ void k_cb_take(const uint32_t *__restrict__ flag, const uint32_t *__restrict__ pos,
+                          const uint32_t *__restrict__ rows, const uint32_t *__restrict__ cols,
+                          const uint8_t *__restrict__ val, int64_t N, uint32_t c0, uint32_t *__restrict__ rk,
+                          uint32_t *__restrict__ ck, uint8_t *__restrict__ vk) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= N || !flag[i]) return;
+    const uint32_t j = pos[i];
+    rk[j] = rows[i];
+    ck[j] = cols[i] - c0;
+    vk[j] = val[i];
+}
+
+void build_colblocks(Layer &L, DScatter &s, int K, int64_t cb) {
+    hipStream_t st = L.stream;
+    const int64_t N = s.nnz;
+    DevBuf<uint32_t> rows, cols, flag, pos, rk, ck, ptrs;
+    DevBuf<uint8_t> vk;
+    rows.ensure((size_t)N + 1);
+    cols.ensure((size_t)N + 1);
+    flag.ensure((size_t)N + 1);
+    pos.ensure((size_t)N + 1);
+    rk.ensure((size_t)N + 1);
+    ck.ensure((size_t)N + 1);
+    vk.ensure((size_t)N + 1);
+    ptrs.ensure((size_t)s.rows + 1);
+    const ScaleView none{nullptr, nullptr, 1};
+    if (N > 0) launch_decode(s.plan(), none, reinterpret_cast<int32_t *>(cols.p), nullptr, rows.p, st);
+    std::vector<DScatter> blocks((size_t)K);
+    for (int k = 0; k < K; ++k) {
+        const int64_t c0 = (int64_t)k * cb, ncols = std::min<int64_t>(cb, s.cols - c0);
+        launch(k_cb_flag, dim3(nblk(N + 1)), dim3(TPB), 0, st, (const uint32_t *)cols.p, N, (uint32_t)cb,
+               (uint32_t)k, flag.p);
+        SILI_HIP(hipGetLastError());
+        device_exclusive_scan_u32(L, flag.p, pos.p, N + 1);
+        uint32_t nk = 0;
+        SILI_HIP(hipMemcpyAsync(&nk, pos.p + N, 4, hipMemcpyDeviceToHost, st));
+        SILI_HIP(hipStreamSynchronize(st));
+        if (N > 0)
+            launch(k_cb_take, dim3(nblk(N)), dim3(TPB), 0, st, (const uint32_t *)flag.p, (const uint32_t *)pos.p,
+                   (const uint32_t *)rows.p, (const uint32_t *)cols.p, (const uint8_t *)s.val.p, N, (uint32_t)c0,
+                   rk.p, ck.p, vk.p);
+        launch(k_ptrs_from_sorted, dim3(nblk(s.rows + 1)), dim3(TPB), 0, st, (const uint32_t *)rk.p, (int64_t)nk,
+               s.rows, ptrs.p);
+        SILI_HIP(hipGetLastError());
+        build_scattered(L, blocks[(size_t)k], s.rows, ncols, (int64_t)nk, ptrs.p, ck.p, vk.p);
+    }
+    s.cblk = std::move(blocks);
+    s.cblk_cb = cb;
 }
 
 // One orientation of block4 from tiles sorted by (major, minor).

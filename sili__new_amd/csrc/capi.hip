@@ -230,6 +230,32 @@ const float *to_feature_major(Layer &L, DevBuf<float> &ws, const float *x, int64
     return ws.p;
 }
 
+}  // namespace
+
+bool gather_colblocked(Layer &L, DScatter &s, const ScaleView &sc, const float *in, int64_t B, float *out,
+                       int64_t out_ld, int skip, hipStream_t st) {
+    // SILI_COLBLOCK (read per call): 0 never, else when the gathered operand
+    // is larger than 4 MiB (one XCD's L2); passes of <= 2 MiB slices
+    const int mode = env_int("SILI_COLBLOCK", 1);
+    if (mode == 0 || s.nnz == 0 || B % 4 != 0 || B > 512 || (reinterpret_cast<uintptr_t>(in) & 15u) != 0) return false;
+    const int64_t opbytes = s.cols * B * 4;
+    if (opbytes <= (int64_t(4) << 20) || opbytes >= (int64_t)0x80000000LL) return false;
+    const int64_t K = std::min<int64_t>(16, (opbytes + (int64_t(2) << 20) - 1) >> 21);
+    const int64_t cb = (s.cols + K - 1) / K;
+    if ((int64_t)s.cblk.size() != K || s.cblk_cb != cb) build_colblocks(L, s, (int)K, cb);
+    for (int64_t k = 0; k < K; ++k) {
+        DScatter &sub = s.cblk[(size_t)k];
+        const int64_t c0 = k * cb;
+        const ScaleView sk{sc.row, sc.ent ? sc.ent + c0 * sc.rank : nullptr, sc.rank};
+        // pass 0 stores (split rows zeroed first), later passes add
+        if (k == 0) launch_zero_split_rows(sub.plan(), out, out_ld, B, st);
+        launch_gather(sub.plan(), sk, in + c0 * B, B, out, out_ld, B, skip, st, k > 0);
+    }
+    return true;
+}
+
+namespace {
+
 void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st) {
     ProfCtx pc(L, "fwd");
     if (B <= 0) throw_error(SILI_ERR_INVALID, "forward_dense: batch must be >= 1");
@@ -246,6 +272,7 @@ void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st
         fill(y, B * L.n_out, 0.0f, st);
     } else if (stream_wanted(L.Wt, ssc, B, B, skip)) {
         stream_gather(L, L.Wt, ssc, xT, B, y, L.n_out, st);
+    } else if (gather_colblocked(L, L.Wt, ssc, xT, B, y, L.n_out, skip, st)) {
     } else {
         launch_zero_split_rows(L.Wt.plan(), y, L.n_out, B, st);
         launch_gather(L.Wt.plan(), ssc, xT, B, y, L.n_out, B, skip, st);
@@ -288,7 +315,8 @@ void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float 
     const bool fused = scat && gw_s &&
                        launch_bwd_fused(L.W.plan(), canon_scales(L), gT, xT, B, dx, L.n_in, gw_s, L.acc_in.p, st);
     if (str) stream_gather(L, L.W, canon_scales(L), gT, B, dx, L.n_in, st);
-    else if (scat && !fused) launch_gather(L.W.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
+    else if (scat && !fused && !gather_colblocked(L, L.W, canon_scales(L), gT, B, dx, L.n_in, SKIP_NONE, st))
+        launch_gather(L.W.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
     if (L.B4.ntiles > 0)
         launch_gather_b4(L.B4.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
     if (scat && gw_s && !fused) launch_sddmm(L.W.plan(), xT, gT, B, gw_s, L.acc_in.p, st);

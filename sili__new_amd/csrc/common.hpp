@@ -180,8 +180,10 @@ struct Block4Plan {
 
 // out[b*out_ld + row] for b < nb: scattered gather (stores; atomics for split
 // rows -- then the caller has zeroed out).  in is feature-major in[c*in_ld + b].
+// accumulate: add to out (batches with nb % 4 == 0 and aligned feature-major
+// input only; used by the column-block passes).
 void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, int64_t in_ld,
-                   float *out, int64_t out_ld, int64_t nb, int skip, hipStream_t st);
+                   float *out, int64_t out_ld, int64_t nb, int skip, hipStream_t st, bool accumulate = false);
 // Block4 contribution, added into out.
 void launch_gather_b4(const Block4Plan &p, const ScaleView &sc, const float *in, int64_t in_ld,
                       float *out, int64_t out_ld, int64_t nb, int skip, hipStream_t st);

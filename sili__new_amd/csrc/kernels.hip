@@ -39,6 +39,7 @@ struct GArgs {
     int64_t out_ld;
     int64_t nb;
     uint32_t in_bytes;  // readable bytes from `in` (buffer range for the fast kernels)
+    int accumulate;     // float4 kernels: add to out instead of storing (column-block passes)
 };
 
 // Per-wave FP4 code -> value table (dequant by lookup).
@@ -532,7 +533,8 @@ constexpr uint32_t ENT_CAP = SEG_BYTES_MAX + 64u;
 template <int BL, int KB>
 __device__ __forceinline__ void store_rows_block(const float4 (&acc)[KB], bool active, uint32_t row,
                                                  bool split, uint32_t nq, float *slice_base,
-                                                 uint32_t slice_stride, float *out, int64_t out_ld) {
+                                                 uint32_t slice_stride, float *out, int64_t out_ld,
+                                                 bool accumulate = false) {
     __shared__ uint32_t s_row[WAVES];
     __shared__ uint32_t s_flag[WAVES];  // bit 0: active, bit 1: split
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
@@ -558,7 +560,7 @@ __device__ __forceinline__ void store_rows_block(const float4 (&acc)[KB], bool a
         const float v = slice_base[w * slice_stride + b];
         float *o = out + (int64_t)b * out_ld + s_row[w];
         if (f & 2u) atomicAdd(o, v);
-        else *o = v;
+        else *o = accumulate ? *o + v : v;  // (a row with one work item: this wave alone writes it)
     }
 }
 
@@ -635,7 +637,8 @@ __global__ __launch_bounds__(256) void k_gather_v4(GArgs a) {
     wave_lds_sync();  // the entry table is reused as this wave's output slice
     }
     store_rows_block<BL, KB>(acc, active, sd.row, (sd.split & SEG_SPLIT) != 0, nq,
-                             reinterpret_cast<float *>(&s_ent[0][0]), ENT_CAP * 2u, a.out, a.out_ld);
+                             reinterpret_cast<float *>(&s_ent[0][0]), ENT_CAP * 2u, a.out, a.out_ld,
+                             a.accumulate != 0);
 }
 
 struct BArgs {
@@ -1975,7 +1978,7 @@ inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 
 }  // namespace
 
 void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, int64_t in_ld,
-                   float *out, int64_t out_ld, int64_t nb_total, int skip, hipStream_t st) {
+                   float *out, int64_t out_ld, int64_t nb_total, int skip, hipStream_t st, bool accumulate) {
     if (p.nseg == 0 || nb_total == 0) return;
     ProfScope ps("gather", st);
     for (int64_t b0 = 0; b0 < nb_total; b0 += 512) {
@@ -1983,7 +1986,9 @@ void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, in
         const int64_t in_bytes = (p.cols * in_ld - b0) * 4;
         const bool small = in_bytes < (int64_t)OOB_OFFSET;
         GArgs a{p.seg, p.nseg, p.idx, p.val, sc, in + b0, in_ld, out + b0 * out_ld, out_ld, nb,
-                small ? (uint32_t)in_bytes : 0u};
+                small ? (uint32_t)in_bytes : 0u, accumulate ? 1 : 0};
+        if (accumulate && !(small && nb % 4 == 0 && in_ld % 4 == 0 && aligned16(a.in)))
+            throw_error(3, "launch_gather: accumulating passes need the float4 kernels");
         const dim3 grid(blocks_for(a.nseg)), block(256);
         if (nb == 1 && small) {
             static const int lane_decode = env_int("SILI_B1_LANE_DECODE", 2);

@@ -78,6 +78,11 @@ struct DScatter {
     DevBuf<uint32_t> split_rows;  // rows with more than one work item
     int64_t n_split = 0;
     DStream stream1, streamK;     // stream copies: whole rows / the last column blocking used
+    // column-block copies for gathers whose operand exceeds one XCD's L2:
+    // cblk[k] holds every row's entries with columns in [k*cblk_cb, ...),
+    // columns relative to the block (built on first use)
+    std::vector<DScatter> cblk;
+    int64_t cblk_cb = 0;
     GatherPlan plan() const {
         return GatherPlan{seg.p, nseg, idx.p, val.p, rows, cols, has_split, split_rows.p, n_split};
     }
@@ -188,6 +193,15 @@ void device_sort_pairs_u32(Layer &L, const uint32_t *kin, uint32_t *kout, const 
                            uint32_t *vout, int64_t n, int bits);
 void device_sort_pairs_u64(Layer &L, const uint64_t *kin, uint64_t *kout, const uint32_t *vin,
                            uint32_t *vout, int64_t n, int bits);
+
+// Column-block copies of s (s.cblk, K blocks of cb columns).
+void build_colblocks(Layer &L, DScatter &s, int K, int64_t cb);
+// out[b*out_ld + row] for b < B over s, in column-block passes when the
+// gathered operand (s.cols x B fp32) exceeds one XCD's L2 (pass 0 stores, the
+// others add; SILI_COLBLOCK=0 disables).  Returns false, launching nothing,
+// when the passes do not apply (then use launch_gather).
+bool gather_colblocked(Layer &L, DScatter &s, const ScaleView &sc, const float *in, int64_t B, float *out,
+                       int64_t out_ld, int skip, hipStream_t st);
 
 // ---- batch-1 stream kernels (stream.hip) ---------------------------------------
 // Whether stream_gather serves this call (batch 1, 2, 4 or 8 with the input
