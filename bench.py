@@ -423,10 +423,10 @@ def run_config4(a, hip, api, rt):
             api.ck(api.L.sili_profile_enable(d["h"], 1))
         step()
         rt.sync()
-        kern = {}
+        kern = {}  # per step (one profiled step; an op may take several launches)
         for d in layers:
             for name, (cnt, tot) in api.profile(d["h"]).items():
-                kern[f"{d['name']}:{name}"] = tot / cnt
+                kern[f"{d['name']}:{name}"] = tot
             api.ck(api.L.sili_profile_enable(d["h"], 0))
         # algorithmic bytes per layer forward (SURVEY 8(d) dense-input fwd)
         alg = {}
@@ -443,7 +443,7 @@ def run_config4(a, hip, api, rt):
                       "achieved_gbs": round(step_bytes / (ms * 1e-3) / 1e9, 2),
                       "pct_hbm_peak": round(100 * step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
                       "steps": steps, "kernels_ms": {k: round(v, 4) for k, v in kern.items()},
-                      "dominant": {"kernel": dom[0], "avg_launch_ms": round(dom[1], 4),
+                      "dominant": {"kernel": dom[0], "op_ms": round(dom[1], 4),
                                    "algorithmic_bytes": alg[dom_layer], "achieved_gbs": round(ach, 2),
                                    "frac": round(ach / HBM_PEAK_GBS, 4)}}
         for d in layers:
@@ -464,7 +464,7 @@ def run_config4(a, hip, api, rt):
         "roofline": {"bound": "hbm", "kernel": r1["dominant"]["kernel"], "achieved": r1["dominant"]["achieved_gbs"],
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": r1["dominant"]["frac"],
                      "traffic": measured_traffic(r1["dominant"]["kernel"], 4),
-                     "avg_launch_ms": r1["dominant"]["avg_launch_ms"],
+                     "op_ms": r1["dominant"]["op_ms"],
                      "algorithmic_bytes": r1["dominant"]["algorithmic_bytes"]},
         "batches": {str(B): r for B, r in results.items()},
         "build_s": round(t_build, 2),
@@ -588,7 +588,9 @@ def main():
     info = pool[0]["L"].info()
     alg = algorithmic(info, n_in, n_out, B, wl)
     dom_name, (dom_cnt, dom_tot) = max(kern.items(), key=lambda kv: kv[1][1])
-    dom_avg_ms = dom_tot / dom_cnt
+    # one op may take several launches (column-block passes): time per op
+    launches = dom_cnt / a.steps
+    dom_avg_ms = dom_tot / a.steps
 
     nnz_s, n_tiles = info["nnz_scattered"], info["n_tiles"]
     units = nnz_s + 16 * n_tiles  # stored synapses (scattered + block4 slots)
@@ -598,7 +600,8 @@ def main():
         achieved = dom_flops / (dom_avg_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "kernel": dom_name, "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 5),
-                "traffic": measured_traffic(dom_name, cfg), "avg_launch_ms": round(dom_avg_ms, 5),
+                "traffic": measured_traffic(dom_name, cfg), "avg_op_ms": round(dom_avg_ms, 5),
+                "launches_per_op": launches,
                 "algorithmic_flops": dom_flops, "algorithmic_bytes": alg.get(dom_name),
                 "note": "fp32 vector FMA work (no MFMA); peak is MI355X dense fp32"}
         step_bytes = alg["fwd:gather_b4"] + alg["bwd:gather_b4"] + alg["bwd:sddmm_b4"]
@@ -609,8 +612,8 @@ def main():
         roof = {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 2) if achieved else None,
                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 5) if achieved else None,
-                "traffic": measured_traffic(dom_name, cfg), "avg_launch_ms": round(dom_avg_ms, 5),
-                "algorithmic_bytes": dom_bytes}
+                "traffic": measured_traffic(dom_name, cfg), "avg_op_ms": round(dom_avg_ms, 5),
+                "launches_per_op": launches, "algorithmic_bytes": dom_bytes}
         if cfg == 0:
             step_bytes = alg["fwd:gather"]
             flops = 2 * units * B

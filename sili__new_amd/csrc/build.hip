@@ -505,11 +505,63 @@ static void build_b4_orientation(Layer &L, DBlock4 &dst, int64_t N, int64_t brow
     dst.nseg = e.nseg;
     dst.has_split = e.has_split;
     dst.tiles.ensure((size_t)N * 16u + 64);
+    dst.cblk.clear();
+    dst.cblk_cbb = 0;
     if (N > 0) {
         launch(k_gather_tiles, dim3(nblk(N)), dim3(TPB), 0, st, d_src_tiles, d_perm, N,
                            transpose ? 1 : 0, dst.tiles.p);
         SILI_HIP(hipGetLastError());
     }
+}
+
+// Tiles of block k (minor in [k*cbb, (k+1)*cbb)): major, relative minor and
+// storage index, compacted in storage order.
+__global__ void k_cb4_take(const uint32_t *__restrict__ flag, const uint32_t *__restrict__ pos,
+                           const uint32_t *__restrict__ major, const uint32_t *__restrict__ minor, int64_t N,
+                           uint32_t m0, uint32_t *__restrict__ mk, uint32_t *__restrict__ nk,
+                           uint32_t *__restrict__ pk) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= N || !flag[i]) return;
+    const uint32_t j = pos[i];
+    mk[j] = major[i];
+    nk[j] = minor[i] - m0;
+    pk[j] = (uint32_t)i;
+}
+
+void build_colblocks_b4(Layer &L, DBlock4 &b, int K, int64_t cbb) {
+    hipStream_t st = L.stream;
+    const int64_t N = b.ntiles;
+    DevBuf<uint32_t> major, minor, flag, pos, mk, nk, pk;
+    major.ensure((size_t)N + 1);
+    minor.ensure((size_t)N + 1);
+    flag.ensure((size_t)N + 1);
+    pos.ensure((size_t)N + 1);
+    mk.ensure((size_t)N + 1);
+    nk.ensure((size_t)N + 1);
+    pk.ensure((size_t)N + 1);
+    if (N > 0) launch_decode_b4(b.plan(), major.p, minor.p, st);
+    std::vector<DBlock4> blocks((size_t)K);
+    for (int k = 0; k < K; ++k) {
+        const int64_t m0 = (int64_t)k * cbb;
+        const int64_t nbc = std::min<int64_t>(cbb, b.bcols - m0);
+        const int64_t c0 = m0 * 4, ncols = std::min<int64_t>(nbc * 4, b.cols - c0);
+        launch(k_cb_flag, dim3(nblk(N + 1)), dim3(TPB), 0, st, (const uint32_t *)minor.p, N, (uint32_t)cbb,
+               (uint32_t)k, flag.p);
+        SILI_HIP(hipGetLastError());
+        device_exclusive_scan_u32(L, flag.p, pos.p, N + 1);
+        uint32_t nt = 0;
+        SILI_HIP(hipMemcpyAsync(&nt, pos.p + N, 4, hipMemcpyDeviceToHost, st));
+        SILI_HIP(hipStreamSynchronize(st));
+        if (N > 0)
+            launch(k_cb4_take, dim3(nblk(N)), dim3(TPB), 0, st, (const uint32_t *)flag.p, (const uint32_t *)pos.p,
+                   (const uint32_t *)major.p, (const uint32_t *)minor.p, N, (uint32_t)m0, mk.p, nk.p, pk.p);
+        SILI_HIP(hipGetLastError());
+        build_b4_orientation(L, blocks[(size_t)k], (int64_t)nt, b.brows, nbc, b.rows, ncols, mk.p, nk.p, pk.p,
+                             b.tiles.p, false);
+    }
+    SILI_HIP(hipStreamSynchronize(st));
+    b.cblk = std::move(blocks);
+    b.cblk_cbb = cbb;
 }
 
 void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_t *d_bc,

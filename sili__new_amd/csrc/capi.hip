@@ -235,12 +235,16 @@ const float *to_feature_major(Layer &L, DevBuf<float> &ws, const float *x, int64
 bool gather_colblocked(Layer &L, DScatter &s, const ScaleView &sc, const float *in, int64_t B, float *out,
                        int64_t out_ld, int skip, hipStream_t st) {
     // SILI_COLBLOCK (read per call): 0 never, else when the gathered operand
-    // is larger than 4 MiB (one XCD's L2); passes of <= 2 MiB slices
+    // is larger than 4 MiB (one XCD's L2); passes of <= SILI_COLBLOCK_MB
+    // (default 2 MiB: measured on c4's down layer at batch 128, 8 passes of
+    // 2 MiB beat 4 of 4 MiB and 2 of 8 MiB)
     const int mode = env_int("SILI_COLBLOCK", 1);
     if (mode == 0 || s.nnz == 0 || B % 4 != 0 || B > 512 || (reinterpret_cast<uintptr_t>(in) & 15u) != 0) return false;
     const int64_t opbytes = s.cols * B * 4;
     if (opbytes <= (int64_t(4) << 20) || opbytes >= (int64_t)0x80000000LL) return false;
-    const int64_t K = std::min<int64_t>(16, (opbytes + (int64_t(2) << 20) - 1) >> 21);
+    const int64_t slice = (int64_t)std::max(1, env_int("SILI_COLBLOCK_MB", 2)) << 20;
+    const int64_t K = std::min<int64_t>(16, (opbytes + slice - 1) / slice);
+    if (K < 2) return false;
     const int64_t cb = (s.cols + K - 1) / K;
     if ((int64_t)s.cblk.size() != K || s.cblk_cb != cb) build_colblocks(L, s, (int)K, cb);
     for (int64_t k = 0; k < K; ++k) {
@@ -250,6 +254,31 @@ bool gather_colblocked(Layer &L, DScatter &s, const ScaleView &sc, const float *
         // pass 0 stores (split rows zeroed first), later passes add
         if (k == 0) launch_zero_split_rows(sub.plan(), out, out_ld, B, st);
         launch_gather(sub.plan(), sk, in + c0 * B, B, out, out_ld, B, skip, st, k > 0);
+    }
+    return true;
+}
+
+bool gather_b4_colblocked(Layer &L, DBlock4 &b, const ScaleView &sc, const float *in, int64_t B, float *out,
+                          int64_t out_ld, int skip, hipStream_t st) {
+    // as gather_colblocked; the block4 gathers add into out, so every pass
+    // adds.  Slices of SILI_COLBLOCK_B4_MB (default 8 MiB: measured on c3,
+    // 2 passes of 8 MiB beat 4 of 4 MiB, 8 of 2 MiB and one of 16 MiB; shorter
+    // block rows per pass cost more than the cache misses they save)
+    const int mode = env_int("SILI_COLBLOCK", 1);
+    if (mode == 0 || b.ntiles == 0 || skip != SKIP_NONE || B % 4 != 0 ||
+        (reinterpret_cast<uintptr_t>(in) & 15u) != 0)
+        return false;
+    const int64_t opbytes = b.cols * B * 4;
+    if (opbytes <= (int64_t(4) << 20) || opbytes >= (int64_t)0x80000000LL) return false;
+    const int64_t slice = (int64_t)std::max(1, env_int("SILI_COLBLOCK_B4_MB", 8)) << 20;
+    const int64_t K = std::min<int64_t>(16, (opbytes + slice - 1) / slice);
+    if (K < 2) return false;
+    const int64_t cbb = (b.bcols + K - 1) / K;
+    if ((int64_t)b.cblk.size() != K || b.cblk_cbb != cbb) build_colblocks_b4(L, b, (int)K, cbb);
+    for (int64_t k = 0; k < K; ++k) {
+        const int64_t c0 = k * cbb * 4;
+        const ScaleView sk{sc.row, sc.ent ? sc.ent + c0 * sc.rank : nullptr, sc.rank};
+        launch_gather_b4(b.cblk[(size_t)k].plan(), sk, in + c0 * B, B, out, out_ld, B, skip, st);
     }
     return true;
 }
@@ -277,7 +306,7 @@ void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st
         launch_zero_split_rows(L.Wt.plan(), y, L.n_out, B, st);
         launch_gather(L.Wt.plan(), ssc, xT, B, y, L.n_out, B, skip, st);
     }
-    if (L.B4t.ntiles > 0)
+    if (L.B4t.ntiles > 0 && !gather_b4_colblocked(L, L.B4t, shadow_scales(L), xT, B, y, L.n_out, SKIP_NONE, st))
         launch_gather_b4(L.B4t.plan(), shadow_scales(L), xT, B, y, L.n_out, B, SKIP_NONE, st);
 }
 
@@ -317,7 +346,7 @@ void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float 
     if (str) stream_gather(L, L.W, canon_scales(L), gT, B, dx, L.n_in, st);
     else if (scat && !fused && !gather_colblocked(L, L.W, canon_scales(L), gT, B, dx, L.n_in, SKIP_NONE, st))
         launch_gather(L.W.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
-    if (L.B4.ntiles > 0)
+    if (L.B4.ntiles > 0 && !gather_b4_colblocked(L, L.B4, canon_scales(L), gT, B, dx, L.n_in, SKIP_NONE, st))
         launch_gather_b4(L.B4.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
     if (scat && gw_s && !fused) launch_sddmm(L.W.plan(), xT, gT, B, gw_s, L.acc_in.p, st);
     if (gw_b && L.B4.ntiles > 0) launch_sddmm_b4(L.B4.plan(), nullptr, xT, gT, B, gw_b, st);

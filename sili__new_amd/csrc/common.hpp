@@ -25,7 +25,7 @@
 
 namespace sili {
 
-// Integer tuning knob from the environment (read by callers once, into statics).
+// Integer tuning knob from the environment.
 inline int env_int(const char *name, int dflt) {
     const char *e = std::getenv(name);
     return e ? std::atoi(e) : dflt;

@@ -1133,7 +1133,10 @@ __global__ __launch_bounds__(256) void k_gather_b4_v4(BArgs a, uint32_t in_bytes
                 }
                 reinterpret_cast<float4 *>(sw + ch.rank * 16u)[lj] = make_float4(wv[0], wv[1], wv[2], wv[3]);
             }
-        } else if (lane >= n && lane < npad) {
+        }
+        // padding slots n .. npad-1 (a terminator lane can sit at or past n when
+        // a varint spans several bytes, so every lane checks)
+        if (lane >= n && lane < npad) {
             // padding tiles: out-of-range rows (read 0), zero weights
             s_off[wave][lane] = OOB_OFFSET;
 #pragma unroll
@@ -1277,7 +1280,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6))) void k
                 }
                 reinterpret_cast<float4 *>(sw + ch.rank * 16u)[j] = make_float4(wv[0], wv[1], wv[2], wv[3]);
             }
-        } else if (lane >= n && lane < npad) {
+        }
+        // padding slots n .. npad-1 (a terminator lane can sit at or past n when
+        // a varint spans several bytes, so every lane checks)
+        if (lane >= n && lane < npad) {
             s_off[wave][lane] = OOB_OFFSET;
 #pragma unroll
             for (int j = 0; j < 4; ++j)
@@ -1396,7 +1402,10 @@ __global__ __launch_bounds__(256) void k_gather_b4_mfma(BArgs a, uint32_t in_byt
 #pragma unroll
             for (int li = 0; li < 4; ++li)
                 reinterpret_cast<float4 *>(sw + ch.rank * 16u)[li] = make_float4(wm[li][0], wm[li][1], wm[li][2], wm[li][3]);
-        } else if (lane >= n && lane < npad) {
+        }
+        // padding slots n .. npad-1 (a terminator lane can sit at or past n when
+        // a varint spans several bytes, so every lane checks)
+        if (lane >= n && lane < npad) {
             s_off[wave][lane] = OOB_OFFSET;
 #pragma unroll
             for (int li = 0; li < 4; ++li)
@@ -2082,10 +2091,10 @@ void launch_gather_b4(const Block4Plan &p, const ScaleView &sc, const float *in,
         const int64_t nq = nb_total / 4;
         const unsigned gx = blocks_for(p.nseg);
         const unsigned gy16 = (unsigned)((nq + 15) / 16);
-        static const int use_mfma = env_int("SILI_B4_MFMA", 0);
+        const int use_mfma = env_int("SILI_B4_MFMA", 0);  // (knobs read per call)
         if (use_mfma && nq >= 12) {
             // matrix cores: 64 batch columns per wave (SILI_B4_MFMA=0: vector path)
-            static const int u = env_int("SILI_B4_MFMA_U", 2);
+            const int u = env_int("SILI_B4_MFMA_U", 2);
             if (u >= 4) launch((k_gather_b4_mfma<4>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
             else if (u >= 2) launch((k_gather_b4_mfma<2>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
             else launch((k_gather_b4_mfma<1>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
@@ -2096,7 +2105,7 @@ void launch_gather_b4(const Block4Plan &p, const ScaleView &sc, const float *in,
         } else {
             // 64 batch columns per wave; lanes per tile and tiles in flight
             // (SILI_B4_BL / SILI_B4_U)
-            static const int bl = env_int("SILI_B4_BL", 16), u = env_int("SILI_B4_U", 2);
+            const int bl = env_int("SILI_B4_BL", 16), u = env_int("SILI_B4_U", 2);
             const unsigned gy8 = (unsigned)((nq + 7) / 8);
             if (bl == 32 && u >= 4) launch((k_gather_b4_v4<8, 1, 4>), dim3(gx, gy8), dim3(256), 0, st, a, (uint32_t)in_bytes);
             else if (bl == 32) launch((k_gather_b4_v4<8, 1, 2>), dim3(gx, gy8), dim3(256), 0, st, a, (uint32_t)in_bytes);
@@ -2207,7 +2216,7 @@ void launch_sddmm_b4(const Block4Plan &p, const uint32_t *, const float *xT, con
         aligned16(gw)) {
         const dim3 grid(blocks_for(p.nseg)), block(256);
         const int64_t nq = B / 4;
-        static const int use_mfma = env_int("SILI_B4_MFMA", 0);
+        const int use_mfma = env_int("SILI_B4_MFMA", 0);  // (knobs read per call)
         if (use_mfma && nq >= 8) {
             if (nq <= 16) launch((k_sddmm_b4_mfma<1, 2>), grid, block, 0, st, a, (uint32_t)gT_bytes);
             else if (nq <= 32) launch((k_sddmm_b4_mfma<2, 2>), grid, block, 0, st, a, (uint32_t)gT_bytes);

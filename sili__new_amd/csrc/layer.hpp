@@ -97,6 +97,9 @@ struct DBlock4 {
     DevBuf<uint8_t> idx;
     DevBuf<uint8_t> tiles;                    // 16 * ntiles
     DevBuf<SegDesc> seg;
+    // column-block copies (as DScatter::cblk, in block columns of cblk_cbb)
+    std::vector<DBlock4> cblk;
+    int64_t cblk_cbb = 0;
     Block4Plan plan() const {
         return Block4Plan{seg.p, nseg, idx.p, tiles.p, rows, cols, has_split};
     }
@@ -194,8 +197,15 @@ void device_sort_pairs_u32(Layer &L, const uint32_t *kin, uint32_t *kout, const 
 void device_sort_pairs_u64(Layer &L, const uint64_t *kin, uint64_t *kout, const uint32_t *vin,
                            uint32_t *vout, int64_t n, int bits);
 
-// Column-block copies of s (s.cblk, K blocks of cb columns).
+// Column-block copies of s (s.cblk, K blocks of cb columns; block4: cbb
+// block columns).
 void build_colblocks(Layer &L, DScatter &s, int K, int64_t cb);
+void build_colblocks_b4(Layer &L, DBlock4 &b, int K, int64_t cbb);
+// Block4 contribution (added into out) in column-block passes when the
+// gathered operand exceeds 4 MiB (slices of SILI_COLBLOCK_B4_MB, default 8);
+// false: not applicable (then use launch_gather_b4).
+bool gather_b4_colblocked(Layer &L, DBlock4 &b, const ScaleView &sc, const float *in, int64_t B, float *out,
+                          int64_t out_ld, int skip, hipStream_t st);
 // out[b*out_ld + row] for b < B over s, in column-block passes when the
 // gathered operand (s.cols x B fp32) exceeds one XCD's L2 (pass 0 stores, the
 // others add; SILI_COLBLOCK=0 disables).  Returns false, launching nothing,

@@ -61,3 +61,30 @@ def test_backward_column_blocks_designed_rows(hip):
                                f"colblock dx {rep}")
         counts = kernel_counts(hip, L, run)
         assert counts.get("bwd:gather") == 3, counts
+
+
+@pytest.mark.parametrize("n_in,n_out,op", [(16383, 301, "fwd"), (301, 16383, "bwd")])
+def test_block4_column_blocks(hip, monkeypatch, n_in, n_out, op):
+    """Block4 gathers (plus scattered synapses outside the tiles) in column-block
+    passes: forward over a 16383-wide input, grad-input over a 16383-wide
+    gradient, batch 128 (8 MB operand: 4 passes of 2 MiB slices), edge tiles
+    at the last block."""
+    monkeypatch.setenv("SILI_COLBLOCK_B4_MB", "2")
+    from tests.test_gpu_parity import _edge_block4_layer
+    br, bc, tiles, ptrs, cols, q, vs = _edge_block4_layer(n_in, n_out, 7, density=0.05)
+    H = HostLayer(n_in, n_out).load_csr(ptrs, cols, w=q).load_tiles(br, bc, tiles).set_scales(vs)
+    L = hip.SparseLinearLayer(n_in, n_out, len(cols) + 16 * len(br) + 64)
+    L.load_weights(ptrs, cols, q)
+    L.load_block4_tiles(br, bc, tiles)
+    L.set_value_scales(vs)
+    rng = np.random.default_rng(8)
+    x = rng.normal(size=(128, n_in)).astype(np.float32)
+    g = rng.normal(size=(128, n_out)).astype(np.float32)
+
+    def run():
+        y = L.forward_dense(x)
+        assert_close_terms(y, H.forward_dense(x), H.forward_dense(x, absmode=True), "b4 colblock fwd")
+        dx = L.backward_dense(g, 0.0)
+        assert_close_terms(dx, H.backward_dense(x, g)[0], H.backward_dense(x, g, absmode=True)[0], "b4 colblock dx")
+    counts = kernel_counts(hip, L, run)
+    assert counts.get(f"{op}:gather_b4") == 4, counts
