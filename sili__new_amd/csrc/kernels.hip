@@ -40,6 +40,7 @@ struct GArgs {
     int64_t nb;
     uint32_t in_bytes;  // readable bytes from `in` (buffer range for the fast kernels)
     int accumulate;     // float4 kernels: add to out instead of storing (column-block passes)
+    int xcd;            // float4 kernels: XCD-contiguous block order (xcd_block)
 };
 
 // Per-wave FP4 code -> value table (dequant by lookup).
@@ -574,7 +575,8 @@ __global__ __launch_bounds__(256) void k_gather_v4(GArgs a) {
     constexpr uint32_t G = 64u / BL;
     constexpr uint32_t STEP = G * U;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
+    const uint32_t bid = a.xcd ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
+    const int64_t si = (int64_t)bid * WAVES + wave;
     const bool active = si < a.nseg;  // inactive waves still join the block epilogue
     const uint32_t g = lane / BL, bl = lane % BL;
     const uint32_t nq = (uint32_t)(a.nb >> 2);
@@ -933,6 +935,7 @@ struct FArgs {
     int64_t dx_ld;
     float *gw;          // one value per stored synapse, elem order
     float *acc_in;      // optional: acc_in[row] += sum_b |xT[row,b]|
+    int xcd;            // XCD-contiguous block order (xcd_block)
 };
 
 // Fused grad-input + nnz-sampled grad-W over the canonical store: one decode
@@ -950,7 +953,8 @@ __global__ __launch_bounds__(256) void k_bwd_v4(FArgs a) {
     constexpr uint32_t G = 64u / BL;
     constexpr uint32_t STEP = G * U;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
+    const uint32_t bid = a.xcd ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
+    const int64_t si = (int64_t)bid * WAVES + wave;
     const bool active = si < a.nseg;  // inactive waves still join the block epilogue
     const uint32_t g = lane / BL, bl = lane % BL;
     const uint32_t nq = (uint32_t)(a.B >> 2);
@@ -1984,6 +1988,12 @@ void gather_v4_skip(const GArgs &a, int skip, hipStream_t st) {
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// SILI_XCD_ORDER (read per call): 1 the float4 segment kernels take their
+// blocks in XCD-contiguous order (xcd_block), 0 in launch order.  Default:
+// on for the fused backward (c1: 26.2 -> 25.7 us), off for the gathers
+// (no gain at batch 64; c4's batch-128 gathers lose 14%).
+inline int xcd_order(int dflt) { return env_int("SILI_XCD_ORDER", dflt) ? 1 : 0; }
+
 }  // namespace
 
 void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, int64_t in_ld,
@@ -1995,7 +2005,7 @@ void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, in
         const int64_t in_bytes = (p.cols * in_ld - b0) * 4;
         const bool small = in_bytes < (int64_t)OOB_OFFSET;
         GArgs a{p.seg, p.nseg, p.idx, p.val, sc, in + b0, in_ld, out + b0 * out_ld, out_ld, nb,
-                small ? (uint32_t)in_bytes : 0u, accumulate ? 1 : 0};
+                small ? (uint32_t)in_bytes : 0u, accumulate ? 1 : 0, xcd_order(0)};
         if (accumulate && !(small && nb % 4 == 0 && in_ld % 4 == 0 && aligned16(a.in)))
             throw_error(3, "launch_gather: accumulating passes need the float4 kernels");
         const dim3 grid(blocks_for(a.nseg)), block(256);
@@ -2178,7 +2188,8 @@ bool launch_bwd_fused(const GatherPlan &p, const ScaleView &sc, const float *gT,
         return false;
     if (p.nseg == 0) return true;
     ProfScope ps("gather_gradw", st);
-    FArgs a{p.seg, p.nseg, p.idx, p.val, sc, gT, (uint32_t)gT_bytes, xT, B, dx, dx_ld, gw, acc_in};
+    FArgs a{p.seg, p.nseg, p.idx, p.val, sc, gT, (uint32_t)gT_bytes, xT, B, dx, dx_ld, gw, acc_in,
+            xcd_order(1)};
     const dim3 grid(blocks_for(p.nseg)), block(256);
     const int64_t nq = B / 4;
     if (nq <= 1) launch((k_bwd_v4<1, 1, 4>), grid, block, 0, st, a);

@@ -215,54 +215,78 @@ struct StreamArgs {
     const uint8_t *idx, *val;    // padded stream
     const uint32_t *ne_row, *ne_start;
     uint32_t nbytes;
+    uint32_t n_ne;               // non-empty rows (the lists hold n_ne + 1)
     const float *in;             // in[c * in_ld + j], c < nx, j < NB (this pass)
     uint32_t in_ld;
     const float *ent;            // column scale (NULL: ones)
     const float *rsc;            // row scale (NULL: ones)
     uint32_t nx;
+    uint32_t rows;               // rows of the store
     float *out;                  // out[j * out_ld + row], zeroed beforehand
     int64_t out_ld;
 };
 
-// Registers of one window: its descriptor and the next one's rs_lo, the
-// lane's 16 index and 16 value bytes, the index dword before the window
-// (lane 0), and one (first byte, row) of the non-empty rows starting in it.
-struct WinRegs {
-    WinDesc m;
-    uint32_t rs_hi;
+// Buffer resources of one launch.  Every memory access of the window loop is
+// a buffer access whose out-of-range offsets read 0 (atomics: are dropped),
+// so each pass of the loop issues the same loads on every path and the
+// compiler's wait counts stay exact: a window's loads are waited for one
+// window after they were issued, never together with the next window's.
+struct StreamRsrc {
+    __amdgpu_buffer_rsrc_t idx, val, nes, ner, win, rsc, out, in, ent;
+};
+
+__device__ __forceinline__ uint4 buffer_load_u4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ uint32_t buffer_load_u1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+}
+
+// A window's descriptor, uniform: row0, carry, rs_lo, and the next window's
+// rs_lo (rs_hi).
+struct WinMeta {
+    uint32_t row0, carry, rs_lo, rs_hi;
+};
+// The same as loaded (per lane, before readfirstlane).
+struct WinRaw {
+    uint4 d;
+    uint32_t hi;
+};
+// One window's per-lane loads: the lane's 16 index and 16 value bytes, the
+// index dword before the window (0 for the first), and for lanes below
+// rs_hi - rs_lo one of the non-empty rows starting in the window (its first
+// byte and row; 0 on other lanes).
+struct WinData {
     uint32_t i[4], v[4], ip;
     uint32_t Rs, Rr;
 };
 
-__device__ __forceinline__ WinDesc uniform_win(const uint4 q) {
-    return WinDesc{uniform(q.x), uniform(q.y), uniform(q.z), uniform(q.w)};
+__device__ __forceinline__ void issue_meta(const StreamRsrc &r, int64_t w, WinRaw &q) {
+    q.d = buffer_load_u4(r.win, (uint32_t)w * 16u);
+    q.hi = buffer_load_u1(r.win, (uint32_t)(w + 1) * 16u + 8u);
 }
-__device__ __forceinline__ uint4 load_win_raw(const WinDesc *p) { return *reinterpret_cast<const uint4 *>(p); }
-__device__ __forceinline__ uint4 buffer_load_u4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+__device__ __forceinline__ WinMeta uniform_meta(const WinRaw &q) {
+    return WinMeta{uniform(q.d.x), uniform(q.d.y), uniform(q.d.z), uniform(q.hi)};
 }
-
-// Issue the loads of window w (descriptors already in r.m / r.rs_hi).
-__device__ __forceinline__ void load_window(const StreamArgs &a, int64_t w, WinRegs &r) {
+// Windows at or past nwin read zeros (no rows, no bytes).
+__device__ __forceinline__ void issue_data(const StreamRsrc &r, int64_t w, const WinMeta &m, WinData &d) {
     const uint32_t lane = lane_id();
     const uint32_t b0 = (uint32_t)w * WIN_BYTES;
-    const uint32_t nb = min(a.nbytes - b0, WIN_BYTES);
-    // 16-byte aligned; lanes past the stream's end read 0, bytes at or past
-    // nb are masked by the decode
-    const uint4 iw = buffer_load_u4(buffer_rsrc(a.idx + b0, nb + 16u), BPL * lane);
-    const uint4 vw = buffer_load_u4(buffer_rsrc(a.val + b0, nb + 16u), BPL * lane);
-    r.i[0] = iw.x;
-    r.i[1] = iw.y;
-    r.i[2] = iw.z;
-    r.i[3] = iw.w;
-    r.v[0] = vw.x;
-    r.v[1] = vw.y;
-    r.v[2] = vw.z;
-    r.v[3] = vw.w;
-    r.ip = (lane == 0u && b0 > 0u) ? *reinterpret_cast<const uint32_t *>(a.idx + b0 - 4u) : 0u;
-    const uint32_t nr = r.rs_hi - r.m.rs_lo;  // non-empty rows starting here (<= 64)
-    r.Rs = lane < nr ? a.ne_start[r.m.rs_lo + lane] : 0u;
-    r.Rr = lane < nr ? a.ne_row[r.m.rs_lo + lane] : 0u;
+    const uint4 iw = buffer_load_u4(r.idx, b0 + BPL * lane);
+    const uint4 vw = buffer_load_u4(r.val, b0 + BPL * lane);
+    d.i[0] = iw.x;
+    d.i[1] = iw.y;
+    d.i[2] = iw.z;
+    d.i[3] = iw.w;
+    d.v[0] = vw.x;
+    d.v[1] = vw.y;
+    d.v[2] = vw.z;
+    d.v[3] = vw.w;
+    d.ip = buffer_load_u1(r.idx, b0 ? b0 - 4u : OOB_OFFSET);
+    const uint32_t nr = m.rs_hi - m.rs_lo;  // non-empty rows starting here (<= 64)
+    const uint32_t o = lane < nr ? (m.rs_lo + lane) * 4u : OOB_OFFSET;
+    d.Rs = buffer_load_u1(r.nes, o);
+    d.Rr = buffer_load_u1(r.ner, o);
 }
 
 // Weight code of value byte K (0..3) of dw: the high nibble.  The conversion
@@ -286,11 +310,12 @@ struct XVec {
 };
 
 // The NB inputs at shifted column c (0: the zero slot).  XLDS: slot c holds
-// NB floats; otherwise buffer loads of in[(c - 1) * in_ld + j] (c = 0 wraps
-// out of range and reads 0).
+// NB floats; otherwise buffer loads of in[(c - 1) * in_ld + j] times the
+// column scale (c = 0 wraps out of range and reads 0; the scale load is made
+// even without scales, against a zero-sized range).
 template <int NB, bool XLDS>
-__device__ __forceinline__ XVec<NB> stream_x(const StreamArgs &a, const float *s_x, __amdgpu_buffer_rsrc_t rin,
-                                             __amdgpu_buffer_rsrc_t rent, uint32_t c) {
+__device__ __forceinline__ XVec<NB> stream_x(const StreamArgs &a, const StreamRsrc &r, const float *s_x,
+                                             uint32_t c) {
     XVec<NB> x;
     if constexpr (XLDS) {
         const float *p = s_x + c * NB;
@@ -315,7 +340,7 @@ __device__ __forceinline__ XVec<NB> stream_x(const StreamArgs &a, const float *s
         if constexpr (NB >= 4) {
 #pragma unroll
             for (int q = 0; q < NB / 4; ++q) {
-                const float4 t = buffer_load_f4(rin, off + 16u * (uint32_t)q);
+                const float4 t = buffer_load_f4(r.in, off + 16u * (uint32_t)q);
                 x.v[4 * q] = t.x;
                 x.v[4 * q + 1] = t.y;
                 x.v[4 * q + 2] = t.z;
@@ -323,10 +348,10 @@ __device__ __forceinline__ XVec<NB> stream_x(const StreamArgs &a, const float *s
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < NB; ++j) x.v[j] = buffer_load_f1(rin, off + 4u * (uint32_t)j);
+            for (int j = 0; j < NB; ++j) x.v[j] = buffer_load_f1(r.in, off + 4u * (uint32_t)j);
         }
+        const float e = buffer_load_f1(r.ent, (c - 1u) * 4u);
         if (a.ent) {
-            const float e = buffer_load_f1(rent, (c - 1u) * 4u);
 #pragma unroll
             for (int j = 0; j < NB; ++j) x.v[j] *= e;
         }
@@ -356,25 +381,32 @@ __device__ __forceinline__ void wave_seg_scan_n(float (&v)[NB], uint32_t f) {
     seg_step_n<NB, DPP_ROW_BCAST31, 0xC>(v, f);
 }
 
+// Window w (descriptor m, loads d): out[j*out_ld + row] += its row pieces.
+// Between the work that needs d and the multiply-adds it issues the loads of
+// window wn (descriptor from qn, into mN / dN) and the descriptor loads of
+// window wn2 (into qn).  FAST: every byte is a one-byte varint and none
+// continues from the window before.
 template <int NB, bool XLDS, bool FAST>
-__device__ __forceinline__ void run_window(const StreamArgs &a, int64_t w, const WinRegs &r, uint32_t *slot,
-                                           const float *s_x, __amdgpu_buffer_rsrc_t rin,
-                                           __amdgpu_buffer_rsrc_t rent) {
+__device__ __forceinline__ void run_window(const StreamArgs &a, const StreamRsrc &r, int64_t w, const WinMeta &m,
+                                           const WinData &d, int64_t wn, int64_t wn2, WinRaw &qn, WinMeta &mN,
+                                           WinData &dN, uint32_t *slot, const float *s_x) {
     const uint32_t lane = lane_id();
     const uint32_t b0 = (uint32_t)w * WIN_BYTES;
-    const uint32_t nr = r.rs_hi - r.m.rs_lo;
+    const uint32_t nr = m.rs_hi - m.rs_lo;
 
     // rows starting in the window -> the lane holding their first 16 bytes
     slot[lane] = SLOT_NONE;
     wave_lds_sync();
-    if (lane < nr) slot[(r.Rs - b0) / BPL] = r.Rr;
+    if (lane < nr) slot[(d.Rs - b0) / BPL] = d.Rr;
     wave_lds_sync();
     const uint32_t sl = slot[lane];
     const bool hs = sl != SLOT_NONE;
     const uint64_t S = __ballot(hs);
     // the lane's row: the latest row start at or before it (rows ascend)
     const uint32_t mrow = wave_max_scan(hs ? sl + 1u : 0u);
-    const uint32_t row = mrow ? mrow - 1u : r.m.row0;
+    const uint32_t row = mrow ? mrow - 1u : m.row0;
+    // its row scale (used by the last lane of each row piece)
+    const float rsv = buffer_load_f1(r.rsc, row * 4u);
 
     // deltas of the entries ending at each byte (0 where no entry ends)
     uint32_t full = 0;
@@ -382,12 +414,12 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, int64_t w, const
     uint32_t tmask = 0xFFFFu;
     if constexpr (FAST) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) full = __builtin_amdgcn_sad_u8(r.i[k], 0u, full);
+        for (int k = 0; k < 4; ++k) full = __builtin_amdgcn_sad_u8(d.i[k], 0u, full);
     } else {
         const uint32_t nb = min(a.nbytes - b0, WIN_BYTES);
         // the previous 4 bytes: the previous lane's, or those before the window
-        const uint32_t pw0 = (uint32_t)__shfl_up((int)r.i[3], 1, 64);
-        const uint32_t pw = lane ? pw0 : r.ip;
+        const uint32_t pw0 = (uint32_t)__shfl_up((int)d.i[3], 1, 64);
+        const uint32_t pw = lane ? pw0 : d.ip;
         uint32_t k = 0;  // trailing continuation bytes before this lane (a varint ending here)
 #pragma unroll
         for (int i = 3; i >= 0; --i) {
@@ -404,7 +436,7 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, int64_t w, const
         tmask = 0;
 #pragma unroll
         for (int i = 0; i < (int)BPL; ++i) {
-            const uint32_t b = (r.i[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+            const uint32_t b = (d.i[i >> 2] >> (8 * (i & 3))) & 0xFFu;
             const bool valid = BPL * lane + (uint32_t)i < nb;
             acc |= (b & 0x7Fu) << (shift < 32u ? shift : 0u);
             const bool term = valid && (b & 0x80u) == 0u;
@@ -419,38 +451,80 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, int64_t w, const
     // shifted column entering the lane: segmented scan of the lanes' delta
     // sums (a lane with a row start begins from 0; the window's first
     // segment continues from the carried column)
-    const uint32_t K = wave_seg_scan(full + ((lane == 0u && !hs) ? r.m.carry : 0u), hs ? 1u : 0u);
+    const uint32_t K = wave_seg_scan(full + ((lane == 0u && !hs) ? m.carry : 0u), hs ? 1u : 0u);
     const uint32_t kprev = wave_prev_u32(K);
-    uint32_t col = hs ? 0u : (lane ? kprev : r.m.carry);
+    const uint32_t col0 = hs ? 0u : (lane ? kprev : m.carry);
+
+    // inputs through the cache (one or two columns): loaded before the next
+    // window's loads are issued, so waiting for them does not wait for those
+    constexpr bool EARLY = !XLDS && NB <= 2;
+    XVec<NB> xe[EARLY ? BPL : 1];
+    if constexpr (EARLY) {
+        uint32_t c = col0;
+#pragma unroll
+        for (int i = 0; i < (int)BPL; ++i) {
+            if constexpr (FAST) c += (d.i[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+            else c += dv[i];
+            const bool t = FAST || ((tmask >> i) & 1u);
+            xe[i] = stream_x<NB, false>(a, r, s_x, t ? c : 0u);
+        }
+    }
+
+    // the next window: descriptor (loaded one window ago), data, and the
+    // descriptor of the window after it
+    mN = uniform_meta(qn);
+    issue_data(r, wn, mN, dN);
+    issue_meta(r, wn2, qn);
 
     float acc[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[j] = 0.0f;
+    uint32_t c = col0;
 #pragma unroll
     for (int i = 0; i < (int)BPL; ++i) {
-        if constexpr (FAST) col += (r.i[i >> 2] >> (8 * (i & 3))) & 0xFFu;
-        else col += dv[i];
-        if (FAST || ((tmask >> i) & 1u)) {
-            const float wq = fp4_code_hi_byte(r.v[i >> 2], i);
-            const XVec<NB> x = stream_x<NB, XLDS>(a, s_x, rin, rent, col);
+        if constexpr (FAST) c += (d.i[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+        else c += dv[i];
+        const bool t = FAST || ((tmask >> i) & 1u);
+        // a byte ending no entry has value byte 0 (weight 0) and reads the
+        // zero slot
+        const float wq = fp4_code_hi_byte(d.v[i >> 2], i);
+        XVec<NB> x;
+        if constexpr (EARLY) x = xe[i];
+        else x = stream_x<NB, XLDS>(a, r, s_x, t ? c : 0u);
 #pragma unroll
-            for (int j = 0; j < NB; ++j) acc[j] = __builtin_fmaf(wq, x.v[j], acc[j]);
-        }
+        for (int j = 0; j < NB; ++j) acc[j] = __builtin_fmaf(wq, x.v[j], acc[j]);
     }
 
     // per-row pieces: segmented sums over the lanes of each row; the last
     // lane of a piece adds them to the output
     wave_seg_scan_n<NB>(acc, hs ? 1u : 0u);
     const bool last = lane == 63u || ((S >> (lane + 1u)) & 1ull) != 0ull;
-    if (last) {
-        const float rs = a.rsc ? a.rsc[row] : 1.0f;
 #pragma unroll
-        for (int j = 0; j < NB; ++j)
-            if (acc[j] != 0.0f) atomicAdd(a.out + (int64_t)j * a.out_ld + row, a.rsc ? acc[j] * rs : acc[j]);
+    for (int j = 0; j < NB; ++j) {
+        const float v = a.rsc ? acc[j] * rsv : acc[j];
+        const uint32_t off = (last && acc[j] != 0.0f) ? ((uint32_t)j * (uint32_t)a.out_ld + row) * 4u : OOB_OFFSET;
+        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(v, r.out, (int)off, 0, 0);
     }
 }
 
+template <int NB, bool XLDS>
+__device__ __forceinline__ void stream_step(const StreamArgs &a, const StreamRsrc &r, int64_t w, const WinMeta &m,
+                                            const WinData &d, int64_t W, WinRaw &qn, WinMeta &mN, WinData &dN,
+                                            uint32_t *slot, const float *s_x) {
+    // fast decode: a whole window of one-byte varints, none continuing from
+    // the window before
+    const bool full = a.nbytes - (uint32_t)w * WIN_BYTES >= WIN_BYTES;
+    const bool cont = ((d.i[0] | d.i[1] | d.i[2] | d.i[3]) & 0x80808080u) != 0u ||
+                      (lane_id() == 0u && (d.ip & 0x80000000u) != 0u);
+    if (full && __ballot(cont) == 0ull)
+        run_window<NB, XLDS, true>(a, r, w, m, d, w + W, w + 2 * W, qn, mN, dN, slot, s_x);
+    else
+        run_window<NB, XLDS, false>(a, r, w, m, d, w + W, w + 2 * W, qn, mN, dN, slot, s_x);
+}
+
 // (8 columns through the cache need more registers than 1024-thread blocks allow)
+// (registers: the compiler's choice, ~100 VGPRs at one column -- capping
+// them at 64 for 8 waves per SIMD measured 4 % slower on c4's layers)
 template <int NB, bool XLDS>
 __global__ __launch_bounds__((NB == 8 && !XLDS) ? 512 : 1024) void k_stream(StreamArgs a) {
     extern __shared__ float s_x[];
@@ -467,40 +541,37 @@ __global__ __launch_bounds__((NB == 8 && !XLDS) ? 512 : 1024) void k_stream(Stre
     const int64_t W = (int64_t)gridDim.x * nw;
     int64_t w = (int64_t)blockIdx.x * nw + wave;
     if (w >= a.nwin) return;
-    const __amdgpu_buffer_rsrc_t rin = buffer_rsrc(a.in, XLDS ? 0u : a.nx * a.in_ld * 4u);
-    const __amdgpu_buffer_rsrc_t rent = buffer_rsrc(a.ent ? a.ent : a.in, (!XLDS && a.ent) ? a.nx * 4u : 0u);
+    StreamRsrc r;
+    r.idx = buffer_rsrc(a.idx, a.nbytes + 16u);
+    r.val = buffer_rsrc(a.val, a.nbytes + 16u);
+    r.nes = buffer_rsrc(a.ne_start, (a.n_ne + 1u) * 4u);
+    r.ner = buffer_rsrc(a.ne_row, (a.n_ne + 1u) * 4u);
+    r.win = buffer_rsrc(a.win, (uint32_t)(a.nwin + 1) * 16u);
+    r.rsc = buffer_rsrc(a.rsc ? a.rsc : a.out, a.rsc ? a.rows * 4u : 0u);
+    r.out = buffer_rsrc(a.out, (uint32_t)(((int64_t)(NB - 1) * a.out_ld + a.rows) * 4));
+    r.in = buffer_rsrc(a.in, XLDS ? 0u : a.nx * a.in_ld * 4u);
+    r.ent = buffer_rsrc(a.ent ? a.ent : a.in, (!XLDS && a.ent) ? a.nx * 4u : 0u);
     uint32_t *slot = s_slot[wave];
-    const uint32_t lane = lane_id();
-    // software pipeline: data of the next window and descriptors of the one
-    // after are in flight while a window is processed
-    WinRegs cur;
-    cur.m = uniform_win(load_win_raw(a.win + w));
-    cur.rs_hi = uniform(load_win_raw(a.win + w + 1).z);
-    load_window(a, w, cur);
-    uint4 nm = make_uint4(0, 0, 0, 0), nmn = make_uint4(0, 0, 0, 0);
-    if (w + W < a.nwin) {
-        nm = load_win_raw(a.win + w + W);
-        nmn = load_win_raw(a.win + w + W + 1);
-    }
-    for (; w < a.nwin; w += W) {
-        WinRegs nxt = cur;
-        if (w + W < a.nwin) {
-            nxt.m = uniform_win(nm);
-            nxt.rs_hi = uniform(nmn.z);
-            load_window(a, w + W, nxt);
-            if (w + 2 * W < a.nwin) {
-                nm = load_win_raw(a.win + w + 2 * W);
-                nmn = load_win_raw(a.win + w + 2 * W + 1);
-            }
-        }
-        // fast decode: a whole window of one-byte varints, none continuing
-        // from the window before
-        const bool full = a.nbytes - (uint32_t)w * WIN_BYTES >= WIN_BYTES;
-        const bool cont = ((cur.i[0] | cur.i[1] | cur.i[2] | cur.i[3]) & 0x80808080u) != 0u ||
-                          (lane == 0u && (cur.ip & 0x80000000u) != 0u);
-        if (full && __ballot(cont) == 0ull) run_window<NB, XLDS, true>(a, w, cur, slot, s_x, rin, rent);
-        else run_window<NB, XLDS, false>(a, w, cur, slot, s_x, rin, rent);
-        cur = nxt;
+    // software pipeline over two register sets: while window w is worked
+    // on, the next window's data and the descriptor of the one after are in
+    // flight
+    WinRaw q;
+    issue_meta(r, w, q);
+    WinMeta mA = uniform_meta(q), mB;
+    WinData dA, dB;
+    issue_data(r, w, mA, dA);
+    issue_meta(r, w + W, q);
+    // an atomic out of range (dropped), as every window ends with: the loop
+    // is entered with the same memory operations in flight as it repeats
+    // with, which keeps the compiler's wait counts exact in its first half
+    __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(0.0f, r.out, (int)OOB_OFFSET, 0, 0);
+    for (;;) {
+        stream_step<NB, XLDS>(a, r, w, mA, dA, W, q, mB, dB, slot, s_x);
+        w += W;
+        if (w >= a.nwin) break;
+        stream_step<NB, XLDS>(a, r, w, mB, dB, W, q, mA, dA, slot, s_x);
+        w += W;
+        if (w >= a.nwin) break;
     }
 }
 
@@ -725,8 +796,9 @@ bool stream_wanted(const DScatter &s, const ScaleView &sc, int64_t nb, int64_t i
     const int mode = env_int("SILI_B1_STREAM", 1);
     if (mode == 0 || (mode == 1 && s.nbytes < (int64_t(1) << 20))) return false;
     if (s.stream1.failed && s.streamK.failed) return false;
+    // (the kernels' buffer offsets: input and output columns in 31 bits)
     return skip == SKIP_NONE && sc.rank == 1 && in_ld == nb && s.cols + 1 < (int64_t(1) << 26) &&
-           (uint64_t)s.cols * (uint64_t)nb * 4u < (1ull << 31);
+           (uint64_t)s.cols * (uint64_t)nb * 4u < (1ull << 31) && (uint64_t)s.rows * (uint64_t)nb * 4u < (1ull << 31);
 }
 
 void stream_gather(Layer &L, DScatter &s, const ScaleView &sc, const float *in, int64_t B, float *out,
@@ -755,6 +827,8 @@ void stream_gather(Layer &L, DScatter &s, const ScaleView &sc, const float *in, 
         }
     }
     if (!d->valid) throw_error(3, "stream copy exceeds 2 GiB");
+    if (((B - 1) * out_ld + s.rows) * 4 >= (int64_t(1) << 31))
+        throw_error(1, "stream_gather: output exceeds 2 GiB");
     {
         ProfScope ps("stream_zero", st);
         for (int64_t b = 0; b < B; ++b)
@@ -775,8 +849,8 @@ void stream_gather(Layer &L, DScatter &s, const ScaleView &sc, const float *in, 
         for (int64_t b0 = 0; b0 < B; b0 += pnb) {
             StreamArgs a{d->win.p + bk.win_off, bk.nwin, d->idx.p + bk.off, d->val.p + bk.off,
                          d->ne_row.p + bk.ne_off, d->ne_start.p + bk.ne_off, (uint32_t)bk.nbytes,
-                         in + bk.c0 * B + b0, (uint32_t)B, sc.ent ? sc.ent + bk.c0 : nullptr, sc.row,
-                         (uint32_t)bk.ncols, out + b0 * out_ld, out_ld};
+                         (uint32_t)bk.n_ne, in + bk.c0 * B + b0, (uint32_t)B, sc.ent ? sc.ent + bk.c0 : nullptr,
+                         sc.row, (uint32_t)bk.ncols, (uint32_t)s.rows, out + b0 * out_ld, out_ld};
             ProfScope ps(sh.xlds ? "stream_lds" : "stream", st);
             launch(stream_kernel(pnb, sh.xlds), dim3(sh.grid), dim3(sh.threads), sh.xlds ? sh.lds : 0u, st, a);
         }

@@ -12,6 +12,19 @@ __device__ __forceinline__ uint32_t uniform(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
 }
 
+// Workgroups of a launch are dispatched round-robin over the 8 XCDs
+// (workgroup n runs on XCD n % 8), each XCD with its own L2.  xcd_block maps
+// the hardware workgroup id to a logical one so that every XCD takes one
+// contiguous range of logical blocks (XCD x: [x*q + min(x, r), ...) for
+// nblocks = 8q + r, q + (x < r) of them); a bijection on [0, nblocks).
+// Blocks on neighbouring rows then write their shares of an output cache
+// line from the same L2.
+__device__ __forceinline__ uint32_t xcd_block(uint32_t n, uint32_t nblocks) {
+    const uint32_t q = nblocks >> 3, r = nblocks & 7u;
+    const uint32_t x = n & 7u, k = n >> 3;
+    return x * q + (x < r ? x : r) + k;
+}
+
 // Make this wave's LDS writes visible to its own later LDS reads (other lanes).
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
