@@ -100,18 +100,20 @@ constexpr uint32_t SEG_SPLIT = 1u;  // the row has several segments (combine wit
 constexpr uint32_t SEG_FIRST = 2u;  // first segment of its row
 
 // ---- stream window ---------------------------------------------------------
-// The batch-1 stream kernels read a padded copy of a scattered store (see
-// DStream in layer.hpp) cut into windows of WIN_BYTES = 64 lanes x 16 bytes.
-// Per window:
-//   row0  : the row holding the window's first byte
-//   carry : shifted column (col + 1) of row0's last entry ending before the
-//           window (0 if none)
+// The stream kernels read a padded copy of a scattered store (see DStream in
+// layer.hpp) cut into windows of WIN_BYTES = 64 lanes x 16 bytes.  Per window:
+//   carry : shifted column (col + 1) of the last entry ending before the
+//           window in the row holding the window's first byte (0 if none)
 //   rs_lo : first non-empty row (index into the store's list of non-empty
 //           rows) whose first byte is at or after the window start
-// A sentinel follows the last window: {rows, 0, number of non-empty rows, 0}.
+//   mask  : bit l set when a non-empty row starts at byte 16 l of the window
+//           (rows start 16-byte aligned; popcount(mask) rows start here, the
+//           next window's rs_lo is rs_lo + popcount(mask), and the row holding
+//           the first byte is list entry rs_lo - 1 unless bit 0 is set)
+// A sentinel follows the last window: {0, number of non-empty rows, 0, 0}.
 constexpr uint32_t WIN_BYTES = 1024;
 struct alignas(16) WinDesc {
-    uint32_t row0, carry, rs_lo, pad;
+    uint32_t carry, rs_lo, mask_lo, mask_hi;
 };
 
 // ---- FP4 E2M1 codec (device + host) -----------------------------------------

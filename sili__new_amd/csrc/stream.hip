@@ -42,8 +42,6 @@ namespace sili {
 namespace {
 
 constexpr unsigned TPB = 256;
-constexpr uint32_t SLOT_NONE = 0xFFFFFFFFu;
-constexpr uint32_t MAX_WAVES = 16;
 constexpr uint32_t BPL = 16;  // index bytes per lane
 
 inline unsigned nblk(int64_t n) { return (unsigned)((n + TPB - 1) / TPB); }
@@ -135,7 +133,7 @@ __global__ void k_sp_ne(const uint32_t *__restrict__ nonempty, const uint32_t *_
 
 // Pass 2: one wave per (block, row): copy the block's entries of the row into
 // the block's padded stream (first delta re-encoded for the shifted column,
-// value bytes placed at their terminators) and write row0 / carry of every
+// value bytes placed at their terminators) and write the carry of every
 // window of the block that starts inside the row's padded range.
 __global__ __launch_bounds__(256) void k_spb_copy(const uint32_t *__restrict__ bs, const uint8_t *__restrict__ idx,
                                                   const uint8_t *__restrict__ val, const BlkMeta *__restrict__ meta,
@@ -157,10 +155,7 @@ __global__ __launch_bounds__(256) void k_spb_copy(const uint32_t *__restrict__ b
     // a window starting before the first entry's last byte: only padding
     // entries (shifted column 0) precede it
     const uint32_t w_pad = (P + WIN_BYTES - 1u) / WIN_BYTES * WIN_BYTES;
-    if (lane == 0u && w_pad < D) {
-        win[w_pad / WIN_BYTES].row0 = (uint32_t)r;
-        win[w_pad / WIN_BYTES].carry = 0u;
-    }
+    if (lane == 0u && w_pad < D) win[w_pad / WIN_BYTES].carry = 0u;
     const uint8_t *row = idx + bs[r];
     const uint32_t o0 = m.s + m.lf;
     uint32_t off = o0, carry = m.c, ebase = m.ei + 1u;
@@ -179,22 +174,21 @@ __global__ __launch_bounds__(256) void k_spb_copy(const uint32_t *__restrict__ b
             const uint64_t before = ch.T & ((1ull << (ws - d0)) - 1ull);
             uint32_t c = carry - c0 + 1u;
             if (before) c = (uint32_t)__shfl((int)ch.col, 63 - (int)__clzll(before), 64) - c0 + 1u;
-            if (lane == 0u) {
-                win[ws / WIN_BYTES].row0 = (uint32_t)r;
-                win[ws / WIN_BYTES].carry = c;
-            }
+            if (lane == 0u) win[ws / WIN_BYTES].carry = c;
         }
         carry = chunk_advance(ch, off, ebase);
     }
 }
 
-// rs_lo of every window of a block: first non-empty row starting at or after it.
-__global__ void k_sp_rs(const uint32_t *__restrict__ ne_start, int64_t n_ne, int64_t nwin, int64_t rows,
+// rs_lo and the row-start mask of every window of a block: the first
+// non-empty row starting at or after the window, and the lanes on which the
+// rows starting inside it begin.
+__global__ void k_sp_rs(const uint32_t *__restrict__ ne_start, int64_t n_ne, int64_t nwin,
                         WinDesc *__restrict__ win) {
     const int64_t w = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (w > nwin) return;
     if (w == nwin) {
-        win[w] = WinDesc{(uint32_t)rows, 0u, (uint32_t)n_ne, 0u};
+        win[w] = WinDesc{0u, (uint32_t)n_ne, 0u, 0u};
         return;
     }
     const uint64_t b0 = (uint64_t)w * WIN_BYTES;
@@ -204,7 +198,12 @@ __global__ void k_sp_rs(const uint32_t *__restrict__ ne_start, int64_t n_ne, int
         if ((uint64_t)ne_start[mid] < b0) lo = mid + 1;
         else hi = mid;
     }
+    uint64_t mask = 0;
+    for (int64_t k = lo; k < n_ne && (uint64_t)ne_start[k] < b0 + WIN_BYTES; ++k)
+        mask |= 1ull << (((uint64_t)ne_start[k] - b0) / BPL);
     win[w].rs_lo = (uint32_t)lo;
+    win[w].mask_lo = (uint32_t)mask;
+    win[w].mask_hi = (uint32_t)(mask >> 32);
 }
 
 // ---- the gather ------------------------------------------------------------
@@ -213,9 +212,9 @@ struct StreamArgs {
     const WinDesc *win;          // nwin + 1
     int64_t nwin;
     const uint8_t *idx, *val;    // padded stream
-    const uint32_t *ne_row, *ne_start;
+    const uint32_t *ne_row;      // non-empty rows, ascending
     uint32_t nbytes;
-    uint32_t n_ne;               // non-empty rows (the lists hold n_ne + 1)
+    uint32_t n_ne;               // non-empty rows
     const float *in;             // in[c * in_ld + j], c < nx, j < NB (this pass)
     uint32_t in_ld;
     const float *ent;            // column scale (NULL: ones)
@@ -232,7 +231,7 @@ struct StreamArgs {
 // compiler's wait counts stay exact: a window's loads are waited for one
 // window after they were issued, never together with the next window's.
 struct StreamRsrc {
-    __amdgpu_buffer_rsrc_t idx, val, nes, ner, win, rsc, out, in, ent;
+    __amdgpu_buffer_rsrc_t idx, val, ner, win, rsc, out, in, ent;
 };
 
 __device__ __forceinline__ uint4 buffer_load_u4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -242,32 +241,31 @@ __device__ __forceinline__ uint32_t buffer_load_u1(__amdgpu_buffer_rsrc_t r, uin
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
 
-// A window's descriptor, uniform: row0, carry, rs_lo, and the next window's
-// rs_lo (rs_hi).
+// A window's descriptor (WinDesc), uniform.
 struct WinMeta {
-    uint32_t row0, carry, rs_lo, rs_hi;
+    uint32_t carry, rs_lo, mask_lo, mask_hi;
 };
 // The same as loaded (per lane, before readfirstlane).
 struct WinRaw {
     uint4 d;
-    uint32_t hi;
 };
 // One window's per-lane loads: the lane's 16 index and 16 value bytes, the
-// index dword before the window (0 for the first), and for lanes below
-// rs_hi - rs_lo one of the non-empty rows starting in the window (its first
-// byte and row; 0 on other lanes).
+// index dword before the window (0 for the first), and Rr = entry
+// rs_lo - h + lane of the list of non-empty rows for lanes below
+// popcount(mask) + h, where h = 1 when no row starts at the window's first
+// byte (then lane 0 holds the row that byte belongs to), else 0.
 struct WinData {
     uint32_t i[4], v[4], ip;
-    uint32_t Rs, Rr;
+    uint32_t Rr;
 };
 
 __device__ __forceinline__ void issue_meta(const StreamRsrc &r, int64_t w, WinRaw &q) {
     q.d = buffer_load_u4(r.win, (uint32_t)w * 16u);
-    q.hi = buffer_load_u1(r.win, (uint32_t)(w + 1) * 16u + 8u);
 }
 __device__ __forceinline__ WinMeta uniform_meta(const WinRaw &q) {
-    return WinMeta{uniform(q.d.x), uniform(q.d.y), uniform(q.d.z), uniform(q.hi)};
+    return WinMeta{uniform(q.d.x), uniform(q.d.y), uniform(q.d.z), uniform(q.d.w)};
 }
+__device__ __forceinline__ uint32_t head_missing(const WinMeta &m) { return (m.mask_lo & 1u) ^ 1u; }
 // Windows at or past nwin read zeros (no rows, no bytes).
 __device__ __forceinline__ void issue_data(const StreamRsrc &r, int64_t w, const WinMeta &m, WinData &d) {
     const uint32_t lane = lane_id();
@@ -283,10 +281,11 @@ __device__ __forceinline__ void issue_data(const StreamRsrc &r, int64_t w, const
     d.v[2] = vw.z;
     d.v[3] = vw.w;
     d.ip = buffer_load_u1(r.idx, b0 ? b0 - 4u : OOB_OFFSET);
-    const uint32_t nr = m.rs_hi - m.rs_lo;  // non-empty rows starting here (<= 64)
-    const uint32_t o = lane < nr ? (m.rs_lo + lane) * 4u : OOB_OFFSET;
-    d.Rs = buffer_load_u1(r.nes, o);
-    d.Rr = buffer_load_u1(r.ner, o);
+    // rows starting here (<= 64; h = 1 only when lane 0 starts none, so
+    // nr + h <= 64)
+    const uint32_t h = head_missing(m);
+    const uint32_t nr = (uint32_t)__builtin_popcount(m.mask_lo) + (uint32_t)__builtin_popcount(m.mask_hi);
+    d.Rr = buffer_load_u1(r.ner, lane < nr + h ? (m.rs_lo - h + lane) * 4u : OOB_OFFSET);
 }
 
 // Weight code of value byte K (0..3) of dw: the high nibble.  The conversion
@@ -389,22 +388,16 @@ __device__ __forceinline__ void wave_seg_scan_n(float (&v)[NB], uint32_t f) {
 template <int NB, bool XLDS, bool FAST>
 __device__ __forceinline__ void run_window(const StreamArgs &a, const StreamRsrc &r, int64_t w, const WinMeta &m,
                                            const WinData &d, int64_t wn, int64_t wn2, WinRaw &qn, WinMeta &mN,
-                                           WinData &dN, uint32_t *slot, const float *s_x) {
+                                           WinData &dN, const float *s_x) {
     const uint32_t lane = lane_id();
     const uint32_t b0 = (uint32_t)w * WIN_BYTES;
-    const uint32_t nr = m.rs_hi - m.rs_lo;
 
-    // rows starting in the window -> the lane holding their first 16 bytes
-    slot[lane] = SLOT_NONE;
-    wave_lds_sync();
-    if (lane < nr) slot[(d.Rs - b0) / BPL] = d.Rr;
-    wave_lds_sync();
-    const uint32_t sl = slot[lane];
-    const bool hs = sl != SLOT_NONE;
-    const uint64_t S = __ballot(hs);
-    // the lane's row: the latest row start at or before it (rows ascend)
-    const uint32_t mrow = wave_max_scan(hs ? sl + 1u : 0u);
-    const uint32_t row = mrow ? mrow - 1u : m.row0;
+    // the lane's row: rows starting at or before the lane (inclusive count
+    // from the row-start mask) pick its entry of the row list
+    const uint64_t S = ((uint64_t)m.mask_hi << 32) | m.mask_lo;
+    const bool hs = ((S >> lane) & 1ull) != 0ull;
+    const uint32_t cnt = __builtin_amdgcn_mbcnt_hi(m.mask_hi, __builtin_amdgcn_mbcnt_lo(m.mask_lo, 0u)) + (hs ? 1u : 0u);
+    const uint32_t row = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((cnt - 1u + head_missing(m)) * 4u), (int)d.Rr);
     // its row scale (used by the last lane of each row piece)
     const float rsv = buffer_load_f1(r.rsc, row * 4u);
 
@@ -448,12 +441,13 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, const StreamRsrc
         }
     }
 
-    // shifted column entering the lane: segmented scan of the lanes' delta
-    // sums (a lane with a row start begins from 0; the window's first
-    // segment continues from the carried column)
-    const uint32_t K = wave_seg_scan(full + ((lane == 0u && !hs) ? m.carry : 0u), hs ? 1u : 0u);
-    const uint32_t kprev = wave_prev_u32(K);
-    const uint32_t col0 = hs ? 0u : (lane ? kprev : m.carry);
+    // shifted column entering the lane: E = carry (unless a row starts at
+    // lane 0) plus the delta sums of the lanes before, minus E at the
+    // latest row start at or before the lane (E never decreases, so a
+    // running maximum over the row-start lanes finds it)
+    const uint32_t seed = full + ((lane == 0u && !hs) ? m.carry : 0u);
+    const uint32_t E = wave_incl_scan(seed) - full;
+    const uint32_t col0 = E - wave_max_scan(hs ? E : 0u);
 
     // inputs through the cache (one or two columns): loaded before the next
     // window's loads are issued, so waiting for them does not wait for those
@@ -475,6 +469,10 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, const StreamRsrc
     mN = uniform_meta(qn);
     issue_data(r, wn, mN, dN);
     issue_meta(r, wn2, qn);
+    // (keep the multiply-adds below the loads: issued after them, the
+    // loads would have only the epilogue to arrive in, and the row-scale
+    // load none)
+    __builtin_amdgcn_sched_barrier(0);
 
     float acc[NB];
 #pragma unroll
@@ -510,16 +508,16 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, const StreamRsrc
 template <int NB, bool XLDS>
 __device__ __forceinline__ void stream_step(const StreamArgs &a, const StreamRsrc &r, int64_t w, const WinMeta &m,
                                             const WinData &d, int64_t W, WinRaw &qn, WinMeta &mN, WinData &dN,
-                                            uint32_t *slot, const float *s_x) {
+                                            const float *s_x) {
     // fast decode: a whole window of one-byte varints, none continuing from
     // the window before
     const bool full = a.nbytes - (uint32_t)w * WIN_BYTES >= WIN_BYTES;
     const bool cont = ((d.i[0] | d.i[1] | d.i[2] | d.i[3]) & 0x80808080u) != 0u ||
                       (lane_id() == 0u && (d.ip & 0x80000000u) != 0u);
     if (full && __ballot(cont) == 0ull)
-        run_window<NB, XLDS, true>(a, r, w, m, d, w + W, w + 2 * W, qn, mN, dN, slot, s_x);
+        run_window<NB, XLDS, true>(a, r, w, m, d, w + W, w + 2 * W, qn, mN, dN, s_x);
     else
-        run_window<NB, XLDS, false>(a, r, w, m, d, w + W, w + 2 * W, qn, mN, dN, slot, s_x);
+        run_window<NB, XLDS, false>(a, r, w, m, d, w + W, w + 2 * W, qn, mN, dN, s_x);
 }
 
 // (8 columns through the cache need more registers than 1024-thread blocks allow)
@@ -528,7 +526,6 @@ __device__ __forceinline__ void stream_step(const StreamArgs &a, const StreamRsr
 template <int NB, bool XLDS>
 __global__ __launch_bounds__((NB == 8 && !XLDS) ? 512 : 1024) void k_stream(StreamArgs a) {
     extern __shared__ float s_x[];
-    __shared__ uint32_t s_slot[MAX_WAVES][64];
     const uint32_t nw = blockDim.x >> 6;
     const uint32_t wave = uniform(threadIdx.x >> 6);
     if constexpr (XLDS) {
@@ -544,14 +541,12 @@ __global__ __launch_bounds__((NB == 8 && !XLDS) ? 512 : 1024) void k_stream(Stre
     StreamRsrc r;
     r.idx = buffer_rsrc(a.idx, a.nbytes + 16u);
     r.val = buffer_rsrc(a.val, a.nbytes + 16u);
-    r.nes = buffer_rsrc(a.ne_start, (a.n_ne + 1u) * 4u);
-    r.ner = buffer_rsrc(a.ne_row, (a.n_ne + 1u) * 4u);
+    r.ner = buffer_rsrc(a.ne_row, a.n_ne * 4u);
     r.win = buffer_rsrc(a.win, (uint32_t)(a.nwin + 1) * 16u);
     r.rsc = buffer_rsrc(a.rsc ? a.rsc : a.out, a.rsc ? a.rows * 4u : 0u);
     r.out = buffer_rsrc(a.out, (uint32_t)(((int64_t)(NB - 1) * a.out_ld + a.rows) * 4));
     r.in = buffer_rsrc(a.in, XLDS ? 0u : a.nx * a.in_ld * 4u);
     r.ent = buffer_rsrc(a.ent ? a.ent : a.in, (!XLDS && a.ent) ? a.nx * 4u : 0u);
-    uint32_t *slot = s_slot[wave];
     // software pipeline over two register sets: while window w is worked
     // on, the next window's data and the descriptor of the one after are in
     // flight
@@ -566,10 +561,10 @@ __global__ __launch_bounds__((NB == 8 && !XLDS) ? 512 : 1024) void k_stream(Stre
     // with, which keeps the compiler's wait counts exact in its first half
     __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(0.0f, r.out, (int)OOB_OFFSET, 0, 0);
     for (;;) {
-        stream_step<NB, XLDS>(a, r, w, mA, dA, W, q, mB, dB, slot, s_x);
+        stream_step<NB, XLDS>(a, r, w, mA, dA, W, q, mB, dB, s_x);
         w += W;
         if (w >= a.nwin) break;
-        stream_step<NB, XLDS>(a, r, w, mB, dB, W, q, mA, dA, slot, s_x);
+        stream_step<NB, XLDS>(a, r, w, mB, dB, W, q, mA, dA, s_x);
         w += W;
         if (w >= a.nwin) break;
     }
@@ -639,7 +634,7 @@ int stream_occupancy(StreamKernel k, unsigned nt, uint32_t lds) {
     return per_cu;
 }
 
-constexpr int64_t STATIC_LDS = (int64_t)MAX_WAVES * 64 * 4;
+constexpr int64_t STATIC_LDS = 0;  // the stream kernels' static LDS
 
 // Launch shape for NB columns per pass: block size with the most resident
 // waves per CU, a grid no larger than what is resident at once.  xmode: 0
@@ -750,7 +745,7 @@ void build_stream(Layer &L, const DScatter &s, DStream &d, int K, int64_t cb) {
                    (const uint32_t *)pstart.p + o, rows, (uint32_t)bk.c0, d.idx.p + bk.off, d.val.p + bk.off,
                    d.win.p + bk.win_off);
         launch(k_sp_rs, dim3(nblk(bk.nwin + 1)), dim3(TPB), 0, st, (const uint32_t *)d.ne_start.p + bk.ne_off,
-               bk.n_ne, bk.nwin, rows, d.win.p + bk.win_off);
+               bk.n_ne, bk.nwin, d.win.p + bk.win_off);
         SILI_HIP(hipGetLastError());
     }
     SILI_HIP(hipStreamSynchronize(st));
@@ -848,7 +843,7 @@ void stream_gather(Layer &L, DScatter &s, const ScaleView &sc, const float *in, 
         }
         for (int64_t b0 = 0; b0 < B; b0 += pnb) {
             StreamArgs a{d->win.p + bk.win_off, bk.nwin, d->idx.p + bk.off, d->val.p + bk.off,
-                         d->ne_row.p + bk.ne_off, d->ne_start.p + bk.ne_off, (uint32_t)bk.nbytes,
+                         d->ne_row.p + bk.ne_off, (uint32_t)bk.nbytes,
                          (uint32_t)bk.n_ne, in + bk.c0 * B + b0, (uint32_t)B, sc.ent ? sc.ent + bk.c0 : nullptr,
                          sc.row, (uint32_t)bk.ncols, (uint32_t)s.rows, out + b0 * out_ld, out_ld};
             ProfScope ps(sh.xlds ? "stream_lds" : "stream", st);
