@@ -237,6 +237,11 @@ struct StreamRsrc {
 __device__ __forceinline__ uint4 buffer_load_u4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
+// The same, non-temporal (cache policy nt): for the stream's bytes, which a
+// pass reads once.
+__device__ __forceinline__ uint4 buffer_load_u4_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2));
+}
 __device__ __forceinline__ uint32_t buffer_load_u1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
 }
@@ -270,8 +275,8 @@ __device__ __forceinline__ uint32_t head_missing(const WinMeta &m) { return (m.m
 __device__ __forceinline__ void issue_data(const StreamRsrc &r, int64_t w, const WinMeta &m, WinData &d) {
     const uint32_t lane = lane_id();
     const uint32_t b0 = (uint32_t)w * WIN_BYTES;
-    const uint4 iw = buffer_load_u4(r.idx, b0 + BPL * lane);
-    const uint4 vw = buffer_load_u4(r.val, b0 + BPL * lane);
+    const uint4 iw = buffer_load_u4_nt(r.idx, b0 + BPL * lane);
+    const uint4 vw = buffer_load_u4_nt(r.val, b0 + BPL * lane);
     d.i[0] = iw.x;
     d.i[1] = iw.y;
     d.i[2] = iw.z;
@@ -358,49 +363,49 @@ __device__ __forceinline__ XVec<NB> stream_x(const StreamArgs &a, const StreamRs
     return x;
 }
 
-// Segmented inclusive scan of NB values sharing one flag ladder (see
-// wave_seg_scan).
+// Segmented inclusive scan of NB values (the wave_seg_scan ladder) whose
+// segments begin at the lanes of the uniform mask S.  The flag each step
+// selects on depends on S alone, so the ladder is built with scalar
+// operations: F |= F moved the way the step moves values (row_shr n: up by
+// n inside each 16-lane row; row_bcast15: lane 15 / 47 into rows 1 / 3;
+// row_bcast31: lane 31 into rows 2 and 3), and each step's select reads the
+// lane's bit of F directly as its condition.
 template <int NB, int CTRL, int RM>
-__device__ __forceinline__ void seg_step_n(float (&v)[NB], uint32_t &f) {
-    const uint32_t tf = dpp_u32<CTRL, RM>(f);
+__device__ __forceinline__ void seg_step_mask(float (&v)[NB], uint64_t F) {
+    const bool f = __builtin_amdgcn_inverse_ballot_w64(F);
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
         const float t = dpp_f32<CTRL, RM>(v[j]);
         v[j] = f ? v[j] : v[j] + t;
     }
-    f |= tf;
 }
 template <int NB>
-__device__ __forceinline__ void wave_seg_scan_n(float (&v)[NB], uint32_t f) {
-    seg_step_n<NB, DPP_ROW_SHR1, 0xF>(v, f);
-    seg_step_n<NB, DPP_ROW_SHR2, 0xF>(v, f);
-    seg_step_n<NB, DPP_ROW_SHR4, 0xF>(v, f);
-    seg_step_n<NB, DPP_ROW_SHR8, 0xF>(v, f);
-    seg_step_n<NB, DPP_ROW_BCAST15, 0xA>(v, f);
-    seg_step_n<NB, DPP_ROW_BCAST31, 0xC>(v, f);
+__device__ __forceinline__ void wave_seg_scan_mask(float (&v)[NB], uint64_t S) {
+    uint64_t F = S;
+    seg_step_mask<NB, DPP_ROW_SHR1, 0xF>(v, F);
+    F |= (F << 1) & 0xFFFEFFFEFFFEFFFEull;
+    seg_step_mask<NB, DPP_ROW_SHR2, 0xF>(v, F);
+    F |= (F << 2) & 0xFFFCFFFCFFFCFFFCull;
+    seg_step_mask<NB, DPP_ROW_SHR4, 0xF>(v, F);
+    F |= (F << 4) & 0xFFF0FFF0FFF0FFF0ull;
+    seg_step_mask<NB, DPP_ROW_SHR8, 0xF>(v, F);
+    F |= (F << 8) & 0xFF00FF00FF00FF00ull;
+    seg_step_mask<NB, DPP_ROW_BCAST15, 0xA>(v, F);
+    F |= (((F >> 15) & 1ull) ? 0x00000000FFFF0000ull : 0ull) | (((F >> 47) & 1ull) ? 0xFFFF000000000000ull : 0ull);
+    seg_step_mask<NB, DPP_ROW_BCAST31, 0xC>(v, F);
 }
 
-// Window w (descriptor m, loads d): out[j*out_ld + row] += its row pieces.
-// Between the work that needs d and the multiply-adds it issues the loads of
-// window wn (descriptor from qn, into mN / dN) and the descriptor loads of
-// window wn2 (into qn).  FAST: every byte is a one-byte varint and none
+// Decode and multiply-adds of window w (descriptor m, loads d) for the
+// lane: acc[j] = sum over the entries in its 16 bytes of weight * input j.
+// Inputs through the cache at one or two columns (EARLY) are loaded here
+// before the data loads of window wn, which this then issues; otherwise the
+// caller issued them.  FAST: every byte is a one-byte varint and none
 // continues from the window before.
 template <int NB, bool XLDS, bool FAST>
-__device__ __forceinline__ void run_window(const StreamArgs &a, const StreamRsrc &r, int64_t w, const WinMeta &m,
-                                           const WinData &d, int64_t wn, int64_t wn2, WinRaw &qn, WinMeta &mN,
-                                           WinData &dN, const float *s_x) {
+__device__ __forceinline__ void window_body(const StreamArgs &a, const StreamRsrc &r, const float *s_x,
+                                            const WinMeta &m, const WinData &d, uint32_t b0, bool hs,
+                                            int64_t wn, const WinMeta &mN, WinData &dN, float (&acc)[NB]) {
     const uint32_t lane = lane_id();
-    const uint32_t b0 = (uint32_t)w * WIN_BYTES;
-
-    // the lane's row: rows starting at or before the lane (inclusive count
-    // from the row-start mask) pick its entry of the row list
-    const uint64_t S = ((uint64_t)m.mask_hi << 32) | m.mask_lo;
-    const bool hs = ((S >> lane) & 1ull) != 0ull;
-    const uint32_t cnt = __builtin_amdgcn_mbcnt_hi(m.mask_hi, __builtin_amdgcn_mbcnt_lo(m.mask_lo, 0u)) + (hs ? 1u : 0u);
-    const uint32_t row = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((cnt - 1u + head_missing(m)) * 4u), (int)d.Rr);
-    // its row scale (used by the last lane of each row piece)
-    const float rsv = buffer_load_f1(r.rsc, row * 4u);
-
     // deltas of the entries ending at each byte (0 where no entry ends)
     uint32_t full = 0;
     uint32_t dv[BPL];
@@ -419,11 +424,11 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, const StreamRsrc
             const bool cont = ((pw >> (8 * i + 7)) & 1u) != 0u;
             k = (k == 3u - (uint32_t)i && cont) ? k + 1u : k;
         }
-        uint32_t acc = 0, shift = 0;
+        uint32_t va = 0, shift = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const bool use = (uint32_t)i >= 4u - k;
-            acc = use ? (acc | (((pw >> (8 * i)) & 0x7Fu) << shift)) : acc;
+            va = use ? (va | (((pw >> (8 * i)) & 0x7Fu) << shift)) : va;
             shift = use ? shift + 7u : shift;
         }
         tmask = 0;
@@ -431,12 +436,12 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, const StreamRsrc
         for (int i = 0; i < (int)BPL; ++i) {
             const uint32_t b = (d.i[i >> 2] >> (8 * (i & 3))) & 0xFFu;
             const bool valid = BPL * lane + (uint32_t)i < nb;
-            acc |= (b & 0x7Fu) << (shift < 32u ? shift : 0u);
+            va |= (b & 0x7Fu) << (shift < 32u ? shift : 0u);
             const bool term = valid && (b & 0x80u) == 0u;
-            dv[i] = term ? acc : 0u;
+            dv[i] = term ? va : 0u;
             tmask |= term ? (1u << i) : 0u;
             full += dv[i];
-            acc = term ? 0u : acc;
+            va = term ? 0u : va;
             shift = term ? 0u : shift + 7u;
         }
     }
@@ -450,7 +455,7 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, const StreamRsrc
     const uint32_t col0 = E - wave_max_scan(hs ? E : 0u);
 
     // inputs through the cache (one or two columns): loaded before the next
-    // window's loads are issued, so waiting for them does not wait for those
+    // window's data, so waiting for them does not wait for that
     constexpr bool EARLY = !XLDS && NB <= 2;
     XVec<NB> xe[EARLY ? BPL : 1];
     if constexpr (EARLY) {
@@ -462,19 +467,10 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, const StreamRsrc
             const bool t = FAST || ((tmask >> i) & 1u);
             xe[i] = stream_x<NB, false>(a, r, s_x, t ? c : 0u);
         }
+        issue_data(r, wn, mN, dN);
+        __builtin_amdgcn_sched_barrier(0);
     }
 
-    // the next window: descriptor (loaded one window ago), data, and the
-    // descriptor of the window after it
-    mN = uniform_meta(qn);
-    issue_data(r, wn, mN, dN);
-    issue_meta(r, wn2, qn);
-    // (keep the multiply-adds below the loads: issued after them, the
-    // loads would have only the epilogue to arrive in, and the row-scale
-    // load none)
-    __builtin_amdgcn_sched_barrier(0);
-
-    float acc[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j) acc[j] = 0.0f;
     uint32_t c = col0;
@@ -492,11 +488,58 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, const StreamRsrc
 #pragma unroll
         for (int j = 0; j < NB; ++j) acc[j] = __builtin_fmaf(wq, x.v[j], acc[j]);
     }
+}
+
+// Window w (descriptor m, loads d): out[j*out_ld + row] += its row pieces.
+// Its memory operations, in this order: the descriptor load of window wn2
+// (into qn, after qn's descriptor of window wn is read into mN), the row
+// scales, the data loads of window wn (into dN), the output atomics.  With
+// the counter of memory operations completing in order, reading a
+// descriptor or a row scale then never waits for data loads issued after
+// it; and the loads sit in straight-line code (the decode branch holds
+// none, or the same ones on both sides), which keeps the compiler's wait
+// counts exact.
+template <int NB, bool XLDS>
+__device__ __forceinline__ void run_window(const StreamArgs &a, const StreamRsrc &r, int64_t w, const WinMeta &m,
+                                           const WinData &d, int64_t wn, int64_t wn2, WinRaw &qn, WinMeta &mN,
+                                           WinData &dN, const float *s_x) {
+    const uint32_t b0 = (uint32_t)w * WIN_BYTES;
+    mN = uniform_meta(qn);
+    issue_meta(r, wn2, qn);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // the lane's row: rows starting at or before the lane (inclusive count
+    // from the row-start mask) pick its entry of the row list
+    const uint64_t S = ((uint64_t)m.mask_hi << 32) | m.mask_lo;
+    const bool hs = __builtin_amdgcn_inverse_ballot_w64(S);
+    const uint32_t cnt = __builtin_amdgcn_mbcnt_hi(m.mask_hi, __builtin_amdgcn_mbcnt_lo(m.mask_lo, 0u)) + (hs ? 1u : 0u);
+    const uint32_t row = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((cnt - 1u + head_missing(m)) * 4u), (int)d.Rr);
+    // its row scale (used by the last lane of each row piece)
+    const float rsv = buffer_load_f1(r.rsc, row * 4u);
+    __builtin_amdgcn_sched_barrier(0);
+    constexpr bool EARLY = !XLDS && NB <= 2;
+    if constexpr (!EARLY) {
+        // (keep the multiply-adds below these loads: issued after them, the
+        // loads would have only the epilogue to arrive in)
+        issue_data(r, wn, mN, dN);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // fast decode: a whole window of one-byte varints, none continuing from
+    // the window before
+    const bool full = a.nbytes - b0 >= WIN_BYTES;
+    const bool cont = ((d.i[0] | d.i[1] | d.i[2] | d.i[3]) & 0x80808080u) != 0u ||
+                      (lane_id() == 0u && (d.ip & 0x80000000u) != 0u);
+    float acc[NB];
+    if (full && __ballot(cont) == 0ull)
+        window_body<NB, XLDS, true>(a, r, s_x, m, d, b0, hs, wn, mN, dN, acc);
+    else
+        window_body<NB, XLDS, false>(a, r, s_x, m, d, b0, hs, wn, mN, dN, acc);
 
     // per-row pieces: segmented sums over the lanes of each row; the last
     // lane of a piece adds them to the output
-    wave_seg_scan_n<NB>(acc, hs ? 1u : 0u);
-    const bool last = lane == 63u || ((S >> (lane + 1u)) & 1ull) != 0ull;
+    wave_seg_scan_mask<NB>(acc, S);
+    const bool last = __builtin_amdgcn_inverse_ballot_w64((S >> 1) | (1ull << 63));
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
         const float v = a.rsc ? acc[j] * rsv : acc[j];
@@ -505,19 +548,22 @@ __device__ __forceinline__ void run_window(const StreamArgs &a, const StreamRsrc
     }
 }
 
+// Window w of a pass with W waves: data of w + 2W and the descriptor of
+// w + 3W are the loads it issues.
 template <int NB, bool XLDS>
 __device__ __forceinline__ void stream_step(const StreamArgs &a, const StreamRsrc &r, int64_t w, const WinMeta &m,
                                             const WinData &d, int64_t W, WinRaw &qn, WinMeta &mN, WinData &dN,
                                             const float *s_x) {
-    // fast decode: a whole window of one-byte varints, none continuing from
-    // the window before
-    const bool full = a.nbytes - (uint32_t)w * WIN_BYTES >= WIN_BYTES;
-    const bool cont = ((d.i[0] | d.i[1] | d.i[2] | d.i[3]) & 0x80808080u) != 0u ||
-                      (lane_id() == 0u && (d.ip & 0x80000000u) != 0u);
-    if (full && __ballot(cont) == 0ull)
-        run_window<NB, XLDS, true>(a, r, w, m, d, w + W, w + 2 * W, qn, mN, dN, s_x);
-    else
-        run_window<NB, XLDS, false>(a, r, w, m, d, w + W, w + 2 * W, qn, mN, dN, s_x);
+    run_window<NB, XLDS>(a, r, w, m, d, w + 2 * W, w + 3 * W, qn, mN, dN, s_x);
+}
+
+// What a window issues besides its data and descriptor loads, with no effect:
+// a row-scale load (kept: marked volatile) and an atomic, both out of range.
+__device__ __forceinline__ void window_dummies_load(const StreamRsrc &r) {
+    (void)__builtin_amdgcn_raw_buffer_load_b32(r.rsc, (int)OOB_OFFSET, 0, (int)(1u << 31));
+}
+__device__ __forceinline__ void window_dummies_atomic(const StreamRsrc &r) {
+    __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(0.0f, r.out, (int)OOB_OFFSET, 0, 0);
 }
 
 // (8 columns through the cache need more registers than 1024-thread blocks allow)
@@ -547,24 +593,34 @@ __global__ __launch_bounds__((NB == 8 && !XLDS) ? 512 : 1024) void k_stream(Stre
     r.out = buffer_rsrc(a.out, (uint32_t)(((int64_t)(NB - 1) * a.out_ld + a.rows) * 4));
     r.in = buffer_rsrc(a.in, XLDS ? 0u : a.nx * a.in_ld * 4u);
     r.ent = buffer_rsrc(a.ent ? a.ent : a.in, (!XLDS && a.ent) ? a.nx * 4u : 0u);
-    // software pipeline over two register sets: while window w is worked
-    // on, the next window's data and the descriptor of the one after are in
-    // flight
+    // software pipeline over three register sets: while window w is
+    // worked on, the data of the next two windows and the descriptor of the
+    // one after those are in flight.  The prologue issues the same sequence
+    // of memory operations as two windows of the loop (their row-scale loads
+    // and atomics as no-op stand-ins), so the loop is entered with the
+    // operations in flight it repeats with and the compiler's wait counts
+    // stay exact throughout.
     WinRaw q;
     issue_meta(r, w, q);
-    WinMeta mA = uniform_meta(q), mB;
-    WinData dA, dB;
-    issue_data(r, w, mA, dA);
+    WinMeta mA = uniform_meta(q), mB, mC;
+    WinData dA, dB, dC;
     issue_meta(r, w + W, q);
-    // an atomic out of range (dropped), as every window ends with: the loop
-    // is entered with the same memory operations in flight as it repeats
-    // with, which keeps the compiler's wait counts exact in its first half
-    __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(0.0f, r.out, (int)OOB_OFFSET, 0, 0);
+    window_dummies_load(r);
+    issue_data(r, w, mA, dA);
+    window_dummies_atomic(r);
+    mB = uniform_meta(q);
+    issue_meta(r, w + 2 * W, q);
+    window_dummies_load(r);
+    issue_data(r, w + W, mB, dB);
+    window_dummies_atomic(r);
     for (;;) {
-        stream_step<NB, XLDS>(a, r, w, mA, dA, W, q, mB, dB, s_x);
+        stream_step<NB, XLDS>(a, r, w, mA, dA, W, q, mC, dC, s_x);
         w += W;
         if (w >= a.nwin) break;
         stream_step<NB, XLDS>(a, r, w, mB, dB, W, q, mA, dA, s_x);
+        w += W;
+        if (w >= a.nwin) break;
+        stream_step<NB, XLDS>(a, r, w, mC, dC, W, q, mB, dB, s_x);
         w += W;
         if (w >= a.nwin) break;
     }
