@@ -443,6 +443,7 @@ def run_config4(a, hip, api, rt):
                       "achieved_gbs": round(step_bytes / (ms * 1e-3) / 1e9, 2),
                       "pct_hbm_peak": round(100 * step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
                       "steps": steps, "kernels_ms": {k: round(v, 4) for k, v in kern.items()},
+                      "layer_algorithmic_bytes": alg,
                       "dominant": {"kernel": dom[0], "op_ms": round(dom[1], 4),
                                    "algorithmic_bytes": alg[dom_layer], "achieved_gbs": round(ach, 2),
                                    "frac": round(ach / HBM_PEAK_GBS, 4)}}
