@@ -132,19 +132,50 @@ int sili_get_output_scale(const sili_layer *layer, float *os);
 int sili_forward_dense(sili_layer *layer, const float *x, int64_t batch, float *y,
                        void *stream);
 
-/* backward_dense at learning_rate 0 (sili/cpu_backend.cpp:496-529,
- * linear_disldo.hpp:462-2113): dx [batch,n_in] = W^T-gather of dy
- * (overwritten).  x may be NULL: then the input of the last forward_dense on
- * this layer is used, as the reference's backward_dense uses its stored
- * last_input (available for batch > 1; with batch 1 pass x).  Always
- * accumulates neuron_input_accum += sum_b|x| and
+/* backward_dense (sili/cpu_backend.cpp:496-529, linear_disldo.hpp:462-2113):
+ * dx [batch,n_in] = W^T-gather of dy (overwritten).  x may be NULL: then the
+ * input of the last forward_dense on this layer is used, as the reference's
+ * backward_dense uses its stored last_input (available for batch > 1; with
+ * batch 1 pass x).  Always accumulates neuron_input_accum += sum_b|x| and
  * neuron_grad_accum += sum_b|dy| (linear_disldo.hpp:515-520).  When gw_s /
- * gw_b are non-NULL, also writes the nnz-sampled grad-W (see
- * sili_sampled_gradw).  learning_rate must be 0 (the fused optimizer update
- * is not implemented yet: SILI_ERR_INVALID otherwise). */
+ * gw_b are non-NULL (learning_rate 0 only), also writes the nnz-sampled
+ * grad-W (see sili_sampled_gradw).  learning_rate != 0 runs the optimizer
+ * update with the binding's defaults, as sili_backward_dense_train with
+ * lr_per_row_nnz 0, damp_by_importance 1, beta2 0.999, eps 1e-8. */
 int sili_backward_dense(sili_layer *layer, const float *x, const float *dy, int64_t batch,
                         float *dx, float *gw_s, float *gw_b, float learning_rate,
                         void *stream);
+
+/* backward_dense with the optimizer update (sili/cpu_backend.cpp:496-529;
+ * disldo_backward, linear_disldo.hpp:466-2113, with RMSpropScalePolicy, no
+ * deferred scale write, BoundedRMSpropSynapsePolicy, beta1 0.9,
+ * min_decay_frac 0, max_abs_delta 2, max_ci 100, zero_escape_eps 0.1): for
+ * every synapse, batch-sequential RMSprop steps on its stored weight code and
+ * importance, re-quantized in place (deterministically or stochastically,
+ * sili_set_stochastic_rounding); dx from the updated weights; the value
+ * scales' RMSprop step, the Adam step of rows without synapses, and the output
+ * scales' step when they are trainable.  batch <= 1024.  Layers holding block4
+ * tiles: SILI_ERR_INVALID (not implemented on the GPU path yet).
+ * learning_rate 0 is plain backward_dense. */
+int sili_backward_dense_train(sili_layer *layer, const float *x, const float *dy, int64_t batch,
+                              float *dx, float learning_rate, int lr_per_row_nnz,
+                              int damp_by_importance, float beta2, float eps, void *stream);
+
+/* Rounding of the update's re-quantization: 1 (default, as the reference's
+ * SparseLinearLayer, sili/cpu_backend.cpp:992) stochastic -- unbiased dithered
+ * rounding (fp4quant.hpp:210-265) driven by a counter-based generator of this
+ * layer (splitmix64 of seed, call and synapse), reproducible for a given seed
+ * and call sequence; 0 deterministic round-to-nearest, as
+ * SparseLinearLayerDeterministic (sili/cpu_backend.cpp:1007). */
+int sili_set_stochastic_rounding(sili_layer *layer, int on);
+/* Restart this layer's rounding generator at seed (fp4_seed_stochastic_rng,
+ * fp4quant.hpp:186-188, is the reference's per-thread counterpart). */
+int sili_seed_stochastic_rounding(sili_layer *layer, uint64_t seed);
+/* The scales' optimizer state (delta_csr_types.hpp:1127-1215), host outputs,
+ * [n*rank] like the scales; any pointer may be NULL.  Zero before the first
+ * update. */
+int sili_get_scale_state(const sili_layer *layer, float *vs_importance, float *os_importance,
+                         float *vs_momentum, uint32_t *vs_step, uint32_t *os_step);
 
 /* nnz-pattern-sampled grad-W: gw_s[e] = sum_b x[b,r(e)]*dy[b,c(e)] for every
  * scattered synapse e in storage order; gw_b[16*t + slot] likewise for every

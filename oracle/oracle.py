@@ -15,6 +15,10 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "_build" / "liboracle.so"
+# The same restatement compiled with a*b+c contracted into FMAs, as the
+# reference's own build does: used only to pin the restatement bit-exactly
+# against the compiled reference where contraction changes fp32 results.
+LIB_FMA_PATH = HERE / "_build" / "liboracle_fma.so"
 REF_PATH = HERE / "_ref" / "libsili_ref.so"
 
 _u8p = C.POINTER(C.c_uint8)
@@ -39,6 +43,24 @@ class _OracleLayerC(C.Structure):
     ]
 
 
+class _TrainParams(C.Structure):
+    _fields_ = [("lr", C.c_float), ("lr_per_row_nnz", C.c_int32), ("damp_by_importance", C.c_int32),
+                ("beta2", C.c_float), ("eps", C.c_float), ("beta1", C.c_float), ("min_decay_frac", C.c_float),
+                ("max_abs_delta", C.c_float), ("max_ci", C.c_float), ("zero_escape_eps", C.c_float)]
+
+
+class _TrainState(C.Structure):
+    _fields_ = [("value_scale", _f32p), ("vs_importance", _f32p), ("vs_momentum", _f32p),
+                ("vs_step", C.POINTER(C.c_uint32)), ("output_scale", _f32p), ("os_importance", _f32p),
+                ("os_step", C.POINTER(C.c_uint32)), ("importance_scale", _f32p),
+                ("output_importance_scale", _f32p), ("out_degree", _i32p), ("output_scale_trainable", C.c_int32),
+                ("quant_out", _f32p), ("imp_out", _f32p)]
+
+
+# the constants sili/cpu_backend.cpp:496-528 passes to disldo_backward
+TRAIN_DEFAULTS = dict(beta1=0.9, min_decay_frac=0.0, max_abs_delta=2.0, max_ci=100.0, zero_escape_eps=0.1)
+
+
 class _SynStats(C.Structure):
     _fields_ = [(n, C.c_int64) for n in (
         "n_prune_target", "n_pruned", "n_grown", "n_demoted_tiles", "n_promoted_tiles",
@@ -51,16 +73,17 @@ def _p(a: np.ndarray | None, t):
     return a.ctypes.data_as(t)
 
 
-_lib = None
+_libs: dict = {}
 _ref = None
 
 
-def lib():
-    global _lib
-    if _lib is None:
-        if not LIB_PATH.exists():
+def lib(contracted: bool = False):
+    """The restatement; contracted=True: its FMA-contracted build."""
+    if contracted not in _libs:
+        path = LIB_FMA_PATH if contracted else LIB_PATH
+        if not path.exists():
             build(ref=False)
-        L = C.CDLL(str(LIB_PATH))
+        L = C.CDLL(str(path))
         L.oracle_fp4_decode.restype = C.c_float
         L.oracle_fp4_decode.argtypes = [C.c_uint8]
         L.oracle_fp4_encode.restype = C.c_uint8
@@ -85,11 +108,14 @@ def lib():
                                              C.c_int64, _f32p, _f32p, _f32p, C.c_int, C.c_int]
         L.oracle_sampled_gradw.argtypes = [C.POINTER(_OracleLayerC), _f32p, _f32p, C.c_int64, _f32p,
                                            _f32p, C.c_int, C.c_int]
+        L.oracle_backward_train.argtypes = [C.POINTER(_OracleLayerC), _u8p, C.POINTER(_TrainState), _f32p, _f32p,
+                                            C.c_int64, _f32p, _f32p, _f32p, C.POINTER(_TrainParams)]
+        L.oracle_backward_train.restype = C.c_int
         L.oracle_synapto_step.argtypes = [C.POINTER(_OracleLayerC), C.c_float, _i32p, _i32p, _f32p, _f32p,
                                           C.c_int64, C.c_int, _i32p, _i32p, _u8p, _i32p, _i32p, _u8p,
                                           C.POINTER(_SynStats)]
-        _lib = L
-    return _lib
+        _libs[contracted] = L
+    return _libs[contracted]
 
 
 def have_ref() -> bool:
@@ -131,6 +157,12 @@ def reflib():
         R.ref_backward_sparse.argtypes = [C.c_void_p, _f32p, _i32p, _i32p, _f32p, C.c_int, _f32p, _f32p,
                                           _f32p, C.c_int]
         R.ref_row_remove_col.restype = C.c_int
+        R.ref_backward_train.argtypes = [C.c_void_p, _f32p, _f32p, C.c_int, _f32p, _f32p, _f32p, C.c_float,
+                                         C.c_int, C.c_int, C.c_float, C.c_float, C.c_int]
+        R.ref_layer_set_importance_scales.argtypes = [C.c_void_p, _f32p, _f32p]
+        _u32p = C.POINTER(C.c_uint32)
+        R.ref_layer_set_train_state.argtypes = [C.c_void_p, _f32p, _f32p, _u32p, _f32p, _u32p, C.c_int]
+        R.ref_layer_get_train_state.argtypes = [C.c_void_p, _f32p, _f32p, _f32p, _u32p, _f32p, _f32p, _u32p]
         R.ref_row_remove_col.argtypes = [C.c_void_p, C.c_int, C.c_int]
         R.ref_row_insert_col.restype = C.c_int
         R.ref_row_insert_col.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_float, C.c_float]
@@ -192,6 +224,15 @@ class HostLayer:
         os_ = np.zeros(n_out * rank, np.float32)
         os_[::rank] = 1.0
         self.value_scale, self.output_scale = vs, os_
+        # the scales' optimizer state (delta_csr_types.hpp:1127-1215)
+        self.vs_importance = np.zeros(n_in * rank, np.float32)
+        self.vs_momentum = np.zeros(n_in * rank, np.float32)
+        self.vs_step = np.zeros(n_in * rank, np.uint32)
+        self.os_importance = np.zeros(n_out * rank, np.float32)
+        self.os_step = np.zeros(n_out * rank, np.uint32)
+        self.importance_scale = None
+        self.output_importance_scale = None
+        self.output_scale_trainable = False
 
     # -- construction ----------------------------------------------------------
     def load_csr(self, ptrs, cols, w=None, imp=None, bytes_=None):
@@ -322,6 +363,38 @@ class HostLayer:
                                      threads, int(absmode))
         return dx, ai, ag
 
+    def out_degree(self) -> np.ndarray:
+        return np.bincount(self.decode_cols(), minlength=self.n_out).astype(np.int32)
+
+    def backward_train(self, x, dy, lr, lr_per_row_nnz=False, damp_by_importance=True, beta2=0.999, eps=1e-8,
+                       acc=None, contracted=False):
+        """Backward with the optimizer update (deterministic rounding, one
+        thread): updates self.val and the scale state in place; returns dx and
+        the activity accumulators.  self.last_quant / self.last_imp: every
+        synapse's weight code value and importance before re-quantization.
+        contracted=True runs the FMA-contracted build of the restatement."""
+        self.last_quant = np.zeros(max(1, self.nnz), np.float32)
+        self.last_imp = np.zeros(max(1, self.nnz), np.float32)
+        x = _c(np.atleast_2d(x), np.float32)
+        dy = _c(np.atleast_2d(dy), np.float32)
+        dx = np.zeros_like(x)
+        ai = np.zeros(self.n_in, np.float32) if acc is None else acc[0]
+        ag = np.zeros(self.n_out, np.float32) if acc is None else acc[1]
+        deg = self.out_degree()
+        isc = None if self.importance_scale is None else _c(self.importance_scale, np.float32)
+        oisc = None if self.output_importance_scale is None else _c(self.output_importance_scale, np.float32)
+        u32p = C.POINTER(C.c_uint32)
+        st = _TrainState(_p(self.value_scale, _f32p), _p(self.vs_importance, _f32p), _p(self.vs_momentum, _f32p),
+                         _p(self.vs_step, u32p), _p(self.output_scale, _f32p), _p(self.os_importance, _f32p),
+                         _p(self.os_step, u32p), _p(isc, _f32p), _p(oisc, _f32p), _p(deg, _i32p),
+                         int(self.output_scale_trainable), _p(self.last_quant, _f32p), _p(self.last_imp, _f32p))
+        P = _TrainParams(lr, int(lr_per_row_nnz), int(damp_by_importance), beta2, eps, **TRAIN_DEFAULTS)
+        s = self._cstruct()
+        if lib(contracted).oracle_backward_train(C.byref(s), _p(self.val, _u8p), C.byref(st), _p(x, _f32p), _p(dy, _f32p),
+                                       x.shape[0], _p(dx, _f32p), _p(ai, _f32p), _p(ag, _f32p), C.byref(P)) != 0:
+            raise ValueError("backward_train: layers with block4 tiles are not supported")
+        return dx, ai, ag
+
     def sampled_gradw(self, x, dy, threads=8, absmode=False):
         x = _c(np.atleast_2d(x), np.float32)
         dy = _c(np.atleast_2d(dy), np.float32)
@@ -439,6 +512,44 @@ class RefLayer:
         ag = np.zeros(self.n_out, np.float32)
         reflib().ref_backward_dense(self.h, _p(x, _f32p), _p(dy, _f32p), x.shape[0], _p(dx, _f32p),
                                     _p(ai, _f32p), _p(ag, _f32p), threads)
+        return dx, ai, ag
+
+    def set_importance_scales(self, is_=None, ois=None):
+        self._is = None if is_ is None else _c(is_, np.float32)
+        self._ois = None if ois is None else _c(ois, np.float32)
+        reflib().ref_layer_set_importance_scales(self.h, _p(self._is, _f32p), _p(self._ois, _f32p))
+
+    def set_train_state(self, vs_imp=None, vs_mom=None, vs_step=None, os_imp=None, os_step=None, os_trainable=-1):
+        u32p = C.POINTER(C.c_uint32)
+        a = [None if v is None else _c(v, t) for v, t in ((vs_imp, np.float32), (vs_mom, np.float32),
+                                                            (vs_step, np.uint32), (os_imp, np.float32),
+                                                            (os_step, np.uint32))]
+        reflib().ref_layer_set_train_state(self.h, _p(a[0], _f32p), _p(a[1], _f32p), _p(a[2], u32p),
+                                           _p(a[3], _f32p), _p(a[4], u32p), int(os_trainable))
+
+    def get_train_state(self, rank=1):
+        nr, nc = self.n_in * rank, self.n_out * rank
+        out = dict(value_scale=np.zeros(nr, np.float32), vs_importance=np.zeros(nr, np.float32),
+                   vs_momentum=np.zeros(nr, np.float32), vs_step=np.zeros(nr, np.uint32),
+                   output_scale=np.zeros(nc, np.float32), os_importance=np.zeros(nc, np.float32),
+                   os_step=np.zeros(nc, np.uint32))
+        u32p = C.POINTER(C.c_uint32)
+        reflib().ref_layer_get_train_state(self.h, _p(out["value_scale"], _f32p), _p(out["vs_importance"], _f32p),
+                                           _p(out["vs_momentum"], _f32p), _p(out["vs_step"], u32p),
+                                           _p(out["output_scale"], _f32p), _p(out["os_importance"], _f32p),
+                                           _p(out["os_step"], u32p))
+        return out
+
+    def backward_train(self, x, dy, lr, lr_per_row_nnz=False, damp_by_importance=True, beta2=0.999, eps=1e-8,
+                       threads=1):
+        x = _c(np.atleast_2d(x), np.float32)
+        dy = _c(np.atleast_2d(dy), np.float32)
+        dx = np.zeros_like(x)
+        ai = np.zeros(self.n_in, np.float32)
+        ag = np.zeros(self.n_out, np.float32)
+        reflib().ref_backward_train(self.h, _p(x, _f32p), _p(dy, _f32p), x.shape[0], _p(dx, _f32p), _p(ai, _f32p),
+                                    _p(ag, _f32p), lr, int(lr_per_row_nnz), int(damp_by_importance), beta2, eps,
+                                    threads)
         return dx, ai, ag
 
     def forward_sparse(self, ptrs, idx, vals, batch, threads=1):

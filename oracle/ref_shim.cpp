@@ -184,6 +184,64 @@ void ref_backward_dense(void *h, const float *x, const float *dy, int batch, flo
                                         2.0f, 100.0f);
 }
 
+// sili/cpu_backend.cpp:496-529 (backward_dense) with the optimizer update, as
+// SparseLinearLayerDeterministic runs it (sili/cpu_backend.cpp:1007:
+// RMSpropScalePolicy, no deferred scale write, deterministic rounding), with
+// the production policy constants.
+void ref_backward_train(void *h, const float *x, const float *dy, int batch, float *dx, float *acc_in,
+                        float *acc_grad, float lr, int lr_per_row_nnz, int damp, float beta2, float eps,
+                        int threads) {
+    auto *L = static_cast<RefLayer *>(h);
+    std::memset(dx, 0, sizeof(float) * size_t(batch) * size_t(L->n_in));
+    disldo_backward<S, FP4BiPacked, COL, RMSpropScalePolicy<float>, false, false>(
+        x, S(batch), S(L->n_in), dy, L->w, dx, acc_in, acc_grad, lr, threads, lr_per_row_nnz != 0, damp != 0,
+        beta2, eps, 0.9f, 0.0f, 2.0f, 100.0f);
+}
+
+// Per-row / per-column importance scales (delta_csr_types.hpp:1006-1031).
+void ref_layer_set_importance_scales(void *h, const float *is, const float *ois) {
+    auto *L = static_cast<RefLayer *>(h);
+    if (is)
+        for (int r = 0; r < L->n_in; ++r) L->w.set_importance_scale_raw(size_t(r), is[r]);
+    if (ois)
+        for (int c = 0; c < L->n_out; ++c) L->w.set_output_importance_scale_raw(size_t(c), ois[c]);
+}
+
+// The scales' optimizer state (delta_csr_types.hpp:1127-1215), rank-major
+// per row / column like the scales; any pointer may be NULL.
+void ref_layer_set_train_state(void *h, const float *vs_imp, const float *vs_mom, const uint32_t *vs_step,
+                               const float *os_imp, const uint32_t *os_step, int os_trainable) {
+    auto *L = static_cast<RefLayer *>(h);
+    const size_t nr = size_t(L->n_in) * L->w.scale_rank, nc = size_t(L->n_out) * L->w.scale_rank;
+    if (vs_imp) L->w.value_scale_importance.assign(vs_imp, vs_imp + nr);
+    if (vs_mom) L->w.value_scale_momentum.assign(vs_mom, vs_mom + nr);
+    if (vs_step) L->w.value_scale_step.assign(vs_step, vs_step + nr);
+    if (os_imp) L->w.output_scale_importance.assign(os_imp, os_imp + nc);
+    if (os_step) L->w.output_scale_step.assign(os_step, os_step + nc);
+    if (os_trainable >= 0) L->w.output_scale_is_trainable = os_trainable != 0;
+}
+
+void ref_layer_get_train_state(void *h, float *vs, float *vs_imp, float *vs_mom, uint32_t *vs_step, float *os,
+                               float *os_imp, uint32_t *os_step) {
+    auto *L = static_cast<RefLayer *>(h);
+    const size_t rk = L->w.scale_rank;
+    for (int r = 0; r < L->n_in; ++r)
+        for (size_t k = 0; k < rk; ++k) {
+            const size_t i = size_t(r) * rk + k;
+            if (vs) vs[i] = L->w.get_value_scale_k(size_t(r), k);
+            if (vs_imp) vs_imp[i] = i < L->w.value_scale_importance.size() ? L->w.value_scale_importance[i] : 0.0f;
+            if (vs_mom) vs_mom[i] = i < L->w.value_scale_momentum.size() ? L->w.value_scale_momentum[i] : 0.0f;
+            if (vs_step) vs_step[i] = i < L->w.value_scale_step.size() ? L->w.value_scale_step[i] : 0u;
+        }
+    for (int c = 0; c < L->n_out; ++c)
+        for (size_t k = 0; k < rk; ++k) {
+            const size_t i = size_t(c) * rk + k;
+            if (os) os[i] = L->w.get_output_scale_k(size_t(c), k);
+            if (os_imp) os_imp[i] = L->w.get_output_scale_importance_k(size_t(c), k);
+            if (os_step) os_step[i] = i < L->w.output_scale_step.size() ? L->w.output_scale_step[i] : 0u;
+        }
+}
+
 // sili/cpu_backend.cpp:571-585 (forward_sparse).
 void ref_forward_sparse(void *h, const int32_t *ptrs, const int32_t *idx, const float *vals,
                         int batch, float *y, int threads) {

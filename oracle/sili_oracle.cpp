@@ -772,3 +772,185 @@ int oracle_synapto_step(const OracleLayer *L, float prune_frac, const int32_t *c
 }
 
 }  // extern "C"
+
+// ---- backward with the optimizer update ------------------------------------
+namespace {
+
+// std::max / std::min as the reference calls them (a NaN first operand is
+// returned as is).
+inline float std_max(float a, float b) { return (a < b) ? b : a; }
+inline float std_min(float a, float b) { return (b < a) ? b : a; }
+
+// BoundedRMSpropSynapsePolicy::update_ci (delta_csr_types.hpp:707-712).
+inline float bounded_update_ci(float ci, float g, float contrib, float beta2, float min_decay_frac,
+                               float max_ci) {
+    const float ema = beta2 * ci + (1.0f - beta2) * (g * g + contrib * contrib);
+    const float floor_ = min_decay_frac * ci;
+    return std_min(std_max(ema, floor_), max_ci);
+}
+
+// BoundedRMSpropSynapsePolicy::update_cw (delta_csr_types.hpp:749-758).
+inline float bounded_update_cw(float g, float ci, float S, float eff_lr, float eps, bool damp,
+                               float max_abs_delta) {
+    float raw = damp ? (-g * S) / (std::sqrt(ci) + eps) : (-g * S);
+    if (raw > max_abs_delta) raw = max_abs_delta;
+    if (raw < -max_abs_delta) raw = -max_abs_delta;
+    return eff_lr * raw;
+}
+
+// RMSpropScalePolicy::update with its bias-correction counter
+// (delta_csr_types.hpp:413-434).
+inline void rmsprop_scale_update(float &scale, float &state, float g_agg, float eff_lr, float beta2,
+                                 float eps, float contrib_agg, uint32_t &step) {
+    if (!std::isfinite(g_agg) || !std::isfinite(contrib_agg)) return;
+    const float new_state = beta2 * state + (1.0f - beta2) * (g_agg * g_agg + contrib_agg * contrib_agg);
+    if (!std::isfinite(new_state)) return;
+    float state_hat = new_state;
+    ++step;
+    const float bias_correction = 1.0f - std::pow(beta2, static_cast<float>(step));
+    if (bias_correction > 0.0f) state_hat = new_state / bias_correction;
+    if (!std::isfinite(state_hat)) return;
+    const float new_scale = scale - eff_lr * g_agg / (std::sqrt(state_hat) + eps);
+    if (!std::isfinite(new_scale)) return;
+    state = new_state;
+    scale = new_scale;
+}
+
+}  // namespace
+
+extern "C" {
+
+// linear_disldo.hpp:466-2113 (scattered loop :624-880, dead-row bootstrap
+// :1944-2040, dx reduction :2043-2048, output_scale update :2050-2080).
+int oracle_backward_train(const OracleLayer *L, uint8_t *val, OracleTrainState *S,
+                          const float *x, const float *dy, int64_t batch, float *dx,
+                          float *acc_in, float *acc_grad, const OracleTrainParams *P) {
+    if (L->n_tiles > 0) return -1;
+    const int64_t n_in = L->n_in, n_out = L->n_out;
+    const int rank = L->rank;
+    const float lr = P->lr;
+    for (int64_t b = 0; b < batch; ++b) {
+        for (int64_t r = 0; r < n_in; ++r) acc_in[r] += std::fabs(x[b * n_in + r]);
+        for (int64_t c = 0; c < n_out; ++c) acc_grad[c] += std::fabs(dy[b * n_out + c]);
+    }
+    std::vector<float> mdx(size_t(batch * n_in), 0.0f);
+    std::vector<float> mcol(size_t(n_out * rank), 0.0f), mcol_c(size_t(n_out * rank), 0.0f);
+    float *vs = S->value_scale, *os = S->output_scale;
+    for (int64_t r = 0; r < n_in; ++r) {
+        const uint64_t e0 = L->row_elem_start[r], e1 = L->row_elem_start[r + 1];
+        const uint64_t nnz_row = e1 - e0;
+        if (nnz_row == 0) continue;
+        const float eff_lr = P->lr_per_row_nnz ? lr / static_cast<float>(nnz_row) : lr;
+        const float scale_eff_lr = lr / static_cast<float>(nnz_row);
+        const float imp_scale = S->importance_scale ? S->importance_scale[r] : 1.0f;
+        double sg[4] = {0, 0, 0, 0}, sgc[4] = {0, 0, 0, 0};
+        uint64_t pos = L->row_byte_start[r];
+        uint32_t col = 0;
+        for (uint64_t vb = e0; vb < e1; ++vb) {
+            col += uleb_dec(L->idx, pos);
+            const float cw_orig = fp4_dec(val[vb] >> 4);
+            const float ci_orig = fp4_dec(val[vb] & 0xFu);
+            const float out_imp_scale = S->output_importance_scale ? S->output_importance_scale[col] : 1.0f;
+            const float combined_imp_scale = imp_scale * out_imp_scale;
+            float ci = ci_orig * combined_imp_scale;
+            float Sc = 0.0f;
+            for (int k = 0; k < rank; ++k) Sc += vs[r * rank + k] * os[int64_t(col) * rank + k];
+            float quant = cw_orig;
+            float cw = quant * Sc;
+            for (int64_t b = 0; b < batch; ++b) {
+                const float iv = x[b * n_in + r];
+                const float dyv = dy[b * n_out + col];
+                const float g = dyv * iv;
+                if (lr != 0.0f) {
+                    const float contrib = iv * cw_orig;
+                    ci = bounded_update_ci(ci, g, contrib, P->beta2, P->min_decay_frac, P->max_ci);
+                    quant += bounded_update_cw(g, ci, Sc, eff_lr, P->eps, P->damp_by_importance != 0,
+                                               P->max_abs_delta);
+                    cw = quant * Sc;
+                    const float qf = (quant == 0.0f) ? P->zero_escape_eps : quant;
+                    for (int k = 0; k < rank; ++k) {
+                        const float os_k = os[int64_t(col) * rank + k];
+                        const float vs_k = vs[r * rank + k];
+                        sg[k] += static_cast<double>(qf) * static_cast<double>(os_k) * g;
+                        mcol[size_t(col) * rank + k] += qf * vs_k * g;
+                        sgc[k] += static_cast<double>(qf) * static_cast<double>(os_k) * contrib;
+                        mcol_c[size_t(col) * rank + k] += qf * vs_k * contrib;
+                    }
+                }
+                mdx[size_t(b * n_in + r)] += cw * dyv;
+            }
+            if (lr != 0.0f) {
+                if (S->quant_out) S->quant_out[vb] = quant;
+                if (S->imp_out) S->imp_out[vb] = ci / combined_imp_scale;
+                val[vb] = uint8_t((fp4_enc(quant) << 4) | fp4_enc(ci / combined_imp_scale));
+            }
+        }
+        if (lr != 0.0f) {
+            for (int k = 0; k < rank; ++k) {
+                const int64_t i = r * rank + k;
+                rmsprop_scale_update(vs[i], S->vs_importance[i], static_cast<float>(sg[k]), scale_eff_lr, P->beta2,
+                                     P->eps, static_cast<float>(sgc[k]), S->vs_step[i]);
+            }
+        }
+    }
+    // rows with no synapse: a two-moment step on value_scale from
+    // g = x[row] * sum_col(os * dy)
+    if (lr != 0.0f) {
+        bool any_dead = false;
+        for (int64_t r = 0; r < n_in && !any_dead; ++r) any_dead = L->row_elem_start[r + 1] == L->row_elem_start[r];
+        if (any_dead) {
+            std::vector<double> dead_S(size_t(batch * rank), 0.0);
+            for (int64_t b = 0; b < batch; ++b)
+                for (int k = 0; k < rank; ++k) {
+                    double s = 0.0;
+                    for (int64_t c = 0; c < n_out; ++c)
+                        s += static_cast<double>(os[c * rank + k]) * static_cast<double>(dy[b * n_out + c]);
+                    dead_S[size_t(b * rank + k)] = s;
+                }
+            for (int64_t r = 0; r < n_in; ++r) {
+                if (L->row_elem_start[r + 1] != L->row_elem_start[r]) continue;
+                for (int k = 0; k < rank; ++k) {
+                    double sum = 0.0;
+                    for (int64_t b = 0; b < batch; ++b) {
+                        const float iv = x[b * n_in + r];
+                        if (iv == 0.0f) continue;
+                        sum += static_cast<double>(iv) * dead_S[size_t(b * rank + k)];
+                    }
+                    if (sum == 0.0) continue;
+                    const float g = static_cast<float>(sum);
+                    if (!std::isfinite(g)) continue;
+                    const int64_t i = r * rank + k;
+                    float &m = S->vs_momentum[i];
+                    float &v = S->vs_importance[i];
+                    const float new_m = P->beta1 * m + (1.0f - P->beta1) * g;
+                    const float new_v = P->beta2 * v + (1.0f - P->beta2) * g * g;
+                    if (!std::isfinite(new_m) || !std::isfinite(new_v)) continue;
+                    const float dead_lr = lr / static_cast<float>(n_out);
+                    const float new_vs = vs[i] - dead_lr * new_m / (std::sqrt(new_v) + P->eps);
+                    if (!std::isfinite(new_vs)) continue;
+                    m = new_m;
+                    v = new_v;
+                    vs[i] = new_vs;
+                }
+            }
+        }
+    }
+    for (size_t i = 0; i < mdx.size(); ++i) dx[i] += mdx[i];
+    if (lr != 0.0f && S->output_scale_trainable) {
+        for (int64_t c = 0; c < n_out; ++c) {
+            const int32_t deg = S->out_degree ? S->out_degree[c] : 0;
+            if (deg == 0) continue;
+            const float col_eff_lr = lr / static_cast<float>(deg);
+            for (int k = 0; k < rank; ++k) {
+                const int64_t i = c * rank + k;
+                const double sum = 0.0 + static_cast<double>(mcol[size_t(i)]);
+                const double sum_c = 0.0 + static_cast<double>(mcol_c[size_t(i)]);
+                rmsprop_scale_update(os[i], S->os_importance[i], static_cast<float>(sum), col_eff_lr, P->beta2,
+                                     P->eps, static_cast<float>(sum_c), S->os_step[i]);
+            }
+        }
+    }
+    return 0;
+}
+
+}  // extern "C"

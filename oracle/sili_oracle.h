@@ -107,6 +107,43 @@ void oracle_sampled_gradw(const OracleLayer *L, const float *x, const float *dy,
                           int64_t batch, float *gw_scattered, float *gw_tiles,
                           int threads, int absmode);
 
+/* ---- backward with the optimizer update (learning_rate != 0) ----
+ * disldo_backward (linear_disldo.hpp:466-2113) as SparseLinearLayerDeterministic
+ * runs it (sili/cpu_backend.cpp:1007: RMSpropScalePolicy, no deferred scale
+ * write, deterministic rounding) with BoundedRMSpropSynapsePolicy and the
+ * constants of sili/cpu_backend.cpp:496-528, on a layer without block4 tiles,
+ * one thread (the accumulation order of num_cpus = 1).  The value bytes and the
+ * scale state are updated in place; dx, acc_in and acc_grad ACCUMULATE. */
+typedef struct {
+    float lr;
+    int32_t lr_per_row_nnz;
+    int32_t damp_by_importance;
+    float beta2, eps, beta1, min_decay_frac, max_abs_delta, max_ci, zero_escape_eps;
+} OracleTrainParams;
+
+typedef struct {
+    float *value_scale;                   /* [n_in*rank]  */
+    float *vs_importance;                 /* [n_in*rank]  */
+    float *vs_momentum;                   /* [n_in*rank]  */
+    uint32_t *vs_step;                    /* [n_in*rank]  */
+    float *output_scale;                  /* [n_out*rank] */
+    float *os_importance;                 /* [n_out*rank] */
+    uint32_t *os_step;                    /* [n_out*rank] */
+    const float *importance_scale;        /* [n_in]  or NULL (ones) */
+    const float *output_importance_scale; /* [n_out] or NULL (ones) */
+    const int32_t *out_degree;            /* [n_out] */
+    int32_t output_scale_trainable;
+    float *quant_out;                     /* [nnz] or NULL: each synapse's updated weight code value
+                                             before re-quantization */
+    float *imp_out;                       /* [nnz] or NULL: its importance (stored units) before it */
+} OracleTrainState;
+
+/* L supplies structure (its val / scale pointers are not read); val: the
+ * layer's value bytes, updated.  Returns -1 on a layer with block4 tiles. */
+int oracle_backward_train(const OracleLayer *L, uint8_t *val, OracleTrainState *S,
+                          const float *x, const float *dy, int64_t batch, float *dx,
+                          float *acc_in, float *acc_grad, const OracleTrainParams *P);
+
 /* ---- bulk synaptogenesis step (magnitude prune + candidate regrow) ----
  * Output capacities: scattered entries <= nnz + n_cand + 16*n_tiles,
  * tiles <= n_tiles + n_cand.  Outputs are absolute: out_ptrs[n_in+1],

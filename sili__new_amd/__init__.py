@@ -22,8 +22,11 @@ except ImportError as e:  # pragma: no cover - exercised only on an unbuilt tree
         f"(looked in {_HERE}): {e}") from e
 
 SparseLinearLayer = _ext.SparseLinearLayer
+SparseLinearLayerDeterministic = _ext.SparseLinearLayerDeterministic
 fp4_quantize_array = _ext.fp4_quantize_array
+seed_fp4_stochastic_rng = _ext.seed_fp4_stochastic_rng
 
 LIB_PATH = os.path.join(_HERE, "libsili_hip.so")
 
-__all__ = ["SparseLinearLayer", "fp4_quantize_array", "LIB_PATH"]
+__all__ = ["SparseLinearLayer", "SparseLinearLayerDeterministic", "fp4_quantize_array", "seed_fp4_stochastic_rng",
+           "LIB_PATH"]

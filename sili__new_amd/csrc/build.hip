@@ -424,6 +424,12 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
     if (N > 0)
         SILI_HIP(hipMemcpyAsync(dst.val.p, tbytes.p, (size_t)N, hipMemcpyDeviceToDevice, st));
     SILI_HIP(hipStreamSynchronize(st));
+    // a training layer keeps the permutation (shadow entry -> canonical
+    // entry): its updates rewrite the canonical value bytes and copy them over
+    if (&dst == &L.Wt) {
+        if (L.keep_perm && N > 0) L.Wt_perm = std::move(perm);
+        else L.Wt_perm.reset();
+    }
 }
 
 // Column-block selection: flag entries of block k; gather them with columns

@@ -216,6 +216,7 @@ void reset_scales(Layer &L) {
     SILI_HIP(hipStreamSynchronize(L.stream));
     L.vs_ones = L.os_ones = (L.rank == 1);
     L.nonfinite_scales = false;
+    L.train_state_ready = false;  // the scales' optimizer state restarts at zero
 }
 
 // Feature-major copy of activations [B, n] -> [n, B] (B == 1: no copy).
@@ -350,6 +351,100 @@ void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float 
         launch_gather_b4(L.B4.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
     if (scat && gw_s && !fused) launch_sddmm(L.W.plan(), xT, gT, B, gw_s, L.acc_in.p, st);
     if (gw_b && L.B4.ntiles > 0) launch_sddmm_b4(L.B4.plan(), nullptr, xT, gT, B, gw_b, st);
+}
+
+// The scales' optimizer state, zeroed on first use (the reference sizes it
+// with zeros inside disldo_backward, linear_disldo.hpp:578-605).
+void ensure_train_state(Layer &L, hipStream_t st) {
+    if (L.train_state_ready) return;
+    const size_t nr = (size_t)(L.n_in * L.rank), nc = (size_t)(L.n_out * L.rank);
+    L.vs_imp.ensure(nr);
+    L.vs_mom.ensure(nr);
+    L.vs_step.ensure(nr);
+    L.os_imp.ensure(nc);
+    L.os_step.ensure(nc);
+    fill(L.vs_imp.p, (int64_t)nr, 0.0f, st);
+    fill(L.vs_mom.p, (int64_t)nr, 0.0f, st);
+    fill(reinterpret_cast<float *>(L.vs_step.p), (int64_t)nr, 0.0f, st);
+    fill(L.os_imp.p, (int64_t)nc, 0.0f, st);
+    fill(reinterpret_cast<float *>(L.os_step.p), (int64_t)nc, 0.0f, st);
+    L.train_state_ready = true;
+}
+
+// pow_tab[s] = powf(beta2, s) for s <= need: the bias correction of
+// RMSpropScalePolicy::update (delta_csr_types.hpp:427), computed with the
+// host's powf (the function the reference calls) and looked up on the device.
+void ensure_pow_table(Layer &L, float beta2, int64_t need, hipStream_t st) {
+    if (L.pow_n >= need && std::memcmp(&L.pow_beta2, &beta2, 4) == 0 && L.pow_tab.p) return;
+    const int64_t n = std::max<int64_t>(need, std::max<int64_t>(1024, 2 * L.pow_n));
+    std::vector<float> t((size_t)n + 1);
+    for (int64_t s = 0; s <= n; ++s) t[(size_t)s] = std::pow(beta2, static_cast<float>(s));
+    L.pow_tab.ensure(t.size());
+    SILI_HIP(hipMemcpyAsync(L.pow_tab.p, t.data(), t.size() * 4, hipMemcpyHostToDevice, st));
+    SILI_HIP(hipStreamSynchronize(st));
+    L.pow_n = n;
+    L.pow_beta2 = beta2;
+}
+
+// The shadow's permutation (shadow entry -> canonical entry): kept from the
+// first update on, by rebuilding the shadow once.
+void ensure_shadow_perm(Layer &L) {
+    if (L.keep_perm && (L.Wt_perm.p || L.W.nnz == 0)) return;
+    L.keep_perm = true;
+    rebuild_shadow(L);
+}
+
+uint64_t splitmix64_host(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// backward_dense with the optimizer update (sili/cpu_backend.cpp:496-529,
+// linear_disldo.hpp:466-2113) on a layer without block4 tiles.
+void backward_dense_train(Layer &L, const float *x, const float *dy, int64_t B, float *dx, const TrainParams &p,
+                          hipStream_t st) {
+    ProfCtx pc(L, "bwd");
+    if (B <= 0) throw_error(SILI_ERR_INVALID, "backward_dense: batch must be >= 1");
+    if (!dy || !dx) throw_error(SILI_ERR_INVALID, "backward_dense: NULL buffer");
+    if (B > TRAIN_MAX_BATCH)
+        throw_error(SILI_ERR_INVALID, "backward_dense with learning_rate != 0: batch must be <= 1024");
+    if (L.B4.ntiles > 0)
+        throw_error(SILI_ERR_INVALID, "backward_dense with learning_rate != 0: layers holding block4 tiles are "
+                                      "not supported on the GPU path yet");
+    const float *xT = nullptr;
+    if (!x) {
+        if (L.xT_cached_batch != B)
+            throw_error(SILI_ERR_INVALID, "backward_dense: x is NULL but no forward_dense input of this batch "
+                                          "(> 1) is stored; pass x");
+        xT = L.ws_xT.p;
+    } else {
+        xT = to_feature_major(L, L.ws_xT, x, B, L.n_in, nullptr, st);
+        L.xT_cached_batch = 0;
+    }
+    // accumulators (linear_disldo.hpp:515-520)
+    const float *gT = to_feature_major(L, L.ws_gT, dy, B, L.n_out, L.acc_grad.p, st);
+    launch_rowabs(xT, B, L.n_in, L.acc_in.p, st);
+    ensure_train_state(L, st);
+    ensure_pow_table(L, p.beta2, L.train_calls + 2, st);
+    ensure_shadow_perm(L);
+    if (L.output_scale_trainable) L.mterm.ensure((size_t)(L.W.nnz * 2 * L.rank));
+    const uint64_t seed = splitmix64_host(L.rng_seed ^ splitmix64_host(L.rng_calls + 1));
+    launch_train_rows(L, xT, gT, B, dx, p, seed, st);
+    launch_train_dead_rows(L, xT, gT, B, p, st);
+    if (L.output_scale_trainable && L.W.nnz > 0) launch_train_cols(L, p, st);
+    launch_shadow_val_refresh(L, st);
+    // copies holding value bytes are stale now: rebuilt on their next use
+    for (DScatter *sc : {&L.W, &L.Wt}) {
+        sc->stream1.valid = sc->streamK.valid = false;
+        sc->cblk.clear();
+        sc->cblk_cb = 0;
+    }
+    L.vs_ones = false;
+    if (L.output_scale_trainable) L.os_ones = false;
+    ++L.train_calls;
+    ++L.rng_calls;
 }
 
 void forward_sparse(Layer &L, const int32_t *ptrs, const int32_t *idx, const float *vals, int64_t nnz_x,
@@ -626,10 +721,72 @@ int sili_backward_dense(sili_layer *layer, const float *x, const float *dy, int6
                         float *gw_s, float *gw_b, float learning_rate, void *stream) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
-        if (learning_rate != 0.0f)
-            throw_error(SILI_ERR_INVALID, "backward_dense: only learning_rate == 0 is implemented on the GPU path");
         set_device(layer->L);
+        if (learning_rate != 0.0f) {
+            if (gw_s || gw_b)
+                throw_error(SILI_ERR_INVALID, "backward_dense: the sampled grad-W is for learning_rate == 0");
+            // the reference binding's defaults (sili/cpu_backend.cpp:496-528)
+            const TrainParams p{learning_rate, 0, 1, 0.999f, 1e-8f, 0.9f, 0.0f, 2.0f, 100.0f, 0.1f};
+            backward_dense_train(layer->L, x, dy, batch, dx, p, pick(layer->L, stream));
+            return;
+        }
         backward_dense(layer->L, x, dy, batch, dx, gw_s, gw_b, pick(layer->L, stream));
+    });
+}
+
+int sili_backward_dense_train(sili_layer *layer, const float *x, const float *dy, int64_t batch, float *dx,
+                              float learning_rate, int lr_per_row_nnz, int damp_by_importance, float beta2,
+                              float eps, void *stream) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        hipStream_t st = pick(layer->L, stream);
+        if (learning_rate == 0.0f) {
+            backward_dense(layer->L, x, dy, batch, dx, nullptr, nullptr, st);
+            return;
+        }
+        const TrainParams p{learning_rate, lr_per_row_nnz ? 1 : 0, damp_by_importance ? 1 : 0, beta2, eps,
+                            0.9f, 0.0f, 2.0f, 100.0f, 0.1f};
+        backward_dense_train(layer->L, x, dy, batch, dx, p, st);
+    });
+}
+
+int sili_set_stochastic_rounding(sili_layer *layer, int on) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        layer->L.stochastic_rounding = on != 0;
+    });
+}
+
+int sili_seed_stochastic_rounding(sili_layer *layer, uint64_t seed) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        layer->L.rng_seed = seed;
+        layer->L.rng_calls = 0;
+    });
+}
+
+int sili_get_scale_state(const sili_layer *layer, float *vs_importance, float *os_importance, float *vs_momentum,
+                         uint32_t *vs_step, uint32_t *os_step) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        const Layer &L = layer->L;
+        set_device(L);
+        const size_t nr = (size_t)(L.n_in * L.rank), nc = (size_t)(L.n_out * L.rank);
+        if (!L.train_state_ready) {
+            if (vs_importance) std::fill(vs_importance, vs_importance + nr, 0.0f);
+            if (vs_momentum) std::fill(vs_momentum, vs_momentum + nr, 0.0f);
+            if (vs_step) std::fill(vs_step, vs_step + nr, 0u);
+            if (os_importance) std::fill(os_importance, os_importance + nc, 0.0f);
+            if (os_step) std::fill(os_step, os_step + nc, 0u);
+            return;
+        }
+        if (vs_importance) SILI_HIP(hipMemcpyAsync(vs_importance, L.vs_imp.p, nr * 4, hipMemcpyDeviceToHost, L.stream));
+        if (vs_momentum) SILI_HIP(hipMemcpyAsync(vs_momentum, L.vs_mom.p, nr * 4, hipMemcpyDeviceToHost, L.stream));
+        if (vs_step) SILI_HIP(hipMemcpyAsync(vs_step, L.vs_step.p, nr * 4, hipMemcpyDeviceToHost, L.stream));
+        if (os_importance) SILI_HIP(hipMemcpyAsync(os_importance, L.os_imp.p, nc * 4, hipMemcpyDeviceToHost, L.stream));
+        if (os_step) SILI_HIP(hipMemcpyAsync(os_step, L.os_step.p, nc * 4, hipMemcpyDeviceToHost, L.stream));
+        SILI_HIP(hipStreamSynchronize(L.stream));
     });
 }
 

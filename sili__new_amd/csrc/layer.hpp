@@ -167,6 +167,21 @@ struct Layer {
     int64_t xT_cached_batch = 0;  // > 0: ws_xT holds the last forward_dense input, feature-major
     Scratch scratch;
     Profiler prof;
+    // backward with the optimizer update: the scales' optimizer state
+    // (delta_csr_types.hpp:1127-1215), allocated and zeroed on first use
+    DevBuf<float> vs_imp, vs_mom, os_imp;  // [n_in*rank], [n_in*rank], [n_out*rank]
+    DevBuf<uint32_t> vs_step, os_step;
+    bool train_state_ready = false;
+    DevBuf<uint32_t> Wt_perm;     // shadow entry -> canonical entry (kept once the layer trains)
+    bool keep_perm = false;
+    DevBuf<float> pow_tab;        // pow_tab[s] = powf(beta2, s), s <= pow_n
+    int64_t pow_n = 0;
+    float pow_beta2 = 0.0f;
+    DevBuf<float> mterm;          // per-synapse output-scale gradient terms
+    DevBuf<double> dead_S;
+    bool stochastic_rounding = true;
+    uint64_t rng_seed = 0x5EEDull, rng_calls = 0;
+    int64_t train_calls = 0;
     uint32_t seg_len = 512;     // max index bytes per decode work item (scattered)
     uint32_t seg_len_b4 = 128;  // max block-index bytes per decode work item (block4)
 };
@@ -223,6 +238,26 @@ bool stream_wanted(const DScatter &s, const ScaleView &sc, int64_t nb, int64_t i
 // use).
 void stream_gather(Layer &L, DScatter &s, const ScaleView &sc, const float *in, int64_t B, float *out,
                    int64_t out_ld, hipStream_t st);
+
+// ---- backward with the optimizer update (train.hip) -------------------------------
+// Largest batch of one update call (the per-row dx accumulator lives in LDS).
+constexpr int64_t TRAIN_MAX_BATCH = 1024;
+struct TrainParams {
+    float lr;
+    int lr_per_row_nnz, damp_by_importance;
+    float beta2, eps, beta1, min_decay_frac, max_abs_delta, max_ci, zero_escape_eps;
+};
+// Per-synapse update of the canonical store, dx, and the value scales of its
+// rows (needs L's train state and pow table).
+void launch_train_rows(Layer &L, const float *xT, const float *gT, int64_t B, float *dx, const TrainParams &p,
+                       uint64_t seed, hipStream_t st);
+// value_scale steps of the rows without synapses.
+void launch_train_dead_rows(Layer &L, const float *xT, const float *gT, int64_t B, const TrainParams &p,
+                            hipStream_t st);
+// output_scale steps (needs L.Wt_perm and L.mterm).
+void launch_train_cols(Layer &L, const TrainParams &p, hipStream_t st);
+// Shadow value bytes from the canonical ones (needs L.Wt_perm).
+void launch_shadow_val_refresh(Layer &L, hipStream_t st);
 
 // ---- seeded synthetic layers (gen.hip) ----------------------------------------
 // Rebuilds the scattered store (and its shadow) from the seeded generator and

@@ -57,6 +57,12 @@ struct DBuf {
     }
 };
 
+// seed_fp4_stochastic_rng: the process-wide seed every layer takes up
+// before its next update (fp4quant.hpp:186-188 seeds the calling thread's
+// generator).
+uint64_t g_seed = 0;
+uint64_t g_seed_epoch = 0;
+
 class Layer {
    public:
     Layer(int64_t n_inputs, int64_t n_outputs, int64_t max_weights, int num_cpus, int device)
@@ -76,6 +82,14 @@ class Layer {
     }
     Layer(const Layer &) = delete;
     Layer &operator=(const Layer &) = delete;
+
+    // before an update: take up a seed_fp4_stochastic_rng issued since the last one
+    void apply_seed() {
+        if (seed_epoch_ != g_seed_epoch) {
+            ck(sili_seed_stochastic_rounding(L_, g_seed));
+            seed_epoch_ = g_seed_epoch;
+        }
+    }
 
     int64_t n_inputs() const { return n_in_; }
     int64_t n_outputs() const { return n_out_; }
@@ -233,7 +247,6 @@ class Layer {
 
     py::array_t<float> backward_dense(carr<float> dy, float learning_rate, bool lr_per_row_nnz,
                                       bool damp_by_importance, float beta2, float eps) {
-        (void)lr_per_row_nnz; (void)damp_by_importance; (void)beta2; (void)eps;
         flush();
         if (last_batch_ == 0) throw std::runtime_error("backward_dense called before forward_dense");
         const int64_t B = last_batch_;
@@ -241,8 +254,50 @@ class Layer {
         float *ddy = (float *)g_.get((size_t)(B * n_out_) * 4);
         ck(sili_memcpy_h2d(L_, ddy, dy.data(), (size_t)(B * n_out_) * 4));
         float *ddx = (float *)dx_.get((size_t)(B * n_in_) * 4);
-        ck(sili_backward_dense(L_, (const float *)last_x_.p, ddy, B, ddx, nullptr, nullptr, learning_rate, nullptr));
+        if (learning_rate == 0.0f) {
+            ck(sili_backward_dense(L_, (const float *)last_x_.p, ddy, B, ddx, nullptr, nullptr, 0.0f, nullptr));
+        } else {
+            apply_seed();
+            ck(sili_backward_dense_train(L_, (const float *)last_x_.p, ddy, B, ddx, learning_rate,
+                                         lr_per_row_nnz ? 1 : 0, damp_by_importance ? 1 : 0, beta2, eps, nullptr));
+            // the update moved the scales: refresh the host mirrors
+            ck(sili_get_value_scale(L_, vs_.data()));
+            ck(sili_get_output_scale(L_, os_.data()));
+        }
         return fetch(ddx, B, n_in_);
+    }
+
+    // The scales' optimizer state (delta_csr_types.hpp:1127-1215).
+    float get_value_scale_importance(int64_t row) {
+        check_index(row, n_in_, "row");
+        std::vector<float> v((size_t)(n_in_ * rank_));
+        ck(sili_get_scale_state(L_, v.data(), nullptr, nullptr, nullptr, nullptr));
+        return v[(size_t)(row * rank_)];
+    }
+    float get_output_scale_importance(int64_t col) {
+        check_index(col, n_out_, "col");
+        std::vector<float> v((size_t)(n_out_ * rank_));
+        ck(sili_get_scale_state(L_, nullptr, v.data(), nullptr, nullptr, nullptr));
+        return v[(size_t)(col * rank_)];
+    }
+    // all of it, [n * rank] arrays
+    py::dict get_scale_state() {
+        const size_t nr = (size_t)(n_in_ * rank_), nc = (size_t)(n_out_ * rank_);
+        py::array_t<float> vi((py::ssize_t)nr), vm((py::ssize_t)nr), oi((py::ssize_t)nc);
+        py::array_t<uint32_t> vst((py::ssize_t)nr), ost((py::ssize_t)nc);
+        ck(sili_get_scale_state(L_, vi.mutable_data(), oi.mutable_data(), vm.mutable_data(), vst.mutable_data(),
+                                ost.mutable_data()));
+        py::dict d;
+        d["vs_importance"] = vi;
+        d["vs_momentum"] = vm;
+        d["vs_step"] = vst;
+        d["os_importance"] = oi;
+        d["os_step"] = ost;
+        return d;
+    }
+    void seed_stochastic_rounding(uint64_t seed) {
+        ck(sili_seed_stochastic_rounding(L_, seed));
+        seed_epoch_ = g_seed_epoch;
     }
 
     // nnz-sampled grad-W for (x, dy): (per scattered synapse, per block4 slot)
@@ -421,9 +476,12 @@ class Layer {
     }
     void synchronize() { ck(sili_synchronize(L_)); }
     uintptr_t handle() const { return reinterpret_cast<uintptr_t>(L_); }
+    // rounding of the update's re-quantization (stochastic by default)
+    void set_stochastic_rounding(bool on) { ck(sili_set_stochastic_rounding(L_, on ? 1 : 0)); }
 
    private:
     sili_layer *L_ = nullptr;
+    uint64_t seed_epoch_ = 0;
     int64_t n_in_ = 0, n_out_ = 0;
     int num_cpus_ = 4;
     int rank_ = 1;
@@ -506,6 +564,16 @@ py::array_t<uint8_t> fp4_quantize_array(carr<float> v) {
     return out;
 }
 
+// SparseLinearLayerDeterministic (sili/cpu_backend.cpp:1007): the same layer
+// with round-to-nearest re-quantization in the update.
+class LayerDeterministic : public Layer {
+   public:
+    LayerDeterministic(int64_t n_inputs, int64_t n_outputs, int64_t max_weights, int num_cpus, int device)
+        : Layer(n_inputs, n_outputs, max_weights, num_cpus, device) {
+        set_stochastic_rounding(false);
+    }
+};
+
 }  // namespace
 
 PYBIND11_MODULE(_sili_hip, m) {
@@ -538,6 +606,11 @@ PYBIND11_MODULE(_sili_hip, m) {
         .def("get_importance_scale", &Layer::get_importance_scale)
         .def("get_output_importance_scale", &Layer::get_output_importance_scale)
         .def("get_scale", &Layer::get_scale)
+        .def("get_value_scale_importance", &Layer::get_value_scale_importance, py::arg("row"))
+        .def("get_output_scale_importance", &Layer::get_output_scale_importance, py::arg("col"))
+        .def("get_scale_state", &Layer::get_scale_state)
+        .def("set_stochastic_rounding", &Layer::set_stochastic_rounding, py::arg("on"))
+        .def("seed_stochastic_rounding", &Layer::seed_stochastic_rounding, py::arg("seed"))
         .def("forward_dense", &Layer::forward_dense, py::arg("x"))
         .def("backward_dense", &Layer::backward_dense, py::arg("dy"), py::arg("learning_rate"),
              py::arg("lr_per_row_nnz") = false, py::arg("damp_by_importance") = true, py::arg("beta2") = 0.999f,
@@ -580,5 +653,15 @@ PYBIND11_MODULE(_sili_hip, m) {
         .def_property_readonly("ptrs", &Layer::ptrs)
         .def_property_readonly("neuron_input_accum", &Layer::neuron_input_accum)
         .def_property_readonly("neuron_grad_accum", &Layer::neuron_grad_accum);
+    py::class_<LayerDeterministic, Layer>(m, "SparseLinearLayerDeterministic")
+        .def(py::init<int64_t, int64_t, int64_t, int, int>(), py::arg("n_inputs"), py::arg("n_outputs"),
+             py::arg("max_weights"), py::arg("num_cpus") = 4, py::arg("device") = 0);
     m.def("fp4_quantize_array", &fp4_quantize_array);
+    m.def(
+        "seed_fp4_stochastic_rng",
+        [](uint64_t seed) {
+            g_seed = seed;
+            ++g_seed_epoch;
+        },
+        py::arg("seed"));
 }

@@ -1,0 +1,430 @@
+// train.hip -- backward with the optimizer update (learning_rate != 0) on the
+// scattered store: per-synapse RMSprop steps on the stored FP4 weight code and
+// its importance, re-quantized in place; the scales' own RMSprop / Adam steps.
+//
+// Semantics: disldo_backward (linear_disldo.hpp:466-2113) with
+// RMSpropScalePolicy, no deferred scale write, BoundedRMSpropSynapsePolicy
+// and the constants of sili/cpu_backend.cpp:496-528; rounding deterministic
+// (SparseLinearLayerDeterministic, sili/cpu_backend.cpp:1007) or stochastic
+// with a counter-based generator (the reference's thread-local xorshift
+// stream, fp4quant.hpp:180-265, cannot be reproduced across thread counts).
+// Every fp32 expression is evaluated as written, no contraction, in the
+// reference's order: per synapse the batch steps run in b order; a row's
+// gradient sums (fp64) add the synapses in storage order -- at batch 1 this is
+// the reference's own summation order.
+#include "layer.hpp"
+#include "wave.hpp"
+
+#pragma clang fp contract(off)
+
+namespace sili {
+
+namespace {
+
+constexpr unsigned TPB = 256;
+constexpr uint32_t WAVES_T = 4;
+
+__device__ __forceinline__ bool finite_f(float v) { return __builtin_isfinite(v); }
+// std::max / std::min as the reference calls them (a NaN first operand is
+// returned as is).
+__device__ __forceinline__ float std_max(float a, float b) { return (a < b) ? b : a; }
+__device__ __forceinline__ float std_min(float a, float b) { return (b < a) ? b : a; }
+
+// BoundedRMSpropSynapsePolicy::update_ci (delta_csr_types.hpp:707-712).
+__device__ __forceinline__ float bounded_update_ci(float ci, float g, float contrib, float beta2, float mdf,
+                                                   float max_ci) {
+    const float ema = beta2 * ci + (1.0f - beta2) * (g * g + contrib * contrib);
+    const float floor_ = mdf * ci;
+    return std_min(std_max(ema, floor_), max_ci);
+}
+// BoundedRMSpropSynapsePolicy::update_cw (delta_csr_types.hpp:749-758).
+__device__ __forceinline__ float bounded_update_cw(float g, float ci, float S, float eff_lr, float eps, bool damp,
+                                                   float max_abs_delta) {
+    float raw = damp ? (-g * S) / (__builtin_sqrtf(ci) + eps) : (-g * S);
+    if (raw > max_abs_delta) raw = max_abs_delta;
+    if (raw < -max_abs_delta) raw = -max_abs_delta;
+    return eff_lr * raw;
+}
+// RMSpropScalePolicy::update (delta_csr_types.hpp:413-434); pow_tab[s] =
+// powf(beta2, s), computed on the host with the reference's own function.
+__device__ __forceinline__ void rmsprop_scale_update(float &scale, float &state, float g_agg, float eff_lr,
+                                                     float beta2, float eps, float contrib_agg, uint32_t &step,
+                                                     const float *pow_tab) {
+    if (!finite_f(g_agg) || !finite_f(contrib_agg)) return;
+    const float new_state = beta2 * state + (1.0f - beta2) * (g_agg * g_agg + contrib_agg * contrib_agg);
+    if (!finite_f(new_state)) return;
+    float state_hat = new_state;
+    ++step;
+    const float bias_correction = 1.0f - pow_tab[step];
+    if (bias_correction > 0.0f) state_hat = new_state / bias_correction;
+    if (!finite_f(state_hat)) return;
+    const float new_scale = scale - eff_lr * g_agg / (__builtin_sqrtf(state_hat) + eps);
+    if (!finite_f(new_scale)) return;
+    state = new_state;
+    scale = new_scale;
+}
+
+// ---- stochastic rounding ------------------------------------------------------
+// One 64-bit draw per quantized value: splitmix64 of (call seed, synapse,
+// which), sliced the way fp4_quantize_stochastic slices its xorshift64*
+// draw (fp4quant.hpp:198-265): top 24 bits -> uniform [0,1), low 22 bits ->
+// dither.
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+// fp4quant.hpp:238-265, with the draw supplied.
+__device__ __forceinline__ uint32_t fp4_encode_stochastic(float v, uint64_t r) {
+    constexpr uint32_t HALF_BITS = 0x3F000000u, ONE_BITS = 0x3F800000u, SIX_BITS = 0x40C00000u;
+    const uint32_t bits = __builtin_bit_cast(uint32_t, v);
+    const uint32_t sign = bits & 0x80000000u, abits = bits & 0x7FFFFFFFu;
+    if (abits > 0x7F800000u) return 0u;
+    const float u01 = (float)((double)(r >> 40) * (1.0 / 16777216.0));
+    uint32_t mag;
+    if (abits >= SIX_BITS) {
+        mag = 7u;
+    } else if (abits < HALF_BITS) {
+        const float av = __builtin_bit_cast(float, abits);
+        mag = (u01 < av * 2.0f) ? 1u : 0u;
+    } else if (abits < ONE_BITS) {
+        const float av = __builtin_bit_cast(float, abits);
+        mag = (u01 < av * 2.0f - 1.0f) ? 2u : 1u;
+    } else {
+        uint32_t rounded = abits + (uint32_t)(r & 0x3FFFFFull);
+        if (rounded > SIX_BITS) rounded = SIX_BITS;
+        mag = ((((rounded >> 23) & 0xFFu) - 126u) << 1) | ((rounded >> 22) & 1u);
+    }
+    if (mag == 0u) return 0u;
+    return (sign ? 8u : 0u) | mag;
+}
+
+struct TrainArgs {
+    const uint32_t *byte_start, *elem_start;  // canonical store
+    const uint8_t *idx;
+    uint8_t *val;
+    int64_t n_in, n_out;
+    int64_t B;
+    const float *xT, *gT;      // feature-major [n_in][B], [n_out][B]
+    float *dx;                 // [B][n_in], overwritten
+    float *vs, *vs_imp;        // [n_in*rank]
+    uint32_t *vs_step;
+    const float *os;           // [n_out*rank]
+    const float *is, *ois;     // importance scales (NULL: ones)
+    const float *pow_tab;
+    float *mterm;              // [nnz * 2 * rank] column-gradient terms, or NULL
+    float lr, beta2, eps, min_decay_frac, max_abs_delta, max_ci, zero_escape_eps;
+    int lr_per_row_nnz, damp, stochastic;
+    uint64_t seed;             // this call's stochastic-rounding seed
+};
+
+// One wave per canonical row (linear_disldo.hpp:624-880).  The row's entries
+// are decoded 64 index bytes at a time; each lane owns one entry and runs its
+// batch steps; the row's fp64 gradient sums are added by lane 0 in entry
+// order; dx[b][row] is the sum over the row's entries of the updated weight
+// times dy, reduced across the lanes per b.
+template <int RANK>
+__global__ __launch_bounds__(256) void k_train_rows(TrainArgs a) {
+    __shared__ double s_part[WAVES_T][64][2 * RANK];
+    __shared__ float s_dx[WAVES_T][TRAIN_MAX_BATCH];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t r = (int64_t)blockIdx.x * WAVES_T + wave;
+    if (r >= a.n_in) return;
+    const uint32_t e0 = a.elem_start[r], e1 = a.elem_start[r + 1];
+    const uint32_t nnz = e1 - e0;
+    const int64_t B = a.B;
+    if (nnz == 0) {
+        for (int64_t b = lane; b < B; b += 64) a.dx[b * a.n_in + r] = 0.0f;
+        return;
+    }
+    float *rdx = s_dx[wave];
+    for (int64_t b = lane; b < B; b += 64) rdx[b] = 0.0f;
+    wave_lds_sync();
+    const float eff_lr = a.lr_per_row_nnz ? a.lr / (float)nnz : a.lr;
+    const float scale_eff_lr = a.lr / (float)nnz;
+    const float imp_scale = a.is ? a.is[r] : 1.0f;
+    float vs_k[RANK];
+#pragma unroll
+    for (int k = 0; k < RANK; ++k) vs_k[k] = a.vs[r * RANK + k];
+    double sg[RANK], sgc[RANK];
+#pragma unroll
+    for (int k = 0; k < RANK; ++k) sg[k] = sgc[k] = 0.0;
+    const float *xrow = a.xT + r * B;
+    uint32_t pos = a.byte_start[r], carry = 0, ebase = e0;
+    const uint32_t end = a.byte_start[r + 1];
+    while (pos < end) {
+        const Chunk ch = decode_chunk(a.idx, pos, end, carry);
+        if (ch.T == 0ull) break;
+        const bool has = ch.term;
+        const uint32_t col = has ? ch.col : 0u;
+        const uint32_t vb = ebase + ch.rank;
+        const uint32_t byte = has ? (uint32_t)a.val[vb] : 0u;
+        const float cw_orig = fp4_decode(byte >> 4);
+        const float ci_orig = fp4_decode(byte & 0xFu);
+        const float out_imp_scale = (a.ois && has) ? a.ois[col] : 1.0f;
+        const float combined_imp_scale = imp_scale * out_imp_scale;
+        float ci = ci_orig * combined_imp_scale;
+        float os_k[RANK];
+        float S = 0.0f;
+#pragma unroll
+        for (int k = 0; k < RANK; ++k) {
+            os_k[k] = has ? a.os[(int64_t)col * RANK + k] : 0.0f;
+            S = S + vs_k[k] * os_k[k];
+        }
+        float quant = cw_orig;
+        float cw = quant * S;
+        double psg[RANK], psgc[RANK];
+        float pm[RANK], pmc[RANK];
+#pragma unroll
+        for (int k = 0; k < RANK; ++k) {
+            psg[k] = psgc[k] = 0.0;
+            pm[k] = pmc[k] = 0.0f;
+        }
+        const float *grow = a.gT + (int64_t)col * B;
+        for (int64_t b = 0; b < B; ++b) {
+            const float iv = xrow[b];
+            const float dyv = has ? grow[b] : 0.0f;
+            const float g = dyv * iv;
+            if (has) {
+                const float contrib = iv * cw_orig;
+                ci = bounded_update_ci(ci, g, contrib, a.beta2, a.min_decay_frac, a.max_ci);
+                quant = quant + bounded_update_cw(g, ci, S, eff_lr, a.eps, a.damp != 0, a.max_abs_delta);
+                cw = quant * S;
+                const float qf = (quant == 0.0f) ? a.zero_escape_eps : quant;
+#pragma unroll
+                for (int k = 0; k < RANK; ++k) {
+                    psg[k] = psg[k] + ((double)qf * (double)os_k[k]) * (double)g;
+                    psgc[k] = psgc[k] + ((double)qf * (double)os_k[k]) * (double)contrib;
+                    pm[k] = pm[k] + (qf * vs_k[k]) * g;
+                    pmc[k] = pmc[k] + (qf * vs_k[k]) * contrib;
+                }
+            }
+            // dx[b][row]: this chunk's share, added to the row's running sum
+            const float t = has ? cw * dyv : 0.0f;
+            const float tot = wave_sum(t);
+            if (lane == 0u) rdx[b] = rdx[b] + tot;
+        }
+        if (has) {
+            uint32_t wq, iq;
+            const float imp_true = ci / combined_imp_scale;
+            if (a.stochastic) {
+                const uint64_t base = a.seed + 2ull * (uint64_t)vb;
+                wq = fp4_encode_stochastic(quant, splitmix64(base));
+                iq = fp4_encode_stochastic(imp_true, splitmix64(base + 1ull));
+            } else {
+                wq = fp4_encode(quant);
+                iq = fp4_encode(imp_true);
+            }
+            a.val[vb] = (uint8_t)((wq << 4) | iq);
+            if (a.mterm) {
+#pragma unroll
+                for (int k = 0; k < RANK; ++k) {
+                    a.mterm[(int64_t)vb * 2 * RANK + k] = pm[k];
+                    a.mterm[(int64_t)vb * 2 * RANK + RANK + k] = pmc[k];
+                }
+            }
+        }
+        // the row's gradient sums, entry by entry in storage order
+#pragma unroll
+        for (int k = 0; k < RANK; ++k) {
+            s_part[wave][lane][k] = has ? psg[k] : 0.0;
+            s_part[wave][lane][RANK + k] = has ? psgc[k] : 0.0;
+        }
+        wave_lds_sync();
+        if (lane == 0u) {
+            uint64_t T = ch.T;
+            while (T) {
+                const uint32_t l = (uint32_t)__builtin_ctzll(T);
+                T &= T - 1ull;
+#pragma unroll
+                for (int k = 0; k < RANK; ++k) {
+                    sg[k] = sg[k] + s_part[wave][l][k];
+                    sgc[k] = sgc[k] + s_part[wave][l][RANK + k];
+                }
+            }
+        }
+        wave_lds_sync();
+        carry = chunk_advance(ch, pos, ebase);
+    }
+    wave_lds_sync();
+    for (int64_t b = lane; b < B; b += 64) a.dx[b * a.n_in + r] = rdx[b];
+    if (lane == 0u) {
+#pragma unroll
+        for (int k = 0; k < RANK; ++k) {
+            const int64_t i = r * RANK + k;
+            float vsv = a.vs[i], st = a.vs_imp[i];
+            uint32_t step = a.vs_step[i];
+            rmsprop_scale_update(vsv, st, (float)sg[k], scale_eff_lr, a.beta2, a.eps, (float)sgc[k], step, a.pow_tab);
+            a.vs[i] = vsv;
+            a.vs_imp[i] = st;
+            a.vs_step[i] = step;
+        }
+    }
+}
+
+// dead_S[b*rank + k] = sum_col os_k(col) * dy[b][col] in fp64
+// (linear_disldo.hpp:1995-2007): one block per (b, k).
+__global__ __launch_bounds__(256) void k_dead_S(const float *__restrict__ os, const float *__restrict__ gT,
+                                                int64_t n_out, int64_t B, int rank, double *__restrict__ dead_S) {
+    __shared__ double part[256];
+    const int64_t b = blockIdx.x / rank;
+    const int k = (int)(blockIdx.x % rank);
+    double s = 0.0;
+    for (int64_t c = threadIdx.x; c < n_out; c += 256)
+        s = s + (double)os[c * rank + k] * (double)gT[c * B + b];
+    part[threadIdx.x] = s;
+    __syncthreads();
+    for (int h = 128; h > 0; h >>= 1) {
+        if ((int)threadIdx.x < h) part[threadIdx.x] = part[threadIdx.x] + part[threadIdx.x + h];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) dead_S[blockIdx.x] = part[0];
+}
+
+// Rows with no synapse: a two-moment step on value_scale
+// (linear_disldo.hpp:2008-2040).
+__global__ __launch_bounds__(256) void k_dead_rows(const uint32_t *__restrict__ elem_start, int64_t n_in,
+                                                   int64_t n_out, int64_t B, int rank,
+                                                   const float *__restrict__ xT, const double *__restrict__ dead_S,
+                                                   float *vs, float *vs_mom, float *vs_imp, float lr, float beta1,
+                                                   float beta2, float eps) {
+    const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (r >= n_in || elem_start[r + 1] != elem_start[r]) return;
+    for (int k = 0; k < rank; ++k) {
+        double sum = 0.0;
+        for (int64_t b = 0; b < B; ++b) {
+            const float iv = xT[r * B + b];
+            if (iv == 0.0f) continue;
+            sum = sum + (double)iv * dead_S[b * rank + k];
+        }
+        if (sum == 0.0) continue;
+        const float g = (float)sum;
+        if (!finite_f(g)) continue;
+        const int64_t i = r * rank + k;
+        const float m = vs_mom[i], v = vs_imp[i];
+        const float new_m = beta1 * m + (1.0f - beta1) * g;
+        const float new_v = beta2 * v + (1.0f - beta2) * g * g;
+        if (!finite_f(new_m) || !finite_f(new_v)) continue;
+        const float dead_lr = lr / (float)n_out;
+        const float new_vs = vs[i] - dead_lr * new_m / (__builtin_sqrtf(new_v) + eps);
+        if (!finite_f(new_vs)) continue;
+        vs_mom[i] = new_m;
+        vs_imp[i] = new_v;
+        vs[i] = new_vs;
+    }
+}
+
+// output_scale's step (linear_disldo.hpp:2050-2080): one thread per column;
+// its synapses' column-gradient terms are summed in shadow order (the
+// column's synapses by ascending row, the reference's single-thread order).
+__global__ __launch_bounds__(256) void k_train_cols(const uint32_t *__restrict__ t_elem_start,
+                                                    const uint32_t *__restrict__ perm, int64_t n_out, int rank,
+                                                    const float *__restrict__ mterm, float *os, float *os_imp,
+                                                    uint32_t *os_step, float lr, float beta2, float eps,
+                                                    const float *pow_tab) {
+    const int64_t c = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (c >= n_out) return;
+    const uint32_t s0 = t_elem_start[c], s1 = t_elem_start[c + 1];
+    const uint32_t deg = s1 - s0;
+    if (deg == 0) return;
+    const float col_eff_lr = lr / (float)deg;
+    for (int k = 0; k < rank; ++k) {
+        float m = 0.0f, mc = 0.0f;
+        for (uint32_t s = s0; s < s1; ++s) {
+            const int64_t e = perm[s];
+            m = m + mterm[e * 2 * rank + k];
+            mc = mc + mterm[e * 2 * rank + rank + k];
+        }
+        const int64_t i = c * rank + k;
+        float osv = os[i], st = os_imp[i];
+        uint32_t step = os_step[i];
+        rmsprop_scale_update(osv, st, (float)(0.0 + (double)m), col_eff_lr, beta2, eps, (float)(0.0 + (double)mc),
+                             step, pow_tab);
+        os[i] = osv;
+        os_imp[i] = st;
+        os_step[i] = step;
+    }
+}
+
+__global__ void k_perm_bytes(const uint8_t *__restrict__ src, const uint32_t *__restrict__ perm, int64_t n,
+                             uint8_t *__restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n) dst[i] = src[perm[i]];
+}
+
+inline unsigned nblk(int64_t n) { return (unsigned)((n + TPB - 1) / TPB); }
+
+}  // namespace
+
+void launch_train_rows(Layer &L, const float *xT, const float *gT, int64_t B, float *dx, const TrainParams &p,
+                       uint64_t seed, hipStream_t st) {
+    TrainArgs a{};
+    a.byte_start = L.W.byte_start.p;
+    a.elem_start = L.W.elem_start.p;
+    a.idx = L.W.idx.p;
+    a.val = L.W.val.p;
+    a.n_in = L.n_in;
+    a.n_out = L.n_out;
+    a.B = B;
+    a.xT = xT;
+    a.gT = gT;
+    a.dx = dx;
+    a.vs = L.vs.p;
+    a.vs_imp = L.vs_imp.p;
+    a.vs_step = L.vs_step.p;
+    a.os = L.os.p;
+    a.is = L.is.p;
+    a.ois = L.ois.p;
+    a.pow_tab = L.pow_tab.p;
+    a.mterm = L.output_scale_trainable ? L.mterm.p : nullptr;
+    a.lr = p.lr;
+    a.beta2 = p.beta2;
+    a.eps = p.eps;
+    a.min_decay_frac = p.min_decay_frac;
+    a.max_abs_delta = p.max_abs_delta;
+    a.max_ci = p.max_ci;
+    a.zero_escape_eps = p.zero_escape_eps;
+    a.lr_per_row_nnz = p.lr_per_row_nnz;
+    a.damp = p.damp_by_importance;
+    a.stochastic = L.stochastic_rounding ? 1 : 0;
+    a.seed = seed;
+    const dim3 grid((unsigned)((L.n_in + WAVES_T - 1) / WAVES_T)), block(256);
+    ProfScope ps("train_rows", st);
+    switch (L.rank) {
+        case 1: launch(k_train_rows<1>, grid, block, 0, st, a); break;
+        case 2: launch(k_train_rows<2>, grid, block, 0, st, a); break;
+        case 3: launch(k_train_rows<3>, grid, block, 0, st, a); break;
+        default: launch(k_train_rows<4>, grid, block, 0, st, a); break;
+    }
+    SILI_HIP(hipGetLastError());
+}
+
+void launch_train_dead_rows(Layer &L, const float *xT, const float *gT, int64_t B, const TrainParams &p,
+                            hipStream_t st) {
+    L.dead_S.ensure((size_t)(B * L.rank));
+    ProfScope ps("train_dead", st);
+    launch(k_dead_S, dim3((unsigned)(B * L.rank)), dim3(256), 0, st, (const float *)L.os.p, gT, L.n_out, B, L.rank,
+           L.dead_S.p);
+    launch(k_dead_rows, dim3(nblk(L.n_in)), dim3(TPB), 0, st, (const uint32_t *)L.W.elem_start.p, L.n_in, L.n_out, B,
+           L.rank, xT, (const double *)L.dead_S.p, L.vs.p, L.vs_mom.p, L.vs_imp.p, p.lr, p.beta1, p.beta2, p.eps);
+    SILI_HIP(hipGetLastError());
+}
+
+void launch_train_cols(Layer &L, const TrainParams &p, hipStream_t st) {
+    ProfScope ps("train_cols", st);
+    launch(k_train_cols, dim3(nblk(L.n_out)), dim3(TPB), 0, st, (const uint32_t *)L.Wt.elem_start.p,
+           (const uint32_t *)L.Wt_perm.p, L.n_out, L.rank, (const float *)L.mterm.p, L.os.p, L.os_imp.p, L.os_step.p,
+           p.lr, p.beta2, p.eps, (const float *)L.pow_tab.p);
+    SILI_HIP(hipGetLastError());
+}
+
+void launch_shadow_val_refresh(Layer &L, hipStream_t st) {
+    if (L.Wt.nnz == 0) return;
+    ProfScope ps("train_shadow", st);
+    launch(k_perm_bytes, dim3(nblk(L.Wt.nnz)), dim3(TPB), 0, st, (const uint8_t *)L.W.val.p,
+           (const uint32_t *)L.Wt_perm.p, L.Wt.nnz, L.Wt.val.p);
+    SILI_HIP(hipGetLastError());
+}
+
+}  // namespace sili

@@ -33,6 +33,12 @@ class Api:
         L.sili_get_accumulators.argtypes = [vp, vp, vp]
         L.sili_zero_accum.argtypes = [vp]
         L.sili_profile_enable.argtypes = [vp, C.c_int]
+        L.sili_load_weights.argtypes = [vp, vp, vp, vp, vp, C.c_int64]
+        L.sili_backward_dense_train.argtypes = [vp, vp, vp, C.c_int64, vp, C.c_float, C.c_int, C.c_int, C.c_float,
+                                                C.c_float, vp]
+        L.sili_set_stochastic_rounding.argtypes = [vp, C.c_int]
+        L.sili_get_scale_state.argtypes = [vp, vp, vp, vp, vp, vp]
+        L.sili_export_scattered.argtypes = [vp, vp, vp, vp, vp]
         self.L = L
 
     def ck(self, rc):
@@ -90,12 +96,65 @@ def test_capi_forward_backward_null_x(api):
         # batch mismatch with a NULL x is an error, not a silent reuse
         rc = api.L.sili_backward_dense(h, None, dev["g"], 32, dev["dx"], None, None, 0.0, st)
         assert rc == 1 and b"stored" in api.L.sili_last_error()
-        # learning_rate != 0 is rejected (optimizer update not on the GPU path)
-        rc = api.L.sili_backward_dense(h, dev["x"], dev["g"], wl.batch, dev["dx"], None, None, 0.01, st)
-        assert rc == 1
+        # learning_rate != 0 runs the optimizer update, which has no sampled grad-W output
+        rc = api.L.sili_backward_dense(h, dev["x"], dev["g"], wl.batch, dev["dx"], dev["gw"], None, 0.01, st)
+        assert rc == 1 and b"learning_rate == 0" in api.L.sili_last_error()
         for p in dev.values():
             api.ck(api.L.sili_device_free(h, p))
     finally:
+        api.L.sili_destroy(h)
+
+
+def test_capi_backward_dense_train(api):
+    """The optimizer update through the C ABI (device buffers, the layer's
+    stream, deterministic rounding) against the IEEE restatement: value bytes
+    and scale state exact at batch 1, dx within the bar."""
+    from train_util import dx_bound, host_layer as train_host, make_train_case
+    c = make_train_case(120, 90, 0.1, 77, imp_scales=True)
+    H = train_host(c)
+    h = C.c_void_p()
+    api.ck(api.L.sili_create(c["n_in"], c["n_out"], len(c["cols"]), 0, C.byref(h)))
+    dev = {}
+    try:
+        ptrs, cols, w, imp = (np.ascontiguousarray(c[k]) for k in ("ptrs", "cols", "w", "imp"))
+        api.ck(api.L.sili_load_weights(h, _ptr(ptrs), _ptr(cols), _ptr(w), _ptr(imp), len(cols)))
+        vs = np.ascontiguousarray(c["vs"])
+        api.ck(api.L.sili_set_value_scale(h, _ptr(vs)))
+        for name, arr in (("importance", c["is"]), ("output_importance", c["ois"])):
+            f = getattr(api.L, f"sili_set_{name}_scale")
+            f.argtypes = [C.c_void_p, C.c_void_p]
+            api.ck(f(h, _ptr(np.ascontiguousarray(arr))))
+        api.ck(api.L.sili_set_stochastic_rounding(h, 0))
+        for k, n in (("x", c["n_in"]), ("g", c["n_out"]), ("dx", c["n_in"])):
+            dev[k] = C.c_void_p()
+            api.ck(api.L.sili_device_alloc(h, n * 4, C.byref(dev[k])))
+        st = api.L.sili_stream(h)
+        nnz = len(cols)
+        for step in range(3):
+            x = c["rng"].normal(size=(1, c["n_in"])).astype(np.float32)
+            dy = c["rng"].normal(size=(1, c["n_out"])).astype(np.float32)
+            api.ck(api.L.sili_memcpy_h2d(h, dev["x"], _ptr(x), x.nbytes))
+            api.ck(api.L.sili_memcpy_h2d(h, dev["g"], _ptr(dy), dy.nbytes))
+            bound = dx_bound(H, dy, 0.05)
+            api.ck(api.L.sili_backward_dense_train(h, dev["x"], dev["g"], 1, dev["dx"], 0.05, 0, 1, 0.999, 1e-8, st))
+            api.ck(api.L.sili_synchronize(h))
+            dxh, _, _ = H.backward_train(x, dy, 0.05)
+            dx = np.zeros_like(x)
+            api.ck(api.L.sili_memcpy_d2h(h, _ptr(dx), dev["dx"], dx.nbytes))
+            val = np.zeros(nnz, np.uint8)
+            api.ck(api.L.sili_export_scattered(h, None, None, None, _ptr(val)))
+            assert np.array_equal(val, H.val[:nnz]), f"value bytes, step {step}"
+            assert_close_terms(dx, dxh, bound, f"dx, step {step}")
+            vsg = np.zeros_like(vs)
+            api.ck(api.L.sili_get_value_scale(h, _ptr(vsg)))
+            vi, vm = np.zeros_like(vs), np.zeros_like(vs)
+            vstep = np.zeros(len(vs), np.uint32)
+            api.ck(api.L.sili_get_scale_state(h, _ptr(vi), None, _ptr(vm), _ptr(vstep), None))
+            assert np.array_equal(vsg, H.value_scale) and np.array_equal(vi, H.vs_importance)
+            assert np.array_equal(vstep, H.vs_step) and np.array_equal(vm, H.vs_momentum)
+    finally:
+        for p in dev.values():
+            api.L.sili_device_free(h, p)
         api.L.sili_destroy(h)
 
 

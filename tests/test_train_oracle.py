@@ -1,0 +1,82 @@
+"""CPU: the oracle's backward with the optimizer update against the
+reference's own compiled disldo_backward, deterministic variant
+(oracle/_ref, this container), over several calls of each seeded case.
+
+The reference's build (its setup.py flags: -O3 -ffast-math on an FMA target)
+contracts a*b+c into FMAs.  The restatement is compiled twice:
+  - contracted, as the reference is: codes, dx, scales and their state match
+    the reference exactly, except one last-place difference in the second
+    moment of rows without synapses (the reference's compiler also
+    re-associates (1 - beta2) * g * g there), held to 1e-6 relative;
+  - IEEE, every expression as written (the build the GPU is checked against):
+    codes match the reference exactly, fp32 results to the last places."""
+import numpy as np
+import pytest
+
+from oracle import have_ref
+from train_util import TRAIN_CASES, dx_bound, host_layer, make_train_case, ref_layer, split_opts
+from util import assert_close_terms
+
+pytestmark = pytest.mark.skipif(not have_ref(), reason="oracle/_ref not built (no reference tree)")
+
+
+def _run(case, contracted):
+    n_in, n_out, dens, seed, B, lr, opts = TRAIN_CASES[case]
+    lopts, copts = split_opts(opts)
+    c = make_train_case(n_in, n_out, dens, seed, **lopts)
+    H, R = host_layer(c), ref_layer(c)
+    rng = c["rng"]
+    for step in range(3):
+        x = rng.normal(size=(B, n_in)).astype(np.float32)
+        dy = rng.normal(size=(B, n_out)).astype(np.float32)
+        bound = dx_bound(H, dy, lr)
+        outs_h = H.backward_train(x, dy, lr, contracted=contracted, **copts)
+        outs_r = R.backward_train(x, dy, lr, **copts)
+        _, _, _, vr = R.export()
+        st = R.get_train_state(c["rank"])
+        yield step, lopts, bound, H, outs_h, vr, st, outs_r
+
+
+@pytest.mark.parametrize("case", range(len(TRAIN_CASES)))
+def test_backward_train_matches_reference(case):
+    """The contracted restatement against the reference: exact."""
+    for step, lopts, _, H, (dxh, aih, agh), vr, st, (dxr, air, agr) in _run(case, True):
+        assert np.array_equal(H.val[:len(vr)], vr), f"codes differ at step {step}"
+        assert np.array_equal(dxh, dxr), f"dx differs at step {step}"
+        assert np.array_equal(aih, air) and np.array_equal(agh, agr)
+        assert np.array_equal(H.value_scale, st["value_scale"]), f"value_scale differs at step {step}"
+        assert np.array_equal(H.output_scale, st["output_scale"]), f"output_scale differs at step {step}"
+        assert np.array_equal(H.vs_step, st["vs_step"]) and np.array_equal(H.os_step, st["os_step"])
+        assert np.array_equal(H.os_importance, st["os_importance"])
+        assert np.array_equal(H.vs_momentum, st["vs_momentum"])
+        np.testing.assert_allclose(H.vs_importance, st["vs_importance"], rtol=1e-6, atol=0)
+        if lopts.get("empty_rows", 0) == 0:
+            assert np.array_equal(H.vs_importance, st["vs_importance"])
+
+
+@pytest.mark.parametrize("case", range(len(TRAIN_CASES)))
+def test_ieee_restatement_against_reference(case):
+    """The IEEE restatement (the GPU's checker) against the reference: codes
+    exact; dx, scales and state within fp32 rounding of the contractions."""
+    for step, _, bound, H, (dxh, aih, agh), vr, st, (dxr, air, agr) in _run(case, False):
+        what = f"case {case} step {step}"
+        assert np.array_equal(H.val[:len(vr)], vr), what + ": codes"
+        assert_close_terms(dxh, dxr, bound, what + ": dx")
+        assert np.array_equal(aih, air) and np.array_equal(agh, agr)
+        for k in ("value_scale", "output_scale", "vs_momentum", "vs_importance", "os_importance"):
+            np.testing.assert_allclose(getattr(H, k), st[k], rtol=1e-5, atol=1e-30, err_msg=what + ": " + k)
+        assert np.array_equal(H.vs_step, st["vs_step"]) and np.array_equal(H.os_step, st["os_step"])
+
+
+def test_learning_rate_zero_is_plain_backward():
+    """lr = 0 changes nothing and gives backward_dense's dx."""
+    c = make_train_case(70, 50, 0.1, 11)
+    H = host_layer(c)
+    val0, vs0 = H.val.copy(), H.value_scale.copy()
+    x = c["rng"].normal(size=(3, 70)).astype(np.float32)
+    dy = c["rng"].normal(size=(3, 50)).astype(np.float32)
+    dx, _, _ = H.backward_train(x, dy, 0.0)
+    dx0, _, _ = H.backward_dense(x, dy, threads=1)
+    assert np.array_equal(H.val, val0) and np.array_equal(H.value_scale, vs0)
+    assert np.array_equal(H.vs_step, np.zeros_like(H.vs_step))
+    np.testing.assert_allclose(dx, dx0, rtol=1e-6, atol=1e-6)

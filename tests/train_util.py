@@ -1,0 +1,97 @@
+"""Seeded layers for the tests of backward with the optimizer update."""
+import numpy as np
+
+from oracle import HostLayer
+
+
+def make_train_case(n_in, n_out, density, seed, rank=1, empty_rows=0, os_trainable=False, imp_scales=False):
+    """Random scattered layer with weights across the FP4 range, importances,
+    value scales (and, when asked, trainable output scales and importance
+    scales); rows [0, empty_rows) hold no synapse."""
+    rng = np.random.default_rng(seed)
+    ptrs, cols = [0], []
+    for r in range(n_in):
+        if r >= empty_rows:
+            k = max(1, int(rng.binomial(n_out, density)))
+            cols.extend(np.sort(rng.choice(n_out, size=min(k, n_out), replace=False)).tolist())
+        ptrs.append(len(cols))
+    c = dict(n_in=n_in, n_out=n_out, rank=rank, os_trainable=os_trainable,
+             ptrs=np.array(ptrs, np.int32), cols=np.array(cols, np.int32))
+    nnz = len(cols)
+    c["w"] = rng.normal(0.0, 1.5, size=nnz).astype(np.float32)
+    c["imp"] = np.abs(rng.normal(0.0, 1.0, size=nnz)).astype(np.float32)
+    vs = np.zeros(n_in * rank, np.float32)
+    vs[::rank] = rng.uniform(0.5, 1.5, n_in)
+    for k in range(1, rank):
+        vs[k::rank] = rng.uniform(0.0, 0.3, n_in)
+    os_ = np.zeros(n_out * rank, np.float32)
+    os_[::rank] = rng.uniform(0.5, 1.5, n_out) if (os_trainable or rank > 1) else 1.0
+    for k in range(1, rank):
+        os_[k::rank] = rng.uniform(0.0, 0.3, n_out)
+    c["vs"], c["os"] = vs, os_
+    c["is"] = rng.uniform(0.5, 2.0, n_in).astype(np.float32) if imp_scales else None
+    c["ois"] = rng.uniform(0.5, 2.0, n_out).astype(np.float32) if imp_scales else None
+    c["rng"] = rng
+    return c
+
+
+def host_layer(c):
+    H = HostLayer(c["n_in"], c["n_out"], c["rank"]).load_csr(c["ptrs"], c["cols"], w=c["w"], imp=c["imp"])
+    H.set_scales(c["vs"], c["os"])
+    H.output_scale_trainable = bool(c["os_trainable"])
+    H.importance_scale = c["is"]
+    H.output_importance_scale = c["ois"]
+    return H
+
+
+def ref_layer(c):
+    from oracle import RefLayer
+    R = RefLayer(c["n_in"], c["n_out"], c["ptrs"], c["cols"], c["w"], c["imp"])
+    R.set_scales(c["vs"], c["os"] if (c["os_trainable"] or c["rank"] > 1) else None, c["rank"])
+    # set_output_scale_raw marks the output scales trainable; keep the case's choice
+    R.set_train_state(os_trainable=int(c["os_trainable"]))
+    if c["is"] is not None:
+        R.set_importance_scales(c["is"], c["ois"])
+    return R
+
+
+# (n_in, n_out, density, seed, batch, lr, options)
+TRAIN_CASES = [
+    (64, 48, 0.2, 1, 1, 0.05, {}),
+    (64, 48, 0.2, 2, 4, 0.05, {}),
+    (200, 300, 0.05, 3, 1, 0.1, {}),
+    (100, 80, 0.1, 4, 2, 0.05, dict(lr_per_row_nnz=True)),
+    (100, 80, 0.1, 5, 1, 0.05, dict(damp_by_importance=False)),
+    (100, 80, 0.1, 6, 3, 0.05, dict(os_trainable=True)),
+    (60, 50, 0.1, 7, 2, 0.05, dict(empty_rows=10)),
+    (80, 64, 0.15, 8, 1, 0.05, dict(rank=2, os_trainable=True)),
+    (90, 70, 0.1, 9, 2, 0.2, dict(imp_scales=True)),
+    (40, 600, 0.3, 10, 1, 0.05, {}),  # rows longer than one 64-byte decode chunk
+]
+LAYER_OPTS = ("rank", "empty_rows", "os_trainable", "imp_scales")
+
+
+def split_opts(opts):
+    layer = {k: v for k, v in opts.items() if k in LAYER_OPTS}
+    call = {k: v for k, v in opts.items() if k not in LAYER_OPTS}
+    return layer, call
+
+
+def dx_bound(H, dy, lr, max_abs_delta=2.0):
+    """sum over a row's synapses of |w| * |dy| with |w| bounded over the whole
+    call: each batch step moves a weight code by at most lr * max_abs_delta,
+    so |quant| <= |code before| + B * lr * max_abs_delta.  Taken before the
+    update (the scales are those the call's dx uses)."""
+    from sili__new_amd.codec import fp4_decode_np
+    dy = np.atleast_2d(dy)
+    B = dy.shape[0]
+    cols = H.decode_cols()
+    rows = np.repeat(np.arange(H.n_in), np.diff(H.row_elem_start.astype(np.int64)))
+    q0 = fp4_decode_np(H.val[:len(cols)] >> 4).astype(np.float64)
+    vs = H.value_scale.reshape(H.n_in, H.rank).astype(np.float64)
+    os_ = H.output_scale.reshape(H.n_out, H.rank).astype(np.float64)
+    S = np.abs(vs[rows] * os_[cols]).sum(1)
+    mag = (np.abs(q0) + B * abs(lr) * max_abs_delta) * S
+    T = np.zeros((H.n_in, B))
+    np.add.at(T, rows, (np.abs(dy[:, cols].astype(np.float64)) * mag).T)
+    return T.T
