@@ -45,6 +45,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--synapto-reps", type=int, default=5, help="config 3: timed synaptogenesis steps")
     p.add_argument("--c4-batches", default="1,8,128", help="config 4: token batches to time")
+    p.add_argument("--train-lr", type=float, default=0.0,
+                   help="config 1: the backward carries the optimizer update at this learning rate "
+                        "(stochastic re-quantization, as the reference's SparseLinearLayer)")
     p.add_argument("--verbose", action="store_true")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run 3 device-to-device copies of MIB MiB (HBM counter calibration)")
@@ -200,6 +203,14 @@ def algorithmic(info, n_in, n_out, B, wl=None):
         "bwd:gather_gradw": Bv + Bi + Bp + Bs + 4 * B * n_out + 4 * B * n_in + 4 * B * n_in + 4 * nnz,
         "fwd:transpose": 8 * B * n_in,
         "bwd:transpose": 8 * B * n_out,
+        # optimizer update over the canonical store: value bytes read and
+        # written, index, row starts (byte + element), the row's scale and its
+        # RMSprop state read and written (vs, importance, step: 12 B), output
+        # scales, xT and gT read, dX written
+        "bwd:train_rows": 2 * Bv + Bi + Bp + 2 * 12 * n_in + 4 * n_out + 4 * B * n_in + 4 * B * n_out
+                          + 4 * B * n_in,
+        # shadow value bytes refreshed through the kept permutation
+        "bwd:train_shadow": 4 * nnz + nnz + nnz,
     }
     # batch-1 byte-split kernels move the same algorithmic bytes as the gather
     for op in ("fwd", "bwd"):
@@ -273,7 +284,7 @@ def build_copy(cfg, wl, hip, api):
     return d
 
 
-def make_step(cfg, api, B, stream):
+def make_step(cfg, api, B, stream, train_lr=0.0):
     L = api.L
 
     def step(d):
@@ -286,10 +297,50 @@ def make_step(cfg, api, B, stream):
         if cfg == 1:
             # x = NULL: backward reads the forward's stored input (feature-major
             # copy), as the reference's backward_dense reads its last_input
-            api.ck(L.sili_backward_dense(h, None, d["g"], B, d["dx"], d["gws"], None, 0.0, stream))
+            if train_lr:
+                api.ck(L.sili_backward_dense(h, None, d["g"], B, d["dx"], None, None, train_lr, stream))
+            else:
+                api.ck(L.sili_backward_dense(h, None, d["g"], B, d["dx"], d["gws"], None, 0.0, stream))
         elif cfg == 3:
             api.ck(L.sili_backward_dense(h, None, d["g"], B, d["dx"], None, d["gwb"], 0.0, stream))
     return step
+
+
+def cpu_baseline_train(wl, seconds, lr):
+    """Config 1 with the optimizer update: the reference's own compiled
+    disldo_forward + disldo_backward(lr) (oracle/_ref, OpenMP) on this host;
+    without _ref, the oracle's single-thread restatement of the update."""
+    from oracle import HostLayer, RefLayer, have_ref
+    x, g = wl.x.astype(np.float32), wl.g.astype(np.float32)
+    if have_ref():
+        threads = os.cpu_count() or 1
+        R = RefLayer(wl.n_in, wl.n_out, wl.ptrs, wl.cols, wl.q).set_scales(wl.value_scale)
+        R.compact()
+
+        def step():
+            R.forward_dense(x, threads=threads)
+            R.backward_train(x, g, lr, threads=threads)
+        kind, what = "reference", "the reference's disldo_forward + disldo_backward(lr) from oracle/_ref"
+    else:
+        threads = 1
+        H = HostLayer(wl.n_in, wl.n_out).load_csr(wl.ptrs, wl.cols, w=wl.q).set_scales(wl.value_scale)
+
+        def step():
+            H.forward_dense(x, threads=1)
+            H.backward_train(x, g, lr)
+        kind, what = "port", "the oracle's forward + backward_train (one thread)"
+    times = []
+    t_end = time.perf_counter() + seconds
+    while True:
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_end or len(times) >= 30:
+            break
+    med = float(np.median(times))
+    return {"value": round(wl.nnz / med / 1e9, 5), "unit": "GNNZ/s", "cores": threads, "kind": kind,
+            "sample": f"full config-1 training step ({what}, lr {lr}), {len(times)} reps, "
+                      f"median {med * 1e3:.1f} ms/step"}
 
 
 def cpu_baseline(cfg, wl, seconds):
@@ -538,7 +589,11 @@ def main():
         pool.append(build_copy(cfg, wl, hip, api))
     t_build = time.perf_counter() - t_build
     stream = api.L.sili_stream(pool[0]["h"])
-    run = make_step(cfg, api, B, stream)
+    train_lr = a.train_lr if cfg == 1 else 0.0
+    if a.train_lr and cfg != 1:
+        print(json.dumps({"error": "--train-lr applies to config 1 only"}))
+        sys.exit(2)
+    run = make_step(cfg, api, B, stream, train_lr)
 
     def step(i):
         run(pool[i % copies])
@@ -621,6 +676,9 @@ def main():
         elif cfg == 2:
             step_bytes = alg["fwd_sparse:gather"] + alg["bwd:gather"]
             flops = 2 * int(np.diff(wl.ptrs)[np.asarray(wl.x_idx)].sum()) + 2 * units * B
+        elif train_lr:
+            step_bytes = alg["fwd:gather"] + alg["bwd:train_rows"] + alg["bwd:train_shadow"]
+            flops = 2 * 2 * units * B
         else:
             # forward + grad-input + sampled grad-W, each op counted as if run
             # alone (the fused backward moves less)
@@ -628,6 +686,10 @@ def main():
             flops = 3 * 2 * units * B
     step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
 
+    workload = workload_text(cfg, wl)
+    if train_lr:
+        workload = workload.replace("grad-input + nnz-sampled grad-W",
+                                    f"backward with the optimizer update (lr {train_lr}, stochastic rounding)")
     out = {
         "metric": "FP4 delta-CSR SpMM GNNZ/s + achieved HBM GB/s (% of peak), fwd+bwd",
         "value": round(units / (ms_step * 1e-3) / 1e9, 4),
@@ -642,7 +704,7 @@ def main():
         "dtype": "fp32",
         "data": "synthetic",
         "config": {
-            "workload": workload_text(cfg, wl),
+            "workload": workload,
             "n_in": n_in, "n_out": n_out, "batch": B, "nnz": units, "nnz_scattered": nnz_s,
             "n_tiles": n_tiles, "index_bytes": info["index_bytes"],
             "copies_rotated": copies, "rotation_mib": round(copies * per_copy / 2**20, 1),
@@ -660,7 +722,12 @@ def main():
     if cfg == 3 and a.synapto_reps > 0:
         pool.clear()
         out["synapto_gpu"] = time_synapto(hip, wl, a.synapto_reps)
-    out["cpu_baseline"] = None if a.no_cpu_baseline else cpu_baseline(cfg, wl, a.cpu_seconds)
+    if a.no_cpu_baseline:
+        out["cpu_baseline"] = None
+    elif train_lr:
+        out["cpu_baseline"] = cpu_baseline_train(wl, a.cpu_seconds, train_lr)
+    else:
+        out["cpu_baseline"] = cpu_baseline(cfg, wl, a.cpu_seconds)
     if a.verbose:
         print(f"build {t_build:.1f}s copies {copies}", file=sys.stderr)
     print(json.dumps(out), flush=True)

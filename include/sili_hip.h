@@ -161,6 +161,16 @@ int sili_backward_dense_train(sili_layer *layer, const float *x, const float *dy
                               float *dx, float learning_rate, int lr_per_row_nnz,
                               int damp_by_importance, float beta2, float eps, void *stream);
 
+/* The scale-update variant of the layer's optimizer update, as the reference's
+ * layer classes fix it (sili/cpu_backend.cpp:992-1013):
+ *   0 (default) RMSprop steps on the scales inside the loop; the stored code is
+ *     stepped by g * S (SparseLinearLayer[Deterministic]);
+ *   1 DeferredScaleWrite: true-units weights stepped by g, codes stored under
+ *     the scales in effect after the call (SparseLinearLayerResync[Deterministic]);
+ *   2 NoScalePolicy: the scales take no step (rows without synapses still do)
+ *     (SparseLinearLayerNoScale[Deterministic]). */
+int sili_set_update_variant(sili_layer *layer, int variant);
+
 /* Rounding of the update's re-quantization: 1 (default, as the reference's
  * SparseLinearLayer, sili/cpu_backend.cpp:992) stochastic -- unbiased dithered
  * rounding (fp4quant.hpp:210-265) driven by a counter-based generator of this

@@ -46,7 +46,13 @@ class _OracleLayerC(C.Structure):
 class _TrainParams(C.Structure):
     _fields_ = [("lr", C.c_float), ("lr_per_row_nnz", C.c_int32), ("damp_by_importance", C.c_int32),
                 ("beta2", C.c_float), ("eps", C.c_float), ("beta1", C.c_float), ("min_decay_frac", C.c_float),
-                ("max_abs_delta", C.c_float), ("max_ci", C.c_float), ("zero_escape_eps", C.c_float)]
+                ("max_abs_delta", C.c_float), ("max_ci", C.c_float), ("zero_escape_eps", C.c_float),
+                ("variant", C.c_int32)]
+
+
+# the scale-update variants of the reference's layer classes
+# (sili/cpu_backend.cpp:992-1013)
+TRAIN_VARIANTS = {"plain": 0, "resync": 1, "noscale": 2}
 
 
 class _TrainState(C.Structure):
@@ -158,7 +164,7 @@ def reflib():
                                           _f32p, C.c_int]
         R.ref_row_remove_col.restype = C.c_int
         R.ref_backward_train.argtypes = [C.c_void_p, _f32p, _f32p, C.c_int, _f32p, _f32p, _f32p, C.c_float,
-                                         C.c_int, C.c_int, C.c_float, C.c_float, C.c_int]
+                                         C.c_int, C.c_int, C.c_float, C.c_float, C.c_int, C.c_int]
         R.ref_layer_set_importance_scales.argtypes = [C.c_void_p, _f32p, _f32p]
         _u32p = C.POINTER(C.c_uint32)
         R.ref_layer_set_train_state.argtypes = [C.c_void_p, _f32p, _f32p, _u32p, _f32p, _u32p, C.c_int]
@@ -367,12 +373,13 @@ class HostLayer:
         return np.bincount(self.decode_cols(), minlength=self.n_out).astype(np.int32)
 
     def backward_train(self, x, dy, lr, lr_per_row_nnz=False, damp_by_importance=True, beta2=0.999, eps=1e-8,
-                       acc=None, contracted=False):
+                       acc=None, contracted=False, variant="plain"):
         """Backward with the optimizer update (deterministic rounding, one
         thread): updates self.val and the scale state in place; returns dx and
         the activity accumulators.  self.last_quant / self.last_imp: every
         synapse's weight code value and importance before re-quantization.
-        contracted=True runs the FMA-contracted build of the restatement."""
+        contracted=True runs the FMA-contracted build of the restatement.
+        variant: "plain", "resync" (DeferredScaleWrite) or "noscale"."""
         self.last_quant = np.zeros(max(1, self.nnz), np.float32)
         self.last_imp = np.zeros(max(1, self.nnz), np.float32)
         x = _c(np.atleast_2d(x), np.float32)
@@ -388,7 +395,8 @@ class HostLayer:
                          _p(self.vs_step, u32p), _p(self.output_scale, _f32p), _p(self.os_importance, _f32p),
                          _p(self.os_step, u32p), _p(isc, _f32p), _p(oisc, _f32p), _p(deg, _i32p),
                          int(self.output_scale_trainable), _p(self.last_quant, _f32p), _p(self.last_imp, _f32p))
-        P = _TrainParams(lr, int(lr_per_row_nnz), int(damp_by_importance), beta2, eps, **TRAIN_DEFAULTS)
+        P = _TrainParams(lr, int(lr_per_row_nnz), int(damp_by_importance), beta2, eps, **TRAIN_DEFAULTS,
+                         variant=TRAIN_VARIANTS[variant])
         s = self._cstruct()
         if lib(contracted).oracle_backward_train(C.byref(s), _p(self.val, _u8p), C.byref(st), _p(x, _f32p), _p(dy, _f32p),
                                        x.shape[0], _p(dx, _f32p), _p(ai, _f32p), _p(ag, _f32p), C.byref(P)) != 0:
@@ -541,7 +549,7 @@ class RefLayer:
         return out
 
     def backward_train(self, x, dy, lr, lr_per_row_nnz=False, damp_by_importance=True, beta2=0.999, eps=1e-8,
-                       threads=1):
+                       threads=1, variant="plain"):
         x = _c(np.atleast_2d(x), np.float32)
         dy = _c(np.atleast_2d(dy), np.float32)
         dx = np.zeros_like(x)
@@ -549,7 +557,7 @@ class RefLayer:
         ag = np.zeros(self.n_out, np.float32)
         reflib().ref_backward_train(self.h, _p(x, _f32p), _p(dy, _f32p), x.shape[0], _p(dx, _f32p), _p(ai, _f32p),
                                     _p(ag, _f32p), lr, int(lr_per_row_nnz), int(damp_by_importance), beta2, eps,
-                                    threads)
+                                    threads, TRAIN_VARIANTS[variant])
         return dx, ai, ag
 
     def forward_sparse(self, ptrs, idx, vals, batch, threads=1):

@@ -39,6 +39,17 @@ static CSRInput<S, float> make_input(const int32_t *ptrs, const int32_t *idx, co
     return csr;
 }
 
+// variant 0: SparseLinearLayerDeterministic, 1: SparseLinearLayerResyncDeterministic,
+// 2: SparseLinearLayerNoScaleDeterministic (sili/cpu_backend.cpp:1007-1013).
+template <typename Policy, bool Deferred>
+static void ref_backward_train_t(RefLayer *L, const float *x, const float *dy, int batch, float *dx, float *acc_in,
+                                 float *acc_grad, float lr, int lr_per_row_nnz, int damp, float beta2, float eps,
+                                 int threads) {
+    disldo_backward<S, FP4BiPacked, COL, Policy, Deferred, false>(
+        x, S(batch), S(L->n_in), dy, L->w, dx, acc_in, acc_grad, lr, threads, lr_per_row_nnz != 0, damp != 0,
+        beta2, eps, 0.9f, 0.0f, 2.0f, 100.0f);
+}
+
 extern "C" {
 
 uint8_t ref_fp4_encode(float v) { return fp4_encode_bits(v); }
@@ -190,12 +201,18 @@ void ref_backward_dense(void *h, const float *x, const float *dy, int batch, flo
 // the production policy constants.
 void ref_backward_train(void *h, const float *x, const float *dy, int batch, float *dx, float *acc_in,
                         float *acc_grad, float lr, int lr_per_row_nnz, int damp, float beta2, float eps,
-                        int threads) {
+                        int threads, int variant) {
     auto *L = static_cast<RefLayer *>(h);
     std::memset(dx, 0, sizeof(float) * size_t(batch) * size_t(L->n_in));
-    disldo_backward<S, FP4BiPacked, COL, RMSpropScalePolicy<float>, false, false>(
-        x, S(batch), S(L->n_in), dy, L->w, dx, acc_in, acc_grad, lr, threads, lr_per_row_nnz != 0, damp != 0,
-        beta2, eps, 0.9f, 0.0f, 2.0f, 100.0f);
+    if (variant == 1)
+        ref_backward_train_t<RMSpropScalePolicy<float>, true>(L, x, dy, batch, dx, acc_in, acc_grad, lr,
+                                                              lr_per_row_nnz, damp, beta2, eps, threads);
+    else if (variant == 2)
+        ref_backward_train_t<NoScalePolicy<float>, false>(L, x, dy, batch, dx, acc_in, acc_grad, lr, lr_per_row_nnz,
+                                                          damp, beta2, eps, threads);
+    else
+        ref_backward_train_t<RMSpropScalePolicy<float>, false>(L, x, dy, batch, dx, acc_in, acc_grad, lr,
+                                                               lr_per_row_nnz, damp, beta2, eps, threads);
 }
 
 // Per-row / per-column importance scales (delta_csr_types.hpp:1006-1031).

@@ -836,6 +836,12 @@ int oracle_backward_train(const OracleLayer *L, uint8_t *val, OracleTrainState *
     std::vector<float> mdx(size_t(batch * n_in), 0.0f);
     std::vector<float> mcol(size_t(n_out * rank), 0.0f), mcol_c(size_t(n_out * rank), 0.0f);
     float *vs = S->value_scale, *os = S->output_scale;
+    const bool deferred = P->variant == 1, no_scale = P->variant == 2;
+    // DeferredScaleWrite: each synapse's true-units (cw, ci) and column, stored
+    // after the scales are final (linear_disldo.hpp:501-509,783,2090-2112)
+    const uint64_t nnz_all = L->row_elem_start[n_in];
+    std::vector<float> def_w(deferred ? nnz_all : 0), def_i(deferred ? nnz_all : 0);
+    std::vector<uint32_t> def_col(deferred ? nnz_all : 0);
     for (int64_t r = 0; r < n_in; ++r) {
         const uint64_t e0 = L->row_elem_start[r], e1 = L->row_elem_start[r + 1];
         const uint64_t nnz_row = e1 - e0;
@@ -853,6 +859,35 @@ int oracle_backward_train(const OracleLayer *L, uint8_t *val, OracleTrainState *
             const float out_imp_scale = S->output_importance_scale ? S->output_importance_scale[col] : 1.0f;
             const float combined_imp_scale = imp_scale * out_imp_scale;
             float ci = ci_orig * combined_imp_scale;
+            if (deferred) {
+                // true-units update under component 0 of both scales
+                // (linear_disldo.hpp:687-790)
+                const float val_scale = vs[r * rank], out_scale = os[int64_t(col) * rank];
+                const float combined_scale = val_scale * out_scale;
+                float cw = cw_orig * combined_scale;
+                for (int64_t b = 0; b < batch; ++b) {
+                    const float iv = x[b * n_in + r];
+                    const float dyv = dy[b * n_out + col];
+                    const float g = dyv * iv;
+                    if (lr != 0.0f) {
+                        const float contrib = iv * cw_orig;
+                        ci = bounded_update_ci(ci, g, contrib, P->beta2, P->min_decay_frac, P->max_ci);
+                        cw += bounded_update_cw(g, ci, 1.0f, eff_lr, P->eps, P->damp_by_importance != 0,
+                                                P->max_abs_delta);
+                        sg[0] += static_cast<double>(cw_orig) * static_cast<double>(out_scale) * g;
+                        mcol[size_t(col) * rank] += cw_orig * val_scale * g;
+                        sgc[0] += static_cast<double>(cw_orig) * static_cast<double>(out_scale) * contrib;
+                        mcol_c[size_t(col) * rank] += cw_orig * val_scale * contrib;
+                    }
+                    mdx[size_t(b * n_in + r)] += cw * dyv;
+                }
+                if (lr != 0.0f) {
+                    def_w[vb] = cw;
+                    def_i[vb] = ci;
+                    def_col[vb] = col;
+                }
+                continue;
+            }
             float Sc = 0.0f;
             for (int k = 0; k < rank; ++k) Sc += vs[r * rank + k] * os[int64_t(col) * rank + k];
             float quant = cw_orig;
@@ -885,11 +920,21 @@ int oracle_backward_train(const OracleLayer *L, uint8_t *val, OracleTrainState *
                 val[vb] = uint8_t((fp4_enc(quant) << 4) | fp4_enc(ci / combined_imp_scale));
             }
         }
-        if (lr != 0.0f) {
-            for (int k = 0; k < rank; ++k) {
-                const int64_t i = r * rank + k;
-                rmsprop_scale_update(vs[i], S->vs_importance[i], static_cast<float>(sg[k]), scale_eff_lr, P->beta2,
-                                     P->eps, static_cast<float>(sgc[k]), S->vs_step[i]);
+        // the row's scale step (linear_disldo.hpp:898-925): every component,
+        // component 0 alone under DeferredScaleWrite, none under NoScalePolicy
+        if (lr != 0.0f && !no_scale) {
+            if (deferred) {
+                // the reference indexes the scale and its second moment by the
+                // row alone here (value_scale[r]: component r % rank of row
+                // r / rank once rank > 1), its step counter by (r, 0)
+                rmsprop_scale_update(vs[r], S->vs_importance[r], static_cast<float>(sg[0]), scale_eff_lr, P->beta2,
+                                     P->eps, static_cast<float>(sgc[0]), S->vs_step[r * rank]);
+            } else {
+                for (int k = 0; k < rank; ++k) {
+                    const int64_t i = r * rank + k;
+                    rmsprop_scale_update(vs[i], S->vs_importance[i], static_cast<float>(sg[k]), scale_eff_lr,
+                                         P->beta2, P->eps, static_cast<float>(sgc[k]), S->vs_step[i]);
+                }
             }
         }
     }
@@ -936,7 +981,7 @@ int oracle_backward_train(const OracleLayer *L, uint8_t *val, OracleTrainState *
         }
     }
     for (size_t i = 0; i < mdx.size(); ++i) dx[i] += mdx[i];
-    if (lr != 0.0f && S->output_scale_trainable) {
+    if (lr != 0.0f && S->output_scale_trainable && !no_scale) {
         for (int64_t c = 0; c < n_out; ++c) {
             const int32_t deg = S->out_degree ? S->out_degree[c] : 0;
             if (deg == 0) continue;
@@ -947,6 +992,23 @@ int oracle_backward_train(const OracleLayer *L, uint8_t *val, OracleTrainState *
                 const double sum_c = 0.0 + static_cast<double>(mcol_c[size_t(i)]);
                 rmsprop_scale_update(os[i], S->os_importance[i], static_cast<float>(sum), col_eff_lr, P->beta2,
                                      P->eps, static_cast<float>(sum_c), S->os_step[i]);
+            }
+        }
+    }
+    // DeferredScaleWrite replay under the final scales (linear_disldo.hpp:2090-2112)
+    if (deferred && lr != 0.0f) {
+        for (int64_t r = 0; r < n_in; ++r) {
+            const float fis = S->importance_scale ? S->importance_scale[r] : 1.0f;
+            for (uint64_t vb = L->row_elem_start[r]; vb < L->row_elem_start[r + 1]; ++vb) {
+                const uint32_t col = def_col[vb];
+                const float fois = S->output_importance_scale ? S->output_importance_scale[col] : 1.0f;
+                const float final_combined_scale = vs[r * rank] * os[int64_t(col) * rank];
+                const float final_combined_imp_scale = fis * fois;
+                const float w = def_w[vb] / final_combined_scale;
+                const float imp = def_i[vb] / final_combined_imp_scale;
+                if (S->quant_out) S->quant_out[vb] = w;
+                if (S->imp_out) S->imp_out[vb] = imp;
+                val[vb] = uint8_t((fp4_enc(w) << 4) | fp4_enc(imp));
             }
         }
     }

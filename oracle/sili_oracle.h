@@ -108,17 +108,22 @@ void oracle_sampled_gradw(const OracleLayer *L, const float *x, const float *dy,
                           int threads, int absmode);
 
 /* ---- backward with the optimizer update (learning_rate != 0) ----
- * disldo_backward (linear_disldo.hpp:466-2113) as SparseLinearLayerDeterministic
- * runs it (sili/cpu_backend.cpp:1007: RMSpropScalePolicy, no deferred scale
- * write, deterministic rounding) with BoundedRMSpropSynapsePolicy and the
- * constants of sili/cpu_backend.cpp:496-528, on a layer without block4 tiles,
- * one thread (the accumulation order of num_cpus = 1).  The value bytes and the
- * scale state are updated in place; dx, acc_in and acc_grad ACCUMULATE. */
+ * disldo_backward (linear_disldo.hpp:466-2113) with deterministic rounding as
+ * the deterministic layer classes run it (sili/cpu_backend.cpp:1007-1013),
+ * BoundedRMSpropSynapsePolicy and the constants of
+ * sili/cpu_backend.cpp:496-528, on a layer without block4 tiles, one thread
+ * (the accumulation order of num_cpus = 1).  variant:
+ *   0  RMSpropScalePolicy, scales written in the loop (SparseLinearLayer*)
+ *   1  RMSpropScalePolicy, DeferredScaleWrite (SparseLinearLayerResync*)
+ *   2  NoScalePolicy (SparseLinearLayerNoScale*)
+ * The value bytes and the scale state are updated in place; dx, acc_in and
+ * acc_grad ACCUMULATE. */
 typedef struct {
     float lr;
     int32_t lr_per_row_nnz;
     int32_t damp_by_importance;
     float beta2, eps, beta1, min_decay_frac, max_abs_delta, max_ci, zero_escape_eps;
+    int32_t variant;
 } OracleTrainParams;
 
 typedef struct {

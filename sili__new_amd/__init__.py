@@ -23,10 +23,15 @@ except ImportError as e:  # pragma: no cover - exercised only on an unbuilt tree
 
 SparseLinearLayer = _ext.SparseLinearLayer
 SparseLinearLayerDeterministic = _ext.SparseLinearLayerDeterministic
+SparseLinearLayerResync = _ext.SparseLinearLayerResync
+SparseLinearLayerResyncDeterministic = _ext.SparseLinearLayerResyncDeterministic
+SparseLinearLayerNoScale = _ext.SparseLinearLayerNoScale
+SparseLinearLayerNoScaleDeterministic = _ext.SparseLinearLayerNoScaleDeterministic
 fp4_quantize_array = _ext.fp4_quantize_array
 seed_fp4_stochastic_rng = _ext.seed_fp4_stochastic_rng
 
 LIB_PATH = os.path.join(_HERE, "libsili_hip.so")
 
-__all__ = ["SparseLinearLayer", "SparseLinearLayerDeterministic", "fp4_quantize_array", "seed_fp4_stochastic_rng",
-           "LIB_PATH"]
+__all__ = ["SparseLinearLayer", "SparseLinearLayerDeterministic", "SparseLinearLayerResync",
+           "SparseLinearLayerResyncDeterministic", "SparseLinearLayerNoScale", "SparseLinearLayerNoScaleDeterministic",
+           "fp4_quantize_array", "seed_fp4_stochastic_rng", "LIB_PATH"]

@@ -433,7 +433,9 @@ void backward_dense_train(Layer &L, const float *x, const float *dy, int64_t B, 
     const uint64_t seed = splitmix64_host(L.rng_seed ^ splitmix64_host(L.rng_calls + 1));
     launch_train_rows(L, xT, gT, B, dx, p, seed, st);
     launch_train_dead_rows(L, xT, gT, B, p, st);
-    if (L.output_scale_trainable && L.W.nnz > 0) launch_train_cols(L, p, st);
+    const bool scales_step = L.update_variant != UPDATE_NOSCALE;
+    if (L.output_scale_trainable && scales_step && L.W.nnz > 0) launch_train_cols(L, p, st);
+    launch_train_store(L, seed, st);
     launch_shadow_val_refresh(L, st);
     // copies holding value bytes are stale now: rebuilt on their next use
     for (DScatter *sc : {&L.W, &L.Wt}) {
@@ -442,7 +444,7 @@ void backward_dense_train(Layer &L, const float *x, const float *dy, int64_t B, 
         sc->cblk_cb = 0;
     }
     L.vs_ones = false;
-    if (L.output_scale_trainable) L.os_ones = false;
+    if (L.output_scale_trainable && scales_step) L.os_ones = false;
     ++L.train_calls;
     ++L.rng_calls;
 }
@@ -748,6 +750,15 @@ int sili_backward_dense_train(sili_layer *layer, const float *x, const float *dy
         const TrainParams p{learning_rate, lr_per_row_nnz ? 1 : 0, damp_by_importance ? 1 : 0, beta2, eps,
                             0.9f, 0.0f, 2.0f, 100.0f, 0.1f};
         backward_dense_train(layer->L, x, dy, batch, dx, p, st);
+    });
+}
+
+int sili_set_update_variant(sili_layer *layer, int variant) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        if (variant < UPDATE_PLAIN || variant > UPDATE_NOSCALE)
+            throw_error(SILI_ERR_INVALID, "update variant must be 0 (plain), 1 (resync) or 2 (noscale)");
+        layer->L.update_variant = variant;
     });
 }
 

@@ -148,6 +148,12 @@ struct Scratch {
     DevBuf<int> flag;        // validation flag
 };
 
+// The scale-update variants of the reference's layer classes
+// (sili/cpu_backend.cpp:992-1013): RMSprop steps on the scales written in the
+// loop (SparseLinearLayer), DeferredScaleWrite (SparseLinearLayerResync),
+// NoScalePolicy (SparseLinearLayerNoScale).
+enum UpdateVariant : int { UPDATE_PLAIN = 0, UPDATE_RESYNC = 1, UPDATE_NOSCALE = 2 };
+
 struct Layer {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -179,6 +185,9 @@ struct Layer {
     float pow_beta2 = 0.0f;
     DevBuf<float> mterm;          // per-synapse output-scale gradient terms
     DevBuf<double> dead_S;
+    DevBuf<float> def_w, def_i;   // DeferredScaleWrite: true-units (cw, ci) per synapse
+    DevBuf<float> vs_snap;        // value scales as the update's rows read them
+    int update_variant = UPDATE_PLAIN;
     bool stochastic_rounding = true;
     uint64_t rng_seed = 0x5EEDull, rng_calls = 0;
     int64_t train_calls = 0;
@@ -258,6 +267,9 @@ void launch_train_dead_rows(Layer &L, const float *xT, const float *gT, int64_t 
 void launch_train_cols(Layer &L, const TrainParams &p, hipStream_t st);
 // Shadow value bytes from the canonical ones (needs L.Wt_perm).
 void launch_shadow_val_refresh(Layer &L, hipStream_t st);
+// DeferredScaleWrite: the value bytes under the final scales (after the
+// scale steps; same seed as launch_train_rows).
+void launch_train_store(Layer &L, uint64_t seed, hipStream_t st);
 
 // ---- seeded synthetic layers (gen.hip) ----------------------------------------
 // Rebuilds the scattered store (and its shadow) from the seeded generator and

@@ -63,6 +63,9 @@ struct DBuf {
 uint64_t g_seed = 0;
 uint64_t g_seed_epoch = 0;
 
+// sili_set_update_variant's values
+constexpr int UPDATE_PLAIN_V = 0, UPDATE_RESYNC_V = 1, UPDATE_NOSCALE_V = 2;
+
 class Layer {
    public:
     Layer(int64_t n_inputs, int64_t n_outputs, int64_t max_weights, int num_cpus, int device)
@@ -478,6 +481,8 @@ class Layer {
     uintptr_t handle() const { return reinterpret_cast<uintptr_t>(L_); }
     // rounding of the update's re-quantization (stochastic by default)
     void set_stochastic_rounding(bool on) { ck(sili_set_stochastic_rounding(L_, on ? 1 : 0)); }
+    // the update's scale-update variant (0 plain, 1 resync, 2 noscale)
+    void set_update_variant(int v) { ck(sili_set_update_variant(L_, v)); }
 
    private:
     sili_layer *L_ = nullptr;
@@ -564,15 +569,30 @@ py::array_t<uint8_t> fp4_quantize_array(carr<float> v) {
     return out;
 }
 
-// SparseLinearLayerDeterministic (sili/cpu_backend.cpp:1007): the same layer
-// with round-to-nearest re-quantization in the update.
-class LayerDeterministic : public Layer {
+// The reference's other concrete layer classes (sili/cpu_backend.cpp:992-1013):
+// the same layer with another scale-update variant of the optimizer update
+// (sili_set_update_variant) and/or round-to-nearest re-quantization.
+template <int Variant, bool Stochastic>
+class LayerVariant : public Layer {
    public:
-    LayerDeterministic(int64_t n_inputs, int64_t n_outputs, int64_t max_weights, int num_cpus, int device)
+    LayerVariant(int64_t n_inputs, int64_t n_outputs, int64_t max_weights, int num_cpus, int device)
         : Layer(n_inputs, n_outputs, max_weights, num_cpus, device) {
-        set_stochastic_rounding(false);
+        set_stochastic_rounding(Stochastic);
+        set_update_variant(Variant);
     }
 };
+using LayerDeterministic = LayerVariant<UPDATE_PLAIN_V, false>;
+using LayerResync = LayerVariant<UPDATE_RESYNC_V, true>;
+using LayerResyncDeterministic = LayerVariant<UPDATE_RESYNC_V, false>;
+using LayerNoScale = LayerVariant<UPDATE_NOSCALE_V, true>;
+using LayerNoScaleDeterministic = LayerVariant<UPDATE_NOSCALE_V, false>;
+
+template <typename T>
+void bind_variant(py::module_ &m, const char *name) {
+    py::class_<T, Layer>(m, name)
+        .def(py::init<int64_t, int64_t, int64_t, int, int>(), py::arg("n_inputs"), py::arg("n_outputs"),
+             py::arg("max_weights"), py::arg("num_cpus") = 4, py::arg("device") = 0);
+}
 
 }  // namespace
 
@@ -610,6 +630,7 @@ PYBIND11_MODULE(_sili_hip, m) {
         .def("get_output_scale_importance", &Layer::get_output_scale_importance, py::arg("col"))
         .def("get_scale_state", &Layer::get_scale_state)
         .def("set_stochastic_rounding", &Layer::set_stochastic_rounding, py::arg("on"))
+        .def("set_update_variant", &Layer::set_update_variant, py::arg("variant"))
         .def("seed_stochastic_rounding", &Layer::seed_stochastic_rounding, py::arg("seed"))
         .def("forward_dense", &Layer::forward_dense, py::arg("x"))
         .def("backward_dense", &Layer::backward_dense, py::arg("dy"), py::arg("learning_rate"),
@@ -653,9 +674,11 @@ PYBIND11_MODULE(_sili_hip, m) {
         .def_property_readonly("ptrs", &Layer::ptrs)
         .def_property_readonly("neuron_input_accum", &Layer::neuron_input_accum)
         .def_property_readonly("neuron_grad_accum", &Layer::neuron_grad_accum);
-    py::class_<LayerDeterministic, Layer>(m, "SparseLinearLayerDeterministic")
-        .def(py::init<int64_t, int64_t, int64_t, int, int>(), py::arg("n_inputs"), py::arg("n_outputs"),
-             py::arg("max_weights"), py::arg("num_cpus") = 4, py::arg("device") = 0);
+    bind_variant<LayerDeterministic>(m, "SparseLinearLayerDeterministic");
+    bind_variant<LayerResync>(m, "SparseLinearLayerResync");
+    bind_variant<LayerResyncDeterministic>(m, "SparseLinearLayerResyncDeterministic");
+    bind_variant<LayerNoScale>(m, "SparseLinearLayerNoScale");
+    bind_variant<LayerNoScaleDeterministic>(m, "SparseLinearLayerNoScaleDeterministic");
     m.def("fp4_quantize_array", &fp4_quantize_array);
     m.def(
         "seed_fp4_stochastic_rng",

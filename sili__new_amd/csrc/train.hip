@@ -100,6 +100,23 @@ __device__ __forceinline__ uint32_t fp4_encode_stochastic(float v, uint64_t r) {
     return (sign ? 8u : 0u) | mag;
 }
 
+// The value byte of a synapse from its updated weight code value and its
+// importance in stored units: ValueAccessor<FP4BiPacked>::set / set_stochastic
+// (fp4quant.hpp:280-467).  Stochastic draws: splitmix64 of (call seed,
+// synapse, which).
+__device__ __forceinline__ uint32_t requantize(float w, float imp, bool stochastic, uint64_t seed, uint32_t vb) {
+    uint32_t wq, iq;
+    if (stochastic) {
+        const uint64_t base = seed + 2ull * (uint64_t)vb;
+        wq = fp4_encode_stochastic(w, splitmix64(base));
+        iq = fp4_encode_stochastic(imp, splitmix64(base + 1ull));
+    } else {
+        wq = fp4_encode(w);
+        iq = fp4_encode(imp);
+    }
+    return (wq << 4) | iq;
+}
+
 struct TrainArgs {
     const uint32_t *byte_start, *elem_start;  // canonical store
     const uint8_t *idx;
@@ -114,8 +131,11 @@ struct TrainArgs {
     const float *is, *ois;     // importance scales (NULL: ones)
     const float *pow_tab;
     float *mterm;              // [nnz * 2 * rank] column-gradient terms, or NULL
+    const float *vs_read;      // the scales the rows read (a snapshot when rows write others' slots)
+    float *def_w, *def_i;      // DeferredScaleWrite: true-units weight and importance per synapse
     float lr, beta2, eps, min_decay_frac, max_abs_delta, max_ci, zero_escape_eps;
     int lr_per_row_nnz, damp, stochastic;
+    int deferred, no_scale;    // DeferredScaleWrite; NoScalePolicy
     uint64_t seed;             // this call's stochastic-rounding seed
 };
 
@@ -124,6 +144,13 @@ struct TrainArgs {
 // batch steps; the row's fp64 gradient sums are added by lane 0 in entry
 // order; dx[b][row] is the sum over the row's entries of the updated weight
 // times dy, reduced across the lanes per b.
+//   scales written in the loop (default): the stored code value `quant` is
+//     stepped by dL/dquant = g * S(row, col), re-quantized in place; scale
+//     gradients weigh each term by quant (0.1 for an exact zero), per
+//     component (linear_disldo.hpp:791-896);
+//   DeferredScaleWrite: the true-units weight cw = code * vs0 * os0 is
+//     stepped by g; scale gradients weigh by the stored code, component 0
+//     only; (cw, ci) are kept for k_train_store (linear_disldo.hpp:687-790).
 template <int RANK>
 __global__ __launch_bounds__(256) void k_train_rows(TrainArgs a) {
     __shared__ double s_part[WAVES_T][64][2 * RANK];
@@ -146,7 +173,9 @@ __global__ __launch_bounds__(256) void k_train_rows(TrainArgs a) {
     const float imp_scale = a.is ? a.is[r] : 1.0f;
     float vs_k[RANK];
 #pragma unroll
-    for (int k = 0; k < RANK; ++k) vs_k[k] = a.vs[r * RANK + k];
+    for (int k = 0; k < RANK; ++k) vs_k[k] = a.vs_read[r * RANK + k];
+    const bool deferred = a.deferred != 0;
+    const int nk = deferred ? 1 : RANK;  // components that take gradient terms
     double sg[RANK], sgc[RANK];
 #pragma unroll
     for (int k = 0; k < RANK; ++k) sg[k] = sgc[k] = 0.0;
@@ -172,8 +201,10 @@ __global__ __launch_bounds__(256) void k_train_rows(TrainArgs a) {
             os_k[k] = has ? a.os[(int64_t)col * RANK + k] : 0.0f;
             S = S + vs_k[k] * os_k[k];
         }
-        float quant = cw_orig;
-        float cw = quant * S;
+        // wv: the stepped weight (code units; true units when deferred)
+        const float S_step = deferred ? 1.0f : S;
+        float wv = deferred ? cw_orig * (vs_k[0] * os_k[0]) : cw_orig;
+        float cw = deferred ? wv : wv * S;
         double psg[RANK], psgc[RANK];
         float pm[RANK], pmc[RANK];
 #pragma unroll
@@ -189,11 +220,12 @@ __global__ __launch_bounds__(256) void k_train_rows(TrainArgs a) {
             if (has) {
                 const float contrib = iv * cw_orig;
                 ci = bounded_update_ci(ci, g, contrib, a.beta2, a.min_decay_frac, a.max_ci);
-                quant = quant + bounded_update_cw(g, ci, S, eff_lr, a.eps, a.damp != 0, a.max_abs_delta);
-                cw = quant * S;
-                const float qf = (quant == 0.0f) ? a.zero_escape_eps : quant;
+                wv = wv + bounded_update_cw(g, ci, S_step, eff_lr, a.eps, a.damp != 0, a.max_abs_delta);
+                cw = deferred ? wv : wv * S;
+                const float qf = deferred ? cw_orig : ((wv == 0.0f) ? a.zero_escape_eps : wv);
 #pragma unroll
                 for (int k = 0; k < RANK; ++k) {
+                    if (k >= nk) break;
                     psg[k] = psg[k] + ((double)qf * (double)os_k[k]) * (double)g;
                     psgc[k] = psgc[k] + ((double)qf * (double)os_k[k]) * (double)contrib;
                     pm[k] = pm[k] + (qf * vs_k[k]) * g;
@@ -206,17 +238,12 @@ __global__ __launch_bounds__(256) void k_train_rows(TrainArgs a) {
             if (lane == 0u) rdx[b] = rdx[b] + tot;
         }
         if (has) {
-            uint32_t wq, iq;
-            const float imp_true = ci / combined_imp_scale;
-            if (a.stochastic) {
-                const uint64_t base = a.seed + 2ull * (uint64_t)vb;
-                wq = fp4_encode_stochastic(quant, splitmix64(base));
-                iq = fp4_encode_stochastic(imp_true, splitmix64(base + 1ull));
+            if (deferred) {
+                a.def_w[vb] = wv;
+                a.def_i[vb] = ci;
             } else {
-                wq = fp4_encode(quant);
-                iq = fp4_encode(imp_true);
+                a.val[vb] = (uint8_t)requantize(wv, ci / combined_imp_scale, a.stochastic != 0, a.seed, vb);
             }
-            a.val[vb] = (uint8_t)((wq << 4) | iq);
             if (a.mterm) {
 #pragma unroll
                 for (int k = 0; k < RANK; ++k) {
@@ -249,17 +276,53 @@ __global__ __launch_bounds__(256) void k_train_rows(TrainArgs a) {
     }
     wave_lds_sync();
     for (int64_t b = lane; b < B; b += 64) a.dx[b * a.n_in + r] = rdx[b];
-    if (lane == 0u) {
+    // the row's scale step (linear_disldo.hpp:898-925)
+    if (lane == 0u && !a.no_scale) {
 #pragma unroll
         for (int k = 0; k < RANK; ++k) {
-            const int64_t i = r * RANK + k;
+            if (k >= nk) break;
+            // DeferredScaleWrite indexes the scale and its second moment by
+            // the row alone (slot r: component r % rank of row r / rank once
+            // rank > 1) and its step counter by (r, 0)
+            const int64_t i = deferred ? r : r * RANK + k;
+            const int64_t is_ = r * RANK + k;
             float vsv = a.vs[i], st = a.vs_imp[i];
-            uint32_t step = a.vs_step[i];
+            uint32_t step = a.vs_step[is_];
             rmsprop_scale_update(vsv, st, (float)sg[k], scale_eff_lr, a.beta2, a.eps, (float)sgc[k], step, a.pow_tab);
             a.vs[i] = vsv;
             a.vs_imp[i] = st;
-            a.vs_step[i] = step;
+            a.vs_step[is_] = step;
         }
+    }
+}
+
+// DeferredScaleWrite's store (linear_disldo.hpp:2090-2112): every synapse's
+// (cw, ci) re-quantized under the scales in effect after the call, one wave
+// per canonical row.
+template <int RANK>
+__global__ __launch_bounds__(256) void k_train_store(TrainArgs a) {
+    const uint32_t wave = threadIdx.x >> 6;
+    const int64_t r = (int64_t)blockIdx.x * WAVES_T + wave;
+    if (r >= a.n_in) return;
+    const uint32_t e0 = a.elem_start[r], e1 = a.elem_start[r + 1];
+    if (e1 == e0) return;
+    const float fvs = a.vs[r * RANK];
+    const float fis = a.is ? a.is[r] : 1.0f;
+    uint32_t pos = a.byte_start[r], carry = 0, ebase = e0;
+    const uint32_t end = a.byte_start[r + 1];
+    while (pos < end) {
+        const Chunk ch = decode_chunk(a.idx, pos, end, carry);
+        if (ch.T == 0ull) break;
+        if (ch.term) {
+            const uint32_t vb = ebase + ch.rank;
+            const float fos = a.os[(int64_t)ch.col * RANK];
+            const float fois = a.ois ? a.ois[ch.col] : 1.0f;
+            const float final_combined_scale = fvs * fos;
+            const float final_combined_imp_scale = fis * fois;
+            a.val[vb] = (uint8_t)requantize(a.def_w[vb] / final_combined_scale,
+                                            a.def_i[vb] / final_combined_imp_scale, a.stochastic != 0, a.seed, vb);
+        }
+        carry = chunk_advance(ch, pos, ebase);
     }
 }
 
@@ -378,6 +441,21 @@ void launch_train_rows(Layer &L, const float *xT, const float *gT, int64_t B, fl
     a.ois = L.ois.p;
     a.pow_tab = L.pow_tab.p;
     a.mterm = L.output_scale_trainable ? L.mterm.p : nullptr;
+    a.deferred = L.update_variant == UPDATE_RESYNC ? 1 : 0;
+    a.no_scale = L.update_variant == UPDATE_NOSCALE ? 1 : 0;
+    a.vs_read = L.vs.p;
+    if (a.deferred) {
+        L.def_w.ensure((size_t)std::max<int64_t>(1, L.W.nnz));
+        L.def_i.ensure((size_t)std::max<int64_t>(1, L.W.nnz));
+        a.def_w = L.def_w.p;
+        a.def_i = L.def_i.p;
+        if (L.rank > 1) {
+            // rows write scale slots that other rows read: rows read a snapshot
+            L.vs_snap.ensure((size_t)(L.n_in * L.rank));
+            SILI_HIP(hipMemcpyAsync(L.vs_snap.p, L.vs.p, (size_t)(L.n_in * L.rank) * 4, hipMemcpyDeviceToDevice, st));
+            a.vs_read = L.vs_snap.p;
+        }
+    }
     a.lr = p.lr;
     a.beta2 = p.beta2;
     a.eps = p.eps;
@@ -396,6 +474,34 @@ void launch_train_rows(Layer &L, const float *xT, const float *gT, int64_t B, fl
         case 2: launch(k_train_rows<2>, grid, block, 0, st, a); break;
         case 3: launch(k_train_rows<3>, grid, block, 0, st, a); break;
         default: launch(k_train_rows<4>, grid, block, 0, st, a); break;
+    }
+    SILI_HIP(hipGetLastError());
+}
+
+void launch_train_store(Layer &L, uint64_t seed, hipStream_t st) {
+    if (L.update_variant != UPDATE_RESYNC || L.W.nnz == 0) return;
+    TrainArgs a{};
+    a.byte_start = L.W.byte_start.p;
+    a.elem_start = L.W.elem_start.p;
+    a.idx = L.W.idx.p;
+    a.val = L.W.val.p;
+    a.n_in = L.n_in;
+    a.n_out = L.n_out;
+    a.vs = L.vs.p;
+    a.os = L.os.p;
+    a.is = L.is.p;
+    a.ois = L.ois.p;
+    a.def_w = L.def_w.p;
+    a.def_i = L.def_i.p;
+    a.stochastic = L.stochastic_rounding ? 1 : 0;
+    a.seed = seed;
+    const dim3 grid((unsigned)((L.n_in + WAVES_T - 1) / WAVES_T)), block(256);
+    ProfScope ps("train_store", st);
+    switch (L.rank) {
+        case 1: launch(k_train_store<1>, grid, block, 0, st, a); break;
+        case 2: launch(k_train_store<2>, grid, block, 0, st, a); break;
+        case 3: launch(k_train_store<3>, grid, block, 0, st, a); break;
+        default: launch(k_train_store<4>, grid, block, 0, st, a); break;
     }
     SILI_HIP(hipGetLastError());
 }

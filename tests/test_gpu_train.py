@@ -14,8 +14,14 @@ from util import assert_close_terms
 pytestmark = pytest.mark.gpu
 
 
-def gpu_layer(hip, c, deterministic=True):
-    cls = hip.SparseLinearLayerDeterministic if deterministic else hip.SparseLinearLayer
+# the reference's layer classes per update variant: (deterministic, stochastic)
+CLASSES = {"plain": ("SparseLinearLayerDeterministic", "SparseLinearLayer"),
+           "resync": ("SparseLinearLayerResyncDeterministic", "SparseLinearLayerResync"),
+           "noscale": ("SparseLinearLayerNoScaleDeterministic", "SparseLinearLayerNoScale")}
+
+
+def gpu_layer(hip, c, deterministic=True, variant="plain"):
+    cls = getattr(hip, CLASSES[variant][0 if deterministic else 1])
     L = cls(c["n_in"], c["n_out"], len(c["cols"]) + 64)
     L.load_weights_with_importance(c["ptrs"], c["cols"], c["w"], c["imp"])
     if c["rank"] > 1:
@@ -50,21 +56,22 @@ def check_state(L, H, exact, what):
                                err_msg=what)
 
 
+@pytest.mark.parametrize("variant", list(CLASSES))
 @pytest.mark.parametrize("case", range(len(TRAIN_CASES)))
-def test_deterministic_update_matches_oracle(hip, case):
+def test_deterministic_update_matches_oracle(hip, case, variant):
     n_in, n_out, dens, seed, B, lr, opts = TRAIN_CASES[case]
     lopts, copts = split_opts(opts)
     c = make_train_case(n_in, n_out, dens, seed, **lopts)
-    H, L = host_layer(c), gpu_layer(hip, c)
+    H, L = host_layer(c), gpu_layer(hip, c, variant=variant)
     rng = c["rng"]
     for step in range(3):
-        what = f"case {case} step {step}"
+        what = f"case {case} {variant} step {step}"
         x = rng.normal(size=(B, n_in)).astype(np.float32)
         dy = rng.normal(size=(B, n_out)).astype(np.float32)
         bound = dx_bound(H, dy, lr)
         L.forward_dense(x)
         dxg = L.backward_dense(dy, lr, **copts)
-        dxh, _, _ = H.backward_train(x, dy, lr, **copts)
+        dxh, _, _ = H.backward_train(x, dy, lr, variant=variant, **copts)
         val = L.export_scattered()["val"]
         assert np.array_equal(val, H.val[:H.nnz]), what + ": value bytes"
         assert_close_terms(dxg, dxh, bound, what + ": dx")
@@ -103,15 +110,16 @@ def bracket(v):
     return lo, hi
 
 
-def test_stochastic_update_brackets_and_is_unbiased(hip):
+@pytest.mark.parametrize("variant", ["plain", "resync"])
+def test_stochastic_update_brackets_and_is_unbiased(hip, variant):
     c = make_train_case(400, 500, 0.1, 31)
-    H, L = host_layer(c), gpu_layer(hip, c, deterministic=False)
+    H, L = host_layer(c), gpu_layer(hip, c, deterministic=False, variant=variant)
     L.seed_stochastic_rounding(1234)
     x = c["rng"].normal(size=(1, 400)).astype(np.float32)
     dy = c["rng"].normal(size=(1, 500)).astype(np.float32)
     L.forward_dense(x)
     L.backward_dense(dy, 0.05)
-    H.backward_train(x, dy, 0.05)
+    H.backward_train(x, dy, 0.05, variant=variant)
     tab = fp4_decode_np(np.arange(16))
     val = L.export_scattered()["val"]
     for what, v, code in (("weight", H.last_quant[:H.nnz], val >> 4), ("importance", H.last_imp[:H.nnz], val & 15)):
