@@ -202,13 +202,28 @@ int sili_forward_sparse(sili_layer *layer, const int32_t *ptrs, const int32_t *i
                         const float *values, int64_t nnz_x, int64_t batch, float *y,
                         void *stream);
 
-/* backward_sparse at learning_rate 0 (sili/cpu_backend.cpp:587-603,
- * sisldo_ops.hpp:589-1104): dense x [batch,n_in], sparse dy CSR (nnz_dy =
- * dy_ptrs[batch]) -> device dx
- * [batch,n_in] (overwritten); accumulates neuron_input_accum / neuron_grad_accum. */
+/* backward_sparse (sili/cpu_backend.cpp:587-603, sisldo_ops.hpp:589-1104):
+ * dense x [batch,n_in], sparse dy CSR (nnz_dy = dy_ptrs[batch], indices
+ * strictly increasing per batch row) -> device dx [batch,n_in] (overwritten);
+ * accumulates neuron_input_accum / neuron_grad_accum.  learning_rate != 0
+ * also runs the optimizer update, as sili_backward_sparse_train with
+ * lr_per_row_nnz 0, damp_by_importance 1, beta2 0.999, eps 1e-8. */
 int sili_backward_sparse(sili_layer *layer, const float *x, const int32_t *dy_ptrs,
                          const int32_t *dy_indices, const float *dy_values, int64_t nnz_dy,
                          int64_t batch, float *dx, float learning_rate, void *stream);
+
+/* backward_sparse with the optimizer update (disldo_backward_sparse_grad,
+ * sisldo_ops.hpp:589-848): batch rows in order; a synapse whose column has a
+ * dy entry in a batch row takes an RMSprop step in true units and is
+ * re-quantized (round to nearest, whatever the layer's rounding setting)
+ * before the next batch row; each row's value scale (slot r, step counter
+ * (r, 0)) takes one bias-corrected RMSprop step after all batch rows.  Output
+ * scales are not updated.  batch <= 1024; layers holding block4 tiles:
+ * SILI_ERR_INVALID.  learning_rate 0 is plain backward_sparse. */
+int sili_backward_sparse_train(sili_layer *layer, const float *x, const int32_t *dy_ptrs,
+                               const int32_t *dy_indices, const float *dy_values, int64_t nnz_dy,
+                               int64_t batch, float *dx, float learning_rate, int lr_per_row_nnz,
+                               int damp_by_importance, float beta2, float eps, void *stream);
 
 /* ---- synaptogenesis ----------------------------------------------------- */
 

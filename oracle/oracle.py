@@ -117,6 +117,10 @@ def lib(contracted: bool = False):
         L.oracle_backward_train.argtypes = [C.POINTER(_OracleLayerC), _u8p, C.POINTER(_TrainState), _f32p, _f32p,
                                             C.c_int64, _f32p, _f32p, _f32p, C.POINTER(_TrainParams)]
         L.oracle_backward_train.restype = C.c_int
+        L.oracle_backward_sparse_train.argtypes = [C.POINTER(_OracleLayerC), _u8p, C.POINTER(_TrainState), _f32p,
+                                                   _i32p, _i32p, _f32p, C.c_int64, _f32p, _f32p, _f32p,
+                                                   C.POINTER(_TrainParams)]
+        L.oracle_backward_sparse_train.restype = C.c_int
         L.oracle_synapto_step.argtypes = [C.POINTER(_OracleLayerC), C.c_float, _i32p, _i32p, _f32p, _f32p,
                                           C.c_int64, C.c_int, _i32p, _i32p, _u8p, _i32p, _i32p, _u8p,
                                           C.POINTER(_SynStats)]
@@ -165,6 +169,8 @@ def reflib():
         R.ref_row_remove_col.restype = C.c_int
         R.ref_backward_train.argtypes = [C.c_void_p, _f32p, _f32p, C.c_int, _f32p, _f32p, _f32p, C.c_float,
                                          C.c_int, C.c_int, C.c_float, C.c_float, C.c_int, C.c_int]
+        R.ref_backward_sparse_train.argtypes = [C.c_void_p, _f32p, _i32p, _i32p, _f32p, C.c_int, _f32p, _f32p, _f32p,
+                                                C.c_float, C.c_int, C.c_int, C.c_float, C.c_float, C.c_int]
         R.ref_layer_set_importance_scales.argtypes = [C.c_void_p, _f32p, _f32p]
         _u32p = C.POINTER(C.c_uint32)
         R.ref_layer_set_train_state.argtypes = [C.c_void_p, _f32p, _f32p, _u32p, _f32p, _u32p, C.c_int]
@@ -403,6 +409,31 @@ class HostLayer:
             raise ValueError("backward_train: layers with block4 tiles are not supported")
         return dx, ai, ag
 
+    def backward_sparse_train(self, x, dptrs, didx, dvals, batch, lr, lr_per_row_nnz=False, damp_by_importance=True,
+                              beta2=0.999, eps=1e-8, contracted=False):
+        """backward_sparse with the optimizer update (one thread): updates
+        self.val and the value scales' state in place; returns dx and the
+        activity accumulators."""
+        x = _c(np.atleast_2d(x), np.float32)
+        dptrs, didx, dvals = _c(dptrs, np.int32), _c(didx, np.int32), _c(dvals, np.float32)
+        dx = np.zeros_like(x)
+        ai = np.zeros(self.n_in, np.float32)
+        ag = np.zeros(self.n_out, np.float32)
+        isc = None if self.importance_scale is None else _c(self.importance_scale, np.float32)
+        oisc = None if self.output_importance_scale is None else _c(self.output_importance_scale, np.float32)
+        u32p = C.POINTER(C.c_uint32)
+        st = _TrainState(_p(self.value_scale, _f32p), _p(self.vs_importance, _f32p), _p(self.vs_momentum, _f32p),
+                         _p(self.vs_step, u32p), _p(self.output_scale, _f32p), _p(self.os_importance, _f32p),
+                         _p(self.os_step, u32p), _p(isc, _f32p), _p(oisc, _f32p), None, 0, None, None)
+        P = _TrainParams(lr, int(lr_per_row_nnz), int(damp_by_importance), beta2, eps, **TRAIN_DEFAULTS, variant=0)
+        s = self._cstruct()
+        if lib(contracted).oracle_backward_sparse_train(C.byref(s), _p(self.val, _u8p), C.byref(st), _p(x, _f32p),
+                                                        _p(dptrs, _i32p), _p(didx, _i32p), _p(dvals, _f32p), batch,
+                                                        _p(dx, _f32p), _p(ai, _f32p), _p(ag, _f32p),
+                                                        C.byref(P)) != 0:
+            raise ValueError("backward_sparse_train: layers with block4 tiles are not supported")
+        return dx, ai, ag
+
     def sampled_gradw(self, x, dy, threads=8, absmode=False):
         x = _c(np.atleast_2d(x), np.float32)
         dy = _c(np.atleast_2d(dy), np.float32)
@@ -558,6 +589,18 @@ class RefLayer:
         reflib().ref_backward_train(self.h, _p(x, _f32p), _p(dy, _f32p), x.shape[0], _p(dx, _f32p), _p(ai, _f32p),
                                     _p(ag, _f32p), lr, int(lr_per_row_nnz), int(damp_by_importance), beta2, eps,
                                     threads, TRAIN_VARIANTS[variant])
+        return dx, ai, ag
+
+    def backward_sparse_train(self, x, dptrs, didx, dvals, batch, lr, lr_per_row_nnz=False, damp_by_importance=True,
+                              beta2=0.999, eps=1e-8, threads=1):
+        x = _c(np.atleast_2d(x), np.float32)
+        dptrs, didx, dvals = _c(dptrs, np.int32), _c(didx, np.int32), _c(dvals, np.float32)
+        dx = np.zeros_like(x)
+        ai = np.zeros(self.n_in, np.float32)
+        ag = np.zeros(self.n_out, np.float32)
+        reflib().ref_backward_sparse_train(self.h, _p(x, _f32p), _p(dptrs, _i32p), _p(didx, _i32p), _p(dvals, _f32p),
+                                           batch, _p(dx, _f32p), _p(ai, _f32p), _p(ag, _f32p), lr,
+                                           int(lr_per_row_nnz), int(damp_by_importance), beta2, eps, threads)
         return dx, ai, ag
 
     def forward_sparse(self, ptrs, idx, vals, batch, threads=1):

@@ -215,6 +215,17 @@ void ref_backward_train(void *h, const float *x, const float *dy, int batch, flo
                                                                lr_per_row_nnz, damp, beta2, eps, threads);
 }
 
+// disldo_backward_sparse_grad with the optimizer update (sili/cpu_backend.cpp:587-603).
+void ref_backward_sparse_train(void *h, const float *x, const int32_t *dptrs, const int32_t *didx,
+                               const float *dvals, int batch, float *dx, float *acc_in, float *acc_grad, float lr,
+                               int lr_per_row_nnz, int damp, float beta2, float eps, int threads) {
+    auto *L = static_cast<RefLayer *>(h);
+    auto g = make_input(dptrs, didx, dvals, batch, L->n_out);
+    std::memset(dx, 0, sizeof(float) * size_t(batch) * size_t(L->n_in));
+    disldo_backward_sparse_grad<S, FP4BiPacked, COL>(x, S(batch), L->w, g, dx, acc_in, acc_grad, lr, threads,
+                                                     lr_per_row_nnz != 0, damp != 0, beta2, eps);
+}
+
 // Per-row / per-column importance scales (delta_csr_types.hpp:1006-1031).
 void ref_layer_set_importance_scales(void *h, const float *is, const float *ois) {
     auto *L = static_cast<RefLayer *>(h);

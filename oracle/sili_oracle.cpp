@@ -1015,4 +1015,87 @@ int oracle_backward_train(const OracleLayer *L, uint8_t *val, OracleTrainState *
     return 0;
 }
 
+// sisldo_ops.hpp:613-848 (scattered section of disldo_backward_sparse_grad).
+int oracle_backward_sparse_train(const OracleLayer *L, uint8_t *val, OracleTrainState *S, const float *x,
+                                 const int32_t *dptrs, const int32_t *didx, const float *dvals, int64_t batch,
+                                 float *dx, float *acc_in, float *acc_grad, const OracleTrainParams *P) {
+    if (L->n_tiles > 0) return -1;
+    const int64_t n_in = L->n_in;
+    const int rank = L->rank;
+    const float lr = P->lr, beta2 = P->beta2, eps = P->eps;
+    for (int64_t b = 0; b < batch; ++b)
+        for (int64_t r = 0; r < n_in; ++r) acc_in[r] += std::fabs(x[b * n_in + r]);
+    for (int64_t b = 0; b < batch; ++b)
+        for (int32_t j = dptrs[b]; j < dptrs[b + 1]; ++j) acc_grad[didx[j]] += std::fabs(dvals[j]);
+    if (L->row_elem_start[n_in] == 0) return 0;
+    float *vs = S->value_scale;
+    const float *os = S->output_scale;
+    std::vector<double> sg(size_t(n_in), 0.0), sgc(size_t(n_in), 0.0);
+    for (int64_t b = 0; b < batch; ++b) {
+        const int32_t og_start = dptrs[b], og_end = dptrs[b + 1];
+        for (int64_t r = 0; r < n_in; ++r) {
+            const uint64_t e0 = L->row_elem_start[r], e1 = L->row_elem_start[r + 1];
+            if (e1 == e0) continue;
+            const float in_val = x[b * n_in + r];
+            const float effective_lr = P->lr_per_row_nnz ? lr / static_cast<float>(e1 - e0) : lr;
+            int32_t og = og_start;
+            float dx_accum = 0.0f;
+            const float imp_scale = S->importance_scale ? S->importance_scale[r] : 1.0f;
+            const float val_scale = vs[r * rank];
+            uint64_t pos = L->row_byte_start[r];
+            uint32_t col = 0;
+            for (uint64_t vb = e0; vb < e1; ++vb) {
+                col += uleb_dec(L->idx, pos);
+                const float w_stored = fp4_dec(val[vb] >> 4);
+                const float out_scale = os[int64_t(col) * rank];
+                const float combined_scale = val_scale * out_scale;
+                const float w = w_stored * combined_scale;
+                // merge with the batch row's sorted gradient columns
+                while (og < og_end && didx[og] < static_cast<int32_t>(col)) ++og;
+                if (og >= og_end || didx[og] != static_cast<int32_t>(col)) continue;
+                const float dy_val = dvals[og];
+                dx_accum += w * dy_val;
+                if (lr != 0.0f) {
+                    const float out_imp_scale =
+                        S->output_importance_scale ? S->output_importance_scale[col] : 1.0f;
+                    const float combined_imp_scale = imp_scale * out_imp_scale;
+                    const float grad = dy_val * in_val;
+                    const float stored_imp = fp4_dec(val[vb] & 0xFu);
+                    float imp = stored_imp * combined_imp_scale;
+                    const float contrib = in_val * w;
+                    imp = beta2 * imp + (1.0f - beta2) * (grad * grad + contrib * contrib);
+                    const float new_w = w + (P->damp_by_importance ? (-effective_lr * grad) / (std::sqrt(imp) + eps)
+                                                                   : (-effective_lr * grad));
+                    val[vb] = uint8_t((fp4_enc(new_w / combined_scale) << 4) | fp4_enc(imp / combined_imp_scale));
+                    sg[size_t(r)] += static_cast<double>(w_stored) * static_cast<double>(out_scale) * (dy_val * in_val);
+                    sgc[size_t(r)] += static_cast<double>(w_stored) * static_cast<double>(out_scale) *
+                                      static_cast<double>(contrib);
+                }
+            }
+            dx[b * n_in + r] += dx_accum;
+        }
+    }
+    if (lr != 0.0f) {
+        // value_scale[r] and its second moment by the row index, the step
+        // counter by (r, 0) (sisldo_ops.hpp:820-846)
+        for (int64_t r = 0; r < n_in; ++r) {
+            if (sg[size_t(r)] == 0.0 && sgc[size_t(r)] == 0.0) continue;
+            const uint64_t nnz_row = L->row_elem_start[r + 1] - L->row_elem_start[r];
+            if (nnz_row == 0) continue;
+            const float scale_eff_lr = lr / static_cast<float>(nnz_row);
+            const float g_agg = static_cast<float>(sg[size_t(r)]);
+            const float contrib_agg = static_cast<float>(sgc[size_t(r)]);
+            float &vs_imp = S->vs_importance[r];
+            const float new_vs_imp = beta2 * vs_imp + (1.0f - beta2) * (g_agg * g_agg + contrib_agg * contrib_agg);
+            uint32_t &step = S->vs_step[r * rank];
+            ++step;
+            const float bias_correction = 1.0f - std::pow(beta2, static_cast<float>(step));
+            const float vs_imp_hat = bias_correction > 0.0f ? new_vs_imp / bias_correction : new_vs_imp;
+            vs_imp = new_vs_imp;
+            vs[r] -= scale_eff_lr * g_agg / (std::sqrt(vs_imp_hat) + eps);
+        }
+    }
+    return 0;
+}
+
 }  // extern "C"

@@ -149,6 +149,19 @@ int oracle_backward_train(const OracleLayer *L, uint8_t *val, OracleTrainState *
                           const float *x, const float *dy, int64_t batch, float *dx,
                           float *acc_in, float *acc_grad, const OracleTrainParams *P);
 
+/* backward_sparse with the optimizer update (sisldo_ops.hpp:589-848, the
+ * scattered store; sili/cpu_backend.cpp:587-603): batch rows outer, each
+ * synapse with a dy entry in that batch row re-quantized after every step
+ * (deterministic rounding, ValueAccessor::set), value_scale stepped once per
+ * row after all batch rows.  Output scales, the step variant of the layer
+ * class and the importance running stats are not involved.  One thread.
+ * dy: CSR with strictly increasing indices per batch row.  S: value_scale,
+ * vs_importance, vs_step, output_scale, importance scales read/updated (the
+ * rest unused).  Returns -1 on a layer with block4 tiles. */
+int oracle_backward_sparse_train(const OracleLayer *L, uint8_t *val, OracleTrainState *S, const float *x,
+                                 const int32_t *dptrs, const int32_t *didx, const float *dvals, int64_t batch,
+                                 float *dx, float *acc_in, float *acc_grad, const OracleTrainParams *P);
+
 /* ---- bulk synaptogenesis step (magnitude prune + candidate regrow) ----
  * Output capacities: scattered entries <= nnz + n_cand + 16*n_tiles,
  * tiles <= n_tiles + n_cand.  Outputs are absolute: out_ptrs[n_in+1],

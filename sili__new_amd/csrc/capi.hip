@@ -482,6 +482,40 @@ void backward_sparse(Layer &L, const float *x, const int32_t *dptrs, const int32
         launch_gather_b4(L.B4.plan(), canon_scales(L), L.ws_gT.p, B, dx, L.n_in, B, SKIP_ZERO, st);
 }
 
+// backward_sparse with the optimizer update (sili/cpu_backend.cpp:587-603,
+// sisldo_ops.hpp:589-848) on a layer without block4 tiles.
+void backward_sparse_train(Layer &L, const float *x, const int32_t *dptrs, const int32_t *didx,
+                           const float *dvals, int64_t nnz_dy, int64_t B, float *dx, const TrainParams &p,
+                           hipStream_t st) {
+    ProfCtx pc(L, "bwd_sparse");
+    if (B <= 0) throw_error(SILI_ERR_INVALID, "backward_sparse: batch must be >= 1");
+    if (!x || !dptrs || !dx) throw_error(SILI_ERR_INVALID, "backward_sparse: NULL buffer");
+    if (B > TRAIN_MAX_BATCH)
+        throw_error(SILI_ERR_INVALID, "backward_sparse with learning_rate != 0: batch must be <= 1024");
+    if (L.B4.ntiles > 0)
+        throw_error(SILI_ERR_INVALID, "backward_sparse with learning_rate != 0: layers holding block4 tiles are "
+                                      "not supported on the GPU path yet");
+    const float *xT = to_feature_major(L, L.ws_xT, x, B, L.n_in, nullptr, st);
+    L.xT_cached_batch = 0;
+    launch_rowabs(xT, B, L.n_in, L.acc_in.p, st);
+    L.ws_gT.ensure((size_t)(L.n_out * B));
+    fill(L.ws_gT.p, L.n_out * B, 0.0f, st);
+    // entries present in dy carry nonzero bits (explicit zeros as -0.0)
+    launch_densify(dptrs, didx, dvals, B, L.n_out, L.ws_gT.p, L.acc_grad.p, true, nnz_dy, st);
+    ensure_train_state(L, st);
+    ensure_pow_table(L, p.beta2, L.train_calls + 2, st);
+    ensure_shadow_perm(L);
+    launch_sparse_train(L, xT, L.ws_gT.p, B, dx, p, st);
+    launch_shadow_val_refresh(L, st);
+    for (DScatter *sc : {&L.W, &L.Wt}) {
+        sc->stream1.valid = sc->streamK.valid = false;
+        sc->cblk.clear();
+        sc->cblk_cb = 0;
+    }
+    L.vs_ones = false;
+    ++L.train_calls;
+}
+
 void export_block4_coords(Layer &L, std::vector<uint32_t> &br, std::vector<uint32_t> &bc) {
     const int64_t n = L.B4.ntiles;
     br.assign((size_t)n, 0);
@@ -834,12 +868,36 @@ int sili_backward_sparse(sili_layer *layer, const float *x, const int32_t *dy_pt
                          void *stream) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
-        if (learning_rate != 0.0f)
-            throw_error(SILI_ERR_INVALID, "backward_sparse: only learning_rate == 0 is implemented on the GPU path");
         if (nnz_dy < 0 || (nnz_dy > 0 && (!dy_indices || !dy_values)))
             throw_error(SILI_ERR_INVALID, "backward_sparse: bad CSR arguments");
         set_device(layer->L);
+        if (learning_rate != 0.0f) {
+            // the reference binding's defaults (sili/cpu_backend.cpp:587-591)
+            const TrainParams p{learning_rate, 0, 1, 0.999f, 1e-8f, 0.9f, 0.0f, 2.0f, 100.0f, 0.1f};
+            backward_sparse_train(layer->L, x, dy_ptrs, dy_indices, dy_values, nnz_dy, batch, dx, p,
+                                  pick(layer->L, stream));
+            return;
+        }
         backward_sparse(layer->L, x, dy_ptrs, dy_indices, dy_values, nnz_dy, batch, dx, pick(layer->L, stream));
+    });
+}
+
+int sili_backward_sparse_train(sili_layer *layer, const float *x, const int32_t *dy_ptrs, const int32_t *dy_indices,
+                               const float *dy_values, int64_t nnz_dy, int64_t batch, float *dx, float learning_rate,
+                               int lr_per_row_nnz, int damp_by_importance, float beta2, float eps, void *stream) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        if (nnz_dy < 0 || (nnz_dy > 0 && (!dy_indices || !dy_values)))
+            throw_error(SILI_ERR_INVALID, "backward_sparse: bad CSR arguments");
+        set_device(layer->L);
+        hipStream_t st = pick(layer->L, stream);
+        if (learning_rate == 0.0f) {
+            backward_sparse(layer->L, x, dy_ptrs, dy_indices, dy_values, nnz_dy, batch, dx, st);
+            return;
+        }
+        const TrainParams p{learning_rate, lr_per_row_nnz ? 1 : 0, damp_by_importance ? 1 : 0, beta2, eps,
+                            0.9f, 0.0f, 2.0f, 100.0f, 0.1f};
+        backward_sparse_train(layer->L, x, dy_ptrs, dy_indices, dy_values, nnz_dy, batch, dx, p, st);
     });
 }
 

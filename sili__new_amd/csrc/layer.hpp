@@ -187,6 +187,7 @@ struct Layer {
     DevBuf<double> dead_S;
     DevBuf<float> def_w, def_i;   // DeferredScaleWrite: true-units (cw, ci) per synapse
     DevBuf<float> vs_snap;        // value scales as the update's rows read them
+    DevBuf<double> train_rowsum;  // backward_sparse update: per-row value-scale gradient sums
     int update_variant = UPDATE_PLAIN;
     bool stochastic_rounding = true;
     uint64_t rng_seed = 0x5EEDull, rng_calls = 0;
@@ -270,6 +271,10 @@ void launch_shadow_val_refresh(Layer &L, hipStream_t st);
 // DeferredScaleWrite: the value bytes under the final scales (after the
 // scale steps; same seed as launch_train_rows).
 void launch_train_store(Layer &L, uint64_t seed, hipStream_t st);
+// backward_sparse's update of the canonical store, dx and the value scales;
+// gT dense feature-major with the sparse dy's entries marked (nonzero bits).
+void launch_sparse_train(Layer &L, const float *xT, const float *gT, int64_t B, float *dx, const TrainParams &p,
+                         hipStream_t st);
 
 // ---- seeded synthetic layers (gen.hip) ----------------------------------------
 // Rebuilds the scattered store (and its shadow) from the seeded generator and

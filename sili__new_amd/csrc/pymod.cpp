@@ -263,11 +263,15 @@ class Layer {
             apply_seed();
             ck(sili_backward_dense_train(L_, (const float *)last_x_.p, ddy, B, ddx, learning_rate,
                                          lr_per_row_nnz ? 1 : 0, damp_by_importance ? 1 : 0, beta2, eps, nullptr));
-            // the update moved the scales: refresh the host mirrors
-            ck(sili_get_value_scale(L_, vs_.data()));
-            ck(sili_get_output_scale(L_, os_.data()));
+            refresh_scale_mirrors();
         }
         return fetch(ddx, B, n_in_);
+    }
+
+    // an update moved the scales: refresh the host mirrors
+    void refresh_scale_mirrors() {
+        ck(sili_get_value_scale(L_, vs_.data()));
+        ck(sili_get_output_scale(L_, os_.data()));
     }
 
     // The scales' optimizer state (delta_csr_types.hpp:1127-1215).
@@ -339,7 +343,6 @@ class Layer {
     py::array_t<float> backward_sparse(carr<float> x, carr<int32_t> dptrs, carr<int32_t> didx, carr<float> dvals,
                                        int64_t batch, float learning_rate, bool lr_per_row_nnz,
                                        bool damp_by_importance, float beta2, float eps) {
-        (void)lr_per_row_nnz; (void)damp_by_importance; (void)beta2; (void)eps;
         flush();
         if (x.size() != batch * n_in_) throw py::value_error("x must be [batch, n_inputs]");
         check_csr(dptrs, didx, dvals, batch, n_out_);
@@ -349,7 +352,9 @@ class Layer {
         int32_t *di = upload_i32(i_, didx);
         float *dv = upload_f32(v_, dvals);
         float *ddx = (float *)dx_.get((size_t)(batch * n_in_) * 4);
-        ck(sili_backward_sparse(L_, dxin, dp, di, dv, (int64_t)didx.size(), batch, ddx, learning_rate, nullptr));
+        ck(sili_backward_sparse_train(L_, dxin, dp, di, dv, (int64_t)didx.size(), batch, ddx, learning_rate,
+                                      lr_per_row_nnz ? 1 : 0, damp_by_importance ? 1 : 0, beta2, eps, nullptr));
+        if (learning_rate != 0.0f) refresh_scale_mirrors();
         return fetch(ddx, batch, n_in_);
     }
 

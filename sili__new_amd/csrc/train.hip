@@ -326,6 +326,132 @@ __global__ __launch_bounds__(256) void k_train_store(TrainArgs a) {
     }
 }
 
+// ---- backward_sparse with the optimizer update ------------------------------------
+struct SparseTrainArgs {
+    const uint32_t *byte_start, *elem_start;  // canonical store
+    const uint8_t *idx;
+    uint8_t *val;
+    int64_t n_in, B;
+    const float *xT;         // [n_in][B]
+    const float *gT;         // [n_out][B], +0.0 where dy has no entry, explicit entries nonzero bits
+    float *dx;               // [B][n_in], overwritten
+    const float *vs, *os;    // [n*rank]; component 0 is read
+    const float *is, *ois;   // importance scales (NULL: ones)
+    double *rowsum;          // [n_in][2]: the row's value-scale gradient sums
+    int rank;
+    float lr, beta2, eps;
+    int lr_per_row_nnz, damp;
+};
+
+// One wave per canonical row (sisldo_ops.hpp:637-729): each lane owns one
+// synapse and takes the batch rows in order; at every batch row whose dy
+// holds the synapse's column, the weight and importance are stepped in true
+// units and stored back (round to nearest), so the next batch row reads the
+// re-quantized code.  No bound on the importance EMA or the step.
+__global__ __launch_bounds__(256) void k_sparse_train_rows(SparseTrainArgs a) {
+    __shared__ double s_part[WAVES_T][64][2];
+    __shared__ float s_dx[WAVES_T][TRAIN_MAX_BATCH];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t r = (int64_t)blockIdx.x * WAVES_T + wave;
+    if (r >= a.n_in) return;
+    const uint32_t e0 = a.elem_start[r], e1 = a.elem_start[r + 1];
+    const int64_t B = a.B;
+    if (e1 == e0) {
+        for (int64_t b = lane; b < B; b += 64) a.dx[b * a.n_in + r] = 0.0f;
+        if (lane == 0u) a.rowsum[2 * r] = a.rowsum[2 * r + 1] = 0.0;
+        return;
+    }
+    float *rdx = s_dx[wave];
+    for (int64_t b = lane; b < B; b += 64) rdx[b] = 0.0f;
+    wave_lds_sync();
+    const float eff_lr = a.lr_per_row_nnz ? a.lr / (float)(e1 - e0) : a.lr;
+    const float imp_scale = a.is ? a.is[r] : 1.0f;
+    const float val_scale = a.vs[r * a.rank];
+    const float *xrow = a.xT + r * B;
+    double sg = 0.0, sgc = 0.0;
+    uint32_t pos = a.byte_start[r], carry = 0, ebase = e0;
+    const uint32_t end = a.byte_start[r + 1];
+    while (pos < end) {
+        const Chunk ch = decode_chunk(a.idx, pos, end, carry);
+        if (ch.T == 0ull) break;
+        const bool has = ch.term;
+        const uint32_t col = has ? ch.col : 0u;
+        const uint32_t vb = ebase + ch.rank;
+        uint32_t byte = has ? (uint32_t)a.val[vb] : 0u;
+        const float out_scale = has ? a.os[(int64_t)col * a.rank] : 0.0f;
+        const float combined_scale = val_scale * out_scale;
+        const float out_imp_scale = (a.ois && has) ? a.ois[col] : 1.0f;
+        const float combined_imp_scale = imp_scale * out_imp_scale;
+        double psg = 0.0, psgc = 0.0;
+        const float *grow = a.gT + (int64_t)col * B;
+        for (int64_t b = 0; b < B; ++b) {
+            const float dyv = has ? grow[b] : 0.0f;
+            const bool present = __builtin_bit_cast(uint32_t, dyv) != 0u;
+            float t = 0.0f;
+            if (present) {
+                const float iv = xrow[b];
+                const float w_stored = fp4_decode(byte >> 4);
+                const float w = w_stored * combined_scale;
+                t = w * dyv;
+                const float grad = dyv * iv;
+                float imp = fp4_decode(byte & 0xFu) * combined_imp_scale;
+                const float contrib = iv * w;
+                imp = a.beta2 * imp + (1.0f - a.beta2) * (grad * grad + contrib * contrib);
+                const float new_w = w + (a.damp ? (-eff_lr * grad) / (__builtin_sqrtf(imp) + a.eps) : (-eff_lr * grad));
+                byte = (fp4_encode(new_w / combined_scale) << 4) | fp4_encode(imp / combined_imp_scale);
+                psg = psg + ((double)w_stored * (double)out_scale) * (double)grad;
+                psgc = psgc + ((double)w_stored * (double)out_scale) * (double)contrib;
+            }
+            const float tot = wave_sum(t);
+            if (lane == 0u) rdx[b] = rdx[b] + tot;
+        }
+        if (has) a.val[vb] = (uint8_t)byte;
+        s_part[wave][lane][0] = has ? psg : 0.0;
+        s_part[wave][lane][1] = has ? psgc : 0.0;
+        wave_lds_sync();
+        if (lane == 0u) {
+            uint64_t T = ch.T;
+            while (T) {
+                const uint32_t l = (uint32_t)__builtin_ctzll(T);
+                T &= T - 1ull;
+                sg = sg + s_part[wave][l][0];
+                sgc = sgc + s_part[wave][l][1];
+            }
+        }
+        wave_lds_sync();
+        carry = chunk_advance(ch, pos, ebase);
+    }
+    wave_lds_sync();
+    for (int64_t b = lane; b < B; b += 64) a.dx[b * a.n_in + r] = rdx[b];
+    if (lane == 0u) {
+        a.rowsum[2 * r] = sg;
+        a.rowsum[2 * r + 1] = sgc;
+    }
+}
+
+// value_scale's step after all batch rows (sisldo_ops.hpp:820-846): slot r of
+// the scale and its second moment, step counter (r, 0), no finiteness guard.
+__global__ __launch_bounds__(256) void k_sparse_train_vs(const uint32_t *__restrict__ elem_start, int64_t n_in,
+                                                         int rank, const double *__restrict__ rowsum, float *vs,
+                                                         float *vs_imp, uint32_t *vs_step, float lr, float beta2,
+                                                         float eps, const float *__restrict__ pow_tab) {
+    const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (r >= n_in) return;
+    const double s = rowsum[2 * r], sc = rowsum[2 * r + 1];
+    if (s == 0.0 && sc == 0.0) return;
+    const uint32_t nnz = elem_start[r + 1] - elem_start[r];
+    if (nnz == 0) return;
+    const float scale_eff_lr = lr / (float)nnz;
+    const float g_agg = (float)s, contrib_agg = (float)sc;
+    const float new_vs_imp = beta2 * vs_imp[r] + (1.0f - beta2) * (g_agg * g_agg + contrib_agg * contrib_agg);
+    const uint32_t step = vs_step[r * rank] + 1u;
+    vs_step[r * rank] = step;
+    const float bias_correction = 1.0f - pow_tab[step];
+    const float vs_imp_hat = bias_correction > 0.0f ? new_vs_imp / bias_correction : new_vs_imp;
+    vs_imp[r] = new_vs_imp;
+    vs[r] = vs[r] - scale_eff_lr * g_agg / (__builtin_sqrtf(vs_imp_hat) + eps);
+}
+
 // dead_S[b*rank + k] = sum_col os_k(col) * dy[b][col] in fp64
 // (linear_disldo.hpp:1995-2007): one block per (b, k).
 __global__ __launch_bounds__(256) void k_dead_S(const float *__restrict__ os, const float *__restrict__ gT,
@@ -475,6 +601,38 @@ void launch_train_rows(Layer &L, const float *xT, const float *gT, int64_t B, fl
         case 3: launch(k_train_rows<3>, grid, block, 0, st, a); break;
         default: launch(k_train_rows<4>, grid, block, 0, st, a); break;
     }
+    SILI_HIP(hipGetLastError());
+}
+
+void launch_sparse_train(Layer &L, const float *xT, const float *gT, int64_t B, float *dx, const TrainParams &p,
+                         hipStream_t st) {
+    L.train_rowsum.ensure((size_t)(2 * L.n_in));
+    SparseTrainArgs a{};
+    a.byte_start = L.W.byte_start.p;
+    a.elem_start = L.W.elem_start.p;
+    a.idx = L.W.idx.p;
+    a.val = L.W.val.p;
+    a.n_in = L.n_in;
+    a.B = B;
+    a.xT = xT;
+    a.gT = gT;
+    a.dx = dx;
+    a.vs = L.vs.p;
+    a.os = L.os.p;
+    a.is = L.is.p;
+    a.ois = L.ois.p;
+    a.rowsum = L.train_rowsum.p;
+    a.rank = L.rank;
+    a.lr = p.lr;
+    a.beta2 = p.beta2;
+    a.eps = p.eps;
+    a.lr_per_row_nnz = p.lr_per_row_nnz;
+    a.damp = p.damp_by_importance;
+    ProfScope ps("sparse_train_rows", st);
+    launch(k_sparse_train_rows, dim3((unsigned)((L.n_in + WAVES_T - 1) / WAVES_T)), dim3(256), 0, st, a);
+    launch(k_sparse_train_vs, dim3(nblk(L.n_in)), dim3(TPB), 0, st, (const uint32_t *)L.W.elem_start.p, L.n_in,
+           L.rank, (const double *)L.train_rowsum.p, L.vs.p, L.vs_imp.p, L.vs_step.p, p.lr, p.beta2, p.eps,
+           (const float *)L.pow_tab.p);
     SILI_HIP(hipGetLastError());
 }
 

@@ -175,3 +175,51 @@ def test_update_rejects_block4_and_oversize_batch(hip):
     L2.forward_dense(xb)
     with pytest.raises(ValueError):
         L2.backward_dense(np.ones((1025, 16), np.float32), 0.05)
+
+
+@pytest.mark.parametrize("case", range(len(TRAIN_CASES)))
+def test_sparse_update_matches_oracle(hip, case):
+    """backward_sparse with the update (sisldo_ops.hpp:589-848) against the
+    IEEE restatement: value bytes exact (round to nearest whatever the layer's
+    rounding setting: the default, stochastic class is used), value scales and
+    their state exact at batch 1, dx within the bar; the forward afterwards
+    reads the refreshed shadow."""
+    from train_util import dx_bound_sparse, sparse_dy
+    n_in, n_out, dens, seed, B, lr, opts = TRAIN_CASES[case]
+    lopts, copts = split_opts(opts)
+    c = make_train_case(n_in, n_out, dens, seed, **lopts)
+    H, L = host_layer(c), gpu_layer(hip, c, deterministic=False)
+    rng = c["rng"]
+    for step in range(3):
+        what = f"case {case} step {step}"
+        x = rng.normal(size=(B, n_in)).astype(np.float32)
+        dp, di, dv, dense = sparse_dy(rng, B, n_out)
+        bound = dx_bound_sparse(H, dense, lr)
+        dxg = L.backward_sparse(x, dp, di, dv, B, lr, **copts)
+        dxh, _, _ = H.backward_sparse_train(x, dp, di, dv, B, lr, **copts)
+        assert np.array_equal(L.export_scattered()["val"], H.val[:H.nnz]), what + ": value bytes"
+        assert_close_terms(dxg, dxh, bound, what + ": dx")
+        vs = L.get_value_scales()
+        st = L.get_scale_state()
+        if B == 1:
+            assert np.array_equal(vs, H.value_scale), what + ": value_scale"
+            assert np.array_equal(st["vs_importance"], H.vs_importance), what + ": vs_importance"
+        else:
+            np.testing.assert_allclose(vs, H.value_scale, rtol=1e-6, atol=0, err_msg=what)
+            np.testing.assert_allclose(st["vs_importance"], H.vs_importance, rtol=1e-5, atol=0, err_msg=what)
+        assert np.array_equal(st["vs_step"], H.vs_step), what + ": vs_step"
+        x2 = rng.normal(size=(2, n_in)).astype(np.float32)
+        assert_close_terms(L.forward_dense(x2), H.forward_dense(x2), H.forward_dense(x2, absmode=True),
+                           what + ": forward after update")
+
+
+def test_sparse_update_default_learning_rate(hip):
+    """backward_sparse's default learning_rate is 0.01 (sili/cpu_backend.cpp:590)."""
+    from train_util import sparse_dy
+    c = make_train_case(80, 60, 0.2, 12)
+    H, L = host_layer(c), gpu_layer(hip, c)
+    x = c["rng"].normal(size=(4, 80)).astype(np.float32)
+    dp, di, dv, _ = sparse_dy(c["rng"], 4, 60)
+    L.backward_sparse(x, dp, di, dv, 4)
+    H.backward_sparse_train(x, dp, di, dv, 4, 0.01)
+    assert np.array_equal(L.export_scattered()["val"], H.val[:H.nnz])

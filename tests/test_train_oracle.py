@@ -90,3 +90,37 @@ def test_learning_rate_zero_is_plain_backward():
     assert np.array_equal(H.val, val0) and np.array_equal(H.value_scale, vs0)
     assert np.array_equal(H.vs_step, np.zeros_like(H.vs_step))
     np.testing.assert_allclose(dx, dx0, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("contracted", [True, False])
+@pytest.mark.parametrize("case", range(len(TRAIN_CASES)))
+def test_backward_sparse_train_matches_reference(case, contracted):
+    """backward_sparse with the update (sisldo_ops.hpp:589-848): codes and the
+    value scales' state exact (both builds); dx exact for the build compiled
+    like the reference, within the fp32 bar for the IEEE one."""
+    from train_util import dx_bound_sparse, sparse_dy
+    n_in, n_out, dens, seed, B, lr, opts = TRAIN_CASES[case]
+    lopts, copts = split_opts(opts)
+    c = make_train_case(n_in, n_out, dens, seed, **lopts)
+    H, R = host_layer(c), ref_layer(c)
+    rng = c["rng"]
+    for step in range(3):
+        what = f"case {case} step {step}"
+        x = rng.normal(size=(B, n_in)).astype(np.float32)
+        dp, di, dv, dense = sparse_dy(rng, B, n_out)
+        bound = dx_bound_sparse(H, dense, lr)
+        dxh, aih, agh = H.backward_sparse_train(x, dp, di, dv, B, lr, contracted=contracted, **copts)
+        dxr, air, agr = R.backward_sparse_train(x, dp, di, dv, B, lr, **copts)
+        _, _, _, vr = R.export()
+        st = R.get_train_state(c["rank"])
+        assert np.array_equal(H.val[:len(vr)], vr), what + ": codes"
+        if contracted:
+            assert np.array_equal(dxh, dxr), what + ": dx"
+        else:
+            assert_close_terms(dxh, dxr, bound, what + ": dx")
+        assert np.array_equal(aih, air) and np.array_equal(agh, agr)
+        for k in ("value_scale", "vs_importance", "vs_step"):
+            if contracted:
+                assert np.array_equal(getattr(H, k), st[k]), what + ": " + k
+            else:
+                np.testing.assert_allclose(getattr(H, k), st[k], rtol=1e-5, atol=1e-30, err_msg=what + ": " + k)

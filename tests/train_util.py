@@ -95,3 +95,41 @@ def dx_bound(H, dy, lr, max_abs_delta=2.0):
     T = np.zeros((H.n_in, B))
     np.add.at(T, rows, (np.abs(dy[:, cols].astype(np.float64)) * mag).T)
     return T.T
+
+
+def sparse_dy(rng, B, n_out, density=0.3):
+    """A sparse dy CSR (strictly increasing indices per batch row), with some
+    explicit zeros and an empty batch row when B > 2; also its dense form."""
+    ptrs, idx, vals = [0], [], []
+    for b in range(B):
+        if B > 2 and b == 1:
+            ptrs.append(len(idx))
+            continue
+        cols = np.flatnonzero(rng.random(n_out) < density)
+        v = rng.normal(size=len(cols)).astype(np.float32)
+        v[rng.random(len(cols)) < 0.05] = 0.0
+        idx.extend(cols.tolist())
+        vals.extend(v.tolist())
+        ptrs.append(len(idx))
+    ptrs, idx, vals = np.array(ptrs, np.int32), np.array(idx, np.int32), np.array(vals, np.float32)
+    dense = np.zeros((B, n_out), np.float32)
+    for b in range(B):
+        dense[b, idx[ptrs[b]:ptrs[b + 1]]] = vals[ptrs[b]:ptrs[b + 1]]
+    return ptrs, idx, vals, dense
+
+
+def dx_bound_sparse(H, dy_dense, lr, max_step=None):
+    """sum over a row's synapses of |w| * |dy|, |w| bounded over the call.
+    Each step moves a weight by |-lr * g| / (sqrt(imp) + eps) and re-quantizes,
+    so the bound takes the largest code (6) for every synapse: coarse but safe."""
+    from sili__new_amd.codec import fp4_decode_np  # noqa: F401
+    dy = np.atleast_2d(dy_dense)
+    B = dy.shape[0]
+    cols = H.decode_cols()
+    rows = np.repeat(np.arange(H.n_in), np.diff(H.row_elem_start.astype(np.int64)))
+    vs = H.value_scale.reshape(H.n_in, H.rank)[:, 0].astype(np.float64)
+    os_ = H.output_scale.reshape(H.n_out, H.rank)[:, 0].astype(np.float64)
+    mag = 6.0 * np.abs(vs[rows] * os_[cols])
+    T = np.zeros((H.n_in, B))
+    np.add.at(T, rows, (np.abs(dy[:, cols].astype(np.float64)) * mag).T)
+    return T.T
