@@ -598,6 +598,11 @@ def main():
     def step(i):
         run(pool[i % copies])
 
+    # set-up: each copy's first call sizes its workspaces (and, with the
+    # optimizer update, allocates its optimizer state); then W warmup steps
+    for d in pool:
+        run(d)
+    rt.sync()
     for i in range(a.warmup):
         step(i)
     rt.sync()
@@ -668,8 +673,16 @@ def main():
         roof = {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 2) if achieved else None,
                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 5) if achieved else None,
-                "traffic": measured_traffic(dom_name, cfg), "avg_op_ms": round(dom_avg_ms, 5),
+                "traffic": None if train_lr else measured_traffic(dom_name, cfg), "avg_op_ms": round(dom_avg_ms, 5),
                 "launches_per_op": launches, "algorithmic_bytes": dom_bytes}
+        if dom_name == "bwd:train_rows":
+            # one synapse's batch steps are a dependent chain of ~80 VALU
+            # instructions each (correctly rounded sqrt and division, clamps,
+            # fp64 gradient terms): the kernel is bound by instruction issue
+            steps = nnz_s * B
+            roof["synapse_steps_per_s"] = round(steps / (dom_avg_ms * 1e-3), 1)
+            roof["note"] = ("k_train_rows is bound by VALU issue (~80 instructions per synapse per batch step, "
+                            "4 cycles per 64-lane instruction per SIMD), not by HBM")
         if cfg == 0:
             step_bytes = alg["fwd:gather"]
             flops = 2 * units * B

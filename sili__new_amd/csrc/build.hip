@@ -77,7 +77,8 @@ __device__ __forceinline__ uint32_t seg_count(uint32_t n, uint64_t last_start_re
 __global__ void k_row_starts(const uint32_t *__restrict__ ptrs, int64_t rows, int64_t N,
                              const uint64_t *__restrict__ pos, uint64_t total,
                              uint32_t *__restrict__ byte_start, uint32_t *__restrict__ elem_start,
-                             uint32_t seg_bytes, int emit_empty, uint32_t *__restrict__ segcnt) {
+                             uint32_t seg_bytes, int emit_empty, uint32_t *__restrict__ segcnt,
+                             uint32_t *__restrict__ n_empty) {
     const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (r > rows) return;
     const uint32_t e = ptrs[r];
@@ -86,6 +87,7 @@ __global__ void k_row_starts(const uint32_t *__restrict__ ptrs, int64_t rows, in
     if (r < rows) {
         const uint32_t e1 = ptrs[r + 1], n = e1 - e;
         segcnt[r] = seg_count(n, n ? pos[e1 - 1] - pos[e] : 0u, seg_bytes - 4u, emit_empty);
+        if (n == 0u) atomicAdd(n_empty, 1u);
     }
 }
 
@@ -224,6 +226,7 @@ struct Encoded {
     int64_t nbytes = 0, nseg = 0;
     bool has_split = false;
     int64_t n_split = 0;
+    int64_t n_empty_rows = 0;
 };
 
 __global__ void k_split_flags(const uint32_t *__restrict__ segcnt, int64_t rows, uint32_t *__restrict__ flag) {
@@ -272,15 +275,20 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
                            pos.p, idx.p);
         SILI_HIP(hipGetLastError());
     }
+    DevBuf<uint32_t> n_empty;
+    n_empty.ensure(1);
+    SILI_HIP(hipMemsetAsync(n_empty.p, 0, sizeof(uint32_t), st));
     launch(k_row_starts, dim3(nblk(rows + 1)), dim3(TPB), 0, st, d_ptrs, rows, N, pos.p,
-                       total, byte_start.p, elem_start.p, seg_len, emit_empty ? 1 : 0, segcnt.p);
+                       total, byte_start.p, elem_start.p, seg_len, emit_empty ? 1 : 0, segcnt.p, n_empty.p);
     SILI_HIP(hipGetLastError());
     SILI_HIP(hipMemsetAsync(segcnt.p + rows, 0, sizeof(uint32_t), st));
     device_exclusive_scan_u32(L, segcnt.p, segoff.p, rows + 1);
-    uint32_t nseg = 0;
+    uint32_t nseg = 0, empty = 0;
     SILI_HIP(hipMemcpyAsync(&nseg, segoff.p + rows, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipMemcpyAsync(&empty, n_empty.p, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
     SILI_HIP(hipStreamSynchronize(st));
     out.nseg = nseg;
+    out.n_empty_rows = empty;
     seg.ensure((size_t)nseg + 1);
     zero_flag(L);
     if (rows > 0) {
@@ -373,6 +381,7 @@ void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64
     dst.nbytes = e.nbytes;
     dst.nseg = e.nseg;
     dst.has_split = e.has_split;
+    dst.n_empty_rows = e.n_empty_rows;
     dst.val.ensure((size_t)N + 64);
     if (N > 0)
         SILI_HIP(hipMemcpyAsync(dst.val.p, d_bytes, (size_t)N, hipMemcpyDeviceToDevice, L.stream));
@@ -420,6 +429,7 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
     dst.nbytes = e.nbytes;
     dst.nseg = e.nseg;
     dst.has_split = e.has_split;
+    dst.n_empty_rows = e.n_empty_rows;
     dst.val.ensure((size_t)N + 64);
     if (N > 0)
         SILI_HIP(hipMemcpyAsync(dst.val.p, tbytes.p, (size_t)N, hipMemcpyDeviceToDevice, st));

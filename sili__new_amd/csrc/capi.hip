@@ -432,7 +432,7 @@ void backward_dense_train(Layer &L, const float *x, const float *dy, int64_t B, 
     if (L.output_scale_trainable) L.mterm.ensure((size_t)(L.W.nnz * 2 * L.rank));
     const uint64_t seed = splitmix64_host(L.rng_seed ^ splitmix64_host(L.rng_calls + 1));
     launch_train_rows(L, xT, gT, B, dx, p, seed, st);
-    launch_train_dead_rows(L, xT, gT, B, p, st);
+    if (L.W.n_empty_rows > 0) launch_train_dead_rows(L, xT, gT, B, p, st);
     const bool scales_step = L.update_variant != UPDATE_NOSCALE;
     if (L.output_scale_trainable && scales_step && L.W.nnz > 0) launch_train_cols(L, p, st);
     launch_train_store(L, seed, st);

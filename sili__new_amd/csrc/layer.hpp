@@ -71,6 +71,7 @@ struct DStream {
 // One orientation of the scattered store.
 struct DScatter {
     int64_t rows = 0, cols = 0, nnz = 0, nbytes = 0, nseg = 0;
+    int64_t n_empty_rows = 0;  // rows holding no synapse
     bool has_split = false;
     DevBuf<uint32_t> byte_start, elem_start;  // rows+1
     DevBuf<uint8_t> idx, val;

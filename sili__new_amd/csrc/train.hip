@@ -117,6 +117,66 @@ __device__ __forceinline__ uint32_t requantize(float w, float imp, bool stochast
     return (wq << 4) | iq;
 }
 
+// Runs t = step(b, x[b], gcol[b]) for b = 0..B-1 in order and adds the sum
+// of t over the wave's lanes into rdx[b].  gcol: one lane's column slice of
+// the feature-major gradient (lanes read different columns).  With
+// B % 4 == 0 the slice is read 8 batch steps at a time as two 16-byte loads,
+// the next group's loads issued before the current group's steps, and the 8
+// steps' t are summed over the lanes together: each lane writes its 8 to
+// sred (512 floats of LDS per wave), each lane then adds one step's values
+// of 8 lanes (read in a rotated order so that the wave's 64 reads hit 64
+// different banks), and three exchanges combine the 8 groups.
+template <typename Step>
+__device__ __forceinline__ void batch_steps(const float *__restrict__ gcol, int64_t B, const float *sx, float *rdx,
+                                            float *sred, Step &step) {
+    const uint32_t lane = __lane_id();
+    if ((B & 3) == 0) {
+        const float4 *g4 = reinterpret_cast<const float4 *>(gcol);
+        const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float4 n0 = g4[0];
+        float4 n1 = B > 4 ? g4[1] : z4;
+        const uint32_t j = lane & 7u, grp = lane >> 3;
+        // lanes' 8 terms of batch steps b0..b0+7 summed into rdx[b0..]
+        auto reduce8 = [&](int64_t b0, const float (&t)[8]) {
+            float4 *w4 = reinterpret_cast<float4 *>(sred + lane * 8);
+            w4[0] = make_float4(t[0], t[1], t[2], t[3]);
+            w4[1] = make_float4(t[4], t[5], t[6], t[7]);
+            wave_lds_sync();
+            float sum = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < 8; ++i) sum += sred[(grp * 8u + ((i + grp) & 7u)) * 8u + j];
+            sum += __shfl_xor(sum, 8, 64);
+            sum += __shfl_xor(sum, 16, 64);
+            sum += __shfl_xor(sum, 32, 64);
+            if (lane < 8u && b0 + lane < B) rdx[b0 + lane] += sum;
+            wave_lds_sync();
+        };
+        const int64_t full = B & ~(int64_t)7;
+        for (int64_t b0 = 0; b0 < full; b0 += 8) {
+            const float4 c0 = n0, c1 = n1;
+            if (b0 + 8 < B) n0 = g4[(b0 + 8) >> 2];
+            if (b0 + 12 < B) n1 = g4[(b0 + 12) >> 2];
+            const float d[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            float t[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) t[q] = step(b0 + q, sx[b0 + q], d[q]);
+            reduce8(b0, t);
+        }
+        if (B & 4) {  // last 4 steps (loaded by the last full group, or up front)
+            const float d[4] = {n0.x, n0.y, n0.z, n0.w};
+            float t[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) t[q] = step(full + q, sx[full + q], d[q]);
+            reduce8(full, t);
+        }
+    } else {
+        for (int64_t b = 0; b < B; ++b) {
+            const float tot = wave_sum(step(b, sx[b], gcol[b]));
+            if (lane == 0u) rdx[b] = rdx[b] + tot;
+        }
+    }
+}
+
 struct TrainArgs {
     const uint32_t *byte_start, *elem_start;  // canonical store
     const uint8_t *idx;
@@ -151,10 +211,10 @@ struct TrainArgs {
 //   DeferredScaleWrite: the true-units weight cw = code * vs0 * os0 is
 //     stepped by g; scale gradients weigh by the stored code, component 0
 //     only; (cw, ci) are kept for k_train_store (linear_disldo.hpp:687-790).
-template <int RANK>
+template <int RANK, bool DEFERRED, bool COLS>
 __global__ __launch_bounds__(256) void k_train_rows(TrainArgs a) {
     __shared__ double s_part[WAVES_T][64][2 * RANK];
-    __shared__ float s_dx[WAVES_T][TRAIN_MAX_BATCH];
+    extern __shared__ __attribute__((aligned(16))) float s_dyn[];  // [wave][dx B | x B]
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const int64_t r = (int64_t)blockIdx.x * WAVES_T + wave;
     if (r >= a.n_in) return;
@@ -165,8 +225,14 @@ __global__ __launch_bounds__(256) void k_train_rows(TrainArgs a) {
         for (int64_t b = lane; b < B; b += 64) a.dx[b * a.n_in + r] = 0.0f;
         return;
     }
-    float *rdx = s_dx[wave];
-    for (int64_t b = lane; b < B; b += 64) rdx[b] = 0.0f;
+    float *rdx = s_dyn + (int64_t)wave * (2 * B + 512);
+    float *sx = rdx + B;       // the row's inputs, read by every lane
+    float *sred = sx + B;      // dx reduction staging (batch_steps)
+    const float *xrow = a.xT + r * B;
+    for (int64_t b = lane; b < B; b += 64) {
+        rdx[b] = 0.0f;
+        sx[b] = xrow[b];
+    }
     wave_lds_sync();
     const float eff_lr = a.lr_per_row_nnz ? a.lr / (float)nnz : a.lr;
     const float scale_eff_lr = a.lr / (float)nnz;
@@ -174,12 +240,11 @@ __global__ __launch_bounds__(256) void k_train_rows(TrainArgs a) {
     float vs_k[RANK];
 #pragma unroll
     for (int k = 0; k < RANK; ++k) vs_k[k] = a.vs_read[r * RANK + k];
-    const bool deferred = a.deferred != 0;
-    const int nk = deferred ? 1 : RANK;  // components that take gradient terms
+    constexpr bool deferred = DEFERRED;
+    constexpr int nk = DEFERRED ? 1 : RANK;  // components that take gradient terms
     double sg[RANK], sgc[RANK];
 #pragma unroll
     for (int k = 0; k < RANK; ++k) sg[k] = sgc[k] = 0.0;
-    const float *xrow = a.xT + r * B;
     uint32_t pos = a.byte_start[r], carry = 0, ebase = e0;
     const uint32_t end = a.byte_start[r + 1];
     while (pos < end) {
@@ -212,31 +277,31 @@ __global__ __launch_bounds__(256) void k_train_rows(TrainArgs a) {
             psg[k] = psgc[k] = 0.0;
             pm[k] = pmc[k] = 0.0f;
         }
-        const float *grow = a.gT + (int64_t)col * B;
-        for (int64_t b = 0; b < B; ++b) {
-            const float iv = xrow[b];
-            const float dyv = has ? grow[b] : 0.0f;
+        // one batch step of this lane's synapse (b in order); lanes without
+        // a synapse step zeros (finite throughout) and contribute nothing
+        auto step = [&](int64_t b, float iv, float dy_raw) -> float {
+            const float dyv = has ? dy_raw : 0.0f;
             const float g = dyv * iv;
-            if (has) {
+            {
                 const float contrib = iv * cw_orig;
                 ci = bounded_update_ci(ci, g, contrib, a.beta2, a.min_decay_frac, a.max_ci);
                 wv = wv + bounded_update_cw(g, ci, S_step, eff_lr, a.eps, a.damp != 0, a.max_abs_delta);
                 cw = deferred ? wv : wv * S;
                 const float qf = deferred ? cw_orig : ((wv == 0.0f) ? a.zero_escape_eps : wv);
 #pragma unroll
-                for (int k = 0; k < RANK; ++k) {
-                    if (k >= nk) break;
+                for (int k = 0; k < nk; ++k) {
                     psg[k] = psg[k] + ((double)qf * (double)os_k[k]) * (double)g;
                     psgc[k] = psgc[k] + ((double)qf * (double)os_k[k]) * (double)contrib;
-                    pm[k] = pm[k] + (qf * vs_k[k]) * g;
-                    pmc[k] = pmc[k] + (qf * vs_k[k]) * contrib;
+                    if constexpr (COLS) {
+                        pm[k] = pm[k] + (qf * vs_k[k]) * g;
+                        pmc[k] = pmc[k] + (qf * vs_k[k]) * contrib;
+                    }
                 }
             }
-            // dx[b][row]: this chunk's share, added to the row's running sum
-            const float t = has ? cw * dyv : 0.0f;
-            const float tot = wave_sum(t);
-            if (lane == 0u) rdx[b] = rdx[b] + tot;
-        }
+            // dx[b][row]: this synapse's term
+            return has ? cw * dyv : 0.0f;
+        };
+        batch_steps(a.gT + (int64_t)col * B, B, sx, rdx, sred, step);
         if (has) {
             if (deferred) {
                 a.def_w[vb] = wv;
@@ -244,7 +309,7 @@ __global__ __launch_bounds__(256) void k_train_rows(TrainArgs a) {
             } else {
                 a.val[vb] = (uint8_t)requantize(wv, ci / combined_imp_scale, a.stochastic != 0, a.seed, vb);
             }
-            if (a.mterm) {
+            if constexpr (COLS) {
 #pragma unroll
                 for (int k = 0; k < RANK; ++k) {
                     a.mterm[(int64_t)vb * 2 * RANK + k] = pm[k];
@@ -279,8 +344,7 @@ __global__ __launch_bounds__(256) void k_train_rows(TrainArgs a) {
     // the row's scale step (linear_disldo.hpp:898-925)
     if (lane == 0u && !a.no_scale) {
 #pragma unroll
-        for (int k = 0; k < RANK; ++k) {
-            if (k >= nk) break;
+        for (int k = 0; k < nk; ++k) {
             // DeferredScaleWrite indexes the scale and its second moment by
             // the row alone (slot r: component r % rank of row r / rank once
             // rank > 1) and its step counter by (r, 0)
@@ -350,7 +414,7 @@ struct SparseTrainArgs {
 // re-quantized code.  No bound on the importance EMA or the step.
 __global__ __launch_bounds__(256) void k_sparse_train_rows(SparseTrainArgs a) {
     __shared__ double s_part[WAVES_T][64][2];
-    __shared__ float s_dx[WAVES_T][TRAIN_MAX_BATCH];
+    extern __shared__ __attribute__((aligned(16))) float s_dyn[];  // [wave][dx B | x B]
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const int64_t r = (int64_t)blockIdx.x * WAVES_T + wave;
     if (r >= a.n_in) return;
@@ -361,13 +425,18 @@ __global__ __launch_bounds__(256) void k_sparse_train_rows(SparseTrainArgs a) {
         if (lane == 0u) a.rowsum[2 * r] = a.rowsum[2 * r + 1] = 0.0;
         return;
     }
-    float *rdx = s_dx[wave];
-    for (int64_t b = lane; b < B; b += 64) rdx[b] = 0.0f;
+    float *rdx = s_dyn + (int64_t)wave * (2 * B + 512);
+    float *sx = rdx + B;
+    float *sred = sx + B;
+    const float *xrow = a.xT + r * B;
+    for (int64_t b = lane; b < B; b += 64) {
+        rdx[b] = 0.0f;
+        sx[b] = xrow[b];
+    }
     wave_lds_sync();
     const float eff_lr = a.lr_per_row_nnz ? a.lr / (float)(e1 - e0) : a.lr;
     const float imp_scale = a.is ? a.is[r] : 1.0f;
     const float val_scale = a.vs[r * a.rank];
-    const float *xrow = a.xT + r * B;
     double sg = 0.0, sgc = 0.0;
     uint32_t pos = a.byte_start[r], carry = 0, ebase = e0;
     const uint32_t end = a.byte_start[r + 1];
@@ -383,28 +452,24 @@ __global__ __launch_bounds__(256) void k_sparse_train_rows(SparseTrainArgs a) {
         const float out_imp_scale = (a.ois && has) ? a.ois[col] : 1.0f;
         const float combined_imp_scale = imp_scale * out_imp_scale;
         double psg = 0.0, psgc = 0.0;
-        const float *grow = a.gT + (int64_t)col * B;
-        for (int64_t b = 0; b < B; ++b) {
-            const float dyv = has ? grow[b] : 0.0f;
+        // lanes whose synapse has no dy entry at b compute and discard
+        auto step = [&](int64_t b, float iv, float dy_raw) -> float {
+            const float dyv = has ? dy_raw : 0.0f;
             const bool present = __builtin_bit_cast(uint32_t, dyv) != 0u;
-            float t = 0.0f;
-            if (present) {
-                const float iv = xrow[b];
-                const float w_stored = fp4_decode(byte >> 4);
-                const float w = w_stored * combined_scale;
-                t = w * dyv;
-                const float grad = dyv * iv;
-                float imp = fp4_decode(byte & 0xFu) * combined_imp_scale;
-                const float contrib = iv * w;
-                imp = a.beta2 * imp + (1.0f - a.beta2) * (grad * grad + contrib * contrib);
-                const float new_w = w + (a.damp ? (-eff_lr * grad) / (__builtin_sqrtf(imp) + a.eps) : (-eff_lr * grad));
-                byte = (fp4_encode(new_w / combined_scale) << 4) | fp4_encode(imp / combined_imp_scale);
-                psg = psg + ((double)w_stored * (double)out_scale) * (double)grad;
-                psgc = psgc + ((double)w_stored * (double)out_scale) * (double)contrib;
-            }
-            const float tot = wave_sum(t);
-            if (lane == 0u) rdx[b] = rdx[b] + tot;
-        }
+            const float w_stored = fp4_decode(byte >> 4);
+            const float w = w_stored * combined_scale;
+            const float grad = dyv * iv;
+            float imp = fp4_decode(byte & 0xFu) * combined_imp_scale;
+            const float contrib = iv * w;
+            imp = a.beta2 * imp + (1.0f - a.beta2) * (grad * grad + contrib * contrib);
+            const float new_w = w + (a.damp ? (-eff_lr * grad) / (__builtin_sqrtf(imp) + a.eps) : (-eff_lr * grad));
+            const uint32_t nb = (fp4_encode(new_w / combined_scale) << 4) | fp4_encode(imp / combined_imp_scale);
+            byte = present ? nb : byte;
+            psg = psg + (present ? ((double)w_stored * (double)out_scale) * (double)grad : 0.0);
+            psgc = psgc + (present ? ((double)w_stored * (double)out_scale) * (double)contrib : 0.0);
+            return present ? w * dyv : 0.0f;
+        };
+        batch_steps(a.gT + (int64_t)col * B, B, sx, rdx, sred, step);
         if (has) a.val[vb] = (uint8_t)byte;
         s_part[wave][lane][0] = has ? psg : 0.0;
         s_part[wave][lane][1] = has ? psgc : 0.0;
@@ -544,6 +609,28 @@ __global__ void k_perm_bytes(const uint8_t *__restrict__ src, const uint32_t *__
 
 inline unsigned nblk(int64_t n) { return (unsigned)((n + TPB - 1) / TPB); }
 
+template <int RANK>
+void launch_rows_rank(bool deferred, bool cols, dim3 grid, dim3 block, uint32_t lds, hipStream_t st,
+                      const TrainArgs &a) {
+    if (deferred) {
+        if (cols) launch(k_train_rows<RANK, true, true>, grid, block, lds, st, a);
+        else launch(k_train_rows<RANK, true, false>, grid, block, lds, st, a);
+    } else {
+        if (cols) launch(k_train_rows<RANK, false, true>, grid, block, lds, st, a);
+        else launch(k_train_rows<RANK, false, false>, grid, block, lds, st, a);
+    }
+}
+
+void launch_rows_kernel(int rank, bool deferred, bool cols, dim3 grid, dim3 block, uint32_t lds, hipStream_t st,
+                        const TrainArgs &a) {
+    switch (rank) {
+        case 1: launch_rows_rank<1>(deferred, cols, grid, block, lds, st, a); break;
+        case 2: launch_rows_rank<2>(deferred, cols, grid, block, lds, st, a); break;
+        case 3: launch_rows_rank<3>(deferred, cols, grid, block, lds, st, a); break;
+        default: launch_rows_rank<4>(deferred, cols, grid, block, lds, st, a); break;
+    }
+}
+
 }  // namespace
 
 void launch_train_rows(Layer &L, const float *xT, const float *gT, int64_t B, float *dx, const TrainParams &p,
@@ -594,13 +681,9 @@ void launch_train_rows(Layer &L, const float *xT, const float *gT, int64_t B, fl
     a.stochastic = L.stochastic_rounding ? 1 : 0;
     a.seed = seed;
     const dim3 grid((unsigned)((L.n_in + WAVES_T - 1) / WAVES_T)), block(256);
+    const uint32_t lds = (uint32_t)(WAVES_T * (2 * B + 512) * sizeof(float));
     ProfScope ps("train_rows", st);
-    switch (L.rank) {
-        case 1: launch(k_train_rows<1>, grid, block, 0, st, a); break;
-        case 2: launch(k_train_rows<2>, grid, block, 0, st, a); break;
-        case 3: launch(k_train_rows<3>, grid, block, 0, st, a); break;
-        default: launch(k_train_rows<4>, grid, block, 0, st, a); break;
-    }
+    launch_rows_kernel(L.rank, a.deferred != 0, a.mterm != nullptr, grid, block, lds, st, a);
     SILI_HIP(hipGetLastError());
 }
 
@@ -629,7 +712,8 @@ void launch_sparse_train(Layer &L, const float *xT, const float *gT, int64_t B, 
     a.lr_per_row_nnz = p.lr_per_row_nnz;
     a.damp = p.damp_by_importance;
     ProfScope ps("sparse_train_rows", st);
-    launch(k_sparse_train_rows, dim3((unsigned)((L.n_in + WAVES_T - 1) / WAVES_T)), dim3(256), 0, st, a);
+    launch(k_sparse_train_rows, dim3((unsigned)((L.n_in + WAVES_T - 1) / WAVES_T)), dim3(256),
+           (uint32_t)(WAVES_T * (2 * B + 512) * sizeof(float)), st, a);
     launch(k_sparse_train_vs, dim3(nblk(L.n_in)), dim3(TPB), 0, st, (const uint32_t *)L.W.elem_start.p, L.n_in,
            L.rank, (const double *)L.train_rowsum.p, L.vs.p, L.vs_imp.p, L.vs_step.p, p.lr, p.beta2, p.eps,
            (const float *)L.pow_tab.p);

@@ -9,6 +9,9 @@ def make_train_case(n_in, n_out, density, seed, rank=1, empty_rows=0, os_trainab
     value scales (and, when asked, trainable output scales and importance
     scales); rows [0, empty_rows) hold no synapse."""
     rng = np.random.default_rng(seed)
+    # rank > 1 sets output-scale components, which marks the output scales
+    # trainable (set_output_scale_raw_k, delta_csr_types.hpp:1217-1222)
+    os_trainable = bool(os_trainable or rank > 1)
     ptrs, cols = [0], []
     for r in range(n_in):
         if r >= empty_rows:
@@ -67,6 +70,10 @@ TRAIN_CASES = [
     (80, 64, 0.15, 8, 1, 0.05, dict(rank=2, os_trainable=True)),
     (90, 70, 0.1, 9, 2, 0.2, dict(imp_scales=True)),
     (40, 600, 0.3, 10, 1, 0.05, {}),  # rows longer than one 64-byte decode chunk
+    # batches the GPU kernels take 8 steps at a time (a partial last group at 12 and 36)
+    (100, 80, 0.1, 13, 12, 0.05, {}),
+    (64, 200, 0.2, 14, 64, 0.02, dict(os_trainable=True)),
+    (50, 60, 0.2, 15, 36, 0.05, dict(rank=2, imp_scales=True)),
 ]
 LAYER_OPTS = ("rank", "empty_rows", "os_trainable", "imp_scales")
 
