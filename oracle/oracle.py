@@ -121,6 +121,12 @@ def lib(contracted: bool = False):
                                                    _i32p, _i32p, _f32p, C.c_int64, _f32p, _f32p, _f32p,
                                                    C.POINTER(_TrainParams)]
         L.oracle_backward_sparse_train.restype = C.c_int
+        L.oracle_build_probes.restype = C.c_int64
+        L.oracle_build_probes.argtypes = [C.POINTER(_OracleLayerC), _f32p, _f32p, C.c_int64, C.c_int, _i32p, _i32p,
+                                          _f32p, C.c_int64]
+        L.oracle_synap_row_step.argtypes = [C.POINTER(_OracleLayerC), C.c_int64, _i32p, _i32p, _f32p, C.c_int64,
+                                            C.c_int, C.c_float, C.c_int64, C.c_int64, C.c_float, _i32p, _i32p, _i32p,
+                                            _u8p, _i32p, _i32p, _u8p, C.POINTER(C.c_int64)]
         L.oracle_synapto_step.argtypes = [C.POINTER(_OracleLayerC), C.c_float, _i32p, _i32p, _f32p, _f32p,
                                           C.c_int64, C.c_int, _i32p, _i32p, _u8p, _i32p, _i32p, _u8p,
                                           C.POINTER(_SynStats)]
@@ -172,6 +178,13 @@ def reflib():
         R.ref_backward_sparse_train.argtypes = [C.c_void_p, _f32p, _i32p, _i32p, _f32p, C.c_int, _f32p, _f32p, _f32p,
                                                 C.c_float, C.c_int, C.c_int, C.c_float, C.c_float, C.c_int]
         R.ref_layer_set_importance_scales.argtypes = [C.c_void_p, _f32p, _f32p]
+        R.ref_layer_new_blank.restype = C.c_void_p
+        R.ref_layer_new_blank.argtypes = [C.c_int, C.c_int, _i32p, _i32p, _f32p, _f32p, C.c_float]
+        R.ref_build_probes.argtypes = [C.c_void_p, _f32p, _f32p, C.c_int, C.c_int]
+        R.ref_get_probes.restype = C.c_int64
+        R.ref_get_probes.argtypes = [C.c_void_p, _i32p, _i32p, _f32p, C.c_int64, C.POINTER(C.c_int)]
+        R.ref_synap_row_step.argtypes = [C.c_void_p, C.POINTER(C.c_int64), C.c_float, C.c_int, C.c_int, C.c_float]
+        R.ref_get_out_degree.argtypes = [C.c_void_p, _i32p]
         _u32p = C.POINTER(C.c_uint32)
         R.ref_layer_set_train_state.argtypes = [C.c_void_p, _f32p, _f32p, _u32p, _f32p, _u32p, C.c_int]
         R.ref_layer_get_train_state.argtypes = [C.c_void_p, _f32p, _f32p, _f32p, _u32p, _f32p, _f32p, _u32p]
@@ -393,7 +406,7 @@ class HostLayer:
         dx = np.zeros_like(x)
         ai = np.zeros(self.n_in, np.float32) if acc is None else acc[0]
         ag = np.zeros(self.n_out, np.float32) if acc is None else acc[1]
-        deg = self.out_degree()
+        deg = self.out_deg if getattr(self, "out_deg", None) is not None else self.out_degree()
         isc = None if self.importance_scale is None else _c(self.importance_scale, np.float32)
         oisc = None if self.output_importance_scale is None else _c(self.output_importance_scale, np.float32)
         u32p = C.POINTER(C.c_uint32)
@@ -433,6 +446,68 @@ class HostLayer:
                                                         C.byref(P)) != 0:
             raise ValueError("backward_sparse_train: layers with block4 tiles are not supported")
         return dx, ai, ag
+
+    # -- the reference's synaptogenesis policy (delta_csr_memory.hpp:1021-1426) --
+    def build_probes(self, acc_in, acc_grad, k, per_row=False):
+        """delta_csr_build_probes with the given activity accumulators."""
+        acc_in, acc_grad = _c(acc_in, np.float32), _c(acc_grad, np.float32)
+        kk = max(int(k), 0)
+        cap = max(1, kk * kk if not per_row else kk * max(kk, 1)) + 1
+        cap = max(cap, kk * min(kk, self.n_out) + 1)
+        prow, pcol = np.zeros(cap, np.int32), np.zeros(cap, np.int32)
+        pval = np.zeros(cap, np.float32)
+        s = self._cstruct()
+        n = lib().oracle_build_probes(C.byref(s), _p(acc_in, _f32p), _p(acc_grad, _f32p), int(k), int(per_row),
+                                      _p(prow, _i32p), _p(pcol, _i32p), _p(pval, _f32p), cap)
+        if not hasattr(self, "probes"):
+            self.probes = (np.zeros(0, np.int32), np.zeros(0, np.int32), np.zeros(0, np.float32))
+            self.probe_nnz = 0
+        if n < 0:               # the reference zeroes the count, keeps the old vectors
+            self.probe_nnz = 0
+            return
+        assert n <= cap
+        self.probes = (prow[:n].copy(), pcol[:n].copy(), pval[:n].copy())
+        self.probe_nnz = int(n)
+
+    def synap_row_step(self, current_row, importance_cutoff, max_row_weights, max_prune_per_step=8,
+                       importance_eps=1e-3):
+        """delta_csr_synap_row_step: returns (did, next cursor)."""
+        if self.n_in == 0:
+            return False, current_row
+        row = int(current_row) % self.n_in
+        nxt = (int(current_row) + 1) % self.n_in
+        if not hasattr(self, "probes"):
+            self.probes = (np.zeros(0, np.int32), np.zeros(0, np.int32), np.zeros(0, np.float32))
+            self.probe_nnz = 0
+        if getattr(self, "out_deg", None) is None:
+            self.out_deg = self.out_degree().astype(np.int32)
+        prow, pcol, pval = (_c(a, t) for a, t in zip(self.probes, (np.int32, np.int32, np.float32)))
+        nnz, nt = self.nnz, self.n_tiles
+        cap_s = nnz + len(prow) + 16 * nt + 1
+        cap_t = nt + len(prow) + 1
+        ptrs = np.zeros(self.n_in + 1, np.int32)
+        cols = np.zeros(cap_s, np.int32)
+        byts = np.zeros(cap_s, np.uint8)
+        tbr, tbc = np.zeros(cap_t, np.int32), np.zeros(cap_t, np.int32)
+        tby = np.zeros(16 * cap_t, np.uint8)
+        ntl = C.c_int64(0)
+        s = self._cstruct()
+        did = lib().oracle_synap_row_step(C.byref(s), row, _p(prow, _i32p), _p(pcol, _i32p), _p(pval, _f32p),
+                                          self.probe_nnz, int(len(prow) > 0), importance_cutoff,
+                                          int(max_row_weights), int(max_prune_per_step), importance_eps,
+                                          _p(self.out_deg, _i32p), _p(ptrs, _i32p), _p(cols, _i32p), _p(byts, _u8p),
+                                          _p(tbr, _i32p), _p(tbc, _i32p), _p(tby, _u8p), C.byref(ntl))
+        n = int(ptrs[-1])
+        k = int(ntl.value)
+        self.load_csr(ptrs, cols[:n], bytes_=byts[:n])
+        self.load_tiles(tbr[:k], tbc[:k], tby[:16 * k])
+        return bool(did), nxt
+
+    def synap_step(self, importance_cutoff, max_row_weights, max_prune_per_step=8, importance_eps=1e-3):
+        cur = getattr(self, "synap_cursor", 0)
+        did, self.synap_cursor = self.synap_row_step(cur, importance_cutoff, max_row_weights, max_prune_per_step,
+                                                     importance_eps)
+        return did
 
     def sampled_gradw(self, x, dy, threads=8, absmode=False):
         x = _c(np.atleast_2d(x), np.float32)
@@ -475,14 +550,41 @@ class HostLayer:
 class RefLayer:
     """The reference's own SparseLinearWeightsDelta, through ref_shim.cpp."""
 
-    def __init__(self, n_in, n_out, ptrs, cols, w, imp=None):
+    def __init__(self, n_in, n_out, ptrs, cols, w, imp=None, blank_fraction=0.2):
         self.n_in, self.n_out = int(n_in), int(n_out)
         R = reflib()
         self._keep = [_c(ptrs, np.int32), _c(cols, np.int32), _c(w, np.float32)]
         if imp is not None:
             self._keep.append(_c(imp, np.float32))
-        self.h = R.ref_layer_new(self.n_in, self.n_out, _p(self._keep[0], _i32p), _p(self._keep[1], _i32p),
-                                 _p(self._keep[2], _f32p), _p(self._keep[3], _f32p) if imp is not None else None)
+        self.h = R.ref_layer_new_blank(self.n_in, self.n_out, _p(self._keep[0], _i32p), _p(self._keep[1], _i32p),
+                                       _p(self._keep[2], _f32p), _p(self._keep[3], _f32p) if imp is not None else None,
+                                       float(blank_fraction))
+
+    def build_probes(self, acc_in, acc_grad, k, per_row=False):
+        acc_in, acc_grad = _c(acc_in, np.float32), _c(acc_grad, np.float32)
+        reflib().ref_build_probes(self.h, _p(acc_in, _f32p), _p(acc_grad, _f32p), int(k), int(per_row))
+
+    def get_probes(self):
+        """(rows, cols, scores) of the probe count, and whether the probe index vectors are non-empty."""
+        has = C.c_int(0)
+        n = reflib().ref_get_probes(self.h, None, None, None, 0, C.byref(has))
+        pr, pc, pv = np.zeros(max(n, 1), np.int32), np.zeros(max(n, 1), np.int32), np.zeros(max(n, 1), np.float32)
+        reflib().ref_get_probes(self.h, _p(pr, _i32p), _p(pc, _i32p), _p(pv, _f32p), n, C.byref(has))
+        return pr[:n], pc[:n], pv[:n], bool(has.value)
+
+    def synap_row_step(self, current_row, importance_cutoff, max_row_weights, max_prune_per_step=8,
+                       importance_eps=1e-3):
+        row = C.c_int64(int(current_row))
+        rc = reflib().ref_synap_row_step(self.h, C.byref(row), importance_cutoff, int(max_row_weights),
+                                         int(max_prune_per_step), importance_eps)
+        if rc == -2:
+            raise RuntimeError("reference synap_row_step ran out of row headroom")
+        return bool(rc), int(row.value)
+
+    def out_degree(self):
+        out = np.zeros(self.n_out, np.int32)
+        reflib().ref_get_out_degree(self.h, _p(out, _i32p))
+        return out
 
     def __del__(self):
         if getattr(self, "h", None):

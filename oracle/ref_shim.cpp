@@ -59,8 +59,18 @@ size_t ref_uleb_encode(uint32_t v, uint8_t *out) { return uleb128_encode<uint32_
 
 // Layer construction mirrors SparseLinearLayerImpl's constructor and
 // load_weights (sili/cpu_backend.cpp:375-447, 859-901).
+void *ref_layer_new_blank(int n_in, int n_out, const int32_t *ptrs, const int32_t *idx, const float *w,
+                          const float *imp, float blank_fraction);
+
 void *ref_layer_new(int n_in, int n_out, const int32_t *ptrs, const int32_t *idx,
                     const float *w, const float *imp) {
+    return ref_layer_new_blank(n_in, n_out, ptrs, idx, w, imp, 0.2f);
+}
+
+// Same, with blank_fraction of per-row headroom (delta_csr_memory.hpp:17-93):
+// the synaptogenesis tests give rows room to grow.
+void *ref_layer_new_blank(int n_in, int n_out, const int32_t *ptrs, const int32_t *idx, const float *w,
+                          const float *imp, float blank_fraction) {
     auto *L = new RefLayer();
     L->n_in = n_in;
     L->n_out = n_out;
@@ -71,7 +81,7 @@ void *ref_layer_new(int n_in, int n_out, const int32_t *ptrs, const int32_t *idx
     std::vector<float> ii(nnz, 0.0f);
     if (imp) ii.assign(imp, imp + nnz);
     L->w.connections = delta_csr_from_absolute<S, FP4BiPacked, COL>(
-        p, ix, ww, ii, size_t(n_in), size_t(n_out), nnz * 8 + 4096, nnz + 64);
+        p, ix, ww, ii, size_t(n_in), size_t(n_out), nnz * 8 + 4096, nnz + 64, blank_fraction);
     L->w.block4.init(size_t(n_in), size_t(n_out));
     L->w.out_degree.assign(size_t(n_out), 0);
     for (S c : ix) ++L->w.out_degree[size_t(c)];
@@ -224,6 +234,49 @@ void ref_backward_sparse_train(void *h, const float *x, const int32_t *dptrs, co
     std::memset(dx, 0, sizeof(float) * size_t(batch) * size_t(L->n_in));
     disldo_backward_sparse_grad<S, FP4BiPacked, COL>(x, S(batch), L->w, g, dx, acc_in, acc_grad, lr, threads,
                                                      lr_per_row_nnz != 0, damp != 0, beta2, eps);
+}
+
+// delta_csr_build_probes (sili/cpu_backend.cpp:606-609), with the layer's
+// accumulators passed in.
+void ref_build_probes(void *h, const float *acc_in, const float *acc_grad, int k, int per_row) {
+    auto *L = static_cast<RefLayer *>(h);
+    delta_csr_build_probes<S, FP4BiPacked, COL>(L->w, acc_in, acc_grad, S(k), per_row != 0);
+}
+
+// The probe list: returns its count (the COO count), writes up to cap entries;
+// *has_probes: the index vectors are non-empty.
+int64_t ref_get_probes(void *h, int32_t *prow, int32_t *pcol, float *pval, int64_t cap, int *has_probes) {
+    auto *L = static_cast<RefLayer *>(h);
+    const auto &pr = L->w.probes;
+    *has_probes = (pr.indices[0] && !pr.indices[0]->empty()) ? 1 : 0;
+    const int64_t n = int64_t(pr.nnz());
+    for (int64_t i = 0; i < n && i < cap; ++i) {
+        prow[i] = int32_t((*pr.indices[0])[size_t(i)]);
+        pcol[i] = int32_t((*pr.indices[1])[size_t(i)]);
+        pval[i] = (*pr.values[0])[size_t(i)];
+    }
+    return n;
+}
+
+// delta_csr_synap_row_step (sili/cpu_backend.cpp:610-615): *row in/out (the
+// reference advances it); returns 1/0 as it returns true/false, -2 when it
+// throws (a row out of headroom).
+int ref_synap_row_step(void *h, int64_t *row, float cutoff, int max_rw, int max_prune, float eps) {
+    auto *L = static_cast<RefLayer *>(h);
+    size_t r = size_t(*row);
+    try {
+        const bool did = delta_csr_synap_row_step<S, FP4BiPacked, COL>(L->w, r, cutoff, S(max_rw), S(max_prune), eps);
+        *row = int64_t(r);
+        return did ? 1 : 0;
+    } catch (const std::exception &) {
+        *row = int64_t(r);
+        return -2;
+    }
+}
+
+void ref_get_out_degree(void *h, int32_t *out) {
+    auto *L = static_cast<RefLayer *>(h);
+    for (int c = 0; c < L->n_out; ++c) out[c] = c < int(L->w.out_degree.size()) ? int32_t(L->w.out_degree[size_t(c)]) : 0;
 }
 
 // Per-row / per-column importance scales (delta_csr_types.hpp:1006-1031).

@@ -9,9 +9,12 @@
 #include "sili_oracle.h"
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstring>
+#include <map>
 #include <numeric>
+#include <unordered_set>
 #include <vector>
 #include <omp.h>
 
@@ -1096,6 +1099,314 @@ int oracle_backward_sparse_train(const OracleLayer *L, uint8_t *val, OracleTrain
         }
     }
     return 0;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// The reference's synaptogenesis policy: delta_csr_build_probes
+// (delta_csr_memory.hpp:1309-1426) and delta_csr_synap_row_step
+// (delta_csr_memory.hpp:1021-1264), restated on a mutable host copy of the
+// layer with the reference's sequential edit semantics: removals in
+// descending column order, a block4 slot removal demoting its tile at once
+// when fewer than 2 slots stay live (a later removal aimed at a slot that
+// demotion already moved to the scattered store then finds no tile and does
+// nothing), inserts one at a time, each followed by the promotion check.
+// The orderings use the same std::sort / std::partial_sort calls with the
+// same comparators and input order as the reference (tie order included).
+namespace {
+
+struct MutLayer {
+    int64_t n_in = 0, n_out = 0;
+    std::vector<std::vector<std::pair<uint32_t, uint8_t>>> rows;  // per row, by column: (col, (w<<4)|imp)
+    std::map<std::pair<uint32_t, uint32_t>, std::array<uint8_t, 16>> tiles;  // (br, bc) -> slot lj*4+li, (imp<<4)|w
+};
+
+MutLayer load_mut(const OracleLayer *L) {
+    MutLayer M;
+    M.n_in = L->n_in;
+    M.n_out = L->n_out;
+    M.rows.resize(size_t(L->n_in));
+    for (int64_t r = 0; r < L->n_in; ++r) {
+        uint64_t pos = L->row_byte_start[r];
+        uint32_t col = 0;
+        for (uint64_t e = L->row_elem_start[r]; e < L->row_elem_start[r + 1]; ++e) {
+            col += uleb_dec(L->idx, pos);
+            M.rows[size_t(r)].push_back({col, L->val[e]});
+        }
+    }
+    for (const auto &t : collect_tiles(L)) {
+        std::array<uint8_t, 16> d;
+        std::memcpy(d.data(), L->tiles + 16 * t.t, 16);
+        M.tiles[{uint32_t(t.br), uint32_t(t.bc)}] = d;
+    }
+    return M;
+}
+
+// ValueAccessor<FP4BiPacked>::set (fp4quant.hpp:280-467): round to nearest.
+inline uint8_t scat_byte(float w, float imp) { return uint8_t((fp4_enc(w) << 4) | fp4_enc(imp)); }
+
+// delta_csr_row_insert_col: false when the column is already stored.
+bool mut_insert(MutLayer &M, uint32_t r, uint32_t c, float w, float imp) {
+    auto &row = M.rows[r];
+    auto it = std::lower_bound(row.begin(), row.end(), std::make_pair(c, uint8_t(0)));
+    if (it != row.end() && it->first == c) return false;
+    row.insert(it, {c, scat_byte(w, imp)});
+    return true;
+}
+
+bool mut_remove(MutLayer &M, uint32_t r, uint32_t c) {
+    auto &row = M.rows[r];
+    auto it = std::lower_bound(row.begin(), row.end(), std::make_pair(c, uint8_t(0)));
+    if (it == row.end() || it->first != c) return false;
+    row.erase(it);
+    return true;
+}
+
+// block4_demote_tile (delta_csr_memory.hpp:949-999).
+void mut_demote(MutLayer &M, uint32_t br, uint32_t bc) {
+    auto it = M.tiles.find({br, bc});
+    if (it == M.tiles.end()) return;
+    const auto d = it->second;
+    for (uint32_t li = 0; li < TILE; ++li) {
+        const uint32_t r = br * TILE + li;
+        if (int64_t(r) >= M.n_in) continue;
+        for (uint32_t lj = 0; lj < TILE; ++lj) {
+            const uint8_t b = d[lj * TILE + li];
+            if (b == 0) continue;
+            const uint32_t c = bc * TILE + lj;
+            if (int64_t(c) >= M.n_out) continue;
+            mut_insert(M, r, c, fp4_dec(b & 0xFu), fp4_dec(b >> 4));
+        }
+    }
+    M.tiles.erase(it);
+}
+
+// block4_maybe_promote (delta_csr_memory.hpp:591-702).
+void mut_maybe_promote(MutLayer &M, uint32_t row, uint32_t col) {
+    const uint32_t br = row / TILE, bc = col / TILE, li = row % TILE, lj = col % TILE;
+    auto tit = M.tiles.find({br, bc});
+    if (tit != M.tiles.end()) {
+        auto &rw = M.rows[row];
+        auto it = std::lower_bound(rw.begin(), rw.end(), std::make_pair(col, uint8_t(0)));
+        if (it == rw.end() || it->first != col) return;
+        const float w = fp4_dec(it->second >> 4), imp = fp4_dec(it->second & 0xFu);
+        tit->second[lj * TILE + li] = uint8_t(fp4_enc(w) | (fp4_enc(imp) << 4));
+        rw.erase(it);
+        return;
+    }
+    const int64_t row_lo = int64_t(br) * TILE, row_hi = std::min<int64_t>(row_lo + TILE, M.n_in);
+    const int64_t col_lo = int64_t(bc) * TILE, col_hi = std::min<int64_t>(col_lo + TILE, M.n_out);
+    struct Found { uint32_t r, c; uint8_t b; };
+    std::vector<Found> found;
+    for (int64_t r = row_lo; r < row_hi; ++r)
+        for (const auto &e : M.rows[size_t(r)])
+            if (int64_t(e.first) >= col_lo && int64_t(e.first) < col_hi) found.push_back({uint32_t(r), e.first, e.second});
+    if (found.size() < size_t(PROMOTE_MIN_LIVE)) return;
+    std::array<uint8_t, 16> d{};
+    for (const auto &f : found) {
+        const float w = fp4_dec(f.b >> 4), imp = fp4_dec(f.b & 0xFu);
+        d[(f.c - uint32_t(col_lo)) * TILE + (f.r - uint32_t(row_lo))] = uint8_t(fp4_enc(w) | (fp4_enc(imp) << 4));
+    }
+    M.tiles[{br, bc}] = d;
+    for (const auto &f : found) mut_remove(M, f.r, f.c);
+}
+
+int64_t mut_store(const MutLayer &M, int32_t *out_ptrs, int32_t *out_cols, uint8_t *out_bytes, int32_t *out_br,
+                  int32_t *out_bc, uint8_t *out_tiles) {
+    int64_t flat = 0;
+    out_ptrs[0] = 0;
+    for (int64_t r = 0; r < M.n_in; ++r) {
+        for (const auto &e : M.rows[size_t(r)]) {
+            out_cols[flat] = int32_t(e.first);
+            out_bytes[flat] = e.second;
+            ++flat;
+        }
+        out_ptrs[r + 1] = int32_t(flat);
+    }
+    int64_t k = 0;
+    for (const auto &t : M.tiles) {
+        out_br[k] = int32_t(t.first.first);
+        out_bc[k] = int32_t(t.first.second);
+        std::memcpy(out_tiles + 16 * k, t.second.data(), 16);
+        ++k;
+    }
+    return k;
+}
+
+}  // namespace
+
+extern "C" {
+
+// delta_csr_build_probes (delta_csr_memory.hpp:1309-1426): the probe list in
+// the reference's order.  Returns the number of probes written (<= cap), or
+// -1 when k <= 0 or the layer is empty (the reference then zeroes the probe
+// count and keeps its old index vectors).
+int64_t oracle_build_probes(const OracleLayer *L, const float *acc_in, const float *acc_grad, int64_t k,
+                            int per_row, int32_t *prow, int32_t *pcol, float *pval, int64_t cap) {
+    const size_t n_in = size_t(L->n_in), n_out = size_t(L->n_out);
+    if (n_in == 0 || n_out == 0 || k <= 0) return -1;
+    const size_t kk_in = std::min(size_t(k), n_in), kk = size_t(k);
+    std::vector<size_t> in_idx(n_in);
+    std::iota(in_idx.begin(), in_idx.end(), 0);
+    std::partial_sort(in_idx.begin(), in_idx.begin() + kk_in, in_idx.end(),
+                      [&](size_t a, size_t b) { return acc_in[a] > acc_in[b]; });
+    in_idx.resize(kk_in);
+    int64_t n = 0;
+    auto emit = [&](size_t r, size_t c) {
+        if (n < cap) {
+            prow[n] = int32_t(r);
+            pcol[n] = int32_t(c);
+            pval[n] = acc_in[r] * acc_grad[c];
+        }
+        ++n;
+    };
+    auto row_cols = [&](size_t r) {
+        std::vector<uint32_t> cols;
+        uint64_t pos = L->row_byte_start[r];
+        uint32_t col = 0;
+        for (uint64_t e = L->row_elem_start[r]; e < L->row_elem_start[r + 1]; ++e) {
+            col += uleb_dec(L->idx, pos);
+            cols.push_back(col);
+        }
+        return cols;
+    };
+    if (!per_row) {
+        const size_t kk_out = std::min(kk, n_out);
+        std::vector<size_t> out_idx(n_out);
+        std::iota(out_idx.begin(), out_idx.end(), 0);
+        std::partial_sort(out_idx.begin(), out_idx.begin() + kk_out, out_idx.end(),
+                          [&](size_t a, size_t b) { return acc_grad[a] > acc_grad[b]; });
+        out_idx.resize(kk_out);
+        for (size_t r : in_idx) {
+            const auto ex = row_cols(r);
+            for (size_t c : out_idx)
+                if (!std::binary_search(ex.begin(), ex.end(), uint32_t(c))) emit(r, c);
+        }
+    } else {
+        for (size_t r : in_idx) {
+            const auto ex = row_cols(r);
+            std::vector<size_t> cand;
+            for (size_t c = 0; c < n_out; ++c)
+                if (!std::binary_search(ex.begin(), ex.end(), uint32_t(c))) cand.push_back(c);
+            const size_t kk_row = std::min(kk, cand.size());
+            if (kk_row == 0) continue;
+            std::partial_sort(cand.begin(), cand.begin() + kk_row, cand.end(),
+                              [&](size_t a, size_t b) { return acc_grad[a] > acc_grad[b]; });
+            for (size_t i = 0; i < kk_row; ++i) emit(r, cand[i]);
+        }
+    }
+    return n;
+}
+
+// delta_csr_synap_row_step on row `row` (already reduced modulo n_in; the
+// caller advances its cursor).  probes: the layer's probe list (pnnz entries
+// read; has_probes: its index vectors are non-empty).  out_degree [n_out] is
+// updated as the reference updates it.  The new structure goes to the out_*
+// arrays (capacities: scattered <= nnz + n_probes + 16 * n_tiles, tiles <=
+// n_tiles + n_probes); *n_tiles_out receives the tile count.  Returns 1 when
+// the reference returns true, 0 when false.
+int oracle_synap_row_step(const OracleLayer *L, int64_t row, const int32_t *prow, const int32_t *pcol,
+                          const float *pval, int64_t pnnz, int has_probes, float importance_cutoff,
+                          int64_t max_row_weights, int64_t max_prune_per_step, float importance_eps,
+                          int32_t *out_degree, int32_t *out_ptrs, int32_t *out_cols, uint8_t *out_bytes,
+                          int32_t *out_br, int32_t *out_bc, uint8_t *out_tiles, int64_t *n_tiles_out) {
+    MutLayer M = load_mut(L);
+    auto finish = [&](int ret) {
+        *n_tiles_out = mut_store(M, out_ptrs, out_cols, out_bytes, out_br, out_bc, out_tiles);
+        return ret;
+    };
+    if (M.n_in == 0) return finish(0);
+    const uint32_t r = uint32_t(row), br = r / TILE, li = r % TILE;
+    const size_t n_scattered = M.rows[r].size();
+    std::vector<uint32_t> b4_bc, b4_lj;
+    for (const auto &t : M.tiles) {
+        if (t.first.first != br) continue;
+        for (uint32_t lj = 0; lj < TILE; ++lj) {
+            if (t.second[lj * TILE + li] == 0) continue;
+            const uint32_t col = t.first.second * TILE + lj;
+            if (int64_t(col) >= M.n_out) continue;
+            b4_bc.push_back(t.first.second);
+            b4_lj.push_back(lj);
+        }
+    }
+    const size_t n_exist = n_scattered + b4_bc.size();
+    if (n_exist == 0 && !has_probes) return finish(0);
+    std::vector<uint32_t> exist_cols(n_exist);
+    std::vector<float> exist_imp(n_exist);
+    std::vector<bool> exist_is_b4(n_exist, false);
+    for (size_t k = 0; k < n_scattered; ++k) {
+        exist_cols[k] = M.rows[r][k].first;
+        exist_imp[k] = fp4_dec(M.rows[r][k].second & 0xFu);
+    }
+    for (size_t j = 0; j < b4_bc.size(); ++j) {
+        const size_t k = n_scattered + j;
+        const uint8_t b = M.tiles[{br, b4_bc[j]}][b4_lj[j] * TILE + li];
+        exist_cols[k] = b4_bc[j] * TILE + b4_lj[j];
+        exist_imp[k] = fp4_dec(b >> 4);
+        exist_is_b4[k] = true;
+    }
+    std::vector<uint32_t> probe_cols;
+    std::vector<float> probe_scores;
+    for (int64_t p = 0; p < pnnz; ++p)
+        if (int64_t(prow[p]) == int64_t(r)) {
+            probe_cols.push_back(uint32_t(pcol[p]));
+            probe_scores.push_back(pval[p]);
+        }
+    std::vector<size_t> by_imp(n_exist);
+    std::iota(by_imp.begin(), by_imp.end(), 0);
+    std::sort(by_imp.begin(), by_imp.end(), [&](size_t a, size_t b) { return exist_imp[a] < exist_imp[b]; });
+    struct RemoveEntry { uint32_t col; bool is_b4; };
+    std::vector<RemoveEntry> to_remove;
+    const size_t max_rw = size_t(max_row_weights), max_prune = size_t(max_prune_per_step);
+    for (size_t rank = 0; rank < n_exist && to_remove.size() < max_prune; ++rank) {
+        const size_t k = by_imp[rank];
+        const size_t keep = n_exist - to_remove.size();
+        if (std::max(exist_imp[k], importance_eps) < importance_cutoff || keep > max_rw)
+            to_remove.push_back({exist_cols[k], exist_is_b4[k]});
+    }
+    std::sort(to_remove.begin(), to_remove.end(), [](const RemoveEntry &a, const RemoveEntry &b) { return a.col > b.col; });
+    {
+        std::unordered_set<uint32_t> exist_set(exist_cols.begin(), exist_cols.end());
+        std::vector<size_t> pidx(probe_cols.size());
+        std::iota(pidx.begin(), pidx.end(), 0);
+        std::sort(pidx.begin(), pidx.end(), [&](size_t a, size_t b) { return probe_scores[a] > probe_scores[b]; });
+        std::vector<uint32_t> add_cols;
+        std::vector<float> add_scores;
+        const size_t slots = max_rw - (n_exist - to_remove.size());
+        for (size_t p : pidx) {
+            if (add_cols.size() >= slots) break;
+            if (!exist_set.count(probe_cols[p])) {
+                add_cols.push_back(probe_cols[p]);
+                add_scores.push_back(probe_scores[p]);
+            }
+        }
+        probe_cols = std::move(add_cols);
+        probe_scores = std::move(add_scores);
+    }
+    for (const auto &re : to_remove) {
+        if (re.is_b4) {
+            const uint32_t bc = re.col / TILE, lj = re.col % TILE;
+            bool should_demote = false;
+            auto it = M.tiles.find({br, bc});
+            if (it != M.tiles.end() && it->second[lj * TILE + li] != 0) {
+                it->second[lj * TILE + li] = 0;
+                int live = 0;
+                for (uint8_t b : it->second) live += b != 0;
+                should_demote = live < PROMOTE_MIN_LIVE;
+            }
+            if (should_demote) mut_demote(M, br, bc);
+        } else {
+            mut_remove(M, r, re.col);
+        }
+        if (out_degree[re.col] > 0) --out_degree[re.col];
+    }
+    for (size_t i = 0; i < probe_cols.size(); ++i) {
+        mut_insert(M, r, probe_cols[i], 0.0f, probe_scores[i]);
+        ++out_degree[probe_cols[i]];
+        mut_maybe_promote(M, r, probe_cols[i]);
+    }
+    return finish(1);
 }
 
 }  // extern "C"

@@ -162,6 +162,22 @@ int oracle_backward_sparse_train(const OracleLayer *L, uint8_t *val, OracleTrain
                                  const int32_t *dptrs, const int32_t *didx, const float *dvals, int64_t batch,
                                  float *dx, float *acc_in, float *acc_grad, const OracleTrainParams *P);
 
+/* ---- the reference's synaptogenesis policy ----
+ * oracle_build_probes: delta_csr_build_probes (delta_csr_memory.hpp:1309-1426);
+ * returns the probe count (entries beyond cap are counted, not written), -1
+ * when k <= 0 or the layer is empty.
+ * oracle_synap_row_step: delta_csr_synap_row_step (delta_csr_memory.hpp:
+ * 1021-1264) on one row, sequential edit semantics; out_degree updated in
+ * place; the new structure in the out_* arrays; returns 1/0 as the reference
+ * returns true/false. */
+int64_t oracle_build_probes(const OracleLayer *L, const float *acc_in, const float *acc_grad, int64_t k,
+                            int per_row, int32_t *prow, int32_t *pcol, float *pval, int64_t cap);
+int oracle_synap_row_step(const OracleLayer *L, int64_t row, const int32_t *prow, const int32_t *pcol,
+                          const float *pval, int64_t pnnz, int has_probes, float importance_cutoff,
+                          int64_t max_row_weights, int64_t max_prune_per_step, float importance_eps,
+                          int32_t *out_degree, int32_t *out_ptrs, int32_t *out_cols, uint8_t *out_bytes,
+                          int32_t *out_br, int32_t *out_bc, uint8_t *out_tiles, int64_t *n_tiles_out);
+
 /* ---- bulk synaptogenesis step (magnitude prune + candidate regrow) ----
  * Output capacities: scattered entries <= nnz + n_cand + 16*n_tiles,
  * tiles <= n_tiles + n_cand.  Outputs are absolute: out_ptrs[n_in+1],
