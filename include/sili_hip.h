@@ -227,6 +227,38 @@ int sili_backward_sparse_train(sili_layer *layer, const float *x, const int32_t 
 
 /* ---- synaptogenesis ----------------------------------------------------- */
 
+/* The reference's own policy (sili/cpu_backend.cpp:606-634).
+ * sili_build_probes: delta_csr_build_probes (delta_csr_memory.hpp:1309-1426)
+ *   over the layer's neuron_input_accum / neuron_grad_accum: the top-k input
+ *   rows by accumulator, crossed with the top-k outputs (shared, or per row
+ *   among the columns the row lacks when per_row), pairs already stored in
+ *   the scattered store skipped, score = acc_in[r] * acc_grad[c].  k <= 0
+ *   zeroes the probe count only, as the reference does.
+ * sili_get_probes: the probe list (count to *n, up to cap entries copied).
+ * sili_synap_row_step: delta_csr_synap_row_step (delta_csr_memory.hpp:
+ *   1021-1264) on row *current_row % n_inputs; *current_row advances (mod
+ *   n_inputs) as in the reference.  Removes the row's lowest-importance
+ *   synapses (scattered and block4) below importance_cutoff (importance floored
+ *   at importance_eps for that test only) or beyond max_row_weights, at most
+ *   max_prune_per_step; grows the row's probes by descending score into the
+ *   capacity left, weight 0 and importance = score; block4 demotion and
+ *   promotion as the reference.  *did: 0 when the row holds nothing and there
+ *   are no probes.  The store never runs out of row headroom here (it is
+ *   rebuilt compactly), where the reference would throw.
+ * sili_synap_step: the same on the layer's own cursor (synap_step).
+ * sili_get_out_degree: out_degree [n_outputs] as the reference keeps it: the
+ *   scattered synapses per column after a load, then +1 / -1 per
+ *   synap_row_step insert / removal entry (delta_csr_memory.hpp:1216,1246).
+ *   It sets the output scales' learning-rate divisor in the update. */
+int sili_build_probes(sili_layer *layer, int64_t k, int per_row);
+int sili_get_probes(sili_layer *layer, int64_t *n, int32_t *rows, int32_t *cols, float *scores, int64_t cap);
+int sili_synap_row_step(sili_layer *layer, int64_t *current_row, float importance_cutoff,
+                        int64_t max_row_weights, int64_t max_prune_per_step, float importance_eps,
+                        int *did);
+int sili_synap_step(sili_layer *layer, float importance_cutoff, int64_t max_row_weights,
+                    int64_t max_prune_per_step, float importance_eps, int *did);
+int sili_get_out_degree(sili_layer *layer, int32_t *out);
+
 /* Bulk synaptogenesis step, on the GPU.  Selection policy (new; the reference
  * prunes by importance row by row, delta_csr_memory.hpp:1019-1258): prune the
  * round(prune_frac*N) stored synapses (scattered + live block4 slots) with the

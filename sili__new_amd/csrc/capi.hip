@@ -600,6 +600,7 @@ int sili_load_weights(sili_layer *layer, const int32_t *ptrs, const int32_t *ind
                       const float *imp, int64_t nnz) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        layer->L.out_deg_tracked = false;  // a load counts out_degree afresh
         set_device(layer->L);
         build_from_host_csr(layer->L, ptrs, indices, nullptr, vals, imp, nnz);
     });
@@ -609,6 +610,7 @@ int sili_load_weight_bytes(sili_layer *layer, const int32_t *ptrs, const int32_t
                            const uint8_t *bytes, int64_t nnz) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        layer->L.out_deg_tracked = false;  // a load counts out_degree afresh
         set_device(layer->L);
         if (nnz > 0 && !bytes) throw_error(SILI_ERR_INVALID, "bytes is NULL");
         std::vector<uint8_t> dummy(1, 0);
@@ -620,6 +622,7 @@ int sili_load_synthetic(sili_layer *layer, uint64_t seed, double keep_prob, floa
                         int64_t *nnz_out) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        layer->L.out_deg_tracked = false;  // a load counts out_degree afresh
         Layer &L = layer->L;
         if (L.rank != 1) throw_error(SILI_ERR_INVALID, "load_synthetic: scale rank must be 1");
         if (!(keep_prob >= 0.0 && keep_prob <= 1.0) || !(sigma > 0.0f) || !(tail_q >= 0.5f && tail_q < 1.0f))
@@ -634,6 +637,7 @@ int sili_load_synthetic(sili_layer *layer, uint64_t seed, double keep_prob, floa
 int sili_load_dense_codes(sili_layer *layer, const uint8_t *wc, const uint8_t *ic) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        layer->L.out_deg_tracked = false;  // a load counts out_degree afresh
         if (!wc || !ic) throw_error(SILI_ERR_INVALID, "code arrays are NULL");
         Layer &L = layer->L;
         set_device(L);
@@ -670,6 +674,7 @@ int sili_load_block4_tiles(sili_layer *layer, const int32_t *br, const int32_t *
                            int64_t n_tiles) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        layer->L.out_deg_tracked = false;  // a load counts out_degree afresh
         Layer &L = layer->L;
         set_device(L);
         if (n_tiles < 0 || n_tiles >= (int64_t(1) << 31)) throw_error(SILI_ERR_INVALID, "n_tiles out of range");
@@ -898,6 +903,55 @@ int sili_backward_sparse_train(sili_layer *layer, const float *x, const int32_t 
         const TrainParams p{learning_rate, lr_per_row_nnz ? 1 : 0, damp_by_importance ? 1 : 0, beta2, eps,
                             0.9f, 0.0f, 2.0f, 100.0f, 0.1f};
         backward_sparse_train(layer->L, x, dy_ptrs, dy_indices, dy_values, nnz_dy, batch, dx, p, st);
+    });
+}
+
+int sili_build_probes(sili_layer *layer, int64_t k, int per_row) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        build_probes(layer->L, k, per_row != 0);
+    });
+}
+
+int sili_get_probes(sili_layer *layer, int64_t *n, int32_t *rows, int32_t *cols, float *scores, int64_t cap) {
+    return guarded([&] {
+        if (!layer || !n) throw_error(SILI_ERR_INVALID, "layer or n is NULL");
+        const Layer &L = layer->L;
+        *n = L.probe_nnz;
+        for (int64_t i = 0; i < L.probe_nnz && i < cap; ++i) {
+            if (rows) rows[i] = L.probe_r[(size_t)i];
+            if (cols) cols[i] = L.probe_c[(size_t)i];
+            if (scores) scores[i] = L.probe_v[(size_t)i];
+        }
+    });
+}
+
+int sili_synap_row_step(sili_layer *layer, int64_t *current_row, float importance_cutoff, int64_t max_row_weights,
+                        int64_t max_prune_per_step, float importance_eps, int *did) {
+    return guarded([&] {
+        if (!layer || !current_row) throw_error(SILI_ERR_INVALID, "layer or current_row is NULL");
+        if (*current_row < 0 || max_row_weights < 0 || max_prune_per_step < 0)
+            throw_error(SILI_ERR_INVALID, "synap_row_step: negative row, max_row_weights or max_prune_per_step");
+        set_device(layer->L);
+        const bool r = synap_row_step(layer->L, *current_row, importance_cutoff, max_row_weights, max_prune_per_step,
+                                      importance_eps);
+        if (did) *did = r ? 1 : 0;
+    });
+}
+
+int sili_synap_step(sili_layer *layer, float importance_cutoff, int64_t max_row_weights, int64_t max_prune_per_step,
+                    float importance_eps, int *did) {
+    if (!layer) return guarded([&] { throw_error(SILI_ERR_INVALID, "layer is NULL"); });
+    return sili_synap_row_step(layer, &layer->L.synap_cursor, importance_cutoff, max_row_weights, max_prune_per_step,
+                               importance_eps, did);
+}
+
+int sili_get_out_degree(sili_layer *layer, int32_t *out) {
+    return guarded([&] {
+        if (!layer || !out) throw_error(SILI_ERR_INVALID, "layer or out is NULL");
+        set_device(layer->L);
+        get_out_degree(layer->L, out);
     });
 }
 

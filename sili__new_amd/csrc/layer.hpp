@@ -190,6 +190,16 @@ struct Layer {
     DevBuf<float> vs_snap;        // value scales as the update's rows read them
     DevBuf<double> train_rowsum;  // backward_sparse update: per-row value-scale gradient sums
     int update_variant = UPDATE_PLAIN;
+    // the reference's synaptogenesis policy: the probe list (COO, host; the
+    // count may be zeroed while the vectors stay, delta_csr_memory.hpp:1338-1342),
+    // the synap_step cursor, and out_degree as the policy keeps it (from the
+    // first policy step on; before that, the scattered synapses per column)
+    std::vector<int32_t> probe_r, probe_c;
+    std::vector<float> probe_v;
+    int64_t probe_nnz = 0;
+    int64_t synap_cursor = 0;
+    DevBuf<int32_t> out_deg;
+    bool out_deg_tracked = false;
     bool stochastic_rounding = true;
     uint64_t rng_seed = 0x5EEDull, rng_calls = 0;
     int64_t train_calls = 0;
@@ -277,6 +287,15 @@ void launch_train_store(Layer &L, uint64_t seed, hipStream_t st);
 void launch_sparse_train(Layer &L, const float *xT, const float *gT, int64_t B, float *dx, const TrainParams &p,
                          hipStream_t st);
 
+// ---- the reference's synaptogenesis policy (policy.hip) -------------------------
+// delta_csr_build_probes over L's activity accumulators.
+void build_probes(Layer &L, int64_t k, bool per_row);
+// delta_csr_synap_row_step on row cursor % n_in (cursor advanced).
+bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t max_row_weights,
+                    int64_t max_prune_per_step, float importance_eps);
+// out_degree [n_out] to host memory.
+void get_out_degree(Layer &L, int32_t *out);
+
 // ---- seeded synthetic layers (gen.hip) ----------------------------------------
 // Rebuilds the scattered store (and its shadow) from the seeded generator and
 // writes the per-row value scales into L.vs (rank 1).  Returns the synapse count.
@@ -286,5 +305,12 @@ int64_t generate_synthetic(Layer &L, uint64_t seed, double keep_prob, float sigm
 void synapto_step(Layer &L, float prune_frac, const int32_t *cand_r, const int32_t *cand_c,
                   const float *cand_v, const float *cand_s, int64_t n_cand, int default_imp,
                   int64_t *stats);
+// The same pipeline; explicit_prune: instead of the smallest |w|, the n_prune
+// stored synapses whose (row << 32 | col) keys prune_keys holds (host memory)
+// are removed (tiles left with < 2 live slots demoted), then every valid
+// candidate is grown (promotion as in synapto_step).
+void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64_t *prune_keys, int64_t n_prune,
+                   const int32_t *cand_r, const int32_t *cand_c, const float *cand_v, const float *cand_s,
+                   int64_t n_cand, int default_imp, int64_t *stats);
 
 }  // namespace sili

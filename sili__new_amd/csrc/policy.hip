@@ -1,0 +1,324 @@
+// policy.hip -- the reference's own synaptogenesis policy on the device store:
+// delta_csr_build_probes (delta_csr_memory.hpp:1309-1426) and
+// delta_csr_synap_row_step (delta_csr_memory.hpp:1021-1264).
+//
+// The policy is control logic over a handful of synapses per call (one row,
+// k x k probes), so its decisions are made on the host from small reads of
+// the device store (one row's index and value bytes, one block row's tiles)
+// with the same std::sort / std::partial_sort calls, comparators and input
+// order as the reference -- its tie order is part of the result.  The edits
+// are then applied on the device by the bulk synaptogenesis pipeline in its
+// explicit-prune mode (synapto.hip), which rebuilds both stores.
+//
+// The reference edits one synapse at a time: removals in descending column
+// order, a block4 slot removal demoting its tile as soon as fewer than 2
+// slots stay live; a later removal aimed at a slot that demotion moved to the
+// scattered store finds no tile and does nothing.  The device pipeline works
+// in phases (all removals, then demotion), so the removals are first replayed
+// here on the block row's tiles and only those the reference performs are
+// passed on.  Inserts are equivalent either way: each insert's promotion check
+// in the reference and the pipeline's one promotion pass leave the same tiles.
+#include "layer.hpp"
+
+#include <algorithm>
+#include <array>
+#include <map>
+#include <numeric>
+#include <unordered_set>
+#include <vector>
+
+namespace sili {
+
+namespace {
+
+constexpr unsigned TPB = 256;
+inline unsigned nblk(int64_t n) { return (unsigned)((n + TPB - 1) / TPB); }
+
+// out_degree before the policy's first step: the scattered synapses per
+// column (the count the reference's load_weights keeps,
+// sili/cpu_backend.cpp:446-447), i.e. the shadow store's row lengths.
+__global__ void k_deg_from_starts(const uint32_t *__restrict__ t_elem_start, int64_t n_out, int32_t *deg) {
+    const int64_t c = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (c < n_out) deg[c] = (int32_t)(t_elem_start[c + 1] - t_elem_start[c]);
+}
+
+// The policy's out_degree edits (delta_csr_memory.hpp:1216-1217,1246-1247):
+// -1 (kept at >= 0) per removal entry, +1 per insert.  The columns of one
+// call are distinct.
+__global__ void k_deg_edit(int32_t *deg, const int32_t *__restrict__ cols, const int32_t *__restrict__ delta,
+                           int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= n) return;
+    const int32_t c = cols[i];
+    if (delta[i] < 0) {
+        if (deg[c] > 0) deg[c] -= 1;
+    } else {
+        deg[c] += 1;
+    }
+}
+
+uint32_t uleb_read(const uint8_t *p, size_t &pos) {
+    uint32_t v = 0;
+    for (uint32_t sh = 0;; sh += 7) {
+        const uint8_t b = p[pos++];
+        v |= (uint32_t)(b & 0x7Fu) << sh;
+        if (!(b & 0x80u)) return v;
+    }
+}
+
+float fp4_value(uint32_t code) { return fp4_decode(code & 0xFu); }
+
+// One row of the canonical scattered store: (col, (w<<4)|imp) in order.
+std::vector<std::pair<uint32_t, uint8_t>> read_row(Layer &L, int64_t r) {
+    hipStream_t st = L.stream;
+    uint32_t bs[2], es[2];
+    SILI_HIP(hipMemcpyAsync(bs, L.W.byte_start.p + r, 8, hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipMemcpyAsync(es, L.W.elem_start.p + r, 8, hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipStreamSynchronize(st));
+    std::vector<uint8_t> idx(bs[1] - bs[0] + 1), val(es[1] - es[0] + 1);
+    if (bs[1] > bs[0]) SILI_HIP(hipMemcpyAsync(idx.data(), L.W.idx.p + bs[0], bs[1] - bs[0], hipMemcpyDeviceToHost, st));
+    if (es[1] > es[0]) SILI_HIP(hipMemcpyAsync(val.data(), L.W.val.p + es[0], es[1] - es[0], hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipStreamSynchronize(st));
+    std::vector<std::pair<uint32_t, uint8_t>> out;
+    size_t pos = 0;
+    uint32_t col = 0;
+    for (uint32_t e = 0; e < es[1] - es[0]; ++e) {
+        col += uleb_read(idx.data(), pos);
+        out.push_back({col, val[e]});
+    }
+    return out;
+}
+
+// The tiles of block row br of the canonical block4 store, by block column:
+// slot lj*4+li, byte (imp<<4)|w.
+std::map<uint32_t, std::array<uint8_t, 16>> read_block_row(Layer &L, int64_t br) {
+    std::map<uint32_t, std::array<uint8_t, 16>> out;
+    if (L.B4.ntiles == 0 || br >= L.B4.brows) return out;
+    hipStream_t st = L.stream;
+    uint32_t bs[2], ts[2];
+    SILI_HIP(hipMemcpyAsync(bs, L.B4.byte_start.p + br, 8, hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipMemcpyAsync(ts, L.B4.tile_start.p + br, 8, hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipStreamSynchronize(st));
+    const uint32_t nt = ts[1] - ts[0];
+    if (nt == 0) return out;
+    std::vector<uint8_t> idx(bs[1] - bs[0] + 1), tiles((size_t)nt * 16);
+    SILI_HIP(hipMemcpyAsync(idx.data(), L.B4.idx.p + bs[0], bs[1] - bs[0], hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipMemcpyAsync(tiles.data(), L.B4.tiles.p + (size_t)ts[0] * 16, (size_t)nt * 16, hipMemcpyDeviceToHost,
+                            st));
+    SILI_HIP(hipStreamSynchronize(st));
+    size_t pos = 0;
+    uint32_t bc = 0;
+    for (uint32_t t = 0; t < nt; ++t) {
+        bc += uleb_read(idx.data(), pos);
+        std::array<uint8_t, 16> d;
+        std::copy(tiles.begin() + (size_t)t * 16, tiles.begin() + (size_t)t * 16 + 16, d.begin());
+        out[bc] = d;
+    }
+    return out;
+}
+
+// L.out_deg holds out_degree; mark: from now on the policy keeps it.
+void ensure_out_deg(Layer &L, bool mark) {
+    if (L.out_deg_tracked) return;
+    L.out_deg.ensure((size_t)std::max<int64_t>(1, L.n_out));
+    if (L.n_out > 0)
+        launch(k_deg_from_starts, dim3(nblk(L.n_out)), dim3(TPB), 0, L.stream, (const uint32_t *)L.Wt.elem_start.p,
+               L.n_out, L.out_deg.p);
+    SILI_HIP(hipGetLastError());
+    L.out_deg_tracked = mark;
+}
+
+}  // namespace
+
+void build_probes(Layer &L, int64_t k, bool per_row) {
+    const size_t n_in = (size_t)L.n_in, n_out = (size_t)L.n_out;
+    if (n_in == 0 || n_out == 0 || k <= 0) {
+        L.probe_nnz = 0;  // the reference zeroes the count only
+        return;
+    }
+    std::vector<float> acc_in(n_in), acc_grad(n_out);
+    SILI_HIP(hipMemcpyAsync(acc_in.data(), L.acc_in.p, n_in * 4, hipMemcpyDeviceToHost, L.stream));
+    SILI_HIP(hipMemcpyAsync(acc_grad.data(), L.acc_grad.p, n_out * 4, hipMemcpyDeviceToHost, L.stream));
+    SILI_HIP(hipStreamSynchronize(L.stream));
+    const size_t kk_in = std::min((size_t)k, n_in), kk = (size_t)k;
+    std::vector<size_t> in_idx(n_in);
+    std::iota(in_idx.begin(), in_idx.end(), 0);
+    std::partial_sort(in_idx.begin(), in_idx.begin() + kk_in, in_idx.end(),
+                      [&](size_t a, size_t b) { return acc_in[a] > acc_in[b]; });
+    in_idx.resize(kk_in);
+    std::vector<int32_t> pr, pc;
+    std::vector<float> pv;
+    auto row_cols = [&](size_t r) {
+        std::vector<uint32_t> cols;
+        for (const auto &e : read_row(L, (int64_t)r)) cols.push_back(e.first);
+        return cols;
+    };
+    if (!per_row) {
+        const size_t kk_out = std::min(kk, n_out);
+        std::vector<size_t> out_idx(n_out);
+        std::iota(out_idx.begin(), out_idx.end(), 0);
+        std::partial_sort(out_idx.begin(), out_idx.begin() + kk_out, out_idx.end(),
+                          [&](size_t a, size_t b) { return acc_grad[a] > acc_grad[b]; });
+        out_idx.resize(kk_out);
+        for (size_t r : in_idx) {
+            const auto ex = row_cols(r);
+            for (size_t c : out_idx) {
+                if (std::binary_search(ex.begin(), ex.end(), (uint32_t)c)) continue;
+                pr.push_back((int32_t)r);
+                pc.push_back((int32_t)c);
+                pv.push_back(acc_in[r] * acc_grad[c]);
+            }
+        }
+    } else {
+        for (size_t r : in_idx) {
+            const auto ex = row_cols(r);
+            std::vector<size_t> cand;
+            cand.reserve(n_out);
+            for (size_t c = 0; c < n_out; ++c)
+                if (!std::binary_search(ex.begin(), ex.end(), (uint32_t)c)) cand.push_back(c);
+            const size_t kk_row = std::min(kk, cand.size());
+            if (kk_row == 0) continue;
+            std::partial_sort(cand.begin(), cand.begin() + kk_row, cand.end(),
+                              [&](size_t a, size_t b) { return acc_grad[a] > acc_grad[b]; });
+            for (size_t i = 0; i < kk_row; ++i) {
+                pr.push_back((int32_t)r);
+                pc.push_back((int32_t)cand[i]);
+                pv.push_back(acc_in[r] * acc_grad[cand[i]]);
+            }
+        }
+    }
+    L.probe_r.swap(pr);
+    L.probe_c.swap(pc);
+    L.probe_v.swap(pv);
+    L.probe_nnz = (int64_t)L.probe_r.size();
+}
+
+bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t max_row_weights,
+                    int64_t max_prune_per_step, float importance_eps) {
+    if (L.n_in == 0) return false;
+    const int64_t row = cursor % L.n_in;
+    cursor = (cursor + 1) % L.n_in;
+    const uint32_t br = (uint32_t)(row / 4), li = (uint32_t)(row % 4);
+    const auto scat = read_row(L, row);
+    auto btiles = read_block_row(L, br);
+    std::vector<uint32_t> exist_cols;
+    std::vector<float> exist_imp;
+    std::vector<bool> exist_is_b4;
+    for (const auto &e : scat) {
+        exist_cols.push_back(e.first);
+        exist_imp.push_back(fp4_value(e.second));
+        exist_is_b4.push_back(false);
+    }
+    for (const auto &t : btiles)
+        for (uint32_t lj = 0; lj < 4; ++lj) {
+            const uint8_t b = t.second[lj * 4 + li];
+            const uint32_t col = t.first * 4 + lj;
+            if (b == 0 || col >= (uint32_t)L.n_out) continue;
+            exist_cols.push_back(col);
+            exist_imp.push_back(fp4_value(b >> 4));
+            exist_is_b4.push_back(true);
+        }
+    const size_t n_exist = exist_cols.size();
+    const bool has_probes = !L.probe_r.empty();
+    if (n_exist == 0 && !has_probes) return false;
+    std::vector<uint32_t> probe_cols;
+    std::vector<float> probe_scores;
+    for (int64_t p = 0; p < L.probe_nnz; ++p)
+        if ((int64_t)L.probe_r[(size_t)p] == row) {
+            probe_cols.push_back((uint32_t)L.probe_c[(size_t)p]);
+            probe_scores.push_back(L.probe_v[(size_t)p]);
+        }
+    // removals: lowest importance first, below the cutoff (importance floored
+    // at eps for this test only) or beyond the row's capacity, at most
+    // max_prune_per_step of them; applied in descending column order
+    std::vector<size_t> by_imp(n_exist);
+    std::iota(by_imp.begin(), by_imp.end(), 0);
+    std::sort(by_imp.begin(), by_imp.end(), [&](size_t a, size_t b) { return exist_imp[a] < exist_imp[b]; });
+    struct Removal { uint32_t col; bool is_b4; };
+    std::vector<Removal> to_remove;
+    const size_t max_rw = (size_t)max_row_weights, max_prune = (size_t)max_prune_per_step;
+    for (size_t rank = 0; rank < n_exist && to_remove.size() < max_prune; ++rank) {
+        const size_t k = by_imp[rank];
+        const size_t keep = n_exist - to_remove.size();
+        if (std::max(exist_imp[k], importance_eps) < importance_cutoff || keep > max_rw)
+            to_remove.push_back({exist_cols[k], exist_is_b4[k]});
+    }
+    std::sort(to_remove.begin(), to_remove.end(), [](const Removal &a, const Removal &b) { return a.col > b.col; });
+    // inserts: the row's probes by descending score that are not stored, up
+    // to the capacity the removals leave (unsigned, as the reference computes it)
+    std::vector<uint32_t> add_cols;
+    std::vector<float> add_scores;
+    {
+        std::unordered_set<uint32_t> exist_set(exist_cols.begin(), exist_cols.end());
+        std::vector<size_t> pidx(probe_cols.size());
+        std::iota(pidx.begin(), pidx.end(), 0);
+        std::sort(pidx.begin(), pidx.end(), [&](size_t a, size_t b) { return probe_scores[a] > probe_scores[b]; });
+        const size_t slots = max_rw - (n_exist - to_remove.size());
+        for (size_t p : pidx) {
+            if (add_cols.size() >= slots) break;
+            if (!exist_set.count(probe_cols[p])) {
+                add_cols.push_back(probe_cols[p]);
+                add_scores.push_back(probe_scores[p]);
+            }
+        }
+    }
+    // replay the removals on the block row's tiles: the ones the reference
+    // carries out
+    std::vector<uint64_t> prune_keys;
+    for (const auto &re : to_remove) {
+        if (re.is_b4) {
+            auto it = btiles.find(re.col / 4);
+            const uint32_t s = (re.col % 4) * 4 + li;
+            if (it == btiles.end() || it->second[s] == 0) continue;
+            it->second[s] = 0;
+            prune_keys.push_back(((uint64_t)row << 32) | re.col);
+            int live = 0;
+            for (uint8_t b : it->second) live += b != 0;
+            if (live < 2) btiles.erase(it);  // demoted: its other slot is scattered now
+        } else {
+            prune_keys.push_back(((uint64_t)row << 32) | re.col);
+        }
+    }
+    // out_degree as the reference keeps it
+    const int64_t n_edit = (int64_t)(to_remove.size() + add_cols.size());
+    if (n_edit > 0) {
+        ensure_out_deg(L, true);
+        std::vector<int32_t> ecol, edelta;
+        for (const auto &re : to_remove) {
+            ecol.push_back((int32_t)re.col);
+            edelta.push_back(-1);
+        }
+        for (uint32_t c : add_cols) {
+            ecol.push_back((int32_t)c);
+            edelta.push_back(1);
+        }
+        DevBuf<int32_t> dcol, ddelta;
+        dcol.ensure((size_t)n_edit);
+        ddelta.ensure((size_t)n_edit);
+        SILI_HIP(hipMemcpyAsync(dcol.p, ecol.data(), (size_t)n_edit * 4, hipMemcpyHostToDevice, L.stream));
+        SILI_HIP(hipMemcpyAsync(ddelta.p, edelta.data(), (size_t)n_edit * 4, hipMemcpyHostToDevice, L.stream));
+        launch(k_deg_edit, dim3(nblk(n_edit)), dim3(TPB), 0, L.stream, L.out_deg.p, (const int32_t *)dcol.p,
+               (const int32_t *)ddelta.p, n_edit);
+        SILI_HIP(hipGetLastError());
+        SILI_HIP(hipStreamSynchronize(L.stream));
+    }
+    if (prune_keys.empty() && add_cols.empty()) return true;
+    // the device edit: explicit removals, then the inserts (weight 0,
+    // importance = the probe score, delta_csr_memory.hpp:1234)
+    std::vector<int32_t> cr(add_cols.size(), (int32_t)row), cc(add_cols.begin(), add_cols.end());
+    std::vector<float> cv(add_cols.size(), 0.0f);
+    const bool tracked = L.out_deg_tracked;
+    synapto_apply(L, 0.0f, true, prune_keys.data(), (int64_t)prune_keys.size(), cr.data(), cc.data(), cv.data(),
+                  add_scores.data(), (int64_t)add_cols.size(), 0, nullptr);
+    L.out_deg_tracked = tracked;
+    return true;
+}
+
+void get_out_degree(Layer &L, int32_t *out) {
+    if (L.n_out == 0) return;
+    ensure_out_deg(L, false);
+    SILI_HIP(hipMemcpyAsync(out, L.out_deg.p, (size_t)L.n_out * 4, hipMemcpyDeviceToHost, L.stream));
+    SILI_HIP(hipStreamSynchronize(L.stream));
+}
+
+}  // namespace sili

@@ -429,13 +429,38 @@ class Layer {
     py::array_t<float> weights_vals() { return absolute()[2].cast<py::array_t<float>>(); }
     py::array_t<float> importance() { return absolute()[3].cast<py::array_t<float>>(); }
     py::array_t<int32_t> out_degree() {
-        auto ix = indices();
         py::array_t<int32_t> d((py::ssize_t)n_out_);
-        auto dm = d.mutable_unchecked<1>();
-        for (py::ssize_t c = 0; c < (py::ssize_t)n_out_; ++c) dm(c) = 0;
-        auto iu = ix.unchecked<1>();
-        for (py::ssize_t k = 0; k < ix.size(); ++k) dm(iu(k))++;
+        if (n_out_ > 0) ck(sili_get_out_degree(L_, d.mutable_data()));
         return d;
+    }
+
+    // ---- the reference's synaptogenesis policy (sili/cpu_backend.cpp:606-634) ----
+    void build_probes(int64_t k, bool per_row) {
+        flush();
+        ck(sili_build_probes(L_, k, per_row ? 1 : 0));
+    }
+    bool synap_row_step(int64_t current_row, float importance_cutoff, int64_t max_row_weights,
+                        int64_t max_prune_per_step, float importance_eps) {
+        flush();
+        int did = 0;
+        ck(sili_synap_row_step(L_, &current_row, importance_cutoff, max_row_weights, max_prune_per_step,
+                               importance_eps, &did));
+        return did != 0;
+    }
+    bool synap_step(float importance_cutoff, int64_t max_row_weights, int64_t max_prune_per_step,
+                    float importance_eps) {
+        flush();
+        int did = 0;
+        ck(sili_synap_step(L_, importance_cutoff, max_row_weights, max_prune_per_step, importance_eps, &did));
+        return did != 0;
+    }
+    py::tuple get_probes() {
+        int64_t n = 0;
+        ck(sili_get_probes(L_, &n, nullptr, nullptr, nullptr, 0));
+        py::array_t<int32_t> r((py::ssize_t)n), c((py::ssize_t)n);
+        py::array_t<float> v((py::ssize_t)n);
+        ck(sili_get_probes(L_, &n, r.mutable_data(), c.mutable_data(), v.mutable_data(), n));
+        return py::make_tuple(r, c, v);
     }
     py::object last_input() {
         if (last_batch_ == 0) return py::none();
@@ -672,6 +697,12 @@ PYBIND11_MODULE(_sili_hip, m) {
         .def_property_readonly("num_cpus", &Layer::num_cpus)
         .def_property_readonly("nnz", &Layer::nnz)
         .def_property_readonly("out_degree", &Layer::out_degree)
+        .def("build_probes", &Layer::build_probes, py::arg("k"), py::arg("per_row") = false)
+        .def("synap_row_step", &Layer::synap_row_step, py::arg("current_row"), py::arg("importance_cutoff"),
+             py::arg("max_row_weights"), py::arg("max_prune_per_step") = 8, py::arg("importance_eps") = 1e-3f)
+        .def("synap_step", &Layer::synap_step, py::arg("importance_cutoff"), py::arg("max_row_weights"),
+             py::arg("max_prune_per_step") = 8, py::arg("importance_eps") = 1e-3f)
+        .def("get_probes", &Layer::get_probes)
         .def_property_readonly("last_input", &Layer::last_input)
         .def_property_readonly("weights_vals", &Layer::weights_vals)
         .def_property_readonly("importance", &Layer::importance)

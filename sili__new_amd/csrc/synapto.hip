@@ -105,6 +105,22 @@ __global__ void k_syn_keys(int64_t Ns, const uint32_t *srow, const uint32_t *sco
     absw[i] = __builtin_bit_cast(uint32_t, w) & 0x7FFFFFFFu;
 }
 
+// Explicit prune list: the slot of every (row, col) key, looked up in the
+// (row, col)-sorted slot keys; a key that is not stored sets *missing.
+__global__ void k_find_slots(const uint64_t *keys, int64_t n, const uint64_t *rc_sorted, const uint32_t *perm,
+                             int64_t M, uint32_t *order, int *missing) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= n) return;
+    const uint64_t key = keys[i];
+    const int64_t p = lower_bound_u64(rc_sorted, M, key);
+    if (p < M && rc_sorted[p] == key) {
+        order[i] = perm[p];
+    } else {
+        order[i] = 0u;
+        atomicOr(missing, 1);
+    }
+}
+
 // Number of live synapses: the KEY_NONE entries sort last.
 __global__ void k_count_live(const uint64_t *rc_sorted, int64_t n, unsigned long long *out) {
     if (blockIdx.x == 0 && threadIdx.x == 0) *out = (unsigned long long)lower_bound_u64(rc_sorted, n, KEY_NONE);
@@ -355,6 +371,17 @@ int64_t compact_positions(Layer &L, const uint32_t *flag, uint32_t *pos, int64_t
 void synapto_step(Layer &L, float prune_frac, const int32_t *cand_r, const int32_t *cand_c,
                   const float *cand_v, const float *cand_s, int64_t n_cand, int default_imp,
                   int64_t *stats) {
+    L.out_deg_tracked = false;  // a structure of this build's own policy: counted afresh
+    synapto_apply(L, prune_frac, false, nullptr, 0, cand_r, cand_c, cand_v, cand_s, n_cand, default_imp, stats);
+}
+
+// The bulk pipeline.  explicit_prune false: prune the round(prune_frac * N)
+// smallest |w| and regrow as many candidates.  True: prune exactly the
+// n_prune stored synapses (row << 32 | col keys, host memory; none when
+// n_prune is 0) and grow every valid candidate.
+void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64_t *prune_keys, int64_t n_prune,
+                   const int32_t *cand_r, const int32_t *cand_c, const float *cand_v, const float *cand_s,
+                   int64_t n_cand, int default_imp, int64_t *stats) {
     hipStream_t st = L.stream;
     const int64_t Ns = L.W.nnz, T = L.B4.ntiles;
     const int64_t n_in = L.n_in, n_out = L.n_out;
@@ -406,13 +433,37 @@ void synapto_step(Layer &L, float prune_frac, const int32_t *cand_r, const int32
         // (row, col) order, then a stable sort by |w| bits
         device_sort_pairs_u64(L, rc.p, rc_sorted.p, iota.p, perm_rc.p, M, 64);
         launch(k_count_live, dim3(1), dim3(64), 0, st, (const uint64_t *)rc_sorted.p, M, counters.p);
-        launch(k_gather_u32_by, dim3(nblk(M)), dim3(TPB), 0, st, (const uint32_t *)absw.p,
-               (const uint32_t *)perm_rc.p, M, absw_rc.p);
         SILI_HIP(hipGetLastError());
-        device_sort_pairs_u32(L, absw_rc.p, absw_sorted.p, perm_rc.p, order.p, M, 32);
+        if (!explicit_prune) {
+            launch(k_gather_u32_by, dim3(nblk(M)), dim3(TPB), 0, st, (const uint32_t *)absw.p,
+                   (const uint32_t *)perm_rc.p, M, absw_rc.p);
+            SILI_HIP(hipGetLastError());
+            device_sort_pairs_u32(L, absw_rc.p, absw_sorted.p, perm_rc.p, order.p, M, 32);
+        }
     }
     const int64_t N = (int64_t)read_back(counters.p, st);  // scattered + live block4 slots
-    const int64_t k = std::min<int64_t>(N, (int64_t)std::llround((double)prune_frac * (double)N));
+    int64_t k = 0;
+    if (explicit_prune) {
+        if (n_prune > 0) {
+            if (n_prune > M) throw_error(SILI_ERR_INVALID, "synapto: more prune keys than stored synapses");
+            DevBuf<uint64_t> dkeys;
+            dkeys.ensure((size_t)n_prune);
+            SILI_HIP(hipMemcpyAsync(dkeys.p, prune_keys, (size_t)n_prune * 8, hipMemcpyHostToDevice, st));
+            L.scratch.flag.ensure(4, 0);
+            SILI_HIP(hipMemsetAsync(L.scratch.flag.p, 0, 4 * sizeof(int), st));
+            launch(k_find_slots, dim3(nblk(n_prune)), dim3(TPB), 0, st, (const uint64_t *)dkeys.p, n_prune,
+                   (const uint64_t *)rc_sorted.p, (const uint32_t *)perm_rc.p, M, order.p, L.scratch.flag.p);
+            SILI_HIP(hipGetLastError());
+            int missing = 0;
+            SILI_HIP(hipMemcpyAsync(&missing, L.scratch.flag.p, sizeof(int), hipMemcpyDeviceToHost, st));
+            SILI_HIP(hipStreamSynchronize(st));
+            if (missing) throw_error(SILI_ERR_RUNTIME, "synapto: a synapse to prune is not stored");
+        }
+        k = n_prune;
+    } else {
+        k = std::min<int64_t>(N, (int64_t)std::llround((double)prune_frac * (double)N));
+    }
+    const int64_t k_grow = explicit_prune ? n_cand : k;  // candidates that may grow
 
     // -- prune ---------------------------------------------------------------
     DevBuf<uint8_t> s_removed, touched, alive, dem_byte;
@@ -511,7 +562,7 @@ void synapto_step(Layer &L, float prune_frac, const int32_t *cand_r, const int32
         SILI_HIP(hipGetLastError());
         device_exclusive_scan_u32(L, first.p, rank.p, n_cand);
         launch(k_syn_insert, dim3(g), dim3(TPB), 0, st, n_cand, (const uint32_t *)first.p,
-               (const uint32_t *)rank.p, k, (const int32_t *)dcr.p, (const int32_t *)dcc.p,
+               (const uint32_t *)rank.p, k_grow, (const int32_t *)dcr.p, (const int32_t *)dcc.p,
                (const float *)dcv.p, cand_s ? (const float *)dcs.p : nullptr, (uint32_t)default_imp, sc,
                (const uint64_t *)tkey.p, T, (const uint8_t *)alive.p, tbytes.p, bcols, key2.p + (Ns + T),
                byte2.p + (Ns + T), win.p, counters.p + 2);

@@ -572,15 +572,17 @@ __global__ __launch_bounds__(256) void k_dead_rows(const uint32_t *__restrict__ 
 // output_scale's step (linear_disldo.hpp:2050-2080): one thread per column;
 // its synapses' column-gradient terms are summed in shadow order (the
 // column's synapses by ascending row, the reference's single-thread order).
+// deg: out_degree as the reference's synaptogenesis policy keeps it, or NULL
+// (then the column's stored synapses).
 __global__ __launch_bounds__(256) void k_train_cols(const uint32_t *__restrict__ t_elem_start,
                                                     const uint32_t *__restrict__ perm, int64_t n_out, int rank,
                                                     const float *__restrict__ mterm, float *os, float *os_imp,
                                                     uint32_t *os_step, float lr, float beta2, float eps,
-                                                    const float *pow_tab) {
+                                                    const float *pow_tab, const int32_t *__restrict__ out_deg) {
     const int64_t c = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (c >= n_out) return;
     const uint32_t s0 = t_elem_start[c], s1 = t_elem_start[c + 1];
-    const uint32_t deg = s1 - s0;
+    const int64_t deg = out_deg ? (int64_t)out_deg[c] : (int64_t)(s1 - s0);
     if (deg == 0) return;
     const float col_eff_lr = lr / (float)deg;
     for (int k = 0; k < rank; ++k) {
@@ -763,7 +765,8 @@ void launch_train_cols(Layer &L, const TrainParams &p, hipStream_t st) {
     ProfScope ps("train_cols", st);
     launch(k_train_cols, dim3(nblk(L.n_out)), dim3(TPB), 0, st, (const uint32_t *)L.Wt.elem_start.p,
            (const uint32_t *)L.Wt_perm.p, L.n_out, L.rank, (const float *)L.mterm.p, L.os.p, L.os_imp.p, L.os_step.p,
-           p.lr, p.beta2, p.eps, (const float *)L.pow_tab.p);
+           p.lr, p.beta2, p.eps, (const float *)L.pow_tab.p,
+           L.out_deg_tracked ? (const int32_t *)L.out_deg.p : nullptr);
     SILI_HIP(hipGetLastError());
 }
 
