@@ -45,6 +45,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--synapto-reps", type=int, default=5, help="config 3: timed synaptogenesis steps")
     p.add_argument("--c4-batches", default="1,8,128", help="config 4: token batches to time")
+    p.add_argument("--synap-cycles", type=int, default=0,
+                   help="config 1: also time N cycles of the reference's synaptogenesis policy "
+                        "(build_probes + synap_step)")
     p.add_argument("--train-lr", type=float, default=0.0,
                    help="config 1: the backward carries the optimizer update at this learning rate "
                         "(stochastic re-quantization, as the reference's SparseLinearLayer)")
@@ -428,6 +431,54 @@ def time_synapto(hip, wl, reps):
             "last_stats": stats}
 
 
+def time_synap_policy(hip, wl, reps, seconds):
+    """The reference's synaptogenesis cycle as DISLDOLayer.synaptogenesis
+    runs it (sili/sparse_rnn.py:216-219): build_probes(4) + synap_step, on
+    config 1 after one backward fills the activity accumulators.  Wall time
+    per cycle on the GPU layer (host decisions, device edit and rebuild), and
+    the reference's own functions (oracle/_ref) on the same layer."""
+    from oracle import RefLayer, have_ref
+    L = hip.SparseLinearLayerDeterministic(wl.n_in, wl.n_out, wl.nnz + 4096)
+    L.load_weights(wl.ptrs, wl.cols, wl.q)
+    L.set_value_scales(wl.value_scale)
+    x, g = wl.x.astype(np.float32), wl.g.astype(np.float32)
+    L.forward_dense(x)
+    L.backward_dense(g, 0.0)
+    ai, ag = L.neuron_input_accum.copy(), L.neuron_grad_accum.copy()
+    L.synchronize()
+    cutoff, max_rw = 0.3, 200
+    L.build_probes(4)
+    L.synap_step(cutoff, max_rw)  # warm-up
+    times, edits = [], 0
+    for i in range(reps):
+        n0 = L.info()["nnz_scattered"]
+        t0 = time.perf_counter()
+        L.build_probes(4)
+        L.synap_step(cutoff, max_rw)
+        L.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+        edits += L.info()["nnz_scattered"] != n0
+    out = {"gpu_ms_median": round(float(np.median(times)), 3), "gpu_ms_min": round(min(times), 3), "reps": reps,
+           "cycles_that_edited": edits,
+           "cycle": "build_probes(4) + synap_step(importance_cutoff 0.3, max_row_weights 200)"}
+    if have_ref():
+        R = RefLayer(wl.n_in, wl.n_out, wl.ptrs, wl.cols, wl.q, blank_fraction=1.0)
+        rt, cur = [], 0
+        t_end = time.perf_counter() + seconds
+        try:
+            while len(rt) < reps and time.perf_counter() < t_end:
+                t0 = time.perf_counter()
+                R.build_probes(ai, ag, 4)
+                _, cur = R.synap_row_step(cur, cutoff, max_rw)
+                rt.append((time.perf_counter() - t0) * 1e3)
+        except RuntimeError as e:  # a row out of its reserved space
+            out["reference_error"] = str(e)
+        if rt:
+            out["reference_ms_median"] = round(float(np.median(rt)), 4)
+        out["reference_note"] = "the reference's delta_csr_build_probes + delta_csr_synap_row_step, one host thread"
+    return out
+
+
 # config 4: the 7 layer shapes of a folded 40 x Mistral-24B-like block stack
 # (SURVEY 8(d)): (name, n_in, n_out); 10% of each kept, |N(0, 0.02)| tail above
 # its 95th percentile, per-row FP4 scales, decode forward at batch 1 / 8 / 128
@@ -735,6 +786,9 @@ def main():
     if cfg == 3 and a.synapto_reps > 0:
         pool.clear()
         out["synapto_gpu"] = time_synapto(hip, wl, a.synapto_reps)
+    if cfg == 1 and a.synap_cycles > 0:
+        pool.clear()
+        out["synap_policy"] = time_synap_policy(hip, wl, a.synap_cycles, a.cpu_seconds)
     if a.no_cpu_baseline:
         out["cpu_baseline"] = None
     elif train_lr:

@@ -245,8 +245,8 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
                     DevBuf<SegDesc> &seg, const char *what, DevBuf<uint32_t> *split_rows = nullptr) {
     Encoded out;
     hipStream_t st = L.stream;
-    DevBuf<uint64_t> len, pos;
-    DevBuf<uint32_t> rowid, segcnt, segoff;
+    TmpBuf<uint64_t> len(L, SILI_TMPKEY(len)), pos(L, SILI_TMPKEY(pos));
+    TmpBuf<uint32_t> rowid(L, SILI_TMPKEY(rowid)), segcnt(L, SILI_TMPKEY(segcnt)), segoff(L, SILI_TMPKEY(segoff));
     len.ensure((size_t)N + 1);
     pos.ensure((size_t)N + 1);
     rowid.ensure((size_t)N + 1);
@@ -275,7 +275,7 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
                            pos.p, idx.p);
         SILI_HIP(hipGetLastError());
     }
-    DevBuf<uint32_t> n_empty;
+    TmpBuf<uint32_t> n_empty(L, SILI_TMPKEY(n_empty));
     n_empty.ensure(1);
     SILI_HIP(hipMemsetAsync(n_empty.p, 0, sizeof(uint32_t), st));
     launch(k_row_starts, dim3(nblk(rows + 1)), dim3(TPB), 0, st, d_ptrs, rows, N, pos.p,
@@ -303,7 +303,7 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
     if (out.has_split && split_rows) {
         // list of the rows that span several work items (their outputs need
         // zeroing before the atomically combined partial sums)
-        DevBuf<uint32_t> flag, fpos;
+        TmpBuf<uint32_t> flag(L, SILI_TMPKEY(flag)), fpos(L, SILI_TMPKEY(fpos));
         flag.ensure((size_t)rows + 1);
         fpos.ensure((size_t)rows + 1);
         launch(k_split_flags, dim3(nblk(rows + 1)), dim3(TPB), 0, st, (const uint32_t *)segcnt.p, rows, flag.p);
@@ -396,8 +396,8 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
                   DScatter &dst) {
     hipStream_t st = L.stream;
     const int64_t N = src.nnz;
-    DevBuf<uint32_t> keys_out, perm_in, perm, trows, ptrs;
-    DevBuf<uint8_t> tbytes;
+    TmpBuf<uint32_t> keys_out(L, SILI_TMPKEY(keys_out)), perm_in(L, SILI_TMPKEY(perm_in)), perm(L, SILI_TMPKEY(perm)), trows(L, SILI_TMPKEY(trows)), ptrs(L, SILI_TMPKEY(ptrs));
+    TmpBuf<uint8_t> tbytes(L, SILI_TMPKEY(tbytes));
     keys_out.ensure((size_t)N + 1);
     perm_in.ensure((size_t)N + 1);
     perm.ensure((size_t)N + 1);
@@ -437,8 +437,13 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
     // a training layer keeps the permutation (shadow entry -> canonical
     // entry): its updates rewrite the canonical value bytes and copy them over
     if (&dst == &L.Wt) {
-        if (L.keep_perm && N > 0) L.Wt_perm = std::move(perm);
-        else L.Wt_perm.reset();
+        if (L.keep_perm && N > 0) {
+            L.Wt_perm.ensure((size_t)N);
+            SILI_HIP(hipMemcpyAsync(L.Wt_perm.p, perm.p, (size_t)N * 4, hipMemcpyDeviceToDevice, st));
+            SILI_HIP(hipStreamSynchronize(st));
+        } else {
+            L.Wt_perm.reset();
+        }
     }
 }
 
@@ -505,7 +510,7 @@ static void build_b4_orientation(Layer &L, DBlock4 &dst, int64_t N, int64_t brow
                                  const uint32_t *d_minor, const uint32_t *d_perm,
                                  const uint8_t *d_src_tiles, bool transpose) {
     hipStream_t st = L.stream;
-    DevBuf<uint32_t> ptrs;
+    TmpBuf<uint32_t> ptrs(L, SILI_TMPKEY(ptrs));
     ptrs.ensure((size_t)brows + 1);
     launch(k_ptrs_from_sorted, dim3(nblk(brows + 1)), dim3(TPB), 0, st, d_major, N, brows,
                        ptrs.p);
@@ -585,8 +590,8 @@ void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_
     hipStream_t st = L.stream;
     const int64_t brows = (L.n_in + 3) / 4, bcols = (L.n_out + 3) / 4;
     const int64_t N = n_tiles;
-    DevBuf<uint64_t> key, key_sorted;
-    DevBuf<uint32_t> perm_in, perm, major, minor;
+    TmpBuf<uint64_t> key(L, SILI_TMPKEY(key)), key_sorted(L, SILI_TMPKEY(key_sorted));
+    TmpBuf<uint32_t> perm_in(L, SILI_TMPKEY(perm_in)), perm(L, SILI_TMPKEY(perm)), major(L, SILI_TMPKEY(major)), minor(L, SILI_TMPKEY(minor));
     key.ensure((size_t)N + 1);
     key_sorted.ensure((size_t)N + 1);
     perm_in.ensure((size_t)N + 1);

@@ -4,6 +4,9 @@
 #include "common.hpp"
 
 #include <string>
+#include <unordered_map>
+
+#include <string>
 #include <utility>
 #include <vector>
 
@@ -200,12 +203,45 @@ struct Layer {
     int64_t synap_cursor = 0;
     DevBuf<int32_t> out_deg;
     bool out_deg_tracked = false;
+    // Temporaries of the structure rebuild, kept between calls while
+    // keep_temps is set (the synaptogenesis policy rebuilds after every edit:
+    // allocating and freeing them each call would cost more than the work).
+    // They are used on the layer's stream only, in stream order.
+    std::unordered_map<std::string, DevBuf<uint8_t>> temps;
+    bool keep_temps = false;
     bool stochastic_rounding = true;
     uint64_t rng_seed = 0x5EEDull, rng_calls = 0;
     int64_t train_calls = 0;
     uint32_t seg_len = 512;     // max index bytes per decode work item (scattered)
     uint32_t seg_len_b4 = 128;  // max block-index bytes per decode work item (block4)
 };
+
+// A temporary device buffer of a structure rebuild: its own allocation, or,
+// while L.keep_temps is set, the layer's kept buffer for this call site.
+template <typename T>
+struct TmpBuf {
+    T *p = nullptr;
+    TmpBuf(Layer &L, const char *key) : L_(&L), key_(key) {}
+    TmpBuf(const TmpBuf &) = delete;
+    TmpBuf &operator=(const TmpBuf &) = delete;
+    void ensure(size_t count, size_t pad = 64) {
+        if (L_->keep_temps) {
+            DevBuf<uint8_t> &b = L_->temps[key_];
+            b.ensure(count * sizeof(T) + pad, 0);
+            p = reinterpret_cast<T *>(b.p);
+        } else {
+            own_.ensure(count, pad);
+            p = own_.p;
+        }
+    }
+   private:
+    Layer *L_;
+    const char *key_;
+    DevBuf<T> own_;
+};
+#define SILI_STR2(x) #x
+#define SILI_STR(x) SILI_STR2(x)
+#define SILI_TMPKEY(name) __FILE__ ":" SILI_STR(__LINE__) ":" #name
 
 // ---- builders (build.hip) ---------------------------------------------------
 // Encode a store from row-sorted entries: ptrs[rows+1] (device), cols[N]

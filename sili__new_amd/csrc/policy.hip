@@ -196,6 +196,7 @@ void build_probes(Layer &L, int64_t k, bool per_row) {
 bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t max_row_weights,
                     int64_t max_prune_per_step, float importance_eps) {
     if (L.n_in == 0) return false;
+    L.keep_temps = true;  // a layer that runs the policy rebuilds often: keep the rebuild's temporaries
     const int64_t row = cursor % L.n_in;
     cursor = (cursor + 1) % L.n_in;
     const uint32_t br = (uint32_t)(row / 4), li = (uint32_t)(row % 4);
@@ -292,7 +293,7 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
             ecol.push_back((int32_t)c);
             edelta.push_back(1);
         }
-        DevBuf<int32_t> dcol, ddelta;
+        TmpBuf<int32_t> dcol(L, SILI_TMPKEY(dcol)), ddelta(L, SILI_TMPKEY(ddelta));
         dcol.ensure((size_t)n_edit);
         ddelta.ensure((size_t)n_edit);
         SILI_HIP(hipMemcpyAsync(dcol.p, ecol.data(), (size_t)n_edit * 4, hipMemcpyHostToDevice, L.stream));

@@ -394,23 +394,23 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
         : ScaleView{L.vs.p, L.os.p, L.rank};
 
     // -- decode both stores --------------------------------------------------
-    DevBuf<uint32_t> srow, scol, tbr, tbc;
+    TmpBuf<uint32_t> srow(L, SILI_TMPKEY(srow)), scol(L, SILI_TMPKEY(scol)), tbr(L, SILI_TMPKEY(tbr)), tbc(L, SILI_TMPKEY(tbc));
     srow.ensure((size_t)Ns + 1);
     scol.ensure((size_t)Ns + 1);
     tbr.ensure((size_t)T + 1);
     tbc.ensure((size_t)T + 1);
     if (Ns > 0) decode_scattered(L, srow.p, scol.p);
     if (T > 0) launch_decode_b4(L.B4.plan(), tbr.p, tbc.p, st);
-    DevBuf<uint8_t> tbytes;  // tile bytes being edited (canonical order)
+    TmpBuf<uint8_t> tbytes(L, SILI_TMPKEY(tbytes));  // tile bytes being edited (canonical order)
     tbytes.ensure((size_t)T * 16 + 1);
     if (T > 0) SILI_HIP(hipMemcpyAsync(tbytes.p, L.B4.tiles.p, (size_t)T * 16, hipMemcpyDeviceToDevice, st));
-    DevBuf<uint64_t> tkey;  // window keys of the canonical tiles (ascending)
+    TmpBuf<uint64_t> tkey(L, SILI_TMPKEY(tkey));  // window keys of the canonical tiles (ascending)
     tkey.ensure((size_t)T + 1);
 
     // -- select: order by (|w| bits, row, col) -------------------------------
-    DevBuf<uint64_t> rc, rc_sorted;
-    DevBuf<uint32_t> absw, absw_rc, absw_sorted, iota, perm_rc, order;
-    DevBuf<unsigned long long> counters;  // live slots, demoted, grown
+    TmpBuf<uint64_t> rc(L, SILI_TMPKEY(rc)), rc_sorted(L, SILI_TMPKEY(rc_sorted));
+    TmpBuf<uint32_t> absw(L, SILI_TMPKEY(absw)), absw_rc(L, SILI_TMPKEY(absw_rc)), absw_sorted(L, SILI_TMPKEY(absw_sorted)), iota(L, SILI_TMPKEY(iota)), perm_rc(L, SILI_TMPKEY(perm_rc)), order(L, SILI_TMPKEY(order));
+    TmpBuf<unsigned long long> counters(L, SILI_TMPKEY(counters));  // live slots, demoted, grown
     counters.ensure(4);
     rc.ensure((size_t)M + 1);
     rc_sorted.ensure((size_t)M + 1);
@@ -446,7 +446,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
     if (explicit_prune) {
         if (n_prune > 0) {
             if (n_prune > M) throw_error(SILI_ERR_INVALID, "synapto: more prune keys than stored synapses");
-            DevBuf<uint64_t> dkeys;
+            TmpBuf<uint64_t> dkeys(L, SILI_TMPKEY(dkeys));
             dkeys.ensure((size_t)n_prune);
             SILI_HIP(hipMemcpyAsync(dkeys.p, prune_keys, (size_t)n_prune * 8, hipMemcpyHostToDevice, st));
             L.scratch.flag.ensure(4, 0);
@@ -466,9 +466,9 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
     const int64_t k_grow = explicit_prune ? n_cand : k;  // candidates that may grow
 
     // -- prune ---------------------------------------------------------------
-    DevBuf<uint8_t> s_removed, touched, alive, dem_byte;
-    DevBuf<uint64_t> pruned, pruned_sorted, dem_key;
-    DevBuf<uint32_t> pruned_v, pruned_vs;
+    TmpBuf<uint8_t> s_removed(L, SILI_TMPKEY(s_removed)), touched(L, SILI_TMPKEY(touched)), alive(L, SILI_TMPKEY(alive)), dem_byte(L, SILI_TMPKEY(dem_byte));
+    TmpBuf<uint64_t> pruned(L, SILI_TMPKEY(pruned)), pruned_sorted(L, SILI_TMPKEY(pruned_sorted)), dem_key(L, SILI_TMPKEY(dem_key));
+    TmpBuf<uint32_t> pruned_v(L, SILI_TMPKEY(pruned_v)), pruned_vs(L, SILI_TMPKEY(pruned_vs));
     s_removed.ensure((size_t)Ns + 1);
     touched.ensure((size_t)T + 1);
     alive.ensure((size_t)T + 1);
@@ -502,9 +502,9 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
 
     // -- scattered set after prune + demote (sorted for lookups) --------------
     const int64_t M2 = Ns + T + n_cand;
-    DevBuf<uint64_t> key2, key2_sorted, set1_sorted;
-    DevBuf<uint8_t> byte2, byte2_sorted, removed2;
-    DevBuf<uint32_t> iota2, perm2;
+    TmpBuf<uint64_t> key2(L, SILI_TMPKEY(key2)), key2_sorted(L, SILI_TMPKEY(key2_sorted)), set1_sorted(L, SILI_TMPKEY(set1_sorted));
+    TmpBuf<uint8_t> byte2(L, SILI_TMPKEY(byte2)), byte2_sorted(L, SILI_TMPKEY(byte2_sorted)), removed2(L, SILI_TMPKEY(removed2));
+    TmpBuf<uint32_t> iota2(L, SILI_TMPKEY(iota2)), perm2(L, SILI_TMPKEY(perm2));
     key2.ensure((size_t)M2 + 1);
     key2_sorted.ensure((size_t)M2 + 1);
     set1_sorted.ensure((size_t)(Ns + T) + 1);
@@ -523,10 +523,10 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
     }
 
     // -- candidates: first valid ones in list order ---------------------------
-    DevBuf<int32_t> dcr, dcc;
-    DevBuf<float> dcv, dcs;
-    DevBuf<uint64_t> ckey, ckey_sorted, win, win_sorted;
-    DevBuf<uint32_t> cidx, cidx_sorted, first, rank, wv, wvs;
+    TmpBuf<int32_t> dcr(L, SILI_TMPKEY(dcr)), dcc(L, SILI_TMPKEY(dcc));
+    TmpBuf<float> dcv(L, SILI_TMPKEY(dcv)), dcs(L, SILI_TMPKEY(dcs));
+    TmpBuf<uint64_t> ckey(L, SILI_TMPKEY(ckey)), ckey_sorted(L, SILI_TMPKEY(ckey_sorted)), win(L, SILI_TMPKEY(win)), win_sorted(L, SILI_TMPKEY(win_sorted));
+    TmpBuf<uint32_t> cidx(L, SILI_TMPKEY(cidx)), cidx_sorted(L, SILI_TMPKEY(cidx_sorted)), first(L, SILI_TMPKEY(first)), rank(L, SILI_TMPKEY(rank)), wv(L, SILI_TMPKEY(wv)), wvs(L, SILI_TMPKEY(wvs));
     if (n_cand > 0) {
         dcr.ensure((size_t)n_cand);
         dcc.ensure((size_t)n_cand);
@@ -581,8 +581,8 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
                (const uint32_t *)perm2.p, M2, byte2_sorted.p);
         SILI_HIP(hipGetLastError());
     }
-    DevBuf<uint32_t> nt_flag, nt_br, nt_bc;
-    DevBuf<uint8_t> nt_bytes;
+    TmpBuf<uint32_t> nt_flag(L, SILI_TMPKEY(nt_flag)), nt_br(L, SILI_TMPKEY(nt_br)), nt_bc(L, SILI_TMPKEY(nt_bc));
+    TmpBuf<uint8_t> nt_bytes(L, SILI_TMPKEY(nt_bytes));
     nt_flag.ensure((size_t)n_cand + 1);
     nt_br.ensure((size_t)n_cand + 1);
     nt_bc.ensure((size_t)n_cand + 1);
@@ -595,8 +595,8 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
     }
 
     // -- compaction + rebuild -------------------------------------------------
-    DevBuf<uint32_t> fflag, fpos, frows, fcols, fptrs;
-    DevBuf<uint8_t> fbytes;
+    TmpBuf<uint32_t> fflag(L, SILI_TMPKEY(fflag)), fpos(L, SILI_TMPKEY(fpos)), frows(L, SILI_TMPKEY(frows)), fcols(L, SILI_TMPKEY(fcols)), fptrs(L, SILI_TMPKEY(fptrs));
+    TmpBuf<uint8_t> fbytes(L, SILI_TMPKEY(fbytes));
     fflag.ensure((size_t)M2 + 1);
     fpos.ensure((size_t)M2 + 1);
     if (M2 > 0) {
@@ -620,8 +620,8 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
     SILI_HIP(hipGetLastError());
 
     const int64_t MT = T + n_cand;
-    DevBuf<uint32_t> tflag, tpos, obr, obc;
-    DevBuf<uint8_t> obytes;
+    TmpBuf<uint32_t> tflag(L, SILI_TMPKEY(tflag)), tpos(L, SILI_TMPKEY(tpos)), obr(L, SILI_TMPKEY(obr)), obc(L, SILI_TMPKEY(obc));
+    TmpBuf<uint8_t> obytes(L, SILI_TMPKEY(obytes));
     tflag.ensure((size_t)MT + 1);
     tpos.ensure((size_t)MT + 1);
     if (MT > 0) {
