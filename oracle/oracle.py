@@ -114,7 +114,7 @@ def lib(contracted: bool = False):
                                              C.c_int64, _f32p, _f32p, _f32p, C.c_int, C.c_int]
         L.oracle_sampled_gradw.argtypes = [C.POINTER(_OracleLayerC), _f32p, _f32p, C.c_int64, _f32p,
                                            _f32p, C.c_int, C.c_int]
-        L.oracle_backward_train.argtypes = [C.POINTER(_OracleLayerC), _u8p, C.POINTER(_TrainState), _f32p, _f32p,
+        L.oracle_backward_train.argtypes = [C.POINTER(_OracleLayerC), _u8p, _u8p, C.POINTER(_TrainState), _f32p, _f32p,
                                             C.c_int64, _f32p, _f32p, _f32p, C.POINTER(_TrainParams)]
         L.oracle_backward_train.restype = C.c_int
         L.oracle_backward_sparse_train.argtypes = [C.POINTER(_OracleLayerC), _u8p, C.POINTER(_TrainState), _f32p,
@@ -180,6 +180,7 @@ def reflib():
         R.ref_layer_set_importance_scales.argtypes = [C.c_void_p, _f32p, _f32p]
         R.ref_layer_new_blank.restype = C.c_void_p
         R.ref_layer_new_blank.argtypes = [C.c_int, C.c_int, _i32p, _i32p, _f32p, _f32p, C.c_float]
+        R.ref_layer_block4_headroom.argtypes = [C.c_void_p, C.c_float, C.c_int]
         R.ref_build_probes.argtypes = [C.c_void_p, _f32p, _f32p, C.c_int, C.c_int]
         R.ref_get_probes.restype = C.c_int64
         R.ref_get_probes.argtypes = [C.c_void_p, _i32p, _i32p, _f32p, C.c_int64, C.POINTER(C.c_int)]
@@ -417,9 +418,13 @@ class HostLayer:
         P = _TrainParams(lr, int(lr_per_row_nnz), int(damp_by_importance), beta2, eps, **TRAIN_DEFAULTS,
                          variant=TRAIN_VARIANTS[variant])
         s = self._cstruct()
-        if lib(contracted).oracle_backward_train(C.byref(s), _p(self.val, _u8p), C.byref(st), _p(x, _f32p), _p(dy, _f32p),
-                                       x.shape[0], _p(dx, _f32p), _p(ai, _f32p), _p(ag, _f32p), C.byref(P)) != 0:
-            raise ValueError("backward_train: layers with block4 tiles are not supported")
+        tiles = self.tiles.copy() if self.n_tiles > 0 else None
+        if lib(contracted).oracle_backward_train(C.byref(s), _p(self.val, _u8p), _p(tiles, _u8p), C.byref(st),
+                                                 _p(x, _f32p), _p(dy, _f32p), x.shape[0], _p(dx, _f32p),
+                                                 _p(ai, _f32p), _p(ag, _f32p), C.byref(P)) != 0:
+            raise ValueError("backward_train failed")
+        if tiles is not None:
+            self.tiles[:] = tiles
         return dx, ai, ag
 
     def backward_sparse_train(self, x, dptrs, didx, dvals, batch, lr, lr_per_row_nnz=False, damp_by_importance=True,
@@ -559,6 +564,10 @@ class RefLayer:
         self.h = R.ref_layer_new_blank(self.n_in, self.n_out, _p(self._keep[0], _i32p), _p(self._keep[1], _i32p),
                                        _p(self._keep[2], _f32p), _p(self._keep[3], _f32p) if imp is not None else None,
                                        float(blank_fraction))
+
+    def block4_headroom(self, blank_fraction=0.2, min_slack_bytes=16):
+        reflib().ref_layer_block4_headroom(self.h, float(blank_fraction), int(min_slack_bytes))
+        return self
 
     def build_probes(self, acc_in, acc_grad, k, per_row=False):
         acc_in, acc_grad = _c(acc_in, np.float32), _c(acc_grad, np.float32)

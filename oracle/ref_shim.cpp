@@ -279,6 +279,14 @@ void ref_get_out_degree(void *h, int32_t *out) {
     for (int c = 0; c < L->n_out; ++c) out[c] = c < int(L->w.out_degree.size()) ? int32_t(L->w.out_degree[size_t(c)]) : 0;
 }
 
+// Reserved tile bytes per block row (delta_csr_memory.hpp:767-835): with
+// min_slack_bytes of room, a row's tiles can all turn dense without the
+// update's eviction rule (block4.hpp merge_row_workspace) firing.
+void ref_layer_block4_headroom(void *h, float blank_fraction, int min_slack_bytes) {
+    auto *L = static_cast<RefLayer *>(h);
+    block4_expand_headroom<S, FP4BiPacked, COL>(L->w, blank_fraction, size_t(min_slack_bytes));
+}
+
 // Per-row / per-column importance scales (delta_csr_types.hpp:1006-1031).
 void ref_layer_set_importance_scales(void *h, const float *is, const float *ois) {
     auto *L = static_cast<RefLayer *>(h);

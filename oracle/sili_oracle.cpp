@@ -825,10 +825,10 @@ extern "C" {
 
 // linear_disldo.hpp:466-2113 (scattered loop :624-880, dead-row bootstrap
 // :1944-2040, dx reduction :2043-2048, output_scale update :2050-2080).
-int oracle_backward_train(const OracleLayer *L, uint8_t *val, OracleTrainState *S,
+int oracle_backward_train(const OracleLayer *L, uint8_t *val, uint8_t *tiles, OracleTrainState *S,
                           const float *x, const float *dy, int64_t batch, float *dx,
                           float *acc_in, float *acc_grad, const OracleTrainParams *P) {
-    if (L->n_tiles > 0) return -1;
+    if (L->n_tiles > 0 && !tiles) return -1;
     const int64_t n_in = L->n_in, n_out = L->n_out;
     const int rank = L->rank;
     const float lr = P->lr;
@@ -941,11 +941,146 @@ int oracle_backward_train(const OracleLayer *L, uint8_t *val, OracleTrainState *
             }
         }
     }
+    // block4 tiles (linear_disldo.hpp:962-1951, FP4): every slot of a tile
+    // trains (row count n_tiles(br) * 4), after the scattered rows' scale
+    // steps, with the same bounded RMSprop step on the code (S = the
+    // rank-summed scale) and the zero-escape coefficient.  A tile whose 4
+    // columns are all in range takes the reference's 4-lane path: per batch
+    // step the row-gradient terms and dx terms of the 4 slots are summed in
+    // fp32 lane order ((t0 + t1) + t2) + t3 before the fp64 / fp32
+    // accumulation; an edge tile takes the scalar path (fp64 per term).
+    // Round to nearest; the block rows' scale step follows (:1923-1951).  The
+    // reference also evicts live slots when a block row's compressed tiles
+    // outgrow its reserved bytes (block4.hpp merge_row_workspace); that
+    // storage-budget rule is not restated (rows are taken to have room).
+    std::vector<uint32_t> b4_live(size_t(n_in), 0);
+    if (L->n_tiles > 0) {
+        const auto tl = collect_tiles(L);
+        const int64_t brows = (n_in + TILE - 1) / TILE;
+        std::vector<int64_t> nt_br(size_t(brows), 0);
+        for (const auto &t : tl) ++nt_br[size_t(t.br)];
+        for (int64_t r = 0; r < n_in; ++r) b4_live[size_t(r)] = uint32_t(nt_br[size_t(r / TILE)] * TILE);
+        if (lr != 0.0f) {
+            std::vector<double> mrow(size_t(n_in * rank), 0.0), mrow_c(size_t(n_in * rank), 0.0);
+            for (const auto &t : tl) {
+                uint8_t *td = tiles + 16 * t.t;
+                const int64_t bc = t.bc;
+                const bool full = bc * TILE + TILE <= n_out;
+                for (int li = 0; li < TILE; ++li) {
+                    const int64_t row = t.br * TILE + li;
+                    if (row >= n_in) continue;
+                    const uint32_t nnz_row = b4_live[size_t(row)];
+                    const float imp_scale = S->importance_scale ? S->importance_scale[row] : 1.0f;
+                    const float effective_lr = P->lr_per_row_nnz ? lr / static_cast<float>(nnz_row) : lr;
+                    float vs_k[4] = {0, 0, 0, 0};
+                    for (int k = 0; k < rank; ++k) vs_k[k] = vs[row * rank + k];
+                    float S4[4], cis4[4], q[4], q0[4], ci[4], osk[4][4];
+                    bool valid[4];
+                    for (int lj = 0; lj < TILE; ++lj) {
+                        const int64_t col = bc * TILE + lj;
+                        valid[lj] = col < n_out;
+                        for (int k = 0; k < 4; ++k) osk[k][lj] = 0.0f;
+                        if (!valid[lj]) {
+                            S4[lj] = cis4[lj] = q[lj] = q0[lj] = ci[lj] = 0.0f;
+                            continue;
+                        }
+                        const uint8_t b = td[lj * TILE + li];
+                        const float ois = S->output_importance_scale ? S->output_importance_scale[col] : 1.0f;
+                        float sc = 0.0f;
+                        for (int k = 0; k < rank; ++k) sc += vs_k[k] * os[col * rank + k];
+                        S4[lj] = sc;
+                        cis4[lj] = imp_scale * ois;
+                        q[lj] = q0[lj] = fp4_dec(b & 0xFu);
+                        ci[lj] = fp4_dec(b >> 4) * cis4[lj];
+                        for (int k = 0; k < rank; ++k) osk[k][lj] = os[col * rank + k];
+                    }
+                    double mr[4] = {0, 0, 0, 0}, mrc[4] = {0, 0, 0, 0};
+                    float mc[4][4] = {}, mcc[4][4] = {};
+                    for (int64_t b = 0; b < batch; ++b) {
+                        const float iv = x[b * n_in + row];
+                        float t_dx[4] = {0, 0, 0, 0}, t_r[4][4] = {}, t_rc[4][4] = {};
+                        for (int lj = 0; lj < TILE; ++lj) {
+                            if (!valid[lj]) continue;
+                            const float dyv = dy[b * n_out + bc * TILE + lj];
+                            const float g = dyv * iv;
+                            const float contrib = q0[lj] * iv;
+                            ci[lj] = bounded_update_ci(ci[lj], g, contrib, P->beta2, P->min_decay_frac, P->max_ci);
+                            q[lj] += bounded_update_cw(g, ci[lj], S4[lj], effective_lr, P->eps, P->damp_by_importance != 0,
+                                                       P->max_abs_delta);
+                            const float qf = (q[lj] == 0.0f) ? P->zero_escape_eps : q[lj];
+                            for (int k = 0; k < rank; ++k) {
+                                if (full) {
+                                    t_r[k][lj] = qf * osk[k][lj] * g;
+                                    t_rc[k][lj] = qf * osk[k][lj] * contrib;
+                                } else {
+                                    mr[k] += static_cast<double>(qf) * static_cast<double>(osk[k][lj]) * g;
+                                    mrc[k] += static_cast<double>(qf) * static_cast<double>(osk[k][lj]) * contrib;
+                                }
+                                mc[k][lj] += qf * vs_k[k] * g;
+                                mcc[k][lj] += qf * vs_k[k] * contrib;
+                            }
+                            if (full) t_dx[lj] = (q[lj] * S4[lj]) * dyv;
+                            else mdx[size_t(b * n_in + row)] += q[lj] * S4[lj] * dyv;
+                        }
+                        if (full) {
+                            for (int k = 0; k < rank; ++k) {
+                                mr[k] += static_cast<double>(((t_r[k][0] + t_r[k][1]) + t_r[k][2]) + t_r[k][3]);
+                                mrc[k] += static_cast<double>(((t_rc[k][0] + t_rc[k][1]) + t_rc[k][2]) + t_rc[k][3]);
+                            }
+                            mdx[size_t(b * n_in + row)] += ((t_dx[0] + t_dx[1]) + t_dx[2]) + t_dx[3];
+                        }
+                    }
+                    for (int k = 0; k < rank; ++k) {
+                        mrow[size_t(row * rank + k)] += mr[k];
+                        mrow_c[size_t(row * rank + k)] += mrc[k];
+                    }
+                    for (int lj = 0; lj < TILE; ++lj) {
+                        if (!valid[lj]) continue;
+                        const int64_t col = bc * TILE + lj;
+                        for (int k = 0; k < rank; ++k) {
+                            mcol[size_t(col * rank + k)] += mc[k][lj];
+                            mcol_c[size_t(col * rank + k)] += mcc[k][lj];
+                        }
+                        td[lj * TILE + li] = uint8_t((fp4_enc(ci[lj] / cis4[lj]) << 4) | fp4_enc(q[lj]));
+                    }
+                }
+            }
+            // the block rows' scale step (linear_disldo.hpp:1923-1951): every
+            // scale variant, its own finiteness guards
+            for (int64_t row = 0; row < n_in; ++row) {
+                const uint32_t nnz_row = b4_live[size_t(row)];
+                if (nnz_row == 0) continue;
+                const float scale_eff_lr = lr / static_cast<float>(nnz_row);
+                for (int k = 0; k < rank; ++k) {
+                    const double sum = mrow[size_t(row * rank + k)], sum_c = mrow_c[size_t(row * rank + k)];
+                    if (sum == 0.0 && sum_c == 0.0) continue;
+                    const float g_agg = static_cast<float>(sum), contrib_agg = static_cast<float>(sum_c);
+                    if (!std::isfinite(g_agg) || !std::isfinite(contrib_agg)) continue;
+                    const int64_t idx = row * rank + k;
+                    float &vs_imp = S->vs_importance[idx];
+                    const float new_vs_imp = P->beta2 * vs_imp + (1.0f - P->beta2) * (g_agg * g_agg + contrib_agg * contrib_agg);
+                    if (!std::isfinite(new_vs_imp)) continue;
+                    uint32_t &step = S->vs_step[idx];
+                    ++step;
+                    const float bias_correction = 1.0f - std::pow(P->beta2, static_cast<float>(step));
+                    const float vs_imp_hat = bias_correction > 0.0f ? new_vs_imp / bias_correction : new_vs_imp;
+                    if (!std::isfinite(vs_imp_hat)) continue;
+                    const float new_vs = vs[idx] - scale_eff_lr * g_agg / (std::sqrt(vs_imp_hat) + P->eps);
+                    if (!std::isfinite(new_vs)) continue;
+                    vs_imp = new_vs_imp;
+                    vs[idx] = new_vs;
+                }
+            }
+        }
+    }
     // rows with no synapse: a two-moment step on value_scale from
     // g = x[row] * sum_col(os * dy)
     if (lr != 0.0f) {
+        auto dead = [&](int64_t r) {
+            return L->row_elem_start[r + 1] == L->row_elem_start[r] && b4_live[size_t(r)] == 0;
+        };
         bool any_dead = false;
-        for (int64_t r = 0; r < n_in && !any_dead; ++r) any_dead = L->row_elem_start[r + 1] == L->row_elem_start[r];
+        for (int64_t r = 0; r < n_in && !any_dead; ++r) any_dead = dead(r);
         if (any_dead) {
             std::vector<double> dead_S(size_t(batch * rank), 0.0);
             for (int64_t b = 0; b < batch; ++b)
@@ -956,7 +1091,7 @@ int oracle_backward_train(const OracleLayer *L, uint8_t *val, OracleTrainState *
                     dead_S[size_t(b * rank + k)] = s;
                 }
             for (int64_t r = 0; r < n_in; ++r) {
-                if (L->row_elem_start[r + 1] != L->row_elem_start[r]) continue;
+                if (!dead(r)) continue;
                 for (int k = 0; k < rank; ++k) {
                     double sum = 0.0;
                     for (int64_t b = 0; b < batch; ++b) {

@@ -144,8 +144,9 @@ typedef struct {
 } OracleTrainState;
 
 /* L supplies structure (its val / scale pointers are not read); val: the
- * layer's value bytes, updated.  Returns -1 on a layer with block4 tiles. */
-int oracle_backward_train(const OracleLayer *L, uint8_t *val, OracleTrainState *S,
+ * layer's value bytes, tiles: its block4 tile bytes (canonical storage order),
+ * both updated.  Returns -1 on a layer with tiles when tiles is NULL. */
+int oracle_backward_train(const OracleLayer *L, uint8_t *val, uint8_t *tiles, OracleTrainState *S,
                           const float *x, const float *dy, int64_t batch, float *dx,
                           float *acc_in, float *acc_grad, const OracleTrainParams *P);
 

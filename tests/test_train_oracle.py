@@ -124,3 +124,54 @@ def test_backward_sparse_train_matches_reference(case, contracted):
                 assert np.array_equal(getattr(H, k), st[k]), what + ": " + k
             else:
                 np.testing.assert_allclose(getattr(H, k), st[k], rtol=1e-5, atol=1e-30, err_msg=what + ": " + k)
+
+
+# (n_in, n_out, scattered density, seed, batch, lr, options, variant): odd
+# output widths give edge tiles (the scalar path), the rest 4-lane tiles
+B4_CASES = [
+    (40, 37, 0.05, 21, 1, 0.3, {}, "plain"),
+    (44, 50, 0.05, 22, 3, 0.3, {}, "plain"),
+    (36, 30, 0.05, 23, 8, 0.2, dict(rank=2), "plain"),
+    (40, 37, 0.05, 24, 2, 0.3, {}, "resync"),
+    (40, 37, 0.05, 25, 2, 0.3, {}, "noscale"),
+    (64, 61, 0.05, 26, 12, 0.1, dict(imp_scales=True, lr_per_row_nnz=True), "plain"),
+    (33, 45, 0.05, 27, 1, 0.5, dict(damp_by_importance=False), "plain"),
+]
+
+
+@pytest.mark.parametrize("case", range(len(B4_CASES)))
+def test_block4_update_matches_reference(case):
+    """Layers holding block4 tiles (linear_disldo.hpp:962-1951): the tiles'
+    update, with the reference's rows given room for dense tiles (no
+    eviction).  Contracted build exact on codes, tile bytes and scale state
+    (dx within the bar: the 4-lane sums are re-associated by -ffast-math)."""
+    from train_util import add_tiles
+    n_in, n_out, dens, seed, B, lr, opts, variant = B4_CASES[case]
+    lopts, copts = split_opts(opts)
+    c = add_tiles(make_train_case(n_in, n_out, dens, seed, **lopts), seed=case)
+    assert len(c["br"]) > 0 and ((c["bc"] * 4 + 4 > n_out).any() or n_out % 4 == 0)
+    tiles0 = c["tiles"].copy()
+    H, R = host_layer(c), ref_layer(c)
+    H.load_tiles(c["br"], c["bc"], c["tiles"])
+    for t in range(len(c["br"])):
+        R.put_tile(int(c["br"][t]), int(c["bc"][t]), c["tiles"][16 * t:16 * t + 16])
+    R.block4_headroom(0.2, 16 * 64)
+    rng = c["rng"]
+    for step in range(3):
+        what = f"case {case} {variant} step {step}"
+        x = rng.normal(size=(B, n_in)).astype(np.float32)
+        dy = rng.normal(size=(B, n_out)).astype(np.float32)
+        bound = dx_bound(H, dy, lr) + np.abs(dy).sum(1, keepdims=True) * 7.0 * np.abs(x).max()
+        dxh, _, _ = H.backward_train(x, dy, lr, contracted=True, variant=variant, **copts)
+        dxr, _, _ = R.backward_train(x, dy, lr, variant=variant, **copts)
+        _, _, _, vr = R.export()
+        br, bc, tr = R.export_tiles()
+        st = R.get_train_state(c["rank"])
+        assert np.array_equal(H.val[:len(vr)], vr), what + ": codes"
+        assert np.array_equal(H.tile_br, br) and np.array_equal(H.tile_bc, bc), what + ": tile set"
+        assert np.array_equal(H.tiles[:len(tr)], tr), what + ": tile bytes"
+        assert_close_terms(dxh, dxr, bound, what + ": dx")
+        for k in ("value_scale", "output_scale", "vs_importance", "os_importance"):
+            assert np.array_equal(getattr(H, k), st[k]), what + ": " + k
+        assert np.array_equal(H.vs_step, st["vs_step"]) and np.array_equal(H.os_step, st["os_step"]), what
+    assert (H.tiles[:len(tiles0)] != tiles0).sum() > 4, "the tiles barely changed"

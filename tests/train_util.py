@@ -140,3 +140,34 @@ def dx_bound_sparse(H, dy_dense, lr, max_step=None):
     T = np.zeros((H.n_in, B))
     np.add.at(T, rows, (np.abs(dy[:, cols].astype(np.float64)) * mag).T)
     return T.T
+
+
+def add_tiles(c, tile_density=0.3, seed=0):
+    """Block4 tiles over the windows of c that hold no scattered synapse (all
+    16 slots coded, some empty), edge windows included."""
+    rng = np.random.default_rng(1000 + seed)
+    n_in, n_out = c["n_in"], c["n_out"]
+    brs, bcs = (n_in + 3) // 4, (n_out + 3) // 4
+    used = np.zeros((brs, bcs), bool)
+    for r in range(n_in):
+        for col in c["cols"][c["ptrs"][r]:c["ptrs"][r + 1]]:
+            used[r // 4, col // 4] = True
+    keys = [k for k in np.flatnonzero(rng.random(brs * bcs) < tile_density) if not used.flat[k]]
+    if n_out % 4:  # at least one edge tile (columns past n_out in the window)
+        free = [b * bcs + bcs - 1 for b in range(brs) if not used[b, bcs - 1]]
+        if free and free[0] not in keys:
+            keys = sorted(keys + [free[0]])
+    br = np.array([k // bcs for k in keys], np.int32)
+    bc = np.array([k % bcs for k in keys], np.int32)
+    codes_w = rng.integers(0, 16, (len(keys), 16))
+    codes_w[codes_w == 8] = 3
+    codes_i = rng.integers(0, 8, (len(keys), 16))
+    tiles = ((codes_i << 4) | codes_w).astype(np.uint8)
+    tiles[rng.random(tiles.shape) < 0.25] = 0
+    for t, (a, b) in enumerate(zip(br, bc)):  # slots outside the layer stay 0
+        for s in range(16):
+            lj, li = divmod(s, 4)
+            if a * 4 + li >= n_in or b * 4 + lj >= n_out:
+                tiles[t, s] = 0
+    c["br"], c["bc"], c["tiles"] = br, bc, tiles.ravel()
+    return c
