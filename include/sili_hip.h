@@ -154,8 +154,13 @@ int sili_backward_dense(sili_layer *layer, const float *x, const float *dy, int6
  * importance, re-quantized in place (deterministically or stochastically,
  * sili_set_stochastic_rounding); dx from the updated weights; the value
  * scales' RMSprop step, the Adam step of rows without synapses, and the output
- * scales' step when they are trainable.  batch <= 1024.  Layers holding block4
- * tiles: SILI_ERR_INVALID (not implemented on the GPU path yet).
+ * scales' step when they are trainable.  batch <= 1024.  Block4 tiles (FP4,
+ * linear_disldo.hpp:962-1951): every slot of a tile steps the same way, rows
+ * count n_tiles(block row) * 4 synapses, tiles whose 4 columns are in range
+ * sum their per-step row terms in the reference's 4-lane order, and the block
+ * rows' scale step follows the scattered one; the reference's eviction of
+ * live slots when a block row outgrows its reserved bytes has no analogue
+ * (the device store is compact and always has room).
  * learning_rate 0 is plain backward_dense. */
 int sili_backward_dense_train(sili_layer *layer, const float *x, const float *dy, int64_t batch,
                               float *dx, float learning_rate, int lr_per_row_nnz,

@@ -181,6 +181,18 @@ __global__ void k_split_keys(const uint64_t *__restrict__ key, int64_t N, uint64
     minor[i] = (uint32_t)(k % minor_extent);
 }
 // dst tile i = src tile perm[i], optionally 4x4-transposed (slot lj*4+li <-> li*4+lj).
+// inv[perm[i]] = i
+__global__ void k_inv_perm(const uint32_t *__restrict__ perm, int64_t N, uint32_t *__restrict__ inv) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < N) inv[perm[i]] = (uint32_t)i;
+}
+// out[j] = inv[perm[j]]
+__global__ void k_compose_perm(const uint32_t *__restrict__ perm, const uint32_t *__restrict__ inv, int64_t N,
+                               uint32_t *__restrict__ out) {
+    const int64_t j = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (j < N) out[j] = inv[perm[j]];
+}
+
 __global__ void k_gather_tiles(const uint8_t *__restrict__ src, const uint32_t *__restrict__ perm,
                                int64_t N, int transpose, uint8_t *__restrict__ dst) {
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
@@ -592,6 +604,7 @@ void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_
     const int64_t N = n_tiles;
     TmpBuf<uint64_t> key(L, SILI_TMPKEY(key)), key_sorted(L, SILI_TMPKEY(key_sorted));
     TmpBuf<uint32_t> perm_in(L, SILI_TMPKEY(perm_in)), perm(L, SILI_TMPKEY(perm)), major(L, SILI_TMPKEY(major)), minor(L, SILI_TMPKEY(minor));
+    TmpBuf<uint32_t> inv(L, SILI_TMPKEY(inv));
     key.ensure((size_t)N + 1);
     key_sorted.ensure((size_t)N + 1);
     perm_in.ensure((size_t)N + 1);
@@ -616,14 +629,31 @@ void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_
             SILI_HIP(hipGetLastError());
         }
         check_flag(L, L.scratch.flag.p, "block4 tiles");
-        if (canon)
+        if (canon) {
             build_b4_orientation(L, L.B4, N, brows, bcols, L.n_in, L.n_out, major.p, minor.p, perm.p,
                                  d_tiles, false);
-        else
+            inv.ensure((size_t)N + 1);
+            if (N > 0) launch(k_inv_perm, dim3(nblk(N)), dim3(TPB), 0, st, (const uint32_t *)perm.p, N, inv.p);
+        } else {
             build_b4_orientation(L, L.B4t, N, bcols, brows, L.n_out, L.n_in, major.p, minor.p, perm.p,
                                  d_tiles, true);
+            // shadow tile -> canonical tile (the update refreshes the shadow through it)
+            L.B4t_perm.ensure((size_t)N + 1);
+            if (N > 0)
+                launch(k_compose_perm, dim3(nblk(N)), dim3(TPB), 0, st, (const uint32_t *)perm.p,
+                       (const uint32_t *)inv.p, N, L.B4t_perm.p);
+        }
+        SILI_HIP(hipGetLastError());
     }
     SILI_HIP(hipStreamSynchronize(st));
+}
+
+void launch_b4_shadow_refresh(Layer &L, hipStream_t st) {
+    if (L.B4.ntiles == 0) return;
+    ProfScope ps("train_b4_shadow", st);
+    launch(k_gather_tiles, dim3(nblk(L.B4.ntiles)), dim3(TPB), 0, st, (const uint8_t *)L.B4.tiles.p,
+           (const uint32_t *)L.B4t_perm.p, L.B4.ntiles, 1, L.B4t.tiles.p);
+    SILI_HIP(hipGetLastError());
 }
 
 void refresh_nonfinite(Layer &L) {

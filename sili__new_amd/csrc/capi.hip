@@ -410,9 +410,6 @@ void backward_dense_train(Layer &L, const float *x, const float *dy, int64_t B, 
     if (!dy || !dx) throw_error(SILI_ERR_INVALID, "backward_dense: NULL buffer");
     if (B > TRAIN_MAX_BATCH)
         throw_error(SILI_ERR_INVALID, "backward_dense with learning_rate != 0: batch must be <= 1024");
-    if (L.B4.ntiles > 0)
-        throw_error(SILI_ERR_INVALID, "backward_dense with learning_rate != 0: layers holding block4 tiles are "
-                                      "not supported on the GPU path yet");
     const float *xT = nullptr;
     if (!x) {
         if (L.xT_cached_batch != B)
@@ -432,16 +429,23 @@ void backward_dense_train(Layer &L, const float *x, const float *dy, int64_t B, 
     if (L.output_scale_trainable) L.mterm.ensure((size_t)(L.W.nnz * 2 * L.rank));
     const uint64_t seed = splitmix64_host(L.rng_seed ^ splitmix64_host(L.rng_calls + 1));
     launch_train_rows(L, xT, gT, B, dx, p, seed, st);
+    // block4 tiles after the scattered rows' scale steps (linear_disldo.hpp:962-1951)
+    launch_train_b4(L, xT, gT, B, dx, p, seed, st);
     if (L.W.n_empty_rows > 0) launch_train_dead_rows(L, xT, gT, B, p, st);
     const bool scales_step = L.update_variant != UPDATE_NOSCALE;
     if (L.output_scale_trainable && scales_step && L.W.nnz > 0) launch_train_cols(L, p, st);
     launch_train_store(L, seed, st);
     launch_shadow_val_refresh(L, st);
+    launch_b4_shadow_refresh(L, st);
     // copies holding value bytes are stale now: rebuilt on their next use
     for (DScatter *sc : {&L.W, &L.Wt}) {
         sc->stream1.valid = sc->streamK.valid = false;
         sc->cblk.clear();
         sc->cblk_cb = 0;
+    }
+    for (DBlock4 *b4 : {&L.B4, &L.B4t}) {
+        b4->cblk.clear();
+        b4->cblk_cbb = 0;
     }
     L.vs_ones = false;
     if (L.output_scale_trainable && scales_step) L.os_ones = false;

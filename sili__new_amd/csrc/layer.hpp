@@ -183,6 +183,8 @@ struct Layer {
     DevBuf<uint32_t> vs_step, os_step;
     bool train_state_ready = false;
     DevBuf<uint32_t> Wt_perm;     // shadow entry -> canonical entry (kept once the layer trains)
+    DevBuf<uint32_t> B4t_perm;    // block4 shadow tile -> canonical tile (kept with every block4 build)
+    DevBuf<float> b4term;         // per tile slot: output-scale gradient terms of the update
     bool keep_perm = false;
     DevBuf<float> pow_tab;        // pow_tab[s] = powf(beta2, s), s <= pow_n
     int64_t pow_n = 0;
@@ -318,6 +320,13 @@ void launch_shadow_val_refresh(Layer &L, hipStream_t st);
 // DeferredScaleWrite: the value bytes under the final scales (after the
 // scale steps; same seed as launch_train_rows).
 void launch_train_store(Layer &L, uint64_t seed, hipStream_t st);
+// The block4 tiles' update (after launch_train_rows; adds into dx), the
+// block rows' scale step; the tiles' output-scale terms into L.b4term when
+// the output scales train.
+void launch_train_b4(Layer &L, const float *xT, const float *gT, int64_t B, float *dx, const TrainParams &p,
+                     uint64_t seed, hipStream_t st);
+// Shadow tile bytes from the canonical ones (through L.B4t_perm).
+void launch_b4_shadow_refresh(Layer &L, hipStream_t st);
 // backward_sparse's update of the canonical store, dx and the value scales;
 // gT dense feature-major with the sparse dy's entries marked (nonzero bits).
 void launch_sparse_train(Layer &L, const float *xT, const float *gT, int64_t B, float *dx, const TrainParams &p,

@@ -517,6 +517,189 @@ __global__ __launch_bounds__(256) void k_sparse_train_vs(const uint32_t *__restr
     vs[r] = vs[r] - scale_eff_lr * g_agg / (__builtin_sqrtf(vs_imp_hat) + eps);
 }
 
+// ---- block4 tiles ------------------------------------------------------------------
+struct B4TrainArgs {
+    const uint32_t *byte_start, *tile_start;  // canonical block4 store
+    const uint8_t *idx;
+    uint8_t *tiles;
+    int64_t brows, n_in, n_out, B, nnz_scattered;
+    const float *xT, *gT;
+    float *dx;                 // [B][n_in], added into
+    float *vs, *vs_imp;
+    uint32_t *vs_step;
+    const float *os, *is, *ois, *pow_tab;
+    float *b4term;             // [tiles * 16][2 * rank] or NULL
+    float lr, beta2, eps, min_decay_frac, max_abs_delta, max_ci, zero_escape_eps;
+    int lr_per_row_nnz, damp, stochastic;
+    uint64_t seed;
+};
+
+// One wave per canonical block row (linear_disldo.hpp:962-1951, FP4): every
+// slot of the row's tiles trains.  Lanes hold 4 tiles x 16 slots, ordered
+// (tile, li, lj) so a quad is one tile row.  A tile whose 4 columns are all
+// in range sums its row's 4 row-gradient and dx terms per batch step in lane
+// order ((t0 + t1) + t2) + t3 in fp32 (the reference's 4-lane path); an
+// edge tile adds its fp64 row-gradient terms one by one (its scalar path).
+// The tiles' fp64 row partials are added in tile order; then the block
+// rows' scale step.
+template <int RANK>
+__global__ __launch_bounds__(256) void k_train_b4(B4TrainArgs a) {
+    __shared__ uint32_t s_bc[WAVES_T][64];
+    __shared__ double s_mr[WAVES_T][4][4][2 * RANK];  // [tile][li][k | contrib k]
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t br = (int64_t)blockIdx.x * WAVES_T + wave;
+    if (br >= a.brows) return;
+    const uint32_t t0 = a.tile_start[br], t1 = a.tile_start[br + 1];
+    if (t0 == t1) return;
+    const int64_t B = a.B;
+    const uint32_t nnz_row = (t1 - t0) * 4u;
+    const float eff_lr = a.lr_per_row_nnz ? a.lr / (float)nnz_row : a.lr;
+    const uint32_t tl = lane >> 4, li = (lane >> 2) & 3u, lj = lane & 3u, qbase = lane & ~3u;
+    const int64_t row = br * 4 + li;
+    const bool row_ok = row < a.n_in;
+    double rowacc[2 * RANK];  // lanes 0..3: row br*4 + lane
+#pragma unroll
+    for (int k = 0; k < 2 * RANK; ++k) rowacc[k] = 0.0;
+    uint32_t pos = a.byte_start[br], carry = 0, ebase = t0;
+    const uint32_t end = a.byte_start[br + 1];
+    while (pos < end) {
+        const Chunk ch = decode_chunk(a.idx, pos, end, carry);
+        if (ch.T == 0ull) break;
+        if (ch.term) s_bc[wave][ch.rank] = ch.col;
+        wave_lds_sync();
+        const uint32_t nt = (uint32_t)__popcll(ch.T);
+        for (uint32_t sub = 0; sub < nt; sub += 4) {
+            const uint32_t trank = sub + tl;
+            const bool tile_ok = trank < nt;
+            const uint32_t bc = tile_ok ? s_bc[wave][trank] : 0u;
+            const int64_t t = (int64_t)ebase + trank;
+            const int64_t col = (int64_t)bc * 4 + lj;
+            const bool has = tile_ok && row_ok && col < a.n_out;
+            const bool full = tile_ok && (int64_t)bc * 4 + 4 <= a.n_out;
+            const uint32_t slot = lj * 4u + li;
+            const uint32_t byte = has ? (uint32_t)a.tiles[t * 16 + slot] : 0u;
+            float vs_k[RANK], os_k[RANK];
+            float S = 0.0f;
+#pragma unroll
+            for (int k = 0; k < RANK; ++k) {
+                vs_k[k] = row_ok ? a.vs[row * RANK + k] : 0.0f;
+                os_k[k] = has ? a.os[col * RANK + k] : 0.0f;
+                S = S + vs_k[k] * os_k[k];
+            }
+            const float imp_scale = (a.is && row_ok) ? a.is[row] : 1.0f;
+            const float cis = imp_scale * ((a.ois && has) ? a.ois[col] : 1.0f);
+            const float q0 = fp4_decode(byte & 0xFu);
+            float q = q0;
+            float ci = fp4_decode(byte >> 4) * cis;
+            double mr[2 * RANK];
+            float mc[2 * RANK];
+#pragma unroll
+            for (int k = 0; k < 2 * RANK; ++k) {
+                mr[k] = 0.0;
+                mc[k] = 0.0f;
+            }
+            const float *xrow = a.xT + (row_ok ? row : 0) * B;
+            const float *gcol = a.gT + (has ? col : 0) * B;
+            for (int64_t b = 0; b < B; ++b) {
+                const float iv = row_ok ? xrow[b] : 0.0f;
+                const float dyv = has ? gcol[b] : 0.0f;
+                const float g = dyv * iv;
+                const float contrib = q0 * iv;
+                ci = bounded_update_ci(ci, g, contrib, a.beta2, a.min_decay_frac, a.max_ci);
+                q = q + bounded_update_cw(g, ci, S, eff_lr, a.eps, a.damp != 0, a.max_abs_delta);
+                const float qf = (q == 0.0f) ? a.zero_escape_eps : q;
+                const float tdx = has ? (q * S) * dyv : 0.0f;
+                float tr[2 * RANK];
+                double dr[2 * RANK];
+#pragma unroll
+                for (int k = 0; k < RANK; ++k) {
+                    tr[k] = (qf * os_k[k]) * g;
+                    tr[RANK + k] = (qf * os_k[k]) * contrib;
+                    dr[k] = has ? ((double)qf * (double)os_k[k]) * (double)g : 0.0;
+                    dr[RANK + k] = has ? ((double)qf * (double)os_k[k]) * (double)contrib : 0.0;
+                    mc[k] = mc[k] + (qf * vs_k[k]) * g;
+                    mc[RANK + k] = mc[RANK + k] + (qf * vs_k[k]) * contrib;
+                }
+                // the tile row's 4 slots, in lane order, on its first lane
+                const float x1 = __shfl(tdx, (int)(qbase + 1), 64), x2 = __shfl(tdx, (int)(qbase + 2), 64),
+                            x3 = __shfl(tdx, (int)(qbase + 3), 64);
+                if (full) {
+                    if (lj == 0u && row_ok) atomicAdd(&a.dx[b * a.n_in + row], ((tdx + x1) + x2) + x3);
+                } else if (has) {
+                    atomicAdd(&a.dx[b * a.n_in + row], tdx);
+                }
+#pragma unroll
+                for (int k = 0; k < 2 * RANK; ++k) {
+                    if (full) {
+                        const float y1 = __shfl(tr[k], (int)(qbase + 1), 64), y2 = __shfl(tr[k], (int)(qbase + 2), 64),
+                                    y3 = __shfl(tr[k], (int)(qbase + 3), 64);
+                        mr[k] = mr[k] + (double)(((tr[k] + y1) + y2) + y3);
+                    } else {
+                        const double z1 = __shfl(dr[k], (int)(qbase + 1), 64), z2 = __shfl(dr[k], (int)(qbase + 2), 64),
+                                     z3 = __shfl(dr[k], (int)(qbase + 3), 64);
+                        mr[k] = (((mr[k] + dr[k]) + z1) + z2) + z3;
+                    }
+                }
+            }
+            if (has) {
+                const float imp = ci / cis;
+                uint32_t wq, iq;
+                if (a.stochastic) {
+                    const uint64_t base = a.seed + 2ull * (uint64_t)(a.nnz_scattered + t * 16 + slot);
+                    wq = fp4_encode_stochastic(q, splitmix64(base));
+                    iq = fp4_encode_stochastic(imp, splitmix64(base + 1ull));
+                } else {
+                    wq = fp4_encode(q);
+                    iq = fp4_encode(imp);
+                }
+                a.tiles[t * 16 + slot] = (uint8_t)((iq << 4) | wq);
+                if (a.b4term) {
+#pragma unroll
+                    for (int k = 0; k < 2 * RANK; ++k) a.b4term[(t * 16 + slot) * 2 * RANK + k] = mc[k];
+                }
+            }
+            // the tile rows' fp64 partials, added per row in tile order
+            if (lj == 0u) {
+#pragma unroll
+                for (int k = 0; k < 2 * RANK; ++k) s_mr[wave][tl][li][k] = tile_ok ? mr[k] : 0.0;
+            }
+            wave_lds_sync();
+            if (lane < 4u) {
+                for (uint32_t u = 0; u < 4u && sub + u < nt; ++u) {
+#pragma unroll
+                    for (int k = 0; k < 2 * RANK; ++k) rowacc[k] = rowacc[k] + s_mr[wave][u][lane][k];
+                }
+            }
+            wave_lds_sync();
+        }
+        carry = chunk_advance(ch, pos, ebase);
+    }
+    // the block rows' scale step (linear_disldo.hpp:1923-1951)
+    const int64_t r = br * 4 + lane;
+    if (lane < 4u && r < a.n_in) {
+        const float scale_eff_lr = a.lr / (float)nnz_row;
+#pragma unroll
+        for (int k = 0; k < RANK; ++k) {
+            const double sum = rowacc[k], sum_c = rowacc[RANK + k];
+            if (sum == 0.0 && sum_c == 0.0) continue;
+            const float g_agg = (float)sum, contrib_agg = (float)sum_c;
+            if (!finite_f(g_agg) || !finite_f(contrib_agg)) continue;
+            const int64_t i = r * RANK + k;
+            const float new_vs_imp = a.beta2 * a.vs_imp[i] + (1.0f - a.beta2) * (g_agg * g_agg + contrib_agg * contrib_agg);
+            if (!finite_f(new_vs_imp)) continue;
+            const uint32_t step = a.vs_step[i] + 1u;
+            a.vs_step[i] = step;
+            const float bias_correction = 1.0f - a.pow_tab[step];
+            const float hat = bias_correction > 0.0f ? new_vs_imp / bias_correction : new_vs_imp;
+            if (!finite_f(hat)) continue;
+            const float new_vs = a.vs[i] - scale_eff_lr * g_agg / (__builtin_sqrtf(hat) + a.eps);
+            if (!finite_f(new_vs)) continue;
+            a.vs_imp[i] = new_vs_imp;
+            a.vs[i] = new_vs;
+        }
+    }
+}
+
 // dead_S[b*rank + k] = sum_col os_k(col) * dy[b][col] in fp64
 // (linear_disldo.hpp:1995-2007): one block per (b, k).
 __global__ __launch_bounds__(256) void k_dead_S(const float *__restrict__ os, const float *__restrict__ gT,
@@ -538,13 +721,16 @@ __global__ __launch_bounds__(256) void k_dead_S(const float *__restrict__ os, co
 
 // Rows with no synapse: a two-moment step on value_scale
 // (linear_disldo.hpp:2008-2040).
-__global__ __launch_bounds__(256) void k_dead_rows(const uint32_t *__restrict__ elem_start, int64_t n_in,
-                                                   int64_t n_out, int64_t B, int rank,
+__global__ __launch_bounds__(256) void k_dead_rows(const uint32_t *__restrict__ elem_start,
+                                                   const uint32_t *__restrict__ b4_tile_start, int64_t brows,
+                                                   int64_t n_in, int64_t n_out, int64_t B, int rank,
                                                    const float *__restrict__ xT, const double *__restrict__ dead_S,
                                                    float *vs, float *vs_mom, float *vs_imp, float lr, float beta1,
                                                    float beta2, float eps) {
     const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (r >= n_in || elem_start[r + 1] != elem_start[r]) return;
+    // a row in a block row holding tiles is not dead (linear_disldo.hpp:1986-1996)
+    if (b4_tile_start && r / 4 < brows && b4_tile_start[r / 4 + 1] != b4_tile_start[r / 4]) return;
     for (int k = 0; k < rank; ++k) {
         double sum = 0.0;
         for (int64_t b = 0; b < B; ++b) {
@@ -574,11 +760,21 @@ __global__ __launch_bounds__(256) void k_dead_rows(const uint32_t *__restrict__ 
 // column's synapses by ascending row, the reference's single-thread order).
 // deg: out_degree as the reference's synaptogenesis policy keeps it, or NULL
 // (then the column's stored synapses).
+// b4: the block4 shadow (tile_start / idx per block column, tile ->
+// canonical tile) and the tiles' terms, added after the scattered ones in
+// (block row, tile row) order, or NULL.
+struct B4ColTerms {
+    const uint32_t *tile_start, *byte_start, *perm;
+    const uint8_t *idx;
+    const float *term;
+    int64_t n_in;
+};
 __global__ __launch_bounds__(256) void k_train_cols(const uint32_t *__restrict__ t_elem_start,
                                                     const uint32_t *__restrict__ perm, int64_t n_out, int rank,
                                                     const float *__restrict__ mterm, float *os, float *os_imp,
                                                     uint32_t *os_step, float lr, float beta2, float eps,
-                                                    const float *pow_tab, const int32_t *__restrict__ out_deg) {
+                                                    const float *pow_tab, const int32_t *__restrict__ out_deg,
+                                                    B4ColTerms b4) {
     const int64_t c = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (c >= n_out) return;
     const uint32_t s0 = t_elem_start[c], s1 = t_elem_start[c + 1];
@@ -591,6 +787,28 @@ __global__ __launch_bounds__(256) void k_train_cols(const uint32_t *__restrict__
             const int64_t e = perm[s];
             m = m + mterm[e * 2 * rank + k];
             mc = mc + mterm[e * 2 * rank + rank + k];
+        }
+        if (b4.term) {
+            const int64_t bcol = c >> 2;
+            const uint32_t lj = (uint32_t)(c & 3);
+            size_t pos = b4.byte_start[bcol];
+            uint32_t brow = 0;
+            for (uint32_t st = b4.tile_start[bcol]; st < b4.tile_start[bcol + 1]; ++st) {
+                uint32_t v = 0;
+                for (uint32_t sh = 0;; sh += 7) {
+                    const uint8_t byte = b4.idx[pos++];
+                    v |= (uint32_t)(byte & 0x7Fu) << sh;
+                    if (!(byte & 0x80u)) break;
+                }
+                brow += v;
+                const int64_t t = b4.perm[st];
+                for (uint32_t li = 0; li < 4u; ++li) {
+                    if ((int64_t)brow * 4 + li >= b4.n_in) continue;
+                    const int64_t q = (t * 16 + lj * 4 + li) * 2 * rank;
+                    m = m + b4.term[q + k];
+                    mc = mc + b4.term[q + rank + k];
+                }
+            }
         }
         const int64_t i = c * rank + k;
         float osv = os[i], st = os_imp[i];
@@ -722,6 +940,55 @@ void launch_sparse_train(Layer &L, const float *xT, const float *gT, int64_t B, 
     SILI_HIP(hipGetLastError());
 }
 
+void launch_train_b4(Layer &L, const float *xT, const float *gT, int64_t B, float *dx, const TrainParams &p,
+                     uint64_t seed, hipStream_t st) {
+    if (L.B4.ntiles == 0) return;
+    B4TrainArgs a{};
+    a.byte_start = L.B4.byte_start.p;
+    a.tile_start = L.B4.tile_start.p;
+    a.idx = L.B4.idx.p;
+    a.tiles = L.B4.tiles.p;
+    a.brows = L.B4.brows;
+    a.n_in = L.n_in;
+    a.n_out = L.n_out;
+    a.B = B;
+    a.nnz_scattered = L.W.nnz;
+    a.xT = xT;
+    a.gT = gT;
+    a.dx = dx;
+    a.vs = L.vs.p;
+    a.vs_imp = L.vs_imp.p;
+    a.vs_step = L.vs_step.p;
+    a.os = L.os.p;
+    a.is = L.is.p;
+    a.ois = L.ois.p;
+    a.pow_tab = L.pow_tab.p;
+    if (L.output_scale_trainable) {
+        L.b4term.ensure((size_t)(L.B4.ntiles * 16 * 2 * L.rank));
+        a.b4term = L.b4term.p;
+    }
+    a.lr = p.lr;
+    a.beta2 = p.beta2;
+    a.eps = p.eps;
+    a.min_decay_frac = p.min_decay_frac;
+    a.max_abs_delta = p.max_abs_delta;
+    a.max_ci = p.max_ci;
+    a.zero_escape_eps = p.zero_escape_eps;
+    a.lr_per_row_nnz = p.lr_per_row_nnz;
+    a.damp = p.damp_by_importance;
+    a.stochastic = L.stochastic_rounding ? 1 : 0;
+    a.seed = seed;
+    const dim3 grid((unsigned)((L.B4.brows + WAVES_T - 1) / WAVES_T)), block(256);
+    ProfScope ps("train_b4", st);
+    switch (L.rank) {
+        case 1: launch(k_train_b4<1>, grid, block, 0, st, a); break;
+        case 2: launch(k_train_b4<2>, grid, block, 0, st, a); break;
+        case 3: launch(k_train_b4<3>, grid, block, 0, st, a); break;
+        default: launch(k_train_b4<4>, grid, block, 0, st, a); break;
+    }
+    SILI_HIP(hipGetLastError());
+}
+
 void launch_train_store(Layer &L, uint64_t seed, hipStream_t st) {
     if (L.update_variant != UPDATE_RESYNC || L.W.nnz == 0) return;
     TrainArgs a{};
@@ -756,7 +1023,8 @@ void launch_train_dead_rows(Layer &L, const float *xT, const float *gT, int64_t 
     ProfScope ps("train_dead", st);
     launch(k_dead_S, dim3((unsigned)(B * L.rank)), dim3(256), 0, st, (const float *)L.os.p, gT, L.n_out, B, L.rank,
            L.dead_S.p);
-    launch(k_dead_rows, dim3(nblk(L.n_in)), dim3(TPB), 0, st, (const uint32_t *)L.W.elem_start.p, L.n_in, L.n_out, B,
+    launch(k_dead_rows, dim3(nblk(L.n_in)), dim3(TPB), 0, st, (const uint32_t *)L.W.elem_start.p,
+           L.B4.ntiles > 0 ? (const uint32_t *)L.B4.tile_start.p : nullptr, L.B4.brows, L.n_in, L.n_out, B,
            L.rank, xT, (const double *)L.dead_S.p, L.vs.p, L.vs_mom.p, L.vs_imp.p, p.lr, p.beta1, p.beta2, p.eps);
     SILI_HIP(hipGetLastError());
 }
@@ -766,7 +1034,10 @@ void launch_train_cols(Layer &L, const TrainParams &p, hipStream_t st) {
     launch(k_train_cols, dim3(nblk(L.n_out)), dim3(TPB), 0, st, (const uint32_t *)L.Wt.elem_start.p,
            (const uint32_t *)L.Wt_perm.p, L.n_out, L.rank, (const float *)L.mterm.p, L.os.p, L.os_imp.p, L.os_step.p,
            p.lr, p.beta2, p.eps, (const float *)L.pow_tab.p,
-           L.out_deg_tracked ? (const int32_t *)L.out_deg.p : nullptr);
+           L.out_deg_tracked ? (const int32_t *)L.out_deg.p : nullptr,
+           L.B4.ntiles > 0 ? B4ColTerms{L.B4t.tile_start.p, L.B4t.byte_start.p, L.B4t_perm.p, L.B4t.idx.p,
+                                        L.b4term.p, L.n_in}
+                           : B4ColTerms{nullptr, nullptr, nullptr, nullptr, nullptr, L.n_in});
     SILI_HIP(hipGetLastError());
 }
 

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 from sili__new_amd.codec import fp4_decode_np
-from train_util import TRAIN_CASES, dx_bound, host_layer, make_train_case, split_opts
+from train_util import B4_CASES, TRAIN_CASES, add_tiles, dx_bound, host_layer, make_train_case, split_opts
 from util import assert_close_terms
 
 pytestmark = pytest.mark.gpu
@@ -37,7 +37,7 @@ def gpu_layer(hip, c, deterministic=True, variant="plain"):
     return L
 
 
-def check_state(L, H, exact, what):
+def check_state(L, H, exact, what, vs_rtol=1e-6):
     vs = L.get_value_scales()
     st = L.get_scale_state()
     if exact:
@@ -45,7 +45,7 @@ def check_state(L, H, exact, what):
         assert np.array_equal(st["vs_importance"], H.vs_importance), what + ": vs_importance"
         assert np.array_equal(st["vs_momentum"], H.vs_momentum), what + ": vs_momentum"
     else:
-        np.testing.assert_allclose(vs, H.value_scale, rtol=1e-6, atol=0, err_msg=what)
+        np.testing.assert_allclose(vs, H.value_scale, rtol=vs_rtol, atol=0, err_msg=what)
         np.testing.assert_allclose(st["vs_importance"], H.vs_importance, rtol=1e-5, atol=0, err_msg=what)
         np.testing.assert_allclose(st["vs_momentum"], H.vs_momentum, rtol=1e-5, atol=0, err_msg=what)
     assert np.array_equal(st["vs_step"], H.vs_step), what + ": vs_step"
@@ -159,16 +159,65 @@ def test_stochastic_update_reproducible_per_seed(hip):
     assert np.array_equal(res[0], res[1])
 
 
-def test_update_rejects_block4_and_oversize_batch(hip):
-    from test_gpu_parity import _edge_block4_layer
-    br, bc, tiles, ptrs, cols, q, vs = _edge_block4_layer(40, 30, 3)
-    L = hip.SparseLinearLayer(40, 30, len(cols) + 16 * len(br) + 64)
-    L.load_weights(ptrs, cols, q)
-    L.load_block4_tiles(br, bc, tiles)
-    x = np.ones((2, 40), np.float32)
-    L.forward_dense(x)
-    with pytest.raises(ValueError):
-        L.backward_dense(np.ones((2, 30), np.float32), 0.05)
+def _sorted_tiles(br, bc, tiles, n_out):
+    bcs = (n_out + 3) // 4
+    o = np.argsort(np.asarray(br, np.int64) * bcs + np.asarray(bc, np.int64), kind="stable")
+    return np.asarray(br)[o], np.asarray(bc)[o], np.asarray(tiles).reshape(-1, 16)[o]
+
+
+@pytest.mark.parametrize("case", range(len(B4_CASES)))
+def test_block4_update_matches_oracle(hip, case):
+    """Layers holding block4 tiles (linear_disldo.hpp:962-1951): tile bytes
+    and value bytes bit-exact, scales as in the scattered cases, dx within
+    the bar (the tile rows' dx terms are added by atomics)."""
+    n_in, n_out, dens, seed, B, lr, opts, variant = B4_CASES[case]
+    lopts, copts = split_opts(opts)
+    c = add_tiles(make_train_case(n_in, n_out, dens, seed, **lopts), seed=case)
+    H = host_layer(c)
+    H.load_tiles(c["br"], c["bc"], c["tiles"])
+    cls = getattr(hip, CLASSES[variant][0])
+    L = cls(n_in, n_out, len(c["cols"]) + 16 * len(c["br"]) + 64)
+    L.load_weights_with_importance(c["ptrs"], c["cols"], c["w"], c["imp"])
+    L.load_block4_tiles(c["br"], c["bc"], c["tiles"])
+    if c["rank"] > 1:
+        L.set_scale_rank(c["rank"])
+    L.set_value_scales(c["vs"])
+    if c["os_trainable"] or c["rank"] > 1:
+        L.set_output_scales(c["os"])
+    if c["is"] is not None:
+        for r in range(n_in):
+            L.set_importance_scale_raw(r, float(c["is"][r]))
+        for col in range(n_out):
+            L.set_output_importance_scale_raw(col, float(c["ois"][col]))
+    tiles0 = c["tiles"].copy()
+    rng = c["rng"]
+    for step in range(3):
+        what = f"block4 case {case} {variant} step {step}"
+        x = rng.normal(size=(B, n_in)).astype(np.float32)
+        dy = rng.normal(size=(B, n_out)).astype(np.float32)
+        bound = dx_bound(H, dy, lr) + np.abs(dy).sum(1, keepdims=True) * 7.0 * np.abs(x).max()
+        L.forward_dense(x)
+        dxg = L.backward_dense(dy, lr, **copts)
+        dxh, _, _ = H.backward_train(x, dy, lr, variant=variant, **copts)
+        assert np.array_equal(L.export_scattered()["val"], H.val[:H.nnz]), what + ": value bytes"
+        ex = L.export_block4()
+        gb, gc, gt = _sorted_tiles(ex["br"], ex["bc"], ex["tiles"], n_out)
+        hb, hc, ht = _sorted_tiles(H.tile_br, H.tile_bc, H.tiles[:16 * H.n_tiles], n_out)
+        assert np.array_equal(gb, hb) and np.array_equal(gc, hc), what + ": tile set"
+        assert np.array_equal(gt, ht), what + ": tile bytes"
+        assert_close_terms(dxg, dxh, bound, what + ": dx")
+        # batch > 1: the fp64 row sums are associated per synapse on the GPU,
+        # per batch step in the oracle; the last-bit differences compound over
+        # the steps and the block rows' second scale step
+        check_state(L, H, B == 1, what, vs_rtol=1e-5)
+        # the forward after the update reads the refreshed block4 shadow
+        x2 = rng.normal(size=(2, n_in)).astype(np.float32)
+        assert_close_terms(L.forward_dense(x2), H.forward_dense(x2), H.forward_dense(x2, absmode=True),
+                           what + ": forward after update")
+    assert (H.tiles[:len(tiles0)] != tiles0).sum() > 4, "the tiles barely changed"
+
+
+def test_update_rejects_oversize_batch(hip):
     c = make_train_case(20, 16, 0.3, 5)
     L2 = gpu_layer(hip, c)
     xb = np.ones((1025, 20), np.float32)

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 from oracle import have_ref
-from train_util import TRAIN_CASES, dx_bound, host_layer, make_train_case, ref_layer, split_opts
+from train_util import B4_CASES, TRAIN_CASES, dx_bound, host_layer, make_train_case, ref_layer, split_opts
 from util import assert_close_terms
 
 pytestmark = pytest.mark.skipif(not have_ref(), reason="oracle/_ref not built (no reference tree)")
@@ -128,17 +128,6 @@ def test_backward_sparse_train_matches_reference(case, contracted):
 
 # (n_in, n_out, scattered density, seed, batch, lr, options, variant): odd
 # output widths give edge tiles (the scalar path), the rest 4-lane tiles
-B4_CASES = [
-    (40, 37, 0.05, 21, 1, 0.3, {}, "plain"),
-    (44, 50, 0.05, 22, 3, 0.3, {}, "plain"),
-    (36, 30, 0.05, 23, 8, 0.2, dict(rank=2), "plain"),
-    (40, 37, 0.05, 24, 2, 0.3, {}, "resync"),
-    (40, 37, 0.05, 25, 2, 0.3, {}, "noscale"),
-    (64, 61, 0.05, 26, 12, 0.1, dict(imp_scales=True, lr_per_row_nnz=True), "plain"),
-    (33, 45, 0.05, 27, 1, 0.5, dict(damp_by_importance=False), "plain"),
-]
-
-
 @pytest.mark.parametrize("case", range(len(B4_CASES)))
 def test_block4_update_matches_reference(case):
     """Layers holding block4 tiles (linear_disldo.hpp:962-1951): the tiles'

@@ -171,3 +171,16 @@ def add_tiles(c, tile_density=0.3, seed=0):
                 tiles[t, s] = 0
     c["br"], c["bc"], c["tiles"] = br, bc, tiles.ravel()
     return c
+
+
+# block4 update cases: (n_in, n_out, density, seed, batch, lr, options, variant);
+# odd widths give edge tiles
+B4_CASES = [
+    (40, 37, 0.05, 21, 1, 0.3, {}, "plain"),
+    (44, 50, 0.05, 22, 3, 0.3, {}, "plain"),
+    (36, 30, 0.05, 23, 8, 0.2, dict(rank=2), "plain"),
+    (40, 37, 0.05, 24, 2, 0.3, {}, "resync"),
+    (40, 37, 0.05, 25, 2, 0.3, {}, "noscale"),
+    (64, 61, 0.05, 26, 12, 0.1, dict(imp_scales=True, lr_per_row_nnz=True), "plain"),
+    (33, 45, 0.05, 27, 1, 0.5, dict(damp_by_importance=False), "plain"),
+]
