@@ -47,7 +47,7 @@ class _TrainParams(C.Structure):
     _fields_ = [("lr", C.c_float), ("lr_per_row_nnz", C.c_int32), ("damp_by_importance", C.c_int32),
                 ("beta2", C.c_float), ("eps", C.c_float), ("beta1", C.c_float), ("min_decay_frac", C.c_float),
                 ("max_abs_delta", C.c_float), ("max_ci", C.c_float), ("zero_escape_eps", C.c_float),
-                ("variant", C.c_int32)]
+                ("variant", C.c_int32), ("draw_mode", C.c_int32), ("draw_seed", C.c_uint64)]
 
 
 # the scale-update variants of the reference's layer classes
@@ -117,7 +117,7 @@ def lib(contracted: bool = False):
         L.oracle_backward_train.argtypes = [C.POINTER(_OracleLayerC), _u8p, _u8p, C.POINTER(_TrainState), _f32p, _f32p,
                                             C.c_int64, _f32p, _f32p, _f32p, C.POINTER(_TrainParams)]
         L.oracle_backward_train.restype = C.c_int
-        L.oracle_backward_sparse_train.argtypes = [C.POINTER(_OracleLayerC), _u8p, C.POINTER(_TrainState), _f32p,
+        L.oracle_backward_sparse_train.argtypes = [C.POINTER(_OracleLayerC), _u8p, _u8p, C.POINTER(_TrainState), _f32p,
                                                    _i32p, _i32p, _f32p, C.c_int64, _f32p, _f32p, _f32p,
                                                    C.POINTER(_TrainParams)]
         L.oracle_backward_sparse_train.restype = C.c_int
@@ -177,6 +177,7 @@ def reflib():
                                          C.c_int, C.c_int, C.c_float, C.c_float, C.c_int, C.c_int]
         R.ref_backward_sparse_train.argtypes = [C.c_void_p, _f32p, _i32p, _i32p, _f32p, C.c_int, _f32p, _f32p, _f32p,
                                                 C.c_float, C.c_int, C.c_int, C.c_float, C.c_float, C.c_int]
+        R.ref_seed_stochastic.argtypes = [C.c_uint64]
         R.ref_layer_set_importance_scales.argtypes = [C.c_void_p, _f32p, _f32p]
         R.ref_layer_new_blank.restype = C.c_void_p
         R.ref_layer_new_blank.argtypes = [C.c_int, C.c_int, _i32p, _i32p, _f32p, _f32p, C.c_float]
@@ -428,10 +429,12 @@ class HostLayer:
         return dx, ai, ag
 
     def backward_sparse_train(self, x, dptrs, didx, dvals, batch, lr, lr_per_row_nnz=False, damp_by_importance=True,
-                              beta2=0.999, eps=1e-8, contracted=False):
+                              beta2=0.999, eps=1e-8, contracted=False, draw_mode=1, draw_seed=0):
         """backward_sparse with the optimizer update (one thread): updates
-        self.val and the value scales' state in place; returns dx and the
-        activity accumulators."""
+        self.val, self.tiles and the value scales' state in place; returns dx
+        and the activity accumulators.  draw_mode / draw_seed: the block4
+        tiles' stochastic rounding (0: the reference's seeded per-thread
+        xorshift64*, 1: the GPU library's counter draws)."""
         x = _c(np.atleast_2d(x), np.float32)
         dptrs, didx, dvals = _c(dptrs, np.int32), _c(didx, np.int32), _c(dvals, np.float32)
         dx = np.zeros_like(x)
@@ -443,13 +446,15 @@ class HostLayer:
         st = _TrainState(_p(self.value_scale, _f32p), _p(self.vs_importance, _f32p), _p(self.vs_momentum, _f32p),
                          _p(self.vs_step, u32p), _p(self.output_scale, _f32p), _p(self.os_importance, _f32p),
                          _p(self.os_step, u32p), _p(isc, _f32p), _p(oisc, _f32p), None, 0, None, None)
-        P = _TrainParams(lr, int(lr_per_row_nnz), int(damp_by_importance), beta2, eps, **TRAIN_DEFAULTS, variant=0)
+        P = _TrainParams(lr, int(lr_per_row_nnz), int(damp_by_importance), beta2, eps, **TRAIN_DEFAULTS, variant=0,
+                         draw_mode=int(draw_mode), draw_seed=int(draw_seed) & (2**64 - 1))
         s = self._cstruct()
-        if lib(contracted).oracle_backward_sparse_train(C.byref(s), _p(self.val, _u8p), C.byref(st), _p(x, _f32p),
+        tiles = _p(self.tiles, _u8p) if self.n_tiles > 0 else None
+        if lib(contracted).oracle_backward_sparse_train(C.byref(s), _p(self.val, _u8p), tiles, C.byref(st), _p(x, _f32p),
                                                         _p(dptrs, _i32p), _p(didx, _i32p), _p(dvals, _f32p), batch,
                                                         _p(dx, _f32p), _p(ai, _f32p), _p(ag, _f32p),
                                                         C.byref(P)) != 0:
-            raise ValueError("backward_sparse_train: layers with block4 tiles are not supported")
+            raise ValueError("backward_sparse_train: tile bytes missing")
         return dx, ai, ag
 
     # -- the reference's synaptogenesis policy (delta_csr_memory.hpp:1021-1426) --
@@ -703,7 +708,12 @@ class RefLayer:
         return dx, ai, ag
 
     def backward_sparse_train(self, x, dptrs, didx, dvals, batch, lr, lr_per_row_nnz=False, damp_by_importance=True,
-                              beta2=0.999, eps=1e-8, threads=1):
+                              beta2=0.999, eps=1e-8, threads=1, draw_seed=None):
+        """draw_seed: reseeds the calling thread's stochastic-rounding RNG
+        first (fp4_seed_stochastic_rng), which the block4 tiles' update draws
+        from (with threads=1 the reference's loop runs on this thread)."""
+        if draw_seed is not None:
+            reflib().ref_seed_stochastic(int(draw_seed) & (2**64 - 1))
         x = _c(np.atleast_2d(x), np.float32)
         dptrs, didx, dvals = _c(dptrs, np.int32), _c(didx, np.int32), _c(dvals, np.float32)
         dx = np.zeros_like(x)

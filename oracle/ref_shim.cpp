@@ -236,6 +236,9 @@ void ref_backward_sparse_train(void *h, const float *x, const int32_t *dptrs, co
                                                      lr_per_row_nnz != 0, damp != 0, beta2, eps);
 }
 
+// fp4_seed_stochastic_rng (fp4quant.hpp:186-188) on the calling thread.
+void ref_seed_stochastic(uint64_t seed) { fp4_seed_stochastic_rng(seed); }
+
 // delta_csr_build_probes (sili/cpu_backend.cpp:606-609), with the layer's
 // accumulators passed in.
 void ref_build_probes(void *h, const float *acc_in, const float *acc_grad, int k, int per_row) {

@@ -1153,11 +1153,170 @@ int oracle_backward_train(const OracleLayer *L, uint8_t *val, uint8_t *tiles, Or
     return 0;
 }
 
-// sisldo_ops.hpp:613-848 (scattered section of disldo_backward_sparse_grad).
-int oracle_backward_sparse_train(const OracleLayer *L, uint8_t *val, OracleTrainState *S, const float *x,
+}  // extern "C"
+
+namespace {
+
+// The stochastic FP4 encoder with its draw supplied (fp4quant.hpp:238-265):
+// top 24 bits -> uniform [0,1) below 1.0, low 22 bits -> dither above.
+uint32_t fp4_enc_stoch(float v, uint64_t r) {
+    uint32_t bits;
+    std::memcpy(&bits, &v, 4);
+    const uint32_t sign = bits & 0x80000000u, abits = bits & 0x7FFFFFFFu;
+    if (abits > 0x7F800000u) return 0u;
+    uint32_t mag;
+    if (abits >= 0x40C00000u) {
+        mag = 7u;
+    } else if (abits < 0x3F800000u) {
+        float av;
+        std::memcpy(&av, &abits, 4);
+        const float u01 = static_cast<float>((r >> 40) * (1.0 / 16777216.0));
+        if (abits < 0x3F000000u) mag = (u01 < av * 2.0f) ? 1u : 0u;
+        else mag = (u01 < av * 2.0f - 1.0f) ? 2u : 1u;
+    } else {
+        uint32_t rounded = abits + uint32_t(r & 0x3FFFFFu);
+        if (rounded > 0x40C00000u) rounded = 0x40C00000u;
+        mag = ((((rounded >> 23) & 0xFFu) - 126u) << 1) | ((rounded >> 22) & 1u);
+    }
+    if (mag == 0u) return 0u;
+    return (sign ? 8u : 0u) | mag;
+}
+
+uint64_t splitmix64_o(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// Draw source of the block4 sparse-gradient update (OracleTrainParams.draw_mode).
+struct Draws {
+    int mode;
+    uint64_t seed, xs;
+    explicit Draws(const OracleTrainParams *P)
+        : mode(P->draw_mode), seed(P->draw_seed), xs((P->draw_seed ^ 0x9E3779B97F4A7C15ULL) | 1ULL) {}
+    uint32_t enc(float v, uint64_t id) {
+        if (mode == 1) return fp4_enc_stoch(v, splitmix64_o(seed + id));
+        uint32_t bits;
+        std::memcpy(&bits, &v, 4);
+        const uint32_t a = bits & 0x7FFFFFFFu;
+        if (a > 0x7F800000u || a >= 0x40C00000u) return fp4_enc_stoch(v, 0);  // no draw taken
+        xs ^= xs >> 12;  // xorshift64* (fp4quant.hpp:196-200)
+        xs ^= xs << 25;
+        xs ^= xs >> 27;
+        return fp4_enc_stoch(v, xs * 0x2545F4914F6CDD1DULL);
+    }
+};
+
+// The block4 section of disldo_backward_sparse_grad (sisldo_ops.hpp:848-1100).
+int sparse_train_b4(const OracleLayer *L, uint8_t *tiles, OracleTrainState *S, const float *x,
+                    const int32_t *dptrs, const int32_t *didx, const float *dvals, int64_t batch, float *dx,
+                    const OracleTrainParams *P) {
+    if (L->n_tiles <= 0) return 0;
+    if (!tiles) return -1;
+    const int64_t n_in = L->n_in, n_out = L->n_out;
+    const int rank = L->rank;
+    const float lr = P->lr, beta2 = P->beta2, eps = P->eps;
+    float *vs = S->value_scale;
+    const float *os = S->output_scale;
+    const auto tl = collect_tiles(L);
+    const int64_t brows = (n_in + TILE - 1) / TILE;
+    std::vector<int64_t> tb(size_t(brows) + 1, 0);
+    for (const auto &t : tl) tb[size_t(t.br) + 1]++;
+    for (int64_t i = 0; i < brows; ++i) tb[size_t(i) + 1] += tb[size_t(i)];
+    std::vector<double> rs(size_t(n_in), 0.0), rsc(size_t(n_in), 0.0);
+    std::vector<float> dyrow(static_cast<size_t>(n_out), 0.0f);
+    Draws dr(P);
+    for (int64_t b = 0; b < batch; ++b) {
+        std::fill(dyrow.begin(), dyrow.end(), 0.0f);
+        for (int32_t j = dptrs[b]; j < dptrs[b + 1]; ++j) dyrow[size_t(didx[j])] = dvals[j];
+        for (int64_t br = 0; br < brows; ++br) {
+            const int64_t ntl = tb[size_t(br) + 1] - tb[size_t(br)];
+            if (ntl == 0) continue;
+            const float nnz_row = static_cast<float>(ntl * TILE);
+            float dx_acc[TILE] = {0, 0, 0, 0};
+            double rg[TILE] = {0, 0, 0, 0}, rgc[TILE] = {0, 0, 0, 0};
+            for (int64_t k = tb[size_t(br)]; k < tb[size_t(br) + 1]; ++k) {
+                uint8_t *td = tiles + 16 * tl[size_t(k)].t;
+                const int64_t bc = tl[size_t(k)].bc;
+                for (int li = 0; li < TILE; ++li) {
+                    const int64_t row = br * TILE + li;
+                    if (row >= n_in) continue;
+                    const float in_val = x[b * n_in + row];
+                    const float val_scale = vs[row * rank];
+                    const float imp_scale = S->importance_scale ? S->importance_scale[row] : 1.0f;
+                    const float effective_lr = P->lr_per_row_nnz ? lr / nnz_row : lr;
+                    for (int lj = 0; lj < TILE; ++lj) {
+                        const int64_t col = bc * TILE + lj;
+                        if (col >= n_out) continue;
+                        const float dy_val = dyrow[size_t(col)];
+                        if (dy_val == 0.0f) continue;
+                        const uint8_t byte = td[lj * TILE + li];
+                        const float w_decoded = fp4_dec(byte & 0xFu);
+                        const float out_scale = os[col * rank];
+                        const float combined_scale = val_scale * out_scale;
+                        const float w = w_decoded * combined_scale;
+                        dx_acc[li] += w * dy_val;
+                        if (lr == 0.0f) continue;
+                        const float ois = S->output_importance_scale ? S->output_importance_scale[col] : 1.0f;
+                        const float combined_imp_scale = imp_scale * ois;
+                        const float grad = dy_val * in_val;
+                        float imp = fp4_dec(byte >> 4) * combined_imp_scale;
+                        const float contrib = in_val * w;
+                        imp = beta2 * imp + (1.0f - beta2) * (grad * grad + contrib * contrib);
+                        const float new_w = w + (P->damp_by_importance ? (-effective_lr * grad) / (std::sqrt(imp) + eps)
+                                                                       : (-effective_lr * grad));
+                        const uint64_t id = 2ull * ((uint64_t(b) * uint64_t(L->n_tiles) + uint64_t(k)) * 16ull +
+                                                    uint64_t(lj * TILE + li));
+                        const uint32_t wq = dr.enc(new_w / combined_scale, id);
+                        const uint32_t iq = dr.enc(imp / combined_imp_scale, id + 1);
+                        td[lj * TILE + li] = uint8_t((iq << 4) | wq);
+                        rg[li] += static_cast<double>(w_decoded) * static_cast<double>(out_scale) * (dy_val * in_val);
+                        rgc[li] += static_cast<double>(w_decoded) * static_cast<double>(out_scale) *
+                                   static_cast<double>(contrib);
+                    }
+                }
+            }
+            for (int li = 0; li < TILE; ++li) {
+                const int64_t row = br * TILE + li;
+                if (row >= n_in) continue;
+                dx[b * n_in + row] += dx_acc[li];
+                rs[size_t(row)] += rg[li];
+                rsc[size_t(row)] += rgc[li];
+            }
+        }
+    }
+    if (lr == 0.0f) return 0;
+    for (int64_t row = 0; row < n_in; ++row) {
+        if (rs[size_t(row)] == 0.0 && rsc[size_t(row)] == 0.0) continue;
+        const int64_t br = row / TILE;
+        const int64_t nnz_row = (tb[size_t(br) + 1] - tb[size_t(br)]) * TILE;
+        if (nnz_row == 0) continue;
+        const float scale_eff_lr = lr / static_cast<float>(nnz_row);
+        const float g_agg = static_cast<float>(rs[size_t(row)]);
+        const float contrib_agg = static_cast<float>(rsc[size_t(row)]);
+        float &vs_imp = S->vs_importance[row];
+        const float new_vs_imp = beta2 * vs_imp + (1.0f - beta2) * (g_agg * g_agg + contrib_agg * contrib_agg);
+        uint32_t &step = S->vs_step[row * rank];
+        ++step;
+        const float bias_correction = 1.0f - std::pow(beta2, static_cast<float>(step));
+        const float vs_imp_hat = bias_correction > 0.0f ? new_vs_imp / bias_correction : new_vs_imp;
+        vs_imp = new_vs_imp;
+        vs[row] -= scale_eff_lr * g_agg / (std::sqrt(vs_imp_hat) + eps);
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+// sisldo_ops.hpp:613-1100 (disldo_backward_sparse_grad): the scattered
+// section, then the block4 section.
+int oracle_backward_sparse_train(const OracleLayer *L, uint8_t *val, uint8_t *tiles, OracleTrainState *S, const float *x,
                                  const int32_t *dptrs, const int32_t *didx, const float *dvals, int64_t batch,
                                  float *dx, float *acc_in, float *acc_grad, const OracleTrainParams *P) {
-    if (L->n_tiles > 0) return -1;
+    if (L->n_tiles > 0 && !tiles) return -1;
     const int64_t n_in = L->n_in;
     const int rank = L->rank;
     const float lr = P->lr, beta2 = P->beta2, eps = P->eps;
@@ -1165,7 +1324,7 @@ int oracle_backward_sparse_train(const OracleLayer *L, uint8_t *val, OracleTrain
         for (int64_t r = 0; r < n_in; ++r) acc_in[r] += std::fabs(x[b * n_in + r]);
     for (int64_t b = 0; b < batch; ++b)
         for (int32_t j = dptrs[b]; j < dptrs[b + 1]; ++j) acc_grad[didx[j]] += std::fabs(dvals[j]);
-    if (L->row_elem_start[n_in] == 0) return 0;
+    if (L->row_elem_start[n_in] == 0) return sparse_train_b4(L, tiles, S, x, dptrs, didx, dvals, batch, dx, P);
     float *vs = S->value_scale;
     const float *os = S->output_scale;
     std::vector<double> sg(size_t(n_in), 0.0), sgc(size_t(n_in), 0.0);
@@ -1233,7 +1392,7 @@ int oracle_backward_sparse_train(const OracleLayer *L, uint8_t *val, OracleTrain
             vs[r] -= scale_eff_lr * g_agg / (std::sqrt(vs_imp_hat) + eps);
         }
     }
-    return 0;
+    return sparse_train_b4(L, tiles, S, x, dptrs, didx, dvals, batch, dx, P);
 }
 
 }  // extern "C"

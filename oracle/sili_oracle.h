@@ -124,6 +124,15 @@ typedef struct {
     int32_t damp_by_importance;
     float beta2, eps, beta1, min_decay_frac, max_abs_delta, max_ci, zero_escape_eps;
     int32_t variant;
+    /* draws of the stochastic rounding in the sparse-gradient update of block4
+     * tiles (the reference rounds those stochastically in every layer class):
+     *   0  the reference's per-thread xorshift64* (fp4quant.hpp:174-200) as
+     *      fp4_seed_stochastic_rng(draw_seed) leaves it, one step per draw in
+     *      call order (draws only for finite |v| < 6)
+     *   1  the GPU library's counter draws: splitmix64(draw_seed + id), id =
+     *      2 * ((b * n_tiles + t) * 16 + slot) (+1 for the importance) */
+    int32_t draw_mode;
+    uint64_t draw_seed;
 } OracleTrainParams;
 
 typedef struct {
@@ -158,8 +167,13 @@ int oracle_backward_train(const OracleLayer *L, uint8_t *val, uint8_t *tiles, Or
  * class and the importance running stats are not involved.  One thread.
  * dy: CSR with strictly increasing indices per batch row.  S: value_scale,
  * vs_importance, vs_step, output_scale, importance scales read/updated (the
- * rest unused).  Returns -1 on a layer with block4 tiles. */
-int oracle_backward_sparse_train(const OracleLayer *L, uint8_t *val, OracleTrainState *S, const float *x,
+ * rest unused).  Block4 tiles (sisldo_ops.hpp:848-1100; tiles: the layer's
+ * tile bytes in canonical order, updated): per batch row, every slot whose dy
+ * is nonzero steps its decoded weight and importance (no bounds) and is
+ * re-quantized stochastically (draw_mode); the block rows' value_scale step
+ * follows, by the row index, step counter (row, 0), no finiteness guards.
+ * Returns -1 on a layer with tiles when tiles is NULL. */
+int oracle_backward_sparse_train(const OracleLayer *L, uint8_t *val, uint8_t *tiles, OracleTrainState *S, const float *x,
                                  const int32_t *dptrs, const int32_t *didx, const float *dvals, int64_t batch,
                                  float *dx, float *acc_in, float *acc_grad, const OracleTrainParams *P);
 

@@ -164,3 +164,43 @@ def test_block4_update_matches_reference(case):
             assert np.array_equal(getattr(H, k), st[k]), what + ": " + k
         assert np.array_equal(H.vs_step, st["vs_step"]) and np.array_equal(H.os_step, st["os_step"]), what
     assert (H.tiles[:len(tiles0)] != tiles0).sum() > 4, "the tiles barely changed"
+
+
+@pytest.mark.parametrize("case", range(len(B4_CASES)))
+def test_block4_sparse_update_matches_reference(case):
+    """backward_sparse with the update on layers holding block4 tiles
+    (sisldo_ops.hpp:848-1100): the reference rounds the tiles stochastically
+    through its per-thread xorshift64*, reseeded before every call; the oracle
+    replays the same draws in the same order (draw_mode 0).  Codes, tile
+    bytes and the value scales' state exact (contracted build), dx within the
+    bar."""
+    from train_util import add_tiles, dx_bound_sparse, sparse_dy
+    n_in, n_out, dens, seed, B, lr, opts, _ = B4_CASES[case]
+    lopts, copts = split_opts(opts)
+    c = add_tiles(make_train_case(n_in, n_out, dens, seed, **lopts), seed=case)
+    tiles0 = c["tiles"].copy()
+    H, R = host_layer(c), ref_layer(c)
+    H.load_tiles(c["br"], c["bc"], c["tiles"])
+    for t in range(len(c["br"])):
+        R.put_tile(int(c["br"][t]), int(c["bc"][t]), c["tiles"][16 * t:16 * t + 16])
+    R.block4_headroom(0.2, 16 * 64)
+    rng = c["rng"]
+    for step in range(3):
+        what = f"block4 sparse case {case} step {step}"
+        x = rng.normal(size=(B, n_in)).astype(np.float32)
+        dp, di, dv, dense = sparse_dy(rng, B, n_out, density=0.6)
+        bound = dx_bound_sparse(H, dense, lr) + np.abs(dense).sum(1, keepdims=True) * 7.0 * np.abs(x).max()
+        dseed = 1000 * case + step + 1
+        dxh, _, _ = H.backward_sparse_train(x, dp, di, dv, B, lr, contracted=True, draw_mode=0, draw_seed=dseed,
+                                            **copts)
+        dxr, _, _ = R.backward_sparse_train(x, dp, di, dv, B, lr, draw_seed=dseed, **copts)
+        _, _, _, vr = R.export()
+        br, bc, tr = R.export_tiles()
+        st = R.get_train_state(c["rank"])
+        assert np.array_equal(H.val[:len(vr)], vr), what + ": codes"
+        assert np.array_equal(H.tile_br, br) and np.array_equal(H.tile_bc, bc), what + ": tile set"
+        assert np.array_equal(H.tiles[:len(tr)], tr), what + ": tile bytes"
+        assert_close_terms(dxh, dxr, bound, what + ": dx")
+        for k in ("value_scale", "vs_importance", "vs_step"):
+            assert np.array_equal(getattr(H, k), st[k]), what + ": " + k
+    assert (H.tiles[:len(tiles0)] != tiles0).sum() > 4, "the tiles barely changed"
