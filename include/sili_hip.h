@@ -223,8 +223,13 @@ int sili_backward_sparse(sili_layer *layer, const float *x, const int32_t *dy_pt
  * re-quantized (round to nearest, whatever the layer's rounding setting)
  * before the next batch row; each row's value scale (slot r, step counter
  * (r, 0)) takes one bias-corrected RMSprop step after all batch rows.  Output
- * scales are not updated.  batch <= 1024; layers holding block4 tiles:
- * SILI_ERR_INVALID.  learning_rate 0 is plain backward_sparse. */
+ * scales are not updated.  batch <= 1024.  Block4 tiles (sisldo_ops.hpp:
+ * 848-1100), after the scattered section: per batch row every slot whose dy
+ * entry is nonzero takes the same unbounded step and is re-quantized
+ * stochastically in every layer class, as the reference does (draws
+ * splitmix64 of the call seed and (batch row, tile, slot), reproducible
+ * under sili_seed_stochastic_rounding); then the block rows' value-scale
+ * step.  learning_rate 0 is plain backward_sparse. */
 int sili_backward_sparse_train(sili_layer *layer, const float *x, const int32_t *dy_ptrs,
                                const int32_t *dy_indices, const float *dy_values, int64_t nnz_dy,
                                int64_t batch, float *dx, float learning_rate, int lr_per_row_nnz,

@@ -424,7 +424,9 @@ void backward_dense_train(Layer &L, const float *x, const float *dy, int64_t B, 
     const float *gT = to_feature_major(L, L.ws_gT, dy, B, L.n_out, L.acc_grad.p, st);
     launch_rowabs(xT, B, L.n_in, L.acc_in.p, st);
     ensure_train_state(L, st);
-    ensure_pow_table(L, p.beta2, L.train_calls + 2, st);
+    // a value scale's counter steps at most twice per call (the scattered
+    // row's step, then its block row's)
+    ensure_pow_table(L, p.beta2, 2 * (L.train_calls + 1) + 1, st);
     ensure_shadow_perm(L);
     if (L.output_scale_trainable) L.mterm.ensure((size_t)(L.W.nnz * 2 * L.rank));
     const uint64_t seed = splitmix64_host(L.rng_seed ^ splitmix64_host(L.rng_calls + 1));
@@ -496,9 +498,6 @@ void backward_sparse_train(Layer &L, const float *x, const int32_t *dptrs, const
     if (!x || !dptrs || !dx) throw_error(SILI_ERR_INVALID, "backward_sparse: NULL buffer");
     if (B > TRAIN_MAX_BATCH)
         throw_error(SILI_ERR_INVALID, "backward_sparse with learning_rate != 0: batch must be <= 1024");
-    if (L.B4.ntiles > 0)
-        throw_error(SILI_ERR_INVALID, "backward_sparse with learning_rate != 0: layers holding block4 tiles are "
-                                      "not supported on the GPU path yet");
     const float *xT = to_feature_major(L, L.ws_xT, x, B, L.n_in, nullptr, st);
     L.xT_cached_batch = 0;
     launch_rowabs(xT, B, L.n_in, L.acc_in.p, st);
@@ -507,17 +506,28 @@ void backward_sparse_train(Layer &L, const float *x, const int32_t *dptrs, const
     // entries present in dy carry nonzero bits (explicit zeros as -0.0)
     launch_densify(dptrs, didx, dvals, B, L.n_out, L.ws_gT.p, L.acc_grad.p, true, nnz_dy, st);
     ensure_train_state(L, st);
-    ensure_pow_table(L, p.beta2, L.train_calls + 2, st);
+    // a value scale's counter steps at most twice per call (the scattered
+    // row's step, then its block row's)
+    ensure_pow_table(L, p.beta2, 2 * (L.train_calls + 1) + 1, st);
     ensure_shadow_perm(L);
     launch_sparse_train(L, xT, L.ws_gT.p, B, dx, p, st);
+    // block4 tiles after the scattered section (sisldo_ops.hpp:848-1100)
+    const uint64_t seed = splitmix64_host(L.rng_seed ^ splitmix64_host(L.rng_calls + 1));
+    launch_sparse_train_b4(L, xT, L.ws_gT.p, B, dx, p, seed, st);
     launch_shadow_val_refresh(L, st);
+    launch_b4_shadow_refresh(L, st);
     for (DScatter *sc : {&L.W, &L.Wt}) {
         sc->stream1.valid = sc->streamK.valid = false;
         sc->cblk.clear();
         sc->cblk_cb = 0;
     }
+    for (DBlock4 *b4 : {&L.B4, &L.B4t}) {
+        b4->cblk.clear();
+        b4->cblk_cbb = 0;
+    }
     L.vs_ones = false;
     ++L.train_calls;
+    ++L.rng_calls;
 }
 
 void export_block4_coords(Layer &L, std::vector<uint32_t> &br, std::vector<uint32_t> &bc) {

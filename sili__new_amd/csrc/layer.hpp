@@ -327,6 +327,9 @@ void launch_train_b4(Layer &L, const float *xT, const float *gT, int64_t B, floa
                      uint64_t seed, hipStream_t st);
 // Shadow tile bytes from the canonical ones (through L.B4t_perm).
 void launch_b4_shadow_refresh(Layer &L, hipStream_t st);
+// The sparse-gradient update of block4 tiles and their block rows' value-scale step.
+void launch_sparse_train_b4(Layer &L, const float *xT, const float *gT, int64_t B, float *dx,
+                            const TrainParams &p, uint64_t seed, hipStream_t st);
 // backward_sparse's update of the canonical store, dx and the value scales;
 // gT dense feature-major with the sparse dy's entries marked (nonzero bits).
 void launch_sparse_train(Layer &L, const float *xT, const float *gT, int64_t B, float *dx, const TrainParams &p,

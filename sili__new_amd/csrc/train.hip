@@ -700,6 +700,155 @@ __global__ __launch_bounds__(256) void k_train_b4(B4TrainArgs a) {
     }
 }
 
+// The sparse-gradient update of block4 tiles (sisldo_ops.hpp:848-1100).
+struct SparseB4Args {
+    const uint32_t *byte_start, *tile_start;
+    const uint8_t *idx;
+    uint8_t *tiles;
+    int64_t brows, n_in, n_out, B, ntiles;
+    const float *xT, *gT;      // gT as SparseTrainArgs
+    float *dx;                 // [B][n_in], added into
+    const float *vs, *os, *is, *ois;  // component 0 of the scales is read
+    double *rowsum;            // [n_in][2], written for rows of block rows with tiles
+    int rank;
+    float lr, beta2, eps;
+    int lr_per_row_nnz, damp;
+    uint64_t seed;
+};
+
+// One wave per canonical block row; batch rows outermost, the row's tiles
+// re-walked per batch row (4 tiles x 16 slots per pass, lanes (tile, li,
+// lj)).  Each slot whose dy entry is nonzero steps its decoded weight and
+// importance (no bounds) from the current byte and is re-quantized at once,
+// stochastically in every layer class as the reference does, with draws
+// splitmix64(seed + 2 id (+1)), id = (b * ntiles + t) * 16 + slot.  Lanes 0..3
+// (one per tile row) add the slots' dx and fp64 row terms in (tile, lj)
+// order per batch row, then into the row's sums, the reference's
+// association.
+__global__ __launch_bounds__(256) void k_sparse_train_b4(SparseB4Args a) {
+    __shared__ uint32_t s_bc[WAVES_T][64];
+    __shared__ float s_dx[WAVES_T][64];
+    __shared__ double s_rg[WAVES_T][64], s_rgc[WAVES_T][64];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t br = (int64_t)blockIdx.x * WAVES_T + wave;
+    if (br >= a.brows) return;
+    const uint32_t t0 = a.tile_start[br], t1 = a.tile_start[br + 1];
+    if (t0 == t1) return;
+    const int64_t B = a.B, rank = a.rank;
+    const float nnz_row = (float)((t1 - t0) * 4u);
+    const float eff_lr = a.lr_per_row_nnz ? a.lr / nnz_row : a.lr;
+    const uint32_t tl = lane >> 4, li = (lane >> 2) & 3u, lj = lane & 3u;
+    const int64_t row = br * 4 + li;
+    const bool row_ok = row < a.n_in;
+    const float val_scale = row_ok ? a.vs[row * rank] : 0.0f;
+    const float imp_scale = (a.is && row_ok) ? a.is[row] : 1.0f;
+    const int64_t my_row = br * 4 + lane;  // lanes 0..3: the row they sum
+    double rs = 0.0, rsc = 0.0;
+    const uint32_t end = a.byte_start[br + 1];
+    for (int64_t b = 0; b < B; ++b) {
+        const float in_val = row_ok ? a.xT[row * B + b] : 0.0f;
+        float dxacc = 0.0f;
+        double rgacc = 0.0, rgcacc = 0.0;
+        uint32_t pos = a.byte_start[br], carry = 0, ebase = t0;
+        while (pos < end) {
+            const Chunk ch = decode_chunk(a.idx, pos, end, carry);
+            if (ch.T == 0ull) break;
+            if (ch.term) s_bc[wave][ch.rank] = ch.col;
+            wave_lds_sync();
+            const uint32_t nt = (uint32_t)__popcll(ch.T);
+            for (uint32_t sub = 0; sub < nt; sub += 4) {
+                const uint32_t trank = sub + tl;
+                const bool tile_ok = trank < nt;
+                const uint32_t bc = tile_ok ? s_bc[wave][trank] : 0u;
+                const int64_t t = (int64_t)ebase + trank;
+                const int64_t col = (int64_t)bc * 4 + lj;
+                const bool has = tile_ok && row_ok && col < a.n_out;
+                const float dy_val = has ? a.gT[col * B + b] : 0.0f;
+                const bool active = has && dy_val != 0.0f;
+                float tdx = 0.0f;
+                double rg = 0.0, rgc = 0.0;
+                if (active) {
+                    const uint32_t slot = lj * 4u + li;
+                    const uint32_t byte = a.tiles[t * 16 + slot];
+                    const float w_decoded = fp4_decode(byte & 0xFu);
+                    const float out_scale = a.os[col * rank];
+                    const float combined_scale = val_scale * out_scale;
+                    const float w = w_decoded * combined_scale;
+                    tdx = w * dy_val;
+                    if (a.lr != 0.0f) {
+                        const float combined_imp_scale = imp_scale * (a.ois ? a.ois[col] : 1.0f);
+                        const float grad = dy_val * in_val;
+                        float imp = fp4_decode(byte >> 4) * combined_imp_scale;
+                        const float contrib = in_val * w;
+                        imp = a.beta2 * imp + (1.0f - a.beta2) * (grad * grad + contrib * contrib);
+                        const float new_w = w + (a.damp ? (-eff_lr * grad) / (__builtin_sqrtf(imp) + a.eps)
+                                                        : (-eff_lr * grad));
+                        const uint64_t id = ((uint64_t)b * (uint64_t)a.ntiles + (uint64_t)t) * 16ull + slot;
+                        const uint64_t base = a.seed + 2ull * id;
+                        const uint32_t wq = fp4_encode_stochastic(new_w / combined_scale, splitmix64(base));
+                        const uint32_t iq = fp4_encode_stochastic(imp / combined_imp_scale, splitmix64(base + 1ull));
+                        a.tiles[t * 16 + slot] = (uint8_t)((iq << 4) | wq);
+                        rg = ((double)w_decoded * (double)out_scale) * (double)grad;
+                        rgc = ((double)w_decoded * (double)out_scale) * (double)contrib;
+                    }
+                }
+                const uint64_t act = __ballot(active);
+                s_dx[wave][lane] = tdx;
+                s_rg[wave][lane] = rg;
+                s_rgc[wave][lane] = rgc;
+                wave_lds_sync();
+                if (lane < 4u) {
+                    for (uint32_t u = 0; u < 4u && sub + u < nt; ++u) {
+                        for (uint32_t j = 0; j < 4u; ++j) {
+                            const uint32_t l = u * 16u + lane * 4u + j;
+                            if (!((act >> l) & 1ull)) continue;
+                            dxacc = dxacc + s_dx[wave][l];
+                            rgacc = rgacc + s_rg[wave][l];
+                            rgcacc = rgcacc + s_rgc[wave][l];
+                        }
+                    }
+                }
+                wave_lds_sync();
+            }
+            carry = chunk_advance(ch, pos, ebase);
+        }
+        if (lane < 4u && my_row < a.n_in) {
+            a.dx[b * a.n_in + my_row] += dxacc;
+            rs = rs + rgacc;
+            rsc = rsc + rgcacc;
+        }
+    }
+    if (lane < 4u && my_row < a.n_in) {
+        a.rowsum[2 * my_row] = rs;
+        a.rowsum[2 * my_row + 1] = rsc;
+    }
+}
+
+// The block rows' value-scale step of the sparse-gradient update
+// (sisldo_ops.hpp:1068-1096): by the row index, step counter (row, 0), no
+// finiteness guards.
+__global__ __launch_bounds__(256) void k_sparse_train_vs_b4(const uint32_t *__restrict__ tile_start, int64_t n_in,
+                                                            int rank, const double *__restrict__ rowsum, float *vs,
+                                                            float *vs_imp, uint32_t *vs_step, float lr, float beta2,
+                                                            float eps, const float *pow_tab) {
+    const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (r >= n_in) return;
+    const int64_t br = r >> 2;
+    const uint32_t nt = tile_start[br + 1] - tile_start[br];
+    if (nt == 0u) return;
+    const double sum = rowsum[2 * r], sum_c = rowsum[2 * r + 1];
+    if (sum == 0.0 && sum_c == 0.0) return;
+    const float scale_eff_lr = lr / (float)(nt * 4u);
+    const float g_agg = (float)sum, contrib_agg = (float)sum_c;
+    const float new_vs_imp = beta2 * vs_imp[r] + (1.0f - beta2) * (g_agg * g_agg + contrib_agg * contrib_agg);
+    const uint32_t step = vs_step[r * rank] + 1u;
+    vs_step[r * rank] = step;
+    const float bias_correction = 1.0f - pow_tab[step];
+    const float hat = bias_correction > 0.0f ? new_vs_imp / bias_correction : new_vs_imp;
+    vs_imp[r] = new_vs_imp;
+    vs[r] = vs[r] - scale_eff_lr * g_agg / (__builtin_sqrtf(hat) + eps);
+}
+
 // dead_S[b*rank + k] = sum_col os_k(col) * dy[b][col] in fp64
 // (linear_disldo.hpp:1995-2007): one block per (b, k).
 __global__ __launch_bounds__(256) void k_dead_S(const float *__restrict__ os, const float *__restrict__ gT,
@@ -935,6 +1084,43 @@ void launch_sparse_train(Layer &L, const float *xT, const float *gT, int64_t B, 
     launch(k_sparse_train_rows, dim3((unsigned)((L.n_in + WAVES_T - 1) / WAVES_T)), dim3(256),
            (uint32_t)(WAVES_T * (2 * B + 512) * sizeof(float)), st, a);
     launch(k_sparse_train_vs, dim3(nblk(L.n_in)), dim3(TPB), 0, st, (const uint32_t *)L.W.elem_start.p, L.n_in,
+           L.rank, (const double *)L.train_rowsum.p, L.vs.p, L.vs_imp.p, L.vs_step.p, p.lr, p.beta2, p.eps,
+           (const float *)L.pow_tab.p);
+    SILI_HIP(hipGetLastError());
+}
+
+void launch_sparse_train_b4(Layer &L, const float *xT, const float *gT, int64_t B, float *dx,
+                            const TrainParams &p, uint64_t seed, hipStream_t st) {
+    if (L.B4.ntiles == 0) return;
+    L.train_rowsum.ensure((size_t)(2 * L.n_in));
+    SparseB4Args a{};
+    a.byte_start = L.B4.byte_start.p;
+    a.tile_start = L.B4.tile_start.p;
+    a.idx = L.B4.idx.p;
+    a.tiles = L.B4.tiles.p;
+    a.brows = L.B4.brows;
+    a.n_in = L.n_in;
+    a.n_out = L.n_out;
+    a.B = B;
+    a.ntiles = L.B4.ntiles;
+    a.xT = xT;
+    a.gT = gT;
+    a.dx = dx;
+    a.vs = L.vs.p;
+    a.os = L.os.p;
+    a.is = L.is.p;
+    a.ois = L.ois.p;
+    a.rowsum = L.train_rowsum.p;
+    a.rank = L.rank;
+    a.lr = p.lr;
+    a.beta2 = p.beta2;
+    a.eps = p.eps;
+    a.lr_per_row_nnz = p.lr_per_row_nnz;
+    a.damp = p.damp_by_importance;
+    a.seed = seed;
+    ProfScope ps("sparse_train_b4", st);
+    launch(k_sparse_train_b4, dim3((unsigned)((L.B4.brows + WAVES_T - 1) / WAVES_T)), dim3(256), 0, st, a);
+    launch(k_sparse_train_vs_b4, dim3(nblk(L.n_in)), dim3(TPB), 0, st, (const uint32_t *)L.B4.tile_start.p, L.n_in,
            L.rank, (const double *)L.train_rowsum.p, L.vs.p, L.vs_imp.p, L.vs_step.p, p.lr, p.beta2, p.eps,
            (const float *)L.pow_tab.p);
     SILI_HIP(hipGetLastError());

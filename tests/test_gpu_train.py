@@ -20,9 +20,9 @@ CLASSES = {"plain": ("SparseLinearLayerDeterministic", "SparseLinearLayer"),
            "noscale": ("SparseLinearLayerNoScaleDeterministic", "SparseLinearLayerNoScale")}
 
 
-def gpu_layer(hip, c, deterministic=True, variant="plain"):
+def gpu_layer(hip, c, deterministic=True, variant="plain", extra=0):
     cls = getattr(hip, CLASSES[variant][0 if deterministic else 1])
-    L = cls(c["n_in"], c["n_out"], len(c["cols"]) + 64)
+    L = cls(c["n_in"], c["n_out"], len(c["cols"]) + 64 + extra)
     L.load_weights_with_importance(c["ptrs"], c["cols"], c["w"], c["imp"])
     if c["rank"] > 1:
         L.set_scale_rank(c["rank"])
@@ -272,3 +272,61 @@ def test_sparse_update_default_learning_rate(hip):
     L.backward_sparse(x, dp, di, dv, 4)
     H.backward_sparse_train(x, dp, di, dv, 4, 0.01)
     assert np.array_equal(L.export_scattered()["val"], H.val[:H.nnz])
+
+
+def _splitmix64(z):
+    M = (1 << 64) - 1
+    z = (z + 0x9E3779B97F4A7C15) & M
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+    return z ^ (z >> 31)
+
+
+@pytest.mark.parametrize("case", range(len(B4_CASES)))
+def test_block4_sparse_update_matches_oracle(hip, case):
+    """backward_sparse with the update on layers holding block4 tiles
+    (sisldo_ops.hpp:848-1100): the reference rounds the tiles stochastically
+    in every layer class; the GPU draws splitmix64(call seed + 2 id), which
+    the oracle replays (draw_mode 1; its other draw mode is pinned exactly to
+    the reference's own draws).  Value bytes and tile bytes bit-exact, the
+    value scales as the scattered sparse update (exact at batch 1), dx within
+    the bar."""
+    from train_util import dx_bound_sparse, sparse_dy
+    n_in, n_out, dens, seed, B, lr, opts, _ = B4_CASES[case]
+    lopts, copts = split_opts(opts)
+    c = add_tiles(make_train_case(n_in, n_out, dens, seed, **lopts), seed=case)
+    H = host_layer(c)
+    H.load_tiles(c["br"], c["bc"], c["tiles"])
+    L = gpu_layer(hip, c, deterministic=(case % 2 == 0), extra=16 * len(c["br"]))
+    L.load_block4_tiles(c["br"], c["bc"], c["tiles"])
+    s0 = 977 + case
+    L.seed_stochastic_rounding(s0)
+    tiles0 = c["tiles"].copy()
+    rng = c["rng"]
+    for step in range(3):
+        what = f"block4 sparse case {case} step {step}"
+        x = rng.normal(size=(B, n_in)).astype(np.float32)
+        dp, di, dv, dense = sparse_dy(rng, B, n_out, density=0.6)
+        bound = dx_bound_sparse(H, dense, lr) + np.abs(dense).sum(1, keepdims=True) * 7.0 * np.abs(x).max()
+        dxg = L.backward_sparse(x, dp, di, dv, B, lr, **copts)
+        call_seed = _splitmix64(s0 ^ _splitmix64(step + 1))
+        dxh, _, _ = H.backward_sparse_train(x, dp, di, dv, B, lr, draw_mode=1, draw_seed=call_seed, **copts)
+        assert np.array_equal(L.export_scattered()["val"], H.val[:H.nnz]), what + ": value bytes"
+        ex = L.export_block4()
+        gb, gc, gt = _sorted_tiles(ex["br"], ex["bc"], ex["tiles"], n_out)
+        hb, hc, ht = _sorted_tiles(H.tile_br, H.tile_bc, H.tiles[:16 * H.n_tiles], n_out)
+        assert np.array_equal(gb, hb) and np.array_equal(gc, hc), what + ": tile set"
+        assert np.array_equal(gt, ht), what + ": tile bytes"
+        assert_close_terms(dxg, dxh, bound, what + ": dx")
+        vs, st = L.get_value_scales(), L.get_scale_state()
+        if B == 1:
+            assert np.array_equal(vs, H.value_scale), what + ": value_scale"
+            assert np.array_equal(st["vs_importance"], H.vs_importance), what + ": vs_importance"
+        else:
+            np.testing.assert_allclose(vs, H.value_scale, rtol=1e-5, atol=0, err_msg=what)
+            np.testing.assert_allclose(st["vs_importance"], H.vs_importance, rtol=1e-5, atol=0, err_msg=what)
+        assert np.array_equal(st["vs_step"], H.vs_step), what + ": vs_step"
+        x2 = rng.normal(size=(2, n_in)).astype(np.float32)
+        assert_close_terms(L.forward_dense(x2), H.forward_dense(x2), H.forward_dense(x2, absmode=True),
+                           what + ": forward after update")
+    assert (H.tiles[:len(tiles0)] != tiles0).sum() > 4, "the tiles barely changed"
