@@ -227,6 +227,11 @@ def algorithmic(info, n_in, n_out, B, wl=None):
         out["fwd:gather_b4"] = Bt_out + Bs + 4 * B * n_in + 4 * B * n_out
         out["bwd:gather_b4"] = Bt_in + Bs + 4 * B * n_out + 4 * B * n_in
         out["bwd:sddmm_b4"] = (Bt_in - 16 * T) + 4 * B * n_in + 4 * B * n_out + 4 * 16 * T
+        # optimizer update of the tiles: tile bytes read and written, block
+        # index and row starts, xT and gT read, dX read and written, the
+        # rows' scales and RMSprop state read and written, output scales
+        out["bwd:train_b4"] = (Bt_in + 16 * T) + 4 * B * n_in + 4 * B * n_out + 8 * B * n_in \
+            + 2 * 12 * n_in + 4 * n_out
     if wl is not None and wl.x_ptrs is not None and wl.cols is not None:
         # sparse-input forward: value + index bytes of the rows any batch row
         # activates, row starts, scales, the input CSR and the dense output
@@ -305,20 +310,35 @@ def make_step(cfg, api, B, stream, train_lr=0.0):
             else:
                 api.ck(L.sili_backward_dense(h, None, d["g"], B, d["dx"], d["gws"], None, 0.0, stream))
         elif cfg == 3:
-            api.ck(L.sili_backward_dense(h, None, d["g"], B, d["dx"], None, d["gwb"], 0.0, stream))
+            if train_lr:
+                api.ck(L.sili_backward_dense(h, None, d["g"], B, d["dx"], None, None, train_lr, stream))
+            else:
+                api.ck(L.sili_backward_dense(h, None, d["g"], B, d["dx"], None, d["gwb"], 0.0, stream))
     return step
 
 
-def cpu_baseline_train(wl, seconds, lr):
-    """Config 1 with the optimizer update: the reference's own compiled
+def cpu_baseline_train(wl, seconds, lr, cfg=1):
+    """Configs 1 and 3 with the optimizer update: the reference's own compiled
     disldo_forward + disldo_backward(lr) (oracle/_ref, OpenMP) on this host;
     without _ref, the oracle's single-thread restatement of the update."""
     from oracle import HostLayer, RefLayer, have_ref
     x, g = wl.x.astype(np.float32), wl.g.astype(np.float32)
+    tiles = cfg == 3 and wl.tile_br is not None and len(wl.tile_br) > 0
+    # a block4-only workload has no scattered store: an empty CSR
+    ptrs = wl.ptrs if wl.ptrs is not None else np.zeros(wl.n_in + 1, np.int32)
+    cols = wl.cols if wl.cols is not None else np.zeros(0, np.int32)
+    q = wl.q if wl.q is not None else np.zeros(0, np.float32)
     if have_ref():
         threads = os.cpu_count() or 1
-        R = RefLayer(wl.n_in, wl.n_out, wl.ptrs, wl.cols, wl.q).set_scales(wl.value_scale)
+        R = RefLayer(wl.n_in, wl.n_out, ptrs, cols, q)
+        if wl.value_scale is not None:
+            R.set_scales(wl.value_scale)
         R.compact()
+        if tiles:
+            tb = np.asarray(wl.tile_bytes, np.uint8).reshape(-1, 16)
+            for t in range(len(wl.tile_br)):
+                R.put_tile(int(wl.tile_br[t]), int(wl.tile_bc[t]), tb[t])
+            R.block4_headroom(0.2, 16 * 64)
 
         def step():
             R.forward_dense(x, threads=threads)
@@ -326,7 +346,11 @@ def cpu_baseline_train(wl, seconds, lr):
         kind, what = "reference", "the reference's disldo_forward + disldo_backward(lr) from oracle/_ref"
     else:
         threads = 1
-        H = HostLayer(wl.n_in, wl.n_out).load_csr(wl.ptrs, wl.cols, w=wl.q).set_scales(wl.value_scale)
+        H = HostLayer(wl.n_in, wl.n_out).load_csr(ptrs, cols, w=q)
+        if wl.value_scale is not None:
+            H.set_scales(wl.value_scale)
+        if tiles:
+            H.load_tiles(wl.tile_br, wl.tile_bc, wl.tile_bytes)
 
         def step():
             H.forward_dense(x, threads=1)
@@ -342,7 +366,7 @@ def cpu_baseline_train(wl, seconds, lr):
             break
     med = float(np.median(times))
     return {"value": round(wl.nnz / med / 1e9, 5), "unit": "GNNZ/s", "cores": threads, "kind": kind,
-            "sample": f"full config-1 training step ({what}, lr {lr}), {len(times)} reps, "
+            "sample": f"full config-{cfg} training step ({what}, lr {lr}), {len(times)} reps, "
                       f"median {med * 1e3:.1f} ms/step"}
 
 
@@ -640,9 +664,9 @@ def main():
         pool.append(build_copy(cfg, wl, hip, api))
     t_build = time.perf_counter() - t_build
     stream = api.L.sili_stream(pool[0]["h"])
-    train_lr = a.train_lr if cfg == 1 else 0.0
-    if a.train_lr and cfg != 1:
-        print(json.dumps({"error": "--train-lr applies to config 1 only"}))
+    train_lr = a.train_lr if cfg in (1, 3) else 0.0
+    if a.train_lr and cfg not in (1, 3):
+        print(json.dumps({"error": "--train-lr applies to configs 1 and 3 only"}))
         sys.exit(2)
     run = make_step(cfg, api, B, stream, train_lr)
 
@@ -706,7 +730,20 @@ def main():
 
     nnz_s, n_tiles = info["nnz_scattered"], info["n_tiles"]
     units = nnz_s + 16 * n_tiles  # stored synapses (scattered + block4 slots)
-    if cfg == 3:
+    if cfg == 3 and train_lr:
+        dom_bytes = alg.get(dom_name)
+        achieved = dom_bytes / (dom_avg_ms * 1e-3) / 1e9 if dom_bytes else None
+        roof = {"bound": "hbm", "kernel": dom_name, "achieved": round(achieved, 2) if achieved else None,
+                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 5) if achieved else None,
+                "traffic": None, "avg_op_ms": round(dom_avg_ms, 5), "launches_per_op": launches,
+                "algorithmic_bytes": dom_bytes,
+                "slot_steps_per_s": round(16 * n_tiles * B / (dom_avg_ms * 1e-3), 1),
+                "note": ("k_train_b4 runs each tile slot's batch steps as a dependent chain of VALU "
+                         "instructions (as k_train_rows per synapse): bound by instruction issue, not HBM")}
+        step_bytes = alg["fwd:gather_b4"] + alg["bwd:train_b4"]
+        flops = 2 * 2 * units * B
+    elif cfg == 3:
         # FP32-compute bound: 2 flops per slot per batch column
         dom_flops = 2 * 16 * n_tiles * B
         achieved = dom_flops / (dom_avg_ms * 1e-3) / 1e12
@@ -792,7 +829,7 @@ def main():
     if a.no_cpu_baseline:
         out["cpu_baseline"] = None
     elif train_lr:
-        out["cpu_baseline"] = cpu_baseline_train(wl, a.cpu_seconds, train_lr)
+        out["cpu_baseline"] = cpu_baseline_train(wl, a.cpu_seconds, train_lr, cfg)
     else:
         out["cpu_baseline"] = cpu_baseline(cfg, wl, a.cpu_seconds)
     if a.verbose:
