@@ -542,19 +542,43 @@ struct B4TrainArgs {
 // edge tile adds its fp64 row-gradient terms one by one (its scalar path).
 // The tiles' fp64 row partials are added in tile order; then the block
 // rows' scale step.
+// Lane J of the calling lane's quad (DPP quad_perm, a VALU move).
+template <int J>
+__device__ __forceinline__ float quad_lane(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), J * 0x55, 0xF, 0xF, false));
+}
+template <int J>
+__device__ __forceinline__ double quad_lane(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)u, J * 0x55, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(u >> 32), J * 0x55, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+// ((l0 + l1) + l2) + l3 over the quad, on every lane of it
+template <typename T>
+__device__ __forceinline__ T quad_sum(T v) {
+    return ((quad_lane<0>(v) + quad_lane<1>(v)) + quad_lane<2>(v)) + quad_lane<3>(v);
+}
+
+constexpr uint32_t WAVES_B4 = 2;  // waves per block of k_train_b4 (LDS: 4 rows x B floats per wave)
+
 template <int RANK>
-__global__ __launch_bounds__(256) void k_train_b4(B4TrainArgs a) {
-    __shared__ uint32_t s_bc[WAVES_T][64];
-    __shared__ double s_mr[WAVES_T][4][4][2 * RANK];  // [tile][li][k | contrib k]
+__global__ __launch_bounds__(128) void k_train_b4(B4TrainArgs a) {
+    __shared__ uint32_t s_bc[WAVES_B4][64];
+    __shared__ double s_mr[WAVES_B4][4][4][2 * RANK];  // [tile][li][k | contrib k]
+    extern __shared__ float s_dxb[];                    // [wave][li][B]: the block row's dx terms
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const int64_t br = (int64_t)blockIdx.x * WAVES_T + wave;
+    const int64_t br = (int64_t)blockIdx.x * WAVES_B4 + wave;
     if (br >= a.brows) return;
     const uint32_t t0 = a.tile_start[br], t1 = a.tile_start[br + 1];
     if (t0 == t1) return;
     const int64_t B = a.B;
+    float *sdx = s_dxb + (int64_t)wave * 4 * B;
+    for (int64_t i = lane; i < 4 * B; i += 64) sdx[i] = 0.0f;
+    wave_lds_sync();
     const uint32_t nnz_row = (t1 - t0) * 4u;
     const float eff_lr = a.lr_per_row_nnz ? a.lr / (float)nnz_row : a.lr;
-    const uint32_t tl = lane >> 4, li = (lane >> 2) & 3u, lj = lane & 3u, qbase = lane & ~3u;
+    const uint32_t tl = lane >> 4, li = (lane >> 2) & 3u, lj = lane & 3u;
     const int64_t row = br * 4 + li;
     const bool row_ok = row < a.n_in;
     double rowacc[2 * RANK];  // lanes 0..3: row br*4 + lane
@@ -609,35 +633,30 @@ __global__ __launch_bounds__(256) void k_train_b4(B4TrainArgs a) {
                 q = q + bounded_update_cw(g, ci, S, eff_lr, a.eps, a.damp != 0, a.max_abs_delta);
                 const float qf = (q == 0.0f) ? a.zero_escape_eps : q;
                 const float tdx = has ? (q * S) * dyv : 0.0f;
-                float tr[2 * RANK];
-                double dr[2 * RANK];
 #pragma unroll
                 for (int k = 0; k < RANK; ++k) {
-                    tr[k] = (qf * os_k[k]) * g;
-                    tr[RANK + k] = (qf * os_k[k]) * contrib;
-                    dr[k] = has ? ((double)qf * (double)os_k[k]) * (double)g : 0.0;
-                    dr[RANK + k] = has ? ((double)qf * (double)os_k[k]) * (double)contrib : 0.0;
                     mc[k] = mc[k] + (qf * vs_k[k]) * g;
                     mc[RANK + k] = mc[RANK + k] + (qf * vs_k[k]) * contrib;
                 }
-                // the tile row's 4 slots, in lane order, on its first lane
-                const float x1 = __shfl(tdx, (int)(qbase + 1), 64), x2 = __shfl(tdx, (int)(qbase + 2), 64),
-                            x3 = __shfl(tdx, (int)(qbase + 3), 64);
+                // the tile row's 4 dx terms, summed on the quad, into the
+                // block row's LDS row (4 tiles of a pass add to one address)
+                const float qdx = quad_sum(tdx);
+                if (lj == 0u && tile_ok) atomicAdd(&sdx[(int64_t)li * B + b], qdx);
+                // a quad is one tile row: full is uniform over it
                 if (full) {
-                    if (lj == 0u && row_ok) atomicAdd(&a.dx[b * a.n_in + row], ((tdx + x1) + x2) + x3);
-                } else if (has) {
-                    atomicAdd(&a.dx[b * a.n_in + row], tdx);
-                }
 #pragma unroll
-                for (int k = 0; k < 2 * RANK; ++k) {
-                    if (full) {
-                        const float y1 = __shfl(tr[k], (int)(qbase + 1), 64), y2 = __shfl(tr[k], (int)(qbase + 2), 64),
-                                    y3 = __shfl(tr[k], (int)(qbase + 3), 64);
-                        mr[k] = mr[k] + (double)(((tr[k] + y1) + y2) + y3);
-                    } else {
-                        const double z1 = __shfl(dr[k], (int)(qbase + 1), 64), z2 = __shfl(dr[k], (int)(qbase + 2), 64),
-                                     z3 = __shfl(dr[k], (int)(qbase + 3), 64);
-                        mr[k] = (((mr[k] + dr[k]) + z1) + z2) + z3;
+                    for (int k = 0; k < RANK; ++k) {
+                        mr[k] = mr[k] + (double)quad_sum((qf * os_k[k]) * g);
+                        mr[RANK + k] = mr[RANK + k] + (double)quad_sum((qf * os_k[k]) * contrib);
+                    }
+                } else {
+#pragma unroll
+                    for (int k = 0; k < RANK; ++k) {
+                        const double d0 = has ? ((double)qf * (double)os_k[k]) * (double)g : 0.0;
+                        const double d1 = has ? ((double)qf * (double)os_k[k]) * (double)contrib : 0.0;
+                        mr[k] = (((mr[k] + quad_lane<0>(d0)) + quad_lane<1>(d0)) + quad_lane<2>(d0)) + quad_lane<3>(d0);
+                        mr[RANK + k] =
+                            (((mr[RANK + k] + quad_lane<0>(d1)) + quad_lane<1>(d1)) + quad_lane<2>(d1)) + quad_lane<3>(d1);
                     }
                 }
             }
@@ -673,6 +692,12 @@ __global__ __launch_bounds__(256) void k_train_b4(B4TrainArgs a) {
             wave_lds_sync();
         }
         carry = chunk_advance(ch, pos, ebase);
+    }
+    wave_lds_sync();
+    for (uint32_t l = 0; l < 4u; ++l) {
+        const int64_t rr = br * 4 + l;
+        if (rr >= a.n_in) break;
+        for (int64_t b = lane; b < B; b += 64) a.dx[b * a.n_in + rr] += sdx[(int64_t)l * B + b];
     }
     // the block rows' scale step (linear_disldo.hpp:1923-1951)
     const int64_t r = br * 4 + lane;
@@ -1164,13 +1189,14 @@ void launch_train_b4(Layer &L, const float *xT, const float *gT, int64_t B, floa
     a.damp = p.damp_by_importance;
     a.stochastic = L.stochastic_rounding ? 1 : 0;
     a.seed = seed;
-    const dim3 grid((unsigned)((L.B4.brows + WAVES_T - 1) / WAVES_T)), block(256);
+    const dim3 grid((unsigned)((L.B4.brows + WAVES_B4 - 1) / WAVES_B4)), block(64 * WAVES_B4);
+    const uint32_t shmem = (uint32_t)(WAVES_B4 * 4 * B * sizeof(float));  // B <= 1024: <= 32 KiB
     ProfScope ps("train_b4", st);
     switch (L.rank) {
-        case 1: launch(k_train_b4<1>, grid, block, 0, st, a); break;
-        case 2: launch(k_train_b4<2>, grid, block, 0, st, a); break;
-        case 3: launch(k_train_b4<3>, grid, block, 0, st, a); break;
-        default: launch(k_train_b4<4>, grid, block, 0, st, a); break;
+        case 1: launch(k_train_b4<1>, grid, block, shmem, st, a); break;
+        case 2: launch(k_train_b4<2>, grid, block, shmem, st, a); break;
+        case 3: launch(k_train_b4<3>, grid, block, shmem, st, a); break;
+        default: launch(k_train_b4<4>, grid, block, shmem, st, a); break;
     }
     SILI_HIP(hipGetLastError());
 }
