@@ -365,7 +365,8 @@ def cpu_baseline_train(wl, seconds, lr, cfg=1):
         if time.perf_counter() > t_end or len(times) >= 30:
             break
     med = float(np.median(times))
-    return {"value": round(wl.nnz / med / 1e9, 5), "unit": "GNNZ/s", "cores": threads, "kind": kind,
+    units = len(cols) + (16 * len(wl.tile_br) if tiles else 0)  # stored synapses, as the GPU line counts them
+    return {"value": round(units / med / 1e9, 5), "unit": "GNNZ/s", "cores": threads, "kind": kind,
             "sample": f"full config-{cfg} training step ({what}, lr {lr}), {len(times)} reps, "
                       f"median {med * 1e3:.1f} ms/step"}
 
