@@ -624,9 +624,10 @@ __global__ __launch_bounds__(128) void k_train_b4(B4TrainArgs a) {
             }
             const float *xrow = a.xT + (row_ok ? row : 0) * B;
             const float *gcol = a.gT + (has ? col : 0) * B;
-            for (int64_t b = 0; b < B; ++b) {
-                const float iv = row_ok ? xrow[b] : 0.0f;
-                const float dyv = has ? gcol[b] : 0.0f;
+            // one batch step of this lane's slot (b in order)
+            auto step = [&](int64_t b, float iv_raw, float dy_raw) {
+                const float iv = row_ok ? iv_raw : 0.0f;
+                const float dyv = has ? dy_raw : 0.0f;
                 const float g = dyv * iv;
                 const float contrib = q0 * iv;
                 ci = bounded_update_ci(ci, g, contrib, a.beta2, a.min_decay_frac, a.max_ci);
@@ -659,7 +660,20 @@ __global__ __launch_bounds__(128) void k_train_b4(B4TrainArgs a) {
                             (((mr[RANK + k] + quad_lane<0>(d1)) + quad_lane<1>(d1)) + quad_lane<2>(d1)) + quad_lane<3>(d1);
                     }
                 }
+            };
+            int64_t b = 0;
+            if ((B & 3) == 0) {
+                // 4 batch steps per pair of 16-byte loads (rows are B floats, B % 4 == 0)
+                for (; b < B; b += 4) {
+                    const float4 xv = *reinterpret_cast<const float4 *>(xrow + b);
+                    const float4 gv = *reinterpret_cast<const float4 *>(gcol + b);
+                    step(b, xv.x, gv.x);
+                    step(b + 1, xv.y, gv.y);
+                    step(b + 2, xv.z, gv.z);
+                    step(b + 3, xv.w, gv.w);
+                }
             }
+            for (; b < B; ++b) step(b, xrow[b], gcol[b]);
             if (has) {
                 const float imp = ci / cis;
                 uint32_t wq, iq;
