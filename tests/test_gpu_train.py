@@ -169,10 +169,12 @@ def _sorted_tiles(br, bc, tiles, n_out):
 def test_block4_update_matches_oracle(hip, case):
     """Layers holding block4 tiles (linear_disldo.hpp:962-1951): tile bytes
     and value bytes bit-exact, scales as in the scattered cases, dx within
-    the bar (the tile rows' dx terms are added by atomics)."""
+    the bar (a tile row's dx terms are summed in a per-wave LDS row buffer,
+    then added to the scattered rows' dx once per row and batch step)."""
+    from train_util import dx_bound_tiles, tile_opts
     n_in, n_out, dens, seed, B, lr, opts, variant = B4_CASES[case]
     lopts, copts = split_opts(opts)
-    c = add_tiles(make_train_case(n_in, n_out, dens, seed, **lopts), seed=case)
+    c = add_tiles(make_train_case(n_in, n_out, dens, seed, **lopts), seed=case, **tile_opts(opts))
     H = host_layer(c)
     H.load_tiles(c["br"], c["bc"], c["tiles"])
     cls = getattr(hip, CLASSES[variant][0])
@@ -195,7 +197,7 @@ def test_block4_update_matches_oracle(hip, case):
         what = f"block4 case {case} {variant} step {step}"
         x = rng.normal(size=(B, n_in)).astype(np.float32)
         dy = rng.normal(size=(B, n_out)).astype(np.float32)
-        bound = dx_bound(H, dy, lr) + np.abs(dy).sum(1, keepdims=True) * 7.0 * np.abs(x).max()
+        bound = dx_bound(H, dy, lr) + dx_bound_tiles(H, dy, lr)
         L.forward_dense(x)
         dxg = L.backward_dense(dy, lr, **copts)
         dxh, _, _ = H.backward_train(x, dy, lr, variant=variant, **copts)
@@ -291,10 +293,10 @@ def test_block4_sparse_update_matches_oracle(hip, case):
     the reference's own draws).  Value bytes and tile bytes bit-exact, the
     value scales as the scattered sparse update (exact at batch 1), dx within
     the bar."""
-    from train_util import dx_bound_sparse, sparse_dy
+    from train_util import dx_bound_sparse, dx_bound_tiles, sparse_dy, tile_opts
     n_in, n_out, dens, seed, B, lr, opts, _ = B4_CASES[case]
     lopts, copts = split_opts(opts)
-    c = add_tiles(make_train_case(n_in, n_out, dens, seed, **lopts), seed=case)
+    c = add_tiles(make_train_case(n_in, n_out, dens, seed, **lopts), seed=case, **tile_opts(opts))
     H = host_layer(c)
     H.load_tiles(c["br"], c["bc"], c["tiles"])
     L = gpu_layer(hip, c, deterministic=(case % 2 == 0), extra=16 * len(c["br"]))
@@ -307,7 +309,7 @@ def test_block4_sparse_update_matches_oracle(hip, case):
         what = f"block4 sparse case {case} step {step}"
         x = rng.normal(size=(B, n_in)).astype(np.float32)
         dp, di, dv, dense = sparse_dy(rng, B, n_out, density=0.6)
-        bound = dx_bound_sparse(H, dense, lr) + np.abs(dense).sum(1, keepdims=True) * 7.0 * np.abs(x).max()
+        bound = dx_bound_sparse(H, dense, lr) + dx_bound_tiles(H, dense, lr, sparse=True)
         dxg = L.backward_sparse(x, dp, di, dv, B, lr, **copts)
         call_seed = _splitmix64(s0 ^ _splitmix64(step + 1))
         dxh, _, _ = H.backward_sparse_train(x, dp, di, dv, B, lr, draw_mode=1, draw_seed=call_seed, **copts)

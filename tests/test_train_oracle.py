@@ -134,23 +134,23 @@ def test_block4_update_matches_reference(case):
     update, with the reference's rows given room for dense tiles (no
     eviction).  Contracted build exact on codes, tile bytes and scale state
     (dx within the bar: the 4-lane sums are re-associated by -ffast-math)."""
-    from train_util import add_tiles
+    from train_util import add_tiles, dx_bound_tiles, tile_opts
     n_in, n_out, dens, seed, B, lr, opts, variant = B4_CASES[case]
     lopts, copts = split_opts(opts)
-    c = add_tiles(make_train_case(n_in, n_out, dens, seed, **lopts), seed=case)
+    c = add_tiles(make_train_case(n_in, n_out, dens, seed, **lopts), seed=case, **tile_opts(opts))
     assert len(c["br"]) > 0 and ((c["bc"] * 4 + 4 > n_out).any() or n_out % 4 == 0)
     tiles0 = c["tiles"].copy()
     H, R = host_layer(c), ref_layer(c)
     H.load_tiles(c["br"], c["bc"], c["tiles"])
     for t in range(len(c["br"])):
         R.put_tile(int(c["br"][t]), int(c["bc"][t]), c["tiles"][16 * t:16 * t + 16])
-    R.block4_headroom(0.2, 16 * 64)
+    R.block4_headroom(0.2, 16 * max(64, int(np.bincount(c["br"]).max())))
     rng = c["rng"]
     for step in range(3):
         what = f"case {case} {variant} step {step}"
         x = rng.normal(size=(B, n_in)).astype(np.float32)
         dy = rng.normal(size=(B, n_out)).astype(np.float32)
-        bound = dx_bound(H, dy, lr) + np.abs(dy).sum(1, keepdims=True) * 7.0 * np.abs(x).max()
+        bound = dx_bound(H, dy, lr) + dx_bound_tiles(H, dy, lr)
         dxh, _, _ = H.backward_train(x, dy, lr, contracted=True, variant=variant, **copts)
         dxr, _, _ = R.backward_train(x, dy, lr, variant=variant, **copts)
         _, _, _, vr = R.export()
@@ -174,22 +174,22 @@ def test_block4_sparse_update_matches_reference(case):
     replays the same draws in the same order (draw_mode 0).  Codes, tile
     bytes and the value scales' state exact (contracted build), dx within the
     bar."""
-    from train_util import add_tiles, dx_bound_sparse, sparse_dy
+    from train_util import add_tiles, dx_bound_sparse, dx_bound_tiles, sparse_dy, tile_opts
     n_in, n_out, dens, seed, B, lr, opts, _ = B4_CASES[case]
     lopts, copts = split_opts(opts)
-    c = add_tiles(make_train_case(n_in, n_out, dens, seed, **lopts), seed=case)
+    c = add_tiles(make_train_case(n_in, n_out, dens, seed, **lopts), seed=case, **tile_opts(opts))
     tiles0 = c["tiles"].copy()
     H, R = host_layer(c), ref_layer(c)
     H.load_tiles(c["br"], c["bc"], c["tiles"])
     for t in range(len(c["br"])):
         R.put_tile(int(c["br"][t]), int(c["bc"][t]), c["tiles"][16 * t:16 * t + 16])
-    R.block4_headroom(0.2, 16 * 64)
+    R.block4_headroom(0.2, 16 * max(64, int(np.bincount(c["br"]).max())))
     rng = c["rng"]
     for step in range(3):
         what = f"block4 sparse case {case} step {step}"
         x = rng.normal(size=(B, n_in)).astype(np.float32)
         dp, di, dv, dense = sparse_dy(rng, B, n_out, density=0.6)
-        bound = dx_bound_sparse(H, dense, lr) + np.abs(dense).sum(1, keepdims=True) * 7.0 * np.abs(x).max()
+        bound = dx_bound_sparse(H, dense, lr) + dx_bound_tiles(H, dense, lr, sparse=True)
         dseed = 1000 * case + step + 1
         dxh, _, _ = H.backward_sparse_train(x, dp, di, dv, B, lr, contracted=True, draw_mode=0, draw_seed=dseed,
                                             **copts)

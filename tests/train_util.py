@@ -80,8 +80,38 @@ LAYER_OPTS = ("rank", "empty_rows", "os_trainable", "imp_scales")
 
 def split_opts(opts):
     layer = {k: v for k, v in opts.items() if k in LAYER_OPTS}
-    call = {k: v for k, v in opts.items() if k not in LAYER_OPTS}
+    call = {k: v for k, v in opts.items() if k not in LAYER_OPTS and k not in TILE_OPTS}
     return layer, call
+
+
+def tile_opts(opts):
+    return {k: v for k, v in opts.items() if k in TILE_OPTS}
+
+
+def dx_bound_tiles(H, dy, lr, max_abs_delta=2.0, sparse=False):
+    """dx_bound (dense update) or dx_bound_sparse (sparse update) over the
+    block4 tile slots of H: sum over each tile row's slots of |w| * |dy|,
+    |w| bounded over the call as for scattered synapses."""
+    from sili__new_amd.codec import fp4_decode_np
+    dy = np.atleast_2d(dy)
+    B = dy.shape[0]
+    T = np.zeros((H.n_in, B))
+    if H.n_tiles == 0:
+        return T.T
+    tiles = H.tiles[:16 * H.n_tiles].reshape(-1, 16)
+    s = np.arange(16)
+    rows = (np.asarray(H.tile_br, np.int64)[:, None] * 4 + s % 4).ravel()
+    cols = (np.asarray(H.tile_bc, np.int64)[:, None] * 4 + s // 4).ravel()
+    ok = (rows < H.n_in) & (cols < H.n_out)
+    rows, cols = rows[ok], cols[ok]
+    q0 = fp4_decode_np(tiles.ravel()[ok] & 0xF).astype(np.float64)
+    q0[~np.isfinite(q0)] = 6.0
+    vs = H.value_scale.reshape(H.n_in, H.rank).astype(np.float64)
+    os_ = H.output_scale.reshape(H.n_out, H.rank).astype(np.float64)
+    S = np.abs(vs[rows] * os_[cols]).sum(1)
+    mag = 6.0 * S if sparse else (np.abs(q0) + B * abs(lr) * max_abs_delta) * S
+    np.add.at(T, rows, (np.abs(dy[:, cols].astype(np.float64)) * mag).T)
+    return T.T
 
 
 def dx_bound(H, dy, lr, max_abs_delta=2.0):
@@ -142,9 +172,11 @@ def dx_bound_sparse(H, dy_dense, lr, max_step=None):
     return T.T
 
 
-def add_tiles(c, tile_density=0.3, seed=0):
+def add_tiles(c, tile_density=0.3, seed=0, tile_gap=None):
     """Block4 tiles over the windows of c that hold no scattered synapse (all
-    16 slots coded, some empty), edge windows included."""
+    16 slots coded, some empty), edge windows included.  tile_gap = (a, b):
+    every other block row holds no tile in block columns [a, b), so its next
+    tile's block-column delta takes a multi-byte ULEB128."""
     rng = np.random.default_rng(1000 + seed)
     n_in, n_out = c["n_in"], c["n_out"]
     brs, bcs = (n_in + 3) // 4, (n_out + 3) // 4
@@ -152,6 +184,8 @@ def add_tiles(c, tile_density=0.3, seed=0):
     for r in range(n_in):
         for col in c["cols"][c["ptrs"][r]:c["ptrs"][r + 1]]:
             used[r // 4, col // 4] = True
+    if tile_gap is not None:
+        used[::2, tile_gap[0]:tile_gap[1]] = True
     keys = [k for k in np.flatnonzero(rng.random(brs * bcs) < tile_density) if not used.flat[k]]
     if n_out % 4:  # at least one edge tile (columns past n_out in the window)
         free = [b * bcs + bcs - 1 for b in range(brs) if not used[b, bcs - 1]]
@@ -174,7 +208,9 @@ def add_tiles(c, tile_density=0.3, seed=0):
 
 
 # block4 update cases: (n_in, n_out, density, seed, batch, lr, options, variant);
-# odd widths give edge tiles
+# odd widths give edge tiles.  The wide cases hold > 64 tiles per block row
+# (block rows over several 64-byte decode windows), block-column gaps of 140
+# (two-byte deltas) and batches past the kernels' 64-step LDS row passes.
 B4_CASES = [
     (40, 37, 0.05, 21, 1, 0.3, {}, "plain"),
     (44, 50, 0.05, 22, 3, 0.3, {}, "plain"),
@@ -183,4 +219,8 @@ B4_CASES = [
     (40, 37, 0.05, 25, 2, 0.3, {}, "noscale"),
     (64, 61, 0.05, 26, 12, 0.1, dict(imp_scales=True, lr_per_row_nnz=True), "plain"),
     (33, 45, 0.05, 27, 1, 0.5, dict(damp_by_importance=False), "plain"),
+    (24, 1030, 0.01, 28, 256, 0.004, dict(tile_density=0.5, tile_gap=(60, 200)), "plain"),
+    (24, 1030, 0.01, 29, 1024, 0.001, dict(tile_density=0.5, tile_gap=(60, 200)), "plain"),
+    (20, 1027, 0.01, 30, 100, 0.01, dict(tile_density=0.5, tile_gap=(61, 201)), "resync"),
 ]
+TILE_OPTS = ("tile_density", "tile_gap")
