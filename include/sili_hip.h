@@ -132,6 +132,20 @@ int sili_get_output_scale(const sili_layer *layer, float *os);
 int sili_forward_dense(sili_layer *layer, const float *x, int64_t batch, float *y,
                        void *stream);
 
+/* forward_dense_noalloc: no counterpart in the reference.  For callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): the same y as sili_forward_dense
+ * (within the fp32 bar), computed without any device allocation.  The
+ * feature-major copy of x lives in a per-device scratch of 32 MiB held by the
+ * library until the process ends, so n_inputs * batch <= 8388608 for
+ * batch > 1 (SILI_ERR_INVALID otherwise).  It reads only structures built at
+ * load (the segment gathers), does not keep x as the stored forward input
+ * (a following backward_dense must pass x), records no profiler events, and
+ * shares the scratch with every other call on the same GPU: calls that overlap
+ * on one GPU race. */
+int sili_forward_dense_noalloc(sili_layer *layer, const float *x, int64_t batch, float *y,
+                               void *stream);
+
 /* backward_dense (sili/cpu_backend.cpp:496-529, linear_disldo.hpp:462-2113):
  * dx [batch,n_in] = W^T-gather of dy (overwritten).  x may be NULL: then the
  * input of the last forward_dense on this layer is used, as the reference's

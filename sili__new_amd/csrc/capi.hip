@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <new>
 #include <stdexcept>
 #include <string>
@@ -16,6 +17,11 @@
 struct sili_layer {
     sili::Layer L;
 };
+
+// The no-allocation forward's scratch: every GPU the library runs on holds its
+// own copy until the process ends.
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(32) << 20;
+static __device__ __align__(256) float scratch[NOALLOC_SCRATCH_BYTES / sizeof(float)];
 
 namespace sili {
 
@@ -111,6 +117,28 @@ void fill(float *p, int64_t n, float v, hipStream_t st) {
 }
 
 void set_device(const Layer &L) { SILI_HIP(hipSetDevice(L.device)); }
+
+// Scratch of sili_forward_dense_noalloc (the file-scope array `scratch`):
+// host code never names the array in a kernel argument or a copy, it uses the
+// per-device address that hipGetSymbolAddress returns, resolved once per
+// device at the first sili_create on that device, with the device current.
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[MAX_DEVICES] = {};
+
+void resolve_scratch(int device) {
+    if (device < 0 || device >= MAX_DEVICES) throw_error(SILI_ERR_INVALID, "device ordinal out of range");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[device]) return;
+    void *ptr = nullptr;
+    SILI_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    g_scratch_ptr[device] = static_cast<float *>(ptr);
+}
+
+float *scratch_on(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return (device >= 0 && device < MAX_DEVICES) ? g_scratch_ptr[device] : nullptr;
+}
 
 hipStream_t pick(const Layer &L, void *stream) {
     return stream ? reinterpret_cast<hipStream_t>(stream) : L.stream;
@@ -309,6 +337,36 @@ void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st
     }
     if (L.B4t.ntiles > 0 && !gather_b4_colblocked(L, L.B4t, shadow_scales(L), xT, B, y, L.n_out, SKIP_NONE, st))
         launch_gather_b4(L.B4t.plan(), shadow_scales(L), xT, B, y, L.n_out, B, SKIP_NONE, st);
+}
+
+// forward_dense without device allocation: the feature-major copy of x goes
+// to the per-device scratch, and only structures built at load are read (the
+// segment gathers over the shadow stores: no stream or column-block copies,
+// which are built on first use).  No profiler context, so no events either.
+void forward_dense_noalloc(Layer &L, const float *x, int64_t B, float *y, hipStream_t st) {
+    if (B <= 0) throw_error(SILI_ERR_INVALID, "forward_dense_noalloc: batch must be >= 1");
+    if (!x || !y) throw_error(SILI_ERR_INVALID, "forward_dense_noalloc: NULL buffer");
+    if (B > 1 && (uint64_t)L.n_in * (uint64_t)B > NOALLOC_SCRATCH_BYTES / sizeof(float))
+        throw_error(SILI_ERR_INVALID, "forward_dense_noalloc: n_inputs * batch exceeds the scratch of " +
+                                          std::to_string(NOALLOC_SCRATCH_BYTES / sizeof(float)) + " floats");
+    float *scr = scratch_on(L.device);
+    if (!scr) throw_error(SILI_ERR_RUNTIME, "forward_dense_noalloc: scratch not resolved on this device");
+    const float *xT = x;
+    if (B > 1) {
+        launch_transpose(x, B, L.n_in, scr, nullptr, st);
+        xT = scr;
+    }
+    // the stored forward input (ws_xT) no longer belongs to the last forward
+    L.xT_cached_batch = 0;
+    const int skip = L.has_nonfinite ? SKIP_ZERO : SKIP_NONE;
+    const ScaleView ssc = shadow_scales(L);
+    if (L.Wt.nnz == 0) {
+        fill(y, B * L.n_out, 0.0f, st);
+    } else {
+        launch_zero_split_rows(L.Wt.plan(), y, L.n_out, B, st);
+        launch_gather(L.Wt.plan(), ssc, xT, B, y, L.n_out, B, skip, st);
+    }
+    if (L.B4t.ntiles > 0) launch_gather_b4(L.B4t.plan(), ssc, xT, B, y, L.n_out, B, SKIP_NONE, st);
 }
 
 void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float *dx, float *gw_s,
@@ -564,6 +622,7 @@ int sili_create(int64_t n_inputs, int64_t n_outputs, int64_t max_weights, int de
         Layer &L = h->L;
         L.device = device;
         set_device(L);
+        resolve_scratch(device);
         SILI_HIP(hipStreamCreateWithFlags(&L.stream, hipStreamNonBlocking));
         L.n_in = n_inputs;
         L.n_out = n_outputs;
@@ -769,6 +828,14 @@ int sili_forward_dense(sili_layer *layer, const float *x, int64_t batch, float *
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
         set_device(layer->L);
         forward_dense(layer->L, x, batch, y, pick(layer->L, stream));
+    });
+}
+
+int sili_forward_dense_noalloc(sili_layer *layer, const float *x, int64_t batch, float *y, void *stream) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        forward_dense_noalloc(layer->L, x, batch, y, pick(layer->L, stream));
     });
 }
 
