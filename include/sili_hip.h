@@ -373,6 +373,30 @@ typedef struct {
 int sili_profile_enable(sili_layer *layer, int enable);
 int sili_profile_read(sili_layer *layer, sili_prof_entry *out, int max_entries, int *n_entries);
 
+/* ---- module utilities (device buffers; synchronous on `stream`) -----------
+ * fp4_quantize_array (sili/cpu_backend.cpp:3157-3172): codes[i] =
+ * fp4_encode(x[i]) (fp4quant.hpp:86-126), n elements. */
+int sili_fp4_quantize(const float *x, int64_t n, uint8_t *codes, void *stream);
+/* dense_to_csr (sili/cpu_backend.cpp:3075-3116): x [rows, cols] row-major ->
+ * CSR of the entries with x > threshold or x < -threshold, in row-major
+ * order; ptrs [rows+1].  *nnz receives the entry count; indices/values are
+ * written when it is <= capacity (else SILI_ERR_RANGE, ptrs still written). */
+int sili_dense_to_csr(const float *x, int64_t rows, int64_t cols, float threshold, int32_t *ptrs,
+                      int32_t *indices, float *values, int64_t capacity, int64_t *nnz, void *stream);
+/* dense_to_top_k_csr (sili/cpu_backend.cpp:3118-3150, csr.hpp:405-505): the
+ * min(k, rows*cols) entries of largest |x| over the whole flattened array
+ * (a global budget, as the reference's), as a CSR in row-major order;
+ * indices/values hold min(k, rows*cols) entries, ptrs rows+1.  Equal
+ * magnitudes at the cut keep the lowest flat index (the reference leaves
+ * that order to its per-thread partial sorts); NaN ranks above every
+ * finite value. */
+int sili_dense_to_top_k_csr(const float *x, int64_t rows, int64_t cols, int64_t k, int32_t *ptrs,
+                            int32_t *indices, float *values, int64_t *nnz, void *stream);
+/* Layer-free device buffers for the utilities above (hipMemcpyDefault). */
+int sili_buffer_alloc(int device, size_t bytes, void **out);
+int sili_buffer_free(int device, void *ptr);
+int sili_buffer_copy(int device, void *dst, const void *src, size_t bytes);
+
 /* ---- device memory helpers (for callers without HIP headers) ------------ */
 int sili_device_alloc(sili_layer *layer, size_t bytes, void **out);
 int sili_device_free(sili_layer *layer, void *ptr);

@@ -197,12 +197,60 @@ def reflib():
         R.ref_demote_tile.argtypes = [C.c_void_p, C.c_int, C.c_int]
         R.ref_zero_tile_slot.restype = C.c_int
         R.ref_zero_tile_slot.argtypes = [C.c_void_p, C.c_int, C.c_int]
+        R.ref_top_k_csr.restype = C.c_int64
+        R.ref_top_k_csr.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, _i32p, _i32p, _f32p]
         _ref = R
     return _ref
 
 
 def _c(a, dtype):
     return np.ascontiguousarray(a, dtype=dtype)
+
+
+def _shape2(x):
+    x = np.ascontiguousarray(x, np.float32)
+    return x.reshape(1, -1) if x.ndim == 1 else x
+
+
+def dense_to_csr(x, threshold=1e-4):
+    """Restatement of the module utility dense_to_csr
+    (sili/cpu_backend.cpp:3075-3116): per row, in column order, the entries
+    with v > threshold or v < -threshold."""
+    x = _shape2(x)
+    keep = (x > np.float32(threshold)) | (x < -np.float32(threshold))
+    ptrs = np.concatenate([[0], np.cumsum(keep.sum(1))]).astype(np.int32)
+    rows, cols = np.nonzero(keep)
+    return ptrs, cols.astype(np.int32), x[rows, cols].astype(np.float32)
+
+
+def dense_to_top_k_csr(x, k):
+    """Restatement of dense_to_top_k_csr (csr.hpp:405-505): the min(k, size)
+    entries of largest |x| over the flattened array (a global budget), as a
+    row-major CSR.  Among equal magnitudes at the cut the lowest flat index
+    is kept (the reference leaves that order to its per-thread partial
+    sorts, so only cuts between distinct magnitudes are pinned)."""
+    x = _shape2(x)
+    rows, cols = x.shape
+    flat = x.ravel()
+    kk = min(int(k), flat.size)
+    mag = (flat.view(np.uint32) & np.uint32(0x7FFFFFFF)).astype(np.int64)
+    order = np.argsort(-mag, kind="stable")[:kk]
+    sel = np.sort(order)
+    ptrs = np.searchsorted(sel, np.arange(rows + 1, dtype=np.int64) * cols).astype(np.int32)
+    return ptrs, (sel % cols).astype(np.int32), flat[sel].astype(np.float32)
+
+
+def ref_top_k_csr(x, k, threads=4):
+    """The reference's own top_k_csr (compiled from its header, _ref)."""
+    x = _shape2(x).copy()
+    rows, cols = x.shape
+    kk = min(int(k), x.size)
+    ptrs = np.zeros(rows + 1, np.int32)
+    idx = np.zeros(max(kk, 1), np.int32)
+    vals = np.zeros(max(kk, 1), np.float32)
+    n = reflib().ref_top_k_csr(_p(x, _f32p), rows, cols, int(k), int(threads), _p(ptrs, _i32p), _p(idx, _i32p),
+                               _p(vals, _f32p))
+    return ptrs, idx[:n], vals[:n]
 
 
 def encode_tiles(n_in: int, br: np.ndarray, bc: np.ndarray, tiles: np.ndarray):

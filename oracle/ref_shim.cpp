@@ -381,4 +381,18 @@ int ref_zero_tile_slot(void *h, int row, int col) {
     return int(t.count_live());
 }
 
+// The module's top-k conversion (csr.hpp:467-505, bound as dense_to_top_k_csr
+// at sili/cpu_backend.cpp:3118-3150): returns the entry count; ptrs [rows+1],
+// idx/vals sized for min(k, rows*cols).
+int64_t ref_top_k_csr(float *x, int rows, int cols, int k, int threads, int32_t *ptrs, int32_t *idx, float *vals) {
+    auto csr = top_k_csr<int, float>(x, size_t(rows), size_t(cols), size_t(k), threads);
+    const auto &p = *csr.ptrs[0];
+    const auto &i = *csr.indices[0];
+    const auto &v = *csr.values[0];
+    std::copy(p.begin(), p.end(), ptrs);
+    std::copy(i.begin(), i.end(), idx);
+    std::copy(v.begin(), v.end(), vals);
+    return int64_t(i.size());
+}
+
 }  // extern "C"

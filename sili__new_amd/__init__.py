@@ -28,10 +28,12 @@ SparseLinearLayerResyncDeterministic = _ext.SparseLinearLayerResyncDeterministic
 SparseLinearLayerNoScale = _ext.SparseLinearLayerNoScale
 SparseLinearLayerNoScaleDeterministic = _ext.SparseLinearLayerNoScaleDeterministic
 fp4_quantize_array = _ext.fp4_quantize_array
+dense_to_csr = _ext.dense_to_csr
+dense_to_top_k_csr = _ext.dense_to_top_k_csr
 seed_fp4_stochastic_rng = _ext.seed_fp4_stochastic_rng
 
 LIB_PATH = os.path.join(_HERE, "libsili_hip.so")
 
 __all__ = ["SparseLinearLayer", "SparseLinearLayerDeterministic", "SparseLinearLayerResync",
            "SparseLinearLayerResyncDeterministic", "SparseLinearLayerNoScale", "SparseLinearLayerNoScaleDeterministic",
-           "fp4_quantize_array", "seed_fp4_stochastic_rng", "LIB_PATH"]
+           "fp4_quantize_array", "dense_to_csr", "dense_to_top_k_csr", "seed_fp4_stochastic_rng", "LIB_PATH"]

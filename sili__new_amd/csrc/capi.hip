@@ -102,6 +102,12 @@ __global__ void k_quantize(const float *__restrict__ w, const float *__restrict_
     out[i] = (uint8_t)((wc << 4) | ic);
 }
 
+// fp4_quantize_array: the raw 4-bit code per element (no importance nibble)
+__global__ void k_fp4_codes(const float *__restrict__ x, int64_t n, uint8_t *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n) out[i] = (uint8_t)fp4_encode(x[i]);
+}
+
 __global__ void k_i32_to_u32(const int32_t *__restrict__ s, int64_t n, uint32_t *__restrict__ d) {
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (i < n) d[i] = (uint32_t)s[i];
@@ -1273,6 +1279,55 @@ int sili_profile_read(sili_layer *layer, sili_prof_entry *out, int max_entries, 
         P.recs.clear();
         if (n_entries) *n_entries = (int)agg.size();
         for (int i = 0; out && i < (int)agg.size() && i < max_entries; ++i) out[i] = agg[(size_t)i];
+    });
+}
+
+int sili_fp4_quantize(const float *x, int64_t n, uint8_t *codes, void *stream) {
+    return guarded([&] {
+        if (n < 0) throw_error(SILI_ERR_INVALID, "fp4_quantize: negative length");
+        if (n == 0) return;
+        if (!x || !codes) throw_error(SILI_ERR_INVALID, "fp4_quantize: NULL buffer");
+        hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+        launch(k_fp4_codes, dim3(nblk(n)), dim3(TPB), 0, st, x, n, codes);
+        SILI_HIP(hipGetLastError());
+        SILI_HIP(hipStreamSynchronize(st));
+    });
+}
+
+int sili_dense_to_csr(const float *x, int64_t rows, int64_t cols, float threshold, int32_t *ptrs, int32_t *indices,
+                      float *values, int64_t capacity, int64_t *nnz, void *stream) {
+    return guarded([&] {
+        if (!nnz) throw_error(SILI_ERR_INVALID, "dense_to_csr: nnz is NULL");
+        dense_to_csr_device(x, rows, cols, threshold, ptrs, indices, values, capacity, nnz,
+                            reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+int sili_dense_to_top_k_csr(const float *x, int64_t rows, int64_t cols, int64_t k, int32_t *ptrs, int32_t *indices,
+                            float *values, int64_t *nnz, void *stream) {
+    return guarded([&] {
+        if (!nnz) throw_error(SILI_ERR_INVALID, "dense_to_top_k_csr: nnz is NULL");
+        dense_to_top_k_csr_device(x, rows, cols, k, ptrs, indices, values, nnz, reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+int sili_buffer_alloc(int device, size_t bytes, void **out) {
+    return guarded([&] {
+        if (!out) throw_error(SILI_ERR_INVALID, "NULL argument");
+        SILI_HIP(hipSetDevice(device));
+        SILI_HIP(hipMalloc(out, bytes ? bytes : 1));
+    });
+}
+int sili_buffer_free(int device, void *ptr) {
+    return guarded([&] {
+        SILI_HIP(hipSetDevice(device));
+        if (ptr) SILI_HIP(hipFree(ptr));
+    });
+}
+int sili_buffer_copy(int device, void *dst, const void *src, size_t bytes) {
+    return guarded([&] {
+        SILI_HIP(hipSetDevice(device));
+        if (bytes) SILI_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDefault));
     });
 }
 

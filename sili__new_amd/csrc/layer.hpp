@@ -263,6 +263,12 @@ void decode_scattered(Layer &L, uint32_t *d_rows, uint32_t *d_cols);
 // Recompute has_nonfinite (code 8 anywhere, or a non-finite scale).
 void refresh_nonfinite(Layer &L);
 
+// Module CSR utilities (csr_util.hip): device buffers, synchronous on st.
+void dense_to_csr_device(const float *x, int64_t rows, int64_t cols, float threshold, int32_t *ptrs, int32_t *idx,
+                         float *vals, int64_t cap, int64_t *nnz, hipStream_t st);
+void dense_to_top_k_csr_device(const float *x, int64_t rows, int64_t cols, int64_t k, int32_t *ptrs, int32_t *idx,
+                               float *vals, int64_t *nnz, hipStream_t st);
+
 // rocprim wrappers
 void device_exclusive_scan_u64(Layer &L, const uint64_t *in, uint64_t *out, int64_t n);
 void device_exclusive_scan_u32(Layer &L, const uint32_t *in, uint32_t *out, int64_t n);

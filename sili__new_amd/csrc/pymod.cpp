@@ -9,6 +9,7 @@
 #include <pybind11/pybind11.h>
 #include <pybind11/stl.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
 #include <string>
@@ -314,11 +315,12 @@ class Layer {
         if (x.size() != B * n_in_ || dy.size() != B * n_out_) throw py::value_error("x [B,n_in], dy [B,n_out]");
         sili_info i;
         ck(sili_get_info(L_, &i));
-        float *dx = (float *)last_x_.get((size_t)(B * n_in_) * 4);
+        // x goes to its own buffer: the stored forward input (last_input)
+        // belongs to forward_dense alone, as the reference's _last_input
+        float *dx = (float *)xs_.get((size_t)(B * n_in_) * 4);
         float *dg = (float *)g_.get((size_t)(B * n_out_) * 4);
         ck(sili_memcpy_h2d(L_, dx, x.data(), (size_t)(B * n_in_) * 4));
         ck(sili_memcpy_h2d(L_, dg, dy.data(), (size_t)(B * n_out_) * 4));
-        last_batch_ = B;
         float *gs = (float *)gws_.get((size_t)i.nnz_scattered * 4 + 4);
         float *gb = (float *)gwb_.get((size_t)i.n_tiles * 64 + 4);
         ck(sili_sampled_gradw(L_, dx, dg, B, gs, gb, nullptr));
@@ -346,7 +348,7 @@ class Layer {
         flush();
         if (x.size() != batch * n_in_) throw py::value_error("x must be [batch, n_inputs]");
         check_csr(dptrs, didx, dvals, batch, n_out_);
-        float *dxin = (float *)last_x_.get((size_t)(batch * n_in_) * 4);
+        float *dxin = (float *)xs_.get((size_t)(batch * n_in_) * 4);
         ck(sili_memcpy_h2d(L_, dxin, x.data(), (size_t)(batch * n_in_) * 4));
         int32_t *dp = upload_i32(p_, dptrs);
         int32_t *di = upload_i32(i_, didx);
@@ -523,9 +525,9 @@ class Layer {
     std::vector<float> vs_, os_, is_, ois_;
     bool dirty_vs_ = false, dirty_os_ = false, dirty_is_ = false, dirty_ois_ = false;
     int64_t last_batch_ = 0;
-    DBuf last_x_, y_, g_, dx_, p_, i_, v_, gws_, gwb_;
+    DBuf last_x_, xs_, y_, g_, dx_, p_, i_, v_, gws_, gwb_;
 
-    std::vector<DBuf *> bufs() { return {&last_x_, &y_, &g_, &dx_, &p_, &i_, &v_, &gws_, &gwb_}; }
+    std::vector<DBuf *> bufs() { return {&last_x_, &xs_, &y_, &g_, &dx_, &p_, &i_, &v_, &gws_, &gwb_}; }
 
     void flush() {
         if (dirty_vs_) ck(sili_set_value_scale(L_, vs_.data()));
@@ -575,28 +577,80 @@ class Layer {
     }
 };
 
-// fp4_quantize_array (sili/cpu_backend.cpp:3157): fp32 -> uint8 codes.
-py::array_t<uint8_t> fp4_quantize_array(carr<float> v) {
-    py::array_t<uint8_t> out(v.request().shape);
-    const float *s = v.data();
-    uint8_t *d = out.mutable_data();
-    for (py::ssize_t i = 0; i < v.size(); ++i) {
-        uint32_t bits;
-        std::memcpy(&bits, &s[i], 4);
-        const uint32_t a = bits & 0x7FFFFFFFu;
-        uint32_t mag;
-        if (a > 0x7F800000u) { d[i] = 0; continue; }
-        if (a < 0x3E800000u) mag = 0;
-        else if (a < 0x3F400000u) mag = 1;
-        else if (a < 0x3F800000u) mag = 2;
-        else {
-            uint32_t r = a + (1u << 21);
-            if (r > 0x40C00000u) r = 0x40C00000u;
-            mag = ((((r >> 23) & 0xFFu) - 126u) << 1) | ((r >> 22) & 1u);
-        }
-        d[i] = mag == 0 ? 0 : (uint8_t)(((bits >> 31) << 3) | mag);
+// A device buffer of the module utilities (no layer): freed on scope exit.
+struct UBuf {
+    int dev = 0;
+    void *p = nullptr;
+    UBuf(int device, size_t bytes) : dev(device) { ck(sili_buffer_alloc(device, bytes, &p)); }
+    ~UBuf() {
+        if (p) (void)sili_buffer_free(dev, p);
     }
+    UBuf(const UBuf &) = delete;
+    UBuf &operator=(const UBuf &) = delete;
+    void put(const void *h, size_t bytes) {
+        if (bytes) ck(sili_buffer_copy(dev, p, h, bytes));
+    }
+    void get(void *h, size_t bytes) const {
+        if (bytes) ck(sili_buffer_copy(dev, h, p, bytes));
+    }
+};
+
+// fp4_quantize_array (sili/cpu_backend.cpp:3157): fp32 -> uint8 codes, on the GPU.
+py::array_t<uint8_t> fp4_quantize_array(carr<float> v, int device) {
+    py::array_t<uint8_t> out(v.request().shape);
+    const size_t n = (size_t)v.size();
+    if (n == 0) return out;
+    UBuf dx(device, 4 * n), dc(device, n);
+    dx.put(v.data(), 4 * n);
+    ck(sili_fp4_quantize(static_cast<const float *>(dx.p), (int64_t)n, static_cast<uint8_t *>(dc.p), nullptr));
+    dc.get(out.mutable_data(), n);
     return out;
+}
+
+// [batch, cols] or [cols] -> (rows, cols) as the reference binding reads them
+std::pair<int64_t, int64_t> csr_shape(const carr<float> &x) {
+    const auto b = x.request();
+    if (b.ndim == 2) return {(int64_t)b.shape[0], (int64_t)b.shape[1]};
+    if (b.ndim == 1) return {1, (int64_t)b.shape[0]};
+    throw py::value_error("expected a 1-D or 2-D float32 array");
+}
+
+// dense_to_csr (sili/cpu_backend.cpp:3075-3116): entries with |v| > threshold.
+py::tuple dense_to_csr(carr<float> x, float threshold, int device) {
+    const auto [rows, cols] = csr_shape(x);
+    const size_t n = (size_t)(rows * cols);
+    UBuf dx(device, 4 * n + 4), dp(device, 4 * ((size_t)rows + 1)), di(device, 4 * n + 4), dv(device, 4 * n + 4);
+    dx.put(x.data(), 4 * n);
+    int64_t nnz = 0;
+    ck(sili_dense_to_csr(static_cast<const float *>(dx.p), rows, cols, threshold, static_cast<int32_t *>(dp.p),
+                         static_cast<int32_t *>(di.p), static_cast<float *>(dv.p), (int64_t)n, &nnz, nullptr));
+    py::array_t<int32_t> ptrs((py::ssize_t)(rows + 1)), idx((py::ssize_t)nnz);
+    py::array_t<float> vals((py::ssize_t)nnz);
+    dp.get(ptrs.mutable_data(), 4 * ((size_t)rows + 1));
+    di.get(idx.mutable_data(), 4 * (size_t)nnz);
+    dv.get(vals.mutable_data(), 4 * (size_t)nnz);
+    return py::make_tuple(ptrs, idx, vals);
+}
+
+// dense_to_top_k_csr (sili/cpu_backend.cpp:3118-3150): global top-k by |v|.
+// num_threads is the reference's OpenMP width; the GPU ignores it.
+py::tuple dense_to_top_k_csr(carr<float> x, int64_t k, int num_threads, int device) {
+    (void)num_threads;
+    const auto [rows, cols] = csr_shape(x);
+    if (k < 0) throw py::value_error("k must be >= 0");
+    const size_t n = (size_t)(rows * cols);
+    const size_t kk = std::min<size_t>((size_t)k, n);
+    UBuf dx(device, 4 * n + 4), dp(device, 4 * ((size_t)rows + 1)), di(device, 4 * kk + 4), dv(device, 4 * kk + 4);
+    dx.put(x.data(), 4 * n);
+    int64_t nnz = 0;
+    ck(sili_dense_to_top_k_csr(static_cast<const float *>(dx.p), rows, cols, k, static_cast<int32_t *>(dp.p),
+                               static_cast<int32_t *>(di.p), static_cast<float *>(dv.p), &nnz, nullptr));
+    py::array_t<int32_t> ptrs((py::ssize_t)(rows + 1)), idx((py::ssize_t)nnz);
+    py::array_t<float> vals((py::ssize_t)nnz);
+    dp.get(ptrs.mutable_data(), 4 * ((size_t)rows + 1));
+    di.get(idx.mutable_data(), 4 * (size_t)nnz);
+    dv.get(vals.mutable_data(), 4 * (size_t)nnz);
+    return py::make_tuple(ptrs, idx, vals);
 }
 
 // The reference's other concrete layer classes (sili/cpu_backend.cpp:992-1013):
@@ -715,7 +769,10 @@ PYBIND11_MODULE(_sili_hip, m) {
     bind_variant<LayerResyncDeterministic>(m, "SparseLinearLayerResyncDeterministic");
     bind_variant<LayerNoScale>(m, "SparseLinearLayerNoScale");
     bind_variant<LayerNoScaleDeterministic>(m, "SparseLinearLayerNoScaleDeterministic");
-    m.def("fp4_quantize_array", &fp4_quantize_array);
+    m.def("fp4_quantize_array", &fp4_quantize_array, py::arg("vals"), py::arg("device") = 0);
+    m.def("dense_to_csr", &dense_to_csr, py::arg("x"), py::arg("threshold") = 1e-4f, py::arg("device") = 0);
+    m.def("dense_to_top_k_csr", &dense_to_top_k_csr, py::arg("x"), py::arg("k"), py::arg("num_threads") = 4,
+          py::arg("device") = 0);
     m.def(
         "seed_fp4_stochastic_rng",
         [](uint64_t seed) {
