@@ -52,6 +52,9 @@ def parse():
                    help="config 1: the backward carries the optimizer update at this learning rate "
                         "(stochastic re-quantization, as the reference's SparseLinearLayer)")
     p.add_argument("--verbose", action="store_true")
+    p.add_argument("--index-decode", type=int, default=0, metavar="G",
+                   help="only time decoding every column of the config-4 q layer from the ULEB128 stream and "
+                        "from a FOR index of group size G")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run 3 device-to-device copies of MIB MiB (HBM counter calibration)")
     return p.parse_args()
@@ -604,6 +607,51 @@ def run_config4(a, hip, api, rt):
     print(json.dumps(out), flush=True)
 
 
+def run_index_decode(a, hip, api, rt):
+    """Column decode of the config-4 q layer (5120 x 204800, ~105 M
+    synapses): the ULEB128 stream (wave-parallel varint decode) against the
+    FOR index (every column = group start + offset).  Algorithmic bytes:
+    what each decoder must read plus 4 bytes written per column."""
+    from sili__new_amd.synth import SEED0
+    G = a.index_decode
+    n_in, n_out = 5120, 204800
+    L = hip.SparseLinearLayer(n_in, n_out, 1)
+    nnz = L.load_synthetic(SEED0 + 4, 0.1, 0.02, 0.95)
+    L.build_for_index(G)
+    info = L.info()
+    h = C.c_void_p(L.handle)
+    for_bytes = len(L.export_for_index()["bytes"])
+    cols = api.alloc(h, 4 * nnz)
+    stream = api.L.sili_stream(h)
+    api.L.sili_decode_columns.argtypes = [C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
+    out = {"workload": f"config-4 q layer {n_in}x{n_out}, {nnz} synapses; decode every column",
+           "group_size": G, "nnz": nnz, "index_bytes": info["index_bytes"], "for_bytes": for_bytes}
+    ngroups = None
+    for use_for, name in ((0, "uleb"), (1, "for")):
+        for _ in range(3):
+            api.ck(api.L.sili_decode_columns(h, cols, use_for, stream))
+        rt.sync()
+        api.ck(api.L.sili_profile_enable(h, 1))
+        reps = 20
+        for _ in range(reps):
+            api.ck(api.L.sili_decode_columns(h, cols, use_for, stream))
+        rt.sync()
+        prof = api.profile(h)
+        api.ck(api.L.sili_profile_enable(h, 0))
+        (cnt, tot), = [v for k, v in prof.items() if k.startswith("index:")]
+        ms = tot / cnt
+        if use_for:
+            ngroups = -(-nnz // G)  # at least; rows' short last groups add a few
+            read = for_bytes + 12 * ngroups
+        else:
+            read = info["index_bytes"] + 32 * info["n_segments"]
+        alg = read + 4 * nnz
+        out[name] = {"ms": round(ms, 4), "gcols_s": round(nnz / (ms * 1e-3) / 1e9, 2),
+                     "algorithmic_bytes": alg, "achieved_gbs": round(alg / (ms * 1e-3) / 1e9, 1)}
+    api.ck(api.L.sili_device_free(h, cols))
+    print(json.dumps(out), flush=True)
+
+
 def cpu_baseline_c4(d, seconds):
     """The CPU port's forward over the q layer (exported from the device) at
     batch 1, on this host's cores: a bounded sample of the config-4 step."""
@@ -643,6 +691,9 @@ def main():
     import sili__new_amd as hip
     from sili__new_amd.synth import make_config
 
+    if a.index_decode:
+        run_index_decode(a, hip, CAbi(hip.LIB_PATH), Hip())
+        return
     cfg = a.config
     if cfg == 4:
         run_config4(a, hip, CAbi(hip.LIB_PATH), Hip())

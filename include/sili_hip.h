@@ -373,6 +373,26 @@ typedef struct {
 int sili_profile_enable(sili_layer *layer, int enable);
 int sili_profile_read(sili_layer *layer, sili_prof_entry *out, int max_entries, int *n_entries);
 
+/* ---- group frame-of-reference index (prototypes/for_delta_encoding/
+ * README.md:18-40, for_encoding_bench.cpp:31-96) ----------------------------
+ * A derived copy of the canonical store's column indices in the reference
+ * prototype's FOR format: per row, groups of group_size (8, 16, 32 or 64)
+ * columns, each a tier byte (0/1/2 = 1/2/4 bytes per offset) and group_size
+ * little-endian offsets from the group start (the previous group's last
+ * column, 0 for a row's first group); a short last group repeats its last
+ * offset.  Built on request, dropped when the store is rebuilt (the ULEB128
+ * stream stays the source of truth). */
+int sili_build_for_index(sili_layer *layer, int group_size);
+/* Host copies: row_byte_start [n_inputs+1] (may be NULL), bytes [*nbytes]
+ * (may be NULL to query the size). */
+int sili_export_for_index(sili_layer *layer, uint64_t *row_byte_start, uint8_t *bytes,
+                          int64_t *nbytes);
+/* Every canonical column (int32, storage order) into device cols, decoded
+ * from the FOR index (use_for_index != 0) or from the ULEB128 stream
+ * (DeltaCSRRowCursor, delta_csr_types.hpp:801-832); profiled as
+ * "index:for" / "index:decode". */
+int sili_decode_columns(sili_layer *layer, int32_t *cols, int use_for_index, void *stream);
+
 /* ---- module utilities (device buffers; synchronous on `stream`) -----------
  * fp4_quantize_array (sili/cpu_backend.cpp:3157-3172): codes[i] =
  * fp4_encode(x[i]) (fp4quant.hpp:86-126), n elements. */

@@ -9,5 +9,6 @@ product (sili__new_amd) never imports, links or runs anything here.
                               (only where /root/reference exists at build time)
 """
 from .oracle import (  # noqa: F401
-    HostLayer, RefLayer, build, dense_to_csr, dense_to_top_k_csr, have_ref, lib, ref_top_k_csr, reflib,
+    HostLayer, RefLayer, build, dense_to_csr, dense_to_top_k_csr, for_encode_row, for_encode_rows, have_ref, lib,
+    ref_for_encode, ref_top_k_csr, reflib,
 )

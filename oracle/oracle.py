@@ -240,6 +240,64 @@ def dense_to_top_k_csr(x, k):
     return ptrs, (sel % cols).astype(np.int32), flat[sel].astype(np.float32)
 
 
+FOR_REF_PATH = HERE / "_ref" / "libfor_ref.so"
+_for_ref = None
+
+
+def for_encode_row(cols, G=16):
+    """Restatement of the reference prototype's group frame-of-reference
+    encoder (prototypes/for_delta_encoding/for_encoding_bench.cpp:31-54,
+    README.md:18-40) for one row's sorted columns: groups of G values, each
+    a tier byte (0/1/2: 1/2/4 bytes per offset, by the group's largest
+    offset) then G little-endian offsets from the group start (the previous
+    group's last column, 0 for the first); a short last group repeats its
+    last offset."""
+    cols = np.asarray(cols, np.int64)
+    out = bytearray()
+    start = 0
+    for g0 in range(0, len(cols), G):
+        grp = cols[g0:g0 + G]
+        off = np.full(G, grp[-1] - start, np.int64)
+        off[:len(grp)] = grp - start
+        m = int(off[-1])
+        tier = 0 if m < 256 else (1 if m < 65536 else 2)
+        w = (1, 2, 4)[tier]
+        out.append(tier)
+        out += off.astype({1: "<u1", 2: "<u2", 4: "<u4"}[w]).tobytes()
+        start = int(grp[-1])
+    return bytes(out)
+
+
+def for_encode_rows(ptrs, cols, G=16):
+    """FOR bytes of every row, concatenated; returns (row_byte_start, bytes)."""
+    ptrs = np.asarray(ptrs, np.int64)
+    parts, starts, n = [], [0], 0
+    for r in range(len(ptrs) - 1):
+        b = for_encode_row(cols[ptrs[r]:ptrs[r + 1]], G)
+        parts.append(b)
+        n += len(b)
+        starts.append(n)
+    return np.array(starts, np.uint64), np.frombuffer(b"".join(parts), np.uint8).copy()
+
+
+def ref_for_encode(cols, G=16):
+    """The reference prototype's own encoder (compiled from its source, _ref)
+    on one row's columns."""
+    global _for_ref
+    if _for_ref is None:
+        R = C.CDLL(str(FOR_REF_PATH))
+        R.ref_for_encode.restype = C.c_int64
+        R.ref_for_encode.argtypes = [C.POINTER(C.c_uint32), C.c_int64, C.c_int, _u8p, C.c_int64]
+        _for_ref = R
+    cols = np.asarray(cols, np.int64)
+    d = np.diff(np.concatenate([[0], cols])).astype(np.uint32)
+    cap = 1 + (len(d) // G + 1) * (1 + 4 * G)
+    out = np.zeros(cap, np.uint8)
+    n = _for_ref.ref_for_encode(d.ctypes.data_as(C.POINTER(C.c_uint32)), len(d), int(G), _p(out, _u8p), cap)
+    assert n >= 0
+    return out[:n].tobytes()
+
+
 def ref_top_k_csr(x, k, threads=4):
     """The reference's own top_k_csr (compiled from its header, _ref)."""
     x = _shape2(x).copy()

@@ -384,6 +384,7 @@ void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64
                                   dst.elem_start, dst.idx, dst.seg, "load_weights", &dst.split_rows);
     dst.n_split = e.n_split;
     dst.stream1.valid = dst.streamK.valid = false;
+    dst.fidx.valid = false;
     dst.stream1.failed = dst.streamK.failed = false;
     dst.cblk.clear();
     dst.cblk_cb = 0;
@@ -433,6 +434,7 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
     dst.n_split = e.n_split;
     dst.stream1.valid = dst.streamK.valid = false;
     dst.stream1.failed = dst.streamK.failed = false;
+    dst.fidx.valid = false;
     dst.cblk.clear();
     dst.cblk_cb = 0;
     dst.rows = src.cols;

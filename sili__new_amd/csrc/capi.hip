@@ -1282,6 +1282,47 @@ int sili_profile_read(sili_layer *layer, sili_prof_entry *out, int max_entries, 
     });
 }
 
+int sili_build_for_index(sili_layer *layer, int group_size) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        ProfCtx pc(layer->L, "index");
+        build_for_index(layer->L, group_size);
+    });
+}
+
+int sili_export_for_index(sili_layer *layer, uint64_t *row_byte_start, uint8_t *bytes, int64_t *nbytes) {
+    return guarded([&] {
+        if (!layer || !nbytes) throw_error(SILI_ERR_INVALID, "NULL argument");
+        Layer &L = layer->L;
+        set_device(L);
+        const DFor &F = L.W.fidx;
+        if (!F.valid) throw_error(SILI_ERR_INVALID, "export_for_index: build the FOR index first");
+        *nbytes = F.nbytes;
+        if (row_byte_start) {
+            std::vector<uint32_t> rg((size_t)L.n_in + 1), gp((size_t)F.ngroups + 1);
+            SILI_HIP(hipMemcpyAsync(rg.data(), F.row_group.p, rg.size() * 4, hipMemcpyDeviceToHost, L.stream));
+            SILI_HIP(hipMemcpyAsync(gp.data(), F.group_pos.p, gp.size() * 4, hipMemcpyDeviceToHost, L.stream));
+            SILI_HIP(hipStreamSynchronize(L.stream));
+            for (size_t r = 0; r < rg.size(); ++r) row_byte_start[r] = gp[rg[r]];
+        }
+        if (bytes && F.nbytes) {
+            SILI_HIP(hipMemcpyAsync(bytes, F.bytes.p, (size_t)F.nbytes, hipMemcpyDeviceToHost, L.stream));
+            SILI_HIP(hipStreamSynchronize(L.stream));
+        }
+    });
+}
+
+int sili_decode_columns(sili_layer *layer, int32_t *cols, int use_for_index, void *stream) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        if (!cols && layer->L.W.nnz > 0) throw_error(SILI_ERR_INVALID, "cols is NULL");
+        ProfCtx pc(layer->L, "index");
+        decode_columns(layer->L, cols, use_for_index != 0, pick(layer->L, stream));
+    });
+}
+
 int sili_fp4_quantize(const float *x, int64_t n, uint8_t *codes, void *stream) {
     return guarded([&] {
         if (n < 0) throw_error(SILI_ERR_INVALID, "fp4_quantize: negative length");

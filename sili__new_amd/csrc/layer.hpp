@@ -71,6 +71,24 @@ struct DStream {
     DevBuf<WinDesc> win;          // per block: nwin + 1 (rs_lo indexes the block's ne lists)
 };
 
+// Derived group frame-of-reference (FOR) copy of a store's column indices
+// (built on request, dropped when the store is rebuilt).  Per row, groups of
+// G columns: a tier byte (0/1/2 = 1/2/4 bytes per offset) and G little-endian
+// offsets from the group start (the previous group's last column, 0 for a
+// row's first group); a short last group repeats its last offset.  The byte
+// stream is the reference prototype's format; the per-group arrays are this
+// device's index into it, so every column decodes independently.
+struct DFor {
+    bool valid = false;
+    int G = 16;
+    int64_t ngroups = 0, nbytes = 0;
+    DevBuf<uint32_t> row_group;   // rows+1: first group of each row
+    DevBuf<uint32_t> group_pos;   // ngroups+1: byte offset of each group's tier byte
+    DevBuf<uint32_t> group_base;  // ngroups: the group start column
+    DevBuf<uint32_t> group_elem;  // ngroups+1: entry index of each group's first column
+    DevBuf<uint8_t> bytes;
+};
+
 // One orientation of the scattered store.
 struct DScatter {
     int64_t rows = 0, cols = 0, nnz = 0, nbytes = 0, nseg = 0;
@@ -82,6 +100,7 @@ struct DScatter {
     DevBuf<uint32_t> split_rows;  // rows with more than one work item
     int64_t n_split = 0;
     DStream stream1, streamK;     // stream copies: whole rows / the last column blocking used
+    DFor fidx;                    // FOR copy of the column indices
     // column-block copies for gathers whose operand exceeds one XCD's L2:
     // cblk[k] holds every row's entries with columns in [k*cblk_cb, ...),
     // columns relative to the block (built on first use)
@@ -262,6 +281,12 @@ void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_
 void decode_scattered(Layer &L, uint32_t *d_rows, uint32_t *d_cols);
 // Recompute has_nonfinite (code 8 anywhere, or a non-finite scale).
 void refresh_nonfinite(Layer &L);
+
+// FOR index of the canonical scattered store (for_index.hip): build (group
+// size 8, 16, 32 or 64), and decode of every column into cols (int32, storage
+// order) from the FOR copy or, for comparison, from the ULEB128 stream.
+void build_for_index(Layer &L, int G);
+void decode_columns(Layer &L, int32_t *cols, bool use_for, hipStream_t st);
 
 // Module CSR utilities (csr_util.hip): device buffers, synchronous on st.
 void dense_to_csr_device(const float *x, int64_t rows, int64_t cols, float threshold, int32_t *ptrs, int32_t *idx,

@@ -500,6 +500,29 @@ class Layer {
         d["bidx"] = bix;
         return d;
     }
+    // the FOR index of the canonical store (derived copy, built on request)
+    void build_for_index(int group_size) { ck(sili_build_for_index(L_, group_size)); }
+    py::dict export_for_index() {
+        int64_t nb = 0;
+        ck(sili_export_for_index(L_, nullptr, nullptr, &nb));
+        py::array_t<uint64_t> rs((py::ssize_t)(n_in_ + 1));
+        py::array_t<uint8_t> b((py::ssize_t)nb);
+        ck(sili_export_for_index(L_, rs.mutable_data(), b.mutable_data(), &nb));
+        py::dict d;
+        d["row_byte_start"] = rs;
+        d["bytes"] = b;
+        return d;
+    }
+    py::array_t<int32_t> decode_columns(bool use_for_index) {
+        sili_info i;
+        ck(sili_get_info(L_, &i));
+        py::array_t<int32_t> c((py::ssize_t)i.nnz_scattered);
+        if (i.nnz_scattered == 0) return c;
+        int32_t *d = (int32_t *)dx_.get((size_t)i.nnz_scattered * 4);
+        ck(sili_decode_columns(L_, d, use_for_index ? 1 : 0, nullptr));
+        ck(sili_memcpy_d2h(L_, c.mutable_data(), d, (size_t)i.nnz_scattered * 4));
+        return c;
+    }
     py::tuple decode_scattered() {
         sili_info i;
         ck(sili_get_info(L_, &i));
@@ -744,6 +767,9 @@ PYBIND11_MODULE(_sili_hip, m) {
         .def("export_scattered", &Layer::export_scattered)
         .def("export_block4", &Layer::export_block4)
         .def("decode_scattered", &Layer::decode_scattered)
+        .def("build_for_index", &Layer::build_for_index, py::arg("group_size") = 16)
+        .def("export_for_index", &Layer::export_for_index)
+        .def("decode_columns", &Layer::decode_columns, py::arg("use_for_index") = true)
         .def("synchronize", &Layer::synchronize)
         .def_property_readonly("handle", &Layer::handle)
         .def_property_readonly("n_inputs", &Layer::n_inputs)
