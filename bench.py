@@ -799,12 +799,13 @@ def main():
         # FP32-compute bound: 2 flops per slot per batch column
         dom_flops = 2 * 16 * n_tiles * B
         achieved = dom_flops / (dom_avg_ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "kernel": dom_name, "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
+        roof = {"bound": "fp32-valu", "kernel": dom_name, "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 5),
                 "traffic": measured_traffic(dom_name, cfg), "avg_op_ms": round(dom_avg_ms, 5),
                 "launches_per_op": launches,
                 "algorithmic_flops": dom_flops, "algorithmic_bytes": alg.get(dom_name),
-                "note": "fp32 vector FMA work (no MFMA); peak is MI355X dense fp32"}
+                "note": ("fp32 vector FMA work: the MFMA variants lose on every op "
+                         "(profiles/c3_block4_mfma_vs_valu.md); peak is MI355X dense fp32")}
         step_bytes = alg["fwd:gather_b4"] + alg["bwd:gather_b4"] + alg["bwd:sddmm_b4"]
         flops = 3 * 2 * units * B
     else:
