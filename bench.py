@@ -14,7 +14,8 @@ Prints ONE JSON line (rank 0).  `value` is GNNZ/s = stored synapses per step
 / step time.  `roofline` is computed live from per-kernel HIP events
 (sili_profile_*) recorded on the stream the kernels run on; `cpu_baseline`
 times the CPU port (oracle/, OpenMP, the reference's algorithm) on the
-host cores of this box.
+host cores of this box, in child processes that never touch the GPU, at the
+host share's thread count and at one thread.
 """
 from __future__ import annotations
 
@@ -295,6 +296,17 @@ def build_copy(cfg, wl, hip, api):
     return d
 
 
+def release_pool(api, pool):
+    """Free every copy's device buffers, then its layer (sili_destroy through
+    the binding object's destructor), in that order."""
+    for d in pool:
+        for k in ("x", "y", "g", "dx", "gws", "gwb", "xp", "xi", "xv"):
+            if k in d:
+                api.ck(api.L.sili_device_free(d["h"], d[k]))
+        d.clear()
+    pool.clear()
+
+
 def make_step(cfg, api, B, stream, train_lr=0.0):
     L = api.L
 
@@ -320,116 +332,132 @@ def make_step(cfg, api, B, stream, train_lr=0.0):
     return step
 
 
-def cpu_baseline_train(wl, seconds, lr, cfg=1):
-    """Configs 1 and 3 with the optimizer update: the reference's own compiled
-    disldo_forward + disldo_backward(lr) (oracle/_ref, OpenMP) on this host;
-    without _ref, the oracle's single-thread restatement of the update."""
-    from oracle import HostLayer, RefLayer, have_ref
-    x, g = wl.x.astype(np.float32), wl.g.astype(np.float32)
-    tiles = cfg == 3 and wl.tile_br is not None and len(wl.tile_br) > 0
-    # a block4-only workload has no scattered store: an empty CSR
-    ptrs = wl.ptrs if wl.ptrs is not None else np.zeros(wl.n_in + 1, np.int32)
-    cols = wl.cols if wl.cols is not None else np.zeros(0, np.int32)
-    q = wl.q if wl.q is not None else np.zeros(0, np.float32)
-    if have_ref():
-        threads = os.cpu_count() or 1
-        R = RefLayer(wl.n_in, wl.n_out, ptrs, cols, q)
-        if wl.value_scale is not None:
-            R.set_scales(wl.value_scale)
-        R.compact()
-        if tiles:
-            tb = np.asarray(wl.tile_bytes, np.uint8).reshape(-1, 16)
-            for t in range(len(wl.tile_br)):
-                R.put_tile(int(wl.tile_br[t]), int(wl.tile_bc[t]), tb[t])
-            R.block4_headroom(0.2, 16 * 64)
+def _time_reps(step, seconds, max_reps, min_reps=2):
+    """Wall time of `step` repeated for about `seconds` (at least min_reps,
+    at most max_reps): (best, median) in seconds, reps."""
+    times = []
+    t_end = time.perf_counter() + seconds
+    while True:
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= max_reps or (len(times) >= min_reps and time.perf_counter() > t_end):
+            break
+    return float(np.min(times)), float(np.median(times)), len(times)
 
-        def step():
-            R.forward_dense(x, threads=threads)
-            R.backward_train(x, g, lr, threads=threads)
-        kind, what = "reference", "the reference's disldo_forward + disldo_backward(lr) from oracle/_ref"
+
+def cpu_child_run(spec):
+    """Child-process side of the CPU baseline: builds the workload on the host
+    (no GPU is touched in this process) and times the CPU port (oracle/: the
+    reference's algorithm -- static row split, per-thread private outputs,
+    serial reduce) at spec["threads"] OpenMP threads."""
+    from oracle import HostLayer
+    from sili__new_amd.synth import make_config
+    cfg, threads, seconds = spec["cfg"], spec["threads"], spec["seconds"]
+    lr = spec.get("lr", 0.0)
+    if cfg == 4:
+        z = np.load(spec["layer_file"])
+        H = HostLayer(int(z["n_in"]), int(z["n_out"]))
+        H.load_encoded(z["row_byte_start"], z["row_elem_start"], z["idx"], z["val"])
+        H.set_scales(z["value_scale"])
+        x = z["x"]
+        best, med, reps = _time_reps(lambda: H.forward_dense(x, threads=threads), seconds, 50)
+        units = int(z["nnz"])
+        sample = f"forward of the q layer ({units} synapses, 5120x204800) at batch 1"
     else:
-        threads = 1
+        wl = make_config(cfg, scale=spec.get("scale", 1.0))
+        ptrs = wl.ptrs if wl.ptrs is not None else np.zeros(wl.n_in + 1, np.int32)
+        cols = wl.cols if wl.cols is not None else np.zeros(0, np.int32)
+        q = wl.q if wl.q is not None else np.zeros(0, np.float32)
         H = HostLayer(wl.n_in, wl.n_out).load_csr(ptrs, cols, w=q)
-        if wl.value_scale is not None:
-            H.set_scales(wl.value_scale)
-        if tiles:
+        if wl.tile_br is not None:
             H.load_tiles(wl.tile_br, wl.tile_bc, wl.tile_bytes)
+        H.set_scales(wl.value_scale)
+        x, B = wl.x.astype(np.float32), wl.batch
+        g = None if wl.g is None else wl.g.astype(np.float32)
+        if lr:
+            # the update's restatement runs on one thread (its batch steps
+            # form a dependent chain per synapse, as in the reference)
+            threads = 1
 
-        def step():
-            H.forward_dense(x, threads=1)
-            H.backward_train(x, g, lr)
-        kind, what = "port", "the oracle's forward + backward_train (one thread)"
-    times = []
-    t_end = time.perf_counter() + seconds
-    while True:
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() > t_end or len(times) >= 30:
-            break
-    med = float(np.median(times))
-    units = len(cols) + (16 * len(wl.tile_br) if tiles else 0)  # stored synapses, as the GPU line counts them
-    return {"value": round(units / med / 1e9, 5), "unit": "GNNZ/s", "cores": threads, "kind": kind,
-            "sample": f"full config-{cfg} training step ({what}, lr {lr}), {len(times)} reps, "
-                      f"median {med * 1e3:.1f} ms/step"}
-
-
-def cpu_baseline(cfg, wl, seconds):
-    """The CPU port (oracle/: the reference's algorithm, OpenMP, per-thread
-    private outputs + serial reduce) on this host, same workload and step."""
-    from oracle import HostLayer, have_ref
-    threads = os.cpu_count() or 1
-    H = HostLayer(wl.n_in, wl.n_out)
-    if wl.cols is not None:
-        H.load_csr(wl.ptrs, wl.cols, w=wl.q)
-    if wl.tile_br is not None:
-        H.load_tiles(wl.tile_br, wl.tile_bc, wl.tile_bytes)
-    H.set_scales(wl.value_scale)
-    x, g, B = wl.x.astype(np.float32), None if wl.g is None else wl.g.astype(np.float32), wl.batch
-
-    def step():
-        if cfg == 0:
-            H.forward_dense(x, threads=threads)
-        elif cfg == 2:
-            H.forward_sparse(wl.x_ptrs, wl.x_idx, wl.x_vals, B, threads=threads)
-            H.backward_dense(x, g, threads=threads)
+            def step():
+                H.forward_dense(x, threads=1)
+                H.backward_train(x, g, lr)
+            sample = f"full config-{cfg} training step (forward + backward with the update, lr {lr})"
         else:
-            H.forward_dense(x, threads=threads)
-            H.backward_dense(x, g, threads=threads)
-            H.sampled_gradw(x, g, threads=threads)
-    times = []
-    t_end = time.perf_counter() + seconds
-    while True:
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() > t_end or len(times) >= 50:
-            break
-    med = float(np.median(times))
-    units = wl.nnz + (0 if wl.tile_br is None else 16 * len(wl.tile_br))
-    out = {"value": round(units / med / 1e9, 5), "unit": "GNNZ/s", "cores": threads, "kind": "port",
-           "sample": f"full config-{cfg} step ({STEP_DOC[cfg][7:]}), {len(times)} reps, "
-                     f"median {med * 1e3:.1f} ms/step"}
-    if cfg == 3 and wl.cand_r is not None:
+            def step():
+                if cfg == 0:
+                    H.forward_dense(x, threads=threads)
+                elif cfg == 2:
+                    H.forward_sparse(wl.x_ptrs, wl.x_idx, wl.x_vals, B, threads=threads)
+                    H.backward_dense(x, g, threads=threads)
+                else:
+                    H.forward_dense(x, threads=threads)
+                    H.backward_dense(x, g, threads=threads)
+                    H.sampled_gradw(x, g, threads=threads)
+            sample = f"full config-{cfg} step ({STEP_DOC[cfg][7:]})"
+        best, med, reps = _time_reps(step, seconds, 50, min_reps=spec.get("min_reps", 2))
+        units = len(cols) + (0 if wl.tile_br is None else 16 * len(wl.tile_br))
+        if spec.get("scale", 1.0) != 1.0:
+            sample += f" at scale {spec['scale']} ({wl.n_in}x{wl.n_out}, {units} synapses)"
+    out = {"value": round(units / med / 1e9, 6), "best_value": round(units / best / 1e9, 6), "unit": "GNNZ/s",
+           "cores": threads, "kind": "port", "median_ms": round(med * 1e3, 3), "best_ms": round(best * 1e3, 3),
+           "sample": f"{sample}, {reps} reps"}
+    if cfg == 3 and not lr and spec.get("synapto") and wl.cand_r is not None:
         t0 = time.perf_counter()
         H.synapto_step(0.01, wl.cand_r, wl.cand_c, wl.cand_v)
         out["synapto_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
-    if cfg == 1 and have_ref():
-        from oracle import RefLayer
-        R = RefLayer(wl.n_in, wl.n_out, wl.ptrs, wl.cols, wl.q).set_scales(wl.value_scale)
-        R.compact()
-        rt = []
-        t_end = time.perf_counter() + seconds / 2
-        while True:
-            t0 = time.perf_counter()
-            R.forward_dense(x, threads=threads)
-            R.backward_dense(x, g, threads=threads)
-            rt.append(time.perf_counter() - t0)
-            if time.perf_counter() > t_end or len(rt) >= 30:
-                break
-        out["reference_fwd_bwd_ms"] = round(float(np.median(rt)) * 1e3, 2)
-        out["reference_note"] = ("the reference's own disldo_forward + disldo_backward(lr=0) built from "
-                                 "its headers (oracle/_ref); it has no standalone grad-W")
+    return out
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(cfg, seconds, lr=0.0, layer_file=None):
+    """The CPU baseline, timed in child processes (nothing of the GPU process's
+    state, and no GPU, in them) with OMP_NUM_THREADS pinned: at the host
+    share's thread count (OMP_NUM_THREADS, else the core count) and at one
+    thread.  `value` is the multi-thread median; best-of-reps beside it."""
+    import subprocess
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or (os.cpu_count() or 1)
+
+    def child(t, **extra):
+        spec = {"cfg": cfg, "threads": t, "seconds": seconds, "lr": lr, "layer_file": layer_file, **extra}
+        print(f"cpu baseline: config {cfg}, {t} thread(s) {extra or ''}", file=sys.stderr, flush=True)
+        env = dict(os.environ, OMP_NUM_THREADS=str(t))
+        r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-child", json.dumps(spec)], env=env,
+                           capture_output=True, text=True, timeout=170)
+        if r.returncode != 0:
+            raise RuntimeError(f"CPU baseline child exited {r.returncode}: {r.stderr[-400:]}")
+        return json.loads([l for l in r.stdout.splitlines() if l.startswith("{")][-1])
+
+    runs = {}
+    try:
+        runs[threads] = child(threads, synapto=True)
+        if threads > 1:
+            # one thread: the full workload when about 16x the multi-thread
+            # step fits the budget, else a smaller instance of the same config
+            # (work ~ scale^2 for configs 1-3)
+            est = runs[threads]["median_ms"] * 1e-3 * threads
+            scale = 1.0
+            while cfg in (1, 2, 3) and est * scale * scale > 2.5 * seconds and scale > 1.0 / 16:
+                scale /= 2
+            runs[1] = child(1, min_reps=1, scale=scale) if scale != 1.0 else child(1, min_reps=1)
+    except (RuntimeError, subprocess.TimeoutExpired) as e:
+        if not runs:
+            return {"error": str(e)[-400:]}
+    out = dict(runs[max(runs)])
+    out["cpu_model"] = cpu_model()
+    out["isolated"] = "child process per thread count, OMP_NUM_THREADS pinned"
+    if 1 in runs and max(runs) > 1:
+        out["one_thread"] = {k: runs[1][k] for k in ("value", "best_value", "median_ms", "best_ms", "sample")}
     return out
 
 
@@ -600,10 +628,11 @@ def run_config4(a, hip, api, rt):
         "batches": {str(B): r for B, r in results.items()},
         "build_s": round(t_build, 2),
     }
-    if not a.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline_c4(layers[0], a.cpu_seconds)
-    else:
-        out["cpu_baseline"] = None
+    cpu = None if a.no_cpu_baseline else cpu_baseline_c4(layers[0], a.cpu_seconds)
+    for d in layers:  # released while the HIP runtime is fully alive
+        d.clear()
+    layers.clear()
+    out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)
 
 
@@ -653,32 +682,30 @@ def run_index_decode(a, hip, api, rt):
 
 
 def cpu_baseline_c4(d, seconds):
-    """The CPU port's forward over the q layer (exported from the device) at
-    batch 1, on this host's cores: a bounded sample of the config-4 step."""
-    from oracle import HostLayer
+    """The CPU port's forward over the q layer at batch 1 (exported from the
+    device to a temporary file the child process loads): a bounded sample of
+    the config-4 step."""
+    import tempfile
     from sili__new_amd.synth import SEED0, Stream
     L = d["L"]
-    threads = os.cpu_count() or 1
-    H = HostLayer(d["n_in"], d["n_out"])
     ex = L.export_scattered()
-    H.load_encoded(ex["row_byte_start"], ex["row_elem_start"], ex["idx"], ex["val"])
-    H.set_scales(np.asarray(L.get_value_scales(), np.float32))
     x = Stream(SEED0 + 4, 7).normal(d["n_in"]).astype(np.float32)[None, :]
-    times = []
-    t_end = time.perf_counter() + seconds
-    while True:
-        t0 = time.perf_counter()
-        H.forward_dense(x, threads=threads)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() > t_end or len(times) >= 50:
-            break
-    med = float(np.median(times))
-    return {"value": round(d["nnz"] / med / 1e9, 4), "unit": "GNNZ/s", "cores": threads, "kind": "port",
-            "sample": f"forward of the q layer ({d['nnz']} synapses, 5120x204800) at batch 1, "
-                      f"{len(times)} reps, median {med * 1e3:.1f} ms"}
+    fd, path = tempfile.mkstemp(suffix=".npz", prefix="sili_c4q_")
+    os.close(fd)
+    try:
+        np.savez(path, n_in=d["n_in"], n_out=d["n_out"], nnz=d["nnz"], row_byte_start=ex["row_byte_start"],
+                 row_elem_start=ex["row_elem_start"], idx=ex["idx"], val=ex["val"],
+                 value_scale=np.asarray(L.get_value_scales(), np.float32), x=x)
+        del ex
+        return cpu_baseline(4, seconds, layer_file=path)
+    finally:
+        os.unlink(path)
 
 
 def main():
+    if len(sys.argv) == 3 and sys.argv[1] == "--cpu-child":
+        print(json.dumps(cpu_child_run(json.loads(sys.argv[2]))), flush=True)
+        return
     a = parse()
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: the layer is sharded by input "
@@ -873,18 +900,18 @@ def main():
         "kernels_ms_per_step": {k: round(v[1] / a.steps, 5) for k, v in kern.items()},
         "profiled_ms_per_step": round(prof_ms_step, 5),
     }
+    # the layers and their device buffers are released here, while the HIP
+    # runtime is fully alive (not at interpreter teardown)
+    release_pool(api, pool)
+    rt.sync()
     if cfg == 3 and a.synapto_reps > 0:
-        pool.clear()
         out["synapto_gpu"] = time_synapto(hip, wl, a.synapto_reps)
     if cfg == 1 and a.synap_cycles > 0:
-        pool.clear()
         out["synap_policy"] = time_synap_policy(hip, wl, a.synap_cycles, a.cpu_seconds)
     if a.no_cpu_baseline:
         out["cpu_baseline"] = None
-    elif train_lr:
-        out["cpu_baseline"] = cpu_baseline_train(wl, a.cpu_seconds, train_lr, cfg)
     else:
-        out["cpu_baseline"] = cpu_baseline(cfg, wl, a.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(cfg, a.cpu_seconds, lr=train_lr)
     if a.verbose:
         print(f"build {t_build:.1f}s copies {copies}", file=sys.stderr)
     print(json.dumps(out), flush=True)
