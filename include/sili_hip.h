@@ -373,6 +373,33 @@ typedef struct {
 int sili_profile_enable(sili_layer *layer, int enable);
 int sili_profile_read(sili_layer *layer, sili_prof_entry *out, int max_entries, int *n_entries);
 
+/* ---- block4 tile encoding (block4.hpp:332-388, 1016-1031) ---------------
+ * The reference stores a tile with <= switch_point (default 10) live slots
+ * sparse-packed: [count][ceil(count/2) bytes of 4-bit slot positions, even
+ * index in the high nibble][count slot bytes].  The device computes on dense
+ * 16-byte tiles and keeps per tile the encoding the reference's store would
+ * hold it in (tile_is_sparse): re-encoded by its live count when loaded,
+ * promoted, given an insert, or rewritten by an optimizer update; a removal
+ * leaves a dense tile dense.  Export, canonical tile order, rows without
+ * headroom: tile_is_sparse [n_tiles], tile_data [*nbytes],
+ * tile_byte_start [ceil(n_inputs/4)+1]; any output may be NULL. */
+int sili_export_block4_packed(sili_layer *layer, uint8_t *tile_is_sparse, uint8_t *tile_data,
+                              uint64_t *tile_byte_start, int64_t *nbytes);
+/* Block4View (sili/cpu_backend.cpp:43-98): the store's counters.  The device
+ * store keeps no per-row tile headroom and never drops an update, so
+ * alloc_bytes == used_bytes and the event counters are 0. */
+typedef struct {
+    int64_t tiles, synapses;
+    uint32_t switch_point;
+    int64_t used_bytes, alloc_bytes;
+    int64_t dropped_growth_events, row_merge_overflow_events, row_merge_overflow_bytes_dropped;
+} sili_block4_stats;
+int sili_block4_view(sili_layer *layer, sili_block4_stats *out);
+/* Block4View.switch_point setter: affects later encodings only, as the
+ * reference's; values above 10 are refused (the reference's pack buffer is
+ * 16 bytes, block4.hpp:332-340). */
+int sili_set_switch_point(sili_layer *layer, uint32_t switch_point);
+
 /* ---- group frame-of-reference index (prototypes/for_delta_encoding/
  * README.md:18-40, for_encoding_bench.cpp:31-96) ----------------------------
  * A derived copy of the canonical store's column indices in the reference

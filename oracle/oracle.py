@@ -197,6 +197,14 @@ def reflib():
         R.ref_demote_tile.argtypes = [C.c_void_p, C.c_int, C.c_int]
         R.ref_zero_tile_slot.restype = C.c_int
         R.ref_zero_tile_slot.argtypes = [C.c_void_p, C.c_int, C.c_int]
+        R.ref_layer_export_tiles_packed.restype = C.c_int64
+        R.ref_layer_export_tiles_packed.argtypes = [C.c_void_p, _u8p, _u8p, _u64p]
+        R.ref_block4_switch_point.restype = C.c_uint32
+        R.ref_block4_switch_point.argtypes = [C.c_void_p, C.c_int]
+        R.ref_block4_used_bytes.restype = C.c_uint64
+        R.ref_block4_used_bytes.argtypes = [C.c_void_p]
+        R.ref_block4_live.restype = C.c_uint64
+        R.ref_block4_live.argtypes = [C.c_void_p]
         R.ref_top_k_csr.restype = C.c_int64
         R.ref_top_k_csr.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, _i32p, _i32p, _f32p]
         _ref = R
@@ -238,6 +246,93 @@ def dense_to_top_k_csr(x, k):
     sel = np.sort(order)
     ptrs = np.searchsorted(sel, np.arange(rows + 1, dtype=np.int64) * cols).astype(np.int32)
     return ptrs, (sel % cols).astype(np.int32), flat[sel].astype(np.float32)
+
+
+SWITCH_POINT = 10  # BLOCK4_SPARSE_MAX_COUNT (block4.hpp:332-340)
+
+
+def sparse_pack_tile(tile16):
+    """block4_sparse_pack (block4.hpp:364-383), restated: [count] then
+    ceil(count/2) bytes of 4-bit slot positions (even index -> high nibble)
+    then the count live bytes, slots ascending."""
+    t = np.asarray(tile16, np.uint8)
+    live = np.flatnonzero(t)
+    n = len(live)
+    pos = bytearray((n + 1) // 2)
+    for i, slot in enumerate(live):
+        pos[i // 2] |= (int(slot) << 4) if i % 2 == 0 else int(slot)
+    return bytes([n]) + bytes(pos) + bytes(t[live])
+
+
+def pack_tiles(tiles, flags):
+    """A block4 store's tiles as stored bytes: sparse-packed where flags[t],
+    else the 16 dense bytes; concatenated in store order."""
+    tiles = np.asarray(tiles, np.uint8).reshape(-1, 16)
+    out = bytearray()
+    for t, f in zip(tiles, flags):
+        out += sparse_pack_tile(t) if f else t.tobytes()
+    return np.frombuffer(bytes(out), np.uint8).copy()
+
+
+def tile_live(tiles):
+    return (np.asarray(tiles, np.uint8).reshape(-1, 16) != 0).sum(1)
+
+
+class TileEncodingState:
+    """Which block4 tiles the reference stores sparse-packed (tile_is_sparse,
+    block4.hpp:1016-1031), restated as the rules its operations apply:
+
+    - a tile written through a handle that was created sparse (every new
+      tile: get_or_create starts it sparse-empty, block4.hpp:1150-1183) is
+      re-encoded when the handle commits: sparse iff live <= switch_point
+      (commit_dirty_sparse_tile, :1226-1290) -- loads (put_tile,
+      block4_load_dense, delta_csr_memory.hpp:884-932) and promotion;
+    - maybe_compress (:1193-1205), called after promotion and after an
+      insert into an existing tile (delta_csr_memory.hpp:656,698), packs a
+      dense tile with live <= switch_point;
+    - the optimizer updates rewrite every tile they touch through a row
+      workspace, re-encoding it by its live count
+      (commit_dirty_tile_in_workspace, :1336-1355): the dense update touches
+      every tile (linear_disldo.hpp:984-1000: every tiled row counts
+      n_tiles * 4 synapses), the sparse-gradient update the tiles with a
+      nonzero dy in one of their columns (sisldo_ops.hpp:945-1016);
+    - a removal writes the slot to 0 in place: a dense tile stays dense
+      (and a tile left with < 2 live slots is demoted away)."""
+
+    def __init__(self, switch_point=SWITCH_POINT):
+        self.sp = int(switch_point)
+        self.flag = {}
+
+    @staticmethod
+    def _keys(br, bc):
+        return list(zip(np.asarray(br).tolist(), np.asarray(bc).tolist()))
+
+    def reencode(self, br, bc, tiles, which=None):
+        live = tile_live(tiles)
+        for i, k in enumerate(self._keys(br, bc)):
+            if which is None or which[i]:
+                self.flag[k] = int(live[i] <= self.sp)
+
+    load = reencode
+
+    def structural(self, before, after):
+        """An edit (removals, inserts into tiles, promotion, demotion) from
+        (br, bc, tiles) `before` to `after`."""
+        old = {k: t for k, t in zip(self._keys(before[0], before[1]),
+                                    np.asarray(before[2], np.uint8).reshape(-1, 16))}
+        tiles = np.asarray(after[2], np.uint8).reshape(-1, 16)
+        live = tile_live(tiles)
+        flag = {}
+        for i, k in enumerate(self._keys(after[0], after[1])):
+            t = old.get(k)
+            if t is None or np.any((t == 0) & (tiles[i] != 0)):
+                flag[k] = int(live[i] <= self.sp)  # promoted, or received an insert
+            else:
+                flag[k] = self.flag[k]
+        self.flag = flag
+
+    def flags(self, br, bc):
+        return np.array([self.flag[k] for k in self._keys(br, bc)], np.uint8)
 
 
 FOR_REF_PATH = HERE / "_ref" / "libfor_ref.so"
@@ -739,6 +834,21 @@ class RefLayer:
         val = np.zeros(max(1, n), np.uint8)
         R.ref_layer_export(self.h, _p(bs, _u64p), _p(es, _u64p), _p(idx, _u8p), _p(val, _u8p))
         return bs, es, idx[:nb], val[:n]
+
+    def export_tiles_packed(self):
+        """(tile_is_sparse flags, stored tile bytes concatenated, per-block-row
+        used bytes) as the reference's Block4Store holds them."""
+        R = reflib()
+        n = R.ref_layer_export_tiles_packed(self.h, None, None, None)
+        nt = len(self.export_tiles()[0])
+        flags = np.zeros(max(nt, 1), np.uint8)
+        packed = np.zeros(max(n, 1), np.uint8)
+        used = np.zeros((self.n_in + 3) // 4, np.uint64)
+        R.ref_layer_export_tiles_packed(self.h, _p(flags, _u8p), _p(packed, _u8p), _p(used, _u64p))
+        return flags[:nt], packed[:n], used
+
+    def switch_point(self, set_to=-1):
+        return int(reflib().ref_block4_switch_point(self.h, int(set_to)))
 
     def export_tiles(self):
         R = reflib()

@@ -175,6 +175,43 @@ int64_t ref_layer_export_tiles(void *h, int32_t *br_out, int32_t *bc_out, uint8_
     return k;
 }
 
+// The block4 store's tile encoding as the reference holds it
+// (block4.hpp:1016-1031): per tile its tile_is_sparse flag and its stored
+// bytes (16 dense, or the sparse pack [count][positions][values],
+// block4.hpp:332-388), the row's tiles concatenated without the row's
+// headroom; row_used[br] = tile_byte_end - tile_byte_start.  Returns the
+// packed byte count (flags and row_used may be NULL).
+int64_t ref_layer_export_tiles_packed(void *h, uint8_t *flags, uint8_t *packed, uint64_t *row_used) {
+    auto *L = static_cast<RefLayer *>(h);
+    auto &B = L->w.block4;
+    int64_t k = 0, nb = 0;
+    for (size_t br = 0; br < B.block_layout.rows; ++br) {
+        const size_t n = B.block_layout.row_nnz(br);
+        size_t pos = B.tile_byte_start[br];
+        for (size_t e = 0; e < n; ++e) {
+            const size_t elem = B.block_layout.elem_start[br] + e;
+            const bool sp = B.tile_is_sparse[elem] != 0;
+            const size_t len = block4_stored_tile_len(sp, &B.tile_data[pos]);
+            if (flags) flags[k] = sp ? 1 : 0;
+            if (packed) std::memcpy(packed + nb, &B.tile_data[pos], len);
+            nb += int64_t(len);
+            pos += len;
+            ++k;
+        }
+        if (row_used) row_used[br] = B.tile_byte_end[br] - B.tile_byte_start[br];
+    }
+    return nb;
+}
+uint32_t ref_block4_switch_point(void *h, int set) {
+    auto *L = static_cast<RefLayer *>(h);
+    if (set >= 0) L->w.block4.switch_point = uint32_t(set);
+    return L->w.block4.switch_point;
+}
+uint64_t ref_block4_used_bytes(void *h) {
+    return static_cast<RefLayer *>(h)->w.block4.total_tile_used_bytes();
+}
+uint64_t ref_block4_live(void *h) { return static_cast<RefLayer *>(h)->w.block4.live_synapses(); }
+
 int64_t ref_layer_combined(void *h, int32_t *ptrs, int32_t *idx, float *w, float *imp) {
     auto *L = static_cast<RefLayer *>(h);
     std::vector<S> op, oi;

@@ -600,7 +600,7 @@ void build_colblocks_b4(Layer &L, DBlock4 &b, int K, int64_t cbb) {
 }
 
 void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_t *d_bc,
-                  const uint8_t *d_tiles) {
+                  const uint8_t *d_tiles, const uint8_t *d_flags) {
     hipStream_t st = L.stream;
     const int64_t brows = (L.n_in + 3) / 4, bcols = (L.n_out + 3) / 4;
     const int64_t N = n_tiles;
@@ -636,6 +636,14 @@ void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_
                                  d_tiles, false);
             inv.ensure((size_t)N + 1);
             if (N > 0) launch(k_inv_perm, dim3(nblk(N)), dim3(TPB), 0, st, (const uint32_t *)perm.p, N, inv.p);
+            // tile_is_sparse of the canonical tiles: carried through the sort,
+            // or (a load) every tile encoded by its live count
+            L.B4.sparse.ensure((size_t)N + 1);
+            if (N > 0 && d_flags)
+                launch(k_gather_u8, dim3(nblk(N)), dim3(TPB), 0, st, d_flags, (const uint32_t *)perm.p, N,
+                       L.B4.sparse.p);
+            else if (N > 0)
+                tiles_reencode(L, nullptr, st);
         } else {
             build_b4_orientation(L, L.B4t, N, bcols, brows, L.n_out, L.n_in, major.p, minor.p, perm.p,
                                  d_tiles, true);

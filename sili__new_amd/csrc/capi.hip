@@ -497,6 +497,9 @@ void backward_dense_train(Layer &L, const float *x, const float *dy, int64_t B, 
     launch_train_rows(L, xT, gT, B, dx, p, seed, st);
     // block4 tiles after the scattered rows' scale steps (linear_disldo.hpp:962-1951)
     launch_train_b4(L, xT, gT, B, dx, p, seed, st);
+    // the update rewrites every tile: each is re-encoded by its live count
+    // (linear_disldo.hpp:1839-1856, block4.hpp:1336-1355)
+    tiles_reencode(L, nullptr, st);
     if (L.W.n_empty_rows > 0) launch_train_dead_rows(L, xT, gT, B, p, st);
     const bool scales_step = L.update_variant != UPDATE_NOSCALE;
     if (L.output_scale_trainable && scales_step && L.W.nnz > 0) launch_train_cols(L, p, st);
@@ -578,6 +581,9 @@ void backward_sparse_train(Layer &L, const float *x, const int32_t *dptrs, const
     // block4 tiles after the scattered section (sisldo_ops.hpp:848-1100)
     const uint64_t seed = splitmix64_host(L.rng_seed ^ splitmix64_host(L.rng_calls + 1));
     launch_sparse_train_b4(L, xT, L.ws_gT.p, B, dx, p, seed, st);
+    // tiles with a nonzero dy in one of their columns were rewritten
+    // (sisldo_ops.hpp:945-1033): re-encoded by their live count
+    tiles_reencode_sparse_update(L, L.ws_gT.p, B, st);
     launch_shadow_val_refresh(L, st);
     launch_b4_shadow_refresh(L, st);
     for (DScatter *sc : {&L.W, &L.Wt}) {
@@ -1279,6 +1285,48 @@ int sili_profile_read(sili_layer *layer, sili_prof_entry *out, int max_entries, 
         P.recs.clear();
         if (n_entries) *n_entries = (int)agg.size();
         for (int i = 0; out && i < (int)agg.size() && i < max_entries; ++i) out[i] = agg[(size_t)i];
+    });
+}
+
+int sili_export_block4_packed(sili_layer *layer, uint8_t *tile_is_sparse, uint8_t *tile_data,
+                              uint64_t *tile_byte_start, int64_t *nbytes) {
+    return guarded([&] {
+        if (!layer || !nbytes) throw_error(SILI_ERR_INVALID, "NULL argument");
+        Layer &L = layer->L;
+        set_device(L);
+        const PackedTiles pk = export_tiles_packed(L);
+        *nbytes = (int64_t)pk.bytes.size();
+        if (tile_is_sparse && !pk.flags.empty()) std::memcpy(tile_is_sparse, pk.flags.data(), pk.flags.size());
+        if (tile_data && !pk.bytes.empty()) std::memcpy(tile_data, pk.bytes.data(), pk.bytes.size());
+        if (tile_byte_start)
+            std::memcpy(tile_byte_start, pk.row_start.data(), pk.row_start.size() * sizeof(uint64_t));
+    });
+}
+
+int sili_block4_view(sili_layer *layer, sili_block4_stats *out) {
+    return guarded([&] {
+        if (!layer || !out) throw_error(SILI_ERR_INVALID, "NULL argument");
+        Layer &L = layer->L;
+        set_device(L);
+        const PackedTiles pk = export_tiles_packed(L);
+        out->tiles = L.B4.ntiles;
+        out->synapses = pk.live;
+        out->switch_point = L.switch_point;
+        out->used_bytes = (int64_t)pk.bytes.size();
+        out->alloc_bytes = (int64_t)pk.bytes.size();
+        out->dropped_growth_events = 0;
+        out->row_merge_overflow_events = 0;
+        out->row_merge_overflow_bytes_dropped = 0;
+    });
+}
+
+int sili_set_switch_point(sili_layer *layer, uint32_t switch_point) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        if (switch_point > 10)
+            throw_error(SILI_ERR_INVALID, "switch_point must be <= 10 (a sparse-packed tile of more live "
+                                          "slots is longer than a dense one, block4.hpp:332-340)");
+        layer->L.switch_point = switch_point;
     });
 }
 

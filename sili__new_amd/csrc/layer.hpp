@@ -119,6 +119,10 @@ struct DBlock4 {
     DevBuf<uint32_t> byte_start, tile_start;  // brows+1
     DevBuf<uint8_t> idx;
     DevBuf<uint8_t> tiles;                    // 16 * ntiles
+    // canonical store only: the reference's tile_is_sparse per tile (the
+    // encoding its Block4Store would hold the tile in; the device computes on
+    // the dense 16 bytes and packs on export)
+    DevBuf<uint8_t> sparse;
     DevBuf<SegDesc> seg;
     // column-block copies (as DScatter::cblk, in block columns of cblk_cbb)
     std::vector<DBlock4> cblk;
@@ -233,6 +237,7 @@ struct Layer {
     bool stochastic_rounding = true;
     uint64_t rng_seed = 0x5EEDull, rng_calls = 0;
     int64_t train_calls = 0;
+    uint32_t switch_point = 10;  // tiles with <= this many live slots are stored sparse-packed
     uint32_t seg_len = 512;     // max index bytes per decode work item (scattered)
     uint32_t seg_len_b4 = 128;  // max block-index bytes per decode work item (block4)
 };
@@ -275,8 +280,10 @@ void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64
 void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const uint32_t *d_cols,
                   DScatter &dst);
 // Block4 store (and its shadow) from an unsorted device tile list.
+// d_flags (optional, parallel to the input tiles): the tiles' tile_is_sparse;
+// NULL: every tile encoded by its live count (a load).
 void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_t *d_bc,
-                  const uint8_t *d_tiles);
+                  const uint8_t *d_tiles, const uint8_t *d_flags = nullptr);
 // Full decode of the canonical scattered store into device arrays.
 void decode_scattered(Layer &L, uint32_t *d_rows, uint32_t *d_cols);
 // Recompute has_nonfinite (code 8 anywhere, or a non-finite scale).
@@ -287,6 +294,19 @@ void refresh_nonfinite(Layer &L);
 // order) from the FOR copy or, for comparison, from the ULEB128 stream.
 void build_for_index(Layer &L, int G);
 void decode_columns(Layer &L, int32_t *cols, bool use_for, hipStream_t st);
+
+// Block4 tile encoding (tile_enc.hip): re-encode tiles by their live count
+// (all, or those with dirty[t] != 0); the tiles a sparse-gradient update
+// touched (a nonzero dy in one of their columns, gT feature-major [n_out, B]);
+// and the reference's stored tile bytes for export.
+void tiles_reencode(Layer &L, const uint8_t *dirty, hipStream_t st);
+void tiles_reencode_sparse_update(Layer &L, const float *gT, int64_t B, hipStream_t st);
+struct PackedTiles {
+    std::vector<uint8_t> flags, bytes;
+    std::vector<uint64_t> row_start;  // brows + 1
+    int64_t live = 0;
+};
+PackedTiles export_tiles_packed(Layer &L);
 
 // Module CSR utilities (csr_util.hip): device buffers, synchronous on st.
 void dense_to_csr_device(const float *x, int64_t rows, int64_t cols, float threshold, int32_t *ptrs, int32_t *idx,

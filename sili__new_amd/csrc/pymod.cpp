@@ -67,6 +67,32 @@ uint64_t g_seed_epoch = 0;
 // sili_set_update_variant's values
 constexpr int UPDATE_PLAIN_V = 0, UPDATE_RESYNC_V = 1, UPDATE_NOSCALE_V = 2;
 
+class Layer;
+
+// Block4View (sili/cpu_backend.cpp:43-98, bound :1428-1469): the block4
+// store's counters and its switch_point, read through the layer.
+class Block4View {
+   public:
+    explicit Block4View(sili_layer *L) : L_(L) {}
+    sili_block4_stats stats() const {
+        sili_block4_stats st{};
+        ck(sili_block4_view(L_, &st));
+        return st;
+    }
+    int64_t tiles() const { return stats().tiles; }
+    int64_t synapses() const { return stats().synapses; }
+    uint32_t get_switch_point() const { return stats().switch_point; }
+    void set_switch_point(uint32_t v) { ck(sili_set_switch_point(L_, v)); }
+    int64_t dropped_growth_events() const { return stats().dropped_growth_events; }
+    int64_t row_merge_overflow_events() const { return stats().row_merge_overflow_events; }
+    int64_t row_merge_overflow_bytes_dropped() const { return stats().row_merge_overflow_bytes_dropped; }
+    int64_t used_bytes() const { return stats().used_bytes; }
+    int64_t alloc_bytes() const { return stats().alloc_bytes; }
+
+   private:
+    sili_layer *L_;
+};
+
 class Layer {
    public:
     Layer(int64_t n_inputs, int64_t n_outputs, int64_t max_weights, int num_cpus, int device)
@@ -500,6 +526,24 @@ class Layer {
         d["bidx"] = bix;
         return d;
     }
+    Block4View block4() { return Block4View(L_); }
+    // the reference's stored tile encoding: tile_is_sparse, tile_data (rows
+    // concatenated without headroom) and each block row's first byte
+    py::dict export_block4_packed() {
+        int64_t nb = 0;
+        sili_info i;
+        ck(sili_get_info(L_, &i));
+        ck(sili_export_block4_packed(L_, nullptr, nullptr, nullptr, &nb));
+        py::array_t<uint8_t> f((py::ssize_t)i.n_tiles), d((py::ssize_t)nb);
+        py::array_t<uint64_t> rs((py::ssize_t)((n_in_ + 3) / 4 + 1));
+        ck(sili_export_block4_packed(L_, f.mutable_data(), d.mutable_data(), rs.mutable_data(), &nb));
+        py::dict out;
+        out["tile_is_sparse"] = f;
+        out["tile_data"] = d;
+        out["tile_byte_start"] = rs;
+        return out;
+    }
+
     // the FOR index of the canonical store (derived copy, built on request)
     void build_for_index(int group_size) { ck(sili_build_for_index(L_, group_size)); }
     py::dict export_for_index() {
@@ -705,6 +749,15 @@ void bind_variant(py::module_ &m, const char *name) {
 
 PYBIND11_MODULE(_sili_hip, m) {
     m.doc() = "gfx950 FP4 delta-CSR sparse linear layer (sili SparseLinearLayer API)";
+    py::class_<Block4View>(m, "Block4View")
+        .def_property_readonly("tiles", &Block4View::tiles)
+        .def_property_readonly("synapses", &Block4View::synapses)
+        .def_property("switch_point", &Block4View::get_switch_point, &Block4View::set_switch_point)
+        .def_property_readonly("dropped_growth_events", &Block4View::dropped_growth_events)
+        .def_property_readonly("row_merge_overflow_events", &Block4View::row_merge_overflow_events)
+        .def_property_readonly("row_merge_overflow_bytes_dropped", &Block4View::row_merge_overflow_bytes_dropped)
+        .def_property_readonly("used_bytes", &Block4View::used_bytes)
+        .def_property_readonly("alloc_bytes", &Block4View::alloc_bytes);
     py::class_<Layer>(m, "SparseLinearLayer")
         .def(py::init<int64_t, int64_t, int64_t, int, int>(), py::arg("n_inputs"), py::arg("n_outputs"),
              py::arg("max_weights"), py::arg("num_cpus") = 4, py::arg("device") = 0)
@@ -768,6 +821,8 @@ PYBIND11_MODULE(_sili_hip, m) {
         .def("export_block4", &Layer::export_block4)
         .def("decode_scattered", &Layer::decode_scattered)
         .def("build_for_index", &Layer::build_for_index, py::arg("group_size") = 16)
+        .def("export_block4_packed", &Layer::export_block4_packed)
+        .def_property_readonly("block4", py::cpp_function(&Layer::block4, py::keep_alive<0, 1>()))
         .def("export_for_index", &Layer::export_for_index)
         .def("decode_columns", &Layer::decode_columns, py::arg("use_for_index") = true)
         .def("synchronize", &Layer::synchronize)

@@ -238,8 +238,8 @@ __global__ void k_syn_first(int64_t n_cand, const uint64_t *ckey_sorted, const u
 __global__ void k_syn_insert(int64_t n_cand, const uint32_t *first, const uint32_t *rank, int64_t k_target,
                              const int32_t *cr, const int32_t *cc, const float *cv, const float *cs,
                              uint32_t default_imp, ScaleView sc, const uint64_t *tkey, int64_t T,
-                             const uint8_t *alive, uint8_t *tbytes, uint64_t bcols, uint64_t *ins_key,
-                             uint8_t *ins_byte, uint64_t *win, unsigned long long *n_grown) {
+                             const uint8_t *alive, uint8_t *tbytes, uint8_t *tins, uint64_t bcols,
+                             uint64_t *ins_key, uint8_t *ins_byte, uint64_t *win, unsigned long long *n_grown) {
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (i >= n_cand) return;
     ins_key[i] = KEY_NONE;
@@ -255,6 +255,7 @@ __global__ void k_syn_insert(int64_t n_cand, const uint32_t *first, const uint32
     const int64_t t = find_tile(tkey, T, alive, wkey);
     if (t >= 0) {
         tbytes[t * 16 + (c & 3u) * 4u + (r & 3u)] = (uint8_t)((ic << 4) | wc);
+        tins[t] = 1;  // an insert into an existing tile re-encodes it (maybe_compress)
     } else {
         ins_key[i] = rc_key(r, c);
         ins_byte[i] = (uint8_t)((wc << 4) | ic);
@@ -334,10 +335,14 @@ __global__ void k_tile_flags(int64_t T, const uint8_t *alive, int64_t n_win, con
     else if (i < T + n_win) flag[i] = nt_flag[i - T];
 }
 
+// Output tiles with their encoding (tile_is_sparse): a surviving tile keeps
+// its own unless it received an insert; inserted and promoted tiles are
+// encoded by their live count (block4.hpp:1193-1205, 1226-1290).
 __global__ void k_emit_tiles(int64_t T, const uint32_t *tbr, const uint32_t *tbc, const uint8_t *tbytes,
-                             int64_t n_win, const uint32_t *nt_br, const uint32_t *nt_bc,
-                             const uint8_t *nt_bytes, const uint32_t *flag, const uint32_t *pos,
-                             uint32_t *obr, uint32_t *obc, uint8_t *obytes) {
+                             const uint8_t *tsparse, const uint8_t *tins, uint32_t sp, int64_t n_win,
+                             const uint32_t *nt_br, const uint32_t *nt_bc, const uint8_t *nt_bytes,
+                             const uint32_t *flag, const uint32_t *pos, uint32_t *obr, uint32_t *obc,
+                             uint8_t *obytes, uint8_t *osparse) {
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (i >= T + n_win || !flag[i]) return;
     const uint32_t o = pos[i];
@@ -346,7 +351,12 @@ __global__ void k_emit_tiles(int64_t T, const uint32_t *tbr, const uint32_t *tbc
     obr[o] = old ? tbr[j] : nt_br[j];
     obc[o] = old ? tbc[j] : nt_bc[j];
     const uint8_t *src = old ? tbytes + j * 16 : nt_bytes + j * 16;
-    for (int s = 0; s < 16; ++s) obytes[(int64_t)o * 16 + s] = src[s];
+    uint32_t live = 0;
+    for (int s = 0; s < 16; ++s) {
+        obytes[(int64_t)o * 16 + s] = src[s];
+        live += src[s] != 0;
+    }
+    osparse[o] = (old && !tins[j]) ? tsparse[j] : (live <= sp ? 1u : 0u);
 }
 
 template <typename T>
@@ -406,6 +416,9 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
     if (T > 0) SILI_HIP(hipMemcpyAsync(tbytes.p, L.B4.tiles.p, (size_t)T * 16, hipMemcpyDeviceToDevice, st));
     TmpBuf<uint64_t> tkey(L, SILI_TMPKEY(tkey));  // window keys of the canonical tiles (ascending)
     tkey.ensure((size_t)T + 1);
+    TmpBuf<uint8_t> tins(L, SILI_TMPKEY(tins));  // tiles that received an insert
+    tins.ensure((size_t)T + 1);
+    launch(k_fill_u8, dim3(nblk(T + 1)), dim3(TPB), 0, st, tins.p, T + 1, (uint8_t)0);
 
     // -- select: order by (|w| bits, row, col) -------------------------------
     TmpBuf<uint64_t> rc(L, SILI_TMPKEY(rc)), rc_sorted(L, SILI_TMPKEY(rc_sorted));
@@ -564,7 +577,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
         launch(k_syn_insert, dim3(g), dim3(TPB), 0, st, n_cand, (const uint32_t *)first.p,
                (const uint32_t *)rank.p, k_grow, (const int32_t *)dcr.p, (const int32_t *)dcc.p,
                (const float *)dcv.p, cand_s ? (const float *)dcs.p : nullptr, (uint32_t)default_imp, sc,
-               (const uint64_t *)tkey.p, T, (const uint8_t *)alive.p, tbytes.p, bcols, key2.p + (Ns + T),
+               (const uint64_t *)tkey.p, T, (const uint8_t *)alive.p, tbytes.p, tins.p, bcols, key2.p + (Ns + T),
                byte2.p + (Ns + T), win.p, counters.p + 2);
         launch(k_iota32, dim3(g), dim3(TPB), 0, st, wv.p, n_cand);
         SILI_HIP(hipGetLastError());
@@ -621,7 +634,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
 
     const int64_t MT = T + n_cand;
     TmpBuf<uint32_t> tflag(L, SILI_TMPKEY(tflag)), tpos(L, SILI_TMPKEY(tpos)), obr(L, SILI_TMPKEY(obr)), obc(L, SILI_TMPKEY(obc));
-    TmpBuf<uint8_t> obytes(L, SILI_TMPKEY(obytes));
+    TmpBuf<uint8_t> obytes(L, SILI_TMPKEY(obytes)), osparse(L, SILI_TMPKEY(osparse));
     tflag.ensure((size_t)MT + 1);
     tpos.ensure((size_t)MT + 1);
     if (MT > 0) {
@@ -633,11 +646,13 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
     obr.ensure((size_t)n_tiles + 1);
     obc.ensure((size_t)n_tiles + 1);
     obytes.ensure((size_t)n_tiles * 16 + 1);
+    osparse.ensure((size_t)n_tiles + 1);
     if (MT > 0) {
         launch(k_emit_tiles, dim3(nblk(MT)), dim3(TPB), 0, st, T, (const uint32_t *)tbr.p,
-               (const uint32_t *)tbc.p, (const uint8_t *)tbytes.p, n_cand, (const uint32_t *)nt_br.p,
+               (const uint32_t *)tbc.p, (const uint8_t *)tbytes.p, (const uint8_t *)L.B4.sparse.p,
+               (const uint8_t *)tins.p, L.switch_point, n_cand, (const uint32_t *)nt_br.p,
                (const uint32_t *)nt_bc.p, (const uint8_t *)nt_bytes.p, (const uint32_t *)tflag.p,
-               (const uint32_t *)tpos.p, obr.p, obc.p, obytes.p);
+               (const uint32_t *)tpos.p, obr.p, obc.p, obytes.p, osparse.p);
         SILI_HIP(hipGetLastError());
     }
     unsigned long long cnt[4];
@@ -646,7 +661,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
 
     build_scattered(L, L.W, n_in, n_out, n_final, fptrs.p, fcols.p, fbytes.p);
     build_shadow(L, L.W, frows.p, fcols.p, L.Wt);
-    build_block4(L, n_tiles, obr.p, obc.p, obytes.p);
+    build_block4(L, n_tiles, obr.p, obc.p, obytes.p, osparse.p);
     refresh_nonfinite(L);
 
     int64_t n_promoted = n_tiles - (T - (int64_t)cnt[1]);
