@@ -494,8 +494,9 @@ def time_synap_policy(hip, wl, reps, seconds):
     per cycle on the GPU layer (host decisions, device edit and rebuild), and
     the reference's own functions (oracle/_ref) on the same layer."""
     from oracle import RefLayer, have_ref
-    L = hip.SparseLinearLayerDeterministic(wl.n_in, wl.n_out, wl.nnz + 4096)
+    L = hip.SparseLinearLayerDeterministic(wl.n_in, wl.n_out, 2 * wl.nnz + 4096)
     L.load_weights(wl.ptrs, wl.cols, wl.q)
+    L.expand_headroom(1.0)  # the rows' room the reference layer below is built with
     L.set_value_scales(wl.value_scale)
     x, g = wl.x.astype(np.float32), wl.g.astype(np.float32)
     L.forward_dense(x)

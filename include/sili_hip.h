@@ -267,8 +267,14 @@ int sili_backward_sparse_train(sili_layer *layer, const float *x, const int32_t 
  *   max_prune_per_step; grows the row's probes by descending score into the
  *   capacity left, weight 0 and importance = score; block4 demotion and
  *   promotion as the reference.  *did: 0 when the row holds nothing and there
- *   are no probes.  The store never runs out of row headroom here (it is
- *   rebuilt compactly), where the reference would throw.
+ *   are no probes.  Each insert is checked against the row's reservation
+ *   (sili_export_layout) as delta_csr_row_insert_col checks it
+ *   (delta_csr_memory.hpp:498-585): when one does not fit, the removals and
+ *   the inserts before it stay applied, the call returns SILI_ERR_RUNTIME with
+ *   the reference's message (:1236-1250) and the cursor does not advance.
+ *   When a demotion would not fit (block4_demote_tile, :949-999) the call
+ *   returns SILI_ERR_RUNTIME with the layer unchanged (the reference leaves
+ *   that tile half demoted).
  * sili_synap_step: the same on the layer's own cursor (synap_step).
  * sili_get_out_degree: out_degree [n_outputs] as the reference keeps it: the
  *   scattered synapses per column after a load, then +1 / -1 per
@@ -303,6 +309,33 @@ int sili_synapto_step(sili_layer *layer, float prune_frac, const int32_t *cand_r
                       const int32_t *cand_cols, const float *cand_vals,
                       const float *cand_scores, int64_t n_cand, int default_imp_code,
                       int64_t *out_stats);
+
+/* ---- the reference's scattered reservations (DeltaCSRLayout) -------------
+ * The device store is compact; the layer keeps, per row, the index bytes and
+ * value elements the reference's store would reserve, so that inserts run out
+ * of room and growth meets the budget (max_weights * 8 + 4096 index bytes,
+ * max_weights + 64 values, grown by loads) where the reference's do.
+ * Loads reserve as delta_csr_from_absolute with blank_fraction 0.2
+ * (delta_csr_memory.hpp:16-93); the bulk sili_synapto_step, which has no
+ * reference counterpart, grows a row's reservation to its content when needed.
+ * sili_compact: compact() (sisldo_ops.hpp:44-96, sili/cpu_backend.cpp:737-748).
+ * sili_expand_headroom[_to]: sisldo_ops.hpp:127-186 (SILI_ERR_NOMEM beyond
+ *   the budget, layer unchanged).  compact and expand re-encode every
+ *   scattered value byte as the reference's rebuild does (code 8 -> 0).
+ * sili_equalize_to_capacity: sili/cpu_backend.cpp:684-729 (target_bytes 0:
+ *   5 * target_elems + 4); SILI_ERR_NOMEM when a row's growth exceeds the
+ *   budget, the rows before it grown.
+ * sili_equalizer_step: the scattered half of equalizer_step
+ *   (sili/cpu_backend.cpp:649-657, delta_csr_memory.hpp:295-306).
+ * sili_export_layout: the reference's byte_start [n_in+1], byte_end [n_in],
+ *   elem_start [n_in+1], elem_end [n_in]; any may be NULL. */
+int sili_compact(sili_layer *layer);
+int sili_expand_headroom(sili_layer *layer, float blank_fraction);
+int sili_expand_headroom_to(sili_layer *layer, int64_t min_nnz_per_row, float blank_fraction);
+int sili_equalize_to_capacity(sili_layer *layer, int64_t target_elems_per_row, int64_t target_bytes_per_row);
+int sili_equalizer_step(sili_layer *layer);
+int sili_export_layout(sili_layer *layer, uint64_t *byte_start, uint64_t *byte_end, uint64_t *elem_start,
+                       uint64_t *elem_end);
 
 /* ---- accumulators ------------------------------------------------------- */
 

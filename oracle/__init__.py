@@ -11,4 +11,5 @@ product (sili__new_amd) never imports, links or runs anything here.
 from .oracle import (  # noqa: F401
     HostLayer, RefLayer, build, dense_to_csr, dense_to_top_k_csr, for_encode_row, for_encode_rows, have_ref, lib,
     ref_for_encode, ref_top_k_csr, reflib, SWITCH_POINT, TileEncodingState, pack_tiles, sparse_pack_tile, tile_live,
+    ScatteredReservations, row_content, synap_no_room_message, demote_no_room_message,
 )

@@ -126,7 +126,8 @@ def lib(contracted: bool = False):
                                           _f32p, C.c_int64]
         L.oracle_synap_row_step.argtypes = [C.POINTER(_OracleLayerC), C.c_int64, _i32p, _i32p, _f32p, C.c_int64,
                                             C.c_int, C.c_float, C.c_int64, C.c_int64, C.c_float, _i32p, _i32p, _i32p,
-                                            _u8p, _i32p, _i32p, _u8p, C.POINTER(C.c_int64)]
+                                            _u8p, _i32p, _i32p, _u8p, C.POINTER(C.c_int64), _u64p, _u64p,
+                                            C.POINTER(C.c_int64)]
         L.oracle_synapto_step.argtypes = [C.POINTER(_OracleLayerC), C.c_float, _i32p, _i32p, _f32p, _f32p,
                                           C.c_int64, C.c_int, _i32p, _i32p, _u8p, _i32p, _i32p, _u8p,
                                           C.POINTER(_SynStats)]
@@ -207,6 +208,16 @@ def reflib():
         R.ref_block4_live.argtypes = [C.c_void_p]
         R.ref_top_k_csr.restype = C.c_int64
         R.ref_top_k_csr.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, C.c_int, _i32p, _i32p, _f32p]
+        R.ref_last_error.restype = C.c_char_p
+        R.ref_sll_new.restype = C.c_void_p
+        R.ref_sll_new.argtypes = [C.c_int, C.c_int, C.c_int]
+        R.ref_sll_load_weights.argtypes = [C.c_void_p, _i32p, _i32p, _f32p, _f32p]
+        R.ref_sll_compact.argtypes = [C.c_void_p]
+        R.ref_sll_expand.argtypes = [C.c_void_p, C.c_float]
+        R.ref_sll_expand_to.argtypes = [C.c_void_p, C.c_int, C.c_float]
+        R.ref_sll_equalize_to_capacity.argtypes = [C.c_void_p, C.c_int, C.c_int]
+        R.ref_sll_equalizer_step.argtypes = [C.c_void_p]
+        R.ref_layer_layout.argtypes = [C.c_void_p, _u64p, _u64p, _u64p, _u64p]
         _ref = R
     return _ref
 
@@ -246,6 +257,137 @@ def dense_to_top_k_csr(x, k):
     sel = np.sort(order)
     ptrs = np.searchsorted(sel, np.arange(rows + 1, dtype=np.int64) * cols).astype(np.int32)
     return ptrs, (sel % cols).astype(np.int32), flat[sel].astype(np.float32)
+
+
+class ScatteredReservations:
+    """The reference's per-row reservations of its scattered store
+    (DeltaCSRLayout, delta_csr_types.hpp:763-797: byte_start/elem_start with
+    blank space between rows) under the calls that set them.  Row contents
+    (index bytes, synapses per row) are passed in by the caller; this class
+    holds only the reservations b[r], e[r], the budgets and the equalizer
+    cursor of SparseLinearLayer (sili/cpu_backend.cpp:371-447, 646-790).
+
+    - from_absolute (delta_csr_memory.hpp:56-66): b = bytes + floor(bytes * f)
+      + 5, e = n + max(1, floor(n * f) + 1), the products in fp32;
+    - load_weights grows the budgets to the load (:866-876) and reserves with
+      f = 0.2; compact (sisldo_ops.hpp:44-96) reserves the content;
+    - expand_headroom[_to] (sisldo_ops.hpp:127-186): from_absolute after its
+      reserve() calls pass the limits (delta_csr_types.hpp:925-938), sizes in
+      double: n' (1 + f) * 6 + 4096 index bytes, (size_t)(n' (1 + f)) + 64
+      values, n' = nnz or max(nnz, rows * min_nnz_per_row); MemoryError else;
+    - delta_csr_shift_row (delta_csr_memory.hpp:224-293): the byte side, then
+      the element side, never on the last row, growth beyond the budget a
+      MemoryError (the byte side already moved);
+    - equalize_to_capacity (sili/cpu_backend.cpp:684-729), equalizer_step
+      (:646-657 -> delta_csr_memory.hpp:295-306)."""
+
+    ULEB_MAX = 5
+
+    def __init__(self, n_in, max_weights):
+        self.n = int(n_in)
+        self.idx_budget = int(max_weights) * 8 + 4096
+        self.val_budget = int(max_weights) + 64
+        self.eq = 0
+        z = np.zeros(self.n, np.uint64)
+        self.from_absolute(z, z, 0.2)
+
+    def from_absolute(self, row_bytes, row_elems, f):
+        f = np.float32(f)
+        rb = np.asarray(row_bytes, np.uint64)
+        re_ = np.asarray(row_elems, np.uint64)
+        self.b = rb + (rb.astype(np.float32) * f).astype(np.uint64) + np.uint64(self.ULEB_MAX)
+        self.e = re_ + np.maximum(np.uint64(1), (re_.astype(np.float32) * f).astype(np.uint64) + np.uint64(1))
+        return self
+
+    def load(self, row_bytes, row_elems):
+        nnz = int(np.sum(np.asarray(row_elems, np.uint64)))
+        self.idx_budget = max(self.idx_budget, nnz * 8 + 4096)
+        self.val_budget = max(self.val_budget, nnz + 64)
+        return self.from_absolute(row_bytes, row_elems, 0.2)
+
+    def compact(self, row_bytes, row_elems):
+        self.b = np.asarray(row_bytes, np.uint64).copy()
+        self.e = np.asarray(row_elems, np.uint64).copy()
+        return self
+
+    def expand(self, row_bytes, row_elems, f=0.2, min_nnz_per_row=None):
+        n = float(np.sum(np.asarray(row_elems, np.uint64)))
+        budget = n if min_nnz_per_row is None else max(n, float(self.n) * float(min_nnz_per_row))
+        grow = 1.0 + float(np.float32(f))
+        index_bytes = int(budget * grow * (self.ULEB_MAX + 1) + 4096.0)
+        values = int(budget * grow) + 64
+        if values > self.val_budget or index_bytes > self.idx_budget:
+            raise MemoryError("expand_headroom beyond the layer's budget")
+        return self.from_absolute(row_bytes, row_elems, f)
+
+    def _shift(self, row, tb, te):
+        if row + 1 >= self.n:
+            return
+        if int(self.b[row]) != tb:
+            if tb > int(self.b[row]) and int(self.b.sum()) + tb - int(self.b[row]) > self.idx_budget:
+                raise MemoryError("delta_csr_shift_row beyond the layer's budget")
+            self.b[row] = tb
+        if int(self.e[row]) != te:
+            if te > int(self.e[row]) and int(self.e.sum()) + te - int(self.e[row]) > self.val_budget:
+                raise MemoryError("delta_csr_shift_row beyond the layer's budget")
+            self.e[row] = te
+
+    def equalize_to_capacity(self, te, tb=0):
+        te = int(te)
+        tb = int(tb) if tb > 0 else te * self.ULEB_MAX + 4
+        for r in range(self.n - 1):
+            ub, ue = max(int(self.b[r]), tb), max(int(self.e[r]), te)
+            if ub == int(self.b[r]) and ue == int(self.e[r]):
+                continue
+            self._shift(r, ub, ue)
+        if self.n > 0:
+            self.b[-1] = max(int(self.b[-1]), tb)
+            self.e[-1] = max(int(self.e[-1]), te)
+        return self
+
+    def equalizer_step(self):
+        if self.n == 0:
+            return self
+        row = self.eq % self.n
+        tb = (int(self.b.sum()) + self.n - 1) // self.n
+        te = (int(self.e.sum()) + self.n - 1) // self.n
+        self._shift(row, tb, te)
+        self.eq = (row + 1) % self.n
+        return self
+
+    def fit(self, row_bytes, row_elems):
+        self.b = np.maximum(self.b, np.asarray(row_bytes, np.uint64))
+        self.e = np.maximum(self.e, np.asarray(row_elems, np.uint64))
+        return self
+
+    def layout(self, row_bytes, row_elems):
+        bs = np.concatenate([[0], np.cumsum(self.b)]).astype(np.uint64)
+        es = np.concatenate([[0], np.cumsum(self.e)]).astype(np.uint64)
+        return dict(byte_start=bs, byte_end=bs[:-1] + np.asarray(row_bytes, np.uint64),
+                    elem_start=es, elem_end=es[:-1] + np.asarray(row_elems, np.uint64))
+
+
+def row_content(row_byte_start, row_elem_start):
+    """(index bytes, synapses) per row of a compact store."""
+    return np.diff(np.asarray(row_byte_start, np.uint64)), np.diff(np.asarray(row_elem_start, np.uint64))
+
+
+def synap_no_room_message(row, fail):
+    """delta_csr_synap_row_step's message when an insert does not fit
+    (delta_csr_memory.hpp:1239-1248); fail = (probe index, column, used
+    bytes, reserved bytes, insertions skipped)."""
+    i, col, used, alloc, skipped = (int(v) for v in fail)
+    return (f"delta_csr_synap_row_step: row {row} ran out of blank space at probe_index={i} col={col} "
+            f"(used {used} / {alloc} bytes, {skipped} insertions skipped). Call equalizer_step() to "
+            "redistribute space from adjacent rows before retrying, or reduce max_row_weights / raise "
+            "importance_cutoff.")
+
+
+def demote_no_room_message(fail):
+    """block4_demote_tile's message (delta_csr_memory.hpp:985-989)."""
+    r, br, bc = (int(v) for v in fail[:3])
+    return (f"block4_demote_tile: row {r} ran out of blank space while demoting tile ({br},{bc}). "
+            "Call equalizer_step() to redistribute space from adjacent rows before retrying.")
 
 
 SWITCH_POINT = 10  # BLOCK4_SPARSE_MAX_COUNT (block4.hpp:332-340)
@@ -681,8 +823,12 @@ class HostLayer:
         self.probe_nnz = int(n)
 
     def synap_row_step(self, current_row, importance_cutoff, max_row_weights, max_prune_per_step=8,
-                       importance_eps=1e-3):
-        """delta_csr_synap_row_step: returns (did, next cursor)."""
+                       importance_eps=1e-3, reservations=None):
+        """delta_csr_synap_row_step: returns (did, next cursor).  With
+        reservations (a ScatteredReservations), an insert or a demotion that
+        does not fit raises RuntimeError with the reference's message: the
+        removals and earlier inserts stay applied after an insert's failure,
+        nothing does after a demotion's."""
         if self.n_in == 0:
             return False, current_row
         row = int(current_row) % self.n_in
@@ -703,21 +849,32 @@ class HostLayer:
         tby = np.zeros(16 * cap_t, np.uint8)
         ntl = C.c_int64(0)
         s = self._cstruct()
+        rb = re_ = None
+        if reservations is not None:
+            rb = _c(reservations.b, np.uint64)
+            re_ = _c(reservations.e, np.uint64)
+        fail = np.zeros(5, np.int64)
         did = lib().oracle_synap_row_step(C.byref(s), row, _p(prow, _i32p), _p(pcol, _i32p), _p(pval, _f32p),
                                           self.probe_nnz, int(len(prow) > 0), importance_cutoff,
                                           int(max_row_weights), int(max_prune_per_step), importance_eps,
                                           _p(self.out_deg, _i32p), _p(ptrs, _i32p), _p(cols, _i32p), _p(byts, _u8p),
-                                          _p(tbr, _i32p), _p(tbc, _i32p), _p(tby, _u8p), C.byref(ntl))
+                                          _p(tbr, _i32p), _p(tbc, _i32p), _p(tby, _u8p), C.byref(ntl),
+                                          _p(rb, _u64p), _p(re_, _u64p), fail.ctypes.data_as(C.POINTER(C.c_int64)))
         n = int(ptrs[-1])
         k = int(ntl.value)
         self.load_csr(ptrs, cols[:n], bytes_=byts[:n])
         self.load_tiles(tbr[:k], tbc[:k], tby[:16 * k])
+        if did == -2:
+            raise RuntimeError(synap_no_room_message(row, fail))
+        if did == -3:
+            raise RuntimeError(demote_no_room_message(fail))
         return bool(did), nxt
 
-    def synap_step(self, importance_cutoff, max_row_weights, max_prune_per_step=8, importance_eps=1e-3):
+    def synap_step(self, importance_cutoff, max_row_weights, max_prune_per_step=8, importance_eps=1e-3,
+                   reservations=None):
         cur = getattr(self, "synap_cursor", 0)
         did, self.synap_cursor = self.synap_row_step(cur, importance_cutoff, max_row_weights, max_prune_per_step,
-                                                     importance_eps)
+                                                     importance_eps, reservations)
         return did
 
     def sampled_gradw(self, x, dy, threads=8, absmode=False):
@@ -771,6 +928,55 @@ class RefLayer:
                                        _p(self._keep[2], _f32p), _p(self._keep[3], _f32p) if imp is not None else None,
                                        float(blank_fraction))
 
+    @classmethod
+    def sll(cls, n_in, n_out, max_weights):
+        """An empty layer as SparseLinearLayer(n_in, n_out, max_weights)
+        constructs it (sili/cpu_backend.cpp:375-447): budgets and limits set."""
+        self = cls.__new__(cls)
+        self.n_in, self.n_out = int(n_in), int(n_out)
+        self._keep = []
+        self.h = reflib().ref_sll_new(self.n_in, self.n_out, int(max_weights))
+        return self
+
+    def _sll(self, rc):
+        if rc != 0:
+            raise MemoryError(reflib().ref_last_error().decode())
+        return self
+
+    def load_weights(self, ptrs, cols, w, imp=None):
+        """SparseLinearLayer.load_weights (sili/cpu_backend.cpp:859-901)."""
+        self._keep = [_c(ptrs, np.int32), _c(cols, np.int32), _c(w, np.float32)]
+        imp = None if imp is None else _c(imp, np.float32)
+        self._keep.append(imp)
+        return self._sll(reflib().ref_sll_load_weights(self.h, _p(self._keep[0], _i32p), _p(self._keep[1], _i32p),
+                                                       _p(self._keep[2], _f32p), _p(imp, _f32p)))
+
+    def compact_layer(self):
+        """SparseLinearLayer.compact (limits re-applied)."""
+        return self._sll(reflib().ref_sll_compact(self.h))
+
+    def expand_headroom(self, blank_fraction=0.2):
+        return self._sll(reflib().ref_sll_expand(self.h, float(blank_fraction)))
+
+    def expand_headroom_to(self, min_nnz_per_row, blank_fraction=0.2):
+        return self._sll(reflib().ref_sll_expand_to(self.h, int(min_nnz_per_row), float(blank_fraction)))
+
+    def equalize_to_capacity(self, target_elems_per_row, target_bytes_per_row=0):
+        return self._sll(reflib().ref_sll_equalize_to_capacity(self.h, int(target_elems_per_row),
+                                                               int(target_bytes_per_row)))
+
+    def equalizer_step(self):
+        return self._sll(reflib().ref_sll_equalizer_step(self.h))
+
+    def layout(self):
+        """The scattered DeltaCSRLayout: byte_start/elem_start [n_in+1],
+        byte_end/elem_end [n_in]."""
+        n = self.n_in
+        bs, be = np.zeros(n + 1, np.uint64), np.zeros(max(n, 1), np.uint64)
+        es, ee = np.zeros(n + 1, np.uint64), np.zeros(max(n, 1), np.uint64)
+        reflib().ref_layer_layout(self.h, _p(bs, _u64p), _p(be, _u64p), _p(es, _u64p), _p(ee, _u64p))
+        return dict(byte_start=bs, byte_end=be[:n], elem_start=es, elem_end=ee[:n])
+
     def block4_headroom(self, blank_fraction=0.2, min_slack_bytes=16):
         reflib().ref_layer_block4_headroom(self.h, float(blank_fraction), int(min_slack_bytes))
         return self
@@ -793,7 +999,7 @@ class RefLayer:
         rc = reflib().ref_synap_row_step(self.h, C.byref(row), importance_cutoff, int(max_row_weights),
                                          int(max_prune_per_step), importance_eps)
         if rc == -2:
-            raise RuntimeError("reference synap_row_step ran out of row headroom")
+            raise RuntimeError(reflib().ref_last_error().decode())
         return bool(rc), int(row.value)
 
     def out_degree(self):

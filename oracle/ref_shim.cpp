@@ -15,6 +15,7 @@
 #include <cstdint>
 #include <cstring>
 #include <memory>
+#include <string>
 #include <vector>
 
 using S = int;
@@ -24,7 +25,25 @@ using Weights = SparseLinearWeightsDelta<S, FP4BiPacked, COL>;
 struct RefLayer {
     Weights w;
     int n_in = 0, n_out = 0;
+    // SparseLinearLayerImpl's budgets and equalizer cursors
+    // (sili/cpu_backend.cpp:371-373, 646-657); SIZE_MAX: a layer built by
+    // ref_layer_new[_blank], whose limits are never set
+    size_t idx_budget = SIZE_MAX, val_budget = SIZE_MAX;
+    size_t eq_row = 0, b4_eq_row = 0;
 };
+
+static std::string g_last_error;
+
+template <typename F>
+static int guarded_ref(F &&f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception &e) {
+        g_last_error = e.what();
+        return -1;
+    }
+}
 
 static CSRInput<S, float> make_input(const int32_t *ptrs, const int32_t *idx, const float *vals,
                                      int batch, int cols) {
@@ -308,7 +327,8 @@ int ref_synap_row_step(void *h, int64_t *row, float cutoff, int max_rw, int max_
         const bool did = delta_csr_synap_row_step<S, FP4BiPacked, COL>(L->w, r, cutoff, S(max_rw), S(max_prune), eps);
         *row = int64_t(r);
         return did ? 1 : 0;
-    } catch (const std::exception &) {
+    } catch (const std::exception &e) {
+        g_last_error = e.what();
         *row = int64_t(r);
         return -2;
     }
@@ -430,6 +450,135 @@ int64_t ref_top_k_csr(float *x, int rows, int cols, int k, int threads, int32_t 
     std::copy(i.begin(), i.end(), idx);
     std::copy(v.begin(), v.end(), vals);
     return int64_t(i.size());
+}
+
+// ---- SparseLinearLayerImpl's reservation calls ------------------------------
+// The class's own wrapper logic (sili/cpu_backend.cpp, which needs pybind and
+// is not built here) restated around the header functions it calls: the
+// constructor's empty layer and limits (:375-447), load_weights (:859-901),
+// compact / expand_headroom[_to] (:737-790), equalize_to_capacity (:684-729)
+// and equalizer_step (:646-657).  Each returns 0, or -1 when the reference
+// throws (bad_alloc: the budget) with the message in ref_last_error().
+const char *ref_last_error() { return g_last_error.c_str(); }
+
+void *ref_sll_new(int n_in, int n_out, int max_weights) {
+    auto *L = new RefLayer();
+    L->n_in = n_in;
+    L->n_out = n_out;
+    L->idx_budget = size_t(max_weights) * 8 + 4096;
+    L->val_budget = size_t(max_weights) + 64;
+    std::vector<S> p(size_t(n_in) + 1, 0), ix;
+    std::vector<float> ww, ii;
+    L->w.connections = delta_csr_from_absolute<S, FP4BiPacked, COL>(p, ix, ww, ii, size_t(n_in), size_t(n_out),
+                                                                    L->idx_budget, L->val_budget);
+    L->w.connections.set_limits(L->idx_budget, ValueAccessor<FP4BiPacked>::projected_byte_size(L->val_budget));
+    L->w.block4.init(size_t(n_in), size_t(n_out));
+    L->w.block4.set_limits(size_t(max_weights) * 8 + 4096,
+                           std::max<size_t>(4, size_t(max_weights) / BLOCK4_TILE_SLOTS) * BLOCK4_TILE_SLOTS);
+    L->w.out_degree.assign(size_t(n_out), 0);
+    L->w.recompute_stats();
+    return L;
+}
+
+int ref_sll_load_weights(void *h, const int32_t *ptrs, const int32_t *idx, const float *w, const float *imp) {
+    auto *L = static_cast<RefLayer *>(h);
+    return guarded_ref([&] {
+        std::vector<S> p(ptrs, ptrs + L->n_in + 1);
+        const size_t nnz = size_t(p.back());
+        std::vector<S> ix(idx, idx + nnz);
+        std::vector<float> ww(w, w + nnz), ii(nnz, 0.0f);
+        if (imp) ii.assign(imp, imp + nnz);
+        L->idx_budget = std::max(L->idx_budget, nnz * 8 + 4096);
+        L->val_budget = std::max(L->val_budget, nnz + 64);
+        L->w.connections = delta_csr_from_absolute<S, FP4BiPacked, COL>(p, ix, ww, ii, size_t(L->n_in),
+                                                                        size_t(L->n_out), L->idx_budget, L->val_budget);
+        L->w.connections.set_limits(L->idx_budget, ValueAccessor<FP4BiPacked>::projected_byte_size(L->val_budget));
+        L->w.recompute_stats();
+        L->w.out_degree.assign(size_t(L->n_out), 0);
+        for (S c : ix) ++L->w.out_degree[size_t(c)];
+    });
+}
+
+static void reapply_limits(RefLayer *L) {
+    L->w.connections.set_limits(L->idx_budget, ValueAccessor<FP4BiPacked>::projected_byte_size(L->val_budget));
+}
+
+int ref_sll_compact(void *h) {
+    auto *L = static_cast<RefLayer *>(h);
+    return guarded_ref([&] {
+        L->w.connections = compact<S, FP4BiPacked, COL>(L->w.connections);
+        reapply_limits(L);
+    });
+}
+
+int ref_sll_expand(void *h, float blank_fraction) {
+    auto *L = static_cast<RefLayer *>(h);
+    return guarded_ref([&] {
+        L->w.connections = expand_headroom<S, FP4BiPacked, COL>(L->w.connections, blank_fraction);
+        reapply_limits(L);
+    });
+}
+
+int ref_sll_expand_to(void *h, int min_nnz_per_row, float blank_fraction) {
+    auto *L = static_cast<RefLayer *>(h);
+    return guarded_ref([&] {
+        L->w.connections =
+            expand_headroom_to<S, FP4BiPacked, COL>(L->w.connections, size_t(min_nnz_per_row), blank_fraction);
+        reapply_limits(L);
+    });
+}
+
+int ref_sll_equalize_to_capacity(void *h, int target_elems, int target_bytes) {
+    auto *L = static_cast<RefLayer *>(h);
+    return guarded_ref([&] {
+        const size_t te = size_t(target_elems);
+        const size_t tb = target_bytes > 0 ? size_t(target_bytes) : te * uleb128_max_bytes<COL>() + 4;
+        auto &dc = L->w.connections;
+        const size_t rows = dc.layout.rows;
+        for (size_t r = 0; r + 1 < rows; ++r) {
+            const size_t cb = dc.layout.row_alloc_bytes(r), ce = dc.layout.row_alloc_elems(r);
+            const size_t ub = std::max(cb, tb), ue = std::max(ce, te);
+            if (ub == cb && ue == ce) continue;
+            delta_csr_shift_row<S, FP4BiPacked, COL>(dc, r, ub, ue);
+        }
+        if (rows > 0) {
+            auto &Ly = dc.layout;
+            const size_t r = rows - 1;
+            const size_t cb = Ly.row_alloc_bytes(r), ce = Ly.row_alloc_elems(r);
+            const size_t ub = std::max(cb, tb), ue = std::max(ce, te);
+            if (ub > cb) {
+                dc.indices_buf.resize(dc.indices_buf.size() + (ub - cb), uint8_t(0));
+                Ly.byte_start[rows] = Ly.byte_start[r] + ub;
+            }
+            if (ue > ce) {
+                const size_t nt = Ly.elem_start[rows] + (ue - ce);
+                ValueAccessor<FP4BiPacked>::resize(dc.values, nt);
+                Ly.elem_start[rows] = nt;
+            }
+        }
+    });
+}
+
+int ref_sll_equalizer_step(void *h) {
+    auto *L = static_cast<RefLayer *>(h);
+    return guarded_ref([&] {
+        delta_csr_equalize_step<S, FP4BiPacked, COL>(L->w.connections, L->eq_row);
+        L->w.block4.equalize_step(L->b4_eq_row);
+    });
+}
+
+// The scattered layout: byte_start/elem_start [n_in+1], byte_end/elem_end [n_in].
+void ref_layer_layout(void *h, uint64_t *bs, uint64_t *be, uint64_t *es, uint64_t *ee) {
+    auto *L = static_cast<RefLayer *>(h);
+    const auto &Ly = L->w.connections.layout;
+    for (size_t r = 0; r <= Ly.rows; ++r) {
+        bs[r] = Ly.byte_start[r];
+        es[r] = Ly.elem_start[r];
+        if (r < Ly.rows) {
+            be[r] = Ly.byte_end[r];
+            ee[r] = Ly.elem_end[r];
+        }
+    }
 }
 
 }  // extern "C"

@@ -1414,7 +1414,29 @@ struct MutLayer {
     int64_t n_in = 0, n_out = 0;
     std::vector<std::vector<std::pair<uint32_t, uint8_t>>> rows;  // per row, by column: (col, (w<<4)|imp)
     std::map<std::pair<uint32_t, uint32_t>, std::array<uint8_t, 16>> tiles;  // (br, bc) -> slot lj*4+li, (imp<<4)|w
+    // per-row reservations of the scattered store (index bytes, elements):
+    // the room delta_csr_row_insert_col checks; NULL: unlimited
+    const uint64_t *res_b = nullptr, *res_e = nullptr;
 };
+
+inline uint64_t uleb_size(uint32_t v) {
+    uint64_t n = 1;
+    while (v >= 0x80u) {
+        v >>= 7;
+        ++n;
+    }
+    return n;
+}
+
+uint64_t row_index_bytes(const std::vector<std::pair<uint32_t, uint8_t>> &row) {
+    uint64_t b = 0;
+    uint32_t prev = 0;
+    for (const auto &e : row) {
+        b += uleb_size(e.first - prev);
+        prev = e.first;
+    }
+    return b;
+}
 
 MutLayer load_mut(const OracleLayer *L) {
     MutLayer M;
@@ -1440,11 +1462,26 @@ MutLayer load_mut(const OracleLayer *L) {
 // ValueAccessor<FP4BiPacked>::set (fp4quant.hpp:280-467): round to nearest.
 inline uint8_t scat_byte(float w, float imp) { return uint8_t((fp4_enc(w) << 4) | fp4_enc(imp)); }
 
-// delta_csr_row_insert_col: false when the column is already stored.
+// delta_csr_row_insert_col (delta_csr_memory.hpp:498-585): false when the
+// column is already stored, or when the new delta (and the re-encoded next
+// one) would exceed the row's reserved bytes, or the row its reserved
+// elements -- the reference's unsigned arithmetic included.
 bool mut_insert(MutLayer &M, uint32_t r, uint32_t c, float w, float imp) {
     auto &row = M.rows[r];
     auto it = std::lower_bound(row.begin(), row.end(), std::make_pair(c, uint8_t(0)));
     if (it != row.end() && it->first == c) return false;
+    if (M.res_b) {
+        const uint32_t prev = it == row.begin() ? 0u : (it - 1)->first;
+        uint64_t grow = uleb_size(c - prev), shrink = 0;
+        if (it != row.end()) {
+            grow += uleb_size(it->first - c);
+            shrink = uleb_size(it->first - prev);
+        }
+        const int64_t idx_delta = int64_t(grow) - int64_t(shrink);
+        const uint64_t used = row_index_bytes(row);
+        if (idx_delta > 0 && uint64_t(idx_delta) > M.res_b[r] - used) return false;
+        if (uint64_t(row.size()) >= M.res_e[r]) return false;
+    }
     row.insert(it, {c, scat_byte(w, imp)});
     return true;
 }
@@ -1457,10 +1494,11 @@ bool mut_remove(MutLayer &M, uint32_t r, uint32_t c) {
     return true;
 }
 
-// block4_demote_tile (delta_csr_memory.hpp:949-999).
-void mut_demote(MutLayer &M, uint32_t br, uint32_t bc) {
+// block4_demote_tile (delta_csr_memory.hpp:949-999).  Returns the row whose
+// insert failed (the reference throws there), or -1.
+int64_t mut_demote(MutLayer &M, uint32_t br, uint32_t bc) {
     auto it = M.tiles.find({br, bc});
-    if (it == M.tiles.end()) return;
+    if (it == M.tiles.end()) return -1;
     const auto d = it->second;
     for (uint32_t li = 0; li < TILE; ++li) {
         const uint32_t r = br * TILE + li;
@@ -1470,10 +1508,11 @@ void mut_demote(MutLayer &M, uint32_t br, uint32_t bc) {
             if (b == 0) continue;
             const uint32_t c = bc * TILE + lj;
             if (int64_t(c) >= M.n_out) continue;
-            mut_insert(M, r, c, fp4_dec(b & 0xFu), fp4_dec(b >> 4));
+            if (!mut_insert(M, r, c, fp4_dec(b & 0xFu), fp4_dec(b >> 4))) return int64_t(r);
         }
     }
     M.tiles.erase(it);
+    return -1;
 }
 
 // block4_maybe_promote (delta_csr_memory.hpp:591-702).
@@ -1600,12 +1639,25 @@ int64_t oracle_build_probes(const OracleLayer *L, const float *acc_in, const flo
 // arrays (capacities: scattered <= nnz + n_probes + 16 * n_tiles, tiles <=
 // n_tiles + n_probes); *n_tiles_out receives the tile count.  Returns 1 when
 // the reference returns true, 0 when false.
+// res_b / res_e [n_in] (may be NULL: unlimited): the rows' reserved index
+// bytes and elements.  An insert that does not fit ends the call as the
+// reference's throw does (delta_csr_memory.hpp:1236-1250): returns -2, the
+// removals and the inserts before it applied, fail[0..4] = probe index,
+// column, the row's used bytes, its reserved bytes, insertions skipped.  A
+// demotion that does not fit (block4_demote_tile's throw, :983-991) returns
+// -3 with the layer as before the call and fail[0..2] = row, br, bc (the
+// reference leaves that tile half demoted).
 int oracle_synap_row_step(const OracleLayer *L, int64_t row, const int32_t *prow, const int32_t *pcol,
                           const float *pval, int64_t pnnz, int has_probes, float importance_cutoff,
                           int64_t max_row_weights, int64_t max_prune_per_step, float importance_eps,
                           int32_t *out_degree, int32_t *out_ptrs, int32_t *out_cols, uint8_t *out_bytes,
-                          int32_t *out_br, int32_t *out_bc, uint8_t *out_tiles, int64_t *n_tiles_out) {
+                          int32_t *out_br, int32_t *out_bc, uint8_t *out_tiles, int64_t *n_tiles_out,
+                          const uint64_t *res_b, const uint64_t *res_e, int64_t *fail) {
     MutLayer M = load_mut(L);
+    M.res_b = res_b;
+    M.res_e = res_b ? res_e : nullptr;
+    const MutLayer M0 = M;
+    std::vector<int32_t> deg0(out_degree, out_degree + L->n_out);
     auto finish = [&](int ret) {
         *n_tiles_out = mut_store(M, out_ptrs, out_cols, out_bytes, out_br, out_bc, out_tiles);
         return ret;
@@ -1689,14 +1741,35 @@ int oracle_synap_row_step(const OracleLayer *L, int64_t row, const int32_t *prow
                 for (uint8_t b : it->second) live += b != 0;
                 should_demote = live < PROMOTE_MIN_LIVE;
             }
-            if (should_demote) mut_demote(M, br, bc);
+            if (should_demote) {
+                const int64_t fr = mut_demote(M, br, bc);
+                if (fr >= 0) {
+                    M = M0;
+                    std::copy(deg0.begin(), deg0.end(), out_degree);
+                    if (fail) {
+                        fail[0] = fr;
+                        fail[1] = br;
+                        fail[2] = bc;
+                    }
+                    return finish(-3);
+                }
+            }
         } else {
             mut_remove(M, r, re.col);
         }
         if (out_degree[re.col] > 0) --out_degree[re.col];
     }
     for (size_t i = 0; i < probe_cols.size(); ++i) {
-        mut_insert(M, r, probe_cols[i], 0.0f, probe_scores[i]);
+        if (!mut_insert(M, r, probe_cols[i], 0.0f, probe_scores[i])) {
+            if (fail) {
+                fail[0] = int64_t(i);
+                fail[1] = probe_cols[i];
+                fail[2] = int64_t(row_index_bytes(M.rows[r]));
+                fail[3] = res_b ? int64_t(res_b[r]) : -1;
+                fail[4] = int64_t(probe_cols.size() - i);
+            }
+            return finish(-2);
+        }
         ++out_degree[probe_cols[i]];
         mut_maybe_promote(M, r, probe_cols[i]);
     }

@@ -184,14 +184,19 @@ int oracle_backward_sparse_train(const OracleLayer *L, uint8_t *val, uint8_t *ti
  * oracle_synap_row_step: delta_csr_synap_row_step (delta_csr_memory.hpp:
  * 1021-1264) on one row, sequential edit semantics; out_degree updated in
  * place; the new structure in the out_* arrays; returns 1/0 as the reference
- * returns true/false. */
+ * returns true/false.  res_b/res_e (NULL: unlimited): the rows' reserved
+ * index bytes and elements; -2 when an insert does not fit (the reference
+ * throws; removals and earlier inserts stay applied; fail[0..4] = probe
+ * index, column, used bytes, reserved bytes, insertions skipped), -3 when a
+ * demotion does not fit (layer as before; fail[0..2] = row, br, bc). */
 int64_t oracle_build_probes(const OracleLayer *L, const float *acc_in, const float *acc_grad, int64_t k,
                             int per_row, int32_t *prow, int32_t *pcol, float *pval, int64_t cap);
 int oracle_synap_row_step(const OracleLayer *L, int64_t row, const int32_t *prow, const int32_t *pcol,
                           const float *pval, int64_t pnnz, int has_probes, float importance_cutoff,
                           int64_t max_row_weights, int64_t max_prune_per_step, float importance_eps,
                           int32_t *out_degree, int32_t *out_ptrs, int32_t *out_cols, uint8_t *out_bytes,
-                          int32_t *out_br, int32_t *out_bc, uint8_t *out_tiles, int64_t *n_tiles_out);
+                          int32_t *out_br, int32_t *out_bc, uint8_t *out_tiles, int64_t *n_tiles_out,
+                          const uint64_t *res_b, const uint64_t *res_e, int64_t *fail);
 
 /* ---- bulk synaptogenesis step (magnitude prune + candidate regrow) ----
  * Output capacities: scattered entries <= nnz + n_cand + 16*n_tiles,

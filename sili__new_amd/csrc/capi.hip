@@ -214,6 +214,9 @@ void build_from_host_csr(Layer &L, const int32_t *ptrs, const int32_t *idx, cons
     build_scattered(L, L.W, L.n_in, L.n_out, nnz, dptrs.p, dcols.p, dbytes.p);
     rebuild_shadow(L);
     refresh_nonfinite(L);
+    // delta_csr_from_absolute's reservations, blank_fraction 0.2
+    // (sili/cpu_backend.cpp:873-874, and the constructor's empty layer)
+    layout_from_absolute(L, 0.2f);
 }
 
 void empty_stores(Layer &L) {
@@ -715,6 +718,7 @@ int sili_load_synthetic(sili_layer *layer, uint64_t seed, double keep_prob, floa
         set_device(L);
         const int64_t nnz = generate_synthetic(L, seed, keep_prob, sigma, tail_q);
         refresh_scale_flags(L);
+        layout_from_absolute(L, 0.2f);  // reserved as load_weights reserves
         if (nnz_out) *nnz_out = nnz;
     });
 }
@@ -1060,6 +1064,58 @@ int sili_synapto_step(sili_layer *layer, float prune_frac, const int32_t *cand_r
         set_device(layer->L);
         synapto_step(layer->L, prune_frac, cand_rows, cand_cols, cand_vals, cand_scores, n_cand, default_imp_code,
                      out_stats);
+        layout_fit(layer->L);
+    });
+}
+
+int sili_compact(sili_layer *layer) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        layout_compact(layer->L);
+    });
+}
+
+int sili_expand_headroom(sili_layer *layer, float blank_fraction) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        layout_expand(layer->L, blank_fraction, -1);
+    });
+}
+
+int sili_expand_headroom_to(sili_layer *layer, int64_t min_nnz_per_row, float blank_fraction) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        // a negative count is a size_t beyond any budget to the reference
+        if (min_nnz_per_row < 0) throw_error(SILI_ERR_NOMEM, "expand_headroom_to: min_nnz_per_row exceeds the budget");
+        set_device(layer->L);
+        layout_expand(layer->L, blank_fraction, min_nnz_per_row);
+    });
+}
+
+int sili_equalize_to_capacity(sili_layer *layer, int64_t target_elems_per_row, int64_t target_bytes_per_row) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        layout_equalize_to_capacity(layer->L, target_elems_per_row, target_bytes_per_row);
+    });
+}
+
+int sili_equalizer_step(sili_layer *layer) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        layout_equalizer_step(layer->L);
+    });
+}
+
+int sili_export_layout(sili_layer *layer, uint64_t *byte_start, uint64_t *byte_end, uint64_t *elem_start,
+                       uint64_t *elem_end) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        export_layout(layer->L, byte_start, byte_end, elem_start, elem_end);
     });
 }
 

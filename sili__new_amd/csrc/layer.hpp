@@ -238,6 +238,11 @@ struct Layer {
     uint64_t rng_seed = 0x5EEDull, rng_calls = 0;
     int64_t train_calls = 0;
     uint32_t switch_point = 10;  // tiles with <= this many live slots are stored sparse-packed
+    // The reference's per-row reservations of its scattered store (index
+    // bytes, value elements: used + blank, DeltaCSRLayout) and its
+    // equalizer_step cursor; the device store itself stays compact.
+    std::vector<uint64_t> lay_b, lay_e;
+    int64_t eq_cursor = 0;
     uint32_t seg_len = 512;     // max index bytes per decode work item (scattered)
     uint32_t seg_len_b4 = 128;  // max block-index bytes per decode work item (block4)
 };
@@ -288,6 +293,20 @@ void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_
 void decode_scattered(Layer &L, uint32_t *d_rows, uint32_t *d_cols);
 // Recompute has_nonfinite (code 8 anywhere, or a non-finite scale).
 void refresh_nonfinite(Layer &L);
+
+// The reference's scattered layout (layout.hip): per-row content read from
+// the device store, reservations kept on the host.
+void row_content(Layer &L, std::vector<uint64_t> &bytes, std::vector<uint64_t> &elems);
+void layout_from_absolute(Layer &L, float blank_fraction);
+void layout_compact(Layer &L);
+// min_nnz_per_row < 0: expand_headroom, else expand_headroom_to
+void layout_expand(Layer &L, float blank_fraction, int64_t min_nnz_per_row);
+void layout_equalize_to_capacity(Layer &L, int64_t target_elems, int64_t target_bytes);
+void layout_equalizer_step(Layer &L);
+// after a structural change the reference has no counterpart for: rows
+// whose content outgrew their reservation get exactly their content
+void layout_fit(Layer &L);
+void export_layout(Layer &L, uint64_t *byte_start, uint64_t *byte_end, uint64_t *elem_start, uint64_t *elem_end);
 
 // FOR index of the canonical scattered store (for_index.hip): build (group
 // size 8, 16, 32 or 64), and decode of every column into cols (int32, storage

@@ -18,6 +18,7 @@
 // here on the block row's tiles and only those the reference performs are
 // passed on.  Inserts are equivalent either way: each insert's promotion check
 // in the reference and the pipeline's one promotion pass leave the same tiles.
+#include "../../include/sili_hip.h"
 #include "layer.hpp"
 
 #include <algorithm>
@@ -117,6 +118,107 @@ std::map<uint32_t, std::array<uint8_t, 16>> read_block_row(Layer &L, int64_t br)
     return out;
 }
 
+inline uint64_t uleb_len(uint32_t v) {
+    uint64_t n = 1;
+    while (v >= 0x80u) {
+        v >>= 7;
+        ++n;
+    }
+    return n;
+}
+
+// The four rows of one block row and its tiles, edited one synapse at a time
+// as the reference edits its store in place: the rows' columns and index
+// bytes, checked against the rows' reservations (L.lay_b, L.lay_e) the way
+// delta_csr_row_insert_col (delta_csr_memory.hpp:498-585) checks them.
+struct BlockRowSim {
+    struct Row {
+        std::vector<uint32_t> cols;  // ascending
+        uint64_t bytes = 0;          // ULEB128 bytes of the row's deltas
+        bool loaded = false;
+    };
+    Layer &L;
+    uint32_t br;
+    std::map<uint32_t, std::array<uint8_t, 16>> &tiles;
+    Row rows[4];
+
+    Row &row(uint32_t li) {
+        Row &R = rows[li];
+        if (!R.loaded) {
+            const int64_t r = (int64_t)br * 4 + li;
+            if (r < L.n_in) set(li, read_row(L, r));
+            R.loaded = true;
+        }
+        return R;
+    }
+    void set(uint32_t li, const std::vector<std::pair<uint32_t, uint8_t>> &entries) {
+        Row &R = rows[li];
+        R.cols.clear();
+        R.bytes = 0;
+        uint32_t prev = 0;
+        for (const auto &e : entries) {
+            R.cols.push_back(e.first);
+            R.bytes += uleb_len(e.first - prev);
+            prev = e.first;
+        }
+        R.loaded = true;
+    }
+    // false: the column is stored already, or does not fit the reservation
+    bool insert(uint32_t li, uint32_t c) {
+        Row &R = row(li);
+        const size_t r = (size_t)br * 4 + li;
+        auto it = std::lower_bound(R.cols.begin(), R.cols.end(), c);
+        if (it != R.cols.end() && *it == c) return false;
+        const uint32_t prev = it == R.cols.begin() ? 0u : *(it - 1);
+        uint64_t grow = uleb_len(c - prev), shrink = 0;
+        if (it != R.cols.end()) {
+            grow += uleb_len(*it - c);
+            shrink = uleb_len(*it - prev);
+        }
+        const int64_t idx_delta = (int64_t)grow - (int64_t)shrink;
+        // unsigned as the reference evaluates it
+        if (idx_delta > 0 && (uint64_t)idx_delta > L.lay_b[r] - R.bytes) return false;
+        if ((uint64_t)R.cols.size() >= L.lay_e[r]) return false;
+        R.cols.insert(it, c);
+        R.bytes = (uint64_t)((int64_t)R.bytes + idx_delta);
+        return true;
+    }
+    void remove(uint32_t li, uint32_t c) {
+        Row &R = row(li);
+        auto it = std::lower_bound(R.cols.begin(), R.cols.end(), c);
+        if (it == R.cols.end() || *it != c) return;
+        const uint32_t prev = it == R.cols.begin() ? 0u : *(it - 1);
+        uint64_t freed = uleb_len(c - prev), merged = 0;
+        if (it + 1 != R.cols.end()) {
+            freed += uleb_len(*(it + 1) - c);
+            merged = uleb_len(*(it + 1) - prev);
+        }
+        R.bytes = R.bytes - freed + merged;
+        R.cols.erase(it);
+    }
+    // block4_maybe_promote (delta_csr_memory.hpp:591-702) after an insert at
+    // (row li, column c): into the window's tile, or a new tile when the
+    // window's four rows hold >= 2 scattered synapses
+    void promote(uint32_t li, uint32_t c) {
+        const uint32_t bc = c / 4;
+        auto t = tiles.find(bc);
+        if (t != tiles.end()) {
+            t->second[(c % 4) * 4 + li] = 1;
+            remove(li, c);
+            return;
+        }
+        std::vector<std::pair<uint32_t, uint32_t>> found;
+        for (uint32_t l = 0; l < 4 && (int64_t)br * 4 + l < L.n_in; ++l)
+            for (uint32_t col : row(l).cols)
+                if (col / 4 == bc) found.push_back({l, col});
+        if (found.size() < 2) return;
+        std::array<uint8_t, 16> d{};
+        for (const auto &f : found) d[(f.second % 4) * 4 + f.first] = 1;
+        tiles[bc] = d;
+        for (const auto &f : found) remove(f.first, f.second);
+    }
+};
+
 // L.out_deg holds out_degree; mark: from now on the policy keeps it.
 void ensure_out_deg(Layer &L, bool mark) {
     if (L.out_deg_tracked) return;
@@ -197,6 +299,8 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
                     int64_t max_prune_per_step, float importance_eps) {
     if (L.n_in == 0) return false;
     L.keep_temps = true;  // a layer that runs the policy rebuilds often: keep the rebuild's temporaries
+    if (L.lay_b.size() != (size_t)L.n_in) layout_fit(L);
+    const int64_t cursor0 = cursor;
     const int64_t row = cursor % L.n_in;
     cursor = (cursor + 1) % L.n_in;
     const uint32_t br = (uint32_t)(row / 4), li = (uint32_t)(row % 4);
@@ -263,8 +367,11 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
             }
         }
     }
-    // replay the removals on the block row's tiles: the ones the reference
-    // carries out
+    // replay the call's edits as the reference makes them, one synapse at a
+    // time: which removals it carries out, and whether every slot a demotion
+    // moves back to its row and every insert fits the row's reservation
+    BlockRowSim sim{L, br, btiles, {}};
+    sim.set(li, scat);
     std::vector<uint64_t> prune_keys;
     for (const auto &re : to_remove) {
         if (re.is_b4) {
@@ -275,10 +382,46 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
             prune_keys.push_back(((uint64_t)row << 32) | re.col);
             int live = 0;
             for (uint8_t b : it->second) live += b != 0;
-            if (live < 2) btiles.erase(it);  // demoted: its other slot is scattered now
+            if (live < 2) {  // block4_demote_tile: the slot left goes back to its row
+                const uint32_t bc = it->first;
+                for (uint32_t l2 = 0; l2 < 4; ++l2)
+                    for (uint32_t j2 = 0; j2 < 4; ++j2) {
+                        const int64_t r2 = (int64_t)br * 4 + l2, c2 = (int64_t)bc * 4 + j2;
+                        if (it->second[j2 * 4 + l2] == 0 || r2 >= L.n_in || c2 >= L.n_out) continue;
+                        if (!sim.insert(l2, (uint32_t)c2)) {
+                            cursor = cursor0;
+                            throw_error(SILI_ERR_RUNTIME,
+                                        "block4_demote_tile: row " + std::to_string(r2) +
+                                            " ran out of blank space while demoting tile (" + std::to_string(br) +
+                                            "," + std::to_string(bc) +
+                                            "). Call equalizer_step() to redistribute space from adjacent rows "
+                                            "before retrying.");
+                        }
+                    }
+                btiles.erase(it);
+            }
         } else {
             prune_keys.push_back(((uint64_t)row << 32) | re.col);
+            sim.remove(li, re.col);
         }
+    }
+    // the inserts, each followed by the promotion check; the first one that
+    // does not fit ends the call (delta_csr_memory.hpp:1236-1250) with the
+    // removals and the inserts before it applied
+    std::string no_room;
+    for (size_t i = 0; i < add_cols.size(); ++i) {
+        if (!sim.insert(li, add_cols[i])) {
+            no_room = "delta_csr_synap_row_step: row " + std::to_string(row) + " ran out of blank space at probe_index=" +
+                      std::to_string(i) + " col=" + std::to_string(add_cols[i]) + " (used " +
+                      std::to_string(sim.row(li).bytes) + " / " + std::to_string(L.lay_b[(size_t)row]) + " bytes, " +
+                      std::to_string(add_cols.size() - i) +
+                      " insertions skipped). Call equalizer_step() to redistribute space from adjacent rows before "
+                      "retrying, or reduce max_row_weights / raise importance_cutoff.";
+            add_cols.resize(i);
+            add_scores.resize(i);
+            break;
+        }
+        sim.promote(li, add_cols[i]);
     }
     // out_degree as the reference keeps it
     const int64_t n_edit = (int64_t)(to_remove.size() + add_cols.size());
@@ -303,15 +446,20 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
         SILI_HIP(hipGetLastError());
         SILI_HIP(hipStreamSynchronize(L.stream));
     }
-    if (prune_keys.empty() && add_cols.empty()) return true;
-    // the device edit: explicit removals, then the inserts (weight 0,
-    // importance = the probe score, delta_csr_memory.hpp:1234)
-    std::vector<int32_t> cr(add_cols.size(), (int32_t)row), cc(add_cols.begin(), add_cols.end());
-    std::vector<float> cv(add_cols.size(), 0.0f);
-    const bool tracked = L.out_deg_tracked;
-    synapto_apply(L, 0.0f, true, prune_keys.data(), (int64_t)prune_keys.size(), cr.data(), cc.data(), cv.data(),
-                  add_scores.data(), (int64_t)add_cols.size(), 0, nullptr);
-    L.out_deg_tracked = tracked;
+    if (!prune_keys.empty() || !add_cols.empty()) {
+        // the device edit: explicit removals, then the inserts (weight 0,
+        // importance = the probe score, delta_csr_memory.hpp:1234)
+        std::vector<int32_t> cr(add_cols.size(), (int32_t)row), cc(add_cols.begin(), add_cols.end());
+        std::vector<float> cv(add_cols.size(), 0.0f);
+        const bool tracked = L.out_deg_tracked;
+        synapto_apply(L, 0.0f, true, prune_keys.data(), (int64_t)prune_keys.size(), cr.data(), cc.data(), cv.data(),
+                      add_scores.data(), (int64_t)add_cols.size(), 0, nullptr);
+        L.out_deg_tracked = tracked;
+    }
+    if (!no_room.empty()) {
+        cursor = cursor0;
+        throw_error(SILI_ERR_RUNTIME, no_room);
+    }
     return true;
 }
 

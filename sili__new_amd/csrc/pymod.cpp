@@ -420,16 +420,41 @@ class Layer {
         return nnz;
     }
 
-    // The device store is always compact and rebuilt on every structural
-    // change, so the reference's headroom management calls have nothing to
-    // do (sisldo_ops.hpp:44-186, delta_csr_memory.hpp:224-306, 767-823).
-    void compact() {}
-    void expand_headroom(float) {}
-    void expand_headroom_to(int, float) {}
-    void equalizer_step() {}
-    void equalize_to_capacity(int, int) {}
+    // The reference's reservation management (sisldo_ops.hpp:44-186,
+    // delta_csr_memory.hpp:224-306, sili/cpu_backend.cpp:649-790): the device
+    // store stays compact while the layer keeps, per row, what the reference's
+    // store would reserve (export_layout), so that synap_row_step runs out of
+    // room and growth meets the budget where the reference's do.
+    void compact() {
+        flush();
+        ck(sili_compact(L_));
+    }
+    void expand_headroom(float bf) {
+        flush();
+        ck(sili_expand_headroom(L_, bf));
+    }
+    void expand_headroom_to(int m, float bf) {
+        flush();
+        ck(sili_expand_headroom_to(L_, m, bf));
+    }
+    void equalizer_step() { ck(sili_equalizer_step(L_)); }
+    void equalize_to_capacity(int te, int tb) { ck(sili_equalize_to_capacity(L_, te, tb)); }
+    // Block rows reserve no tile bytes beyond their content on the device
+    // (delta_csr_memory.hpp:767-835 has nothing to reserve), so these keep
+    // the tiles as they are.
     void expand_block4_headroom(float) {}
     void compact_block4() {}
+    py::dict export_layout() {
+        py::array_t<uint64_t> bs((py::ssize_t)(n_in_ + 1)), be((py::ssize_t)n_in_), es((py::ssize_t)(n_in_ + 1)),
+            ee((py::ssize_t)n_in_);
+        ck(sili_export_layout(L_, bs.mutable_data(), be.mutable_data(), es.mutable_data(), ee.mutable_data()));
+        py::dict d;
+        d["byte_start"] = bs;
+        d["byte_end"] = be;
+        d["elem_start"] = es;
+        d["elem_end"] = ee;
+        return d;
+    }
 
     // ---- accumulators / exports -----------------------------------------------
     py::array_t<float> neuron_input_accum() {
@@ -818,6 +843,7 @@ PYBIND11_MODULE(_sili_hip, m) {
         .def("zero_accum", &Layer::zero_accum)
         .def("info", &Layer::info)
         .def("export_scattered", &Layer::export_scattered)
+        .def("export_layout", &Layer::export_layout)
         .def("export_block4", &Layer::export_block4)
         .def("decode_scattered", &Layer::decode_scattered)
         .def("build_for_index", &Layer::build_for_index, py::arg("group_size") = 16)

@@ -5,9 +5,12 @@ binding, against the oracle after every call.
   :1152 backward, :1206-1212 synaptogenesis): budget n_in*n_out, load_weights
   of scale-divided values, per-row set_value_scale_raw (and, in rank1 mode,
   per-column set_output_scale_raw), set_importance_scale_raw(lr/6),
-  equalize_to_capacity(mrw, bpr), compact; forward_dense per suffix and the
-  fold sum; backward_dense(dy tiled over the folds, lr, lr_per_row_nnz=True);
-  build_probes(k) + n_inputs x synap_step + equalizer_step + zero_accum.
+  equalize_to_capacity(mrw, bpr) (compact_after_build=False: a compacted
+  layer has no room left to grow, and synaptogenesis raises there as in the
+  reference); forward_dense per suffix and the fold sum; backward_dense(dy
+  tiled over the folds, lr, lr_per_row_nnz=True); build_probes(k) +
+  n_inputs x synap_step + equalizer_step + zero_accum, the rows' reservations
+  checked against their restatement after every sweep.
 - SISLDOLayer (sili/sparse_rnn.py:779-803 with _preseed_random_sparse,
   :249-320): load_weights + equalize_to_capacity(per_row); forward_sparse of
   a top-k CSR input (CSR.from_dense, :80-97); backward through
@@ -23,7 +26,7 @@ import numpy as np
 import pytest
 
 import oracle
-from oracle import HostLayer
+from oracle import HostLayer, ScatteredReservations, row_content
 from train_util import dx_bound, dx_bound_sparse
 from util import assert_close_terms
 
@@ -72,7 +75,7 @@ def test_folded_layer_sequence(hip, batch):
     mrw = 20
     bits = max(1, n_out - 1).bit_length()
     bpr = mrw * ((bits + 6) // 7) + 4
-    layers, hosts = {}, {}
+    layers, hosts, res = {}, {}, {}
     for suffix, rank1 in (("q", False), ("up", True)):
         ptrs, cols, vals, rs, cs = folded_suffix(rng, n_in, n_out, 0.12, rank1)
         L = hip.SparseLinearLayerDeterministic(n_in, n_out, n_in * n_out, 4)
@@ -86,8 +89,10 @@ def test_folded_layer_sequence(hip, batch):
         for r in range(n_in):
             L.set_importance_scale_raw(r, lr / FP4_MAX)
         L.equalize_to_capacity(mrw, bpr)
-        L.compact()
         H = HostLayer(n_in, n_out).load_csr(ptrs, cols, w=vals)
+        S = ScatteredReservations(n_in, n_in * n_out)
+        S.load(*row_content(H.row_byte_start, H.row_elem_start)).equalize_to_capacity(mrw, bpr)
+        res[suffix] = S
         H.set_scales(rs, cs)
         # set_output_scale_raw marks the output scales trainable
         H.output_scale_trainable = bool(rank1)
@@ -133,9 +138,11 @@ def test_folded_layer_sequence(hip, batch):
                 pr, pc, pv = L.get_probes()
                 assert np.array_equal(pr, H.probes[0][:H.probe_nnz]) and \
                     np.array_equal(pc, H.probes[1][:H.probe_nnz]), f"{what} {s}: probes"
+                S = res[s]
                 for _ in range(L.n_inputs):
-                    assert L.synap_step(0.6, mrw) == H.synap_step(0.6, mrw), f"{what} {s}: synap_step"
+                    assert L.synap_step(0.6, mrw) == H.synap_step(0.6, mrw, reservations=S), f"{what} {s}: synap_step"
                 L.equalizer_step()
+                S.equalizer_step()
                 L.zero_accum()
                 H.acc[0][:] = 0
                 H.acc[1][:] = 0
@@ -145,6 +152,9 @@ def test_folded_layer_sequence(hip, batch):
                 assert np.array_equal(e["val"], H.val[:len(e["val"])]), f"{what} {s}: value bytes"
                 assert np.array_equal(L.out_degree, H.out_deg), f"{what} {s}: out_degree"
                 assert not np.any(L.neuron_input_accum) and not np.any(L.neuron_grad_accum)
+                lay = L.export_layout()
+                want = S.layout(*row_content(H.row_byte_start, H.row_elem_start))
+                assert all(np.array_equal(lay[k], want[k]) for k in want), f"{what} {s}: reservations"
 
 
 def test_sisldo_layer_sequence(hip):

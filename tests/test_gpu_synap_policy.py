@@ -14,9 +14,11 @@ pytestmark = pytest.mark.gpu
 
 
 def gpu_policy_layer(hip, c, cls="SparseLinearLayerDeterministic"):
-    L = getattr(hip, cls)(c["n_in"], c["n_out"], len(c["cols"]) + 16 * len(c["br"]) + 4096)
+    L = getattr(hip, cls)(c["n_in"], c["n_out"], 9 * len(c["cols"]) + 16 * len(c["br"]) + 4096)
     L.load_weights_with_importance(c["ptrs"], c["cols"], c["w"], c["imp"])
     L.load_block4_tiles(c["br"], c["bc"], c["tiles"])
+    # rows reserve what the pinned reference layers reserve (blank_fraction 8)
+    L.expand_headroom(8.0)
     return L
 
 
