@@ -56,6 +56,9 @@ def parse():
     p.add_argument("--index-decode", type=int, default=0, metavar="G",
                    help="only time decoding every column of the config-4 q layer from the ULEB128 stream and "
                         "from a FOR index of group size G")
+    p.add_argument("--sparse-sweep", action="store_true",
+                   help="only time the sparse-input forward of the config-2 layer at several input densities, "
+                        "pushed from the canonical store and gathered through the shadow store")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run 3 device-to-device copies of MIB MiB (HBM counter calibration)")
     return p.parse_args()
@@ -682,6 +685,57 @@ def run_index_decode(a, hip, api, rt):
     print(json.dumps(out), flush=True)
 
 
+def run_sparse_sweep(a, hip, api, rt):
+    """forward_sparse on the config-2 layer (16384 x 16384, Zipf rows,
+    batch 32) at input densities 0.5-10 %: the push kernel (work ~ the active
+    synapse visits) against the densify + shadow gather (work ~ nnz * B),
+    each forced with SILI_PUSH, device buffers in place, one layer copy."""
+    from sili__new_amd.synth import Stream, make_config
+    wl = make_config(2)
+    B, n_in, n_out = wl.batch, wl.n_in, wl.n_out
+    L = hip.SparseLinearLayer(n_in, n_out, wl.nnz)
+    L.load_weights(wl.ptrs, wl.cols, wl.q)
+    L.set_value_scales(wl.value_scale)
+    h = C.c_void_p(L.handle)
+    stream = api.L.sili_stream(h)
+    y = api.alloc(h, 4 * B * n_out)
+    out = {"workload": f"config-2 layer {n_in}x{n_out}, {wl.nnz} synapses, batch {B}; forward_sparse",
+           "densities": {}}
+    rng = Stream(SEED_SWEEP, 3)
+    for dens in (0.005, 0.01, 0.03, 0.1):
+        keep = rng.u64(B * n_in).reshape(B, n_in) % 1000 < int(dens * 1000)
+        xp = np.concatenate([[0], np.cumsum(keep.sum(1))]).astype(np.int32)
+        xi = np.nonzero(keep)[1].astype(np.int32)
+        xv = np.abs(rng.normal(len(xi))).astype(np.float32) + 0.01
+        dp, di, dv = api.upload(h, xp), api.upload(h, xi), api.upload(h, xv)
+        row = {"active_inputs": int(len(xi)),
+               "synapse_visits": int(np.diff(wl.ptrs)[xi].sum())}
+        for mode, name in (("2", "push"), ("0", "gather")):
+            os.environ["SILI_PUSH"] = mode
+            for _ in range(3):
+                api.ck(api.L.sili_forward_sparse(h, dp, di, dv, len(xi), B, y, stream))
+            rt.sync()
+            api.ck(api.L.sili_profile_enable(h, 1))
+            reps = 20
+            for _ in range(reps):
+                api.ck(api.L.sili_forward_sparse(h, dp, di, dv, len(xi), B, y, stream))
+            rt.sync()
+            prof = api.profile(h)
+            api.ck(api.L.sili_profile_enable(h, 0))
+            row[name + "_us"] = round(sum(tot for k, (cnt, tot) in prof.items()
+                                          if k.startswith("fwd_sparse:")) / reps * 1e3, 2)
+            row[name + "_kernels_us"] = {k: round(tot / reps * 1e3, 2) for k, (cnt, tot) in prof.items()}
+        os.environ.pop("SILI_PUSH", None)
+        for k in (dp, di, dv):
+            api.ck(api.L.sili_device_free(h, k))
+        out["densities"][f"{dens:g}"] = row
+    api.ck(api.L.sili_device_free(h, y))
+    print(json.dumps(out), flush=True)
+
+
+SEED_SWEEP = 20261290
+
+
 def cpu_baseline_c4(d, seconds):
     """The CPU port's forward over the q layer at batch 1 (exported from the
     device to a temporary file the child process loads): a bounded sample of
@@ -721,6 +775,9 @@ def main():
 
     if a.index_decode:
         run_index_decode(a, hip, CAbi(hip.LIB_PATH), Hip())
+        return
+    if a.sparse_sweep:
+        run_sparse_sweep(a, hip, CAbi(hip.LIB_PATH), Hip())
         return
     cfg = a.config
     if cfg == 4:

@@ -385,6 +385,7 @@ void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64
     dst.n_split = e.n_split;
     dst.stream1.valid = dst.streamK.valid = false;
     dst.fidx.valid = false;
+    dst.dcol_valid = false;
     dst.stream1.failed = dst.streamK.failed = false;
     dst.cblk.clear();
     dst.cblk_cb = 0;
@@ -435,6 +436,7 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
     dst.stream1.valid = dst.streamK.valid = false;
     dst.stream1.failed = dst.streamK.failed = false;
     dst.fidx.valid = false;
+    dst.dcol_valid = false;
     dst.cblk.clear();
     dst.cblk_cb = 0;
     dst.rows = src.cols;

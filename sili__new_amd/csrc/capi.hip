@@ -530,13 +530,27 @@ void forward_sparse(Layer &L, const int32_t *ptrs, const int32_t *idx, const flo
     ProfCtx pc(L, "fwd_sparse");
     if (B <= 0) throw_error(SILI_ERR_INVALID, "forward_sparse: batch must be >= 1");
     if (!ptrs || !y) throw_error(SILI_ERR_INVALID, "forward_sparse: NULL buffer");
-    L.ws_xT.ensure((size_t)(L.n_in * B));
     L.xT_cached_batch = 0;
-    fill(L.ws_xT.p, L.n_in * B, 0.0f, st);
-    launch_densify(ptrs, idx, vals, B, L.n_in, L.ws_xT.p, nullptr, true, nnz_x, st);
-    launch_zero_split_rows(L.Wt.plan(), y, L.n_out, B, st);
-    // only the active rows of each batch row contribute (sisldo_ops.hpp:271-313)
-    launch_gather(L.Wt.plan(), shadow_scales(L), L.ws_xT.p, B, y, L.n_out, B, SKIP_POSZERO, st);
+    // only the active rows of each batch row contribute (sisldo_ops.hpp:271-313).
+    // Sparse inputs are pushed from the canonical store (work ~ the active
+    // synapse visits); denser ones take the shadow gather (work ~ nnz * B),
+    // which is faster above ~2 % active inputs on MI355X (config-2 layer:
+    // push 21.3 / 25.7 / 37.8 / 76.8 us at 0.5 / 1 / 3 / 10 %, densify +
+    // gather ~32.5 us at any density).
+    // SILI_PUSH: 0 never, 2 whenever supported, else below 2 % active pairs.
+    const int push_mode = env_int("SILI_PUSH", 1);
+    const bool sparse_enough = (double)nnz_x < 0.02 * (double)B * (double)L.n_in;
+    const bool push = push_supported(L) && push_mode != 0 && (push_mode == 2 || sparse_enough);
+    if (push) launch_push_fwd(L, ptrs, idx, vals, B, canon_scales(L), y, false, st);
+    if (!push || L.B4t.ntiles > 0) {
+        L.ws_xT.ensure((size_t)(L.n_in * B));
+        fill(L.ws_xT.p, L.n_in * B, 0.0f, st);
+        launch_densify(ptrs, idx, vals, B, L.n_in, L.ws_xT.p, nullptr, true, nnz_x, st);
+    }
+    if (!push) {
+        launch_zero_split_rows(L.Wt.plan(), y, L.n_out, B, st);
+        launch_gather(L.Wt.plan(), shadow_scales(L), L.ws_xT.p, B, y, L.n_out, B, SKIP_POSZERO, st);
+    }
     if (L.B4t.ntiles > 0)
         launch_gather_b4(L.B4t.plan(), shadow_scales(L), L.ws_xT.p, B, y, L.n_out, B, SKIP_POSZERO, st);
 }

@@ -101,6 +101,10 @@ struct DScatter {
     int64_t n_split = 0;
     DStream stream1, streamK;     // stream copies: whole rows / the last column blocking used
     DFor fidx;                    // FOR copy of the column indices
+    // decoded column of every synapse (u16), for the sparse-input forward's
+    // random access (built on first use)
+    DevBuf<uint8_t> dcol;
+    bool dcol_valid = false;
     // column-block copies for gathers whose operand exceeds one XCD's L2:
     // cblk[k] holds every row's entries with columns in [k*cblk_cb, ...),
     // columns relative to the block (built on first use)
@@ -311,6 +315,15 @@ void export_layout(Layer &L, uint64_t *byte_start, uint64_t *byte_end, uint64_t 
 // FOR index of the canonical scattered store (for_index.hip): build (group
 // size 8, 16, 32 or 64), and decode of every column into cols (int32, storage
 // order) from the FOR copy or, for comparison, from the ULEB128 stream.
+// The sparse-input forward over the active (batch row, input row) pairs
+// (push.hip): y[b, :] (+)= sum over batch row b's CSR entries (r, x) of
+// x * W[r, :].  push_supported: the layer's output row fits a block's LDS.
+constexpr size_t PUSH_LDS_MAX = 150 * 1024;
+bool push_supported(const Layer &L);
+void ensure_decoded_cols(Layer &L, hipStream_t st);
+void launch_push_fwd(Layer &L, const int32_t *xptrs, const int32_t *xidx, const float *xval, int64_t B,
+                     const ScaleView &sc, float *y, bool add, hipStream_t st);
+
 void build_for_index(Layer &L, int G);
 void decode_columns(Layer &L, int32_t *cols, bool use_for, hipStream_t st);
 
