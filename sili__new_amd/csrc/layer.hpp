@@ -33,9 +33,12 @@ struct DevBuf {
     }
     // Ensure capacity for `count` elements (+ `pad` bytes of slack so vector
     // loads near the end stay in bounds).  Contents are not preserved.
+    // A buffer that has to grow again takes 1/8 more than asked, so a store
+    // rebuilt at slowly rising sizes is not reallocated every time.
     void ensure(size_t count, size_t pad = 64) {
-        const size_t want = count + (pad + sizeof(T) - 1) / sizeof(T);
+        size_t want = count + (pad + sizeof(T) - 1) / sizeof(T);
         if (want <= n && p) return;
+        if (p) want += want / 8;
         reset();
         SILI_HIP(hipMalloc(reinterpret_cast<void **>(&p), want * sizeof(T)));
         n = want;
@@ -261,8 +264,12 @@ struct TmpBuf {
     TmpBuf &operator=(const TmpBuf &) = delete;
     void ensure(size_t count, size_t pad = 64) {
         if (L_->keep_temps) {
+            // a kept buffer that must grow takes half again as much: a layer
+            // whose synapse count rises step by step reallocates (and, with
+            // hipFree, waits for the device) only every few steps
             DevBuf<uint8_t> &b = L_->temps[key_];
-            b.ensure(count * sizeof(T) + pad, 0);
+            const size_t need = count * sizeof(T) + pad;
+            b.ensure(b.p && b.n < need ? need + need / 2 : need, 0);
             p = reinterpret_cast<T *>(b.p);
         } else {
             own_.ensure(count, pad);

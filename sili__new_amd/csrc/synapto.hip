@@ -87,22 +87,172 @@ __global__ void k_syn_keys(int64_t Ns, const uint32_t *srow, const uint32_t *sco
         const float w = fp4_decode((uint32_t)sval[i] >> 4) * scale_at(sc, r, c);
         rc[i] = rc_key(r, c);
         absw[i] = __builtin_bit_cast(uint32_t, w) & 0x7FFFFFFFu;
-        return;
+    } else if (i - Ns < 16 * T) {
+        const int64_t s = i - Ns;
+        const int64_t t = s >> 4;
+        const uint32_t sl = (uint32_t)(s & 15), lj = sl >> 2, li = sl & 3u;
+        const uint32_t r = tbr[t] * 4u + li, c = tbc[t] * 4u + lj;
+        const uint32_t b = tiles[s];
+        if (b == 0u || r >= n_in || c >= n_out) {
+            rc[i] = KEY_NONE;
+            absw[i] = 0xFFFFFFFFu;
+        } else {
+            const float w = fp4_decode(b & 0xFu) * scale_at(sc, r, c);
+            rc[i] = rc_key(r, c);
+            absw[i] = __builtin_bit_cast(uint32_t, w) & 0x7FFFFFFFu;
+        }
     }
-    const int64_t s = i - Ns;
-    if (s >= 16 * T) return;
-    const int64_t t = s >> 4;
-    const uint32_t sl = (uint32_t)(s & 15), lj = sl >> 2, li = sl & 3u;
-    const uint32_t r = tbr[t] * 4u + li, c = tbc[t] * 4u + lj;
-    const uint32_t b = tiles[s];
-    if (b == 0u || r >= n_in || c >= n_out) {
-        rc[i] = KEY_NONE;
-        absw[i] = 0xFFFFFFFFu;
-        return;
+}
+
+// ---- radix select of the k smallest (|w| bits, row, col) ------------------
+// Histogram levels of at most 12 bits, from the top, over the 31 |w| bits of
+// the live slots fix the k-th smallest value t and how many live slots lie
+// below it; every slot below t is pruned.  Of the slots equal to t, the
+// first ones in (row, col) order are taken by a second select over their
+// (row << 32 | col) keys (unique).  The same set as a full sort by
+// (|w|, row, col) gives, without sorting every slot.
+struct SelState {
+    unsigned long long prefix;  // the high bits of the threshold fixed so far
+    unsigned long long need;    // keys still to take at or above the prefix
+    unsigned long long less;    // keys below the prefix
+    unsigned long long pad;
+};
+
+// Histogram of bits [shift, shift + width) of the keys below `limit` whose
+// bits above shift + width equal the state's prefix (level > 0).  Lanes of a
+// wave that share a bin add once (ties concentrate on one bin).
+template <typename K>
+__global__ void k_sel_hist(const K *__restrict__ keys, int64_t n, K limit, int shift, int width, int level,
+                           const SelState *__restrict__ st, uint32_t *__restrict__ hist) {
+    __shared__ uint32_t s_h[4096];
+    for (uint32_t b = threadIdx.x; b < 4096u; b += TPB) s_h[b] = 0u;
+    __syncthreads();
+    const unsigned long long prefix = level > 0 ? st->prefix : 0ull;
+    const uint32_t mask = (1u << width) - 1u, lane = threadIdx.x & 63u;
+    const int64_t stride = (int64_t)gridDim.x * TPB;
+    // every lane runs the same trip count (the wave-level ballots below)
+    const int64_t trips = (n + stride - 1) / stride;
+    for (int64_t j = 0; j < trips; ++j) {
+        const int64_t i = j * stride + (int64_t)blockIdx.x * TPB + threadIdx.x;
+        bool act = false;
+        uint32_t bin = 0;
+        if (i < n) {
+            const K v = keys[i];
+            if (v < limit && (level == 0 || ((unsigned long long)v >> (shift + width)) == prefix)) {
+                act = true;
+                bin = (uint32_t)((unsigned long long)v >> shift) & mask;
+            }
+        }
+        const uint64_t am = __ballot(act);
+        if (!am) continue;
+        const uint32_t leader = (uint32_t)__builtin_ctzll(am);
+        const uint32_t b0 = (uint32_t)__shfl((int)bin, (int)leader, 64);
+        const uint64_t same = __ballot(act && bin == b0);
+        if (same == am) {
+            if (lane == leader) atomicAdd(&s_h[b0], (uint32_t)__popcll(am));
+        } else if (act) {
+            atomicAdd(&s_h[bin], 1u);
+        }
     }
-    const float w = fp4_decode(b & 0xFu) * scale_at(sc, r, c);
-    rc[i] = rc_key(r, c);
-    absw[i] = __builtin_bit_cast(uint32_t, w) & 0x7FFFFFFFu;
+    __syncthreads();
+    for (uint32_t b = threadIdx.x; b < 4096u; b += TPB)
+        if (s_h[b]) atomicAdd(hist + b, s_h[b]);
+}
+
+// One block: the bin holding the need-th key; the state moves to it.
+__global__ __launch_bounds__(TPB) void k_sel_find(const uint32_t *__restrict__ hist, uint32_t nbins, int width,
+                                                  SelState *__restrict__ st) {
+    __shared__ unsigned long long s_part[TPB / 64];
+    const uint32_t t = threadIdx.x, per = (nbins + TPB - 1) / TPB;
+    unsigned long long mine = 0;
+    for (uint32_t j = 0; j < per; ++j) {
+        const uint32_t b = t * per + j;
+        mine += b < nbins ? hist[b] : 0u;
+    }
+    unsigned long long incl = mine;
+    for (int off = 1; off < 64; off <<= 1) {
+        const unsigned long long y = __shfl_up(incl, off, 64);
+        if ((t & 63u) >= (uint32_t)off) incl += y;
+    }
+    if ((t & 63u) == 63u) s_part[t >> 6] = incl;
+    __syncthreads();
+    unsigned long long before = incl - mine;
+    for (uint32_t w = 0; w < (t >> 6); ++w) before += s_part[w];
+    const unsigned long long need = st->need;
+    __syncthreads();
+    if (before < need && need <= before + mine) {
+        unsigned long long c = before;
+        for (uint32_t j = 0; j < per; ++j) {
+            const uint32_t b = t * per + j;
+            const uint32_t h = b < nbins ? hist[b] : 0u;
+            if (c + h >= need) {
+                st->prefix = (st->prefix << width) | b;
+                st->need = need - c;
+                st->less += c;
+                break;
+            }
+            c += h;
+        }
+    }
+}
+
+// Per slot: (below t) in the low word, (equal to t) in the high word, for
+// one scan that places both; dead slots (0xFFFFFFFF) are neither.
+__global__ void k_sel_flags(const uint32_t *__restrict__ absw, int64_t M, const SelState *__restrict__ st,
+                            uint64_t *__restrict__ flags) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i > M) return;
+    const uint32_t t = (uint32_t)st->prefix;
+    const uint32_t v = i < M ? absw[i] : 0xFFFFFFFFu;
+    flags[i] = (uint64_t)(v < t) | ((uint64_t)(v == t) << 32);
+}
+
+// Slots below t to order[] (slot order), slots at t to the tie list.
+__global__ void k_sel_scatter(const uint32_t *__restrict__ absw, const uint64_t *__restrict__ rc, int64_t M,
+                              const SelState *__restrict__ st, const uint64_t *__restrict__ pos,
+                              uint32_t *__restrict__ order, uint32_t *__restrict__ tie_idx,
+                              uint64_t *__restrict__ tie_key) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= M) return;
+    const uint32_t t = (uint32_t)st->prefix, v = absw[i];
+    const uint64_t p = pos[i];
+    if (v < t) order[(uint32_t)p] = (uint32_t)i;
+    else if (v == t) {
+        tie_idx[p >> 32] = (uint32_t)i;
+        tie_key[p >> 32] = rc[i];
+    }
+}
+
+// Ties whose key is at most the take-th smallest (flags for a scan).
+__global__ void k_sel_tie_flags(const uint64_t *__restrict__ tie_key, int64_t n, const SelState *__restrict__ st,
+                                uint32_t *__restrict__ flags) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i <= n) flags[i] = (i < n && tie_key[i] <= st->prefix) ? 1u : 0u;
+}
+__global__ void k_sel_tie_scatter(const uint32_t *__restrict__ flags, const uint32_t *__restrict__ pos,
+                                  const uint32_t *__restrict__ tie_idx, int64_t n, uint32_t *__restrict__ order) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n && flags[i]) order[pos[i]] = tie_idx[i];
+}
+
+// The live slots: the sum of the first histogram level (every live key).
+__global__ void k_hist_sum(const uint32_t *__restrict__ hist, uint32_t nbins, unsigned long long *out) {
+    __shared__ unsigned long long s_part[TPB / 64];
+    unsigned long long v = 0;
+    for (uint32_t b = threadIdx.x; b < nbins; b += TPB) v += hist[b];
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    if ((threadIdx.x & 63u) == 0u) s_part[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long t = 0;
+        for (uint32_t w = 0; w < TPB / 64; ++w) t += s_part[w];
+        *out = t;
+    }
+}
+
+__global__ void k_copy_u32(const uint32_t *__restrict__ src, int64_t n, uint32_t *__restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n) dst[i] = src[i];
 }
 
 // Explicit prune list: the slot of every (row, col) key, looked up in the
@@ -135,11 +285,6 @@ __global__ void k_tile_wkeys(const uint32_t *tbr, const uint32_t *tbc, int64_t T
                              uint64_t *tkey) {
     const int64_t t = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (t < T) tkey[t] = (uint64_t)tbr[t] * bcols + tbc[t];
-}
-
-__global__ void k_gather_u32_by(const uint32_t *src, const uint32_t *perm, int64_t n, uint32_t *dst) {
-    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
-    if (i < n) dst[i] = src[perm[i]];
 }
 
 // The k smallest: order[] lists synapse indices by (|w|, row, col).
@@ -376,12 +521,97 @@ int64_t compact_positions(Layer &L, const uint32_t *flag, uint32_t *pos, int64_t
     return (int64_t)last_pos + last_flag;
 }
 
+template <typename K>
+void sel_histogram(Layer &L, const K *keys, int64_t n, K limit, int shift, int width, int level,
+                   const SelState *state, uint32_t *hist) {
+    hipStream_t st = L.stream;
+    const unsigned hb = (unsigned)std::min<int64_t>(1024, std::max<int64_t>(1, nblk(n)));
+    launch(k_fill_u32, dim3(nblk(4096)), dim3(TPB), 0, st, hist, (int64_t)4096, 0u);
+    launch(k_sel_hist<K>, dim3(hb), dim3(TPB), 0, st, keys, n, limit, shift, width, level, state, hist);
+}
+
+// Radix select over keys[0, n) below `limit` (bits significant bits): the
+// state ends at the need-th smallest key (prefix), with `less` keys below it.
+// have_level0: hist already holds the first level's histogram.
+template <typename K>
+void radix_select(Layer &L, const K *keys, int64_t n, K limit, int bits, SelState *state, uint32_t *hist,
+                  bool have_level0 = false) {
+    hipStream_t st = L.stream;
+    int done = 0;
+    for (int level = 0; done < bits; ++level) {
+        const int width = std::min(12, bits - done);
+        const int shift = bits - done - width;
+        if (!(level == 0 && have_level0)) sel_histogram(L, keys, n, limit, shift, width, level, state, hist);
+        launch(k_sel_find, dim3(1), dim3(TPB), 0, st, (const uint32_t *)hist, (uint32_t)(1u << width), width, state);
+        done += width;
+    }
+    SILI_HIP(hipGetLastError());
+}
+
+// |w| bits of the live slots: 31 significant bits, dead slots 0xFFFFFFFF.
+constexpr int ABSW_BITS = 31;
+constexpr uint32_t ABSW_LIMIT = 0x80000000u;
+
+// order[0, k) = the k live slots smallest by (|w| bits, row, col), in no
+// particular order.  hist holds the first |w| level (count_live's).
+void select_smallest(Layer &L, const uint32_t *absw, const uint64_t *rc, int64_t M, int64_t k, int rc_bits,
+                     uint32_t *hist, uint32_t *order) {
+    hipStream_t st = L.stream;
+    TmpBuf<SelState> state(L, SILI_TMPKEY(state));
+    state.ensure(2);
+    const SelState s0{0ull, (unsigned long long)k, 0ull, 0ull};
+    SILI_HIP(hipMemcpyAsync(state.p, &s0, sizeof(s0), hipMemcpyHostToDevice, st));
+    radix_select<uint32_t>(L, absw, M, ABSW_LIMIT, ABSW_BITS, state.p, hist, true);
+    TmpBuf<uint64_t> flags(L, SILI_TMPKEY(flags)), pos(L, SILI_TMPKEY(pos));
+    flags.ensure((size_t)M + 1);
+    pos.ensure((size_t)M + 1);
+    launch(k_sel_flags, dim3(nblk(M + 1)), dim3(TPB), 0, st, absw, M, (const SelState *)state.p, flags.p);
+    SILI_HIP(hipGetLastError());
+    device_exclusive_scan_u64(L, flags.p, pos.p, M + 1);
+    SelState sf{};
+    uint64_t tot = 0;
+    SILI_HIP(hipMemcpyAsync(&sf, state.p, sizeof(SelState), hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipMemcpyAsync(&tot, pos.p + M, sizeof(uint64_t), hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipStreamSynchronize(st));
+    const int64_t less = (int64_t)(uint32_t)tot, ties = (int64_t)(tot >> 32), take = k - less;
+    if ((int64_t)sf.less != less || (int64_t)sf.need != take || take < 1 || take > ties)
+        throw_error(SILI_ERR_RUNTIME, "synapto: selection of the smallest synapses is inconsistent");
+    TmpBuf<uint32_t> tie_idx(L, SILI_TMPKEY(tie_idx)), tflag(L, SILI_TMPKEY(tflag)), tpos(L, SILI_TMPKEY(tpos));
+    TmpBuf<uint64_t> tie_key(L, SILI_TMPKEY(tie_key));
+    tie_idx.ensure((size_t)ties + 1);
+    tie_key.ensure((size_t)ties + 1);
+    launch(k_sel_scatter, dim3(nblk(M)), dim3(TPB), 0, st, absw, rc, M, (const SelState *)state.p,
+           (const uint64_t *)pos.p, order, tie_idx.p, tie_key.p);
+    SILI_HIP(hipGetLastError());
+    if (take == ties) {
+        launch(k_copy_u32, dim3(nblk(take)), dim3(TPB), 0, st, (const uint32_t *)tie_idx.p, take, order + less);
+        SILI_HIP(hipGetLastError());
+        return;
+    }
+    // the first `take` ties in (row, col) order: keys up to the take-th smallest
+    const SelState s1{0ull, (unsigned long long)take, 0ull, 0ull};
+    SILI_HIP(hipMemcpyAsync(state.p + 1, &s1, sizeof(s1), hipMemcpyHostToDevice, st));
+    radix_select<uint64_t>(L, tie_key.p, ties, ~0ull, rc_bits, state.p + 1, hist);
+    tflag.ensure((size_t)ties + 1);
+    tpos.ensure((size_t)ties + 1);
+    launch(k_sel_tie_flags, dim3(nblk(ties + 1)), dim3(TPB), 0, st, (const uint64_t *)tie_key.p, ties,
+           (const SelState *)(state.p + 1), tflag.p);
+    device_exclusive_scan_u32(L, tflag.p, tpos.p, ties + 1);
+    launch(k_sel_tie_scatter, dim3(nblk(ties)), dim3(TPB), 0, st, (const uint32_t *)tflag.p, (const uint32_t *)tpos.p,
+           (const uint32_t *)tie_idx.p, ties, order + less);
+    SILI_HIP(hipGetLastError());
+}
+
 }  // namespace
 
 void synapto_step(Layer &L, float prune_frac, const int32_t *cand_r, const int32_t *cand_c,
                   const float *cand_v, const float *cand_s, int64_t n_cand, int default_imp,
                   int64_t *stats) {
     L.out_deg_tracked = false;  // a structure of this build's own policy: counted afresh
+    // a layer that takes bulk steps keeps the step's temporaries (about 50
+    // bytes per synapse slot) instead of allocating them every step, up to
+    // 2^26 slots
+    if (L.W.nnz + 16 * L.B4.ntiles < (int64_t(1) << 26)) L.keep_temps = true;
     synapto_apply(L, prune_frac, false, nullptr, 0, cand_r, cand_c, cand_v, cand_s, n_cand, default_imp, stats);
 }
 
@@ -397,6 +627,16 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
     const int64_t n_in = L.n_in, n_out = L.n_out;
     const uint64_t bcols = (uint64_t)((n_out + 3) / 4);
     const int64_t M = Ns + 16 * T;  // synapse slots considered
+    // radix-sort widths: (row << 32 | col) keys use 32 + bits(n_in) bits and
+    // window keys bits(brows * bcols); every valid key then stays below the
+    // low bits of KEY_NONE (all ones), which still sorts last
+    auto bits_of = [](uint64_t v) {
+        int b = 1;
+        while (b < 64 && (v >> b) != 0) ++b;
+        return b;
+    };
+    const int rc_bits = 32 + bits_of((uint64_t)n_in);
+    const int win_bits = bits_of((uint64_t)((n_in + 3) / 4) * bcols);
     if (Ns + T + n_cand >= (int64_t(1) << 32) - 1 || M >= (int64_t(1) << 32) - 1)
         throw_error(SILI_ERR_RANGE, "synapto_step: layer too large for one step");
     const ScaleView sc = L.rank == 1
@@ -420,19 +660,21 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
     tins.ensure((size_t)T + 1);
     launch(k_fill_u8, dim3(nblk(T + 1)), dim3(TPB), 0, st, tins.p, T + 1, (uint8_t)0);
 
-    // -- select: order by (|w| bits, row, col) -------------------------------
+    // -- select: the k smallest by (|w| bits, row, col) ------------------------
     TmpBuf<uint64_t> rc(L, SILI_TMPKEY(rc)), rc_sorted(L, SILI_TMPKEY(rc_sorted));
-    TmpBuf<uint32_t> absw(L, SILI_TMPKEY(absw)), absw_rc(L, SILI_TMPKEY(absw_rc)), absw_sorted(L, SILI_TMPKEY(absw_sorted)), iota(L, SILI_TMPKEY(iota)), perm_rc(L, SILI_TMPKEY(perm_rc)), order(L, SILI_TMPKEY(order));
+    TmpBuf<uint32_t> absw(L, SILI_TMPKEY(absw)), iota(L, SILI_TMPKEY(iota)), perm_rc(L, SILI_TMPKEY(perm_rc)), order(L, SILI_TMPKEY(order));
     TmpBuf<unsigned long long> counters(L, SILI_TMPKEY(counters));  // live slots, demoted, grown
+    TmpBuf<uint32_t> sel_hist(L, SILI_TMPKEY(sel_hist));
     counters.ensure(4);
+    sel_hist.ensure(4096);
     rc.ensure((size_t)M + 1);
-    rc_sorted.ensure((size_t)M + 1);
     absw.ensure((size_t)M + 1);
-    absw_rc.ensure((size_t)M + 1);
-    absw_sorted.ensure((size_t)M + 1);
-    iota.ensure((size_t)M + 1);
-    perm_rc.ensure((size_t)M + 1);
     order.ensure((size_t)M + 1);
+    if (explicit_prune) {
+        rc_sorted.ensure((size_t)M + 1);
+        iota.ensure((size_t)M + 1);
+        perm_rc.ensure((size_t)M + 1);
+    }
     {
         std::vector<unsigned long long> z(4, 0ull);
         SILI_HIP(hipMemcpyAsync(counters.p, z.data(), 4 * sizeof(unsigned long long), hipMemcpyHostToDevice, st));
@@ -441,17 +683,18 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
         launch(k_syn_keys, dim3(nblk(M)), dim3(TPB), 0, st, Ns, (const uint32_t *)srow.p,
                (const uint32_t *)scol.p, (const uint8_t *)L.W.val.p, T, (const uint32_t *)tbr.p,
                (const uint32_t *)tbc.p, (const uint8_t *)L.B4.tiles.p, n_in, n_out, sc, rc.p, absw.p);
-        launch(k_iota32, dim3(nblk(M)), dim3(TPB), 0, st, iota.p, M);
-        SILI_HIP(hipGetLastError());
-        // (row, col) order, then a stable sort by |w| bits
-        device_sort_pairs_u64(L, rc.p, rc_sorted.p, iota.p, perm_rc.p, M, 64);
-        launch(k_count_live, dim3(1), dim3(64), 0, st, (const uint64_t *)rc_sorted.p, M, counters.p);
         SILI_HIP(hipGetLastError());
         if (!explicit_prune) {
-            launch(k_gather_u32_by, dim3(nblk(M)), dim3(TPB), 0, st, (const uint32_t *)absw.p,
-                   (const uint32_t *)perm_rc.p, M, absw_rc.p);
+            // the live slots: the first |w| level of the selection below
+            sel_histogram<uint32_t>(L, absw.p, M, ABSW_LIMIT, ABSW_BITS - 12, 12, 0, nullptr, sel_hist.p);
+            launch(k_hist_sum, dim3(1), dim3(TPB), 0, st, (const uint32_t *)sel_hist.p, 4096u, counters.p);
             SILI_HIP(hipGetLastError());
-            device_sort_pairs_u32(L, absw_rc.p, absw_sorted.p, perm_rc.p, order.p, M, 32);
+        } else {
+            // (row, col) order: the explicit prune keys are looked up in it
+            launch(k_iota32, dim3(nblk(M)), dim3(TPB), 0, st, iota.p, M);
+            device_sort_pairs_u64(L, rc.p, rc_sorted.p, iota.p, perm_rc.p, M, rc_bits);
+            launch(k_count_live, dim3(1), dim3(64), 0, st, (const uint64_t *)rc_sorted.p, M, counters.p);
+            SILI_HIP(hipGetLastError());
         }
     }
     const int64_t N = (int64_t)read_back(counters.p, st);  // scattered + live block4 slots
@@ -475,6 +718,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
         k = n_prune;
     } else {
         k = std::min<int64_t>(N, (int64_t)std::llround((double)prune_frac * (double)N));
+        if (k > 0) select_smallest(L, absw.p, rc.p, M, k, rc_bits, sel_hist.p, order.p);
     }
     const int64_t k_grow = explicit_prune ? n_cand : k;  // candidates that may grow
 
@@ -498,7 +742,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
                (const uint64_t *)rc.p, s_removed.p, tbytes.p, touched.p, pruned.p);
         launch(k_iota32, dim3(nblk(k)), dim3(TPB), 0, st, pruned_v.p, k);
         SILI_HIP(hipGetLastError());
-        device_sort_pairs_u64(L, pruned.p, pruned_sorted.p, pruned_v.p, pruned_vs.p, k, 64);
+        device_sort_pairs_u64(L, pruned.p, pruned_sorted.p, pruned_v.p, pruned_vs.p, k, rc_bits);
     }
 
     // -- demote --------------------------------------------------------------
@@ -532,7 +776,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
                (const uint8_t *)dem_byte.p, key2.p, byte2.p);
         launch(k_iota32, dim3(nblk(Ns + T)), dim3(TPB), 0, st, iota2.p, Ns + T);
         SILI_HIP(hipGetLastError());
-        device_sort_pairs_u64(L, key2.p, set1_sorted.p, iota2.p, perm2.p, Ns + T, 64);
+        device_sort_pairs_u64(L, key2.p, set1_sorted.p, iota2.p, perm2.p, Ns + T, rc_bits);
     }
 
     // -- candidates: first valid ones in list order ---------------------------
@@ -569,7 +813,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
         launch(k_iota32, dim3(g), dim3(TPB), 0, st, cidx.p, n_cand);
         launch(k_fill_u32, dim3(g), dim3(TPB), 0, st, first.p, n_cand, 0u);
         SILI_HIP(hipGetLastError());
-        device_sort_pairs_u64(L, ckey.p, ckey_sorted.p, cidx.p, cidx_sorted.p, n_cand, 64);
+        device_sort_pairs_u64(L, ckey.p, ckey_sorted.p, cidx.p, cidx_sorted.p, n_cand, rc_bits);
         launch(k_syn_first, dim3(g), dim3(TPB), 0, st, n_cand, (const uint64_t *)ckey_sorted.p,
                (const uint32_t *)cidx_sorted.p, first.p);
         SILI_HIP(hipGetLastError());
@@ -581,7 +825,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
                byte2.p + (Ns + T), win.p, counters.p + 2);
         launch(k_iota32, dim3(g), dim3(TPB), 0, st, wv.p, n_cand);
         SILI_HIP(hipGetLastError());
-        device_sort_pairs_u64(L, win.p, win_sorted.p, wv.p, wvs.p, n_cand, 64);
+        device_sort_pairs_u64(L, win.p, win_sorted.p, wv.p, wvs.p, n_cand, win_bits);
     }
 
     // -- final scattered set (sorted) and promotion ---------------------------
@@ -589,7 +833,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
         launch(k_iota32, dim3(nblk(M2)), dim3(TPB), 0, st, iota2.p, M2);
         launch(k_fill_u8, dim3(nblk(M2)), dim3(TPB), 0, st, removed2.p, M2, (uint8_t)0);
         SILI_HIP(hipGetLastError());
-        device_sort_pairs_u64(L, key2.p, key2_sorted.p, iota2.p, perm2.p, M2, 64);
+        device_sort_pairs_u64(L, key2.p, key2_sorted.p, iota2.p, perm2.p, M2, rc_bits);
         launch(k_gather_u8_by, dim3(nblk(M2)), dim3(TPB), 0, st, (const uint8_t *)byte2.p,
                (const uint32_t *)perm2.p, M2, byte2_sorted.p);
         SILI_HIP(hipGetLastError());
