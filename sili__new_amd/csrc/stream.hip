@@ -626,9 +626,17 @@ __global__ __launch_bounds__((NB == 8 && !XLDS) ? 512 : 1024) void k_stream(Stre
     }
 }
 
-__global__ __launch_bounds__(256) void k_fill0(float *__restrict__ p, int64_t n) {
+// Zero n floats of each of gridDim.y rows of stride ld (one launch for the
+// whole batch); float4 stores when V4 (n, ld and p multiples of 4 floats).
+template <bool V4>
+__global__ __launch_bounds__(256) void k_fill0_rows(float *__restrict__ p, int64_t n, int64_t ld) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) p[i] = 0.0f;
+    float *row = p + (int64_t)blockIdx.y * ld;
+    if constexpr (V4) {
+        if (4 * i < n) reinterpret_cast<float4 *>(row)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+        if (i < n) row[i] = 0.0f;
+    }
 }
 
 using StreamKernel = void (*)(StreamArgs);
@@ -882,8 +890,11 @@ void stream_gather(Layer &L, DScatter &s, const ScaleView &sc, const float *in, 
         throw_error(1, "stream_gather: output exceeds 2 GiB");
     {
         ProfScope ps("stream_zero", st);
-        for (int64_t b = 0; b < B; ++b)
-            launch(k_fill0, dim3((unsigned)((s.rows + 255) / 256)), dim3(256), 0, st, out + b * out_ld, s.rows);
+        const bool v4 = s.rows % 4 == 0 && out_ld % 4 == 0 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+        const int64_t per = v4 ? s.rows / 4 : s.rows;
+        const dim3 grid((unsigned)((per + 255) / 256), (unsigned)B);
+        if (v4) launch(k_fill0_rows<true>, grid, dim3(256), 0, st, out, s.rows, out_ld);
+        else launch(k_fill0_rows<false>, grid, dim3(256), 0, st, out, s.rows, out_ld);
     }
     // input staging: off when forced, forced on when forced or when column
     // blocks (made for it) or several passes are in use, else automatic
