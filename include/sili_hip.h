@@ -337,6 +337,16 @@ int sili_equalizer_step(sili_layer *layer);
 int sili_export_layout(sili_layer *layer, uint64_t *byte_start, uint64_t *byte_end, uint64_t *elem_start,
                        uint64_t *elem_end);
 
+/* No counterpart in the reference: a test hook.  Digests (FNV-1a) of the
+ * layer's internal stores -- [0] canonical scattered, [1] its shadow, [2]
+ * canonical block4 (with tile_is_sparse), [3] its shadow, [4] the shadow's
+ * entry permutation (0 when not kept), [5] the block4 shadow's tile
+ * permutation -- each over its sizes, row starts, index bytes, values or
+ * tiles, work items and split-row list.  Two layers with equal digests hold
+ * the same structure byte for byte (used to compare a row patch with a full
+ * rebuild). */
+int sili_debug_store_digest(sili_layer *layer, uint64_t digest[6]);
+
 /* ---- accumulators ------------------------------------------------------- */
 
 /* neuron_input_accum / neuron_grad_accum (sili/cpu_backend.cpp:946-951):

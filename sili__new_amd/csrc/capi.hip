@@ -1208,6 +1208,60 @@ int sili_export_scattered(sili_layer *layer, uint64_t *row_byte_start, uint64_t 
     });
 }
 
+namespace {
+// FNV-1a over bytes copied from the device
+uint64_t fnv(uint64_t h, const void *d_ptr, size_t bytes) {
+    std::vector<uint8_t> v(bytes);
+    if (bytes) SILI_HIP(hipMemcpy(v.data(), d_ptr, bytes, hipMemcpyDeviceToHost));
+    for (uint8_t b : v) h = (h ^ b) * 0x100000001B3ull;
+    return h;
+}
+uint64_t fnv_val(uint64_t h, int64_t x) {
+    for (int k = 0; k < 8; ++k) h = (h ^ (uint8_t)(x >> (8 * k))) * 0x100000001B3ull;
+    return h;
+}
+uint64_t digest_scatter(const DScatter &s) {
+    uint64_t h = 0xCBF29CE484222325ull;
+    for (int64_t x : {s.rows, s.cols, s.nnz, s.nbytes, s.nseg, s.n_empty_rows, (int64_t)s.has_split, s.n_split})
+        h = fnv_val(h, x);
+    h = fnv(h, s.byte_start.p, (size_t)(s.rows + 1) * 4);
+    h = fnv(h, s.elem_start.p, (size_t)(s.rows + 1) * 4);
+    h = fnv(h, s.idx.p, (size_t)s.nbytes);
+    h = fnv(h, s.val.p, (size_t)s.nnz);
+    h = fnv(h, s.seg.p, (size_t)s.nseg * sizeof(SegDesc));
+    if (s.n_split) h = fnv(h, s.split_rows.p, (size_t)s.n_split * 4);
+    return h;
+}
+uint64_t digest_b4(const DBlock4 &b, bool sparse) {
+    uint64_t h = 0xCBF29CE484222325ull;
+    for (int64_t x : {b.brows, b.bcols, b.ntiles, b.nbytes, b.nseg, (int64_t)b.has_split}) h = fnv_val(h, x);
+    if (!b.byte_start.p) return h;
+    h = fnv(h, b.byte_start.p, (size_t)(b.brows + 1) * 4);
+    h = fnv(h, b.tile_start.p, (size_t)(b.brows + 1) * 4);
+    h = fnv(h, b.idx.p, (size_t)b.nbytes);
+    h = fnv(h, b.tiles.p, (size_t)b.ntiles * 16);
+    h = fnv(h, b.seg.p, (size_t)b.nseg * sizeof(SegDesc));
+    if (sparse) h = fnv(h, b.sparse.p, (size_t)b.ntiles);
+    return h;
+}
+}  // namespace
+
+int sili_debug_store_digest(sili_layer *layer, uint64_t *digest) {
+    return guarded([&] {
+        if (!layer || !digest) throw_error(SILI_ERR_INVALID, "layer or digest is NULL");
+        Layer &L = layer->L;
+        set_device(L);
+        SILI_HIP(hipStreamSynchronize(L.stream));
+        digest[0] = digest_scatter(L.W);
+        digest[1] = digest_scatter(L.Wt);
+        digest[2] = digest_b4(L.B4, true);
+        digest[3] = digest_b4(L.B4t, false);
+        const uint64_t h0 = 0xCBF29CE484222325ull;
+        digest[4] = L.Wt_perm.p ? fnv(h0, L.Wt_perm.p, (size_t)L.Wt.nnz * 4) : 0;
+        digest[5] = L.B4t_perm.p ? fnv(h0, L.B4t_perm.p, (size_t)L.B4t.ntiles * 4) : 0;
+    });
+}
+
 int sili_export_block4(sili_layer *layer, int32_t *br, int32_t *bc, uint8_t *tiles, uint64_t *brow_byte_start,
                        uint64_t *brow_tile_start, uint8_t *bidx) {
     return guarded([&] {

@@ -3,10 +3,11 @@
 
 #include "common.hpp"
 
+#include <algorithm>
+#include <array>
+#include <map>
 #include <string>
 #include <unordered_map>
-
-#include <string>
 #include <utility>
 #include <vector>
 
@@ -139,6 +140,43 @@ struct DBlock4 {
     }
 };
 
+// Pinned host memory (hipHostMalloc), readable and writable by kernels: the
+// staging area of the synaptogenesis policy's small reads.  Grows, never
+// shrinks.
+struct PinBuf {
+    uint8_t *h = nullptr;
+    size_t n = 0;
+    PinBuf() = default;
+    PinBuf(const PinBuf &) = delete;
+    PinBuf &operator=(const PinBuf &) = delete;
+    ~PinBuf() { reset(); }
+    void reset() {
+        if (h) (void)hipHostFree(h);
+        h = nullptr;
+        n = 0;
+    }
+    void ensure(size_t bytes) {
+        if (h && bytes <= n) return;
+        const size_t want = std::max<size_t>(bytes + bytes / 2, 1 << 16);
+        reset();
+        SILI_HIP(hipHostMalloc(reinterpret_cast<void **>(&h), want, hipHostMallocDefault));
+        n = want;
+    }
+};
+
+// The second buffer of each array a row patch rewrites (patch.hip): the
+// patch writes the new array here, then the two swap.
+struct ScatSpare {
+    DevBuf<uint32_t> byte_start, elem_start, perm;
+    DevBuf<uint8_t> idx, val;
+    DevBuf<SegDesc> seg;
+};
+struct B4Spare {
+    DevBuf<uint32_t> byte_start, tile_start, perm;
+    DevBuf<uint8_t> idx, tiles, sparse;
+    DevBuf<SegDesc> seg;
+};
+
 // Per-kernel event timing of one layer (see ProfScope in common.hpp).
 struct Profiler {
     bool enabled = false;
@@ -252,6 +290,12 @@ struct Layer {
     int64_t eq_cursor = 0;
     uint32_t seg_len = 512;     // max index bytes per decode work item (scattered)
     uint32_t seg_len_b4 = 128;  // max block-index bytes per decode work item (block4)
+    // the policy's row patches: pinned staging (reads in, patch content out),
+    // the device copy of the patch content, and the arrays' second buffers
+    PinBuf pin_rows, pin_stage, pin_patch, pin_deg;
+    DevBuf<uint8_t> patch_blob;
+    ScatSpare sp_W, sp_Wt;
+    B4Spare sp_B4, sp_B4t;
 };
 
 // A temporary device buffer of a structure rebuild: its own allocation, or,
@@ -444,11 +488,61 @@ void synapto_step(Layer &L, float prune_frac, const int32_t *cand_r, const int32
                   const float *cand_v, const float *cand_s, int64_t n_cand, int default_imp,
                   int64_t *stats);
 // The same pipeline; explicit_prune: instead of the smallest |w|, the n_prune
-// stored synapses whose (row << 32 | col) keys prune_keys holds (host memory)
-// are removed (tiles left with < 2 live slots demoted), then every valid
-// candidate is grown (promotion as in synapto_step).
+// stored synapses whose (row << 32 | col) keys prune_keys holds (host memory;
+// with PRUNE_TILE set: the synapse's tile slot, for a synapse stored both in
+// its row and in a tile) are removed (tiles left with < 2 live slots
+// demoted), then every valid candidate is grown (promotion as in
+// synapto_step).
+constexpr uint64_t PRUNE_TILE = 1ull << 63;
 void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64_t *prune_keys, int64_t n_prune,
                    const int32_t *cand_r, const int32_t *cand_c, const float *cand_v, const float *cand_s,
                    int64_t n_cand, int default_imp, int64_t *stats);
+
+// ---- row patches for the synaptogenesis policy (patch.hip) ----------------------
+// One row of a store as staged from the device: its byte and element
+// extents, its work items [slo, shi), index bytes, element bytes (value bytes
+// or 16-byte tiles) and, when asked, flag bytes and permutation values.
+struct StagedRow {
+    uint32_t row = 0, b0 = 0, b1 = 0, e0 = 0, e1 = 0, slo = 0, shi = 0;
+    std::vector<uint8_t> idx, elems, flags;
+    std::vector<uint32_t> perm;
+};
+// A read of some rows of one store orientation: scattered (s) or block4 (b).
+struct StageReq {
+    const DScatter *s = nullptr;
+    const DBlock4 *b = nullptr;
+    const uint8_t *flags = nullptr;   // per-element flag bytes to read too (block4 canonical: tile_is_sparse)
+    const uint32_t *perm = nullptr;   // per-element permutation values to read too
+    std::vector<uint32_t> rows;       // ascending, distinct
+    std::vector<StagedRow> out;
+};
+// Every request in one round trip: the kernels write pinned memory, one sync.
+void stage_rows(Layer &L, const std::vector<StageReq *> &reqs);
+// The columns (block columns) of a staged row, from its ULEB128 deltas.
+std::vector<uint32_t> staged_cols(const StagedRow &r);
+
+// The block row a policy call edits, before and after: its scattered rows
+// (col, value byte), ascending, and its tiles (block column -> 16 bytes, slot
+// lj*4+li, byte (imp<<4)|w, and the tile's tile_is_sparse).
+struct PolicyTile {
+    std::array<uint8_t, 16> b{};
+    uint8_t sparse = 0;
+    bool operator==(const PolicyTile &o) const { return b == o.b && sparse == o.sparse; }
+    bool operator!=(const PolicyTile &o) const { return !(*this == o); }
+};
+struct BlockRowState {
+    uint32_t br = 0;
+    std::vector<std::pair<uint32_t, uint8_t>> rows[4];
+    std::map<uint32_t, PolicyTile> tiles;
+};
+// Rewrite the stores for block row br going from `old` to `nu`: the changed
+// canonical rows and block row, the shadow rows and block rows they touch,
+// their work items and the permutations, with the arrays of every other row
+// copied over shifted (no sort, no re-encode of unchanged rows).  w_rows: the
+// canonical rows of br as staged for `old`; b4_row: block row br as staged
+// (NULL when the layer has no block4 store yet).  Returns false, changing
+// nothing, when a patch does not apply (then rebuild instead).
+bool patch_block_row(Layer &L, const BlockRowState &old, const BlockRowState &nu,
+                     const std::vector<StagedRow> &w_rows, const StagedRow *b4_row);
 
 }  // namespace sili

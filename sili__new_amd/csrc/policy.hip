@@ -4,20 +4,23 @@
 //
 // The policy is control logic over a handful of synapses per call (one row,
 // k x k probes), so its decisions are made on the host from small reads of
-// the device store (one row's index and value bytes, one block row's tiles)
-// with the same std::sort / std::partial_sort calls, comparators and input
-// order as the reference -- its tie order is part of the result.  The edits
-// are then applied on the device by the bulk synaptogenesis pipeline in its
-// explicit-prune mode (synapto.hip), which rebuilds both stores.
+// the device store (the block row being edited, staged into pinned memory in
+// one round trip) with the same std::sort / std::partial_sort calls,
+// comparators and input order as the reference -- its tie order is part of
+// the result.
 //
 // The reference edits one synapse at a time: removals in descending column
 // order, a block4 slot removal demoting its tile as soon as fewer than 2
 // slots stay live; a later removal aimed at a slot that demotion moved to the
-// scattered store finds no tile and does nothing.  The device pipeline works
-// in phases (all removals, then demotion), so the removals are first replayed
-// here on the block row's tiles and only those the reference performs are
-// passed on.  Inserts are equivalent either way: each insert's promotion check
-// in the reference and the pipeline's one promotion pass leave the same tiles.
+// scattered store finds no tile and does nothing.  The edits here run in
+// phases (all removals, then demotion, inserts, promotion) as the bulk
+// synaptogenesis pipeline runs them (synapto.hip), so the removals are first
+// replayed on the block row's tiles and only those the reference performs
+// are kept.  Inserts are equivalent either way: each insert's promotion check
+// in the reference and one promotion pass leave the same tiles.  The block
+// row's new state is computed here and written into the stores as a row
+// patch (patch.hip); the bulk pipeline in its explicit-prune mode remains the
+// path for what a patch does not cover (and SILI_POLICY_PATCH=0).
 #include "../../include/sili_hip.h"
 #include "layer.hpp"
 
@@ -25,6 +28,7 @@
 #include <array>
 #include <map>
 #include <numeric>
+#include <set>
 #include <unordered_set>
 #include <vector>
 
@@ -69,53 +73,142 @@ uint32_t uleb_read(const uint8_t *p, size_t &pos) {
 
 float fp4_value(uint32_t code) { return fp4_decode(code & 0xFu); }
 
-// One row of the canonical scattered store: (col, (w<<4)|imp) in order.
-std::vector<std::pair<uint32_t, uint8_t>> read_row(Layer &L, int64_t r) {
-    hipStream_t st = L.stream;
-    uint32_t bs[2], es[2];
-    SILI_HIP(hipMemcpyAsync(bs, L.W.byte_start.p + r, 8, hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipMemcpyAsync(es, L.W.elem_start.p + r, 8, hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipStreamSynchronize(st));
-    std::vector<uint8_t> idx(bs[1] - bs[0] + 1), val(es[1] - es[0] + 1);
-    if (bs[1] > bs[0]) SILI_HIP(hipMemcpyAsync(idx.data(), L.W.idx.p + bs[0], bs[1] - bs[0], hipMemcpyDeviceToHost, st));
-    if (es[1] > es[0]) SILI_HIP(hipMemcpyAsync(val.data(), L.W.val.p + es[0], es[1] - es[0], hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipStreamSynchronize(st));
-    std::vector<std::pair<uint32_t, uint8_t>> out;
-    size_t pos = 0;
-    uint32_t col = 0;
-    for (uint32_t e = 0; e < es[1] - es[0]; ++e) {
-        col += uleb_read(idx.data(), pos);
-        out.push_back({col, val[e]});
-    }
+// A staged canonical row as (col, (w<<4)|imp) in order.
+std::vector<std::pair<uint32_t, uint8_t>> row_entries(const StagedRow &R) {
+    const auto cols = staged_cols(R);
+    std::vector<std::pair<uint32_t, uint8_t>> out(cols.size());
+    for (size_t k = 0; k < cols.size(); ++k) out[k] = {cols[k], R.elems[k]};
     return out;
 }
 
-// The tiles of block row br of the canonical block4 store, by block column:
-// slot lj*4+li, byte (imp<<4)|w.
-std::map<uint32_t, std::array<uint8_t, 16>> read_block_row(Layer &L, int64_t br) {
-    std::map<uint32_t, std::array<uint8_t, 16>> out;
-    if (L.B4.ntiles == 0 || br >= L.B4.brows) return out;
-    hipStream_t st = L.stream;
-    uint32_t bs[2], ts[2];
-    SILI_HIP(hipMemcpyAsync(bs, L.B4.byte_start.p + br, 8, hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipMemcpyAsync(ts, L.B4.tile_start.p + br, 8, hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipStreamSynchronize(st));
-    const uint32_t nt = ts[1] - ts[0];
-    if (nt == 0) return out;
-    std::vector<uint8_t> idx(bs[1] - bs[0] + 1), tiles((size_t)nt * 16);
-    SILI_HIP(hipMemcpyAsync(idx.data(), L.B4.idx.p + bs[0], bs[1] - bs[0], hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipMemcpyAsync(tiles.data(), L.B4.tiles.p + (size_t)ts[0] * 16, (size_t)nt * 16, hipMemcpyDeviceToHost,
-                            st));
-    SILI_HIP(hipStreamSynchronize(st));
-    size_t pos = 0;
-    uint32_t bc = 0;
-    for (uint32_t t = 0; t < nt; ++t) {
-        bc += uleb_read(idx.data(), pos);
-        std::array<uint8_t, 16> d;
-        std::copy(tiles.begin() + (size_t)t * 16, tiles.begin() + (size_t)t * 16 + 16, d.begin());
-        out[bc] = d;
+// Block row br as the policy sees it: its canonical rows (w_rows) and, when
+// the layer has its block4 store, its tiles (b4), staged in one round trip.
+struct StagedBlockRow {
+    StageReq w, b;
+    bool has_b4 = false;
+    BlockRowState state;
+};
+void stage_block_row(Layer &L, uint32_t br, StagedBlockRow &S) {
+    const int64_t r0 = (int64_t)br * 4;
+    for (int64_t r = r0; r < std::min<int64_t>(r0 + 4, L.n_in); ++r) S.w.rows.push_back((uint32_t)r);
+    S.w.s = &L.W;
+    S.has_b4 = L.B4.brows > (int64_t)br && L.B4.byte_start.p != nullptr;
+    std::vector<StageReq *> reqs{&S.w};
+    if (S.has_b4) {
+        S.b.b = &L.B4;
+        S.b.flags = L.B4.sparse.p;
+        S.b.rows = {br};
+        reqs.push_back(&S.b);
     }
-    return out;
+    stage_rows(L, reqs);
+    S.state.br = br;
+    for (size_t l = 0; l < S.w.out.size(); ++l) S.state.rows[l] = row_entries(S.w.out[l]);
+    if (S.has_b4) {
+        const StagedRow &R = S.b.out[0];
+        const auto bcs = staged_cols(R);
+        for (size_t k = 0; k < bcs.size(); ++k) {
+            PolicyTile t;
+            std::copy(R.elems.begin() + k * 16, R.elems.begin() + k * 16 + 16, t.b.begin());
+            t.sparse = R.flags[k];
+            S.state.tiles[bcs[k]] = t;
+        }
+    }
+}
+
+inline uint8_t requant(uint32_t code) { return code == 8u ? 0u : (uint8_t)code; }
+
+// The block row after the bulk pipeline's explicit-prune edit
+// (synapto_apply): the removals (a scattered synapse, or with PRUNE_TILE a
+// tile slot); every touched tile left with < 2 live slots demoted, its live slot
+// becoming a scattered synapse with both nibbles requantized and swapped;
+// the inserts of row li0 (weight 0, importance fp4(score)) into a surviving
+// tile's slot, else scattered; every window that received a scattered insert
+// and holds >= 2 scattered synapses promoted into a new tile.  A tile's
+// tile_is_sparse is kept unless it received an insert or is new (then: live
+// slots <= switch_point).
+BlockRowState bulk_edit(const Layer &L, const BlockRowState &old, const std::vector<uint64_t> &prune_keys,
+                        uint32_t li0, const std::vector<uint32_t> &add_cols, const std::vector<float> &add_scores) {
+    BlockRowState s = old;
+    const int64_t r0 = (int64_t)s.br * 4;
+    const uint32_t nr = (uint32_t)std::min<int64_t>(4, L.n_in - r0);
+    auto find = [](std::vector<std::pair<uint32_t, uint8_t>> &row, uint32_t c) {
+        return std::lower_bound(row.begin(), row.end(), std::make_pair(c, (uint8_t)0),
+                                [](const std::pair<uint32_t, uint8_t> &a, const std::pair<uint32_t, uint8_t> &b) {
+                                    return a.first < b.first;
+                                });
+    };
+    auto put = [&](uint32_t li, uint32_t c, uint8_t byte) {
+        auto &row = s.rows[li];
+        auto it = find(row, c);
+        if (it != row.end() && it->first == c) it->second = byte;
+        else row.insert(it, {c, byte});
+    };
+    std::set<uint32_t> touched;
+    for (uint64_t key : prune_keys) {
+        const uint32_t li = (uint32_t)((int64_t)((key & ~PRUNE_TILE) >> 32) - r0), c = (uint32_t)(key & 0xFFFFFFFFu);
+        if (!(key & PRUNE_TILE)) {
+            auto &row = s.rows[li];
+            auto it = find(row, c);
+            if (it != row.end() && it->first == c) row.erase(it);
+            continue;
+        }
+        auto t = s.tiles.find(c / 4);
+        if (t != s.tiles.end()) {
+            t->second.b[(c % 4) * 4 + li] = 0;
+            touched.insert(c / 4);
+        }
+    }
+    for (uint32_t bc : touched) {
+        auto t = s.tiles.find(bc);
+        int live = 0;
+        for (uint8_t b : t->second.b) live += b != 0;
+        if (live >= 2) continue;
+        for (uint32_t sl = 0; sl < 16; ++sl) {
+            const uint32_t b = t->second.b[sl], li = sl & 3u, c = bc * 4 + (sl >> 2);
+            if (b == 0 || li >= nr || (int64_t)c >= L.n_out) continue;
+            put(li, c, (uint8_t)((requant(b & 0xFu) << 4) | requant(b >> 4)));
+        }
+        s.tiles.erase(t);
+    }
+    std::set<uint32_t> windows, tins;
+    for (size_t i = 0; i < add_cols.size(); ++i) {
+        const uint32_t c = add_cols[i], bc = c / 4;
+        const uint32_t ic = fp4_encode(add_scores[i]);  // the weight's code is fp4(0 / S) = 0
+        auto t = s.tiles.find(bc);
+        if (t != s.tiles.end()) {
+            t->second.b[(c % 4) * 4 + li0] = (uint8_t)(ic << 4);
+            tins.insert(bc);
+        } else {
+            put(li0, c, (uint8_t)ic);
+            windows.insert(bc);
+        }
+    }
+    for (uint32_t bc : windows) {
+        std::vector<std::pair<uint32_t, std::pair<uint32_t, uint8_t>>> found;  // (li, (c, byte))
+        for (uint32_t li = 0; li < nr; ++li)
+            for (auto it = find(s.rows[li], bc * 4); it != s.rows[li].end() && it->first < bc * 4 + 4; ++it)
+                found.push_back({li, *it});
+        if (found.size() < 2) continue;
+        PolicyTile nt;
+        for (const auto &f : found) {
+            const uint32_t c = f.second.first, b = f.second.second;
+            nt.b[(c - bc * 4) * 4 + f.first] = (uint8_t)(requant(b >> 4) | (requant(b & 0xFu) << 4));
+            auto &row = s.rows[f.first];
+            row.erase(find(row, c));
+        }
+        uint32_t live = 0;
+        for (uint8_t b : nt.b) live += b != 0;
+        nt.sparse = live <= L.switch_point ? 1 : 0;
+        s.tiles[bc] = nt;
+    }
+    for (uint32_t bc : tins) {
+        auto t = s.tiles.find(bc);
+        if (t == s.tiles.end()) continue;
+        uint32_t live = 0;
+        for (uint8_t b : t->second.b) live += b != 0;
+        t->second.sparse = live <= L.switch_point ? 1 : 0;
+    }
+    return s;
 }
 
 inline uint64_t uleb_len(uint32_t v) {
@@ -142,13 +235,10 @@ struct BlockRowSim {
     std::map<uint32_t, std::array<uint8_t, 16>> &tiles;
     Row rows[4];
 
+    // rows past n_in stay empty; every other row is set from the staged block row
     Row &row(uint32_t li) {
         Row &R = rows[li];
-        if (!R.loaded) {
-            const int64_t r = (int64_t)br * 4 + li;
-            if (r < L.n_in) set(li, read_row(L, r));
-            R.loaded = true;
-        }
+        R.loaded = true;
         return R;
     }
     void set(uint32_t li, const std::vector<std::pair<uint32_t, uint8_t>> &entries) {
@@ -238,9 +328,11 @@ void build_probes(Layer &L, int64_t k, bool per_row) {
         L.probe_nnz = 0;  // the reference zeroes the count only
         return;
     }
-    std::vector<float> acc_in(n_in), acc_grad(n_out);
-    SILI_HIP(hipMemcpyAsync(acc_in.data(), L.acc_in.p, n_in * 4, hipMemcpyDeviceToHost, L.stream));
-    SILI_HIP(hipMemcpyAsync(acc_grad.data(), L.acc_grad.p, n_out * 4, hipMemcpyDeviceToHost, L.stream));
+    L.keep_temps = true;  // a layer that runs the policy keeps its small temporaries
+    L.pin_patch.ensure((n_in + n_out) * 4);
+    const float *acc_in = reinterpret_cast<const float *>(L.pin_patch.h), *acc_grad = acc_in + n_in;
+    SILI_HIP(hipMemcpyAsync(L.pin_patch.h, L.acc_in.p, n_in * 4, hipMemcpyDeviceToHost, L.stream));
+    SILI_HIP(hipMemcpyAsync(L.pin_patch.h + n_in * 4, L.acc_grad.p, n_out * 4, hipMemcpyDeviceToHost, L.stream));
     SILI_HIP(hipStreamSynchronize(L.stream));
     const size_t kk_in = std::min((size_t)k, n_in), kk = (size_t)k;
     std::vector<size_t> in_idx(n_in);
@@ -250,10 +342,15 @@ void build_probes(Layer &L, int64_t k, bool per_row) {
     in_idx.resize(kk_in);
     std::vector<int32_t> pr, pc;
     std::vector<float> pv;
+    // the top rows' stored columns, staged in one round trip
+    StageReq q;
+    q.s = &L.W;
+    for (size_t r : in_idx) q.rows.push_back((uint32_t)r);
+    std::sort(q.rows.begin(), q.rows.end());
+    stage_rows(L, {&q});
     auto row_cols = [&](size_t r) {
-        std::vector<uint32_t> cols;
-        for (const auto &e : read_row(L, (int64_t)r)) cols.push_back(e.first);
-        return cols;
+        const size_t j = std::lower_bound(q.rows.begin(), q.rows.end(), (uint32_t)r) - q.rows.begin();
+        return staged_cols(q.out[j]);
     };
     if (!per_row) {
         const size_t kk_out = std::min(kk, n_out);
@@ -304,8 +401,11 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
     const int64_t row = cursor % L.n_in;
     cursor = (cursor + 1) % L.n_in;
     const uint32_t br = (uint32_t)(row / 4), li = (uint32_t)(row % 4);
-    const auto scat = read_row(L, row);
-    auto btiles = read_block_row(L, br);
+    StagedBlockRow SB;
+    stage_block_row(L, br, SB);
+    const auto &scat = SB.state.rows[li];
+    std::map<uint32_t, std::array<uint8_t, 16>> btiles;
+    for (const auto &t : SB.state.tiles) btiles[t.first] = t.second.b;
     std::vector<uint32_t> exist_cols;
     std::vector<float> exist_imp;
     std::vector<bool> exist_is_b4;
@@ -371,7 +471,7 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
     // time: which removals it carries out, and whether every slot a demotion
     // moves back to its row and every insert fits the row's reservation
     BlockRowSim sim{L, br, btiles, {}};
-    sim.set(li, scat);
+    for (uint32_t l = 0; l < (uint32_t)SB.w.rows.size(); ++l) sim.set(l, SB.state.rows[l]);
     std::vector<uint64_t> prune_keys;
     for (const auto &re : to_remove) {
         if (re.is_b4) {
@@ -379,7 +479,7 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
             const uint32_t s = (re.col % 4) * 4 + li;
             if (it == btiles.end() || it->second[s] == 0) continue;
             it->second[s] = 0;
-            prune_keys.push_back(((uint64_t)row << 32) | re.col);
+            prune_keys.push_back(((uint64_t)row << 32) | re.col | PRUNE_TILE);
             int live = 0;
             for (uint8_t b : it->second) live += b != 0;
             if (live < 2) {  // block4_demote_tile: the slot left goes back to its row
@@ -427,35 +527,45 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
     const int64_t n_edit = (int64_t)(to_remove.size() + add_cols.size());
     if (n_edit > 0) {
         ensure_out_deg(L, true);
-        std::vector<int32_t> ecol, edelta;
+        // the edit list in pinned memory (its copy runs with the stream; the
+        // call ends with a sync)
+        L.pin_deg.ensure((size_t)n_edit * 8);
+        int32_t *ecol = reinterpret_cast<int32_t *>(L.pin_deg.h), *edelta = ecol + n_edit;
+        int64_t k = 0;
         for (const auto &re : to_remove) {
-            ecol.push_back((int32_t)re.col);
-            edelta.push_back(-1);
+            ecol[k] = (int32_t)re.col;
+            edelta[k++] = -1;
         }
         for (uint32_t c : add_cols) {
-            ecol.push_back((int32_t)c);
-            edelta.push_back(1);
+            ecol[k] = (int32_t)c;
+            edelta[k++] = 1;
         }
-        TmpBuf<int32_t> dcol(L, SILI_TMPKEY(dcol)), ddelta(L, SILI_TMPKEY(ddelta));
-        dcol.ensure((size_t)n_edit);
-        ddelta.ensure((size_t)n_edit);
-        SILI_HIP(hipMemcpyAsync(dcol.p, ecol.data(), (size_t)n_edit * 4, hipMemcpyHostToDevice, L.stream));
-        SILI_HIP(hipMemcpyAsync(ddelta.p, edelta.data(), (size_t)n_edit * 4, hipMemcpyHostToDevice, L.stream));
-        launch(k_deg_edit, dim3(nblk(n_edit)), dim3(TPB), 0, L.stream, L.out_deg.p, (const int32_t *)dcol.p,
-               (const int32_t *)ddelta.p, n_edit);
+        TmpBuf<int32_t> dedit(L, SILI_TMPKEY(dedit));
+        dedit.ensure((size_t)n_edit * 2);
+        SILI_HIP(hipMemcpyAsync(dedit.p, ecol, (size_t)n_edit * 8, hipMemcpyHostToDevice, L.stream));
+        launch(k_deg_edit, dim3(nblk(n_edit)), dim3(TPB), 0, L.stream, L.out_deg.p, (const int32_t *)dedit.p,
+               (const int32_t *)(dedit.p + n_edit), n_edit);
         SILI_HIP(hipGetLastError());
-        SILI_HIP(hipStreamSynchronize(L.stream));
     }
     if (!prune_keys.empty() || !add_cols.empty()) {
         // the device edit: explicit removals, then the inserts (weight 0,
-        // importance = the probe score, delta_csr_memory.hpp:1234)
-        std::vector<int32_t> cr(add_cols.size(), (int32_t)row), cc(add_cols.begin(), add_cols.end());
-        std::vector<float> cv(add_cols.size(), 0.0f);
-        const bool tracked = L.out_deg_tracked;
-        synapto_apply(L, 0.0f, true, prune_keys.data(), (int64_t)prune_keys.size(), cr.data(), cc.data(), cv.data(),
-                      add_scores.data(), (int64_t)add_cols.size(), 0, nullptr);
-        L.out_deg_tracked = tracked;
+        // importance = the probe score, delta_csr_memory.hpp:1234), as a row
+        // patch of the block row, or through the bulk pipeline
+        bool done = false;
+        if (env_int("SILI_POLICY_PATCH", 1) != 0) {
+            const BlockRowState nu = bulk_edit(L, SB.state, prune_keys, li, add_cols, add_scores);
+            done = patch_block_row(L, SB.state, nu, SB.w.out, SB.has_b4 ? &SB.b.out[0] : nullptr);
+        }
+        if (!done) {
+            std::vector<int32_t> cr(add_cols.size(), (int32_t)row), cc(add_cols.begin(), add_cols.end());
+            std::vector<float> cv(add_cols.size(), 0.0f);
+            const bool tracked = L.out_deg_tracked;
+            synapto_apply(L, 0.0f, true, prune_keys.data(), (int64_t)prune_keys.size(), cr.data(), cc.data(),
+                          cv.data(), add_scores.data(), (int64_t)add_cols.size(), 0, nullptr);
+            L.out_deg_tracked = tracked;
+        }
     }
+    SILI_HIP(hipStreamSynchronize(L.stream));
     if (!no_room.empty()) {
         cursor = cursor0;
         throw_error(SILI_ERR_RUNTIME, no_room);

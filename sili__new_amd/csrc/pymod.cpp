@@ -455,6 +455,12 @@ class Layer {
         d["elem_end"] = ee;
         return d;
     }
+    // test hook: digests of the internal stores (sili_debug_store_digest)
+    py::array_t<uint64_t> _store_digest() {
+        py::array_t<uint64_t> d(6);
+        ck(sili_debug_store_digest(L_, d.mutable_data()));
+        return d;
+    }
 
     // ---- accumulators / exports -----------------------------------------------
     py::array_t<float> neuron_input_accum() {
@@ -844,6 +850,7 @@ PYBIND11_MODULE(_sili_hip, m) {
         .def("info", &Layer::info)
         .def("export_scattered", &Layer::export_scattered)
         .def("export_layout", &Layer::export_layout)
+        .def("_store_digest", &Layer::_store_digest)
         .def("export_block4", &Layer::export_block4)
         .def("decode_scattered", &Layer::decode_scattered)
         .def("build_for_index", &Layer::build_for_index, py::arg("group_size") = 16)

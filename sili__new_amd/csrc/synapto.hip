@@ -256,19 +256,23 @@ __global__ void k_copy_u32(const uint32_t *__restrict__ src, int64_t n, uint32_t
 }
 
 // Explicit prune list: the slot of every (row, col) key, looked up in the
-// (row, col)-sorted slot keys; a key that is not stored sets *missing.
+// (row, col)-sorted slot keys; a key that is not stored sets *missing.  A
+// synapse can be stored twice, in its row and in a tile slot (a tile slot
+// an update made live over a scattered synapse): PRUNE_TILE in a key picks
+// the tile slot, otherwise the scattered entry (slot indices < Ns).
 __global__ void k_find_slots(const uint64_t *keys, int64_t n, const uint64_t *rc_sorted, const uint32_t *perm,
-                             int64_t M, uint32_t *order, int *missing) {
+                             int64_t M, int64_t Ns, uint32_t *order, int *missing) {
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (i >= n) return;
-    const uint64_t key = keys[i];
-    const int64_t p = lower_bound_u64(rc_sorted, M, key);
-    if (p < M && rc_sorted[p] == key) {
-        order[i] = perm[p];
-    } else {
-        order[i] = 0u;
-        atomicOr(missing, 1);
-    }
+    const bool tile = (keys[i] & PRUNE_TILE) != 0;
+    const uint64_t key = keys[i] & ~PRUNE_TILE;
+    for (int64_t p = lower_bound_u64(rc_sorted, M, key); p < M && rc_sorted[p] == key; ++p)
+        if (((int64_t)perm[p] >= Ns) == tile) {
+            order[i] = perm[p];
+            return;
+        }
+    order[i] = 0u;
+    atomicOr(missing, 1);
 }
 
 // Number of live synapses: the KEY_NONE entries sort last.
@@ -708,7 +712,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
             L.scratch.flag.ensure(4, 0);
             SILI_HIP(hipMemsetAsync(L.scratch.flag.p, 0, 4 * sizeof(int), st));
             launch(k_find_slots, dim3(nblk(n_prune)), dim3(TPB), 0, st, (const uint64_t *)dkeys.p, n_prune,
-                   (const uint64_t *)rc_sorted.p, (const uint32_t *)perm_rc.p, M, order.p, L.scratch.flag.p);
+                   (const uint64_t *)rc_sorted.p, (const uint32_t *)perm_rc.p, M, Ns, order.p, L.scratch.flag.p);
             SILI_HIP(hipGetLastError());
             int missing = 0;
             SILI_HIP(hipMemcpyAsync(&missing, L.scratch.flag.p, sizeof(int), hipMemcpyDeviceToHost, st));
