@@ -509,16 +509,19 @@ def time_synap_policy(hip, wl, reps, seconds):
     cutoff, max_rw = 0.3, 200
     L.build_probes(4)
     L.synap_step(cutoff, max_rw)  # warm-up
-    times, edits = [], 0
+    times, t_probe, edits = [], [], 0
     for i in range(reps):
         n0 = L.info()["nnz_scattered"]
         t0 = time.perf_counter()
         L.build_probes(4)
+        t1 = time.perf_counter()
         L.synap_step(cutoff, max_rw)
         L.synchronize()
         times.append((time.perf_counter() - t0) * 1e3)
+        t_probe.append((t1 - t0) * 1e3)
         edits += L.info()["nnz_scattered"] != n0
     out = {"gpu_ms_median": round(float(np.median(times)), 3), "gpu_ms_min": round(min(times), 3), "reps": reps,
+           "build_probes_ms_median": round(float(np.median(t_probe)), 3),
            "cycles_that_edited": edits,
            "cycle": "build_probes(4) + synap_step(importance_cutoff 0.3, max_row_weights 200)"}
     if have_ref():

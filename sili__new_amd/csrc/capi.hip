@@ -122,7 +122,10 @@ void fill(float *p, int64_t n, float v, hipStream_t st) {
     SILI_HIP(hipGetLastError());
 }
 
-void set_device(const Layer &L) { SILI_HIP(hipSetDevice(L.device)); }
+void set_device(const Layer &L) {
+    ++L.api_calls;  // every entry point that reaches the layer's device state comes here first
+    SILI_HIP(hipSetDevice(L.device));
+}
 
 // Scratch of sili_forward_dense_noalloc (the file-scope array `scratch`):
 // host code never names the array in a kernel argument or a copy, it uses the

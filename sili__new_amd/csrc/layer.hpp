@@ -177,6 +177,35 @@ struct B4Spare {
     DevBuf<SegDesc> seg;
 };
 
+// One row of a store as staged from the device: its byte and element
+// extents, its work items [slo, shi), index bytes, element bytes (value bytes
+// or 16-byte tiles) and, when asked, flag bytes and permutation values.
+struct StagedRow {
+    uint32_t row = 0, b0 = 0, b1 = 0, e0 = 0, e1 = 0, slo = 0, shi = 0;
+    std::vector<uint8_t> idx, elems, flags;
+    std::vector<uint32_t> perm;
+};
+// A read of some rows of one store orientation: scattered (s) or block4 (b).
+struct StageReq {
+    const DScatter *s = nullptr;
+    const DBlock4 *b = nullptr;
+    const uint8_t *flags = nullptr;   // per-element flag bytes to read too (block4 canonical: tile_is_sparse)
+    const uint32_t *perm = nullptr;   // per-element permutation values to read too
+    std::vector<uint32_t> rows;       // ascending, distinct
+    std::vector<StagedRow> out;
+};
+// A block row staged ahead for the next policy call (build_probes stages the
+// block row of the synap_step cursor in its own round trip): used only when
+// that call is the layer's very next entry point (stamp: the layer's entry
+// count when staged), so nothing can have changed the stores in between.
+struct PolicyPrefetch {
+    bool valid = false;
+    uint64_t stamp = 0;
+    uint32_t br = 0;
+    StageReq w, b;
+    bool has_b4 = false;
+};
+
 // Per-kernel event timing of one layer (see ProfScope in common.hpp).
 struct Profiler {
     bool enabled = false;
@@ -293,6 +322,8 @@ struct Layer {
     // the policy's row patches: pinned staging (reads in, patch content out),
     // the device copy of the patch content, and the arrays' second buffers
     PinBuf pin_rows, pin_stage, pin_patch, pin_deg;
+    PolicyPrefetch prefetch;
+    mutable uint64_t api_calls = 0;  // entry points called on this layer (set_device counts them)
     DevBuf<uint8_t> patch_blob;
     ScatSpare sp_W, sp_Wt;
     B4Spare sp_B4, sp_B4t;
@@ -499,25 +530,11 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
                    int64_t n_cand, int default_imp, int64_t *stats);
 
 // ---- row patches for the synaptogenesis policy (patch.hip) ----------------------
-// One row of a store as staged from the device: its byte and element
-// extents, its work items [slo, shi), index bytes, element bytes (value bytes
-// or 16-byte tiles) and, when asked, flag bytes and permutation values.
-struct StagedRow {
-    uint32_t row = 0, b0 = 0, b1 = 0, e0 = 0, e1 = 0, slo = 0, shi = 0;
-    std::vector<uint8_t> idx, elems, flags;
-    std::vector<uint32_t> perm;
-};
-// A read of some rows of one store orientation: scattered (s) or block4 (b).
-struct StageReq {
-    const DScatter *s = nullptr;
-    const DBlock4 *b = nullptr;
-    const uint8_t *flags = nullptr;   // per-element flag bytes to read too (block4 canonical: tile_is_sparse)
-    const uint32_t *perm = nullptr;   // per-element permutation values to read too
-    std::vector<uint32_t> rows;       // ascending, distinct
-    std::vector<StagedRow> out;
-};
 // Every request in one round trip: the kernels write pinned memory, one sync.
 void stage_rows(Layer &L, const std::vector<StageReq *> &reqs);
+// acc_in (n_in) then acc_grad (n_out) in pinned memory, valid until the
+// next call that stages or patches.
+const float *stage_accumulators(Layer &L);
 // The columns (block columns) of a staged row, from its ULEB128 deltas.
 std::vector<uint32_t> staged_cols(const StagedRow &r);
 

@@ -41,21 +41,48 @@ inline unsigned nblk(int64_t n) { return (unsigned)((n + TPB - 1) / TPB); }
 // then per row its payload: index bytes, element bytes (elem_bytes each),
 // flag bytes (flags != NULL), each padded to whole words, then permutation
 // words (perm != NULL).  Nothing past the header is written when the
-// payload does not fit `cap` words.
-constexpr uint32_t STAGE_MAX_ROWS = 4096;
+// payload does not fit `cap` words.  Up to STAGE_INLINE row numbers travel
+// in the arguments; longer lists in device memory (rows).
+constexpr uint32_t STAGE_MAX_ROWS = 4096, STAGE_INLINE = 192, STAGE_TPB = 1024;
 struct StageArgs {
     const uint32_t *bstart, *estart;
     const uint8_t *idx, *elems, *flags;
     const uint32_t *perm;
     const SegDesc *seg;
-    uint32_t nseg, elem_bytes, m, pad;
+    uint32_t nseg, elem_bytes, m, nrows;
     const uint32_t *rows;
     uint32_t *out;
     uint64_t cap;
+    uint32_t inl[STAGE_INLINE];
 };
 
-__device__ __forceinline__ uint32_t seg_lower(const SegDesc *seg, uint32_t n, uint32_t row) {
-    uint32_t lo = 0, hi = n;
+// First work item of a row >= `row` (items ordered by row), by a galloping
+// search from item `g` (a row's items start near row * nseg / rows), then
+// bisection: a few dependent loads instead of log2(nseg).
+__device__ __forceinline__ uint32_t seg_lower(const SegDesc *seg, uint32_t n, uint32_t row, uint32_t g) {
+    uint32_t lo = 0, hi = n;  // the answer lies in [lo, hi]
+    if (g < n) {
+        uint32_t s = 1;
+        if (seg[g].row >= row) {
+            hi = g;
+            while (true) {
+                if (hi < s) { lo = 0; break; }
+                const uint32_t p = hi - s;
+                if (seg[p].row < row) { lo = p + 1; break; }
+                hi = p;
+                s <<= 1;
+            }
+        } else {
+            lo = g + 1;
+            while (true) {
+                const uint64_t p = (uint64_t)lo + s - 1;
+                if (p >= n) { hi = n; break; }
+                if (seg[p].row >= row) { hi = (uint32_t)p; break; }
+                lo = (uint32_t)p + 1;
+                s <<= 1;
+            }
+        }
+    }
     while (lo < hi) {
         const uint32_t mid = (lo + hi) >> 1;
         if (seg[mid].row < row) lo = mid + 1;
@@ -71,58 +98,87 @@ __device__ __forceinline__ uint32_t pack4(const uint8_t *p, uint64_t i, uint64_t
 }
 __device__ __forceinline__ uint32_t words_of(uint64_t bytes) { return (uint32_t)((bytes + 3u) / 4u); }
 
-__global__ __launch_bounds__(TPB) void k_stage_rows(StageArgs a) {
+// Rows in parallel: each thread sizes up to 4 consecutive rows, a block
+// scan places them, then each wave copies whole rows.
+__global__ __launch_bounds__(STAGE_TPB) void k_stage_rows(StageArgs a) {
     __shared__ uint32_t s_off[STAGE_MAX_ROWS + 1];
-    const uint32_t t = threadIdx.x;
-    for (uint32_t j = t; j < a.m; j += TPB) {
-        const uint32_t r = a.rows[j];
+    __shared__ uint32_t s_wave[STAGE_TPB / 64];
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    const uint32_t per = (a.m + STAGE_TPB - 1) / STAGE_TPB;  // rows per thread (<= 4)
+    uint32_t mine = 0;
+    for (uint32_t k = 0; k < per; ++k) {
+        const uint32_t j = t * per + k;
+        if (j >= a.m) break;
+        const uint32_t r = a.m <= STAGE_INLINE ? a.inl[j] : a.rows[j];
         const uint32_t b0 = a.bstart[r], b1 = a.bstart[r + 1], e0 = a.estart[r], e1 = a.estart[r + 1];
-        const uint32_t slo = seg_lower(a.seg, a.nseg, r), shi = seg_lower(a.seg, a.nseg, r + 1u);
         uint32_t *h = a.out + 1u + 6u * j;
         h[0] = b0;
         h[1] = b1;
         h[2] = e0;
         h[3] = e1;
-        h[4] = slo;
-        h[5] = shi;
+        const uint32_t g = (uint32_t)((uint64_t)r * a.nseg / max(a.nrows, 1u));
+        h[4] = seg_lower(a.seg, a.nseg, r, g);
+        h[5] = seg_lower(a.seg, a.nseg, r + 1u, h[4]);
         const uint32_t ne = e1 - e0;
-        s_off[j] = words_of(b1 - b0) + words_of((uint64_t)ne * a.elem_bytes) + (a.flags ? words_of(ne) : 0u) +
-                   (a.perm ? ne : 0u);
+        const uint32_t w = words_of(b1 - b0) + words_of((uint64_t)ne * a.elem_bytes) + (a.flags ? words_of(ne) : 0u) +
+                           (a.perm ? ne : 0u);
+        s_off[j] = w;
+        mine += w;
     }
-    __syncthreads();
-    if (t == 0) {
-        uint32_t run = 0;
-        for (uint32_t j = 0; j < a.m; ++j) {
-            const uint32_t w = s_off[j];
-            s_off[j] = run;
-            run += w;
-        }
-        s_off[a.m] = run;
-        a.out[0] = 1u + 6u * a.m + run;
+    // exclusive scan of the threads' totals
+    uint32_t incl = mine;
+    for (uint32_t o = 1; o < 64u; o <<= 1) {
+        const uint32_t y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
     }
+    if (lane == 63u) s_wave[wave] = incl;
     __syncthreads();
-    if ((uint64_t)1u + 6u * a.m + s_off[a.m] > a.cap) return;
+    uint32_t before = 0, total = 0;
+    for (uint32_t w = 0; w < STAGE_TPB / 64u; ++w) {
+        const uint32_t v = s_wave[w];
+        before += w < wave ? v : 0u;
+        total += v;
+    }
+    uint32_t run = before + incl - mine;
+    for (uint32_t k = 0; k < per; ++k) {
+        const uint32_t j = t * per + k;
+        if (j >= a.m) break;
+        const uint32_t w = s_off[j];
+        s_off[j] = run;
+        run += w;
+    }
+    if (t == 0) a.out[0] = 1u + 6u * a.m + total;
+    __syncthreads();
+    if ((uint64_t)1u + 6u * a.m + total > a.cap) return;
     uint32_t *pay = a.out + 1u + 6u * a.m;
-    for (uint32_t j = 0; j < a.m; ++j) {
-        const uint32_t r = a.rows[j];
+    for (uint32_t j = wave; j < a.m; j += STAGE_TPB / 64u) {
+        const uint32_t r = a.m <= STAGE_INLINE ? a.inl[j] : a.rows[j];
         const uint32_t b0 = a.bstart[r], b1 = a.bstart[r + 1], e0 = a.estart[r], e1 = a.estart[r + 1];
         const uint32_t ne = e1 - e0;
         uint32_t *o = pay + s_off[j];
         const uint32_t wi = words_of(b1 - b0);
-        for (uint32_t w = t; w < wi; w += TPB) o[w] = pack4(a.idx, (uint64_t)b0 + 4u * w, b1);
+        for (uint32_t w = lane; w < wi; w += 64u) o[w] = pack4(a.idx, (uint64_t)b0 + 4u * w, b1);
         o += wi;
         const uint64_t eb0 = (uint64_t)e0 * a.elem_bytes, eb1 = (uint64_t)e1 * a.elem_bytes;
         const uint32_t we = words_of(eb1 - eb0);
-        for (uint32_t w = t; w < we; w += TPB) o[w] = pack4(a.elems, eb0 + 4u * w, eb1);
+        for (uint32_t w = lane; w < we; w += 64u) o[w] = pack4(a.elems, eb0 + 4u * w, eb1);
         o += we;
         if (a.flags) {
             const uint32_t wf = words_of(ne);
-            for (uint32_t w = t; w < wf; w += TPB) o[w] = pack4(a.flags, (uint64_t)e0 + 4u * w, e1);
+            for (uint32_t w = lane; w < wf; w += 64u) o[w] = pack4(a.flags, (uint64_t)e0 + 4u * w, e1);
             o += wf;
         }
         if (a.perm)
-            for (uint32_t k = t; k < ne; k += TPB) o[k] = a.perm[e0 + k];
+            for (uint32_t k = lane; k < ne; k += 64u) o[k] = a.perm[e0 + k];
     }
+}
+
+// The activity accumulators (acc_in then acc_grad) into pinned memory.
+__global__ void k_stage_acc(const float *__restrict__ a, int64_t na, const float *__restrict__ b, int64_t nb,
+                            float *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < na) out[i] = a[i];
+    else if (i < na + nb) out[i] = b[i - na];
 }
 
 // ---- the patch kernel --------------------------------------------------------
@@ -161,9 +217,31 @@ __global__ __launch_bounds__(TPB) void k_patch_apply(const PatchPiece *__restric
     const uint64_t base = (uint64_t)(b - P.chunk0) * ce;
     const uint64_t end = min<uint64_t>(P.n, base + ce);
     if (P.mode == PM_BYTES) {
+        // whole aligned destination words from two aligned source words each
+        // (v_alignbyte); the bytes of partial words at the chunk's ends one by
+        // one (neighbouring pieces own the rest of those words)
         const uint8_t *s = reinterpret_cast<const uint8_t *>(P.src);
         uint8_t *d = reinterpret_cast<uint8_t *>(P.dst);
-        for (uint64_t i = base + threadIdx.x; i < end; i += TPB) d[i] = s[i];
+        const uint64_t dlo = P.dst + base, dhi = P.dst + end;
+        const uint64_t wlo = (dlo + 3u) & ~uint64_t(3), whi = dhi & ~uint64_t(3);
+        if (wlo >= whi) {
+            for (uint64_t i = base + threadIdx.x; i < end; i += TPB) d[i] = s[i];
+        } else {
+            const uint64_t head = wlo - dlo, tail = dhi - whi;
+            if (threadIdx.x < head) d[base + threadIdx.x] = s[base + threadIdx.x];
+            if (threadIdx.x < tail) d[(whi - P.dst) + threadIdx.x] = s[(whi - P.dst) + threadIdx.x];
+            const uint64_t nw = (whi - wlo) / 4u;
+            const uint64_t s0 = P.src + (wlo - P.dst);  // source address of the first whole word
+            const uint32_t k = (uint32_t)(s0 & 3u);
+            const uint32_t *sw = reinterpret_cast<const uint32_t *>(s0 & ~uint64_t(3));
+            uint32_t *dw = reinterpret_cast<uint32_t *>(wlo);
+            if (k == 0u) {
+                for (uint64_t i = threadIdx.x; i < nw; i += TPB) dw[i] = sw[i];
+            } else {
+                for (uint64_t i = threadIdx.x; i < nw; i += TPB)
+                    dw[i] = __builtin_amdgcn_alignbyte(sw[i + 1], sw[i], k);
+            }
+        }
     } else if (P.mode == PM_U32_ADD) {
         const uint32_t *s = reinterpret_cast<const uint32_t *>(P.src);
         uint32_t *d = reinterpret_cast<uint32_t *>(P.dst);
@@ -432,20 +510,26 @@ void stage_rows(Layer &L, const std::vector<StageReq *> &reqs) {
         if (q->rows.size() > STAGE_MAX_ROWS) throw_error(SILI_ERR_RANGE, "stage_rows: too many rows");
         nrows += q->rows.size();
     }
-    // row lists to the device (one copy), output regions in pinned memory
+    // row lists beyond STAGE_INLINE to the device (one copy), output
+    // regions in pinned memory
     std::vector<size_t> cap(reqs.size(), 0), out_off(reqs.size(), 0);
     for (int attempt = 0; attempt < 2; ++attempt) {
-        L.pin_rows.ensure((nrows + 1) * 4);
-        uint32_t *rl = reinterpret_cast<uint32_t *>(L.pin_rows.h);
         size_t k = 0;
         std::vector<size_t> row_off(reqs.size());
         for (size_t i = 0; i < reqs.size(); ++i) {
             row_off[i] = k;
-            for (uint32_t r : reqs[i]->rows) rl[k++] = r;
+            if (reqs[i]->rows.size() > STAGE_INLINE) k += reqs[i]->rows.size();
         }
         TmpBuf<uint32_t> drows(L, SILI_TMPKEY(drows));
-        drows.ensure(nrows + 1);
-        if (nrows) SILI_HIP(hipMemcpyAsync(drows.p, rl, nrows * 4, hipMemcpyHostToDevice, st));
+        if (k) {
+            L.pin_rows.ensure(k * 4);
+            uint32_t *rl = reinterpret_cast<uint32_t *>(L.pin_rows.h);
+            for (size_t i = 0; i < reqs.size(); ++i)
+                if (reqs[i]->rows.size() > STAGE_INLINE)
+                    std::copy(reqs[i]->rows.begin(), reqs[i]->rows.end(), rl + row_off[i]);
+            drows.ensure(k);
+            SILI_HIP(hipMemcpyAsync(drows.p, rl, k * 4, hipMemcpyHostToDevice, st));
+        }
         size_t total = 0;
         for (size_t i = 0; i < reqs.size(); ++i) {
             if (cap[i] == 0) {
@@ -472,6 +556,7 @@ void stage_rows(Layer &L, const std::vector<StageReq *> &reqs) {
                 a.elems = q.s->val.p;
                 a.seg = q.s->seg.p;
                 a.nseg = (uint32_t)q.s->nseg;
+                a.nrows = (uint32_t)q.s->rows;
                 a.elem_bytes = 1;
             } else {
                 a.bstart = q.b->byte_start.p;
@@ -480,16 +565,18 @@ void stage_rows(Layer &L, const std::vector<StageReq *> &reqs) {
                 a.elems = q.b->tiles.p;
                 a.seg = q.b->seg.p;
                 a.nseg = (uint32_t)q.b->nseg;
+                a.nrows = (uint32_t)q.b->brows;
                 a.elem_bytes = 16;
             }
             a.flags = q.flags;
             a.perm = q.perm;
             a.m = (uint32_t)q.rows.size();
-            a.rows = drows.p + row_off[i];
+            if (a.m <= STAGE_INLINE) std::copy(q.rows.begin(), q.rows.end(), a.inl);
+            else a.rows = drows.p + row_off[i];
             a.out = out + out_off[i];
             a.cap = cap[i];
             out[out_off[i]] = 0;
-            if (a.m) launch(k_stage_rows, dim3(1), dim3(TPB), 0, st, a);
+            if (a.m) launch(k_stage_rows, dim3(1), dim3(STAGE_TPB), 0, st, a);
         }
         SILI_HIP(hipGetLastError());
         SILI_HIP(hipStreamSynchronize(st));
@@ -543,6 +630,17 @@ void stage_rows(Layer &L, const std::vector<StageReq *> &reqs) {
         }
         return;
     }
+}
+
+const float *stage_accumulators(Layer &L) {
+    const int64_t n = L.n_in + L.n_out;
+    L.pin_patch.ensure((size_t)n * 4 + 4);
+    if (n > 0)
+        launch(k_stage_acc, dim3(nblk(n)), dim3(TPB), 0, L.stream, (const float *)L.acc_in.p, L.n_in,
+               (const float *)L.acc_grad.p, L.n_out, reinterpret_cast<float *>(L.pin_patch.h));
+    SILI_HIP(hipGetLastError());
+    SILI_HIP(hipStreamSynchronize(L.stream));
+    return reinterpret_cast<const float *>(L.pin_patch.h);
 }
 
 std::vector<uint32_t> staged_cols(const StagedRow &r) {
@@ -747,21 +845,27 @@ bool patch_block_row(Layer &L, const BlockRowState &old, const BlockRowState &nu
         return (uint32_t)(w_rows[li].e0 + row_shift[li] + (it - v.begin()));
     };
     // ---- shadow scattered rows: the columns whose (row, byte) sets differ ----------
-    std::map<uint32_t, std::vector<std::pair<uint32_t, int>>> t_edit;  // col -> (row, +byte+1 add | -1 remove)
+    std::map<uint32_t, std::vector<std::pair<uint32_t, int>>> t_edit;  // col -> (row, byte + 1 add | -1 remove)
     for (uint32_t li = 0; li < nr; ++li) {
         if (old.rows[li] == nu.rows[li]) continue;
         const uint32_t r = (uint32_t)(r0 + li);
-        std::map<uint32_t, uint8_t> a(old.rows[li].begin(), old.rows[li].end()), b(nu.rows[li].begin(), nu.rows[li].end());
-        for (const auto &e : a) {
-            auto it = b.find(e.first);
-            if (it == b.end()) t_edit[e.first].push_back({r, -1});
-            else if (it->second != e.second) {
-                t_edit[e.first].push_back({r, -1});
-                t_edit[e.first].push_back({r, (int)it->second + 1});
+        const auto &a = old.rows[li], &b = nu.rows[li];
+        size_t i = 0, k = 0;
+        while (i < a.size() || k < b.size()) {
+            if (k == b.size() || (i < a.size() && a[i].first < b[k].first)) {
+                t_edit[a[i++].first].push_back({r, -1});
+            } else if (i == a.size() || b[k].first < a[i].first) {
+                t_edit[b[k].first].push_back({r, (int)b[k].second + 1});
+                ++k;
+            } else {
+                if (a[i].second != b[k].second) {
+                    t_edit[a[i].first].push_back({r, -1});
+                    t_edit[a[i].first].push_back({r, (int)b[k].second + 1});
+                }
+                ++i;
+                ++k;
             }
         }
-        for (const auto &e : b)
-            if (!a.count(e.first)) t_edit[e.first].push_back({r, (int)e.second + 1});
     }
     // ---- block4: the block row and the block columns whose tiles differ ------------
     const bool b4_changed = has_b4 && old.tiles != nu.tiles;
@@ -840,28 +944,42 @@ bool patch_block_row(Layer &L, const BlockRowState &old, const BlockRowState &nu
         const StagedRow &S = qt.out[j];
         const uint32_t c = S.row;
         const auto cols = staged_cols(S);
-        std::map<uint32_t, std::pair<uint8_t, uint32_t>> ent;  // row -> (byte, perm)
-        for (size_t k = 0; k < cols.size(); ++k) ent[cols[k]] = {S.elems[k], keep_wperm ? S.perm[k] : 0u};
-        for (const auto &ed : t_edit[c]) {
-            if (ed.second < 0) ent.erase(ed.first);
-            else ent[ed.first] = {(uint8_t)(ed.second - 1), ~0u};
-        }
+        const auto &ed = t_edit[c];  // by row, ascending; a row's removal before its add
         NewRow R;
         R.row = c;
-        for (const auto &e : ent) {
-            const uint32_t r = e.first;
+        const uint32_t E0 = w_new.empty() ? 0u : w_old.front().e0;
+        auto emit = [&](uint32_t r, uint8_t byte, uint32_t old_perm, bool is_new) {
             R.cols.push_back(r);
-            R.elems.push_back(e.second.first);
-            if (keep_wperm) {
-                uint32_t v;
-                if (r >= r0 && r < r0 + nr) {
-                    v = new_w_index(r - (uint32_t)r0, c);
-                } else {
-                    const uint32_t o = e.second.second;
-                    const uint32_t E0 = w_new.empty() ? 0u : w_old.front().e0;
-                    v = (w_new.empty() || o < E0) ? o : (uint32_t)((int64_t)o + w_de_total);
+            R.elems.push_back(byte);
+            if (!keep_wperm) return;
+            uint32_t v;
+            if (r >= r0 && r < r0 + nr) v = new_w_index(r - (uint32_t)r0, c);
+            else if (is_new || w_new.empty() || old_perm < E0) v = old_perm;
+            else v = (uint32_t)((int64_t)old_perm + w_de_total);
+            R.perm.push_back(v);
+        };
+        size_t i = 0, e = 0;
+        while (i < cols.size() || e < ed.size()) {
+            if (e < ed.size() && (i == cols.size() || ed[e].first <= cols[i])) {
+                const uint32_t r = ed[e].first;
+                bool have = i < cols.size() && cols[i] == r;
+                uint8_t byte = have ? S.elems[i] : 0;
+                const uint32_t op = have && keep_wperm ? S.perm[i] : 0u;
+                if (have) ++i;
+                bool added = false;
+                for (; e < ed.size() && ed[e].first == r; ++e) {
+                    if (ed[e].second < 0) {
+                        have = false;
+                    } else {
+                        have = true;
+                        added = true;
+                        byte = (uint8_t)(ed[e].second - 1);
+                    }
                 }
-                R.perm.push_back(v);
+                if (have) emit(r, byte, op, added);
+            } else {
+                emit(cols[i], S.elems[i], keep_wperm ? S.perm[i] : 0u, false);
+                ++i;
             }
         }
         t_new.push_back(std::move(R));
@@ -1003,8 +1121,9 @@ bool patch_block_row(Layer &L, const BlockRowState &old, const BlockRowState &nu
         launch(k_patch_apply, dim3(chunks), dim3(TPB), 0, st,
                reinterpret_cast<const PatchPiece *>(L.patch_blob.p + pieces_off), np);
     SILI_HIP(hipGetLastError());
-    // the pinned patch content must outlive the copy
-    SILI_HIP(hipStreamSynchronize(st));
+    // No wait here: the next host write of the pinned content or the edit
+    // lists follows the next staging sync, and later work on the layer is
+    // stream-ordered behind the patch.
     // ---- swap and bookkeeping ---------------------------------------------------------------
     if (!w_new.empty()) {
         swap_store(L.W, L.sp_W, nullptr);

@@ -61,6 +61,23 @@ __global__ void k_deg_edit(int32_t *deg, const int32_t *__restrict__ cols, const
         deg[c] += 1;
     }
 }
+// The same for a short list carried in the arguments: col | 1 << 31 for a
+// removal.
+constexpr int DEG_INLINE = 256;
+struct DegEdits {
+    uint32_t n;
+    uint32_t e[DEG_INLINE];
+};
+__global__ void k_deg_edit_inl(int32_t *deg, DegEdits d) {
+    const uint32_t i = threadIdx.x;
+    if (i >= d.n) return;
+    const int32_t c = (int32_t)(d.e[i] & 0x7FFFFFFFu);
+    if (d.e[i] >> 31) {
+        if (deg[c] > 0) deg[c] -= 1;
+    } else {
+        deg[c] += 1;
+    }
+}
 
 uint32_t uleb_read(const uint8_t *p, size_t &pos) {
     uint32_t v = 0;
@@ -81,26 +98,30 @@ std::vector<std::pair<uint32_t, uint8_t>> row_entries(const StagedRow &R) {
     return out;
 }
 
-// Block row br as the policy sees it: its canonical rows (w_rows) and, when
-// the layer has its block4 store, its tiles (b4), staged in one round trip.
+// Block row br as the policy sees it: its canonical rows (w) and, when the
+// layer has its block4 store, its tiles (b), staged in one round trip.
 struct StagedBlockRow {
     StageReq w, b;
     bool has_b4 = false;
     BlockRowState state;
 };
-void stage_block_row(Layer &L, uint32_t br, StagedBlockRow &S) {
+// The staging requests for block row br.
+void block_row_requests(Layer &L, uint32_t br, StageReq &w, StageReq &b, bool &has_b4) {
     const int64_t r0 = (int64_t)br * 4;
-    for (int64_t r = r0; r < std::min<int64_t>(r0 + 4, L.n_in); ++r) S.w.rows.push_back((uint32_t)r);
-    S.w.s = &L.W;
-    S.has_b4 = L.B4.brows > (int64_t)br && L.B4.byte_start.p != nullptr;
-    std::vector<StageReq *> reqs{&S.w};
-    if (S.has_b4) {
-        S.b.b = &L.B4;
-        S.b.flags = L.B4.sparse.p;
-        S.b.rows = {br};
-        reqs.push_back(&S.b);
+    w = StageReq{};
+    b = StageReq{};
+    for (int64_t r = r0; r < std::min<int64_t>(r0 + 4, L.n_in); ++r) w.rows.push_back((uint32_t)r);
+    w.s = &L.W;
+    has_b4 = L.B4.brows > (int64_t)br && L.B4.byte_start.p != nullptr;
+    if (has_b4) {
+        b.b = &L.B4;
+        b.flags = L.B4.sparse.p;
+        b.rows = {br};
     }
-    stage_rows(L, reqs);
+}
+// Its state from the staged rows.
+void block_row_state(uint32_t br, StagedBlockRow &S) {
+    S.state = BlockRowState{};
     S.state.br = br;
     for (size_t l = 0; l < S.w.out.size(); ++l) S.state.rows[l] = row_entries(S.w.out[l]);
     if (S.has_b4) {
@@ -113,6 +134,23 @@ void stage_block_row(Layer &L, uint32_t br, StagedBlockRow &S) {
             S.state.tiles[bcs[k]] = t;
         }
     }
+}
+// Block row br for a policy call: the one build_probes staged ahead when
+// this call follows it directly, else staged now.
+void stage_block_row(Layer &L, uint32_t br, StagedBlockRow &S) {
+    PolicyPrefetch &P = L.prefetch;
+    if (P.valid && P.stamp + 1 == L.api_calls && P.br == br) {
+        S.w = std::move(P.w);
+        S.b = std::move(P.b);
+        S.has_b4 = P.has_b4;
+    } else {
+        block_row_requests(L, br, S.w, S.b, S.has_b4);
+        std::vector<StageReq *> reqs{&S.w};
+        if (S.has_b4) reqs.push_back(&S.b);
+        stage_rows(L, reqs);
+    }
+    P.valid = false;
+    block_row_state(br, S);
 }
 
 inline uint8_t requant(uint32_t code) { return code == 8u ? 0u : (uint8_t)code; }
@@ -324,16 +362,13 @@ void ensure_out_deg(Layer &L, bool mark) {
 
 void build_probes(Layer &L, int64_t k, bool per_row) {
     const size_t n_in = (size_t)L.n_in, n_out = (size_t)L.n_out;
+    L.prefetch.valid = false;
     if (n_in == 0 || n_out == 0 || k <= 0) {
         L.probe_nnz = 0;  // the reference zeroes the count only
         return;
     }
     L.keep_temps = true;  // a layer that runs the policy keeps its small temporaries
-    L.pin_patch.ensure((n_in + n_out) * 4);
-    const float *acc_in = reinterpret_cast<const float *>(L.pin_patch.h), *acc_grad = acc_in + n_in;
-    SILI_HIP(hipMemcpyAsync(L.pin_patch.h, L.acc_in.p, n_in * 4, hipMemcpyDeviceToHost, L.stream));
-    SILI_HIP(hipMemcpyAsync(L.pin_patch.h + n_in * 4, L.acc_grad.p, n_out * 4, hipMemcpyDeviceToHost, L.stream));
-    SILI_HIP(hipStreamSynchronize(L.stream));
+    const float *acc_in = stage_accumulators(L), *acc_grad = acc_in + n_in;
     const size_t kk_in = std::min((size_t)k, n_in), kk = (size_t)k;
     std::vector<size_t> in_idx(n_in);
     std::iota(in_idx.begin(), in_idx.end(), 0);
@@ -342,12 +377,21 @@ void build_probes(Layer &L, int64_t k, bool per_row) {
     in_idx.resize(kk_in);
     std::vector<int32_t> pr, pc;
     std::vector<float> pv;
-    // the top rows' stored columns, staged in one round trip
+    // the top rows' stored columns, staged in one round trip with the block
+    // row the next synap_step edits
     StageReq q;
     q.s = &L.W;
     for (size_t r : in_idx) q.rows.push_back((uint32_t)r);
     std::sort(q.rows.begin(), q.rows.end());
-    stage_rows(L, {&q});
+    PolicyPrefetch &P = L.prefetch;
+    const uint32_t next_br = (uint32_t)((L.synap_cursor % L.n_in) / 4);
+    block_row_requests(L, next_br, P.w, P.b, P.has_b4);
+    std::vector<StageReq *> reqs{&q, &P.w};
+    if (P.has_b4) reqs.push_back(&P.b);
+    stage_rows(L, reqs);
+    P.valid = true;
+    P.stamp = L.api_calls;
+    P.br = next_br;
     auto row_cols = [&](size_t r) {
         const size_t j = std::lower_bound(q.rows.begin(), q.rows.end(), (uint32_t)r) - q.rows.begin();
         return staged_cols(q.out[j]);
@@ -527,24 +571,33 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
     const int64_t n_edit = (int64_t)(to_remove.size() + add_cols.size());
     if (n_edit > 0) {
         ensure_out_deg(L, true);
-        // the edit list in pinned memory (its copy runs with the stream; the
-        // call ends with a sync)
-        L.pin_deg.ensure((size_t)n_edit * 8);
-        int32_t *ecol = reinterpret_cast<int32_t *>(L.pin_deg.h), *edelta = ecol + n_edit;
-        int64_t k = 0;
-        for (const auto &re : to_remove) {
-            ecol[k] = (int32_t)re.col;
-            edelta[k++] = -1;
+        if (n_edit <= DEG_INLINE) {
+            DegEdits d{};
+            d.n = (uint32_t)n_edit;
+            uint32_t k = 0;
+            for (const auto &re : to_remove) d.e[k++] = re.col | 0x80000000u;
+            for (uint32_t c : add_cols) d.e[k++] = c;
+            launch(k_deg_edit_inl, dim3(1), dim3(DEG_INLINE), 0, L.stream, L.out_deg.p, d);
+        } else {
+            // the edit list in pinned memory (its copy runs with the stream;
+            // the next write follows the next call's staging sync)
+            L.pin_deg.ensure((size_t)n_edit * 8);
+            int32_t *ecol = reinterpret_cast<int32_t *>(L.pin_deg.h), *edelta = ecol + n_edit;
+            int64_t k = 0;
+            for (const auto &re : to_remove) {
+                ecol[k] = (int32_t)re.col;
+                edelta[k++] = -1;
+            }
+            for (uint32_t c : add_cols) {
+                ecol[k] = (int32_t)c;
+                edelta[k++] = 1;
+            }
+            TmpBuf<int32_t> dedit(L, SILI_TMPKEY(dedit));
+            dedit.ensure((size_t)n_edit * 2);
+            SILI_HIP(hipMemcpyAsync(dedit.p, ecol, (size_t)n_edit * 8, hipMemcpyHostToDevice, L.stream));
+            launch(k_deg_edit, dim3(nblk(n_edit)), dim3(TPB), 0, L.stream, L.out_deg.p, (const int32_t *)dedit.p,
+                   (const int32_t *)(dedit.p + n_edit), n_edit);
         }
-        for (uint32_t c : add_cols) {
-            ecol[k] = (int32_t)c;
-            edelta[k++] = 1;
-        }
-        TmpBuf<int32_t> dedit(L, SILI_TMPKEY(dedit));
-        dedit.ensure((size_t)n_edit * 2);
-        SILI_HIP(hipMemcpyAsync(dedit.p, ecol, (size_t)n_edit * 8, hipMemcpyHostToDevice, L.stream));
-        launch(k_deg_edit, dim3(nblk(n_edit)), dim3(TPB), 0, L.stream, L.out_deg.p, (const int32_t *)dedit.p,
-               (const int32_t *)(dedit.p + n_edit), n_edit);
         SILI_HIP(hipGetLastError());
     }
     if (!prune_keys.empty() || !add_cols.empty()) {
@@ -565,7 +618,6 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
             L.out_deg_tracked = tracked;
         }
     }
-    SILI_HIP(hipStreamSynchronize(L.stream));
     if (!no_room.empty()) {
         cursor = cursor0;
         throw_error(SILI_ERR_RUNTIME, no_room);

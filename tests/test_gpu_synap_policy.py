@@ -123,3 +123,29 @@ def test_update_after_policy_uses_its_out_degree(hip):
         got = np.array([L.get_output_scale_k(col, 0) for col in range(n_out)], np.float32)
         assert np.array_equal(got, H.output_scale), f"step {step}: output scales"
         assert got[0] == os_[0], "column 0 (out_degree 0) takes no step"
+
+
+@pytest.mark.parametrize("patch", [True, False])
+@pytest.mark.parametrize("case", ["scattered_low", "tile_low", "both_low"])
+def test_synapse_stored_twice(hip, monkeypatch, case, patch):
+    """A synapse held both in its row and in a live tile slot: the removal
+    takes the copy the reference takes, by row patch and by the bulk
+    pipeline (pinned against the compiled reference in
+    test_synap_policy_oracle.py)."""
+    monkeypatch.setenv("SILI_POLICY_PATCH", "1" if patch else "0")
+    n_in, n_out = 4, 12
+    ptrs = np.array([0, 0, 3, 3, 3], np.int32)
+    cols = np.array([2, 5, 9], np.int32)
+    w = np.array([1.0, -1.5, 2.0], np.float32)
+    imp_s, imp_code = {"scattered_low": (0.0, 7), "tile_low": (6.0, 0), "both_low": (0.0, 1)}[case]
+    imp = np.array([6.0, imp_s, 6.0], np.float32)
+    tile = np.zeros(16, np.uint8)
+    tile[1 * 4 + 1] = (imp_code << 4) | 0x3
+    tile[2 * 4 + 1] = 0x72
+    tile[3 * 4 + 0] = 0x71
+    c = dict(n_in=n_in, n_out=n_out, ptrs=ptrs, cols=cols, w=w, imp=imp, br=np.array([0], np.int32),
+             bc=np.array([1], np.int32), tiles=tile)
+    L, H = gpu_policy_layer(hip, c), host_policy_layer(c)
+    assert_same(L, H, "load")
+    assert L.synap_row_step(1, 1.0, 30, 8, 1e-3) == H.synap_row_step(1, 1.0, 30, 8, 1e-3)[0]
+    assert_same(L, H, case)

@@ -153,3 +153,35 @@ def test_empty_row_without_probes_returns_false():
     assert H.synap_row_step(0, 0.5, 4) == (False, 1)
     assert R.synap_row_step(0, 0.5, 4) == (False, 1)
     assert_same(H, R, "empty row")
+
+
+@pytest.mark.parametrize("case", ["scattered_low", "tile_low", "both_low"])
+def test_synapse_stored_twice(case):
+    """A synapse held both in its row and in a live tile slot (a load that
+    puts a tile over a scattered synapse, or an update that makes a zero slot
+    live): each removal takes the copy its entry names, the row's or the
+    tile's (delta_csr_memory.hpp:1183-1225)."""
+    from oracle import RefLayer
+    n_in, n_out = 4, 12
+    ptrs = np.array([0, 0, 3, 3, 3], np.int32)
+    cols = np.array([2, 5, 9], np.int32)  # row 1
+    w = np.array([1.0, -1.5, 2.0], np.float32)
+    imp_s, imp_t = {"scattered_low": (0.0, 6.0), "tile_low": (6.0, 0.0), "both_low": (0.0, 0.5)}[case]
+    imp = np.array([6.0, imp_s, 6.0], np.float32)
+    tile = np.zeros(16, np.uint8)
+    imp_code = {0.0: 0, 0.5: 1, 6.0: 7}[imp_t]
+    tile[1 * 4 + 1] = (imp_code << 4) | 0x3  # (row 1, col 5): the same synapse in the tile
+    tile[2 * 4 + 1] = 0x72                   # (row 1, col 6)
+    tile[3 * 4 + 0] = 0x71                   # (row 0, col 7)
+    H = HostLayer(n_in, n_out).load_csr(ptrs, cols, w=w, imp=imp).load_tiles([0], [1], tile)
+    R = RefLayer(n_in, n_out, ptrs, cols, w, imp, blank_fraction=8.0)
+    R.put_tile(0, 1, tile)
+    H.out_deg = R.out_degree().copy()
+    did_h, nxt_h = H.synap_row_step(1, 1.0, 30, 8, 1e-3)
+    did_r, nxt_r = R.synap_row_step(1, 1.0, 30, 8, 1e-3)
+    assert did_h == did_r and nxt_h == nxt_r
+    assert_same(H, R, case)
+    r1 = H.decode_cols()[int(H.row_elem_start[1]):int(H.row_elem_start[2])]
+    slot = int(H.tiles[1 * 4 + 1])
+    assert (5 in r1) == (case == "tile_low"), case + ": the row's copy"
+    assert (slot != 0) == (case == "scattered_low"), case + ": the tile's copy"
