@@ -524,6 +524,23 @@ def time_synap_policy(hip, wl, reps, seconds):
            "build_probes_ms_median": round(float(np.median(t_probe)), 3),
            "cycles_that_edited": edits,
            "cycle": "build_probes(4) + synap_step(importance_cutoff 0.3, max_row_weights 200)"}
+    # FoldedLayer's sweep (sili/sparse_rnn.py:1206-1212): build_probes once,
+    # synap_step on every row, then the next entry point writes the edits;
+    # deferred (one flush for the sweep) and patched per call
+    def sweep():
+        t0 = time.perf_counter()
+        L.build_probes(4)
+        for _ in range(wl.n_in):
+            L.synap_step(cutoff, max_rw)
+        L.synchronize()
+        return (time.perf_counter() - t0) * 1e3
+    out["sweep_rows"] = wl.n_in
+    out["sweep_ms_deferred"] = round(min(sweep() for _ in range(2)), 2)
+    os.environ["SILI_POLICY_DEFER"] = "0"
+    try:
+        out["sweep_ms_patch_per_call"] = round(sweep(), 2)
+    finally:
+        del os.environ["SILI_POLICY_DEFER"]
     if have_ref():
         R = RefLayer(wl.n_in, wl.n_out, wl.ptrs, wl.cols, wl.q, blank_fraction=1.0)
         rt, cur = [], 0
@@ -538,6 +555,15 @@ def time_synap_policy(hip, wl, reps, seconds):
             out["reference_error"] = str(e)
         if rt:
             out["reference_ms_median"] = round(float(np.median(rt)), 4)
+            if "reference_error" not in out:
+                t0 = time.perf_counter()
+                try:
+                    R.build_probes(ai, ag, 4)
+                    for _ in range(wl.n_in):
+                        _, cur = R.synap_row_step(cur, cutoff, max_rw)
+                    out["reference_sweep_ms"] = round((time.perf_counter() - t0) * 1e3, 2)
+                except RuntimeError as e:
+                    out["reference_error"] = str(e)
         out["reference_note"] = "the reference's delta_csr_build_probes + delta_csr_synap_row_step, one host thread"
     return out
 

@@ -122,10 +122,18 @@ void fill(float *p, int64_t n, float v, hipStream_t st) {
     SILI_HIP(hipGetLastError());
 }
 
-void set_device(const Layer &L) {
-    ++L.api_calls;  // every entry point that reaches the layer's device state comes here first
+// Every entry point that reaches a layer's device state comes here first.
+// The policy's own (policy = true) leave its pending edits pending; any
+// other writes them first and ends the validity of the policy's staged rows.
+void set_device(Layer &L, bool policy = false) {
     SILI_HIP(hipSetDevice(L.device));
+    if (!policy) {
+        if (!L.policy_pending.empty()) policy_flush(L);
+        ++L.policy_epoch;
+    }
 }
+// Readers of the scales only (no store access).
+void set_device(const Layer &L) { SILI_HIP(hipSetDevice(L.device)); }
 
 // Scratch of sili_forward_dense_noalloc (the file-scope array `scratch`):
 // host code never names the array in a kernel argument or a copy, it uses the
@@ -1023,7 +1031,7 @@ int sili_backward_sparse_train(sili_layer *layer, const float *x, const int32_t 
 int sili_build_probes(sili_layer *layer, int64_t k, int per_row) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
-        set_device(layer->L);
+        set_device(layer->L, true);
         build_probes(layer->L, k, per_row != 0);
     });
 }
@@ -1047,7 +1055,7 @@ int sili_synap_row_step(sili_layer *layer, int64_t *current_row, float importanc
         if (!layer || !current_row) throw_error(SILI_ERR_INVALID, "layer or current_row is NULL");
         if (*current_row < 0 || max_row_weights < 0 || max_prune_per_step < 0)
             throw_error(SILI_ERR_INVALID, "synap_row_step: negative row, max_row_weights or max_prune_per_step");
-        set_device(layer->L);
+        set_device(layer->L, true);
         const bool r = synap_row_step(layer->L, *current_row, importance_cutoff, max_row_weights, max_prune_per_step,
                                       importance_eps);
         if (did) *did = r ? 1 : 0;
@@ -1064,7 +1072,7 @@ int sili_synap_step(sili_layer *layer, float importance_cutoff, int64_t max_row_
 int sili_get_out_degree(sili_layer *layer, int32_t *out) {
     return guarded([&] {
         if (!layer || !out) throw_error(SILI_ERR_INVALID, "layer or out is NULL");
-        set_device(layer->L);
+        set_device(layer->L, true);
         get_out_degree(layer->L, out);
     });
 }

@@ -194,16 +194,34 @@ struct StageReq {
     std::vector<uint32_t> rows;       // ascending, distinct
     std::vector<StagedRow> out;
 };
-// A block row staged ahead for the next policy call (build_probes stages the
-// block row of the synap_step cursor in its own round trip): used only when
-// that call is the layer's very next entry point (stamp: the layer's entry
-// count when staged), so nothing can have changed the stores in between.
-struct PolicyPrefetch {
-    bool valid = false;
-    uint64_t stamp = 0;
+// The block row a policy call edits, before and after: its scattered rows
+// (col, value byte), ascending, and its tiles (block column -> 16 bytes, slot
+// lj*4+li, byte (imp<<4)|w, and the tile's tile_is_sparse).
+struct PolicyTile {
+    std::array<uint8_t, 16> b{};
+    uint8_t sparse = 0;
+    bool operator==(const PolicyTile &o) const { return b == o.b && sparse == o.sparse; }
+    bool operator!=(const PolicyTile &o) const { return !(*this == o); }
+};
+struct BlockRowState {
     uint32_t br = 0;
-    StageReq w, b;
+    std::vector<std::pair<uint32_t, uint8_t>> rows[4];
+    std::map<uint32_t, PolicyTile> tiles;
+};
+// A block row as staged from the device for the policy: its canonical rows
+// and (when the layer has its block4 store) its row of tiles, with the state
+// they decode to.
+struct StagedBlock {
+    std::vector<StagedRow> w;
     bool has_b4 = false;
+    StagedRow b;
+    BlockRowState state;
+};
+// A block row the policy has edited but not yet written to the device: its
+// device version as staged, and its state now.
+struct PendingBlock {
+    StagedBlock orig;
+    BlockRowState cur;
 };
 
 // Per-kernel event timing of one layer (see ProfScope in common.hpp).
@@ -322,8 +340,13 @@ struct Layer {
     // the policy's row patches: pinned staging (reads in, patch content out),
     // the device copy of the patch content, and the arrays' second buffers
     PinBuf pin_rows, pin_stage, pin_patch, pin_deg;
-    PolicyPrefetch prefetch;
-    mutable uint64_t api_calls = 0;  // entry points called on this layer (set_device counts them)
+    // The policy's block rows: staged and unchanged (clean, valid while no
+    // other entry point has run: policy_epoch), and edited but not yet
+    // written (pending, written by policy_flush before any other entry
+    // point touches the layer).
+    std::map<uint32_t, StagedBlock> policy_clean;
+    std::map<uint32_t, PendingBlock> policy_pending;
+    uint64_t policy_epoch = 0, clean_epoch = ~0ull;
     DevBuf<uint8_t> patch_blob;
     ScatSpare sp_W, sp_Wt;
     B4Spare sp_B4, sp_B4t;
@@ -538,20 +561,6 @@ const float *stage_accumulators(Layer &L);
 // The columns (block columns) of a staged row, from its ULEB128 deltas.
 std::vector<uint32_t> staged_cols(const StagedRow &r);
 
-// The block row a policy call edits, before and after: its scattered rows
-// (col, value byte), ascending, and its tiles (block column -> 16 bytes, slot
-// lj*4+li, byte (imp<<4)|w, and the tile's tile_is_sparse).
-struct PolicyTile {
-    std::array<uint8_t, 16> b{};
-    uint8_t sparse = 0;
-    bool operator==(const PolicyTile &o) const { return b == o.b && sparse == o.sparse; }
-    bool operator!=(const PolicyTile &o) const { return !(*this == o); }
-};
-struct BlockRowState {
-    uint32_t br = 0;
-    std::vector<std::pair<uint32_t, uint8_t>> rows[4];
-    std::map<uint32_t, PolicyTile> tiles;
-};
 // Rewrite the stores for block row br going from `old` to `nu`: the changed
 // canonical rows and block row, the shadow rows and block rows they touch,
 // their work items and the permutations, with the arrays of every other row
@@ -561,5 +570,11 @@ struct BlockRowState {
 // nothing, when a patch does not apply (then rebuild instead).
 bool patch_block_row(Layer &L, const BlockRowState &old, const BlockRowState &nu,
                      const std::vector<StagedRow> &w_rows, const StagedRow *b4_row);
+// The pending edits of many block rows at once: the changed canonical rows
+// and block rows patched in, then both shadows rebuilt from the canonical
+// stores (the device sort and encode every load uses).
+void patch_blocks_rebuild_shadows(Layer &L, const std::vector<const PendingBlock *> &blocks);
+// Write every pending policy edit to the device (policy.hip).
+void policy_flush(Layer &L);
 
 }  // namespace sili

@@ -801,7 +801,86 @@ int64_t seg_bound(int64_t nseg, const std::vector<StagedRow> &old, const std::ve
     return n;
 }
 
+// Upload the patch content and pieces, check every piece against the
+// arrays it reads and the second buffers it writes, and launch the splice.
+void launch_patch(Layer &L, PatchBuilder &P, std::initializer_list<StoreArrays *> stores,
+                  std::initializer_list<uint64_t> remaps) {
+    hipStream_t st = L.stream;
+    const size_t pieces_off = (P.blob.size() + 63) & ~size_t(63);
+    const uint32_t np = (uint32_t)P.pieces.size();
+    const size_t total = pieces_off + (size_t)np * sizeof(PatchPiece);
+    L.patch_blob.ensure(total + 64);
+    const uint64_t dblob = reinterpret_cast<uint64_t>(L.patch_blob.p);
+    // remaps' map fields become device addresses
+    for (uint64_t ro : remaps) {
+        if (ro == ~0ull) continue;
+        Remap R;
+        std::memcpy(&R, P.blob.data() + ro, sizeof(R));
+        R.map += dblob;
+        std::memcpy(P.blob.data() + ro, &R, sizeof(R));
+    }
+    L.pin_patch.ensure(total);
+    std::memcpy(L.pin_patch.h, P.blob.data(), P.blob.size());
+    PatchPiece *pp = reinterpret_cast<PatchPiece *>(L.pin_patch.h + pieces_off);
+    // every piece reads inside one array (or the content) and writes inside
+    // one second buffer: checked here, before anything is launched
+    std::vector<std::pair<uint64_t, uint64_t>> srcs, dsts;  // [begin, end) bytes
+    auto add = [](std::vector<std::pair<uint64_t, uint64_t>> &v, const void *p, size_t bytes) {
+        if (p) v.push_back({reinterpret_cast<uint64_t>(p), reinterpret_cast<uint64_t>(p) + bytes});
+    };
+    for (StoreArrays *A : stores) {
+        add(srcs, A->bstart->p, A->bstart->n * 4);
+        add(srcs, A->estart->p, A->estart->n * 4);
+        add(srcs, A->idx->p, A->idx->n);
+        add(srcs, A->elems->p, A->elems->n);
+        add(srcs, A->seg->p, A->seg->n * sizeof(SegDesc));
+        if (A->flags) add(srcs, A->flags->p, A->flags->n);
+        if (A->perm) add(srcs, A->perm->p, A->perm->n * 4);
+        add(dsts, A->sp_bstart->p, A->sp_bstart->n * 4);
+        add(dsts, A->sp_estart->p, A->sp_estart->n * 4);
+        add(dsts, A->sp_idx->p, A->sp_idx->n);
+        add(dsts, A->sp_elems->p, A->sp_elems->n);
+        add(dsts, A->sp_seg->p, A->sp_seg->n * sizeof(SegDesc));
+        if (A->flags) add(dsts, A->sp_flags->p, A->sp_flags->n);
+        if (A->perm) add(dsts, A->sp_perm->p, A->sp_perm->n * 4);
+    }
+    auto inside = [](const std::vector<std::pair<uint64_t, uint64_t>> &v, uint64_t a, uint64_t b) {
+        for (const auto &r : v)
+            if (a >= r.first && b <= r.second) return true;
+        return false;
+    };
+    for (uint32_t i = 0; i < np; ++i) {
+        const PatchPiece &p = P.pieces[i].p;
+        const uint64_t es = p.mode == PM_BYTES ? 1 : p.mode == PM_SEG ? sizeof(SegDesc) : 4;
+        const bool src_ok = P.pieces[i].src_blob ? p.src + p.n * es <= P.blob.size()
+                                                 : inside(srcs, p.src, p.src + p.n * es);
+        const bool aux_ok = p.mode != PM_U32_REMAP || (P.pieces[i].aux_blob && p.aux + sizeof(Remap) <= P.blob.size());
+        if (!src_ok || !aux_ok || !inside(dsts, p.dst, p.dst + p.n * es))
+            throw_error(SILI_ERR_RUNTIME, "row patch: a piece falls outside its arrays (internal error)");
+    }
+    uint32_t chunks = 0;
+    for (uint32_t i = 0; i < np; ++i) {
+        PatchPiece p = P.pieces[i].p;
+        if (P.pieces[i].src_blob) p.src += dblob;
+        if (P.pieces[i].aux_blob) p.aux += dblob;
+        p.chunk0 = chunks;
+        chunks += (uint32_t)((p.n + chunk_elems(p.mode) - 1) / chunk_elems(p.mode));
+        pp[i] = p;
+    }
+    SILI_HIP(hipMemcpyAsync(L.patch_blob.p, L.pin_patch.h, total, hipMemcpyHostToDevice, st));
+    if (chunks > 0)
+        launch(k_patch_apply, dim3(chunks), dim3(TPB), 0, st,
+               reinterpret_cast<const PatchPiece *>(L.patch_blob.p + pieces_off), np);
+    SILI_HIP(hipGetLastError());
+}
+
+__global__ void k_copy_bytes(const uint8_t *__restrict__ src, int64_t n, uint8_t *__restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n) dst[i] = src[i];
+}
+
 }  // namespace
+
 
 bool patch_block_row(Layer &L, const BlockRowState &old, const BlockRowState &nu,
                      const std::vector<StagedRow> &w_rows, const StagedRow *b4_row) {
@@ -1054,73 +1133,7 @@ bool patch_block_row(Layer &L, const BlockRowState &old, const BlockRowState &nu
         dBt = plan_store(P, ABt, qbt.out, bt_new, b_remap);
     }
     // ---- upload and launch ----------------------------------------------------------------
-    hipStream_t st = L.stream;
-    const size_t pieces_off = (P.blob.size() + 63) & ~size_t(63);
-    const uint32_t np = (uint32_t)P.pieces.size();
-    const size_t total = pieces_off + (size_t)np * sizeof(PatchPiece);
-    L.patch_blob.ensure(total + 64);
-    const uint64_t dblob = reinterpret_cast<uint64_t>(L.patch_blob.p);
-    // remaps' map fields become device addresses
-    for (uint64_t ro : {w_remap, b_remap}) {
-        if (ro == ~0ull) continue;
-        Remap R;
-        std::memcpy(&R, P.blob.data() + ro, sizeof(R));
-        R.map += dblob;
-        std::memcpy(P.blob.data() + ro, &R, sizeof(R));
-    }
-    L.pin_patch.ensure(total);
-    std::memcpy(L.pin_patch.h, P.blob.data(), P.blob.size());
-    PatchPiece *pp = reinterpret_cast<PatchPiece *>(L.pin_patch.h + pieces_off);
-    // every piece reads inside one array (or the content) and writes inside
-    // one second buffer: checked here, before anything is launched
-    std::vector<std::pair<uint64_t, uint64_t>> srcs, dsts;  // [begin, end) bytes
-    auto add = [](std::vector<std::pair<uint64_t, uint64_t>> &v, const void *p, size_t bytes) {
-        if (p) v.push_back({reinterpret_cast<uint64_t>(p), reinterpret_cast<uint64_t>(p) + bytes});
-    };
-    for (StoreArrays *A : {&AW, &AT, &AB, &ABt}) {
-        add(srcs, A->bstart->p, A->bstart->n * 4);
-        add(srcs, A->estart->p, A->estart->n * 4);
-        add(srcs, A->idx->p, A->idx->n);
-        add(srcs, A->elems->p, A->elems->n);
-        add(srcs, A->seg->p, A->seg->n * sizeof(SegDesc));
-        if (A->flags) add(srcs, A->flags->p, A->flags->n);
-        if (A->perm) add(srcs, A->perm->p, A->perm->n * 4);
-        add(dsts, A->sp_bstart->p, A->sp_bstart->n * 4);
-        add(dsts, A->sp_estart->p, A->sp_estart->n * 4);
-        add(dsts, A->sp_idx->p, A->sp_idx->n);
-        add(dsts, A->sp_elems->p, A->sp_elems->n);
-        add(dsts, A->sp_seg->p, A->sp_seg->n * sizeof(SegDesc));
-        if (A->flags) add(dsts, A->sp_flags->p, A->sp_flags->n);
-        if (A->perm) add(dsts, A->sp_perm->p, A->sp_perm->n * 4);
-    }
-    auto inside = [](const std::vector<std::pair<uint64_t, uint64_t>> &v, uint64_t a, uint64_t b) {
-        for (const auto &r : v)
-            if (a >= r.first && b <= r.second) return true;
-        return false;
-    };
-    for (uint32_t i = 0; i < np; ++i) {
-        const PatchPiece &p = P.pieces[i].p;
-        const uint64_t es = p.mode == PM_BYTES ? 1 : p.mode == PM_SEG ? sizeof(SegDesc) : 4;
-        const bool src_ok = P.pieces[i].src_blob ? p.src + p.n * es <= P.blob.size()
-                                                 : inside(srcs, p.src, p.src + p.n * es);
-        const bool aux_ok = p.mode != PM_U32_REMAP || (P.pieces[i].aux_blob && p.aux + sizeof(Remap) <= P.blob.size());
-        if (!src_ok || !aux_ok || !inside(dsts, p.dst, p.dst + p.n * es))
-            throw_error(SILI_ERR_RUNTIME, "row patch: a piece falls outside its arrays (internal error)");
-    }
-    uint32_t chunks = 0;
-    for (uint32_t i = 0; i < np; ++i) {
-        PatchPiece p = P.pieces[i].p;
-        if (P.pieces[i].src_blob) p.src += dblob;
-        if (P.pieces[i].aux_blob) p.aux += dblob;
-        p.chunk0 = chunks;
-        chunks += (uint32_t)((p.n + chunk_elems(p.mode) - 1) / chunk_elems(p.mode));
-        pp[i] = p;
-    }
-    SILI_HIP(hipMemcpyAsync(L.patch_blob.p, L.pin_patch.h, total, hipMemcpyHostToDevice, st));
-    if (chunks > 0)
-        launch(k_patch_apply, dim3(chunks), dim3(TPB), 0, st,
-               reinterpret_cast<const PatchPiece *>(L.patch_blob.p + pieces_off), np);
-    SILI_HIP(hipGetLastError());
+    launch_patch(L, P, {&AW, &AT, &AB, &ABt}, {w_remap, b_remap});
     // No wait here: the next host write of the pinned content or the edit
     // lists follows the next staging sync, and later work on the layer is
     // stream-ordered behind the patch.
@@ -1161,6 +1174,94 @@ bool patch_block_row(Layer &L, const BlockRowState &old, const BlockRowState &nu
     // a removed or requantized weight may have been the last code 8
     if (L.has_nonfinite) refresh_nonfinite(L);
     return true;
+}
+
+void patch_blocks_rebuild_shadows(Layer &L, const std::vector<const PendingBlock *> &blocks) {
+    hipStream_t st = L.stream;
+    // canonical rows and block rows that changed, in store order
+    std::vector<StagedRow> w_old, b_old;
+    std::vector<NewRow> w_new, b_new;
+    for (const PendingBlock *pb : blocks) {
+        const BlockRowState &o = pb->orig.state, &n = pb->cur;
+        for (size_t li = 0; li < pb->orig.w.size(); ++li) {
+            if (o.rows[li] == n.rows[li]) continue;
+            NewRow R;
+            R.row = pb->orig.w[li].row;
+            for (const auto &e : n.rows[li]) {
+                R.cols.push_back(e.first);
+                R.elems.push_back(e.second);
+            }
+            w_old.push_back(pb->orig.w[li]);
+            w_new.push_back(std::move(R));
+        }
+        if (pb->orig.has_b4 && o.tiles != n.tiles) {
+            NewRow R;
+            R.row = n.br;
+            for (const auto &t : n.tiles) {
+                R.cols.push_back(t.first);
+                R.elems.insert(R.elems.end(), t.second.b.begin(), t.second.b.end());
+                R.flags.push_back(t.second.sparse);
+            }
+            b_old.push_back(pb->orig.b);
+            b_new.push_back(std::move(R));
+        } else if (!pb->orig.has_b4 && !n.tiles.empty()) {
+            throw_error(SILI_ERR_RUNTIME, "policy flush: tiles on a layer without a block4 store (internal error)");
+        }
+    }
+    if (w_new.empty() && b_new.empty()) return;
+    PatchBuilder P;
+    StoreArrays AW = arrays_of(L.W, L.sp_W, nullptr, L.seg_len);
+    StoreArrays AB = arrays_of(L.B4, L.sp_B4, true, nullptr, L.seg_len_b4);
+    StoreDelta dW, dB;
+    if (!w_new.empty()) {
+        L.sp_W.seg.ensure((size_t)seg_bound(L.W.nseg, w_old, w_new, L.seg_len) + 1);
+        dW = plan_store(P, AW, w_old, w_new, ~0ull);
+    }
+    if (!b_new.empty()) {
+        L.sp_B4.seg.ensure((size_t)seg_bound(L.B4.nseg, b_old, b_new, L.seg_len_b4) + 1);
+        dB = plan_store(P, AB, b_old, b_new, ~0ull);
+    }
+    launch_patch(L, P, {&AW, &AB}, {});
+    if (!w_new.empty()) {
+        swap_store(L.W, L.sp_W, nullptr);
+        L.W.nbytes += dW.dbytes;
+        L.W.nnz += dW.delems;
+        L.W.nseg += dW.dseg;
+        L.W.n_empty_rows += dW.dempty;
+        invalidate_derived(L.W);
+        if (dW.split_maybe_changed) refresh_split(L, L.W);
+        // the shadow (and its permutation, when kept) from the canonical store
+        DevBuf<uint32_t> rows, cols;
+        rows.ensure((size_t)L.W.nnz + 1);
+        cols.ensure((size_t)L.W.nnz + 1);
+        if (L.W.nnz > 0) decode_scattered(L, rows.p, cols.p);
+        build_shadow(L, L.W, rows.p, cols.p, L.Wt);
+    }
+    if (!b_new.empty()) {
+        swap_store(L.B4, L.sp_B4, true, nullptr);
+        L.B4.nbytes += dB.dbytes;
+        L.B4.ntiles += dB.delems;
+        L.B4.nseg += dB.dseg;
+        if (dB.split_maybe_changed) refresh_split_b4(L, L.B4);
+        // both block4 orientations (and the shadow's permutation) rebuilt
+        // from the patched canonical tiles, their flags carried along
+        const int64_t T = L.B4.ntiles;
+        DevBuf<uint32_t> br, bc;
+        DevBuf<uint8_t> tiles, flags;
+        br.ensure((size_t)T + 1);
+        bc.ensure((size_t)T + 1);
+        tiles.ensure((size_t)T * 16 + 16);
+        flags.ensure((size_t)T + 1);
+        if (T > 0) {
+            launch_decode_b4(L.B4.plan(), br.p, bc.p, st);
+            launch(k_copy_bytes, dim3(nblk(T * 16)), dim3(TPB), 0, st, (const uint8_t *)L.B4.tiles.p, T * 16, tiles.p);
+            launch(k_copy_bytes, dim3(nblk(T)), dim3(TPB), 0, st, (const uint8_t *)L.B4.sparse.p, T, flags.p);
+            SILI_HIP(hipGetLastError());
+        }
+        build_block4(L, T, br.p, bc.p, tiles.p, flags.p);
+    }
+    if (L.has_nonfinite) refresh_nonfinite(L);
+    SILI_HIP(hipStreamSynchronize(st));
 }
 
 }  // namespace sili

@@ -98,59 +98,90 @@ std::vector<std::pair<uint32_t, uint8_t>> row_entries(const StagedRow &R) {
     return out;
 }
 
-// Block row br as the policy sees it: its canonical rows (w) and, when the
-// layer has its block4 store, its tiles (b), staged in one round trip.
-struct StagedBlockRow {
-    StageReq w, b;
-    bool has_b4 = false;
-    BlockRowState state;
-};
-// The staging requests for block row br.
-void block_row_requests(Layer &L, uint32_t br, StageReq &w, StageReq &b, bool &has_b4) {
-    const int64_t r0 = (int64_t)br * 4;
-    w = StageReq{};
-    b = StageReq{};
-    for (int64_t r = r0; r < std::min<int64_t>(r0 + 4, L.n_in); ++r) w.rows.push_back((uint32_t)r);
-    w.s = &L.W;
-    has_b4 = L.B4.brows > (int64_t)br && L.B4.byte_start.p != nullptr;
-    if (has_b4) {
-        b.b = &L.B4;
-        b.flags = L.B4.sparse.p;
-        b.rows = {br};
-    }
-}
-// Its state from the staged rows.
-void block_row_state(uint32_t br, StagedBlockRow &S) {
-    S.state = BlockRowState{};
+// Block rows as the policy sees them.  A block row the policy has edited is
+// pending: its state lives here until policy_flush writes it.  Any other one
+// is read from the device, STAGE_AHEAD block rows per round trip (the next
+// calls' rows, as a sweep takes them), and kept as clean while no other
+// entry point has run on the layer (policy_epoch).
+constexpr uint32_t STAGE_AHEAD = 8;
+
+StagedBlock block_from_staged(Layer &L, uint32_t br, StageReq &w, size_t w0, size_t nw, StageReq *b, size_t bj) {
+    StagedBlock S;
     S.state.br = br;
-    for (size_t l = 0; l < S.w.out.size(); ++l) S.state.rows[l] = row_entries(S.w.out[l]);
-    if (S.has_b4) {
-        const StagedRow &R = S.b.out[0];
-        const auto bcs = staged_cols(R);
+    S.w.assign(w.out.begin() + (long)w0, w.out.begin() + (long)(w0 + nw));
+    for (size_t l = 0; l < nw; ++l) S.state.rows[l] = row_entries(S.w[l]);
+    S.has_b4 = b != nullptr;
+    if (b) {
+        S.b = b->out[bj];
+        const auto bcs = staged_cols(S.b);
         for (size_t k = 0; k < bcs.size(); ++k) {
             PolicyTile t;
-            std::copy(R.elems.begin() + k * 16, R.elems.begin() + k * 16 + 16, t.b.begin());
-            t.sparse = R.flags[k];
+            std::copy(S.b.elems.begin() + k * 16, S.b.elems.begin() + k * 16 + 16, t.b.begin());
+            t.sparse = S.b.flags[k];
             S.state.tiles[bcs[k]] = t;
         }
     }
+    (void)L;
+    return S;
 }
-// Block row br for a policy call: the one build_probes staged ahead when
-// this call follows it directly, else staged now.
-void stage_block_row(Layer &L, uint32_t br, StagedBlockRow &S) {
-    PolicyPrefetch &P = L.prefetch;
-    if (P.valid && P.stamp + 1 == L.api_calls && P.br == br) {
-        S.w = std::move(P.w);
-        S.b = std::move(P.b);
-        S.has_b4 = P.has_b4;
-    } else {
-        block_row_requests(L, br, S.w, S.b, S.has_b4);
-        std::vector<StageReq *> reqs{&S.w};
-        if (S.has_b4) reqs.push_back(&S.b);
-        stage_rows(L, reqs);
+
+// Requests staging block rows [br, br + n) that are neither pending nor
+// clean (into `brs`), added to `reqs` (w: their canonical rows, b: their
+// tiles).
+void add_block_requests(Layer &L, uint32_t br, uint32_t n, StageReq &w, StageReq &b, std::vector<uint32_t> &brs) {
+    const int64_t brows = (L.n_in + 3) / 4;
+    const bool has_b4 = L.B4.byte_start.p != nullptr && L.B4.brows == brows;
+    w.s = &L.W;
+    b.b = &L.B4;
+    b.flags = L.B4.sparse.p;
+    for (uint32_t k = 0; k < n && (int64_t)(br + k) < brows; ++k) {
+        const uint32_t q = br + k;
+        if (L.policy_pending.count(q) || L.policy_clean.count(q)) continue;
+        brs.push_back(q);
+        for (int64_t r = (int64_t)q * 4; r < std::min<int64_t>((int64_t)q * 4 + 4, L.n_in); ++r)
+            w.rows.push_back((uint32_t)r);
+        if (has_b4) b.rows.push_back(q);
     }
-    P.valid = false;
-    block_row_state(br, S);
+    (void)has_b4;
+}
+// The staged rows into clean block rows.
+void keep_clean(Layer &L, const std::vector<uint32_t> &brs, StageReq &w, StageReq &b) {
+    size_t w0 = 0;
+    for (size_t j = 0; j < brs.size(); ++j) {
+        const uint32_t q = brs[j];
+        const size_t nw = (size_t)(std::min<int64_t>((int64_t)q * 4 + 4, L.n_in) - (int64_t)q * 4);
+        L.policy_clean[q] = block_from_staged(L, q, w, w0, nw, b.rows.empty() ? nullptr : &b, j);
+        w0 += nw;
+    }
+}
+void clean_valid(Layer &L) {
+    if (L.clean_epoch != L.policy_epoch) {
+        L.policy_clean.clear();
+        L.clean_epoch = L.policy_epoch;
+    }
+}
+
+// Block row br for a policy call, and whether it is pending.
+StagedBlock &block_row(Layer &L, uint32_t br, BlockRowState *&cur) {
+    auto p = L.policy_pending.find(br);
+    if (p != L.policy_pending.end()) {
+        cur = &p->second.cur;
+        return p->second.orig;
+    }
+    clean_valid(L);
+    auto c = L.policy_clean.find(br);
+    if (c == L.policy_clean.end()) {
+        StageReq w, b;
+        std::vector<uint32_t> brs;
+        add_block_requests(L, br, STAGE_AHEAD, w, b, brs);
+        std::vector<StageReq *> reqs{&w};
+        if (!b.rows.empty()) reqs.push_back(&b);
+        stage_rows(L, reqs);
+        keep_clean(L, brs, w, b);
+        c = L.policy_clean.find(br);
+    }
+    cur = &c->second.state;
+    return c->second;
 }
 
 inline uint8_t requant(uint32_t code) { return code == 8u ? 0u : (uint8_t)code; }
@@ -362,7 +393,6 @@ void ensure_out_deg(Layer &L, bool mark) {
 
 void build_probes(Layer &L, int64_t k, bool per_row) {
     const size_t n_in = (size_t)L.n_in, n_out = (size_t)L.n_out;
-    L.prefetch.valid = false;
     if (n_in == 0 || n_out == 0 || k <= 0) {
         L.probe_nnz = 0;  // the reference zeroes the count only
         return;
@@ -377,24 +407,36 @@ void build_probes(Layer &L, int64_t k, bool per_row) {
     in_idx.resize(kk_in);
     std::vector<int32_t> pr, pc;
     std::vector<float> pv;
-    // the top rows' stored columns, staged in one round trip with the block
-    // row the next synap_step edits
-    StageReq q;
-    q.s = &L.W;
-    for (size_t r : in_idx) q.rows.push_back((uint32_t)r);
-    std::sort(q.rows.begin(), q.rows.end());
-    PolicyPrefetch &P = L.prefetch;
-    const uint32_t next_br = (uint32_t)((L.synap_cursor % L.n_in) / 4);
-    block_row_requests(L, next_br, P.w, P.b, P.has_b4);
-    std::vector<StageReq *> reqs{&q, &P.w};
-    if (P.has_b4) reqs.push_back(&P.b);
-    stage_rows(L, reqs);
-    P.valid = true;
-    P.stamp = L.api_calls;
-    P.br = next_br;
+    // the top rows' stored columns (edited block rows from their pending
+    // state), staged in one round trip with the block row the next
+    // synap_step edits
+    clean_valid(L);
+    {
+        std::set<uint32_t> want;
+        for (size_t r : in_idx) {
+            const uint32_t q = (uint32_t)(r / 4);
+            if (!L.policy_pending.count(q) && !L.policy_clean.count(q)) want.insert(q);
+        }
+        // the next synap_step's (a sweep's later calls stage theirs ahead)
+        const uint32_t next_br = (uint32_t)((L.synap_cursor % L.n_in) / 4);
+        if (!L.policy_pending.count(next_br) && !L.policy_clean.count(next_br)) want.insert(next_br);
+        StageReq w, b;
+        std::vector<uint32_t> brs;
+        for (uint32_t q : want) add_block_requests(L, q, 1, w, b, brs);
+        if (!brs.empty()) {
+            std::vector<StageReq *> reqs{&w};
+            if (!b.rows.empty()) reqs.push_back(&b);
+            stage_rows(L, reqs);
+            keep_clean(L, brs, w, b);
+        }
+    }
     auto row_cols = [&](size_t r) {
-        const size_t j = std::lower_bound(q.rows.begin(), q.rows.end(), (uint32_t)r) - q.rows.begin();
-        return staged_cols(q.out[j]);
+        const uint32_t q = (uint32_t)(r / 4);
+        auto p = L.policy_pending.find(q);
+        const BlockRowState &st = p != L.policy_pending.end() ? p->second.cur : L.policy_clean.at(q).state;
+        std::vector<uint32_t> cols;
+        for (const auto &e : st.rows[r % 4]) cols.push_back(e.first);
+        return cols;
     };
     if (!per_row) {
         const size_t kk_out = std::min(kk, n_out);
@@ -440,16 +482,22 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
                     int64_t max_prune_per_step, float importance_eps) {
     if (L.n_in == 0) return false;
     L.keep_temps = true;  // a layer that runs the policy rebuilds often: keep the rebuild's temporaries
-    if (L.lay_b.size() != (size_t)L.n_in) layout_fit(L);
+    if (L.lay_b.size() != (size_t)L.n_in) {
+        policy_flush(L);  // the reservations fit the device's rows
+        layout_fit(L);
+    }
     const int64_t cursor0 = cursor;
     const int64_t row = cursor % L.n_in;
     cursor = (cursor + 1) % L.n_in;
     const uint32_t br = (uint32_t)(row / 4), li = (uint32_t)(row % 4);
-    StagedBlockRow SB;
-    stage_block_row(L, br, SB);
-    const auto &scat = SB.state.rows[li];
+    const int patch_mode = env_int("SILI_POLICY_PATCH", 1), defer = env_int("SILI_POLICY_DEFER", 1);
+    if (!(patch_mode && defer) && !L.policy_pending.empty()) policy_flush(L);
+    BlockRowState *curp = nullptr;
+    StagedBlock &SB = block_row(L, br, curp);
+    const BlockRowState state = *curp;  // the block row as the edits find it
+    const auto &scat = state.rows[li];
     std::map<uint32_t, std::array<uint8_t, 16>> btiles;
-    for (const auto &t : SB.state.tiles) btiles[t.first] = t.second.b;
+    for (const auto &t : state.tiles) btiles[t.first] = t.second.b;
     std::vector<uint32_t> exist_cols;
     std::vector<float> exist_imp;
     std::vector<bool> exist_is_b4;
@@ -515,7 +563,7 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
     // time: which removals it carries out, and whether every slot a demotion
     // moves back to its row and every insert fits the row's reservation
     BlockRowSim sim{L, br, btiles, {}};
-    for (uint32_t l = 0; l < (uint32_t)SB.w.rows.size(); ++l) sim.set(l, SB.state.rows[l]);
+    for (uint32_t l = 0; l < (uint32_t)SB.w.size(); ++l) sim.set(l, state.rows[l]);
     std::vector<uint64_t> prune_keys;
     for (const auto &re : to_remove) {
         if (re.is_b4) {
@@ -605,9 +653,25 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
         // importance = the probe score, delta_csr_memory.hpp:1234), as a row
         // patch of the block row, or through the bulk pipeline
         bool done = false;
-        if (env_int("SILI_POLICY_PATCH", 1) != 0) {
-            const BlockRowState nu = bulk_edit(L, SB.state, prune_keys, li, add_cols, add_scores);
-            done = patch_block_row(L, SB.state, nu, SB.w.out, SB.has_b4 ? &SB.b.out[0] : nullptr);
+        if (patch_mode) {
+            BlockRowState nu = bulk_edit(L, state, prune_keys, li, add_cols, add_scores);
+            if (defer) {
+                // kept on the host until an entry point other than the policy's
+                // runs (policy_flush)
+                auto p = L.policy_pending.find(br);
+                if (p != L.policy_pending.end()) {
+                    p->second.cur = std::move(nu);
+                } else {
+                    auto c = L.policy_clean.find(br);
+                    PendingBlock pb{std::move(c->second), std::move(nu)};
+                    L.policy_clean.erase(c);
+                    L.policy_pending.emplace(br, std::move(pb));
+                }
+                done = true;
+            } else {
+                done = patch_block_row(L, state, nu, SB.w, SB.has_b4 ? &SB.b : nullptr);
+                L.policy_clean.clear();
+            }
         }
         if (!done) {
             std::vector<int32_t> cr(add_cols.size(), (int32_t)row), cc(add_cols.begin(), add_cols.end());
@@ -616,6 +680,7 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
             synapto_apply(L, 0.0f, true, prune_keys.data(), (int64_t)prune_keys.size(), cr.data(), cc.data(),
                           cv.data(), add_scores.data(), (int64_t)add_cols.size(), 0, nullptr);
             L.out_deg_tracked = tracked;
+            L.policy_clean.clear();
         }
     }
     if (!no_room.empty()) {
@@ -623,6 +688,18 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
         throw_error(SILI_ERR_RUNTIME, no_room);
     }
     return true;
+}
+
+void policy_flush(Layer &L) {
+    if (L.policy_pending.empty()) return;
+    std::vector<const PendingBlock *> v;
+    for (const auto &kv : L.policy_pending) v.push_back(&kv.second);
+    bool done = false;
+    if (v.size() == 1)
+        done = patch_block_row(L, v[0]->orig.state, v[0]->cur, v[0]->orig.w, v[0]->orig.has_b4 ? &v[0]->orig.b : nullptr);
+    if (!done) patch_blocks_rebuild_shadows(L, v);
+    L.policy_pending.clear();
+    L.policy_clean.clear();
 }
 
 void get_out_degree(Layer &L, int32_t *out) {

@@ -9,7 +9,9 @@ calls return and raise the same, and the layers compute the same.  Cases:
 promotion and demotion of tiles, rows long enough to split into several work
 items in either orientation, a layer that keeps the shadow permutation
 (after an update), and a full sweep of synap_step over every row
-(FoldedLayer's, sili/sparse_rnn.py:1206-1212)."""
+(FoldedLayer's, sili/sparse_rnn.py:1206-1212) -- compared after every call
+(each flush then writes one block row) and compared only after the sweep
+(one flush writes every block row the sweep edited)."""
 import numpy as np
 import pytest
 
@@ -117,3 +119,37 @@ def test_patch_matches_rebuild_kept_permutation(hip, monkeypatch):
 def test_patch_matches_rebuild_full_sweep(hip, monkeypatch):
     c = policy_case(90, n_in=36, n_out=50, density=0.12, tile_density=0.06)
     run_sequence(hip, monkeypatch, c, 2 * 36, 90, sweep=True)
+
+
+@pytest.mark.parametrize("case", ["tiles", "trained", "large"])
+def test_deferred_sweep_matches_rebuild(hip, monkeypatch, case):
+    """synap_step over every row with nothing else in between: the edits of
+    all block rows stay pending on the host and are written in one flush
+    (the changed canonical rows and block rows patched, both shadows rebuilt
+    from them) when another entry point runs -- here the digest.  Calls
+    return as the rebuilding layer's do; the final stores are the same."""
+    shape = {"tiles": (36, 50, 0.12, 0.06), "trained": (40, 64, 0.1, 0.05), "large": (200, 300, 0.05, 0.02)}[case]
+    n_in, n_out, density, tile_density = shape
+    c = policy_case(95, n_in=n_in, n_out=n_out, density=density, tile_density=tile_density)
+    A, B = gpu_policy_layer(hip, c), gpu_policy_layer(hip, c)
+    rng = np.random.default_rng(95)
+    if case == "trained":
+        for L in (A, B):
+            r = np.random.default_rng(96)
+            L.forward_dense(r.normal(size=(4, n_in)).astype(np.float32))
+            L.backward_dense(r.normal(size=(4, n_out)).astype(np.float32), 0.05)
+    for sweep in range(2):
+        s = int(rng.integers(0, 1 << 30))
+        for L in (A, B):
+            feed_accumulators(L, np.random.default_rng(s), n_in, n_out)
+        k = int(rng.integers(3, 9))
+        call(monkeypatch, True, A.build_probes, k)
+        call(monkeypatch, False, B.build_probes, k)
+        cutoff, max_rw, max_prune = [(0.3, 30, 4), (1.2, 8, 6)][sweep]
+        for i in range(n_in):
+            ra = call(monkeypatch, True, A.synap_step, cutoff, max_rw, max_prune, 1e-3)
+            rb = call(monkeypatch, False, B.synap_step, cutoff, max_rw, max_prune, 1e-3)
+            assert ra == rb, f"sweep {sweep} step {i}"
+        same_state(A, B, f"after sweep {sweep}")
+        x = rng.normal(size=(3, n_in)).astype(np.float32)
+        np.testing.assert_allclose(A.forward_dense(x), B.forward_dense(x), rtol=1e-6, atol=1e-6)
