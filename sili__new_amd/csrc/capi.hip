@@ -279,21 +279,84 @@ const float *to_feature_major(Layer &L, DevBuf<float> &ws, const float *x, int64
     return ws.p;
 }
 
+inline bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// The independent small tasks an entry point issues before its gathers,
+// collected and run in one launch (k_prep); a task whose shape the fused
+// kernel does not take is launched on its own at once (it is independent
+// of the others).
+struct Prep {
+    PrepTask t[PREP_MAX];
+    int n = 0;
+    hipStream_t st;
+    explicit Prep(hipStream_t s) : st(s) {}
+    bool room() const { return n < PREP_MAX; }
+    void add(int kind, const float *src, float *dst, float *acc, int64_t B, int64_t cnt, int64_t ld = 0,
+             const uint32_t *rows = nullptr, float v = 0.0f) {
+        t[n++] = PrepTask{kind, 0u, src, dst, acc, B, cnt, ld, rows, v};
+    }
+    // feature-major copy [B, n] -> [n, B] (B == 1: none), sum |.| into acc
+    const float *feature_major(DevBuf<float> &ws, const float *x, int64_t B, int64_t cols, float *acc) {
+        if (B == 1) {
+            if (acc) colabs(x, 1, cols, acc);
+            return x;
+        }
+        ws.ensure((size_t)(cols * B));
+        if (room() && B % 4 == 0 && cols % 4 == 0 && al16(x) && al16(ws.p)) add(PREP_TRANSPOSE, x, ws.p, acc, B, cols);
+        else launch_transpose(x, B, cols, ws.p, acc, st);
+        return ws.p;
+    }
+    void colabs(const float *x, int64_t B, int64_t cols, float *acc) {
+        if (room() && cols % 4 == 0 && al16(x) && al16(acc)) add(PREP_COLABS, x, nullptr, acc, B, cols);
+        else launch_colabs(x, B, cols, acc, st);
+    }
+    void rowabs(const float *xT, int64_t B, int64_t cols, float *acc) {
+        if (room()) add(PREP_ROWABS, xT, nullptr, acc, B, cols);
+        else launch_rowabs(xT, B, cols, acc, st);
+    }
+    void fill(float *p, int64_t cnt, float v) {
+        const int64_t n4 = al16(p) ? cnt / 4 : 0;
+        if (n4 > 0 && room()) {
+            add(PREP_FILL4, nullptr, p, nullptr, 0, n4, 0, nullptr, v);
+            if (cnt - 4 * n4 > 0) ::sili::fill(p + 4 * n4, cnt - 4 * n4, v, st);
+        } else {
+            ::sili::fill(p, cnt, v, st);
+        }
+    }
+    // out[b, row] = 0 for every split row (launch_zero_split_rows' rule)
+    void zero_split(const GatherPlan &p, float *out, int64_t ld, int64_t nb) {
+        if (p.nseg == 0 || nb == 0 || !p.has_split || p.n_split == 0) return;
+        if (p.n_split * 4 >= p.rows) fill(out, nb * ld, 0.0f);
+        else if (room()) add(PREP_ZERO_LIST, nullptr, out, nullptr, nb, p.n_split, ld, p.split_rows);
+        else launch_zero_split_rows(p, out, ld, nb, st);
+    }
+    void run() {
+        launch_prep(t, n, st);
+        n = 0;
+    }
+};
+
 }  // namespace
+
+// Column-block passes of a scattered gather over s, or 0 when they do not
+// apply.  SILI_COLBLOCK (read per call): 0 never, else when the gathered
+// operand is larger than 4 MiB (one XCD's L2); passes of <= SILI_COLBLOCK_MB
+// (default 2 MiB: measured on c4's down layer at batch 128, 8 passes of
+// 2 MiB beat 4 of 4 MiB and 2 of 8 MiB).
+int64_t colblock_passes(const DScatter &s, const float *in, int64_t B) {
+    const int mode = env_int("SILI_COLBLOCK", 1);
+    if (mode == 0 || s.nnz == 0 || B % 4 != 0 || B > 512 || (reinterpret_cast<uintptr_t>(in) & 15u) != 0) return 0;
+    const int64_t opbytes = s.cols * B * 4;
+    if (opbytes <= (int64_t(4) << 20) || opbytes >= (int64_t)0x80000000LL) return 0;
+    const int64_t slice = (int64_t)std::max(1, env_int("SILI_COLBLOCK_MB", 2)) << 20;
+    const int64_t K = std::min<int64_t>(16, (opbytes + slice - 1) / slice);
+    return K < 2 ? 0 : K;
+}
 
 bool gather_colblocked(Layer &L, DScatter &s, const ScaleView &sc, const float *in, int64_t B, float *out,
                        int64_t out_ld, int skip, hipStream_t st) {
-    // SILI_COLBLOCK (read per call): 0 never, else when the gathered operand
-    // is larger than 4 MiB (one XCD's L2); passes of <= SILI_COLBLOCK_MB
-    // (default 2 MiB: measured on c4's down layer at batch 128, 8 passes of
-    // 2 MiB beat 4 of 4 MiB and 2 of 8 MiB)
-    const int mode = env_int("SILI_COLBLOCK", 1);
-    if (mode == 0 || s.nnz == 0 || B % 4 != 0 || B > 512 || (reinterpret_cast<uintptr_t>(in) & 15u) != 0) return false;
-    const int64_t opbytes = s.cols * B * 4;
-    if (opbytes <= (int64_t(4) << 20) || opbytes >= (int64_t)0x80000000LL) return false;
-    const int64_t slice = (int64_t)std::max(1, env_int("SILI_COLBLOCK_MB", 2)) << 20;
-    const int64_t K = std::min<int64_t>(16, (opbytes + slice - 1) / slice);
-    if (K < 2) return false;
+    const int64_t K = colblock_passes(s, in, B);
+    if (K == 0) return false;
     const int64_t cb = (s.cols + K - 1) / K;
     if ((int64_t)s.cblk.size() != K || s.cblk_cb != cb) build_colblocks(L, s, (int)K, cb);
     for (int64_t k = 0; k < K; ++k) {
@@ -338,7 +401,9 @@ void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st
     ProfCtx pc(L, "fwd");
     if (B <= 0) throw_error(SILI_ERR_INVALID, "forward_dense: batch must be >= 1");
     if (!x || !y) throw_error(SILI_ERR_INVALID, "forward_dense: NULL buffer");
-    const float *xT = to_feature_major(L, L.ws_xT, x, B, L.n_in, nullptr, st);
+    // the input's feature-major copy and the output's zeroing in one launch
+    Prep prep(st);
+    const float *xT = prep.feature_major(L.ws_xT, x, B, L.n_in, nullptr);
     // the feature-major copy doubles as the stored forward input that
     // backward_dense reads when called without x (sili/cpu_backend.cpp:481)
     L.xT_cached_batch = B > 1 ? B : 0;
@@ -346,15 +411,15 @@ void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st
     // observable with non-finite weights, so the skip is compiled in only then
     const int skip = L.has_nonfinite ? SKIP_ZERO : SKIP_NONE;
     const ScaleView ssc = shadow_scales(L);
-    if (L.Wt.nnz == 0) {
-        fill(y, B * L.n_out, 0.0f, st);
-    } else if (stream_wanted(L.Wt, ssc, B, B, skip)) {
-        stream_gather(L, L.Wt, ssc, xT, B, y, L.n_out, st);
-    } else if (gather_colblocked(L, L.Wt, ssc, xT, B, y, L.n_out, skip, st)) {
-    } else {
-        launch_zero_split_rows(L.Wt.plan(), y, L.n_out, B, st);
-        launch_gather(L.Wt.plan(), ssc, xT, B, y, L.n_out, B, skip, st);
-    }
+    const bool str = L.Wt.nnz > 0 && stream_wanted(L.Wt, ssc, B, B, skip);
+    const bool plain = L.Wt.nnz > 0 && !str && colblock_passes(L.Wt, xT, B) == 0;
+    if (L.Wt.nnz == 0) prep.fill(y, B * L.n_out, 0.0f);
+    else if (plain) prep.zero_split(L.Wt.plan(), y, L.n_out, B);
+    prep.run();
+    if (str) stream_gather(L, L.Wt, ssc, xT, B, y, L.n_out, st);
+    else if (plain) launch_gather(L.Wt.plan(), ssc, xT, B, y, L.n_out, B, skip, st);
+    else if (L.Wt.nnz > 0 && !gather_colblocked(L, L.Wt, ssc, xT, B, y, L.n_out, skip, st))
+        throw_error(SILI_ERR_RUNTIME, "forward_dense: column-block passes did not apply (internal error)");
     if (L.B4t.ntiles > 0 && !gather_b4_colblocked(L, L.B4t, shadow_scales(L), xT, B, y, L.n_out, SKIP_NONE, st))
         launch_gather_b4(L.B4t.plan(), shadow_scales(L), xT, B, y, L.n_out, B, SKIP_NONE, st);
 }
@@ -395,6 +460,9 @@ void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float 
     if (B <= 0) throw_error(SILI_ERR_INVALID, "backward_dense: batch must be >= 1");
     if (!dy || !dx) throw_error(SILI_ERR_INVALID, "backward_dense: NULL buffer");
     const bool want_gw = gw_s || gw_b;
+    // the feature-major copies, the accumulators' sums and dx's zeroing in
+    // one launch
+    Prep prep(st);
     const float *xT = nullptr;
     if (!x) {
         if (L.xT_cached_batch != B)
@@ -402,24 +470,26 @@ void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float 
                                           "(> 1) is stored; pass x");
         xT = L.ws_xT.p;
     } else if (want_gw) {
-        xT = to_feature_major(L, L.ws_xT, x, B, L.n_in, nullptr, st);
+        xT = prep.feature_major(L.ws_xT, x, B, L.n_in, nullptr);
         L.xT_cached_batch = 0;
     }
     // accumulators always advance (linear_disldo.hpp:515-520); sum|x| rides
     // on the grad-W kernel when it runs
-    const float *gT = to_feature_major(L, L.ws_gT, dy, B, L.n_out, L.acc_grad.p, st);
+    const float *gT = prep.feature_major(L.ws_gT, dy, B, L.n_out, L.acc_grad.p);
     const bool scat = L.W.nnz > 0;
-    // sum|x| rides on the scattered grad-W kernel when that runs
+    // sum|x| rides on the scattered grad-W kernel when that runs (a copy of x
+    // made in this launch is summed from x itself)
     if (!(scat && gw_s)) {
-        if (xT) launch_rowabs(xT, B, L.n_in, L.acc_in.p, st);
-        else launch_colabs(x, B, L.n_in, L.acc_in.p, st);
+        if (xT && xT == L.ws_xT.p && x == nullptr) prep.rowabs(xT, B, L.n_in, L.acc_in.p);
+        else prep.colabs(x, B, L.n_in, L.acc_in.p);
     }
     // grad-input and grad-W read the same gT row per synapse: one fused pass
     // when grad-W is wanted; otherwise the stream kernels (small batches) or
     // the segment gather
     const bool str = scat && !gw_s && stream_wanted(L.W, canon_scales(L), B, B, SKIP_NONE);
-    if (!scat) fill(dx, B * L.n_in, 0.0f, st);
-    else if (!str) launch_zero_split_rows(L.W.plan(), dx, L.n_in, B, st);
+    if (!scat) prep.fill(dx, B * L.n_in, 0.0f);
+    else if (!str) prep.zero_split(L.W.plan(), dx, L.n_in, B);
+    prep.run();
     const bool fused = scat && gw_s &&
                        launch_bwd_fused(L.W.plan(), canon_scales(L), gT, xT, B, dx, L.n_in, gw_s, L.acc_in.p, st);
     if (str) stream_gather(L, L.W, canon_scales(L), gT, B, dx, L.n_in, st);
@@ -555,8 +625,7 @@ void forward_sparse(Layer &L, const int32_t *ptrs, const int32_t *idx, const flo
     if (push) launch_push_fwd(L, ptrs, idx, vals, B, canon_scales(L), y, false, st);
     if (!push || L.B4t.ntiles > 0) {
         L.ws_xT.ensure((size_t)(L.n_in * B));
-        fill(L.ws_xT.p, L.n_in * B, 0.0f, st);
-        launch_densify(ptrs, idx, vals, B, L.n_in, L.ws_xT.p, nullptr, true, nnz_x, st);
+        launch_densify_full(ptrs, idx, vals, B, L.n_in, L.ws_xT.p, nullptr, true, nnz_x, st);
     }
     if (!push) {
         launch_zero_split_rows(L.Wt.plan(), y, L.n_out, B, st);
@@ -573,8 +642,7 @@ void backward_sparse(Layer &L, const float *x, const int32_t *dptrs, const int32
     if (!x || !dptrs || !dx) throw_error(SILI_ERR_INVALID, "backward_sparse: NULL buffer");
     launch_colabs(x, B, L.n_in, L.acc_in.p, st);
     L.ws_gT.ensure((size_t)(L.n_out * B));
-    fill(L.ws_gT.p, L.n_out * B, 0.0f, st);
-    launch_densify(dptrs, didx, dvals, B, L.n_out, L.ws_gT.p, L.acc_grad.p, true, nnz_dy, st);
+    launch_densify_full(dptrs, didx, dvals, B, L.n_out, L.ws_gT.p, L.acc_grad.p, true, nnz_dy, st);
     launch_zero_split_rows(L.W.plan(), dx, L.n_in, B, st);
     // scattered: merge-join visits only present dy entries (sisldo_ops.hpp:705-713);
     // block4: skips dy == 0 per slot (sisldo_ops.hpp:886-897)
@@ -597,9 +665,8 @@ void backward_sparse_train(Layer &L, const float *x, const int32_t *dptrs, const
     L.xT_cached_batch = 0;
     launch_rowabs(xT, B, L.n_in, L.acc_in.p, st);
     L.ws_gT.ensure((size_t)(L.n_out * B));
-    fill(L.ws_gT.p, L.n_out * B, 0.0f, st);
     // entries present in dy carry nonzero bits (explicit zeros as -0.0)
-    launch_densify(dptrs, didx, dvals, B, L.n_out, L.ws_gT.p, L.acc_grad.p, true, nnz_dy, st);
+    launch_densify_full(dptrs, didx, dvals, B, L.n_out, L.ws_gT.p, L.acc_grad.p, true, nnz_dy, st);
     ensure_train_state(L, st);
     // a value scale's counter steps at most twice per call (the scattered
     // row's step, then its block row's)

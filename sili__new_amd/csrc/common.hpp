@@ -200,6 +200,28 @@ void launch_sddmm(const GatherPlan &p, const float *xT, const float *gT, int64_t
                   float *acc_in, hipStream_t st);
 // acc[j] += sum_b |xT[j*B+b]| (feature-major input).
 void launch_rowabs(const float *xT, int64_t B, int64_t n, float *acc, hipStream_t st);
+// Independent small tasks in one launch (k_prep): a transpose [B, n] -> [n, B]
+// with optional sum |.| per column into acc (B % 4 == 0, n % 4 == 0,
+// 16-byte aligned src and dst), sum |src[b, j]| over the batch into acc[j]
+// (n % 4 == 0, aligned src and acc), sum over a feature-major row into acc,
+// a float4 fill of n float4 with v, zeroing out[b * ld + rows[r]] for
+// r < n split rows and b < B.
+enum : int { PREP_TRANSPOSE = 0, PREP_COLABS = 1, PREP_ROWABS = 2, PREP_FILL4 = 3, PREP_ZERO_LIST = 4 };
+struct PrepTask {
+    int kind;
+    uint32_t first;  // set by launch_prep
+    const float *src;
+    float *dst, *acc;
+    int64_t B, n, ld;
+    const uint32_t *rows;
+    float v;
+};
+constexpr int PREP_MAX = 4;
+struct PrepArgs {
+    PrepTask t[PREP_MAX];
+    int nt;
+};
+void launch_prep(const PrepTask *tasks, int nt, hipStream_t st);
 void launch_sddmm_b4(const Block4Plan &p, const uint32_t *tile_base, const float *xT,
                      const float *gT, int64_t B, float *gw, hipStream_t st);
 // [B, n] -> [n, B]; when acc != NULL also acc[j] += sum_b |src[b, j]|.
@@ -212,8 +234,11 @@ void launch_colabs(const float *src, int64_t B, int64_t n, float *acc, hipStream
 // SKIP_POSZERO can tell them from absent entries.
 // nnz_hint: the number of stored entries (ptrs[batch]) when known on the
 // host -- one thread per entry; 0: one block per batch row.
-void launch_densify(const int32_t *ptrs, const int32_t *idx, const float *vals, int64_t B,
-                    int64_t n, float *dst, float *acc_abs, bool mark_explicit, int64_t nnz_hint, hipStream_t st);
+// The whole feature-major [n, B] array from CSR activations whose indices
+// ascend within each batch row (zeros where absent; explicit zeros -0.0 when
+// mark_explicit; acc_abs[j] += |v| when given): no separate zero fill.
+void launch_densify_full(const int32_t *ptrs, const int32_t *idx, const float *vals, int64_t B, int64_t n,
+                         float *dst, float *acc_abs, bool mark_explicit, int64_t nnz, hipStream_t st);
 // Zero out[b, row] of the rows split over several work items of `p`.
 void launch_zero_split_rows(const GatherPlan &p, float *out, int64_t out_ld, int64_t nb, hipStream_t st);
 

@@ -6,7 +6,7 @@
 //   k_sddmm      nnz-sampled grad-W over the scattered store
 //   k_sddmm_b4   nnz-sampled grad-W over every block4 slot
 //   k_transpose  [B,n] -> [n,B] activations, fused sum_b |x| accumulators
-//   k_densify    CSR activations -> dense feature-major
+//   k_densify_tiles  CSR activations -> the whole dense feature-major array
 //   k_decode*    device decode of a store (export / parity / rebuild)
 //
 // Work item = one SegDesc decoded by one wave64.  The wave walks the
@@ -1707,11 +1707,10 @@ __global__ __launch_bounds__(256) void k_transpose(const float *__restrict__ src
 // The same with float4 rows: a 64(b) x 32(j) tile, 128-byte reads along j,
 // 256-byte writes along b.  Needs n % 4 == 0, B % 4 == 0 and 16-byte aligned
 // src / dst.
-__global__ __launch_bounds__(256) void k_transpose_v4(const float *__restrict__ src, int64_t B,
-                                                      int64_t n, float *__restrict__ dst,
-                                                      float *__restrict__ acc) {
-    __shared__ float tile[64][33];
-    const int64_t j0 = (int64_t)blockIdx.x * 32, b0 = (int64_t)blockIdx.y * 64;
+__device__ __forceinline__ void transpose_v4_body(const float *__restrict__ src, int64_t B, int64_t n,
+                                                  float *__restrict__ dst, float *__restrict__ acc, uint32_t bx,
+                                                  uint32_t by, uint32_t gy, float (*tile)[33]) {
+    const int64_t j0 = (int64_t)bx * 32, b0 = (int64_t)by * 64;
     const uint32_t t = threadIdx.x;
     {
         const uint32_t q = t & 7u, bb = t >> 3;  // 8 float4 per row, 32 rows per pass
@@ -1742,23 +1741,33 @@ __global__ __launch_bounds__(256) void k_transpose_v4(const float *__restrict__ 
                           (__builtin_fabsf(v.z) + __builtin_fabsf(v.w));
                 s = group_sum_last<16>(s);
                 if (q == 15u && j < n) {
-                    if (gridDim.y == 1) acc[j] += s;
+                    if (gy == 1) acc[j] += s;
                     else atomicAdd(acc + j, s);
                 }
             }
         }
     }
 }
+__global__ __launch_bounds__(256) void k_transpose_v4(const float *__restrict__ src, int64_t B,
+                                                      int64_t n, float *__restrict__ dst,
+                                                      float *__restrict__ acc) {
+    __shared__ float tile[64][33];
+    transpose_v4_body(src, B, n, dst, acc, blockIdx.x, blockIdx.y, gridDim.y, tile);
+}
 
 // acc[j] += sum_b |xT[j*B + b]| over a feature-major copy (one wave per row).
-__global__ __launch_bounds__(256) void k_rowabs(const float *__restrict__ xT, int64_t B, int64_t n,
-                                                float *__restrict__ acc) {
-    const int64_t j = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+__device__ __forceinline__ void rowabs_body(const float *__restrict__ xT, int64_t B, int64_t n,
+                                            float *__restrict__ acc, uint32_t bx) {
+    const int64_t j = (int64_t)bx * 4 + (threadIdx.x >> 6);
     if (j >= n) return;
     float s = 0.0f;
     for (int64_t b = threadIdx.x & 63u; b < B; b += 64) s += __builtin_fabsf(xT[j * B + b]);
     s = wave_sum(s);
     if ((threadIdx.x & 63u) == 0) acc[j] += s;
+}
+__global__ __launch_bounds__(256) void k_rowabs(const float *__restrict__ xT, int64_t B, int64_t n,
+                                                float *__restrict__ acc) {
+    rowabs_body(xT, B, n, acc, blockIdx.x);
 }
 
 __global__ __launch_bounds__(256) void k_colabs(const float *__restrict__ src, int64_t B, int64_t n,
@@ -1773,11 +1782,10 @@ __global__ __launch_bounds__(256) void k_colabs(const float *__restrict__ src, i
 // acc[j] += sum_b |src[b, j]| over a batch-major [B, n] array: 64 columns
 // per block as 16 float4 lanes x 16 batch groups, summed through LDS.
 // Needs n % 4 == 0 and a 16-byte aligned src.
-__global__ __launch_bounds__(256) void k_colabs_v4(const float *__restrict__ src, int64_t B, int64_t n,
-                                                   float *__restrict__ acc) {
-    __shared__ float4 part[16][16];
+__device__ __forceinline__ void colabs_v4_body(const float *__restrict__ src, int64_t B, int64_t n,
+                                               float *__restrict__ acc, uint32_t bx, float4 (*part)[16]) {
     const uint32_t t = threadIdx.x, q = t & 15u, bg = t >> 4;
-    const int64_t j = (int64_t)blockIdx.x * 64 + 4 * q;
+    const int64_t j = (int64_t)bx * 64 + 4 * q;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     if (j < n) {
         for (int64_t b = bg; b < B; b += 16) {
@@ -1800,6 +1808,67 @@ __global__ __launch_bounds__(256) void k_colabs_v4(const float *__restrict__ src
         float4 cur = *a4;
         cur.x += tot.x; cur.y += tot.y; cur.z += tot.z; cur.w += tot.w;
         *a4 = cur;
+    }
+}
+__global__ __launch_bounds__(256) void k_colabs_v4(const float *__restrict__ src, int64_t B, int64_t n,
+                                                   float *__restrict__ acc) {
+    __shared__ float4 part[16][16];
+    colabs_v4_body(src, B, n, acc, blockIdx.x, part);
+}
+
+// Zero out[b, row] for every row split over several work items (their
+// partial sums add atomically); rows with one work item are stored whole.
+// One thread per (batch index, split row).
+__global__ __launch_bounds__(256) void k_zero_split_rows(const uint32_t *__restrict__ rows, int64_t n_split,
+                                                         float *__restrict__ out, int64_t out_ld, int64_t nb) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n_split * nb) return;
+    const int64_t b = i / n_split, k = i - b * n_split;
+    out[b * out_ld + rows[k]] = 0.0f;
+}
+
+__global__ __launch_bounds__(256) void k_zero_f4(float4 *__restrict__ p, int64_t n4) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n4) p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+__global__ __launch_bounds__(256) void k_zero_f1(float *__restrict__ p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = 0.0f;
+}
+
+// Independent small tasks of one entry point in one launch: each block runs
+// the task whose block range holds it (tasks[k].first .. + blocks).
+__global__ __launch_bounds__(256) void k_prep(PrepArgs a) {
+    __shared__ float tile[64][33];
+    uint32_t k = 0;
+    while (k + 1 < (uint32_t)a.nt && blockIdx.x >= a.t[k + 1].first) ++k;
+    const PrepTask &T = a.t[k];
+    const uint32_t vb = blockIdx.x - T.first;
+    switch (T.kind) {
+    case PREP_TRANSPOSE: {
+        const uint32_t gx = (uint32_t)((T.n + 31) / 32), gy = (uint32_t)((T.B + 63) / 64);
+        transpose_v4_body(T.src, T.B, T.n, T.dst, T.acc, vb % gx, vb / gx, gy, tile);
+        break;
+    }
+    case PREP_COLABS:
+        colabs_v4_body(T.src, T.B, T.n, T.acc, vb, reinterpret_cast<float4 (*)[16]>(&tile[0][0]));
+        break;
+    case PREP_ROWABS:
+        rowabs_body(T.src, T.B, T.n, T.acc, vb);
+        break;
+    case PREP_FILL4: {
+        const int64_t i = (int64_t)vb * 256 + threadIdx.x;
+        if (i < T.n) reinterpret_cast<float4 *>(T.dst)[i] = make_float4(T.v, T.v, T.v, T.v);
+        break;
+    }
+    default: {  // PREP_ZERO_LIST: out[b * ld + rows[k]] = 0, n = split rows, B = batch
+        const int64_t i = (int64_t)vb * 256 + threadIdx.x;
+        if (i < T.n * T.B) {
+            const int64_t b = i / T.n, r = i - b * T.n;
+            T.dst[b * T.ld + T.rows[r]] = 0.0f;
+        }
+        break;
+    }
     }
 }
 
@@ -1829,40 +1898,90 @@ __global__ __launch_bounds__(256) void k_densify_entries(const int32_t *__restri
     dst[j * B + lo] = v;
 }
 
-// Zero out[b, row] for every row split over several work items (their
-// partial sums add atomically); rows with one work item are stored whole.
-// One thread per (batch index, split row).
-__global__ __launch_bounds__(256) void k_zero_split_rows(const uint32_t *__restrict__ rows, int64_t n_split,
-                                                         float *__restrict__ out, int64_t out_ld, int64_t nb) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n_split * nb) return;
-    const int64_t b = i / n_split, k = i - b * n_split;
-    out[b * out_ld + rows[k]] = 0.0f;
-}
-
-__global__ __launch_bounds__(256) void k_zero_f4(float4 *__restrict__ p, int64_t n4) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < n4) p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-}
-__global__ __launch_bounds__(256) void k_zero_f1(float *__restrict__ p, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) p[i] = 0.0f;
-}
-
-__global__ __launch_bounds__(256) void k_densify(const int32_t *__restrict__ ptrs,
-                                                 const int32_t *__restrict__ idx,
-                                                 const float *__restrict__ vals, int64_t B,
-                                                 int64_t n, float *__restrict__ dst,
-                                                 float *__restrict__ acc_abs, int mark) {
-    const int64_t b = blockIdx.x;
-    const int64_t p0 = ptrs[b], p1 = ptrs[b + 1];
-    for (int64_t p = p0 + threadIdx.x; p < p1; p += 256) {
+// CSR activations (indices ascending within a batch row) -> the whole
+// feature-major dst[j * B + b], zeros where absent: one block per tile of R
+// rows, built in LDS and written out whole -- the zero fill and the scatter
+// in one pass.  Each batch row's first and last entries in the tile are
+// found at once by a group of G lanes each (a G-ary search: every round the
+// group samples G evenly spaced indices and keeps the bracket that holds
+// the key, so a row of len entries takes log_G(len) dependent loads); a
+// block scan places the entries and all of them are loaded in one round.
+// Explicit zeros become -0.0 when `mark`; acc_abs[j] += |v| (optional).
+// 2 * B * G <= 1024, G in [2, 32], B <= DENSIFY_TILE_MAX_B.
+constexpr int64_t DENSIFY_TILE_MAX_B = 256;
+__global__ __launch_bounds__(1024) void k_densify_tiles(const int32_t *__restrict__ ptrs,
+                                                        const int32_t *__restrict__ idx,
+                                                        const float *__restrict__ vals, int64_t B, int64_t n,
+                                                        int64_t R, uint32_t lg, float *__restrict__ dst,
+                                                        float *__restrict__ acc_abs, int mark) {
+    extern __shared__ float tile[];  // R * B floats
+    __shared__ int32_t s_lo[DENSIFY_TILE_MAX_B], s_hi[DENSIFY_TILE_MAX_B];
+    __shared__ uint32_t s_pre[DENSIFY_TILE_MAX_B + 1];
+    __shared__ uint32_t s_wave[16];
+    const int64_t j0 = (int64_t)blockIdx.x * R;
+    const int64_t rows = min<int64_t>(R, n - j0), cnt = rows * B;
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    for (int64_t i = t; i < cnt; i += 1024) tile[i] = 0.0f;
+    const uint32_t G = 1u << lg, q = t >> lg, k = t & (G - 1u);
+    if ((int64_t)q < 2 * B) {
+        const int64_t b = q >> 1, key = j0 + ((q & 1u) ? rows : 0);
+        int64_t lo = ptrs[b], hi = ptrs[b + 1];  // the answer lies in [lo, hi]
+        const uint64_t gmask = (((uint64_t)1 << G) - 1u) << (lane & ~(G - 1u));
+        while (lo < hi) {
+            const int64_t step = (hi - lo + G - 1) >> lg;
+            const int64_t pos = lo + (int64_t)k * step;
+            const bool below = pos < hi && idx[pos] < key;
+            const int64_t c = __popcll(__ballot(below) & gmask);
+            if (c == 0) {
+                hi = lo;
+            } else {
+                hi = min<int64_t>(hi, lo + c * step);
+                lo = lo + (c - 1) * step + 1;
+            }
+        }
+        if (k == 0) ((q & 1u) ? s_hi : s_lo)[b] = (int32_t)lo;
+    }
+    __syncthreads();
+    const uint32_t c = (int64_t)t < B ? (uint32_t)(s_hi[t] - s_lo[t]) : 0u;
+    // exclusive scan of the counts over the batch rows
+    uint32_t incl = c;
+    for (uint32_t o = 1; o < 64u; o <<= 1) {
+        const uint32_t y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    if (lane == 63u) s_wave[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0, total = 0;
+    for (uint32_t w = 0; w < 16u; ++w) {
+        const uint32_t v = s_wave[w];
+        before += w < wave ? v : 0u;
+        total += v;
+    }
+    if ((int64_t)t < B) s_pre[t] = before + incl - c;
+    if (t == 0) s_pre[B] = total;
+    __syncthreads();
+    for (uint32_t e = t; e < total; e += 1024) {
+        uint32_t lo = 0, hi = (uint32_t)B;  // last b with s_pre[b] <= e
+        while (hi - lo > 1) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (s_pre[mid] <= e) lo = mid;
+            else hi = mid;
+        }
+        const int64_t p = s_lo[lo] + (int64_t)(e - s_pre[lo]);
         const int64_t j = idx[p];
-        if (j < 0 || j >= n) continue;  // host validated; never write out of bounds
+        if (j < j0 || j >= j0 + rows) continue;  // never written out of its tile
         float v = vals[p];
         if (acc_abs) atomicAdd(acc_abs + j, __builtin_fabsf(v));
         if (mark && __builtin_bit_cast(uint32_t, v) == 0u) v = -0.0f;
-        dst[j * B + b] = v;
+        tile[(j - j0) * B + lo] = v;
+    }
+    __syncthreads();
+    float *out = dst + j0 * B;
+    if ((reinterpret_cast<uintptr_t>(out) & 15u) == 0 && (cnt & 3) == 0) {
+        for (int64_t i = t; i < cnt / 4; i += 1024)
+            reinterpret_cast<float4 *>(out)[i] = reinterpret_cast<const float4 *>(tile)[i];
+    } else {
+        for (int64_t i = t; i < cnt; i += 1024) out[i] = tile[i];
     }
 }
 
@@ -2260,6 +2379,36 @@ void launch_transpose(const float *src, int64_t B, int64_t n, float *dst, float 
     SILI_HIP(hipGetLastError());
 }
 
+uint32_t prep_blocks(const PrepTask &t) {
+    switch (t.kind) {
+    case PREP_TRANSPOSE: return (uint32_t)(((t.n + 31) / 32) * ((t.B + 63) / 64));
+    case PREP_COLABS: return (uint32_t)((t.n + 63) / 64);
+    case PREP_ROWABS: return (uint32_t)((t.n + 3) / 4);
+    case PREP_FILL4: return (uint32_t)((t.n + 255) / 256);
+    default: return (uint32_t)((t.n * t.B + 255) / 256);
+    }
+}
+
+void launch_prep(const PrepTask *tasks, int nt, hipStream_t st) {
+    PrepArgs a{};
+    uint32_t blocks = 0;
+    for (int k = 0; k < nt; ++k) {
+        const uint32_t nb = prep_blocks(tasks[k]);
+        if (nb == 0) continue;
+        if (a.nt == PREP_MAX) throw_error(3, "launch_prep: too many tasks (internal error)");
+        a.t[a.nt] = tasks[k];
+        a.t[a.nt].first = blocks;
+        blocks += nb;
+        ++a.nt;
+    }
+    if (blocks == 0) return;
+    // named for its task when it holds one (the names of the separate launches)
+    static const char *const names[] = {"transpose", "colabs", "rowabs", "fill", "zero_split"};
+    ProfScope ps(a.nt == 1 ? names[a.t[0].kind] : "prep", st);
+    launch(k_prep, dim3(blocks), dim3(256), 0, st, a);
+    SILI_HIP(hipGetLastError());
+}
+
 void launch_rowabs(const float *xT, int64_t B, int64_t n, float *acc, hipStream_t st) {
     if (B == 0 || n == 0) return;
     ProfScope ps("rowabs", st);
@@ -2294,16 +2443,28 @@ void launch_zero_split_rows(const GatherPlan &p, float *out, int64_t out_ld, int
     SILI_HIP(hipGetLastError());
 }
 
-void launch_densify(const int32_t *ptrs, const int32_t *idx, const float *vals, int64_t B,
-                    int64_t n, float *dst, float *acc_abs, bool mark_explicit, int64_t nnz_hint, hipStream_t st) {
-    if (B == 0) return;
+void launch_densify_full(const int32_t *ptrs, const int32_t *idx, const float *vals, int64_t B, int64_t n,
+                         float *dst, float *acc_abs, bool mark_explicit, int64_t nnz, hipStream_t st) {
+    if (B == 0 || n == 0) return;
     ProfScope ps("densify", st);
-    if (nnz_hint > 0)
-        launch(k_densify_entries, dim3((unsigned)((nnz_hint + 255) / 256)), dim3(256), 0, st, ptrs, idx, vals, B, n,
-               dst, acc_abs, mark_explicit ? 1 : 0);
-    else
-        launch(k_densify, dim3((unsigned)B), dim3(256), 0, st, ptrs, idx, vals, B, n, dst,
-                           acc_abs, mark_explicit ? 1 : 0);
+    if (B > DENSIFY_TILE_MAX_B) {
+        // a zero fill, then one thread per entry
+        const int64_t cnt = B * n;
+        const int64_t n4 = aligned16(dst) ? cnt / 4 : 0;
+        if (n4 > 0) launch(k_zero_f4, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, reinterpret_cast<float4 *>(dst), n4);
+        if (cnt - 4 * n4 > 0) launch(k_zero_f1, dim3((unsigned)((cnt - 4 * n4 + 255) / 256)), dim3(256), 0, st, dst + 4 * n4, cnt - 4 * n4);
+        if (nnz > 0)
+            launch(k_densify_entries, dim3((unsigned)((nnz + 255) / 256)), dim3(256), 0, st, ptrs, idx, vals, B, n, dst,
+                   acc_abs, mark_explicit ? 1 : 0);
+        SILI_HIP(hipGetLastError());
+        return;
+    }
+    const int64_t R = std::max<int64_t>(1, std::min<int64_t>(256, 2048 / B));
+    const size_t lds = (size_t)(R * B) * sizeof(float);
+    uint32_t lg = 5;  // lanes per search: 2 * B * 2^lg <= 1024
+    while ((2 * B) << lg > 1024) --lg;
+    launch(k_densify_tiles, dim3((unsigned)((n + R - 1) / R)), dim3(1024), (uint32_t)lds, st, ptrs, idx, vals, B, n, R,
+           lg, dst, acc_abs, mark_explicit ? 1 : 0);
     SILI_HIP(hipGetLastError());
 }
 

@@ -201,3 +201,28 @@ def test_block4_only_layer_forward_backward(hip):
         assert_close_terms(y, H.forward_dense(x), H.forward_dense(x, absmode=True), "b4-only fwd")
         dx = L.backward_dense(g, 0.0)
         assert_close_terms(dx, H.backward_dense(x, g)[0], H.backward_dense(x, g, absmode=True)[0], "b4-only dx")
+
+
+@pytest.mark.parametrize("batch", [1, 5, 33, 256, 257, 1025])
+def test_sparse_input_forward_ragged(hip, batch):
+    """Sparse-input forward over ragged activations: empty batch rows, a full
+    row, explicit zeros among the stored entries, and a batch above the
+    one-pass densify's limit of 256 rows (zero fill + per-entry scatter)."""
+    wl = make_config(2, scale=0.03125, batch=batch)
+    H = host_layer(wl)
+    L = gpu_layer(hip, wl)
+    rng = np.random.default_rng(batch)
+    x = rng.normal(size=(batch, wl.n_in)).astype(np.float32)
+    x[rng.random(x.shape) < 0.9] = 0.0
+    x[::4] = 0.0                     # empty rows
+    if batch > 1:
+        x[1] = rng.normal(size=wl.n_in)  # a full row
+    keep = x != 0
+    keep[rng.random(x.shape) < 0.02] = True  # explicit zeros stored
+    ptrs = np.concatenate([[0], np.cumsum(keep.sum(1))]).astype(np.int32)
+    idx = np.nonzero(keep)[1].astype(np.int32)
+    vals = x[keep].astype(np.float32)
+    y = L.forward_sparse(ptrs, idx, vals, batch)
+    want = H.forward_sparse(ptrs, idx, vals, batch)
+    bnd = H.forward_sparse(ptrs, idx, vals, batch, absmode=True)
+    assert_close_terms(y, want, bnd, f"sparse fwd B{batch}")
