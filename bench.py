@@ -524,6 +524,20 @@ def time_synap_policy(hip, wl, reps, seconds):
            "build_probes_ms_median": round(float(np.median(t_probe)), 3),
            "cycles_that_edited": edits,
            "cycle": "build_probes(4) + synap_step(importance_cutoff 0.3, max_row_weights 200)"}
+    # the same cycle after a call that may change the accumulators (as a
+    # training step's backward does): build_probes stages them again
+    times_r = []
+    for i in range(reps):
+        L.forward_dense(x[:1])  # untimed; ends the validity of the staged accumulators
+        L.synchronize()
+        t0 = time.perf_counter()
+        L.build_probes(4)
+        L.synap_step(cutoff, max_rw)
+        L.synchronize()
+        times_r.append((time.perf_counter() - t0) * 1e3)
+    out["gpu_ms_median_restaged"] = round(float(np.median(times_r)), 3)
+    out["restaged_note"] = ("each cycle after an untimed forward_dense, so build_probes re-reads the "
+                            "accumulators; gpu_ms_median: back-to-back cycles, which keep them")
     # FoldedLayer's sweep (sili/sparse_rnn.py:1206-1212): build_probes once,
     # synap_step on every row, then the next entry point writes the edits;
     # deferred (one flush for the sweep) and patched per call

@@ -124,13 +124,20 @@ void fill(float *p, int64_t n, float v, hipStream_t st) {
 
 // Every entry point that reaches a layer's device state comes here first.
 // The policy's own (policy = true) leave its pending edits pending; any
-// other writes them first and ends the validity of the policy's staged rows.
+// other writes them first and, unless it only reads the layer
+// (set_device_read), ends the validity of what the policy has staged (its
+// block rows, the accumulators and their top-k selections).
 void set_device(Layer &L, bool policy = false) {
     SILI_HIP(hipSetDevice(L.device));
     if (!policy) {
         if (!L.policy_pending.empty()) policy_flush(L);
         ++L.policy_epoch;
     }
+}
+// Entry points that change nothing of the layer's stores or accumulators.
+void set_device_read(Layer &L) {
+    SILI_HIP(hipSetDevice(L.device));
+    if (!L.policy_pending.empty()) policy_flush(L);
 }
 // Readers of the scales only (no store access).
 void set_device(const Layer &L) { SILI_HIP(hipSetDevice(L.device)); }
@@ -769,7 +776,7 @@ void sili_destroy(sili_layer *layer) {
 int sili_synchronize(sili_layer *layer) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
-        set_device(layer->L);
+        set_device_read(layer->L);
         SILI_HIP(hipStreamSynchronize(layer->L.stream));
     });
 }
@@ -1215,7 +1222,7 @@ int sili_get_accumulators(sili_layer *layer, float *acc_in, float *acc_grad) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
         Layer &L = layer->L;
-        set_device(L);
+        set_device_read(L);
         SILI_HIP(hipStreamSynchronize(L.stream));
         if (acc_in) SILI_HIP(hipMemcpy(acc_in, L.acc_in.p, (size_t)L.n_in * 4, hipMemcpyDeviceToHost));
         if (acc_grad) SILI_HIP(hipMemcpy(acc_grad, L.acc_grad.p, (size_t)L.n_out * 4, hipMemcpyDeviceToHost));
@@ -1236,7 +1243,7 @@ int sili_get_info(sili_layer *layer, sili_info *out) {
     return guarded([&] {
         if (!layer || !out) throw_error(SILI_ERR_INVALID, "NULL argument");
         Layer &L = layer->L;
-        set_device(L);
+        set_device_read(L);
         std::memset(out, 0, sizeof(*out));
         out->n_inputs = L.n_in;
         out->n_outputs = L.n_out;
@@ -1270,7 +1277,7 @@ int sili_export_scattered(sili_layer *layer, uint64_t *row_byte_start, uint64_t 
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
         Layer &L = layer->L;
-        set_device(L);
+        set_device_read(L);
         SILI_HIP(hipStreamSynchronize(L.stream));
         std::vector<uint32_t> tmp((size_t)L.n_in + 1);
         if (row_byte_start) {
@@ -1328,7 +1335,7 @@ int sili_debug_store_digest(sili_layer *layer, uint64_t *digest) {
     return guarded([&] {
         if (!layer || !digest) throw_error(SILI_ERR_INVALID, "layer or digest is NULL");
         Layer &L = layer->L;
-        set_device(L);
+        set_device_read(L);
         SILI_HIP(hipStreamSynchronize(L.stream));
         digest[0] = digest_scatter(L.W);
         digest[1] = digest_scatter(L.Wt);
@@ -1345,7 +1352,7 @@ int sili_export_block4(sili_layer *layer, int32_t *br, int32_t *bc, uint8_t *til
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
         Layer &L = layer->L;
-        set_device(L);
+        set_device_read(L);
         SILI_HIP(hipStreamSynchronize(L.stream));
         if (br || bc) {
             std::vector<uint32_t> ubr, ubc;
@@ -1374,7 +1381,7 @@ int sili_decode_scattered(sili_layer *layer, int32_t *cols, float *w_true) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
         Layer &L = layer->L;
-        set_device(L);
+        set_device_read(L);
         const size_t n = (size_t)L.W.nnz;
         if (n == 0) return;
         DevBuf<int32_t> dc;
@@ -1393,7 +1400,7 @@ int sili_export_absolute(sili_layer *layer, int32_t *ptrs, int32_t *indices, flo
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
         Layer &L = layer->L;
-        set_device(L);
+        set_device_read(L);
         const size_t n = (size_t)L.W.nnz;
         std::vector<int32_t> cols(n);
         std::vector<uint8_t> val(n);

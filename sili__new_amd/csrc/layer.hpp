@@ -339,11 +339,17 @@ struct Layer {
     uint32_t seg_len_b4 = 128;  // max block-index bytes per decode work item (block4)
     // the policy's row patches: pinned staging (reads in, patch content out),
     // the device copy of the patch content, and the arrays' second buffers
-    PinBuf pin_rows, pin_stage, pin_patch, pin_deg;
+    PinBuf pin_rows, pin_stage, pin_patch, pin_deg, pin_acc;
+    // The activity accumulators as build_probes last staged them (pin_acc),
+    // with its top-k selections over them (k, indices), valid while acc_epoch
+    // == policy_epoch: no entry point that may change them has run since.
+    uint64_t acc_epoch = ~0ull;
+    int64_t sel_in_k = -1, sel_out_k = -1;
+    std::vector<size_t> sel_in, sel_out;
     // The policy's block rows: staged and unchanged (clean, valid while no
-    // other entry point has run: policy_epoch), and edited but not yet
-    // written (pending, written by policy_flush before any other entry
-    // point touches the layer).
+    // entry point that may change the layer has run: policy_epoch), and
+    // edited but not yet written (pending, written by policy_flush before any
+    // other entry point touches the layer).
     std::map<uint32_t, StagedBlock> policy_clean;
     std::map<uint32_t, PendingBlock> policy_pending;
     uint64_t policy_epoch = 0, clean_epoch = ~0ull;

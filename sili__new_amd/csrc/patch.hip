@@ -634,13 +634,16 @@ void stage_rows(Layer &L, const std::vector<StageReq *> &reqs) {
 
 const float *stage_accumulators(Layer &L) {
     const int64_t n = L.n_in + L.n_out;
-    L.pin_patch.ensure((size_t)n * 4 + 4);
+    if (L.acc_epoch == L.policy_epoch) return reinterpret_cast<const float *>(L.pin_acc.h);
+    L.pin_acc.ensure((size_t)n * 4 + 4);
     if (n > 0)
         launch(k_stage_acc, dim3(nblk(n)), dim3(TPB), 0, L.stream, (const float *)L.acc_in.p, L.n_in,
-               (const float *)L.acc_grad.p, L.n_out, reinterpret_cast<float *>(L.pin_patch.h));
+               (const float *)L.acc_grad.p, L.n_out, reinterpret_cast<float *>(L.pin_acc.h));
     SILI_HIP(hipGetLastError());
     SILI_HIP(hipStreamSynchronize(L.stream));
-    return reinterpret_cast<const float *>(L.pin_patch.h);
+    L.acc_epoch = L.policy_epoch;
+    L.sel_in_k = L.sel_out_k = -1;
+    return reinterpret_cast<const float *>(L.pin_acc.h);
 }
 
 std::vector<uint32_t> staged_cols(const StagedRow &r) {

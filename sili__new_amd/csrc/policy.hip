@@ -400,11 +400,16 @@ void build_probes(Layer &L, int64_t k, bool per_row) {
     L.keep_temps = true;  // a layer that runs the policy keeps its small temporaries
     const float *acc_in = stage_accumulators(L), *acc_grad = acc_in + n_in;
     const size_t kk_in = std::min((size_t)k, n_in), kk = (size_t)k;
-    std::vector<size_t> in_idx(n_in);
-    std::iota(in_idx.begin(), in_idx.end(), 0);
-    std::partial_sort(in_idx.begin(), in_idx.begin() + kk_in, in_idx.end(),
-                      [&](size_t a, size_t b) { return acc_in[a] > acc_in[b]; });
-    in_idx.resize(kk_in);
+    if (L.sel_in_k != k) {  // the top rows, kept with the staged accumulators
+        std::vector<size_t> in_idx(n_in);
+        std::iota(in_idx.begin(), in_idx.end(), 0);
+        std::partial_sort(in_idx.begin(), in_idx.begin() + kk_in, in_idx.end(),
+                          [&](size_t a, size_t b) { return acc_in[a] > acc_in[b]; });
+        in_idx.resize(kk_in);
+        L.sel_in.swap(in_idx);
+        L.sel_in_k = k;
+    }
+    const std::vector<size_t> &in_idx = L.sel_in;
     std::vector<int32_t> pr, pc;
     std::vector<float> pv;
     // the top rows' stored columns (edited block rows from their pending
@@ -440,11 +445,16 @@ void build_probes(Layer &L, int64_t k, bool per_row) {
     };
     if (!per_row) {
         const size_t kk_out = std::min(kk, n_out);
-        std::vector<size_t> out_idx(n_out);
-        std::iota(out_idx.begin(), out_idx.end(), 0);
-        std::partial_sort(out_idx.begin(), out_idx.begin() + kk_out, out_idx.end(),
-                          [&](size_t a, size_t b) { return acc_grad[a] > acc_grad[b]; });
-        out_idx.resize(kk_out);
+        if (L.sel_out_k != k) {
+            std::vector<size_t> out_idx(n_out);
+            std::iota(out_idx.begin(), out_idx.end(), 0);
+            std::partial_sort(out_idx.begin(), out_idx.begin() + kk_out, out_idx.end(),
+                              [&](size_t a, size_t b) { return acc_grad[a] > acc_grad[b]; });
+            out_idx.resize(kk_out);
+            L.sel_out.swap(out_idx);
+            L.sel_out_k = k;
+        }
+        const std::vector<size_t> &out_idx = L.sel_out;
         for (size_t r : in_idx) {
             const auto ex = row_cols(r);
             for (size_t c : out_idx) {

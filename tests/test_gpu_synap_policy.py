@@ -89,6 +89,45 @@ def test_synap_policy_matches_oracle(hip, seed):
     assert_close_terms(L.forward_dense(x), H.forward_dense(x), H.forward_dense(x, absmode=True), "forward")
 
 
+def test_probes_follow_accumulators(hip):
+    """build_probes keeps the accumulators it staged, and its top-k
+    selections over them, while only policy calls and calls that read the
+    layer run (exports, info, synchronize); after a call that changes them
+    (backward, zero_accum) it reads them again.  Probes match the
+    oracle's over the accumulators at each call."""
+    c = policy_case(6)
+    L, H = gpu_policy_layer(hip, c), host_policy_layer(c)
+    rng = np.random.default_rng(11)
+    n_in, n_out = c["n_in"], c["n_out"]
+
+    def probes_match(k, per_row, what):
+        ai, ag = L.neuron_input_accum.copy(), L.neuron_grad_accum.copy()
+        L.build_probes(k, per_row)
+        H.build_probes(ai, ag, k, per_row)
+        pr, pc, pv = L.get_probes()
+        n = H.probe_nnz
+        assert np.array_equal(pr, H.probes[0][:n]) and np.array_equal(pc, H.probes[1][:n]) and \
+            np.array_equal(pv, H.probes[2][:n]), what
+        return ai, ag
+
+    feed_accumulators(L, rng, n_in, n_out)
+    a0 = probes_match(4, False, "first")
+    for it in range(6):
+        assert L.synap_step(0.3, 20, 4, 1e-3) == H.synap_step(0.3, 20, 4, 1e-3)
+        L.synchronize()
+        L.info()
+        assert_same(L, H, f"step {it}")
+        probes_match([4, 4, 3, 5, 4, 2][it], it % 2 == 1, f"cached, call {it}")
+    L.forward_dense(accum(rng, n_in)[None, :])
+    L.backward_dense(accum(rng, n_out)[None, :], 0.0)  # both accumulators change
+    a1 = probes_match(4, False, "after backward")
+    assert not np.array_equal(a0[0], a1[0]) and not np.array_equal(a0[1], a1[1])
+    probes_match(3, True, "after backward, per row")
+    L.zero_accum()
+    probes_match(4, False, "after zero_accum")
+    assert L.get_probes()[2].size == 0 or not L.get_probes()[2].any()
+
+
 def test_update_after_policy_uses_its_out_degree(hip):
     """The output scales' step divides by out_degree and skips a column whose
     out_degree is 0 (linear_disldo.hpp:2061-2064); the policy's count differs
