@@ -544,6 +544,7 @@ static void build_b4_orientation(Layer &L, DBlock4 &dst, int64_t N, int64_t brow
     dst.tiles.ensure((size_t)N * 16u + 64);
     dst.cblk.clear();
     dst.cblk_cbb = 0;
+    dst.rng_k = 0;
     if (N > 0) {
         launch(k_gather_tiles, dim3(nblk(N)), dim3(TPB), 0, st, d_src_tiles, d_perm, N,
                            transpose ? 1 : 0, dst.tiles.p);
@@ -599,6 +600,47 @@ void build_colblocks_b4(Layer &L, DBlock4 &b, int K, int64_t cbb) {
     SILI_HIP(hipStreamSynchronize(st));
     b.cblk = std::move(blocks);
     b.cblk_cbb = cbb;
+}
+
+// start[x*brows + br] = the first tile of block row br whose block column
+// is >= x * cbb (x < K), start[K*brows + br] = the row's end.
+__global__ void k_range_starts(const uint32_t *__restrict__ tile_start, const uint32_t *__restrict__ tcol,
+                               int64_t brows, int64_t K, int64_t cbb, uint32_t *__restrict__ start) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= (K + 1) * brows) return;
+    const int64_t x = i / brows, br = i % brows;
+    uint32_t lo = tile_start[br], hi = tile_start[br + 1];
+    if (x == K) {
+        start[i] = hi;
+        return;
+    }
+    const uint64_t key = (uint64_t)x * (uint64_t)cbb;
+    while (lo < hi) {
+        const uint32_t mid = lo + ((hi - lo) >> 1);
+        if ((uint64_t)tcol[mid] < key) lo = mid + 1;
+        else hi = mid;
+    }
+    start[i] = lo;
+}
+
+void ensure_col_ranges(Layer &L, DBlock4 &b, int K) {
+    if (K < 1) throw_error(1, "column ranges: K must be >= 1");
+    if (b.rng_k == K) return;
+    hipStream_t st = L.stream;
+    const int64_t N = b.ntiles;
+    b.rng_col.ensure((size_t)N + 1);
+    b.rng_start.ensure((size_t)(K + 1) * (size_t)b.brows + 1);
+    DevBuf<uint32_t> major;
+    major.ensure((size_t)N + 1);
+    if (N > 0) launch_decode_b4(b.plan(), major.p, b.rng_col.p, st);
+    const int64_t cbb = (b.bcols + K - 1) / K;
+    const int64_t n = (int64_t)(K + 1) * b.brows;
+    if (n > 0)
+        launch(k_range_starts, dim3(nblk(n)), dim3(TPB), 0, st, (const uint32_t *)b.tile_start.p,
+               (const uint32_t *)b.rng_col.p, b.brows, (int64_t)K, cbb, b.rng_start.p);
+    SILI_HIP(hipGetLastError());
+    SILI_HIP(hipStreamSynchronize(st));
+    b.rng_k = K;
 }
 
 void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_t *d_bc,

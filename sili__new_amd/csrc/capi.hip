@@ -434,6 +434,22 @@ void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st
 // forward_dense without device allocation: the feature-major copy of x goes
 // to the per-device scratch, and only structures built at load are read (the
 // segment gathers over the shadow stores: no stream or column-block copies,
+
+// The block4 sampled grad-W by column range: ceil(gT bytes / 4 MiB) ranges
+// (at most 8), so that each XCD's L2 (4 MiB) holds its range's gT rows
+// (SILI_SDDMM_RANGES: the number of ranges, 0 for the store's work items).
+void sddmm_b4(Layer &L, const float *xT, const float *gT, int64_t B, float *gw, hipStream_t st) {
+    const int64_t gT_bytes = L.B4.cols * B * 4, l2 = int64_t(4) << 20;
+    const int K = env_int("SILI_SDDMM_RANGES", (int)std::min<int64_t>(8, std::max<int64_t>(1, (gT_bytes + l2 - 1) / l2)));
+    if (K >= 1) {
+        ensure_col_ranges(L, L.B4, K);
+        const B4Ranges r = L.B4.ranges();
+        launch_sddmm_b4(L.B4.plan(), &r, xT, gT, B, gw, st);
+    } else {
+        launch_sddmm_b4(L.B4.plan(), nullptr, xT, gT, B, gw, st);
+    }
+}
+
 // which are built on first use).  No profiler context, so no events either.
 void forward_dense_noalloc(Layer &L, const float *x, int64_t B, float *y, hipStream_t st) {
     if (B <= 0) throw_error(SILI_ERR_INVALID, "forward_dense_noalloc: batch must be >= 1");
@@ -505,7 +521,7 @@ void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float 
     if (L.B4.ntiles > 0 && !gather_b4_colblocked(L, L.B4, canon_scales(L), gT, B, dx, L.n_in, SKIP_NONE, st))
         launch_gather_b4(L.B4.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
     if (scat && gw_s && !fused) launch_sddmm(L.W.plan(), xT, gT, B, gw_s, L.acc_in.p, st);
-    if (gw_b && L.B4.ntiles > 0) launch_sddmm_b4(L.B4.plan(), nullptr, xT, gT, B, gw_b, st);
+    if (gw_b && L.B4.ntiles > 0) sddmm_b4(L, xT, gT, B, gw_b, st);
 }
 
 // The scales' optimizer state, zeroed on first use (the reference sizes it
@@ -1049,7 +1065,7 @@ int sili_sampled_gradw(sili_layer *layer, const float *x, const float *dy, int64
         L.xT_cached_batch = 0;
         const float *gT = to_feature_major(L, L.ws_gT, dy, batch, L.n_out, nullptr, st);
         if (gw_s) launch_sddmm(L.W.plan(), xT, gT, batch, gw_s, nullptr, st);
-        if (gw_b && L.B4.ntiles > 0) launch_sddmm_b4(L.B4.plan(), nullptr, xT, gT, batch, gw_b, st);
+        if (gw_b && L.B4.ntiles > 0) sddmm_b4(L, xT, gT, batch, gw_b, st);
     });
 }
 

@@ -222,7 +222,15 @@ struct PrepArgs {
     int nt;
 };
 void launch_prep(const PrepTask *tasks, int nt, hipStream_t st);
-void launch_sddmm_b4(const Block4Plan &p, const uint32_t *tile_base, const float *xT,
+// A block4 store's tiles by column range: tcol[t] = the block column of
+// tile t; run (x, br) = tiles [start[x*brows + br], start[(x+1)*brows + br]).
+struct B4Ranges {
+    const uint32_t *tcol, *start;
+    int64_t K, brows;
+};
+// gw[16t + lj*4+li] = sum_b xT[4br+li, b] * gT[4bc+lj, b] for every tile t;
+// rng (optional, K >= 1 built): by column range, range x on XCD x.
+void launch_sddmm_b4(const Block4Plan &p, const B4Ranges *rng, const float *xT,
                      const float *gT, int64_t B, float *gw, hipStream_t st);
 // [B, n] -> [n, B]; when acc != NULL also acc[j] += sum_b |src[b, j]|.
 void launch_transpose(const float *src, int64_t B, int64_t n, float *dst, float *acc,

@@ -655,6 +655,11 @@ struct BArgs {
     float *out;
     int64_t out_ld;
     int64_t nb;
+    // k_gather_b4_v4 only: 0 for a (segments, batch chunks) grid; else the
+    // segment blocks per batch chunk of a 1-D grid taken in XCD-contiguous
+    // order chunk-major, so that each XCD works on one batch chunk (its L2
+    // then holds only that chunk's share of every input row)
+    uint32_t xq_gx;
 };
 
 // SKIP: SKIP_NONE (dense paths), SKIP_ZERO (entry value 0 skipped), or
@@ -1076,11 +1081,17 @@ __global__ __launch_bounds__(256) void k_gather_b4_v4(BArgs a, uint32_t in_bytes
     constexpr uint32_t NBC = 4u * BL * KB;  // batch columns per wave
     static_assert(4u * NBC <= 64u * 16u, "output slice must fit the weight table");
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
+    uint32_t bx = blockIdx.x, by = blockIdx.y;
+    if (a.xq_gx) {
+        const uint32_t lb = xcd_block(blockIdx.x, gridDim.x);
+        by = lb / a.xq_gx;
+        bx = lb % a.xq_gx;
+    }
+    const int64_t si = (int64_t)bx * WAVES + wave;
     const bool active = si < a.nseg;
     const uint32_t g = lane / BL, bl = lane % BL;
     const uint32_t nq = (uint32_t)(a.nb >> 2);
-    const uint32_t q0 = blockIdx.y * (BL * KB);
+    const uint32_t q0 = by * (BL * KB);
     float4 acc[4][KB];
 #pragma unroll
     for (int li = 0; li < 4; ++li)
@@ -1611,6 +1622,82 @@ __global__ __launch_bounds__(256) void k_sddmm_b4_v4(SBArgs a, uint32_t gT_bytes
         }
         wave_lds_sync();
         carry = chunk_advance(ch, pos, ebase);
+    }
+}
+
+// The same sampled grad-W over runs of tiles: run (x, br) = the tiles of
+// block row br in column range x (B4Ranges), one wave per run, runs in order
+// x-major and the blocks in XCD-contiguous order (xcd_block), so that XCD x
+// takes range x's runs: its L2 then holds only that range's gT rows (the
+// whole gT of a large layer does not fit one XCD's L2).  The tiles' block
+// columns come from tcol (no varint decode).  Per lane the arithmetic and the
+// reduction are k_sddmm_b4_v4's, so the results are the same bit for bit.
+struct SRArgs {
+    const uint32_t *tcol, *start;
+    int64_t nruns, brows;
+    int64_t rows;
+    const float *xT, *gT;
+    int64_t B;
+    float *gw;
+};
+template <int BL, int KB>
+__global__ __launch_bounds__(256) void k_sddmm_b4_rng(SRArgs a, uint32_t gT_bytes) {
+    constexpr uint32_t G = 64u / BL;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t run = (int64_t)xcd_block(blockIdx.x, gridDim.x) * WAVES + wave;
+    if (run >= a.nruns) return;
+    const int64_t br = run % a.brows;
+    const uint32_t t0 = a.start[run], t1 = a.start[run + a.brows];
+    if (t0 >= t1) return;
+    const uint32_t g = lane / BL, bl = lane % BL;
+    const uint32_t nq = (uint32_t)(a.B >> 2);
+    const uint32_t ld_bytes = (uint32_t)a.B * 4u;
+    const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(a.gT, gT_bytes);
+    uint32_t lane_off[KB];
+    float4 xr[4][KB];
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+        const uint32_t q = bl + BL * (uint32_t)k;
+        lane_off[k] = q < nq ? q * 16u : OOB_OFFSET;
+#pragma unroll
+        for (int li = 0; li < 4; ++li) {
+            const int64_t r = br * 4 + li;
+            xr[li][k] = (q < nq && r < a.rows)
+                ? reinterpret_cast<const float4 *>(a.xT + r * a.B)[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    for (uint32_t j = t0; j < t1; j += G) {
+        const uint32_t t = j + g;
+        const bool ok = t < t1;
+        const uint32_t off = ok ? a.tcol[t] * 4u * ld_bytes : OOB_OFFSET;
+        float d[16];
+#pragma unroll
+        for (int lj = 0; lj < 4; ++lj) {
+            float4 gv[KB];
+#pragma unroll
+            for (int k = 0; k < KB; ++k) gv[k] = buffer_load_f4(rg, off + (uint32_t)lj * ld_bytes + lane_off[k]);
+#pragma unroll
+            for (int li = 0; li < 4; ++li) {
+                float d0 = 0.f, d1 = 0.f;
+#pragma unroll
+                for (int k = 0; k < KB; ++k) {
+                    d0 = __builtin_fmaf(xr[li][k].x, gv[k].x, d0);
+                    d1 = __builtin_fmaf(xr[li][k].y, gv[k].y, d1);
+                    d0 = __builtin_fmaf(xr[li][k].z, gv[k].z, d0);
+                    d1 = __builtin_fmaf(xr[li][k].w, gv[k].w, d1);
+                }
+                d[lj * 4 + li] = d0 + d1;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) d[s] = group_sum_last<BL>(d[s]);
+        if (bl == BL - 1u && ok) {
+            float4 *o = reinterpret_cast<float4 *>(a.gw + (size_t)t * 16u);
+            o[0] = make_float4(d[0], d[1], d[2], d[3]);
+            o[1] = make_float4(d[4], d[5], d[6], d[7]);
+            o[2] = make_float4(d[8], d[9], d[10], d[11]);
+            o[3] = make_float4(d[12], d[13], d[14], d[15]);
+        }
     }
 }
 
@@ -2236,6 +2323,27 @@ void launch_gather_b4(const Block4Plan &p, const ScaleView &sc, const float *in,
             // (SILI_B4_BL / SILI_B4_U)
             const int bl = env_int("SILI_B4_BL", 16), u = env_int("SILI_B4_U", 2);
             const unsigned gy8 = (unsigned)((nq + 7) / 8);
+            // batches of 128 and more: 128 columns per wave (32 lanes per
+            // tile, 2 tile groups in flight), so each tile is decoded and
+            // dequantised by half as many waves (SILI_B4_WIDE)
+            if (nq >= 32 && bl == 16 && u == 2 && env_int("SILI_B4_WIDE", 1)) {
+                const unsigned gyw = (unsigned)((nq + 31) / 32);
+                if (env_int("SILI_B4_XCDQ", 1) && gyw > 1) a.xq_gx = gx;
+                const dim3 gw = a.xq_gx ? dim3(gx * gyw) : dim3(gx, gyw);
+                launch((k_gather_b4_v4<32, 1, 2>), gw, dim3(256), 0, st, a, (uint32_t)in_bytes);
+                SILI_HIP(hipGetLastError());
+                return;
+            }
+            // batch chunks on their own XCDs (SILI_B4_XCDQ)
+            if (env_int("SILI_B4_XCDQ", 1) && bl == 16 && gy16 > 1) {
+                a.xq_gx = gx;
+                const dim3 g1(gx * gy16);
+                if (u >= 4) launch((k_gather_b4_v4<16, 1, 4>), g1, dim3(256), 0, st, a, (uint32_t)in_bytes);
+                else if (u >= 2) launch((k_gather_b4_v4<16, 1, 2>), g1, dim3(256), 0, st, a, (uint32_t)in_bytes);
+                else launch((k_gather_b4_v4<16, 1, 1>), g1, dim3(256), 0, st, a, (uint32_t)in_bytes);
+                SILI_HIP(hipGetLastError());
+                return;
+            }
             if (bl == 32 && u >= 4) launch((k_gather_b4_v4<8, 1, 4>), dim3(gx, gy8), dim3(256), 0, st, a, (uint32_t)in_bytes);
             else if (bl == 32) launch((k_gather_b4_v4<8, 1, 2>), dim3(gx, gy8), dim3(256), 0, st, a, (uint32_t)in_bytes);
             else if (bl == 64 && u >= 8) launch((k_gather_b4_w<8>), dim3(gx, gy16), dim3(256), 0, st, a, (uint32_t)in_bytes);
@@ -2336,7 +2444,7 @@ bool launch_bwd_fused(const GatherPlan &p, const ScaleView &sc, const float *gT,
     return true;
 }
 
-void launch_sddmm_b4(const Block4Plan &p, const uint32_t *, const float *xT, const float *gT,
+void launch_sddmm_b4(const Block4Plan &p, const B4Ranges *rng, const float *xT, const float *gT,
                      int64_t B, float *gw, hipStream_t st) {
     if (p.nseg == 0) return;
     ProfScope ps("sddmm_b4", st);
@@ -2346,6 +2454,18 @@ void launch_sddmm_b4(const Block4Plan &p, const uint32_t *, const float *xT, con
         aligned16(gw)) {
         const dim3 grid(blocks_for(p.nseg)), block(256);
         const int64_t nq = B / 4;
+        if (rng && rng->K >= 1 && rng->tcol && rng->start) {
+            const int64_t nruns = rng->K * rng->brows;
+            SRArgs r{rng->tcol, rng->start, nruns, rng->brows, p.rows, xT, gT, B, gw};
+            const dim3 rgrid(blocks_for(nruns));
+            if (nq <= 4) launch((k_sddmm_b4_rng<4, 1>), rgrid, block, 0, st, r, (uint32_t)gT_bytes);
+            else if (nq <= 8) launch((k_sddmm_b4_rng<8, 1>), rgrid, block, 0, st, r, (uint32_t)gT_bytes);
+            else if (nq <= 16) launch((k_sddmm_b4_rng<16, 1>), rgrid, block, 0, st, r, (uint32_t)gT_bytes);
+            else if (nq <= 32) launch((k_sddmm_b4_rng<16, 2>), rgrid, block, 0, st, r, (uint32_t)gT_bytes);
+            else launch((k_sddmm_b4_rng<16, 4>), rgrid, block, 0, st, r, (uint32_t)gT_bytes);
+            SILI_HIP(hipGetLastError());
+            return;
+        }
         const int use_mfma = env_int("SILI_B4_MFMA", 0);  // (knobs read per call)
         if (use_mfma && nq >= 8) {
             if (nq <= 16) launch((k_sddmm_b4_mfma<1, 2>), grid, block, 0, st, a, (uint32_t)gT_bytes);

@@ -135,6 +135,13 @@ struct DBlock4 {
     // column-block copies (as DScatter::cblk, in block columns of cblk_cbb)
     std::vector<DBlock4> cblk;
     int64_t cblk_cbb = 0;
+    // the tiles by column range (built on first use, kept until the structure
+    // changes): each tile's block column, and for range x of rng_k and block
+    // row br the first tile of the row in that range, rng_start[x*brows + br]
+    // (x = rng_k: the row's end)
+    DevBuf<uint32_t> rng_col, rng_start;
+    int64_t rng_k = 0;
+    B4Ranges ranges() const { return B4Ranges{rng_col.p, rng_start.p, rng_k, brows}; }
     Block4Plan plan() const {
         return Block4Plan{seg.p, nseg, idx.p, tiles.p, rows, cols, has_split};
     }
@@ -469,6 +476,8 @@ void device_sort_pairs_u64(Layer &L, const uint64_t *kin, uint64_t *kout, const 
 // block columns).
 void build_colblocks(Layer &L, DScatter &s, int K, int64_t cb);
 void build_colblocks_b4(Layer &L, DBlock4 &b, int K, int64_t cbb);
+// b.rng_* for K column ranges of ceil(bcols / K) block columns.
+void ensure_col_ranges(Layer &L, DBlock4 &b, int K);
 // Block4 contribution (added into out) in column-block passes when the
 // gathered operand exceeds 4 MiB (slices of SILI_COLBLOCK_B4_MB, default 8);
 // false: not applicable (then use launch_gather_b4).

@@ -1171,6 +1171,7 @@ bool patch_block_row(Layer &L, const BlockRowState &old, const BlockRowState &nu
         L.B4.cblk_cbb = 0;
         L.B4t.cblk.clear();
         L.B4t.cblk_cbb = 0;
+        L.B4.rng_k = L.B4t.rng_k = 0;
         if (dB.split_maybe_changed) refresh_split_b4(L, L.B4);
         if (dBt.split_maybe_changed) refresh_split_b4(L, L.B4t);
     }
@@ -1242,6 +1243,7 @@ void patch_blocks_rebuild_shadows(Layer &L, const std::vector<const PendingBlock
     }
     if (!b_new.empty()) {
         swap_store(L.B4, L.sp_B4, true, nullptr);
+        L.B4.rng_k = 0;
         L.B4.nbytes += dB.dbytes;
         L.B4.ntiles += dB.delems;
         L.B4.nseg += dB.dseg;
