@@ -640,7 +640,7 @@ def run_config4(a, hip, api, rt):
             alg[d["name"]] = (info["nnz_scattered"] + info["index_bytes"] + 8 * (d["n_out"] + 1)
                               + 4 * (d["n_in"] + d["n_out"]) + 4 * B * (d["n_in"] + d["n_out"]))
         step_bytes = sum(alg.values())
-        gath = {k: v for k, v in kern.items() if k.split(":")[-1] in ("gather", "stream", "stream_lds")}
+        gath = {k: v for k, v in kern.items() if k.split(":")[-1] in ("gather", "stream", "stream_lds", "gather_staged")}
         dom = max(gath.items(), key=lambda kv: kv[1])
         dom_layer = dom[0].split(":")[0]
         ach = alg[dom_layer] / (dom[1] * 1e-3) / 1e9

@@ -386,6 +386,7 @@ void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64
     dst.stream1.valid = dst.streamK.valid = false;
     dst.fidx.valid = false;
     dst.dcol_valid = false;
+    dst.slc_w = 0;
     dst.stream1.failed = dst.streamK.failed = false;
     dst.cblk.clear();
     dst.cblk_cb = 0;
@@ -437,6 +438,7 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
     dst.stream1.failed = dst.streamK.failed = false;
     dst.fidx.valid = false;
     dst.dcol_valid = false;
+    dst.slc_w = 0;
     dst.cblk.clear();
     dst.cblk_cb = 0;
     dst.rows = src.cols;

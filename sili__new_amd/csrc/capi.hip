@@ -419,11 +419,14 @@ void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st
     const int skip = L.has_nonfinite ? SKIP_ZERO : SKIP_NONE;
     const ScaleView ssc = shadow_scales(L);
     const bool str = L.Wt.nnz > 0 && stream_wanted(L.Wt, ssc, B, B, skip);
-    const bool plain = L.Wt.nnz > 0 && !str && colblock_passes(L.Wt, xT, B) == 0;
+    // batches 65..128: the input staged in LDS slice by slice (SILI_STAGED)
+    const bool staged = L.Wt.nnz > 0 && !str && env_int("SILI_STAGED", 1) && staged_supported(L, L.Wt, ssc, xT, B, skip);
+    const bool plain = L.Wt.nnz > 0 && !str && !staged && colblock_passes(L.Wt, xT, B) == 0;
     if (L.Wt.nnz == 0) prep.fill(y, B * L.n_out, 0.0f);
     else if (plain) prep.zero_split(L.Wt.plan(), y, L.n_out, B);
     prep.run();
     if (str) stream_gather(L, L.Wt, ssc, xT, B, y, L.n_out, st);
+    else if (staged) launch_gather_staged(L, L.Wt, ssc, xT, B, y, L.n_out, st);
     else if (plain) launch_gather(L.Wt.plan(), ssc, xT, B, y, L.n_out, B, skip, st);
     else if (L.Wt.nnz > 0 && !gather_colblocked(L, L.Wt, ssc, xT, B, y, L.n_out, skip, st))
         throw_error(SILI_ERR_RUNTIME, "forward_dense: column-block passes did not apply (internal error)");

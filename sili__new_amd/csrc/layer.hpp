@@ -109,6 +109,13 @@ struct DScatter {
     // random access (built on first use)
     DevBuf<uint8_t> dcol;
     bool dcol_valid = false;
+    // the synapses by input slice for the staged-input gather (built on first
+    // use): each synapse's column within its slice of slc_w columns, and per
+    // row the first synapse of each of the slc_n slices (rows x (slc_n + 1));
+    // slc_w == 0: not built
+    DevBuf<uint8_t> slc_col;
+    DevBuf<uint32_t> slc_off;
+    int64_t slc_w = 0, slc_n = 0;
     // column-block copies for gathers whose operand exceeds one XCD's L2:
     // cblk[k] holds every row's entries with columns in [k*cblk_cb, ...),
     // columns relative to the block (built on first use)
@@ -296,6 +303,7 @@ struct Layer {
     DevBuf<float> acc_in, acc_grad;
     // per-call workspace (grown on demand)
     DevBuf<float> ws_xT, ws_gT, ws_out;
+    DevBuf<float> ws_xs;  // the staged-input gather's column-scaled input copy
     int64_t xT_cached_batch = 0;  // > 0: ws_xT holds the last forward_dense input, feature-major
     Scratch scratch;
     Profiler prof;
@@ -476,6 +484,11 @@ void device_sort_pairs_u64(Layer &L, const uint64_t *kin, uint64_t *kout, const 
 // block columns).
 void build_colblocks(Layer &L, DScatter &s, int K, int64_t cb);
 void build_colblocks_b4(Layer &L, DBlock4 &b, int K, int64_t cbb);
+// The staged-input gather (staged.hip): whether it takes this case, and
+// out[b, r] for every row r of s (written, not added).
+bool staged_supported(const Layer &L, const DScatter &s, const ScaleView &sc, const float *in, int64_t B, int skip);
+void launch_gather_staged(Layer &L, DScatter &s, const ScaleView &sc, const float *in, int64_t B, float *out,
+                          int64_t out_ld, hipStream_t st);
 // b.rng_* for K column ranges of ceil(bcols / K) block columns.
 void ensure_col_ranges(Layer &L, DBlock4 &b, int K);
 // Block4 contribution (added into out) in column-block passes when the

@@ -22,8 +22,10 @@ def synthetic(hip, n_in, n_out, keep, seed):
 
 
 @pytest.mark.parametrize("B,passes", [(32, 1), (64, 1), (128, 4), (256, 8)])
-def test_forward_column_blocks(hip, B, passes):
+def test_forward_column_blocks(hip, monkeypatch, B, passes):
     # shadow columns = n_in = 16384: operand 64 KiB per batch column
+    # (batches 65..128 take the staged-input gather unless it is switched off)
+    monkeypatch.setenv("SILI_STAGED", "0")
     H, L = synthetic(hip, 16384, 300, 0.4, 99)
     x = np.random.default_rng(B).normal(size=(B, 16384)).astype(np.float32)
     counts = kernel_counts(hip, L, lambda: assert_close_terms(
@@ -31,8 +33,18 @@ def test_forward_column_blocks(hip, B, passes):
     assert counts.get("fwd:gather") == passes, counts
 
 
+def test_forward_staged_at_batch_128(hip):
+    """By default batch 128 stages the input in LDS: one launch, no passes."""
+    H, L = synthetic(hip, 16384, 300, 0.4, 97)
+    x = np.random.default_rng(7).normal(size=(128, 16384)).astype(np.float32)
+    counts = kernel_counts(hip, L, lambda: assert_close_terms(
+        L.forward_dense(x), H.forward_dense(x), H.forward_dense(x, absmode=True), "staged fwd B128"))
+    assert counts.get("fwd:gather_staged") == 1 and "fwd:gather" not in counts, counts
+
+
 def test_forward_column_blocks_off(hip, monkeypatch):
     monkeypatch.setenv("SILI_COLBLOCK", "0")
+    monkeypatch.setenv("SILI_STAGED", "0")
     H, L = synthetic(hip, 16384, 300, 0.4, 98)
     x = np.random.default_rng(5).normal(size=(128, 16384)).astype(np.float32)
     counts = kernel_counts(hip, L, lambda: assert_close_terms(
