@@ -255,6 +255,10 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
                     const uint32_t *d_cols, uint32_t seg_len, bool emit_empty,
                     DevBuf<uint32_t> &byte_start, DevBuf<uint32_t> &elem_start, DevBuf<uint8_t> &idx,
                     DevBuf<SegDesc> &seg, const char *what, DevBuf<uint32_t> *split_rows = nullptr) {
+    // Two host round trips: the index stream's size (its buffer is allocated
+    // to it) with the input check, then every count at the end.  The work
+    // items and the split-row list are allocated to their bounds (a row of
+    // b index bytes holds at most b / (seg_len - 4) + 1 work items).
     Encoded out;
     hipStream_t st = L.stream;
     TmpBuf<uint64_t> len(L, SILI_TMPKEY(len)), pos(L, SILI_TMPKEY(pos));
@@ -268,13 +272,15 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
                            len.p, rowid.p, L.scratch.flag.p);
         SILI_HIP(hipGetLastError());
     }
-    check_flag(L, L.scratch.flag.p, what);
     // pos = exclusive scan of len (N+1 entries: pos[N] = total)
     SILI_HIP(hipMemsetAsync(len.p + N, 0, sizeof(uint64_t), st));
     device_exclusive_scan_u64(L, len.p, pos.p, N + 1);
     uint64_t total = 0;
+    int bad = 0;
     SILI_HIP(hipMemcpyAsync(&total, pos.p + N, sizeof(uint64_t), hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipMemcpyAsync(&bad, L.scratch.flag.p, sizeof(int), hipMemcpyDeviceToHost, st));
     SILI_HIP(hipStreamSynchronize(st));
+    if (bad) throw_error(1, std::string(what) + (bad & 2 ? ": duplicate entries" : ": malformed input (unsorted, duplicate or out-of-range index)"));
     if (total >= (1ull << 32)) throw_error(2, std::string(what) + ": index stream exceeds 4 GiB");
     out.nbytes = (int64_t)total;
     idx.ensure((size_t)total + 64);
@@ -295,42 +301,42 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
     SILI_HIP(hipGetLastError());
     SILI_HIP(hipMemsetAsync(segcnt.p + rows, 0, sizeof(uint32_t), st));
     device_exclusive_scan_u32(L, segcnt.p, segoff.p, rows + 1);
-    uint32_t nseg = 0, empty = 0;
-    SILI_HIP(hipMemcpyAsync(&nseg, segoff.p + rows, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipMemcpyAsync(&empty, n_empty.p, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipStreamSynchronize(st));
-    out.nseg = nseg;
-    out.n_empty_rows = empty;
-    seg.ensure((size_t)nseg + 1);
+    const int64_t seg_max = rows + (int64_t)(total / (seg_len - 4u)) + 1;
+    seg.ensure((size_t)seg_max + 1);
     zero_flag(L);
     if (rows > 0) {
         launch(k_seg_write, dim3(nblk(rows)), dim3(TPB), 0, st, d_ptrs, rows, byte_start.p,
                            d_cols, pos.p, segoff.p, seg_len, emit_empty ? 1 : 0, seg.p, L.scratch.flag.p);
         SILI_HIP(hipGetLastError());
     }
-    int split = 0;
-    SILI_HIP(hipMemcpyAsync(&split, L.scratch.flag.p, sizeof(int), hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipStreamSynchronize(st));
-    out.has_split = split != 0;
-    if (out.has_split && split_rows) {
-        // list of the rows that span several work items (their outputs need
-        // zeroing before the atomically combined partial sums)
-        TmpBuf<uint32_t> flag(L, SILI_TMPKEY(flag)), fpos(L, SILI_TMPKEY(fpos));
+    TmpBuf<uint32_t> fpos(L, SILI_TMPKEY(fpos));
+    if (split_rows) {
+        // the rows that span several work items (their outputs need zeroing
+        // before the atomically combined partial sums), listed whether or not
+        // there are any
+        TmpBuf<uint32_t> flag(L, SILI_TMPKEY(flag));
         flag.ensure((size_t)rows + 1);
         fpos.ensure((size_t)rows + 1);
         launch(k_split_flags, dim3(nblk(rows + 1)), dim3(TPB), 0, st, (const uint32_t *)segcnt.p, rows, flag.p);
         SILI_HIP(hipGetLastError());
         device_exclusive_scan_u32(L, flag.p, fpos.p, rows + 1);
-        uint32_t ns = 0;
-        SILI_HIP(hipMemcpyAsync(&ns, fpos.p + rows, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-        SILI_HIP(hipStreamSynchronize(st));
-        split_rows->ensure((size_t)ns + 1);
+        split_rows->ensure((size_t)rows + 1);
         launch(k_split_list, dim3(nblk(rows)), dim3(TPB), 0, st, (const uint32_t *)flag.p, (const uint32_t *)fpos.p,
                rows, split_rows->p);
         SILI_HIP(hipGetLastError());
-        SILI_HIP(hipStreamSynchronize(st));
-        out.n_split = ns;
     }
+    uint32_t nseg = 0, empty = 0, ns = 0;
+    int split = 0;
+    SILI_HIP(hipMemcpyAsync(&nseg, segoff.p + rows, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipMemcpyAsync(&empty, n_empty.p, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipMemcpyAsync(&split, L.scratch.flag.p, sizeof(int), hipMemcpyDeviceToHost, st));
+    if (split_rows) SILI_HIP(hipMemcpyAsync(&ns, fpos.p + rows, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+    SILI_HIP(hipStreamSynchronize(st));
+    if ((int64_t)nseg > seg_max) throw_error(3, std::string(what) + ": work items exceed their bound (internal error)");
+    out.nseg = nseg;
+    out.n_empty_rows = empty;
+    out.has_split = split != 0;
+    if (out.has_split && split_rows) out.n_split = ns;
     return out;
 }
 
