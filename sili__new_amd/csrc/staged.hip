@@ -246,9 +246,14 @@ __global__ __launch_bounds__(SL_WAVES * 64) void k_gather_staged(StArgs a) {
 
 }  // namespace
 
+// Also: at least one synapse per (row, slice) on average -- the slice copy's
+// offsets take 4 bytes per (row, slice), and each row pays a fixed cost per
+// slice, so a wide and very sparse layer stays on the segment gather.
 bool staged_supported(const Layer &L, const DScatter &s, const ScaleView &sc, const float *in, int64_t B, int skip) {
+    const int64_t S = (s.cols + SL_W - 1) / SL_W;
     return s.nnz > 0 && s.nnz < (int64_t(1) << 32) && B > 64 && B <= (int64_t)SL_B && B % 4 == 0 &&
-           sc.rank == 1 && skip == SKIP_NONE && (reinterpret_cast<uintptr_t>(in) & 15u) == 0;
+           sc.rank == 1 && skip == SKIP_NONE && (reinterpret_cast<uintptr_t>(in) & 15u) == 0 &&
+           s.rows * (S + 1) <= s.nnz;
 }
 
 void ensure_slices(Layer &L, DScatter &s, hipStream_t st) {

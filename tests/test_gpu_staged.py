@@ -81,3 +81,22 @@ def test_staged_forward_after_structure_changes(hip, monkeypatch):
     agree("after a synaptogenesis step")
     L.synapto_step(0.5, e, e, np.zeros(0, np.float32))
     agree("after pruning half")
+
+
+def test_wide_sparse_layer_stays_on_segment_gather(hip):
+    """Fewer synapses than (row, slice) pairs: no slice copy, the segment
+    gather runs, and the result matches the oracle."""
+    from tests.test_gpu_stream import kernel_counts
+    n_in, n_out = 20000, 40
+    rng = np.random.default_rng(11)
+    keep = rng.random((n_in, n_out)) < 0.0005  # ~400 synapses; 40 rows x 80 slices
+    ptrs = np.concatenate([[0], np.cumsum(keep.sum(1))]).astype(np.int32)
+    cols = np.nonzero(keep)[1].astype(np.int32)
+    q = rng.normal(0, 0.5, len(cols)).astype(np.float32)
+    H = HostLayer(n_in, n_out).load_csr(ptrs, cols, w=q)
+    L = hip.SparseLinearLayer(n_in, n_out, len(cols) + 64)
+    L.load_weights(ptrs, cols, q)
+    x = rng.normal(size=(128, n_in)).astype(np.float32)
+    counts = kernel_counts(hip, L, lambda: assert_close_terms(
+        L.forward_dense(x), H.forward_dense(x), H.forward_dense(x, absmode=True), "wide sparse B128"))
+    assert "fwd:gather_staged" not in counts and "fwd:slices" not in counts, counts
