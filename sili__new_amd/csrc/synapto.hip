@@ -115,7 +115,7 @@ struct SelState {
     unsigned long long prefix;  // the high bits of the threshold fixed so far
     unsigned long long need;    // keys still to take at or above the prefix
     unsigned long long less;    // keys below the prefix
-    unsigned long long pad;
+    unsigned long long pad;     // keys in the chosen bin (after the last level: the ties)
 };
 
 // Histogram of bits [shift, shift + width) of the keys below `limit` whose
@@ -189,6 +189,7 @@ __global__ __launch_bounds__(TPB) void k_sel_find(const uint32_t *__restrict__ h
                 st->prefix = (st->prefix << width) | b;
                 st->need = need - c;
                 st->less += c;
+                st->pad = h;  // at the last level: the keys equal to the threshold
                 break;
             }
             c += h;
@@ -198,28 +199,65 @@ __global__ __launch_bounds__(TPB) void k_sel_find(const uint32_t *__restrict__ h
 
 // Per slot: (below t) in the low word, (equal to t) in the high word, for
 // one scan that places both; dead slots (0xFFFFFFFF) are neither.
-__global__ void k_sel_flags(const uint32_t *__restrict__ absw, int64_t M, const SelState *__restrict__ st,
-                            uint64_t *__restrict__ flags) {
-    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
-    if (i > M) return;
-    const uint32_t t = (uint32_t)st->prefix;
+// The selection's compaction in slot order without a scan over the slots:
+// k_sel_count writes each block's (below, at) counts packed in one word,
+// an exclusive scan over the blocks gives their offsets, and k_sel_place
+// puts each slot below the threshold into order[] and each slot at it into
+// the tie list (with its key), ranked within its block by wave ballots.
+__device__ __forceinline__ void sel_flags(const uint32_t *absw, int64_t M, uint32_t t, int64_t i, bool &lo, bool &eq) {
     const uint32_t v = i < M ? absw[i] : 0xFFFFFFFFu;
-    flags[i] = (uint64_t)(v < t) | ((uint64_t)(v == t) << 32);
+    lo = i < M && v < t;
+    eq = i < M && v == t;
 }
-
-// Slots below t to order[] (slot order), slots at t to the tie list.
-__global__ void k_sel_scatter(const uint32_t *__restrict__ absw, const uint64_t *__restrict__ rc, int64_t M,
-                              const SelState *__restrict__ st, const uint64_t *__restrict__ pos,
-                              uint32_t *__restrict__ order, uint32_t *__restrict__ tie_idx,
-                              uint64_t *__restrict__ tie_key) {
+__global__ void k_sel_count(const uint32_t *__restrict__ absw, int64_t M, const SelState *__restrict__ st,
+                            uint64_t *__restrict__ bcnt) {
+    __shared__ uint32_t s_lo[TPB / 64], s_eq[TPB / 64];
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;  // every lane reaches the ballots
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    bool lo, eq;
+    sel_flags(absw, M, (uint32_t)st->prefix, i, lo, eq);
+    const unsigned long long mlo = __ballot(lo), meq = __ballot(eq);
+    if (lane == 0) {
+        s_lo[wave] = (uint32_t)__popcll(mlo);
+        s_eq[wave] = (uint32_t)__popcll(meq);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t a = 0, b = 0;
+        for (uint32_t w = 0; w < TPB / 64; ++w) {
+            a += s_lo[w];
+            b += s_eq[w];
+        }
+        bcnt[blockIdx.x] = a | (b << 32);
+    }
+}
+__global__ void k_sel_place(const uint32_t *__restrict__ absw, const uint64_t *__restrict__ rc, int64_t M,
+                            const SelState *__restrict__ st, const uint64_t *__restrict__ boff,
+                            uint32_t *__restrict__ order, uint32_t *__restrict__ tie_idx,
+                            uint64_t *__restrict__ tie_key) {
+    __shared__ uint32_t s_lo[TPB / 64], s_eq[TPB / 64];
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
-    if (i >= M) return;
-    const uint32_t t = (uint32_t)st->prefix, v = absw[i];
-    const uint64_t p = pos[i];
-    if (v < t) order[(uint32_t)p] = (uint32_t)i;
-    else if (v == t) {
-        tie_idx[p >> 32] = (uint32_t)i;
-        tie_key[p >> 32] = rc[i];
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    bool lo, eq;
+    sel_flags(absw, M, (uint32_t)st->prefix, i, lo, eq);
+    const unsigned long long mlo = __ballot(lo), meq = __ballot(eq);
+    if (lane == 0) {
+        s_lo[wave] = (uint32_t)__popcll(mlo);
+        s_eq[wave] = (uint32_t)__popcll(meq);
+    }
+    __syncthreads();
+    const uint64_t base = boff[blockIdx.x];
+    uint64_t plo = (uint32_t)base, peq = base >> 32;
+    for (uint32_t w = 0; w < wave; ++w) {
+        plo += s_lo[w];
+        peq += s_eq[w];
+    }
+    const unsigned long long below = (1ull << lane) - 1ull;
+    if (lo) order[plo + (uint64_t)__popcll(mlo & below)] = (uint32_t)i;
+    if (eq) {
+        const uint64_t p = peq + (uint64_t)__popcll(meq & below);
+        tie_idx[p] = (uint32_t)i;
+        tie_key[p] = rc[i];
     }
 }
 
@@ -566,26 +604,25 @@ void select_smallest(Layer &L, const uint32_t *absw, const uint64_t *rc, int64_t
     const SelState s0{0ull, (unsigned long long)k, 0ull, 0ull};
     SILI_HIP(hipMemcpyAsync(state.p, &s0, sizeof(s0), hipMemcpyHostToDevice, st));
     radix_select<uint32_t>(L, absw, M, ABSW_LIMIT, ABSW_BITS, state.p, hist, true);
-    TmpBuf<uint64_t> flags(L, SILI_TMPKEY(flags)), pos(L, SILI_TMPKEY(pos));
-    flags.ensure((size_t)M + 1);
-    pos.ensure((size_t)M + 1);
-    launch(k_sel_flags, dim3(nblk(M + 1)), dim3(TPB), 0, st, absw, M, (const SelState *)state.p, flags.p);
-    SILI_HIP(hipGetLastError());
-    device_exclusive_scan_u64(L, flags.p, pos.p, M + 1);
     SelState sf{};
-    uint64_t tot = 0;
     SILI_HIP(hipMemcpyAsync(&sf, state.p, sizeof(SelState), hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipMemcpyAsync(&tot, pos.p + M, sizeof(uint64_t), hipMemcpyDeviceToHost, st));
     SILI_HIP(hipStreamSynchronize(st));
-    const int64_t less = (int64_t)(uint32_t)tot, ties = (int64_t)(tot >> 32), take = k - less;
-    if ((int64_t)sf.less != less || (int64_t)sf.need != take || take < 1 || take > ties)
+    const int64_t less = (int64_t)sf.less, ties = (int64_t)sf.pad, take = k - less;
+    if ((int64_t)sf.need != take || take < 1 || take > ties)
         throw_error(SILI_ERR_RUNTIME, "synapto: selection of the smallest synapses is inconsistent");
     TmpBuf<uint32_t> tie_idx(L, SILI_TMPKEY(tie_idx)), tflag(L, SILI_TMPKEY(tflag)), tpos(L, SILI_TMPKEY(tpos));
     TmpBuf<uint64_t> tie_key(L, SILI_TMPKEY(tie_key));
+    TmpBuf<uint64_t> bcnt(L, SILI_TMPKEY(bcnt)), boff(L, SILI_TMPKEY(boff));
     tie_idx.ensure((size_t)ties + 1);
     tie_key.ensure((size_t)ties + 1);
-    launch(k_sel_scatter, dim3(nblk(M)), dim3(TPB), 0, st, absw, rc, M, (const SelState *)state.p,
-           (const uint64_t *)pos.p, order, tie_idx.p, tie_key.p);
+    const int64_t nb = nblk(M);
+    bcnt.ensure((size_t)nb + 1);
+    boff.ensure((size_t)nb + 1);
+    launch(k_sel_count, dim3((unsigned)nb), dim3(TPB), 0, st, absw, M, (const SelState *)state.p, bcnt.p);
+    SILI_HIP(hipGetLastError());
+    device_exclusive_scan_u64(L, bcnt.p, boff.p, nb);
+    launch(k_sel_place, dim3((unsigned)nb), dim3(TPB), 0, st, absw, rc, M, (const SelState *)state.p,
+           (const uint64_t *)boff.p, order, tie_idx.p, tie_key.p);
     SILI_HIP(hipGetLastError());
     if (take == ties) {
         launch(k_copy_u32, dim3(nblk(take)), dim3(TPB), 0, st, (const uint32_t *)tie_idx.p, take, order + less);
