@@ -277,9 +277,10 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
     device_exclusive_scan_u64(L, len.p, pos.p, N + 1);
     uint64_t total = 0;
     int bad = 0;
-    SILI_HIP(hipMemcpyAsync(&total, pos.p + N, sizeof(uint64_t), hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipMemcpyAsync(&bad, L.scratch.flag.p, sizeof(int), hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipStreamSynchronize(st));
+    ReadBack rb(L);
+    rb.add(&total, pos.p + N, sizeof(uint64_t));
+    rb.add(&bad, L.scratch.flag.p, sizeof(int));
+    rb.wait();
     if (bad) throw_error(1, std::string(what) + (bad & 2 ? ": duplicate entries" : ": malformed input (unsorted, duplicate or out-of-range index)"));
     if (total >= (1ull << 32)) throw_error(2, std::string(what) + ": index stream exceeds 4 GiB");
     out.nbytes = (int64_t)total;
@@ -327,11 +328,11 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
     }
     uint32_t nseg = 0, empty = 0, ns = 0;
     int split = 0;
-    SILI_HIP(hipMemcpyAsync(&nseg, segoff.p + rows, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipMemcpyAsync(&empty, n_empty.p, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipMemcpyAsync(&split, L.scratch.flag.p, sizeof(int), hipMemcpyDeviceToHost, st));
-    if (split_rows) SILI_HIP(hipMemcpyAsync(&ns, fpos.p + rows, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipStreamSynchronize(st));
+    rb.add(&nseg, segoff.p + rows, sizeof(uint32_t));
+    rb.add(&empty, n_empty.p, sizeof(uint32_t));
+    rb.add(&split, L.scratch.flag.p, sizeof(int));
+    if (split_rows) rb.add(&ns, fpos.p + rows, sizeof(uint32_t));
+    rb.wait();
     if ((int64_t)nseg > seg_max) throw_error(3, std::string(what) + ": work items exceed their bound (internal error)");
     out.nseg = nseg;
     out.n_empty_rows = empty;
@@ -347,7 +348,7 @@ void device_exclusive_scan_u64(Layer &L, const uint64_t *in, uint64_t *out, int6
     size_t bytes = 0;
     SILI_HIP(rocprim::exclusive_scan(nullptr, bytes, in, out, uint64_t(0), (size_t)n,
                                      rocprim::plus<uint64_t>(), L.stream));
-    L.scratch.temp.ensure(bytes + 16);
+    L.scratch.temp_for(bytes);
     SILI_HIP(rocprim::exclusive_scan(L.scratch.temp.p, bytes, in, out, uint64_t(0), (size_t)n,
                                      rocprim::plus<uint64_t>(), L.stream));
 }
@@ -355,7 +356,7 @@ void device_exclusive_scan_u32(Layer &L, const uint32_t *in, uint32_t *out, int6
     size_t bytes = 0;
     SILI_HIP(rocprim::exclusive_scan(nullptr, bytes, in, out, uint32_t(0), (size_t)n,
                                      rocprim::plus<uint32_t>(), L.stream));
-    L.scratch.temp.ensure(bytes + 16);
+    L.scratch.temp_for(bytes);
     SILI_HIP(rocprim::exclusive_scan(L.scratch.temp.p, bytes, in, out, uint32_t(0), (size_t)n,
                                      rocprim::plus<uint32_t>(), L.stream));
 }
@@ -364,7 +365,7 @@ void device_sort_pairs_u32(Layer &L, const uint32_t *kin, uint32_t *kout, const 
     size_t bytes = 0;
     SILI_HIP(rocprim::radix_sort_pairs(nullptr, bytes, kin, kout, vin, vout, (size_t)n, 0u,
                                        (unsigned)bits, L.stream));
-    L.scratch.temp.ensure(bytes + 16);
+    L.scratch.temp_for(bytes);
     SILI_HIP(rocprim::radix_sort_pairs(L.scratch.temp.p, bytes, kin, kout, vin, vout, (size_t)n, 0u,
                                        (unsigned)bits, L.stream));
 }
@@ -373,7 +374,7 @@ void device_sort_pairs_u64(Layer &L, const uint64_t *kin, uint64_t *kout, const 
     size_t bytes = 0;
     SILI_HIP(rocprim::radix_sort_pairs(nullptr, bytes, kin, kout, vin, vout, (size_t)n, 0u,
                                        (unsigned)bits, L.stream));
-    L.scratch.temp.ensure(bytes + 16);
+    L.scratch.temp_for(bytes);
     SILI_HIP(rocprim::radix_sort_pairs(L.scratch.temp.p, bytes, kin, kout, vin, vout, (size_t)n, 0u,
                                        (unsigned)bits, L.stream));
 }

@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <array>
+#include <cstring>
 #include <map>
 #include <string>
 #include <unordered_map>
@@ -279,6 +280,15 @@ struct ProfCtx {
 struct Scratch {
     DevBuf<uint8_t> temp;    // rocprim temporary storage
     DevBuf<int> flag;        // validation flag
+    // rocprim's temporary storage for a call needing `bytes`: when it must
+    // grow it takes half again as much, so sorts that grow step by step
+    // (a layer whose synapse count rises) reallocate, and wait on hipFree,
+    // only every few steps
+    void *temp_for(size_t bytes) {
+        const size_t need = bytes + 16;
+        temp.ensure(temp.p && temp.n < need + 64 ? need + need / 2 : need);
+        return temp.p;
+    }
 };
 
 // The scale-update variants of the reference's layer classes
@@ -355,6 +365,7 @@ struct Layer {
     // the policy's row patches: pinned staging (reads in, patch content out),
     // the device copy of the patch content, and the arrays' second buffers
     PinBuf pin_rows, pin_stage, pin_patch, pin_deg, pin_acc;
+    PinBuf pin_read;  // ReadBack's staging
     // The activity accumulators as build_probes last staged them (pin_acc),
     // with its top-k selections over them (k, indices), valid while acc_epoch
     // == policy_epoch: no entry point that may change them has run since.
@@ -475,6 +486,31 @@ void dense_to_top_k_csr_device(const float *x, int64_t rows, int64_t cols, int64
 // rocprim wrappers
 void device_exclusive_scan_u64(Layer &L, const uint64_t *in, uint64_t *out, int64_t n);
 void device_exclusive_scan_u32(Layer &L, const uint32_t *in, uint32_t *out, int64_t n);
+// Small device values read back with one stream synchronization: each
+// value is copied asynchronously into pinned memory, then one wait, then the
+// values are copied out.  (A copy into pageable host memory waits for the
+// stream by itself: one round trip per value.)  At most 8 values of up to 64
+// bytes each; one ReadBack in flight per layer.
+struct ReadBack {
+    Layer &L;
+    struct Item {
+        void *dst;
+        size_t bytes;
+    } items[8];
+    int n = 0;
+    explicit ReadBack(Layer &l) : L(l) { L.pin_read.ensure(8 * 64); }
+    void add(void *dst, const void *src, size_t bytes) {
+        if (n == 8 || bytes > 64) throw_error(1, "ReadBack: too many or too large values (internal error)");
+        SILI_HIP(hipMemcpyAsync(L.pin_read.h + 64 * n, src, bytes, hipMemcpyDeviceToHost, L.stream));
+        items[n++] = Item{dst, bytes};
+    }
+    void wait() {
+        SILI_HIP(hipStreamSynchronize(L.stream));
+        for (int i = 0; i < n; ++i) std::memcpy(items[i].dst, L.pin_read.h + 64 * i, items[i].bytes);
+        n = 0;
+    }
+};
+
 void device_sort_pairs_u32(Layer &L, const uint32_t *kin, uint32_t *kout, const uint32_t *vin,
                            uint32_t *vout, int64_t n, int bits);
 void device_sort_pairs_u64(Layer &L, const uint64_t *kin, uint64_t *kout, const uint32_t *vin,

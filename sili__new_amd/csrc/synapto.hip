@@ -558,8 +558,11 @@ T read_back(const T *d, hipStream_t st) {
 int64_t compact_positions(Layer &L, const uint32_t *flag, uint32_t *pos, int64_t n) {
     if (n == 0) return 0;
     device_exclusive_scan_u32(L, flag, pos, n);
-    const uint32_t last_pos = read_back(pos + n - 1, L.stream);
-    const uint32_t last_flag = read_back(flag + n - 1, L.stream);
+    uint32_t last_pos = 0, last_flag = 0;
+    ReadBack rb(L);
+    rb.add(&last_pos, pos + n - 1, sizeof(uint32_t));
+    rb.add(&last_flag, flag + n - 1, sizeof(uint32_t));
+    rb.wait();
     return (int64_t)last_pos + last_flag;
 }
 
