@@ -177,6 +177,7 @@ __global__ void k_split_keys(const uint64_t *__restrict__ key, int64_t N, uint64
     if (i >= N) return;
     const uint64_t k = key[i];
     if (i > 0 && key[i - 1] == k) atomicOr(bad, 2);  // duplicate tile
+    if (i > 0 && key[i - 1] > k) atomicOr(bad, 4);   // merged runs out of order
     major[i] = (uint32_t)(k / minor_extent);
     minor[i] = (uint32_t)(k % minor_extent);
 }
@@ -224,6 +225,7 @@ void check_flag(Layer &L, int *d_flag, const char *what) {
     int h = 0;
     SILI_HIP(hipMemcpyAsync(&h, d_flag, sizeof(int), hipMemcpyDeviceToHost, L.stream));
     SILI_HIP(hipStreamSynchronize(L.stream));
+    if (h & 4) throw_error(3, std::string(what) + ": merged tile runs out of order (internal error)");
     if (h) throw_error(1, std::string(what) + (h & 2 ? ": duplicate entries" : ": malformed input (unsorted, duplicate or out-of-range index)"));
 }
 
@@ -377,6 +379,18 @@ void device_sort_pairs_u64(Layer &L, const uint64_t *kin, uint64_t *kout, const 
     L.scratch.temp_for(bytes);
     SILI_HIP(rocprim::radix_sort_pairs(L.scratch.temp.p, bytes, kin, kout, vin, vout, (size_t)n, 0u,
                                        (unsigned)bits, L.stream));
+}
+
+// Two sorted runs of (key, value) pairs merged into one sorted sequence.
+static void device_merge_pairs_u64(Layer &L, const uint64_t *k1, const uint64_t *k2, uint64_t *kout,
+                                   const uint32_t *v1, const uint32_t *v2, uint32_t *vout, int64_t n1,
+                                   int64_t n2) {
+    size_t bytes = 0;
+    SILI_HIP(rocprim::merge(nullptr, bytes, k1, k2, kout, v1, v2, vout, (size_t)n1, (size_t)n2,
+                            rocprim::less<uint64_t>(), L.stream));
+    void *temp = L.scratch.temp_for(bytes);
+    SILI_HIP(rocprim::merge(temp, bytes, k1, k2, kout, v1, v2, vout, (size_t)n1, (size_t)n2,
+                            rocprim::less<uint64_t>(), L.stream));
 }
 
 static int bits_for(uint64_t max_value) {
@@ -653,7 +667,7 @@ void ensure_col_ranges(Layer &L, DBlock4 &b, int K) {
 }
 
 void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_t *d_bc,
-                  const uint8_t *d_tiles, const uint8_t *d_flags) {
+                  const uint8_t *d_tiles, const uint8_t *d_flags, int64_t sorted_head) {
     hipStream_t st = L.stream;
     const int64_t brows = (L.n_in + 3) / 4, bcols = (L.n_out + 3) / 4;
     const int64_t N = n_tiles;
@@ -677,8 +691,14 @@ void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_
                                (uint64_t)mnr_ext, maj_ext, key.p, L.scratch.flag.p);
             launch(k_iota, dim3(nblk(N)), dim3(TPB), 0, st, perm_in.p, N);
             SILI_HIP(hipGetLastError());
-            device_sort_pairs_u64(L, key.p, key_sorted.p, perm_in.p, perm.p, N,
-                                  bits_for((uint64_t)maj_ext * (uint64_t)mnr_ext));
+            if (canon && sorted_head >= 0 && sorted_head <= N)
+                // two runs already in canonical order: merged, not sorted
+                // (k_split_keys flags a merge whose runs were not)
+                device_merge_pairs_u64(L, key.p, key.p + sorted_head, key_sorted.p, perm_in.p,
+                                       perm_in.p + sorted_head, perm.p, sorted_head, N - sorted_head);
+            else
+                device_sort_pairs_u64(L, key.p, key_sorted.p, perm_in.p, perm.p, N,
+                                      bits_for((uint64_t)maj_ext * (uint64_t)mnr_ext));
             launch(k_split_keys, dim3(nblk(N)), dim3(TPB), 0, st, key_sorted.p, N,
                                (uint64_t)mnr_ext, major.p, minor.p, L.scratch.flag.p);
             SILI_HIP(hipGetLastError());

@@ -427,9 +427,11 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
                   DScatter &dst);
 // Block4 store (and its shadow) from an unsorted device tile list.
 // d_flags (optional, parallel to the input tiles): the tiles' tile_is_sparse;
-// NULL: every tile encoded by its live count (a load).
+// NULL: every tile encoded by its live count (a load).  sorted_head >= 0:
+// tiles [0, sorted_head) and [sorted_head, n_tiles) are each in canonical
+// (block row, block column) order, and the canonical build merges them.
 void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_t *d_bc,
-                  const uint8_t *d_tiles, const uint8_t *d_flags = nullptr);
+                  const uint8_t *d_tiles, const uint8_t *d_flags = nullptr, int64_t sorted_head = -1);
 // Full decode of the canonical scattered store into device arrays.
 void decode_scattered(Layer &L, uint32_t *d_rows, uint32_t *d_cols);
 // Recompute has_nonfinite (code 8 anywhere, or a non-finite scale).

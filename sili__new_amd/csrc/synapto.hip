@@ -554,16 +554,25 @@ T read_back(const T *d, hipStream_t st) {
     return h;
 }
 
-// Exclusive scan of flag[0, n) into pos; returns the total.
-int64_t compact_positions(Layer &L, const uint32_t *flag, uint32_t *pos, int64_t n) {
-    if (n == 0) return 0;
+// Exclusive scan of flag[0, n) into pos; returns the total.  With n_mid:
+// also the count of flags in [0, mid), read in the same round trip.
+int64_t compact_positions(Layer &L, const uint32_t *flag, uint32_t *pos, int64_t n, int64_t mid = -1,
+                          int64_t *n_mid = nullptr) {
+    if (n == 0) {
+        if (n_mid) *n_mid = 0;
+        return 0;
+    }
     device_exclusive_scan_u32(L, flag, pos, n);
-    uint32_t last_pos = 0, last_flag = 0;
+    uint32_t last_pos = 0, last_flag = 0, at_mid = 0;
     ReadBack rb(L);
     rb.add(&last_pos, pos + n - 1, sizeof(uint32_t));
     rb.add(&last_flag, flag + n - 1, sizeof(uint32_t));
+    const bool inner = n_mid && mid >= 0 && mid < n;
+    if (inner) rb.add(&at_mid, pos + mid, sizeof(uint32_t));
     rb.wait();
-    return (int64_t)last_pos + last_flag;
+    const int64_t total = (int64_t)last_pos + last_flag;
+    if (n_mid) *n_mid = inner ? (int64_t)at_mid : total;
+    return total;
 }
 
 template <typename K>
@@ -930,7 +939,10 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
                (const uint32_t *)nt_flag.p, tflag.p);
         SILI_HIP(hipGetLastError());
     }
-    const int64_t n_tiles = compact_positions(L, tflag.p, tpos.p, MT);
+    // the surviving tiles come first, in store order, then the promoted
+    // windows in window order: two runs of canonical order
+    int64_t n_kept_tiles = 0;
+    const int64_t n_tiles = compact_positions(L, tflag.p, tpos.p, MT, T, &n_kept_tiles);
     obr.ensure((size_t)n_tiles + 1);
     obc.ensure((size_t)n_tiles + 1);
     obytes.ensure((size_t)n_tiles * 16 + 1);
@@ -949,7 +961,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
 
     build_scattered(L, L.W, n_in, n_out, n_final, fptrs.p, fcols.p, fbytes.p);
     build_shadow(L, L.W, frows.p, fcols.p, L.Wt);
-    build_block4(L, n_tiles, obr.p, obc.p, obytes.p, osparse.p);
+    build_block4(L, n_tiles, obr.p, obc.p, obytes.p, osparse.p, n_kept_tiles);
     refresh_nonfinite(L);
 
     int64_t n_promoted = n_tiles - (T - (int64_t)cnt[1]);
