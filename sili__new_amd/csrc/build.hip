@@ -38,9 +38,15 @@ __device__ __forceinline__ uint32_t row_of(const uint32_t *__restrict__ ptrs, in
 __global__ void k_entry_len(const uint32_t *__restrict__ ptrs, int64_t rows, int64_t ncols,
                             const uint32_t *__restrict__ cols, int64_t N,
                             uint64_t *__restrict__ len, uint32_t *__restrict__ rowid,
-                            int *__restrict__ bad) {
+                            int *__restrict__ bad, uint32_t *__restrict__ n_empty) {
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
-    if (i >= N) return;
+    if (i >= N) {
+        if (i == N) {  // the scan's last term and the empty-row counter start at zero
+            len[N] = 0;
+            *n_empty = 0u;
+        }
+        return;
+    }
     const uint32_t r = row_of(ptrs, rows, (uint32_t)i);
     const uint32_t c = cols[i];
     const bool first = (uint32_t)i == ptrs[r];
@@ -78,7 +84,7 @@ __global__ void k_row_starts(const uint32_t *__restrict__ ptrs, int64_t rows, in
                              const uint64_t *__restrict__ pos, uint64_t total,
                              uint32_t *__restrict__ byte_start, uint32_t *__restrict__ elem_start,
                              uint32_t seg_bytes, int emit_empty, uint32_t *__restrict__ segcnt,
-                             uint32_t *__restrict__ n_empty) {
+                             uint32_t *__restrict__ n_empty, int *__restrict__ flag) {
     const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (r > rows) return;
     const uint32_t e = ptrs[r];
@@ -88,6 +94,9 @@ __global__ void k_row_starts(const uint32_t *__restrict__ ptrs, int64_t rows, in
         const uint32_t e1 = ptrs[r + 1], n = e1 - e;
         segcnt[r] = seg_count(n, n ? pos[e1 - 1] - pos[e] : 0u, seg_bytes - 4u, emit_empty);
         if (n == 0u) atomicAdd(n_empty, 1u);
+    } else {
+        segcnt[rows] = 0u;  // the scan's last term
+        *flag = 0;          // the work-item writer's split flag
     }
 }
 
@@ -269,13 +278,13 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
     pos.ensure((size_t)N + 1);
     rowid.ensure((size_t)N + 1);
     zero_flag(L);
-    if (N > 0) {
-        launch(k_entry_len, dim3(nblk(N)), dim3(TPB), 0, st, d_ptrs, rows, ncols, d_cols, N,
-                           len.p, rowid.p, L.scratch.flag.p);
-        SILI_HIP(hipGetLastError());
-    }
+    TmpBuf<uint32_t> n_empty(L, SILI_TMPKEY(n_empty));
+    n_empty.ensure(1);
+    // len[N] and n_empty are zeroed by the length kernel's thread N
+    launch(k_entry_len, dim3(nblk(N + 1)), dim3(TPB), 0, st, d_ptrs, rows, ncols, d_cols, N, len.p, rowid.p,
+           L.scratch.flag.p, n_empty.p);
+    SILI_HIP(hipGetLastError());
     // pos = exclusive scan of len (N+1 entries: pos[N] = total)
-    SILI_HIP(hipMemsetAsync(len.p + N, 0, sizeof(uint64_t), st));
     device_exclusive_scan_u64(L, len.p, pos.p, N + 1);
     uint64_t total = 0;
     int bad = 0;
@@ -296,17 +305,14 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
                            pos.p, idx.p);
         SILI_HIP(hipGetLastError());
     }
-    TmpBuf<uint32_t> n_empty(L, SILI_TMPKEY(n_empty));
-    n_empty.ensure(1);
-    SILI_HIP(hipMemsetAsync(n_empty.p, 0, sizeof(uint32_t), st));
+    // segcnt[rows] and the split flag are zeroed by the row kernel's thread rows
     launch(k_row_starts, dim3(nblk(rows + 1)), dim3(TPB), 0, st, d_ptrs, rows, N, pos.p,
-                       total, byte_start.p, elem_start.p, seg_len, emit_empty ? 1 : 0, segcnt.p, n_empty.p);
+                       total, byte_start.p, elem_start.p, seg_len, emit_empty ? 1 : 0, segcnt.p, n_empty.p,
+                       L.scratch.flag.p);
     SILI_HIP(hipGetLastError());
-    SILI_HIP(hipMemsetAsync(segcnt.p + rows, 0, sizeof(uint32_t), st));
     device_exclusive_scan_u32(L, segcnt.p, segoff.p, rows + 1);
     const int64_t seg_max = rows + (int64_t)(total / (seg_len - 4u)) + 1;
     seg.ensure((size_t)seg_max + 1);
-    zero_flag(L);
     if (rows > 0) {
         launch(k_seg_write, dim3(nblk(rows)), dim3(TPB), 0, st, d_ptrs, rows, byte_start.p,
                            d_cols, pos.p, segoff.p, seg_len, emit_empty ? 1 : 0, seg.p, L.scratch.flag.p);
