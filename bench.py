@@ -61,41 +61,7 @@ def parse():
                         "pushed from the canonical store and gathered through the shadow store")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run 3 device-to-device copies of MIB MiB (HBM counter calibration)")
-    p.add_argument("--probe", choices=["load", "lds"], default=None,
-                   help="only run a measurement probe (sili__new_amd/probe/probes.hip): random 256-byte row "
-                        "loads through the per-CU load path, or LDS read patterns")
     return p.parse_args()
-
-
-def run_probe(kind):
-    """The probes behind the gathers' design: random 256-byte rows (c1's
-    operand: 8192 rows of 64 fp32, 1,343,538 rows read, the c1 gather's
-    loads) in the gathers' lane layouts, and the same from a 128 KiB table
-    (L2-independent); LDS read patterns of the staged-input gather."""
-    lib = C.CDLL(os.path.join(ROOT, "sili__new_amd", "libsili_probe.so"))
-    out = {"probe": kind}
-    if kind == "load":
-        lib.sili_probe_load_rows.argtypes = [C.c_int, C.c_int64, C.c_int64, C.c_int, C.POINTER(C.c_double)]
-        n = 1343538
-        for rows in (8192, 512):
-            for bl in (4, 8, 16):
-                ms = C.c_double()
-                rc = lib.sili_probe_load_rows(bl, rows, n, 10, C.byref(ms))
-                if rc:
-                    raise RuntimeError(f"load probe failed ({rc})")
-                out[f"table_{rows * 256 // 1024}KiB_bl{bl}"] = {"us": round(ms.value * 1e3, 2),
-                                                              "tb_s": round(n * 256 / (ms.value * 1e-3) / 1e12, 2)}
-    else:
-        lib.sili_probe_lds.argtypes = [C.c_int, C.c_int, C.POINTER(C.c_double)]
-        names = {0: "16-lane groups, random rows 512 B apart", 1: "the same with a 16-byte row skew",
-                 2: "32-lane halves, one row each"}
-        for mode in (0, 1, 2):
-            v = C.c_double()
-            rc = lib.sili_probe_lds(mode, 5, C.byref(v))
-            if rc:
-                raise RuntimeError(f"lds probe failed ({rc})")
-            out[names[mode]] = {"bytes_per_clk_cu": round(v.value, 1)}
-    print(json.dumps(out), flush=True)
 
 
 class Hip:
@@ -844,9 +810,6 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU: the layer is sharded by input "
                                    "rows only on paper, no multi-GPU path is built -- run with --gpus 1"}))
         sys.exit(2)
-    if a.probe:
-        run_probe(a.probe)
-        return
     if a.copy_probe:
         n = Hip().copy_probe(a.copy_probe)
         print(json.dumps({"copy_probe_bytes": n, "copies": 3}), flush=True)

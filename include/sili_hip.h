@@ -142,7 +142,10 @@ int sili_forward_dense(sili_layer *layer, const float *x, int64_t batch, float *
  * load (the segment gathers), does not keep x as the stored forward input
  * (a following backward_dense must pass x), records no profiler events, and
  * shares the scratch with every other call on the same GPU: calls that overlap
- * on one GPU race. */
+ * on one GPU race.  While synap_row_step / synap_step edits are still pending
+ * on the layer (they are written by the next other entry point, and writing
+ * them allocates), it returns SILI_ERR_INVALID without computing anything:
+ * call sili_synchronize first. */
 int sili_forward_dense_noalloc(sili_layer *layer, const float *x, int64_t batch, float *y,
                                void *stream);
 

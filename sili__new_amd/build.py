@@ -5,7 +5,6 @@
 Outputs (git-ignored, shipped with the tree to the GPU box):
     sili__new_amd/libsili_hip.so              HIP kernels + C ABI (include/sili_hip.h)
     sili__new_amd/_sili_hip<ext-suffix>.so    pybind11 module over the C ABI
-    sili__new_amd/libsili_probe.so            measurement probes (bench.py --probe)
 Intermediate objects go to sili__new_amd/_build/.
 
 Every HIP translation unit is compiled with packed-FP32 instructions disabled
@@ -26,7 +25,6 @@ REPO = PKG.parent
 CSRC = PKG / "csrc"
 OUT = PKG / "_build"
 LIB = PKG / "libsili_hip.so"
-PROBE_LIB = PKG / "libsili_probe.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("SILI_OFFLOAD_ARCH", "gfx950")
 
@@ -91,17 +89,9 @@ def build_binding(verbose: bool = False) -> Path:
     return out
 
 
-def build_probes(verbose: bool = False) -> Path:
-    tmp = PROBE_LIB.with_suffix(".so.tmp")
-    _run([HIPCC, *HIP_FLAGS, "-shared", str(PKG / "probe" / "probes.hip"), "-o", str(tmp)], verbose)
-    os.replace(tmp, PROBE_LIB)
-    return PROBE_LIB
-
-
 def build(verbose: bool = False) -> None:
     build_library(verbose)
     build_binding(verbose)
-    build_probes(verbose)
 
 
 if __name__ == "__main__":

@@ -184,6 +184,27 @@ ScaleView shadow_scales(const Layer &L) {
     return ScaleView{L.os.p, L.vs.p, L.rank};
 }
 
+// The sparse-input forward and the sparse-gradient backward read component 0
+// of every scale only, whatever the rank: stored * (vs[r,0] * os[c,0])
+// (sisldo_ops.hpp:302-306,527-531 and the lr == 0 dx of
+// disldo_backward_sparse_grad).  A rank > 1 layer's component 0 is strided,
+// so it is gathered into a rank-1 pair first.
+__global__ void k_scale_comp0(const float *__restrict__ vs, const float *__restrict__ os, int64_t n_in,
+                              int64_t n_out, int rank, float *__restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n_in) out[i] = vs[i * rank];
+    else if (i < n_in + n_out) out[i] = os[(i - n_in) * rank];
+}
+ScaleView comp0_scales(Layer &L, bool shadow, hipStream_t st) {
+    if (L.rank == 1) return shadow ? shadow_scales(L) : canon_scales(L);
+    L.ws_s0.ensure((size_t)(L.n_in + L.n_out));
+    launch(k_scale_comp0, dim3(nblk(L.n_in + L.n_out)), dim3(TPB), 0, st, (const float *)L.vs.p,
+           (const float *)L.os.p, L.n_in, L.n_out, L.rank, L.ws_s0.p);
+    SILI_HIP(hipGetLastError());
+    const float *v0 = L.ws_s0.p, *o0 = L.ws_s0.p + L.n_in;
+    return shadow ? ScaleView{o0, v0, 1} : ScaleView{v0, o0, 1};
+}
+
 void rebuild_shadow(Layer &L) {
     DevBuf<uint32_t> rows, cols;
     rows.ensure((size_t)L.W.nnz + 1);
@@ -648,17 +669,17 @@ void forward_sparse(Layer &L, const int32_t *ptrs, const int32_t *idx, const flo
     const int push_mode = env_int("SILI_PUSH", 1);
     const bool sparse_enough = (double)nnz_x < 0.02 * (double)B * (double)L.n_in;
     const bool push = push_supported(L) && push_mode != 0 && (push_mode == 2 || sparse_enough);
-    if (push) launch_push_fwd(L, ptrs, idx, vals, B, canon_scales(L), y, false, st);
+    if (push) launch_push_fwd(L, ptrs, idx, vals, B, comp0_scales(L, false, st), y, false, st);
     if (!push || L.B4t.ntiles > 0) {
         L.ws_xT.ensure((size_t)(L.n_in * B));
         launch_densify_full(ptrs, idx, vals, B, L.n_in, L.ws_xT.p, nullptr, true, nnz_x, st);
     }
+    const ScaleView ssc = comp0_scales(L, true, st);
     if (!push) {
         launch_zero_split_rows(L.Wt.plan(), y, L.n_out, B, st);
-        launch_gather(L.Wt.plan(), shadow_scales(L), L.ws_xT.p, B, y, L.n_out, B, SKIP_POSZERO, st);
+        launch_gather(L.Wt.plan(), ssc, L.ws_xT.p, B, y, L.n_out, B, SKIP_POSZERO, st);
     }
-    if (L.B4t.ntiles > 0)
-        launch_gather_b4(L.B4t.plan(), shadow_scales(L), L.ws_xT.p, B, y, L.n_out, B, SKIP_POSZERO, st);
+    if (L.B4t.ntiles > 0) launch_gather_b4(L.B4t.plan(), ssc, L.ws_xT.p, B, y, L.n_out, B, SKIP_POSZERO, st);
 }
 
 void backward_sparse(Layer &L, const float *x, const int32_t *dptrs, const int32_t *didx,
@@ -672,9 +693,9 @@ void backward_sparse(Layer &L, const float *x, const int32_t *dptrs, const int32
     launch_zero_split_rows(L.W.plan(), dx, L.n_in, B, st);
     // scattered: merge-join visits only present dy entries (sisldo_ops.hpp:705-713);
     // block4: skips dy == 0 per slot (sisldo_ops.hpp:886-897)
-    launch_gather(L.W.plan(), canon_scales(L), L.ws_gT.p, B, dx, L.n_in, B, SKIP_POSZERO, st);
-    if (L.B4.ntiles > 0)
-        launch_gather_b4(L.B4.plan(), canon_scales(L), L.ws_gT.p, B, dx, L.n_in, B, SKIP_ZERO, st);
+    const ScaleView csc = comp0_scales(L, false, st);
+    launch_gather(L.W.plan(), csc, L.ws_gT.p, B, dx, L.n_in, B, SKIP_POSZERO, st);
+    if (L.B4.ntiles > 0) launch_gather_b4(L.B4.plan(), csc, L.ws_gT.p, B, dx, L.n_in, B, SKIP_ZERO, st);
 }
 
 // backward_sparse with the optimizer update (sili/cpu_backend.cpp:587-603,
@@ -968,7 +989,13 @@ int sili_forward_dense(sili_layer *layer, const float *x, int64_t batch, float *
 int sili_forward_dense_noalloc(sili_layer *layer, const float *x, int64_t batch, float *y, void *stream) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
-        set_device(layer->L);
+        // writing the policy's pending edits allocates: refused here rather
+        // than done (any other entry point, sili_synchronize included, writes
+        // them); the call only reads the layer, so the policy's caches stay
+        SILI_HIP(hipSetDevice(layer->L.device));
+        if (!layer->L.policy_pending.empty())
+            throw_error(SILI_ERR_INVALID, "forward_dense_noalloc: the layer holds pending synaptogenesis policy "
+                                          "edits, and writing them allocates; call sili_synchronize first");
         forward_dense_noalloc(layer->L, x, batch, y, pick(layer->L, stream));
     });
 }

@@ -164,19 +164,43 @@ struct PinBuf {
     PinBuf() = default;
     PinBuf(const PinBuf &) = delete;
     PinBuf &operator=(const PinBuf &) = delete;
-    ~PinBuf() { reset(); }
+    ~PinBuf() {
+        if (in_flight) (void)hipEventSynchronize(ev);
+        in_flight = false;
+        reset();
+        if (ev) (void)hipEventDestroy(ev);
+    }
     void reset() {
+        wait();
         if (h) (void)hipHostFree(h);
         h = nullptr;
         n = 0;
     }
+    // A copy queued from this buffer that nothing else waits for: mark()
+    // after queueing it, wait() before the host writes the buffer again.
+    void mark(hipStream_t st) {
+        if (!ev) SILI_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+        SILI_HIP(hipEventRecord(ev, st));
+        in_flight = true;
+    }
+    void wait() {
+        if (in_flight) {
+            in_flight = false;
+            SILI_HIP(hipEventSynchronize(ev));
+        }
+    }
     void ensure(size_t bytes) {
+        wait();
         if (h && bytes <= n) return;
         const size_t want = std::max<size_t>(bytes + bytes / 2, 1 << 16);
         reset();
         SILI_HIP(hipHostMalloc(reinterpret_cast<void **>(&h), want, hipHostMallocDefault));
         n = want;
     }
+
+   private:
+    hipEvent_t ev = nullptr;
+    bool in_flight = false;
 };
 
 // The second buffer of each array a row patch rewrites (patch.hip): the
@@ -313,6 +337,7 @@ struct Layer {
     DevBuf<float> acc_in, acc_grad;
     // per-call workspace (grown on demand)
     DevBuf<float> ws_xT, ws_gT, ws_out;
+    DevBuf<float> ws_s0;  // component 0 of rank > 1 scales: value [n_in], then output [n_out]
     DevBuf<float> ws_xs;  // the staged-input gather's column-scaled input copy
     int64_t xT_cached_batch = 0;  // > 0: ws_xT holds the last forward_dense input, feature-major
     Scratch scratch;

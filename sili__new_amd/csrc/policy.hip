@@ -637,8 +637,8 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
             for (uint32_t c : add_cols) d.e[k++] = c;
             launch(k_deg_edit_inl, dim3(1), dim3(DEG_INLINE), 0, L.stream, L.out_deg.p, d);
         } else {
-            // the edit list in pinned memory (its copy runs with the stream;
-            // the next write follows the next call's staging sync)
+            // the edit list in pinned memory; its copy runs with the stream,
+            // and the next call that writes the buffer waits for it (ensure)
             L.pin_deg.ensure((size_t)n_edit * 8);
             int32_t *ecol = reinterpret_cast<int32_t *>(L.pin_deg.h), *edelta = ecol + n_edit;
             int64_t k = 0;
@@ -653,6 +653,7 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
             TmpBuf<int32_t> dedit(L, SILI_TMPKEY(dedit));
             dedit.ensure((size_t)n_edit * 2);
             SILI_HIP(hipMemcpyAsync(dedit.p, ecol, (size_t)n_edit * 8, hipMemcpyHostToDevice, L.stream));
+            L.pin_deg.mark(L.stream);
             launch(k_deg_edit, dim3(nblk(n_edit)), dim3(TPB), 0, L.stream, L.out_deg.p, (const int32_t *)dedit.p,
                    (const int32_t *)(dedit.p + n_edit), n_edit);
         }

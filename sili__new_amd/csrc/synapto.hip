@@ -525,6 +525,17 @@ __global__ void k_tile_flags(int64_t T, const uint8_t *alive, int64_t n_win, con
 // Output tiles with their encoding (tile_is_sparse): a surviving tile keeps
 // its own unless it received an insert; inserted and promoted tiles are
 // encoded by their live count (block4.hpp:1193-1205, 1226-1290).
+// counter += 1 for each tile i > 0 (other than the second run's first) whose
+// canonical key is not above its predecessor's: runs [0, head) and
+// [head, n) must each be strictly increasing
+__global__ void k_tile_runs_order(const uint32_t *__restrict__ br, const uint32_t *__restrict__ bc, int64_t n,
+                                  int64_t head, uint64_t bcols, unsigned long long *__restrict__ bad) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i <= 0 || i >= n || i == head) return;
+    const uint64_t a = (uint64_t)br[i - 1] * bcols + bc[i - 1], b = (uint64_t)br[i] * bcols + bc[i];
+    if (a >= b) atomicAdd(bad, 1ull);
+}
+
 __global__ void k_emit_tiles(int64_t T, const uint32_t *tbr, const uint32_t *tbc, const uint8_t *tbytes,
                              const uint8_t *tsparse, const uint8_t *tins, uint32_t sp, int64_t n_win,
                              const uint32_t *nt_br, const uint32_t *nt_bc, const uint8_t *nt_bytes,
@@ -955,13 +966,23 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
                (const uint32_t *)tpos.p, obr.p, obc.p, obytes.p, osparse.p);
         SILI_HIP(hipGetLastError());
     }
+    // both tile runs strictly increasing in (block row, block column)?  Read
+    // back with the counters, before any store is replaced: a run out of
+    // order (never expected) takes the full sort instead of the merge
+    if (n_tiles > 1) {
+        launch(k_tile_runs_order, dim3(nblk(n_tiles)), dim3(TPB), 0, st, (const uint32_t *)obr.p,
+               (const uint32_t *)obc.p, n_tiles, n_kept_tiles, (uint64_t)bcols, counters.p + 3);
+        SILI_HIP(hipGetLastError());
+    }
     unsigned long long cnt[4];
     SILI_HIP(hipMemcpyAsync(cnt, counters.p, sizeof(cnt), hipMemcpyDeviceToHost, st));
     SILI_HIP(hipStreamSynchronize(st));
+    // SILI_TILE_MERGE=0 always sorts (the two paths build the same store)
+    const bool merge = cnt[3] == 0 && env_int("SILI_TILE_MERGE", 1) != 0;
 
     build_scattered(L, L.W, n_in, n_out, n_final, fptrs.p, fcols.p, fbytes.p);
     build_shadow(L, L.W, frows.p, fcols.p, L.Wt);
-    build_block4(L, n_tiles, obr.p, obc.p, obytes.p, osparse.p, n_kept_tiles);
+    build_block4(L, n_tiles, obr.p, obc.p, obytes.p, osparse.p, merge ? n_kept_tiles : -1);
     refresh_nonfinite(L);
 
     int64_t n_promoted = n_tiles - (T - (int64_t)cnt[1]);

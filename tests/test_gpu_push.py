@@ -93,10 +93,11 @@ def test_push_rank2_scales(hip):
     os_ = rng.uniform(0.5, 2.0, n_out * rank).astype(np.float32)
     L.set_value_scales(vs)
     L.set_output_scales(os_)
-    # the rank-2 scale S(r, c) = sum_k vs[r, k] os[c, k] on a dense reference
-    # of the decoded codes (unit scales)
+    # sisldo_forward reads component 0 of each scale whatever the rank,
+    # stored * (vs[r, 0] * os[c, 0]) (sisldo_ops.hpp:302-306): on a dense
+    # reference of the decoded codes (unit scales)
     dense = HostLayer(n_in, n_out).load_csr(ptrs, idx, w=w).dense().astype(np.float64)
-    S = vs.reshape(n_in, rank).astype(np.float64) @ os_.reshape(n_out, rank).astype(np.float64).T
+    S = np.outer(vs[::rank], os_[::rank]).astype(np.float32).astype(np.float64)
     xp, xi, xv = sparse_x(rng, 8, n_in, 0.2)
     X = np.zeros((8, n_in), np.float64)
     for b in range(8):
@@ -104,6 +105,10 @@ def test_push_rank2_scales(hip):
     want = X @ (dense * S)
     bound = np.abs(X) @ np.abs(dense * S)
     assert_close_terms(L.forward_sparse(xp, xi, xv, 8), want, bound, "rank 2")
+    # and the oracle's restatement agrees
+    H = HostLayer(n_in, n_out, rank).load_csr(ptrs, idx, w=w).set_scales(vs, os_)
+    assert_close_terms(L.forward_sparse(xp, xi, xv, 8), H.forward_sparse(xp, xi, xv, 8),
+                       H.forward_sparse(xp, xi, xv, 8, absmode=True), "rank 2 vs oracle")
 
 
 def test_push_nan_weight_meets_explicit_zero(hip):
