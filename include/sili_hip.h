@@ -328,8 +328,9 @@ int sili_synapto_step(sili_layer *layer, float prune_frac, const int32_t *cand_r
  * sili_equalize_to_capacity: sili/cpu_backend.cpp:684-729 (target_bytes 0:
  *   5 * target_elems + 4); SILI_ERR_NOMEM when a row's growth exceeds the
  *   budget, the rows before it grown.
- * sili_equalizer_step: the scattered half of equalizer_step
- *   (sili/cpu_backend.cpp:649-657, delta_csr_memory.hpp:295-306).
+ * sili_equalizer_step: equalizer_step (sili/cpu_backend.cpp:646-657): the
+ *   scattered store's step (delta_csr_memory.hpp:295-306), then the block4
+ *   store's (Block4Store::equalize_step, block4.hpp:1208-1220).
  * sili_export_layout: the reference's byte_start [n_in+1], byte_end [n_in],
  *   elem_start [n_in+1], elem_end [n_in]; any may be NULL. */
 int sili_compact(sili_layer *layer);
@@ -431,9 +432,40 @@ int sili_profile_read(sili_layer *layer, sili_prof_entry *out, int max_entries, 
  * tile_byte_start [ceil(n_inputs/4)+1]; any output may be NULL. */
 int sili_export_block4_packed(sili_layer *layer, uint8_t *tile_is_sparse, uint8_t *tile_data,
                               uint64_t *tile_byte_start, int64_t *nbytes);
-/* Block4View (sili/cpu_backend.cpp:43-98): the store's counters.  The device
- * store keeps no per-row tile headroom and never drops an update, so
- * alloc_bytes == used_bytes and the event counters are 0. */
+/* ---- block4 reservations (block4.hpp:1016-1031, 497-946) -----------------
+ * The device store is compact; beside it the layer keeps, per block row, the
+ * block-column index bytes, tile slots and tile bytes the reference's
+ * Block4Store would reserve, with its budgets (max_weights * 8 + 4096 and
+ * max(4, max_weights / 16) * 16 from the constructor; load_dense_codes sets
+ * its own, delta_csr_memory.hpp:884-905), under the reference's rules: a new
+ * tile (a load's or a promotion's) grows a row without room by
+ * block4_ensure_row_headroom, a growth beyond a budget is SILI_ERR_NOMEM, a
+ * tile's growth beyond the tile budget is dropped and counted
+ * (dropped_growth_events); load_dense_codes reserves 20 % + 16 bytes per row
+ * (block4_expand_headroom).  The optimizer updates write each block row back
+ * as merge_row_workspace does (block4.hpp:1367-1462): a row whose stored
+ * tiles outgrow its reserved tile bytes loses its live slots of lowest
+ * |importance code x importance_scale[row] x output_importance_scale[col]|
+ * until it fits.  sili_load_block4_tiles (no counterpart) reserves as its
+ * tiles placed one by one in canonical order would, and refuses with
+ * SILI_ERR_NOMEM what would exceed the budgets.  The bulk sili_synapto_step
+ * (no counterpart) grows a row's reservations to its content when needed.
+ * sili_expand_block4_headroom: expand_block4_headroom (sili/cpu_backend.cpp:
+ *   932-934, delta_csr_memory.hpp:767-823): tile bytes = used + (size_t)(used
+ *   * f) + 16 per block row; SILI_ERR_NOMEM beyond the tile budget (layer
+ *   unchanged).
+ * sili_compact_block4: compact_block4 (:941-943): tile bytes = used.
+ * sili_export_block4_layout: per block row [ceil(n_inputs/4)] the reserved
+ *   index bytes, tile slots and tile bytes, and the used ones; out[6]:
+ *   dropped_growth_events, row_merge_overflow_events,
+ *   row_merge_overflow_bytes_dropped, the index and tile budgets, and the
+ *   slots the updates' write-back evicted.  Any pointer may be NULL. */
+int sili_expand_block4_headroom(sili_layer *layer, float blank_fraction);
+int sili_compact_block4(sili_layer *layer);
+int sili_export_block4_layout(sili_layer *layer, uint64_t *ia, uint64_t *ea, uint64_t *ta, uint64_t *ui,
+                              uint64_t *ue, uint64_t *ut, uint64_t *out);
+/* Block4View (sili/cpu_backend.cpp:43-98): the store's counters;
+ * alloc_bytes is the sum of the block rows' reserved tile bytes. */
 typedef struct {
     int64_t tiles, synapses;
     uint32_t switch_point;

@@ -55,12 +55,24 @@ class _TrainParams(C.Structure):
 TRAIN_VARIANTS = {"plain": 0, "resync": 1, "noscale": 2}
 
 
+class _B4Merge(C.Structure):
+    _fields_ = [("tile_alloc", C.POINTER(C.c_uint64)), ("tile_sparse", C.POINTER(C.c_uint8)),
+                ("switch_point", C.c_uint32), ("evicted", C.c_uint64), ("overflow_events", C.c_uint64),
+                ("overflow_bytes", C.c_uint64)]
+
+
+class _B4Res(C.Structure):
+    _fields_ = [("ia", C.POINTER(C.c_uint64)), ("ea", C.POINTER(C.c_uint64)), ("ta", C.POINTER(C.c_uint64)),
+                ("idx_budget", C.c_uint64), ("tile_budget", C.c_uint64), ("switch_point", C.c_uint32),
+                ("flags_in", C.POINTER(C.c_uint8)), ("flags_out", C.POINTER(C.c_uint8)), ("dropped", C.c_uint64)]
+
+
 class _TrainState(C.Structure):
     _fields_ = [("value_scale", _f32p), ("vs_importance", _f32p), ("vs_momentum", _f32p),
                 ("vs_step", C.POINTER(C.c_uint32)), ("output_scale", _f32p), ("os_importance", _f32p),
                 ("os_step", C.POINTER(C.c_uint32)), ("importance_scale", _f32p),
                 ("output_importance_scale", _f32p), ("out_degree", _i32p), ("output_scale_trainable", C.c_int32),
-                ("quant_out", _f32p), ("imp_out", _f32p)]
+                ("quant_out", _f32p), ("imp_out", _f32p), ("b4", C.POINTER(_B4Merge))]
 
 
 # the constants sili/cpu_backend.cpp:496-528 passes to disldo_backward
@@ -128,6 +140,7 @@ def lib(contracted: bool = False):
                                             C.c_int, C.c_float, C.c_int64, C.c_int64, C.c_float, _i32p, _i32p, _i32p,
                                             _u8p, _i32p, _i32p, _u8p, C.POINTER(C.c_int64), _u64p, _u64p,
                                             C.POINTER(C.c_int64)]
+        L.oracle_synap_row_step2.argtypes = list(L.oracle_synap_row_step.argtypes) + [C.POINTER(_B4Res)]
         L.oracle_synapto_step.argtypes = [C.POINTER(_OracleLayerC), C.c_float, _i32p, _i32p, _f32p, _f32p,
                                           C.c_int64, C.c_int, _i32p, _i32p, _u8p, _i32p, _i32p, _u8p,
                                           C.POINTER(_SynStats)]
@@ -218,6 +231,12 @@ def reflib():
         R.ref_sll_equalize_to_capacity.argtypes = [C.c_void_p, C.c_int, C.c_int]
         R.ref_sll_equalizer_step.argtypes = [C.c_void_p]
         R.ref_layer_layout.argtypes = [C.c_void_p, _u64p, _u64p, _u64p, _u64p]
+        R.ref_block4_reservations.restype = C.c_int64
+        R.ref_block4_reservations.argtypes = [C.c_void_p] + [_u64p] * 7
+        R.ref_block4_equalize_step.argtypes = [C.c_void_p]
+        R.ref_block4_expand.argtypes = [C.c_void_p, C.c_float, C.c_int]
+        R.ref_sll_load_dense_codes.argtypes = [C.c_void_p, _u8p, _u8p]
+        R.ref_sll_put_tile.argtypes = [C.c_void_p, C.c_int, C.c_int, _u8p]
         _ref = R
     return _ref
 
@@ -477,6 +496,199 @@ class TileEncodingState:
         return np.array([self.flag[k] for k in self._keys(br, bc)], np.uint8)
 
 
+def uleb_len(v):
+    """Bytes of the unsigned LEB128 encoding of v (delta_csr_types.hpp:209-241)."""
+    n = 1
+    v = int(v)
+    while v >= 0x80:
+        v >>= 7
+        n += 1
+    return n
+
+
+def tile_len(flag, live):
+    """A tile's stored length (block4_stored_tile_len, block4.hpp:340-345,
+    386-388): sparse-packed 1 + ceil(live/2) + live, dense 16."""
+    live = int(live)
+    return 1 + (live + 1) // 2 + live if flag else 16
+
+
+def tile_len_by_live(live, switch_point=SWITCH_POINT):
+    """The length a commit gives a tile: sparse iff live <= switch_point."""
+    return tile_len(int(live) <= int(switch_point), live)
+
+
+class Block4Reservations:
+    """The reference's per-block-row reservations of its Block4Store
+    (block4.hpp:1016-1031): block-column index bytes ia[br] (block_layout
+    byte_start), tile slots ea[br] (elem_start) and tile bytes ta[br]
+    (tile_byte_start), the budgets (max_indices_bytes, max_tile_bytes), the
+    equalizer cursor and dropped_growth_events, under the calls that set
+    them.  Row contents -- used index bytes ui, tiles ue, stored tile bytes
+    ut -- are passed in by the caller.
+
+    - the layer's constructor (sili/cpu_backend.cpp:403-441): nothing
+      reserved, budgets max_weights*8+4096 and max(4, max_weights/16)*16;
+    - block4_row_insert_tile (block4.hpp:670-771): a new tile takes its
+      block-column delta change, one slot and 1 tile byte (sparse-empty) of
+      its row's room; without room get_or_create (:1170-1183) grows the row
+      by block4_ensure_row_headroom (:648-668): +5 index bytes, +1 tile
+      byte, +1 slot, through block4_row_shift (:497-617; targets clamped to
+      the row's use, index side then tile side then slot side, each growth
+      beyond its budget a MemoryError, never on the last row) or
+      block4_grow_last_row (:619-646) for the last row;
+    - a tile's commit (commit_dirty_sparse_tile, :1226-1290 ->
+      block4_resize_tile_in_row, :906-946): growth beyond the row's room
+      takes the shortfall from the buffer; beyond max_tile_bytes the commit
+      is dropped (dropped_growth_events += 1, the tile keeps its bytes);
+    - block4_load_dense (delta_csr_memory.hpp:841-945): new budgets
+      (rows*cols*16 index bytes, (size_t)(rows*cols*16 * (1.0 + 0.2f)) +
+      rows*16 tile bytes), a tile at every (br, bc) in row-major order,
+      each committed, then block4_expand_headroom(0.2);
+    - block4_expand_headroom (:767-823): ta = ut + (size_t)(ut * f) + slack,
+      the product in fp32, MemoryError beyond max_tile_bytes (nothing
+      changed); compact_block4 is f = 0, slack 0;
+    - Block4Store::equalize_step (block4.hpp:1208-1220): the cursor row
+      shifted towards the ceil-average of each reservation."""
+
+    ULEB_MAX = 5
+    NO_LIMIT = (1 << 64) - 1
+
+    def __init__(self, n_in, max_weights=None, switch_point=SWITCH_POINT):
+        self.rows = (int(n_in) + 3) // 4
+        self.ia = [0] * self.rows
+        self.ea = [0] * self.rows
+        self.ta = [0] * self.rows
+        if max_weights is None:
+            self.idx_budget = self.tile_budget = self.NO_LIMIT
+        else:
+            self.idx_budget = int(max_weights) * 8 + 4096
+            self.tile_budget = max(4, int(max_weights) // 16) * 16
+        self.sp = int(switch_point)
+        self.eq = 0
+        self.dropped = 0
+
+    # -- block4_row_shift / block4_grow_last_row / ensure_row_headroom --------
+    def _shift(self, row, ti, tt, te, ui, ue, ut):
+        ti, tt, te = max(ti, ui), max(tt, ut), max(te, ue)
+        if row + 1 >= self.rows:
+            return
+        if self.ia[row] != ti:
+            if ti > self.ia[row] and sum(self.ia) + ti - self.ia[row] > self.idx_budget:
+                raise MemoryError("block4_row_shift: index bytes beyond max_indices_bytes")
+            self.ia[row] = ti
+        if self.ta[row] != tt:
+            if tt > self.ta[row] and sum(self.ta) + tt - self.ta[row] > self.tile_budget:
+                raise MemoryError("block4_row_shift: tile bytes beyond max_tile_bytes")
+            self.ta[row] = tt
+        if self.ea[row] != te:
+            self.ea[row] = te
+
+    def _grow_last(self, ti, tt, te):
+        r = self.rows - 1
+        if ti > self.ia[r]:
+            if sum(self.ia) + ti - self.ia[r] > self.idx_budget:
+                raise MemoryError("block4_grow_last_row: index bytes beyond max_indices_bytes")
+            self.ia[r] = ti
+        if tt > self.ta[r]:
+            if sum(self.ta) + tt - self.ta[r] > self.tile_budget:
+                raise MemoryError("block4_grow_last_row: tile bytes beyond max_tile_bytes")
+            self.ta[r] = tt
+        if te > self.ea[r]:
+            self.ea[r] = te
+
+    def insert_tile(self, row, idx_delta, ui, ue, ut):
+        """get_or_create of a new tile in block row `row` whose block-column
+        delta bytes change by idx_delta; (ui, ue, ut) is the row's use
+        before.  Returns the use after (the new tile sparse-empty, 1 byte)."""
+        fits = (not (idx_delta > 0 and idx_delta > self.ia[row] - ui) and ue < self.ea[row]
+                and 1 <= self.ta[row] - ut)
+        if not fits:
+            ti, tt, te = self.ia[row] + self.ULEB_MAX, self.ta[row] + 1, self.ea[row] + 1
+            if row + 1 < self.rows:
+                self._shift(row, ti, tt, te, ui, ue, ut)
+            else:
+                self._grow_last(ti, tt, te)
+        return ui + idx_delta, ue + 1, ut + 1
+
+    def commit(self, row, old_len, new_len, ut):
+        """A tile of block row `row` re-stored from old_len to new_len bytes;
+        ut: the row's stored bytes before.  Returns (committed, ut after)."""
+        d = int(new_len) - int(old_len)
+        if d > 0:
+            room = self.ta[row] - ut
+            if d > room:
+                short = d - room
+                if sum(self.ta) + short > self.tile_budget:
+                    self.dropped += 1
+                    return False, ut
+                self.ta[row] += short
+        return True, ut + d
+
+    # -- whole-store calls -------------------------------------------------------
+    def load_dense(self, n_in, n_out, wc, ic):
+        """block4_load_dense of codes wc, ic [n_in * n_out]; returns the use
+        (ui, ue, ut) per block row."""
+        brows, bcols = (n_in + 3) // 4, (n_out + 3) // 4
+        assert brows == self.rows
+        self.ia, self.ea, self.ta = [0] * brows, [0] * brows, [0] * brows
+        self.idx_budget = brows * bcols * 16
+        self.tile_budget = int(float(brows * bcols * 16) * (1.0 + float(np.float32(0.2)))) + brows * 16
+        codes = np.zeros((brows * 4, bcols * 4), np.uint8)
+        codes[:n_in, :n_out] = (np.asarray(wc, np.uint8) | (np.asarray(ic, np.uint8) << 4)).reshape(n_in, n_out)
+        live = (codes.reshape(brows, 4, bcols, 4) != 0).sum(axis=(1, 3))
+        ui, ue, ut = [0] * brows, [0] * brows, [0] * brows
+        for br in range(brows):
+            u = (0, 0, 0)
+            for bc in range(bcols):
+                u = self.insert_tile(br, 1, *u)  # deltas 0, 1, 1, ...: one byte each
+                ok, t = self.commit(br, 1, tile_len_by_live(live[br, bc], self.sp), u[2])
+                u = (u[0], u[1], t)
+            ui[br], ue[br], ut[br] = u
+        self.expand(ut, 0.2, 16)
+        return ui, ue, ut
+
+    def expand(self, ut, f=0.2, slack=16):
+        f = np.float32(f)
+        new = [int(u) + int(np.float32(u) * f) + int(slack) for u in ut]
+        if sum(new) > self.tile_budget:
+            raise MemoryError("block4_expand_headroom beyond max_tile_bytes")
+        self.ta = new
+        return self
+
+    def compact(self, ut):
+        return self.expand(ut, 0.0, 0)
+
+    def equalize_step(self, ui, ue, ut):
+        if self.rows == 0:
+            return self
+        row = self.eq % self.rows
+        n = self.rows
+        ti = (sum(self.ia) + n - 1) // n
+        tt = (sum(self.ta) + n - 1) // n
+        te = (sum(self.ea) + n - 1) // n
+        self._shift(row, ti, tt, te, int(ui[row]), int(ue[row]), int(ut[row]))
+        self.eq = (self.eq + 1) % n
+        return self
+
+
+def block4_row_use(n_in, br, bc, tiles, flags):
+    """(ui, ue, ut) per block row of a compact block4 store (tiles sorted by
+    (br, bc)): block-column ULEB128 bytes, tiles, stored tile bytes."""
+    rows = (int(n_in) + 3) // 4
+    ui, ue, ut = [0] * rows, [0] * rows, [0] * rows
+    live = tile_live(tiles)
+    prev_r, prev_c = -1, 0
+    for i, (r, c) in enumerate(zip(np.asarray(br).tolist(), np.asarray(bc).tolist())):
+        if r != prev_r:
+            prev_r, prev_c = r, 0
+        ui[r] += uleb_len(c - prev_c)
+        prev_c = c
+        ue[r] += 1
+        ut[r] += tile_len(flags[i], live[i])
+    return ui, ue, ut
+
+
 FOR_REF_PATH = HERE / "_ref" / "libfor_ref.so"
 _for_ref = None
 
@@ -603,6 +815,13 @@ class HostLayer:
         self.importance_scale = None
         self.output_importance_scale = None
         self.output_scale_trainable = False
+        # the block rows' tile-byte reservations and the tiles' encoding, for
+        # the updates' write-back (None: rows taken to have room)
+        self.b4_alloc = None   # uint64 [ceil(n_in/4)]
+        self.b4_flags = None   # uint8 [n_tiles], tile_is_sparse in canonical order
+        self.b4res = None      # a Block4Reservations: the policy keeps it, the updates read its ta
+        self.b4_switch_point = SWITCH_POINT
+        self.b4_counters = [0, 0, 0]  # evicted slots, merge overflow events, overflow bytes
 
     # -- construction ----------------------------------------------------------
     def load_csr(self, ptrs, cols, w=None, imp=None, bytes_=None):
@@ -736,6 +955,20 @@ class HostLayer:
     def out_degree(self) -> np.ndarray:
         return np.bincount(self.decode_cols(), minlength=self.n_out).astype(np.int32)
 
+    def _b4_merge(self):
+        alloc = self.b4res.ta if self.b4res is not None else self.b4_alloc
+        if alloc is None or self.n_tiles == 0:
+            return None
+        self._b4_alloc_c = np.ascontiguousarray(np.asarray(alloc, np.uint64))
+        assert len(self.b4_flags) >= self.n_tiles
+        return _B4Merge(self._b4_alloc_c.ctypes.data_as(C.POINTER(C.c_uint64)),
+                        self.b4_flags.ctypes.data_as(C.POINTER(C.c_uint8)), int(self.b4_switch_point), 0, 0, 0)
+
+    def _b4_merged(self, m):
+        if m is not None:
+            self.b4_counters = [self.b4_counters[0] + m.evicted, self.b4_counters[1] + m.overflow_events,
+                                self.b4_counters[2] + m.overflow_bytes]
+
     def backward_train(self, x, dy, lr, lr_per_row_nnz=False, damp_by_importance=True, beta2=0.999, eps=1e-8,
                        acc=None, contracted=False, variant="plain"):
         """Backward with the optimizer update (deterministic rounding, one
@@ -755,10 +988,12 @@ class HostLayer:
         isc = None if self.importance_scale is None else _c(self.importance_scale, np.float32)
         oisc = None if self.output_importance_scale is None else _c(self.output_importance_scale, np.float32)
         u32p = C.POINTER(C.c_uint32)
+        m = self._b4_merge()
         st = _TrainState(_p(self.value_scale, _f32p), _p(self.vs_importance, _f32p), _p(self.vs_momentum, _f32p),
                          _p(self.vs_step, u32p), _p(self.output_scale, _f32p), _p(self.os_importance, _f32p),
                          _p(self.os_step, u32p), _p(isc, _f32p), _p(oisc, _f32p), _p(deg, _i32p),
-                         int(self.output_scale_trainable), _p(self.last_quant, _f32p), _p(self.last_imp, _f32p))
+                         int(self.output_scale_trainable), _p(self.last_quant, _f32p), _p(self.last_imp, _f32p),
+                         None if m is None else C.pointer(m))
         P = _TrainParams(lr, int(lr_per_row_nnz), int(damp_by_importance), beta2, eps, **TRAIN_DEFAULTS,
                          variant=TRAIN_VARIANTS[variant])
         s = self._cstruct()
@@ -769,6 +1004,7 @@ class HostLayer:
             raise ValueError("backward_train failed")
         if tiles is not None:
             self.tiles[:] = tiles
+        self._b4_merged(m)
         return dx, ai, ag
 
     def backward_sparse_train(self, x, dptrs, didx, dvals, batch, lr, lr_per_row_nnz=False, damp_by_importance=True,
@@ -786,9 +1022,11 @@ class HostLayer:
         isc = None if self.importance_scale is None else _c(self.importance_scale, np.float32)
         oisc = None if self.output_importance_scale is None else _c(self.output_importance_scale, np.float32)
         u32p = C.POINTER(C.c_uint32)
+        m = self._b4_merge()
         st = _TrainState(_p(self.value_scale, _f32p), _p(self.vs_importance, _f32p), _p(self.vs_momentum, _f32p),
                          _p(self.vs_step, u32p), _p(self.output_scale, _f32p), _p(self.os_importance, _f32p),
-                         _p(self.os_step, u32p), _p(isc, _f32p), _p(oisc, _f32p), None, 0, None, None)
+                         _p(self.os_step, u32p), _p(isc, _f32p), _p(oisc, _f32p), None, 0, None, None,
+                         None if m is None else C.pointer(m))
         P = _TrainParams(lr, int(lr_per_row_nnz), int(damp_by_importance), beta2, eps, **TRAIN_DEFAULTS, variant=0,
                          draw_mode=int(draw_mode), draw_seed=int(draw_seed) & (2**64 - 1))
         s = self._cstruct()
@@ -798,6 +1036,7 @@ class HostLayer:
                                                         _p(dx, _f32p), _p(ai, _f32p), _p(ag, _f32p),
                                                         C.byref(P)) != 0:
             raise ValueError("backward_sparse_train: tile bytes missing")
+        self._b4_merged(m)
         return dx, ai, ag
 
     # -- the reference's synaptogenesis policy (delta_csr_memory.hpp:1021-1426) --
@@ -854,16 +1093,33 @@ class HostLayer:
             rb = _c(reservations.b, np.uint64)
             re_ = _c(reservations.e, np.uint64)
         fail = np.zeros(5, np.int64)
-        did = lib().oracle_synap_row_step(C.byref(s), row, _p(prow, _i32p), _p(pcol, _i32p), _p(pval, _f32p),
-                                          self.probe_nnz, int(len(prow) > 0), importance_cutoff,
-                                          int(max_row_weights), int(max_prune_per_step), importance_eps,
-                                          _p(self.out_deg, _i32p), _p(ptrs, _i32p), _p(cols, _i32p), _p(byts, _u8p),
-                                          _p(tbr, _i32p), _p(tbc, _i32p), _p(tby, _u8p), C.byref(ntl),
-                                          _p(rb, _u64p), _p(re_, _u64p), fail.ctypes.data_as(C.POINTER(C.c_int64)))
+        b4 = None
+        if self.b4res is not None:
+            R = self.b4res
+            arrs = [np.array(v, np.uint64) for v in (R.ia, R.ea, R.ta)]
+            fin = np.ascontiguousarray(self.b4_flags[:max(1, nt)], np.uint8)
+            fout = np.zeros(cap_t, np.uint8)
+            u64p = C.POINTER(C.c_uint64)
+            b4 = _B4Res(*[a.ctypes.data_as(u64p) for a in arrs], R.idx_budget, R.tile_budget, R.sp,
+                        fin.ctypes.data_as(C.POINTER(C.c_uint8)), fout.ctypes.data_as(C.POINTER(C.c_uint8)),
+                        R.dropped)
+        did = lib().oracle_synap_row_step2(C.byref(s), row, _p(prow, _i32p), _p(pcol, _i32p), _p(pval, _f32p),
+                                           self.probe_nnz, int(len(prow) > 0), importance_cutoff,
+                                           int(max_row_weights), int(max_prune_per_step), importance_eps,
+                                           _p(self.out_deg, _i32p), _p(ptrs, _i32p), _p(cols, _i32p), _p(byts, _u8p),
+                                           _p(tbr, _i32p), _p(tbc, _i32p), _p(tby, _u8p), C.byref(ntl),
+                                           _p(rb, _u64p), _p(re_, _u64p), fail.ctypes.data_as(C.POINTER(C.c_int64)),
+                                           None if b4 is None else C.byref(b4))
         n = int(ptrs[-1])
         k = int(ntl.value)
         self.load_csr(ptrs, cols[:n], bytes_=byts[:n])
         self.load_tiles(tbr[:k], tbc[:k], tby[:16 * k])
+        if b4 is not None:
+            R.ia, R.ea, R.ta = ([int(v) for v in a] for a in arrs)
+            R.dropped = int(b4.dropped)
+            self.b4_flags = fout[:max(1, k)].copy()
+        if did == -4:
+            raise MemoryError("std::bad_alloc")
         if did == -2:
             raise RuntimeError(synap_no_room_message(row, fail))
         if did == -3:
@@ -981,6 +1237,31 @@ class RefLayer:
         reflib().ref_layer_block4_headroom(self.h, float(blank_fraction), int(min_slack_bytes))
         return self
 
+    def block4_reservations(self):
+        """Per block row (ia, ea, ta, ui, ue, ut) as lists, and (dropped
+        growth events, merge overflow events, overflow bytes, index budget,
+        tile budget)."""
+        R = reflib()
+        n = R.ref_block4_reservations(self.h, *([None] * 7))
+        arrs = [np.zeros(max(1, n), np.uint64) for _ in range(6)]
+        out = np.zeros(5, np.uint64)
+        R.ref_block4_reservations(self.h, *[_p(a, _u64p) for a in arrs], _p(out, _u64p))
+        return tuple([int(v) for v in a[:n]] for a in arrs), tuple(int(v) for v in out)
+
+    def block4_equalize_step(self):
+        self._sll(reflib().ref_block4_equalize_step(self.h))
+
+    def block4_expand(self, blank_fraction=0.2, min_slack_bytes=16):
+        self._sll(reflib().ref_block4_expand(self.h, float(blank_fraction), int(min_slack_bytes)))
+
+    def sll_load_dense_codes(self, wc, ic):
+        wc, ic = _c(wc, np.uint8), _c(ic, np.uint8)
+        self._sll(reflib().ref_sll_load_dense_codes(self.h, _p(wc, _u8p), _p(ic, _u8p)))
+
+    def sll_put_tile(self, br, bc, tile16):
+        t = _c(tile16, np.uint8)
+        self._sll(reflib().ref_sll_put_tile(self.h, int(br), int(bc), _p(t, _u8p)))
+
     def build_probes(self, acc_in, acc_grad, k, per_row=False):
         acc_in, acc_grad = _c(acc_in, np.float32), _c(acc_grad, np.float32)
         reflib().ref_build_probes(self.h, _p(acc_in, _f32p), _p(acc_grad, _f32p), int(k), int(per_row))
@@ -999,7 +1280,10 @@ class RefLayer:
         rc = reflib().ref_synap_row_step(self.h, C.byref(row), importance_cutoff, int(max_row_weights),
                                          int(max_prune_per_step), importance_eps)
         if rc == -2:
-            raise RuntimeError(reflib().ref_last_error().decode())
+            msg = reflib().ref_last_error().decode()
+            if msg == "std::bad_alloc":  # the budget (std::bad_alloc -> MemoryError in the binding)
+                raise MemoryError(msg)
+            raise RuntimeError(msg)
         return bool(rc), int(row.value)
 
     def out_degree(self):

@@ -221,6 +221,70 @@ int64_t ref_layer_export_tiles_packed(void *h, uint8_t *flags, uint8_t *packed, 
     }
     return nb;
 }
+// Block4Store's reservations per block row (block4.hpp:1016-1031): the
+// allocated and used block-column index bytes (block_layout byte_start /
+// byte_end), tile slots (elem_start / elem_end) and tile bytes
+// (tile_byte_start / tile_byte_end).  out: dropped_growth_events,
+// row_merge_overflow_events, row_merge_overflow_bytes_dropped,
+// max_indices_bytes, max_tile_bytes.  Any array may be NULL; returns the
+// block row count.
+int64_t ref_block4_reservations(void *h, uint64_t *ia, uint64_t *ea, uint64_t *ta, uint64_t *ui, uint64_t *ue,
+                                uint64_t *ut, uint64_t *out) {
+    auto *L = static_cast<RefLayer *>(h);
+    auto &B = L->w.block4;
+    const auto &Ly = B.block_layout;
+    for (size_t br = 0; br < Ly.rows; ++br) {
+        if (ia) ia[br] = Ly.row_alloc_bytes(br);
+        if (ea) ea[br] = Ly.row_alloc_elems(br);
+        if (ta) ta[br] = B.tile_byte_start[br + 1] - B.tile_byte_start[br];
+        if (ui) ui[br] = Ly.row_byte_len(br);
+        if (ue) ue[br] = Ly.row_nnz(br);
+        if (ut) ut[br] = B.tile_byte_end[br] - B.tile_byte_start[br];
+    }
+    if (out) {
+        out[0] = B.dropped_growth_events;
+        out[1] = B.row_merge_overflow_events;
+        out[2] = B.row_merge_overflow_bytes_dropped;
+        out[3] = B.max_indices_bytes;
+        out[4] = B.max_tile_bytes;
+    }
+    return int64_t(Ly.rows);
+}
+// Block4Store::equalize_step alone (block4.hpp:1208-1220), on its own cursor;
+// 0, or -1 when it throws (bad_alloc: the budget).
+int ref_block4_equalize_step(void *h) {
+    auto *L = static_cast<RefLayer *>(h);
+    return guarded_ref([&] { L->w.block4.equalize_step(L->b4_eq_row); });
+}
+// block4_expand_headroom (delta_csr_memory.hpp:767-823) under the binding's
+// expand_block4_headroom / compact_block4 (sili/cpu_backend.cpp:932-943):
+// 0, or -1 when it throws.
+int ref_block4_expand(void *h, float blank_fraction, int min_slack_bytes) {
+    auto *L = static_cast<RefLayer *>(h);
+    return guarded_ref([&] {
+        block4_expand_headroom<S, FP4BiPacked, COL>(L->w, blank_fraction, size_t(min_slack_bytes));
+    });
+}
+// block4_load_dense under the binding's load_dense_codes (sili/cpu_backend.cpp:
+// 910-921): 0, or -1 when it throws.
+int ref_sll_load_dense_codes(void *h, const uint8_t *wc, const uint8_t *ic) {
+    auto *L = static_cast<RefLayer *>(h);
+    return guarded_ref([&] {
+        block4_load_dense<S, FP4BiPacked, COL>(L->w, wc, ic, size_t(L->n_in), size_t(L->n_out));
+    });
+}
+// A tile placed by Block4Store::get_or_create and a handle's slot writes
+// (the reference's own tests' fixture, test_disldo_block4_forward.cpp:34-45):
+// 0, or -1 when get_or_create throws.
+int ref_sll_put_tile(void *h, int br, int bc, const uint8_t *tile16) {
+    auto *L = static_cast<RefLayer *>(h);
+    return guarded_ref([&] {
+        auto t = L->w.block4.get_or_create(uint32_t(br), uint32_t(bc));
+        for (uint32_t lj = 0; lj < 4; ++lj)
+            for (uint32_t li = 0; li < 4; ++li) t.at(li, lj) = tile16[lj * 4 + li];
+    });
+}
+
 uint32_t ref_block4_switch_point(void *h, int set) {
     auto *L = static_cast<RefLayer *>(h);
     if (set >= 0) L->w.block4.switch_point = uint32_t(set);

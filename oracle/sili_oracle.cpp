@@ -118,6 +118,78 @@ std::vector<TileRef> collect_tiles(const OracleLayer *L) {
     return v;
 }
 
+// Stored length of a tile (block4_stored_tile_len, block4.hpp:340-345).
+uint64_t b4_tile_len(const uint8_t *td, bool sparse) {
+    uint64_t live = 0;
+    for (int s = 0; s < 16; ++s) live += td[s] != 0;
+    return sparse ? 1 + (live + 1) / 2 + live : 16;
+}
+uint8_t b4_encode_flag(const uint8_t *td, uint32_t sp) {
+    uint32_t live = 0;
+    for (int s = 0; s < 16; ++s) live += td[s] != 0;
+    return live <= sp ? 1 : 0;
+}
+
+// Block4Store::merge_row_workspace (block4.hpp:1367-1462) for the block row
+// holding tiles tl[k0, k1): eviction by lowest |true importance| until the
+// row's stored bytes fit its reservation, then the whole-tile clamp's
+// counters.
+void b4_merge_row(const OracleLayer *L, uint8_t *tiles, const std::vector<TileRef> &tl, int64_t k0, int64_t k1,
+                  const OracleTrainState *S, OracleB4Merge *M) {
+    if (k0 >= k1) return;
+    const int64_t br = tl[size_t(k0)].br;
+    const uint64_t alloc = M->tile_alloc[br];
+    auto len_of = [&](int64_t k) {
+        const int64_t t = tl[size_t(k)].t;
+        return b4_tile_len(tiles + 16 * t, M->tile_sparse[t] != 0);
+    };
+    uint64_t used = 0;
+    for (int64_t k = k0; k < k1; ++k) used += len_of(k);
+    while (used > alloc) {
+        double best = -1.0;
+        int64_t bk = -1;
+        int bslot = 0;
+        for (int64_t k = k0; k < k1; ++k) {
+            const uint8_t *td = tiles + 16 * tl[size_t(k)].t;
+            for (int li = 0; li < TILE; ++li)
+                for (int lj = 0; lj < TILE; ++lj) {
+                    const uint8_t byte = td[lj * TILE + li];
+                    if (byte == 0) continue;
+                    const int64_t row = br * TILE + li, col = tl[size_t(k)].bc * TILE + lj;
+                    const float is = (S->importance_scale && row < L->n_in) ? S->importance_scale[row] : 1.0f;
+                    const float ois =
+                        (S->output_importance_scale && col < L->n_out) ? S->output_importance_scale[col] : 1.0f;
+                    const double a = std::fabs(static_cast<double>(fp4_dec(byte >> 4)) * static_cast<double>(is) *
+                                               static_cast<double>(ois));
+                    if (best < 0.0 || a < best) {
+                        best = a;
+                        bk = k;
+                        bslot = lj * TILE + li;
+                    }
+                }
+        }
+        if (bk < 0) break;  // nothing live left
+        const int64_t t = tl[size_t(bk)].t;
+        const uint64_t before = len_of(bk);
+        tiles[16 * t + bslot] = 0;
+        M->tile_sparse[t] = b4_encode_flag(tiles + 16 * t, M->switch_point);
+        used = used - before + len_of(bk);
+        ++M->evicted;
+    }
+    uint64_t fit_pos = 0;
+    int64_t fit = 0;
+    for (int64_t k = k0; k < k1; ++k) {
+        const uint64_t tlen = len_of(k);
+        if (fit_pos + tlen > alloc) break;
+        fit_pos += tlen;
+        ++fit;
+    }
+    if (fit < k1 - k0) {
+        ++M->overflow_events;
+        M->overflow_bytes += used - fit_pos;
+    }
+}
+
 int nthreads_of(int threads) { return threads > 0 ? threads : 1; }
 
 }  // namespace
@@ -1045,6 +1117,19 @@ int oracle_backward_train(const OracleLayer *L, uint8_t *val, uint8_t *tiles, Or
                     }
                 }
             }
+            // the tiles are rewritten through each block row's workspace:
+            // re-encoded by live count, then written back with eviction
+            // (linear_disldo.hpp:1839-1880)
+            if (S->b4) {
+                for (const auto &t : tl)
+                    S->b4->tile_sparse[t.t] = b4_encode_flag(tiles + 16 * t.t, S->b4->switch_point);
+                for (int64_t k0 = 0; k0 < int64_t(tl.size());) {
+                    int64_t k1 = k0;
+                    while (k1 < int64_t(tl.size()) && tl[size_t(k1)].br == tl[size_t(k0)].br) ++k1;
+                    b4_merge_row(L, tiles, tl, k0, k1, S, S->b4);
+                    k0 = k1;
+                }
+            }
             // the block rows' scale step (linear_disldo.hpp:1923-1951): every
             // scale variant, its own finiteness guards
             for (int64_t row = 0; row < n_in; ++row) {
@@ -1239,6 +1324,7 @@ int sparse_train_b4(const OracleLayer *L, uint8_t *tiles, OracleTrainState *S, c
             for (int64_t k = tb[size_t(br)]; k < tb[size_t(br) + 1]; ++k) {
                 uint8_t *td = tiles + 16 * tl[size_t(k)].t;
                 const int64_t bc = tl[size_t(k)].bc;
+                bool dirty = false;
                 for (int li = 0; li < TILE; ++li) {
                     const int64_t row = br * TILE + li;
                     if (row >= n_in) continue;
@@ -1271,12 +1357,18 @@ int sparse_train_b4(const OracleLayer *L, uint8_t *tiles, OracleTrainState *S, c
                         const uint32_t wq = dr.enc(new_w / combined_scale, id);
                         const uint32_t iq = dr.enc(imp / combined_imp_scale, id + 1);
                         td[lj * TILE + li] = uint8_t((iq << 4) | wq);
+                        dirty = true;
                         rg[li] += static_cast<double>(w_decoded) * static_cast<double>(out_scale) * (dy_val * in_val);
                         rgc[li] += static_cast<double>(w_decoded) * static_cast<double>(out_scale) *
                                    static_cast<double>(contrib);
                     }
                 }
+                // a rewritten tile is re-encoded by its live count
+                // (commit_dirty_tile_in_workspace, sisldo_ops.hpp:1032-1034)
+                if (dirty && S->b4) S->b4->tile_sparse[tl[size_t(k)].t] = b4_encode_flag(td, S->b4->switch_point);
             }
+            // the block row's workspace written back (sisldo_ops.hpp:1036-1052)
+            if (lr != 0.0f && S->b4) b4_merge_row(L, tiles, tl, tb[size_t(br)], tb[size_t(br) + 1], S, S->b4);
             for (int li = 0; li < TILE; ++li) {
                 const int64_t row = br * TILE + li;
                 if (row >= n_in) continue;
@@ -1410,15 +1502,6 @@ int oracle_backward_sparse_train(const OracleLayer *L, uint8_t *val, uint8_t *ti
 // same comparators and input order as the reference (tie order included).
 namespace {
 
-struct MutLayer {
-    int64_t n_in = 0, n_out = 0;
-    std::vector<std::vector<std::pair<uint32_t, uint8_t>>> rows;  // per row, by column: (col, (w<<4)|imp)
-    std::map<std::pair<uint32_t, uint32_t>, std::array<uint8_t, 16>> tiles;  // (br, bc) -> slot lj*4+li, (imp<<4)|w
-    // per-row reservations of the scattered store (index bytes, elements):
-    // the room delta_csr_row_insert_col checks; NULL: unlimited
-    const uint64_t *res_b = nullptr, *res_e = nullptr;
-};
-
 inline uint64_t uleb_size(uint32_t v) {
     uint64_t n = 1;
     while (v >= 0x80u) {
@@ -1426,6 +1509,129 @@ inline uint64_t uleb_size(uint32_t v) {
         ++n;
     }
     return n;
+}
+
+struct MutLayer {
+    int64_t n_in = 0, n_out = 0;
+    std::vector<std::vector<std::pair<uint32_t, uint8_t>>> rows;  // per row, by column: (col, (w<<4)|imp)
+    std::map<std::pair<uint32_t, uint32_t>, std::array<uint8_t, 16>> tiles;  // (br, bc) -> slot lj*4+li, (imp<<4)|w
+    // per-row reservations of the scattered store (index bytes, elements):
+    // the room delta_csr_row_insert_col checks; NULL: unlimited
+    const uint64_t *res_b = nullptr, *res_e = nullptr;
+    // the block4 store's reservations and tile encoding (NULL: not kept)
+    OracleB4Res *b4 = nullptr;
+    std::map<std::pair<uint32_t, uint32_t>, uint8_t> flags;  // tile_is_sparse
+};
+
+// ---- the block4 store's reservations (block4.hpp:497-946) -------------------
+uint64_t b4_total(const uint64_t *v, size_t n) {
+    uint64_t s = 0;
+    for (size_t i = 0; i < n; ++i) s += v[i];
+    return s;
+}
+struct B4Budget {};  // thrown when a row's growth exceeds a budget
+
+// block row br's use: block-column ULEB128 bytes, tiles, stored tile bytes
+void b4_use(const MutLayer &M, uint32_t br, uint64_t &ui, uint64_t &ue, uint64_t &ut) {
+    ui = ue = ut = 0;
+    uint32_t prev = 0;
+    for (auto it = M.tiles.lower_bound({br, 0u}); it != M.tiles.end() && it->first.first == br; ++it) {
+        ui += uleb_size(it->first.second - prev);
+        prev = it->first.second;
+        ++ue;
+        ut += b4_tile_len(it->second.data(), M.flags.at(it->first) != 0);
+    }
+}
+
+// block4_row_shift (block4.hpp:497-617) / block4_grow_last_row (:619-646)
+// towards targets (ti, tt, te) for block row br, clamped to its use
+void b4_shift(OracleB4Res *R, size_t rows, size_t br, uint64_t ti, uint64_t tt, uint64_t te, uint64_t ui,
+              uint64_t ue, uint64_t ut, bool last_row_grows) {
+    if (br + 1 >= rows) {
+        if (!last_row_grows) return;
+        if (ti > R->ia[br]) {
+            if (b4_total(R->ia, rows) + (ti - R->ia[br]) > R->idx_budget) throw B4Budget{};
+            R->ia[br] = ti;
+        }
+        if (tt > R->ta[br]) {
+            if (b4_total(R->ta, rows) + (tt - R->ta[br]) > R->tile_budget) throw B4Budget{};
+            R->ta[br] = tt;
+        }
+        if (te > R->ea[br]) R->ea[br] = te;
+        return;
+    }
+    ti = std::max(ti, ui);
+    tt = std::max(tt, ut);
+    te = std::max(te, ue);
+    if (R->ia[br] != ti) {
+        if (ti > R->ia[br] && b4_total(R->ia, rows) + (ti - R->ia[br]) > R->idx_budget) throw B4Budget{};
+        R->ia[br] = ti;
+    }
+    if (R->ta[br] != tt) {
+        if (tt > R->ta[br] && b4_total(R->ta, rows) + (tt - R->ta[br]) > R->tile_budget) throw B4Budget{};
+        R->ta[br] = tt;
+    }
+    if (R->ea[br] != te) R->ea[br] = te;
+}
+
+// block4_row_insert_tile's room check and get_or_create's growth
+// (block4.hpp:670-771,1170-1183) for a new tile (br, bc); throws B4Budget
+void b4_insert_tile(MutLayer &M, uint32_t br, uint32_t bc) {
+    OracleB4Res *R = M.b4;
+    const size_t rows = size_t((M.n_in + TILE - 1) / TILE);
+    uint64_t ui, ue, ut;
+    b4_use(M, br, ui, ue, ut);
+    auto nx = M.tiles.upper_bound({br, bc});
+    uint32_t prev = 0;
+    if (nx != M.tiles.begin() && std::prev(nx)->first.first == br) prev = std::prev(nx)->first.second;
+    int64_t d = int64_t(uleb_size(bc - prev));
+    if (nx != M.tiles.end() && nx->first.first == br)
+        d += int64_t(uleb_size(nx->first.second - bc)) - int64_t(uleb_size(nx->first.second - prev));
+    const bool fits = !(d > 0 && uint64_t(d) > R->ia[br] - ui) && ue < R->ea[br] && 1 <= R->ta[br] - ut;
+    if (fits) return;
+    b4_shift(R, rows, br, R->ia[br] + 5, R->ta[br] + 1, R->ea[br] + 1, ui, ue, ut, true);
+}
+
+// a sparse tile's handle commit (commit_dirty_sparse_tile, block4.hpp:
+// 1226-1290): the tile re-encoded by live count; growth beyond the row's room
+// takes the shortfall, beyond the tile budget the commit is dropped
+bool b4_commit(MutLayer &M, uint32_t br, uint32_t bc, const std::array<uint8_t, 16> &nt) {
+    OracleB4Res *R = M.b4;
+    const size_t rows = size_t((M.n_in + TILE - 1) / TILE);
+    auto &cur = M.tiles[{br, bc}];
+    uint8_t &fl = M.flags[{br, bc}];
+    const uint64_t old_len = b4_tile_len(cur.data(), fl != 0);
+    const uint8_t nfl = b4_encode_flag(nt.data(), R->switch_point);
+    const uint64_t new_len = b4_tile_len(nt.data(), nfl != 0);
+    if (new_len > old_len) {
+        uint64_t ui, ue, ut;
+        b4_use(M, br, ui, ue, ut);
+        const uint64_t d = new_len - old_len, room = R->ta[br] - ut;
+        if (d > room) {
+            const uint64_t shortfall = d - room;
+            if (b4_total(R->ta, rows) + shortfall > R->tile_budget) {
+                ++R->dropped;
+                return false;
+            }
+            R->ta[br] += shortfall;
+        }
+    }
+    cur = nt;
+    fl = nfl;
+    return true;
+}
+
+// a slot written through a handle: in place in a dense tile, a commit of a
+// sparse one
+void b4_write_slot(MutLayer &M, uint32_t br, uint32_t bc, uint32_t slot, uint8_t byte) {
+    auto &t = M.tiles[{br, bc}];
+    if (!M.b4 || M.flags.at({br, bc}) == 0) {
+        t[slot] = byte;
+        return;
+    }
+    std::array<uint8_t, 16> nt = t;
+    nt[slot] = byte;
+    b4_commit(M, br, bc, nt);
 }
 
 uint64_t row_index_bytes(const std::vector<std::pair<uint32_t, uint8_t>> &row) {
@@ -1511,6 +1717,7 @@ int64_t mut_demote(MutLayer &M, uint32_t br, uint32_t bc) {
             if (!mut_insert(M, r, c, fp4_dec(b & 0xFu), fp4_dec(b >> 4))) return int64_t(r);
         }
     }
+    M.flags.erase(it->first);
     M.tiles.erase(it);
     return -1;
 }
@@ -1524,7 +1731,11 @@ void mut_maybe_promote(MutLayer &M, uint32_t row, uint32_t col) {
         auto it = std::lower_bound(rw.begin(), rw.end(), std::make_pair(col, uint8_t(0)));
         if (it == rw.end() || it->first != col) return;
         const float w = fp4_dec(it->second >> 4), imp = fp4_dec(it->second & 0xFu);
-        tit->second[lj * TILE + li] = uint8_t(fp4_enc(w) | (fp4_enc(imp) << 4));
+        b4_write_slot(M, br, bc, lj * TILE + li, uint8_t(fp4_enc(w) | (fp4_enc(imp) << 4)));
+        if (M.b4) {  // maybe_compress (block4.hpp:1193-1205)
+            uint8_t &fl = M.flags[{br, bc}];
+            if (fl == 0 && b4_encode_flag(tit->second.data(), M.b4->switch_point)) fl = 1;
+        }
         rw.erase(it);
         return;
     }
@@ -1541,7 +1752,16 @@ void mut_maybe_promote(MutLayer &M, uint32_t row, uint32_t col) {
         const float w = fp4_dec(f.b >> 4), imp = fp4_dec(f.b & 0xFu);
         d[(f.c - uint32_t(col_lo)) * TILE + (f.r - uint32_t(row_lo))] = uint8_t(fp4_enc(w) | (fp4_enc(imp) << 4));
     }
-    M.tiles[{br, bc}] = d;
+    if (M.b4) {
+        // get_or_create: a sparse-empty tile (may throw B4Budget), then the
+        // handle's commit of its slots
+        b4_insert_tile(M, br, bc);
+        M.tiles[{br, bc}] = std::array<uint8_t, 16>{};
+        M.flags[{br, bc}] = 1;
+        b4_commit(M, br, bc, d);
+    } else {
+        M.tiles[{br, bc}] = d;
+    }
     for (const auto &f : found) mut_remove(M, f.r, f.c);
 }
 
@@ -1647,19 +1867,36 @@ int64_t oracle_build_probes(const OracleLayer *L, const float *acc_in, const flo
 // demotion that does not fit (block4_demote_tile's throw, :983-991) returns
 // -3 with the layer as before the call and fail[0..2] = row, br, bc (the
 // reference leaves that tile half demoted).
-int oracle_synap_row_step(const OracleLayer *L, int64_t row, const int32_t *prow, const int32_t *pcol,
-                          const float *pval, int64_t pnnz, int has_probes, float importance_cutoff,
-                          int64_t max_row_weights, int64_t max_prune_per_step, float importance_eps,
-                          int32_t *out_degree, int32_t *out_ptrs, int32_t *out_cols, uint8_t *out_bytes,
-                          int32_t *out_br, int32_t *out_bc, uint8_t *out_tiles, int64_t *n_tiles_out,
-                          const uint64_t *res_b, const uint64_t *res_e, int64_t *fail) {
+int oracle_synap_row_step2(const OracleLayer *L, int64_t row, const int32_t *prow, const int32_t *pcol,
+                           const float *pval, int64_t pnnz, int has_probes, float importance_cutoff,
+                           int64_t max_row_weights, int64_t max_prune_per_step, float importance_eps,
+                           int32_t *out_degree, int32_t *out_ptrs, int32_t *out_cols, uint8_t *out_bytes,
+                           int32_t *out_br, int32_t *out_bc, uint8_t *out_tiles, int64_t *n_tiles_out,
+                           const uint64_t *res_b, const uint64_t *res_e, int64_t *fail, OracleB4Res *b4) {
     MutLayer M = load_mut(L);
     M.res_b = res_b;
     M.res_e = res_b ? res_e : nullptr;
+    M.b4 = b4;
+    if (b4) {
+        int64_t k = 0;
+        for (const auto &t : M.tiles) M.flags[t.first] = b4->flags_in[k++];
+    }
     const MutLayer M0 = M;
     std::vector<int32_t> deg0(out_degree, out_degree + L->n_out);
+    const size_t rows4 = size_t((L->n_in + TILE - 1) / TILE);
+    std::vector<uint64_t> ia0, ea0, ta0;
+    const uint64_t dropped0 = b4 ? b4->dropped : 0;
+    if (b4) {
+        ia0.assign(b4->ia, b4->ia + rows4);
+        ea0.assign(b4->ea, b4->ea + rows4);
+        ta0.assign(b4->ta, b4->ta + rows4);
+    }
     auto finish = [&](int ret) {
         *n_tiles_out = mut_store(M, out_ptrs, out_cols, out_bytes, out_br, out_bc, out_tiles);
+        if (b4) {
+            int64_t k = 0;
+            for (const auto &t : M.tiles) b4->flags_out[k++] = M.flags.at(t.first);
+        }
         return ret;
     };
     if (M.n_in == 0) return finish(0);
@@ -1736,7 +1973,7 @@ int oracle_synap_row_step(const OracleLayer *L, int64_t row, const int32_t *prow
             bool should_demote = false;
             auto it = M.tiles.find({br, bc});
             if (it != M.tiles.end() && it->second[lj * TILE + li] != 0) {
-                it->second[lj * TILE + li] = 0;
+                b4_write_slot(M, br, bc, lj * TILE + li, 0);
                 int live = 0;
                 for (uint8_t b : it->second) live += b != 0;
                 should_demote = live < PROMOTE_MIN_LIVE;
@@ -1746,6 +1983,12 @@ int oracle_synap_row_step(const OracleLayer *L, int64_t row, const int32_t *prow
                 if (fr >= 0) {
                     M = M0;
                     std::copy(deg0.begin(), deg0.end(), out_degree);
+                    if (b4) {  // the layer as before, reservations included
+                        std::copy(ia0.begin(), ia0.end(), b4->ia);
+                        std::copy(ea0.begin(), ea0.end(), b4->ea);
+                        std::copy(ta0.begin(), ta0.end(), b4->ta);
+                        b4->dropped = dropped0;
+                    }
                     if (fail) {
                         fail[0] = fr;
                         fail[1] = br;
@@ -1771,9 +2014,25 @@ int oracle_synap_row_step(const OracleLayer *L, int64_t row, const int32_t *prow
             return finish(-2);
         }
         ++out_degree[probe_cols[i]];
-        mut_maybe_promote(M, r, probe_cols[i]);
+        try {
+            mut_maybe_promote(M, r, probe_cols[i]);
+        } catch (const B4Budget &) {
+            if (fail) fail[0] = int64_t(i);
+            return finish(-4);
+        }
     }
     return finish(1);
+}
+
+int oracle_synap_row_step(const OracleLayer *L, int64_t row, const int32_t *prow, const int32_t *pcol,
+                          const float *pval, int64_t pnnz, int has_probes, float importance_cutoff,
+                          int64_t max_row_weights, int64_t max_prune_per_step, float importance_eps,
+                          int32_t *out_degree, int32_t *out_ptrs, int32_t *out_cols, uint8_t *out_bytes,
+                          int32_t *out_br, int32_t *out_bc, uint8_t *out_tiles, int64_t *n_tiles_out,
+                          const uint64_t *res_b, const uint64_t *res_e, int64_t *fail) {
+    return oracle_synap_row_step2(L, row, prow, pcol, pval, pnnz, has_probes, importance_cutoff, max_row_weights,
+                                  max_prune_per_step, importance_eps, out_degree, out_ptrs, out_cols, out_bytes,
+                                  out_br, out_bc, out_tiles, n_tiles_out, res_b, res_e, fail, nullptr);
 }
 
 }  // extern "C"

@@ -135,6 +135,24 @@ typedef struct {
     uint64_t draw_seed;
 } OracleTrainParams;
 
+/* The block rows' write-back of an optimizer update
+ * (Block4Store::merge_row_workspace, block4.hpp:1367-1462): a block row whose
+ * stored tiles (sparse-packed or 16 bytes, by tile_sparse) outgrow its
+ * reserved tile bytes loses its live slots of lowest |true importance|
+ * (decoded importance x importance_scale[row] x output_importance_scale[col]
+ * in fp64; the first in (tile, tile row, tile column) order on ties), each
+ * eviction re-encoding its tile by its live count, until the row fits; a row
+ * that still does not fit counts an overflow event and the bytes beyond its
+ * last whole tile that fits. */
+typedef struct {
+    const uint64_t *tile_alloc; /* [ceil(n_in/4)] reserved tile bytes per block row */
+    uint8_t *tile_sparse;       /* [n_tiles] tile_is_sparse, updated */
+    uint32_t switch_point;      /* a commit stores a tile sparse-packed iff live <= switch_point */
+    uint64_t evicted;           /* out (added to): slots evicted */
+    uint64_t overflow_events;   /* out (added to): row_merge_overflow_events */
+    uint64_t overflow_bytes;    /* out (added to): row_merge_overflow_bytes_dropped */
+} OracleB4Merge;
+
 typedef struct {
     float *value_scale;                   /* [n_in*rank]  */
     float *vs_importance;                 /* [n_in*rank]  */
@@ -150,6 +168,9 @@ typedef struct {
     float *quant_out;                     /* [nnz] or NULL: each synapse's updated weight code value
                                              before re-quantization */
     float *imp_out;                       /* [nnz] or NULL: its importance (stored units) before it */
+    OracleB4Merge *b4;                    /* NULL: block rows taken to have room (no eviction); else
+                                             the updates re-encode the tiles they rewrite by live count
+                                             and write each block row back as merge_row_workspace */
 } OracleTrainState;
 
 /* L supplies structure (its val / scale pointers are not read); val: the
@@ -191,12 +212,37 @@ int oracle_backward_sparse_train(const OracleLayer *L, uint8_t *val, uint8_t *ti
  * demotion does not fit (layer as before; fail[0..2] = row, br, bc). */
 int64_t oracle_build_probes(const OracleLayer *L, const float *acc_in, const float *acc_grad, int64_t k,
                             int per_row, int32_t *prow, int32_t *pcol, float *pval, int64_t cap);
+/* The block4 store's reservations and tile encoding for
+ * oracle_synap_row_step2 (block4.hpp:497-946,1170-1290): per block row the
+ * reserved index bytes ia, tile slots ea and tile bytes ta (updated), the
+ * budgets, switch_point, and tile_is_sparse of the input tiles (canonical
+ * order) / of the output tiles. */
+typedef struct {
+    uint64_t *ia, *ea, *ta;
+    uint64_t idx_budget, tile_budget;
+    uint32_t switch_point;
+    const uint8_t *flags_in;
+    uint8_t *flags_out;
+    uint64_t dropped; /* out (added to): dropped_growth_events */
+} OracleB4Res;
 int oracle_synap_row_step(const OracleLayer *L, int64_t row, const int32_t *prow, const int32_t *pcol,
                           const float *pval, int64_t pnnz, int has_probes, float importance_cutoff,
                           int64_t max_row_weights, int64_t max_prune_per_step, float importance_eps,
                           int32_t *out_degree, int32_t *out_ptrs, int32_t *out_cols, uint8_t *out_bytes,
                           int32_t *out_br, int32_t *out_bc, uint8_t *out_tiles, int64_t *n_tiles_out,
                           const uint64_t *res_b, const uint64_t *res_e, int64_t *fail);
+/* The same with the block4 store's reservations (b4, see OracleB4Res): a new
+ * tile grows its block row without room (get_or_create), a tile's growth
+ * beyond the tile budget is dropped (the tile keeps its bytes), and -4 when
+ * a new tile's row growth exceeds a budget (the reference throws bad_alloc
+ * there: the edits before it and that insert's scattered synapse stay,
+ * fail[0] = the probe index). */
+int oracle_synap_row_step2(const OracleLayer *L, int64_t row, const int32_t *prow, const int32_t *pcol,
+                           const float *pval, int64_t pnnz, int has_probes, float importance_cutoff,
+                           int64_t max_row_weights, int64_t max_prune_per_step, float importance_eps,
+                           int32_t *out_degree, int32_t *out_ptrs, int32_t *out_cols, uint8_t *out_bytes,
+                           int32_t *out_br, int32_t *out_bc, uint8_t *out_tiles, int64_t *n_tiles_out,
+                           const uint64_t *res_b, const uint64_t *res_e, int64_t *fail, OracleB4Res *b4);
 
 /* ---- bulk synaptogenesis step (magnitude prune + candidate regrow) ----
  * Output capacities: scattered entries <= nnz + n_cand + 16*n_tiles,

@@ -29,7 +29,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("SILI_OFFLOAD_ARCH", "gfx950")
 
 HIP_SOURCES = ["kernels.hip", "stream.hip", "build.hip", "synapto.hip", "policy.hip", "gen.hip", "train.hip",
-               "csr_util.hip", "for_index.hip", "tile_enc.hip", "layout.hip", "push.hip", "patch.hip", "staged.hip", "capi.hip"]
+               "csr_util.hip", "for_index.hip", "tile_enc.hip", "layout.hip", "b4res.hip", "push.hip", "patch.hip", "staged.hip", "capi.hip"]
 
 HIP_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",

@@ -10,6 +10,7 @@
 #include <memory>
 #include <mutex>
 #include <new>
+#include <numeric>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -629,8 +630,10 @@ void backward_dense_train(Layer &L, const float *x, const float *dy, int64_t B, 
     // block4 tiles after the scattered rows' scale steps (linear_disldo.hpp:962-1951)
     launch_train_b4(L, xT, gT, B, dx, p, seed, st);
     // the update rewrites every tile: each is re-encoded by its live count
-    // (linear_disldo.hpp:1839-1856, block4.hpp:1336-1355)
+    // (linear_disldo.hpp:1839-1856, block4.hpp:1336-1355), then each block
+    // row is written back, evicting where it outgrew its reservation
     tiles_reencode(L, nullptr, st);
+    launch_b4_merge(L, st);
     if (L.W.n_empty_rows > 0) launch_train_dead_rows(L, xT, gT, B, p, st);
     const bool scales_step = L.update_variant != UPDATE_NOSCALE;
     if (L.output_scale_trainable && scales_step && L.W.nnz > 0) launch_train_cols(L, p, st);
@@ -722,10 +725,10 @@ void backward_sparse_train(Layer &L, const float *x, const int32_t *dptrs, const
     launch_sparse_train(L, xT, L.ws_gT.p, B, dx, p, st);
     // block4 tiles after the scattered section (sisldo_ops.hpp:848-1100)
     const uint64_t seed = splitmix64_host(L.rng_seed ^ splitmix64_host(L.rng_calls + 1));
+    // (it re-encodes the tiles it rewrites by their live count and writes
+    // each block row back, with eviction, after every batch row,
+    // sisldo_ops.hpp:945-1052)
     launch_sparse_train_b4(L, xT, L.ws_gT.p, B, dx, p, seed, st);
-    // tiles with a nonzero dy in one of their columns were rewritten
-    // (sisldo_ops.hpp:945-1033): re-encoded by their live count
-    tiles_reencode_sparse_update(L, L.ws_gT.p, B, st);
     launch_shadow_val_refresh(L, st);
     launch_b4_shadow_refresh(L, st);
     for (DScatter *sc : {&L.W, &L.Wt}) {
@@ -785,6 +788,8 @@ int sili_create(int64_t n_inputs, int64_t n_outputs, int64_t max_weights, int de
         L.idx_budget = max_weights * 8 + 4096;
         L.val_budget = max_weights + 64;
         L.tile_budget = std::max<int64_t>(4, max_weights / 16) * 16;
+        // the block4 store's budgets (sili/cpu_backend.cpp:438-441), nothing reserved
+        b4res_reset(L, (uint64_t)max_weights * 8 + 4096, (uint64_t)L.tile_budget);
         // segment byte limits (tuning knobs; the kernels stage at most SEG_BYTES_MAX)
         if (const char *e = std::getenv("SILI_SEG_BYTES"))
             L.seg_len = (uint32_t)std::min<int>((int)SEG_BYTES_MAX, std::max(16, std::atoi(e)));
@@ -888,6 +893,12 @@ int sili_load_dense_codes(sili_layer *layer, const uint8_t *wc, const uint8_t *i
                         tiles[(size_t)t * 16 + (size_t)(lj * 4 + li)] = (uint8_t)(wc[k] | (ic[k] << 4));
                     }
             }
+        // the reservations block4_load_dense leaves (delta_csr_memory.hpp:
+        // 841-945): new budgets, every tile committed, 20 % headroom
+        std::vector<uint8_t> live((size_t)n, 0);
+        for (int64_t t = 0; t < n; ++t)
+            for (int sl = 0; sl < 16; ++sl) live[(size_t)t] += tiles[(size_t)t * 16 + (size_t)sl] != 0;
+        b4res_load_dense(L, live);
         DevBuf<uint32_t> dbr, dbc;
         DevBuf<uint8_t> dt;
         upload(dbr, br.data(), br.size(), L.stream);
@@ -907,13 +918,49 @@ int sili_load_block4_tiles(sili_layer *layer, const int32_t *br, const int32_t *
         set_device(L);
         if (n_tiles < 0 || n_tiles >= (int64_t(1) << 31)) throw_error(SILI_ERR_INVALID, "n_tiles out of range");
         if (n_tiles > 0 && (!br || !bc || !tile_bytes)) throw_error(SILI_ERR_INVALID, "tile arrays are NULL");
-        if (n_tiles * 16 > L.tile_budget)
-            throw_error(SILI_ERR_NOMEM, "block4 tiles exceed the layer's tile budget (max(4, max_weights/16)*16 bytes)");
         std::vector<uint32_t> ubr((size_t)n_tiles), ubc((size_t)n_tiles);
+        const int64_t brows = (L.n_in + 3) / 4, bcols = (L.n_out + 3) / 4;
         for (int64_t i = 0; i < n_tiles; ++i) {
             if (br[i] < 0 || bc[i] < 0) throw_error(SILI_ERR_INVALID, "negative tile coordinate");
+            if (br[i] >= brows || bc[i] >= bcols)
+                throw_error(SILI_ERR_INVALID, "block4 tiles: malformed input (unsorted, duplicate or out-of-range index)");
             ubr[(size_t)i] = (uint32_t)br[i];
             ubc[(size_t)i] = (uint32_t)bc[i];
+        }
+        // the store's reservations as the tiles placed one by one in
+        // canonical order through get_or_create and a handle's writes leave
+        // them (block4.hpp:1170-1183,1226-1290): refused with MemoryError,
+        // before any device work, where the budget would refuse a row's
+        // growth or drop a tile's content
+        {
+            std::vector<uint32_t> ord((size_t)n_tiles);
+            std::iota(ord.begin(), ord.end(), 0u);
+            std::sort(ord.begin(), ord.end(), [&](uint32_t a, uint32_t b) {
+                return ubr[a] != ubr[b] ? ubr[a] < ubr[b] : ubc[a] < ubc[b];
+            });
+            std::vector<uint32_t> sbr((size_t)n_tiles), sbc((size_t)n_tiles);
+            std::vector<uint8_t> st((size_t)n_tiles * 16);
+            for (int64_t i = 0; i < n_tiles; ++i) {
+                const uint32_t k = ord[(size_t)i];
+                sbr[(size_t)i] = ubr[k];
+                sbc[(size_t)i] = ubc[k];
+                if (i > 0 && sbr[(size_t)i] == sbr[(size_t)i - 1] && sbc[(size_t)i] == sbc[(size_t)i - 1])
+                    throw_error(SILI_ERR_INVALID, "block4 tiles: duplicate entries");
+                std::memcpy(&st[(size_t)i * 16], tile_bytes + (size_t)k * 16, 16);
+            }
+            const auto ia = L.b4_ia, ea = L.b4_ea, ta = L.b4_ta;
+            const uint64_t dropped = L.b4_dropped;
+            try {
+                b4res_reset(L, L.b4_idx_budget, L.b4_tile_budget);
+                b4res_put_tiles(L, n_tiles, sbr.data(), sbc.data(), st.data());
+            } catch (...) {
+                L.b4_ia = ia;
+                L.b4_ea = ea;
+                L.b4_ta = ta;
+                L.b4_dropped = dropped;
+                L.b4_ta_stale = true;
+                throw;
+            }
         }
         DevBuf<uint32_t> dbr, dbc;
         DevBuf<uint8_t> dt;
@@ -1210,6 +1257,7 @@ int sili_synapto_step(sili_layer *layer, float prune_frac, const int32_t *cand_r
         synapto_step(layer->L, prune_frac, cand_rows, cand_cols, cand_vals, cand_scores, n_cand, default_imp_code,
                      out_stats);
         layout_fit(layer->L);
+        b4res_fit(layer->L);
     });
 }
 
@@ -1251,7 +1299,55 @@ int sili_equalizer_step(sili_layer *layer) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
         set_device(layer->L);
+        // the scattered store's step, then the block4 store's
+        // (sili/cpu_backend.cpp:646-657)
         layout_equalizer_step(layer->L);
+        b4res_equalize_step(layer->L);
+    });
+}
+
+int sili_expand_block4_headroom(sili_layer *layer, float blank_fraction) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        b4res_expand(layer->L, blank_fraction, 16, b4_row_use(layer->L).ut);
+    });
+}
+
+int sili_compact_block4(sili_layer *layer) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        set_device(layer->L);
+        b4res_expand(layer->L, 0.0f, 0, b4_row_use(layer->L).ut);
+    });
+}
+
+int sili_export_block4_layout(sili_layer *layer, uint64_t *ia, uint64_t *ea, uint64_t *ta, uint64_t *ui,
+                              uint64_t *ue, uint64_t *ut, uint64_t *out) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "layer is NULL");
+        Layer &L = layer->L;
+        set_device_read(L);
+        const B4Use u = b4_row_use(L);
+        const size_t rows = L.b4_ia.size();
+        for (size_t r = 0; r < rows; ++r) {
+            if (ia) ia[r] = L.b4_ia[r];
+            if (ea) ea[r] = L.b4_ea[r];
+            if (ta) ta[r] = L.b4_ta[r];
+            if (ui) ui[r] = u.ui[r];
+            if (ue) ue[r] = u.ue[r];
+            if (ut) ut[r] = u.ut[r];
+        }
+        if (out) {
+            uint64_t ctr[3];
+            b4res_read_counters(L, ctr);
+            out[0] = L.b4_dropped;
+            out[1] = ctr[1];
+            out[2] = ctr[2];
+            out[3] = L.b4_idx_budget;
+            out[4] = L.b4_tile_budget;
+            out[5] = ctr[0];
+        }
     });
 }
 
@@ -1568,10 +1664,13 @@ int sili_block4_view(sili_layer *layer, sili_block4_stats *out) {
         out->synapses = pk.live;
         out->switch_point = L.switch_point;
         out->used_bytes = (int64_t)pk.bytes.size();
-        out->alloc_bytes = (int64_t)pk.bytes.size();
-        out->dropped_growth_events = 0;
-        out->row_merge_overflow_events = 0;
-        out->row_merge_overflow_bytes_dropped = 0;
+        uint64_t alloc = 0, ctr[3];
+        for (uint64_t v : L.b4_ta) alloc += v;
+        b4res_read_counters(L, ctr);
+        out->alloc_bytes = (int64_t)alloc;
+        out->dropped_growth_events = (int64_t)L.b4_dropped;
+        out->row_merge_overflow_events = (int64_t)ctr[1];
+        out->row_merge_overflow_bytes_dropped = (int64_t)ctr[2];
     });
 }
 

@@ -151,6 +151,13 @@ __host__ __device__ __forceinline__ uint32_t uleb_len(uint32_t v) {
     return v < (1u << 7) ? 1u : v < (1u << 14) ? 2u : v < (1u << 21) ? 3u : v < (1u << 28) ? 4u : 5u;
 }
 
+// A block4 tile's stored length (block4_stored_tile_len, block4.hpp:340-345):
+// sparse-packed [count][ceil(live/2) position bytes][live values], or the 16
+// dense bytes.
+__host__ __device__ __forceinline__ uint32_t tile_len(bool sparse, uint32_t live) {
+    return sparse ? 1u + (live + 1u) / 2u + live : 16u;
+}
+
 // ---- host-side launchers (kernels.hip / build.hip / synapto.hip) -----------
 struct ScaleView {
     const float *row;   // scale indexed by the gather row   [rows*rank]

@@ -385,6 +385,20 @@ struct Layer {
     // equalizer_step cursor; the device store itself stays compact.
     std::vector<uint64_t> lay_b, lay_e;
     int64_t eq_cursor = 0;
+    // The reference's per-block-row reservations of its block4 store (index
+    // bytes, tile slots, tile bytes: block_layout byte_start / elem_start and
+    // tile_byte_start), its budgets (max_indices_bytes, max_tile_bytes), its
+    // equalize_step cursor and dropped_growth_events.  b4_ta_dev: the tile
+    // bytes as the updates' write-back reads them (re-uploaded when stale);
+    // b4_ctr: [evicted slots, row_merge_overflow_events, bytes dropped].
+    std::vector<uint64_t> b4_ia, b4_ea, b4_ta;
+    uint64_t b4_idx_budget = ~0ull, b4_tile_budget = ~0ull;
+    int64_t b4_eq_cursor = 0;
+    uint64_t b4_dropped = 0;
+    bool b4_ta_stale = true;
+    DevBuf<uint32_t> b4_ta_dev;
+    DevBuf<unsigned long long> b4_ctr;
+    PinBuf pin_b4ta;
     uint32_t seg_len = 512;     // max index bytes per decode work item (scattered)
     uint32_t seg_len_b4 = 128;  // max block-index bytes per decode work item (block4)
     // the policy's row patches: pinned staging (reads in, patch content out),
@@ -475,6 +489,25 @@ void layout_equalizer_step(Layer &L);
 // whose content outgrew their reservation get exactly their content
 void layout_fit(Layer &L);
 void export_layout(Layer &L, uint64_t *byte_start, uint64_t *byte_end, uint64_t *elem_start, uint64_t *elem_end);
+
+// ---- the reference's block4 reservations (b4res.hip) ------------------------
+struct B4Use {  // per block row: block-column index bytes, tiles, stored tile bytes
+    std::vector<uint64_t> ui, ue, ut;
+};
+B4Use b4_row_use(Layer &L);
+void b4res_reset(Layer &L, uint64_t idx_budget, uint64_t tile_budget);
+void b4res_shift(Layer &L, size_t row, uint64_t ti, uint64_t tt, uint64_t te, uint64_t ui, uint64_t ue,
+                 uint64_t ut);
+void b4res_insert_tile(Layer &L, size_t row, int64_t idx_delta, uint64_t ui, uint64_t ue, uint64_t ut);
+bool b4res_commit(Layer &L, size_t row, uint64_t old_len, uint64_t new_len, uint64_t ut);
+void b4res_expand(Layer &L, float blank_fraction, uint64_t slack, const std::vector<uint64_t> &ut);
+void b4res_load_dense(Layer &L, const std::vector<uint8_t> &live);
+void b4res_put_tiles(Layer &L, int64_t n, const uint32_t *br, const uint32_t *bc, const uint8_t *tiles);
+void b4res_equalize_step(Layer &L);
+void b4res_fit(Layer &L);
+const uint32_t *b4res_device_alloc(Layer &L, hipStream_t st);
+unsigned long long *b4res_counters(Layer &L, hipStream_t st);
+void b4res_read_counters(Layer &L, uint64_t out[3]);
 
 // FOR index of the canonical scattered store (for_index.hip): build (group
 // size 8, 16, 32 or 64), and decode of every column into cols (int32, storage
@@ -606,6 +639,11 @@ void launch_train_b4(Layer &L, const float *xT, const float *gT, int64_t B, floa
                      uint64_t seed, hipStream_t st);
 // Shadow tile bytes from the canonical ones (through L.B4t_perm).
 void launch_b4_shadow_refresh(Layer &L, hipStream_t st);
+// the dense update's block-row write-back with eviction (merge_row_workspace),
+// after the tiles were re-encoded by live count
+void launch_b4_merge(Layer &L, hipStream_t st);
+// the canonical block4 tiles' block columns (decoded once per structure)
+const uint32_t *b4_tile_cols(Layer &L);
 // The sparse-gradient update of block4 tiles and their block rows' value-scale step.
 void launch_sparse_train_b4(Layer &L, const float *xT, const float *gT, int64_t B, float *dx,
                             const TrainParams &p, uint64_t seed, hipStream_t st);

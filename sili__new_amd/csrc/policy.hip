@@ -196,7 +196,8 @@ inline uint8_t requant(uint32_t code) { return code == 8u ? 0u : (uint8_t)code; 
 // tile_is_sparse is kept unless it received an insert or is new (then: live
 // slots <= switch_point).
 BlockRowState bulk_edit(const Layer &L, const BlockRowState &old, const std::vector<uint64_t> &prune_keys,
-                        uint32_t li0, const std::vector<uint32_t> &add_cols, const std::vector<float> &add_scores) {
+                        uint32_t li0, const std::vector<uint32_t> &add_cols, const std::vector<float> &add_scores,
+                        int64_t no_promote = -1) {
     BlockRowState s = old;
     const int64_t r0 = (int64_t)s.br * 4;
     const uint32_t nr = (uint32_t)std::min<int64_t>(4, L.n_in - r0);
@@ -253,6 +254,7 @@ BlockRowState bulk_edit(const Layer &L, const BlockRowState &old, const std::vec
         }
     }
     for (uint32_t bc : windows) {
+        if ((int64_t)bc == no_promote) continue;
         std::vector<std::pair<uint32_t, std::pair<uint32_t, uint8_t>>> found;  // (li, (c, byte))
         for (uint32_t li = 0; li < nr; ++li)
             for (auto it = find(s.rows[li], bc * 4); it != s.rows[li].end() && it->first < bc * 4 + 4; ++it)
@@ -377,6 +379,146 @@ struct BlockRowSim {
         for (const auto &f : found) remove(f.first, f.second);
     }
 };
+
+// The block4 store's reservations under one synap_row_step
+// (delta_csr_memory.hpp:1203-1258), replayed edit by edit on block row br as
+// the reference makes them: a tile slot's removal through a handle (a
+// sparse tile re-committed, a dense one written in place), a demotion's
+// erase, and each insert's promotion -- a write into an existing tile
+// (committed when sparse, then maybe_compress) or a new tile
+// (get_or_create: the row grown without room, the budget's MemoryError;
+// then the commit of its slots).  A commit dropped at the tile budget
+// leaves its tile as it was (counted in L.b4_dropped); such tiles are
+// returned with their final bytes, which the call's new state takes.  When
+// a new tile's row growth meets the budget, *nomem_at is set to that
+// insert's index (its scattered insert stands, its window is not promoted,
+// later inserts are not made).
+struct B4Replay {
+    std::map<uint32_t, PolicyTile> dropped;  // tiles whose commit was dropped: their final state
+    int64_t nomem_at = -1;
+    uint32_t nomem_bc = 0;
+    std::string nomem_msg;
+};
+
+B4Replay b4_policy_replay(Layer &L, const BlockRowState &state, uint32_t li, const std::vector<uint32_t> &rm_cols,
+                          const std::vector<bool> &rm_is_b4, const std::vector<uint32_t> &add_cols,
+                          const std::vector<float> &add_scores) {
+    B4Replay out;
+    const size_t br = state.br;
+    const uint32_t nr = (uint32_t)std::min<int64_t>(4, L.n_in - (int64_t)br * 4);
+    std::map<uint32_t, PolicyTile> tiles = state.tiles;
+    std::map<uint32_t, uint8_t> rows[4];
+    for (uint32_t l = 0; l < 4; ++l)
+        for (const auto &e : state.rows[l]) rows[l][e.first] = e.second;
+    std::set<uint32_t> touched_by_drop;
+    auto live_of = [](const PolicyTile &t) {
+        uint32_t n = 0;
+        for (uint8_t b : t.b) n += b != 0;
+        return n;
+    };
+    auto len_of = [&](const PolicyTile &t) { return (uint64_t)tile_len(t.sparse != 0, live_of(t)); };
+    auto use = [&](uint64_t &ui, uint64_t &ue, uint64_t &ut) {
+        ui = ue = ut = 0;
+        uint32_t prev = 0;
+        for (const auto &kv : tiles) {
+            ui += uleb_len(kv.first - prev);
+            prev = kv.first;
+            ++ue;
+            ut += len_of(kv.second);
+        }
+    };
+    // a sparse tile's handle commits its slots re-encoded by live count; a
+    // dense one is written in place.  false: the commit was dropped
+    auto write_slot = [&](uint32_t bc, uint32_t slot, uint8_t byte) {
+        PolicyTile &t = tiles[bc];
+        if (!t.sparse) {
+            t.b[slot] = byte;
+            return true;
+        }
+        uint64_t ui, ue, ut;
+        use(ui, ue, ut);
+        PolicyTile nt = t;
+        nt.b[slot] = byte;
+        const uint32_t live = live_of(nt);
+        nt.sparse = live <= L.switch_point ? 1 : 0;
+        if (!b4res_commit(L, br, len_of(t), len_of(nt), ut)) {
+            touched_by_drop.insert(bc);
+            return false;
+        }
+        t = nt;
+        return true;
+    };
+    for (size_t k = 0; k < rm_cols.size(); ++k) {
+        const uint32_t c = rm_cols[k];
+        if (!rm_is_b4[k]) {
+            rows[li].erase(c);
+            continue;
+        }
+        auto it = tiles.find(c / 4);
+        const uint32_t slot = (c % 4) * 4 + li;
+        if (it == tiles.end() || it->second.b[slot] == 0) continue;
+        write_slot(c / 4, slot, 0);
+        it = tiles.find(c / 4);
+        if (live_of(it->second) < 2) {  // block4_demote_tile, then the tile's erase
+            const uint32_t bc = it->first;
+            for (uint32_t sl = 0; sl < 16; ++sl) {
+                const uint32_t b = it->second.b[sl], l2 = sl & 3u, c2 = bc * 4 + (sl >> 2);
+                if (b == 0 || l2 >= nr || (int64_t)c2 >= L.n_out) continue;
+                rows[l2][c2] = (uint8_t)((requant(b & 0xFu) << 4) | requant(b >> 4));
+            }
+            tiles.erase(it);
+        }
+    }
+    for (size_t i = 0; i < add_cols.size(); ++i) {
+        const uint32_t c = add_cols[i], bc = c / 4;
+        rows[li][c] = (uint8_t)fp4_encode(add_scores[i]);  // weight code fp4(0) = 0
+        auto it = tiles.find(bc);
+        if (it != tiles.end()) {
+            const uint8_t sb = rows[li][c];
+            write_slot(bc, (c % 4) * 4 + li, (uint8_t)(requant(sb >> 4) | (requant(sb & 0xFu) << 4)));
+            PolicyTile &t = tiles[bc];
+            if (!t.sparse && live_of(t) <= L.switch_point) t.sparse = 1;  // maybe_compress
+            rows[li].erase(c);
+            continue;
+        }
+        std::vector<std::pair<uint32_t, uint32_t>> found;  // (row in block, column)
+        for (uint32_t l = 0; l < nr; ++l)
+            for (auto e = rows[l].lower_bound(bc * 4); e != rows[l].end() && e->first < bc * 4 + 4; ++e)
+                found.push_back({l, e->first});
+        if (found.size() < 2) continue;
+        uint64_t ui, ue, ut;
+        use(ui, ue, ut);
+        auto nx = tiles.upper_bound(bc);
+        const uint32_t prev = nx == tiles.begin() ? 0u : std::prev(nx)->first;
+        int64_t d = (int64_t)uleb_len(bc - prev);
+        if (nx != tiles.end()) d += (int64_t)uleb_len(nx->first - bc) - (int64_t)uleb_len(nx->first - prev);
+        try {
+            b4res_insert_tile(L, br, d, ui, ue, ut);
+        } catch (const Error &e) {
+            out.nomem_at = (int64_t)i;
+            out.nomem_bc = bc;
+            out.nomem_msg = e.msg;
+            break;
+        }
+        PolicyTile nt;
+        nt.sparse = 1;  // new tiles start sparse-empty (1 byte)
+        tiles[bc] = nt;
+        PolicyTile full = nt;
+        for (const auto &f : found) {
+            const uint8_t sb = rows[f.first][f.second];
+            full.b[(f.second - bc * 4) * 4 + f.first] = (uint8_t)(requant(sb >> 4) | (requant(sb & 0xFu) << 4));
+        }
+        full.sparse = live_of(full) <= L.switch_point ? 1 : 0;
+        if (b4res_commit(L, br, 1, len_of(full), ut + 1)) tiles[bc] = full;
+        else touched_by_drop.insert(bc);
+        for (const auto &f : found) rows[f.first].erase(f.second);
+    }
+    for (uint32_t bc : touched_by_drop) {
+        auto it = tiles.find(bc);
+        if (it != tiles.end()) out.dropped[bc] = it->second;
+    }
+    return out;
+}
 
 // L.out_deg holds out_degree; mark: from now on the policy keeps it.
 void ensure_out_deg(Layer &L, bool mark) {
@@ -625,6 +767,21 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
         }
         sim.promote(li, add_cols[i]);
     }
+    // the block4 store's reservations under these edits
+    B4Replay b4r;
+    {
+        std::vector<uint32_t> rm_cols;
+        std::vector<bool> rm_b4;
+        for (const auto &re : to_remove) {
+            rm_cols.push_back(re.col);
+            rm_b4.push_back(re.is_b4);
+        }
+        b4r = b4_policy_replay(L, state, li, rm_cols, rm_b4, add_cols, add_scores);
+        if (b4r.nomem_at >= 0) {
+            add_cols.resize((size_t)b4r.nomem_at + 1);
+            add_scores.resize((size_t)b4r.nomem_at + 1);
+        }
+    }
     // out_degree as the reference keeps it
     const int64_t n_edit = (int64_t)(to_remove.size() + add_cols.size());
     if (n_edit > 0) {
@@ -665,7 +822,9 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
         // patch of the block row, or through the bulk pipeline
         bool done = false;
         if (patch_mode) {
-            BlockRowState nu = bulk_edit(L, state, prune_keys, li, add_cols, add_scores);
+            BlockRowState nu = bulk_edit(L, state, prune_keys, li, add_cols, add_scores,
+                                         b4r.nomem_at >= 0 ? (int64_t)b4r.nomem_bc : -1);
+            for (const auto &kv : b4r.dropped) nu.tiles[kv.first] = kv.second;
             if (defer) {
                 // kept on the host until an entry point other than the policy's
                 // runs (policy_flush)
@@ -693,6 +852,10 @@ bool synap_row_step(Layer &L, int64_t &cursor, float importance_cutoff, int64_t 
             L.out_deg_tracked = tracked;
             L.policy_clean.clear();
         }
+    }
+    if (b4r.nomem_at >= 0) {
+        cursor = cursor0;
+        throw_error(SILI_ERR_NOMEM, b4r.nomem_msg);
     }
     if (!no_room.empty()) {
         cursor = cursor0;

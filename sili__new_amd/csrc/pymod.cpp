@@ -439,11 +439,32 @@ class Layer {
     }
     void equalizer_step() { ck(sili_equalizer_step(L_)); }
     void equalize_to_capacity(int te, int tb) { ck(sili_equalize_to_capacity(L_, te, tb)); }
-    // Block rows reserve no tile bytes beyond their content on the device
-    // (delta_csr_memory.hpp:767-835 has nothing to reserve), so these keep
-    // the tiles as they are.
-    void expand_block4_headroom(float) {}
-    void compact_block4() {}
+    // the block rows' tile-byte reservations (sili/cpu_backend.cpp:932-943)
+    void expand_block4_headroom(float bf) { ck(sili_expand_block4_headroom(L_, bf)); }
+    void compact_block4() { ck(sili_compact_block4(L_)); }
+    // the block4 store's reservations per block row, as the reference's
+    // Block4Store holds them (sili_export_block4_layout)
+    py::dict export_block4_layout() {
+        const py::ssize_t rows = (py::ssize_t)((n_in_ + 3) / 4);
+        py::array_t<uint64_t> ia(rows), ea(rows), ta(rows), ui(rows), ue(rows), ut(rows), out(6);
+        ck(sili_export_block4_layout(L_, ia.mutable_data(), ea.mutable_data(), ta.mutable_data(), ui.mutable_data(),
+                                     ue.mutable_data(), ut.mutable_data(), out.mutable_data()));
+        py::dict d;
+        d["ia"] = ia;
+        d["ea"] = ea;
+        d["ta"] = ta;
+        d["ui"] = ui;
+        d["ue"] = ue;
+        d["ut"] = ut;
+        auto o = out.unchecked<1>();
+        d["dropped_growth_events"] = o(0);
+        d["row_merge_overflow_events"] = o(1);
+        d["row_merge_overflow_bytes_dropped"] = o(2);
+        d["idx_budget"] = o(3);
+        d["tile_budget"] = o(4);
+        d["evicted"] = o(5);
+        return d;
+    }
     py::dict export_layout() {
         py::array_t<uint64_t> bs((py::ssize_t)(n_in_ + 1)), be((py::ssize_t)n_in_), es((py::ssize_t)(n_in_ + 1)),
             ee((py::ssize_t)n_in_);
@@ -846,6 +867,7 @@ PYBIND11_MODULE(_sili_hip, m) {
              py::arg("target_bytes_per_row") = 0)
         .def("expand_block4_headroom", &Layer::expand_block4_headroom, py::arg("blank_fraction") = 0.2f)
         .def("compact_block4", &Layer::compact_block4)
+        .def("export_block4_layout", &Layer::export_block4_layout)
         .def("zero_accum", &Layer::zero_accum)
         .def("info", &Layer::info)
         .def("export_scattered", &Layer::export_scattered)

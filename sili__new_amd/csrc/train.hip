@@ -739,6 +739,124 @@ __global__ __launch_bounds__(128) void k_train_b4(B4TrainArgs a) {
     }
 }
 
+// ---- the block rows' write-back with eviction --------------------------------
+// Block4Store::merge_row_workspace (block4.hpp:1367-1462) for one block row,
+// tiles t0..t1 (canonical order, tcol[t] the tile's block column), by one
+// wave: every lane calls it with the same arguments.  used: the row's stored
+// bytes (tiles sparse-packed or 16 bytes by flags[t]), alloc: its reserved
+// tile bytes.  While the row does not fit, its live slot of lowest
+// |importance code x is[row] x ois[col]| (fp64) is zeroed -- in the
+// reference's scan order (tile, tile row, tile column), the first on ties;
+// a NaN importance met first is never displaced -- and its tile re-encoded by
+// live count.  A row that still does not fit counts an overflow event and
+// the bytes past its last whole tile that fits.  Tile words are read and
+// written at device scope (they are rewritten while other lanes scan them);
+// lane 0 makes every write.  ctr: [evicted, overflow events, overflow bytes].
+__device__ __forceinline__ uint32_t tile_word_load(const uint8_t *tiles, uint64_t w) {
+    return __hip_atomic_load(reinterpret_cast<const uint32_t *>(tiles) + w, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t word_live(uint32_t v) {
+    return (uint32_t)((v & 0xFFu) != 0u) + (uint32_t)((v & 0xFF00u) != 0u) + (uint32_t)((v & 0xFF0000u) != 0u) +
+           (uint32_t)((v & 0xFF000000u) != 0u);
+}
+
+__device__ void b4_merge_row_wave(uint8_t *tiles, uint8_t *flags, const uint32_t *__restrict__ tcol, uint32_t t0,
+                                  uint32_t t1, int64_t br, uint64_t used, uint64_t alloc, const float *is,
+                                  const float *ois, int64_t n_in, int64_t n_out, uint32_t sp,
+                                  unsigned long long *ctr) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t npos = (t1 - t0) * 16u;
+    while (used > alloc) {
+        uint32_t first = 0xFFFFFFFFu, bp = 0xFFFFFFFFu;
+        double first_a = 0.0, ba = 0.0;
+        for (uint32_t p = lane; p < npos; p += 64u) {
+            const uint32_t t = t0 + (p >> 4), li = (p >> 2) & 3u, lj = p & 3u, slot = lj * 4u + li;
+            const uint32_t v = tile_word_load(tiles, (uint64_t)t * 4u + (slot >> 2));
+            const uint32_t byte = (v >> (8u * (slot & 3u))) & 0xFFu;
+            if (byte == 0u) continue;
+            const int64_t row = br * 4 + li, col = (int64_t)tcol[t] * 4 + lj;
+            const float isv = (is && row < n_in) ? is[row] : 1.0f;
+            const float oisv = (ois && col < n_out) ? ois[col] : 1.0f;
+            const double a = __builtin_fabs((double)fp4_decode(byte >> 4) * (double)isv * (double)oisv);
+            if (p < first) {
+                first = p;
+                first_a = a;
+            }
+            if (!__builtin_isnan(a) && (bp == 0xFFFFFFFFu || a < ba || (a == ba && p < bp))) {
+                ba = a;
+                bp = p;
+            }
+        }
+        // wave minima: the first live slot, and the lowest (|imp|, position)
+        // over the slots whose importance is a number
+        for (int off = 32; off >= 1; off >>= 1) {
+            const uint32_t of = (uint32_t)__shfl_xor((int)first, off);
+            const double ofa = __shfl_xor(first_a, off);
+            if (of < first) {
+                first = of;
+                first_a = ofa;
+            }
+            const uint32_t obp = (uint32_t)__shfl_xor((int)bp, off);
+            const double oba = __shfl_xor(ba, off);
+            if (obp != 0xFFFFFFFFu && (bp == 0xFFFFFFFFu || oba < ba || (oba == ba && obp < bp))) {
+                ba = oba;
+                bp = obp;
+            }
+        }
+        if (first == 0xFFFFFFFFu) break;  // nothing live left
+        const uint32_t win = __builtin_isnan(first_a) ? first : bp;
+        const uint32_t t = t0 + (win >> 4), li = (win >> 2) & 3u, lj = win & 3u, slot = lj * 4u + li;
+        uint32_t live = 0;
+        for (uint32_t w = 0; w < 4u; ++w) live += word_live(tile_word_load(tiles, (uint64_t)t * 4u + w));
+        const uint32_t before = tile_len(flags[t] != 0, live);
+        const uint32_t nsp = (live - 1u) <= sp ? 1u : 0u;
+        if (lane == 0u) {
+            uint32_t *wp = reinterpret_cast<uint32_t *>(tiles) + (uint64_t)t * 4u + (slot >> 2);
+            const uint32_t v = __hip_atomic_load(wp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(wp, v & ~(0xFFu << (8u * (slot & 3u))), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            flags[t] = (uint8_t)nsp;
+            atomicAdd(ctr, 1ull);
+        }
+        __threadfence();
+        used = used - before + tile_len(nsp != 0u, live - 1u);
+    }
+    if (used > alloc && lane == 0u) {
+        // the write-back clamped to the whole tiles that fit
+        uint64_t fit = 0;
+        for (uint32_t t = t0; t < t1; ++t) {
+            uint32_t live = 0;
+            for (uint32_t w = 0; w < 4u; ++w) live += word_live(tile_word_load(tiles, (uint64_t)t * 4u + w));
+            const uint32_t len = tile_len(flags[t] != 0, live);
+            if (fit + len > alloc) break;
+            fit += len;
+        }
+        atomicAdd(ctr + 1, 1ull);
+        atomicAdd(ctr + 2, (unsigned long long)(used - fit));
+    }
+}
+
+// The dense update's write-back (linear_disldo.hpp:1839-1880): one wave per
+// block row, after its tiles were re-encoded by live count.
+__global__ __launch_bounds__(256) void k_b4_merge(uint8_t *tiles, uint8_t *flags, const uint32_t *tile_start,
+                                                  const uint32_t *tcol, const uint32_t *alloc, int64_t brows,
+                                                  const float *is, const float *ois, int64_t n_in, int64_t n_out,
+                                                  uint32_t sp, unsigned long long *ctr) {
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t br = (int64_t)blockIdx.x * WAVES_T + wave;
+    if (br >= brows) return;
+    const uint32_t t0 = tile_start[br], t1 = tile_start[br + 1];
+    if (t0 == t1) return;
+    uint64_t used = 0;
+    for (uint32_t t = t0 + lane; t < t1; t += 64u) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(tiles + (uint64_t)t * 16u);
+        used += tile_len(flags[t] != 0, word_live(v.x) + word_live(v.y) + word_live(v.z) + word_live(v.w));
+    }
+    for (int off = 32; off >= 1; off >>= 1) used += (uint64_t)__shfl_xor((long long)used, off);
+    if (used <= alloc[br]) return;
+    b4_merge_row_wave(tiles, flags, tcol, t0, t1, br, used, alloc[br], is, ois, n_in, n_out, sp, ctr);
+}
+
 // The sparse-gradient update of block4 tiles (sisldo_ops.hpp:848-1100).
 struct SparseB4Args {
     const uint32_t *byte_start, *tile_start;
@@ -753,6 +871,13 @@ struct SparseB4Args {
     float lr, beta2, eps;
     int lr_per_row_nnz, damp;
     uint64_t seed;
+    // the write-back after every (batch row, block row): tile_is_sparse,
+    // the tiles' block columns, the rows' reserved tile bytes, switch_point
+    // and the counters (b4_merge_row_wave)
+    uint8_t *flags;
+    const uint32_t *tcol, *alloc;
+    uint32_t sp;
+    unsigned long long *ctr;
 };
 
 // One wave per canonical block row; batch rows outermost, the row's tiles
@@ -784,10 +909,12 @@ __global__ __launch_bounds__(256) void k_sparse_train_b4(SparseB4Args a) {
     const int64_t my_row = br * 4 + lane;  // lanes 0..3: the row they sum
     double rs = 0.0, rsc = 0.0;
     const uint32_t end = a.byte_start[br + 1];
+    const bool merge = a.lr != 0.0f && a.alloc != nullptr;
     for (int64_t b = 0; b < B; ++b) {
         const float in_val = row_ok ? a.xT[row * B + b] : 0.0f;
         float dxacc = 0.0f;
         double rgacc = 0.0, rgcacc = 0.0;
+        uint64_t used = 0;  // the row's stored tile bytes after this batch row
         uint32_t pos = a.byte_start[br], carry = 0, ebase = t0;
         while (pos < end) {
             const Chunk ch = decode_chunk(a.idx, pos, end, carry);
@@ -806,8 +933,9 @@ __global__ __launch_bounds__(256) void k_sparse_train_b4(SparseB4Args a) {
                 const bool active = has && dy_val != 0.0f;
                 float tdx = 0.0f;
                 double rg = 0.0, rgc = 0.0;
+                const uint32_t slot = lj * 4u + li;
+                uint32_t newbyte = (merge && has) ? a.tiles[t * 16 + slot] : 0u;
                 if (active) {
-                    const uint32_t slot = lj * 4u + li;
                     const uint32_t byte = a.tiles[t * 16 + slot];
                     const float w_decoded = fp4_decode(byte & 0xFu);
                     const float out_scale = a.os[col * rank];
@@ -827,11 +955,32 @@ __global__ __launch_bounds__(256) void k_sparse_train_b4(SparseB4Args a) {
                         const uint32_t wq = fp4_encode_stochastic(new_w / combined_scale, splitmix64(base));
                         const uint32_t iq = fp4_encode_stochastic(imp / combined_imp_scale, splitmix64(base + 1ull));
                         a.tiles[t * 16 + slot] = (uint8_t)((iq << 4) | wq);
+                        newbyte = (iq << 4) | wq;
                         rg = ((double)w_decoded * (double)out_scale) * (double)grad;
                         rgc = ((double)w_decoded * (double)out_scale) * (double)contrib;
                     }
                 }
                 const uint64_t act = __ballot(active);
+                if (merge) {
+                    // a rewritten tile is re-encoded by its live count
+                    // (commit_dirty_tile_in_workspace); the row's stored
+                    // bytes add up tile by tile
+                    const uint64_t livem = __ballot(newbyte != 0u);
+                    for (uint32_t u = 0; u < 4u && sub + u < nt; ++u) {
+                        const uint32_t live = (uint32_t)__popcll((livem >> (16u * u)) & 0xFFFFull);
+                        const bool dirty = ((act >> (16u * u)) & 0xFFFFull) != 0ull;
+                        const int64_t tu = (int64_t)ebase + sub + u;
+                        // lane 16u handles tile tu at every batch row: it
+                        // alone reads and writes the tile's flag
+                        uint32_t f = 0;
+                        if (lane == 16u * u) {
+                            f = dirty ? (live <= a.sp ? 1u : 0u) : (uint32_t)a.flags[tu];
+                            if (dirty) a.flags[tu] = (uint8_t)f;
+                        }
+                        f = (uint32_t)__shfl((int)f, (int)(16u * u));
+                        used += tile_len(f != 0u, live);
+                    }
+                }
                 s_dx[wave][lane] = tdx;
                 s_rg[wave][lane] = rg;
                 s_rgc[wave][lane] = rgc;
@@ -855,6 +1004,12 @@ __global__ __launch_bounds__(256) void k_sparse_train_b4(SparseB4Args a) {
             a.dx[b * a.n_in + my_row] += dxacc;
             rs = rs + rgacc;
             rsc = rsc + rgcacc;
+        }
+        // the block row's workspace written back (sisldo_ops.hpp:1036-1052)
+        if (merge && used > a.alloc[br]) {
+            __threadfence();  // this batch row's tile writes, before the scan reads them
+            b4_merge_row_wave(a.tiles, a.flags, a.tcol, t0, t1, br, used, a.alloc[br], a.is, a.ois, a.n_in,
+                              a.n_out, a.sp, a.ctr);
         }
     }
     if (lane < 4u && my_row < a.n_in) {
@@ -1128,6 +1283,18 @@ void launch_sparse_train(Layer &L, const float *xT, const float *gT, int64_t B, 
     SILI_HIP(hipGetLastError());
 }
 
+void launch_b4_merge(Layer &L, hipStream_t st) {
+    if (L.B4.ntiles == 0) return;
+    const uint32_t *tcol = b4_tile_cols(L);
+    const uint32_t *alloc = b4res_device_alloc(L, st);
+    unsigned long long *ctr = b4res_counters(L, st);
+    ProfScope ps("b4_merge", st);
+    launch(k_b4_merge, dim3((unsigned)((L.B4.brows + WAVES_T - 1) / WAVES_T)), dim3(256), 0, st, L.B4.tiles.p,
+           L.B4.sparse.p, (const uint32_t *)L.B4.tile_start.p, tcol, alloc, L.B4.brows, (const float *)L.is.p,
+           (const float *)L.ois.p, L.n_in, L.n_out, L.switch_point, ctr);
+    SILI_HIP(hipGetLastError());
+}
+
 void launch_sparse_train_b4(Layer &L, const float *xT, const float *gT, int64_t B, float *dx,
                             const TrainParams &p, uint64_t seed, hipStream_t st) {
     if (L.B4.ntiles == 0) return;
@@ -1157,6 +1324,11 @@ void launch_sparse_train_b4(Layer &L, const float *xT, const float *gT, int64_t 
     a.lr_per_row_nnz = p.lr_per_row_nnz;
     a.damp = p.damp_by_importance;
     a.seed = seed;
+    a.flags = L.B4.sparse.p;
+    a.tcol = b4_tile_cols(L);
+    a.alloc = b4res_device_alloc(L, st);
+    a.sp = L.switch_point;
+    a.ctr = b4res_counters(L, st);
     ProfScope ps("sparse_train_b4", st);
     launch(k_sparse_train_b4, dim3((unsigned)((L.B4.brows + WAVES_T - 1) / WAVES_T)), dim3(256), 0, st, a);
     launch(k_sparse_train_vs_b4, dim3(nblk(L.n_in)), dim3(TPB), 0, st, (const uint32_t *)L.B4.tile_start.p, L.n_in,

@@ -204,3 +204,83 @@ def test_block4_sparse_update_matches_reference(case):
         for k in ("value_scale", "vs_importance", "vs_step"):
             assert np.array_equal(getattr(H, k), st[k]), what + ": " + k
     assert (H.tiles[:len(tiles0)] != tiles0).sum() > 4, "the tiles barely changed"
+
+
+# the block4 cases whose tiles grow past rows reserved to their content
+EVICTING_CASES = (0, 1, 2, 3, 4)
+
+
+def _tight_pair(case, slack):
+    """Host and reference layers of block4 case `case` whose block rows
+    reserve their tiles' stored bytes plus `slack` (block4_expand_headroom(0,
+    slack)), so tiles that grow in the update outgrow their rows."""
+    from train_util import add_tiles, tile_opts
+    n_in, n_out, dens, seed, B, lr, opts, variant = B4_CASES[case]
+    lopts, copts = split_opts(opts)
+    c = add_tiles(make_train_case(n_in, n_out, dens, seed, **lopts), seed=case, **tile_opts(opts))
+    H, R = host_layer(c), ref_layer(c)
+    H.load_tiles(c["br"], c["bc"], c["tiles"])
+    for t in range(len(c["br"])):
+        R.put_tile(int(c["br"][t]), int(c["bc"][t]), c["tiles"][16 * t:16 * t + 16])
+    R.block4_headroom(0.0, slack)
+    (_, _, ta, _, _, _), _ = R.block4_reservations()
+    H.b4_alloc = np.array(ta, np.uint64)
+    H.b4_flags = R.export_tiles_packed()[0][:len(c["br"])].copy()
+    return c, H, R, B, lr, variant, copts
+
+
+def _same_tiles(H, R, what):
+    br, bc, tr = R.export_tiles()
+    assert np.array_equal(H.tile_br, br) and np.array_equal(H.tile_bc, bc), what + ": tile set"
+    assert np.array_equal(H.tiles[:len(tr)], tr), what + ": tile bytes"
+    assert np.array_equal(H.b4_flags[:len(br)], R.export_tiles_packed()[0][:len(br)]), what + ": tile_is_sparse"
+    _, ctr = R.block4_reservations()
+    assert (H.b4_counters[1], H.b4_counters[2]) == (ctr[1], ctr[2]), what + ": merge overflow counters"
+
+
+@pytest.mark.parametrize("slack", [0, 3])
+@pytest.mark.parametrize("case", range(len(B4_CASES)))
+def test_block4_update_eviction_matches_reference(case, slack):
+    """The dense update on block rows with little room: tiles that grow past
+    their row's reserved bytes lose their lowest-|true importance| live slots
+    (Block4Store::merge_row_workspace, block4.hpp:1367-1462; called at
+    linear_disldo.hpp:1865-1878).  Tile bytes, tile_is_sparse and the
+    overflow counters exact against the reference, dx within the bar."""
+    from train_util import dx_bound_tiles
+    c, H, R, B, lr, variant, copts = _tight_pair(case, slack)
+    rng = c["rng"]
+    for step in range(3):
+        what = f"case {case} slack {slack} step {step}"
+        x = rng.normal(size=(B, c["n_in"])).astype(np.float32)
+        dy = rng.normal(size=(B, c["n_out"])).astype(np.float32)
+        bound = dx_bound(H, dy, lr) + dx_bound_tiles(H, dy, lr)
+        dxh, _, _ = H.backward_train(x, dy, lr, contracted=True, variant=variant, **copts)
+        dxr, _, _ = R.backward_train(x, dy, lr, variant=variant, **copts)
+        _same_tiles(H, R, what)
+        assert_close_terms(dxh, dxr, bound, what + ": dx")
+    if slack == 0 and case in EVICTING_CASES:
+        assert H.b4_counters[0] > 0, "nothing was evicted"
+
+
+@pytest.mark.parametrize("slack", [0, 3])
+@pytest.mark.parametrize("case", range(len(B4_CASES)))
+def test_block4_sparse_update_eviction_matches_reference(case, slack):
+    """The sparse-gradient update on block rows with little room: the write-
+    back with eviction after every (batch row, block row)
+    (sisldo_ops.hpp:1036-1052), the reference's seeded draws replayed."""
+    from train_util import dx_bound_sparse, dx_bound_tiles, sparse_dy
+    c, H, R, B, lr, _, copts = _tight_pair(case, slack)
+    rng = c["rng"]
+    for step in range(3):
+        what = f"sparse case {case} slack {slack} step {step}"
+        x = rng.normal(size=(B, c["n_in"])).astype(np.float32)
+        dp, di, dv, dense = sparse_dy(rng, B, c["n_out"], density=0.6)
+        bound = dx_bound_sparse(H, dense, lr) + dx_bound_tiles(H, dense, lr, sparse=True)
+        dseed = 7000 * case + step + 1
+        dxh, _, _ = H.backward_sparse_train(x, dp, di, dv, B, lr, contracted=True, draw_mode=0, draw_seed=dseed,
+                                            **copts)
+        dxr, _, _ = R.backward_sparse_train(x, dp, di, dv, B, lr, draw_seed=dseed, **copts)
+        _same_tiles(H, R, what)
+        assert_close_terms(dxh, dxr, bound, what + ": dx")
+    if slack == 0 and case in EVICTING_CASES:
+        assert H.b4_counters[0] > 0, "nothing was evicted"
