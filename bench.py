@@ -43,6 +43,8 @@ def parse():
     p.add_argument("--config", type=int, default=1)
     p.add_argument("--copies", type=int, default=0, help="0 = enough for > 512 MiB")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-configs", action="store_true",
+                   help="config 1: leave out the summary of configs 2, 3 and 4 timed after the line's own step")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--synapto-reps", type=int, default=5, help="config 3: timed synaptogenesis steps")
     p.add_argument("--c4-batches", default="1,8,128", help="config 4: token batches to time")
@@ -681,7 +683,7 @@ def run_config4(a, hip, api, rt):
         d.clear()
     layers.clear()
     out["cpu_baseline"] = cpu
-    print(json.dumps(out), flush=True)
+    return out
 
 
 def run_index_decode(a, hip, api, rt):
@@ -815,7 +817,6 @@ def main():
         print(json.dumps({"copy_probe_bytes": n, "copies": 3}), flush=True)
         return
     import sili__new_amd as hip
-    from sili__new_amd.synth import make_config
 
     if a.index_decode:
         run_index_decode(a, hip, CAbi(hip.LIB_PATH), Hip())
@@ -824,13 +825,22 @@ def main():
         run_sparse_sweep(a, hip, CAbi(hip.LIB_PATH), Hip())
         return
     cfg = a.config
+    api, rt = CAbi(hip.LIB_PATH), Hip()
     if cfg == 4:
-        run_config4(a, hip, CAbi(hip.LIB_PATH), Hip())
-        return
+        out = run_config4(a, hip, api, rt)
+    else:
+        out = run_layer_config(a, hip, api, rt, cfg, a.steps, a.warmup, a.train_lr,
+                               synapto_reps=a.synapto_reps, cpu=not a.no_cpu_baseline)
+    if cfg == 1 and not a.train_lr and not a.no_configs:
+        out["configs"] = other_configs(a, hip, api, rt)
+    print(json.dumps(out), flush=True)
+
+
+def run_layer_config(a, hip, api, rt, cfg, steps, warmup, train_lr, synapto_reps=0, cpu=True):
+    """One step of config 0-3 over rotated layer copies: the bench line."""
+    from sili__new_amd.synth import make_config
     wl = make_config(cfg)
     B, n_in, n_out = wl.batch, wl.n_in, wl.n_out
-    api = CAbi(hip.LIB_PATH)
-    rt = Hip()
 
     # one layer + activation set per copy, all driven on copy 0's stream;
     # enough copies (> 512 MiB) that the 256 MiB MALL cannot serve a step
@@ -845,8 +855,7 @@ def main():
         pool.append(build_copy(cfg, wl, hip, api))
     t_build = time.perf_counter() - t_build
     stream = api.L.sili_stream(pool[0]["h"])
-    train_lr = a.train_lr if cfg in (1, 3) else 0.0
-    if a.train_lr and cfg not in (1, 3):
+    if train_lr and cfg not in (1, 3):
         print(json.dumps({"error": "--train-lr applies to configs 1 and 3 only"}))
         sys.exit(2)
     run = make_step(cfg, api, B, stream, train_lr)
@@ -859,7 +868,7 @@ def main():
     for d in pool:
         run(d)
     rt.sync()
-    for i in range(a.warmup):
+    for i in range(warmup):
         step(i)
     rt.sync()
 
@@ -868,22 +877,22 @@ def main():
     rt.sync()
     rt.record(e0, stream)
     t0 = time.perf_counter()
-    for i in range(a.steps):
+    for i in range(steps):
         step(i)
     rt.record(e1, stream)
     rt.sync()
     wall = time.perf_counter() - t0
-    ms_step = rt.elapsed_ms(e0, e1) / a.steps
+    ms_step = rt.elapsed_ms(e0, e1) / steps
 
     # warm (cache-resident) rate: a single copy, same step count
     w0, w1 = rt.event(), rt.event()
     rt.sync()
     rt.record(w0, stream)
-    for i in range(a.steps):
+    for i in range(steps):
         step(0)
     rt.record(w1, stream)
     rt.sync()
-    warm_ms_step = rt.elapsed_ms(w0, w1) / a.steps
+    warm_ms_step = rt.elapsed_ms(w0, w1) / steps
 
     # profiled pass (same steps): per-kernel times from the dispatches' own
     # begin/end stamps, on the stream the kernels run on
@@ -891,11 +900,11 @@ def main():
         api.ck(api.L.sili_profile_enable(d["h"], 1))
     p0, p1 = rt.event(), rt.event()
     rt.record(p0, stream)
-    for i in range(a.steps):
+    for i in range(steps):
         step(i)
     rt.record(p1, stream)
     rt.sync()
-    prof_ms_step = rt.elapsed_ms(p0, p1) / a.steps
+    prof_ms_step = rt.elapsed_ms(p0, p1) / steps
     kern = {}
     for d in pool:
         for name, (cnt, tot) in api.profile(d["h"]).items():
@@ -906,8 +915,8 @@ def main():
     alg = algorithmic(info, n_in, n_out, B, wl)
     dom_name, (dom_cnt, dom_tot) = max(kern.items(), key=lambda kv: kv[1][1])
     # one op may take several launches (column-block passes): time per op
-    launches = dom_cnt / a.steps
-    dom_avg_ms = dom_tot / a.steps
+    launches = dom_cnt / steps
+    dom_avg_ms = dom_tot / steps
 
     nnz_s, n_tiles = info["nnz_scattered"], info["n_tiles"]
     units = nnz_s + 16 * n_tiles  # stored synapses (scattered + block4 slots)
@@ -978,8 +987,8 @@ def main():
         "value": round(units / (ms_step * 1e-3) / 1e9, 4),
         "unit": "GNNZ/s",
         "n_gpus": 1,
-        "steps": a.steps,
-        "warmup": a.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -999,24 +1008,51 @@ def main():
         "warm_value": round(units / (warm_ms_step * 1e-3) / 1e9, 4),
         "wall_s_timed": round(wall, 4),
         "roofline": roof,
-        "kernels_ms_per_step": {k: round(v[1] / a.steps, 5) for k, v in kern.items()},
+        "kernels_ms_per_step": {k: round(v[1] / steps, 5) for k, v in kern.items()},
         "profiled_ms_per_step": round(prof_ms_step, 5),
     }
     # the layers and their device buffers are released here, while the HIP
     # runtime is fully alive (not at interpreter teardown)
     release_pool(api, pool)
     rt.sync()
-    if cfg == 3 and a.synapto_reps > 0:
-        out["synapto_gpu"] = time_synapto(hip, wl, a.synapto_reps)
+    if cfg == 3 and synapto_reps > 0:
+        out["synapto_gpu"] = time_synapto(hip, wl, synapto_reps)
     if cfg == 1 and a.synap_cycles > 0:
         out["synap_policy"] = time_synap_policy(hip, wl, a.synap_cycles, a.cpu_seconds)
-    if a.no_cpu_baseline:
-        out["cpu_baseline"] = None
-    else:
-        out["cpu_baseline"] = cpu_baseline(cfg, a.cpu_seconds, lr=train_lr)
+    out["cpu_baseline"] = cpu_baseline(cfg, a.cpu_seconds, lr=train_lr) if cpu else None
     if a.verbose:
         print(f"build {t_build:.1f}s copies {copies}", file=sys.stderr)
-    print(json.dumps(out), flush=True)
+    return out
+
+
+def other_configs(a, hip, api, rt):
+    """Configs 2, 3 (with its synaptogenesis step) and 4 (batches 1, 8, 128)
+    timed as config 1 is (rotated copies, HIP events over the timed steps,
+    the dominant kernel's algorithmic rate from the profiled pass), at fewer
+    steps; a summary of each line."""
+    res = {}
+    for cfg, steps in ((2, 100), (3, 20)):
+        t0 = time.perf_counter()
+        o = run_layer_config(a, hip, api, rt, cfg, steps, 5, 0.0, synapto_reps=10 if cfg == 3 else 0, cpu=False)
+        r = o["roofline"]
+        res[str(cfg)] = {"workload": o["config"]["workload"], "value": o["value"], "unit": o["unit"],
+                         "ms_per_step": o["ms_per_step"], "steps": o["steps"],
+                         "warm_ms_per_step": o["warm_ms_per_step"],
+                         "dominant": {k: r.get(k) for k in ("kernel", "bound", "achieved", "unit", "peak", "frac",
+                                                           "avg_op_ms")},
+                         "kernels_ms_per_step": o["kernels_ms_per_step"], "wall_s": round(time.perf_counter() - t0, 1)}
+        if cfg == 3:
+            res["3"]["synapto_gpu"] = o["synapto_gpu"]
+    t0 = time.perf_counter()
+    a4 = argparse.Namespace(**vars(a))
+    a4.c4_batches, a4.steps, a4.warmup, a4.no_cpu_baseline = "1,8,128", 200, 5, True
+    o = run_config4(a4, hip, api, rt)
+    res["4"] = {"workload": o["config"]["workload"], "nnz": o["config"]["nnz"],
+                "batches": {b: {"ms_per_step": r["ms_per_step"], "gnnz_s": r["gnnz_s"], "steps": r["steps"],
+                                "pct_hbm_peak": r["pct_hbm_peak"], "dominant": r["dominant"]}
+                            for b, r in o["batches"].items()},
+                "build_s": o["build_s"], "wall_s": round(time.perf_counter() - t0, 1)}
+    return res
 
 
 if __name__ == "__main__":

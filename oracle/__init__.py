@@ -12,5 +12,5 @@ from .oracle import (  # noqa: F401
     HostLayer, RefLayer, build, dense_to_csr, dense_to_top_k_csr, for_encode_row, for_encode_rows, have_ref, lib,
     ref_for_encode, ref_top_k_csr, reflib, SWITCH_POINT, TileEncodingState, pack_tiles, sparse_pack_tile, tile_live,
     ScatteredReservations, row_content, synap_no_room_message, demote_no_room_message,
-    Block4Reservations, block4_row_use, tile_len, tile_len_by_live, uleb_len,
+    Block4Reservations, block4_row_use, tile_len, tile_len_by_live, uleb_len, Block4PutModel, block4_put_layer,
 )

@@ -689,6 +689,72 @@ def block4_row_use(n_in, br, bc, tiles, flags):
     return ui, ue, ut
 
 
+class Block4PutModel:
+    """A block4 store's tiles as Block4Store::get_or_create and a handle's
+    slot writes leave them (block4.hpp:1170-1183,1226-1290; the reference's
+    own tests' fixture, test_disldo_block4_forward.cpp:34-45), with their
+    tile_is_sparse flags and the store's reservations (Block4Reservations)
+    alongside.  put() raises MemoryError where get_or_create's row growth
+    meets a budget; a commit dropped at the tile budget leaves the tile as
+    it was."""
+
+    def __init__(self, n_in, max_weights):
+        self.n_in = n_in
+        self.M = Block4Reservations(n_in, max_weights)
+        self.sp = self.M.sp
+        self.rows = [dict() for _ in range(self.M.rows)]  # bc -> (flag, 16 bytes)
+
+    def use(self):
+        ui, ue, ut = [], [], []
+        for row in self.rows:
+            cols = sorted(row)
+            ui.append(sum(uleb_len(c - p) for c, p in zip(cols, [0] + cols[:-1])))
+            ue.append(len(cols))
+            ut.append(sum(tile_len(row[c][0], np.count_nonzero(row[c][1])) for c in cols))
+        return ui, ue, ut
+
+    def put(self, br, bc, tile):
+        row = self.rows[br]
+        ui, ue, ut = (u[br] for u in self.use())
+        if bc not in row:
+            cols = sorted(row)
+            prev = max([c for c in cols if c < bc], default=0)
+            nxt = min([c for c in cols if c > bc], default=None)
+            d = uleb_len(bc - prev)
+            if nxt is not None:
+                d += uleb_len(nxt - bc) - uleb_len(nxt - prev)
+            self.M.insert_tile(br, d, ui, ue, ut)  # raises MemoryError with the row unchanged
+            row[bc] = (1, np.zeros(16, np.uint8))
+            ut += 1
+        flag, old = row[bc]
+        if flag:  # a sparse tile's handle writes a scratch copy and commits it
+            ok, _ = self.M.commit(br, tile_len(1, np.count_nonzero(old)), tile_len_by_live(np.count_nonzero(tile), self.sp), ut)
+            if ok:
+                row[bc] = (int(np.count_nonzero(tile) <= self.sp), tile.copy())
+        else:  # a dense tile is written in place
+            row[bc] = (0, tile.copy())
+
+
+    def canonical(self):
+        """(br, bc, tiles, flags) in canonical order."""
+        keys = [(b, c) for b, row in enumerate(self.rows) for c in sorted(row)]
+        br = np.array([k[0] for k in keys], np.int32)
+        bc = np.array([k[1] for k in keys], np.int32)
+        tiles = np.concatenate([self.rows[b][c][1] for b, c in keys]) if keys else np.zeros(0, np.uint8)
+        flags = np.array([self.rows[b][c][0] for b, c in keys], np.uint8)
+        return br, bc, tiles, flags
+
+
+def block4_put_layer(n_in, max_weights, br, bc, tiles):
+    """The store a layer's tiles placed one by one in canonical order leave
+    (load_block4_tiles): (Block4PutModel, flags in canonical order)."""
+    T = Block4PutModel(n_in, max_weights)
+    tiles = np.asarray(tiles, np.uint8).reshape(-1, 16)
+    for i in np.lexsort((np.asarray(bc), np.asarray(br))):
+        T.put(int(br[i]), int(bc[i]), tiles[i])
+    return T, T.canonical()[3]
+
+
 FOR_REF_PATH = HERE / "_ref" / "libfor_ref.so"
 _for_ref = None
 
@@ -794,6 +860,8 @@ class HostLayer:
         self.row_elem_start = np.zeros(n_in + 1, np.uint64)
         self.idx = np.zeros(1, np.uint8)
         self.val = np.zeros(1, np.uint8)
+        self.nnz = 0
+        self.index_bytes = 0
         self.n_tiles = 0
         self.brow_byte_start = np.zeros((n_in + 3) // 4 + 1, np.uint64)
         self.brow_tile_start = np.zeros((n_in + 3) // 4 + 1, np.uint64)

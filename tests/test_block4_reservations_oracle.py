@@ -16,8 +16,7 @@ and tile bytes, the budgets and dropped_growth_events, after
 import numpy as np
 import pytest
 
-from oracle import (Block4Reservations, RefLayer, SWITCH_POINT, block4_row_use, have_ref, tile_len,
-                    tile_len_by_live, uleb_len)
+from oracle import Block4PutModel, Block4Reservations, RefLayer, block4_row_use, have_ref
 
 pytestmark = pytest.mark.skipif(not have_ref(), reason="oracle/_ref not built (needs the reference tree)")
 
@@ -108,52 +107,12 @@ def test_expand_beyond_the_tile_budget_raises():
     assert_same(M, use, R, "after a refused expand")
 
 
-class TileModel:
-    """The tiles of a store as get_or_create + handle writes leave them,
-    with the reservation model alongside."""
-
-    def __init__(self, n_in, max_weights):
-        self.n_in = n_in
-        self.M = Block4Reservations(n_in, max_weights)
-        self.rows = [dict() for _ in range(self.M.rows)]  # bc -> (flag, 16 bytes)
-
-    def use(self):
-        ui, ue, ut = [], [], []
-        for row in self.rows:
-            cols = sorted(row)
-            ui.append(sum(uleb_len(c - p) for c, p in zip(cols, [0] + cols[:-1])))
-            ue.append(len(cols))
-            ut.append(sum(tile_len(row[c][0], np.count_nonzero(row[c][1])) for c in cols))
-        return ui, ue, ut
-
-    def put(self, br, bc, tile):
-        row = self.rows[br]
-        ui, ue, ut = (u[br] for u in self.use())
-        if bc not in row:
-            cols = sorted(row)
-            prev = max([c for c in cols if c < bc], default=0)
-            nxt = min([c for c in cols if c > bc], default=None)
-            d = uleb_len(bc - prev)
-            if nxt is not None:
-                d += uleb_len(nxt - bc) - uleb_len(nxt - prev)
-            self.M.insert_tile(br, d, ui, ue, ut)  # raises MemoryError with the row unchanged
-            row[bc] = (1, np.zeros(16, np.uint8))
-            ut += 1
-        flag, old = row[bc]
-        if flag:  # a sparse tile's handle writes a scratch copy and commits it
-            ok, _ = self.M.commit(br, tile_len(1, np.count_nonzero(old)), tile_len_by_live(np.count_nonzero(tile)), ut)
-            if ok:
-                row[bc] = (int(np.count_nonzero(tile) <= SWITCH_POINT), tile.copy())
-        else:  # a dense tile is written in place
-            row[bc] = (0, tile.copy())
-
-
 @pytest.mark.parametrize("seed,max_weights", [(0, 16), (1, 64), (2, 200), (3, 2000), (4, 40)])
 def test_tiles_placed_one_by_one(seed, max_weights):
     rng = np.random.default_rng(50 + seed)
     n_in, n_out = 24, 2400  # block columns up to 600: two-byte deltas
     R = RefLayer.sll(n_in, n_out, max_weights)
-    T = TileModel(n_in, max_weights)
+    T = Block4PutModel(n_in, max_weights)
     n_err = 0
     for step in range(120):
         br = int(rng.integers(0, T.M.rows))
@@ -197,7 +156,7 @@ def test_policy_sequences_keep_the_reference_reservations(seed, max_weights):
     R.load_weights(c["ptrs"], c["cols"], c["w"], c["imp"])
     H = HostLayer(n_in, n_out).load_csr(c["ptrs"], c["cols"], w=c["w"], imp=c["imp"])
     S = ScatteredReservations(n_in, max_weights).load(*row_content(H.row_byte_start, H.row_elem_start))
-    T = TileModel(n_in, max_weights)
+    T = Block4PutModel(n_in, max_weights)
     tiles = c["tiles"].reshape(-1, 16)
     for t in range(len(c["br"])):
         R.sll_put_tile(int(c["br"][t]), int(c["bc"][t]), tiles[t])

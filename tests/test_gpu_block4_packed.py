@@ -32,7 +32,9 @@ def check(L, S, what):
     assert np.array_equal(pk["tile_byte_start"], np.concatenate([[0], np.cumsum(rows)]).astype(np.uint64))
     v = L.block4
     assert v.tiles == len(br) and v.synapses == int(tile_live(tiles).sum())
-    assert v.used_bytes == v.alloc_bytes == len(pk["tile_data"])
+    assert v.used_bytes == len(pk["tile_data"])
+    # alloc_bytes: the rows' reserved tile bytes, which hold their content
+    assert v.alloc_bytes == int(np.sum(L.export_block4_layout()["ta"])) >= v.used_bytes
     assert v.dropped_growth_events == v.row_merge_overflow_events == v.row_merge_overflow_bytes_dropped == 0
     return br, bc, tiles
 
@@ -82,8 +84,10 @@ def test_updates_reencode(hip):
         n_in, n_out, dens, seed, B, lr, opts, variant = B4_CASES[case]
         lopts, copts = split_opts(opts)
         c = add_tiles(make_train_case(n_in, n_out, dens, seed, **lopts), seed=case, **tile_opts(opts))
-        L = gpu_layer(hip, c, variant=variant, extra=16 * len(c["br"]))
+        L = gpu_layer(hip, c, variant=variant, extra=1024 * len(c["br"]))
         L.load_block4_tiles(c["br"], c["bc"], c["tiles"])
+        # rows with room for all their tiles dense: no slot is evicted
+        L.expand_block4_headroom(15.0)
         S = TileEncodingState()
         ex = L.export_block4()
         S.load(ex["br"], ex["bc"], ex["tiles"])

@@ -26,7 +26,7 @@ import numpy as np
 import pytest
 
 import oracle
-from oracle import HostLayer, ScatteredReservations, row_content
+from oracle import Block4Reservations, HostLayer, ScatteredReservations, block4_row_use, row_content
 from train_util import dx_bound, dx_bound_sparse
 from util import assert_close_terms
 
@@ -99,8 +99,13 @@ def test_folded_layer_sequence(hip, batch):
         H.importance_scale = np.full(n_in, np.float32(lr / FP4_MAX), np.float32)
         H.out_deg = np.bincount(cols, minlength=n_out).astype(np.int32)
         H.acc = (np.zeros(n_in, np.float32), np.zeros(n_out, np.float32))
+        # the block4 store as the constructor leaves it: nothing reserved;
+        # promotions grow their rows, the update's write-back evicts
+        H.b4res = Block4Reservations(n_in, n_in * n_out)
+        H.b4_flags = np.zeros(1, np.uint8)
         layers[suffix], hosts[suffix] = L, H
-    for step in range(6):
+    n_tiles = {s: 0 for s in layers}
+    for step in range(9):
         what = f"B{batch} step {step}"
         x = rng.normal(size=(batch, n_in)).astype(np.float32)
         parts, want, bound = [], 0, 0
@@ -128,6 +133,7 @@ def test_folded_layer_sequence(hip, batch):
                 np.testing.assert_allclose(L.get_value_scales(), H.value_scale, rtol=1e-5, atol=0)
             assert_close_terms(L.neuron_input_accum, H.acc[0], H.acc[0], f"{what} {s}: acc_in")
             assert_close_terms(L.neuron_grad_accum, H.acc[1], H.acc[1], f"{what} {s}: acc_grad")
+            same_block4(L, H, f"{what} {s}")
         if step % 3 == 2:
             # FoldedLayer.synaptogenesis(k, importance_cutoff, max_row_weights)
             for s, L in layers.items():
@@ -143,6 +149,9 @@ def test_folded_layer_sequence(hip, batch):
                     assert L.synap_step(0.6, mrw) == H.synap_step(0.6, mrw, reservations=S), f"{what} {s}: synap_step"
                 L.equalizer_step()
                 S.equalizer_step()
+                # equalizer_step steps the block4 store's rows too
+                H.b4res.equalize_step(*block4_row_use(n_in, H.tile_br, H.tile_bc, H.tiles[:16 * H.n_tiles],
+                                                       H.b4_flags[:H.n_tiles]))
                 L.zero_accum()
                 H.acc[0][:] = 0
                 H.acc[1][:] = 0
@@ -155,6 +164,24 @@ def test_folded_layer_sequence(hip, batch):
                 lay = L.export_layout()
                 want = S.layout(*row_content(H.row_byte_start, H.row_elem_start))
                 assert all(np.array_equal(lay[k], want[k]) for k in want), f"{what} {s}: reservations"
+                same_block4(L, H, f"{what} {s} synaptogenesis")
+                n_tiles[s] = max(n_tiles[s], H.n_tiles)
+    assert max(n_tiles.values()) > 0, "no tile was promoted"
+    assert sum(h.b4_counters[0] for h in hosts.values()) > 0, "the update's write-back evicted nothing"
+
+
+def same_block4(L, H, what):
+    """Tiles, their encoding, the block4 reservations and Block4View's
+    counters as the oracle holds them."""
+    from train_util import check_b4_reservations
+    b = L.export_block4()
+    assert np.array_equal(b["br"], H.tile_br) and np.array_equal(b["bc"], H.tile_bc), what + ": tiles"
+    assert np.array_equal(b["tiles"], H.tiles[:16 * len(b["br"])]), what + ": tile bytes"
+    check_b4_reservations(L, H, what)
+    v = L.block4
+    assert v.alloc_bytes == sum(H.b4res.ta), what + ": Block4View.alloc_bytes"
+    assert (v.dropped_growth_events, v.row_merge_overflow_events, v.row_merge_overflow_bytes_dropped) == \
+        (H.b4res.dropped, H.b4_counters[1], H.b4_counters[2]), what + ": Block4View counters"
 
 
 def test_sisldo_layer_sequence(hip):

@@ -8,7 +8,8 @@ import numpy as np
 import pytest
 
 from sili__new_amd.codec import fp4_decode_np
-from train_util import B4_CASES, TRAIN_CASES, add_tiles, dx_bound, host_layer, make_train_case, split_opts
+from train_util import (B4_CASES, TRAIN_CASES, add_tiles, b4_reserve_like_device, check_b4_reservations, dx_bound,
+                        host_layer, make_train_case, split_opts)
 from util import assert_close_terms
 
 pytestmark = pytest.mark.gpu
@@ -178,9 +179,13 @@ def test_block4_update_matches_oracle(hip, case):
     H = host_layer(c)
     H.load_tiles(c["br"], c["bc"], c["tiles"])
     cls = getattr(hip, CLASSES[variant][0])
-    L = cls(n_in, n_out, len(c["cols"]) + 16 * len(c["br"]) + 64)
+    mw = len(c["cols"]) + 16 * len(c["br"]) + 64
+    L = cls(n_in, n_out, mw)
     L.load_weights_with_importance(c["ptrs"], c["cols"], c["w"], c["imp"])
     L.load_block4_tiles(c["br"], c["bc"], c["tiles"])
+    # the rows reserve their tiles' stored bytes: tiles that grow in the
+    # update lose slots in the write-back, on both sides
+    b4_reserve_like_device(L, H, mw)
     if c["rank"] > 1:
         L.set_scale_rank(c["rank"])
     L.set_value_scales(c["vs"])
@@ -207,6 +212,7 @@ def test_block4_update_matches_oracle(hip, case):
         hb, hc, ht = _sorted_tiles(H.tile_br, H.tile_bc, H.tiles[:16 * H.n_tiles], n_out)
         assert np.array_equal(gb, hb) and np.array_equal(gc, hc), what + ": tile set"
         assert np.array_equal(gt, ht), what + ": tile bytes"
+        check_b4_reservations(L, H, what)
         assert_close_terms(dxg, dxh, bound, what + ": dx")
         # batch > 1: the fp64 row sums are associated per synapse on the GPU,
         # per batch step in the oracle; the last-bit differences compound over
@@ -301,6 +307,7 @@ def test_block4_sparse_update_matches_oracle(hip, case):
     H.load_tiles(c["br"], c["bc"], c["tiles"])
     L = gpu_layer(hip, c, deterministic=(case % 2 == 0), extra=16 * len(c["br"]))
     L.load_block4_tiles(c["br"], c["bc"], c["tiles"])
+    b4_reserve_like_device(L, H, len(c["cols"]) + 64 + 16 * len(c["br"]))
     s0 = 977 + case
     L.seed_stochastic_rounding(s0)
     tiles0 = c["tiles"].copy()
@@ -319,6 +326,7 @@ def test_block4_sparse_update_matches_oracle(hip, case):
         hb, hc, ht = _sorted_tiles(H.tile_br, H.tile_bc, H.tiles[:16 * H.n_tiles], n_out)
         assert np.array_equal(gb, hb) and np.array_equal(gc, hc), what + ": tile set"
         assert np.array_equal(gt, ht), what + ": tile bytes"
+        check_b4_reservations(L, H, what)
         assert_close_terms(dxg, dxh, bound, what + ": dx")
         vs, st = L.get_value_scales(), L.get_scale_state()
         if B == 1:

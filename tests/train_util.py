@@ -224,3 +224,29 @@ B4_CASES = [
     (20, 1027, 0.01, 30, 100, 0.01, dict(tile_density=0.5, tile_gap=(61, 201)), "resync"),
 ]
 TILE_OPTS = ("tile_density", "tile_gap")
+
+
+def b4_reserve_like_device(L, H, max_weights):
+    """Give the oracle layer H the block4 reservations and tile encoding that
+    L's load_block4_tiles left (tiles placed one by one in canonical order,
+    oracle.block4_put_layer), checking the device holds the same; the
+    updates' write-back then evicts on both alike."""
+    from oracle import block4_put_layer
+    T, flags = block4_put_layer(H.n_in, max_weights, H.tile_br, H.tile_bc, H.tiles[:16 * H.n_tiles])
+    H.b4res = T.M
+    H.b4_flags = flags.copy() if len(flags) else np.zeros(1, np.uint8)
+    check_b4_reservations(L, H, "load")
+
+
+def check_b4_reservations(L, H, what):
+    """The device's block4 reservations, tile_is_sparse and write-back
+    counters against the oracle's."""
+    d = L.export_block4_layout()
+    M = H.b4res
+    assert list(d["ia"]) == M.ia and list(d["ea"]) == M.ea and list(d["ta"]) == M.ta, what + ": reservations"
+    assert d["dropped_growth_events"] == M.dropped, what + ": dropped growth events"
+    assert (d["evicted"], d["row_merge_overflow_events"], d["row_merge_overflow_bytes_dropped"]) == \
+        tuple(H.b4_counters), what + ": write-back counters"
+    if H.n_tiles:
+        assert np.array_equal(L.export_block4_packed()["tile_is_sparse"], H.b4_flags[:H.n_tiles]), \
+            what + ": tile_is_sparse"
