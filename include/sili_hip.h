@@ -10,6 +10,9 @@
  * Memory: arguments documented "device" are device pointers; "host" are host
  * pointers.  Compute entry points are asynchronous on the given stream unless
  * documented otherwise; sili_synchronize() waits for the layer's stream.
+ * Calls on one layer share its workspaces (staged activations, split-row
+ * partial sums and arrival counters): calls on one layer that overlap on
+ * different streams race; order them on one stream or with events.
  *
  * Layout conventions (the reference's):
  *   - matrix rows are INPUT neurons: y[b,c] = sum_r x[b,r] * W(r,c)
@@ -373,6 +376,9 @@ typedef struct {
     int32_t has_nonfinite;     /* a weight code 8 (NaN) or non-finite scale */
     int32_t stream_canonical;  /* batch-1 stream copy of the canonical store is built */
     int32_t stream_shadow;     /* ... of the shadow (forward) store */
+    int32_t split_combined;    /* split rows summed in item order, not with float atomics
+                                  (SILI_SPLIT_COMBINE=1 when the store was built): bit 0 the
+                                  canonical store, bit 1 the shadow store */
 } sili_info;
 int sili_get_info(sili_layer *layer, sili_info *out);
 

@@ -405,6 +405,34 @@ static int bits_for(uint64_t max_value) {
     return b;
 }
 
+__global__ void k_clear_u32(uint32_t *__restrict__ p, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+// SILI_SPLIT_COMBINE=1 (read when a store is built; default 0): the float4
+// gathers combine a split row's work items in item order instead of with
+// float atomics, so the rows' sums do not depend on the order in which the
+// items finish (bitwise reproducible).  It costs time: on the config-2
+// grad-input gather (1594 split rows in 5445 items) 41.5 us against 36.5 us
+// with atomics, the combining waves waiting on their write-through stores.
+// Buffers: arrival counters (cleared here; each combining launch leaves them
+// zero) and one partial-sum slot per work item and batch column, for passes
+// of up to 128 columns and at most 16 Mi floats (a store past that, or a
+// wider pass, combines with atomics).
+void prepare_split_combine(Layer &L, DScatter &s) {
+    const int64_t cap = s.nseg * 128;
+    if (!s.has_split || s.nseg == 0 || cap > ((int64_t)16 << 20) || env_int("SILI_SPLIT_COMBINE", 0) == 0) {
+        s.part_cap = 0;
+        return;
+    }
+    s.part.ensure((size_t)cap, 0);
+    s.split_cnt.ensure((size_t)s.rows + 1);
+    launch(k_clear_u32, dim3(nblk(s.rows + 1)), dim3(TPB), 0, L.stream, s.split_cnt.p, s.rows + 1);
+    SILI_HIP(hipGetLastError());
+    s.part_cap = cap;
+}
+
 void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64_t N,
                      const uint32_t *d_ptrs, const uint32_t *d_cols, const uint8_t *d_bytes) {
     const Encoded e = encode_rows(L, rows, ncols, N, d_ptrs, d_cols, L.seg_len, true, dst.byte_start,
@@ -424,6 +452,7 @@ void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64
     dst.nseg = e.nseg;
     dst.has_split = e.has_split;
     dst.n_empty_rows = e.n_empty_rows;
+    prepare_split_combine(L, dst);
     dst.val.ensure((size_t)N + 64);
     if (N > 0)
         SILI_HIP(hipMemcpyAsync(dst.val.p, d_bytes, (size_t)N, hipMemcpyDeviceToDevice, L.stream));
@@ -475,6 +504,7 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
     dst.nseg = e.nseg;
     dst.has_split = e.has_split;
     dst.n_empty_rows = e.n_empty_rows;
+    prepare_split_combine(L, dst);
     dst.val.ensure((size_t)N + 64);
     if (N > 0)
         SILI_HIP(hipMemcpyAsync(dst.val.p, tbytes.p, (size_t)N, hipMemcpyDeviceToDevice, st));

@@ -1398,6 +1398,7 @@ int sili_get_info(sili_layer *layer, sili_info *out) {
         out->has_nonfinite = L.has_nonfinite ? 1 : 0;
         out->stream_canonical = (L.W.stream1.valid || L.W.streamK.valid) ? 1 : 0;
         out->stream_shadow = (L.Wt.stream1.valid || L.Wt.streamK.valid) ? 1 : 0;
+        out->split_combined = (L.W.part_cap > 0 ? 1 : 0) | (L.Wt.part_cap > 0 ? 2 : 0);
         if (L.B4.ntiles > 0) {
             std::vector<uint32_t> br, bc;
             export_block4_coords(L, br, bc);

@@ -176,6 +176,15 @@ struct GatherPlan {      // one orientation of the scattered store
     bool has_split;
     const uint32_t *split_rows;  // rows spanning several work items (n_split of them)
     int64_t n_split;
+    // split rows combined without float atomics (the float4 gather): each
+    // work item of a split row leaves its partial sums in part[si * nb ...],
+    // the last one of its row to finish (arrivals counted in split_cnt, by
+    // entries against elem_start) adds the row's items in order; part ==
+    // nullptr: combined by atomics.  part_cap: floats part holds.
+    const uint32_t *elem_start = nullptr;
+    uint32_t *split_cnt = nullptr;
+    float *part = nullptr;
+    int64_t part_cap = 0;
 };
 
 struct Block4Plan {

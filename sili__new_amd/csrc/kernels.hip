@@ -41,6 +41,10 @@ struct GArgs {
     uint32_t in_bytes;  // readable bytes from `in` (buffer range for the fast kernels)
     int accumulate;     // float4 kernels: add to out instead of storing (column-block passes)
     int xcd;            // float4 kernels: XCD-contiguous block order (xcd_block)
+    // k_gather_v4: split rows combined in order by their last item (GatherPlan)
+    const uint32_t *elem_start;
+    uint32_t *split_cnt;
+    float *part;
 };
 
 // Per-wave FP4 code -> value table (dequant by lookup).
@@ -529,39 +533,92 @@ constexpr uint32_t ENT_CAP = SEG_BYTES_MAX + 64u;
 // (`slice`, >= nb floats; lanes of group 0 hold float4 chunk q = bl + BL*k),
 // then the block writes them with consecutive lanes on consecutive rows, so
 // consecutive segments (rows) of one batch index leave as one run instead
-// of WAVES scattered 4-byte stores.  Split rows add atomically.  Every
-// thread of the block must call this (it holds a block barrier).
+// of WAVES scattered 4-byte stores.  Split rows add atomically, or are
+// combined in order (below).  Every thread of the block must call this (it
+// holds a block barrier).
+// Split rows, without float atomics (sc.part != nullptr): a wave holding one
+// work item of a split row leaves its partial sums in part[si * nb ...]; the
+// last item of the row to finish (its entries counted into cnt[row] against
+// the row's entries) adds the row's items in item order and writes the row,
+// then clears the counter.  The result does not depend on the finishing order.
+// The partials cross compute units and XCDs (whose L2s are not coherent with
+// each other), so they move as agent-scope atomic stores and loads (written
+// through to, and read from, the agent's coherence point); the wave waits for
+// its stores to complete before it counts its arrival.  A device-scope fence
+// would order them too, but it writes back and invalidates the whole L2 of
+// the XCD, which the gather's input reuse depends on.
+struct SplitCombine {
+    const SegDesc *seg;
+    int64_t nseg;
+    const uint32_t *elem_start;
+    uint32_t *cnt;
+    float *part;  // nullptr: split rows add with atomics
+};
+
+// s_waitcnt vmcnt(0) (gfx9 encoding: expcnt and lgkmcnt left at their maxima)
+constexpr int WAITCNT_VM0 = 0x0F70;
+
 template <int BL, int KB>
 __device__ __forceinline__ void store_rows_block(const float4 (&acc)[KB], bool active, uint32_t row,
                                                  bool split, uint32_t nq, float *slice_base,
                                                  uint32_t slice_stride, float *out, int64_t out_ld,
-                                                 bool accumulate = false) {
+                                                 bool accumulate = false,
+                                                 SplitCombine sc = SplitCombine{nullptr, 0, nullptr, nullptr, nullptr},
+                                                 int64_t si = 0, uint32_t n_items = 0) {
     __shared__ uint32_t s_row[WAVES];
-    __shared__ uint32_t s_flag[WAVES];  // bit 0: active, bit 1: split
+    __shared__ uint32_t s_flag[WAVES];  // bit 0: active, bit 1: split (atomics), bit 2: split (combined)
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const uint32_t g = lane / BL, bl = lane % BL;
     float *slice = slice_base + wave * slice_stride;
+    const bool combine = split && sc.part != nullptr;
     if (active && g == 0) {
 #pragma unroll
         for (int k = 0; k < KB; ++k) {
             const uint32_t q = bl + BL * (uint32_t)k;
-            if (q < nq) reinterpret_cast<float4 *>(slice)[q] = acc[k];
+            if (q < nq) *reinterpret_cast<float4 *>(slice + q * 4u) = acc[k];
         }
     }
     if (lane == 0) {
         s_row[wave] = row;
-        s_flag[wave] = (active ? 1u : 0u) | (split ? 2u : 0u);
+        s_flag[wave] = (active ? 1u : 0u) | (split && !combine ? 2u : 0u) | (combine ? 4u : 0u);
     }
     __syncthreads();
     const uint32_t nb = nq * 4u;
     for (uint32_t i = threadIdx.x; i < nb * WAVES; i += blockDim.x) {
         const uint32_t w = i % WAVES, b = i / WAVES;
         const uint32_t f = s_flag[w];
-        if (!(f & 1u)) continue;
+        if (!(f & 1u) || (f & 4u)) continue;
         const float v = slice_base[w * slice_stride + b];
         float *o = out + (int64_t)b * out_ld + s_row[w];
         if (f & 2u) atomicAdd(o, v);
         else *o = accumulate ? *o + v : v;  // (a row with one work item: this wave alone writes it)
+    }
+    if (active && combine) {
+        float *dst = sc.part + si * (int64_t)nb;
+        for (uint32_t b = lane; b < nb; b += 64u)
+            __hip_atomic_store(dst + b, slice[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");  // (keeps the stores above the wait)
+        __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);
+        uint32_t last = 0;
+        if (lane == 0) {
+            const uint32_t old = __hip_atomic_fetch_add(sc.cnt + row, n_items, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
+            last = (old + n_items == sc.elem_start[row + 1] - sc.elem_start[row]) ? 1u : 0u;
+        }
+        last = (uint32_t)__shfl((int)last, 0);
+        if (last) {
+            int64_t k0 = si, k1 = si + 1;
+            while (k0 > 0 && sc.seg[k0 - 1].row == row) --k0;
+            while (k1 < sc.nseg && sc.seg[k1].row == row) ++k1;
+            for (uint32_t b = lane; b < nb; b += 64u) {
+                float s = 0.0f;
+                for (int64_t k = k0; k < k1; ++k)
+                    s += __hip_atomic_load(sc.part + k * (int64_t)nb + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                float *o = out + (int64_t)b * out_ld + row;
+                *o = accumulate ? *o + s : s;
+            }
+            if (lane == 0) __hip_atomic_store(sc.cnt + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -640,7 +697,8 @@ __global__ __launch_bounds__(256) void k_gather_v4(GArgs a) {
     }
     store_rows_block<BL, KB>(acc, active, sd.row, (sd.split & SEG_SPLIT) != 0, nq,
                              reinterpret_cast<float *>(&s_ent[0][0]), ENT_CAP * 2u, a.out, a.out_ld,
-                             a.accumulate != 0);
+                             a.accumulate != 0, SplitCombine{a.seg, a.nseg, a.elem_start, a.split_cnt, a.part},
+                             si, sd.elem_end - sd.elem_begin);
 }
 
 struct BArgs {
@@ -941,6 +999,10 @@ struct FArgs {
     float *gw;          // one value per stored synapse, elem order
     float *acc_in;      // optional: acc_in[row] += sum_b |xT[row,b]|
     int xcd;            // XCD-contiguous block order (xcd_block)
+    // split rows of dx combined in order by their last item (GatherPlan)
+    const uint32_t *elem_start;
+    uint32_t *split_cnt;
+    float *part;
 };
 
 // Fused grad-input + nnz-sampled grad-W over the canonical store: one decode
@@ -1031,7 +1093,9 @@ __global__ __launch_bounds__(256) void k_bwd_v4(FArgs a) {
     wave_lds_sync();  // the entry table is reused as this wave's output slice
     }
     store_rows_block<BL, KB>(acc, active, sd.row, (sd.split & SEG_SPLIT) != 0, nq,
-                             reinterpret_cast<float *>(&s_ent[0][0]), ENT_CAP * 2u, a.dx, a.dx_ld);
+                             reinterpret_cast<float *>(&s_ent[0][0]), ENT_CAP * 2u, a.dx, a.dx_ld, false,
+                             SplitCombine{a.seg, a.nseg, a.elem_start, a.split_cnt, a.part}, si,
+                             sd.elem_end - sd.elem_begin);
 }
 
 // Block epilogue for block4 waves: out[b, 4*brow+li] for the block's (up to
@@ -2211,9 +2275,16 @@ void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, in
         const int64_t in_bytes = (p.cols * in_ld - b0) * 4;
         const bool small = in_bytes < (int64_t)OOB_OFFSET;
         GArgs a{p.seg, p.nseg, p.idx, p.val, sc, in + b0, in_ld, out + b0 * out_ld, out_ld, nb,
-                small ? (uint32_t)in_bytes : 0u, accumulate ? 1 : 0, xcd_order(0)};
+                small ? (uint32_t)in_bytes : 0u, accumulate ? 1 : 0, xcd_order(0), nullptr, nullptr, nullptr};
         if (accumulate && !(small && nb % 4 == 0 && in_ld % 4 == 0 && aligned16(a.in)))
             throw_error(3, "launch_gather: accumulating passes need the float4 kernels");
+        const bool v4 = small && nb % 4 == 0 && in_ld % 4 == 0 && aligned16(a.in);
+        if (v4 && p.has_split && p.part && p.nseg * nb <= p.part_cap) {
+            a.elem_start = p.elem_start;
+            a.split_cnt = p.split_cnt;
+            a.part = p.part;
+        }
+
         const dim3 grid(blocks_for(a.nseg)), block(256);
         if (nb == 1 && small) {
             static const int lane_decode = env_int("SILI_B1_LANE_DECODE", 2);
@@ -2263,7 +2334,7 @@ void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, in
                     default: launch(k_gather_b1<SKIP_NONE>, grid, block, 0, st, a); break;
                 }
             }
-        } else if (small && nb % 4 == 0 && in_ld % 4 == 0 && aligned16(a.in)) {
+        } else if (v4) {
             const int64_t nq = nb / 4;
             if (nq <= 1) gather_v4_skip<1, 1>(a, skip, st);
             else if (nq <= 2) gather_v4_skip<2, 1>(a, skip, st);
@@ -2416,7 +2487,12 @@ bool launch_bwd_fused(const GatherPlan &p, const ScaleView &sc, const float *gT,
     if (p.nseg == 0) return true;
     ProfScope ps("gather_gradw", st);
     FArgs a{p.seg, p.nseg, p.idx, p.val, sc, gT, (uint32_t)gT_bytes, xT, B, dx, dx_ld, gw, acc_in,
-            xcd_order(1)};
+            xcd_order(1), nullptr, nullptr, nullptr};
+    if (p.has_split && p.part && p.nseg * B <= p.part_cap) {
+        a.elem_start = p.elem_start;
+        a.split_cnt = p.split_cnt;
+        a.part = p.part;
+    }
     const dim3 grid(blocks_for(p.nseg)), block(256);
     const int64_t nq = B / 4;
     if (nq <= 1) launch((k_bwd_v4<1, 1, 4>), grid, block, 0, st, a);

@@ -122,8 +122,21 @@ struct DScatter {
     // columns relative to the block (built on first use)
     std::vector<DScatter> cblk;
     int64_t cblk_cb = 0;
+    // split rows combined in item order by the float4 gather: arrivals per
+    // row (rows+1, zero between launches) and per-item partial sums
+    // (part_cap floats; empty: combined by atomics)
+    DevBuf<uint32_t> split_cnt;
+    DevBuf<float> part;
+    int64_t part_cap = 0;
     GatherPlan plan() const {
-        return GatherPlan{seg.p, nseg, idx.p, val.p, rows, cols, has_split, split_rows.p, n_split};
+        GatherPlan p{seg.p, nseg, idx.p, val.p, rows, cols, has_split, split_rows.p, n_split};
+        if (has_split && part_cap > 0) {
+            p.elem_start = elem_start.p;
+            p.split_cnt = split_cnt.p;
+            p.part = part.p;
+            p.part_cap = part_cap;
+        }
+        return p;
     }
 };
 
@@ -458,6 +471,7 @@ struct TmpBuf {
 // Encode a store from row-sorted entries: ptrs[rows+1] (device), cols[N]
 // (device, strictly increasing within a row, < ncols), value bytes[N].
 // Throws SILI_ERR_INVALID on malformed input.
+void prepare_split_combine(Layer &L, DScatter &s);
 void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64_t N,
                      const uint32_t *d_ptrs, const uint32_t *d_cols, const uint8_t *d_bytes);
 // Build the shadow (transposed) store of `src` whose decoded entries are

@@ -700,6 +700,7 @@ void refresh_split(Layer &L, DScatter &s) {
     SILI_HIP(hipStreamSynchronize(st));
     s.n_split = ns;
     s.has_split = ns > 0;
+    prepare_split_combine(L, s);
     if (ns > 0) {
         s.split_rows.ensure((size_t)ns + 1);
         launch(k_list_rows, dim3(nblk(s.rows)), dim3(TPB), 0, st, (const uint32_t *)flag.p, (const uint32_t *)pos.p,

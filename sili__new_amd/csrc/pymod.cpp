@@ -147,6 +147,7 @@ class Layer {
         d["has_nonfinite"] = bool(i.has_nonfinite);
         d["stream_canonical"] = bool(i.stream_canonical);
         d["stream_shadow"] = bool(i.stream_shadow);
+        d["split_combined"] = (int)i.split_combined;
         return d;
     }
 
