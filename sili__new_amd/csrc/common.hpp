@@ -93,8 +93,10 @@ struct alignas(32) SegDesc {
     uint32_t elem_end;
     uint32_t pad1;
 };
-// Index bytes per segment are capped (the kernels stage a whole segment in LDS).
-constexpr uint32_t SEG_BYTES_MAX = 512;
+// Index bytes per segment are capped (the kernels stage a whole segment in
+// LDS).  448: a block of 4 float4-gather waves then needs 20,384 bytes of
+// LDS (staged bytes + the entry table), so 8 blocks share a CU's 160 KiB.
+constexpr uint32_t SEG_BYTES_MAX = 448;
 
 constexpr uint32_t SEG_SPLIT = 1u;  // the row has several segments (combine with atomics)
 constexpr uint32_t SEG_FIRST = 2u;  // first segment of its row

@@ -180,8 +180,17 @@ __global__ __launch_bounds__(256) void k_gather_b1(GArgs a) {
     }
 }
 
+// Staged bytes of one segment for the batch-1 kernels, whose lane L owns
+// the index bytes [8L, 8L+8): 64 lanes cover 512 bytes.
+constexpr uint32_t B1_SEG_BYTES = 512;  // one 8-byte slice per lane covers a segment
+static_assert(SEG_BYTES_MAX <= B1_SEG_BYTES, "one 8-byte slice per lane");
+struct B1Stage {
+    uint32_t idx[B1_SEG_BYTES / 4 + 8];  // idx[0] = 0, raw dwords from idx[1]
+    uint32_t val[B1_SEG_BYTES / 4 + 8];
+};
+
 // Batch 1 with lane-parallel decode: lane L owns the index bytes
-// [8L, 8L+8) of the segment (SEG_BYTES_MAX = 512 = 64 x 8) and decodes the
+// [8L, 8L+8) of the segment (64 x 8 bytes cover SEG_BYTES_MAX) and decodes the
 // varints whose last byte lies there (looking back over at most 4
 // continuation bytes for a varint that starts in the previous slice).  Two
 // wave scans give each lane its first entry index and the column before
@@ -192,16 +201,15 @@ __global__ __launch_bounds__(256) void k_gather_b1(GArgs a) {
 // aligned dwords.  RANK1: scale rank 1 (row factor uniform per segment).
 template <int SKIP, bool RANK1>
 __global__ __launch_bounds__(256) void k_gather_b1s(GArgs a, uint32_t ent_bytes) {
-    __shared__ SegStage s_stage[WAVES];
+    __shared__ B1Stage s_stage[WAVES];
     __shared__ float s_fp4[WAVES][16];
     __shared__ uint2 s_ent[WAVES][SEG_BYTES_MAX];
-    static_assert(SEG_BYTES_MAX == 512, "one 8-byte slice per lane");
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const int64_t si = (int64_t)blockIdx.x * WAVES + wave;
     if (si >= a.nseg) return;
     const SegDesc sd = a.seg[si];
     fp4_table_init(s_fp4[wave]);
-    SegStage &S = s_stage[wave];
+    B1Stage &S = s_stage[wave];
     const uint32_t end = sd.byte_end - sd.byte_begin < SEG_BYTES_MAX ? sd.byte_end - sd.byte_begin : SEG_BYTES_MAX;
     {
         // realigned copy: dst dword k (k >= 1) = segment bytes 4(k-1) .. 4(k-1)+3
@@ -321,10 +329,7 @@ __global__ __launch_bounds__(256) void k_gather_b1s(GArgs a, uint32_t ent_bytes)
 // staged bytes with the segment's byte alignment, a zero dword in front),
 // an LDS entry table in segment order, then the gather with 64 consecutive
 // entries per load instruction and one wave reduction.
-struct B1Stage {
-    uint32_t idx[SEG_BYTES_MAX / 4 + 8];  // idx[0] = 0, raw dwords from idx[1]
-    uint32_t val[SEG_BYTES_MAX / 4 + 8];
-};
+
 
 // XLDS (rank 1, no skip rules, in_ld == 1): the block first copies the
 // whole input, times the column scale, into LDS (dynamic shared memory,
@@ -336,7 +341,6 @@ __global__ __launch_bounds__(256) void k_gather_b1p(GArgs a, uint32_t ent_bytes)
     __shared__ float s_fp4[WAVES][16];
     __shared__ uint32_t s_ent[WAVES][SEG_BYTES_MAX];  // col | code << 28
     extern __shared__ float s_x[];
-    static_assert(SEG_BYTES_MAX == 512, "one 8-byte slice per lane");
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const int64_t W = (int64_t)gridDim.x * WAVES;
     if constexpr (XLDS) {
@@ -625,7 +629,8 @@ __device__ __forceinline__ void store_rows_block(const float4 (&acc)[KB], bool a
 
 
 template <int BL, int KB, int U, int SKIP>
-__global__ __launch_bounds__(256) void k_gather_v4(GArgs a) {
+__global__ __attribute__((amdgpu_flat_work_group_size(1, 256), amdgpu_waves_per_eu(KB <= 2 && U <= 4 ? 8 : 1)))
+void k_gather_v4(GArgs a) {
     __shared__ SegStage s_stage[WAVES];
     __shared__ uint2 s_ent[WAVES][ENT_CAP];
     __shared__ float s_fp4[WAVES][16];
@@ -1013,7 +1018,8 @@ struct FArgs {
 // batch), xT[row] in registers as k_sddmm_v4.  Needs B % 4 == 0, 16-byte
 // aligned xT / gT and B <= 64*KB*4/ (64/BL) -- the launcher checks.
 template <int BL, int KB, int U>
-__global__ __launch_bounds__(256) void k_bwd_v4(FArgs a) {
+__global__ __attribute__((amdgpu_flat_work_group_size(1, 256), amdgpu_waves_per_eu(KB <= 2 && KB * U <= 4 ? 8 : 1)))
+void k_bwd_v4(FArgs a) {
     __shared__ SegStage s_stage[WAVES];
     __shared__ uint2 s_ent[WAVES][ENT_CAP];
     __shared__ float s_fp4[WAVES][16];
@@ -2222,14 +2228,14 @@ void gather_v4_skip_u(const GArgs &a, int skip, hipStream_t st) {
     }
 }
 
-// entries in flight per lane: SILI_GATHER_U in {4, 8, 16} (tuning knob)
 // Launch-shape knobs of the float4 kernels (environment, read once):
 //   SILI_GATHER_BL  lanes per entry at batch 64 / 128 (4, 8 or 16)
 //   SILI_GATHER_U   entries per lane group in flight
 // Defaults: 8 lanes per entry (G = 8 entries per load instruction, two
-// float4 chunks per lane at batch 64) and 4 entries per group in flight --
-// the fastest measured shape for the fused backward at batch 64; the
-// forward gather is within 2% at every shape.
+// float4 chunks per lane at batch 64); 4 entries per group in flight in the
+// gathers and 2 in the fused backward, the shapes that keep 8 waves per
+// SIMD (64 VGPRs, 20 KiB of LDS per block of 4 waves): config 1's 8192
+// work items then run in one round of resident waves.
 inline int gather_bl() {
     static const int v = [] {
         const int b = env_int("SILI_GATHER_BL", 8);
@@ -2505,7 +2511,10 @@ bool launch_bwd_fused(const GatherPlan &p, const ScaleView &sc, const float *gT,
             if (u >= 2) launch((k_bwd_v4<4, 4, 2>), grid, block, 0, st, a);
             else launch((k_bwd_v4<4, 4, 1>), grid, block, 0, st, a);
         } else if (nq > 8 && bl == 8) {
-            if (u == 0 || u >= 4) launch((k_bwd_v4<8, 2, 4>), grid, block, 0, st, a);
+            // 2 entries per group in flight: 60 VGPRs, so 8 waves per SIMD
+            // (4 in flight: 80 VGPRs, 6 waves; 22.6 against 26.1 us on the
+            // config-1 grad-input + grad-W)
+            if (u >= 4) launch((k_bwd_v4<8, 2, 4>), grid, block, 0, st, a);
             else launch((k_bwd_v4<8, 2, 2>), grid, block, 0, st, a);
         } else launch((k_bwd_v4<16, 1, 4>), grid, block, 0, st, a);
     } else if (nq <= 32) {

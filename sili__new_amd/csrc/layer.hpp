@@ -412,7 +412,7 @@ struct Layer {
     DevBuf<uint32_t> b4_ta_dev;
     DevBuf<unsigned long long> b4_ctr;
     PinBuf pin_b4ta;
-    uint32_t seg_len = 512;     // max index bytes per decode work item (scattered)
+    uint32_t seg_len = SEG_BYTES_MAX;  // max index bytes per decode work item (scattered)
     uint32_t seg_len_b4 = 128;  // max block-index bytes per decode work item (block4)
     // the policy's row patches: pinned staging (reads in, patch content out),
     // the device copy of the patch content, and the arrays' second buffers
