@@ -379,6 +379,12 @@ typedef struct {
     int32_t split_combined;    /* split rows summed in item order, not with float atomics
                                   (SILI_SPLIT_COMBINE=1 when the store was built): bit 0 the
                                   canonical store, bit 1 the shadow store */
+    int32_t pad0;
+    int64_t short_rows_canonical; /* short rows (whole rows of <= 28 index bytes) the float4
+                                     gather packs up to 16 to a wave, canonical store (0 until
+                                     a gather at batch 4..64 has used them, or when fewer than a
+                                     quarter of the work items are such rows) */
+    int64_t short_rows_shadow;    /* ... of the shadow store */
 } sili_info;
 int sili_get_info(sili_layer *layer, sili_info *out);
 

@@ -41,9 +41,10 @@ __global__ void k_entry_len(const uint32_t *__restrict__ ptrs, int64_t rows, int
                             int *__restrict__ bad, uint32_t *__restrict__ n_empty) {
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (i >= N) {
-        if (i == N) {  // the scan's last term and the empty-row counter start at zero
+        if (i == N) {  // the scan's last term and the row counters start at zero
             len[N] = 0;
-            *n_empty = 0u;
+            n_empty[0] = 0u;
+            n_empty[1] = 0u;
         }
         return;
     }
@@ -88,16 +89,26 @@ __global__ void k_row_starts(const uint32_t *__restrict__ ptrs, int64_t rows, in
     const int64_t r = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (r > rows) return;
     const uint32_t e = ptrs[r];
-    byte_start[r] = (uint32_t)(((int64_t)e < N) ? pos[e] : total);
+    const uint64_t b0 = ((int64_t)e < N) ? pos[e] : total;
+    byte_start[r] = (uint32_t)b0;
     elem_start[r] = e;
+    // n_empty[1]: rows that are one work item of at most SHORT_ROW_BYTES
+    // index bytes (the short rows the float4 gather packs several to a wave),
+    // counted per wave
+    bool short_row = false;
     if (r < rows) {
         const uint32_t e1 = ptrs[r + 1], n = e1 - e;
-        segcnt[r] = seg_count(n, n ? pos[e1 - 1] - pos[e] : 0u, seg_bytes - 4u, emit_empty);
+        const uint32_t cnt = seg_count(n, n ? pos[e1 - 1] - pos[e] : 0u, seg_bytes - 4u, emit_empty);
+        segcnt[r] = cnt;
         if (n == 0u) atomicAdd(n_empty, 1u);
+        const uint64_t b1 = (int64_t)e1 < N ? pos[e1] : total;
+        short_row = cnt == 1u && b1 - b0 <= SHORT_ROW_BYTES;
     } else {
         segcnt[rows] = 0u;  // the scan's last term
         *flag = 0;          // the work-item writer's split flag
     }
+    const uint64_t sb = __ballot(short_row);
+    if (sb != 0ull && (threadIdx.x & 63u) == (uint32_t)__builtin_ctzll(sb)) atomicAdd(n_empty + 1, (uint32_t)__popcll(sb));
 }
 
 // first entry in [lo, hi) whose varint starts at or after row offset `off`
@@ -250,6 +261,7 @@ struct Encoded {
     bool has_split = false;
     int64_t n_split = 0;
     int64_t n_empty_rows = 0;
+    int64_t n_short = 0;  // rows that are one work item of <= SHORT_ROW_BYTES index bytes
 };
 
 __global__ void k_split_flags(const uint32_t *__restrict__ segcnt, int64_t rows, uint32_t *__restrict__ flag) {
@@ -279,7 +291,7 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
     rowid.ensure((size_t)N + 1);
     zero_flag(L);
     TmpBuf<uint32_t> n_empty(L, SILI_TMPKEY(n_empty));
-    n_empty.ensure(1);
+    n_empty.ensure(2);
     // len[N] and n_empty are zeroed by the length kernel's thread N
     launch(k_entry_len, dim3(nblk(N + 1)), dim3(TPB), 0, st, d_ptrs, rows, ncols, d_cols, N, len.p, rowid.p,
            L.scratch.flag.p, n_empty.p);
@@ -334,16 +346,18 @@ Encoded encode_rows(Layer &L, int64_t rows, int64_t ncols, int64_t N, const uint
                rows, split_rows->p);
         SILI_HIP(hipGetLastError());
     }
-    uint32_t nseg = 0, empty = 0, ns = 0;
+    uint32_t nseg = 0, empty = 0, ns = 0, nshort = 0;
     int split = 0;
     rb.add(&nseg, segoff.p + rows, sizeof(uint32_t));
     rb.add(&empty, n_empty.p, sizeof(uint32_t));
+    rb.add(&nshort, n_empty.p + 1, sizeof(uint32_t));
     rb.add(&split, L.scratch.flag.p, sizeof(int));
     if (split_rows) rb.add(&ns, fpos.p + rows, sizeof(uint32_t));
     rb.wait();
     if ((int64_t)nseg > seg_max) throw_error(3, std::string(what) + ": work items exceed their bound (internal error)");
     out.nseg = nseg;
     out.n_empty_rows = empty;
+    out.n_short = nshort;
     out.has_split = split != 0;
     if (out.has_split && split_rows) out.n_split = ns;
     return out;
@@ -433,6 +447,72 @@ void prepare_split_combine(Layer &L, DScatter &s) {
     s.part_cap = cap;
 }
 
+namespace {
+// flag[i]: work item i is a whole row of <= SHORT_ROW_BYTES index bytes
+// (flag[n] = 0, the scan's last term)
+__global__ void k_short_flags(const SegDesc *__restrict__ seg, int64_t n, uint32_t *__restrict__ flag) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n) {
+        const SegDesc d = seg[i];
+        flag[i] = (!(d.split & SEG_SPLIT) && d.byte_end - d.byte_begin <= SHORT_ROW_BYTES) ? 1u : 0u;
+    } else if (i == n) {
+        flag[n] = 0u;
+    }
+}
+__global__ void k_short_split(const SegDesc *__restrict__ seg, int64_t n, const uint32_t *__restrict__ flag,
+                              const uint32_t *__restrict__ pos, SegDesc *__restrict__ sh, SegDesc *__restrict__ lg) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= n) return;
+    if (flag[i]) sh[pos[i]] = seg[i];
+    else lg[i - (int64_t)pos[i]] = seg[i];
+}
+
+// Split s's work items into short rows and the others (DScatter::sh_seg),
+// once per structure, where a quarter of the items or more are short rows
+// (SILI_SHORT_ROWS=0: never).
+void ensure_short_rows(Layer &L, DScatter &s) {
+    if (s.sh_valid) return;
+    s.sh_valid = true;
+    s.n_sh = 0;
+    s.n_lg = s.nseg;
+    if (env_int("SILI_SHORT_ROWS", 1) == 0) return;
+    if (s.nseg == 0 || s.n_short_hint < 1024 || s.n_short_hint * 4 < s.nseg) return;
+    hipStream_t st = L.stream;
+    TmpBuf<uint32_t> flag(L, SILI_TMPKEY(flag)), pos(L, SILI_TMPKEY(pos));
+    flag.ensure((size_t)s.nseg + 1);
+    pos.ensure((size_t)s.nseg + 1);
+    launch(k_short_flags, dim3(nblk(s.nseg + 1)), dim3(TPB), 0, st, (const SegDesc *)s.seg.p, s.nseg, flag.p);
+    SILI_HIP(hipGetLastError());
+    device_exclusive_scan_u32(L, flag.p, pos.p, s.nseg + 1);
+    uint32_t nsh = 0;
+    ReadBack rb(L);
+    rb.add(&nsh, pos.p + s.nseg, sizeof(uint32_t));
+    rb.wait();
+    if (nsh < 1024 || (int64_t)nsh * 4 < s.nseg) return;
+    s.sh_seg.ensure((size_t)nsh);
+    s.lg_seg.ensure((size_t)(s.nseg - nsh) + 1);
+    launch(k_short_split, dim3(nblk(s.nseg)), dim3(TPB), 0, st, (const SegDesc *)s.seg.p, s.nseg,
+           (const uint32_t *)flag.p, (const uint32_t *)pos.p, s.sh_seg.p, s.lg_seg.p);
+    SILI_HIP(hipGetLastError());
+    s.n_sh = nsh;
+    s.n_lg = s.nseg - nsh;
+}
+}  // namespace
+
+GatherPlan gather_plan(Layer &L, DScatter &s, int64_t nb) {
+    GatherPlan p = s.plan();
+    if (nb > 1 && nb <= SHORT_MAX_BATCH && nb % 4 == 0) {
+        ensure_short_rows(L, s);
+        if (s.n_sh > 0) {
+            p.sh_seg = s.sh_seg.p;
+            p.n_sh = s.n_sh;
+            p.lg_seg = s.lg_seg.p;
+            p.n_lg = s.n_lg;
+        }
+    }
+    return p;
+}
+
 void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64_t N,
                      const uint32_t *d_ptrs, const uint32_t *d_cols, const uint8_t *d_bytes) {
     const Encoded e = encode_rows(L, rows, ncols, N, d_ptrs, d_cols, L.seg_len, true, dst.byte_start,
@@ -441,6 +521,8 @@ void build_scattered(Layer &L, DScatter &dst, int64_t rows, int64_t ncols, int64
     dst.stream1.valid = dst.streamK.valid = false;
     dst.fidx.valid = false;
     dst.dcol_valid = false;
+    dst.sh_valid = false;
+    dst.n_short_hint = e.n_short;
     dst.slc_w = 0;
     dst.stream1.failed = dst.streamK.failed = false;
     dst.cblk.clear();
@@ -494,6 +576,8 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
     dst.stream1.failed = dst.streamK.failed = false;
     dst.fidx.valid = false;
     dst.dcol_valid = false;
+    dst.sh_valid = false;
+    dst.n_short_hint = e.n_short;
     dst.slc_w = 0;
     dst.cblk.clear();
     dst.cblk_cb = 0;

@@ -449,7 +449,7 @@ void forward_dense(Layer &L, const float *x, int64_t B, float *y, hipStream_t st
     prep.run();
     if (str) stream_gather(L, L.Wt, ssc, xT, B, y, L.n_out, st);
     else if (staged) launch_gather_staged(L, L.Wt, ssc, xT, B, y, L.n_out, st);
-    else if (plain) launch_gather(L.Wt.plan(), ssc, xT, B, y, L.n_out, B, skip, st);
+    else if (plain) launch_gather(gather_plan(L, L.Wt, B), ssc, xT, B, y, L.n_out, B, skip, st);
     else if (L.Wt.nnz > 0 && !gather_colblocked(L, L.Wt, ssc, xT, B, y, L.n_out, skip, st))
         throw_error(SILI_ERR_RUNTIME, "forward_dense: column-block passes did not apply (internal error)");
     if (L.B4t.ntiles > 0 && !gather_b4_colblocked(L, L.B4t, shadow_scales(L), xT, B, y, L.n_out, SKIP_NONE, st))
@@ -542,7 +542,7 @@ void backward_dense(Layer &L, const float *x, const float *dy, int64_t B, float 
                        launch_bwd_fused(L.W.plan(), canon_scales(L), gT, xT, B, dx, L.n_in, gw_s, L.acc_in.p, st);
     if (str) stream_gather(L, L.W, canon_scales(L), gT, B, dx, L.n_in, st);
     else if (scat && !fused && !gather_colblocked(L, L.W, canon_scales(L), gT, B, dx, L.n_in, SKIP_NONE, st))
-        launch_gather(L.W.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
+        launch_gather(gather_plan(L, L.W, B), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
     if (L.B4.ntiles > 0 && !gather_b4_colblocked(L, L.B4, canon_scales(L), gT, B, dx, L.n_in, SKIP_NONE, st))
         launch_gather_b4(L.B4.plan(), canon_scales(L), gT, B, dx, L.n_in, B, SKIP_NONE, st);
     if (scat && gw_s && !fused) launch_sddmm(L.W.plan(), xT, gT, B, gw_s, L.acc_in.p, st);
@@ -680,7 +680,7 @@ void forward_sparse(Layer &L, const int32_t *ptrs, const int32_t *idx, const flo
     const ScaleView ssc = comp0_scales(L, true, st);
     if (!push) {
         launch_zero_split_rows(L.Wt.plan(), y, L.n_out, B, st);
-        launch_gather(L.Wt.plan(), ssc, L.ws_xT.p, B, y, L.n_out, B, SKIP_POSZERO, st);
+        launch_gather(gather_plan(L, L.Wt, B), ssc, L.ws_xT.p, B, y, L.n_out, B, SKIP_POSZERO, st);
     }
     if (L.B4t.ntiles > 0) launch_gather_b4(L.B4t.plan(), ssc, L.ws_xT.p, B, y, L.n_out, B, SKIP_POSZERO, st);
 }
@@ -697,7 +697,7 @@ void backward_sparse(Layer &L, const float *x, const int32_t *dptrs, const int32
     // scattered: merge-join visits only present dy entries (sisldo_ops.hpp:705-713);
     // block4: skips dy == 0 per slot (sisldo_ops.hpp:886-897)
     const ScaleView csc = comp0_scales(L, false, st);
-    launch_gather(L.W.plan(), csc, L.ws_gT.p, B, dx, L.n_in, B, SKIP_POSZERO, st);
+    launch_gather(gather_plan(L, L.W, B), csc, L.ws_gT.p, B, dx, L.n_in, B, SKIP_POSZERO, st);
     if (L.B4.ntiles > 0) launch_gather_b4(L.B4.plan(), csc, L.ws_gT.p, B, dx, L.n_in, B, SKIP_ZERO, st);
 }
 
@@ -1399,6 +1399,8 @@ int sili_get_info(sili_layer *layer, sili_info *out) {
         out->stream_canonical = (L.W.stream1.valid || L.W.streamK.valid) ? 1 : 0;
         out->stream_shadow = (L.Wt.stream1.valid || L.Wt.streamK.valid) ? 1 : 0;
         out->split_combined = (L.W.part_cap > 0 ? 1 : 0) | (L.Wt.part_cap > 0 ? 2 : 0);
+        out->short_rows_canonical = L.W.sh_valid ? L.W.n_sh : 0;
+        out->short_rows_shadow = L.Wt.sh_valid ? L.Wt.n_sh : 0;
         if (L.B4.ntiles > 0) {
             std::vector<uint32_t> br, bc;
             export_block4_coords(L, br, bc);

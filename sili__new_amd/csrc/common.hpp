@@ -187,7 +187,23 @@ struct GatherPlan {      // one orientation of the scattered store
     uint32_t *split_cnt = nullptr;
     float *part = nullptr;
     int64_t part_cap = 0;
+    // short rows packed several to a wave by the float4 gather (set only by
+    // gather_plan; nullptr: every work item takes a wave): sh_seg lists the
+    // work items that are whole rows of at most SHORT_ROW_BYTES index bytes,
+    // lg_seg the others, both in store order
+    const SegDesc *sh_seg = nullptr;
+    int64_t n_sh = 0;
+    const SegDesc *lg_seg = nullptr;
+    int64_t n_lg = 0;
 };
+
+// Short rows: a wave of the float4 gather takes up to SHORT_R_MAX of them,
+// their index bytes staged back to back (SHORT_R_MAX * SHORT_ROW_BYTES <=
+// SEG_BYTES_MAX) and their results held in the wave's entry table
+// (SHORT_R_MAX * batch floats, batch <= SHORT_MAX_BATCH).
+constexpr uint32_t SHORT_R_MAX = 16;
+constexpr uint32_t SHORT_ROW_BYTES = 28;
+constexpr int64_t SHORT_MAX_BATCH = 64;
 
 struct Block4Plan {
     const SegDesc *seg;

@@ -45,6 +45,12 @@ struct GArgs {
     const uint32_t *elem_start;
     uint32_t *split_cnt;
     float *part;
+    // k_gather_v4 with short rows (sh_seg != nullptr): blocks [0, n_lgblk)
+    // take the work items seg[0, nseg) a wave each, the blocks after them the
+    // short rows sh_seg[0, n_sh), up to SHORT_R_MAX to a wave
+    const SegDesc *sh_seg;
+    int64_t n_sh;
+    uint32_t n_lgblk;
 };
 
 // Per-wave FP4 code -> value table (dequant by lookup).
@@ -628,6 +634,198 @@ __device__ __forceinline__ void store_rows_block(const float4 (&acc)[KB], bool a
 
 
 
+// Short rows, up to SHORT_R_MAX to a wave (the blocks of k_gather_v4 past
+// a.n_lgblk): every item of a.sh_seg is a whole row of at most
+// SHORT_ROW_BYTES index bytes, and wave gi of these blocks takes items
+// [gi*R, gi*R + R), R = SHORT_R_MAX.  A wave per such row would spend its
+// staging, decode and epilogue latency on a handful of entries; here
+//   - the rows' index and value bytes are staged back to back (32 lanes per
+//     row, byte loads, all issued before the first wait);
+//   - 64-byte windows are decoded as in decode_chunk, the column scan
+//     restarting at each row's first byte (a segmented scan over the head
+//     flags); each entry's row is the last head at or before it (a running
+//     maximum of the row ids), so the scales see the right row;
+//   - lane group g (BL lanes, float4 batch chunks as in the segment path)
+//     accumulates rows g, g + G, ... of the wave in registers;
+//   - the results go through the wave's entry table to a block epilogue that
+//     writes the block's rows per batch index (stores, or adds with
+//     a.accumulate).
+// The entry table holds at most SEG_BYTES_MAX entries while decoding; its
+// tail (entries SEG_BYTES_MAX ..) holds the head flags.  Needs a.nb <=
+// SHORT_MAX_BATCH (R * nb floats fit the table).
+// The float4 gather shapes that hold the short-row path: batch chunks of at
+// most SHORT_MAX_BATCH columns (larger shapes would carry its registers).
+constexpr bool short_rows_shape(int BL, int KB) { return 4 * BL * KB <= (int)SHORT_MAX_BATCH; }
+
+template <int BL, int KB, int SKIP>
+__device__ __forceinline__ void gather_short_body(const GArgs &a, uint32_t sblk, SegStage *stage,
+                                                  uint2 (*ents)[ENT_CAP], float (*fp4s)[16]) {
+    constexpr uint32_t G = 64u / BL;
+    constexpr uint32_t RPG = (SHORT_R_MAX + G - 1u) / G;  // rows per lane group
+    constexpr uint32_t US = KB * RPG >= 4u ? 1u : 2u;     // entries per row in flight
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t g = lane / BL, bl = lane % BL;
+    const uint32_t nq = (uint32_t)(a.nb >> 2), nbv = nq * 4u;
+    const int64_t i0 = ((int64_t)sblk * WAVES + wave) * SHORT_R_MAX;
+    const uint32_t nrows = i0 < a.n_sh ? (uint32_t)min<int64_t>((int64_t)SHORT_R_MAX, a.n_sh - i0) : 0u;
+    SegStage &S = stage[wave];
+    uint2 *ent = ents[wave];
+    uint32_t *rowid = S.idx;  // after the decode: the wave's rows, then their count
+    if (nrows > 0) {
+        fp4_table_init(fp4s[wave]);
+        uint32_t nby = 0, nen = 0, row = 0, bb = 0, eb = 0;
+        if (lane < nrows) {
+            const SegDesc d = a.sh_seg[i0 + lane];
+            nby = d.byte_end - d.byte_begin;
+            nen = d.elem_end - d.elem_begin;
+            row = d.row;
+            bb = d.byte_begin;
+            eb = d.elem_begin;
+        }
+        const uint32_t binc = wave_incl_scan(nby), einc = wave_incl_scan(nen);
+        const uint32_t boff = binc - nby, eoff = einc - nen;
+        const uint32_t tot_b = (uint32_t)__builtin_amdgcn_readlane((int)binc, 63);
+        uint8_t *sidx = reinterpret_cast<uint8_t *>(S.idx);
+        uint8_t *sval = reinterpret_cast<uint8_t *>(S.val);
+        uint8_t *hd = reinterpret_cast<uint8_t *>(ent + SEG_BYTES_MAX);
+        for (uint32_t i = lane; i < SEG_BYTES_MAX / 4u; i += 64u) reinterpret_cast<uint32_t *>(hd)[i] = 0u;
+        // the rows' bytes, two rows per pass (32 lanes each)
+        uint32_t bv[SHORT_R_MAX / 2], vv[SHORT_R_MAX / 2];
+        const uint32_t npass = (nrows + 1u) >> 1;
+#pragma unroll
+        for (uint32_t p = 0; p < SHORT_R_MAX / 2; ++p) {
+            const uint32_t ri = 2u * p + (lane >> 5), off = lane & 31u;
+            const uint32_t rb = (uint32_t)__shfl((int)bb, (int)ri), rn = (uint32_t)__shfl((int)nby, (int)ri);
+            const uint32_t re = (uint32_t)__shfl((int)eb, (int)ri), rm = (uint32_t)__shfl((int)nen, (int)ri);
+            bv[p] = (p < npass && off < rn) ? (uint32_t)a.idx[rb + off] : 0u;
+            vv[p] = (p < npass && off < rm) ? (uint32_t)a.val[re + off] : 0u;
+        }
+#pragma unroll
+        for (uint32_t p = 0; p < SHORT_R_MAX / 2; ++p) {
+            const uint32_t ri = 2u * p + (lane >> 5), off = lane & 31u;
+            const uint32_t rn = (uint32_t)__shfl((int)nby, (int)ri), rm = (uint32_t)__shfl((int)nen, (int)ri);
+            const uint32_t ro = (uint32_t)__shfl((int)boff, (int)ri), rv = (uint32_t)__shfl((int)eoff, (int)ri);
+            if (p < npass && off < rn) sidx[ro + off] = (uint8_t)bv[p];
+            if (p < npass && off < rm) sval[rv + off] = (uint8_t)vv[p];
+        }
+        if (lane < nrows && nby > 0u) hd[boff] = (uint8_t)(lane + 1u);  // row id + 1 at its first byte
+        wave_lds_sync();
+        // decode, the scans restarting at row starts
+        const float *tab = fp4s[wave];
+        const uint32_t ld_bytes = (uint32_t)a.in_ld * 4u;
+        uint32_t pos = 0, carry = 0, crow = 0, ebase = 0;
+        while (pos < tot_b) {
+            const Chunk ch = decode_chunk(sidx, pos, tot_b, 0u);
+            if (ch.T == 0ull) break;
+            const uint32_t p = pos + lane;
+            const uint32_t rid = p < tot_b ? (uint32_t)hd[p] : 0u;
+            const uint64_t H = __ballot(rid != 0u);
+            const uint64_t le = lane == 63u ? ~0ull : ((2ull << lane) - 1ull);
+            const bool headed = (H & le) != 0ull;
+            const uint32_t col = wave_seg_scan(ch.v, rid != 0u ? 1u : 0u) + (headed ? 0u : carry);
+            const uint32_t mr = wave_max_scan(rid);
+            const uint32_t rl = headed ? mr - 1u : crow;
+            const uint32_t grow = (uint32_t)__shfl((int)row, (int)rl);
+            if (ch.term) {
+                const uint32_t e = ebase + ch.rank;
+                const float w = tab[(uint32_t)sval[e] >> 4] * scale_at(a.sc, grow, col);
+                ent[e] = make_uint2(col * ld_bytes, __builtin_bit_cast(uint32_t, w));
+            }
+            const uint32_t hi = 63u - (uint32_t)__clzll(ch.T);
+            carry = uniform((uint32_t)__shfl((int)col, (int)hi));
+            crow = uniform((uint32_t)__shfl((int)rl, (int)hi));
+            pos += hi + 1u;
+            ebase += (uint32_t)__popcll(ch.T);
+        }
+        wave_lds_sync();
+        // each lane group's rows
+        const __amdgpu_buffer_rsrc_t rin = buffer_rsrc(a.in, a.in_bytes);
+        uint32_t lane_off[KB];
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            const uint32_t q = bl + BL * (uint32_t)k;
+            lane_off[k] = q < nq ? q * 16u : OOB_OFFSET;
+        }
+        uint32_t eo[RPG], ne[RPG], nmax = 0;
+#pragma unroll
+        for (uint32_t t = 0; t < RPG; ++t) {
+            const uint32_t i = g + G * t;
+            const uint32_t src = i < 64u ? i : 0u;
+            eo[t] = (uint32_t)__shfl((int)eoff, (int)src);
+            const uint32_t n = (uint32_t)__shfl((int)nen, (int)src);
+            ne[t] = i < nrows ? n : 0u;
+            nmax = max(nmax, ne[t]);
+        }
+        float4 acc[RPG][KB];
+#pragma unroll
+        for (uint32_t t = 0; t < RPG; ++t)
+#pragma unroll
+            for (int k = 0; k < KB; ++k) acc[t][k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (uint32_t j = 0; j < nmax; j += US) {
+            uint2 e[RPG][US];
+            float4 x[RPG][US][KB];
+#pragma unroll
+            for (uint32_t t = 0; t < RPG; ++t)
+#pragma unroll
+                for (uint32_t u = 0; u < US; ++u)
+                    e[t][u] = j + u < ne[t] ? ent[eo[t] + j + u] : make_uint2(OOB_OFFSET, 0u);
+#pragma unroll
+            for (uint32_t t = 0; t < RPG; ++t)
+#pragma unroll
+                for (uint32_t u = 0; u < US; ++u)
+#pragma unroll
+                    for (int k = 0; k < KB; ++k) x[t][u][k] = buffer_load_f4(rin, e[t][u].x + lane_off[k]);
+#pragma unroll
+            for (uint32_t t = 0; t < RPG; ++t)
+#pragma unroll
+                for (uint32_t u = 0; u < US; ++u) {
+                    const float w = __builtin_bit_cast(float, e[t][u].y);
+#pragma unroll
+                    for (int k = 0; k < KB; ++k) {
+                        const float4 xv = x[t][u][k];
+                        float4 &A = acc[t][k];
+                        if constexpr (SKIP == SKIP_NONE) {
+                            A.x = __builtin_fmaf(w, xv.x, A.x);
+                            A.y = __builtin_fmaf(w, xv.y, A.y);
+                            A.z = __builtin_fmaf(w, xv.z, A.z);
+                            A.w = __builtin_fmaf(w, xv.w, A.w);
+                        } else {
+                            if (!skip_x<SKIP>(xv.x)) A.x = __builtin_fmaf(w, xv.x, A.x);
+                            if (!skip_x<SKIP>(xv.y)) A.y = __builtin_fmaf(w, xv.y, A.y);
+                            if (!skip_x<SKIP>(xv.z)) A.z = __builtin_fmaf(w, xv.z, A.z);
+                            if (!skip_x<SKIP>(xv.w)) A.w = __builtin_fmaf(w, xv.w, A.w);
+                        }
+                    }
+                }
+        }
+        wave_lds_sync();  // every group is done with the entry table: it becomes the result slice
+        float *slice = reinterpret_cast<float *>(ent);
+#pragma unroll
+        for (uint32_t t = 0; t < RPG; ++t) {
+            const uint32_t i = g + G * t;
+            if (i < nrows) {
+#pragma unroll
+                for (int k = 0; k < KB; ++k) {
+                    const uint32_t q = bl + BL * (uint32_t)k;
+                    if (q < nq) *reinterpret_cast<float4 *>(slice + i * nbv + q * 4u) = acc[t][k];
+                }
+            }
+        }
+        if (lane < nrows) rowid[lane] = row;
+    }
+    if (lane == 0) rowid[SHORT_R_MAX] = nrows;
+    __syncthreads();
+    // the block's rows per batch index: consecutive threads on consecutive rows
+    constexpr uint32_t PER_B = WAVES * SHORT_R_MAX;
+    for (uint32_t i = threadIdx.x; i < nbv * PER_B; i += blockDim.x) {
+        const uint32_t r = i % SHORT_R_MAX, w = (i / SHORT_R_MAX) % WAVES, b = i / PER_B;
+        if (r >= stage[w].idx[SHORT_R_MAX]) continue;
+        const float v = reinterpret_cast<const float *>(ents[w])[r * nbv + b];
+        float *o = a.out + (int64_t)b * a.out_ld + stage[w].idx[r];
+        *o = a.accumulate ? *o + v : v;
+    }
+}
+
 template <int BL, int KB, int U, int SKIP>
 __global__ __attribute__((amdgpu_flat_work_group_size(1, 256), amdgpu_waves_per_eu(KB <= 2 && U <= 4 ? 8 : 1)))
 void k_gather_v4(GArgs a) {
@@ -636,8 +834,15 @@ void k_gather_v4(GArgs a) {
     __shared__ float s_fp4[WAVES][16];
     constexpr uint32_t G = 64u / BL;
     constexpr uint32_t STEP = G * U;
+    if constexpr (short_rows_shape(BL, KB)) {
+        if (a.sh_seg != nullptr && blockIdx.x >= a.n_lgblk) {
+            gather_short_body<BL, KB, SKIP>(a, blockIdx.x - a.n_lgblk, s_stage, s_ent, s_fp4);
+            return;
+        }
+    }
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const uint32_t bid = a.xcd ? xcd_block(blockIdx.x, gridDim.x) : blockIdx.x;
+    const uint32_t nlb = a.sh_seg != nullptr ? a.n_lgblk : gridDim.x;
+    const uint32_t bid = a.xcd ? xcd_block(blockIdx.x, nlb) : blockIdx.x;
     const int64_t si = (int64_t)bid * WAVES + wave;
     const bool active = si < a.nseg;  // inactive waves still join the block epilogue
     const uint32_t g = lane / BL, bl = lane % BL;
@@ -2220,7 +2425,10 @@ void gather_b4_dispatch_skip(const BArgs &a, int skip, hipStream_t st) {
 
 template <int BL, int KB, int U>
 void gather_v4_skip_u(const GArgs &a, int skip, hipStream_t st) {
-    const dim3 grid(blocks_for(a.nseg)), block(256);
+    // with short rows: the long work items' blocks, then the short rows' blocks
+    const dim3 grid(a.sh_seg ? a.n_lgblk + blocks_for((a.n_sh + SHORT_R_MAX - 1) / SHORT_R_MAX)
+                             : blocks_for(a.nseg)),
+        block(256);
     switch (skip) {
         case SKIP_ZERO: launch((k_gather_v4<BL, KB, U, SKIP_ZERO>), grid, block, 0, st, a); break;
         case SKIP_POSZERO: launch((k_gather_v4<BL, KB, U, SKIP_POSZERO>), grid, block, 0, st, a); break;
@@ -2289,6 +2497,15 @@ void launch_gather(const GatherPlan &p, const ScaleView &sc, const float *in, in
             a.elem_start = p.elem_start;
             a.split_cnt = p.split_cnt;
             a.part = p.part;
+        }
+        // short rows several to a wave (the shapes up to SHORT_MAX_BATCH
+        // columns; the dispatch below picks one of them for nb <= 64)
+        if (v4 && p.sh_seg && p.n_sh > 0 && nb > 1 && nb <= SHORT_MAX_BATCH) {
+            a.seg = p.lg_seg;
+            a.nseg = p.n_lg;
+            a.sh_seg = p.sh_seg;
+            a.n_sh = p.n_sh;
+            a.n_lgblk = blocks_for(p.n_lg);
         }
 
         const dim3 grid(blocks_for(a.nseg)), block(256);

@@ -128,6 +128,15 @@ struct DScatter {
     DevBuf<uint32_t> split_cnt;
     DevBuf<float> part;
     int64_t part_cap = 0;
+    // the work items split into short rows (whole rows of <= SHORT_ROW_BYTES
+    // index bytes, packed several to a wave by the float4 gather) and the
+    // others, both in store order (built on first use by gather_plan when at
+    // least a quarter of the items are short rows; n_sh == 0: not used).
+    // n_short_hint: the short rows the last encode counted (kept, as an
+    // estimate, through row patches)
+    DevBuf<SegDesc> sh_seg, lg_seg;
+    int64_t n_sh = 0, n_lg = 0, n_short_hint = 0;
+    bool sh_valid = false;
     GatherPlan plan() const {
         GatherPlan p{seg.p, nseg, idx.p, val.p, rows, cols, has_split, split_rows.p, n_split};
         if (has_split && part_cap > 0) {
@@ -558,6 +567,9 @@ void dense_to_top_k_csr_device(const float *x, int64_t rows, int64_t cols, int64
                                float *vals, int64_t *nnz, hipStream_t st);
 
 // rocprim wrappers
+// The plan of a scattered store for a float4 gather over nb batch columns:
+// with its short rows split off (built on first use) where that applies.
+GatherPlan gather_plan(Layer &L, DScatter &s, int64_t nb);
 void device_exclusive_scan_u64(Layer &L, const uint64_t *in, uint64_t *out, int64_t n);
 void device_exclusive_scan_u32(Layer &L, const uint32_t *in, uint32_t *out, int64_t n);
 // Small device values read back with one stream synchronization: each

@@ -680,6 +680,7 @@ void invalidate_derived(DScatter &s) {
     s.stream1.failed = s.streamK.failed = false;
     s.fidx.valid = false;
     s.dcol_valid = false;
+    s.sh_valid = false;
     s.slc_w = 0;
     s.cblk.clear();
     s.cblk_cb = 0;

@@ -148,6 +148,8 @@ class Layer {
         d["stream_canonical"] = bool(i.stream_canonical);
         d["stream_shadow"] = bool(i.stream_shadow);
         d["split_combined"] = (int)i.split_combined;
+        d["short_rows_canonical"] = i.short_rows_canonical;
+        d["short_rows_shadow"] = i.short_rows_shadow;
         return d;
     }
 

@@ -137,6 +137,7 @@ struct Chunk {
     uint64_t T;     // terminator mask (wave-uniform)
     uint32_t col;   // absolute column (terminator lanes)
     uint32_t rank;  // entry rank within the window (terminator lanes)
+    uint32_t v;     // the entry's column delta (terminator lanes), else 0
     bool term;
 };
 
@@ -168,6 +169,7 @@ __device__ __forceinline__ Chunk decode_chunk(const uint8_t *__restrict__ idx, u
     v = run >= 4u ? ((v << 7) | (b4 & 0x7Fu)) : v;
     v = term ? v : 0u;
     ch.col = carry + wave_incl_scan(v);
+    ch.v = v;
     ch.rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(T >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)T, 0u));
     ch.term = term;
     ch.T = T;
