@@ -1348,9 +1348,10 @@ __device__ __forceinline__ void store_rows4_block(bool active, uint32_t brow, bo
 // the batch) and accumulating the tile's 4 output rows.  Needs nb % 4 == 0,
 // in_ld % 4 == 0, a 16-byte aligned `in` and a < 2 GiB input.
 template <int BL, int KB, int U>
-__global__ __launch_bounds__(256) void k_gather_b4_v4(BArgs a, uint32_t in_bytes) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(U <= 2 ? 4 : 1))) void k_gather_b4_v4(BArgs a, uint32_t in_bytes) {
     __shared__ uint32_t s_off[WAVES][64];
     __shared__ __align__(16) float s_w[WAVES][64 * 16];
+    __shared__ float s_fp4[WAVES][16];
     constexpr uint32_t G = 64u / BL;
     constexpr uint32_t STEP = G * U;
     constexpr uint32_t NBC = 4u * BL * KB;  // batch columns per wave
@@ -1385,6 +1386,9 @@ __global__ __launch_bounds__(256) void k_gather_b4_v4(BArgs a, uint32_t in_bytes
         lane_off[k] = q < nq ? q * 16u : OOB_OFFSET;
     }
     float *sw = s_w[wave];
+    fp4_table_init(s_fp4[wave]);
+    wave_lds_sync();
+    const float *tab = s_fp4[wave];
     // rank-1 scales of the block row's 4 rows (uniform over the segment)
     float rs[4];
 #pragma unroll
@@ -1401,27 +1405,50 @@ __global__ __launch_bounds__(256) void k_gather_b4_v4(BArgs a, uint32_t in_bytes
         const uint32_t npad = (n + STEP - 1u) / STEP * STEP;
         if (ch.term) {
             // the lane that decoded tile `rank` dequantises its 16 slots:
-            // one 16-byte load of the tile, scales S(r,c) as scale_at
+            // one 16-byte load of the tile, scales S(r,c) as scale_at; the
+            // scale rank is one uniform branch here (a per-slot choice would
+            // carry scale_at's loop into every slot), codes by the LDS table
             const uint32_t bc = ch.col;
             s_off[wave][ch.rank] = bc * 4u * ld_bytes;
             const uint4 tb = *reinterpret_cast<const uint4 *>(a.tiles + (size_t)(ebase + ch.rank) * 16u);
             const uint32_t words[4] = {tb.x, tb.y, tb.z, tb.w};  // word lj holds slots lj*4 .. lj*4+3
+            bool rok[4];
 #pragma unroll
-            for (int lj = 0; lj < 4; ++lj) {
-                const uint32_t c = bc * 4u + (uint32_t)lj;
-                const bool cok = c < a.cols;
-                const float cs = (a.sc.rank == 1 && a.sc.ent && cok) ? a.sc.ent[c] : 1.0f;
-                float wv[4];
+            for (int li = 0; li < 4; ++li) rok[li] = br * 4u + (uint32_t)li < a.rows;
+            if (a.sc.rank == 1) {
+                float cs[4];
 #pragma unroll
-                for (int li = 0; li < 4; ++li) {
-                    const uint32_t r = br * 4u + (uint32_t)li;
-                    const uint32_t code = (words[lj] >> (8 * li)) & 0xFu;
-                    float S;
-                    if (a.sc.rank == 1) S = a.sc.ent ? rs[li] * cs : rs[li];
-                    else S = (r < a.rows && cok) ? scale_at(a.sc, r, c) : 1.0f;
-                    wv[li] = (r < a.rows && cok) ? fp4_decode(code) * S : 0.0f;
+                for (int lj = 0; lj < 4; ++lj) {
+                    const uint32_t c = bc * 4u + (uint32_t)lj;
+                    cs[lj] = (a.sc.ent && c < a.cols) ? a.sc.ent[c] : 1.0f;
                 }
-                reinterpret_cast<float4 *>(sw + ch.rank * 16u)[lj] = make_float4(wv[0], wv[1], wv[2], wv[3]);
+#pragma unroll
+                for (int lj = 0; lj < 4; ++lj) {
+                    const bool cok = bc * 4u + (uint32_t)lj < a.cols;
+                    float wv[4];
+#pragma unroll
+                    for (int li = 0; li < 4; ++li) {
+                        const float S = a.sc.ent ? rs[li] * cs[lj] : rs[li];
+                        const float d = tab[(words[lj] >> (8 * li)) & 0xFu];
+                        wv[li] = (rok[li] && cok) ? d * S : 0.0f;
+                    }
+                    reinterpret_cast<float4 *>(sw + ch.rank * 16u)[lj] = make_float4(wv[0], wv[1], wv[2], wv[3]);
+                }
+            } else {
+#pragma unroll
+                for (int lj = 0; lj < 4; ++lj) {
+                    const uint32_t c = bc * 4u + (uint32_t)lj;
+                    const bool cok = c < a.cols;
+                    float wv[4];
+#pragma unroll
+                    for (int li = 0; li < 4; ++li) {
+                        const uint32_t r = br * 4u + (uint32_t)li;
+                        const float S = (rok[li] && cok) ? scale_at(a.sc, r, c) : 1.0f;
+                        const float d = tab[(words[lj] >> (8 * li)) & 0xFu];
+                        wv[li] = (rok[li] && cok) ? d * S : 0.0f;
+                    }
+                    reinterpret_cast<float4 *>(sw + ch.rank * 16u)[lj] = make_float4(wv[0], wv[1], wv[2], wv[3]);
+                }
             }
         }
         // padding slots n .. npad-1 (a terminator lane can sit at or past n when
