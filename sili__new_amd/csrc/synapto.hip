@@ -330,12 +330,11 @@ __global__ void k_tile_wkeys(const uint32_t *tbr, const uint32_t *tbc, int64_t T
 }
 
 // The k smallest: order[] lists synapse indices by (|w|, row, col).
-__global__ void k_syn_prune(const uint32_t *order, int64_t k, int64_t Ns, const uint64_t *rc,
-                            uint8_t *s_removed, uint8_t *tbytes, uint8_t *touched, uint64_t *pruned) {
+__global__ void k_syn_prune(const uint32_t *order, int64_t k, int64_t Ns, uint8_t *s_removed, uint8_t *tbytes,
+                            uint8_t *touched) {
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (i >= k) return;
     const uint32_t e = order[i];
-    pruned[i] = rc[e];
     if ((int64_t)e < Ns) {
         s_removed[e] = 1;
     } else {
@@ -388,21 +387,27 @@ __global__ void k_syn_set1(int64_t Ns, int64_t T, const uint64_t *rc, const uint
 
 // Static validity of each candidate: in range, not just pruned, not stored
 // (scattered after prune + demote, or a live slot of a surviving tile).
-// Valid ones get their rc key, the rest KEY_NONE.
+// Valid ones get their rc key, the rest KEY_NONE.  Read off the stores as
+// they were before the step: a position is taken exactly when it held a
+// synapse there -- an entry of the scattered store, or a nonzero slot byte of
+// a tile -- whether this step pruned it (it may not regrow in the step that
+// pruned it), kept it, or moved it from a demoted tile to the scattered set.
+// rc_scat: the scattered entries' (row << 32 | col) keys in store order
+// (ascending); tiles_old: the tiles' bytes before the step.
 __global__ void k_syn_cand_static(int64_t n_cand, const int32_t *cr, const int32_t *cc, int64_t n_in,
-                                  int64_t n_out, const uint64_t *pruned, int64_t k, const uint64_t *set1,
-                                  int64_t n_set1, const uint64_t *tkey, int64_t T, const uint8_t *alive,
-                                  const uint8_t *tbytes, uint64_t bcols, uint64_t *ckey) {
+                                  int64_t n_out, const uint64_t *rc_scat, int64_t Ns, const uint64_t *tkey,
+                                  int64_t T, const uint8_t *tiles_old, uint64_t bcols, uint64_t *ckey) {
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (i >= n_cand) return;
     const int32_t r = cr[i], c = cc[i];
     uint64_t key = KEY_NONE;
     if (r >= 0 && r < n_in && c >= 0 && c < n_out) {
         const uint64_t rc = rc_key((uint32_t)r, (uint32_t)c);
-        bool ok = !contains_u64(pruned, k, rc) && !contains_u64(set1, n_set1, rc);
+        bool ok = !contains_u64(rc_scat, Ns, rc);
         if (ok) {
-            const int64_t t = find_tile(tkey, T, alive, (uint64_t)(r >> 2) * bcols + (uint64_t)(c >> 2));
-            if (t >= 0 && tbytes[t * 16 + (c & 3) * 4 + (r & 3)] != 0) ok = false;
+            const uint64_t wkey = (uint64_t)(r >> 2) * bcols + (uint64_t)(c >> 2);
+            const int64_t t = lower_bound_u64(tkey, T, wkey);
+            if (t < T && tkey[t] == wkey && tiles_old[t * 16 + (c & 3) * 4 + (r & 3)] != 0) ok = false;
         }
         if (ok) key = rc;
     }
@@ -788,25 +793,18 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
 
     // -- prune ---------------------------------------------------------------
     TmpBuf<uint8_t> s_removed(L, SILI_TMPKEY(s_removed)), touched(L, SILI_TMPKEY(touched)), alive(L, SILI_TMPKEY(alive)), dem_byte(L, SILI_TMPKEY(dem_byte));
-    TmpBuf<uint64_t> pruned(L, SILI_TMPKEY(pruned)), pruned_sorted(L, SILI_TMPKEY(pruned_sorted)), dem_key(L, SILI_TMPKEY(dem_key));
-    TmpBuf<uint32_t> pruned_v(L, SILI_TMPKEY(pruned_v)), pruned_vs(L, SILI_TMPKEY(pruned_vs));
+    TmpBuf<uint64_t> dem_key(L, SILI_TMPKEY(dem_key));
     s_removed.ensure((size_t)Ns + 1);
     touched.ensure((size_t)T + 1);
     alive.ensure((size_t)T + 1);
     dem_byte.ensure((size_t)T + 1);
     dem_key.ensure((size_t)T + 1);
-    pruned.ensure((size_t)k + 1);
-    pruned_sorted.ensure((size_t)k + 1);
-    pruned_v.ensure((size_t)k + 1);
-    pruned_vs.ensure((size_t)k + 1);
     if (Ns > 0) launch(k_fill_u8, dim3(nblk(Ns)), dim3(TPB), 0, st, s_removed.p, Ns, (uint8_t)0);
     if (T > 0) launch(k_fill_u8, dim3(nblk(T)), dim3(TPB), 0, st, touched.p, T, (uint8_t)0);
     if (k > 0) {
-        launch(k_syn_prune, dim3(nblk(k)), dim3(TPB), 0, st, (const uint32_t *)order.p, k, Ns,
-               (const uint64_t *)rc.p, s_removed.p, tbytes.p, touched.p, pruned.p);
-        launch(k_iota32, dim3(nblk(k)), dim3(TPB), 0, st, pruned_v.p, k);
+        launch(k_syn_prune, dim3(nblk(k)), dim3(TPB), 0, st, (const uint32_t *)order.p, k, Ns, s_removed.p,
+               tbytes.p, touched.p);
         SILI_HIP(hipGetLastError());
-        device_sort_pairs_u64(L, pruned.p, pruned_sorted.p, pruned_v.p, pruned_vs.p, k, rc_bits);
     }
 
     // -- demote --------------------------------------------------------------
@@ -821,14 +819,13 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
         SILI_HIP(hipGetLastError());
     }
 
-    // -- scattered set after prune + demote (sorted for lookups) --------------
+    // -- scattered set after prune + demote -----------------------------------
     const int64_t M2 = Ns + T + n_cand;
-    TmpBuf<uint64_t> key2(L, SILI_TMPKEY(key2)), key2_sorted(L, SILI_TMPKEY(key2_sorted)), set1_sorted(L, SILI_TMPKEY(set1_sorted));
+    TmpBuf<uint64_t> key2(L, SILI_TMPKEY(key2)), key2_sorted(L, SILI_TMPKEY(key2_sorted));
     TmpBuf<uint8_t> byte2(L, SILI_TMPKEY(byte2)), byte2_sorted(L, SILI_TMPKEY(byte2_sorted)), removed2(L, SILI_TMPKEY(removed2));
     TmpBuf<uint32_t> iota2(L, SILI_TMPKEY(iota2)), perm2(L, SILI_TMPKEY(perm2));
     key2.ensure((size_t)M2 + 1);
     key2_sorted.ensure((size_t)M2 + 1);
-    set1_sorted.ensure((size_t)(Ns + T) + 1);
     byte2.ensure((size_t)M2 + 1);
     byte2_sorted.ensure((size_t)M2 + 1);
     removed2.ensure((size_t)M2 + 1);
@@ -838,9 +835,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
         launch(k_syn_set1, dim3(nblk(Ns + T)), dim3(TPB), 0, st, Ns, T, (const uint64_t *)rc.p,
                (const uint8_t *)L.W.val.p, (const uint8_t *)s_removed.p, (const uint64_t *)dem_key.p,
                (const uint8_t *)dem_byte.p, key2.p, byte2.p);
-        launch(k_iota32, dim3(nblk(Ns + T)), dim3(TPB), 0, st, iota2.p, Ns + T);
         SILI_HIP(hipGetLastError());
-        device_sort_pairs_u64(L, key2.p, set1_sorted.p, iota2.p, perm2.p, Ns + T, rc_bits);
     }
 
     // -- candidates: first valid ones in list order ---------------------------
@@ -871,9 +866,8 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
         wvs.ensure((size_t)n_cand);
         const unsigned g = nblk(n_cand);
         launch(k_syn_cand_static, dim3(g), dim3(TPB), 0, st, n_cand, (const int32_t *)dcr.p,
-               (const int32_t *)dcc.p, n_in, n_out, (const uint64_t *)pruned_sorted.p, k,
-               (const uint64_t *)set1_sorted.p, Ns + T, (const uint64_t *)tkey.p, T,
-               (const uint8_t *)alive.p, (const uint8_t *)tbytes.p, bcols, ckey.p);
+               (const int32_t *)dcc.p, n_in, n_out, (const uint64_t *)rc.p, Ns, (const uint64_t *)tkey.p, T,
+               (const uint8_t *)L.B4.tiles.p, bcols, ckey.p);
         launch(k_iota32, dim3(g), dim3(TPB), 0, st, cidx.p, n_cand);
         launch(k_fill_u32, dim3(g), dim3(TPB), 0, st, first.p, n_cand, 0u);
         SILI_HIP(hipGetLastError());
