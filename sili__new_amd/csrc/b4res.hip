@@ -58,13 +58,15 @@ uint64_t total(const std::vector<uint64_t> &v) {
 }
 
 // stored bytes per block row: its tiles' lengths by tile_is_sparse and live count
+// (one wave per block row, its lanes over the row's tiles)
 __global__ void k_row_tile_bytes(const uint8_t *__restrict__ tiles, const uint8_t *__restrict__ flags,
                                  const uint32_t *__restrict__ tile_start, int64_t brows,
                                  uint64_t *__restrict__ out) {
-    const int64_t br = (int64_t)blockIdx.x * TPB + threadIdx.x;
-    if (br >= brows) return;
-    uint64_t s = 0;
-    for (uint32_t t = tile_start[br]; t < tile_start[br + 1]; ++t) {
+    const int64_t br = (int64_t)blockIdx.x * (TPB / 64) + (threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63u;
+    if (br >= brows) return;  // (the whole wave)
+    unsigned long long s = 0;
+    for (uint32_t t = tile_start[br] + lane; t < tile_start[br + 1]; t += 64u) {
         const uint4 v = *reinterpret_cast<const uint4 *>(tiles + (size_t)t * 16u);
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
         uint32_t live = 0;
@@ -72,7 +74,8 @@ __global__ void k_row_tile_bytes(const uint8_t *__restrict__ tiles, const uint8_
             for (int b = 0; b < 4; ++b) live += ((w[i] >> (8 * b)) & 0xFFu) != 0u;
         s += tile_len(flags[t] != 0, live);
     }
-    out[br] = s;
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (lane == 0) out[br] = (uint64_t)s;
 }
 
 }  // namespace
@@ -96,15 +99,17 @@ B4Use b4_row_use(Layer &L) {
     if (rows == 0 || L.B4.ntiles == 0) return u;
     hipStream_t st = L.stream;
     std::vector<uint32_t> bs((size_t)rows + 1), ts((size_t)rows + 1);
-    DevBuf<uint64_t> ut;
+    TmpBuf<uint64_t> ut(L, SILI_TMPKEY(b4res_ut));
     ut.ensure((size_t)rows);
-    launch(k_row_tile_bytes, dim3(nblk(rows)), dim3(TPB), 0, st, (const uint8_t *)L.B4.tiles.p,
-           (const uint8_t *)L.B4.sparse.p, (const uint32_t *)L.B4.tile_start.p, rows, ut.p);
+    launch(k_row_tile_bytes, dim3((unsigned)((rows + TPB / 64 - 1) / (TPB / 64))), dim3(TPB), 0, st,
+           (const uint8_t *)L.B4.tiles.p, (const uint8_t *)L.B4.sparse.p, (const uint32_t *)L.B4.tile_start.p, rows,
+           ut.p);
     SILI_HIP(hipGetLastError());
-    SILI_HIP(hipMemcpyAsync(bs.data(), L.B4.byte_start.p, bs.size() * 4, hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipMemcpyAsync(ts.data(), L.B4.tile_start.p, ts.size() * 4, hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipMemcpyAsync(u.ut.data(), ut.p, (size_t)rows * 8, hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipStreamSynchronize(st));
+    BulkRead rd(L);
+    rd.add(bs.data(), L.B4.byte_start.p, bs.size() * 4);
+    rd.add(ts.data(), L.B4.tile_start.p, ts.size() * 4);
+    rd.add(u.ut.data(), ut.p, (size_t)rows * 8);
+    rd.wait();
     for (int64_t r = 0; r < rows; ++r) {
         u.ui[(size_t)r] = bs[(size_t)r + 1] - bs[(size_t)r];
         u.ue[(size_t)r] = ts[(size_t)r + 1] - ts[(size_t)r];

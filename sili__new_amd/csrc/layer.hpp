@@ -427,6 +427,7 @@ struct Layer {
     // the device copy of the patch content, and the arrays' second buffers
     PinBuf pin_rows, pin_stage, pin_patch, pin_deg, pin_acc;
     PinBuf pin_read;  // ReadBack's staging
+    PinBuf pin_bulk;  // BulkRead's staging
     // The activity accumulators as build_probes last staged them (pin_acc),
     // with its top-k selections over them (k, indices), valid while acc_epoch
     // == policy_epoch: no entry point that may change them has run since.
@@ -594,6 +595,39 @@ struct ReadBack {
         SILI_HIP(hipStreamSynchronize(L.stream));
         for (int i = 0; i < n; ++i) std::memcpy(items[i].dst, L.pin_read.h + 64 * i, items[i].bytes);
         n = 0;
+    }
+};
+
+// Whole device arrays read to the host through pinned memory (L.pin_bulk):
+// every copy queued, then one wait.  Destinations are written at wait().
+struct BulkRead {
+    Layer &L;
+    struct Item {
+        void *dst;
+        const void *src;
+        size_t bytes;
+    };
+    std::vector<Item> items;
+    explicit BulkRead(Layer &l) : L(l) {}
+    void add(void *dst, const void *src, size_t bytes) {
+        if (bytes) items.push_back(Item{dst, src, bytes});
+    }
+    void wait() {
+        size_t total = 0;
+        for (const Item &it : items) total += (it.bytes + 15) & ~size_t(15);
+        L.pin_bulk.ensure(total);
+        size_t off = 0;
+        for (const Item &it : items) {
+            SILI_HIP(hipMemcpyAsync(L.pin_bulk.h + off, it.src, it.bytes, hipMemcpyDeviceToHost, L.stream));
+            off += (it.bytes + 15) & ~size_t(15);
+        }
+        SILI_HIP(hipStreamSynchronize(L.stream));
+        off = 0;
+        for (const Item &it : items) {
+            std::memcpy(it.dst, L.pin_bulk.h + off, it.bytes);
+            off += (it.bytes + 15) & ~size_t(15);
+        }
+        items.clear();
     }
 };
 

@@ -91,9 +91,10 @@ void row_content(Layer &L, std::vector<uint64_t> &bytes, std::vector<uint64_t> &
     const size_t rows = (size_t)L.n_in;
     std::vector<uint32_t> bs(rows + 1, 0), es(rows + 1, 0);
     if (rows > 0 && L.W.byte_start.p) {
-        SILI_HIP(hipMemcpyAsync(bs.data(), L.W.byte_start.p, (rows + 1) * 4, hipMemcpyDeviceToHost, L.stream));
-        SILI_HIP(hipMemcpyAsync(es.data(), L.W.elem_start.p, (rows + 1) * 4, hipMemcpyDeviceToHost, L.stream));
-        SILI_HIP(hipStreamSynchronize(L.stream));
+        BulkRead rd(L);
+        rd.add(bs.data(), L.W.byte_start.p, (rows + 1) * 4);
+        rd.add(es.data(), L.W.elem_start.p, (rows + 1) * 4);
+        rd.wait();
     }
     bytes.resize(rows);
     elems.resize(rows);
