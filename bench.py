@@ -1025,6 +1025,47 @@ def run_layer_config(a, hip, api, rt, cfg, steps, warmup, train_lr, synapto_reps
     return out
 
 
+def time_binding(hip, steps=50, warmup=5):
+    """Config 1 through the pybind module the way FoldedLayer / DISLDOLayer
+    call it (sili/sparse_rnn.py:1004-1212): numpy arrays in, numpy arrays out,
+    so every call copies its input to the device and its output back.  Wall
+    time per step of forward_dense + backward_dense(lr 0), and of each call."""
+    from sili__new_amd.synth import make_config
+    wl = make_config(1)
+    L = hip.SparseLinearLayer(wl.n_in, wl.n_out, wl.nnz)
+    L.load_weights(wl.ptrs, wl.cols, wl.q)
+    L.set_value_scales(wl.value_scale)
+    x = np.ascontiguousarray(wl.x, dtype=np.float32)
+    g = np.ascontiguousarray(wl.g, dtype=np.float32)
+    def run(xin, gin):
+        for _ in range(warmup):
+            L.forward_dense(xin)
+            L.backward_dense(gin, 0.0)
+        tf = tb = 0.0
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            L.forward_dense(xin)
+            t1 = time.perf_counter()
+            L.backward_dense(gin, 0.0)
+            t2 = time.perf_counter()
+            tf += t1 - t0
+            tb += t2 - t1
+        return {"ms_per_step": round((tf + tb) * 1e3 / steps, 4), "fwd_ms": round(tf * 1e3 / steps, 4),
+                "bwd_ms": round(tb * 1e3 / steps, 4)}
+
+    host_bytes = 4 * (x.size + g.size + wl.batch * (wl.n_out + wl.n_in))
+    out = {"workload": "config 1 forward_dense + backward_dense(lr 0) through the pybind module, numpy in and "
+                       "out (grad-input only: the module's backward returns dx); inputs either ordinary numpy "
+                       "arrays or arrays the module returned (page-locked, as a chained layer's input is)",
+           "steps": steps, "host_bytes_per_step": host_bytes}
+    out["numpy_inputs"] = run(x, g)
+    # arrays the module returned: its outputs live in page-locked blocks
+    xp = L.forward_dense(x)
+    gp = L.backward_dense(g, 0.0)
+    out["module_arrays_as_inputs"] = run(xp, gp)
+    return out
+
+
 def other_configs(a, hip, api, rt):
     """Configs 2, 3 (with its synaptogenesis step) and 4 (batches 1, 8, 128)
     timed as config 1 is (rotated copies, HIP events over the timed steps,
@@ -1052,6 +1093,7 @@ def other_configs(a, hip, api, rt):
                                 "pct_hbm_peak": r["pct_hbm_peak"], "dominant": r["dominant"]}
                             for b, r in o["batches"].items()},
                 "build_s": o["build_s"], "wall_s": round(time.perf_counter() - t0, 1)}
+    res["binding"] = time_binding(hip)
     return res
 
 

@@ -540,6 +540,20 @@ int sili_device_free(sili_layer *layer, void *ptr);
 int sili_memcpy_h2d(sili_layer *layer, void *dst, const void *src, size_t bytes);
 int sili_memcpy_d2h(sili_layer *layer, void *dst, const void *src, size_t bytes);
 int sili_memset_device(sili_layer *layer, void *dst, int value, size_t bytes);
+/* Page-locked host memory (hipHostMalloc): copies from and to it run as DMA
+ * without a staging copy.  No counterpart in the reference (a CPU library);
+ * for binding layers that hand host arrays across the boundary. */
+int sili_host_alloc(size_t bytes, void **out);
+int sili_host_free(void *ptr);
+/* Host -> device copy ordered on the layer's stream (after the work queued on
+ * it, before the work queued after it), without waiting for it: the source
+ * must stay unchanged until the stream has passed the copy (sili_synchronize,
+ * or an ordered device -> host copy, returns).  From page-locked memory it is
+ * one DMA on the stream. */
+int sili_memcpy_h2d_ordered(sili_layer *layer, void *dst, const void *src, size_t bytes);
+/* Device -> host copy ordered on the layer's stream; returns when it has
+ * landed (one wait for the stream). */
+int sili_memcpy_d2h_ordered(sili_layer *layer, void *dst, const void *src, size_t bytes);
 
 #ifdef __cplusplus
 }

@@ -1807,6 +1807,36 @@ int sili_memcpy_d2h(sili_layer *layer, void *dst, const void *src, size_t bytes)
         if (bytes) SILI_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
     });
 }
+int sili_host_alloc(size_t bytes, void **out) {
+    return guarded([&] {
+        if (!out) throw_error(SILI_ERR_INVALID, "NULL argument");
+        *out = nullptr;
+        if (hipHostMalloc(out, bytes ? bytes : 4, hipHostMallocDefault) != hipSuccess || !*out) {
+            (void)hipGetLastError();
+            throw_error(SILI_ERR_NOMEM, "sili_host_alloc: hipHostMalloc failed");
+        }
+    });
+}
+int sili_host_free(void *ptr) {
+    return guarded([&] {
+        if (ptr) SILI_HIP(hipHostFree(ptr));
+    });
+}
+int sili_memcpy_h2d_ordered(sili_layer *layer, void *dst, const void *src, size_t bytes) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "NULL argument");
+        set_device(layer->L);
+        if (bytes) SILI_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, layer->L.stream));
+    });
+}
+int sili_memcpy_d2h_ordered(sili_layer *layer, void *dst, const void *src, size_t bytes) {
+    return guarded([&] {
+        if (!layer) throw_error(SILI_ERR_INVALID, "NULL argument");
+        set_device(layer->L);
+        if (bytes) SILI_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, layer->L.stream));
+        SILI_HIP(hipStreamSynchronize(layer->L.stream));
+    });
+}
 int sili_memset_device(sili_layer *layer, void *dst, int value, size_t bytes) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "NULL argument");

@@ -12,6 +12,8 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -36,6 +38,86 @@ inline void ck(int code) {
 
 template <typename T>
 using carr = py::array_t<T, py::array::c_style | py::array::forcecast>;
+
+// Page-locked host blocks behind the arrays the module returns.  A returned
+// numpy array keeps its block (a capsule hands it back to the pool when the
+// array dies), so a device -> host copy lands in place by DMA, and an array
+// passed back in -- a chained layer's input, the backward's dy built from an
+// output -- goes to the device by DMA as well.  Blocks come in 64 KiB size
+// classes; at most 1 GiB of free blocks is kept, and past 2 GiB of blocks
+// held by live arrays the module returns ordinary (pageable) arrays.  The
+// pool is never destroyed: the HIP runtime may be gone when the interpreter
+// exits.
+class PinnedPool {
+   public:
+    static PinnedPool &get() {
+        static PinnedPool *p = new PinnedPool();
+        return *p;
+    }
+    static size_t size_class(size_t bytes) { return (bytes + 65535) & ~size_t(65535); }
+    // a block of at least `bytes`, or nullptr past the live cap
+    void *take(size_t bytes) {
+        const size_t c = size_class(bytes ? bytes : 4);
+        {
+            std::lock_guard<std::mutex> g(m_);
+            auto it = free_.find(c);
+            if (it != free_.end()) {
+                void *p = it->second;
+                free_.erase(it);
+                free_bytes_ -= c;
+                held_bytes_ += c;
+                return p;
+            }
+            if (held_bytes_ + c > HELD_CAP) return nullptr;
+        }
+        void *p = nullptr;
+        if (sili_host_alloc(c, &p) != SILI_OK || !p) return nullptr;
+        std::lock_guard<std::mutex> g(m_);
+        blocks_[(uintptr_t)p] = c;
+        held_bytes_ += c;
+        return p;
+    }
+    void give(void *p) {
+        size_t c = 0;
+        {
+            std::lock_guard<std::mutex> g(m_);
+            auto it = blocks_.find((uintptr_t)p);
+            if (it == blocks_.end()) return;
+            c = it->second;
+            held_bytes_ -= c;
+            if (free_bytes_ + c <= FREE_CAP) {
+                free_.emplace(c, p);
+                free_bytes_ += c;
+                return;
+            }
+            blocks_.erase(it);
+        }
+        (void)sili_host_free(p);
+    }
+
+   private:
+    static constexpr size_t FREE_CAP = size_t(1) << 30, HELD_CAP = size_t(2) << 30;
+    std::mutex m_;
+    std::multimap<size_t, void *> free_;
+    std::map<uintptr_t, size_t> blocks_;
+    size_t free_bytes_ = 0, held_bytes_ = 0;
+};
+
+// A float32 array of `shape` over a page-locked block (pageable when the pool
+// declines); *data receives its buffer.
+py::array_t<float> host_array(const std::vector<py::ssize_t> &shape, float **data) {
+    size_t n = 1;
+    for (py::ssize_t d : shape) n *= (size_t)d;
+    void *p = PinnedPool::get().take(n * 4);
+    if (!p) {
+        py::array_t<float> r(shape);
+        *data = r.mutable_data();
+        return r;
+    }
+    py::capsule owner(p, [](void *q) { PinnedPool::get().give(q); });
+    *data = static_cast<float *>(p);
+    return py::array_t<float>(shape, static_cast<float *>(p), owner);
+}
 
 // A device buffer owned by one layer wrapper, grown on demand.
 struct DBuf {
@@ -271,7 +353,7 @@ class Layer {
         const int64_t cols = x.ndim() == 2 ? (int64_t)x.shape(1) : (int64_t)x.shape(0);
         if (x.ndim() > 2 || cols != n_in_) throw py::value_error("x must be [batch, n_inputs] or [n_inputs]");
         float *dx = (float *)last_x_.get((size_t)(B * n_in_) * 4);
-        ck(sili_memcpy_h2d(L_, dx, x.data(), (size_t)(B * n_in_) * 4));
+        ck(sili_memcpy_h2d_ordered(L_, dx, x.data(), (size_t)(B * n_in_) * 4));
         last_batch_ = B;
         float *dy = (float *)y_.get((size_t)(B * n_out_) * 4);
         ck(sili_forward_dense(L_, dx, B, dy, nullptr));
@@ -285,7 +367,7 @@ class Layer {
         const int64_t B = last_batch_;
         if (dy.size() != B * n_out_) throw py::value_error("dy must be [batch, n_outputs] of the last forward");
         float *ddy = (float *)g_.get((size_t)(B * n_out_) * 4);
-        ck(sili_memcpy_h2d(L_, ddy, dy.data(), (size_t)(B * n_out_) * 4));
+        ck(sili_memcpy_h2d_ordered(L_, ddy, dy.data(), (size_t)(B * n_out_) * 4));
         float *ddx = (float *)dx_.get((size_t)(B * n_in_) * 4);
         if (learning_rate == 0.0f) {
             ck(sili_backward_dense(L_, (const float *)last_x_.p, ddy, B, ddx, nullptr, nullptr, 0.0f, nullptr));
@@ -348,14 +430,16 @@ class Layer {
         // belongs to forward_dense alone, as the reference's _last_input
         float *dx = (float *)xs_.get((size_t)(B * n_in_) * 4);
         float *dg = (float *)g_.get((size_t)(B * n_out_) * 4);
-        ck(sili_memcpy_h2d(L_, dx, x.data(), (size_t)(B * n_in_) * 4));
-        ck(sili_memcpy_h2d(L_, dg, dy.data(), (size_t)(B * n_out_) * 4));
+        ck(sili_memcpy_h2d_ordered(L_, dx, x.data(), (size_t)(B * n_in_) * 4));
+        ck(sili_memcpy_h2d_ordered(L_, dg, dy.data(), (size_t)(B * n_out_) * 4));
         float *gs = (float *)gws_.get((size_t)i.nnz_scattered * 4 + 4);
         float *gb = (float *)gwb_.get((size_t)i.n_tiles * 64 + 4);
         ck(sili_sampled_gradw(L_, dx, dg, B, gs, gb, nullptr));
-        py::array_t<float> a((py::ssize_t)i.nnz_scattered), b((py::ssize_t)(i.n_tiles * 16));
-        ck(sili_memcpy_d2h(L_, a.mutable_data(), gs, (size_t)i.nnz_scattered * 4));
-        ck(sili_memcpy_d2h(L_, b.mutable_data(), gb, (size_t)i.n_tiles * 64));
+        float *ha = nullptr, *hb = nullptr;
+        py::array_t<float> a = host_array({(py::ssize_t)i.nnz_scattered}, &ha);
+        py::array_t<float> b = host_array({(py::ssize_t)(i.n_tiles * 16)}, &hb);
+        ck(sili_memcpy_d2h_ordered(L_, ha, gs, (size_t)i.nnz_scattered * 4));
+        ck(sili_memcpy_d2h_ordered(L_, hb, gb, (size_t)i.n_tiles * 64));
         return py::make_tuple(a, b);
     }
 
@@ -378,7 +462,7 @@ class Layer {
         if (x.size() != batch * n_in_) throw py::value_error("x must be [batch, n_inputs]");
         check_csr(dptrs, didx, dvals, batch, n_out_);
         float *dxin = (float *)xs_.get((size_t)(batch * n_in_) * 4);
-        ck(sili_memcpy_h2d(L_, dxin, x.data(), (size_t)(batch * n_in_) * 4));
+        ck(sili_memcpy_h2d_ordered(L_, dxin, x.data(), (size_t)(batch * n_in_) * 4));
         int32_t *dp = upload_i32(p_, dptrs);
         int32_t *di = upload_i32(i_, didx);
         float *dv = upload_f32(v_, dvals);
@@ -682,19 +766,23 @@ class Layer {
                     throw py::value_error("sparse indices must be strictly increasing within a batch row");
             }
     }
+    // (uploads are ordered on the layer's stream without a wait: every entry
+    // point that makes them returns through fetch or an ordered device ->
+    // host copy, which waits for the stream, while its arguments are alive)
     int32_t *upload_i32(DBuf &b, const carr<int32_t> &a) {
         void *d = b.get((size_t)a.size() * 4 + 4);
-        ck(sili_memcpy_h2d(L_, d, a.data(), (size_t)a.size() * 4));
+        ck(sili_memcpy_h2d_ordered(L_, d, a.data(), (size_t)a.size() * 4));
         return (int32_t *)d;
     }
     float *upload_f32(DBuf &b, const carr<float> &a) {
         void *d = b.get((size_t)a.size() * 4 + 4);
-        ck(sili_memcpy_h2d(L_, d, a.data(), (size_t)a.size() * 4));
+        ck(sili_memcpy_h2d_ordered(L_, d, a.data(), (size_t)a.size() * 4));
         return (float *)d;
     }
     py::array_t<float> fetch(const float *d, int64_t B, int64_t n) {
-        py::array_t<float> r({(py::ssize_t)B, (py::ssize_t)n});
-        ck(sili_memcpy_d2h(L_, r.mutable_data(), d, (size_t)(B * n) * 4));
+        float *h = nullptr;
+        py::array_t<float> r = host_array({(py::ssize_t)B, (py::ssize_t)n}, &h);
+        ck(sili_memcpy_d2h_ordered(L_, h, d, (size_t)(B * n) * 4));
         return r;
     }
 };
