@@ -425,6 +425,29 @@ def cpu_model():
     return "unknown"
 
 
+def cpu_host():
+    """What the host reports beside its model name (the VMs of the pool name
+    only the family): clock, CPUs online and usable by this process, load
+    averages when the baseline ran -- the context of the baseline's spread."""
+    out = {}
+    try:
+        mhz = [float(l.split(":", 1)[1]) for l in open("/proc/cpuinfo") if l.startswith("cpu MHz")]
+        if mhz:
+            out["cpu_mhz"] = round(sum(mhz) / len(mhz), 1)
+    except (OSError, ValueError):
+        pass
+    out["cpus_online"] = os.cpu_count()
+    try:
+        out["cpus_usable"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        pass
+    try:
+        out["loadavg"] = [round(v, 2) for v in os.getloadavg()]
+    except OSError:
+        pass
+    return out
+
+
 def cpu_baseline(cfg, seconds, lr=0.0, layer_file=None):
     """The CPU baseline, timed in child processes (nothing of the GPU process's
     state, and no GPU, in them) with OMP_NUM_THREADS pinned: at the host
@@ -460,6 +483,7 @@ def cpu_baseline(cfg, seconds, lr=0.0, layer_file=None):
             return {"error": str(e)[-400:]}
     out = dict(runs[max(runs)])
     out["cpu_model"] = cpu_model()
+    out["host"] = cpu_host()
     out["isolated"] = "child process per thread count, OMP_NUM_THREADS pinned"
     if 1 in runs and max(runs) > 1:
         out["one_thread"] = {k: runs[1][k] for k in ("value", "best_value", "median_ms", "best_ms", "sample")}

@@ -60,8 +60,9 @@ class PinnedPool {
         const size_t c = size_class(bytes ? bytes : 4);
         {
             std::lock_guard<std::mutex> g(m_);
-            auto it = free_.find(c);
-            if (it != free_.end()) {
+            // the most recently freed block of the class (its pages are warm)
+            auto it = free_.upper_bound(c);
+            if (it != free_.begin() && (--it)->first == c) {
                 void *p = it->second;
                 free_.erase(it);
                 free_bytes_ -= c;
