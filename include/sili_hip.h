@@ -548,11 +548,13 @@ int sili_host_free(void *ptr);
 /* Host -> device copy ordered on the layer's stream (after the work queued on
  * it, before the work queued after it), without waiting for it: the source
  * must stay unchanged until the stream has passed the copy (sili_synchronize,
- * or an ordered device -> host copy, returns).  From page-locked memory it is
- * one DMA on the stream. */
+ * or an ordered device -> host copy, returns).  From page-locked memory
+ * (sili_host_alloc) it is one copy kernel on the stream, which reads the host
+ * pages directly; from pageable memory, the runtime's staged copy. */
 int sili_memcpy_h2d_ordered(sili_layer *layer, void *dst, const void *src, size_t bytes);
 /* Device -> host copy ordered on the layer's stream; returns when it has
- * landed (one wait for the stream). */
+ * landed (one wait for the stream).  Into page-locked memory it is one copy
+ * kernel on the stream, which writes the host pages directly. */
 int sili_memcpy_d2h_ordered(sili_layer *layer, void *dst, const void *src, size_t bytes);
 
 #ifdef __cplusplus

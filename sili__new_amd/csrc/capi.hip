@@ -123,6 +123,54 @@ void fill(float *p, int64_t n, float v, hipStream_t st) {
     SILI_HIP(hipGetLastError());
 }
 
+// n elements of T, then `tail` (< sizeof(T)) single bytes, by a grid-stride
+// loop; src or dst may be page-locked host memory, which the device reads or
+// writes over the host link.
+template <typename T>
+__global__ __launch_bounds__(256) void k_copy_vec(const T *__restrict__ src, T *__restrict__ dst, int64_t n,
+                                                  const uint8_t *__restrict__ src_tail,
+                                                  uint8_t *__restrict__ dst_tail, int tail) {
+    const int64_t stride = (int64_t)gridDim.x * TPB;
+    for (int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+    if (blockIdx.x == 0 && (int)threadIdx.x < tail) dst_tail[threadIdx.x] = src_tail[threadIdx.x];
+}
+
+// Whether `p` is page-locked host memory that the device addresses at the
+// same address (hipHostMalloc memory on ROCm).  Pageable memory is not known
+// to the runtime: the query fails and its error is cleared.
+bool host_locked(const void *p) {
+    hipPointerAttribute_t a{};
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return a.type == hipMemoryTypeHost && a.devicePointer == p;
+}
+
+// A copy between device memory and page-locked host memory as one kernel on
+// `st`.  The runtime's DMA copies on a stream have been measured at about a
+// quarter of their usual rate (2 MiB in 0.15-0.2 ms against 0.045 ms) on
+// streams of a process after a large layer was built, and staying so; the
+// kernel moves 2 MiB in about 0.05 ms on any stream.  Up to 128 blocks of
+// 32 KiB each per pass (the host link, not the grid, bounds it).
+void kernel_copy(void *dst, const void *src, size_t bytes, hipStream_t st) {
+    const uintptr_t al = reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src);
+    auto go = [&](auto tag) {
+        using T = decltype(tag);
+        const int64_t n = (int64_t)(bytes / sizeof(T));
+        const int tail = (int)(bytes - (size_t)n * sizeof(T));
+        const unsigned grid = (unsigned)std::min<int64_t>(128, std::max<int64_t>(1, (n + 2047) / 2048));
+        ProfScope ps("copy_host", st);
+        launch(k_copy_vec<T>, dim3(grid), dim3(TPB), 0, st, static_cast<const T *>(src), static_cast<T *>(dst), n,
+               static_cast<const uint8_t *>(src) + (size_t)n * sizeof(T),
+               static_cast<uint8_t *>(dst) + (size_t)n * sizeof(T), tail);
+    };
+    if ((al & 15u) == 0) go(uint4{});
+    else if ((al & 3u) == 0) go(uint32_t{});
+    else go(uint8_t{});
+    SILI_HIP(hipGetLastError());
+}
+
 // Every entry point that reaches a layer's device state comes here first.
 // The policy's own (policy = true) leave its pending edits pending; any
 // other writes them first and, unless it only reads the layer
@@ -1826,14 +1874,17 @@ int sili_memcpy_h2d_ordered(sili_layer *layer, void *dst, const void *src, size_
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "NULL argument");
         set_device(layer->L);
-        if (bytes) SILI_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, layer->L.stream));
+        if (!bytes) return;
+        if (host_locked(src)) kernel_copy(dst, src, bytes, layer->L.stream);
+        else SILI_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, layer->L.stream));
     });
 }
 int sili_memcpy_d2h_ordered(sili_layer *layer, void *dst, const void *src, size_t bytes) {
     return guarded([&] {
         if (!layer) throw_error(SILI_ERR_INVALID, "NULL argument");
         set_device(layer->L);
-        if (bytes) SILI_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, layer->L.stream));
+        if (bytes && host_locked(dst)) kernel_copy(dst, src, bytes, layer->L.stream);
+        else if (bytes) SILI_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, layer->L.stream));
         SILI_HIP(hipStreamSynchronize(layer->L.stream));
     });
 }

@@ -78,6 +78,15 @@ class PinnedPool {
         held_bytes_ += c;
         return p;
     }
+    // whether [p, p + bytes) lies in one block of the pool
+    bool owns(const void *p, size_t bytes) {
+        const uintptr_t a = (uintptr_t)p;
+        std::lock_guard<std::mutex> g(m_);
+        auto it = blocks_.upper_bound(a);
+        if (it == blocks_.begin()) return false;
+        --it;
+        return a >= it->first && a + bytes <= it->first + it->second;
+    }
     void give(void *p) {
         size_t c = 0;
         {
@@ -191,7 +200,8 @@ class Layer {
     }
     ~Layer() {
         for (DBuf *b : bufs()) b->release();
-        sili_destroy(L_);
+        sili_destroy(L_);  // waits for the stream
+        release_staged();
     }
     Layer(const Layer &) = delete;
     Layer &operator=(const Layer &) = delete;
@@ -354,7 +364,7 @@ class Layer {
         const int64_t cols = x.ndim() == 2 ? (int64_t)x.shape(1) : (int64_t)x.shape(0);
         if (x.ndim() > 2 || cols != n_in_) throw py::value_error("x must be [batch, n_inputs] or [n_inputs]");
         float *dx = (float *)last_x_.get((size_t)(B * n_in_) * 4);
-        ck(sili_memcpy_h2d_ordered(L_, dx, x.data(), (size_t)(B * n_in_) * 4));
+        ck(sili_memcpy_h2d_ordered(L_, dx, stage(x.data(), (size_t)(B * n_in_) * 4), (size_t)(B * n_in_) * 4));
         last_batch_ = B;
         float *dy = (float *)y_.get((size_t)(B * n_out_) * 4);
         ck(sili_forward_dense(L_, dx, B, dy, nullptr));
@@ -368,7 +378,7 @@ class Layer {
         const int64_t B = last_batch_;
         if (dy.size() != B * n_out_) throw py::value_error("dy must be [batch, n_outputs] of the last forward");
         float *ddy = (float *)g_.get((size_t)(B * n_out_) * 4);
-        ck(sili_memcpy_h2d_ordered(L_, ddy, dy.data(), (size_t)(B * n_out_) * 4));
+        ck(sili_memcpy_h2d_ordered(L_, ddy, stage(dy.data(), (size_t)(B * n_out_) * 4), (size_t)(B * n_out_) * 4));
         float *ddx = (float *)dx_.get((size_t)(B * n_in_) * 4);
         if (learning_rate == 0.0f) {
             ck(sili_backward_dense(L_, (const float *)last_x_.p, ddy, B, ddx, nullptr, nullptr, 0.0f, nullptr));
@@ -431,8 +441,8 @@ class Layer {
         // belongs to forward_dense alone, as the reference's _last_input
         float *dx = (float *)xs_.get((size_t)(B * n_in_) * 4);
         float *dg = (float *)g_.get((size_t)(B * n_out_) * 4);
-        ck(sili_memcpy_h2d_ordered(L_, dx, x.data(), (size_t)(B * n_in_) * 4));
-        ck(sili_memcpy_h2d_ordered(L_, dg, dy.data(), (size_t)(B * n_out_) * 4));
+        ck(sili_memcpy_h2d_ordered(L_, dx, stage(x.data(), (size_t)(B * n_in_) * 4), (size_t)(B * n_in_) * 4));
+        ck(sili_memcpy_h2d_ordered(L_, dg, stage(dy.data(), (size_t)(B * n_out_) * 4), (size_t)(B * n_out_) * 4));
         float *gs = (float *)gws_.get((size_t)i.nnz_scattered * 4 + 4);
         float *gb = (float *)gwb_.get((size_t)i.n_tiles * 64 + 4);
         ck(sili_sampled_gradw(L_, dx, dg, B, gs, gb, nullptr));
@@ -441,6 +451,7 @@ class Layer {
         py::array_t<float> b = host_array({(py::ssize_t)(i.n_tiles * 16)}, &hb);
         ck(sili_memcpy_d2h_ordered(L_, ha, gs, (size_t)i.nnz_scattered * 4));
         ck(sili_memcpy_d2h_ordered(L_, hb, gb, (size_t)i.n_tiles * 64));
+        release_staged();
         return py::make_tuple(a, b);
     }
 
@@ -463,7 +474,7 @@ class Layer {
         if (x.size() != batch * n_in_) throw py::value_error("x must be [batch, n_inputs]");
         check_csr(dptrs, didx, dvals, batch, n_out_);
         float *dxin = (float *)xs_.get((size_t)(batch * n_in_) * 4);
-        ck(sili_memcpy_h2d_ordered(L_, dxin, x.data(), (size_t)(batch * n_in_) * 4));
+        ck(sili_memcpy_h2d_ordered(L_, dxin, stage(x.data(), (size_t)(batch * n_in_) * 4), (size_t)(batch * n_in_) * 4));
         int32_t *dp = upload_i32(p_, dptrs);
         int32_t *di = upload_i32(i_, didx);
         float *dv = upload_f32(v_, dvals);
@@ -733,6 +744,7 @@ class Layer {
     bool dirty_vs_ = false, dirty_os_ = false, dirty_is_ = false, dirty_ois_ = false;
     int64_t last_batch_ = 0;
     DBuf last_x_, xs_, y_, g_, dx_, p_, i_, v_, gws_, gwb_;
+    std::vector<void *> staged_;  // pool blocks that queued uploads read
 
     std::vector<DBuf *> bufs() { return {&last_x_, &xs_, &y_, &g_, &dx_, &p_, &i_, &v_, &gws_, &gwb_}; }
 
@@ -772,19 +784,39 @@ class Layer {
     // host copy, which waits for the stream, while its arguments are alive)
     int32_t *upload_i32(DBuf &b, const carr<int32_t> &a) {
         void *d = b.get((size_t)a.size() * 4 + 4);
-        ck(sili_memcpy_h2d_ordered(L_, d, a.data(), (size_t)a.size() * 4));
+        ck(sili_memcpy_h2d_ordered(L_, d, stage(a.data(), (size_t)a.size() * 4), (size_t)a.size() * 4));
         return (int32_t *)d;
     }
     float *upload_f32(DBuf &b, const carr<float> &a) {
         void *d = b.get((size_t)a.size() * 4 + 4);
-        ck(sili_memcpy_h2d_ordered(L_, d, a.data(), (size_t)a.size() * 4));
+        ck(sili_memcpy_h2d_ordered(L_, d, stage(a.data(), (size_t)a.size() * 4), (size_t)a.size() * 4));
         return (float *)d;
     }
     py::array_t<float> fetch(const float *d, int64_t B, int64_t n) {
         float *h = nullptr;
         py::array_t<float> r = host_array({(py::ssize_t)B, (py::ssize_t)n}, &h);
         ck(sili_memcpy_d2h_ordered(L_, h, d, (size_t)(B * n) * 4));
+        release_staged();
         return r;
+    }
+    // The host source of an upload: an array of this module's pool as it is
+    // (page-locked: one copy kernel reads it), else, from 64 KiB up, a copy in
+    // a page-locked block of the pool (a CPU copy of a few tens of us per
+    // 2 MiB, where the runtime's staged copy of pageable memory took 0.08 ms
+    // and, on streams where its DMA runs slow, 0.3 ms).  The block is held
+    // until a wait for the layer's stream (release_staged).
+    const void *stage(const void *src, size_t bytes) {
+        if (bytes < (size_t(64) << 10) || PinnedPool::get().owns(src, bytes)) return src;
+        void *p = PinnedPool::get().take(bytes);
+        if (!p) return src;
+        std::memcpy(p, src, bytes);
+        staged_.push_back(p);
+        return p;
+    }
+    // after a wait for the layer's stream: the staged blocks go back
+    void release_staged() {
+        for (void *p : staged_) PinnedPool::get().give(p);
+        staged_.clear();
     }
 };
 

@@ -65,3 +65,32 @@ def test_blocks_reused_after_arrays_die(hip):
     assert len({a.ctypes.data for a in live}) == 8
     for a in live:
         assert np.array_equal(a, want)
+
+
+def test_interior_and_staged_inputs(hip):
+    """Inputs that start inside a returned (page-locked) array, at 4- and
+    16-byte offsets, and ordinary numpy inputs above the 64 KiB staging size
+    give the bytes a plain copy of them gives, on every path that uploads."""
+    wl = make_config(1, scale=0.125, batch=16)
+    assert wl.n_in == wl.n_out
+    L = gpu_layer(hip, wl)
+    big = L.forward_dense(np.concatenate([wl.x, wl.x]))  # 32 rows, page-locked
+    flat = big.reshape(-1)
+    n = wl.n_in
+    for off in (1, 4, n):
+        xin = flat[off:off + 16 * n].reshape(16, n)
+        assert not xin.flags.owndata
+        y_a = L.forward_dense(xin)
+        y_b = L.forward_dense(np.array(xin, copy=True))
+        assert np.array_equal(y_a, y_b), off
+        # (split rows add their partial sums atomically: same values to 1e-6)
+        dx_a = L.backward_dense(xin, 0.0)
+        dx_b = L.backward_dense(np.array(xin, copy=True), 0.0)
+        np.testing.assert_allclose(dx_a, dx_b, rtol=1e-6, atol=0, err_msg=str(off))
+        gs_a, gb_a = L.sampled_gradw(xin, xin)
+        gs_b, gb_b = L.sampled_gradw(np.array(xin), np.array(xin))
+        np.testing.assert_allclose(gs_a, gs_b, rtol=1e-6, atol=0, err_msg=str(off))
+        np.testing.assert_allclose(gb_a, gb_b, rtol=1e-6, atol=0, err_msg=str(off))
+    H = host_layer(wl)
+    y = L.forward_dense(wl.x)
+    assert_close_terms(y, H.forward_dense(wl.x), H.forward_dense(wl.x, absmode=True), "forward")

@@ -266,3 +266,54 @@ def test_capi_profiler_names_and_counts(api):
             api.ck(api.L.sili_device_free(h, p))
     finally:
         api.L.sili_destroy(h)
+
+
+@pytest.mark.parametrize("offset", [0, 1, 4, 12])
+def test_capi_ordered_copies_page_locked(api, offset):
+    """sili_memcpy_h2d_ordered / _d2h_ordered between device memory and
+    page-locked host memory (sili_host_alloc) run as a copy kernel on the
+    layer's stream: every byte arrives for sizes with 16-, 4- and 1-byte
+    tails at 16-, 4- and 1-byte host offsets; pageable memory takes the
+    runtime's copy and gives the same bytes."""
+    vp = C.c_void_p
+    L = api.L
+    L.sili_host_alloc.argtypes = [C.c_size_t, C.POINTER(vp)]
+    L.sili_host_free.argtypes = [vp]
+    L.sili_memcpy_h2d_ordered.argtypes = [vp, vp, vp, C.c_size_t]
+    L.sili_memcpy_d2h_ordered.argtypes = [vp, vp, vp, C.c_size_t]
+    h = vp()
+    api.ck(L.sili_create(64, 64, 16, 0, C.byref(h)))
+    cap = (3 << 20) + 64
+    hp, dv = vp(), vp()
+    try:
+        api.ck(L.sili_host_alloc(cap, C.byref(hp)))
+        api.ck(L.sili_device_alloc(h, cap, C.byref(dv)))
+        host = np.ctypeslib.as_array(C.cast(hp, C.POINTER(C.c_uint8)), shape=(cap,))
+        rng = np.random.default_rng(7 + offset)
+        for nbytes in (1, 3, 17, 64, 1000, 65536 + 5, (2 << 20) + 13, 3 << 20):
+            src = rng.integers(0, 256, nbytes, dtype=np.uint8)
+            host[:] = 0
+            host[offset:offset + nbytes] = src
+            api.ck(L.sili_memcpy_h2d_ordered(h, dv, hp.value + offset, nbytes))
+            # back through pageable memory (the runtime's copy) ...
+            back = np.zeros(nbytes, np.uint8)
+            api.ck(L.sili_memcpy_d2h_ordered(h, _ptr(back), dv, nbytes))
+            assert np.array_equal(back, src), nbytes
+            # ... and through the page-locked block at another offset
+            host[:] = 0
+            o2 = (offset + 3) % 16
+            api.ck(L.sili_memcpy_d2h_ordered(h, hp.value + o2, dv, nbytes))
+            assert np.array_equal(host[o2:o2 + nbytes], src), nbytes
+            assert not host[:o2].any() and not host[o2 + nbytes:].any(), nbytes
+            # pageable source, page-locked destination
+            src2 = src[::-1].copy()
+            api.ck(L.sili_memcpy_h2d_ordered(h, dv, _ptr(src2), nbytes))
+            api.ck(L.sili_memcpy_d2h_ordered(h, hp.value, dv, nbytes))
+            assert np.array_equal(host[:nbytes], src2), nbytes
+        del host
+    finally:
+        if dv.value:
+            L.sili_device_free(h, dv)
+        if hp.value:
+            L.sili_host_free(hp)
+        L.sili_destroy(h)
