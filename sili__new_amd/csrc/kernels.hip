@@ -1901,15 +1901,16 @@ __global__ __launch_bounds__(256) void k_sddmm_b4_v4(SBArgs a, uint32_t gT_bytes
                 for (int k = 0; k < KB; ++k) gv[k] = buffer_load_f4(rg, off + (uint32_t)lj * ld_bytes + lane_off[k]);
 #pragma unroll
                 for (int li = 0; li < 4; ++li) {
-                    float d0 = 0.f, d1 = 0.f;
+                    // one chain per slot (16 independent chains per lane)
+                    float d0 = 0.f;
 #pragma unroll
                     for (int k = 0; k < KB; ++k) {
                         d0 = __builtin_fmaf(xr[li][k].x, gv[k].x, d0);
-                        d1 = __builtin_fmaf(xr[li][k].y, gv[k].y, d1);
+                        d0 = __builtin_fmaf(xr[li][k].y, gv[k].y, d0);
                         d0 = __builtin_fmaf(xr[li][k].z, gv[k].z, d0);
-                        d1 = __builtin_fmaf(xr[li][k].w, gv[k].w, d1);
+                        d0 = __builtin_fmaf(xr[li][k].w, gv[k].w, d0);
                     }
-                    d[lj * 4 + li] = d0 + d1;
+                    d[lj * 4 + li] = d0;
                 }
             }
 #pragma unroll
@@ -1980,15 +1981,16 @@ __global__ __launch_bounds__(256) void k_sddmm_b4_rng(SRArgs a, uint32_t gT_byte
             for (int k = 0; k < KB; ++k) gv[k] = buffer_load_f4(rg, off + (uint32_t)lj * ld_bytes + lane_off[k]);
 #pragma unroll
             for (int li = 0; li < 4; ++li) {
-                float d0 = 0.f, d1 = 0.f;
+                // one chain per slot (16 independent chains per lane)
+                float d0 = 0.f;
 #pragma unroll
                 for (int k = 0; k < KB; ++k) {
                     d0 = __builtin_fmaf(xr[li][k].x, gv[k].x, d0);
-                    d1 = __builtin_fmaf(xr[li][k].y, gv[k].y, d1);
+                    d0 = __builtin_fmaf(xr[li][k].y, gv[k].y, d0);
                     d0 = __builtin_fmaf(xr[li][k].z, gv[k].z, d0);
-                    d1 = __builtin_fmaf(xr[li][k].w, gv[k].w, d1);
+                    d0 = __builtin_fmaf(xr[li][k].w, gv[k].w, d0);
                 }
-                d[lj * 4 + li] = d0 + d1;
+                d[lj * 4 + li] = d0;
             }
         }
 #pragma unroll

@@ -34,15 +34,18 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 // DPP lane moves (gfx9 encodings).  Lanes whose source falls outside the
 // row (or rows not selected by ROW_MASK) read 0.  Call with all lanes active.
+// (bound_ctrl set: an out-of-row source reads 0, the same as the old value 0
+// gives, and the compiler then needs no zeroed register per move.)
 template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xF, true);
 }
 template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ float dpp_f32(float x) {
     return __builtin_bit_cast(float, dpp_u32<CTRL, ROW_MASK>(__builtin_bit_cast(uint32_t, x)));
 }
 constexpr int DPP_ROW_SHR1 = 0x111, DPP_ROW_SHR2 = 0x112, DPP_ROW_SHR4 = 0x114, DPP_ROW_SHR8 = 0x118;
+constexpr int DPP_ROW_ROR1 = 0x121, DPP_ROW_ROR2 = 0x122, DPP_ROW_ROR4 = 0x124, DPP_ROW_ROR8 = 0x128;
 constexpr int DPP_ROW_BCAST15 = 0x142, DPP_ROW_BCAST31 = 0x143;
 
 // Inclusive prefix sum over the 64 lanes: Hillis-Steele inside each 16-lane
@@ -110,13 +113,16 @@ __device__ __forceinline__ uint32_t wave_prev_u32(uint32_t x) { return dpp_u32<0
 __device__ __forceinline__ float wave_prev_f32(float x) { return dpp_f32<0x138>(x); }
 
 // Sum over each aligned group of BL lanes (BL a power of two <= 64); the
-// group's total lands in its last lane (lane % BL == BL-1).
+// group's total lands in its last lane (lane % BL == BL-1).  Inside a row the
+// steps rotate (row_ror 1, 2, 4, 8): the last lane of a group adds the same
+// lanes in the same order as with row_shr, and since every lane has a source
+// each step is one v_add_f32 with DPP (row_shr:8 took a separate move).
 template <int BL>
 __device__ __forceinline__ float group_sum_last(float v) {
-    if constexpr (BL >= 2) v += dpp_f32<DPP_ROW_SHR1>(v);
-    if constexpr (BL >= 4) v += dpp_f32<DPP_ROW_SHR2>(v);
-    if constexpr (BL >= 8) v += dpp_f32<DPP_ROW_SHR4>(v);
-    if constexpr (BL >= 16) v += dpp_f32<DPP_ROW_SHR8>(v);
+    if constexpr (BL >= 2) v += dpp_f32<DPP_ROW_ROR1>(v);
+    if constexpr (BL >= 4) v += dpp_f32<DPP_ROW_ROR2>(v);
+    if constexpr (BL >= 8) v += dpp_f32<DPP_ROW_ROR4>(v);
+    if constexpr (BL >= 16) v += dpp_f32<DPP_ROW_ROR8>(v);
     if constexpr (BL >= 32) v += dpp_f32<DPP_ROW_BCAST15, 0xA>(v);
     if constexpr (BL >= 64) v += dpp_f32<DPP_ROW_BCAST31, 0xC>(v);
     return v;
