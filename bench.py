@@ -713,8 +713,10 @@ def run_config4(a, hip, api, rt):
 def run_index_decode(a, hip, api, rt):
     """Column decode of the config-4 q layer (5120 x 204800, ~105 M
     synapses): the ULEB128 stream (wave-parallel varint decode) against the
-    FOR index (every column = group start + offset).  Algorithmic bytes:
-    what each decoder must read plus 4 bytes written per column."""
+    FOR index (every column = group start + offset), the latter by its
+    lane-per-slot decoder ("for") and by its thread-per-group one.
+    Algorithmic bytes: what each decoder must read plus 4 bytes written per
+    column."""
     from sili__new_amd.synth import SEED0
     G = a.index_decode
     n_in, n_out = 5120, 204800
@@ -730,7 +732,7 @@ def run_index_decode(a, hip, api, rt):
     out = {"workload": f"config-4 q layer {n_in}x{n_out}, {nnz} synapses; decode every column",
            "group_size": G, "nnz": nnz, "index_bytes": info["index_bytes"], "for_bytes": for_bytes}
     ngroups = None
-    for use_for, name in ((0, "uleb"), (1, "for")):
+    for use_for, name in ((0, "uleb"), (1, "for"), (2, "for_thread_per_group")):
         for _ in range(3):
             api.ck(api.L.sili_decode_columns(h, cols, use_for, stream))
         rt.sync()

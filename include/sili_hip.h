@@ -505,9 +505,12 @@ int sili_build_for_index(sili_layer *layer, int group_size);
 int sili_export_for_index(sili_layer *layer, uint64_t *row_byte_start, uint8_t *bytes,
                           int64_t *nbytes);
 /* Every canonical column (int32, storage order) into device cols, decoded
- * from the FOR index (use_for_index != 0) or from the ULEB128 stream
- * (DeltaCSRRowCursor, delta_csr_types.hpp:801-832); profiled as
- * "index:for" / "index:decode". */
+ * from the ULEB128 stream (use_for_index 0; DeltaCSRRowCursor,
+ * delta_csr_types.hpp:801-832) or from the FOR index: 1, one lane per slot
+ * with the wave's group bytes loaded as coalesced dwords; 2, one thread per
+ * group (G 8 and 16) or one thread per slot with byte loads (G 32 and 64), kept
+ * for comparison.  Other values: SILI_ERR_INVALID.  Profiled as "index:for" /
+ * "index:uleb". */
 int sili_decode_columns(sili_layer *layer, int32_t *cols, int use_for_index, void *stream);
 
 /* ---- module utilities (device buffers; synchronous on `stream`) -----------

@@ -1772,7 +1772,8 @@ int sili_decode_columns(sili_layer *layer, int32_t *cols, int use_for_index, voi
         set_device(layer->L);
         if (!cols && layer->L.W.nnz > 0) throw_error(SILI_ERR_INVALID, "cols is NULL");
         ProfCtx pc(layer->L, "index");
-        decode_columns(layer->L, cols, use_for_index != 0, pick(layer->L, stream));
+        if (use_for_index < 0 || use_for_index > 2) throw_error(SILI_ERR_INVALID, "use_for_index must be 0, 1 or 2");
+        decode_columns(layer->L, cols, use_for_index, pick(layer->L, stream));
     });
 }
 

@@ -151,6 +151,47 @@ __global__ __launch_bounds__(TPB) void k_for_decode_tg(const uint8_t *__restrict
     }
 }
 
+// Decode, one wave per 64 / G groups and one lane per slot.  The wave's
+// groups are contiguous in the byte stream: at most 64/G * (1 + 4G) bytes
+// (267 with the alignment), so lane l loads the aligned dwords D0 + l and
+// D0 + 64 + l once, coalesced (indices clamped to the buffer; the clamped
+// words are never selected for a byte in use).  Each lane then takes the two
+// dwords that hold its offset from the lanes that loaded them (__shfl), and
+// realigns them to its byte.  The group's tier byte and its three index words
+// are per-lane loads that the wave's lanes share (4 addresses per wave at G =
+// 16).  G from 8 to 64.
+template <uint32_t G>
+__global__ __launch_bounds__(TPB) void k_for_decode_wave(const uint8_t *__restrict__ bytes, uint32_t ndw,
+                                                         const uint32_t *__restrict__ group_pos,
+                                                         const uint32_t *__restrict__ group_base,
+                                                         const uint32_t *__restrict__ group_elem, uint32_t ngroups,
+                                                         int32_t *__restrict__ cols) {
+    constexpr uint32_t GPW = 64u / G;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t g0 = ((blockIdx.x * TPB + threadIdx.x) >> 6) * GPW;
+    if (g0 >= ngroups) return;  // the whole wave
+    const uint32_t g = g0 + lane / G, k = lane % G;
+    const bool gv = g < ngroups;
+    const uint32_t gg = gv ? g : g0;
+    const uint32_t pos = group_pos[gg], base = group_base[gg], e0 = group_elem[gg];
+    const uint32_t n = group_elem[gg + 1] - e0;
+    const uint32_t pos0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)pos);  // lane 0: group g0
+    const uint32_t D0 = pos0 >> 2;
+    const uint32_t *dw = reinterpret_cast<const uint32_t *>(bytes);
+    const uint32_t wa = dw[min(D0 + lane, ndw - 1u)], wb = dw[min(D0 + 64u + lane, ndw - 1u)];
+    const uint32_t tier = bytes[pos];
+    const uint32_t w = tier == 0u ? 1u : (tier == 1u ? 2u : 4u);
+    const uint32_t rb = pos - 4u * D0 + 1u + k * w;  // this slot's first byte, from the window's start
+    const uint32_t di = rb >> 2;                     // < 67
+    const uint32_t la = (uint32_t)__shfl((int)wa, (int)(di & 63u), 64), lb = (uint32_t)__shfl((int)wb, (int)(di & 63u), 64);
+    const uint32_t ha = (uint32_t)__shfl((int)wa, (int)((di + 1u) & 63u), 64),
+                   hb = (uint32_t)__shfl((int)wb, (int)((di + 1u) & 63u), 64);
+    const uint32_t lo = di < 64u ? la : lb, hi = di + 1u < 64u ? ha : hb;
+    const uint32_t v = __builtin_amdgcn_alignbyte(hi, lo, rb & 3u);
+    const uint32_t off = w == 4u ? v : (v & ((1u << (8u * w)) - 1u));
+    if (gv && k < n) cols[e0 + k] = (int32_t)(base + off);
+}
+
 void scan_u32(const uint32_t *in, uint32_t *out, int64_t n, DevBuf<uint8_t> &temp, hipStream_t st) {
     size_t bytes = 0;
     SILI_HIP(rocprim::exclusive_scan(nullptr, bytes, in, out, uint32_t(0), (size_t)n, rocprim::plus<uint32_t>(), st));
@@ -208,7 +249,7 @@ void build_for_index(Layer &L, int G) {
     F.valid = true;
 }
 
-void decode_columns(Layer &L, int32_t *cols, bool use_for, hipStream_t st) {
+void decode_columns(Layer &L, int32_t *cols, int use_for, hipStream_t st) {
     DScatter &W = L.W;
     if (W.nnz == 0) return;
     if (!use_for) {
@@ -226,6 +267,21 @@ void decode_columns(Layer &L, int32_t *cols, bool use_for, hipStream_t st) {
                *ge = (const uint32_t *)F.group_elem.p;
     const dim3 grid(nblk(nslots));
     const dim3 ggrid(nblk(F.ngroups));
+    if (use_for == 1) {
+        // one lane per slot, the group bytes by coalesced dword loads
+        const uint32_t ndw = (uint32_t)(F.bytes.n / 4);
+        const int64_t waves = (F.ngroups + 64 / F.G - 1) / (64 / F.G);
+        const dim3 wgrid((unsigned)((waves + TPB / 64 - 1) / (TPB / 64)));
+        switch (F.G) {
+            case 8: launch(k_for_decode_wave<8>, wgrid, dim3(TPB), 0, st, bp, ndw, gp, gb, ge, (uint32_t)F.ngroups, cols); break;
+            case 16: launch(k_for_decode_wave<16>, wgrid, dim3(TPB), 0, st, bp, ndw, gp, gb, ge, (uint32_t)F.ngroups, cols); break;
+            case 32: launch(k_for_decode_wave<32>, wgrid, dim3(TPB), 0, st, bp, ndw, gp, gb, ge, (uint32_t)F.ngroups, cols); break;
+            default: launch(k_for_decode_wave<64>, wgrid, dim3(TPB), 0, st, bp, ndw, gp, gb, ge, (uint32_t)F.ngroups, cols); break;
+        }
+        SILI_HIP(hipGetLastError());
+        return;
+    }
+    // use_for == 2: one thread per group (G 8, 16) or per slot with byte loads
     switch (F.G) {
         case 8: launch(k_for_decode_tg<8>, ggrid, dim3(TPB), 0, st, bp, gp, gb, ge, (uint32_t)F.ngroups, cols); break;
         case 16: launch(k_for_decode_tg<16>, ggrid, dim3(TPB), 0, st, bp, gp, gb, ge, (uint32_t)F.ngroups, cols); break;

@@ -546,7 +546,7 @@ void launch_push_fwd(Layer &L, const int32_t *xptrs, const int32_t *xidx, const 
                      const ScaleView &sc, float *y, bool add, hipStream_t st);
 
 void build_for_index(Layer &L, int G);
-void decode_columns(Layer &L, int32_t *cols, bool use_for, hipStream_t st);
+void decode_columns(Layer &L, int32_t *cols, int use_for, hipStream_t st);
 
 // Block4 tile encoding (tile_enc.hip): re-encode tiles by their live count
 // (all, or those with dirty[t] != 0); the tiles a sparse-gradient update

@@ -708,13 +708,13 @@ class Layer {
         d["bytes"] = b;
         return d;
     }
-    py::array_t<int32_t> decode_columns(bool use_for_index) {
+    py::array_t<int32_t> decode_columns(int use_for_index) {
         sili_info i;
         ck(sili_get_info(L_, &i));
         py::array_t<int32_t> c((py::ssize_t)i.nnz_scattered);
         if (i.nnz_scattered == 0) return c;
         int32_t *d = (int32_t *)dx_.get((size_t)i.nnz_scattered * 4);
-        ck(sili_decode_columns(L_, d, use_for_index ? 1 : 0, nullptr));
+        ck(sili_decode_columns(L_, d, use_for_index, nullptr));
         ck(sili_memcpy_d2h(L_, c.mutable_data(), d, (size_t)i.nnz_scattered * 4));
         return c;
     }
@@ -1003,7 +1003,7 @@ PYBIND11_MODULE(_sili_hip, m) {
         .def("export_block4_packed", &Layer::export_block4_packed)
         .def_property_readonly("block4", py::cpp_function(&Layer::block4, py::keep_alive<0, 1>()))
         .def("export_for_index", &Layer::export_for_index)
-        .def("decode_columns", &Layer::decode_columns, py::arg("use_for_index") = true)
+        .def("decode_columns", &Layer::decode_columns, py::arg("use_for_index") = 1)
         .def("synchronize", &Layer::synchronize)
         .def_property_readonly("handle", &Layer::handle)
         .def_property_readonly("n_inputs", &Layer::n_inputs)

@@ -29,8 +29,9 @@ def _check(L, ptrs, cols, G, what):
     rs, b = oracle.for_encode_rows(ptrs, cols, G)
     assert np.array_equal(ex["row_byte_start"], rs), what + ": row starts"
     assert np.array_equal(ex["bytes"], b), what + ": bytes"
-    assert np.array_equal(L.decode_columns(True), cols), what + ": FOR decode"
-    assert np.array_equal(L.decode_columns(False), cols), what + ": ULEB decode"
+    assert np.array_equal(L.decode_columns(1), cols), what + ": FOR decode (lane per slot)"
+    assert np.array_equal(L.decode_columns(2), cols), what + ": FOR decode (thread per group)"
+    assert np.array_equal(L.decode_columns(0), cols), what + ": ULEB decode"
 
 
 @pytest.mark.parametrize("G", [8, 16, 32, 64])
