@@ -171,6 +171,11 @@ __global__ void k_gather_u32(const uint32_t *__restrict__ src, const uint32_t *_
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (i < N) dst[i] = src[perm[i]];
 }
+__global__ void k_gather_u64(const uint64_t *__restrict__ src, const uint32_t *__restrict__ perm,
+                             int64_t N, uint64_t *__restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < N) dst[i] = src[perm[i]];
+}
 __global__ void k_gather_u8(const uint8_t *__restrict__ src, const uint32_t *__restrict__ perm,
                             int64_t N, uint8_t *__restrict__ dst) {
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
@@ -179,6 +184,107 @@ __global__ void k_gather_u8(const uint8_t *__restrict__ src, const uint32_t *__r
 __global__ void k_iota(uint32_t *__restrict__ v, int64_t N) {
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (i < N) v[i] = (uint32_t)i;
+}
+
+// ---- ordering entries by (major, minor), keys unique --------------------
+// A counting pass by major (atomics), an exclusive scan into each major's
+// first position, a scatter into the majors' segments (arbitrary order within
+// a segment), then each segment ordered by minor: one wave per segment, a
+// bitonic network over the wave's lanes (up to 64 entries) or in the wave's
+// LDS slice (up to SEGSORT_CAP).  The order within a segment is unique since
+// the keys are, so the result equals a sort of the keys.  About five launches
+// where a device radix sort of a few hundred thousand keys took about twenty.
+constexpr uint32_t SEGSORT_CAP = 2048;
+constexpr uint32_t SEGSORT_WAVES = 4;
+
+__global__ void k_fill_u32_b(uint32_t *__restrict__ p, int64_t n, uint32_t v) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+__global__ void k_count_major(const uint32_t *__restrict__ maj, int64_t N, int64_t maj_ext,
+                              uint32_t *__restrict__ cnt, int *__restrict__ bad) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= N) return;
+    const uint32_t m = maj[i];
+    if ((int64_t)m >= maj_ext) {
+        atomicOr(bad, 1);
+        return;
+    }
+    atomicAdd(cnt + m, 1u);
+}
+
+// cnt (the counts) is consumed: each entry takes position ptr[m] + (its
+// count after the decrement).
+__global__ void k_scatter_major(const uint32_t *__restrict__ maj, const uint32_t *__restrict__ mnr, int64_t N,
+                                int64_t maj_ext, const uint32_t *__restrict__ ptr, uint32_t *__restrict__ cnt,
+                                uint32_t *__restrict__ seg_mnr, uint32_t *__restrict__ seg_idx) {
+    const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
+    if (i >= N) return;
+    const uint32_t m = maj[i];
+    if ((int64_t)m >= maj_ext) return;
+    const uint32_t p = ptr[m] + atomicSub(cnt + m, 1u) - 1u;
+    seg_mnr[p] = mnr[i];
+    seg_idx[p] = (uint32_t)i;
+}
+
+// perm[p] for every position of segment m (one wave per segment); a segment
+// longer than SEGSORT_CAP sets *too_long and is left unsorted.
+__global__ __launch_bounds__(SEGSORT_WAVES * 64) void k_seg_sort_minor(const uint32_t *__restrict__ ptr, int64_t nseg,
+                                                                      const uint32_t *__restrict__ seg_mnr,
+                                                                      const uint32_t *__restrict__ seg_idx,
+                                                                      uint32_t *__restrict__ perm,
+                                                                      int *__restrict__ too_long) {
+    __shared__ uint2 s[SEGSORT_WAVES][SEGSORT_CAP];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const int64_t m = (int64_t)blockIdx.x * SEGSORT_WAVES + wave;
+    if (m >= nseg) return;
+    const uint32_t b = ptr[m], len = ptr[m + 1] - b;
+    if (len <= 1u) {
+        if (len == 1u && lane == 0) perm[b] = seg_idx[b];
+        return;
+    }
+    if (len <= 64u) {
+        // bitonic network over the lanes; padding sorts last (minor < 2^32 - 1)
+        uint32_t key = lane < len ? seg_mnr[b + lane] : 0xFFFFFFFFu;
+        uint32_t idx = lane < len ? seg_idx[b + lane] : 0u;
+        for (uint32_t k = 2; k <= 64u; k <<= 1)
+            for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+                const uint32_t ok = (uint32_t)__shfl_xor((int)key, (int)j, 64);
+                const uint32_t oi = (uint32_t)__shfl_xor((int)idx, (int)j, 64);
+                const bool up = (lane & k) == 0u, lower = (lane & j) == 0u;
+                if (lower == up ? ok < key : ok > key) {
+                    key = ok;
+                    idx = oi;
+                }
+            }
+        if (lane < len) perm[b + lane] = idx;
+        return;
+    }
+    if (len > SEGSORT_CAP) {
+        if (lane == 0) atomicOr(too_long, 1);
+        return;
+    }
+    uint32_t n2 = 128;
+    while (n2 < len) n2 <<= 1;
+    uint2 *t = s[wave];
+    for (uint32_t q = lane; q < n2; q += 64u)
+        t[q] = q < len ? make_uint2(seg_mnr[b + q], seg_idx[b + q]) : make_uint2(0xFFFFFFFFu, 0u);
+    wave_lds_sync();
+    for (uint32_t k = 2; k <= n2; k <<= 1)
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            for (uint32_t q = lane; q < n2 / 2u; q += 64u) {
+                const uint32_t lo = (q / j) * 2u * j + (q % j), hi = lo + j;
+                const bool up = (lo & k) == 0u;
+                const uint2 x = t[lo], y = t[hi];
+                if (up ? x.x > y.x : x.x < y.x) {
+                    t[lo] = y;
+                    t[hi] = x;
+                }
+            }
+            wave_lds_sync();
+        }
+    for (uint32_t q = lane; q < len; q += 64u) perm[b + q] = t[q].y;
 }
 
 // Block4: key = major * minor_extent + minor.
@@ -413,6 +519,42 @@ static void device_merge_pairs_u64(Layer &L, const uint64_t *k1, const uint64_t 
                             rocprim::less<uint64_t>(), L.stream));
 }
 
+// perm[p]: the entry at position p when the N entries are ordered by
+// (major, minor) (keys unique); ptr[0, maj_ext]: each major's first position
+// (ptr[maj_ext] = N).  A major out of range sets *bad |= 1; *bad is read back
+// here and, if set, raised as `what`'s malformed-input error.  False, with
+// nothing usable written, when a major holds more than SEGSORT_CAP entries:
+// the caller sorts the keys instead.  One wait on the stream.
+static bool sort_major_minor(Layer &L, const uint32_t *maj, const uint32_t *mnr, int64_t N, int64_t maj_ext,
+                             uint32_t *perm, uint32_t *ptr, int *bad, const char *what) {
+    hipStream_t st = L.stream;
+    TmpBuf<uint32_t> cnt(L, SILI_TMPKEY(mm_cnt)), smn(L, SILI_TMPKEY(mm_mnr)), sidx(L, SILI_TMPKEY(mm_idx));
+    TmpBuf<int> flag(L, SILI_TMPKEY(mm_flag));
+    cnt.ensure((size_t)maj_ext + 1);
+    smn.ensure((size_t)N + 1);
+    sidx.ensure((size_t)N + 1);
+    flag.ensure(1);
+    launch(k_fill_u32_b, dim3(nblk(maj_ext + 1)), dim3(TPB), 0, st, cnt.p, maj_ext + 1, 0u);
+    launch(k_fill_u32_b, dim3(1), dim3(TPB), 0, st, reinterpret_cast<uint32_t *>(flag.p), (int64_t)1, 0u);
+    if (N > 0) launch(k_count_major, dim3(nblk(N)), dim3(TPB), 0, st, maj, N, maj_ext, cnt.p, bad);
+    device_exclusive_scan_u32(L, cnt.p, ptr, maj_ext + 1);
+    if (N > 0) {
+        launch(k_scatter_major, dim3(nblk(N)), dim3(TPB), 0, st, maj, mnr, N, maj_ext, (const uint32_t *)ptr, cnt.p,
+               smn.p, sidx.p);
+        launch(k_seg_sort_minor, dim3((unsigned)((maj_ext + SEGSORT_WAVES - 1) / SEGSORT_WAVES)),
+               dim3(SEGSORT_WAVES * 64), 0, st, (const uint32_t *)ptr, maj_ext, (const uint32_t *)smn.p,
+               (const uint32_t *)sidx.p, perm, flag.p);
+    }
+    SILI_HIP(hipGetLastError());
+    int h = 0, hb = 0;
+    ReadBack rb(L);
+    rb.add(&h, flag.p, sizeof(int));
+    rb.add(&hb, bad, sizeof(int));
+    rb.wait();
+    if (hb) throw_error(1, std::string(what) + ": malformed input (unsorted, duplicate or out-of-range index)");
+    return h == 0;
+}
+
 static int bits_for(uint64_t max_value) {
     int b = 1;
     while (b < 64 && (max_value >> b) != 0) ++b;
@@ -557,18 +699,27 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
     trows.ensure((size_t)N + 1);
     tbytes.ensure((size_t)N + 1);
     ptrs.ensure((size_t)src.cols + 1);
-    if (N > 0) {
+    // by (column, row): the canonical entries are in (row, column) order, so
+    // this is the stable order by column (SILI_SEGSORT=0: a device radix sort)
+    zero_flag(L);
+    const bool counted = env_int("SILI_SEGSORT", 1) &&
+                         sort_major_minor(L, d_cols, d_rows, N, src.cols, perm.p, ptrs.p, L.scratch.flag.p,
+                                          "shadow build");
+    if (!counted && N > 0) {
         launch(k_iota, dim3(nblk(N)), dim3(TPB), 0, st, perm_in.p, N);
-        // stable by column: entries keep ascending row order within a column
         device_sort_pairs_u32(L, d_cols, keys_out.p, perm_in.p, perm.p, N,
                               bits_for((uint64_t)std::max<int64_t>(src.cols - 1, 1)));
+    }
+    if (N > 0) {
         launch(k_gather_u32, dim3(nblk(N)), dim3(TPB), 0, st, d_rows, perm.p, N, trows.p);
         launch(k_gather_u8, dim3(nblk(N)), dim3(TPB), 0, st, src.val.p, perm.p, N, tbytes.p);
         SILI_HIP(hipGetLastError());
     }
-    launch(k_ptrs_from_sorted, dim3(nblk(src.cols + 1)), dim3(TPB), 0, st, keys_out.p, N,
-                       src.cols, ptrs.p);
-    SILI_HIP(hipGetLastError());
+    if (!counted) {
+        launch(k_ptrs_from_sorted, dim3(nblk(src.cols + 1)), dim3(TPB), 0, st, keys_out.p, N,
+                           src.cols, ptrs.p);
+        SILI_HIP(hipGetLastError());
+    }
     const Encoded e = encode_rows(L, src.cols, src.rows, N, ptrs.p, trows.p, L.seg_len, true, dst.byte_start,
                                   dst.elem_start, dst.idx, dst.seg, "shadow build", &dst.split_rows);
     dst.n_split = e.n_split;
@@ -793,7 +944,7 @@ void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_
     const int64_t N = n_tiles;
     TmpBuf<uint64_t> key(L, SILI_TMPKEY(key)), key_sorted(L, SILI_TMPKEY(key_sorted));
     TmpBuf<uint32_t> perm_in(L, SILI_TMPKEY(perm_in)), perm(L, SILI_TMPKEY(perm)), major(L, SILI_TMPKEY(major)), minor(L, SILI_TMPKEY(minor));
-    TmpBuf<uint32_t> inv(L, SILI_TMPKEY(inv));
+    TmpBuf<uint32_t> inv(L, SILI_TMPKEY(inv)), mptr(L, SILI_TMPKEY(mptr));
     key.ensure((size_t)N + 1);
     key_sorted.ensure((size_t)N + 1);
     perm_in.ensure((size_t)N + 1);
@@ -811,14 +962,21 @@ void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_
                                (uint64_t)mnr_ext, maj_ext, key.p, L.scratch.flag.p);
             launch(k_iota, dim3(nblk(N)), dim3(TPB), 0, st, perm_in.p, N);
             SILI_HIP(hipGetLastError());
-            if (canon && sorted_head >= 0 && sorted_head <= N)
+            if (canon && sorted_head >= 0 && sorted_head <= N) {
                 // two runs already in canonical order: merged, not sorted
                 // (k_split_keys flags a merge whose runs were not)
                 device_merge_pairs_u64(L, key.p, key.p + sorted_head, key_sorted.p, perm_in.p,
                                        perm_in.p + sorted_head, perm.p, sorted_head, N - sorted_head);
-            else
+            } else if (env_int("SILI_SEGSORT", 1) &&
+                       (mptr.ensure((size_t)maj_ext + 1),
+                        sort_major_minor(L, maj, mnr, N, maj_ext, perm.p, mptr.p, L.scratch.flag.p, "block4 tiles"))) {
+                // counted by major, each major's tiles ordered by minor
+                launch(k_gather_u64, dim3(nblk(N)), dim3(TPB), 0, st, (const uint64_t *)key.p, (const uint32_t *)perm.p,
+                       N, key_sorted.p);
+            } else {
                 device_sort_pairs_u64(L, key.p, key_sorted.p, perm_in.p, perm.p, N,
                                       bits_for((uint64_t)maj_ext * (uint64_t)mnr_ext));
+            }
             launch(k_split_keys, dim3(nblk(N)), dim3(TPB), 0, st, key_sorted.p, N,
                                (uint64_t)mnr_ext, major.p, minor.p, L.scratch.flag.p);
             SILI_HIP(hipGetLastError());
