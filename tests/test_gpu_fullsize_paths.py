@@ -123,6 +123,28 @@ def test_config3_synapto_tile_merge_equals_sort(hip, c3, monkeypatch):
         assert np.array_equal(La._store_digest(), Lb._store_digest()), f"step {i}"
 
 
+def test_config3_synapto_segment_order_equals_sort(hip, c3, monkeypatch):
+    """The shadow builds order entries by a count per major and a per-segment
+    network (SILI_SEGSORT, the default); SILI_SEGSORT=0 sorts the keys.  The
+    load and three bulk steps give identical stores either way."""
+    wl = c3
+    monkeypatch.setenv("SILI_SEGSORT", "1")
+    La = _c3_synapto_layer(hip, wl)
+    monkeypatch.setenv("SILI_SEGSORT", "0")
+    Lb = _c3_synapto_layer(hip, wl)
+    assert np.array_equal(La._store_digest(), Lb._store_digest()), "load"
+    for i in range(3):
+        cr, cc, cv = _bench_candidates(wl, i)
+        monkeypatch.setenv("SILI_SEGSORT", "1")
+        sa = La.synapto_step(0.01, cr, cc, cv)
+        monkeypatch.setenv("SILI_SEGSORT", "0")
+        sb = Lb.synapto_step(0.01, cr, cc, cv)
+        assert sa == sb, i
+        assert sa["n_scattered"] > 0, sa
+        assert np.array_equal(La._store_digest(), Lb._store_digest()), f"step {i}"
+    monkeypatch.delenv("SILI_SEGSORT")
+
+
 def _exported(L, n_in, n_out):
     ex = L.export_scattered()
     H = HostLayer(n_in, n_out).load_encoded(ex["row_byte_start"], ex["row_elem_start"], ex["idx"], ex["val"])
