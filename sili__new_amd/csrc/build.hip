@@ -228,6 +228,77 @@ __global__ void k_scatter_major(const uint32_t *__restrict__ maj, const uint32_t
     seg_idx[p] = (uint32_t)i;
 }
 
+// The same two passes with each block's share counted in LDS first, for at
+// most MM_BINS majors: one global atomic per (block, major present) instead
+// of one per entry, which matters when few majors take many entries each
+// (a block4 store's 4096 block columns of ~127 tiles).  Each block takes
+// MM_CHUNK consecutive entries, MM_PER = MM_CHUNK / 256 per thread.
+constexpr uint32_t MM_BINS = 8192, MM_PER = 32, MM_CHUNK = 256 * MM_PER;
+
+__global__ __launch_bounds__(256) void k_count_major_lds(const uint32_t *__restrict__ maj, int64_t N,
+                                                         int64_t maj_ext, uint32_t *__restrict__ cnt,
+                                                         int *__restrict__ bad) {
+    __shared__ uint32_t h[MM_BINS];
+    for (uint32_t i = threadIdx.x; i < (uint32_t)maj_ext; i += 256u) h[i] = 0u;
+    __syncthreads();
+    const int64_t e0 = (int64_t)blockIdx.x * MM_CHUNK + threadIdx.x;
+#pragma unroll 4
+    for (uint32_t k = 0; k < MM_PER; ++k) {
+        const int64_t e = e0 + (int64_t)k * 256;
+        if (e < N) {
+            const uint32_t m = maj[e];
+            if ((int64_t)m >= maj_ext) atomicOr(bad, 1);
+            else atomicAdd(&h[m], 1u);
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < (uint32_t)maj_ext; i += 256u)
+        if (h[i]) atomicAdd(cnt + i, h[i]);
+}
+
+// Positions: an entry's rank among its block's entries of the same major (LDS
+// atomics), plus the block's base in the major's segment, taken from cnt (the
+// counts, consumed) by one atomic per major present.
+__global__ __launch_bounds__(256) void k_scatter_major_lds(const uint32_t *__restrict__ maj,
+                                                           const uint32_t *__restrict__ mnr, int64_t N,
+                                                           int64_t maj_ext, const uint32_t *__restrict__ ptr,
+                                                           uint32_t *__restrict__ cnt, uint32_t *__restrict__ seg_mnr,
+                                                           uint32_t *__restrict__ seg_idx) {
+    __shared__ uint32_t h[MM_BINS];
+    for (uint32_t i = threadIdx.x; i < (uint32_t)maj_ext; i += 256u) h[i] = 0u;
+    __syncthreads();
+    const int64_t e0 = (int64_t)blockIdx.x * MM_CHUNK + threadIdx.x;
+    uint32_t rk[MM_PER];
+#pragma unroll
+    for (uint32_t k = 0; k < MM_PER; ++k) {
+        const int64_t e = e0 + (int64_t)k * 256;
+        rk[k] = 0u;
+        if (e < N) {
+            const uint32_t m = maj[e];
+            if ((int64_t)m < maj_ext) rk[k] = atomicAdd(&h[m], 1u);
+        }
+    }
+    __syncthreads();
+    // h[m] becomes the block's first position in major m's segment
+    for (uint32_t i = threadIdx.x; i < (uint32_t)maj_ext; i += 256u) {
+        const uint32_t c = h[i];
+        if (c) h[i] = ptr[i] + atomicSub(cnt + i, c) - c;
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t k = 0; k < MM_PER; ++k) {
+        const int64_t e = e0 + (int64_t)k * 256;
+        if (e < N) {
+            const uint32_t m = maj[e];
+            if ((int64_t)m < maj_ext) {
+                const uint32_t p = h[m] + rk[k];
+                seg_mnr[p] = mnr[e];
+                seg_idx[p] = (uint32_t)e;
+            }
+        }
+    }
+}
+
 // perm[p] for every position of segment m (one wave per segment); a segment
 // longer than SEGSORT_CAP sets *too_long and is left unsorted.
 __global__ __launch_bounds__(SEGSORT_WAVES * 64) void k_seg_sort_minor(const uint32_t *__restrict__ ptr, int64_t nseg,
@@ -536,11 +607,18 @@ static bool sort_major_minor(Layer &L, const uint32_t *maj, const uint32_t *mnr,
     flag.ensure(1);
     launch(k_fill_u32_b, dim3(nblk(maj_ext + 1)), dim3(TPB), 0, st, cnt.p, maj_ext + 1, 0u);
     launch(k_fill_u32_b, dim3(1), dim3(TPB), 0, st, reinterpret_cast<uint32_t *>(flag.p), (int64_t)1, 0u);
-    if (N > 0) launch(k_count_major, dim3(nblk(N)), dim3(TPB), 0, st, maj, N, maj_ext, cnt.p, bad);
+    const bool lds = maj_ext <= (int64_t)MM_BINS;
+    const unsigned cgrid = (unsigned)((N + MM_CHUNK - 1) / MM_CHUNK);
+    if (N > 0 && lds) launch(k_count_major_lds, dim3(cgrid), dim3(256), 0, st, maj, N, maj_ext, cnt.p, bad);
+    else if (N > 0) launch(k_count_major, dim3(nblk(N)), dim3(TPB), 0, st, maj, N, maj_ext, cnt.p, bad);
     device_exclusive_scan_u32(L, cnt.p, ptr, maj_ext + 1);
     if (N > 0) {
-        launch(k_scatter_major, dim3(nblk(N)), dim3(TPB), 0, st, maj, mnr, N, maj_ext, (const uint32_t *)ptr, cnt.p,
-               smn.p, sidx.p);
+        if (lds)
+            launch(k_scatter_major_lds, dim3(cgrid), dim3(256), 0, st, maj, mnr, N, maj_ext, (const uint32_t *)ptr,
+                   cnt.p, smn.p, sidx.p);
+        else
+            launch(k_scatter_major, dim3(nblk(N)), dim3(TPB), 0, st, maj, mnr, N, maj_ext, (const uint32_t *)ptr,
+                   cnt.p, smn.p, sidx.p);
         launch(k_seg_sort_minor, dim3((unsigned)((maj_ext + SEGSORT_WAVES - 1) / SEGSORT_WAVES)),
                dim3(SEGSORT_WAVES * 64), 0, st, (const uint32_t *)ptr, maj_ext, (const uint32_t *)smn.p,
                (const uint32_t *)sidx.p, perm, flag.p);
