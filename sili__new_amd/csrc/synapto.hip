@@ -570,6 +570,309 @@ T read_back(const T *d, hipStream_t st) {
     return h;
 }
 
+// ---- 64-bit keys in order by (major, minor), with no wait on the host ------
+// The step's key sets are (row << 32 | col) pairs or window numbers
+// (block row * bcols + block col), with KEY_NONE for empty entries.  Rather
+// than a radix sort over all the key bits (two dozen launches for the final
+// set), the entries are counted per major, placed in their major's segment
+// (one atomic per run of equal majors in a wave), and each segment ordered
+// by (minor, entry index): one wave per segment, a bitonic
+// network over the lanes (up to 64) or in the wave's LDS (up to KO_CAP), and
+// for a longer segment one block on it in global memory.  Equal keys end up in
+// ascending entry index, as a stable sort leaves them.  KEY_NONE entries form
+// one more segment after every major, left in no particular order (the
+// step's readers skip them).  Six launches; nothing is read back.
+constexpr uint32_t KO_BINS = 16384 + 1024;
+// KO_CAP bounds the LDS network's segment (KO_WAVES * KO_CAP * 8 bytes of LDS
+// per block): at 2048 the 64 KiB block left 8 waves per CU, and the launch
+// over 16384 short segments took 25 us whatever their lengths.
+constexpr uint32_t KO_WAVES = 4, KO_CAP = 512, KO_LONG_BLOCKS = 32;
+
+struct KeySplit {
+    uint64_t div;    // 0: major = key >> 32, minor = low 32 bits
+    uint32_t n_maj;  // majors are < n_maj; KEY_NONE takes major n_maj
+    __device__ __forceinline__ uint32_t major(uint64_t k) const {
+        if (k == KEY_NONE) return n_maj;
+        const uint64_t m = div ? k / div : k >> 32;
+        return m < n_maj ? (uint32_t)m : n_maj;  // (never: every real key's major is < n_maj)
+    }
+    __device__ __forceinline__ uint32_t minor(uint64_t k) const { return div ? (uint32_t)(k % div) : (uint32_t)k; }
+    __device__ __forceinline__ uint64_t key(uint32_t m, uint32_t mn) const {
+        return div ? (uint64_t)m * div + mn : ((uint64_t)m << 32) | mn;
+    }
+};
+
+// A wave's runs of equal majors (the final set's survivors arrive sorted, so
+// a run is often the whole wave): the run's first lane, its length and this
+// lane's rank in it.  Every lane must be active.
+struct KoRun {
+    uint32_t head, len, rank;
+};
+__device__ __forceinline__ KoRun ko_run(uint32_t m, uint32_t lane) {
+    const uint32_t prev = (uint32_t)__shfl_up((int)m, 1, 64);
+    const uint64_t bnd = __ballot(lane == 0u || prev != m);
+    const uint64_t upto = bnd & (lane == 63u ? ~0ull : ((2ull << lane) - 1ull));
+    const uint32_t head = 63u - (uint32_t)__builtin_clzll(upto);
+    const uint64_t after = head == 63u ? 0ull : bnd >> (head + 1u);
+    const uint32_t end = after ? head + 1u + (uint32_t)__builtin_ctzll(after) : 64u;
+    return KoRun{head, end - head, lane - head};
+}
+
+// Counts per major: one global atomic per run of equal majors in a wave
+// (sorted input: about one per major; random input: about one per entry,
+// which beats counting in LDS first when the majors far outnumber a block's
+// entries).  KEY_NONE entries are not counted: their segment runs from the
+// other majors' total to N.  They may fill most of the input (the final set's
+// empty tile entries), and one counter taking an atomic per wave serializes,
+// so k_ko_scatter places them with one atomic per block.
+__global__ __launch_bounds__(256) void k_ko_count(const uint64_t *__restrict__ key, int64_t N, KeySplit ks,
+                                                  uint32_t *__restrict__ cnt) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t m = e < N ? ks.major(key[e]) : 0xFFFFFFFFu;
+    const KoRun r = ko_run(m, lane);
+    if (m < ks.n_maj && r.rank == 0u) atomicAdd(cnt + m, r.len);
+}
+
+// ptr[0, n) = exclusive scan of cnt[0, n) (n <= KO_BINS), ptr[n] = n_all, by
+// one block: the counts pass through LDS (coalesced loads and stores), thread t
+// scans its KO_SCAN_PER consecutive ones (an odd stride: no bank conflicts),
+// and a wave scan plus a scan over the 16 wave totals give its base.
+constexpr uint32_t KO_SCAN_PER = (KO_BINS + 1023u) / 1024u;
+__global__ __launch_bounds__(1024) void k_ko_scan(const uint32_t *__restrict__ cnt, uint32_t n, uint32_t n_all,
+                                                  uint32_t *__restrict__ ptr) {
+    __shared__ uint32_t wsum[16];
+    __shared__ uint32_t sv[KO_SCAN_PER * 1024];
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6, b = t * KO_SCAN_PER;
+#pragma unroll
+    for (uint32_t k = 0; k < KO_SCAN_PER; ++k) {
+        const uint32_t i = k * 1024u + t;
+        sv[i] = i < n ? cnt[i] : 0u;
+    }
+    __syncthreads();
+    uint32_t v[KO_SCAN_PER], s = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < KO_SCAN_PER; ++k) {
+        v[k] = sv[b + k];
+        s += v[k];
+    }
+    uint32_t inc = s;
+#pragma unroll
+    for (uint32_t d = 1; d < 64u; d <<= 1) {
+        const uint32_t o = (uint32_t)__shfl_up((int)inc, d, 64);
+        if (lane >= d) inc += o;
+    }
+    if (lane == 63u) wsum[wave] = inc;
+    __syncthreads();
+    uint32_t base = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < 16u; ++w) base += w < wave ? wsum[w] : 0u;
+    uint32_t run = base + inc - s;
+#pragma unroll
+    for (uint32_t k = 0; k < KO_SCAN_PER; ++k) {
+        sv[b + k] = run;
+        run += v[k];
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t k = 0; k < KO_SCAN_PER; ++k) {
+        const uint32_t i = k * 1024u + t;
+        if (i < n) ptr[i] = sv[i];
+    }
+    if (t == 0) ptr[n] = n_all;  // the KEY_NONE segment (major n - 1, never counted) ends at n_all
+}
+
+// Each entry's place in its major's segment: ptr[m] plus the count left
+// after its wave's run takes its share (cnt is consumed), plus its rank in the
+// run.  KEY_NONE entries are final here: a block reserves its share of that
+// segment by one atomic on none_fill, its waves' shares ranked in LDS.  Each
+// thread takes KO_PER entries, 256 apart.
+constexpr uint32_t KO_PER = 4, KO_CHUNK = 256 * KO_PER;
+__global__ __launch_bounds__(256) void k_ko_scatter(const uint64_t *__restrict__ key, int64_t N, KeySplit ks,
+                                                    const uint32_t *__restrict__ ptr, uint32_t *__restrict__ cnt,
+                                                    uint32_t *__restrict__ none_fill,
+                                                    uint32_t *__restrict__ seg_mnr, uint32_t *__restrict__ seg_idx,
+                                                    uint64_t *__restrict__ key_out, uint32_t *__restrict__ perm) {
+    __shared__ uint32_t s_none, s_base;
+    if (threadIdx.x == 0) s_none = 0u;
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u;
+    const int64_t e0 = (int64_t)blockIdx.x * KO_CHUNK + threadIdx.x;
+    uint32_t noff[KO_PER];
+#pragma unroll
+    for (uint32_t k = 0; k < KO_PER; ++k) {
+        const int64_t e = e0 + (int64_t)k * 256;
+        const uint64_t kv = e < N ? key[e] : 0ull;
+        const uint32_t m = e < N ? ks.major(kv) : 0xFFFFFFFFu;
+        const KoRun r = ko_run(m, lane);
+        uint32_t old = 0;
+        if (m < ks.n_maj && r.rank == 0u) old = atomicSub(cnt + m, r.len);
+        old = (uint32_t)__shfl((int)old, (int)r.head, 64);
+        if (m < ks.n_maj) {
+            const uint32_t p = ptr[m] + old - r.len + r.rank;
+            seg_mnr[p] = ks.minor(kv);
+            seg_idx[p] = (uint32_t)e;
+        }
+        const uint64_t none = __ballot(m == ks.n_maj);
+        noff[k] = 0xFFFFFFFFu;
+        if (none) {
+            const uint32_t lead = (uint32_t)(__ffsll((unsigned long long)none) - 1);
+            uint32_t o = 0;
+            if (lane == lead) o = atomicAdd(&s_none, (uint32_t)__popcll(none));
+            o = (uint32_t)__shfl((int)o, (int)lead, 64);
+            if (m == ks.n_maj)
+                noff[k] = o + __builtin_amdgcn_mbcnt_hi((uint32_t)(none >> 32),
+                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)none, 0u));
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) s_base = s_none ? ptr[ks.n_maj] + atomicAdd(none_fill, s_none) : 0u;
+    __syncthreads();
+    const uint32_t base = s_base;
+#pragma unroll
+    for (uint32_t k = 0; k < KO_PER; ++k) {
+        if (noff[k] != 0xFFFFFFFFu) {
+            const int64_t e = e0 + (int64_t)k * 256;
+            key_out[base + noff[k]] = key[e];
+            perm[base + noff[k]] = (uint32_t)e;
+        }
+    }
+}
+
+__device__ __forceinline__ uint64_t ko_pack(uint32_t mnr, uint32_t idx) { return ((uint64_t)mnr << 32) | idx; }
+
+// One wave per major segment below n_maj; a segment longer than KO_CAP is
+// listed for k_ko_long.
+__global__ __launch_bounds__(KO_WAVES * 64) void k_ko_seg(const uint32_t *__restrict__ ptr, KeySplit ks,
+                                                          const uint32_t *__restrict__ seg_mnr,
+                                                          const uint32_t *__restrict__ seg_idx,
+                                                          uint64_t *__restrict__ key_out, uint32_t *__restrict__ perm,
+                                                          uint32_t *__restrict__ n_long, uint32_t *__restrict__ longs) {
+    __shared__ uint64_t s[KO_WAVES][KO_CAP];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t m = blockIdx.x * KO_WAVES + wave;
+    if (m >= ks.n_maj) return;
+    const uint32_t b = ptr[m], len = ptr[m + 1] - b;
+    if (len == 0u) return;
+    if (len <= 64u) {
+        // padding (all ones) sorts last: real pairs have idx < 2^31
+        uint64_t v = lane < len ? ko_pack(seg_mnr[b + lane], seg_idx[b + lane]) : ~0ull;
+        for (uint32_t k = 2; k <= 64u; k <<= 1)
+            for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+                const uint32_t lo32 = (uint32_t)__shfl_xor((int)(uint32_t)v, (int)j, 64);
+                const uint32_t hi32 = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), (int)j, 64);
+                const uint64_t o = ((uint64_t)hi32 << 32) | lo32;
+                const bool up = (lane & k) == 0u, lower = (lane & j) == 0u;
+                if (lower == up ? o < v : o > v) v = o;
+            }
+        if (lane < len) {
+            key_out[b + lane] = ks.key(m, (uint32_t)(v >> 32));
+            perm[b + lane] = (uint32_t)v;
+        }
+        return;
+    }
+    if (len > KO_CAP) {
+        if (lane == 0) longs[atomicAdd(n_long, 1u)] = m;
+        return;
+    }
+    uint32_t n2 = 128;
+    while (n2 < len) n2 <<= 1;
+    uint64_t *t = s[wave];
+    for (uint32_t q = lane; q < n2; q += 64u) t[q] = q < len ? ko_pack(seg_mnr[b + q], seg_idx[b + q]) : ~0ull;
+    wave_lds_sync();
+    for (uint32_t k = 2; k <= n2; k <<= 1)
+        for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+            for (uint32_t q = lane; q < n2 / 2u; q += 64u) {
+                const uint32_t lo = (q / j) * 2u * j + (q % j), hi = lo + j;
+                const bool up = (lo & k) == 0u;
+                const uint64_t x = t[lo], y = t[hi];
+                if (up ? x > y : x < y) {
+                    t[lo] = y;
+                    t[hi] = x;
+                }
+            }
+            wave_lds_sync();
+        }
+    for (uint32_t q = lane; q < len; q += 64u) {
+        const uint64_t v = t[q];
+        key_out[b + q] = ks.key(m, (uint32_t)(v >> 32));
+        perm[b + q] = (uint32_t)v;
+    }
+}
+
+// The listed long segments, one block each, sorted in place in seg_mnr /
+// seg_idx by a bitonic network whose comparators all put the smaller pair
+// first (each merge starts by comparing mirrored positions), so positions at
+// or past the segment's end act as +infinity and their comparators are
+// skipped.  Rare: a major holding more than KO_CAP of the step's entries.
+__global__ __launch_bounds__(256) void k_ko_long(const uint32_t *__restrict__ ptr, KeySplit ks,
+                                                 const uint32_t *__restrict__ n_long,
+                                                 const uint32_t *__restrict__ longs, uint32_t *seg_mnr,
+                                                 uint32_t *seg_idx, uint64_t *__restrict__ key_out,
+                                                 uint32_t *__restrict__ perm) {
+    const uint32_t nl = *n_long;
+    for (uint32_t q = blockIdx.x; q < nl; q += gridDim.x) {
+        const uint32_t m = longs[q], b = ptr[m], len = ptr[m + 1] - b;
+        uint32_t *mn = seg_mnr + b, *ix = seg_idx + b;
+        uint32_t n2 = 1;
+        while (n2 < len) n2 <<= 1;
+        for (uint32_t k = 2; k <= n2; k <<= 1)
+            for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+                for (uint32_t t = threadIdx.x; t < n2 / 2u; t += 256u) {
+                    const uint32_t lo = (t / j) * 2u * j + (t % j);
+                    const uint32_t hi = j == (k >> 1) ? (lo / k) * k + (k - 1u) - (lo % k) : lo + j;
+                    if (hi < len) {
+                        const uint64_t x = ko_pack(mn[lo], ix[lo]), y = ko_pack(mn[hi], ix[hi]);
+                        if (x > y) {
+                            mn[lo] = (uint32_t)(y >> 32);
+                            ix[lo] = (uint32_t)y;
+                            mn[hi] = (uint32_t)(x >> 32);
+                            ix[hi] = (uint32_t)x;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        for (uint32_t t = threadIdx.x; t < len; t += 256u) {
+            key_out[b + t] = ks.key(m, mn[t]);
+            perm[b + t] = ix[t];
+        }
+        __syncthreads();
+    }
+}
+
+// key_out = key[0, N) in order, perm = the entries' indices in that order
+// (what a stable radix sort of (key, index) pairs gives).  False, with nothing
+// launched, when the majors do not fit KO_BINS or N reaches 2^31: the caller
+// sorts instead.  Set SILI_KEYORDER=0 to always sort.
+bool order_keys(Layer &L, const uint64_t *key, int64_t N, uint32_t n_maj, uint64_t div, uint64_t *key_out,
+                uint32_t *perm) {
+    if (env_int("SILI_KEYORDER", 1) == 0 || (uint64_t)n_maj + 1u > KO_BINS || N >= (int64_t(1) << 31)) return false;
+    if (N == 0) return true;
+    hipStream_t st = L.stream;
+    const KeySplit ks{div, n_maj};
+    const uint32_t nb = n_maj + 1u;
+    const int64_t max_long = N / (KO_CAP + 1) + 1;
+    TmpBuf<uint32_t> cnt(L, SILI_TMPKEY(ko_cnt)), ptr(L, SILI_TMPKEY(ko_ptr)), smn(L, SILI_TMPKEY(ko_mnr)),
+        sidx(L, SILI_TMPKEY(ko_idx)), longs(L, SILI_TMPKEY(ko_longs));
+    cnt.ensure((size_t)nb + 2);  // [nb]: the long-segment count, [nb + 1]: KEY_NONE places taken
+    ptr.ensure((size_t)nb + 1);
+    smn.ensure((size_t)N);
+    sidx.ensure((size_t)N);
+    longs.ensure((size_t)max_long);
+    launch(k_fill_u32, dim3(nblk(nb + 2)), dim3(TPB), 0, st, cnt.p, (int64_t)nb + 2, 0u);
+    launch(k_ko_count, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, st, key, N, ks, cnt.p);
+    launch(k_ko_scan, dim3(1), dim3(1024), 0, st, (const uint32_t *)cnt.p, nb, (uint32_t)N, ptr.p);
+    launch(k_ko_scatter, dim3((unsigned)((N + KO_CHUNK - 1) / KO_CHUNK)), dim3(256), 0, st, key, N, ks,
+           (const uint32_t *)ptr.p, cnt.p, cnt.p + nb + 1, smn.p, sidx.p, key_out, perm);
+    launch(k_ko_seg, dim3((n_maj + KO_WAVES - 1) / KO_WAVES), dim3(KO_WAVES * 64), 0, st, (const uint32_t *)ptr.p,
+           ks, (const uint32_t *)smn.p, (const uint32_t *)sidx.p, key_out, perm, cnt.p + nb, longs.p);
+    launch(k_ko_long, dim3(KO_LONG_BLOCKS), dim3(256), 0, st, (const uint32_t *)ptr.p, ks,
+           (const uint32_t *)(cnt.p + nb), (const uint32_t *)longs.p, smn.p, sidx.p, key_out, perm);
+    SILI_HIP(hipGetLastError());
+    return true;
+}
+
 // Exclusive scan of flag[0, n) into pos; returns the total.  With n_mid:
 // also the count of flags in [0, mid), read in the same round trip.
 int64_t compact_positions(Layer &L, const uint32_t *flag, uint32_t *pos, int64_t n, int64_t mid = -1,
@@ -868,10 +1171,12 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
         launch(k_syn_cand_static, dim3(g), dim3(TPB), 0, st, n_cand, (const int32_t *)dcr.p,
                (const int32_t *)dcc.p, n_in, n_out, (const uint64_t *)rc.p, Ns, (const uint64_t *)tkey.p, T,
                (const uint8_t *)L.B4.tiles.p, bcols, ckey.p);
-        launch(k_iota32, dim3(g), dim3(TPB), 0, st, cidx.p, n_cand);
         launch(k_fill_u32, dim3(g), dim3(TPB), 0, st, first.p, n_cand, 0u);
         SILI_HIP(hipGetLastError());
-        device_sort_pairs_u64(L, ckey.p, ckey_sorted.p, cidx.p, cidx_sorted.p, n_cand, rc_bits);
+        if (!order_keys(L, ckey.p, n_cand, (uint32_t)n_in, 0, ckey_sorted.p, cidx_sorted.p)) {
+            launch(k_iota32, dim3(g), dim3(TPB), 0, st, cidx.p, n_cand);
+            device_sort_pairs_u64(L, ckey.p, ckey_sorted.p, cidx.p, cidx_sorted.p, n_cand, rc_bits);
+        }
         launch(k_syn_first, dim3(g), dim3(TPB), 0, st, n_cand, (const uint64_t *)ckey_sorted.p,
                (const uint32_t *)cidx_sorted.p, first.p);
         SILI_HIP(hipGetLastError());
@@ -881,17 +1186,21 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
                (const float *)dcv.p, cand_s ? (const float *)dcs.p : nullptr, (uint32_t)default_imp, sc,
                (const uint64_t *)tkey.p, T, (const uint8_t *)alive.p, tbytes.p, tins.p, bcols, key2.p + (Ns + T),
                byte2.p + (Ns + T), win.p, counters.p + 2);
-        launch(k_iota32, dim3(g), dim3(TPB), 0, st, wv.p, n_cand);
         SILI_HIP(hipGetLastError());
-        device_sort_pairs_u64(L, win.p, win_sorted.p, wv.p, wvs.p, n_cand, win_bits);
+        if (!order_keys(L, win.p, n_cand, (uint32_t)((n_in + 3) / 4), bcols, win_sorted.p, wvs.p)) {
+            launch(k_iota32, dim3(g), dim3(TPB), 0, st, wv.p, n_cand);
+            device_sort_pairs_u64(L, win.p, win_sorted.p, wv.p, wvs.p, n_cand, win_bits);
+        }
     }
 
     // -- final scattered set (sorted) and promotion ---------------------------
     if (M2 > 0) {
-        launch(k_iota32, dim3(nblk(M2)), dim3(TPB), 0, st, iota2.p, M2);
         launch(k_fill_u8, dim3(nblk(M2)), dim3(TPB), 0, st, removed2.p, M2, (uint8_t)0);
         SILI_HIP(hipGetLastError());
-        device_sort_pairs_u64(L, key2.p, key2_sorted.p, iota2.p, perm2.p, M2, rc_bits);
+        if (!order_keys(L, key2.p, M2, (uint32_t)n_in, 0, key2_sorted.p, perm2.p)) {
+            launch(k_iota32, dim3(nblk(M2)), dim3(TPB), 0, st, iota2.p, M2);
+            device_sort_pairs_u64(L, key2.p, key2_sorted.p, iota2.p, perm2.p, M2, rc_bits);
+        }
         launch(k_gather_u8_by, dim3(nblk(M2)), dim3(TPB), 0, st, (const uint8_t *)byte2.p,
                (const uint32_t *)perm2.p, M2, byte2_sorted.p);
         SILI_HIP(hipGetLastError());

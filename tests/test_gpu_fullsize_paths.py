@@ -123,26 +123,28 @@ def test_config3_synapto_tile_merge_equals_sort(hip, c3, monkeypatch):
         assert np.array_equal(La._store_digest(), Lb._store_digest()), f"step {i}"
 
 
-def test_config3_synapto_segment_order_equals_sort(hip, c3, monkeypatch):
-    """The shadow builds order entries by a count per major and a per-segment
-    network (SILI_SEGSORT, the default); SILI_SEGSORT=0 sorts the keys.  The
-    load and three bulk steps give identical stores either way."""
+@pytest.mark.parametrize("knob", ["SILI_SEGSORT", "SILI_KEYORDER"])
+def test_config3_synapto_segment_order_equals_sort(hip, c3, monkeypatch, knob):
+    """The shadow builds (SILI_SEGSORT) and the step's candidate, window and
+    final-set keys (SILI_KEYORDER) are ordered by a count per major and a
+    per-segment network by default; =0 sorts the keys.  The load and three
+    bulk steps give identical stores either way."""
     wl = c3
-    monkeypatch.setenv("SILI_SEGSORT", "1")
+    monkeypatch.setenv(knob, "1")
     La = _c3_synapto_layer(hip, wl)
-    monkeypatch.setenv("SILI_SEGSORT", "0")
+    monkeypatch.setenv(knob, "0")
     Lb = _c3_synapto_layer(hip, wl)
     assert np.array_equal(La._store_digest(), Lb._store_digest()), "load"
     for i in range(3):
         cr, cc, cv = _bench_candidates(wl, i)
-        monkeypatch.setenv("SILI_SEGSORT", "1")
+        monkeypatch.setenv(knob, "1")
         sa = La.synapto_step(0.01, cr, cc, cv)
-        monkeypatch.setenv("SILI_SEGSORT", "0")
+        monkeypatch.setenv(knob, "0")
         sb = Lb.synapto_step(0.01, cr, cc, cv)
         assert sa == sb, i
         assert sa["n_scattered"] > 0, sa
         assert np.array_equal(La._store_digest(), Lb._store_digest()), f"step {i}"
-    monkeypatch.delenv("SILI_SEGSORT")
+    monkeypatch.delenv(knob)
 
 
 def _exported(L, n_in, n_out):
