@@ -551,6 +551,18 @@ void device_exclusive_scan_u64(Layer &L, const uint64_t *in, uint64_t *out, int6
     SILI_HIP(rocprim::exclusive_scan(L.scratch.temp.p, bytes, in, out, uint64_t(0), (size_t)n,
                                      rocprim::plus<uint64_t>(), L.stream));
 }
+// Lane i * 64 + b copies byte b of value i into the pinned buffer (kernels
+// write pinned host memory directly; the wait that follows makes it visible).
+__global__ __launch_bounds__(512) void k_readback(ReadBackSrc a, uint8_t *__restrict__ dst) {
+    const int i = (int)(threadIdx.x >> 6), b = (int)(threadIdx.x & 63u);
+    if (i < a.n && (uint32_t)b < a.bytes[i]) dst[64 * i + b] = static_cast<const uint8_t *>(a.src[i])[b];
+}
+
+void readback_launch(Layer &L, const ReadBackSrc &a) {
+    launch(k_readback, dim3(1), dim3(512), 0, L.stream, a, L.pin_read.h);
+    SILI_HIP(hipGetLastError());
+}
+
 void device_exclusive_scan_u32(Layer &L, const uint32_t *in, uint32_t *out, int64_t n) {
     size_t bytes = 0;
     SILI_HIP(rocprim::exclusive_scan(nullptr, bytes, in, out, uint32_t(0), (size_t)n,

@@ -578,23 +578,31 @@ void device_exclusive_scan_u32(Layer &L, const uint32_t *in, uint32_t *out, int6
 // values are copied out.  (A copy into pageable host memory waits for the
 // stream by itself: one round trip per value.)  At most 8 values of up to 64
 // bytes each; one ReadBack in flight per layer.
+// The values are fetched at wait() by one kernel that writes them into the
+// pinned buffer (where a copy per value cost a runtime copy launch each), so
+// nothing queued between add() and wait() may change them.
+struct ReadBackSrc {
+    const void *src[8];
+    uint32_t bytes[8];
+    int n;
+};
+void readback_launch(Layer &L, const ReadBackSrc &a);  // build.hip
 struct ReadBack {
     Layer &L;
-    struct Item {
-        void *dst;
-        size_t bytes;
-    } items[8];
-    int n = 0;
+    void *dst[8];
+    ReadBackSrc a{};
     explicit ReadBack(Layer &l) : L(l) { L.pin_read.ensure(8 * 64); }
-    void add(void *dst, const void *src, size_t bytes) {
-        if (n == 8 || bytes > 64) throw_error(1, "ReadBack: too many or too large values (internal error)");
-        SILI_HIP(hipMemcpyAsync(L.pin_read.h + 64 * n, src, bytes, hipMemcpyDeviceToHost, L.stream));
-        items[n++] = Item{dst, bytes};
+    void add(void *d, const void *src, size_t bytes) {
+        if (a.n == 8 || bytes > 64) throw_error(1, "ReadBack: too many or too large values (internal error)");
+        dst[a.n] = d;
+        a.src[a.n] = src;
+        a.bytes[a.n++] = (uint32_t)bytes;
     }
     void wait() {
+        if (a.n) readback_launch(L, a);
         SILI_HIP(hipStreamSynchronize(L.stream));
-        for (int i = 0; i < n; ++i) std::memcpy(items[i].dst, L.pin_read.h + 64 * i, items[i].bytes);
-        n = 0;
+        for (int i = 0; i < a.n; ++i) std::memcpy(dst[i], L.pin_read.h + 64 * i, a.bytes[i]);
+        a.n = 0;
     }
 };
 

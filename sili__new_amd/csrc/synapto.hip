@@ -118,6 +118,10 @@ struct SelState {
     unsigned long long pad;     // keys in the chosen bin (after the last level: the ties)
 };
 
+// A selection's initial state, written by a kernel (a host copy of a stack
+// value costs a runtime staging launch).
+__global__ void k_put_state(SelState *p, SelState v) { *p = v; }
+
 // Histogram of bits [shift, shift + width) of the keys below `limit` whose
 // bits above shift + width equal the state's prefix (level > 0).  Lanes of a
 // wave that share a bin add once (ties concentrate on one bin).
@@ -563,10 +567,11 @@ __global__ void k_emit_tiles(int64_t T, const uint32_t *tbr, const uint32_t *tbc
 }
 
 template <typename T>
-T read_back(const T *d, hipStream_t st) {
+T read_back(Layer &L, const T *d) {
     T h{};
-    SILI_HIP(hipMemcpyAsync(&h, d, sizeof(T), hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipStreamSynchronize(st));
+    ReadBack rb(L);
+    rb.add(&h, d, sizeof(T));
+    rb.wait();
     return h;
 }
 
@@ -933,11 +938,9 @@ void select_smallest(Layer &L, const uint32_t *absw, const uint64_t *rc, int64_t
     TmpBuf<SelState> state(L, SILI_TMPKEY(state));
     state.ensure(2);
     const SelState s0{0ull, (unsigned long long)k, 0ull, 0ull};
-    SILI_HIP(hipMemcpyAsync(state.p, &s0, sizeof(s0), hipMemcpyHostToDevice, st));
+    launch(k_put_state, dim3(1), dim3(1), 0, st, state.p, s0);
     radix_select<uint32_t>(L, absw, M, ABSW_LIMIT, ABSW_BITS, state.p, hist, true);
-    SelState sf{};
-    SILI_HIP(hipMemcpyAsync(&sf, state.p, sizeof(SelState), hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipStreamSynchronize(st));
+    const SelState sf = read_back(L, (const SelState *)state.p);
     const int64_t less = (int64_t)sf.less, ties = (int64_t)sf.pad, take = k - less;
     if ((int64_t)sf.need != take || take < 1 || take > ties)
         throw_error(SILI_ERR_RUNTIME, "synapto: selection of the smallest synapses is inconsistent");
@@ -962,7 +965,7 @@ void select_smallest(Layer &L, const uint32_t *absw, const uint64_t *rc, int64_t
     }
     // the first `take` ties in (row, col) order: keys up to the take-th smallest
     const SelState s1{0ull, (unsigned long long)take, 0ull, 0ull};
-    SILI_HIP(hipMemcpyAsync(state.p + 1, &s1, sizeof(s1), hipMemcpyHostToDevice, st));
+    launch(k_put_state, dim3(1), dim3(1), 0, st, state.p + 1, s1);
     radix_select<uint64_t>(L, tie_key.p, ties, ~0ull, rc_bits, state.p + 1, hist);
     tflag.ensure((size_t)ties + 1);
     tpos.ensure((size_t)ties + 1);
@@ -1047,10 +1050,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
         iota.ensure((size_t)M + 1);
         perm_rc.ensure((size_t)M + 1);
     }
-    {
-        std::vector<unsigned long long> z(4, 0ull);
-        SILI_HIP(hipMemcpyAsync(counters.p, z.data(), 4 * sizeof(unsigned long long), hipMemcpyHostToDevice, st));
-    }
+    launch(k_fill_u32, dim3(1), dim3(TPB), 0, st, reinterpret_cast<uint32_t *>(counters.p), (int64_t)8, 0u);
     if (M > 0) {
         launch(k_syn_keys, dim3(nblk(M)), dim3(TPB), 0, st, Ns, (const uint32_t *)srow.p,
                (const uint32_t *)scol.p, (const uint8_t *)L.W.val.p, T, (const uint32_t *)tbr.p,
@@ -1069,7 +1069,7 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
             SILI_HIP(hipGetLastError());
         }
     }
-    const int64_t N = (int64_t)read_back(counters.p, st);  // scattered + live block4 slots
+    const int64_t N = (int64_t)read_back(L, counters.p);  // scattered + live block4 slots
     int64_t k = 0;
     if (explicit_prune) {
         if (n_prune > 0) {
@@ -1278,8 +1278,11 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
         SILI_HIP(hipGetLastError());
     }
     unsigned long long cnt[4];
-    SILI_HIP(hipMemcpyAsync(cnt, counters.p, sizeof(cnt), hipMemcpyDeviceToHost, st));
-    SILI_HIP(hipStreamSynchronize(st));
+    {
+        ReadBack rb(L);
+        rb.add(cnt, counters.p, sizeof(cnt));
+        rb.wait();
+    }
     // SILI_TILE_MERGE=0 always sorts (the two paths build the same store)
     const bool merge = cnt[3] == 0 && env_int("SILI_TILE_MERGE", 1) != 0;
 
