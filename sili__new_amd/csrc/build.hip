@@ -191,10 +191,12 @@ __global__ void k_iota(uint32_t *__restrict__ v, int64_t N) {
 // first position, a scatter into the majors' segments (arbitrary order within
 // a segment), then each segment ordered by minor: one wave per segment, a
 // bitonic network over the wave's lanes (up to 64 entries) or in the wave's
-// LDS slice (up to SEGSORT_CAP).  The order within a segment is unique since
-// the keys are, so the result equals a sort of the keys.  About five launches
-// where a device radix sort of a few hundred thousand keys took about twenty.
-constexpr uint32_t SEGSORT_CAP = 2048;
+// LDS slice (up to SEGSORT_CAP; at 2048 its 64 KiB blocks left 8 waves per
+// CU), a longer segment by one block in global memory.  The order within a
+// segment is unique since the keys are, so the result equals a sort of the
+// keys.  About six launches where a device radix sort of a few hundred
+// thousand keys took about twenty.
+constexpr uint32_t SEGSORT_CAP = 512;
 constexpr uint32_t SEGSORT_WAVES = 4;
 
 __global__ void k_fill_u32_b(uint32_t *__restrict__ p, int64_t n, uint32_t v) {
@@ -209,20 +211,26 @@ __global__ void k_count_major(const uint32_t *__restrict__ maj, int64_t N, int64
     const uint32_t m = maj[i];
     if ((int64_t)m >= maj_ext) {
         atomicOr(bad, 1);
+        atomicAdd(cnt + maj_ext, 1u);  // kept last, so that perm stays a permutation
         return;
     }
     atomicAdd(cnt + m, 1u);
 }
 
 // cnt (the counts) is consumed: each entry takes position ptr[m] + (its
-// count after the decrement).
+// count after the decrement).  An out-of-range major (flagged by the count)
+// goes after every segment, directly into perm.
 __global__ void k_scatter_major(const uint32_t *__restrict__ maj, const uint32_t *__restrict__ mnr, int64_t N,
                                 int64_t maj_ext, const uint32_t *__restrict__ ptr, uint32_t *__restrict__ cnt,
-                                uint32_t *__restrict__ seg_mnr, uint32_t *__restrict__ seg_idx) {
+                                uint32_t *__restrict__ seg_mnr, uint32_t *__restrict__ seg_idx,
+                                uint32_t *__restrict__ perm) {
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
     if (i >= N) return;
     const uint32_t m = maj[i];
-    if ((int64_t)m >= maj_ext) return;
+    if ((int64_t)m >= maj_ext) {
+        perm[ptr[maj_ext] + atomicSub(cnt + maj_ext, 1u) - 1u] = (uint32_t)i;
+        return;
+    }
     const uint32_t p = ptr[m] + atomicSub(cnt + m, 1u) - 1u;
     seg_mnr[p] = mnr[i];
     seg_idx[p] = (uint32_t)i;
@@ -238,8 +246,8 @@ constexpr uint32_t MM_BINS = 8192, MM_PER = 32, MM_CHUNK = 256 * MM_PER;
 __global__ __launch_bounds__(256) void k_count_major_lds(const uint32_t *__restrict__ maj, int64_t N,
                                                          int64_t maj_ext, uint32_t *__restrict__ cnt,
                                                          int *__restrict__ bad) {
-    __shared__ uint32_t h[MM_BINS];
-    for (uint32_t i = threadIdx.x; i < (uint32_t)maj_ext; i += 256u) h[i] = 0u;
+    __shared__ uint32_t h[MM_BINS + 1];  // [maj_ext]: out-of-range majors
+    for (uint32_t i = threadIdx.x; i <= (uint32_t)maj_ext; i += 256u) h[i] = 0u;
     __syncthreads();
     const int64_t e0 = (int64_t)blockIdx.x * MM_CHUNK + threadIdx.x;
 #pragma unroll 4
@@ -248,11 +256,11 @@ __global__ __launch_bounds__(256) void k_count_major_lds(const uint32_t *__restr
         if (e < N) {
             const uint32_t m = maj[e];
             if ((int64_t)m >= maj_ext) atomicOr(bad, 1);
-            else atomicAdd(&h[m], 1u);
+            atomicAdd(&h[(int64_t)m < maj_ext ? m : (uint32_t)maj_ext], 1u);
         }
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < (uint32_t)maj_ext; i += 256u)
+    for (uint32_t i = threadIdx.x; i <= (uint32_t)maj_ext; i += 256u)
         if (h[i]) atomicAdd(cnt + i, h[i]);
 }
 
@@ -263,9 +271,9 @@ __global__ __launch_bounds__(256) void k_scatter_major_lds(const uint32_t *__res
                                                            const uint32_t *__restrict__ mnr, int64_t N,
                                                            int64_t maj_ext, const uint32_t *__restrict__ ptr,
                                                            uint32_t *__restrict__ cnt, uint32_t *__restrict__ seg_mnr,
-                                                           uint32_t *__restrict__ seg_idx) {
-    __shared__ uint32_t h[MM_BINS];
-    for (uint32_t i = threadIdx.x; i < (uint32_t)maj_ext; i += 256u) h[i] = 0u;
+                                                           uint32_t *__restrict__ seg_idx, uint32_t *__restrict__ perm) {
+    __shared__ uint32_t h[MM_BINS + 1];  // [maj_ext]: out-of-range majors, placed last
+    for (uint32_t i = threadIdx.x; i <= (uint32_t)maj_ext; i += 256u) h[i] = 0u;
     __syncthreads();
     const int64_t e0 = (int64_t)blockIdx.x * MM_CHUNK + threadIdx.x;
     uint32_t rk[MM_PER];
@@ -275,12 +283,12 @@ __global__ __launch_bounds__(256) void k_scatter_major_lds(const uint32_t *__res
         rk[k] = 0u;
         if (e < N) {
             const uint32_t m = maj[e];
-            if ((int64_t)m < maj_ext) rk[k] = atomicAdd(&h[m], 1u);
+            rk[k] = atomicAdd(&h[(int64_t)m < maj_ext ? m : (uint32_t)maj_ext], 1u);
         }
     }
     __syncthreads();
     // h[m] becomes the block's first position in major m's segment
-    for (uint32_t i = threadIdx.x; i < (uint32_t)maj_ext; i += 256u) {
+    for (uint32_t i = threadIdx.x; i <= (uint32_t)maj_ext; i += 256u) {
         const uint32_t c = h[i];
         if (c) h[i] = ptr[i] + atomicSub(cnt + i, c) - c;
     }
@@ -294,18 +302,21 @@ __global__ __launch_bounds__(256) void k_scatter_major_lds(const uint32_t *__res
                 const uint32_t p = h[m] + rk[k];
                 seg_mnr[p] = mnr[e];
                 seg_idx[p] = (uint32_t)e;
+            } else {
+                perm[h[maj_ext] + rk[k]] = (uint32_t)e;
             }
         }
     }
 }
 
 // perm[p] for every position of segment m (one wave per segment); a segment
-// longer than SEGSORT_CAP sets *too_long and is left unsorted.
+// longer than SEGSORT_CAP is listed for k_seg_sort_long.
 __global__ __launch_bounds__(SEGSORT_WAVES * 64) void k_seg_sort_minor(const uint32_t *__restrict__ ptr, int64_t nseg,
                                                                       const uint32_t *__restrict__ seg_mnr,
                                                                       const uint32_t *__restrict__ seg_idx,
                                                                       uint32_t *__restrict__ perm,
-                                                                      int *__restrict__ too_long) {
+                                                                      uint32_t *__restrict__ n_long,
+                                                                      uint32_t *__restrict__ longs) {
     __shared__ uint2 s[SEGSORT_WAVES][SEGSORT_CAP];
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     const int64_t m = (int64_t)blockIdx.x * SEGSORT_WAVES + wave;
@@ -333,7 +344,7 @@ __global__ __launch_bounds__(SEGSORT_WAVES * 64) void k_seg_sort_minor(const uin
         return;
     }
     if (len > SEGSORT_CAP) {
-        if (lane == 0) atomicOr(too_long, 1);
+        if (lane == 0) longs[atomicAdd(n_long, 1u)] = (uint32_t)m;
         return;
     }
     uint32_t n2 = 128;
@@ -356,6 +367,44 @@ __global__ __launch_bounds__(SEGSORT_WAVES * 64) void k_seg_sort_minor(const uin
             wave_lds_sync();
         }
     for (uint32_t q = lane; q < len; q += 64u) perm[b + q] = t[q].y;
+}
+
+// The listed long segments, one block each, ordered in place in seg_mnr /
+// seg_idx by a bitonic network whose comparators all put the smaller minor
+// first (each merge starts by comparing mirrored positions), so positions at
+// or past the segment's end act as +infinity and their comparators are
+// skipped; then perm.  Minors are unique within a segment.
+__global__ __launch_bounds__(256) void k_seg_sort_long(const uint32_t *__restrict__ ptr,
+                                                       const uint32_t *__restrict__ n_long,
+                                                       const uint32_t *__restrict__ longs, uint32_t *seg_mnr,
+                                                       uint32_t *seg_idx, uint32_t *__restrict__ perm) {
+    const uint32_t nl = *n_long;
+    for (uint32_t q = blockIdx.x; q < nl; q += gridDim.x) {
+        const uint32_t m = longs[q], b = ptr[m], len = ptr[m + 1] - b;
+        uint32_t *mn = seg_mnr + b, *ix = seg_idx + b;
+        uint32_t n2 = 1;
+        while (n2 < len) n2 <<= 1;
+        for (uint32_t k = 2; k <= n2; k <<= 1)
+            for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+                for (uint32_t t = threadIdx.x; t < n2 / 2u; t += 256u) {
+                    const uint32_t lo = (t / j) * 2u * j + (t % j);
+                    const uint32_t hi = j == (k >> 1) ? (lo / k) * k + (k - 1u) - (lo % k) : lo + j;
+                    if (hi < len) {
+                        const uint32_t a = mn[lo], c = mn[hi];
+                        if (a > c) {
+                            const uint32_t ia = ix[lo];
+                            mn[lo] = c;
+                            mn[hi] = a;
+                            ix[lo] = ix[hi];
+                            ix[hi] = ia;
+                        }
+                    }
+                }
+                __syncthreads();
+            }
+        for (uint32_t t = threadIdx.x; t < len; t += 256u) perm[b + t] = ix[t];
+        __syncthreads();
+    }
 }
 
 // Block4: key = major * minor_extent + minor.
@@ -420,8 +469,9 @@ __global__ void k_scan_nan_codes(const uint8_t *__restrict__ v, int64_t N, int h
 
 void check_flag(Layer &L, int *d_flag, const char *what) {
     int h = 0;
-    SILI_HIP(hipMemcpyAsync(&h, d_flag, sizeof(int), hipMemcpyDeviceToHost, L.stream));
-    SILI_HIP(hipStreamSynchronize(L.stream));
+    ReadBack rb(L);
+    rb.add(&h, d_flag, sizeof(int));
+    rb.wait();
     if (h & 4) throw_error(3, std::string(what) + ": merged tile runs out of order (internal error)");
     if (h) throw_error(1, std::string(what) + (h & 2 ? ": duplicate entries" : ": malformed input (unsorted, duplicate or out-of-range index)"));
 }
@@ -604,21 +654,21 @@ static void device_merge_pairs_u64(Layer &L, const uint64_t *k1, const uint64_t 
 
 // perm[p]: the entry at position p when the N entries are ordered by
 // (major, minor) (keys unique); ptr[0, maj_ext]: each major's first position
-// (ptr[maj_ext] = N).  A major out of range sets *bad |= 1; *bad is read back
-// here and, if set, raised as `what`'s malformed-input error.  False, with
-// nothing usable written, when a major holds more than SEGSORT_CAP entries:
-// the caller sorts the keys instead.  One wait on the stream.
-static bool sort_major_minor(Layer &L, const uint32_t *maj, const uint32_t *mnr, int64_t N, int64_t maj_ext,
+// (ptr[maj_ext] = N).  A major out of range sets *bad |= 1 (its entries go
+// last, so perm is a permutation whatever the input).  *bad is read back here
+// and, if set, raised as `what`'s malformed-input error -- one wait on the
+// stream -- except in a build from the layer's own arrays
+// (L.trusted_build), which queues everything and returns at once.
+static void sort_major_minor(Layer &L, const uint32_t *maj, const uint32_t *mnr, int64_t N, int64_t maj_ext,
                              uint32_t *perm, uint32_t *ptr, int *bad, const char *what) {
     hipStream_t st = L.stream;
-    TmpBuf<uint32_t> cnt(L, SILI_TMPKEY(mm_cnt)), smn(L, SILI_TMPKEY(mm_mnr)), sidx(L, SILI_TMPKEY(mm_idx));
-    TmpBuf<int> flag(L, SILI_TMPKEY(mm_flag));
-    cnt.ensure((size_t)maj_ext + 1);
+    TmpBuf<uint32_t> cnt(L, SILI_TMPKEY(mm_cnt)), smn(L, SILI_TMPKEY(mm_mnr)), sidx(L, SILI_TMPKEY(mm_idx)),
+        longs(L, SILI_TMPKEY(mm_longs));
+    cnt.ensure((size_t)maj_ext + 2);  // [maj_ext + 1]: the long-segment count
     smn.ensure((size_t)N + 1);
     sidx.ensure((size_t)N + 1);
-    flag.ensure(1);
-    launch(k_fill_u32_b, dim3(nblk(maj_ext + 1)), dim3(TPB), 0, st, cnt.p, maj_ext + 1, 0u);
-    launch(k_fill_u32_b, dim3(1), dim3(TPB), 0, st, reinterpret_cast<uint32_t *>(flag.p), (int64_t)1, 0u);
+    longs.ensure((size_t)(N / (SEGSORT_CAP + 1) + 1));
+    launch(k_fill_u32_b, dim3(nblk(maj_ext + 2)), dim3(TPB), 0, st, cnt.p, maj_ext + 2, 0u);
     const bool lds = maj_ext <= (int64_t)MM_BINS;
     const unsigned cgrid = (unsigned)((N + MM_CHUNK - 1) / MM_CHUNK);
     if (N > 0 && lds) launch(k_count_major_lds, dim3(cgrid), dim3(256), 0, st, maj, N, maj_ext, cnt.p, bad);
@@ -627,22 +677,23 @@ static bool sort_major_minor(Layer &L, const uint32_t *maj, const uint32_t *mnr,
     if (N > 0) {
         if (lds)
             launch(k_scatter_major_lds, dim3(cgrid), dim3(256), 0, st, maj, mnr, N, maj_ext, (const uint32_t *)ptr,
-                   cnt.p, smn.p, sidx.p);
+                   cnt.p, smn.p, sidx.p, perm);
         else
             launch(k_scatter_major, dim3(nblk(N)), dim3(TPB), 0, st, maj, mnr, N, maj_ext, (const uint32_t *)ptr,
-                   cnt.p, smn.p, sidx.p);
+                   cnt.p, smn.p, sidx.p, perm);
         launch(k_seg_sort_minor, dim3((unsigned)((maj_ext + SEGSORT_WAVES - 1) / SEGSORT_WAVES)),
                dim3(SEGSORT_WAVES * 64), 0, st, (const uint32_t *)ptr, maj_ext, (const uint32_t *)smn.p,
-               (const uint32_t *)sidx.p, perm, flag.p);
+               (const uint32_t *)sidx.p, perm, cnt.p + maj_ext + 1, longs.p);
+        launch(k_seg_sort_long, dim3(32), dim3(256), 0, st, (const uint32_t *)ptr,
+               (const uint32_t *)(cnt.p + maj_ext + 1), (const uint32_t *)longs.p, smn.p, sidx.p, perm);
     }
     SILI_HIP(hipGetLastError());
-    int h = 0, hb = 0;
+    if (L.trusted_build) return;
+    int hb = 0;
     ReadBack rb(L);
-    rb.add(&h, flag.p, sizeof(int));
     rb.add(&hb, bad, sizeof(int));
     rb.wait();
     if (hb) throw_error(1, std::string(what) + ": malformed input (unsorted, duplicate or out-of-range index)");
-    return h == 0;
 }
 
 static int bits_for(uint64_t max_value) {
@@ -792,9 +843,8 @@ void build_shadow(Layer &L, const DScatter &src, const uint32_t *d_rows, const u
     // by (column, row): the canonical entries are in (row, column) order, so
     // this is the stable order by column (SILI_SEGSORT=0: a device radix sort)
     zero_flag(L);
-    const bool counted = env_int("SILI_SEGSORT", 1) &&
-                         sort_major_minor(L, d_cols, d_rows, N, src.cols, perm.p, ptrs.p, L.scratch.flag.p,
-                                          "shadow build");
+    const bool counted = env_int("SILI_SEGSORT", 1) != 0;
+    if (counted) sort_major_minor(L, d_cols, d_rows, N, src.cols, perm.p, ptrs.p, L.scratch.flag.p, "shadow build");
     if (!counted && N > 0) {
         launch(k_iota, dim3(nblk(N)), dim3(TPB), 0, st, perm_in.p, N);
         device_sort_pairs_u32(L, d_cols, keys_out.p, perm_in.p, perm.p, N,
@@ -1057,10 +1107,10 @@ void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_
                 // (k_split_keys flags a merge whose runs were not)
                 device_merge_pairs_u64(L, key.p, key.p + sorted_head, key_sorted.p, perm_in.p,
                                        perm_in.p + sorted_head, perm.p, sorted_head, N - sorted_head);
-            } else if (env_int("SILI_SEGSORT", 1) &&
-                       (mptr.ensure((size_t)maj_ext + 1),
-                        sort_major_minor(L, maj, mnr, N, maj_ext, perm.p, mptr.p, L.scratch.flag.p, "block4 tiles"))) {
+            } else if (env_int("SILI_SEGSORT", 1)) {
                 // counted by major, each major's tiles ordered by minor
+                mptr.ensure((size_t)maj_ext + 1);
+                sort_major_minor(L, maj, mnr, N, maj_ext, perm.p, mptr.p, L.scratch.flag.p, "block4 tiles");
                 launch(k_gather_u64, dim3(nblk(N)), dim3(TPB), 0, st, (const uint64_t *)key.p, (const uint32_t *)perm.p,
                        N, key_sorted.p);
             } else {
@@ -1071,7 +1121,9 @@ void build_block4(Layer &L, int64_t n_tiles, const uint32_t *d_br, const uint32_
                                (uint64_t)mnr_ext, major.p, minor.p, L.scratch.flag.p);
             SILI_HIP(hipGetLastError());
         }
-        check_flag(L, L.scratch.flag.p, "block4 tiles");
+        // (a build from the layer's own arrays: its tiles are in range and
+        // its merged runs were checked in order before)
+        if (!L.trusted_build) check_flag(L, L.scratch.flag.p, "block4 tiles");
         if (canon) {
             build_b4_orientation(L, L.B4, N, brows, bcols, L.n_in, L.n_out, major.p, minor.p, perm.p,
                                  d_tiles, false);

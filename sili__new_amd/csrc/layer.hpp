@@ -349,6 +349,10 @@ struct Layer {
     int64_t n_in = 0, n_out = 0, max_weights = 0;
     int64_t idx_budget = 0, val_budget = 0, tile_budget = 0;
     int rank = 1;
+    // Set while a step rebuilds the stores from arrays it produced itself
+    // (in range and ordered by construction): the builds then skip their
+    // input checks' waits on the stream.
+    bool trusted_build = false;
     bool vs_ones = true, os_ones = true;  // rank 1 and all ones
     bool output_scale_trainable = false;
     bool has_nonfinite = false;

@@ -1287,8 +1287,15 @@ void synapto_apply(Layer &L, float prune_frac, bool explicit_prune, const uint64
     const bool merge = cnt[3] == 0 && env_int("SILI_TILE_MERGE", 1) != 0;
 
     build_scattered(L, L.W, n_in, n_out, n_final, fptrs.p, fcols.p, fbytes.p);
-    build_shadow(L, L.W, frows.p, fcols.p, L.Wt);
-    build_block4(L, n_tiles, obr.p, obc.p, obytes.p, osparse.p, merge ? n_kept_tiles : -1);
+    {
+        struct Trusted {
+            Layer &L;
+            ~Trusted() { L.trusted_build = false; }
+        } guard{L};
+        L.trusted_build = true;
+        build_shadow(L, L.W, frows.p, fcols.p, L.Wt);
+        build_block4(L, n_tiles, obr.p, obc.p, obytes.p, osparse.p, merge ? n_kept_tiles : -1);
+    }
     refresh_nonfinite(L);
 
     int64_t n_promoted = n_tiles - (T - (int64_t)cnt[1]);

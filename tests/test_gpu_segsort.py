@@ -1,7 +1,7 @@
 """GPU: the shadow builds' ordering by (major, minor) -- a count per major,
 a scatter into the majors' segments and a per-segment bitonic network (the
-wave's lanes up to 64 entries, its LDS slice up to 2048, the device radix sort
-beyond) -- builds the same stores as the radix sort (SILI_SEGSORT=0), on
+wave's lanes up to 64 entries, its LDS slice up to 512, one block in global
+memory beyond) -- builds the same stores as the radix sort (SILI_SEGSORT=0), on
 layers whose columns and block columns fall in each of the three cases, and
 the results match the oracle."""
 import numpy as np
@@ -13,8 +13,9 @@ pytestmark = pytest.mark.gpu
 
 
 def _designed(rng, n_in, n_out):
-    # column 7: every row (n_in > 2048: the radix-sort fallback); columns
-    # 100..109: ~1000 rows each (LDS network); the rest: a few rows each
+    # column 7: every row (> 512: the global-memory network); columns
+    # 100..109: ~450 or ~900 rows each (LDS network, or global memory); the
+    # rest: a few rows each
     rows = []
     for r in range(n_in):
         c = set(rng.choice(n_out, 3, replace=False).tolist())
