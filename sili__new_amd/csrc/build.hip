@@ -198,6 +198,7 @@ __global__ void k_iota(uint32_t *__restrict__ v, int64_t N) {
 // thousand keys took about twenty.
 constexpr uint32_t SEGSORT_CAP = 512;
 constexpr uint32_t SEGSORT_WAVES = 4;
+constexpr uint32_t LONG_LDS_CAP = 8192, LONG_MAX_BLOCKS = 65536;
 
 __global__ void k_fill_u32_b(uint32_t *__restrict__ p, int64_t n, uint32_t v) {
     const int64_t i = (int64_t)blockIdx.x * TPB + threadIdx.x;
@@ -369,7 +370,8 @@ __global__ __launch_bounds__(SEGSORT_WAVES * 64) void k_seg_sort_minor(const uin
     for (uint32_t q = lane; q < len; q += 64u) perm[b + q] = t[q].y;
 }
 
-// The listed long segments, one block each, ordered in place in seg_mnr /
+// The listed long segments, one block each: up to LONG_LDS_CAP entries by a
+// bitonic network in the block's LDS; beyond, in place in seg_mnr /
 // seg_idx by a bitonic network whose comparators all put the smaller minor
 // first (each merge starts by comparing mirrored positions), so positions at
 // or past the segment's end act as +infinity and their comparators are
@@ -378,12 +380,35 @@ __global__ __launch_bounds__(256) void k_seg_sort_long(const uint32_t *__restric
                                                        const uint32_t *__restrict__ n_long,
                                                        const uint32_t *__restrict__ longs, uint32_t *seg_mnr,
                                                        uint32_t *seg_idx, uint32_t *__restrict__ perm) {
+    __shared__ uint2 t[LONG_LDS_CAP];
     const uint32_t nl = *n_long;
     for (uint32_t q = blockIdx.x; q < nl; q += gridDim.x) {
         const uint32_t m = longs[q], b = ptr[m], len = ptr[m + 1] - b;
         uint32_t *mn = seg_mnr + b, *ix = seg_idx + b;
         uint32_t n2 = 1;
         while (n2 < len) n2 <<= 1;
+        if (len <= LONG_LDS_CAP) {
+            // the block's LDS: a plain bitonic network, padding sorting last
+            for (uint32_t i = threadIdx.x; i < n2; i += 256u)
+                t[i] = i < len ? make_uint2(mn[i], ix[i]) : make_uint2(0xFFFFFFFFu, 0u);
+            __syncthreads();
+            for (uint32_t k = 2; k <= n2; k <<= 1)
+                for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+                    for (uint32_t i = threadIdx.x; i < n2 / 2u; i += 256u) {
+                        const uint32_t lo = (i / j) * 2u * j + (i % j), hi = lo + j;
+                        const bool up = (lo & k) == 0u;
+                        const uint2 x = t[lo], y = t[hi];
+                        if (up ? x.x > y.x : x.x < y.x) {
+                            t[lo] = y;
+                            t[hi] = x;
+                        }
+                    }
+                    __syncthreads();
+                }
+            for (uint32_t i = threadIdx.x; i < len; i += 256u) perm[b + i] = t[i].y;
+            __syncthreads();
+            continue;
+        }
         for (uint32_t k = 2; k <= n2; k <<= 1)
             for (uint32_t j = k >> 1; j > 0; j >>= 1) {
                 for (uint32_t t = threadIdx.x; t < n2 / 2u; t += 256u) {
@@ -684,7 +709,10 @@ static void sort_major_minor(Layer &L, const uint32_t *maj, const uint32_t *mnr,
         launch(k_seg_sort_minor, dim3((unsigned)((maj_ext + SEGSORT_WAVES - 1) / SEGSORT_WAVES)),
                dim3(SEGSORT_WAVES * 64), 0, st, (const uint32_t *)ptr, maj_ext, (const uint32_t *)smn.p,
                (const uint32_t *)sidx.p, perm, cnt.p + maj_ext + 1, longs.p);
-        launch(k_seg_sort_long, dim3(32), dim3(256), 0, st, (const uint32_t *)ptr,
+        // (one block per possible long segment, up to LONG_MAX_BLOCKS; blocks
+        // past the listed count return at once)
+        const unsigned lgrid = (unsigned)std::min<int64_t>(N / (SEGSORT_CAP + 1) + 1, LONG_MAX_BLOCKS);
+        launch(k_seg_sort_long, dim3(lgrid), dim3(256), 0, st, (const uint32_t *)ptr,
                (const uint32_t *)(cnt.p + maj_ext + 1), (const uint32_t *)longs.p, smn.p, sidx.p, perm);
     }
     SILI_HIP(hipGetLastError());

@@ -591,7 +591,7 @@ constexpr uint32_t KO_BINS = 16384 + 1024;
 // KO_CAP bounds the LDS network's segment (KO_WAVES * KO_CAP * 8 bytes of LDS
 // per block): at 2048 the 64 KiB block left 8 waves per CU, and the launch
 // over 16384 short segments took 25 us whatever their lengths.
-constexpr uint32_t KO_WAVES = 4, KO_CAP = 512, KO_LONG_BLOCKS = 32;
+constexpr uint32_t KO_WAVES = 4, KO_CAP = 512, KO_LONG_LDS = 8192, KO_LONG_MAX_BLOCKS = 65536;
 
 struct KeySplit {
     uint64_t div;    // 0: major = key >> 32, minor = low 32 bits
@@ -805,7 +805,8 @@ __global__ __launch_bounds__(KO_WAVES * 64) void k_ko_seg(const uint32_t *__rest
     }
 }
 
-// The listed long segments, one block each, sorted in place in seg_mnr /
+// The listed long segments, one block each: up to KO_LONG_LDS entries by a
+// bitonic network in the block's LDS; beyond, in place in seg_mnr /
 // seg_idx by a bitonic network whose comparators all put the smaller pair
 // first (each merge starts by comparing mirrored positions), so positions at
 // or past the segment's end act as +infinity and their comparators are
@@ -815,12 +816,37 @@ __global__ __launch_bounds__(256) void k_ko_long(const uint32_t *__restrict__ pt
                                                  const uint32_t *__restrict__ longs, uint32_t *seg_mnr,
                                                  uint32_t *seg_idx, uint64_t *__restrict__ key_out,
                                                  uint32_t *__restrict__ perm) {
+    __shared__ uint64_t t[KO_LONG_LDS];
     const uint32_t nl = *n_long;
     for (uint32_t q = blockIdx.x; q < nl; q += gridDim.x) {
         const uint32_t m = longs[q], b = ptr[m], len = ptr[m + 1] - b;
         uint32_t *mn = seg_mnr + b, *ix = seg_idx + b;
         uint32_t n2 = 1;
         while (n2 < len) n2 <<= 1;
+        if (len <= KO_LONG_LDS) {
+            // the block's LDS: a plain bitonic network, padding sorting last
+            for (uint32_t i = threadIdx.x; i < n2; i += 256u) t[i] = i < len ? ko_pack(mn[i], ix[i]) : ~0ull;
+            __syncthreads();
+            for (uint32_t k = 2; k <= n2; k <<= 1)
+                for (uint32_t j = k >> 1; j > 0; j >>= 1) {
+                    for (uint32_t i = threadIdx.x; i < n2 / 2u; i += 256u) {
+                        const uint32_t lo = (i / j) * 2u * j + (i % j), hi = lo + j;
+                        const bool up = (lo & k) == 0u;
+                        const uint64_t x = t[lo], y = t[hi];
+                        if (up ? x > y : x < y) {
+                            t[lo] = y;
+                            t[hi] = x;
+                        }
+                    }
+                    __syncthreads();
+                }
+            for (uint32_t i = threadIdx.x; i < len; i += 256u) {
+                key_out[b + i] = ks.key(m, (uint32_t)(t[i] >> 32));
+                perm[b + i] = (uint32_t)t[i];
+            }
+            __syncthreads();
+            continue;
+        }
         for (uint32_t k = 2; k <= n2; k <<= 1)
             for (uint32_t j = k >> 1; j > 0; j >>= 1) {
                 for (uint32_t t = threadIdx.x; t < n2 / 2u; t += 256u) {
@@ -872,7 +898,7 @@ bool order_keys(Layer &L, const uint64_t *key, int64_t N, uint32_t n_maj, uint64
            (const uint32_t *)ptr.p, cnt.p, cnt.p + nb + 1, smn.p, sidx.p, key_out, perm);
     launch(k_ko_seg, dim3((n_maj + KO_WAVES - 1) / KO_WAVES), dim3(KO_WAVES * 64), 0, st, (const uint32_t *)ptr.p,
            ks, (const uint32_t *)smn.p, (const uint32_t *)sidx.p, key_out, perm, cnt.p + nb, longs.p);
-    launch(k_ko_long, dim3(KO_LONG_BLOCKS), dim3(256), 0, st, (const uint32_t *)ptr.p, ks,
+    launch(k_ko_long, dim3((unsigned)std::min<int64_t>(max_long, KO_LONG_MAX_BLOCKS)), dim3(256), 0, st, (const uint32_t *)ptr.p, ks,
            (const uint32_t *)(cnt.p + nb), (const uint32_t *)longs.p, smn.p, sidx.p, key_out, perm);
     SILI_HIP(hipGetLastError());
     return true;

@@ -1,7 +1,7 @@
 """GPU: the shadow builds' ordering by (major, minor) -- a count per major,
 a scatter into the majors' segments and a per-segment bitonic network (the
-wave's lanes up to 64 entries, its LDS slice up to 512, one block in global
-memory beyond) -- builds the same stores as the radix sort (SILI_SEGSORT=0), on
+wave's lanes up to 64 entries, its LDS slice up to 512, one block beyond: in
+its LDS up to 8192, in global memory past that) -- builds the same stores as the radix sort (SILI_SEGSORT=0), on
 layers whose columns and block columns fall in each of the three cases, and
 the results match the oracle."""
 import numpy as np
@@ -13,9 +13,10 @@ pytestmark = pytest.mark.gpu
 
 
 def _designed(rng, n_in, n_out):
-    # column 7: every row (> 512: the global-memory network); columns
-    # 100..109: ~450 or ~900 rows each (LDS network, or global memory); the
-    # rest: a few rows each
+    # column 7: every row (> 512: one block's network, in global memory
+    # past 8192 rows); columns
+    # 100..109: 30 % of the rows each (the wave's LDS network, or one
+    # block's); the rest: a few rows each
     rows = []
     for r in range(n_in):
         c = set(rng.choice(n_out, 3, replace=False).tolist())
@@ -43,7 +44,7 @@ def _block4(rng, n_in, n_out):
     return np.asarray(br, np.int32), np.asarray(bc, np.int32), tiles
 
 
-@pytest.mark.parametrize("n_in", [1500, 3000])
+@pytest.mark.parametrize("n_in", [1500, 3000, 9000])
 def test_segment_order_equals_sort(hip, monkeypatch, n_in):
     rng = np.random.default_rng(n_in)
     n_out = 4096

@@ -1,7 +1,7 @@
 """GPU: the synaptogenesis step's key orderings (candidate keys, inserted
 windows, the final scattered set) by a count per major and per-segment
 bitonic networks -- the wave's lanes up to 64 entries, its LDS up to 512, one
-block in global memory beyond 512 -- leave the same layer and statistics as the
+block beyond 512, in its LDS up to 8192 and in global memory past that -- leave the same layer and statistics as the
 device radix sort (SILI_KEYORDER=0) and as the oracle, on a layer and
 candidate list designed to put segments in each of the three cases, with
 repeated candidates (equal keys, ordered by list position) and empty
@@ -36,7 +36,8 @@ def _designed(rng, n_in, n_out):
 def _candidates(rng, n_in, n_out):
     # row 7: 2600 distinct columns, so more than 512 candidate keys and, once
     # inserted, more than 512 window entries in block row 1; row 11: 300
-    # (LDS); 3000 spread out; then 800 repeats of earlier candidates
+    # (LDS); 3000 spread out; then 800 repeats of earlier candidates and 6000
+    # of row 7's (its candidate keys past 8192: the global-memory network)
     r7 = np.full(2600, 7)
     c7 = rng.choice(n_out, 2600, replace=False)
     r11 = np.full(300, 11)
@@ -45,8 +46,9 @@ def _candidates(rng, n_in, n_out):
     cr = np.concatenate([r7, r11, rs]).astype(np.int32)
     cc = np.concatenate([c7, c11, cs]).astype(np.int32)
     rep = rng.integers(0, len(cr), 800)
-    cr = np.concatenate([cr, cr[rep], [-1, n_in]]).astype(np.int32)
-    cc = np.concatenate([cc, cc[rep], [0, 0]]).astype(np.int32)
+    rep7 = rng.integers(0, 2600, 6000)
+    cr = np.concatenate([cr, cr[rep], np.full(6000, 7), [-1, n_in]]).astype(np.int32)
+    cc = np.concatenate([cc, cc[rep], c7[rep7], [0, 0]]).astype(np.int32)
     perm = rng.permutation(len(cr))
     cv = rng.normal(0, 0.5, len(cr)).astype(np.float32)
     return cr[perm], cc[perm], cv[perm]
